@@ -1,0 +1,331 @@
+"""checkers_amd — MI355X (gfx950) checkpoint-compression hot path.
+
+Python view of the C ABI in include/checkers_amd.h (libcheckers_amd.so, built
+in-tree by checkers_amd/build.py).  Device buffers are torch tensors on the
+current HIP device; torch is used only for device memory and streams.
+
+Loading is strict: if the shared library is missing or fails to load, every
+entry point raises.  There is no CPU fallback.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libcheckers_amd.so")
+
+# dtype tags: include/checkers/TensorResource.hpp:30-37 (reference)
+F32, BF16, F16, I8, I32, UNKNOWN = 0, 1, 2, 3, 4, 255
+M = 4096
+L = 1 << 23
+LANES = 256
+
+CKR_OK, CKR_E_INVALID, CKR_E_HIP, CKR_E_CAPACITY, CKR_E_TABLE, CKR_E_CORRUPT = 0, -1, -2, -3, -4, -5
+
+EXPORTED = [  # every symbol include/checkers_amd.h declares
+    "ckr_last_error", "ckr_version", "ckr_element_size", "ckr_sidecar_bytes_per_elem",
+    "ckr_extract_mantissa", "ckr_byte_histogram", "ckr_byte_histogram_raw", "ckr_build_table",
+    "ckr_num_units", "ckr_encode_max_output_bytes", "ckr_encode_workspace_bytes", "ckr_encode",
+    "ckr_compress", "ckr_decode_workspace_bytes", "ckr_decode", "ckr_analyze_workspace_bytes",
+    "ckr_analyze",
+]
+
+
+class CkrError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"{msg} (status {code})")
+        self.code = code
+
+
+class StreamHeader(ctypes.Structure):
+    _fields_ = [("final_state", ctypes.c_uint32), ("byte_count", ctypes.c_uint32),
+                ("buf_offset", ctypes.c_uint32), ("pad", ctypes.c_uint32)]
+
+
+HEADER_DTYPE = np.dtype([("final_state", "<u4"), ("byte_count", "<u4"), ("buf_offset", "<u4"), ("pad", "<u4")])
+
+
+class FreqTable(ctypes.Structure):
+    """ckr_freq_table (40000 bytes, 64-byte aligned in C; see aligned_table())."""
+    _fields_ = [("norm_freq", ctypes.c_uint32 * 256), ("cum_freq", ctypes.c_uint32 * 257),
+                ("x_max", ctypes.c_uint32 * 256), ("decode_sym", ctypes.c_uint8 * 4096),
+                ("decode_freq", ctypes.c_uint32 * 4096), ("decode_cum", ctypes.c_uint32 * 4096),
+                ("_pad", ctypes.c_uint8 * 60)]
+
+
+assert ctypes.sizeof(FreqTable) == 40000
+
+
+class StatsRecord(ctypes.Structure):
+    _fields_ = [("d_ptr", ctypes.c_void_p), ("num_elements", ctypes.c_uint64),
+                ("histogram_bins", ctypes.c_uint32), ("data_type", ctypes.c_uint32),
+                ("d_histogram", ctypes.c_void_p), ("d_raw_moments", ctypes.c_void_p),
+                ("d_minmax", ctypes.c_void_p), ("d_fingerprint", ctypes.c_void_p)]
+
+
+class _AlignedTable:
+    """A FreqTable placed at a 64-byte aligned address (the C type is alignas(64))."""
+
+    def __init__(self):
+        self._buf = ctypes.create_string_buffer(40000 + 64)
+        addr = ctypes.addressof(self._buf)
+        self.table = FreqTable.from_address((addr + 63) & ~63)
+
+    @property
+    def ptr(self):
+        return ctypes.byref(self.table)
+
+    @property
+    def norm(self):
+        return np.frombuffer(self.table.norm_freq, dtype=np.uint32).copy()
+
+    @property
+    def cum(self):
+        return np.frombuffer(self.table.cum_freq, dtype=np.uint32).copy()
+
+    def raw_bytes(self):
+        return ctypes.string_at(ctypes.addressof(self.table), 40000 - 60)
+
+
+def aligned_table():
+    return _AlignedTable()
+
+
+_lib = None
+
+
+def lib():
+    """Load libcheckers_amd.so once; raise if it is missing (no fallback)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"checkers_amd: {LIB_PATH} not built; run `python -m checkers_amd.build`")
+    L_ = ctypes.CDLL(LIB_PATH)
+    u64, i32, vp = ctypes.c_uint64, ctypes.c_int, ctypes.c_void_p
+    sig = {
+        "ckr_last_error": (ctypes.c_char_p, []),
+        "ckr_version": (ctypes.c_char_p, []),
+        "ckr_element_size": (i32, [i32]),
+        "ckr_sidecar_bytes_per_elem": (i32, [i32]),
+        "ckr_extract_mantissa": (i32, [vp, u64, i32, vp, vp, vp]),
+        "ckr_byte_histogram": (i32, [vp, u64, i32, vp, vp]),
+        "ckr_byte_histogram_raw": (i32, [vp, u64, vp, vp]),
+        "ckr_build_table": (i32, [vp, i32, vp, vp]),
+        "ckr_num_units": (u64, [u64, i32, u64]),
+        "ckr_encode_max_output_bytes": (u64, [u64, i32, u64]),
+        "ckr_encode_workspace_bytes": (u64, [u64, i32, u64]),
+        "ckr_encode": (i32, [vp, u64, i32, vp, u64, vp, u64, vp, vp, vp, vp, u64, vp, vp]),
+        "ckr_compress": (i32, [vp, u64, i32, u64, i32, vp, u64, vp, vp, vp, vp, u64, vp, vp, vp]),
+        "ckr_decode_workspace_bytes": (u64, [u64, i32, u64]),
+        "ckr_decode": (i32, [vp, vp, vp, vp, u64, i32, u64, vp, vp, vp, u64, vp, vp]),
+        "ckr_analyze_workspace_bytes": (u64, [vp, u64]),
+        "ckr_analyze": (i32, [vp, u64, vp, u64, vp]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L_, name)
+        f.restype = res
+        f.argtypes = args
+    _lib = L_
+    return _lib
+
+
+def _check(rc):
+    if rc != CKR_OK:
+        raise CkrError(rc, lib().ckr_last_error().decode())
+
+
+def element_size(dtype):
+    return lib().ckr_element_size(dtype)
+
+
+def sidecar_bytes_per_elem(dtype):
+    return lib().ckr_sidecar_bytes_per_elem(dtype)
+
+
+def num_units(n_elems, dtype, unit_bytes):
+    return lib().ckr_num_units(n_elems, dtype, unit_bytes)
+
+
+def build_table(hist, ensure_full_alphabet=False):
+    """Host table from a 256-bin histogram (ANSCompressor::normalize_histogram)."""
+    h = np.ascontiguousarray(np.asarray(hist, dtype=np.uint32))
+    assert h.shape == (256,)
+    t = aligned_table()
+    s = ctypes.c_uint32(0)
+    _check(lib().ckr_build_table(h.ctypes.data, int(bool(ensure_full_alphabet)), t.ptr, ctypes.byref(s)))
+    return t, s.value
+
+
+# --------------------------------------------------------------- torch helpers
+def _torch():
+    import torch
+    return torch
+
+
+def torch_tag(dtype):
+    """C tag of a torch dtype (explicit; see checkers_py for the reference's string parser)."""
+    torch = _torch()
+    return {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.int8: I8,
+            torch.int32: I32}.get(dtype, UNKNOWN)
+
+
+def _stream(stream):
+    torch = _torch()
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+def _empty(nbytes, device):
+    torch = _torch()
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+class Encoded:
+    """Device-resident result of encode(): data[:total], headers, unit offsets, sidecar."""
+
+    def __init__(self, data, headers, unit_offsets, sidecar, total, n_elems, dtype, unit_bytes, table):
+        self.data, self.headers, self.unit_offsets, self.sidecar = data, headers, unit_offsets, sidecar
+        self.total, self.n_elems, self.dtype, self.unit_bytes, self.table = total, n_elems, dtype, unit_bytes, table
+
+    def headers_np(self):
+        return self.headers.cpu().numpy().view(HEADER_DTYPE).reshape(-1)
+
+    def data_np(self):
+        return self.data[: self.total].cpu().numpy()
+
+
+class Encoder:
+    """Reusable buffers for repeated encodes of one tensor shape (bench / tests)."""
+
+    def __init__(self, n_elems, dtype, unit_bytes, device="cuda"):
+        torch = _torch()
+        self.n_elems, self.dtype, self.unit_bytes = int(n_elems), dtype, int(unit_bytes)
+        Lb = lib()
+        es = Lb.ckr_element_size(dtype)
+        if es == 0:
+            raise CkrError(CKR_E_INVALID, f"unknown dtype tag {dtype}")
+        self.n_bytes = self.n_elems * es
+        self.n_units = int(Lb.ckr_num_units(self.n_elems, dtype, self.unit_bytes))
+        self.ws_bytes = int(Lb.ckr_encode_workspace_bytes(self.n_elems, dtype, self.unit_bytes))
+        self.out_cap = int(Lb.ckr_encode_max_output_bytes(self.n_elems, dtype, self.unit_bytes))
+        self.ws = _empty(self.ws_bytes, device)
+        self.out = _empty(self.out_cap, device)
+        self.headers = torch.empty(max(self.n_units, 1) * LANES * 4, dtype=torch.int32, device=device)
+        self.unit_offsets = torch.empty(self.n_units + 1, dtype=torch.int64, device=device)
+        spe = Lb.ckr_sidecar_bytes_per_elem(dtype)
+        self.sidecar = _empty(self.n_elems * spe, device) if spe else None
+
+    def encode(self, src, table, stream=None, sync_total=True):
+        tot = ctypes.c_uint64(0)
+        _check(lib().ckr_encode(
+            src.data_ptr(), self.n_elems, self.dtype, table.ptr, self.unit_bytes,
+            self.out.data_ptr(), self.out_cap, self.headers.data_ptr(), self.unit_offsets.data_ptr(),
+            self.sidecar.data_ptr() if self.sidecar is not None else None,
+            self.ws.data_ptr(), self.ws_bytes, ctypes.byref(tot) if sync_total else None, _stream(stream)))
+        return Encoded(self.out, self.headers, self.unit_offsets, self.sidecar,
+                       tot.value if sync_total else None, self.n_elems, self.dtype, self.unit_bytes, table)
+
+    def compress(self, src, ensure_full_alphabet=False, stream=None):
+        tot = ctypes.c_uint64(0)
+        t = aligned_table()
+        _check(lib().ckr_compress(
+            src.data_ptr(), self.n_elems, self.dtype, self.unit_bytes, int(bool(ensure_full_alphabet)),
+            self.out.data_ptr(), self.out_cap, self.headers.data_ptr(), self.unit_offsets.data_ptr(),
+            self.sidecar.data_ptr() if self.sidecar is not None else None,
+            self.ws.data_ptr(), self.ws_bytes, t.ptr, ctypes.byref(tot), _stream(stream)))
+        return Encoded(self.out, self.headers, self.unit_offsets, self.sidecar, tot.value, self.n_elems,
+                       self.dtype, self.unit_bytes, t)
+
+
+def byte_histogram(src, dtype, n_elems=None, stream=None):
+    """256-bin histogram of the masked byte stream of `src` (torch device tensor)."""
+    torch = _torch()
+    n = src.numel() if n_elems is None else n_elems
+    h = torch.empty(256, dtype=torch.int32, device=src.device)
+    _check(lib().ckr_byte_histogram(src.data_ptr(), n, dtype, h.data_ptr(), _stream(stream)))
+    return h
+
+
+def extract_mantissa(src, dtype, n_elems=None, stream=None):
+    torch = _torch()
+    n = src.numel() if n_elems is None else n_elems
+    es, spe = element_size(dtype), sidecar_bytes_per_elem(dtype)
+    masked = torch.empty(max(n * es, 1), dtype=torch.uint8, device=src.device)
+    side = torch.empty(max(n * spe, 1), dtype=torch.uint8, device=src.device)
+    _check(lib().ckr_extract_mantissa(src.data_ptr(), n, dtype, masked.data_ptr(), side.data_ptr(), _stream(stream)))
+    return masked[: n * es], side[: n * spe]
+
+
+def encode(src, dtype, table, unit_bytes, n_elems=None, stream=None):
+    n = src.numel() if n_elems is None else n_elems
+    enc = Encoder(n, dtype, unit_bytes, device=src.device)
+    return enc.encode(src, table, stream=stream)
+
+
+def compress(src, dtype, unit_bytes, ensure_full_alphabet=False, n_elems=None, stream=None):
+    n = src.numel() if n_elems is None else n_elems
+    return Encoder(n, dtype, unit_bytes, device=src.device).compress(src, ensure_full_alphabet, stream=stream)
+
+
+class Decoder:
+    def __init__(self, n_elems, dtype, unit_bytes, device="cuda"):
+        self.n_elems, self.dtype, self.unit_bytes = int(n_elems), dtype, int(unit_bytes)
+        self.ws_bytes = int(lib().ckr_decode_workspace_bytes(self.n_elems, dtype, self.unit_bytes))
+        self.ws = _empty(self.ws_bytes, device)
+
+    def decode(self, data, headers, unit_offsets, table, sidecar, dst, stream=None, check=True):
+        bad = ctypes.c_uint64(0)
+        _check(lib().ckr_decode(
+            data.data_ptr(), headers.data_ptr(), unit_offsets.data_ptr(), table.ptr, self.n_elems, self.dtype,
+            self.unit_bytes, sidecar.data_ptr() if sidecar is not None else None, dst.data_ptr(),
+            self.ws.data_ptr(), self.ws_bytes, ctypes.byref(bad) if check else None, _stream(stream)))
+        return bad.value if check else None
+
+
+def decode(enc, dst=None, stream=None):
+    """Decode an Encoded back into original bytes; returns (dst uint8 tensor, bad_lanes)."""
+    torch = _torch()
+    nb = enc.n_elems * element_size(enc.dtype)
+    if dst is None:
+        dst = torch.empty(max(nb, 1), dtype=torch.uint8, device=enc.data.device)
+    d = Decoder(enc.n_elems, enc.dtype, enc.unit_bytes, device=enc.data.device)
+    bad = d.decode(enc.data, enc.headers, enc.unit_offsets, enc.table, enc.sidecar, dst, stream=stream)
+    return dst[:nb], bad
+
+
+def analyze(tensors, tags, bins=256, stream=None):
+    """TensorAnalyzer statistics for a list of device tensors.
+
+    Returns a list of dicts with histogram (np.uint32), moments (mean, var,
+    skew, kurt), minmax and fingerprint, all copied to the host."""
+    torch = _torch()
+    n = len(tensors)
+    dev = tensors[0].device if n else "cuda"
+    nb = min(bins, 256)
+    hist = torch.zeros((max(n, 1), max(nb, 1)), dtype=torch.int32, device=dev)
+    mom = torch.zeros((max(n, 1), 4), dtype=torch.float32, device=dev)
+    mm = torch.zeros((max(n, 1), 2), dtype=torch.float32, device=dev)
+    fp = torch.zeros((max(n, 1), 5), dtype=torch.float32, device=dev)
+    recs = (StatsRecord * max(n, 1))()
+    for i, (t, tag) in enumerate(zip(tensors, tags)):
+        recs[i].d_ptr = t.data_ptr() if t.numel() else None
+        recs[i].num_elements = t.numel()
+        recs[i].histogram_bins = bins
+        recs[i].data_type = tag
+        recs[i].d_histogram = hist[i].data_ptr()
+        recs[i].d_raw_moments = mom[i].data_ptr()
+        recs[i].d_minmax = mm[i].data_ptr()
+        recs[i].d_fingerprint = fp[i].data_ptr()
+    wsb = int(lib().ckr_analyze_workspace_bytes(recs, n))
+    ws = _empty(wsb, dev)
+    _check(lib().ckr_analyze(recs, n, ws.data_ptr(), wsb, _stream(stream)))
+    torch.cuda.synchronize()
+    out = []
+    for i in range(n):
+        out.append(dict(histogram=hist[i, :nb].cpu().numpy().view(np.uint32).copy(),
+                        moments=mom[i].cpu().numpy().copy(), minmax=mm[i].cpu().numpy().copy(),
+                        fingerprint=fp[i].cpu().numpy().copy()))
+    return out

@@ -1,0 +1,376 @@
+// checkers_amd/csrc/ckr_api.cpp — the extern "C" layer (include/checkers_amd.h).
+//
+// Host responsibilities: argument checks, workspace carving, the histogram →
+// table step (host code, as in the reference), and batching of encode units
+// so the lane scratch stays within a fixed budget whatever the tensor size.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "checkers_amd.h"
+#include "ckr_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+#define CKR_HIP(call)                                                                      \
+    do {                                                                                   \
+        hipError_t _e = (call);                                                            \
+        if (_e != hipSuccess)                                                              \
+            return fail(CKR_E_HIP, "[ckr] HIP error in %s: %s", #call, hipGetErrorString(_e)); \
+    } while (0)
+
+constexpr uint64_t kAlign = 256;
+constexpr uint64_t kScratchBudget = 2ull << 30;  // lane scratch per encode batch
+
+inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool dtype_ok(int dt) { return dt == CKR_F32 || dt == CKR_BF16 || dt == CKR_F16 || dt == CKR_I8 || dt == CKR_I32; }
+
+// Unit geometry of a tensor; returns false (with the error set) for a unit size
+// the format cannot express.
+bool make_geom(uint64_t n_elems, int dtype, uint64_t unit_bytes, ckr::EncodeGeom* g) {
+    const int es = ckr_element_size(dtype);
+    g->es = es;
+    g->spe = ckr_sidecar_bytes_per_elem(dtype);
+    g->n_bytes = n_elems * (uint64_t)es;
+    if (g->n_bytes == 0) { g->unit = 0; g->n_units = 0; g->wmax = 0; return true; }
+    if (unit_bytes == 0 || unit_bytes >= g->n_bytes) {
+        if (g->n_bytes > 0xFFFFFFFFull) {  // u32 byte_count / buf_offset (ANSCompressor.hpp:79-84)
+            fail(CKR_E_INVALID, "[ckr] single-unit layout needs n_bytes < 2^32 (got %llu); use unit_bytes",
+                 (unsigned long long)g->n_bytes);
+            return false;
+        }
+        g->unit = g->n_bytes;
+        g->n_units = 1;
+    } else {
+        if (unit_bytes % 256 != 0 || unit_bytes > 0xFFFFFFFFull) {
+            fail(CKR_E_INVALID, "[ckr] unit_bytes must be a multiple of 256 below 2^32 (got %llu)",
+                 (unsigned long long)unit_bytes);
+            return false;
+        }
+        g->unit = unit_bytes;
+        g->n_units = (g->n_bytes + unit_bytes - 1) / unit_bytes;
+    }
+    const uint64_t K = (g->unit + 255) / 256;  // symbols of lane 0
+    g->wmax = (uint32_t)((2 * K + 3) / 4);     // worst case 2 bytes per symbol
+    return true;
+}
+
+struct EncodeLayout {
+    uint64_t off_enc, off_hist, off_usize, off_scratch, total;
+    uint64_t batch_units;
+};
+
+EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
+    EncodeLayout L{};
+    const uint64_t per_unit = (uint64_t)g.wmax * 256 * 4;
+    uint64_t bu = per_unit ? std::max<uint64_t>(1, kScratchBudget / per_unit) : 1;
+    bu = std::min<uint64_t>(bu, std::max<uint64_t>(g.n_units, 1));
+    L.batch_units = bu;
+    uint64_t o = 0;
+    L.off_enc = o;     o = align_up(o + 256 * sizeof(ckr::EncSym), kAlign);
+    L.off_hist = o;    o = align_up(o + 256 * 4, kAlign);
+    L.off_usize = o;   o = align_up(o + bu * 4, kAlign);
+    L.off_scratch = o; o = align_up(o + bu * per_unit, kAlign);
+    L.total = o;
+    return L;
+}
+
+bool table_arg(const ckr_freq_table* t, ckr::TableArg* a) {
+    for (int s = 0; s < 256; s++) {
+        if (t->norm_freq[s] > CKR_M) { fail(CKR_E_TABLE, "[ckr] norm_freq[%d]=%u > 4096", s, t->norm_freq[s]); return false; }
+        a->norm[s] = (uint16_t)t->norm_freq[s];
+    }
+    for (int s = 0; s <= 256; s++) {
+        if (t->cum_freq[s] > 0xFFFFu) { fail(CKR_E_TABLE, "[ckr] cum_freq[%d]=%u too large", s, t->cum_freq[s]); return false; }
+        a->cum[s] = (uint16_t)t->cum_freq[s];
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ckr_last_error(void) { return g_last_error.c_str(); }
+const char* ckr_version(void) { return "checkers_amd 0.1 gfx950"; }
+
+int ckr_element_size(int dtype) {
+    switch (dtype) {
+        case CKR_F32: return 4; case CKR_BF16: return 2; case CKR_F16: return 2;
+        case CKR_I8: return 1; case CKR_I32: return 4; default: return 0;
+    }
+}
+
+int ckr_sidecar_bytes_per_elem(int dtype) {
+    switch (dtype) {
+        case CKR_F32: return 2; case CKR_BF16: return 1; case CKR_F16: return 1; default: return 0;
+    }
+}
+
+int ckr_extract_mantissa(const void* d_src, uint64_t n_elems, int dtype, void* d_masked, void* d_sidecar,
+                         void* stream) {
+    const int spe = ckr_sidecar_bytes_per_elem(dtype);
+    if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
+    if (spe == 0) return fail(CKR_E_INVALID, "[ckr] dtype %d has no mantissa sidecar", dtype);
+    if (n_elems == 0) return CKR_OK;
+    if (!d_src || !d_masked || !d_sidecar) return fail(CKR_E_INVALID, "[ckr] null pointer");
+    if (!aligned16(d_src) || !aligned16(d_masked) || !aligned16(d_sidecar))
+        return fail(CKR_E_INVALID, "[ckr] buffers must be 16-byte aligned");
+    CKR_HIP(ckr::launch_extract_mantissa(static_cast<const uint8_t*>(d_src), n_elems, ckr_element_size(dtype), spe,
+                                         static_cast<uint8_t*>(d_masked), static_cast<uint8_t*>(d_sidecar),
+                                         (hipStream_t)stream));
+    return CKR_OK;
+}
+
+int ckr_byte_histogram(const void* d_src, uint64_t n_elems, int dtype, uint32_t* d_hist, void* stream) {
+    if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
+    if (!d_hist || (n_elems && !d_src)) return fail(CKR_E_INVALID, "[ckr] null pointer");
+    if (n_elems && !aligned16(d_src)) return fail(CKR_E_INVALID, "[ckr] source must be 16-byte aligned");
+    const int es = ckr_element_size(dtype);
+    CKR_HIP(ckr::launch_masked_hist(static_cast<const uint8_t*>(d_src), n_elems * (uint64_t)es, es,
+                                    ckr_sidecar_bytes_per_elem(dtype), d_hist, (hipStream_t)stream));
+    return CKR_OK;
+}
+
+int ckr_byte_histogram_raw(const void* d_bytes, uint64_t n_bytes, uint32_t* d_hist, void* stream) {
+    return ckr_byte_histogram(d_bytes, n_bytes, CKR_I8, d_hist, stream);
+}
+
+// ANSCompressor::normalize_histogram (src/ANSCompressor.cpp:416-503): proportional
+// slots, then one correction pass ordered by libstdc++ std::sort of the
+// fractional parts (descending, ties in the order that sort leaves them).
+int ckr_build_table(const uint32_t* h, int ensure_full_alphabet, ckr_freq_table* t, uint32_t* h_table_sum) {
+    if (!h || !t) return fail(CKR_E_INVALID, "[ckr] null pointer");
+    std::memset(t, 0, sizeof(*t));
+    uint64_t total = 0;
+    int distinct = 0;
+    for (int i = 0; i < 256; i++) { total += h[i]; distinct += h[i] > 0; }
+    if ((ensure_full_alphabet ? 256 : distinct) == 0) {
+        t->norm_freq[0] = CKR_M;
+        for (int i = 1; i <= 256; i++) t->cum_freq[i] = CKR_M;
+        t->x_max[0] = CKR_NORM_BASE * CKR_M;
+        for (uint32_t j = 0; j < CKR_M; j++) { t->decode_sym[j] = 0; t->decode_freq[j] = CKR_M; t->decode_cum[j] = 0; }
+        if (h_table_sum) *h_table_sum = CKR_M;
+        return CKR_OK;
+    }
+    uint32_t norm[256] = {};
+    uint32_t assigned = 0;
+    for (int i = 0; i < 256; i++) {
+        if (!ensure_full_alphabet && h[i] == 0) continue;
+        uint32_t slots = total ? (uint32_t)((uint64_t)std::max(h[i], 1u) * CKR_M / total) : 0u;
+        norm[i] = slots ? slots : 1u;
+        assigned += norm[i];
+    }
+    struct Frac { int sym; double frac; };
+    std::vector<Frac> fr;
+    fr.reserve(256);
+    for (int i = 0; i < 256; i++) {
+        if (!norm[i]) continue;
+        const double exact = total ? (double)std::max(h[i], 1u) * CKR_M / (double)total : 1.0;
+        fr.push_back({i, exact - (double)(int)exact});
+    }
+    std::sort(fr.begin(), fr.end(), [](const Frac& a, const Frac& b) { return a.frac > b.frac; });
+    if (assigned < CKR_M) {
+        uint32_t rem = CKR_M - assigned;
+        for (size_t k = 0; k < fr.size() && rem; k++, rem--) norm[fr[k].sym]++;
+    } else if (assigned > CKR_M) {
+        uint32_t rem = assigned - CKR_M;
+        for (int k = (int)fr.size() - 1; k >= 0 && rem; k--)
+            if (norm[fr[k].sym] > 1) { norm[fr[k].sym]--; rem--; }
+    }
+    t->cum_freq[0] = 0;
+    for (int i = 0; i < 256; i++) { t->norm_freq[i] = norm[i]; t->cum_freq[i + 1] = t->cum_freq[i] + norm[i]; }
+    for (int s = 0; s < 256; s++) {
+        if (!norm[s]) continue;
+        t->x_max[s] = CKR_NORM_BASE * norm[s];
+        for (uint32_t j = t->cum_freq[s]; j < t->cum_freq[s + 1] && j < CKR_M; j++) {
+            t->decode_sym[j] = (uint8_t)s;
+            t->decode_freq[j] = norm[s];
+            t->decode_cum[j] = t->cum_freq[s];
+        }
+    }
+    if (h_table_sum) *h_table_sum = t->cum_freq[256];
+    return CKR_OK;
+}
+
+uint64_t ckr_num_units(uint64_t n_elems, int dtype, uint64_t unit_bytes) {
+    ckr::EncodeGeom g;
+    if (!dtype_ok(dtype) || !make_geom(n_elems, dtype, unit_bytes, &g)) return 0;
+    return g.n_units;
+}
+
+uint64_t ckr_encode_max_output_bytes(uint64_t n_elems, int dtype, uint64_t unit_bytes) {
+    (void)unit_bytes;  // every unit is at most its own length (passthrough rule)
+    return n_elems * (uint64_t)ckr_element_size(dtype);
+}
+
+uint64_t ckr_encode_workspace_bytes(uint64_t n_elems, int dtype, uint64_t unit_bytes) {
+    ckr::EncodeGeom g;
+    if (!dtype_ok(dtype) || !make_geom(n_elems, dtype, unit_bytes, &g)) return 0;
+    return encode_layout(g).total;
+}
+
+int ckr_encode(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table, uint64_t unit_bytes,
+               uint8_t* d_out, uint64_t out_capacity, ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
+               uint8_t* d_sidecar, void* d_workspace, uint64_t workspace_bytes, uint64_t* h_total_out,
+               void* stream) {
+    if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
+    ckr::EncodeGeom g;
+    if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
+    hipStream_t s = (hipStream_t)stream;
+    if (!h_table || !d_unit_offsets) return fail(CKR_E_INVALID, "[ckr] null table or offsets");
+    if (g.n_units == 0) {
+        CKR_HIP(ckr::launch_set_u64(d_unit_offsets, 0, s));
+        if (h_total_out) *h_total_out = 0;
+        return CKR_OK;
+    }
+    if (!d_src || !d_out || !d_headers || !d_workspace) return fail(CKR_E_INVALID, "[ckr] null pointer");
+    if (!aligned16(d_src) || !aligned16(d_workspace) || (d_sidecar && !aligned16(d_sidecar)))
+        return fail(CKR_E_INVALID, "[ckr] source, sidecar and workspace must be 16-byte aligned");
+    if (out_capacity < g.n_bytes)
+        return fail(CKR_E_CAPACITY, "[ckr] output capacity %llu < %llu", (unsigned long long)out_capacity,
+                    (unsigned long long)g.n_bytes);
+    const EncodeLayout L = encode_layout(g);
+    if (workspace_bytes < L.total)
+        return fail(CKR_E_CAPACITY, "[ckr] workspace %llu < %llu", (unsigned long long)workspace_bytes,
+                    (unsigned long long)L.total);
+    ckr::TableArg ta;
+    if (!table_arg(h_table, &ta)) return CKR_E_TABLE;
+    uint8_t* ws = static_cast<uint8_t*>(d_workspace);
+    auto* enc = reinterpret_cast<ckr::EncSym*>(ws + L.off_enc);
+    auto* usize = reinterpret_cast<uint32_t*>(ws + L.off_usize);
+    auto* scratch = reinterpret_cast<uint32_t*>(ws + L.off_scratch);
+    CKR_HIP(ckr::launch_build_enc_table(ta, enc, s));
+    for (uint64_t u0 = 0; u0 < g.n_units; u0 += L.batch_units) {
+        const uint64_t nb = std::min<uint64_t>(L.batch_units, g.n_units - u0);
+        CKR_HIP(ckr::launch_encode_batch(static_cast<const uint8_t*>(d_src), g, u0, nb, enc, scratch, d_headers,
+                                         g.spe ? d_sidecar : nullptr, usize, d_unit_offsets, d_out, s));
+    }
+    if (h_total_out) {
+        CKR_HIP(hipMemcpyAsync(h_total_out, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
+        CKR_HIP(hipStreamSynchronize(s));
+    }
+    return CKR_OK;
+}
+
+int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_bytes, int ensure_full_alphabet,
+                 uint8_t* d_out, uint64_t out_capacity, ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
+                 uint8_t* d_sidecar, void* d_workspace, uint64_t workspace_bytes, ckr_freq_table* h_table,
+                 uint64_t* h_total_out, void* stream) {
+    if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
+    ckr::EncodeGeom g;
+    if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
+    const EncodeLayout L = encode_layout(g);
+    if (!d_workspace || workspace_bytes < L.total)
+        return fail(CKR_E_CAPACITY, "[ckr] workspace too small (%llu < %llu)", (unsigned long long)workspace_bytes,
+                    (unsigned long long)L.total);
+    hipStream_t s = (hipStream_t)stream;
+    uint32_t* d_hist = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(d_workspace) + L.off_hist);
+    int rc = ckr_byte_histogram(d_src, n_elems, dtype, d_hist, stream);
+    if (rc) return rc;
+    uint32_t hh[256];
+    CKR_HIP(hipMemcpyAsync(hh, d_hist, sizeof(hh), hipMemcpyDeviceToHost, s));
+    CKR_HIP(hipStreamSynchronize(s));
+    ckr_freq_table local;
+    ckr_freq_table* t = h_table ? h_table : &local;
+    rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
+    if (rc) return rc;
+    return ckr_encode(d_src, n_elems, dtype, t, unit_bytes, d_out, out_capacity, d_headers, d_unit_offsets,
+                      d_sidecar, d_workspace, workspace_bytes, h_total_out, stream);
+}
+
+uint64_t ckr_decode_workspace_bytes(uint64_t, int, uint64_t) { return align_up(4096 * 4 + 64, kAlign); }
+
+int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const uint64_t* d_unit_offsets,
+               const ckr_freq_table* h_table, uint64_t n_elems, int dtype, uint64_t unit_bytes,
+               const uint8_t* d_sidecar, void* d_dst, void* d_workspace, uint64_t workspace_bytes,
+               uint64_t* h_bad_lanes, void* stream) {
+    if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
+    ckr::EncodeGeom g;
+    if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
+    if (h_bad_lanes) *h_bad_lanes = 0;
+    if (g.n_units == 0) return CKR_OK;
+    if (!h_table || !d_data || !d_headers || !d_unit_offsets || !d_dst || !d_workspace)
+        return fail(CKR_E_INVALID, "[ckr] null pointer");
+    if (g.spe && !d_sidecar) return fail(CKR_E_INVALID, "[ckr] dtype %d needs its sidecar", dtype);
+    if (!aligned16(d_dst) || !aligned16(d_workspace) || (d_sidecar && !aligned16(d_sidecar)))
+        return fail(CKR_E_INVALID, "[ckr] destination, sidecar and workspace must be 16-byte aligned");
+    if (workspace_bytes < ckr_decode_workspace_bytes(n_elems, dtype, unit_bytes))
+        return fail(CKR_E_CAPACITY, "[ckr] decode workspace too small");
+    if (h_table->cum_freq[256] != CKR_M)
+        return fail(CKR_E_TABLE, "[ckr] table sums to %u, not 4096: stream not decodable", h_table->cum_freq[256]);
+    ckr::TableArg ta;
+    if (!table_arg(h_table, &ta)) return CKR_E_TABLE;
+    hipStream_t s = (hipStream_t)stream;
+    auto* dec = static_cast<uint32_t*>(d_workspace);
+    auto* bad = reinterpret_cast<unsigned long long*>(static_cast<uint8_t*>(d_workspace) + 4096 * 4);
+    CKR_HIP(ckr::launch_build_dec_table(ta, dec, s));
+    CKR_HIP(ckr::launch_set_counter(bad, 0, s));
+    CKR_HIP(ckr::launch_decode(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, static_cast<uint8_t*>(d_dst),
+                               bad, s));
+    if (h_bad_lanes) {
+        unsigned long long nb = 0;
+        CKR_HIP(hipMemcpyAsync(&nb, bad, 8, hipMemcpyDeviceToHost, s));
+        CKR_HIP(hipStreamSynchronize(s));
+        *h_bad_lanes = nb;
+    }
+    return CKR_OK;
+}
+
+// ---- analyzer: per record [p1 nblk][p2 nblk][params][hist partial nblk*256]
+static uint64_t stats_record_bytes(uint32_t nblk) {
+    return align_up(nblk * sizeof(ckr::StatsPartial1), kAlign) + align_up(nblk * sizeof(ckr::StatsPartial2), kAlign) +
+           align_up(sizeof(ckr::StatsParams), kAlign) + align_up((uint64_t)nblk * 256 * 4, kAlign);
+}
+
+uint64_t ckr_analyze_workspace_bytes(const ckr_stats_record* recs, uint64_t n) {
+    uint64_t tot = 0;
+    for (uint64_t i = 0; i < n; i++) tot += stats_record_bytes(ckr::stats_num_blocks(recs[i].num_elements));
+    return tot;
+}
+
+int ckr_analyze(const ckr_stats_record* recs, uint64_t n, void* d_workspace, uint64_t workspace_bytes, void* stream) {
+    if (n && !recs) return fail(CKR_E_INVALID, "[ckr] null records");
+    const uint64_t need = ckr_analyze_workspace_bytes(recs, n);
+    if (need && (!d_workspace || workspace_bytes < need)) return fail(CKR_E_CAPACITY, "[ckr] analyze workspace too small");
+    uint8_t* ws = static_cast<uint8_t*>(d_workspace);
+    hipStream_t s = (hipStream_t)stream;
+    for (uint64_t i = 0; i < n; i++) {
+        const ckr_stats_record& r = recs[i];
+        const uint32_t nblk = ckr::stats_num_blocks(r.num_elements);
+        uint8_t* base = ws;
+        ws += stats_record_bytes(nblk);
+        if (!r.d_ptr || r.num_elements == 0) continue;  // TensorAnalyzer.cpp:68
+        if (!dtype_ok((int)r.data_type)) continue;       // tensor_stats_kernel default branch
+        auto* p1 = reinterpret_cast<ckr::StatsPartial1*>(base);
+        base += align_up(nblk * sizeof(ckr::StatsPartial1), kAlign);
+        auto* p2 = reinterpret_cast<ckr::StatsPartial2*>(base);
+        base += align_up(nblk * sizeof(ckr::StatsPartial2), kAlign);
+        auto* prm = reinterpret_cast<ckr::StatsParams*>(base);
+        base += align_up(sizeof(ckr::StatsParams), kAlign);
+        auto* hp = reinterpret_cast<uint32_t*>(base);
+        CKR_HIP(ckr::launch_stats(r, nblk, p1, p2, prm, hp, s));
+    }
+    return CKR_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,81 @@
+// checkers_amd/csrc/ckr_internal.h — shared between the kernels and the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <string>
+
+#include "checkers_amd.h"
+
+namespace ckr {
+
+// Table passed to kernels by value (1028 B of kernel arguments), so no host
+// buffer has to outlive an asynchronous copy.  norm <= 4096 and cum <= 4096+256
+// for every table normalize_histogram can produce, so 16 bits suffice.
+struct TableArg {
+    uint16_t norm[256];
+    uint16_t cum[257];
+};
+
+// Per-symbol encode entry kept in LDS (16 B).  The division x/f of the
+// reference's state update is replaced by a multiply-high with a per-symbol
+// reciprocal (F. Giesen, "rans_byte.h", public domain, RansEncSymbolInit):
+//   f >= 2: l = ceil(log2 f), rcp = ceil(2^(31+l)/f), rsh = l-1, bias = cum
+//   f == 1: rcp = 2^32-1, rsh = 0, bias = cum + M - 1
+//   q = mulhi(x, rcp) >> rsh == floor(x/f) for every x < 2^31
+//   x' = x + bias + q*(M-f) == ((x/f) << 12) + cum + x%f
+// xmax == 0 marks a symbol with f == 0 (the reference's raw-byte escape).
+struct EncSym {
+    uint32_t rcp;
+    uint32_t bias;
+    uint32_t cmpl_rsh;  // (M - f) | rsh << 16
+    uint32_t xmax;      // 2^19 * f
+};
+
+// Decode slot entry: sym | (f-1) << 8 | cum << 20 (valid tables: f, cum < 4096).
+// ------------------------------------------------------------------ launchers
+// All return hipError_t of the launch; geometry is decided inside.
+hipError_t launch_build_enc_table(const TableArg& t, EncSym* d_enc, hipStream_t s);
+hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, hipStream_t s);
+
+hipError_t launch_extract_mantissa(const uint8_t* src, uint64_t n_elems, int es, int spe,
+                                   uint8_t* masked, uint8_t* sidecar, hipStream_t s);
+
+// Masked histogram into d_hist[256] (overwritten).
+uint32_t hist_num_blocks(uint64_t n_bytes);
+hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int spe, uint32_t* d_hist,
+                              hipStream_t s);
+hipError_t launch_set_u64(uint64_t* p, uint64_t v, hipStream_t s);
+hipError_t launch_set_counter(unsigned long long* p, unsigned long long v, hipStream_t s);
+
+// Encode one batch of units [u0, u0+nb).
+struct EncodeGeom {
+    uint64_t n_bytes;   // masked stream length n_b
+    uint64_t unit;      // unit length U (multiple of 256, or n_b when single)
+    uint64_t n_units;   // total units of the tensor
+    uint32_t wmax;      // dword slots per lane in scratch
+    int es, spe;
+};
+hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t u0, uint64_t nb,
+                               const EncSym* d_enc, uint32_t* scratch,
+                               ckr_stream_header* hdrs, uint8_t* sidecar, uint32_t* unit_size,
+                               uint64_t* unit_off, uint8_t* out, hipStream_t s);
+
+hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
+                         const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar,
+                         uint8_t* dst, unsigned long long* bad, hipStream_t s);
+
+// Analyzer.
+struct StatsParams {     // per record, device resident between passes
+    float smin, smax, mean, scale;
+    uint32_t use_range;  // range > 1e-9f
+    uint32_t bins;
+    uint32_t pad[2];
+};
+struct StatsPartial1 { float mn, mx; double sum; };
+struct StatsPartial2 { double m2, m3, m4, pad; };
+uint32_t stats_num_blocks(uint64_t n);
+hipError_t launch_stats(const ckr_stats_record& r, uint32_t nblk, StatsPartial1* p1,
+                        StatsPartial2* p2, StatsParams* prm, uint32_t* hist_partial,
+                        hipStream_t s);
+
+}  // namespace ckr

@@ -1,0 +1,706 @@
+// checkers_amd/csrc/ckr_kernels.hip — gfx950 kernels of the checkpoint-compression path.
+//
+// Data layout (HBM):
+//   source tensor          n_b bytes, 16-byte aligned, read with 128-bit or 32-bit loads;
+//   masked byte stream     never materialised: the low `spe` bytes of every element
+//                          are zeroed on load (bf16/fp16: byte 0, fp32: bytes 0-1);
+//   sidecar                element-interleaved low bytes, written by the encode pass;
+//   units                  the masked stream cut into `unit` bytes (multiple of 256);
+//                          in a unit, lane t owns bytes t, t+256, … (256 lanes);
+//   thread ↔ lanes         one thread owns the 4 lanes of one 32-bit column
+//                          (lanes 4j..4j+3), so one wave64 owns one unit and each
+//                          row of 256 bytes is a single coalesced 256 B load;
+//   encode scratch         per unit, per lane, 32-bit slots interleaved across lanes
+//                          (slot w of lane t at (w*256 + t)*4) holding the lane's
+//                          output backward from its end, 4 bytes per store;
+//   packed output          unit after unit, lane streams in lane order.
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+#include "ckr_internal.h"
+
+namespace ckr {
+
+static constexpr uint32_t M = 4096u;
+static constexpr uint32_t L = 1u << 23;
+
+// ------------------------------------------------------------------ tables
+// Encode entries from norm/cum (see EncSym in ckr_internal.h for the algebra).
+__global__ void __launch_bounds__(256) build_enc_table_kernel(TableArg t, EncSym* out) {
+    const uint32_t s = threadIdx.x;
+    const uint32_t f = t.norm[s], cum = t.cum[s];
+    EncSym e;
+    if (f == 0) {
+        e.rcp = 0; e.bias = 0; e.cmpl_rsh = 0; e.xmax = 0;
+    } else if (f == 1) {
+        e.rcp = 0xFFFFFFFFu; e.bias = cum + M - 1u; e.cmpl_rsh = (M - 1u); e.xmax = (1u << 19);
+    } else {
+        uint32_t l = 0;
+        while ((1u << l) < f) l++;
+        const uint64_t rcp = ((1ull << (31 + l)) + f - 1) / f;
+        e.rcp = (uint32_t)rcp; e.bias = cum; e.cmpl_rsh = (M - f) | ((l - 1) << 16); e.xmax = f << 19;
+    }
+    out[s] = e;
+}
+
+// Decode slots from norm/cum: slot j in [cum[s], cum[s]+norm[s]) → s.
+__global__ void __launch_bounds__(256) build_dec_table_kernel(TableArg t, uint32_t* out) {
+    const uint32_t s = threadIdx.x;
+    const uint32_t f = t.norm[s], cum = t.cum[s];
+    for (uint32_t j = cum; j < cum + f && j < M; j++) out[j] = s | ((f - 1u) << 8) | (cum << 20);
+}
+
+// ------------------------------------------------------------------ byte-plane split
+template <int SPE>
+__device__ __forceinline__ uint32_t live_mask32() {
+    return SPE == 2 ? 0xFFFF0000u : (SPE == 1 ? 0xFF00FF00u : 0xFFFFFFFFu);
+}
+__device__ __forceinline__ bool byte_live(uint64_t pos, int es, int spe) {
+    return (int)(pos % (uint64_t)es) >= spe;
+}
+
+// 128-bit loads; masked = src & live mask, sidecar gathered per element.
+template <int SPE>
+__global__ void __launch_bounds__(256) extract_mantissa_kernel(const uint8_t* __restrict__ src,
+                                                               uint64_t n_bytes,
+                                                               uint8_t* __restrict__ masked,
+                                                               uint8_t* __restrict__ sidecar) {
+    const uint64_t nvec = n_bytes / 16;
+    const uint32_t lm = live_mask32<SPE>();
+    for (uint64_t v = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; v < nvec;
+         v += (uint64_t)gridDim.x * blockDim.x) {
+        uint4 x = reinterpret_cast<const uint4*>(src)[v];
+        reinterpret_cast<uint4*>(masked)[v] = make_uint4(x.x & lm, x.y & lm, x.z & lm, x.w & lm);
+        if (SPE == 2) {  // 4 fp32 elements → 8 sidecar bytes
+            uint2 sc;
+            sc.x = (x.x & 0xFFFFu) | (x.y << 16);
+            sc.y = (x.z & 0xFFFFu) | (x.w << 16);
+            reinterpret_cast<uint2*>(sidecar)[v] = sc;
+        } else {         // 8 two-byte elements → 8 sidecar bytes (byte 0 of each)
+            uint2 sc;
+            sc.x = (x.x & 0xFFu) | ((x.x >> 8) & 0xFF00u) | ((x.y & 0xFFu) << 16) | ((x.y >> 16) & 0xFFu) << 24;
+            sc.y = (x.z & 0xFFu) | ((x.z >> 8) & 0xFF00u) | ((x.w & 0xFFu) << 16) | ((x.w >> 16) & 0xFFu) << 24;
+            reinterpret_cast<uint2*>(sidecar)[v] = sc;
+        }
+    }
+    // tail bytes (fewer than 16)
+    if (blockIdx.x == 0) {
+        const int es = SPE == 2 ? 4 : 2;
+        for (uint64_t p = nvec * 16 + threadIdx.x; p < n_bytes; p += blockDim.x) {
+            const uint8_t b = src[p];
+            const int plane = (int)(p % es);
+            masked[p] = plane < SPE ? 0 : b;
+            if (plane < SPE) sidecar[(p / es) * SPE + plane] = b;
+        }
+    }
+}
+
+hipError_t launch_extract_mantissa(const uint8_t* src, uint64_t n_elems, int es, int spe,
+                                   uint8_t* masked, uint8_t* sidecar, hipStream_t s) {
+    const uint64_t n_bytes = n_elems * (uint64_t)es;
+    const uint64_t nvec = n_bytes / 16;
+    uint32_t grid = (uint32_t)std::min<uint64_t>((nvec + 255) / 256, 8192);
+    if (grid == 0) grid = 1;
+    if (spe == 2) extract_mantissa_kernel<2><<<grid, 256, 0, s>>>(src, n_bytes, masked, sidecar);
+    else extract_mantissa_kernel<1><<<grid, 256, 0, s>>>(src, n_bytes, masked, sidecar);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ masked histogram
+// 32 bank-interleaved LDS copies (bin b of copy c at b*32 + c, copy = lane & 31),
+// so the ds_add of a wave never hits the same bank twice whatever the data; the
+// zero planes are not counted here (their count, n_elems*spe, is put in bin 0
+// by the init kernel).  Each block adds its 256 sums to the global histogram
+// with integer atomics (order-independent, so the result is deterministic).
+static constexpr uint32_t HIST_COPIES = 32;
+
+template <int SPE>
+__device__ __forceinline__ void hist_add_dword(uint32_t* sh, uint32_t v, uint32_t c) {
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        if (SPE == 2 && b < 2) continue;
+        if (SPE == 1 && (b & 1) == 0) continue;
+        atomicAdd(&sh[((v >> (8 * b)) & 255u) * HIST_COPIES + c], 1u);
+    }
+}
+
+__global__ void __launch_bounds__(256) hist_init_kernel(uint32_t* __restrict__ hist, uint64_t zero_count) {
+    hist[threadIdx.x] = (threadIdx.x == 0) ? (uint32_t)zero_count : 0u;
+}
+
+template <int SPE>
+__global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restrict__ src, uint64_t n_bytes,
+                                                          int es, uint32_t* __restrict__ hist) {
+    __shared__ uint32_t sh[256 * HIST_COPIES];
+    for (uint32_t i = threadIdx.x; i < 256 * HIST_COPIES; i += blockDim.x) sh[i] = 0;
+    __syncthreads();
+    const uint32_t c = threadIdx.x & (HIST_COPIES - 1);
+    const uint64_t nvec = n_bytes / 16;
+    const uint4* v4 = reinterpret_cast<const uint4*>(src);
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    uint64_t v = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; v + 3 * stride < nvec; v += 4 * stride) {  // 4 loads in flight per thread
+        uint4 a = v4[v], b = v4[v + stride], d = v4[v + 2 * stride], e = v4[v + 3 * stride];
+        hist_add_dword<SPE>(sh, a.x, c); hist_add_dword<SPE>(sh, a.y, c);
+        hist_add_dword<SPE>(sh, a.z, c); hist_add_dword<SPE>(sh, a.w, c);
+        hist_add_dword<SPE>(sh, b.x, c); hist_add_dword<SPE>(sh, b.y, c);
+        hist_add_dword<SPE>(sh, b.z, c); hist_add_dword<SPE>(sh, b.w, c);
+        hist_add_dword<SPE>(sh, d.x, c); hist_add_dword<SPE>(sh, d.y, c);
+        hist_add_dword<SPE>(sh, d.z, c); hist_add_dword<SPE>(sh, d.w, c);
+        hist_add_dword<SPE>(sh, e.x, c); hist_add_dword<SPE>(sh, e.y, c);
+        hist_add_dword<SPE>(sh, e.z, c); hist_add_dword<SPE>(sh, e.w, c);
+    }
+    for (; v < nvec; v += stride) {
+        uint4 a = v4[v];
+        hist_add_dword<SPE>(sh, a.x, c); hist_add_dword<SPE>(sh, a.y, c);
+        hist_add_dword<SPE>(sh, a.z, c); hist_add_dword<SPE>(sh, a.w, c);
+    }
+    if (blockIdx.x == 0) {  // tail bytes
+        for (uint64_t p = nvec * 16 + threadIdx.x; p < n_bytes; p += blockDim.x)
+            if ((int)(p % (uint64_t)es) >= SPE) atomicAdd(&sh[(uint32_t)src[p] * HIST_COPIES + c], 1u);
+    }
+    __syncthreads();
+    uint32_t sum = 0;
+    const uint32_t bin = threadIdx.x;
+#pragma unroll 8
+    for (uint32_t k = 0; k < HIST_COPIES; k++) sum += sh[bin * HIST_COPIES + ((k + bin) & (HIST_COPIES - 1))];
+    if (sum) atomicAdd(&hist[bin], sum);
+}
+
+uint32_t hist_num_blocks(uint64_t n_bytes) {
+    const uint64_t nvec = n_bytes / 16;
+    uint64_t nb = (nvec + 1023) / 1024;  // >= 4 vectors per thread
+    if (nb < 1) nb = 1;
+    if (nb > 2048) nb = 2048;
+    return (uint32_t)nb;
+}
+
+hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int spe, uint32_t* d_hist,
+                              hipStream_t s) {
+    const uint64_t zero_count = (es > 0) ? (n_bytes / (uint64_t)es) * (uint64_t)spe : 0;
+    hist_init_kernel<<<1, 256, 0, s>>>(d_hist, zero_count);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (n_bytes == 0) return hipSuccess;
+    const uint32_t nblk = hist_num_blocks(n_bytes);
+    if (spe == 2) masked_hist_kernel<2><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist);
+    else if (spe == 1) masked_hist_kernel<1><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist);
+    else masked_hist_kernel<0><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist);
+    return hipGetLastError();
+}
+
+// Small fills used instead of hipMemsetAsync (safe inside captured graphs).
+__global__ void set_u64_kernel(uint64_t* p, uint64_t v) { *p = v; }
+__global__ void set_u64x_kernel(unsigned long long* p, unsigned long long v) { *p = v; }
+hipError_t launch_set_u64(uint64_t* p, uint64_t v, hipStream_t s) {
+    set_u64_kernel<<<1, 1, 0, s>>>(p, v);
+    return hipGetLastError();
+}
+hipError_t launch_set_counter(unsigned long long* p, unsigned long long v, hipStream_t s) {
+    set_u64x_kernel<<<1, 1, 0, s>>>(p, v);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ rANS encode
+// Lane state: x, 32-bit output accumulator, bytes pending in it, slots flushed.
+struct LaneOut {
+    uint32_t x, acc, nacc, w;
+};
+
+// Emission order equals the reference's backward writes: the first byte emitted
+// is the last byte of the lane's stream.  acc = acc<<8 | b keeps the latest
+// byte lowest, so a full acc stored little-endian holds 4 stream bytes in
+// stream order; slot w (counted from the stream's end) is stored at
+// lane_base + w*1024.
+__device__ __forceinline__ void emit_byte(LaneOut& o, uint32_t b, uint32_t* lane_base) {
+    o.acc = (o.acc << 8) | b;
+    if (++o.nacc == 4) {
+        lane_base[(uint64_t)o.w * 256] = o.acc;
+        o.w++;
+        o.nacc = 0;
+        o.acc = 0;
+    }
+}
+
+// One symbol of rans_encode_kernel's loop body (ANSCompressor.cpp:180-202).
+__device__ __forceinline__ void encode_symbol(LaneOut& o, uint32_t sym, const EncSym* tab, uint32_t* lane_base) {
+    const EncSym e = tab[sym];
+    if (e.xmax == 0) {  // f == 0: raw byte, no state update (:185-192)
+        emit_byte(o, sym, lane_base);
+        return;
+    }
+    if (o.x >= e.xmax) {  // renormalise: at most two bytes since x < 2^32 and xmax >= 2^19
+        emit_byte(o, o.x & 255u, lane_base);
+        o.x >>= 8;
+        if (o.x >= e.xmax) {
+            emit_byte(o, o.x & 255u, lane_base);
+            o.x >>= 8;
+        }
+    }
+    const uint32_t q = __umulhi(o.x, e.rcp) >> (e.cmpl_rsh >> 16);
+    o.x = o.x + e.bias + q * (e.cmpl_rsh & 0xFFFFu);
+}
+
+template <int SPE>
+__device__ __forceinline__ void write_sidecar_row(uint8_t* sidecar, uint64_t pos, uint32_t v, uint32_t nvalid) {
+    // pos = tensor byte offset of this 32-bit column (multiple of 4)
+    if (SPE == 2) {
+        *reinterpret_cast<uint16_t*>(sidecar + (pos >> 1)) = (uint16_t)(v & 0xFFFFu);
+    } else if (SPE == 1) {
+        const uint64_t e0 = pos >> 1;
+        if (nvalid >= 4) *reinterpret_cast<uint16_t*>(sidecar + e0) = (uint16_t)((v & 0xFFu) | ((v >> 8) & 0xFF00u));
+        else sidecar[e0] = (uint8_t)(v & 0xFFu);  // one element left (2 valid bytes)
+    }
+}
+
+// One wave per unit, one thread per 32-bit column (4 lanes).  Rows are taken
+// from the top of the unit down (the reference's reverse order) in groups of
+// 8 rows whose loads are issued together.
+template <int SPE>
+__global__ void __launch_bounds__(256) encode_kernel(const uint8_t* __restrict__ src, EncodeGeom g, uint64_t u0,
+                                                     uint64_t nb, const EncSym* __restrict__ d_enc,
+                                                     uint32_t* __restrict__ scratch,
+                                                     ckr_stream_header* __restrict__ hdrs,
+                                                     uint8_t* __restrict__ sidecar) {
+    __shared__ EncSym tab[256];
+    tab[threadIdx.x] = d_enc[threadIdx.x];
+    __syncthreads();
+
+    const uint32_t j = threadIdx.x & 63;
+    const uint64_t ub = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // unit within batch
+    if (ub >= nb) return;
+    const uint64_t u = u0 + ub;
+    const uint64_t ubase = u * g.unit;
+    const uint64_t len = (g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit;
+    const uint8_t* usrc = src + ubase;
+    uint32_t* uscr = scratch + ub * (uint64_t)g.wmax * 256;
+    const uint32_t lm = live_mask32<SPE>();
+
+    LaneOut o[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) { o[b].x = L; o[b].acc = 0; o[b].nacc = 0; o[b].w = 0; }
+
+    const uint64_t col = 4ull * j;
+    const uint64_t K = (len > col) ? (len - col + 255) / 256 : 0;
+    if (K > 0) {
+        // top row: may be partial
+        const uint64_t k = K - 1;
+        const uint64_t p = 256 * k + col;
+        uint32_t nvalid = (uint32_t)((len - p) < 4 ? (len - p) : 4);
+        uint32_t v = 0;
+        if (nvalid == 4) v = *reinterpret_cast<const uint32_t*>(usrc + p);
+        else for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)usrc[p + b] << (8 * b);
+        if (sidecar && SPE > 0) write_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
+        v &= lm;
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+            if ((uint32_t)b < nvalid) encode_symbol(o[b], (v >> (8 * b)) & 255u, tab, uscr + 4 * j + b);
+        // full rows, 8 at a time
+        int64_t kk = (int64_t)K - 2;
+        for (; kk >= 7; kk -= 8) {
+            uint32_t r[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) r[i] = *reinterpret_cast<const uint32_t*>(usrc + 256 * (uint64_t)(kk - i) + col);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (sidecar && SPE > 0) write_sidecar_row<SPE>(sidecar, ubase + 256 * (uint64_t)(kk - i) + col, r[i], 4);
+                const uint32_t w = r[i] & lm;
+#pragma unroll
+                for (int b = 0; b < 4; b++) encode_symbol(o[b], (w >> (8 * b)) & 255u, tab, uscr + 4 * j + b);
+            }
+        }
+        for (; kk >= 0; kk--) {
+            const uint32_t r = *reinterpret_cast<const uint32_t*>(usrc + 256 * (uint64_t)kk + col);
+            if (sidecar && SPE > 0) write_sidecar_row<SPE>(sidecar, ubase + 256 * (uint64_t)kk + col, r, 4);
+            const uint32_t w = r & lm;
+#pragma unroll
+            for (int b = 0; b < 4; b++) encode_symbol(o[b], (w >> (8 * b)) & 255u, tab, uscr + 4 * j + b);
+        }
+    }
+    // flush partial accumulators and write headers (buf_offset set by the finalize kernel)
+    ckr_stream_header* uh = hdrs + u * 256;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        uint32_t* lb = uscr + 4 * j + b;
+        if (o[b].nacc) lb[(uint64_t)o[b].w * 256] = o[b].acc;
+        ckr_stream_header h;
+        h.final_state = o[b].x;
+        h.byte_count = o[b].w * 4 + o[b].nacc;
+        h.buf_offset = 0;
+        h.pad = 0;
+        uh[4 * j + b] = h;
+    }
+}
+
+// Per unit: lane offsets (exclusive scan of byte_count), unit size, and the
+// passthrough decision (packed size >= unit length ⇒ raw, ANSCompressor.cpp:694-713).
+__global__ void __launch_bounds__(256) unit_finalize_kernel(EncodeGeom g, uint64_t u0,
+                                                            ckr_stream_header* __restrict__ hdrs,
+                                                            uint32_t* __restrict__ unit_size) {
+    __shared__ uint32_t sc[256];
+    const uint64_t u = u0 + blockIdx.x;
+    const uint64_t ubase = u * g.unit;
+    const uint64_t len = (g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit;
+    const uint32_t t = threadIdx.x;
+    ckr_stream_header* uh = hdrs + u * 256;
+    const uint32_t c = uh[t].byte_count;
+    sc[t] = c;
+    __syncthreads();
+    for (uint32_t d = 1; d < 256; d <<= 1) {  // inclusive Hillis-Steele scan
+        uint32_t v = (t >= d) ? sc[t - d] : 0u;
+        __syncthreads();
+        sc[t] += v;
+        __syncthreads();
+    }
+    const uint64_t total = sc[255];
+    const bool raw = total >= len;
+    if (raw) {
+        ckr_stream_header h;
+        h.final_state = 0; h.byte_count = (t == 0) ? (uint32_t)len : 0u; h.buf_offset = 0; h.pad = 0;
+        uh[t] = h;
+    } else {
+        uh[t].buf_offset = sc[t] - c;
+    }
+    if (t == 0) unit_size[blockIdx.x] = raw ? (uint32_t)len : (uint32_t)total;
+}
+
+// Exclusive scan of unit sizes into unit_off[u0 .. u0+nb] (64-bit), continuing
+// from unit_off[u0] written by the previous batch (0 for the first).
+__global__ void __launch_bounds__(1024) unit_scan_kernel(const uint32_t* __restrict__ unit_size, uint64_t u0,
+                                                         uint64_t nb, uint64_t* __restrict__ unit_off) {
+    __shared__ uint64_t sh[1024];
+    const uint32_t t = threadIdx.x;
+    const uint64_t base = (u0 == 0) ? 0ull : unit_off[u0];  // read before any thread writes
+    const uint64_t seg = (nb + 1023) / 1024;
+    const uint64_t b0 = t * seg, b1 = (b0 + seg < nb) ? b0 + seg : nb;
+    uint64_t s = 0;
+    for (uint64_t i = b0; i < b1; i++) s += unit_size[i];
+    sh[t] = s;
+    __syncthreads();
+    for (uint32_t d = 1; d < 1024; d <<= 1) {
+        uint64_t v = (t >= d) ? sh[t - d] : 0ull;
+        __syncthreads();
+        sh[t] += v;
+        __syncthreads();
+    }
+    uint64_t run = base + sh[t] - s;
+    for (uint64_t i = b0; i < b1; i++) { unit_off[u0 + i] = run; run += unit_size[i]; }
+    if (t == 1023) unit_off[u0 + nb] = base + sh[1023];
+}
+
+// Copy every lane stream of a unit to its packed place, or the masked bytes of a
+// raw unit.  One block per unit; wave v copies lanes v, v+4, …
+template <int SPE>
+__global__ void __launch_bounds__(256) compact_kernel(const uint8_t* __restrict__ src, EncodeGeom g, uint64_t u0,
+                                                      const uint32_t* __restrict__ scratch,
+                                                      const ckr_stream_header* __restrict__ hdrs,
+                                                      const uint32_t* __restrict__ unit_size,
+                                                      const uint64_t* __restrict__ unit_off,
+                                                      uint8_t* __restrict__ out) {
+    const uint64_t ub = blockIdx.x;
+    const uint64_t u = u0 + ub;
+    const uint64_t ubase = u * g.unit;
+    const uint64_t len = (g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit;
+    uint8_t* dst = out + unit_off[u];
+    const ckr_stream_header* uh = hdrs + u * 256;
+    const bool raw = (uint64_t)unit_size[ub] == len && uh[0].byte_count == (uint32_t)len && uh[0].final_state == 0;
+    if (raw) {
+        for (uint64_t p = threadIdx.x; p < len; p += 256) {
+            const uint8_t b = src[ubase + p];
+            dst[p] = byte_live(p, g.es, g.spe) ? b : 0;
+        }
+        return;
+    }
+    const uint8_t* uscr = reinterpret_cast<const uint8_t*>(scratch + ub * (uint64_t)g.wmax * 256);
+    const uint32_t wv = threadIdx.x >> 6, li = threadIdx.x & 63;
+    for (uint32_t l = wv; l < 256; l += 4) {
+        const ckr_stream_header h = uh[l];
+        const uint32_t B = h.byte_count, W = B >> 2, r = B & 3;
+        uint8_t* d = dst + h.buf_offset;
+        for (uint32_t q = li; q < B; q += 64) {
+            uint32_t slot, byte;
+            if (q < r) { slot = W; byte = q; }
+            else { const uint32_t q2 = q - r; slot = W - 1 - (q2 >> 2); byte = q2 & 3; }
+            d[q] = uscr[((uint64_t)slot * 256 + l) * 4 + byte];
+        }
+    }
+}
+
+hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t u0, uint64_t nb,
+                               const EncSym* d_enc, uint32_t* scratch, ckr_stream_header* hdrs,
+                               uint8_t* sidecar, uint32_t* unit_size, uint64_t* unit_off, uint8_t* out,
+                               hipStream_t s) {
+    const uint32_t grid = (uint32_t)((nb + 3) / 4);
+    if (g.spe == 2) encode_kernel<2><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, scratch, hdrs, sidecar);
+    else if (g.spe == 1) encode_kernel<1><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, scratch, hdrs, sidecar);
+    else encode_kernel<0><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, scratch, hdrs, nullptr);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    unit_finalize_kernel<<<(uint32_t)nb, 256, 0, s>>>(g, u0, hdrs, unit_size);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    unit_scan_kernel<<<1, 1024, 0, s>>>(unit_size, u0, nb, unit_off);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if (g.spe == 2) compact_kernel<2><<<(uint32_t)nb, 256, 0, s>>>(src, g, u0, scratch, hdrs, unit_size, unit_off, out);
+    else if (g.spe == 1) compact_kernel<1><<<(uint32_t)nb, 256, 0, s>>>(src, g, u0, scratch, hdrs, unit_size, unit_off, out);
+    else compact_kernel<0><<<(uint32_t)nb, 256, 0, s>>>(src, g, u0, scratch, hdrs, unit_size, unit_off, out);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ rANS decode
+struct LaneIn {
+    uint32_t x;
+    const uint8_t* p;
+    const uint8_t* end;
+};
+
+__device__ __forceinline__ uint32_t decode_symbol(LaneIn& in, const uint32_t* tab) {
+    const uint32_t slot = in.x & (M - 1u);
+    const uint32_t e = tab[slot];
+    const uint32_t f = ((e >> 8) & 4095u) + 1u, cum = e >> 20;
+    in.x = f * (in.x >> 12) + slot - cum;
+    while (in.x < L && in.p < in.end) in.x = (in.x << 8) | *in.p++;
+    return e & 255u;
+}
+
+template <int SPE>
+__device__ __forceinline__ uint32_t merge_sidecar_row(const uint8_t* sidecar, uint64_t pos, uint32_t dec, uint32_t nvalid) {
+    if (SPE == 2) return dec | *reinterpret_cast<const uint16_t*>(sidecar + (pos >> 1));
+    if (SPE == 1) {
+        const uint64_t e0 = pos >> 1;
+        if (nvalid >= 4) {
+            const uint32_t s = *reinterpret_cast<const uint16_t*>(sidecar + e0);
+            return dec | (s & 0xFFu) | ((s & 0xFF00u) << 8);
+        }
+        return dec | sidecar[e0];
+    }
+    return dec;
+}
+
+template <int SPE>
+__global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__ data,
+                                                     const ckr_stream_header* __restrict__ hdrs,
+                                                     const uint64_t* __restrict__ unit_off,
+                                                     const uint32_t* __restrict__ d_dec, EncodeGeom g,
+                                                     const uint8_t* __restrict__ sidecar,
+                                                     uint8_t* __restrict__ dst, unsigned long long* bad) {
+    __shared__ uint32_t tab[4096];
+    for (uint32_t i = threadIdx.x; i < 4096; i += 256) tab[i] = d_dec[i];
+    __syncthreads();
+    const uint32_t j = threadIdx.x & 63;
+    const uint64_t u = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= g.n_units) return;
+    const uint64_t ubase = u * g.unit;
+    const uint64_t len = (g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit;
+    const uint8_t* ud = data + unit_off[u];
+    const uint64_t usize = unit_off[u + 1] - unit_off[u];
+    const ckr_stream_header* uh = hdrs + u * 256;
+    const uint64_t col = 4ull * j;
+    uint8_t* udst = dst + ubase;
+    if (usize == len && uh[0].byte_count == (uint32_t)len) {  // raw unit: masked bytes | sidecar
+        for (uint64_t p = col; p < len; p += 256) {
+            const uint32_t nvalid = (uint32_t)((len - p) < 4 ? (len - p) : 4);
+            uint32_t v = 0;
+            for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)ud[p + b] << (8 * b);
+            if (SPE > 0) v = merge_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
+            for (uint32_t b = 0; b < nvalid; b++) udst[p + b] = (uint8_t)(v >> (8 * b));
+        }
+        return;
+    }
+    LaneIn in[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const ckr_stream_header h = uh[4 * j + b];
+        in[b].x = h.final_state;
+        in[b].p = ud + h.buf_offset;
+        in[b].end = in[b].p + h.byte_count;
+    }
+    const uint64_t K = (len > col) ? (len - col + 255) / 256 : 0;
+    for (uint64_t k = 0; k < K; k++) {
+        const uint64_t p = 256 * k + col;
+        const uint32_t nvalid = (uint32_t)((len - p) < 4 ? (len - p) : 4);
+        uint32_t v = 0;
+        if (nvalid == 4) {
+#pragma unroll
+            for (int b = 0; b < 4; b++) v |= decode_symbol(in[b], tab) << (8 * b);
+            if (SPE > 0) v = merge_sidecar_row<SPE>(sidecar, ubase + p, v, 4);
+            *reinterpret_cast<uint32_t*>(udst + p) = v;
+        } else {
+            for (uint32_t b = 0; b < nvalid; b++) v |= decode_symbol(in[b], tab) << (8 * b);
+            if (SPE > 0) v = merge_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
+            for (uint32_t b = 0; b < nvalid; b++) udst[p + b] = (uint8_t)(v >> (8 * b));
+        }
+    }
+    uint32_t nbad = 0;
+#pragma unroll
+    for (int b = 0; b < 4; b++) nbad += (in[b].x != L || in[b].p != in[b].end) ? 1u : 0u;
+    if (nbad) atomicAdd(bad, (unsigned long long)nbad);
+}
+
+hipError_t launch_build_enc_table(const TableArg& t, EncSym* d_enc, hipStream_t s) {
+    build_enc_table_kernel<<<1, 256, 0, s>>>(t, d_enc);
+    return hipGetLastError();
+}
+hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, hipStream_t s) {
+    build_dec_table_kernel<<<1, 256, 0, s>>>(t, d_dec);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
+                         const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
+                         unsigned long long* bad, hipStream_t s) {
+    const uint32_t grid = (uint32_t)((g.n_units + 3) / 4);
+    if (grid == 0) return hipSuccess;
+    if (g.spe == 2) decode_kernel<2><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad);
+    else if (g.spe == 1) decode_kernel<1><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad);
+    else decode_kernel<0><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ analyzer
+// compute_tensor_stats<T> (TensorAnalyzer.cpp:64-198) spread over many blocks.
+// min/max are exact whatever the order; the histogram is bit-exact given them
+// (scale rounded once from an fp64 quotient: double rounding of a float/float
+// quotient through fp64 is innocuous since 53 >= 2*24+2); sums are fp64.
+__device__ __forceinline__ float elem_as_float(const void* p, uint64_t i, uint32_t dt) {
+    switch (dt) {
+        case CKR_F32: return reinterpret_cast<const float*>(p)[i];
+        case CKR_BF16: return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16);
+        case CKR_F16: return (float)reinterpret_cast<const _Float16*>(p)[i];
+        case CKR_I8: return (float)reinterpret_cast<const int8_t*>(p)[i];
+        case CKR_I32: return (float)reinterpret_cast<const int32_t*>(p)[i];
+        default: return 0.f;
+    }
+}
+
+__global__ void __launch_bounds__(256) stats_pass1_kernel(const void* __restrict__ p, uint64_t n, uint32_t dt,
+                                                          StatsPartial1* __restrict__ out) {
+    __shared__ float smn[256], smx[256];
+    __shared__ double ssm[256];
+    float mn = 1e37f, mx = -1e37f;
+    double sm = 0.0;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
+        const float x = elem_as_float(p, i, dt);
+        mn = fminf(mn, x);
+        mx = fmaxf(mx, x);
+        sm += (double)x;
+    }
+    smn[threadIdx.x] = mn; smx[threadIdx.x] = mx; ssm[threadIdx.x] = sm;
+    __syncthreads();
+    for (uint32_t s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            smn[threadIdx.x] = fminf(smn[threadIdx.x], smn[threadIdx.x + s]);
+            smx[threadIdx.x] = fmaxf(smx[threadIdx.x], smx[threadIdx.x + s]);
+            ssm[threadIdx.x] += ssm[threadIdx.x + s];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) { out[blockIdx.x].mn = smn[0]; out[blockIdx.x].mx = smx[0]; out[blockIdx.x].sum = ssm[0]; }
+}
+
+__global__ void stats_mid_kernel(const StatsPartial1* __restrict__ p1, uint32_t nblk, uint64_t n, uint32_t bins_in,
+                                 StatsParams* __restrict__ prm) {
+    if (threadIdx.x != 0) return;
+    float mn = 1e37f, mx = -1e37f;
+    double sm = 0.0;
+    for (uint32_t b = 0; b < nblk; b++) { mn = fminf(mn, p1[b].mn); mx = fmaxf(mx, p1[b].mx); sm += p1[b].sum; }
+    const uint32_t bins = bins_in < 256u ? bins_in : 256u;
+    const float range = mx - mn;
+    StatsParams q;
+    q.smin = mn; q.smax = mx;
+    q.mean = (float)(sm / (double)n);
+    q.use_range = range > 1e-9f ? 1u : 0u;
+    q.scale = q.use_range ? (float)((double)((float)bins - 1.0f) / (double)range) : 0.0f;
+    q.bins = bins; q.pad[0] = q.pad[1] = 0;
+    *prm = q;
+}
+
+__global__ void __launch_bounds__(256) stats_pass2_kernel(const void* __restrict__ p, uint64_t n, uint32_t dt,
+                                                          const StatsParams* __restrict__ prm,
+                                                          StatsPartial2* __restrict__ out,
+                                                          uint32_t* __restrict__ hist_partial) {
+    __shared__ uint32_t sh[256 * 8];
+    __shared__ double r2[256], r3[256], r4[256];
+    for (uint32_t i = threadIdx.x; i < 256 * 8; i += 256) sh[i] = 0;
+    __syncthreads();
+    const StatsParams q = *prm;
+    const uint32_t c = threadIdx.x & 7;
+    double a2 = 0, a3 = 0, a4 = 0;
+    const double mean = (double)q.mean;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
+        const float x = elem_as_float(p, i, dt);
+        if (q.bins > 0) {
+            int b = 0;
+            if (q.use_range) {
+                const float t = __fmul_rn(__fsub_rn(x, q.smin), q.scale);
+                b = (t != t) ? 0 : (int)fminf(fmaxf(t, -2147483648.0f), 2147483520.0f);
+                b = max(0, min(b, (int)q.bins - 1));
+            }
+            atomicAdd(&sh[b * 8 + c], 1u);
+        }
+        const double d = (double)x - mean, d2 = d * d;
+        a2 += d2; a3 += d2 * d; a4 += d2 * d2;
+    }
+    r2[threadIdx.x] = a2; r3[threadIdx.x] = a3; r4[threadIdx.x] = a4;
+    __syncthreads();
+    for (uint32_t s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s) { r2[threadIdx.x] += r2[threadIdx.x + s]; r3[threadIdx.x] += r3[threadIdx.x + s]; r4[threadIdx.x] += r4[threadIdx.x + s]; }
+        __syncthreads();
+    }
+    uint32_t hs = 0;
+    for (uint32_t k = 0; k < 8; k++) hs += sh[threadIdx.x * 8 + k];
+    hist_partial[(uint64_t)blockIdx.x * 256 + threadIdx.x] = hs;
+    if (threadIdx.x == 0) { out[blockIdx.x].m2 = r2[0]; out[blockIdx.x].m3 = r3[0]; out[blockIdx.x].m4 = r4[0]; out[blockIdx.x].pad = 0; }
+}
+
+__global__ void __launch_bounds__(256) stats_final_kernel(const StatsPartial2* __restrict__ p2,
+                                                          const uint32_t* __restrict__ hist_partial, uint32_t nblk,
+                                                          uint64_t n, const StatsParams* __restrict__ prm,
+                                                          ckr_stats_record r) {
+    const StatsParams q = *prm;
+    const uint32_t t = threadIdx.x;
+    if (t < q.bins && r.d_histogram) {
+        uint32_t s = 0;
+        for (uint32_t b = 0; b < nblk; b++) s += hist_partial[(uint64_t)b * 256 + t];
+        r.d_histogram[t] = s;
+    }
+    if (t == 0) {
+        double m2 = 0, m3 = 0, m4 = 0;
+        for (uint32_t b = 0; b < nblk; b++) { m2 += p2[b].m2; m3 += p2[b].m3; m4 += p2[b].m4; }
+        const float M2 = (float)(m2 / (double)n), M3 = (float)(m3 / (double)n), M4 = (float)(m4 / (double)n);
+        const float var = M2;
+        float skew = 0.f, kurt = 0.f;
+        if (var > 1e-9f) {
+            const float sd = sqrtf(var);
+            skew = M3 / (var * sd);
+            kurt = M4 / (var * var);
+        }
+        if (r.d_raw_moments) { r.d_raw_moments[0] = q.mean; r.d_raw_moments[1] = var; r.d_raw_moments[2] = skew; r.d_raw_moments[3] = kurt; }
+        if (r.d_minmax) { r.d_minmax[0] = q.smin; r.d_minmax[1] = q.smax; }
+        if (r.d_fingerprint) {  // TensorAnalyzer.cpp:281-290
+            r.d_fingerprint[0] = q.mean; r.d_fingerprint[1] = var; r.d_fingerprint[2] = skew;
+            r.d_fingerprint[3] = kurt; r.d_fingerprint[4] = q.smax - q.smin;
+        }
+    }
+}
+
+uint32_t stats_num_blocks(uint64_t n) {
+    uint64_t nb = (n + 4095) / 4096;
+    if (nb < 1) nb = 1;
+    if (nb > 2048) nb = 2048;
+    return (uint32_t)nb;
+}
+
+hipError_t launch_stats(const ckr_stats_record& r, uint32_t nblk, StatsPartial1* p1, StatsPartial2* p2,
+                        StatsParams* prm, uint32_t* hist_partial, hipStream_t s) {
+    stats_pass1_kernel<<<nblk, 256, 0, s>>>(r.d_ptr, r.num_elements, r.data_type, p1);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    stats_mid_kernel<<<1, 64, 0, s>>>(p1, nblk, r.num_elements, r.histogram_bins, prm);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    stats_pass2_kernel<<<nblk, 256, 0, s>>>(r.d_ptr, r.num_elements, r.data_type, prm, p2, hist_partial);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    stats_final_kernel<<<1, 256, 0, s>>>(p2, hist_partial, nblk, r.num_elements, prm, r);
+    return hipGetLastError();
+}
+
+}  // namespace ckr

@@ -1,0 +1,187 @@
+/*
+ * checkers_amd.h — C ABI of the MI355X (gfx950) checkpoint-compression hot path.
+ *
+ * Every entry point takes plain pointers and sizes, returns an int status
+ * (CKR_OK == 0, negative on error) and never throws; the message of the last
+ * error on the calling thread is available from ckr_last_error().  Device
+ * pointers ("d_" prefix) must be HIP device allocations on the current device;
+ * host pointers ("h_" prefix) are ordinary host memory.  `stream` is a
+ * hipStream_t passed as void* so that this header needs no HIP include.
+ *
+ * Reference interfaces replaced (paths relative to the reference tree):
+ *   - ckr_extract_mantissa   ← extract_mantissa_kernel / ANSCompressor::extract_mantissa
+ *                              (src/ANSCompressor.cpp:258-279, :945-1009)
+ *   - ckr_byte_histogram     ← byte_histogram_kernel on the masked buffer
+ *                              (src/ANSCompressor.cpp:109-126, launch :1225-1236)
+ *   - ckr_byte_histogram_raw ← ANSCompressor::build_byte_histogram (src/ANSCompressor.cpp:393-411)
+ *   - ckr_build_table        ← ANSCompressor::normalize_histogram (src/ANSCompressor.cpp:416-503)
+ *   - ckr_encode             ← rans_encode_kernel + compact_streams_kernel + the host prefix
+ *                              sum and passthrough fallback of ANSCompressor::compress_tensor
+ *                              (src/ANSCompressor.cpp:154-211, :225-238, :509-718)
+ *   - ckr_decode             ← no counterpart: the reference has no decoder; this is the
+ *                              inverse of rans_encode_kernel plus the sidecar merge
+ *                              (include/checkers/ANSCompressor.hpp:165-171)
+ *   - ckr_analyze            ← tensor_stats_kernel / compute_tensor_stats<T>
+ *                              (src/TensorAnalyzer.cpp:64-229, launch :294-320)
+ *   - ckr_fingerprints       ← TensorAnalyzer::compute_fingerprints (src/TensorAnalyzer.cpp:271-292)
+ */
+#ifndef CHECKERS_AMD_H
+#define CHECKERS_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CKR_API __attribute__((visibility("default")))
+
+/* ---- status codes ---- */
+#define CKR_OK             0
+#define CKR_E_INVALID    (-1)  /* bad argument (null pointer, size, dtype, unit) */
+#define CKR_E_HIP        (-2)  /* a HIP runtime call failed                     */
+#define CKR_E_CAPACITY   (-3)  /* caller-provided buffer too small              */
+#define CKR_E_TABLE      (-4)  /* frequency table unusable for the operation    */
+#define CKR_E_CORRUPT    (-5)  /* compressed stream failed a decode check       */
+
+/* ---- dtype tags: include/checkers/TensorResource.hpp:30-37 ---- */
+#define CKR_F32      0
+#define CKR_BF16     1
+#define CKR_F16      2
+#define CKR_I8       3
+#define CKR_I32      4
+#define CKR_UNKNOWN  255
+
+/* rANS constants: include/checkers/ANSCompressor.hpp:51-55 */
+#define CKR_SCALE_BITS 12u
+#define CKR_M          4096u
+#define CKR_L          (1u << 23)
+#define CKR_NORM_BASE  (1u << 19)
+#define CKR_LANES      256u
+
+/* Per-lane stream header: include/checkers/ANSCompressor.hpp:79-84 (16 bytes).
+ * After ckr_encode, buf_offset is the lane's byte offset inside its chunk's
+ * data (for a single-chunk tensor: inside the tensor's data, exactly as the
+ * reference's compacted headers, src/ANSCompressor.cpp:685-691). */
+typedef struct ckr_stream_header {
+    uint32_t final_state;
+    uint32_t byte_count;
+    uint32_t buf_offset;
+    uint32_t pad;
+} ckr_stream_header;
+
+/* Frequency table: include/checkers/ANSCompressor.hpp:64-74 (alignas(64), 40000 bytes). */
+typedef struct __attribute__((aligned(64))) ckr_freq_table {
+    uint32_t norm_freq[256];
+    uint32_t cum_freq[257];
+    uint32_t x_max[256];
+    uint8_t  decode_sym[4096];
+    uint32_t decode_freq[4096];
+    uint32_t decode_cum[4096];
+} ckr_freq_table;
+
+/* Per-tensor analysis output (the three slab buffers of a DeviceTensorRecord,
+ * include/checkers/MemoryManager.hpp:60-72; all device pointers, any may be NULL). */
+typedef struct ckr_stats_record {
+    const void* d_ptr;          /* tensor data                                  */
+    uint64_t    num_elements;
+    uint32_t    histogram_bins; /* clamped to 256 as in TensorAnalyzer.cpp:73    */
+    uint32_t    data_type;      /* CKR_* tag                                    */
+    uint32_t*   d_histogram;    /* [min(bins,256)] u32                          */
+    float*      d_raw_moments;  /* [4] mean, var, skew, kurt                     */
+    float*      d_minmax;       /* [2] min, max                                  */
+    float*      d_fingerprint;  /* [5] mean, var, skew, kurt, max-min (or NULL)  */
+} ckr_stats_record;
+
+/* ---- library ---- */
+CKR_API const char* ckr_last_error(void);
+CKR_API const char* ckr_version(void);
+/* Element size of a dtype tag (TensorResource.hpp:39-48); 0 for unknown tags. */
+CKR_API int ckr_element_size(int dtype);
+/* Low bytes moved to the sidecar per element (ANSCompressor.cpp:955-967): bf16/fp16 1, fp32 2, else 0. */
+CKR_API int ckr_sidecar_bytes_per_elem(int dtype);
+
+/* ---- byte-plane split (masked copy + element-interleaved sidecar) ---- */
+CKR_API int ckr_extract_mantissa(const void* d_src, uint64_t n_elems, int dtype,
+                                 void* d_masked, void* d_sidecar, void* stream);
+
+/* ---- byte histogram of the masked byte stream, masking fused into the load.
+ * d_hist[256] is overwritten (not accumulated).  For dtypes without a sidecar
+ * the histogram is that of the raw bytes. ---- */
+CKR_API int ckr_byte_histogram(const void* d_src, uint64_t n_elems, int dtype,
+                               uint32_t* d_hist, void* stream);
+/* Histogram of an arbitrary byte buffer (d_hist overwritten). */
+CKR_API int ckr_byte_histogram_raw(const void* d_bytes, uint64_t n_bytes,
+                                   uint32_t* d_hist, void* stream);
+
+/* ---- host: histogram → table, same arithmetic and std::sort tie order as the
+ * reference.  Returns CKR_OK; *h_table_sum receives sum(norm_freq) (4096 for a
+ * valid table; larger in the reference's full-alphabet defect case, in which
+ * the decode arrays are filled only up to slot 4095). ---- */
+CKR_API int ckr_build_table(const uint32_t* h_hist, int ensure_full_alphabet,
+                            ckr_freq_table* h_table, uint32_t* h_table_sum);
+
+/* ---- chunked rANS encode ----
+ * The masked byte stream of the tensor (n_b = n_elems * element_size bytes) is
+ * cut into units of `unit_bytes` (a multiple of 256; unit_bytes >= n_b or 0
+ * means one unit = the whole tensor, the reference layout).  Every unit is
+ * coded exactly as rans_encode_kernel codes a whole tensor: 256 interleaved
+ * lanes, each lane in reverse order, 12-bit table, byte renormalisation; the
+ * lane streams are packed in lane order; a unit whose packed size is >= its
+ * length is stored raw (the masked bytes; header 0 byte_count = length, all
+ * other headers zero), the reference's passthrough rule applied per unit.
+ * Outputs:
+ *   d_out              packed data of all units, unit after unit;
+ *   d_headers          n_units * 256 headers;
+ *   d_unit_offsets     n_units + 1 u64: start of each unit's data in d_out,
+ *                      the last entry is the total compressed size C;
+ *   d_sidecar          sidecar bytes (n_elems * sidecar_bytes_per_elem) or NULL.
+ * The table is given on the host.  The workspace must hold
+ * ckr_encode_workspace_bytes(...) bytes; d_out must hold
+ * ckr_encode_max_output_bytes(...) bytes.  If h_total_out is not NULL the
+ * call synchronises `stream` and stores C there. ---- */
+CKR_API uint64_t ckr_num_units(uint64_t n_elems, int dtype, uint64_t unit_bytes);
+CKR_API uint64_t ckr_encode_max_output_bytes(uint64_t n_elems, int dtype, uint64_t unit_bytes);
+CKR_API uint64_t ckr_encode_workspace_bytes(uint64_t n_elems, int dtype, uint64_t unit_bytes);
+CKR_API int ckr_encode(const void* d_src, uint64_t n_elems, int dtype,
+                       const ckr_freq_table* h_table, uint64_t unit_bytes,
+                       uint8_t* d_out, uint64_t out_capacity,
+                       ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
+                       uint8_t* d_sidecar,
+                       void* d_workspace, uint64_t workspace_bytes,
+                       uint64_t* h_total_out, void* stream);
+
+/* ---- full tensor compression as ANSCompressor::compress_tensor does it for a
+ * singleton (histogram → host table → encode), in one call.  The table built
+ * is returned in h_table (may be NULL). ---- */
+CKR_API int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_bytes,
+                         int ensure_full_alphabet,
+                         uint8_t* d_out, uint64_t out_capacity,
+                         ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
+                         uint8_t* d_sidecar,
+                         void* d_workspace, uint64_t workspace_bytes,
+                         ckr_freq_table* h_table, uint64_t* h_total_out, void* stream);
+
+/* ---- decode: inverse of ckr_encode, sidecar merged back (original bits).
+ * d_sidecar may be NULL only for dtypes without a sidecar.  The table must sum
+ * to 4096.  Stream checks (every lane ends in state 2^23 having consumed
+ * exactly byte_count bytes) are accumulated on the device; if h_bad_lanes is
+ * not NULL the call synchronises and stores the number of failing lanes. ---- */
+CKR_API uint64_t ckr_decode_workspace_bytes(uint64_t n_elems, int dtype, uint64_t unit_bytes);
+CKR_API int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers,
+                       const uint64_t* d_unit_offsets,
+                       const ckr_freq_table* h_table, uint64_t n_elems, int dtype,
+                       uint64_t unit_bytes, const uint8_t* d_sidecar, void* d_dst,
+                       void* d_workspace, uint64_t workspace_bytes,
+                       uint64_t* h_bad_lanes, void* stream);
+
+/* ---- TensorAnalyzer statistics pass over n records ---- */
+CKR_API uint64_t ckr_analyze_workspace_bytes(const ckr_stats_record* h_records, uint64_t n);
+CKR_API int ckr_analyze(const ckr_stats_record* h_records, uint64_t n,
+                        void* d_workspace, uint64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CHECKERS_AMD_H */

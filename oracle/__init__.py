@@ -1,0 +1,151 @@
+"""CPU oracle of the checkpoint-compression hot path — TEST INFRASTRUCTURE ONLY.
+
+ctypes view of oracle/libckr_oracle.so (a C++ restatement of the reference's
+code, see ckr_oracle.cpp for the file:line each function follows).  Only
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, and
+only as the checker or the timed CPU baseline; the product never imports it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libckr_oracle.so")
+
+HEADER_DTYPE = np.dtype([("final_state", "<u4"), ("byte_count", "<u4"), ("buf_offset", "<u4"), ("pad", "<u4")])
+TABLE_DTYPE = np.dtype([("norm_freq", "<u4", 256), ("cum_freq", "<u4", 257), ("x_max", "<u4", 256),
+                        ("decode_sym", "u1", 4096), ("decode_freq", "<u4", 4096), ("decode_cum", "<u4", 4096),
+                        ("_pad", "u1", 60)])
+assert TABLE_DTYPE.itemsize == 40000
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE, "libckr_oracle.so"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        vp, u64, i32, u32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_int, ctypes.c_uint32
+        sig = {
+            "oc_element_size": (i32, [i32]),
+            "oc_sidecar_per_elem": (i32, [i32]),
+            "oc_extract_mantissa": (i32, [vp, u64, i32, vp, vp]),
+            "oc_byte_hist": (None, [vp, u64, vp]),
+            "oc_normalize_histogram": (u32, [vp, i32, vp]),
+            "oc_num_units": (u64, [u64, u64]),
+            "oc_encode": (u64, [vp, u64, vp, u64, vp, vp, vp, i32]),
+            "oc_decode": (u64, [vp, vp, vp, vp, u64, u64, vp]),
+            "oc_merge_sidecar": (None, [vp, vp, u64, i32, vp]),
+            "oc_tensor_stats": (None, [vp, u64, i32, u32, vp, vp, vp, vp]),
+        }
+        for k, (r, a) in sig.items():
+            f = getattr(L, k)
+            f.restype = r
+            f.argtypes = a
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data
+
+
+ES = {0: 4, 1: 2, 2: 2, 3: 1, 4: 4}
+SPE = {0: 2, 1: 1, 2: 1, 3: 0, 4: 0}
+
+
+def as_bytes(arr):
+    return np.ascontiguousarray(arr).view(np.uint8).reshape(-1)
+
+
+def extract_mantissa(raw, n, dtype):
+    """(masked bytes, sidecar bytes) of n elements given as raw bytes."""
+    es, spe = ES[dtype], SPE[dtype]
+    raw = as_bytes(raw)
+    masked = np.empty(n * es, np.uint8)
+    side = np.empty(max(n * spe, 1), np.uint8)
+    got = lib().oc_extract_mantissa(_p(raw), n, dtype, _p(masked), _p(side))
+    if got == 0:
+        return raw[: n * es].copy(), np.empty(0, np.uint8)
+    return masked, side[: n * spe]
+
+
+def byte_hist(data):
+    data = as_bytes(data)
+    h = np.zeros(256, np.uint32)
+    lib().oc_byte_hist(_p(data), data.size, _p(h))
+    return h
+
+
+def normalize_histogram(hist, ensure_full_alphabet=False):
+    """Returns (table record of TABLE_DTYPE, table sum)."""
+    h = np.ascontiguousarray(np.asarray(hist, np.uint32))
+    t = np.zeros(1, TABLE_DTYPE)
+    s = lib().oc_normalize_histogram(_p(h), int(bool(ensure_full_alphabet)), _p(t))
+    return t[0], int(s)
+
+
+def num_units(n_b, unit):
+    return int(lib().oc_num_units(n_b, unit))
+
+
+def encode(masked, table, unit, n_threads=1):
+    """Chunked encode of a masked byte stream: (data, headers, unit_offsets)."""
+    masked = as_bytes(masked)
+    nb = masked.size
+    nu = num_units(nb, unit)
+    t = np.zeros(1, TABLE_DTYPE)
+    t[0] = table
+    out = np.zeros(max(nb, 1), np.uint8)
+    hdr = np.zeros(max(nu, 1) * 256, HEADER_DTYPE)
+    off = np.zeros(nu + 1, np.uint64)
+    total = lib().oc_encode(_p(masked), nb, _p(t), unit, _p(out), _p(hdr), _p(off), n_threads)
+    return out[:total], hdr[: nu * 256], off
+
+
+def decode(data, headers, unit_offsets, table, n_b, unit):
+    """(masked bytes, bad lane count)."""
+    t = np.zeros(1, TABLE_DTYPE)
+    t[0] = table
+    data = np.ascontiguousarray(data, np.uint8) if data.size else np.zeros(1, np.uint8)
+    headers = np.ascontiguousarray(headers)
+    off = np.ascontiguousarray(unit_offsets, np.uint64)
+    out = np.zeros(max(n_b, 1), np.uint8)
+    bad = lib().oc_decode(_p(data), _p(headers), _p(off), _p(t), n_b, unit, _p(out))
+    return out[:n_b], int(bad)
+
+
+def merge_sidecar(masked, sidecar, n, dtype):
+    out = np.empty(n * ES[dtype], np.uint8)
+    masked = as_bytes(masked)
+    sidecar = as_bytes(sidecar) if sidecar.size else np.zeros(1, np.uint8)
+    lib().oc_merge_sidecar(_p(masked), _p(sidecar), n, dtype, _p(out))
+    return out
+
+
+def tensor_stats(raw, n, dtype, bins=256):
+    """Reference-order fp32 statistics + fp64 values: dict(histogram, moments, minmax, moments64)."""
+    raw = as_bytes(raw) if n else np.zeros(4, np.uint8)
+    nb = min(bins, 256)
+    h = np.zeros(max(nb, 1), np.uint32)
+    mom = np.zeros(4, np.float32)
+    mm = np.zeros(2, np.float32)
+    m64 = np.zeros(4, np.float64)
+    lib().oc_tensor_stats(_p(raw), n, dtype, bins, _p(h), _p(mom), _p(mm), _p(m64))
+    return dict(histogram=h[:nb], moments=mom, minmax=mm, moments64=m64)
+
+
+def compress_tensor(raw, n, dtype, unit, ensure_full_alphabet=False):
+    """Whole reference compress path for one tensor: mask → histogram → table → encode."""
+    masked, side = extract_mantissa(raw, n, dtype)
+    table, tsum = normalize_histogram(byte_hist(masked), ensure_full_alphabet)
+    data, hdr, off = encode(masked, table, unit)
+    return dict(masked=masked, sidecar=side, table=table, table_sum=tsum, data=data, headers=hdr, unit_offsets=off)
