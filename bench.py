@@ -1,0 +1,269 @@
+#!/usr/bin/env python3
+"""Benchmark of the checkpoint-compression hot path on one MI355X.
+
+Workload: the Llama-3-8B ZeRO-3 rank-0-of-8 shard,
+1,003,782,656 elements in each of four tensors — bf16 params ~N(0,0.02), fp32
+master = the same values upcast, fp32 exp_avg ~N(0,1e-3), fp32 exp_avg_sq =
+N(0,1e-3)^2 + 1e-12 — 14.05 GB resident in HBM, coded in 64 KiB units.
+
+A step is one full compression of the shard: per tensor the masked byte
+histogram, the host table, the chunked rANS encode with sidecar split and
+packing (ckr_compress).  `value` = uncompressed shard bytes / encode time per
+step.  Decode of the same shard is timed the same way right after and reported
+beside it, with the compression ratios, a bit-exact round-trip check, the
+dominant kernel's roofline, and the CPU oracle timed on a bounded sample.
+
+Usage: python bench.py [--steps K] [--warmup W] [--config 3] [--unit 65536]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "encode/decode GB/s on 1 MI355X (8B ZeRO-3 rank shard) + compression ratio"
+HBM_PEAK_GBPS = 8000.0
+
+# element counts of the benchmark configurations
+LLAMA8B_RANK0_OF_8 = 8_030_261_248 // 8
+LLAMA70B_RANK0_OF_8 = 70_553_706_496 // 8
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def make_shard(cfg, torch, dev, seed=0):
+    """Synthetic tensors of the configuration, generated on the GPU (torch Philox)."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    tensors = []
+    if cfg == 1:
+        n = 4096 * 4096
+        tensors.append(("exp_avg", (torch.randn(n, generator=g, device=dev) * 1e-3).contiguous()))
+    elif cfg in (3, 5):
+        n = LLAMA8B_RANK0_OF_8 if cfg == 3 else LLAMA70B_RANK0_OF_8
+        p = (torch.randn(n, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        tensors.append(("params_bf16", p))
+        tensors.append(("master_weights", p.float()))
+        tensors.append(("exp_avg", torch.randn(n, generator=g, device=dev) * 1e-3))
+        x = torch.randn(n, generator=g, device=dev) * 1e-3
+        tensors.append(("exp_avg_sq", x * x + 1e-12))
+        del x
+    elif cfg == 2:
+        shapes = [("q_proj", 4096 * 4096), ("k_proj", 1024 * 4096), ("v_proj", 1024 * 4096),
+                  ("o_proj", 4096 * 4096), ("gate_proj", 14336 * 4096), ("up_proj", 14336 * 4096),
+                  ("down_proj", 4096 * 14336)]
+        for name, n in shapes:
+            tensors.append((name, (torch.randn(n, generator=g, device=dev) * 0.02).to(torch.bfloat16)))
+        for name in ("input_layernorm", "post_attention_layernorm"):
+            tensors.append((name, torch.ones(4096, dtype=torch.bfloat16, device=dev)))
+    elif cfg == 4:
+        n = 256 * 1024 * 1024
+        x = torch.exp(torch.randn(n, generator=g, device=dev) * 5.0 - 12.0)
+        idx = torch.randint(0, n, (n // 1000,), generator=g, device=dev)
+        x[idx] = 0.0
+        idx = torch.randint(0, n, (n // 10000,), generator=g, device=dev)
+        x[idx] = torch.rand(idx.numel(), generator=g, device=dev) * 1e-39
+        idx = torch.randint(0, n, (n // 100000,), generator=g, device=dev)
+        x[idx] = torch.tensor([float("inf"), float("-inf"), float("nan")], device=dev)[
+            torch.randint(0, 3, (idx.numel(),), generator=g, device=dev)]
+        blk = 16 * 1024 * 1024
+        x.view(torch.int32)[:blk] = torch.randint(-2**31, 2**31 - 1, (blk,), generator=g, device=dev,
+                                                  dtype=torch.int32)
+        tensors.append(("adversarial", x))
+    torch.cuda.synchronize()
+    return tensors
+
+
+def cpu_baseline(shard, ck, sample_bytes_per_tensor, unit):
+    """The CPU oracle (C++ restatement, OpenMP over units) on a bounded sample."""
+    import oracle as oc
+    try:
+        cores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        cores = os.cpu_count() or 1
+    cores = max(1, min(cores, 16))
+    total = 0
+    t_all = 0.0
+    for name, t in shard:
+        tag = ck.torch_tag(t.dtype)
+        es = t.element_size()
+        n = min(t.numel(), sample_bytes_per_tensor // es)
+        raw = t[:n].contiguous().view(-1).cpu().view(__import__("torch").uint8).numpy()
+        t0 = time.perf_counter()
+        masked, side = oc.extract_mantissa(raw, n, tag)
+        table, _ = oc.normalize_histogram(oc.byte_hist(masked))
+        oc.encode(masked, table, unit, n_threads=cores)
+        t_all += time.perf_counter() - t0
+        total += n * es
+    return dict(value=round(total / t_all / 1e9, 4), unit="GB/s", cores=cores, kind="port",
+                sample=f"first {sample_bytes_per_tensor >> 20} MiB of each of the {len(shard)} tensors "
+                       f"({total / 1e6:.0f} MB): oracle mask+histogram+table single-thread, "
+                       f"rANS encode OpenMP over {unit}-byte units",
+                seconds=round(t_all, 3))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--unit", type=int, default=65536)
+    ap.add_argument("--cpu-sample-mib", type=int, default=128)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-profile", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (one ZeRO-3 rank's shard per GPU; "
+              "ranks share nothing on this path). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import checkers_amd as ck
+    ck.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    unit = args.unit if args.config != 5 else max(args.unit, 1 << 20)
+
+    log(f"[bench] generating config {args.config} shard")
+    shard = make_shard(args.config, torch, dev)
+    n_in = sum(t.numel() * t.element_size() for _, t in shard)
+    log(f"[bench] {len(shard)} tensors, {n_in / 1e9:.3f} GB; unit {unit}")
+
+    encs = [ck.Encoder(t.numel(), ck.torch_tag(t.dtype), unit, device=dev) for _, t in shard]
+    decs = [ck.Decoder(t.numel(), ck.torch_tag(t.dtype), unit, device=dev) for _, t in shard]
+    dsts = [torch.empty_like(t) for _, t in shard]
+
+    def encode_all(sync_total=False):
+        return [e.compress(t) if sync_total else e.compress(t) for e, (_, t) in zip(encs, shard)]
+
+    def decode_all(results, check=False):
+        bads = []
+        for d, r, dst in zip(decs, results, dsts):
+            bads.append(d.decode(r.data, r.headers, r.unit_offsets, r.table, r.sidecar, dst, check=check))
+        return bads
+
+    for i in range(args.warmup):
+        res = encode_all()
+        decode_all(res)
+        log(f"[bench] warmup {i + 1}/{args.warmup} done")
+    torch.cuda.synchronize()
+
+    # ---- timed encode steps
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        res = encode_all()
+    ev1.record()
+    torch.cuda.synchronize()
+    enc_wall = (time.perf_counter() - t0) / args.steps
+    enc_ev = ev0.elapsed_time(ev1) / 1e3 / args.steps
+    log(f"[bench] encode {enc_wall * 1e3:.2f} ms/step wall, {enc_ev * 1e3:.2f} ms/step events")
+
+    # ---- timed decode steps
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        decode_all(res)
+    ev1.record()
+    torch.cuda.synchronize()
+    dec_wall = (time.perf_counter() - t0) / args.steps
+    dec_ev = ev0.elapsed_time(ev1) / 1e3 / args.steps
+    log(f"[bench] decode {dec_wall * 1e3:.2f} ms/step wall, {dec_ev * 1e3:.2f} ms/step events")
+
+    # ---- size-independent checks: bit-exact round trip, lane postconditions
+    bads = decode_all(res, check=True)
+    roundtrip = all(torch.equal(d.view(torch.uint8), t.view(torch.uint8)) for d, (_, t) in zip(dsts, shard))
+    ok = roundtrip and all(b == 0 for b in bads)
+    C = sum(r.total for r in res)
+    S = sum(r.sidecar.numel() if r.sidecar is not None else 0 for r in res)
+    n_units = sum(e.n_units for e in encs)
+    H = n_units * 256 * 16 + (n_units + len(encs)) * 8 + len(encs) * 2308
+    log(f"[bench] roundtrip={ok} C={C / 1e9:.3f} GB S={S / 1e9:.3f} GB units={n_units}")
+
+    # ---- per-kernel profile of one encode + one decode
+    kernels, roof = {}, None
+    if not args.no_profile:
+        ck.profile_begin()
+        r2 = encode_all()
+        decode_all(r2)
+        prof = ck.profile_end()
+        kernels = {k: dict(launches=c, total_ms=round(ms, 4), avg_ms=round(ms / c, 5)) for k, (c, ms) in prof.items()}
+        # algorithmic bytes per kernel over the whole shard (one encode / one decode)
+        alg = {
+            "encode_kernel": n_in + S + C,        # read tensor, write sidecar + lane streams
+            "masked_hist_kernel": n_in,           # read tensor
+            "compact_kernel": 2 * C,              # read lane streams, write packed
+            "decode_kernel": C + S + n_in,        # read packed + sidecar, write tensor
+        }
+        dom = max((k for k in alg if k in prof), key=lambda k: prof[k][1])
+        ach = alg[dom] / (prof[dom][1] / 1e3) / 1e9
+        roof = dict(bound="hbm", kernel=dom, achieved=round(ach, 2), peak=HBM_PEAK_GBPS, unit="GB/s",
+                    frac=round(ach / HBM_PEAK_GBPS, 4), traffic=None,
+                    algorithmic_bytes=int(alg[dom]), launches=prof[dom][0],
+                    avg_launch_ms=round(prof[dom][1] / prof[dom][0], 5))
+        for k in alg:
+            if k in prof:
+                kernels[k]["achieved_GBps"] = round(alg[k] / (prof[k][1] / 1e3) / 1e9, 2)
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        cpu = cpu_baseline(shard, ck, args.cpu_sample_mib << 20, unit)
+        log(f"[bench] cpu {cpu}")
+
+    workload = {1: "cfg1 fp32 4096x4096 N(0,1e-3)", 2: "cfg2 llama3-8b decoder layer bf16",
+                3: "cfg3 llama3-8b zero3 rank0-of-8 shard (bf16 params, fp32 master, exp_avg, exp_avg_sq)",
+                4: "cfg4 adversarial fp32 256M", 5: "cfg5 llama3-70b zero3 rank0-of-8 shard"}[args.config]
+    out = {
+        "metric": METRIC,
+        "value": round(n_in / enc_wall / 1e9, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(enc_wall * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic: torch Philox on the GPU, seed 0, distributions of BASELINE.json configs",
+        "config": {"workload": workload, "elements_per_tensor": [t.numel() for _, t in shard],
+                   "tensors": [n for n, _ in shard], "unit_bytes": unit, "input_bytes": n_in,
+                   "table_bits": 12, "lanes": 256},
+        "encode_GBps": round(n_in / enc_wall / 1e9, 3),
+        "decode_GBps": round(n_in / dec_wall / 1e9, 3),
+        "encode_ms": round(enc_wall * 1e3, 3),
+        "decode_ms": round(dec_wall * 1e3, 3),
+        "encode_ms_events": round(enc_ev * 1e3, 3),
+        "decode_ms_events": round(dec_ev * 1e3, 3),
+        "encode_roofline_frac": round((n_in + S + C + H) / enc_wall / 1e9 / HBM_PEAK_GBPS, 4),
+        "decode_roofline_frac": round((n_in + S + C + H) / dec_wall / 1e9 / HBM_PEAK_GBPS, 4),
+        "compressed_bytes": C,
+        "sidecar_bytes": S,
+        "header_bytes": H,
+        "ans_ratio": round(n_in / C, 4),
+        "disk_ratio": round(n_in / (C + S), 4),
+        "container_ratio": round(n_in / (C + S + H), 4),
+        "roundtrip_bit_exact": ok,
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+    }
+    print(json.dumps(out), flush=True)
+    if not ok:
+        sys.exit(1)
+
+
+if __name__ == "__main__":
+    main()

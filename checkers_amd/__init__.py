@@ -28,7 +28,7 @@ EXPORTED = [  # every symbol include/checkers_amd.h declares
     "ckr_extract_mantissa", "ckr_byte_histogram", "ckr_byte_histogram_raw", "ckr_build_table",
     "ckr_num_units", "ckr_encode_max_output_bytes", "ckr_encode_workspace_bytes", "ckr_encode",
     "ckr_compress", "ckr_decode_workspace_bytes", "ckr_decode", "ckr_analyze_workspace_bytes",
-    "ckr_analyze",
+    "ckr_analyze", "ckr_profile_begin", "ckr_profile_end",
 ]
 
 
@@ -122,6 +122,8 @@ def lib():
         "ckr_decode": (i32, [vp, vp, vp, vp, u64, i32, u64, vp, vp, vp, u64, vp, vp]),
         "ckr_analyze_workspace_bytes": (u64, [vp, u64]),
         "ckr_analyze": (i32, [vp, u64, vp, u64, vp]),
+        "ckr_profile_begin": (i32, []),
+        "ckr_profile_end": (i32, [ctypes.c_char_p, u64]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L_, name)
@@ -134,6 +136,21 @@ def lib():
 def _check(rc):
     if rc != CKR_OK:
         raise CkrError(rc, lib().ckr_last_error().decode())
+
+
+def profile_begin():
+    _check(lib().ckr_profile_begin())
+
+
+def profile_end():
+    """{kernel: (launches, total_ms)} of the launches since profile_begin()."""
+    buf = ctypes.create_string_buffer(1 << 16)
+    _check(lib().ckr_profile_end(buf, len(buf)))
+    out = {}
+    for line in buf.value.decode().splitlines():
+        name, cnt, ms = line.split()
+        out[name] = (int(cnt), float(ms))
+    return out
 
 
 def element_size(dtype):

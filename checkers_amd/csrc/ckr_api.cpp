@@ -7,6 +7,8 @@
 
 #include <algorithm>
 #include <cstdarg>
+#include <map>
+#include <mutex>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -106,9 +108,71 @@ bool table_arg(const ckr_freq_table* t, ckr::TableArg* a) {
     return true;
 }
 
+// ---- optional per-kernel timing
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+struct ProfRec {
+    const char* name;
+    hipEvent_t a, b;
+};
+std::vector<ProfRec> g_prof;
+
 }  // namespace
 
+namespace ckr {
+void prof_mark(const char* name, hipStream_t s, bool begin) {
+    if (!g_prof_on) return;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return;
+    (void)hipEventRecord(e, s);
+    if (begin) g_prof.push_back({name, e, nullptr});
+    else if (!g_prof.empty() && g_prof.back().b == nullptr) g_prof.back().b = e;
+    else (void)hipEventDestroy(e);
+}
+}  // namespace ckr
+
 extern "C" {
+
+int ckr_profile_begin(void) {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    for (auto& r : g_prof) { (void)hipEventDestroy(r.a); if (r.b) (void)hipEventDestroy(r.b); }
+    g_prof.clear();
+    g_prof_on = true;
+    return CKR_OK;
+}
+
+// Writes one line per kernel name: "<name> <launches> <total_ms>\n".
+int ckr_profile_end(char* buf, uint64_t buflen) {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    g_prof_on = false;
+    std::map<std::string, std::pair<uint64_t, double>> agg;
+    for (auto& r : g_prof) {
+        if (r.b) {
+            if (hipEventSynchronize(r.b) != hipSuccess) return fail(CKR_E_HIP, "[ckr] profile event sync failed");
+            float ms = 0.f;
+            (void)hipEventElapsedTime(&ms, r.a, r.b);
+            auto& v = agg[r.name];
+            v.first++;
+            v.second += ms;
+            (void)hipEventDestroy(r.b);
+        }
+        (void)hipEventDestroy(r.a);
+    }
+    g_prof.clear();
+    std::string out;
+    for (auto& kv : agg) {
+        char line[256];
+        std::snprintf(line, sizeof(line), "%s %llu %.6f\n", kv.first.c_str(), (unsigned long long)kv.second.first,
+                      kv.second.second);
+        out += line;
+    }
+    if (buf && buflen) {
+        std::strncpy(buf, out.c_str(), buflen - 1);
+        buf[buflen - 1] = 0;
+    }
+    return CKR_OK;
+}
 
 const char* ckr_last_error(void) { return g_last_error.c_str(); }
 const char* ckr_version(void) { return "checkers_amd 0.1 gfx950"; }

@@ -32,6 +32,16 @@ struct EncSym {
 };
 
 // Decode slot entry: sym | (f-1) << 8 | cum << 20 (valid tables: f, cum < 4096).
+
+// Optional per-kernel timing (ckr_profile_begin / ckr_profile_end): when on,
+// every launch below is bracketed by HIP events recorded on its own stream.
+void prof_mark(const char* name, hipStream_t s, bool begin);
+#define CKR_LAUNCH(name, s, ...)              \
+    do {                                      \
+        ::ckr::prof_mark(name, s, true);      \
+        __VA_ARGS__;                          \
+        ::ckr::prof_mark(name, s, false);     \
+    } while (0)
 // ------------------------------------------------------------------ launchers
 // All return hipError_t of the launch; geometry is decided inside.
 hipError_t launch_build_enc_table(const TableArg& t, EncSym* d_enc, hipStream_t s);

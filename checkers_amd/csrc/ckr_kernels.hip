@@ -101,8 +101,8 @@ hipError_t launch_extract_mantissa(const uint8_t* src, uint64_t n_elems, int es,
     const uint64_t nvec = n_bytes / 16;
     uint32_t grid = (uint32_t)std::min<uint64_t>((nvec + 255) / 256, 8192);
     if (grid == 0) grid = 1;
-    if (spe == 2) extract_mantissa_kernel<2><<<grid, 256, 0, s>>>(src, n_bytes, masked, sidecar);
-    else extract_mantissa_kernel<1><<<grid, 256, 0, s>>>(src, n_bytes, masked, sidecar);
+    if (spe == 2) CKR_LAUNCH("extract_mantissa_kernel", s, extract_mantissa_kernel<2><<<grid, 256, 0, s>>>(src, n_bytes, masked, sidecar));
+    else CKR_LAUNCH("extract_mantissa_kernel", s, extract_mantissa_kernel<1><<<grid, 256, 0, s>>>(src, n_bytes, masked, sidecar));
     return hipGetLastError();
 }
 
@@ -178,14 +178,14 @@ uint32_t hist_num_blocks(uint64_t n_bytes) {
 hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int spe, uint32_t* d_hist,
                               hipStream_t s) {
     const uint64_t zero_count = (es > 0) ? (n_bytes / (uint64_t)es) * (uint64_t)spe : 0;
-    hist_init_kernel<<<1, 256, 0, s>>>(d_hist, zero_count);
+    CKR_LAUNCH("hist_init_kernel", s, hist_init_kernel<<<1, 256, 0, s>>>(d_hist, zero_count));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (n_bytes == 0) return hipSuccess;
     const uint32_t nblk = hist_num_blocks(n_bytes);
-    if (spe == 2) masked_hist_kernel<2><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist);
-    else if (spe == 1) masked_hist_kernel<1><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist);
-    else masked_hist_kernel<0><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist);
+    if (spe == 2) CKR_LAUNCH("masked_hist_kernel", s, masked_hist_kernel<2><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist));
+    else if (spe == 1) CKR_LAUNCH("masked_hist_kernel", s, masked_hist_kernel<1><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist));
+    else CKR_LAUNCH("masked_hist_kernel", s, masked_hist_kernel<0><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist));
     return hipGetLastError();
 }
 
@@ -193,11 +193,11 @@ hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int 
 __global__ void set_u64_kernel(uint64_t* p, uint64_t v) { *p = v; }
 __global__ void set_u64x_kernel(unsigned long long* p, unsigned long long v) { *p = v; }
 hipError_t launch_set_u64(uint64_t* p, uint64_t v, hipStream_t s) {
-    set_u64_kernel<<<1, 1, 0, s>>>(p, v);
+    CKR_LAUNCH("set_u64_kernel", s, set_u64_kernel<<<1, 1, 0, s>>>(p, v));
     return hipGetLastError();
 }
 hipError_t launch_set_counter(unsigned long long* p, unsigned long long v, hipStream_t s) {
-    set_u64x_kernel<<<1, 1, 0, s>>>(p, v);
+    CKR_LAUNCH("set_u64x_kernel", s, set_u64x_kernel<<<1, 1, 0, s>>>(p, v));
     return hipGetLastError();
 }
 
@@ -431,18 +431,18 @@ hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t
                                uint8_t* sidecar, uint32_t* unit_size, uint64_t* unit_off, uint8_t* out,
                                hipStream_t s) {
     const uint32_t grid = (uint32_t)((nb + 3) / 4);
-    if (g.spe == 2) encode_kernel<2><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, scratch, hdrs, sidecar);
-    else if (g.spe == 1) encode_kernel<1><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, scratch, hdrs, sidecar);
-    else encode_kernel<0><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, scratch, hdrs, nullptr);
+    if (g.spe == 2) CKR_LAUNCH("encode_kernel", s, encode_kernel<2><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, scratch, hdrs, sidecar));
+    else if (g.spe == 1) CKR_LAUNCH("encode_kernel", s, encode_kernel<1><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, scratch, hdrs, sidecar));
+    else CKR_LAUNCH("encode_kernel", s, encode_kernel<0><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, scratch, hdrs, nullptr));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    unit_finalize_kernel<<<(uint32_t)nb, 256, 0, s>>>(g, u0, hdrs, unit_size);
+    CKR_LAUNCH("unit_finalize_kernel", s, unit_finalize_kernel<<<(uint32_t)nb, 256, 0, s>>>(g, u0, hdrs, unit_size));
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    unit_scan_kernel<<<1, 1024, 0, s>>>(unit_size, u0, nb, unit_off);
+    CKR_LAUNCH("unit_scan_kernel", s, unit_scan_kernel<<<1, 1024, 0, s>>>(unit_size, u0, nb, unit_off));
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (g.spe == 2) compact_kernel<2><<<(uint32_t)nb, 256, 0, s>>>(src, g, u0, scratch, hdrs, unit_size, unit_off, out);
-    else if (g.spe == 1) compact_kernel<1><<<(uint32_t)nb, 256, 0, s>>>(src, g, u0, scratch, hdrs, unit_size, unit_off, out);
-    else compact_kernel<0><<<(uint32_t)nb, 256, 0, s>>>(src, g, u0, scratch, hdrs, unit_size, unit_off, out);
+    if (g.spe == 2) CKR_LAUNCH("compact_kernel", s, compact_kernel<2><<<(uint32_t)nb, 256, 0, s>>>(src, g, u0, scratch, hdrs, unit_size, unit_off, out));
+    else if (g.spe == 1) CKR_LAUNCH("compact_kernel", s, compact_kernel<1><<<(uint32_t)nb, 256, 0, s>>>(src, g, u0, scratch, hdrs, unit_size, unit_off, out));
+    else CKR_LAUNCH("compact_kernel", s, compact_kernel<0><<<(uint32_t)nb, 256, 0, s>>>(src, g, u0, scratch, hdrs, unit_size, unit_off, out));
     return hipGetLastError();
 }
 
@@ -507,12 +507,18 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
         return;
     }
     LaneIn in[4];
+    uint32_t nbad = 0;
 #pragma unroll
     for (int b = 0; b < 4; b++) {
         const ckr_stream_header h = uh[4 * j + b];
         in[b].x = h.final_state;
-        in[b].p = ud + h.buf_offset;
-        in[b].end = in[b].p + h.byte_count;
+        if ((uint64_t)h.buf_offset + h.byte_count <= usize) {
+            in[b].p = ud + h.buf_offset;
+            in[b].end = in[b].p + h.byte_count;
+        } else {  // header points outside its unit: read nothing, count the lane as bad
+            in[b].p = in[b].end = ud;
+            nbad++;
+        }
     }
     const uint64_t K = (len > col) ? (len - col + 255) / 256 : 0;
     for (uint64_t k = 0; k < K; k++) {
@@ -530,18 +536,17 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
             for (uint32_t b = 0; b < nvalid; b++) udst[p + b] = (uint8_t)(v >> (8 * b));
         }
     }
-    uint32_t nbad = 0;
 #pragma unroll
     for (int b = 0; b < 4; b++) nbad += (in[b].x != L || in[b].p != in[b].end) ? 1u : 0u;
     if (nbad) atomicAdd(bad, (unsigned long long)nbad);
 }
 
 hipError_t launch_build_enc_table(const TableArg& t, EncSym* d_enc, hipStream_t s) {
-    build_enc_table_kernel<<<1, 256, 0, s>>>(t, d_enc);
+    CKR_LAUNCH("build_enc_table_kernel", s, build_enc_table_kernel<<<1, 256, 0, s>>>(t, d_enc));
     return hipGetLastError();
 }
 hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, hipStream_t s) {
-    build_dec_table_kernel<<<1, 256, 0, s>>>(t, d_dec);
+    CKR_LAUNCH("build_dec_table_kernel", s, build_dec_table_kernel<<<1, 256, 0, s>>>(t, d_dec));
     return hipGetLastError();
 }
 
@@ -550,9 +555,9 @@ hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, con
                          unsigned long long* bad, hipStream_t s) {
     const uint32_t grid = (uint32_t)((g.n_units + 3) / 4);
     if (grid == 0) return hipSuccess;
-    if (g.spe == 2) decode_kernel<2><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad);
-    else if (g.spe == 1) decode_kernel<1><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad);
-    else decode_kernel<0><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad);
+    if (g.spe == 2) CKR_LAUNCH("decode_kernel", s, decode_kernel<2><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
+    else if (g.spe == 1) CKR_LAUNCH("decode_kernel", s, decode_kernel<1><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
+    else CKR_LAUNCH("decode_kernel", s, decode_kernel<0><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
     return hipGetLastError();
 }
 
@@ -692,14 +697,14 @@ uint32_t stats_num_blocks(uint64_t n) {
 
 hipError_t launch_stats(const ckr_stats_record& r, uint32_t nblk, StatsPartial1* p1, StatsPartial2* p2,
                         StatsParams* prm, uint32_t* hist_partial, hipStream_t s) {
-    stats_pass1_kernel<<<nblk, 256, 0, s>>>(r.d_ptr, r.num_elements, r.data_type, p1);
+    CKR_LAUNCH("stats_pass1_kernel", s, stats_pass1_kernel<<<nblk, 256, 0, s>>>(r.d_ptr, r.num_elements, r.data_type, p1));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    stats_mid_kernel<<<1, 64, 0, s>>>(p1, nblk, r.num_elements, r.histogram_bins, prm);
+    CKR_LAUNCH("stats_mid_kernel", s, stats_mid_kernel<<<1, 64, 0, s>>>(p1, nblk, r.num_elements, r.histogram_bins, prm));
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    stats_pass2_kernel<<<nblk, 256, 0, s>>>(r.d_ptr, r.num_elements, r.data_type, prm, p2, hist_partial);
+    CKR_LAUNCH("stats_pass2_kernel", s, stats_pass2_kernel<<<nblk, 256, 0, s>>>(r.d_ptr, r.num_elements, r.data_type, prm, p2, hist_partial));
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    stats_final_kernel<<<1, 256, 0, s>>>(p2, hist_partial, nblk, r.num_elements, prm, r);
+    CKR_LAUNCH("stats_final_kernel", s, stats_final_kernel<<<1, 256, 0, s>>>(p2, hist_partial, nblk, r.num_elements, prm, r));
     return hipGetLastError();
 }
 

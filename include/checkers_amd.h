@@ -22,8 +22,9 @@
  *                              inverse of rans_encode_kernel plus the sidecar merge
  *                              (include/checkers/ANSCompressor.hpp:165-171)
  *   - ckr_analyze            ← tensor_stats_kernel / compute_tensor_stats<T>
- *                              (src/TensorAnalyzer.cpp:64-229, launch :294-320)
- *   - ckr_fingerprints       ← TensorAnalyzer::compute_fingerprints (src/TensorAnalyzer.cpp:271-292)
+ *                              (src/TensorAnalyzer.cpp:64-229, launch :294-320), with the
+ *                              fingerprint of TensorAnalyzer::compute_fingerprints
+ *                              (src/TensorAnalyzer.cpp:271-292) written by the same pass
  */
 #ifndef CHECKERS_AMD_H
 #define CHECKERS_AMD_H
@@ -180,6 +181,13 @@ CKR_API int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers
 CKR_API uint64_t ckr_analyze_workspace_bytes(const ckr_stats_record* h_records, uint64_t n);
 CKR_API int ckr_analyze(const ckr_stats_record* h_records, uint64_t n,
                         void* d_workspace, uint64_t workspace_bytes, void* stream);
+
+/* ---- per-kernel timing, no counterpart in the reference (its only timings are
+ * host wall clocks, ANSCompressor.hpp:105-110).  Between begin and end every
+ * kernel the library launches is bracketed by HIP events on its stream; end
+ * synchronises them and writes "<kernel> <launches> <total_ms>" lines. ---- */
+CKR_API int ckr_profile_begin(void);
+CKR_API int ckr_profile_end(char* buf, uint64_t buflen);
 
 #ifdef __cplusplus
 }

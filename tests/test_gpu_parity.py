@@ -1,0 +1,192 @@
+"""GPU parity: the HIP library (through its C ABI) against the CPU oracle.
+
+Bar: bit-exact histograms and tables, byte-identical encoded data, headers,
+unit offsets and sidecars at the same unit size, and decode back to the input
+bits.  Moments are the only floating-point outputs; their tolerance is stated
+in test_analyzer_parity.
+"""
+import numpy as np
+import pytest
+
+import oracle as oc
+from tests import datagen as dg
+
+pytestmark = pytest.mark.gpu
+
+
+def _ck():
+    import checkers_amd as ck
+    return ck
+
+
+def _to_dev(arr, gpu):
+    import torch
+    b = dg.raw_bytes(arr)
+    t = torch.empty(max(b.size, 16), dtype=torch.uint8, device=gpu)
+    if b.size:
+        t[: b.size].copy_(torch.from_numpy(b.copy()))
+    return t
+
+
+CASES = [
+    # (name, dtype, n, unit, generator)
+    ("f32_normal_64k", dg.F32, 16384 * 5 + 1000, 65536, lambda n: dg.normal_f32(n, 1e-3, 0)),
+    ("f32_normal_whole", dg.F32, 40000, 0, lambda n: dg.normal_f32(n, 1e-3, 1)),
+    ("f32_normal_768", dg.F32, 20011, 768, lambda n: dg.normal_f32(n, 1e-3, 2)),
+    ("f32_expavgsq_64k", dg.F32, 16384 * 3, 65536, lambda n: dg.exp_avg_sq(n, 3)),
+    ("f32_upcast_bf16", dg.F32, 50000, 65536,
+     lambda n: (dg.normal_bf16(n, 0.02, 4).astype(np.uint32) << 16).view(np.float32)),
+    ("bf16_normal_64k", dg.BF16, 32768 * 3 + 1, 65536, lambda n: dg.normal_bf16(n, 0.02, 5)),
+    ("bf16_normal_whole", dg.BF16, 30001, 0, lambda n: dg.normal_bf16(n, 0.02, 6)),
+    ("bf16_normal_4k", dg.BF16, 70000, 4096, lambda n: dg.normal_bf16(n, 0.02, 7)),
+    ("bf16_rmsnorm_ones", dg.BF16, 4096, 65536, lambda n: dg.f32_to_bf16_bits(np.ones(n, np.float32))),
+    ("f16_normal", dg.F16, 10001, 1024, lambda n: (np.random.default_rng(8).standard_normal(n) * 0.02).astype(np.float16)),
+    ("i8_random", dg.I8, 100000, 2048, lambda n: np.random.default_rng(9).integers(-128, 128, n).astype(np.int8)),
+    ("i8_const", dg.I8, 3000, 512, lambda n: np.full(n, 7, np.int8)),
+    ("i32_small", dg.I32, 50000, 65536, lambda n: np.random.default_rng(10).integers(-3, 4, n).astype(np.int32)),
+    ("adversarial_f32", dg.F32, 300000, 65536, lambda n: dg.adversarial_f32(n, 11, (100000, 150000))),
+    ("tiny_f32_1", dg.F32, 1, 65536, lambda n: np.array([1.5], np.float32)),
+    ("tiny_bf16_3", dg.BF16, 3, 0, lambda n: dg.normal_bf16(n, 0.02, 12)),
+    ("tiny_i8_255", dg.I8, 255, 0, lambda n: np.arange(n, dtype=np.uint8).view(np.int8)),
+    ("tiny_i8_256", dg.I8, 256, 256, lambda n: np.arange(n, dtype=np.uint8).view(np.int8)),
+    ("tiny_i8_257", dg.I8, 257, 256, lambda n: np.arange(n, dtype=np.uint8).view(np.int8)),
+    ("empty_f32", dg.F32, 0, 65536, lambda n: np.zeros(0, np.float32)),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_compress_parity_and_roundtrip(case, gpu):
+    import torch
+    ck = _ck()
+    name, dt, n, unit, gen = case
+    print(f"[case] {name} dtype={dt} n={n} unit={unit}", flush=True)
+    raw = gen(n)
+    ref = oc.compress_tensor(raw, n, dt, unit)
+    src = _to_dev(raw, gpu)
+    enc = ck.compress(src, dt, unit, n_elems=n)
+    torch.cuda.synchronize()
+    # table
+    assert np.array_equal(enc.table.norm, ref["table"]["norm_freq"])
+    assert np.array_equal(enc.table.cum, ref["table"]["cum_freq"])
+    # packed data, headers, unit offsets
+    assert enc.total == ref["data"].size
+    nu = ref["unit_offsets"].size - 1
+    assert np.array_equal(enc.unit_offsets[: nu + 1].cpu().numpy().view(np.uint64), ref["unit_offsets"])
+    if nu:
+        assert np.array_equal(enc.headers_np()[: nu * 256], ref["headers"])
+    assert np.array_equal(enc.data_np(), ref["data"])
+    # sidecar
+    spe = oc.SPE[dt]
+    if spe and n:
+        assert np.array_equal(enc.sidecar[: n * spe].cpu().numpy(), ref["sidecar"])
+    # decode → original bits
+    dst, bad = ck.decode(enc)
+    torch.cuda.synchronize()
+    assert bad == 0
+    assert np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
+
+
+@pytest.mark.parametrize("dt,gen", [
+    (dg.F32, lambda n: dg.normal_f32(n, 1e-3, 20)),
+    (dg.BF16, lambda n: dg.normal_bf16(n, 0.02, 21)),
+    (dg.F16, lambda n: (np.random.default_rng(22).standard_normal(n)).astype(np.float16)),
+    (dg.I8, lambda n: np.random.default_rng(23).integers(-128, 128, n).astype(np.int8)),
+])
+@pytest.mark.parametrize("n", [1, 7, 4099, 1 << 20])
+def test_histogram_and_split_parity(dt, gen, n, gpu):
+    import torch
+    ck = _ck()
+    print(f"[case] hist dtype={dt} n={n}", flush=True)
+    raw = gen(n)
+    masked, side = oc.extract_mantissa(raw, n, dt)
+    src = _to_dev(raw, gpu)
+    h = ck.byte_histogram(src, dt, n_elems=n)
+    torch.cuda.synchronize()
+    assert np.array_equal(h.cpu().numpy().view(np.uint32), oc.byte_hist(masked))
+    if oc.SPE[dt]:
+        m, s = ck.extract_mantissa(src, dt, n_elems=n)
+        torch.cuda.synchronize()
+        assert np.array_equal(m.cpu().numpy(), masked)
+        assert np.array_equal(s.cpu().numpy(), side)
+
+
+def test_passthrough_unit_with_mismatched_table(gpu):
+    """A table that prices the data badly makes units expand → stored raw (ANSCompressor.cpp:694-713)."""
+    import torch
+    ck = _ck()
+    n, unit = 20000, 1024
+    rng = np.random.default_rng(30)
+    raw = rng.integers(-128, 128, n).astype(np.int8)
+    raw[:3000] = 0  # first units compress, the rest expand
+    h = np.ones(256, np.uint32)
+    h[0] = 1_000_000
+    t_ck, s_ck = ck.build_table(h)
+    t_oc, s_oc = oc.normalize_histogram(h)
+    assert s_ck == s_oc == 4096
+    data, hdr, off = oc.encode(dg.raw_bytes(raw), t_oc, unit)
+    src = _to_dev(raw, gpu)
+    enc = ck.encode(src, dg.I8, t_ck, unit, n_elems=n)
+    torch.cuda.synchronize()
+    sizes = np.diff(off.astype(np.int64))
+    assert (sizes == unit).any() and (sizes < unit).any()  # both kinds of unit present
+    assert enc.total == data.size
+    assert np.array_equal(enc.data_np(), data)
+    assert np.array_equal(enc.headers_np()[: hdr.size], hdr)
+    dst, bad = ck.decode(enc)
+    assert bad == 0 and np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
+
+
+def test_escape_symbols_match_reference_bytes(gpu):
+    """Symbols with f == 0 take the reference's raw-byte escape (ANSCompressor.cpp:185-192)."""
+    import torch
+    ck = _ck()
+    n, unit = 8192, 4096
+    raw = np.random.default_rng(31).integers(0, 16, n).astype(np.int8)
+    h = np.zeros(256, np.uint32)
+    h[:10] = 100  # symbols 10..15 absent from the table
+    t_ck, _ = ck.build_table(h)
+    t_oc, _ = oc.normalize_histogram(h)
+    data, hdr, off = oc.encode(dg.raw_bytes(raw), t_oc, unit)
+    enc = ck.encode(_to_dev(raw, gpu), dg.I8, t_ck, unit, n_elems=n)
+    torch.cuda.synchronize()
+    assert enc.total == data.size
+    assert np.array_equal(enc.data_np(), data)
+    assert np.array_equal(enc.headers_np()[: hdr.size], hdr)
+
+
+@pytest.mark.parametrize("dt,n,bins,gen", [
+    (dg.F32, 100000, 256, lambda n: dg.normal_f32(n, 1e-3, 40)),
+    (dg.F32, 4097, 16, lambda n: dg.exp_avg_sq(n, 41)),
+    (dg.BF16, 70001, 4096, lambda n: dg.normal_bf16(n, 0.02, 42)),
+    (dg.F16, 5000, 256, lambda n: (np.random.default_rng(43).standard_normal(n)).astype(np.float16)),
+    (dg.I8, 3001, 256, lambda n: np.random.default_rng(44).integers(-128, 128, n).astype(np.int8)),
+    (dg.I32, 3001, 100, lambda n: np.random.default_rng(45).integers(-10**6, 10**6, n).astype(np.int32)),
+    (dg.F32, 1000, 256, lambda n: np.full(n, 0.25, np.float32)),           # range 0 → bin 0
+    (dg.F32, 20000, 256, lambda n: dg.adversarial_f32(n, 46)),             # NaN / inf / denormals
+])
+def test_analyzer_parity(dt, n, bins, gen, gpu):
+    ck = _ck()
+    import torch
+    print(f"[case] analyze dtype={dt} n={n} bins={bins}", flush=True)
+    raw = gen(n)
+    ref = oc.tensor_stats(raw, n, dt, bins)
+    got = ck.analyze([_to_dev(raw, gpu)[: n * oc.ES[dt]]], [dt], bins=bins)[0]
+    torch.cuda.synchronize()
+    # min/max are order-independent: exact (== treats ±0 alike)
+    assert np.array_equal(got["minmax"], ref["minmax"]) or (got["minmax"] == ref["minmax"]).all()
+    # histogram: bit-exact given exact min/max and IEEE fp32 sub/mul
+    assert np.array_equal(got["histogram"], ref["histogram"])
+    # moments: the GPU sums in fp64, the reference in fp32; compare both with the
+    # fp64 closed form: mean to 1e-6 of the spread, var/skew/kurt to 1e-4 relative.
+    m64 = ref["moments64"]
+    if np.all(np.isfinite(m64)):
+        spread = max(abs(float(ref["minmax"][1]) - float(ref["minmax"][0])), 1e-30)
+        assert abs(got["moments"][0] - m64[0]) <= 1e-6 * spread + 1e-30
+        assert abs(got["moments"][1] - m64[1]) <= 1e-4 * abs(m64[1]) + 1e-30
+        if m64[1] > 1e-9 * (1 + 1e-4):  # skew/kurt only above the reference's var > 1e-9 gate
+            for k in (2, 3):
+                assert abs(got["moments"][k] - m64[k]) <= 1e-4 * max(abs(m64[k]), 1.0), (k, got["moments"], m64)
+        elif m64[1] < 1e-9 * (1 - 1e-4):
+            assert got["moments"][2] == 0 and got["moments"][3] == 0
+    fp = got["fingerprint"]
+    assert np.array_equal(fp[:4], got["moments"]) and fp[4] == np.float32(got["minmax"][1] - got["minmax"][0])
