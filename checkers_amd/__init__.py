@@ -195,6 +195,20 @@ def _stream(stream):
     return ctypes.c_void_p(stream.cuda_stream)
 
 
+def _n_elems(src, dtype, n_elems):
+    """Element count of `src` read as `dtype` (from its byte size), or n_elems if given;
+    never more elements than the tensor's bytes hold."""
+    es = element_size(dtype)
+    if es == 0:
+        raise CkrError(CKR_E_INVALID, f"unknown dtype tag {dtype}")
+    cap = src.numel() * src.element_size() // es
+    if n_elems is None:
+        return cap
+    if n_elems > cap:
+        raise CkrError(CKR_E_INVALID, f"n_elems={n_elems} exceeds the {cap} elements the tensor holds")
+    return int(n_elems)
+
+
 def _empty(nbytes, device):
     torch = _torch()
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
@@ -235,7 +249,12 @@ class Encoder:
         spe = Lb.ckr_sidecar_bytes_per_elem(dtype)
         self.sidecar = _empty(self.n_elems * spe, device) if spe else None
 
+    def _check_src(self, src):
+        if src.numel() * src.element_size() < self.n_bytes:
+            raise CkrError(CKR_E_INVALID, f"source holds {src.numel() * src.element_size()} bytes, need {self.n_bytes}")
+
     def encode(self, src, table, stream=None, sync_total=True):
+        self._check_src(src)
         tot = ctypes.c_uint64(0)
         _check(lib().ckr_encode(
             src.data_ptr(), self.n_elems, self.dtype, table.ptr, self.unit_bytes,
@@ -246,6 +265,7 @@ class Encoder:
                        tot.value if sync_total else None, self.n_elems, self.dtype, self.unit_bytes, table)
 
     def compress(self, src, ensure_full_alphabet=False, stream=None):
+        self._check_src(src)
         tot = ctypes.c_uint64(0)
         t = aligned_table()
         _check(lib().ckr_compress(
@@ -260,7 +280,7 @@ class Encoder:
 def byte_histogram(src, dtype, n_elems=None, stream=None):
     """256-bin histogram of the masked byte stream of `src` (torch device tensor)."""
     torch = _torch()
-    n = src.numel() if n_elems is None else n_elems
+    n = _n_elems(src, dtype, n_elems)
     h = torch.empty(256, dtype=torch.int32, device=src.device)
     _check(lib().ckr_byte_histogram(src.data_ptr(), n, dtype, h.data_ptr(), _stream(stream)))
     return h
@@ -268,7 +288,7 @@ def byte_histogram(src, dtype, n_elems=None, stream=None):
 
 def extract_mantissa(src, dtype, n_elems=None, stream=None):
     torch = _torch()
-    n = src.numel() if n_elems is None else n_elems
+    n = _n_elems(src, dtype, n_elems)
     es, spe = element_size(dtype), sidecar_bytes_per_elem(dtype)
     masked = torch.empty(max(n * es, 1), dtype=torch.uint8, device=src.device)
     side = torch.empty(max(n * spe, 1), dtype=torch.uint8, device=src.device)
@@ -277,13 +297,13 @@ def extract_mantissa(src, dtype, n_elems=None, stream=None):
 
 
 def encode(src, dtype, table, unit_bytes, n_elems=None, stream=None):
-    n = src.numel() if n_elems is None else n_elems
+    n = _n_elems(src, dtype, n_elems)
     enc = Encoder(n, dtype, unit_bytes, device=src.device)
     return enc.encode(src, table, stream=stream)
 
 
 def compress(src, dtype, unit_bytes, ensure_full_alphabet=False, n_elems=None, stream=None):
-    n = src.numel() if n_elems is None else n_elems
+    n = _n_elems(src, dtype, n_elems)
     return Encoder(n, dtype, unit_bytes, device=src.device).compress(src, ensure_full_alphabet, stream=stream)
 
 
@@ -328,8 +348,9 @@ def analyze(tensors, tags, bins=256, stream=None):
     fp = torch.zeros((max(n, 1), 5), dtype=torch.float32, device=dev)
     recs = (StatsRecord * max(n, 1))()
     for i, (t, tag) in enumerate(zip(tensors, tags)):
-        recs[i].d_ptr = t.data_ptr() if t.numel() else None
-        recs[i].num_elements = t.numel()
+        ne = _n_elems(t, tag, None)
+        recs[i].d_ptr = t.data_ptr() if ne else None
+        recs[i].num_elements = ne
         recs[i].histogram_bins = bins
         recs[i].data_type = tag
         recs[i].d_histogram = hist[i].data_ptr()
