@@ -28,7 +28,7 @@ EXPORTED = [  # every symbol include/checkers_amd.h declares
     "ckr_extract_mantissa", "ckr_byte_histogram", "ckr_byte_histogram_raw", "ckr_build_table",
     "ckr_num_units", "ckr_encode_max_output_bytes", "ckr_encode_workspace_bytes", "ckr_encode",
     "ckr_compress", "ckr_decode_workspace_bytes", "ckr_decode", "ckr_analyze_workspace_bytes",
-    "ckr_analyze", "ckr_profile_begin", "ckr_profile_end",
+    "ckr_analyze", "ckr_profile_begin", "ckr_profile_end", "ckr_set_fast_paths",
 ]
 
 
@@ -122,6 +122,7 @@ def lib():
         "ckr_decode": (i32, [vp, vp, vp, vp, u64, i32, u64, vp, vp, vp, u64, vp, vp]),
         "ckr_analyze_workspace_bytes": (u64, [vp, u64]),
         "ckr_analyze": (i32, [vp, u64, vp, u64, vp]),
+        "ckr_set_fast_paths": (i32, [i32]),
         "ckr_profile_begin": (i32, []),
         "ckr_profile_end": (i32, [ctypes.c_char_p, u64]),
     }
@@ -136,6 +137,11 @@ def lib():
 def _check(rc):
     if rc != CKR_OK:
         raise CkrError(rc, lib().ckr_last_error().decode())
+
+
+def set_fast_paths(enable):
+    """Select the fast kernels (default) or the general ones; returns the previous setting."""
+    return bool(lib().ckr_set_fast_paths(int(bool(enable))))
 
 
 def profile_begin():

@@ -76,8 +76,30 @@ bool make_geom(uint64_t n_elems, int dtype, uint64_t unit_bytes, ckr::EncodeGeom
     return true;
 }
 
+// Lane counts of the zero-plane canonical streams: full units (k0) and the two
+// lane counts of the last unit (k1 = ceil, k2 = floor of its length / 256).
+struct CanonKs {
+    uint32_t k0, k1, k2, cw;
+};
+CanonKs canon_ks(const ckr::EncodeGeom& g) {
+    CanonKs c{};
+    if (g.n_units == 0) return c;
+    const uint64_t last = g.n_bytes - (g.n_units - 1) * g.unit;
+    c.k0 = (uint32_t)((g.unit + 255) / 256);
+    c.k1 = (uint32_t)((last + 255) / 256);
+    c.k2 = (uint32_t)(last / 256);
+    c.cw = (2 * c.k0 + 3) / 4 + 1;
+    return c;
+}
+constexpr uint32_t kDedupMaxK = 4096;  // zero-plane dedup up to 1 MiB units
+bool g_fast_paths = true;              // ckr_set_fast_paths
+
+bool use_dedup(const ckr::EncodeGeom& g) {
+    return g_fast_paths && g.spe > 0 && g.n_units > 0 && (g.unit + 255) / 256 <= kDedupMaxK;
+}
+
 struct EncodeLayout {
-    uint64_t off_enc, off_hist, off_usize, off_scratch, total;
+    uint64_t off_enc, off_hist, off_canon, off_usize, off_scratch, total;
     uint64_t batch_units;
 };
 
@@ -87,11 +109,32 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     uint64_t bu = per_unit ? std::max<uint64_t>(1, kScratchBudget / per_unit) : 1;
     bu = std::min<uint64_t>(bu, std::max<uint64_t>(g.n_units, 1));
     L.batch_units = bu;
+    const CanonKs ck = canon_ks(g);
     uint64_t o = 0;
     L.off_enc = o;     o = align_up(o + 256 * sizeof(ckr::EncSym), kAlign);
     L.off_hist = o;    o = align_up(o + 256 * 4, kAlign);
+    L.off_canon = o;   o = align_up(o + (use_dedup(g) ? 3ull * (4 + ck.cw) * 4 : 0), kAlign);
     L.off_usize = o;   o = align_up(o + bu * 4, kAlign);
     L.off_scratch = o; o = align_up(o + bu * per_unit, kAlign);
+    L.total = o;
+    return L;
+}
+
+// Decode workspace: enc table, canonical streams, decode table, bad-lane counter, unit mask.
+struct DecodeLayout {
+    uint64_t off_enc, off_canon, off_dec, off_bad, off_mask, total;
+    bool fast;
+};
+DecodeLayout decode_layout(const ckr::EncodeGeom& g) {
+    DecodeLayout L{};
+    const CanonKs ck = canon_ks(g);
+    L.fast = g_fast_paths && g.spe > 0 && g.n_units > 0 && ck.cw <= ckr::decode_fast_max_cw();
+    uint64_t o = 0;
+    L.off_enc = o;   o = align_up(o + 256 * sizeof(ckr::EncSym), kAlign);
+    L.off_canon = o; o = align_up(o + (L.fast ? 3ull * (4 + ck.cw) * 4 : 0), kAlign);
+    L.off_dec = o;   o = align_up(o + 4096 * 4, kAlign);
+    L.off_bad = o;   o = align_up(o + 8, kAlign);
+    L.off_mask = o;  o = align_up(o + (L.fast ? g.n_units * 4 : 0), kAlign);
     L.total = o;
     return L;
 }
@@ -175,6 +218,12 @@ int ckr_profile_end(char* buf, uint64_t buflen) {
 }
 
 const char* ckr_last_error(void) { return g_last_error.c_str(); }
+
+int ckr_set_fast_paths(int enable) {
+    const int prev = g_fast_paths ? 1 : 0;
+    g_fast_paths = enable != 0;
+    return prev;
+}
 const char* ckr_version(void) { return "checkers_amd 0.1 gfx950"; }
 
 int ckr_element_size(int dtype) {
@@ -321,13 +370,18 @@ int ckr_encode(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_ta
     if (!table_arg(h_table, &ta)) return CKR_E_TABLE;
     uint8_t* ws = static_cast<uint8_t*>(d_workspace);
     auto* enc = reinterpret_cast<ckr::EncSym*>(ws + L.off_enc);
+    auto* canon = reinterpret_cast<uint32_t*>(ws + L.off_canon);
     auto* usize = reinterpret_cast<uint32_t*>(ws + L.off_usize);
     auto* scratch = reinterpret_cast<uint32_t*>(ws + L.off_scratch);
+    const bool dedup = use_dedup(g);
+    const CanonKs ck = canon_ks(g);
     CKR_HIP(ckr::launch_build_enc_table(ta, enc, s));
+    if (dedup) CKR_HIP(ckr::launch_canon(enc, ck.k0, ck.k1, ck.k2, ck.cw, canon, s));
     for (uint64_t u0 = 0; u0 < g.n_units; u0 += L.batch_units) {
         const uint64_t nb = std::min<uint64_t>(L.batch_units, g.n_units - u0);
-        CKR_HIP(ckr::launch_encode_batch(static_cast<const uint8_t*>(d_src), g, u0, nb, enc, scratch, d_headers,
-                                         g.spe ? d_sidecar : nullptr, usize, d_unit_offsets, d_out, s));
+        CKR_HIP(ckr::launch_encode_batch(static_cast<const uint8_t*>(d_src), g, u0, nb, enc, canon, ck.cw, dedup,
+                                         scratch, d_headers, g.spe ? d_sidecar : nullptr, usize, d_unit_offsets,
+                                         d_out, s));
     }
     if (h_total_out) {
         CKR_HIP(hipMemcpyAsync(h_total_out, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
@@ -362,7 +416,11 @@ int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_b
                       d_sidecar, d_workspace, workspace_bytes, h_total_out, stream);
 }
 
-uint64_t ckr_decode_workspace_bytes(uint64_t, int, uint64_t) { return align_up(4096 * 4 + 64, kAlign); }
+uint64_t ckr_decode_workspace_bytes(uint64_t n_elems, int dtype, uint64_t unit_bytes) {
+    ckr::EncodeGeom g;
+    if (!dtype_ok(dtype) || !make_geom(n_elems, dtype, unit_bytes, &g)) return 0;
+    return decode_layout(g).total;
+}
 
 int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const uint64_t* d_unit_offsets,
                const ckr_freq_table* h_table, uint64_t n_elems, int dtype, uint64_t unit_bytes,
@@ -378,19 +436,28 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
     if (g.spe && !d_sidecar) return fail(CKR_E_INVALID, "[ckr] dtype %d needs its sidecar", dtype);
     if (!aligned16(d_dst) || !aligned16(d_workspace) || (d_sidecar && !aligned16(d_sidecar)))
         return fail(CKR_E_INVALID, "[ckr] destination, sidecar and workspace must be 16-byte aligned");
-    if (workspace_bytes < ckr_decode_workspace_bytes(n_elems, dtype, unit_bytes))
-        return fail(CKR_E_CAPACITY, "[ckr] decode workspace too small");
+    const DecodeLayout L = decode_layout(g);
+    if (workspace_bytes < L.total) return fail(CKR_E_CAPACITY, "[ckr] decode workspace too small");
     if (h_table->cum_freq[256] != CKR_M)
         return fail(CKR_E_TABLE, "[ckr] table sums to %u, not 4096: stream not decodable", h_table->cum_freq[256]);
     ckr::TableArg ta;
     if (!table_arg(h_table, &ta)) return CKR_E_TABLE;
     hipStream_t s = (hipStream_t)stream;
-    auto* dec = static_cast<uint32_t*>(d_workspace);
-    auto* bad = reinterpret_cast<unsigned long long*>(static_cast<uint8_t*>(d_workspace) + 4096 * 4);
+    uint8_t* ws = static_cast<uint8_t*>(d_workspace);
+    auto* enc = reinterpret_cast<ckr::EncSym*>(ws + L.off_enc);
+    auto* canon = reinterpret_cast<uint32_t*>(ws + L.off_canon);
+    auto* dec = reinterpret_cast<uint32_t*>(ws + L.off_dec);
+    auto* bad = reinterpret_cast<unsigned long long*>(ws + L.off_bad);
+    auto* mask = reinterpret_cast<uint32_t*>(ws + L.off_mask);
+    const CanonKs ck = canon_ks(g);
     CKR_HIP(ckr::launch_build_dec_table(ta, dec, s));
+    if (L.fast) {
+        CKR_HIP(ckr::launch_build_enc_table(ta, enc, s));
+        CKR_HIP(ckr::launch_canon(enc, ck.k0, ck.k1, ck.k2, ck.cw, canon, s));
+    }
     CKR_HIP(ckr::launch_set_counter(bad, 0, s));
     CKR_HIP(ckr::launch_decode(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, static_cast<uint8_t*>(d_dst),
-                               bad, s));
+                               bad, L.fast ? canon : nullptr, ck.cw, L.fast ? mask : nullptr, s));
     if (h_bad_lanes) {
         unsigned long long nb = 0;
         CKR_HIP(hipMemcpyAsync(&nb, bad, 8, hipMemcpyDeviceToHost, s));

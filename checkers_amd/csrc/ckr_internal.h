@@ -66,13 +66,23 @@ struct EncodeGeom {
     int es, spe;
 };
 hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t u0, uint64_t nb,
-                               const EncSym* d_enc, uint32_t* scratch,
-                               ckr_stream_header* hdrs, uint8_t* sidecar, uint32_t* unit_size,
-                               uint64_t* unit_off, uint8_t* out, hipStream_t s);
+                               const EncSym* d_enc, const uint32_t* canon, uint32_t cw, bool dedup,
+                               uint32_t* scratch, ckr_stream_header* hdrs, uint8_t* sidecar,
+                               uint32_t* unit_size, uint64_t* unit_off, uint8_t* out, hipStream_t s);
 
+// Canonical zero-plane streams for lane counts k0, k1, k2 (3 entries of 4 + cw dwords).
+hipError_t launch_canon(const EncSym* d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw, uint32_t* canon,
+                        hipStream_t s);
+
+// Decode; with canon and unit_mask (n_units u32) the LDS-staged fast kernel runs
+// first for units <= 64 KiB of masked dtypes (canonical entries of cw <=
+// decode_fast_max_cw() dwords) and the general kernel takes the units it left.
+uint32_t decode_fast_lds_bytes();
+uint32_t decode_fast_max_cw();
 hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
-                         const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar,
-                         uint8_t* dst, unsigned long long* bad, hipStream_t s);
+                         const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
+                         unsigned long long* bad, const uint32_t* canon, uint32_t cw, uint32_t* unit_mask,
+                         hipStream_t s);
 
 // Analyzer.
 struct StatsParams {     // per record, device resident between passes

@@ -202,43 +202,85 @@ hipError_t launch_set_counter(unsigned long long* p, unsigned long long v, hipSt
 }
 
 // ------------------------------------------------------------------ rANS encode
-// Lane state: x, 32-bit output accumulator, bytes pending in it, slots flushed.
+// Lane state: x, pending output bytes (up to 7, newest lowest) and dword slots
+// flushed.  The first byte emitted is the last byte of the lane's stream, so a
+// dword taken from the top of the pending bytes, stored little-endian, holds 4
+// stream bytes in stream order; slot w (counted from the stream's end) of a
+// lane lives at lane_base[w * STRIDE].
 struct LaneOut {
-    uint32_t x, acc, nacc, w;
+    uint32_t x, nacc, w;
+    uint64_t acc;
 };
 
-// Emission order equals the reference's backward writes: the first byte emitted
-// is the last byte of the lane's stream.  acc = acc<<8 | b keeps the latest
-// byte lowest, so a full acc stored little-endian holds 4 stream bytes in
-// stream order; slot w (counted from the stream's end) is stored at
-// lane_base + w*1024.
-__device__ __forceinline__ void emit_byte(LaneOut& o, uint32_t b, uint32_t* lane_base) {
-    o.acc = (o.acc << 8) | b;
-    if (++o.nacc == 4) {
-        lane_base[(uint64_t)o.w * 256] = o.acc;
+__device__ __forceinline__ void lane_init(LaneOut& o) { o.x = L; o.nacc = 0; o.w = 0; o.acc = 0; }
+
+template <uint32_t STRIDE>
+__device__ __forceinline__ void push_bytes(LaneOut& o, uint32_t v, uint32_t n, uint32_t* lane_base) {
+    o.acc = (o.acc << (8 * n)) | v;
+    o.nacc += n;
+    if (o.nacc >= 4) {
+        lane_base[(uint64_t)o.w * STRIDE] = (uint32_t)(o.acc >> (8 * (o.nacc - 4)));
         o.w++;
-        o.nacc = 0;
-        o.acc = 0;
+        o.nacc -= 4;
     }
 }
 
 // One symbol of rans_encode_kernel's loop body (ANSCompressor.cpp:180-202).
+// Renormalisation emits at most two bytes (x < 2^32 and xmax >= 2^19); both
+// are computed without branches and appended in one step.
+template <uint32_t STRIDE>
 __device__ __forceinline__ void encode_symbol(LaneOut& o, uint32_t sym, const EncSym* tab, uint32_t* lane_base) {
     const EncSym e = tab[sym];
     if (e.xmax == 0) {  // f == 0: raw byte, no state update (:185-192)
-        emit_byte(o, sym, lane_base);
+        push_bytes<STRIDE>(o, sym, 1, lane_base);
         return;
     }
-    if (o.x >= e.xmax) {  // renormalise: at most two bytes since x < 2^32 and xmax >= 2^19
-        emit_byte(o, o.x & 255u, lane_base);
-        o.x >>= 8;
-        if (o.x >= e.xmax) {
-            emit_byte(o, o.x & 255u, lane_base);
-            o.x >>= 8;
-        }
+    const uint32_t x = o.x;
+    const uint32_t e1 = x >= e.xmax ? 1u : 0u;
+    const uint32_t x1 = e1 ? (x >> 8) : x;
+    const uint32_t e2 = (e1 && x1 >= e.xmax) ? 1u : 0u;
+    const uint32_t n = e1 + e2;
+    if (n) {
+        const uint32_t v = e2 ? (((x & 255u) << 8) | ((x >> 8) & 255u)) : (x & 255u);
+        push_bytes<STRIDE>(o, v, n, lane_base);
     }
-    const uint32_t q = __umulhi(o.x, e.rcp) >> (e.cmpl_rsh >> 16);
-    o.x = o.x + e.bias + q * (e.cmpl_rsh & 0xFFFFu);
+    const uint32_t xr = e2 ? (x1 >> 8) : x1;
+    const uint32_t q = __umulhi(xr, e.rcp) >> (e.cmpl_rsh >> 16);
+    o.x = xr + e.bias + q * (e.cmpl_rsh & 0xFFFFu);
+}
+
+template <uint32_t STRIDE>
+__device__ __forceinline__ void lane_flush(LaneOut& o, uint32_t* lane_base) {
+    if (o.nacc) lane_base[(uint64_t)o.w * STRIDE] = (uint32_t)o.acc;  // low nacc bytes = first stream bytes
+}
+__device__ __forceinline__ uint32_t lane_bytes(const LaneOut& o) { return o.w * 4 + o.nacc; }
+
+// Canonical streams of the zero planes.  A lane of a masked plane codes K
+// zero bytes from state L whatever the data, so its stream depends only on K
+// and the table: it is coded once per distinct K (at most three per tensor:
+// full units, and the two lane counts of the last unit) instead of once per
+// lane.  Entry i: {K, final_state, byte_count, pad} then cw dword slots.
+__global__ void canon_kernel(const EncSym* __restrict__ d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw,
+                             uint32_t* __restrict__ canon) {
+    const uint32_t t = threadIdx.x;
+    if (t >= 3) return;
+    const uint32_t K = t == 0 ? k0 : (t == 1 ? k1 : k2);
+    uint32_t* base = canon + (uint64_t)t * (4 + cw);
+    LaneOut o;
+    lane_init(o);
+    for (uint32_t k = 0; k < K; k++) encode_symbol<1>(o, 0u, d_enc, base + 4);
+    lane_flush<1>(o, base + 4);
+    base[0] = K;
+    base[1] = o.x;
+    base[2] = lane_bytes(o);
+    base[3] = 0;
+}
+
+__device__ __forceinline__ const uint32_t* canon_entry(const uint32_t* canon, uint32_t cw, uint32_t K) {
+    // entries hold distinct K values except when two coincide; first match wins
+    if (canon[0] == K) return canon;
+    if (canon[4 + cw] == K) return canon + 4 + cw;
+    return canon + 2 * (4 + cw);
 }
 
 template <int SPE>
@@ -253,12 +295,19 @@ __device__ __forceinline__ void write_sidecar_row(uint8_t* sidecar, uint64_t pos
     }
 }
 
-// One wave per unit, one thread per 32-bit column (4 lanes).  Rows are taken
-// from the top of the unit down (the reference's reverse order) in groups of
-// 8 rows whose loads are issued together.
 template <int SPE>
+__device__ __forceinline__ constexpr bool lane_is_live(int b) {
+    return SPE == 2 ? (b >= 2) : (SPE == 1 ? (b & 1) == 1 : true);
+}
+
+// One wave per unit, one thread per 32-bit column (4 lanes).  Rows are taken
+// from the top of the unit down (the reference's reverse order), 8 row loads
+// in flight per thread.  DEDUP: lanes of masked planes are not coded; their
+// headers come from the canonical streams.
+template <int SPE, bool DEDUP>
 __global__ void __launch_bounds__(256) encode_kernel(const uint8_t* __restrict__ src, EncodeGeom g, uint64_t u0,
                                                      uint64_t nb, const EncSym* __restrict__ d_enc,
+                                                     const uint32_t* __restrict__ canon, uint32_t cw,
                                                      uint32_t* __restrict__ scratch,
                                                      ckr_stream_header* __restrict__ hdrs,
                                                      uint8_t* __restrict__ sidecar) {
@@ -278,7 +327,7 @@ __global__ void __launch_bounds__(256) encode_kernel(const uint8_t* __restrict__
 
     LaneOut o[4];
 #pragma unroll
-    for (int b = 0; b < 4; b++) { o[b].x = L; o[b].acc = 0; o[b].nacc = 0; o[b].w = 0; }
+    for (int b = 0; b < 4; b++) lane_init(o[b]);
 
     const uint64_t col = 4ull * j;
     const uint64_t K = (len > col) ? (len - col + 255) / 256 : 0;
@@ -286,7 +335,7 @@ __global__ void __launch_bounds__(256) encode_kernel(const uint8_t* __restrict__
         // top row: may be partial
         const uint64_t k = K - 1;
         const uint64_t p = 256 * k + col;
-        uint32_t nvalid = (uint32_t)((len - p) < 4 ? (len - p) : 4);
+        const uint32_t nvalid = (uint32_t)((len - p) < 4 ? (len - p) : 4);
         uint32_t v = 0;
         if (nvalid == 4) v = *reinterpret_cast<const uint32_t*>(usrc + p);
         else for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)usrc[p + b] << (8 * b);
@@ -294,7 +343,8 @@ __global__ void __launch_bounds__(256) encode_kernel(const uint8_t* __restrict__
         v &= lm;
 #pragma unroll
         for (int b = 0; b < 4; b++)
-            if ((uint32_t)b < nvalid) encode_symbol(o[b], (v >> (8 * b)) & 255u, tab, uscr + 4 * j + b);
+            if ((!DEDUP || lane_is_live<SPE>(b)) && (uint32_t)b < nvalid)
+                encode_symbol<256>(o[b], (v >> (8 * b)) & 255u, tab, uscr + 4 * j + b);
         // full rows, 8 at a time
         int64_t kk = (int64_t)K - 2;
         for (; kk >= 7; kk -= 8) {
@@ -306,7 +356,8 @@ __global__ void __launch_bounds__(256) encode_kernel(const uint8_t* __restrict__
                 if (sidecar && SPE > 0) write_sidecar_row<SPE>(sidecar, ubase + 256 * (uint64_t)(kk - i) + col, r[i], 4);
                 const uint32_t w = r[i] & lm;
 #pragma unroll
-                for (int b = 0; b < 4; b++) encode_symbol(o[b], (w >> (8 * b)) & 255u, tab, uscr + 4 * j + b);
+                for (int b = 0; b < 4; b++)
+                    if (!DEDUP || lane_is_live<SPE>(b)) encode_symbol<256>(o[b], (w >> (8 * b)) & 255u, tab, uscr + 4 * j + b);
             }
         }
         for (; kk >= 0; kk--) {
@@ -314,20 +365,28 @@ __global__ void __launch_bounds__(256) encode_kernel(const uint8_t* __restrict__
             if (sidecar && SPE > 0) write_sidecar_row<SPE>(sidecar, ubase + 256 * (uint64_t)kk + col, r, 4);
             const uint32_t w = r & lm;
 #pragma unroll
-            for (int b = 0; b < 4; b++) encode_symbol(o[b], (w >> (8 * b)) & 255u, tab, uscr + 4 * j + b);
+            for (int b = 0; b < 4; b++)
+                if (!DEDUP || lane_is_live<SPE>(b)) encode_symbol<256>(o[b], (w >> (8 * b)) & 255u, tab, uscr + 4 * j + b);
         }
     }
-    // flush partial accumulators and write headers (buf_offset set by the finalize kernel)
+    // flush pending bytes and write headers (buf_offset is set by the finalize kernel)
     ckr_stream_header* uh = hdrs + u * 256;
 #pragma unroll
     for (int b = 0; b < 4; b++) {
-        uint32_t* lb = uscr + 4 * j + b;
-        if (o[b].nacc) lb[(uint64_t)o[b].w * 256] = o[b].acc;
         ckr_stream_header h;
-        h.final_state = o[b].x;
-        h.byte_count = o[b].w * 4 + o[b].nacc;
         h.buf_offset = 0;
         h.pad = 0;
+        if (DEDUP && !lane_is_live<SPE>(b)) {
+            const uint64_t pb = col + b;
+            const uint32_t Kb = (uint32_t)(len > pb ? (len - pb + 255) / 256 : 0);
+            const uint32_t* ce = canon_entry(canon, cw, Kb);
+            h.final_state = ce[1];
+            h.byte_count = ce[2];
+        } else {
+            lane_flush<256>(o[b], uscr + 4 * j + b);
+            h.final_state = o[b].x;
+            h.byte_count = lane_bytes(o[b]);
+        }
         uh[4 * j + b] = h;
     }
 }
@@ -388,78 +447,122 @@ __global__ void __launch_bounds__(1024) unit_scan_kernel(const uint32_t* __restr
     if (t == 1023) unit_off[u0 + nb] = base + sh[1023];
 }
 
-// Copy every lane stream of a unit to its packed place, or the masked bytes of a
-// raw unit.  One block per unit; wave v copies lanes v, v+4, …
-template <int SPE>
+// Byte sink writing a byte sequence to an arbitrary destination with 32-bit
+// stores once the destination is aligned (byte stores only at the ends).
+struct ByteSink {
+    uint8_t* d;
+    uint64_t buf;
+    uint32_t nb;
+    __device__ __forceinline__ void drain() {
+        while (nb > 0 && (reinterpret_cast<uintptr_t>(d) & 3u)) { *d++ = (uint8_t)buf; buf >>= 8; nb--; }
+        while (nb >= 4) { *reinterpret_cast<uint32_t*>(d) = (uint32_t)buf; d += 4; buf >>= 32; nb -= 4; }
+    }
+    __device__ __forceinline__ void push(uint32_t v, uint32_t n) {
+        buf |= (uint64_t)v << (8 * nb);
+        nb += n;
+        drain();
+    }
+    __device__ __forceinline__ void finish() {
+        while (nb > 0) { *d++ = (uint8_t)buf; buf >>= 8; nb--; }
+    }
+};
+
+// Push one lane stream (slot format: partial dword of r bytes at slot W, then
+// slots W-1 .. 0) into the sink.
+__device__ __forceinline__ void sink_stream(ByteSink& s, const uint32_t* base, uint32_t stride, uint32_t B) {
+    const uint32_t W = B >> 2, r = B & 3;
+    if (r) s.push(base[(uint64_t)W * stride] & ((1u << (8 * r)) - 1u), r);
+    for (uint32_t w = W; w-- > 0;) s.push(base[(uint64_t)w * stride], 4);
+}
+
+// Pack every lane stream of a unit to its place, or the masked bytes of a raw
+// unit.  One wave per unit; thread j writes the contiguous bytes of lanes
+// 4j..4j+3 (zero-plane lanes from the canonical streams when DEDUP).
+template <int SPE, bool DEDUP>
 __global__ void __launch_bounds__(256) compact_kernel(const uint8_t* __restrict__ src, EncodeGeom g, uint64_t u0,
-                                                      const uint32_t* __restrict__ scratch,
+                                                      uint64_t nb, const uint32_t* __restrict__ scratch,
+                                                      const uint32_t* __restrict__ canon, uint32_t cw,
                                                       const ckr_stream_header* __restrict__ hdrs,
                                                       const uint32_t* __restrict__ unit_size,
                                                       const uint64_t* __restrict__ unit_off,
                                                       uint8_t* __restrict__ out) {
-    const uint64_t ub = blockIdx.x;
+    const uint32_t j = threadIdx.x & 63;
+    const uint64_t ub = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (ub >= nb) return;
     const uint64_t u = u0 + ub;
     const uint64_t ubase = u * g.unit;
     const uint64_t len = (g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit;
     uint8_t* dst = out + unit_off[u];
     const ckr_stream_header* uh = hdrs + u * 256;
-    const bool raw = (uint64_t)unit_size[ub] == len && uh[0].byte_count == (uint32_t)len && uh[0].final_state == 0;
-    if (raw) {
-        for (uint64_t p = threadIdx.x; p < len; p += 256) {
-            const uint8_t b = src[ubase + p];
-            dst[p] = byte_live(p, g.es, g.spe) ? b : 0;
+    if ((uint64_t)unit_size[ub] == len && uh[0].byte_count == (uint32_t)len && uh[0].final_state == 0) {
+        // raw unit: masked bytes, 256 B per row
+        for (uint64_t p = 4ull * j; p < len; p += 256) {
+            const uint32_t nvalid = (uint32_t)((len - p) < 4 ? (len - p) : 4);
+            for (uint32_t b = 0; b < nvalid; b++) {
+                const uint8_t v = src[ubase + p + b];
+                dst[p + b] = byte_live(p + b, g.es, g.spe) ? v : 0;
+            }
         }
         return;
     }
-    const uint8_t* uscr = reinterpret_cast<const uint8_t*>(scratch + ub * (uint64_t)g.wmax * 256);
-    const uint32_t wv = threadIdx.x >> 6, li = threadIdx.x & 63;
-    for (uint32_t l = wv; l < 256; l += 4) {
-        const ckr_stream_header h = uh[l];
-        const uint32_t B = h.byte_count, W = B >> 2, r = B & 3;
-        uint8_t* d = dst + h.buf_offset;
-        for (uint32_t q = li; q < B; q += 64) {
-            uint32_t slot, byte;
-            if (q < r) { slot = W; byte = q; }
-            else { const uint32_t q2 = q - r; slot = W - 1 - (q2 >> 2); byte = q2 & 3; }
-            d[q] = uscr[((uint64_t)slot * 256 + l) * 4 + byte];
+    const uint32_t* uscr = scratch + ub * (uint64_t)g.wmax * 256;
+    ByteSink s;
+    s.d = dst + uh[4 * j].buf_offset;
+    s.buf = 0;
+    s.nb = 0;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        const uint32_t B = uh[4 * j + b].byte_count;
+        if (DEDUP && !lane_is_live<SPE>(b)) {
+            const uint64_t pb = 4ull * j + b;
+            const uint32_t Kb = (uint32_t)(len > pb ? (len - pb + 255) / 256 : 0);
+            sink_stream(s, canon_entry(canon, cw, Kb) + 4, 1, B);
+        } else {
+            sink_stream(s, uscr + 4 * j + b, 256, B);
         }
     }
+    s.finish();
 }
 
-hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t u0, uint64_t nb,
-                               const EncSym* d_enc, uint32_t* scratch, ckr_stream_header* hdrs,
-                               uint8_t* sidecar, uint32_t* unit_size, uint64_t* unit_off, uint8_t* out,
-                               hipStream_t s) {
+hipError_t launch_canon(const EncSym* d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw, uint32_t* canon,
+                        hipStream_t s) {
+    CKR_LAUNCH("canon_kernel", s, canon_kernel<<<1, 64, 0, s>>>(d_enc, k0, k1, k2, cw, canon));
+    return hipGetLastError();
+}
+
+template <int SPE, bool DEDUP>
+static hipError_t encode_batch_t(const uint8_t* src, const EncodeGeom& g, uint64_t u0, uint64_t nb,
+                                 const EncSym* d_enc, const uint32_t* canon, uint32_t cw, uint32_t* scratch,
+                                 ckr_stream_header* hdrs, uint8_t* sidecar, uint32_t* unit_size, uint64_t* unit_off,
+                                 uint8_t* out, hipStream_t s) {
     const uint32_t grid = (uint32_t)((nb + 3) / 4);
-    if (g.spe == 2) CKR_LAUNCH("encode_kernel", s, encode_kernel<2><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, scratch, hdrs, sidecar));
-    else if (g.spe == 1) CKR_LAUNCH("encode_kernel", s, encode_kernel<1><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, scratch, hdrs, sidecar));
-    else CKR_LAUNCH("encode_kernel", s, encode_kernel<0><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, scratch, hdrs, nullptr));
+    CKR_LAUNCH("encode_kernel", s, encode_kernel<SPE, DEDUP><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     CKR_LAUNCH("unit_finalize_kernel", s, unit_finalize_kernel<<<(uint32_t)nb, 256, 0, s>>>(g, u0, hdrs, unit_size));
     if ((e = hipGetLastError()) != hipSuccess) return e;
     CKR_LAUNCH("unit_scan_kernel", s, unit_scan_kernel<<<1, 1024, 0, s>>>(unit_size, u0, nb, unit_off));
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    if (g.spe == 2) CKR_LAUNCH("compact_kernel", s, compact_kernel<2><<<(uint32_t)nb, 256, 0, s>>>(src, g, u0, scratch, hdrs, unit_size, unit_off, out));
-    else if (g.spe == 1) CKR_LAUNCH("compact_kernel", s, compact_kernel<1><<<(uint32_t)nb, 256, 0, s>>>(src, g, u0, scratch, hdrs, unit_size, unit_off, out));
-    else CKR_LAUNCH("compact_kernel", s, compact_kernel<0><<<(uint32_t)nb, 256, 0, s>>>(src, g, u0, scratch, hdrs, unit_size, unit_off, out));
+    CKR_LAUNCH("compact_kernel", s, compact_kernel<SPE, DEDUP><<<grid, 256, 0, s>>>(src, g, u0, nb, scratch, canon, cw, hdrs, unit_size, unit_off, out));
     return hipGetLastError();
 }
 
-// ------------------------------------------------------------------ rANS decode
-struct LaneIn {
-    uint32_t x;
-    const uint8_t* p;
-    const uint8_t* end;
-};
+hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t u0, uint64_t nb, const EncSym* d_enc,
+                               const uint32_t* canon, uint32_t cw, bool dedup, uint32_t* scratch,
+                               ckr_stream_header* hdrs, uint8_t* sidecar, uint32_t* unit_size, uint64_t* unit_off,
+                               uint8_t* out, hipStream_t s) {
+    if (g.spe == 2)
+        return dedup ? encode_batch_t<2, true>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, unit_size, unit_off, out, s)
+                     : encode_batch_t<2, false>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, unit_size, unit_off, out, s);
+    if (g.spe == 1)
+        return dedup ? encode_batch_t<1, true>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, unit_size, unit_off, out, s)
+                     : encode_batch_t<1, false>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, unit_size, unit_off, out, s);
+    return encode_batch_t<0, false>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, nullptr, unit_size, unit_off, out, s);
+}
 
-__device__ __forceinline__ uint32_t decode_symbol(LaneIn& in, const uint32_t* tab) {
-    const uint32_t slot = in.x & (M - 1u);
-    const uint32_t e = tab[slot];
-    const uint32_t f = ((e >> 8) & 4095u) + 1u, cum = e >> 20;
-    in.x = f * (in.x >> 12) + slot - cum;
-    while (in.x < L && in.p < in.end) in.x = (in.x << 8) | *in.p++;
-    return e & 255u;
+// ------------------------------------------------------------------ rANS decode
+__device__ __forceinline__ uint32_t unit_len(const EncodeGeom& g, uint64_t ubase) {
+    return (uint32_t)((g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit);
 }
 
 template <int SPE>
@@ -476,34 +579,61 @@ __device__ __forceinline__ uint32_t merge_sidecar_row(const uint8_t* sidecar, ui
     return dec;
 }
 
+// Raw unit: masked bytes | sidecar, written by one wave (thread j: column j).
+template <int SPE>
+__device__ __forceinline__ void decode_raw_unit(const uint8_t* ud, uint64_t ubase, uint32_t len, uint32_t j,
+                                                const uint8_t* sidecar, uint8_t* dst) {
+    for (uint64_t p = 4ull * j; p < len; p += 256) {
+        const uint32_t nvalid = (uint32_t)((len - p) < 4 ? (len - p) : 4);
+        uint32_t v = 0;
+        for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)ud[p + b] << (8 * b);
+        if (SPE > 0) v = merge_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
+        uint8_t* d = dst + ubase + p;
+        if (nvalid == 4) *reinterpret_cast<uint32_t*>(d) = v;
+        else for (uint32_t b = 0; b < nvalid; b++) d[b] = (uint8_t)(v >> (8 * b));
+    }
+}
+
+// General decoder: any unit size; every lane decoded from global memory.  With
+// unit_mask, only units whose mask entry is non-zero are decoded.
+struct LaneIn {
+    uint32_t x;
+    const uint8_t* p;
+    const uint8_t* end;
+};
+
+__device__ __forceinline__ uint32_t decode_symbol(LaneIn& in, const uint32_t* tab) {
+    const uint32_t slot = in.x & (M - 1u);
+    const uint32_t e = tab[slot];
+    const uint32_t f = ((e >> 8) & 4095u) + 1u, cum = e >> 20;
+    in.x = f * (in.x >> 12) + slot - cum;
+    while (in.x < L && in.p < in.end) in.x = (in.x << 8) | *in.p++;
+    return e & 255u;
+}
+
 template <int SPE>
 __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__ data,
                                                      const ckr_stream_header* __restrict__ hdrs,
                                                      const uint64_t* __restrict__ unit_off,
                                                      const uint32_t* __restrict__ d_dec, EncodeGeom g,
                                                      const uint8_t* __restrict__ sidecar,
-                                                     uint8_t* __restrict__ dst, unsigned long long* bad) {
+                                                     uint8_t* __restrict__ dst, unsigned long long* bad,
+                                                     const uint32_t* __restrict__ unit_mask) {
     __shared__ uint32_t tab[4096];
     for (uint32_t i = threadIdx.x; i < 4096; i += 256) tab[i] = d_dec[i];
     __syncthreads();
     const uint32_t j = threadIdx.x & 63;
     const uint64_t u = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (u >= g.n_units) return;
+    if (unit_mask && unit_mask[u] == 0) return;
     const uint64_t ubase = u * g.unit;
-    const uint64_t len = (g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit;
+    const uint32_t len = unit_len(g, ubase);
     const uint8_t* ud = data + unit_off[u];
     const uint64_t usize = unit_off[u + 1] - unit_off[u];
     const ckr_stream_header* uh = hdrs + u * 256;
     const uint64_t col = 4ull * j;
-    uint8_t* udst = dst + ubase;
-    if (usize == len && uh[0].byte_count == (uint32_t)len) {  // raw unit: masked bytes | sidecar
-        for (uint64_t p = col; p < len; p += 256) {
-            const uint32_t nvalid = (uint32_t)((len - p) < 4 ? (len - p) : 4);
-            uint32_t v = 0;
-            for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)ud[p + b] << (8 * b);
-            if (SPE > 0) v = merge_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
-            for (uint32_t b = 0; b < nvalid; b++) udst[p + b] = (uint8_t)(v >> (8 * b));
-        }
+    if (usize == len && uh[0].byte_count == len) {
+        decode_raw_unit<SPE>(ud, ubase, len, j, sidecar, dst);
         return;
     }
     LaneIn in[4];
@@ -521,6 +651,7 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
         }
     }
     const uint64_t K = (len > col) ? (len - col + 255) / 256 : 0;
+    uint8_t* udst = dst + ubase;
     for (uint64_t k = 0; k < K; k++) {
         const uint64_t p = 256 * k + col;
         const uint32_t nvalid = (uint32_t)((len - p) < 4 ? (len - p) : 4);
@@ -531,13 +662,169 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
             if (SPE > 0) v = merge_sidecar_row<SPE>(sidecar, ubase + p, v, 4);
             *reinterpret_cast<uint32_t*>(udst + p) = v;
         } else {
-            for (uint32_t b = 0; b < nvalid; b++) v |= decode_symbol(in[b], tab) << (8 * b);
+#pragma unroll
+            for (int b = 0; b < 4; b++)
+                if ((uint32_t)b < nvalid) v |= decode_symbol(in[b], tab) << (8 * b);
             if (SPE > 0) v = merge_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
             for (uint32_t b = 0; b < nvalid; b++) udst[p + b] = (uint8_t)(v >> (8 * b));
         }
     }
 #pragma unroll
     for (int b = 0; b < 4; b++) nbad += (in[b].x != L || in[b].p != in[b].end) ? 1u : 0u;
+    if (nbad) atomicAdd(bad, (unsigned long long)nbad);
+}
+
+// Fast decoder for units of at most 64 KiB with masked planes (spe > 0).
+// Block = 4 waves, one unit per wave; LDS holds the decode table (16 KiB,
+// shared), the canonical zero-plane streams, and per wave the packed bytes of
+// its unit's live lanes (each thread stages the contiguous byte range of the
+// live lanes of its column with 32-bit loads).  Live lanes decode from LDS;
+// zero-plane lanes are checked against the canonical stream (header and
+// bytes) and produce zeros.  A unit whose staged bytes exceed the per-wave
+// budget is left to decode_kernel (marked in unit_mask).
+static constexpr uint32_t FAST_STAGE_BYTES = 34 * 1024;  // per wave
+static constexpr uint32_t FAST_CANON_DWORDS = 3 * (4 + 130);
+
+template <int SPE>
+__global__ void __launch_bounds__(256) decode_fast_kernel(const uint8_t* __restrict__ data,
+                                                          const ckr_stream_header* __restrict__ hdrs,
+                                                          const uint64_t* __restrict__ unit_off,
+                                                          const uint32_t* __restrict__ d_dec,
+                                                          const uint32_t* __restrict__ canon, uint32_t cw,
+                                                          EncodeGeom g, const uint8_t* __restrict__ sidecar,
+                                                          uint8_t* __restrict__ dst, unsigned long long* bad,
+                                                          uint32_t* __restrict__ unit_mask) {
+    extern __shared__ uint32_t lds[];
+    uint32_t* tab = lds;                                   // 4096
+    uint32_t* can = lds + 4096;                            // FAST_CANON_DWORDS
+    uint8_t* stage_all = reinterpret_cast<uint8_t*>(lds + 4096 + FAST_CANON_DWORDS);
+    for (uint32_t i = threadIdx.x; i < 4096; i += 256) tab[i] = d_dec[i];
+    for (uint32_t i = threadIdx.x; i < 3 * (4 + cw); i += 256) can[i] = canon[i];
+    __syncthreads();
+
+    const uint32_t j = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const uint64_t u = (uint64_t)blockIdx.x * 4 + wv;
+    if (u >= g.n_units) return;
+    uint8_t* stage = stage_all + wv * (FAST_STAGE_BYTES + 16);
+    const uint64_t ubase = u * g.unit;
+    const uint32_t len = unit_len(g, ubase);
+    const uint64_t uoff = unit_off[u];
+    const uint8_t* ud = data + uoff;
+    const uint32_t usize = (uint32_t)(unit_off[u + 1] - uoff);
+    const uint8_t* data_end = data + unit_off[g.n_units];
+    const ckr_stream_header* uh = hdrs + u * 256;
+    if (usize == len && uh[0].byte_count == len) {
+        unit_mask[u] = 0;
+        decode_raw_unit<SPE>(ud, ubase, len, j, sidecar, dst);
+        return;
+    }
+    constexpr int FL = SPE == 2 ? 2 : 1;  // first live lane of a column
+    const ckr_stream_header h0 = uh[4 * j + FL];
+    const ckr_stream_header h3 = uh[4 * j + 3];
+    // staged range: [start of lane 4j+FL, end of lane 4j+3), widened to 4-byte alignment
+    const uint32_t r0 = h0.buf_offset, r1 = h3.buf_offset + h3.byte_count;
+    bool bad_range = r1 < r0 || r1 > usize;
+    const uint64_t g0 = (uoff + r0) & ~3ull;
+    const uint64_t g1 = bad_range ? g0 : ((uoff + r1 + 3) & ~3ull);
+    const uint32_t nst = (uint32_t)(g1 - g0);
+    // wave-wide exclusive scan of staged sizes
+    uint32_t incl = nst;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t v = __shfl_up(incl, d, 64);
+        if ((int)j >= d) incl += v;
+    }
+    const uint32_t total = __shfl(incl, 63, 64);
+    if (total > FAST_STAGE_BYTES) {  // leave the unit to decode_kernel
+        if (j == 0) unit_mask[u] = 1;
+        return;
+    }
+    if (j == 0) unit_mask[u] = 0;
+    const uint32_t sbase = incl - nst;  // multiple of 4
+    {
+        const uint32_t* gsrc = reinterpret_cast<const uint32_t*>(data + g0);
+        uint32_t* sdst = reinterpret_cast<uint32_t*>(stage + sbase);
+        const uint32_t nw = nst >> 2;
+        for (uint32_t i = 0; i < nw; i++) {
+            const uint8_t* a = data + g0 + 4ull * i;
+            uint32_t v;
+            if (a + 4 <= data_end) v = gsrc[i];
+            else { v = 0; for (uint32_t b = 0; a + b < data_end; b++) v |= (uint32_t)a[b] << (8 * b); }
+            sdst[i] = v;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // live lanes: LDS byte pointers
+    uint32_t x[2], p[2], e[2];
+    uint32_t nbad = bad_range ? 2u : 0u;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int b = i == 0 ? FL : 3;
+        const ckr_stream_header h = uh[4 * j + b];
+        x[i] = h.final_state;
+        const uint32_t s0 = sbase + (uint32_t)(uoff + h.buf_offset - g0);
+        const bool ok = !bad_range && h.buf_offset >= r0 && (uint64_t)h.buf_offset + h.byte_count <= r1;
+        p[i] = ok ? s0 : sbase;
+        e[i] = ok ? s0 + h.byte_count : sbase;
+        if (!ok && !bad_range) nbad++;
+    }
+    const uint64_t col = 4ull * j;
+    const uint32_t K = len > col ? (uint32_t)((len - col + 255) / 256) : 0u;
+    uint8_t* udst = dst + ubase;
+    for (uint32_t k = 0; k < K; k++) {
+        const uint32_t pos = 256 * k + (uint32_t)col;
+        const uint32_t nvalid = (len - pos) < 4 ? (len - pos) : 4;
+        uint32_t sym[2] = {0u, 0u};
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            if (i == 1 && nvalid < 4) break;  // bf16 top row: lane 4j+3 has one symbol fewer
+            const uint32_t c0 = stage[p[i]], c1 = stage[p[i] + 1];  // speculative: used only if consumed
+            const uint32_t slot = x[i] & (M - 1u);
+            const uint32_t te = tab[slot];
+            const uint32_t f = ((te >> 8) & 4095u) + 1u, cum = te >> 20;
+            uint32_t xx = f * (x[i] >> 12) + slot - cum;
+            const uint32_t t1 = (xx < L && p[i] < e[i]) ? 1u : 0u;
+            xx = t1 ? ((xx << 8) | c0) : xx;
+            const uint32_t t2 = (t1 && xx < L && p[i] + 1 < e[i]) ? 1u : 0u;
+            xx = t2 ? ((xx << 8) | c1) : xx;
+            p[i] += t1 + t2;
+            x[i] = xx;
+            sym[i] = te & 255u;
+        }
+        uint32_t v;
+        if (SPE == 2) v = (sym[0] << 16) | (sym[1] << 24);
+        else v = (sym[0] << 8) | (sym[1] << 24);
+        v = merge_sidecar_row<SPE>(sidecar, ubase + pos, v, nvalid);
+        if (nvalid == 4) *reinterpret_cast<uint32_t*>(udst + pos) = v;
+        else for (uint32_t b = 0; b < nvalid; b++) udst[pos + b] = (uint8_t)(v >> (8 * b));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) nbad += (x[i] != L || p[i] != e[i]) ? 1u : 0u;
+    // zero-plane lanes: header and bytes must be the canonical stream
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        if (lane_is_live<SPE>(b)) continue;
+        const uint64_t pb = col + b;
+        const uint32_t Kb = (uint32_t)(len > pb ? (len - pb + 255) / 256 : 0);
+        const uint32_t* ce = canon_entry(can, cw, Kb);
+        const ckr_stream_header h = uh[4 * j + b];
+        bool ok = h.final_state == ce[1] && h.byte_count == ce[2] &&
+                  (uint64_t)h.buf_offset + h.byte_count <= usize;
+        if (ok) {
+            const uint32_t B = h.byte_count, W = B >> 2, r = B & 3;
+            const uint8_t* gb = ud + h.buf_offset;
+            for (uint32_t q = 0; q < B && ok; q++) {
+                uint32_t slot, byte;
+                if (q < r) { slot = W; byte = q; }
+                else { slot = W - 1 - ((q - r) >> 2); byte = (q - r) & 3; }
+                ok = gb[q] == (uint8_t)(ce[4 + slot] >> (8 * byte));
+            }
+        }
+        nbad += ok ? 0u : 1u;
+    }
     if (nbad) atomicAdd(bad, (unsigned long long)nbad);
 }
 
@@ -550,14 +837,33 @@ hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, hipStream_
     return hipGetLastError();
 }
 
+uint32_t decode_fast_lds_bytes() { return (4096 + FAST_CANON_DWORDS) * 4 + 4 * (FAST_STAGE_BYTES + 16); }
+uint32_t decode_fast_max_cw() { return 130; }
+
 hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
                          const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
-                         unsigned long long* bad, hipStream_t s) {
+                         unsigned long long* bad, const uint32_t* canon, uint32_t cw, uint32_t* unit_mask,
+                         hipStream_t s) {
     const uint32_t grid = (uint32_t)((g.n_units + 3) / 4);
     if (grid == 0) return hipSuccess;
-    if (g.spe == 2) CKR_LAUNCH("decode_kernel", s, decode_kernel<2><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
-    else if (g.spe == 1) CKR_LAUNCH("decode_kernel", s, decode_kernel<1><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
-    else CKR_LAUNCH("decode_kernel", s, decode_kernel<0><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
+    hipError_t e;
+    if (canon && unit_mask && g.spe > 0) {  // fast path, then the general kernel for the units it left
+        const uint32_t lb = decode_fast_lds_bytes();
+        if (g.spe == 2) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_fast_kernel<2>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);
+            CKR_LAUNCH("decode_fast_kernel", s, decode_fast_kernel<2><<<grid, 256, lb, s>>>(data, hdrs, unit_off, d_dec, canon, cw, g, sidecar, dst, bad, unit_mask));
+        } else {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_fast_kernel<1>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);
+            CKR_LAUNCH("decode_fast_kernel", s, decode_fast_kernel<1><<<grid, 256, lb, s>>>(data, hdrs, unit_off, d_dec, canon, cw, g, sidecar, dst, bad, unit_mask));
+        }
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    const uint32_t* mask = (canon && unit_mask && g.spe > 0) ? unit_mask : nullptr;
+    if (g.spe == 2) CKR_LAUNCH("decode_kernel", s, decode_kernel<2><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad, mask));
+    else if (g.spe == 1) CKR_LAUNCH("decode_kernel", s, decode_kernel<1><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad, mask));
+    else CKR_LAUNCH("decode_kernel", s, decode_kernel<0><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad, mask));
     return hipGetLastError();
 }
 

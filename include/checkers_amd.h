@@ -182,6 +182,14 @@ CKR_API uint64_t ckr_analyze_workspace_bytes(const ckr_stats_record* h_records, 
 CKR_API int ckr_analyze(const ckr_stats_record* h_records, uint64_t n,
                         void* d_workspace, uint64_t workspace_bytes, void* stream);
 
+/* ---- path selection, no counterpart in the reference.  With fast paths on
+ * (the default) lanes of masked planes are coded once per lane count (their
+ * streams are identical) and units of at most 64 KiB decode from LDS; off,
+ * every lane is coded and decoded independently from global memory.  Output
+ * bytes are identical either way; tests use this to cover both.  Process-wide;
+ * returns the previous setting. ---- */
+CKR_API int ckr_set_fast_paths(int enable);
+
 /* ---- per-kernel timing, no counterpart in the reference (its only timings are
  * host wall clocks, ANSCompressor.hpp:105-110).  Between begin and end every
  * kernel the library launches is bracketed by HIP events on its stream; end

@@ -45,6 +45,12 @@ CASES = [
     ("i8_const", dg.I8, 3000, 512, lambda n: np.full(n, 7, np.int8)),
     ("i32_small", dg.I32, 50000, 65536, lambda n: np.random.default_rng(10).integers(-3, 4, n).astype(np.int32)),
     ("adversarial_f32", dg.F32, 300000, 65536, lambda n: dg.adversarial_f32(n, 11, (100000, 150000))),
+    ("random_bits_f32", dg.F32, 16384 * 4, 65536,  # live lanes ~9 bits/symbol: decode staging overflows
+     lambda n: np.random.default_rng(13).integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32).view(np.float32)),
+    ("random_bits_bf16", dg.BF16, 32768 * 2 + 6, 65536,
+     lambda n: np.random.default_rng(14).integers(0, 2**16, n).astype(np.uint16)),
+    ("f32_1mib_units", dg.F32, 262144 * 2 + 4097, 1 << 20, lambda n: dg.normal_f32(n, 1e-3, 15)),
+    ("bf16_partial_units", dg.BF16, 3 * 512 + 1, 1024, lambda n: dg.normal_bf16(n, 0.02, 16)),
     ("tiny_f32_1", dg.F32, 1, 65536, lambda n: np.array([1.5], np.float32)),
     ("tiny_bf16_3", dg.BF16, 3, 0, lambda n: dg.normal_bf16(n, 0.02, 12)),
     ("tiny_i8_255", dg.I8, 255, 0, lambda n: np.arange(n, dtype=np.uint8).view(np.int8)),
@@ -54,12 +60,20 @@ CASES = [
 ]
 
 
+@pytest.fixture(params=[True, False], ids=["fast", "general"])
+def paths(request):
+    ck = _ck()
+    prev = ck.set_fast_paths(request.param)
+    yield request.param
+    ck.set_fast_paths(prev)
+
+
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_compress_parity_and_roundtrip(case, gpu):
+def test_compress_parity_and_roundtrip(case, paths, gpu):
     import torch
     ck = _ck()
     name, dt, n, unit, gen = case
-    print(f"[case] {name} dtype={dt} n={n} unit={unit}", flush=True)
+    print(f"[case] {name} dtype={dt} n={n} unit={unit} fast={paths}", flush=True)
     raw = gen(n)
     ref = oc.compress_tensor(raw, n, dt, unit)
     src = _to_dev(raw, gpu)
