@@ -43,11 +43,22 @@ __global__ void __launch_bounds__(256) build_enc_table_kernel(TableArg t, EncSym
     out[s] = e;
 }
 
-// Decode slots from norm/cum: slot j in [cum[s], cum[s]+norm[s]) → s.
+// Decode slots from norm/cum: slot j in [cum[s], cum[s]+norm[s]) → s.  One
+// thread per slot (16 blocks of 256): the symbol is the last s with cum[s] <= j
+// and norm[s] > 0, found by binary search over the prefix sums.
 __global__ void __launch_bounds__(256) build_dec_table_kernel(TableArg t, uint32_t* out) {
-    const uint32_t s = threadIdx.x;
-    const uint32_t f = t.norm[s], cum = t.cum[s];
-    for (uint32_t j = cum; j < cum + f && j < M; j++) out[j] = s | ((f - 1u) << 8) | (cum << 20);
+    __shared__ uint32_t cum[257];
+    for (uint32_t i = threadIdx.x; i < 257; i += 256) cum[i] = t.cum[i];
+    __syncthreads();
+    const uint32_t j = blockIdx.x * 256 + threadIdx.x;
+    // largest s with cum[s] <= j < cum[s+1] (empty symbols have cum[s] == cum[s+1])
+    uint32_t lo = 0, hi = 256;
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (cum[mid] <= j) lo = mid; else hi = mid;
+    }
+    const uint32_t f = t.norm[lo];
+    if (j < cum[256] && f) out[j] = lo | ((f - 1u) << 8) | (cum[lo] << 20);
 }
 
 // ------------------------------------------------------------------ byte-plane split
@@ -245,8 +256,8 @@ __device__ __forceinline__ void encode_symbol(LaneOut& o, uint32_t sym, const En
         push_bytes<STRIDE>(o, v, n, lane_base);
     }
     const uint32_t xr = e2 ? (x1 >> 8) : x1;
-    const uint32_t q = __umulhi(xr, e.rcp) >> (e.cmpl_rsh >> 16);
-    o.x = xr + e.bias + q * (e.cmpl_rsh & 0xFFFFu);
+    const uint32_t q = __umulhi(xr, e.rcp) >> (e.cmpl_rsh >> 16);  // q < 2^19 after renormalisation
+    o.x = xr + e.bias + __umul24(q, e.cmpl_rsh & 0xFFFFu);
 }
 
 template <uint32_t STRIDE>
@@ -263,12 +274,15 @@ __device__ __forceinline__ uint32_t lane_bytes(const LaneOut& o) { return o.w * 
 __global__ void canon_kernel(const EncSym* __restrict__ d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw,
                              uint32_t* __restrict__ canon) {
     const uint32_t t = threadIdx.x;
+    __shared__ EncSym e0[1];
+    if (t == 0) e0[0] = d_enc[0];
+    __syncthreads();
     if (t >= 3) return;
     const uint32_t K = t == 0 ? k0 : (t == 1 ? k1 : k2);
     uint32_t* base = canon + (uint64_t)t * (4 + cw);
     LaneOut o;
     lane_init(o);
-    for (uint32_t k = 0; k < K; k++) encode_symbol<1>(o, 0u, d_enc, base + 4);
+    for (uint32_t k = 0; k < K; k++) encode_symbol<1>(o, 0u, e0, base + 4);
     lane_flush<1>(o, base + 4);
     base[0] = K;
     base[1] = o.x;
@@ -468,11 +482,19 @@ struct ByteSink {
 };
 
 // Push one lane stream (slot format: partial dword of r bytes at slot W, then
-// slots W-1 .. 0) into the sink.
+// slots W-1 .. 0) into the sink; slot loads are issued 16 at a time.
 __device__ __forceinline__ void sink_stream(ByteSink& s, const uint32_t* base, uint32_t stride, uint32_t B) {
     const uint32_t W = B >> 2, r = B & 3;
     if (r) s.push(base[(uint64_t)W * stride] & ((1u << (8 * r)) - 1u), r);
-    for (uint32_t w = W; w-- > 0;) s.push(base[(uint64_t)w * stride], 4);
+    uint32_t w = W;
+    for (; w >= 16; w -= 16) {
+        uint32_t v[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) v[k] = base[(uint64_t)(w - 1 - k) * stride];
+#pragma unroll
+        for (int k = 0; k < 16; k++) s.push(v[k], 4);
+    }
+    while (w-- > 0) s.push(base[(uint64_t)w * stride], 4);
 }
 
 // Pack every lane stream of a unit to its place, or the masked bytes of a raw
@@ -699,7 +721,24 @@ __global__ void __launch_bounds__(256) decode_fast_kernel(const uint8_t* __restr
     uint32_t* can = lds + 4096;                            // FAST_CANON_DWORDS
     uint8_t* stage_all = reinterpret_cast<uint8_t*>(lds + 4096 + FAST_CANON_DWORDS);
     for (uint32_t i = threadIdx.x; i < 4096; i += 256) tab[i] = d_dec[i];
-    for (uint32_t i = threadIdx.x; i < 3 * (4 + cw); i += 256) can[i] = canon[i];
+    // canonical entries: header words as they are, then the stream in byte order
+    for (uint32_t i = threadIdx.x; i < 3 * (4 + cw); i += 256) {
+        const uint32_t ent = i / (4 + cw), w = i % (4 + cw);
+        if (w < 4) { can[i] = canon[i]; continue; }
+        // stream dword d (bytes 4d..4d+3) assembled from the slot format
+        const uint32_t* ce = canon + ent * (4 + cw);
+        const uint32_t B = ce[2], W = B >> 2, r = B & 3, d = w - 4;
+        uint32_t v = 0;
+        for (uint32_t b = 0; b < 4; b++) {
+            const uint32_t q = 4 * d + b;
+            if (q >= B) break;
+            uint32_t slot, byte;
+            if (q < r) { slot = W; byte = q; }
+            else { slot = W - 1 - ((q - r) >> 2); byte = (q - r) & 3; }
+            v |= ((ce[4 + slot] >> (8 * byte)) & 255u) << (8 * b);
+        }
+        can[i] = v;
+    }
     __syncthreads();
 
     const uint32_t j = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -742,14 +781,25 @@ __global__ void __launch_bounds__(256) decode_fast_kernel(const uint8_t* __restr
     if (j == 0) unit_mask[u] = 0;
     const uint32_t sbase = incl - nst;  // multiple of 4
     {
+        // 16 loads in flight per thread; only the very last dword of the packed
+        // data can reach past its end and is read bytewise
         const uint32_t* gsrc = reinterpret_cast<const uint32_t*>(data + g0);
         uint32_t* sdst = reinterpret_cast<uint32_t*>(stage + sbase);
         const uint32_t nw = nst >> 2;
-        for (uint32_t i = 0; i < nw; i++) {
+        const uint32_t nsafe = (data + g0 + 4ull * nw <= data_end) ? nw : (nw ? nw - 1 : 0);
+        uint32_t i = 0;
+        for (; i + 16 <= nsafe; i += 16) {
+            uint32_t v[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = gsrc[i + k];
+#pragma unroll
+            for (int k = 0; k < 16; k++) sdst[i + k] = v[k];
+        }
+        for (; i < nsafe; i++) sdst[i] = gsrc[i];
+        for (; i < nw; i++) {
             const uint8_t* a = data + g0 + 4ull * i;
-            uint32_t v;
-            if (a + 4 <= data_end) v = gsrc[i];
-            else { v = 0; for (uint32_t b = 0; a + b < data_end; b++) v |= (uint32_t)a[b] << (8 * b); }
+            uint32_t v = 0;
+            for (uint32_t b = 0; b < 4 && a + b < data_end; b++) v |= (uint32_t)a[b] << (8 * b);
             sdst[i] = v;
         }
     }
@@ -813,15 +863,29 @@ __global__ void __launch_bounds__(256) decode_fast_kernel(const uint8_t* __restr
         const ckr_stream_header h = uh[4 * j + b];
         bool ok = h.final_state == ce[1] && h.byte_count == ce[2] &&
                   (uint64_t)h.buf_offset + h.byte_count <= usize;
-        if (ok) {
-            const uint32_t B = h.byte_count, W = B >> 2, r = B & 3;
-            const uint8_t* gb = ud + h.buf_offset;
-            for (uint32_t q = 0; q < B && ok; q++) {
-                uint32_t slot, byte;
-                if (q < r) { slot = W; byte = q; }
-                else { slot = W - 1 - ((q - r) >> 2); byte = (q - r) & 3; }
-                ok = gb[q] == (uint8_t)(ce[4 + slot] >> (8 * byte));
+        if (ok) {  // compare in 32-bit words, 8 loads in flight
+            const uint8_t* cb = reinterpret_cast<const uint8_t*>(ce + 4);
+            const uint64_t gs = uoff + h.buf_offset, ge = gs + h.byte_count;
+            const uint8_t* dend = data_end;
+            uint32_t diff = 0;
+            for (uint64_t a = gs & ~3ull; a < ge; a += 32) {
+                uint32_t v[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const uint8_t* ga = data + a + 4 * k;
+                    if (a + 4 * k >= ge) v[k] = 0;
+                    else if (ga + 4 <= dend) v[k] = *reinterpret_cast<const uint32_t*>(ga);
+                    else { v[k] = 0; for (uint32_t b = 0; ga + b < dend; b++) v[k] |= (uint32_t)ga[b] << (8 * b); }
+                }
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+#pragma unroll
+                    for (int b = 0; b < 4; b++) {
+                        const uint64_t g = a + 4 * k + b;
+                        if (g >= gs && g < ge) diff |= ((v[k] >> (8 * b)) & 255u) ^ cb[g - gs];
+                    }
             }
+            ok = diff == 0;
         }
         nbad += ok ? 0u : 1u;
     }
@@ -833,7 +897,7 @@ hipError_t launch_build_enc_table(const TableArg& t, EncSym* d_enc, hipStream_t 
     return hipGetLastError();
 }
 hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, hipStream_t s) {
-    CKR_LAUNCH("build_dec_table_kernel", s, build_dec_table_kernel<<<1, 256, 0, s>>>(t, d_dec));
+    CKR_LAUNCH("build_dec_table_kernel", s, build_dec_table_kernel<<<16, 256, 0, s>>>(t, d_dec));
     return hipGetLastError();
 }
 
