@@ -139,9 +139,10 @@ def _check(rc):
         raise CkrError(rc, lib().ckr_last_error().decode())
 
 
-def set_fast_paths(enable):
-    """Select the fast kernels (default) or the general ones; returns the previous setting."""
-    return bool(lib().ckr_set_fast_paths(int(bool(enable))))
+def set_fast_paths(mode):
+    """1: fast kernels (default); 0: general kernels; 2: fast kernels with minimal
+    LDS lane slots (overflow route).  Returns the previous mode."""
+    return int(lib().ckr_set_fast_paths(int(mode)))
 
 
 def profile_begin():

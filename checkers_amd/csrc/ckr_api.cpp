@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <map>
 #include <mutex>
@@ -92,14 +93,58 @@ CanonKs canon_ks(const ckr::EncodeGeom& g) {
     return c;
 }
 constexpr uint32_t kDedupMaxK = 4096;  // zero-plane dedup up to 1 MiB units
-bool g_fast_paths = true;              // ckr_set_fast_paths
+constexpr uint32_t kFastMaxK = 256;    // LDS-staged encode / decode up to 64 KiB units
+int g_fast_paths = 1;                  // ckr_set_fast_paths: 0 general, 1 fast, 2 fast with minimal LDS slots
 
 bool use_dedup(const ckr::EncodeGeom& g) {
     return g_fast_paths && g.spe > 0 && g.n_units > 0 && (g.unit + 255) / 256 <= kDedupMaxK;
 }
+bool use_fast_encode(const ckr::EncodeGeom& g) { return use_dedup(g) && (g.unit + 255) / 256 <= kFastMaxK; }
 
+int max_lds_per_block() {
+    static int v = -1;
+    if (v < 0) {
+        int dev = 0, x = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&x, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+            x = 64 * 1024;
+        v = x;
+    }
+    return v;
+}
+
+// LDS bytes reserved per live lane: the expected coded size of K symbols under
+// the table plus six standard deviations (from the plane's histogram), or, with
+// no histogram, K times the dearest symbol's cost.  A lane that still overflows
+// only sends its unit through the general kernels.
+uint32_t lane_slot_bytes(const uint32_t* plane_hist, const ckr_freq_table* t, uint32_t K) {
+    double cost[256];
+    for (int s = 0; s < 256; s++)
+        cost[s] = t->norm_freq[s] ? std::log2((double)CKR_M / (double)t->norm_freq[s]) : 8.0;
+    double bits;
+    if (plane_hist) {
+        double n = 0, m = 0, v = 0;
+        for (int s = 0; s < 256; s++) { n += plane_hist[s]; m += plane_hist[s] * cost[s]; }
+        if (n == 0) return 8;
+        m /= n;
+        for (int s = 0; s < 256; s++) v += plane_hist[s] * (cost[s] - m) * (cost[s] - m);
+        v /= n;
+        bits = K * m + 6.0 * std::sqrt(K * v) + 32.0;
+    } else {
+        double mx = 0;
+        for (int s = 0; s < 256; s++) mx = std::max(mx, t->norm_freq[s] ? cost[s] : 0.0);
+        bits = K * std::max(mx, 8.0) + 32.0;
+    }
+    uint64_t bytes = (uint64_t)std::ceil(bits / 8.0) + 8;
+    bytes = (bytes + 3) & ~3ull;
+    return (uint32_t)std::min<uint64_t>(std::max<uint64_t>(bytes, 8), 2ull * K + 8);
+}
+
+// Encode workspace: tables, histograms, canonical streams, the fast path's
+// look-back state and redo list, and lane scratch for general-kernel batches
+// (sized for the whole tensor's units, capped by kScratchBudget).
 struct EncodeLayout {
-    uint64_t off_enc, off_hist, off_canon, off_usize, off_scratch, total;
+    uint64_t off_enc, off_hist, off_canon, off_status, off_ctl, off_redo, off_usize, off_scratch, total;
     uint64_t batch_units;
 };
 
@@ -112,8 +157,11 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     const CanonKs ck = canon_ks(g);
     uint64_t o = 0;
     L.off_enc = o;     o = align_up(o + 256 * sizeof(ckr::EncSym), kAlign);
-    L.off_hist = o;    o = align_up(o + 256 * 4, kAlign);
-    L.off_canon = o;   o = align_up(o + (use_dedup(g) ? 3ull * (4 + ck.cw) * 4 : 0), kAlign);
+    L.off_hist = o;    o = align_up(o + 768 * 4, kAlign);
+    L.off_canon = o;   o = align_up(o + 3ull * (4 + ck.cw) * 4, kAlign);
+    L.off_status = o;  o = align_up(o + g.n_units * 8, kAlign);
+    L.off_ctl = o;     o = align_up(o + 16, kAlign);
+    L.off_redo = o;    o = align_up(o + g.n_units * 4, kAlign);
     L.off_usize = o;   o = align_up(o + bu * 4, kAlign);
     L.off_scratch = o; o = align_up(o + bu * per_unit, kAlign);
     L.total = o;
@@ -128,7 +176,7 @@ struct DecodeLayout {
 DecodeLayout decode_layout(const ckr::EncodeGeom& g) {
     DecodeLayout L{};
     const CanonKs ck = canon_ks(g);
-    L.fast = g_fast_paths && g.spe > 0 && g.n_units > 0 && ck.cw <= ckr::decode_fast_max_cw();
+    L.fast = g_fast_paths != 0 && g.spe > 0 && g.n_units > 0 && ck.cw <= ckr::decode_fast_max_cw();
     uint64_t o = 0;
     L.off_enc = o;   o = align_up(o + 256 * sizeof(ckr::EncSym), kAlign);
     L.off_canon = o; o = align_up(o + (L.fast ? 3ull * (4 + ck.cw) * 4 : 0), kAlign);
@@ -219,9 +267,9 @@ int ckr_profile_end(char* buf, uint64_t buflen) {
 
 const char* ckr_last_error(void) { return g_last_error.c_str(); }
 
-int ckr_set_fast_paths(int enable) {
-    const int prev = g_fast_paths ? 1 : 0;
-    g_fast_paths = enable != 0;
+int ckr_set_fast_paths(int mode) {
+    const int prev = g_fast_paths;
+    g_fast_paths = (mode < 0 || mode > 2) ? 1 : mode;
     return prev;
 }
 const char* ckr_version(void) { return "checkers_amd 0.1 gfx950"; }
@@ -260,7 +308,7 @@ int ckr_byte_histogram(const void* d_src, uint64_t n_elems, int dtype, uint32_t*
     if (n_elems && !aligned16(d_src)) return fail(CKR_E_INVALID, "[ckr] source must be 16-byte aligned");
     const int es = ckr_element_size(dtype);
     CKR_HIP(ckr::launch_masked_hist(static_cast<const uint8_t*>(d_src), n_elems * (uint64_t)es, es,
-                                    ckr_sidecar_bytes_per_elem(dtype), d_hist, (hipStream_t)stream));
+                                    ckr_sidecar_bytes_per_elem(dtype), d_hist, nullptr, (hipStream_t)stream));
     return CKR_OK;
 }
 
@@ -342,10 +390,16 @@ uint64_t ckr_encode_workspace_bytes(uint64_t n_elems, int dtype, uint64_t unit_b
     return encode_layout(g).total;
 }
 
-int ckr_encode(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table, uint64_t unit_bytes,
-               uint8_t* d_out, uint64_t out_capacity, ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
-               uint8_t* d_sidecar, void* d_workspace, uint64_t workspace_bytes, uint64_t* h_total_out,
-               void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Encode with an optional pair of live-plane histograms (host) used to size the
+// fast path's LDS slots.
+int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table, uint64_t unit_bytes,
+                uint8_t* d_out, uint64_t out_capacity, ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
+                uint8_t* d_sidecar, void* d_workspace, uint64_t workspace_bytes, uint64_t* h_total_out,
+                const uint32_t* h_planes, void* stream) {
     if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
     ckr::EncodeGeom g;
     if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
@@ -375,19 +429,65 @@ int ckr_encode(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_ta
     auto* scratch = reinterpret_cast<uint32_t*>(ws + L.off_scratch);
     const bool dedup = use_dedup(g);
     const CanonKs ck = canon_ks(g);
+    uint8_t* side = g.spe ? d_sidecar : nullptr;
     CKR_HIP(ckr::launch_build_enc_table(ta, enc, s));
     if (dedup) CKR_HIP(ckr::launch_canon(enc, ck.k0, ck.k1, ck.k2, ck.cw, canon, s));
-    for (uint64_t u0 = 0; u0 < g.n_units; u0 += L.batch_units) {
-        const uint64_t nb = std::min<uint64_t>(L.batch_units, g.n_units - u0);
-        CKR_HIP(ckr::launch_encode_batch(static_cast<const uint8_t*>(d_src), g, u0, nb, enc, canon, ck.cw, dedup,
-                                         scratch, d_headers, g.spe ? d_sidecar : nullptr, usize, d_unit_offsets,
-                                         d_out, s));
+
+    bool fast = use_fast_encode(g);
+    ckr::FastEncParamsHost fp{};
+    if (fast) {
+        const uint32_t K = (uint32_t)((g.unit + 255) / 256);
+        fp.cw = ck.cw;
+        fp.canon_bytes = 4 * ck.cw;
+        if (g_fast_paths == 2) {
+            fp.sl0 = fp.sl1 = 8;
+        } else {
+            fp.sl0 = lane_slot_bytes(h_planes, h_table, K);
+            fp.sl1 = lane_slot_bytes(h_planes ? h_planes + 256 : nullptr, h_table, K);
+        }
+        fast = (int)ckr::encode_fast_lds_bytes(fp) <= max_lds_per_block();
+    }
+    if (fast) {
+        auto* status = reinterpret_cast<uint64_t*>(ws + L.off_status);
+        auto* ctl = reinterpret_cast<uint32_t*>(ws + L.off_ctl);
+        auto* redo = reinterpret_cast<uint32_t*>(ws + L.off_redo);
+        CKR_HIP(ckr::launch_encode_fast(static_cast<const uint8_t*>(d_src), g, enc, canon, fp, d_headers, side, d_out,
+                                        d_unit_offsets, status, ctl, redo, s));
+        uint32_t hctl[4];
+        CKR_HIP(hipMemcpyAsync(hctl, ctl, sizeof(hctl), hipMemcpyDeviceToHost, s));
+        CKR_HIP(hipStreamSynchronize(s));
+        if (hctl[2]) return fail(CKR_E_HIP, "[ckr] encode look-back did not complete (flag %u)", hctl[2]);
+        // units whose lanes outgrew their LDS slots: bytes from the general kernels,
+        // at the offsets the fast kernel published
+        for (uint64_t r0 = 0; r0 < hctl[1]; r0 += L.batch_units) {
+            const uint64_t nb = std::min<uint64_t>(L.batch_units, hctl[1] - r0);
+            CKR_HIP(ckr::launch_encode_batch(static_cast<const uint8_t*>(d_src), g, r0, nb, enc, canon, ck.cw, true,
+                                             scratch, d_headers, nullptr, usize, d_unit_offsets, d_out, redo, s));
+        }
+    } else {
+        for (uint64_t u0 = 0; u0 < g.n_units; u0 += L.batch_units) {
+            const uint64_t nb = std::min<uint64_t>(L.batch_units, g.n_units - u0);
+            CKR_HIP(ckr::launch_encode_batch(static_cast<const uint8_t*>(d_src), g, u0, nb, enc, canon, ck.cw, dedup,
+                                             scratch, d_headers, side, usize, d_unit_offsets, d_out, nullptr, s));
+        }
     }
     if (h_total_out) {
         CKR_HIP(hipMemcpyAsync(h_total_out, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
         CKR_HIP(hipStreamSynchronize(s));
     }
     return CKR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ckr_encode(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table, uint64_t unit_bytes,
+               uint8_t* d_out, uint64_t out_capacity, ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
+               uint8_t* d_sidecar, void* d_workspace, uint64_t workspace_bytes, uint64_t* h_total_out,
+               void* stream) {
+    return encode_impl(d_src, n_elems, dtype, h_table, unit_bytes, d_out, out_capacity, d_headers, d_unit_offsets,
+                       d_sidecar, d_workspace, workspace_bytes, h_total_out, nullptr, stream);
 }
 
 int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_bytes, int ensure_full_alphabet,
@@ -401,19 +501,21 @@ int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_b
     if (!d_workspace || workspace_bytes < L.total)
         return fail(CKR_E_CAPACITY, "[ckr] workspace too small (%llu < %llu)", (unsigned long long)workspace_bytes,
                     (unsigned long long)L.total);
+    if (n_elems && (!d_src || !aligned16(d_src))) return fail(CKR_E_INVALID, "[ckr] source must be 16-byte aligned");
     hipStream_t s = (hipStream_t)stream;
     uint32_t* d_hist = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(d_workspace) + L.off_hist);
-    int rc = ckr_byte_histogram(d_src, n_elems, dtype, d_hist, stream);
-    if (rc) return rc;
-    uint32_t hh[256];
+    const int es = ckr_element_size(dtype);
+    CKR_HIP(ckr::launch_masked_hist(static_cast<const uint8_t*>(d_src), n_elems * (uint64_t)es, es, g.spe, d_hist,
+                                    d_hist + 256, s));
+    uint32_t hh[768];
     CKR_HIP(hipMemcpyAsync(hh, d_hist, sizeof(hh), hipMemcpyDeviceToHost, s));
     CKR_HIP(hipStreamSynchronize(s));
     ckr_freq_table local;
     ckr_freq_table* t = h_table ? h_table : &local;
-    rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
+    int rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
     if (rc) return rc;
-    return ckr_encode(d_src, n_elems, dtype, t, unit_bytes, d_out, out_capacity, d_headers, d_unit_offsets,
-                      d_sidecar, d_workspace, workspace_bytes, h_total_out, stream);
+    return encode_impl(d_src, n_elems, dtype, t, unit_bytes, d_out, out_capacity, d_headers, d_unit_offsets,
+                       d_sidecar, d_workspace, workspace_bytes, h_total_out, g.spe ? hh + 256 : nullptr, stream);
 }
 
 uint64_t ckr_decode_workspace_bytes(uint64_t n_elems, int dtype, uint64_t unit_bytes) {

@@ -50,10 +50,11 @@ hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, hipStream_
 hipError_t launch_extract_mantissa(const uint8_t* src, uint64_t n_elems, int es, int spe,
                                    uint8_t* masked, uint8_t* sidecar, hipStream_t s);
 
-// Masked histogram into d_hist[256] (overwritten).
+// Masked histogram into d_hist[256] (overwritten); for masked dtypes, when
+// d_planes is not null, d_planes[512] receives the two live planes' histograms.
 uint32_t hist_num_blocks(uint64_t n_bytes);
 hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int spe, uint32_t* d_hist,
-                              hipStream_t s);
+                              uint32_t* d_planes, hipStream_t s);
 hipError_t launch_set_u64(uint64_t* p, uint64_t v, hipStream_t s);
 hipError_t launch_set_counter(unsigned long long* p, unsigned long long v, hipStream_t s);
 
@@ -65,10 +66,25 @@ struct EncodeGeom {
     uint32_t wmax;      // dword slots per lane in scratch
     int es, spe;
 };
+// ulist: when non-null, the batch is units ulist[u0 .. u0+nb) (offsets already
+// known: no scan); otherwise units [u0, u0+nb).
 hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t u0, uint64_t nb,
                                const EncSym* d_enc, const uint32_t* canon, uint32_t cw, bool dedup,
                                uint32_t* scratch, ckr_stream_header* hdrs, uint8_t* sidecar,
-                               uint32_t* unit_size, uint64_t* unit_off, uint8_t* out, hipStream_t s);
+                               uint32_t* unit_size, uint64_t* unit_off, uint8_t* out, const uint32_t* ulist,
+                               hipStream_t s);
+
+// LDS-staged encode of all units (masked dtypes, units <= 64 KiB).  status:
+// n_units u64, ctl: 4 u32 ({ticket, redo count, error, 0}), redo_list: n_units
+// u32 — units whose bytes must then be produced by launch_encode_batch.
+struct FastEncParamsHost {
+    uint32_t sl0, sl1, cw, canon_bytes;
+};
+uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p);
+hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
+                              const FastEncParamsHost& hp, ckr_stream_header* hdrs, uint8_t* sidecar, uint8_t* out,
+                              uint64_t* unit_off, uint64_t* status, uint32_t* ctl, uint32_t* redo_list,
+                              hipStream_t s);
 
 // Canonical zero-plane streams for lane counts k0, k1, k2 (3 entries of 4 + cw dwords).
 hipError_t launch_canon(const EncSym* d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw, uint32_t* canon,

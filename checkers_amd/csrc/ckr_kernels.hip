@@ -125,23 +125,37 @@ hipError_t launch_extract_mantissa(const uint8_t* src, uint64_t n_elems, int es,
 // with integer atomics (order-independent, so the result is deterministic).
 static constexpr uint32_t HIST_COPIES = 32;
 
+// LDS slot of a count: raw dtypes 32 copies of one histogram; masked dtypes 16
+// copies of each of the two live planes (rank 0: byte 2 of fp32 / byte 1 of a
+// 16-bit pair, rank 1: byte 3), so per-plane histograms come for free.
+template <int SPE>
+__device__ __forceinline__ uint32_t hist_slot(uint32_t bin, uint32_t rank, uint32_t c) {
+    if (SPE == 0) return bin * HIST_COPIES + c;
+    return (rank * 256 + bin) * 16 + (c & 15);
+}
+
 template <int SPE>
 __device__ __forceinline__ void hist_add_dword(uint32_t* sh, uint32_t v, uint32_t c) {
 #pragma unroll
     for (int b = 0; b < 4; b++) {
         if (SPE == 2 && b < 2) continue;
         if (SPE == 1 && (b & 1) == 0) continue;
-        atomicAdd(&sh[((v >> (8 * b)) & 255u) * HIST_COPIES + c], 1u);
+        atomicAdd(&sh[hist_slot<SPE>((v >> (8 * b)) & 255u, b == 3 ? 1u : 0u, c)], 1u);
     }
 }
 
-__global__ void __launch_bounds__(256) hist_init_kernel(uint32_t* __restrict__ hist, uint64_t zero_count) {
+// hist[256]: total, the zero planes counted in closed form into bin 0;
+// planes[512] (optional, masked dtypes): the two live planes.
+__global__ void __launch_bounds__(256) hist_init_kernel(uint32_t* __restrict__ hist, uint64_t zero_count,
+                                                        uint32_t* __restrict__ planes) {
     hist[threadIdx.x] = (threadIdx.x == 0) ? (uint32_t)zero_count : 0u;
+    if (planes) { planes[threadIdx.x] = 0; planes[256 + threadIdx.x] = 0; }
 }
 
 template <int SPE>
 __global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restrict__ src, uint64_t n_bytes,
-                                                          int es, uint32_t* __restrict__ hist) {
+                                                          int es, uint32_t* __restrict__ hist,
+                                                          uint32_t* __restrict__ planes) {
     __shared__ uint32_t sh[256 * HIST_COPIES];
     for (uint32_t i = threadIdx.x; i < 256 * HIST_COPIES; i += blockDim.x) sh[i] = 0;
     __syncthreads();
@@ -167,15 +181,33 @@ __global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restr
         hist_add_dword<SPE>(sh, a.z, c); hist_add_dword<SPE>(sh, a.w, c);
     }
     if (blockIdx.x == 0) {  // tail bytes
-        for (uint64_t p = nvec * 16 + threadIdx.x; p < n_bytes; p += blockDim.x)
-            if ((int)(p % (uint64_t)es) >= SPE) atomicAdd(&sh[(uint32_t)src[p] * HIST_COPIES + c], 1u);
+        for (uint64_t p = nvec * 16 + threadIdx.x; p < n_bytes; p += blockDim.x) {
+            const int plane = (int)(p % (uint64_t)es);
+            if (plane < SPE) continue;
+            const uint32_t r = (SPE > 0 && (p & 3) == 3) ? 1u : 0u;  // live-plane rank
+            atomicAdd(&sh[hist_slot<SPE>((uint32_t)src[p], r, c)], 1u);
+        }
     }
     __syncthreads();
-    uint32_t sum = 0;
     const uint32_t bin = threadIdx.x;
+    if (SPE == 0) {
+        uint32_t sum = 0;
 #pragma unroll 8
-    for (uint32_t k = 0; k < HIST_COPIES; k++) sum += sh[bin * HIST_COPIES + ((k + bin) & (HIST_COPIES - 1))];
-    if (sum) atomicAdd(&hist[bin], sum);
+        for (uint32_t k = 0; k < HIST_COPIES; k++) sum += sh[bin * HIST_COPIES + ((k + bin) & (HIST_COPIES - 1))];
+        if (sum) atomicAdd(&hist[bin], sum);
+    } else {
+        uint32_t s0 = 0, s1 = 0;
+#pragma unroll 8
+        for (uint32_t k = 0; k < 16; k++) {
+            s0 += sh[hist_slot<SPE>(bin, 0, (k + bin) & 15)];
+            s1 += sh[hist_slot<SPE>(bin, 1, (k + bin) & 15)];
+        }
+        if (s0 + s1) atomicAdd(&hist[bin], s0 + s1);
+        if (planes) {  // per live plane, rank 0 / rank 1
+            if (s0) atomicAdd(&planes[bin], s0);
+            if (s1) atomicAdd(&planes[256 + bin], s1);
+        }
+    }
 }
 
 uint32_t hist_num_blocks(uint64_t n_bytes) {
@@ -187,16 +219,17 @@ uint32_t hist_num_blocks(uint64_t n_bytes) {
 }
 
 hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int spe, uint32_t* d_hist,
-                              hipStream_t s) {
+                              uint32_t* d_planes, hipStream_t s) {
     const uint64_t zero_count = (es > 0) ? (n_bytes / (uint64_t)es) * (uint64_t)spe : 0;
-    CKR_LAUNCH("hist_init_kernel", s, hist_init_kernel<<<1, 256, 0, s>>>(d_hist, zero_count));
+    if (spe == 0) d_planes = nullptr;
+    CKR_LAUNCH("hist_init_kernel", s, hist_init_kernel<<<1, 256, 0, s>>>(d_hist, zero_count, d_planes));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (n_bytes == 0) return hipSuccess;
     const uint32_t nblk = hist_num_blocks(n_bytes);
-    if (spe == 2) CKR_LAUNCH("masked_hist_kernel", s, masked_hist_kernel<2><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist));
-    else if (spe == 1) CKR_LAUNCH("masked_hist_kernel", s, masked_hist_kernel<1><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist));
-    else CKR_LAUNCH("masked_hist_kernel", s, masked_hist_kernel<0><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist));
+    if (spe == 2) CKR_LAUNCH("masked_hist_kernel", s, masked_hist_kernel<2><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist, d_planes));
+    else if (spe == 1) CKR_LAUNCH("masked_hist_kernel", s, masked_hist_kernel<1><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist, d_planes));
+    else CKR_LAUNCH("masked_hist_kernel", s, masked_hist_kernel<0><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist, nullptr));
     return hipGetLastError();
 }
 
@@ -324,7 +357,8 @@ __global__ void __launch_bounds__(256) encode_kernel(const uint8_t* __restrict__
                                                      const uint32_t* __restrict__ canon, uint32_t cw,
                                                      uint32_t* __restrict__ scratch,
                                                      ckr_stream_header* __restrict__ hdrs,
-                                                     uint8_t* __restrict__ sidecar) {
+                                                     uint8_t* __restrict__ sidecar,
+                                                     const uint32_t* __restrict__ ulist) {
     __shared__ EncSym tab[256];
     tab[threadIdx.x] = d_enc[threadIdx.x];
     __syncthreads();
@@ -332,7 +366,7 @@ __global__ void __launch_bounds__(256) encode_kernel(const uint8_t* __restrict__
     const uint32_t j = threadIdx.x & 63;
     const uint64_t ub = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // unit within batch
     if (ub >= nb) return;
-    const uint64_t u = u0 + ub;
+    const uint64_t u = ulist ? (uint64_t)ulist[u0 + ub] : u0 + ub;
     const uint64_t ubase = u * g.unit;
     const uint64_t len = (g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit;
     const uint8_t* usrc = src + ubase;
@@ -409,9 +443,10 @@ __global__ void __launch_bounds__(256) encode_kernel(const uint8_t* __restrict__
 // passthrough decision (packed size >= unit length ⇒ raw, ANSCompressor.cpp:694-713).
 __global__ void __launch_bounds__(256) unit_finalize_kernel(EncodeGeom g, uint64_t u0,
                                                             ckr_stream_header* __restrict__ hdrs,
-                                                            uint32_t* __restrict__ unit_size) {
+                                                            uint32_t* __restrict__ unit_size,
+                                                            const uint32_t* __restrict__ ulist) {
     __shared__ uint32_t sc[256];
-    const uint64_t u = u0 + blockIdx.x;
+    const uint64_t u = ulist ? (uint64_t)ulist[u0 + blockIdx.x] : u0 + blockIdx.x;
     const uint64_t ubase = u * g.unit;
     const uint64_t len = (g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit;
     const uint32_t t = threadIdx.x;
@@ -507,11 +542,12 @@ __global__ void __launch_bounds__(256) compact_kernel(const uint8_t* __restrict_
                                                       const ckr_stream_header* __restrict__ hdrs,
                                                       const uint32_t* __restrict__ unit_size,
                                                       const uint64_t* __restrict__ unit_off,
-                                                      uint8_t* __restrict__ out) {
+                                                      uint8_t* __restrict__ out,
+                                                      const uint32_t* __restrict__ ulist) {
     const uint32_t j = threadIdx.x & 63;
     const uint64_t ub = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (ub >= nb) return;
-    const uint64_t u = u0 + ub;
+    const uint64_t u = ulist ? (uint64_t)ulist[u0 + ub] : u0 + ub;
     const uint64_t ubase = u * g.unit;
     const uint64_t len = (g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit;
     uint8_t* dst = out + unit_off[u];
@@ -556,30 +592,337 @@ template <int SPE, bool DEDUP>
 static hipError_t encode_batch_t(const uint8_t* src, const EncodeGeom& g, uint64_t u0, uint64_t nb,
                                  const EncSym* d_enc, const uint32_t* canon, uint32_t cw, uint32_t* scratch,
                                  ckr_stream_header* hdrs, uint8_t* sidecar, uint32_t* unit_size, uint64_t* unit_off,
-                                 uint8_t* out, hipStream_t s) {
+                                 uint8_t* out, const uint32_t* ulist, hipStream_t s) {
     const uint32_t grid = (uint32_t)((nb + 3) / 4);
-    CKR_LAUNCH("encode_kernel", s, encode_kernel<SPE, DEDUP><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar));
+    CKR_LAUNCH("encode_kernel", s, encode_kernel<SPE, DEDUP><<<grid, 256, 0, s>>>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, ulist));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    CKR_LAUNCH("unit_finalize_kernel", s, unit_finalize_kernel<<<(uint32_t)nb, 256, 0, s>>>(g, u0, hdrs, unit_size));
+    CKR_LAUNCH("unit_finalize_kernel", s, unit_finalize_kernel<<<(uint32_t)nb, 256, 0, s>>>(g, u0, hdrs, unit_size, ulist));
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    CKR_LAUNCH("unit_scan_kernel", s, unit_scan_kernel<<<1, 1024, 0, s>>>(unit_size, u0, nb, unit_off));
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    CKR_LAUNCH("compact_kernel", s, compact_kernel<SPE, DEDUP><<<grid, 256, 0, s>>>(src, g, u0, nb, scratch, canon, cw, hdrs, unit_size, unit_off, out));
+    if (!ulist) {  // a redo batch keeps the offsets the fast kernel published
+        CKR_LAUNCH("unit_scan_kernel", s, unit_scan_kernel<<<1, 1024, 0, s>>>(unit_size, u0, nb, unit_off));
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    CKR_LAUNCH("compact_kernel", s, compact_kernel<SPE, DEDUP><<<grid, 256, 0, s>>>(src, g, u0, nb, scratch, canon, cw, hdrs, unit_size, unit_off, out, ulist));
     return hipGetLastError();
 }
 
 hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t u0, uint64_t nb, const EncSym* d_enc,
                                const uint32_t* canon, uint32_t cw, bool dedup, uint32_t* scratch,
                                ckr_stream_header* hdrs, uint8_t* sidecar, uint32_t* unit_size, uint64_t* unit_off,
-                               uint8_t* out, hipStream_t s) {
+                               uint8_t* out, const uint32_t* ulist, hipStream_t s) {
     if (g.spe == 2)
-        return dedup ? encode_batch_t<2, true>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, unit_size, unit_off, out, s)
-                     : encode_batch_t<2, false>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, unit_size, unit_off, out, s);
+        return dedup ? encode_batch_t<2, true>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, unit_size, unit_off, out, ulist, s)
+                     : encode_batch_t<2, false>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, unit_size, unit_off, out, ulist, s);
     if (g.spe == 1)
-        return dedup ? encode_batch_t<1, true>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, unit_size, unit_off, out, s)
-                     : encode_batch_t<1, false>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, unit_size, unit_off, out, s);
-    return encode_batch_t<0, false>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, nullptr, unit_size, unit_off, out, s);
+        return dedup ? encode_batch_t<1, true>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, unit_size, unit_off, out, ulist, s)
+                     : encode_batch_t<1, false>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, sidecar, unit_size, unit_off, out, ulist, s);
+    return encode_batch_t<0, false>(src, g, u0, nb, d_enc, canon, cw, scratch, hdrs, nullptr, unit_size, unit_off, out, ulist, s);
+}
+
+// ------------------------------------------------------------------ fast encode (LDS-staged, look-back)
+// Units of at most 64 KiB of masked dtypes.  One wave per unit (taken in order
+// from a ticket counter), one thread per 32-bit column, coding only the two
+// live lanes of its column.  Each live lane emits into LDS (plane-major,
+// interleaved by 32-bit words across the 64 columns so that threads emitting
+// their e-th byte hit different banks); the zero-plane lanes are the canonical
+// streams.  When the unit is coded its size is known, its place in the packed
+// output comes from a decoupled look-back over the units before it, and the
+// packed bytes are written with 32-bit stores that cover whole cache lines.
+// A lane that outgrows its LDS slot keeps counting (sizes, states and headers
+// stay exact) and the unit's bytes are produced afterwards by the general
+// kernels (redo list).
+static constexpr uint64_t LB_AGG = 1ull << 62, LB_PFX = 2ull << 62, LB_VAL = (1ull << 62) - 1;
+static constexpr uint32_t LB_SPIN_LIMIT = 1u << 26;
+
+struct FastEncParams {
+    uint32_t sl0, sl1;      // LDS bytes per lane, live lanes of rank 0 and 1 (multiples of 4)
+    uint32_t cw;            // canonical entry size (dwords after the 4 header words)
+    uint32_t canon_bytes;   // bytes per canonical entry in the LDS copy (stream order)
+};
+
+__device__ __forceinline__ void lds_emit(uint8_t* st, uint32_t& e, uint32_t sl, uint32_t j, uint32_t v) {
+    if (e < sl) st[(((e >> 2) * 64 + j) << 2) + (e & 3)] = (uint8_t)v;
+    e++;
+}
+
+__device__ __forceinline__ void enc_sym_lds(uint32_t& x, uint32_t& e, uint32_t sym, const EncSym* tab, uint8_t* st,
+                                            uint32_t sl, uint32_t j) {
+    const EncSym s = tab[sym];
+    if (s.xmax == 0) {  // f == 0: raw byte, no state update (ANSCompressor.cpp:185-192)
+        lds_emit(st, e, sl, j, sym);
+        return;
+    }
+    if (x >= s.xmax) {
+        lds_emit(st, e, sl, j, x & 255u);
+        x >>= 8;
+        if (x >= s.xmax) {
+            lds_emit(st, e, sl, j, x & 255u);
+            x >>= 8;
+        }
+    }
+    const uint32_t q = __umulhi(x, s.rcp) >> (s.cmpl_rsh >> 16);
+    x = x + s.bias + __umul24(q, s.cmpl_rsh & 0xFFFFu);
+}
+
+__device__ __forceinline__ uint64_t lb_load(const uint64_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void lb_store(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Exclusive prefix of the packed sizes of units [0, u) (one thread).  Every
+// unit before u holds a ticket taken earlier, so it is running or done and
+// will publish; the wait is bounded all the same (error flag, no hang).
+__device__ uint64_t lookback(uint64_t* status, uint64_t u, uint64_t size, uint32_t* err) {
+    if (u == 0) {
+        lb_store(&status[0], LB_PFX | size);
+        return 0;
+    }
+    lb_store(&status[u], LB_AGG | size);
+    uint64_t excl = 0;
+    uint64_t v = u - 1;
+    uint32_t spins = 0;
+    while (true) {
+        const uint64_t st = lb_load(&status[v]);
+        if ((st >> 62) == 0) {
+            if (++spins > LB_SPIN_LIMIT) {
+                atomicOr(err, 1u);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            continue;
+        }
+        excl += st & LB_VAL;
+        if ((st >> 62) == 2 || v == 0) break;
+        v--;
+    }
+    lb_store(&status[u], LB_PFX | (excl + size));
+    return excl;
+}
+
+template <int SPE>
+__global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
+                                                         const EncSym* __restrict__ d_enc,
+                                                         const uint32_t* __restrict__ canon, FastEncParams fp,
+                                                         ckr_stream_header* __restrict__ hdrs,
+                                                         uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out,
+                                                         uint64_t* __restrict__ unit_off,
+                                                         uint64_t* __restrict__ status, uint32_t* __restrict__ ctl,
+                                                         uint32_t* __restrict__ redo_list) {
+    extern __shared__ uint32_t lds[];
+    EncSym* tab = reinterpret_cast<EncSym*>(lds);                  // 1024 dwords
+    uint32_t* loff = lds + 1024;                                     // 260 dwords
+    uint32_t* chdr = loff + 260;                                     // 3 x {K, final_state, bytes, 0}
+    uint8_t* cbytes = reinterpret_cast<uint8_t*>(chdr + 12);         // 3 x canon_bytes, stream order
+    uint8_t* st0 = cbytes + 3 * fp.canon_bytes;                      // 64 * sl0
+    uint8_t* st1 = st0 + 64 * fp.sl0;                                // 64 * sl1
+    const uint32_t j = threadIdx.x;
+
+    for (uint32_t i = j; i < 256; i += 64) tab[i] = d_enc[i];
+    for (uint32_t i = j; i < 3 * fp.canon_bytes; i += 64) {
+        const uint32_t ent = i / fp.canon_bytes, q = i % fp.canon_bytes;
+        const uint32_t* ce = canon + ent * (4 + fp.cw);
+        const uint32_t B = ce[2], W = B >> 2, r = B & 3;
+        uint8_t v = 0;
+        if (q < B) {
+            uint32_t slot, byte;
+            if (q < r) { slot = W; byte = q; }
+            else { slot = W - 1 - ((q - r) >> 2); byte = (q - r) & 3; }
+            v = (uint8_t)(ce[4 + slot] >> (8 * byte));
+        }
+        cbytes[i] = v;
+    }
+    if (j < 12) chdr[j] = canon[(j >> 2) * (4 + fp.cw) + (j & 3)];
+    uint32_t tk = 0;
+    if (j == 0) tk = atomicAdd(&ctl[0], 1u);
+    const uint64_t u = __shfl(tk, 0, 64);
+    __syncthreads();
+    if (u >= g.n_units) return;
+
+    const uint64_t ubase = u * g.unit;
+    const uint32_t len = (uint32_t)((g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit);
+    const uint8_t* usrc = src + ubase;
+    constexpr int FL = SPE == 2 ? 2 : 1;  // byte of the first live lane in a column
+    const uint32_t lm = live_mask32<SPE>();
+    uint32_t x0 = L, x1 = L, e0 = 0, e1 = 0;
+
+    const uint32_t col = 4 * j;
+    const uint32_t K = len > col ? (len - col + 255) / 256 : 0u;
+    if (K > 0) {
+        {   // top row: may be partial (bf16 tail: lane 4j+3 has one symbol fewer)
+            const uint32_t p = 256 * (K - 1) + col;
+            const uint32_t nvalid = (len - p) < 4 ? (len - p) : 4;
+            uint32_t v = 0;
+            if (nvalid == 4) v = *reinterpret_cast<const uint32_t*>(usrc + p);
+            else for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)usrc[p + b] << (8 * b);
+            if (sidecar) write_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
+            v &= lm;
+            enc_sym_lds(x0, e0, (v >> (8 * FL)) & 255u, tab, st0, fp.sl0, j);
+            if (nvalid == 4) enc_sym_lds(x1, e1, v >> 24, tab, st1, fp.sl1, j);
+        }
+        int32_t kk = (int32_t)K - 2;
+        for (; kk >= 7; kk -= 8) {
+            uint32_t r[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) r[i] = *reinterpret_cast<const uint32_t*>(usrc + 256 * (uint32_t)(kk - i) + col);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (sidecar) write_sidecar_row<SPE>(sidecar, ubase + 256 * (uint32_t)(kk - i) + col, r[i], 4);
+                enc_sym_lds(x0, e0, (r[i] >> (8 * FL)) & 255u, tab, st0, fp.sl0, j);
+                enc_sym_lds(x1, e1, r[i] >> 24, tab, st1, fp.sl1, j);
+            }
+        }
+        for (; kk >= 0; kk--) {
+            const uint32_t r = *reinterpret_cast<const uint32_t*>(usrc + 256 * (uint32_t)kk + col);
+            if (sidecar) write_sidecar_row<SPE>(sidecar, ubase + 256 * (uint32_t)kk + col, r, 4);
+            enc_sym_lds(x0, e0, (r >> (8 * FL)) & 255u, tab, st0, fp.sl0, j);
+            enc_sym_lds(x1, e1, r >> 24, tab, st1, fp.sl1, j);
+        }
+    }
+    // byte counts and final states of the four lanes of this column
+    uint32_t cnt[4], fs[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        if (b == FL) { cnt[b] = e0; fs[b] = x0; }
+        else if (b == 3) { cnt[b] = e1; fs[b] = x1; }
+        else {
+            const uint32_t pb = col + b;
+            const uint32_t Kb = len > pb ? (len - pb + 255) / 256 : 0u;
+            const uint32_t* ch = (chdr[0] == Kb) ? chdr : ((chdr[4] == Kb) ? chdr + 4 : chdr + 8);
+            fs[b] = ch[1];
+            cnt[b] = ch[2];
+        }
+    }
+    const uint32_t tsum = cnt[0] + cnt[1] + cnt[2] + cnt[3];
+    uint32_t incl = tsum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t v = __shfl_up(incl, d, 64);
+        if ((int)j >= d) incl += v;
+    }
+    const uint32_t total = __shfl(incl, 63, 64);
+    const uint32_t excl = incl - tsum;
+    const bool raw = total >= len;
+    const uint32_t size = raw ? len : total;
+    const bool over = e0 > fp.sl0 || e1 > fp.sl1;
+    const bool any_over = __ballot(over) != 0;
+
+    uint64_t off0 = 0;
+    if (j == 0) off0 = lookback(status, u, size, &ctl[2]);
+    const uint64_t off = __shfl(off0, 0, 64);
+    if (j == 0) {
+        unit_off[u] = off;
+        if (u + 1 == g.n_units) unit_off[u + 1] = off + size;
+    }
+    // headers (4 per thread, 64 contiguous bytes)
+    {
+        ckr_stream_header* uh = hdrs + u * 256 + 4 * j;
+        uint32_t run = excl;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            ckr_stream_header h;
+            if (raw) {
+                h.final_state = 0; h.byte_count = (j == 0 && b == 0) ? len : 0u; h.buf_offset = 0;
+            } else {
+                h.final_state = fs[b]; h.byte_count = cnt[b]; h.buf_offset = run;
+            }
+            h.pad = 0;
+            uh[b] = h;
+            run += cnt[b];
+        }
+    }
+    uint8_t* dst = out + off;
+    if (raw) {  // masked bytes of the unit, byte stores (rare)
+        for (uint32_t q = j; q < len; q += 64) {
+            const uint8_t v = usrc[q];
+            dst[q] = byte_live(q, g.es, g.spe) ? v : 0;
+        }
+        return;
+    }
+    if (any_over) {  // bytes come from the general kernels
+        if (j == 0) redo_list[atomicAdd(&ctl[1], 1u)] = (uint32_t)u;
+        return;
+    }
+    {
+        uint32_t run = excl;
+#pragma unroll
+        for (int b = 0; b < 4; b++) { loff[4 * j + b] = run; run += cnt[b]; }
+        if (j == 63) loff[256] = total;
+    }
+    __syncthreads();
+    // packed bytes: 32-bit destination words d in [first, last), thread j takes
+    // j, j+64, ...; each byte is found through the lane offsets (cursor L only
+    // moves forward)
+    const uint64_t a0 = reinterpret_cast<uintptr_t>(dst);
+    const uint64_t dfirst = a0 >> 2, dlast = (a0 + size + 3) >> 2;
+    uint32_t Lc = 0;
+    for (uint64_t d = dfirst + j; d < dlast; d += 64) {
+        const int64_t q0 = (int64_t)(d << 2) - (int64_t)a0;
+        uint32_t v = 0, valid = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int64_t q = q0 + b;
+            if (q < 0 || q >= (int64_t)size) continue;
+            const uint32_t qq = (uint32_t)q;
+            while (loff[Lc + 1] <= qq) Lc++;
+            const uint32_t i = qq - loff[Lc];
+            const uint32_t lb = Lc & 3, lc = Lc >> 2;
+            uint32_t byte;
+            if (lb == FL || lb == 3) {
+                const uint32_t B = loff[Lc + 1] - loff[Lc];
+                const uint32_t e = B - 1 - i;
+                const uint8_t* stl = (lb == 3) ? st1 : st0;
+                byte = stl[(((e >> 2) * 64 + lc) << 2) + (e & 3)];
+            } else {
+                const uint32_t pb = Lc;
+                const uint32_t Kb = len > pb ? (len - pb + 255) / 256 : 0u;
+                const uint32_t ent = (chdr[0] == Kb) ? 0u : ((chdr[4] == Kb) ? 1u : 2u);
+                byte = cbytes[ent * fp.canon_bytes + i];
+            }
+            v |= byte << (8 * b);
+            valid |= 1u << b;
+        }
+        uint8_t* w = reinterpret_cast<uint8_t*>(d << 2);
+        if (valid == 15u) *reinterpret_cast<uint32_t*>(w) = v;
+        else
+            for (int b = 0; b < 4; b++)
+                if (valid & (1u << b)) w[b] = (uint8_t)(v >> (8 * b));
+    }
+}
+
+__global__ void encode_fast_reset_kernel(uint64_t* status, uint64_t n, uint32_t* ctl) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) status[i] = 0;
+    if (i < 4) ctl[i] = 0;
+}
+
+uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p) {
+    return 1024 * 4 + 260 * 4 + 12 * 4 + 3 * p.canon_bytes + 64 * (p.sl0 + p.sl1);
+}
+
+hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
+                              const FastEncParamsHost& hp, ckr_stream_header* hdrs, uint8_t* sidecar, uint8_t* out,
+                              uint64_t* unit_off, uint64_t* status, uint32_t* ctl, uint32_t* redo_list,
+                              hipStream_t s) {
+    FastEncParams fp;
+    fp.sl0 = hp.sl0; fp.sl1 = hp.sl1; fp.cw = hp.cw; fp.canon_bytes = hp.canon_bytes;
+    const uint64_t n = g.n_units;
+    CKR_LAUNCH("encode_fast_reset_kernel", s, encode_fast_reset_kernel<<<(uint32_t)((n + 255) / 256), 256, 0, s>>>(status, n, ctl));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t lb = encode_fast_lds_bytes(hp);
+    if (g.spe == 2) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&encode_fast_kernel<2>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);
+        CKR_LAUNCH("encode_fast_kernel", s, encode_fast_kernel<2><<<(uint32_t)n, 64, lb, s>>>(src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status, ctl, redo_list));
+    } else {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&encode_fast_kernel<1>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);
+        CKR_LAUNCH("encode_fast_kernel", s, encode_fast_kernel<1><<<(uint32_t)n, 64, lb, s>>>(src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status, ctl, redo_list));
+    }
+    return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ rANS decode
@@ -824,32 +1167,49 @@ __global__ void __launch_bounds__(256) decode_fast_kernel(const uint8_t* __restr
     const uint64_t col = 4ull * j;
     const uint32_t K = len > col ? (uint32_t)((len - col + 255) / 256) : 0u;
     uint8_t* udst = dst + ubase;
-    for (uint32_t k = 0; k < K; k++) {
-        const uint32_t pos = 256 * k + (uint32_t)col;
-        const uint32_t nvalid = (len - pos) < 4 ? (len - pos) : 4;
-        uint32_t sym[2] = {0u, 0u};
+    for (uint32_t k0 = 0; k0 < K; k0 += 8) {
+        // sidecar words of 8 rows requested before the rows are decoded
+        uint32_t scv[8];
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            if (i == 1 && nvalid < 4) break;  // bf16 top row: lane 4j+3 has one symbol fewer
-            const uint32_t c0 = stage[p[i]], c1 = stage[p[i] + 1];  // speculative: used only if consumed
-            const uint32_t slot = x[i] & (M - 1u);
-            const uint32_t te = tab[slot];
-            const uint32_t f = ((te >> 8) & 4095u) + 1u, cum = te >> 20;
-            uint32_t xx = f * (x[i] >> 12) + slot - cum;
-            const uint32_t t1 = (xx < L && p[i] < e[i]) ? 1u : 0u;
-            xx = t1 ? ((xx << 8) | c0) : xx;
-            const uint32_t t2 = (t1 && xx < L && p[i] + 1 < e[i]) ? 1u : 0u;
-            xx = t2 ? ((xx << 8) | c1) : xx;
-            p[i] += t1 + t2;
-            x[i] = xx;
-            sym[i] = te & 255u;
+        for (int r = 0; r < 8; r++) {
+            const uint32_t k = k0 + r;
+            scv[r] = 0;
+            if (k < K) {
+                const uint32_t pos = 256 * k + (uint32_t)col;
+                const uint32_t nvalid = (len - pos) < 4 ? (len - pos) : 4;
+                scv[r] = merge_sidecar_row<SPE>(sidecar, ubase + pos, 0u, nvalid);
+            }
         }
-        uint32_t v;
-        if (SPE == 2) v = (sym[0] << 16) | (sym[1] << 24);
-        else v = (sym[0] << 8) | (sym[1] << 24);
-        v = merge_sidecar_row<SPE>(sidecar, ubase + pos, v, nvalid);
-        if (nvalid == 4) *reinterpret_cast<uint32_t*>(udst + pos) = v;
-        else for (uint32_t b = 0; b < nvalid; b++) udst[pos + b] = (uint8_t)(v >> (8 * b));
+#pragma unroll
+        for (int r = 0; r < 8; r++) {
+            const uint32_t k = k0 + r;
+            if (k >= K) break;
+            const uint32_t pos = 256 * k + (uint32_t)col;
+            const uint32_t nvalid = (len - pos) < 4 ? (len - pos) : 4;
+            uint32_t sym[2] = {0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                if (i == 1 && nvalid < 4) break;  // bf16 top row: lane 4j+3 has one symbol fewer
+                const uint32_t c0 = stage[p[i]], c1 = stage[p[i] + 1];  // speculative: used only if consumed
+                const uint32_t slot = x[i] & (M - 1u);
+                const uint32_t te = tab[slot];
+                const uint32_t f = ((te >> 8) & 4095u) + 1u, cum = te >> 20;
+                uint32_t xx = f * (x[i] >> 12) + slot - cum;
+                const uint32_t t1 = (xx < L && p[i] < e[i]) ? 1u : 0u;
+                xx = t1 ? ((xx << 8) | c0) : xx;
+                const uint32_t t2 = (t1 && xx < L && p[i] + 1 < e[i]) ? 1u : 0u;
+                xx = t2 ? ((xx << 8) | c1) : xx;
+                p[i] += t1 + t2;
+                x[i] = xx;
+                sym[i] = te & 255u;
+            }
+            uint32_t v;
+            if (SPE == 2) v = (sym[0] << 16) | (sym[1] << 24);
+            else v = (sym[0] << 8) | (sym[1] << 24);
+            v |= scv[r];
+            if (nvalid == 4) *reinterpret_cast<uint32_t*>(udst + pos) = v;
+            else for (uint32_t b = 0; b < nvalid; b++) udst[pos + b] = (uint8_t)(v >> (8 * b));
+        }
     }
 #pragma unroll
     for (int i = 0; i < 2; i++) nbad += (x[i] != L || p[i] != e[i]) ? 1u : 0u;

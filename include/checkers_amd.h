@@ -182,13 +182,15 @@ CKR_API uint64_t ckr_analyze_workspace_bytes(const ckr_stats_record* h_records, 
 CKR_API int ckr_analyze(const ckr_stats_record* h_records, uint64_t n,
                         void* d_workspace, uint64_t workspace_bytes, void* stream);
 
-/* ---- path selection, no counterpart in the reference.  With fast paths on
- * (the default) lanes of masked planes are coded once per lane count (their
- * streams are identical) and units of at most 64 KiB decode from LDS; off,
- * every lane is coded and decoded independently from global memory.  Output
- * bytes are identical either way; tests use this to cover both.  Process-wide;
- * returns the previous setting. ---- */
-CKR_API int ckr_set_fast_paths(int enable);
+/* ---- path selection, no counterpart in the reference.  mode 1 (default):
+ * fast kernels — lanes of masked planes coded once per lane count (their
+ * streams are identical), units of at most 64 KiB coded and decoded through
+ * LDS; mode 0: every lane coded and decoded independently through global
+ * memory; mode 2: fast kernels with minimal LDS lane slots, so that nearly
+ * every unit takes the overflow route back through the general kernels.  The
+ * output bytes are identical in every mode; tests use this to cover all
+ * routes.  Process-wide; returns the previous mode. ---- */
+CKR_API int ckr_set_fast_paths(int mode);
 
 /* ---- per-kernel timing, no counterpart in the reference (its only timings are
  * host wall clocks, ANSCompressor.hpp:105-110).  Between begin and end every

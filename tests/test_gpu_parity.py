@@ -60,7 +60,7 @@ CASES = [
 ]
 
 
-@pytest.fixture(params=[True, False], ids=["fast", "general"])
+@pytest.fixture(params=[1, 0, 2], ids=["fast", "general", "overflow"])
 def paths(request):
     ck = _ck()
     prev = ck.set_fast_paths(request.param)

@@ -104,5 +104,7 @@ def test_argument_errors_are_status_codes():
 
 
 def test_fast_path_switch_round_trips():
-    prev = ck.set_fast_paths(False)
-    assert ck.set_fast_paths(prev) is False
+    prev = ck.set_fast_paths(0)
+    assert ck.set_fast_paths(2) == 0
+    assert ck.set_fast_paths(prev) == 2
+    assert ck.set_fast_paths(prev) == prev
