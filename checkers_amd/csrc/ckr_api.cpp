@@ -158,7 +158,7 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     uint64_t o = 0;
     L.off_enc = o;     o = align_up(o + 256 * sizeof(ckr::EncSym), kAlign);
     L.off_hist = o;    o = align_up(o + 768 * 4, kAlign);
-    L.off_canon = o;   o = align_up(o + 3ull * (4 + ck.cw) * 4, kAlign);
+    L.off_canon = o;   o = align_up(o + 3ull * (4 + 2 * ck.cw) * 4, kAlign);
     L.off_status = o;  o = align_up(o + g.n_units * 8, kAlign);
     L.off_ctl = o;     o = align_up(o + 16, kAlign);
     L.off_redo = o;    o = align_up(o + g.n_units * 4, kAlign);
@@ -179,7 +179,7 @@ DecodeLayout decode_layout(const ckr::EncodeGeom& g) {
     L.fast = g_fast_paths != 0 && g.spe > 0 && g.n_units > 0 && ck.cw <= ckr::decode_fast_max_cw();
     uint64_t o = 0;
     L.off_enc = o;   o = align_up(o + 256 * sizeof(ckr::EncSym), kAlign);
-    L.off_canon = o; o = align_up(o + (L.fast ? 3ull * (4 + ck.cw) * 4 : 0), kAlign);
+    L.off_canon = o; o = align_up(o + (L.fast ? 3ull * (4 + 2 * ck.cw) * 4 : 0), kAlign);
     L.off_dec = o;   o = align_up(o + 4096 * 4, kAlign);
     L.off_bad = o;   o = align_up(o + 8, kAlign);
     L.off_mask = o;  o = align_up(o + (L.fast ? g.n_units * 4 : 0), kAlign);

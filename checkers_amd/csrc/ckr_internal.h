@@ -86,7 +86,9 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
                               uint64_t* unit_off, uint64_t* status, uint32_t* ctl, uint32_t* redo_list,
                               hipStream_t s);
 
-// Canonical zero-plane streams for lane counts k0, k1, k2 (3 entries of 4 + cw dwords).
+// Canonical zero-plane streams for lane counts k0, k1, k2: 3 entries of 4 + cw
+// dwords (header, then the stream in slot format), followed by the 3 streams in
+// byte order (cw dwords each).
 hipError_t launch_canon(const EncSym* d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw, uint32_t* canon,
                         hipStream_t s);
 

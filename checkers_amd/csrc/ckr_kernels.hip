@@ -321,6 +321,21 @@ __global__ void canon_kernel(const EncSym* __restrict__ d_enc, uint32_t k0, uint
     base[1] = o.x;
     base[2] = lane_bytes(o);
     base[3] = 0;
+    // the same stream in byte order (cw dwords per entry after the three entries)
+    uint32_t* sb = canon + 3ull * (4 + cw) + (uint64_t)t * cw;
+    const uint32_t B = lane_bytes(o), W = B >> 2, r = B & 3;
+    for (uint32_t d = 0; d < cw; d++) {
+        uint32_t v = 0;
+        for (uint32_t b = 0; b < 4; b++) {
+            const uint32_t q = 4 * d + b;
+            if (q >= B) break;
+            uint32_t slot, byte;
+            if (q < r) { slot = W; byte = q; }
+            else { slot = W - 1 - ((q - r) >> 2); byte = (q - r) & 3; }
+            v |= ((base[4 + slot] >> (8 * byte)) & 255u) << (8 * b);
+        }
+        sb[d] = v;
+    }
 }
 
 __device__ __forceinline__ const uint32_t* canon_entry(const uint32_t* canon, uint32_t cw, uint32_t K) {
@@ -633,7 +648,7 @@ hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t
 // stay exact) and the unit's bytes are produced afterwards by the general
 // kernels (redo list).
 static constexpr uint64_t LB_AGG = 1ull << 62, LB_PFX = 2ull << 62, LB_VAL = (1ull << 62) - 1;
-static constexpr uint32_t LB_SPIN_LIMIT = 1u << 26;
+static constexpr uint32_t LB_SPIN_LIMIT = 1u << 20;
 
 struct FastEncParams {
     uint32_t sl0, sl1;      // LDS bytes per lane, live lanes of rank 0 and 1 (multiples of 4)
@@ -720,21 +735,25 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
     uint8_t* st1 = st0 + 64 * fp.sl0;                                // 64 * sl1
     const uint32_t j = threadIdx.x;
 
-    for (uint32_t i = j; i < 256; i += 64) tab[i] = d_enc[i];
-    for (uint32_t i = j; i < 3 * fp.canon_bytes; i += 64) {
-        const uint32_t ent = i / fp.canon_bytes, q = i % fp.canon_bytes;
-        const uint32_t* ce = canon + ent * (4 + fp.cw);
-        const uint32_t B = ce[2], W = B >> 2, r = B & 3;
-        uint8_t v = 0;
-        if (q < B) {
-            uint32_t slot, byte;
-            if (q < r) { slot = W; byte = q; }
-            else { slot = W - 1 - ((q - r) >> 2); byte = (q - r) & 3; }
-            v = (uint8_t)(ce[4 + slot] >> (8 * byte));
+    {   // table, canonical headers and canonical streams (byte order), loads batched
+        const uint32_t* d_tab = reinterpret_cast<const uint32_t*>(d_enc);
+        uint32_t tv[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) tv[k] = d_tab[j + 64 * k];
+#pragma unroll
+        for (int k = 0; k < 16; k++) lds[j + 64 * k] = tv[k];
+        const uint32_t* cs = canon + 3 * (4 + fp.cw);
+        uint32_t* cb32 = reinterpret_cast<uint32_t*>(cbytes);
+        const uint32_t ncw = 3 * fp.cw;
+        for (uint32_t i0 = 0; i0 < ncw; i0 += 512) {
+            uint32_t cv[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) { const uint32_t i = i0 + j + 64 * k; cv[k] = i < ncw ? cs[i] : 0u; }
+#pragma unroll
+            for (int k = 0; k < 8; k++) { const uint32_t i = i0 + j + 64 * k; if (i < ncw) cb32[i] = cv[k]; }
         }
-        cbytes[i] = v;
+        if (j < 12) chdr[j] = canon[(j >> 2) * (4 + fp.cw) + (j & 3)];
     }
-    if (j < 12) chdr[j] = canon[(j >> 2) * (4 + fp.cw) + (j & 3)];
     uint32_t tk = 0;
     if (j == 0) tk = atomicAdd(&ctl[0], 1u);
     const uint64_t u = __shfl(tk, 0, 64);
@@ -1063,24 +1082,17 @@ __global__ void __launch_bounds__(256) decode_fast_kernel(const uint8_t* __restr
     uint32_t* tab = lds;                                   // 4096
     uint32_t* can = lds + 4096;                            // FAST_CANON_DWORDS
     uint8_t* stage_all = reinterpret_cast<uint8_t*>(lds + 4096 + FAST_CANON_DWORDS);
-    for (uint32_t i = threadIdx.x; i < 4096; i += 256) tab[i] = d_dec[i];
+    {
+        uint32_t tv[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) tv[k] = d_dec[threadIdx.x + 256 * k];
+#pragma unroll
+        for (int k = 0; k < 16; k++) tab[threadIdx.x + 256 * k] = tv[k];
+    }
     // canonical entries: header words as they are, then the stream in byte order
     for (uint32_t i = threadIdx.x; i < 3 * (4 + cw); i += 256) {
         const uint32_t ent = i / (4 + cw), w = i % (4 + cw);
-        if (w < 4) { can[i] = canon[i]; continue; }
-        // stream dword d (bytes 4d..4d+3) assembled from the slot format
-        const uint32_t* ce = canon + ent * (4 + cw);
-        const uint32_t B = ce[2], W = B >> 2, r = B & 3, d = w - 4;
-        uint32_t v = 0;
-        for (uint32_t b = 0; b < 4; b++) {
-            const uint32_t q = 4 * d + b;
-            if (q >= B) break;
-            uint32_t slot, byte;
-            if (q < r) { slot = W; byte = q; }
-            else { slot = W - 1 - ((q - r) >> 2); byte = (q - r) & 3; }
-            v |= ((ce[4 + slot] >> (8 * byte)) & 255u) << (8 * b);
-        }
-        can[i] = v;
+        can[i] = (w < 4) ? canon[i] : canon[3 * (4 + cw) + ent * cw + (w - 4)];
     }
     __syncthreads();
 
