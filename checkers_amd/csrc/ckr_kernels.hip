@@ -781,23 +781,38 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
             enc_sym_lds(x0, e0, (v >> (8 * FL)) & 255u, tab, st0, fp.sl0, j);
             if (nvalid == 4) enc_sym_lds(x1, e1, v >> 24, tab, st1, fp.sl1, j);
         }
+        // rows K-2 .. 0 in groups of 32; the next group's loads are in flight
+        // while the current group is coded (one wave per SIMD has nothing else
+        // to hide memory latency with)
         int32_t kk = (int32_t)K - 2;
-        for (; kk >= 7; kk -= 8) {
-            uint32_t r[8];
+        uint32_t ra[32], rb[32];
+        // row k of this column: 32 bits at usrc + 256k + 4j; its sidecar: 16 bits at
+        // sidecar + (ubase + 256k + 4j) / 2
+        const uint32_t* in32 = reinterpret_cast<const uint32_t*>(usrc + col);
+        uint16_t* sc16 = sidecar ? reinterpret_cast<uint16_t*>(sidecar + (ubase >> 1) + 2 * j) : nullptr;
+        auto load_rows = [&](uint32_t (&r)[32], int32_t top) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) r[i] = *reinterpret_cast<const uint32_t*>(usrc + 256 * (uint32_t)(kk - i) + col);
+            for (int i = 0; i < 32; i++) r[i] = (top - i >= 0) ? in32[64 * (top - i)] : 0u;
+        };
+        auto code_rows = [&](const uint32_t (&r)[32], int32_t top) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                if (sidecar) write_sidecar_row<SPE>(sidecar, ubase + 256 * (uint32_t)(kk - i) + col, r[i], 4);
+            for (int i = 0; i < 32; i++) {
+                const int32_t k = top - i;
+                if (k < 0) break;
+                if (sc16) sc16[64 * k] = (uint16_t)(SPE == 2 ? (r[i] & 0xFFFFu) : ((r[i] & 0xFFu) | ((r[i] >> 8) & 0xFF00u)));
                 enc_sym_lds(x0, e0, (r[i] >> (8 * FL)) & 255u, tab, st0, fp.sl0, j);
                 enc_sym_lds(x1, e1, r[i] >> 24, tab, st1, fp.sl1, j);
             }
-        }
-        for (; kk >= 0; kk--) {
-            const uint32_t r = *reinterpret_cast<const uint32_t*>(usrc + 256 * (uint32_t)kk + col);
-            if (sidecar) write_sidecar_row<SPE>(sidecar, ubase + 256 * (uint32_t)kk + col, r, 4);
-            enc_sym_lds(x0, e0, (r >> (8 * FL)) & 255u, tab, st0, fp.sl0, j);
-            enc_sym_lds(x1, e1, r >> 24, tab, st1, fp.sl1, j);
+        };
+        if (kk >= 0) load_rows(ra, kk);
+        while (kk >= 0) {
+            if (kk - 32 >= 0) load_rows(rb, kk - 32);
+            code_rows(ra, kk);
+            kk -= 32;
+            if (kk < 0) break;
+            if (kk - 32 >= 0) load_rows(ra, kk - 32);
+            code_rows(rb, kk);
+            kk -= 32;
         }
     }
     // byte counts and final states of the four lanes of this column
@@ -1060,14 +1075,45 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
 
 // Fast decoder for units of at most 64 KiB with masked planes (spe > 0).
 // Block = 4 waves, one unit per wave; LDS holds the decode table (16 KiB,
-// shared), the canonical zero-plane streams, and per wave the packed bytes of
-// its unit's live lanes (each thread stages the contiguous byte range of the
-// live lanes of its column with 32-bit loads).  Live lanes decode from LDS;
-// zero-plane lanes are checked against the canonical stream (header and
-// bytes) and produce zeros.  A unit whose staged bytes exceed the per-wave
-// budget is left to decode_kernel (marked in unit_mask).
-static constexpr uint32_t FAST_STAGE_BYTES = 34 * 1024;  // per wave
+// shared), the canonical zero-plane streams, and per wave its unit's packed
+// bytes, brought in with coalesced 16-byte loads.  Live lanes decode from LDS
+// (two per thread) with the sidecar of the next 32 rows already requested;
+// zero-plane lanes are checked against the canonical stream (header and bytes)
+// and produce zeros.  A unit larger than the per-wave budget is left to
+// decode_kernel (marked in unit_mask).
+static constexpr uint32_t FAST_STAGE_BYTES = 35 * 1024;  // per wave
 static constexpr uint32_t FAST_CANON_DWORDS = 3 * (4 + 130);
+
+// 16 bytes at data[a..a+16) of which only those below data_len exist.
+__device__ __forceinline__ uint4 load_tail16(const uint8_t* data, uint64_t a, uint64_t data_len) {
+    uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
+#pragma unroll
+    for (int b = 0; b < 16; b++) {
+        const uint32_t v = (a + b < data_len) ? (uint32_t)data[a + b] : 0u;
+        if (b < 4) w0 |= v << (8 * b);
+        else if (b < 8) w1 |= v << (8 * (b - 4));
+        else if (b < 12) w2 |= v << (8 * (b - 8));
+        else w3 |= v << (8 * (b - 12));
+    }
+    return make_uint4(w0, w1, w2, w3);
+}
+
+template <int SPE>
+__device__ __forceinline__ uint32_t decode_live_sym(uint32_t& x, uint32_t& p, uint32_t e, const uint8_t* stage,
+                                                    const uint32_t* tab) {
+    const uint32_t c0 = stage[p], c1 = stage[p + 1];  // speculative: used only if consumed
+    const uint32_t slot = x & (M - 1u);
+    const uint32_t te = tab[slot];
+    const uint32_t f = ((te >> 8) & 4095u) + 1u, cum = te >> 20;
+    uint32_t xx = f * (x >> 12) + slot - cum;
+    const uint32_t t1 = (xx < L && p < e) ? 1u : 0u;
+    xx = t1 ? ((xx << 8) | c0) : xx;
+    const uint32_t t2 = (t1 && xx < L && p + 1 < e) ? 1u : 0u;
+    xx = t2 ? ((xx << 8) | c1) : xx;
+    p += t1 + t2;
+    x = xx;
+    return te & 255u;
+}
 
 template <int SPE>
 __global__ void __launch_bounds__(256) decode_fast_kernel(const uint8_t* __restrict__ data,
@@ -1099,129 +1145,109 @@ __global__ void __launch_bounds__(256) decode_fast_kernel(const uint8_t* __restr
     const uint32_t j = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const uint64_t u = (uint64_t)blockIdx.x * 4 + wv;
     if (u >= g.n_units) return;
-    uint8_t* stage = stage_all + wv * (FAST_STAGE_BYTES + 16);
+    uint8_t* stage = stage_all + wv * (FAST_STAGE_BYTES + 32);
     const uint64_t ubase = u * g.unit;
     const uint32_t len = unit_len(g, ubase);
     const uint64_t uoff = unit_off[u];
     const uint8_t* ud = data + uoff;
     const uint32_t usize = (uint32_t)(unit_off[u + 1] - uoff);
-    const uint8_t* data_end = data + unit_off[g.n_units];
+    const uint64_t data_len = unit_off[g.n_units];
     const ckr_stream_header* uh = hdrs + u * 256;
     if (usize == len && uh[0].byte_count == len) {
-        unit_mask[u] = 0;
+        if (j == 0) unit_mask[u] = 0;
         decode_raw_unit<SPE>(ud, ubase, len, j, sidecar, dst);
         return;
     }
-    constexpr int FL = SPE == 2 ? 2 : 1;  // first live lane of a column
-    const ckr_stream_header h0 = uh[4 * j + FL];
-    const ckr_stream_header h3 = uh[4 * j + 3];
-    // staged range: [start of lane 4j+FL, end of lane 4j+3), widened to 4-byte alignment
-    const uint32_t r0 = h0.buf_offset, r1 = h3.buf_offset + h3.byte_count;
-    bool bad_range = r1 < r0 || r1 > usize;
-    const uint64_t g0 = (uoff + r0) & ~3ull;
-    const uint64_t g1 = bad_range ? g0 : ((uoff + r1 + 3) & ~3ull);
-    const uint32_t nst = (uint32_t)(g1 - g0);
-    // wave-wide exclusive scan of staged sizes
-    uint32_t incl = nst;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t v = __shfl_up(incl, d, 64);
-        if ((int)j >= d) incl += v;
-    }
-    const uint32_t total = __shfl(incl, 63, 64);
-    if (total > FAST_STAGE_BYTES) {  // leave the unit to decode_kernel
+    // stage [uoff, uoff+usize) with 16-byte loads from the enclosing aligned blocks
+    const uint64_t gs = uoff & ~15ull, ge = (uoff + usize + 15) & ~15ull;
+    const uint32_t nst = (uint32_t)(ge - gs), shift = (uint32_t)(uoff - gs);
+    if (nst > FAST_STAGE_BYTES) {
         if (j == 0) unit_mask[u] = 1;
         return;
     }
     if (j == 0) unit_mask[u] = 0;
-    const uint32_t sbase = incl - nst;  // multiple of 4
     {
-        // 16 loads in flight per thread; only the very last dword of the packed
-        // data can reach past its end and is read bytewise
-        const uint32_t* gsrc = reinterpret_cast<const uint32_t*>(data + g0);
-        uint32_t* sdst = reinterpret_cast<uint32_t*>(stage + sbase);
-        const uint32_t nw = nst >> 2;
-        const uint32_t nsafe = (data + g0 + 4ull * nw <= data_end) ? nw : (nw ? nw - 1 : 0);
-        uint32_t i = 0;
-        for (; i + 16 <= nsafe; i += 16) {
-            uint32_t v[16];
+        const uint32_t nv = nst >> 4;
+        const uint4* gsrc = reinterpret_cast<const uint4*>(data + gs);
+        uint4* sdst = reinterpret_cast<uint4*>(stage);
+        for (uint32_t i0 = 0; i0 < nv; i0 += 64 * 12) {
+            uint4 v[12];
 #pragma unroll
-            for (int k = 0; k < 16; k++) v[k] = gsrc[i + k];
+            for (int k = 0; k < 12; k++) {
+                const uint32_t i = i0 + j + 64 * k;
+                v[k] = make_uint4(0, 0, 0, 0);
+                if (i < nv) {
+                    if (gs + 16ull * (i + 1) <= data_len) v[k] = gsrc[i];
+                    else v[k] = load_tail16(data, gs + 16ull * i, data_len);  // holds the data's end
+                }
+            }
 #pragma unroll
-            for (int k = 0; k < 16; k++) sdst[i + k] = v[k];
-        }
-        for (; i < nsafe; i++) sdst[i] = gsrc[i];
-        for (; i < nw; i++) {
-            const uint8_t* a = data + g0 + 4ull * i;
-            uint32_t v = 0;
-            for (uint32_t b = 0; b < 4 && a + b < data_end; b++) v |= (uint32_t)a[b] << (8 * b);
-            sdst[i] = v;
+            for (int k = 0; k < 12; k++) {
+                const uint32_t i = i0 + j + 64 * k;
+                if (i < nv) sdst[i] = v[k];
+            }
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // live lanes: LDS byte pointers
+    constexpr int FL = SPE == 2 ? 2 : 1;  // first live lane of a column
     uint32_t x[2], p[2], e[2];
-    uint32_t nbad = bad_range ? 2u : 0u;
+    uint32_t nbad = 0;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int b = i == 0 ? FL : 3;
         const ckr_stream_header h = uh[4 * j + b];
         x[i] = h.final_state;
-        const uint32_t s0 = sbase + (uint32_t)(uoff + h.buf_offset - g0);
-        const bool ok = !bad_range && h.buf_offset >= r0 && (uint64_t)h.buf_offset + h.byte_count <= r1;
-        p[i] = ok ? s0 : sbase;
-        e[i] = ok ? s0 + h.byte_count : sbase;
-        if (!ok && !bad_range) nbad++;
+        const bool ok = (uint64_t)h.buf_offset + h.byte_count <= usize;
+        p[i] = ok ? shift + h.buf_offset : shift;
+        e[i] = ok ? shift + h.buf_offset + h.byte_count : shift;
+        nbad += ok ? 0u : 1u;
     }
     const uint64_t col = 4ull * j;
     const uint32_t K = len > col ? (uint32_t)((len - col + 255) / 256) : 0u;
     uint8_t* udst = dst + ubase;
-    for (uint32_t k0 = 0; k0 < K; k0 += 8) {
-        // sidecar words of 8 rows requested before the rows are decoded
-        uint32_t scv[8];
+    // rows 0 .. K-2 are full 32-bit columns; row K-1 may be partial (bf16 tail)
+    const uint32_t Kf = K ? K - 1 : 0;
+    // sidecar of row k for this column: 16 bits at (ubase + 256k + 4j) / 2
+    const uint16_t* sc16 = reinterpret_cast<const uint16_t*>(sidecar + (ubase >> 1) + 2 * j);
+    uint32_t* out32 = reinterpret_cast<uint32_t*>(udst + col);
+    uint32_t sa[32], sb[32];
+    auto load_sc = [&](uint32_t (&sc)[32], uint32_t k0) {
 #pragma unroll
-        for (int r = 0; r < 8; r++) {
-            const uint32_t k = k0 + r;
-            scv[r] = 0;
-            if (k < K) {
-                const uint32_t pos = 256 * k + (uint32_t)col;
-                const uint32_t nvalid = (len - pos) < 4 ? (len - pos) : 4;
-                scv[r] = merge_sidecar_row<SPE>(sidecar, ubase + pos, 0u, nvalid);
-            }
+        for (int r = 0; r < 32; r++) sc[r] = (k0 + r < Kf) ? (uint32_t)sc16[64 * (k0 + r)] : 0u;
+    };
+    auto decode_rows = [&](const uint32_t (&sc)[32], uint32_t k0) {
+#pragma unroll
+        for (int r = 0; r < 32; r++) {
+            if (k0 + r >= Kf) break;
+            const uint32_t s0 = decode_live_sym<SPE>(x[0], p[0], e[0], stage, tab);
+            const uint32_t s1 = decode_live_sym<SPE>(x[1], p[1], e[1], stage, tab);
+            const uint32_t side = SPE == 2 ? sc[r] : ((sc[r] & 0xFFu) | ((sc[r] & 0xFF00u) << 8));
+            out32[64 * (k0 + r)] = (SPE == 2 ? (s0 << 16) : (s0 << 8)) | (s1 << 24) | side;
         }
-#pragma unroll
-        for (int r = 0; r < 8; r++) {
-            const uint32_t k = k0 + r;
-            if (k >= K) break;
-            const uint32_t pos = 256 * k + (uint32_t)col;
-            const uint32_t nvalid = (len - pos) < 4 ? (len - pos) : 4;
-            uint32_t sym[2] = {0u, 0u};
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                if (i == 1 && nvalid < 4) break;  // bf16 top row: lane 4j+3 has one symbol fewer
-                const uint32_t c0 = stage[p[i]], c1 = stage[p[i] + 1];  // speculative: used only if consumed
-                const uint32_t slot = x[i] & (M - 1u);
-                const uint32_t te = tab[slot];
-                const uint32_t f = ((te >> 8) & 4095u) + 1u, cum = te >> 20;
-                uint32_t xx = f * (x[i] >> 12) + slot - cum;
-                const uint32_t t1 = (xx < L && p[i] < e[i]) ? 1u : 0u;
-                xx = t1 ? ((xx << 8) | c0) : xx;
-                const uint32_t t2 = (t1 && xx < L && p[i] + 1 < e[i]) ? 1u : 0u;
-                xx = t2 ? ((xx << 8) | c1) : xx;
-                p[i] += t1 + t2;
-                x[i] = xx;
-                sym[i] = te & 255u;
-            }
-            uint32_t v;
-            if (SPE == 2) v = (sym[0] << 16) | (sym[1] << 24);
-            else v = (sym[0] << 8) | (sym[1] << 24);
-            v |= scv[r];
-            if (nvalid == 4) *reinterpret_cast<uint32_t*>(udst + pos) = v;
-            else for (uint32_t b = 0; b < nvalid; b++) udst[pos + b] = (uint8_t)(v >> (8 * b));
-        }
+    };
+    uint32_t k0 = 0;
+    if (Kf) load_sc(sa, 0);
+    while (k0 < Kf) {
+        if (k0 + 32 < Kf) load_sc(sb, k0 + 32);
+        decode_rows(sa, k0);
+        k0 += 32;
+        if (k0 >= Kf) break;
+        if (k0 + 32 < Kf) load_sc(sa, k0 + 32);
+        decode_rows(sb, k0);
+        k0 += 32;
+    }
+    if (K) {  // last row
+        const uint32_t pos = 256 * Kf + (uint32_t)col;
+        const uint32_t nvalid = (len - pos) < 4 ? (len - pos) : 4;
+        const uint32_t s0 = decode_live_sym<SPE>(x[0], p[0], e[0], stage, tab);
+        uint32_t s1 = 0;
+        if (nvalid == 4) s1 = decode_live_sym<SPE>(x[1], p[1], e[1], stage, tab);
+        const uint32_t v = merge_sidecar_row<SPE>(sidecar, ubase + pos, (SPE == 2 ? (s0 << 16) : (s0 << 8)) | (s1 << 24), nvalid);
+        if (nvalid == 4) *reinterpret_cast<uint32_t*>(udst + pos) = v;
+        else for (uint32_t b = 0; b < nvalid; b++) udst[pos + b] = (uint8_t)(v >> (8 * b));
     }
 #pragma unroll
     for (int i = 0; i < 2; i++) nbad += (x[i] != L || p[i] != e[i]) ? 1u : 0u;
@@ -1235,28 +1261,11 @@ __global__ void __launch_bounds__(256) decode_fast_kernel(const uint8_t* __restr
         const ckr_stream_header h = uh[4 * j + b];
         bool ok = h.final_state == ce[1] && h.byte_count == ce[2] &&
                   (uint64_t)h.buf_offset + h.byte_count <= usize;
-        if (ok) {  // compare in 32-bit words, 8 loads in flight
+        if (ok) {
             const uint8_t* cb = reinterpret_cast<const uint8_t*>(ce + 4);
-            const uint64_t gs = uoff + h.buf_offset, ge = gs + h.byte_count;
-            const uint8_t* dend = data_end;
+            const uint8_t* sl = stage + shift + h.buf_offset;
             uint32_t diff = 0;
-            for (uint64_t a = gs & ~3ull; a < ge; a += 32) {
-                uint32_t v[8];
-#pragma unroll
-                for (int k = 0; k < 8; k++) {
-                    const uint8_t* ga = data + a + 4 * k;
-                    if (a + 4 * k >= ge) v[k] = 0;
-                    else if (ga + 4 <= dend) v[k] = *reinterpret_cast<const uint32_t*>(ga);
-                    else { v[k] = 0; for (uint32_t b = 0; ga + b < dend; b++) v[k] |= (uint32_t)ga[b] << (8 * b); }
-                }
-#pragma unroll
-                for (int k = 0; k < 8; k++)
-#pragma unroll
-                    for (int b = 0; b < 4; b++) {
-                        const uint64_t g = a + 4 * k + b;
-                        if (g >= gs && g < ge) diff |= ((v[k] >> (8 * b)) & 255u) ^ cb[g - gs];
-                    }
-            }
+            for (uint32_t q = 0; q < h.byte_count; q++) diff |= sl[q] ^ cb[q];
             ok = diff == 0;
         }
         nbad += ok ? 0u : 1u;
@@ -1273,7 +1282,7 @@ hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, hipStream_
     return hipGetLastError();
 }
 
-uint32_t decode_fast_lds_bytes() { return (4096 + FAST_CANON_DWORDS) * 4 + 4 * (FAST_STAGE_BYTES + 16); }
+uint32_t decode_fast_lds_bytes() { return (4096 + FAST_CANON_DWORDS) * 4 + 4 * (FAST_STAGE_BYTES + 32); }
 uint32_t decode_fast_max_cw() { return 130; }
 
 hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
