@@ -99,6 +99,19 @@ int g_fast_paths = 1;                  // ckr_set_fast_paths: 0 general, 1 fast,
 bool use_dedup(const ckr::EncodeGeom& g) {
     return g_fast_paths && g.spe > 0 && g.n_units > 0 && (g.unit + 255) / 256 <= kDedupMaxK;
 }
+// Bytes of the canonical zero-plane stream of K symbols (the state update of
+// rans_encode_kernel, ANSCompressor.cpp:180-202, for symbol 0, whose cum is 0).
+uint32_t canon_stream_bytes(const ckr_freq_table* t, uint32_t K) {
+    const uint32_t f = t->norm_freq[0];
+    if (f == 0) return K;  // every symbol takes the raw-byte escape
+    uint32_t x = CKR_L, bytes = 0;
+    for (uint32_t k = 0; k < K; k++) {
+        while (x >= (f << 19)) { bytes++; x >>= 8; }
+        x = ((x / f) << CKR_SCALE_BITS) + (x % f);
+    }
+    return bytes;
+}
+
 bool use_fast_encode(const ckr::EncodeGeom& g) { return use_dedup(g) && (g.unit + 255) / 256 <= kFastMaxK; }
 
 int max_lds_per_block() {
@@ -438,7 +451,9 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
     if (fast) {
         const uint32_t K = (uint32_t)((g.unit + 255) / 256);
         fp.cw = ck.cw;
-        fp.canon_bytes = 4 * ck.cw;
+        const uint32_t cbmax = std::max(canon_stream_bytes(h_table, ck.k0),
+                                        std::max(canon_stream_bytes(h_table, ck.k1), canon_stream_bytes(h_table, ck.k2)));
+        fp.canon_bytes = std::min<uint32_t>((cbmax + 3) & ~3u, 4 * ck.cw);
         if (g_fast_paths == 2) {
             fp.sl0 = fp.sl1 = 8;
         } else {

@@ -638,41 +638,49 @@ hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t
 // ------------------------------------------------------------------ fast encode (LDS-staged, look-back)
 // Units of at most 64 KiB of masked dtypes.  One wave per unit (taken in order
 // from a ticket counter), one thread per 32-bit column, coding only the two
-// live lanes of its column.  Each live lane emits into LDS (plane-major,
-// interleaved by 32-bit words across the 64 columns so that threads emitting
-// their e-th byte hit different banks); the zero-plane lanes are the canonical
-// streams.  When the unit is coded its size is known, its place in the packed
-// output comes from a decoupled look-back over the units before it, and the
-// packed bytes are written with 32-bit stores that cover whole cache lines.
-// A lane that outgrows its LDS slot keeps counting (sizes, states and headers
-// stay exact) and the unit's bytes are produced afterwards by the general
-// kernels (redo list).
+// live lanes of its column.  Each live lane writes its stream backward into its
+// own LDS slot, so that the stream ends up contiguous and in stream order; the
+// slot stride is chosen so that the 64 threads writing their e-th bytes hit
+// different banks.  The zero-plane lanes are the canonical streams.  When the
+// unit is coded its size is known, its place in the packed output comes from a
+// decoupled look-back over the units before it, and the packed bytes are
+// written in 16-byte chunks (one wave instruction covers 1 KiB of output).
+// A lane that outgrows its slot keeps counting (sizes, states and headers stay
+// exact) and the unit's bytes are produced afterwards by the general kernels
+// (redo list).
 static constexpr uint64_t LB_AGG = 1ull << 62, LB_PFX = 2ull << 62, LB_VAL = (1ull << 62) - 1;
 static constexpr uint32_t LB_SPIN_LIMIT = 1u << 20;
 
 struct FastEncParams {
-    uint32_t sl0, sl1;      // LDS bytes per lane, live lanes of rank 0 and 1 (multiples of 4)
-    uint32_t cw;            // canonical entry size (dwords after the 4 header words)
-    uint32_t canon_bytes;   // bytes per canonical entry in the LDS copy (stream order)
+    uint32_t sl0, sl1;          // LDS slot bytes per lane, live lanes of rank 0 and 1 (multiples of 4)
+    uint32_t stride0, stride1;  // slot strides (slot bytes + bank padding)
+    uint32_t cw;                // canonical entry size (dwords after the 4 header words)
+    uint32_t canon_bytes;       // bytes per canonical entry in the LDS copy (stream order)
 };
 
-__device__ __forceinline__ void lds_emit(uint8_t* st, uint32_t& e, uint32_t sl, uint32_t j, uint32_t v) {
-    if (e < sl) st[(((e >> 2) * 64 + j) << 2) + (e & 3)] = (uint8_t)v;
+// LDS layout (bytes): table 4096 | loff 257 x u32 (+pad) | delta 256 x i32 |
+// canonical headers 12 x u32 | canonical bytes 3 x canon_bytes | rank-0 slots
+// 64 x stride0 | rank-1 slots 64 x stride1 | 32 bytes of read padding.
+static constexpr uint32_t FE_TAB = 0, FE_LOFF = 4096, FE_DELTA = 4096 + 1040, FE_CHDR = 4096 + 1040 + 1024,
+                          FE_CBYTES = FE_CHDR + 48;
+
+__device__ __forceinline__ void lds_emit(uint8_t* slot, uint32_t& e, uint32_t sl, uint32_t v) {
+    if (e < sl) slot[sl - 1 - e] = (uint8_t)v;  // first byte emitted = last byte of the stream
     e++;
 }
 
-__device__ __forceinline__ void enc_sym_lds(uint32_t& x, uint32_t& e, uint32_t sym, const EncSym* tab, uint8_t* st,
-                                            uint32_t sl, uint32_t j) {
+__device__ __forceinline__ void enc_sym_lds(uint32_t& x, uint32_t& e, uint32_t sym, const EncSym* tab, uint8_t* slot,
+                                            uint32_t sl) {
     const EncSym s = tab[sym];
     if (s.xmax == 0) {  // f == 0: raw byte, no state update (ANSCompressor.cpp:185-192)
-        lds_emit(st, e, sl, j, sym);
+        lds_emit(slot, e, sl, sym);
         return;
     }
     if (x >= s.xmax) {
-        lds_emit(st, e, sl, j, x & 255u);
+        lds_emit(slot, e, sl, x & 255u);
         x >>= 8;
         if (x >= s.xmax) {
-            lds_emit(st, e, sl, j, x & 255u);
+            lds_emit(slot, e, sl, x & 255u);
             x >>= 8;
         }
     }
@@ -717,6 +725,24 @@ __device__ uint64_t lookback(uint64_t* status, uint64_t u, uint64_t size, uint32
     return excl;
 }
 
+// 16 LDS bytes from an arbitrary byte address (5 aligned 32-bit reads).
+__device__ __forceinline__ uint4 lds_read16(const uint8_t* lds8, uint32_t a) {
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(lds8 + (a & ~3u));
+    const uint32_t sh = a & 3u;
+    const uint32_t d0 = w[0], d1 = w[1], d2 = w[2], d3 = w[3], d4 = w[4];
+    return make_uint4(__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
+                      __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh));
+}
+
+// Largest lane L with loff[L] <= q (q < loff[256]).
+__device__ __forceinline__ uint32_t lane_of(const uint32_t* loff, uint32_t q) {
+    uint32_t lo = 0;
+#pragma unroll
+    for (uint32_t step = 128; step > 0; step >>= 1)
+        if (loff[lo + step] <= q) lo += step;
+    return lo;
+}
+
 template <int SPE>
 __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
                                                          const EncSym* __restrict__ d_enc,
@@ -727,12 +753,13 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
                                                          uint64_t* __restrict__ status, uint32_t* __restrict__ ctl,
                                                          uint32_t* __restrict__ redo_list) {
     extern __shared__ uint32_t lds[];
-    EncSym* tab = reinterpret_cast<EncSym*>(lds);                  // 1024 dwords
-    uint32_t* loff = lds + 1024;                                     // 260 dwords
-    uint32_t* chdr = loff + 260;                                     // 3 x {K, final_state, bytes, 0}
-    uint8_t* cbytes = reinterpret_cast<uint8_t*>(chdr + 12);         // 3 x canon_bytes, stream order
-    uint8_t* st0 = cbytes + 3 * fp.canon_bytes;                      // 64 * sl0
-    uint8_t* st1 = st0 + 64 * fp.sl0;                                // 64 * sl1
+    uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
+    const EncSym* tab = reinterpret_cast<const EncSym*>(lds8 + FE_TAB);
+    uint32_t* loff = reinterpret_cast<uint32_t*>(lds8 + FE_LOFF);
+    int32_t* delta = reinterpret_cast<int32_t*>(lds8 + FE_DELTA);
+    uint32_t* chdr = reinterpret_cast<uint32_t*>(lds8 + FE_CHDR);
+    const uint32_t st0_off = FE_CBYTES + 3 * fp.canon_bytes;
+    const uint32_t st1_off = st0_off + 64 * fp.stride0;
     const uint32_t j = threadIdx.x;
 
     {   // table, canonical headers and canonical streams (byte order), loads batched
@@ -743,14 +770,18 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
 #pragma unroll
         for (int k = 0; k < 16; k++) lds[j + 64 * k] = tv[k];
         const uint32_t* cs = canon + 3 * (4 + fp.cw);
-        uint32_t* cb32 = reinterpret_cast<uint32_t*>(cbytes);
-        const uint32_t ncw = 3 * fp.cw;
-        for (uint32_t i0 = 0; i0 < ncw; i0 += 512) {
+        uint32_t* cb32 = reinterpret_cast<uint32_t*>(lds8 + FE_CBYTES);
+        const uint32_t ncb = 3 * fp.canon_bytes / 4;
+        const uint32_t cb_per = fp.canon_bytes / 4;
+        for (uint32_t i0 = 0; i0 < ncb; i0 += 512) {
             uint32_t cv[8];
 #pragma unroll
-            for (int k = 0; k < 8; k++) { const uint32_t i = i0 + j + 64 * k; cv[k] = i < ncw ? cs[i] : 0u; }
+            for (int k = 0; k < 8; k++) {
+                const uint32_t i = i0 + j + 64 * k;
+                cv[k] = i < ncb ? cs[(i / cb_per) * fp.cw + (i % cb_per)] : 0u;
+            }
 #pragma unroll
-            for (int k = 0; k < 8; k++) { const uint32_t i = i0 + j + 64 * k; if (i < ncw) cb32[i] = cv[k]; }
+            for (int k = 0; k < 8; k++) { const uint32_t i = i0 + j + 64 * k; if (i < ncb) cb32[i] = cv[k]; }
         }
         if (j < 12) chdr[j] = canon[(j >> 2) * (4 + fp.cw) + (j & 3)];
     }
@@ -765,6 +796,8 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
     const uint8_t* usrc = src + ubase;
     constexpr int FL = SPE == 2 ? 2 : 1;  // byte of the first live lane in a column
     const uint32_t lm = live_mask32<SPE>();
+    uint8_t* slot0 = lds8 + st0_off + j * fp.stride0;
+    uint8_t* slot1 = lds8 + st1_off + j * fp.stride1;
     uint32_t x0 = L, x1 = L, e0 = 0, e1 = 0;
 
     const uint32_t col = 4 * j;
@@ -778,12 +811,11 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
             else for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)usrc[p + b] << (8 * b);
             if (sidecar) write_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
             v &= lm;
-            enc_sym_lds(x0, e0, (v >> (8 * FL)) & 255u, tab, st0, fp.sl0, j);
-            if (nvalid == 4) enc_sym_lds(x1, e1, v >> 24, tab, st1, fp.sl1, j);
+            enc_sym_lds(x0, e0, (v >> (8 * FL)) & 255u, tab, slot0, fp.sl0);
+            if (nvalid == 4) enc_sym_lds(x1, e1, v >> 24, tab, slot1, fp.sl1);
         }
         // rows K-2 .. 0 in groups of 32; the next group's loads are in flight
-        // while the current group is coded (one wave per SIMD has nothing else
-        // to hide memory latency with)
+        // while the current group is coded
         int32_t kk = (int32_t)K - 2;
         uint32_t ra[32], rb[32];
         // row k of this column: 32 bits at usrc + 256k + 4j; its sidecar: 16 bits at
@@ -800,8 +832,8 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
                 const int32_t k = top - i;
                 if (k < 0) break;
                 if (sc16) sc16[64 * k] = (uint16_t)(SPE == 2 ? (r[i] & 0xFFFFu) : ((r[i] & 0xFFu) | ((r[i] >> 8) & 0xFF00u)));
-                enc_sym_lds(x0, e0, (r[i] >> (8 * FL)) & 255u, tab, st0, fp.sl0, j);
-                enc_sym_lds(x1, e1, r[i] >> 24, tab, st1, fp.sl1, j);
+                enc_sym_lds(x0, e0, (r[i] >> (8 * FL)) & 255u, tab, slot0, fp.sl0);
+                enc_sym_lds(x1, e1, r[i] >> 24, tab, slot1, fp.sl1);
             }
         };
         if (kk >= 0) load_rows(ra, kk);
@@ -815,18 +847,19 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
             kk -= 32;
         }
     }
-    // byte counts and final states of the four lanes of this column
-    uint32_t cnt[4], fs[4];
+    // byte counts, final states and LDS stream starts of the four lanes of this column
+    uint32_t cnt[4], fs[4], sa[4];
 #pragma unroll
     for (int b = 0; b < 4; b++) {
-        if (b == FL) { cnt[b] = e0; fs[b] = x0; }
-        else if (b == 3) { cnt[b] = e1; fs[b] = x1; }
+        if (b == FL) { cnt[b] = e0; fs[b] = x0; sa[b] = st0_off + j * fp.stride0 + fp.sl0 - min(e0, fp.sl0); }
+        else if (b == 3) { cnt[b] = e1; fs[b] = x1; sa[b] = st1_off + j * fp.stride1 + fp.sl1 - min(e1, fp.sl1); }
         else {
             const uint32_t pb = col + b;
             const uint32_t Kb = len > pb ? (len - pb + 255) / 256 : 0u;
-            const uint32_t* ch = (chdr[0] == Kb) ? chdr : ((chdr[4] == Kb) ? chdr + 4 : chdr + 8);
-            fs[b] = ch[1];
-            cnt[b] = ch[2];
+            const uint32_t ent = (chdr[0] == Kb) ? 0u : ((chdr[4] == Kb) ? 1u : 2u);
+            fs[b] = chdr[4 * ent + 1];
+            cnt[b] = chdr[4 * ent + 2];
+            sa[b] = FE_CBYTES + ent * fp.canon_bytes;
         }
     }
     const uint32_t tsum = cnt[0] + cnt[1] + cnt[2] + cnt[3];
@@ -850,8 +883,7 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
         unit_off[u] = off;
         if (u + 1 == g.n_units) unit_off[u + 1] = off + size;
     }
-    // headers (4 per thread, 64 contiguous bytes)
-    {
+    {   // headers (4 per thread, 64 contiguous bytes) and the lane tables for packing
         ckr_stream_header* uh = hdrs + u * 256 + 4 * j;
         uint32_t run = excl;
 #pragma unroll
@@ -864,8 +896,11 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
             }
             h.pad = 0;
             uh[b] = h;
+            loff[4 * j + b] = run;
+            delta[4 * j + b] = (int32_t)sa[b] - (int32_t)run;
             run += cnt[b];
         }
+        if (j == 63) loff[256] = total;
     }
     uint8_t* dst = out + off;
     if (raw) {  // masked bytes of the unit, byte stores (rare)
@@ -879,50 +914,32 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
         if (j == 0) redo_list[atomicAdd(&ctl[1], 1u)] = (uint32_t)u;
         return;
     }
-    {
-        uint32_t run = excl;
-#pragma unroll
-        for (int b = 0; b < 4; b++) { loff[4 * j + b] = run; run += cnt[b]; }
-        if (j == 63) loff[256] = total;
-    }
     __syncthreads();
-    // packed bytes: 32-bit destination words d in [first, last), thread j takes
-    // j, j+64, ...; each byte is found through the lane offsets (cursor L only
-    // moves forward)
-    const uint64_t a0 = reinterpret_cast<uintptr_t>(dst);
-    const uint64_t dfirst = a0 >> 2, dlast = (a0 + size + 3) >> 2;
-    uint32_t Lc = 0;
-    for (uint64_t d = dfirst + j; d < dlast; d += 64) {
-        const int64_t q0 = (int64_t)(d << 2) - (int64_t)a0;
-        uint32_t v = 0, valid = 0;
+    // packed bytes in 16-byte destination chunks, thread j taking chunk j, j+64, ...
+    // of [a0, a1); four chunks in flight, each finding its lane by binary search
+    const uint64_t ab = reinterpret_cast<uintptr_t>(dst);
+    const uint64_t a0 = ab & ~15ull, a1 = (ab + size + 15) & ~15ull;
+    const uint32_t nchunk = (uint32_t)((a1 - a0) >> 4);
+    for (uint32_t c0 = 0; c0 < nchunk; c0 += 256) {
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const int64_t q = q0 + b;
-            if (q < 0 || q >= (int64_t)size) continue;
-            const uint32_t qq = (uint32_t)q;
-            while (loff[Lc + 1] <= qq) Lc++;
-            const uint32_t i = qq - loff[Lc];
-            const uint32_t lb = Lc & 3, lc = Lc >> 2;
-            uint32_t byte;
-            if (lb == FL || lb == 3) {
-                const uint32_t B = loff[Lc + 1] - loff[Lc];
-                const uint32_t e = B - 1 - i;
-                const uint8_t* stl = (lb == 3) ? st1 : st0;
-                byte = stl[(((e >> 2) * 64 + lc) << 2) + (e & 3)];
+        for (int k = 0; k < 4; k++) {
+            const uint32_t c = c0 + j + 64 * k;
+            if (c >= nchunk) break;
+            const int64_t q0 = (int64_t)(a0 + 16ull * c) - (int64_t)ab;  // unit-relative first byte
+            uint8_t* w = reinterpret_cast<uint8_t*>(a0 + 16ull * c);
+            const uint32_t qf = q0 < 0 ? 0u : (uint32_t)q0;
+            uint32_t Lc = lane_of(loff, qf);
+            if (q0 >= 0 && q0 + 16 <= (int64_t)size && q0 + 16 <= (int64_t)loff[Lc + 1]) {
+                *reinterpret_cast<uint4*>(w) = lds_read16(lds8, (uint32_t)(delta[Lc] + (int32_t)q0));
             } else {
-                const uint32_t pb = Lc;
-                const uint32_t Kb = len > pb ? (len - pb + 255) / 256 : 0u;
-                const uint32_t ent = (chdr[0] == Kb) ? 0u : ((chdr[4] == Kb) ? 1u : 2u);
-                byte = cbytes[ent * fp.canon_bytes + i];
+                for (int b = 0; b < 16; b++) {
+                    const int64_t q = q0 + b;
+                    if (q < 0 || q >= (int64_t)size) continue;
+                    while (loff[Lc + 1] <= (uint32_t)q) Lc++;
+                    w[b] = lds8[delta[Lc] + (int32_t)q];
+                }
             }
-            v |= byte << (8 * b);
-            valid |= 1u << b;
         }
-        uint8_t* w = reinterpret_cast<uint8_t*>(d << 2);
-        if (valid == 15u) *reinterpret_cast<uint32_t*>(w) = v;
-        else
-            for (int b = 0; b < 4; b++)
-                if (valid & (1u << b)) w[b] = (uint8_t)(v >> (8 * b));
     }
 }
 
@@ -932,8 +949,13 @@ __global__ void encode_fast_reset_kernel(uint64_t* status, uint64_t n, uint32_t*
     if (i < 4) ctl[i] = 0;
 }
 
+static uint32_t slot_stride(uint32_t sl) {
+    // consecutive lanes' slots start (stride / 4) banks apart: keep that odd
+    return ((sl >> 2) & 1u) ? sl + 4 : sl + 8;
+}
+
 uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p) {
-    return 1024 * 4 + 260 * 4 + 12 * 4 + 3 * p.canon_bytes + 64 * (p.sl0 + p.sl1);
+    return FE_CBYTES + 3 * p.canon_bytes + 64 * (slot_stride(p.sl0) + slot_stride(p.sl1)) + 32;
 }
 
 hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
@@ -942,6 +964,7 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
                               hipStream_t s) {
     FastEncParams fp;
     fp.sl0 = hp.sl0; fp.sl1 = hp.sl1; fp.cw = hp.cw; fp.canon_bytes = hp.canon_bytes;
+    fp.stride0 = slot_stride(hp.sl0); fp.stride1 = slot_stride(hp.sl1);
     const uint64_t n = g.n_units;
     CKR_LAUNCH("encode_fast_reset_kernel", s, encode_fast_reset_kernel<<<(uint32_t)((n + 255) / 256), 256, 0, s>>>(status, n, ctl));
     hipError_t e = hipGetLastError();
