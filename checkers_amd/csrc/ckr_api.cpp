@@ -449,6 +449,14 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
     bool fast = use_fast_encode(g);
     ckr::FastEncParamsHost fp{};
     if (fast) {
+        // with the data's own live-plane histograms at hand, escapes are excluded
+        // when every symbol they contain has a slot
+        fp.escapes = true;
+        if (h_planes) {
+            fp.escapes = false;
+            for (int s2 = 0; s2 < 256; s2++)
+                if ((h_planes[s2] || h_planes[256 + s2]) && !h_table->norm_freq[s2]) fp.escapes = true;
+        }
         const uint32_t K = (uint32_t)((g.unit + 255) / 256);
         fp.cw = ck.cw;
         const uint32_t cbmax = std::max(canon_stream_bytes(h_table, ck.k0),

@@ -79,6 +79,7 @@ hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t
 // u32 — units whose bytes must then be produced by launch_encode_batch.
 struct FastEncParamsHost {
     uint32_t sl0, sl1, cw, canon_bytes;
+    bool escapes;  // the data may hold symbols with f == 0 (table not built from it)
 };
 uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p);
 hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,

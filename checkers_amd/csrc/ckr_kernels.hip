@@ -664,28 +664,28 @@ struct FastEncParams {
 static constexpr uint32_t FE_TAB = 0, FE_LOFF = 4096, FE_DELTA = 4096 + 1040, FE_CHDR = 4096 + 1040 + 1024,
                           FE_CBYTES = FE_CHDR + 48;
 
-__device__ __forceinline__ void lds_emit(uint8_t* slot, uint32_t& e, uint32_t sl, uint32_t v) {
-    if (e < sl) slot[sl - 1 - e] = (uint8_t)v;  // first byte emitted = last byte of the stream
-    e++;
-}
-
-__device__ __forceinline__ void enc_sym_lds(uint32_t& x, uint32_t& e, uint32_t sym, const EncSym* tab, uint8_t* slot,
-                                            uint32_t sl) {
-    const EncSym s = tab[sym];
-    if (s.xmax == 0) {  // f == 0: raw byte, no state update (ANSCompressor.cpp:185-192)
-        lds_emit(slot, e, sl, sym);
-        return;
-    }
-    if (x >= s.xmax) {
-        lds_emit(slot, e, sl, x & 255u);
-        x >>= 8;
-        if (x >= s.xmax) {
-            lds_emit(slot, e, sl, x & 255u);
-            x >>= 8;
-        }
-    }
-    const uint32_t q = __umulhi(x, s.rcp) >> (s.cmpl_rsh >> 16);
-    x = x + s.bias + __umul24(q, s.cmpl_rsh & 0xFFFFu);
+// One symbol of rans_encode_kernel's loop body (ANSCompressor.cpp:180-202)
+// without branches: the (at most two) renormalisation bytes are always stored,
+// to the lane's slot when emitted and to a per-thread dummy byte otherwise; the
+// first byte emitted is the last byte of the stream (slot filled from its end).
+// ESC: the table may give f == 0 to a symbol of the data (raw-byte escape, no
+// state update, :185-192); tables built from the data itself never do.
+template <bool ESC>
+__device__ __forceinline__ void enc_sym_lds(uint32_t& x, uint32_t& e, uint32_t sym, const EncSym& s, uint8_t* slot,
+                                            uint32_t sl, uint8_t* dummy) {
+    const bool esc = ESC && s.xmax == 0;
+    const bool e1 = esc || x >= s.xmax;
+    const uint32_t x1 = (e1 && !esc) ? (x >> 8) : x;
+    const bool e2 = !esc && e1 && x1 >= s.xmax;
+    const uint32_t xr = e2 ? (x1 >> 8) : x1;
+    uint8_t* a1 = (e1 && e < sl) ? slot + (sl - 1 - e) : dummy;
+    uint8_t* a2 = (e2 && e + 1 < sl) ? slot + (sl - 2 - e) : dummy;
+    *a1 = (uint8_t)(esc ? sym : x);
+    *a2 = (uint8_t)x1;
+    e += (e1 ? 1u : 0u) + (e2 ? 1u : 0u);
+    const uint32_t q = __umulhi(xr, s.rcp) >> (s.cmpl_rsh >> 16);
+    const uint32_t xn = xr + s.bias + __umul24(q, s.cmpl_rsh & 0xFFFFu);
+    x = esc ? x : xn;
 }
 
 __device__ __forceinline__ uint64_t lb_load(const uint64_t* p) {
@@ -743,7 +743,7 @@ __device__ __forceinline__ uint32_t lane_of(const uint32_t* loff, uint32_t q) {
     return lo;
 }
 
-template <int SPE>
+template <int SPE, bool ESC, bool SIDE>
 __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
                                                          const EncSym* __restrict__ d_enc,
                                                          const uint32_t* __restrict__ canon, FastEncParams fp,
@@ -798,6 +798,7 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
     const uint32_t lm = live_mask32<SPE>();
     uint8_t* slot0 = lds8 + st0_off + j * fp.stride0;
     uint8_t* slot1 = lds8 + st1_off + j * fp.stride1;
+    uint8_t* dummy = lds8 + st1_off + 64 * fp.stride1 + 4 * j;  // 256 bytes after the slots
     uint32_t x0 = L, x1 = L, e0 = 0, e1 = 0;
 
     const uint32_t col = 4 * j;
@@ -809,31 +810,48 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
             uint32_t v = 0;
             if (nvalid == 4) v = *reinterpret_cast<const uint32_t*>(usrc + p);
             else for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)usrc[p + b] << (8 * b);
-            if (sidecar) write_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
+            if (SIDE) write_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
             v &= lm;
-            enc_sym_lds(x0, e0, (v >> (8 * FL)) & 255u, tab, slot0, fp.sl0);
-            if (nvalid == 4) enc_sym_lds(x1, e1, v >> 24, tab, slot1, fp.sl1);
+            const uint32_t sy0 = (v >> (8 * FL)) & 255u, sy1 = v >> 24;
+            const EncSym t0 = tab[sy0], t1 = tab[sy1];
+            enc_sym_lds<ESC>(x0, e0, sy0, t0, slot0, fp.sl0, dummy);
+            if (nvalid == 4) enc_sym_lds<ESC>(x1, e1, sy1, t1, slot1, fp.sl1, dummy);
         }
         // rows K-2 .. 0 in groups of 32; the next group's loads are in flight
-        // while the current group is coded
+        // while the current group is coded.  In a full unit every column has
+        // the same K: kk is then wave-uniform and the row guards are scalar.
         int32_t kk = (int32_t)K - 2;
+        if (len == g.unit) kk = __builtin_amdgcn_readfirstlane(kk);
         uint32_t ra[32], rb[32];
         // row k of this column: 32 bits at usrc + 256k + 4j; its sidecar: 16 bits at
         // sidecar + (ubase + 256k + 4j) / 2
         const uint32_t* in32 = reinterpret_cast<const uint32_t*>(usrc + col);
-        uint16_t* sc16 = sidecar ? reinterpret_cast<uint16_t*>(sidecar + (ubase >> 1) + 2 * j) : nullptr;
+        uint16_t* sc16 = SIDE ? reinterpret_cast<uint16_t*>(sidecar + (ubase >> 1) + 2 * j) : nullptr;
         auto load_rows = [&](uint32_t (&r)[32], int32_t top) {
 #pragma unroll
             for (int i = 0; i < 32; i++) r[i] = (top - i >= 0) ? in32[64 * (top - i)] : 0u;
         };
+        // 8 rows at a time: the 16 table entries are read before any of the
+        // slot stores of those rows, so their LDS latency overlaps
         auto code_rows = [&](const uint32_t (&r)[32], int32_t top) {
 #pragma unroll
-            for (int i = 0; i < 32; i++) {
-                const int32_t k = top - i;
-                if (k < 0) break;
-                if (sc16) sc16[64 * k] = (uint16_t)(SPE == 2 ? (r[i] & 0xFFFFu) : ((r[i] & 0xFFu) | ((r[i] >> 8) & 0xFF00u)));
-                enc_sym_lds(x0, e0, (r[i] >> (8 * FL)) & 255u, tab, slot0, fp.sl0);
-                enc_sym_lds(x1, e1, r[i] >> 24, tab, slot1, fp.sl1);
+            for (int i0 = 0; i0 < 32; i0 += 8) {
+                if (top - i0 < 0) break;
+                EncSym t0[8], t1[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    t0[i] = tab[(r[i0 + i] >> (8 * FL)) & 255u];
+                    t1[i] = tab[r[i0 + i] >> 24];
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int32_t k = top - i0 - i;
+                    if (k < 0) break;
+                    const uint32_t w = r[i0 + i];
+                    if (SIDE) sc16[64 * k] = (uint16_t)(SPE == 2 ? (w & 0xFFFFu) : ((w & 0xFFu) | ((w >> 8) & 0xFF00u)));
+                    enc_sym_lds<ESC>(x0, e0, (w >> (8 * FL)) & 255u, t0[i], slot0, fp.sl0, dummy);
+                    enc_sym_lds<ESC>(x1, e1, w >> 24, t1[i], slot1, fp.sl1, dummy);
+                }
             }
         };
         if (kk >= 0) load_rows(ra, kk);
@@ -951,11 +969,11 @@ __global__ void encode_fast_reset_kernel(uint64_t* status, uint64_t n, uint32_t*
 
 static uint32_t slot_stride(uint32_t sl) {
     // consecutive lanes' slots start (stride / 4) banks apart: keep that odd
-    return ((sl >> 2) & 1u) ? sl + 4 : sl + 8;
+    return ((sl >> 2) & 1u) ? sl + 8 : sl + 4;
 }
 
 uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p) {
-    return FE_CBYTES + 3 * p.canon_bytes + 64 * (slot_stride(p.sl0) + slot_stride(p.sl1)) + 32;
+    return FE_CBYTES + 3 * p.canon_bytes + 64 * (slot_stride(p.sl0) + slot_stride(p.sl1)) + 256 + 32;
 }
 
 hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
@@ -970,15 +988,23 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t lb = encode_fast_lds_bytes(hp);
+#define CKR_FAST_ENC(SPE_, ESC_, SIDE_)                                                                        \
+    do {                                                                                                      \
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&encode_fast_kernel<SPE_, ESC_, SIDE_>),      \
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);                       \
+        CKR_LAUNCH("encode_fast_kernel", s,                                                                   \
+                   encode_fast_kernel<SPE_, ESC_, SIDE_><<<(uint32_t)n, 64, lb, s>>>(                         \
+                       src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status, ctl, redo_list));      \
+    } while (0)
+    const bool side = sidecar != nullptr;
     if (g.spe == 2) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&encode_fast_kernel<2>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);
-        CKR_LAUNCH("encode_fast_kernel", s, encode_fast_kernel<2><<<(uint32_t)n, 64, lb, s>>>(src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status, ctl, redo_list));
+        if (hp.escapes) { if (side) CKR_FAST_ENC(2, true, true); else CKR_FAST_ENC(2, true, false); }
+        else { if (side) CKR_FAST_ENC(2, false, true); else CKR_FAST_ENC(2, false, false); }
     } else {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&encode_fast_kernel<1>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);
-        CKR_LAUNCH("encode_fast_kernel", s, encode_fast_kernel<1><<<(uint32_t)n, 64, lb, s>>>(src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status, ctl, redo_list));
+        if (hp.escapes) { if (side) CKR_FAST_ENC(1, true, true); else CKR_FAST_ENC(1, true, false); }
+        else { if (side) CKR_FAST_ENC(1, false, true); else CKR_FAST_ENC(1, false, false); }
     }
+#undef CKR_FAST_ENC
     return hipGetLastError();
 }
 
