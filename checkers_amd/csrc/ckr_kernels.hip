@@ -818,10 +818,11 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
             if (nvalid == 4) enc_sym_lds<ESC>(x1, e1, sy1, t1, slot1, fp.sl1, dummy);
         }
         // rows K-2 .. 0 in groups of 32; the next group's loads are in flight
-        // while the current group is coded.  In a full unit every column has
-        // the same K: kk is then wave-uniform and the row guards are scalar.
+        // while the current group is coded.  When the unit length is a multiple
+        // of 256 every column has the same K: kk is then wave-uniform and the
+        // row guards are scalar.
         int32_t kk = (int32_t)K - 2;
-        if (len == g.unit) kk = __builtin_amdgcn_readfirstlane(kk);
+        if ((len & 255u) == 0) kk = __builtin_amdgcn_readfirstlane(kk);
         uint32_t ra[32], rb[32];
         // row k of this column: 32 bits at usrc + 256k + 4j; its sidecar: 16 bits at
         // sidecar + (ubase + 256k + 4j) / 2
