@@ -695,33 +695,39 @@ __device__ __forceinline__ void lb_store(uint64_t* p, uint64_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Exclusive prefix of the packed sizes of units [0, u) (one thread).  Every
-// unit before u holds a ticket taken earlier, so it is running or done and
-// will publish; the wait is bounded all the same (error flag, no hang).
-__device__ uint64_t lookback(uint64_t* status, uint64_t u, uint64_t size, uint32_t* err) {
-    if (u == 0) {
-        lb_store(&status[0], LB_PFX | size);
-        return 0;
-    }
-    lb_store(&status[u], LB_AGG | size);
+// Exclusive prefix of the packed sizes of units [0, u), computed by the whole
+// wave: lane j reads the status of unit base-1-j, the nearest published
+// inclusive prefix (ballot) ends the walk, aggregates before it are summed;
+// each step covers 64 units.  Every unit before u holds a ticket taken earlier,
+// so it is running or done and will publish; the wait is bounded all the same
+// (error flag, no hang).  Publishes u's aggregate first and its prefix last.
+__device__ uint64_t lookback_wave(uint64_t* status, uint64_t u, uint64_t size, uint32_t* err, uint32_t j) {
+    if (j == 0) lb_store(&status[u], (u == 0 ? LB_PFX : LB_AGG) | size);
     uint64_t excl = 0;
-    uint64_t v = u - 1;
+    int64_t base = (int64_t)u;  // walk covers units < base
     uint32_t spins = 0;
-    while (true) {
-        const uint64_t st = lb_load(&status[v]);
-        if ((st >> 62) == 0) {
+    while (base > 0) {
+        const int64_t idx = base - 1 - (int64_t)j;
+        const uint64_t st = idx >= 0 ? lb_load(&status[idx]) : LB_PFX;
+        const uint64_t pfx = __ballot((st >> 62) == 2);
+        const uint32_t stop = pfx ? (uint32_t)__builtin_ctzll(pfx) : 63u;  // last lane needed
+        const uint64_t need = (stop == 63u) ? ~0ull : ((2ull << stop) - 1);
+        if (__ballot((st >> 62) == 0) & need) {  // a unit in the window has not published yet
             if (++spins > LB_SPIN_LIMIT) {
-                atomicOr(err, 1u);
+                if (j == 0) atomicOr(err, 1u);
                 break;
             }
-            __builtin_amdgcn_s_sleep(1);
+            __builtin_amdgcn_s_sleep(2);
             continue;
         }
-        excl += st & LB_VAL;
-        if ((st >> 62) == 2 || v == 0) break;
-        v--;
+        uint64_t v = (j <= stop) ? (st & LB_VAL) : 0ull;
+#pragma unroll
+        for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+        excl += v;
+        if (pfx) break;
+        base -= 64;
     }
-    lb_store(&status[u], LB_PFX | (excl + size));
+    if (j == 0 && u > 0) lb_store(&status[u], LB_PFX | (excl + size));
     return excl;
 }
 
@@ -895,9 +901,7 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
     const bool over = e0 > fp.sl0 || e1 > fp.sl1;
     const bool any_over = __ballot(over) != 0;
 
-    uint64_t off0 = 0;
-    if (j == 0) off0 = lookback(status, u, size, &ctl[2]);
-    const uint64_t off = __shfl(off0, 0, 64);
+    const uint64_t off = lookback_wave(status, u, size, &ctl[2], j);
     if (j == 0) {
         unit_off[u] = off;
         if (u + 1 == g.n_units) unit_off[u + 1] = off + size;
