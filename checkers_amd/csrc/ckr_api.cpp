@@ -220,6 +220,13 @@ struct ProfRec {
     hipEvent_t a, b;
 };
 std::vector<ProfRec> g_prof;
+// phase stamps of fast-encode launches: {device buffer, units, stream}
+struct PhaseRec {
+    uint64_t* buf;
+    uint64_t n;
+    hipStream_t s;
+};
+std::vector<PhaseRec> g_phase;
 
 }  // namespace
 
@@ -233,6 +240,15 @@ void prof_mark(const char* name, hipStream_t s, bool begin) {
     if (begin) g_prof.push_back({name, e, nullptr});
     else if (!g_prof.empty() && g_prof.back().b == nullptr) g_prof.back().b = e;
     else (void)hipEventDestroy(e);
+}
+uint64_t* prof_phase_buffer(uint64_t n, hipStream_t s) {
+    if (!g_prof_on || n == 0) return nullptr;
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    void* p = nullptr;
+    if (hipMalloc(&p, n * 8) != hipSuccess) return nullptr;
+    if (hipMemsetAsync(p, 0, n * 8, s) != hipSuccess) { (void)hipFree(p); return nullptr; }
+    g_phase.push_back({static_cast<uint64_t*>(p), n / 5, s});
+    return static_cast<uint64_t*>(p);
 }
 }  // namespace ckr
 
@@ -264,6 +280,33 @@ int ckr_profile_end(char* buf, uint64_t buflen) {
         (void)hipEventDestroy(r.a);
     }
     g_prof.clear();
+    // fast-encode phases: mean per unit (us) of prologue+ticket, coding,
+    // look-back and packing, and the mean unit lifetime
+    {
+        double sum[4] = {0, 0, 0, 0}, life = 0;
+        uint64_t units = 0;
+        for (auto& pr : g_phase) {
+            std::vector<uint64_t> h(pr.n * 5);
+            if (hipStreamSynchronize(pr.s) == hipSuccess &&
+                hipMemcpy(h.data(), pr.buf, h.size() * 8, hipMemcpyDeviceToHost) == hipSuccess) {
+                for (uint64_t u = 0; u < pr.n; u++) {
+                    const uint64_t* t = &h[5 * u];
+                    if (!t[4]) continue;  // unit left to the general kernels
+                    for (int k = 0; k < 4; k++) sum[k] += (double)(t[k + 1] - t[k]) * 0.01;
+                    life += (double)(t[4] - t[0]) * 0.01;
+                    units++;
+                }
+            }
+            (void)hipFree(pr.buf);
+        }
+        g_phase.clear();
+        if (units) {
+            const char* nm[4] = {"encode_fast.phase_prologue_us", "encode_fast.phase_code_us",
+                                 "encode_fast.phase_lookback_us", "encode_fast.phase_pack_us"};
+            for (int k = 0; k < 4; k++) agg[nm[k]] = {units, sum[k] / 1000.0};
+            agg["encode_fast.unit_lifetime_us"] = {units, life / 1000.0};
+        }
+    }
     std::string out;
     for (auto& kv : agg) {
         char line[256];

@@ -757,8 +757,10 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
                                                          uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out,
                                                          uint64_t* __restrict__ unit_off,
                                                          uint64_t* __restrict__ status, uint32_t* __restrict__ ctl,
-                                                         uint32_t* __restrict__ redo_list) {
+                                                         uint32_t* __restrict__ redo_list,
+                                                         uint64_t* __restrict__ phase) {
     extern __shared__ uint32_t lds[];
+    const uint64_t t_start = wall_clock64();
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
     const EncSym* tab = reinterpret_cast<const EncSym*>(lds8 + FE_TAB);
     uint32_t* loff = reinterpret_cast<uint32_t*>(lds8 + FE_LOFF);
@@ -797,6 +799,7 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
     __syncthreads();
     if (u >= g.n_units) return;
 
+    const uint64_t t_ready = wall_clock64();
     const uint64_t ubase = u * g.unit;
     const uint32_t len = (uint32_t)((g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit);
     const uint8_t* usrc = src + ubase;
@@ -901,7 +904,9 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
     const bool over = e0 > fp.sl0 || e1 > fp.sl1;
     const bool any_over = __ballot(over) != 0;
 
+    const uint64_t t_coded = wall_clock64();
     const uint64_t off = lookback_wave(status, u, size, &ctl[2], j);
+    const uint64_t t_placed = wall_clock64();
     if (j == 0) {
         unit_off[u] = off;
         if (u + 1 == g.n_units) unit_off[u + 1] = off + size;
@@ -964,6 +969,10 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
             }
         }
     }
+    if (phase && j == 0) {  // per-unit phase stamps (100 MHz clock) for ckr_profile_end
+        uint64_t* ph = phase + 5 * u;
+        ph[0] = t_start; ph[1] = t_ready; ph[2] = t_coded; ph[3] = t_placed; ph[4] = wall_clock64();
+    }
 }
 
 __global__ void encode_fast_reset_kernel(uint64_t* status, uint64_t n, uint32_t* ctl) {
@@ -985,6 +994,7 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
                               const FastEncParamsHost& hp, ckr_stream_header* hdrs, uint8_t* sidecar, uint8_t* out,
                               uint64_t* unit_off, uint64_t* status, uint32_t* ctl, uint32_t* redo_list,
                               hipStream_t s) {
+    uint64_t* phase = prof_phase_buffer(g.n_units * 5, s);
     FastEncParams fp;
     fp.sl0 = hp.sl0; fp.sl1 = hp.sl1; fp.cw = hp.cw; fp.canon_bytes = hp.canon_bytes;
     fp.stride0 = slot_stride(hp.sl0); fp.stride1 = slot_stride(hp.sl1);
@@ -999,7 +1009,7 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);                       \
         CKR_LAUNCH("encode_fast_kernel", s,                                                                   \
                    encode_fast_kernel<SPE_, ESC_, SIDE_><<<(uint32_t)n, 64, lb, s>>>(                         \
-                       src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status, ctl, redo_list));      \
+                       src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status, ctl, redo_list, phase)); \
     } while (0)
     const bool side = sidecar != nullptr;
     if (g.spe == 2) {
