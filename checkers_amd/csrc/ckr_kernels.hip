@@ -943,29 +943,69 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
         return;
     }
     __syncthreads();
-    // packed bytes in 16-byte destination chunks, thread j taking chunk j, j+64, ...
-    // of [a0, a1); four chunks in flight, each finding its lane by binary search
+    // packed bytes in 16-byte destination chunks, thread j taking chunks j,
+    // j+64, j+128, j+192 of every 256; the four binary searches for the lane
+    // at each chunk's first byte advance together.  A chunk is the OR of one
+    // masked 16-byte LDS read per lane it covers (usually one, at a lane
+    // boundary two).  The unit's first and last chunks are shared with the
+    // neighbouring units: bytes outside the unit are not stored.
     const uint64_t ab = reinterpret_cast<uintptr_t>(dst);
     const uint64_t a0 = ab & ~15ull, a1 = (ab + size + 15) & ~15ull;
     const uint32_t nchunk = (uint32_t)((a1 - a0) >> 4);
+    const int32_t qbase = (int32_t)(a0 - ab);  // unit-relative byte of chunk 0 (-15..0)
     for (uint32_t c0 = 0; c0 < nchunk; c0 += 256) {
+        uint32_t lo[4];
+        int32_t q0[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            q0[k] = qbase + 16 * (int32_t)(c0 + j + 64 * k);
+            lo[k] = 0;
+        }
+#pragma unroll
+        for (uint32_t step = 128; step > 0; step >>= 1)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t qf = q0[k] < 0 ? 0u : (uint32_t)q0[k];
+                if (loff[lo[k] + step] <= qf) lo[k] += step;
+            }
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const uint32_t c = c0 + j + 64 * k;
             if (c >= nchunk) break;
-            const int64_t q0 = (int64_t)(a0 + 16ull * c) - (int64_t)ab;  // unit-relative first byte
-            uint8_t* w = reinterpret_cast<uint8_t*>(a0 + 16ull * c);
-            const uint32_t qf = q0 < 0 ? 0u : (uint32_t)q0;
-            uint32_t Lc = lane_of(loff, qf);
-            if (q0 >= 0 && q0 + 16 <= (int64_t)size && q0 + 16 <= (int64_t)loff[Lc + 1]) {
-                *reinterpret_cast<uint4*>(w) = lds_read16(lds8, (uint32_t)(delta[Lc] + (int32_t)q0));
-            } else {
-                for (int b = 0; b < 16; b++) {
-                    const int64_t q = q0 + b;
-                    if (q < 0 || q >= (int64_t)size) continue;
-                    while (loff[Lc + 1] <= (uint32_t)q) Lc++;
-                    w[b] = lds8[delta[Lc] + (int32_t)q];
+            const int32_t q = q0[k];
+            uint4 v = make_uint4(0, 0, 0, 0);
+            // lanes covering [max(q,0), min(q+16, size)), each contributing its bytes
+            uint32_t Lc = lo[k];
+            const int32_t qend = min(q + 16, (int32_t)size);
+            while (Lc < 256 && (int32_t)loff[Lc] < qend) {
+                const int32_t s0 = max((int32_t)loff[Lc], q), s1 = min((int32_t)loff[Lc + 1], qend);
+                if (s1 > s0) {
+                    const uint4 r = lds_read16(lds8, (uint32_t)(delta[Lc] + q));
+                    // byte b of the chunk belongs to this lane iff s0 - q <= b < s1 - q
+                    const uint32_t b0 = (uint32_t)(s0 - q), b1 = (uint32_t)(s1 - q);
+                    uint32_t m[4];
+#pragma unroll
+                    for (int w4 = 0; w4 < 4; w4++) {
+                        uint32_t mm = 0;
+#pragma unroll
+                        for (int bb = 0; bb < 4; bb++) {
+                            const uint32_t bi = 4 * w4 + bb;
+                            mm |= (bi >= b0 && bi < b1) ? (0xFFu << (8 * bb)) : 0u;
+                        }
+                        m[w4] = mm;
+                    }
+                    v.x |= r.x & m[0]; v.y |= r.y & m[1]; v.z |= r.z & m[2]; v.w |= r.w & m[3];
                 }
+                Lc++;
+            }
+            uint8_t* wp = reinterpret_cast<uint8_t*>(a0 + 16ull * c);
+            if (q >= 0 && q + 16 <= (int32_t)size) {
+                *reinterpret_cast<uint4*>(wp) = v;
+            } else {
+                const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int bb = 0; bb < 16; bb++)
+                    if (q + bb >= 0 && q + bb < (int32_t)size) wp[bb] = (uint8_t)(vv[bb >> 2] >> (8 * (bb & 3)));
             }
         }
     }
