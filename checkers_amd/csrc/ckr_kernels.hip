@@ -688,11 +688,15 @@ __device__ __forceinline__ void enc_sym_lds(uint32_t& x, uint32_t& e, uint32_t s
     x = esc ? x : xn;
 }
 
+// Look-back status words.  Their values carry everything the protocol needs
+// (sizes and prefixes); no other data is published through them, so relaxed
+// device-scope atomics suffice — acquire/release at this scope would write
+// back or invalidate the whole L2 of the XCD on every access.
 __device__ __forceinline__ uint64_t lb_load(const uint64_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void lb_store(uint64_t* p, uint64_t v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Exclusive prefix of the packed sizes of units [0, u), computed by the whole
