@@ -81,6 +81,18 @@ def make_shard(cfg, torch, dev, seed=0):
     return tensors
 
 
+def measured_traffic(kernel, cfg):
+    """HBM bytes per launch of `kernel` on config `cfg` from the committed counter
+    summary profiles/traffic_<kernel>_cfg<cfg>.json (FETCH_SIZE + WRITE_SIZE runs,
+    scaled by the same counters on a copy of known size), or (None, None)."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{kernel}_cfg{cfg}.json")
+    if not os.path.exists(path):
+        return None, None
+    with open(path) as f:
+        d = json.load(f)
+    return int(d["hbm_bytes_per_launch"]), os.path.relpath(path, ROOT)
+
+
 def cpu_baseline(shard, ck, sample_bytes_per_tensor, unit):
     """The CPU oracle (C++ restatement, OpenMP over units) on a bounded sample."""
     import oracle as oc
@@ -119,6 +131,8 @@ def main():
     ap.add_argument("--cpu-sample-mib", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run one 1 GiB device-to-device copy (known HBM traffic) for counter scaling")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (one ZeRO-3 rank's shard per GPU; "
@@ -149,6 +163,13 @@ def main():
         for d, r, dst in zip(decs, results, dsts):
             bads.append(d.decode(r.data, r.headers, r.unit_offsets, r.table, r.sidecar, dst, check=check))
         return bads
+
+    if args.copy_calibration:  # 1 GiB read + 1 GiB written by one elementwise copy kernel
+        a = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        b = torch.empty_like(a)
+        b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
 
     for i in range(args.warmup):
         res = encode_all()
@@ -200,18 +221,27 @@ def main():
         prof = ck.profile_end()
         kernels = {k: dict(launches=c, total_ms=round(ms, 4), avg_ms=round(ms / c, 5)) for k, (c, ms) in prof.items()}
         # algorithmic bytes per kernel over the whole shard (one encode / one decode)
+        # algorithmic bytes of each kernel over the whole shard (one encode, one
+        # decode): what it must read and write at least once
         alg = {
-            "encode_kernel": n_in + S + C,        # read tensor, write sidecar + lane streams
-            "masked_hist_kernel": n_in,           # read tensor
-            "compact_kernel": 2 * C,              # read lane streams, write packed
-            "decode_kernel": C + S + n_in,        # read packed + sidecar, write tensor
+            "encode_fast_kernel": n_in + S + C + H,   # read tensor; write sidecar, packed data, headers
+            "encode_kernel": n_in + S + C,            # general path: read tensor, write sidecar + lane streams
+            "masked_hist_kernel": n_in,               # read tensor
+            "compact_kernel": 2 * C,                  # general path: read lane streams, write packed
+            "decode_fast_kernel": C + S + H + n_in,   # read packed + sidecar + headers, write tensor
+            "decode_kernel": C + S + n_in,            # general path
         }
+        # only units taken by a kernel count for it: the general kernels run for
+        # the few units the fast ones leave, so they are not the dominant kernel
         dom = max((k for k in alg if k in prof), key=lambda k: prof[k][1])
         ach = alg[dom] / (prof[dom][1] / 1e3) / 1e9
+        traffic, tsrc = measured_traffic(dom, args.config)
         roof = dict(bound="hbm", kernel=dom, achieved=round(ach, 2), peak=HBM_PEAK_GBPS, unit="GB/s",
-                    frac=round(ach / HBM_PEAK_GBPS, 4), traffic=None,
+                    frac=round(ach / HBM_PEAK_GBPS, 4), traffic=traffic,
                     algorithmic_bytes=int(alg[dom]), launches=prof[dom][0],
                     avg_launch_ms=round(prof[dom][1] / prof[dom][0], 5))
+        if tsrc:
+            roof["traffic_source"] = tsrc
         for k in alg:
             if k in prof:
                 kernels[k]["achieved_GBps"] = round(alg[k] / (prof[k][1] / 1e3) / 1e9, 2)
