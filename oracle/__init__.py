@@ -45,6 +45,9 @@ def lib():
             "oc_decode": (u64, [vp, vp, vp, vp, u64, u64, vp]),
             "oc_merge_sidecar": (None, [vp, vp, u64, i32, vp]),
             "oc_tensor_stats": (None, [vp, u64, i32, u32, vp, vp, vp, vp]),
+            "oc_repair_bucket_count": (u64, [u64]),
+            "oc_repair_build": (u32, [vp, u64, i32, u32, u32, vp, vp, vp, vp]),
+            "oc_repair_apply": (u64, [vp, u64, i32, u32, vp, u32, vp]),
         }
         for k, (r, a) in sig.items():
             f = getattr(L, k)
@@ -149,3 +152,36 @@ def compress_tensor(raw, n, dtype, unit, ensure_full_alphabet=False):
     table, tsum = normalize_histogram(byte_hist(masked), ensure_full_alphabet)
     data, hdr, off = encode(masked, table, unit)
     return dict(masked=masked, sidecar=side, table=table, table_sum=tsum, data=data, headers=hdr, unit_offsets=off)
+
+
+# ---- prefix-mask repair (Re-Pair over masked words)
+REPAIR_LAYOUT = {"float32": (4, 23), "float16": (2, 10), "fp16": (2, 10), "bfloat16": (2, 7), "bf16": (2, 7)}
+
+
+def repair_bucket_count(n):
+    return int(lib().oc_repair_bucket_count(n))
+
+
+def repair_build(raw, n, storage_bytes, masked_bits, max_rules=50, want_seq=False):
+    """dict(rules=[(replacement, lhs, rhs, freq)], out_len, max_pair, seq)."""
+    raw = as_bytes(raw) if n else np.zeros(4, np.uint8)
+    rules = np.zeros(max(max_rules, 1) * 4, np.uint64)
+    out_len = np.zeros(1, np.uint64)
+    mp = np.zeros(1, np.uint64)
+    seq = np.zeros(max(n, 1), np.uint64) if want_seq else None
+    nr = lib().oc_repair_build(_p(raw), n, storage_bytes, masked_bits, max_rules, _p(rules), _p(out_len),
+                               _p(mp), _p(seq) if want_seq else None)
+    r = dict(rules=[tuple(int(v) for v in rules[4 * i:4 * i + 4]) for i in range(nr)],
+             out_len=int(out_len[0]), max_pair=int(mp[0]))
+    if want_seq:
+        r["seq"] = seq[: r["out_len"]]
+    return r
+
+
+def repair_apply(raw, n, storage_bytes, masked_bits, rules, want_seq=False):
+    raw = as_bytes(raw) if n else np.zeros(4, np.uint8)
+    rr = np.array([v for rule in rules for v in rule] or [0], np.uint64)
+    seq = np.zeros(max(n, 1), np.uint64) if want_seq else None
+    m = int(lib().oc_repair_apply(_p(raw), n, storage_bytes, masked_bits, _p(rr), len(rules),
+                                  _p(seq) if want_seq else None))
+    return (m, seq[:m]) if want_seq else m

@@ -15,6 +15,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <unordered_map>
 #include <vector>
 
 #ifdef _OPENMP
@@ -406,6 +407,103 @@ void oc_tensor_stats(const uint8_t* data, uint64_t N, int dtype, uint32_t bins_i
         moments64[2] = c2 > 0 ? c3 / (c2 * std::sqrt(c2)) : 0.0;
         moments64[3] = c2 > 0 ? c4 / (c2 * c2) : 0.0;
     }
+}
+
+// ---------------------------------------------------------------- prefix-mask repair
+// src/tensor_group_prefix_mask_repair.cpp: build_masked_sequence (:328-353),
+// find_best_pair (:376-405), apply_rule (:407-426), build_shared_grammar
+// (:428-457), apply_existing_grammar (:459-467).
+//
+// The pair counts live in a libstdc++ std::unordered_map with the same key
+// hash (lhs ^ (rhs + 0x9e3779b97f4a7c15 + (lhs << 6) + (lhs >> 2)), identity
+// std::hash<uint64_t>) and the same reserve(size) call per round, so the
+// iteration order that breaks ties between equally frequent pairs is the
+// library's own.  A symbol is a uint64_t: masked words keep their bit
+// positions, rule i is 2^63 + i.
+
+struct oc_pair { uint64_t l, r; bool operator==(const oc_pair& o) const { return l == o.l && r == o.r; } };
+struct oc_pair_hash {
+    size_t operator()(const oc_pair& k) const {
+        const size_t a = std::hash<uint64_t>{}(k.l), b = std::hash<uint64_t>{}(k.r);
+        return a ^ (b + 0x9e3779b97f4a7c15ull + (a << 6) + (a >> 2));
+    }
+};
+
+// Masked word sequence of n little-endian words of `storage_bytes` (2 or 4)
+// with the low `masked_bits` bits cleared.
+static std::vector<uint64_t> repair_masked_words(const uint8_t* raw, uint64_t n, int storage_bytes,
+                                                 uint32_t masked_bits) {
+    const uint64_t mask = masked_bits ? ((uint64_t)1 << masked_bits) - 1 : 0;
+    std::vector<uint64_t> w(n);
+    for (uint64_t i = 0; i < n; i++) {
+        uint64_t v = 0;
+        for (int b = 0; b < storage_bytes; b++) v |= (uint64_t)raw[i * storage_bytes + b] << (8 * b);
+        w[i] = v & ~mask;
+    }
+    return w;
+}
+
+// One greedy left-to-right pass replacing non-overlapping (l, r) by `sym`.
+static uint64_t repair_apply_rule(std::vector<uint64_t>& t, uint64_t l, uint64_t r, uint64_t sym) {
+    uint64_t o = 0, rep = 0;
+    for (uint64_t i = 0; i < t.size();) {
+        if (i + 1 < t.size() && t[i] == l && t[i + 1] == r) { t[o++] = sym; i += 2; rep++; }
+        else t[o++] = t[i++];
+    }
+    t.resize(o);
+    return rep;
+}
+
+// Bucket count std::unordered_map picks for reserve(n) (for tests of the
+// product's own computation of it).
+uint64_t oc_repair_bucket_count(uint64_t n) {
+    std::unordered_map<oc_pair, size_t, oc_pair_hash> m;
+    m.reserve(n);
+    return m.bucket_count();
+}
+
+// build_shared_grammar on the masked sequence.  rules[4*i..] = {replacement,
+// lhs, rhs, frequency}.  Returns the rule count; *out_len the compressed
+// length, *max_pair the largest pair count seen in any round.  seq_out (n
+// entries, may be NULL) receives the compressed sequence.
+uint32_t oc_repair_build(const uint8_t* raw, uint64_t n, int storage_bytes, uint32_t masked_bits,
+                         uint32_t max_rules, uint64_t* rules, uint64_t* out_len, uint64_t* max_pair,
+                         uint64_t* seq_out) {
+    std::vector<uint64_t> t = repair_masked_words(raw, n, storage_bytes, masked_bits);
+    uint64_t next = (uint64_t)1 << 63, maxf = 0;
+    uint32_t nr = 0;
+    for (uint32_t ri = 0; ri < max_rules; ri++) {
+        if (t.size() < 2) break;
+        std::unordered_map<oc_pair, size_t, oc_pair_hash> counts;
+        counts.reserve(t.size());
+        for (size_t i = 0; i + 1 < t.size(); i++) ++counts[{t[i], t[i + 1]}];
+        size_t best = 0;
+        oc_pair bp{0, 0};
+        for (const auto& kv : counts) {
+            maxf = std::max<uint64_t>(maxf, kv.second);
+            if (kv.second > best) { best = kv.second; bp = kv.first; }
+        }
+        if (best < 2) break;
+        const uint64_t sym = next++;
+        const size_t before = t.size();
+        const uint64_t rep = repair_apply_rule(t, bp.l, bp.r, sym);
+        if (t.size() >= before || rep == 0) break;
+        rules[4 * nr + 0] = sym; rules[4 * nr + 1] = bp.l; rules[4 * nr + 2] = bp.r; rules[4 * nr + 3] = best;
+        nr++;
+    }
+    *out_len = t.size();
+    *max_pair = maxf;
+    if (seq_out) std::copy(t.begin(), t.end(), seq_out);
+    return nr;
+}
+
+// apply_existing_grammar: every rule in order, greedy left to right.
+uint64_t oc_repair_apply(const uint8_t* raw, uint64_t n, int storage_bytes, uint32_t masked_bits,
+                         const uint64_t* rules, uint32_t n_rules, uint64_t* seq_out) {
+    std::vector<uint64_t> t = repair_masked_words(raw, n, storage_bytes, masked_bits);
+    for (uint32_t i = 0; i < n_rules; i++) repair_apply_rule(t, rules[4 * i + 1], rules[4 * i + 2], rules[4 * i]);
+    if (seq_out) std::copy(t.begin(), t.end(), seq_out);
+    return t.size();
 }
 
 }  // extern "C"
