@@ -29,6 +29,8 @@ EXPORTED = [  # every symbol include/checkers_amd.h declares
     "ckr_num_units", "ckr_encode_max_output_bytes", "ckr_encode_workspace_bytes", "ckr_encode",
     "ckr_compress", "ckr_decode_workspace_bytes", "ckr_decode", "ckr_analyze_workspace_bytes",
     "ckr_analyze", "ckr_profile_begin", "ckr_profile_end", "ckr_set_fast_paths",
+    "ckr_repair_masked_bits", "ckr_repair_bucket_count", "ckr_repair_workspace_bytes",
+    "ckr_repair_build", "ckr_repair_apply",
 ]
 
 
@@ -125,6 +127,11 @@ def lib():
         "ckr_set_fast_paths": (i32, [i32]),
         "ckr_profile_begin": (i32, []),
         "ckr_profile_end": (i32, [ctypes.c_char_p, u64]),
+        "ckr_repair_masked_bits": (i32, [i32, i32]),
+        "ckr_repair_bucket_count": (u64, [u64]),
+        "ckr_repair_workspace_bytes": (u64, [u64, i32, i32, ctypes.c_uint32]),
+        "ckr_repair_build": (i32, [vp, u64, i32, i32, ctypes.c_uint32, vp, vp, vp, vp, vp, vp, u64, vp]),
+        "ckr_repair_apply": (i32, [vp, u64, i32, i32, vp, ctypes.c_uint32, vp, vp, vp, u64, vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L_, name)
@@ -374,3 +381,74 @@ def analyze(tensors, tags, bins=256, stream=None):
                         moments=mom[i].cpu().numpy().copy(), minmax=mm[i].cpu().numpy().copy(),
                         fingerprint=fp[i].cpu().numpy().copy()))
     return out
+
+
+# ---- tensor-group prefix-mask repair
+class RepairRule(ctypes.Structure):
+    """SharedGrammarRule (tensor_group_prefix_mask_repair.cpp:70-75)."""
+    _fields_ = [("replacement", ctypes.c_uint64), ("lhs", ctypes.c_uint64), ("rhs", ctypes.c_uint64),
+                ("frequency", ctypes.c_uint64)]
+
+
+def repair_masked_bits(dtype, request=None):
+    """Masked mantissa bits used for a dtype (request None: all mantissa bits)."""
+    k = int(lib().ckr_repair_masked_bits(dtype, -1 if request is None else int(request)))
+    if k < 0:
+        raise CkrError(CKR_E_INVALID, f"Unsupported dtype for mantissa-mask compression: tag {dtype}")
+    return k
+
+
+def repair_bucket_count(n):
+    return int(lib().ckr_repair_bucket_count(n))
+
+
+class Repairer:
+    """Workspace holder for build_shared_grammar / apply_existing_grammar on
+    device tensors of at most n_elems words."""
+
+    def __init__(self, n_elems, dtype, masked_bits=None, max_rules=50, device="cuda"):
+        self.n, self.dtype, self.max_rules = int(n_elems), dtype, int(max_rules)
+        self.mb = -1 if masked_bits is None else int(masked_bits)
+        repair_masked_bits(dtype, masked_bits)
+        wsb = int(lib().ckr_repair_workspace_bytes(self.n, dtype, self.mb, self.max_rules))
+        if wsb == 0:
+            raise CkrError(CKR_E_INVALID, lib().ckr_last_error().decode())
+        self.wsb = wsb
+        self.ws = _empty(wsb, device)
+
+    def build(self, src, want_seq=False, stream=None):
+        """dict(rules=[(replacement, lhs, rhs, freq)], out_len, max_pair[, seq])."""
+        torch = _torch()
+        n = _n_elems(src, self.dtype, None)
+        if n > self.n:
+            raise CkrError(CKR_E_INVALID, f"tensor of {n} words exceeds the workspace's {self.n}")
+        rules = (RepairRule * max(self.max_rules, 1))()
+        nr, out_len, mp = ctypes.c_uint32(0), ctypes.c_uint64(0), ctypes.c_uint64(0)
+        seq = torch.empty(max(n, 1), dtype=torch.int64, device=src.device) if want_seq else None
+        _check(lib().ckr_repair_build(src.data_ptr() if n else None, n, self.dtype, self.mb, self.max_rules,
+                                      rules, ctypes.byref(nr), ctypes.byref(out_len), ctypes.byref(mp),
+                                      seq.data_ptr() if want_seq else None, self.ws.data_ptr(), self.wsb,
+                                      _stream(stream)))
+        r = dict(rules=[(rules[i].replacement, rules[i].lhs, rules[i].rhs, rules[i].frequency)
+                        for i in range(nr.value)], out_len=out_len.value, max_pair=mp.value)
+        if want_seq:
+            r["seq"] = seq[: out_len.value].cpu().numpy().view(np.uint64)
+        return r
+
+    def apply(self, src, rules, want_seq=False, stream=None):
+        """Token count after applying the rules in order (and the sequence)."""
+        torch = _torch()
+        n = _n_elems(src, self.dtype, None)
+        if n > self.n or len(rules) > self.max_rules:
+            raise CkrError(CKR_E_INVALID, "tensor or rule list exceeds the workspace")
+        rr = (RepairRule * max(len(rules), 1))()
+        for i, (rep, lhs, rhs, f) in enumerate(rules):
+            rr[i].replacement, rr[i].lhs, rr[i].rhs, rr[i].frequency = rep, lhs, rhs, f
+        out_len = ctypes.c_uint64(0)
+        seq = torch.empty(max(n, 1), dtype=torch.int64, device=src.device) if want_seq else None
+        _check(lib().ckr_repair_apply(src.data_ptr() if n else None, n, self.dtype, self.mb, rr, len(rules),
+                                      ctypes.byref(out_len), seq.data_ptr() if want_seq else None,
+                                      self.ws.data_ptr(), self.wsb, _stream(stream)))
+        if want_seq:
+            return out_len.value, seq[: out_len.value].cpu().numpy().view(np.uint64)
+        return out_len.value

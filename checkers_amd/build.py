@@ -13,7 +13,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libcheckers_amd.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["ckr_kernels.hip", "ckr_api.cpp"]
+SOURCES = ["ckr_kernels.hip", "ckr_repair.hip", "ckr_api.cpp"]
 
 # -packed-fp32-ops: no v_pk_*_f32 generated anywhere (wrong results seen with
 # some of their forms on these machines).
@@ -25,12 +25,23 @@ FLAGS = [
 ]
 
 
+CLI = os.path.join(HERE, "ckr_prefix_mask_repair")
+
+
 def build(verbose=True):
     cmd = [HIPCC] + FLAGS + ["-x", "hip"] + [os.path.join(CSRC, s) for s in SOURCES] + ["-o", LIB + ".tmp"]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(LIB + ".tmp", LIB)
+    # the prefix-mask-repair command line: host code over the C ABI
+    cli = [HIPCC, "-O2", "-std=c++17", "-Wall", "-I", os.path.join(ROOT, "include"),
+           os.path.join(CSRC, "ckr_repair_cli.cpp"), "-o", CLI + ".tmp",
+           "-L", HERE, "-lcheckers_amd", "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cli), flush=True)
+    subprocess.run(cli, check=True)
+    os.replace(CLI + ".tmp", CLI)
     return LIB
 
 

@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "checkers_amd.h"
@@ -670,6 +671,178 @@ int ckr_analyze(const ckr_stats_record* recs, uint64_t n, void* d_workspace, uin
         CKR_HIP(ckr::launch_stats(r, nblk, p1, p2, prm, hp, s));
     }
     return CKR_OK;
+}
+
+}  // extern "C"
+
+// ---- prefix-mask repair
+namespace {
+
+int repair_mantissa_bits(int dtype) {  // parse_dtype_layout (tensor_group_prefix_mask_repair.cpp:190-202)
+    switch (dtype) {
+        case CKR_F32: return 23;
+        case CKR_F16: return 10;
+        case CKR_BF16: return 7;
+        default: return -1;
+    }
+}
+
+// Bucket count std::unordered_map::reserve(n) gives an empty map: rehash with
+// max(bucket count for 1 element, for n elements), rounded by the prime policy
+// (libstdc++ bits/hashtable.h rehash, bits/hashtable_policy.h reserve).  The
+// policy object is libstdc++'s own, so the numbers are the library's.
+uint64_t lib_bucket_count(uint64_t n) {
+    std::__detail::_Prime_rehash_policy pol;
+    const size_t want = std::max<size_t>(pol._M_bkt_for_elements(1), pol._M_bkt_for_elements((size_t)n));
+    return pol._M_next_bkt(want);
+}
+
+// Ascending bucket counts covering every size in [2, n]: entry j serves the
+// sizes (entry j-1, entry j].
+std::vector<uint64_t> bucket_table(uint64_t n) {
+    std::vector<uint64_t> t;
+    uint64_t lo = 2;
+    for (;;) {
+        const uint64_t p = lib_bucket_count(lo);
+        t.push_back(p);
+        if (p >= n || t.size() >= ckr::kRepairMaxPrimes) break;
+        lo = p + 1;
+    }
+    return t;
+}
+
+struct RepairPrep {
+    int es = 0;
+    uint32_t k = 0;
+    ckr::RepairLayout layout{};
+    std::vector<uint64_t> primes;
+};
+
+int repair_prep(uint64_t n, int dtype, int masked_bits, uint32_t max_rules, bool build, RepairPrep* p) {
+    const int mb = repair_mantissa_bits(dtype);
+    if (mb < 0) return fail(CKR_E_INVALID, "[ckr] Unsupported dtype for mantissa-mask compression: tag %d", dtype);
+    if (n >= (1ull << 31)) return fail(CKR_E_INVALID, "[ckr] repair needs n_elems < 2^31 (got %llu)", (unsigned long long)n);
+    p->es = ckr_element_size(dtype);
+    p->k = (uint32_t)ckr_repair_masked_bits(dtype, masked_bits);
+    uint64_t nb = 1;
+    if (build && n >= 2) {
+        p->primes = bucket_table(n);
+        nb = p->primes.back();
+    }
+    p->layout = ckr::repair_layout(n, p->es, p->k, max_rules, nb);
+    return CKR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ckr_repair_masked_bits(int dtype, int request) {
+    const int mb = repair_mantissa_bits(dtype);
+    if (mb < 0) return -1;
+    return (request < 0 || request > mb) ? mb : request;
+}
+
+uint64_t ckr_repair_bucket_count(uint64_t n) {
+    if (n < 2) return lib_bucket_count(n);
+    const std::vector<uint64_t> t = bucket_table(n);
+    return *std::lower_bound(t.begin(), t.end(), n);
+}
+
+uint64_t ckr_repair_workspace_bytes(uint64_t n_elems, int dtype, int masked_bits, uint32_t max_rules) {
+    RepairPrep p;
+    if (repair_prep(n_elems, dtype, masked_bits, max_rules, true, &p) != CKR_OK) return 0;
+    return p.layout.bytes;
+}
+
+static int repair_run(const void* d_words, uint64_t n, int dtype, int masked_bits, uint32_t max_rules, bool build,
+                      const ckr_repair_rule* h_rules_in, uint32_t n_rules_in, ckr_repair_rule* h_rules_out,
+                      uint32_t* h_n_rules, uint64_t* h_out_tokens, uint64_t* h_max_pair, uint64_t* d_seq_out,
+                      void* d_ws, uint64_t ws_bytes, void* stream) {
+    RepairPrep p;
+    int rc = repair_prep(n, dtype, masked_bits, build ? max_rules : n_rules_in, build, &p);
+    if (rc != CKR_OK) return rc;
+    if (!h_out_tokens) return fail(CKR_E_INVALID, "[ckr] null output count");
+    if (build && (!h_rules_out || !h_n_rules || !h_max_pair)) return fail(CKR_E_INVALID, "[ckr] null rule outputs");
+    if (!build && n_rules_in && !h_rules_in) return fail(CKR_E_INVALID, "[ckr] null rules");
+    if (!build)
+        for (uint32_t i = 0; i < n_rules_in; i++)
+            if (h_rules_in[i].replacement != (1ull << 63) + i)
+                return fail(CKR_E_INVALID, "[ckr] rule %u must have replacement 2^63 + %u", i, i);
+    if (build) { *h_n_rules = 0; *h_max_pair = 0; }
+    *h_out_tokens = n;
+    // fewer than 2 words: no pair, no rule, nothing on the device
+    // (find_best_pair returns before counting, :380-382)
+    const bool trivial = build ? n < 2 : (n < 2 || n_rules_in == 0);
+    hipStream_t s = (hipStream_t)stream;
+    if (trivial) {
+        if (d_seq_out && n) {
+            // masked words as symbols: one word, or no rule to apply
+            std::vector<uint64_t> h(n, 0);
+            std::vector<uint8_t> raw(n * p.es);
+            CKR_HIP(hipMemcpyAsync(raw.data(), d_words, raw.size(), hipMemcpyDeviceToHost, s));
+            CKR_HIP(hipStreamSynchronize(s));
+            const uint64_t mask = p.k ? ((1ull << p.k) - 1) : 0;
+            for (uint64_t i = 0; i < n; i++) {
+                uint64_t v = 0;
+                std::memcpy(&v, raw.data() + i * p.es, p.es);
+                h[i] = v & ~mask;
+            }
+            CKR_HIP(hipMemcpyAsync(d_seq_out, h.data(), n * 8, hipMemcpyHostToDevice, s));
+            CKR_HIP(hipStreamSynchronize(s));
+        }
+        return CKR_OK;
+    }
+    if (!d_words) return fail(CKR_E_INVALID, "[ckr] null words");
+    if (!d_ws || ws_bytes < p.layout.bytes)
+        return fail(CKR_E_CAPACITY, "[ckr] repair workspace too small (%llu < %llu)", (unsigned long long)ws_bytes,
+                    (unsigned long long)p.layout.bytes);
+    ckr::RepairArgs a{};
+    a.words = static_cast<const uint8_t*>(d_words);
+    a.n = n;
+    a.es = p.es;
+    a.k = p.k;
+    a.build = build ? 1 : 0;
+    a.max_rules = build ? max_rules : n_rules_in;
+    a.h_rules = h_rules_in;
+    a.n_rules = n_rules_in;
+    a.h_primes = p.primes.data();
+    a.n_primes = (uint32_t)p.primes.size();
+    a.d_seq_out = d_seq_out;
+    a.ws = static_cast<uint8_t*>(d_ws);
+    a.layout = p.layout;
+    CKR_HIP(ckr::repair_launch(a, s));
+    ckr::RepairCtl ctl{};
+    uint8_t* ws = static_cast<uint8_t*>(d_ws);
+    CKR_HIP(hipMemcpyAsync(&ctl, ws + p.layout.o_ctl, sizeof(ctl), hipMemcpyDeviceToHost, s));
+    std::vector<ckr_repair_rule> rules(build ? std::max<uint32_t>(max_rules, 1) : 0);
+    if (build && max_rules)
+        CKR_HIP(hipMemcpyAsync(rules.data(), ws + p.layout.o_rules, sizeof(ckr_repair_rule) * max_rules,
+                               hipMemcpyDeviceToHost, s));
+    CKR_HIP(hipStreamSynchronize(s));
+    if (ctl.err) return fail(CKR_E_CAPACITY, "[ckr] repair hash table overflow (flags %u)", ctl.err);
+    *h_out_tokens = ctl.n_cur;
+    if (build) {
+        *h_n_rules = ctl.round;
+        *h_max_pair = ctl.max_pair;
+        std::memcpy(h_rules_out, rules.data(), sizeof(ckr_repair_rule) * ctl.round);
+    }
+    return CKR_OK;
+}
+
+int ckr_repair_build(const void* d_words, uint64_t n_elems, int dtype, int masked_bits, uint32_t max_rules,
+                     ckr_repair_rule* h_rules, uint32_t* h_n_rules, uint64_t* h_out_tokens,
+                     uint64_t* h_max_pair_frequency, uint64_t* d_seq_out, void* d_workspace,
+                     uint64_t workspace_bytes, void* stream) {
+    return repair_run(d_words, n_elems, dtype, masked_bits, max_rules, true, nullptr, 0, h_rules, h_n_rules,
+                      h_out_tokens, h_max_pair_frequency, d_seq_out, d_workspace, workspace_bytes, stream);
+}
+
+int ckr_repair_apply(const void* d_words, uint64_t n_elems, int dtype, int masked_bits,
+                     const ckr_repair_rule* h_rules, uint32_t n_rules, uint64_t* h_out_tokens, uint64_t* d_seq_out,
+                     void* d_workspace, uint64_t workspace_bytes, void* stream) {
+    return repair_run(d_words, n_elems, dtype, masked_bits, n_rules, false, h_rules, n_rules, nullptr, nullptr,
+                      h_out_tokens, nullptr, d_seq_out, d_workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

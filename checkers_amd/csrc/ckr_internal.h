@@ -120,4 +120,40 @@ hipError_t launch_stats(const ckr_stats_record& r, uint32_t nblk, StatsPartial1*
                         StatsPartial2* p2, StatsParams* prm, uint32_t* hist_partial,
                         hipStream_t s);
 
+// Prefix-mask repair (ckr_repair.hip).
+struct RepairCtl {
+    uint64_t pick;        // tie-break: max of (bucket first occurrence << 32 | first occurrence)
+    uint32_t n_cur, n_next, done, round;
+    uint32_t best, ncand, chosen, d;   // d: occupied pair-table slots
+    uint32_t a0, a, b, c;              // alphabet size; pair (a, b) → c of this round
+    uint32_t skip, cur, err, max_pair; // cur: which token buffer holds the sequence
+};
+constexpr uint32_t kRepairMaxPrimes = 512;
+struct RepairLayout {
+    uint32_t w;           // live bits per word
+    bool direct;          // w <= 16: alphabet by bitmap, else by hash set
+    uint64_t pair_cap, vcap, n_buckets;
+    uint64_t o_ctl, o_buf0, o_buf1, o_sym, o_bitmap, o_rank, o_vkey, o_vrank, o_occ;
+    uint64_t o_pkey, o_pcnt, o_pfirst, o_touched, o_bfirst, o_primes, o_bfun, o_boff, o_rules, o_rmap;
+    uint64_t bytes;
+};
+// n_buckets: bucket count of reserve(n) (size of the bucket first-occurrence array).
+RepairLayout repair_layout(uint64_t n, int es, uint32_t k, uint32_t max_rules, uint64_t n_buckets);
+struct RepairArgs {
+    const uint8_t* words;
+    uint64_t n;
+    int es;
+    uint32_t k;
+    int build;                        // 1: build_shared_grammar, 0: apply rules
+    uint32_t max_rules;
+    const ckr_repair_rule* h_rules;   // apply: the rules
+    uint32_t n_rules;
+    const uint64_t* h_primes;         // build: library bucket counts covering [2, n], ascending
+    uint32_t n_primes;
+    uint64_t* d_seq_out;
+    uint8_t* ws;
+    RepairLayout layout;
+};
+hipError_t repair_launch(const RepairArgs& a, hipStream_t s);
+
 }  // namespace ckr

@@ -25,6 +25,8 @@
  *                              (src/TensorAnalyzer.cpp:64-229, launch :294-320), with the
  *                              fingerprint of TensorAnalyzer::compute_fingerprints
  *                              (src/TensorAnalyzer.cpp:271-292) written by the same pass
+ *   - ckr_repair_build/apply ← build_shared_grammar / apply_existing_grammar of the
+ *                              prefix-mask-repair CLI (src/tensor_group_prefix_mask_repair.cpp:328-467)
  */
 #ifndef CHECKERS_AMD_H
 #define CHECKERS_AMD_H
@@ -181,6 +183,46 @@ CKR_API int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers
 CKR_API uint64_t ckr_analyze_workspace_bytes(const ckr_stats_record* h_records, uint64_t n);
 CKR_API int ckr_analyze(const ckr_stats_record* h_records, uint64_t n,
                         void* d_workspace, uint64_t workspace_bytes, void* stream);
+
+/* ---- tensor-group prefix-mask repair (Re-Pair over masked words) ----
+ * Replaces build_masked_sequence / find_best_pair / apply_rule /
+ * build_shared_grammar / apply_existing_grammar of
+ * src/tensor_group_prefix_mask_repair.cpp (:328-353, :376-467), the reference's
+ * CPU-only CLI.  Words are the tensor's elements (F32, BF16 or F16) with their
+ * low masked_bits mantissa bits cleared; masked_bits < 0 means all mantissa
+ * bits (23, 7, 10), larger requests are clamped to them, as the reference does
+ * (:333-336).  Rules are SharedGrammarRule (:70-75): rule i replaces the pair
+ * (lhs, rhs) by the symbol 2^63 + i; symbols below 2^63 are masked words.
+ * Ties between equally frequent pairs are broken as the reference's
+ * std::unordered_map iteration order breaks them (libstdc++).  n_elems must be
+ * below 2^31. ---- */
+typedef struct {
+    uint64_t replacement;
+    uint64_t lhs;
+    uint64_t rhs;
+    uint64_t frequency;
+} ckr_repair_rule;
+
+/* Masked bit count the reference uses for a dtype and a request (<0: all
+ * mantissa bits); -1 for a dtype the repair does not support. */
+CKR_API int ckr_repair_masked_bits(int dtype, int request);
+/* Bucket count of std::unordered_map::reserve(n) (libstdc++), the modulus of
+ * the tie-break order; exported for tests. */
+CKR_API uint64_t ckr_repair_bucket_count(uint64_t n);
+CKR_API uint64_t ckr_repair_workspace_bytes(uint64_t n_elems, int dtype, int masked_bits, uint32_t max_rules);
+/* build_shared_grammar on the tensor: up to max_rules rules into h_rules,
+ * their count, the compressed token count and the largest pair count seen.
+ * d_seq_out (n_elems u64, may be NULL) receives the compressed sequence as
+ * reference symbols.  Synchronises `stream`. */
+CKR_API int ckr_repair_build(const void* d_words, uint64_t n_elems, int dtype, int masked_bits,
+                             uint32_t max_rules, ckr_repair_rule* h_rules, uint32_t* h_n_rules,
+                             uint64_t* h_out_tokens, uint64_t* h_max_pair_frequency, uint64_t* d_seq_out,
+                             void* d_workspace, uint64_t workspace_bytes, void* stream);
+/* apply_existing_grammar: the rules in order, each a greedy left-to-right
+ * pass.  Rule i must have replacement 2^63 + i.  Synchronises `stream`. */
+CKR_API int ckr_repair_apply(const void* d_words, uint64_t n_elems, int dtype, int masked_bits,
+                             const ckr_repair_rule* h_rules, uint32_t n_rules, uint64_t* h_out_tokens,
+                             uint64_t* d_seq_out, void* d_workspace, uint64_t workspace_bytes, void* stream);
 
 /* ---- path selection, no counterpart in the reference.  mode 1 (default):
  * fast kernels — lanes of masked planes coded once per lane count (their

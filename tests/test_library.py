@@ -108,3 +108,19 @@ def test_fast_path_switch_round_trips():
     assert ck.set_fast_paths(2) == 0
     assert ck.set_fast_paths(prev) == 2
     assert ck.set_fast_paths(prev) == prev
+
+
+def test_repair_host_helpers():
+    """Bucket counts of the tie-break order come from libstdc++'s own policy:
+    they must equal std::unordered_map::reserve(n).bucket_count()."""
+    import random
+    import oracle as oc
+    rnd = random.Random(7)
+    ns = list(range(0, 300)) + [rnd.randrange(2, 5_000_000) for _ in range(200)]
+    assert all(ck.repair_bucket_count(n) == oc.repair_bucket_count(n) for n in ns)
+    assert ck.repair_masked_bits(ck.F32) == 23 and ck.repair_masked_bits(ck.BF16) == 7
+    assert ck.repair_masked_bits(ck.F16) == 10 and ck.repair_masked_bits(ck.F16, 3) == 3
+    assert ck.repair_masked_bits(ck.BF16, 40) == 7 and ck.repair_masked_bits(ck.F32, 0) == 0
+    with pytest.raises(ck.CkrError):
+        ck.repair_masked_bits(ck.I32)
+    assert ck.lib().ckr_repair_workspace_bytes(1 << 31, ck.F32, -1, 50) == 0

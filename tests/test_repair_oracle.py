@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import oracle as oc
-import repair_fixtures as rf
+from tests import repair_fixtures as rf
 
 MB = 1024.0 * 1024.0
 
