@@ -31,6 +31,8 @@ EXPORTED = [  # every symbol include/checkers_amd.h declares
     "ckr_analyze", "ckr_profile_begin", "ckr_profile_end", "ckr_set_fast_paths",
     "ckr_repair_masked_bits", "ckr_repair_bucket_count", "ckr_repair_workspace_bytes",
     "ckr_repair_build", "ckr_repair_apply",
+    "ckr_fingerprint_weights", "ckr_cluster", "ckr_ckpt_write", "ckr_ckpt_open", "ckr_ckpt_count",
+    "ckr_ckpt_info", "ckr_ckpt_restore", "ckr_ckpt_close",
 ]
 
 
@@ -132,6 +134,14 @@ def lib():
         "ckr_repair_workspace_bytes": (u64, [u64, i32, i32, ctypes.c_uint32]),
         "ckr_repair_build": (i32, [vp, u64, i32, i32, ctypes.c_uint32, vp, vp, vp, vp, vp, vp, u64, vp]),
         "ckr_repair_apply": (i32, [vp, u64, i32, i32, vp, ctypes.c_uint32, vp, vp, vp, u64, vp]),
+        "ckr_fingerprint_weights": (i32, [vp, u64, vp]),
+        "ckr_cluster": (i32, [vp, vp, u64, vp, vp]),
+        "ckr_ckpt_write": (i32, [ctypes.c_char_p, i32, vp, u64, u64, i32, vp, vp]),
+        "ckr_ckpt_open": (i32, [ctypes.c_char_p, i32, vp]),
+        "ckr_ckpt_count": (u64, [vp]),
+        "ckr_ckpt_info": (i32, [vp, u64, vp]),
+        "ckr_ckpt_restore": (i32, [vp, u64, vp, vp]),
+        "ckr_ckpt_close": (None, [vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L_, name)
@@ -452,3 +462,116 @@ class Repairer:
         if want_seq:
             return out_len.value, seq[: out_len.value].cpu().numpy().view(np.uint64)
         return out_len.value
+
+
+# ---- fingerprint weights, clusters, rank checkpoint files
+def fingerprint_weights(fingerprints):
+    """compute_fingerprint_weights: 5 weights from n x 5 fingerprints."""
+    fp = np.ascontiguousarray(np.asarray(fingerprints, np.float32).reshape(-1, 5))
+    w = np.zeros(5, np.float64)
+    _check(lib().ckr_fingerprint_weights(fp.ctypes.data, fp.shape[0], w.ctypes.data))
+    return w
+
+
+def cluster(names, fingerprints):
+    """build_knn_clusters: (cluster id per record, -1 for singletons; thresholds
+    of the non-empty categories in name order)."""
+    fp = np.ascontiguousarray(np.asarray(fingerprints, np.float32).reshape(-1, 5))
+    n = fp.shape[0]
+    arr = (ctypes.c_char_p * max(n, 1))(*[x.encode() for x in names])
+    out = np.zeros(max(n, 1), np.int32)
+    thr = np.zeros(4, np.float64)
+    _check(lib().ckr_cluster(arr, fp.ctypes.data, n, out.ctypes.data, thr.ctypes.data))
+    ncat = len({_category(x) for x in names})
+    return out[:n].tolist(), thr[:ncat].tolist()
+
+
+def _category(name):
+    for p, c in (("optimizer.exp_avg_sq::", "exp_avg_sq"), ("optimizer.exp_avg::", "exp_avg"),
+                 ("master_weights::", "master_weights")):
+        if name.startswith(p):
+            return c
+    return "model_state"
+
+
+class CkptTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("d_ptr", ctypes.c_void_p), ("num_elements", ctypes.c_uint64),
+                ("dtype", ctypes.c_int32), ("cluster_id", ctypes.c_int32)]
+
+
+class CkptStats(ctypes.Structure):
+    _fields_ = [("record_index", ctypes.c_uint64), ("original_bytes", ctypes.c_uint64),
+                ("ans_bytes", ctypes.c_uint64), ("sidecar_bytes", ctypes.c_uint64),
+                ("owns_table", ctypes.c_uint32), ("table_sum", ctypes.c_uint32),
+                ("table_repaired", ctypes.c_uint32), ("pad", ctypes.c_uint32)]
+
+
+class CkptEntry(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 256), ("anchor_name", ctypes.c_char * 256),
+                ("dtype", ctypes.c_uint32), ("is_raw", ctypes.c_uint32), ("owns_table", ctypes.c_uint32),
+                ("version", ctypes.c_uint32), ("original_bytes", ctypes.c_uint64),
+                ("num_elements", ctypes.c_uint64), ("data_size", ctypes.c_uint64), ("n_units", ctypes.c_uint64),
+                ("unit_bytes", ctypes.c_uint64), ("sidecar_bytes", ctypes.c_uint64)]
+
+
+def write_checkpoint(output_dir, rank, tensors, unit_bytes=0, repair_tables=False, stream=None):
+    """compress_and_save_all: tensors is a list of (name, device tensor or None,
+    dtype tag, cluster id); returns one stats dict per written tensor."""
+    n = len(tensors)
+    names = [t[0].encode() for t in tensors]
+    arr = (CkptTensor * max(n, 1))()
+    for i, (name, t, tag, cid) in enumerate(tensors):
+        ne = _n_elems(t, tag, None) if t is not None else 0
+        arr[i].name = names[i]
+        arr[i].d_ptr = t.data_ptr() if (t is not None and ne) else None
+        arr[i].num_elements = ne
+        arr[i].dtype = tag
+        arr[i].cluster_id = cid
+    st = (CkptStats * max(n, 1))()
+    _check(lib().ckr_ckpt_write(os.fsencode(output_dir), rank, arr, n, unit_bytes, int(bool(repair_tables)), st,
+                                _stream(stream)))
+    written = sum(1 for i in range(n) if arr[i].d_ptr and arr[i].num_elements)
+    return [{f[0]: getattr(st[i], f[0]) for f in CkptStats._fields_ if f[0] != "pad"} for i in range(written)]
+
+
+class Checkpoint:
+    """Reader of a rank's .ansc (v2 or v3) / .mant / .dict files; restores
+    tensors on the device."""
+
+    def __init__(self, directory, rank=0):
+        self._h = ctypes.c_void_p()
+        _check(lib().ckr_ckpt_open(os.fsencode(directory), rank, ctypes.byref(self._h)))
+
+    def __len__(self):
+        return int(lib().ckr_ckpt_count(self._h))
+
+    def info(self, i):
+        e = CkptEntry()
+        _check(lib().ckr_ckpt_info(self._h, i, ctypes.byref(e)))
+        d = {f[0]: getattr(e, f[0]) for f in CkptEntry._fields_}
+        d["name"] = e.name.decode()
+        d["anchor_name"] = e.anchor_name.decode()
+        return d
+
+    def restore(self, i, dst=None, device="cuda", stream=None):
+        """Decode tensor i into dst (a device tensor of its byte size; a new
+        uint8 tensor when None); returns dst."""
+        torch = _torch()
+        info = self.info(i)
+        if dst is None:
+            dst = torch.empty(max(info["original_bytes"], 1), dtype=torch.uint8, device=device)
+        elif dst.numel() * dst.element_size() < info["original_bytes"]:
+            raise CkrError(CKR_E_CAPACITY, "destination too small")
+        _check(lib().ckr_ckpt_restore(self._h, i, dst.data_ptr(), _stream(stream)))
+        return dst
+
+    def close(self):
+        if self._h:
+            lib().ckr_ckpt_close(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

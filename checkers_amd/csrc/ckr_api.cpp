@@ -33,6 +33,15 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
+}  // namespace
+
+int ckr::set_error(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+namespace {
+
 #define CKR_HIP(call)                                                                      \
     do {                                                                                   \
         hipError_t _e = (call);                                                            \

@@ -45,6 +45,9 @@ uint64_t* prof_phase_buffer(uint64_t n, hipStream_t s);
         __VA_ARGS__;                          \
         ::ckr::prof_mark(name, s, false);     \
     } while (0)
+// Sets the calling thread's last error (ckr_last_error) and returns code.
+int set_error(int code, const std::string& msg);
+
 // ------------------------------------------------------------------ launchers
 // All return hipError_t of the launch; geometry is decided inside.
 hipError_t launch_build_enc_table(const TableArg& t, EncSym* d_enc, hipStream_t s);

@@ -224,6 +224,79 @@ CKR_API int ckr_repair_apply(const void* d_words, uint64_t n_elems, int dtype, i
                              const ckr_repair_rule* h_rules, uint32_t n_rules, uint64_t* h_out_tokens,
                              uint64_t* d_seq_out, void* d_workspace, uint64_t workspace_bytes, void* stream);
 
+/* ---- fingerprint weights and clusters (host) ----
+ * ckr_fingerprint_weights ← TensorAnalyzer::compute_fingerprint_weights
+ * (src/TensorAnalyzer.cpp:322-380): h_fp holds n fingerprints of 5 floats
+ * (mean, variance, skewness, kurtosis, range — what ckr_analyze writes);
+ * h_weights[5] = per-dimension variance over the records / sum(variance + 1e-8).
+ * ckr_cluster ← TensorAnalyzer::build_knn_clusters (:440-598): records are
+ * grouped by name prefix ("optimizer.exp_avg_sq::", "optimizer.exp_avg::",
+ * "master_weights::", else model state), fingerprints z-scored per category,
+ * pairs closer than the lower quartile of all pairwise distances merged.
+ * h_cluster_of[i] = cluster id (numbered per category in name order, then by
+ * union-find root) or -1 for a singleton; h_threshold (optional, 4 doubles)
+ * receives the merge threshold of each non-empty category in that order. */
+CKR_API int ckr_fingerprint_weights(const float* h_fp, uint64_t n, double* h_weights);
+CKR_API int ckr_cluster(const char* const* names, const float* h_fp, uint64_t n, int32_t* h_cluster_of,
+                        double* h_threshold);
+
+/* ---- rank checkpoint files ----
+ * ckr_ckpt_write ← ANSCompressor::compress_and_save_all + write_rank_states_file /
+ * write_rank_mantissa_file / write_rank_tables_file (src/ANSCompressor.cpp:1014-1401,
+ * :721-931).  Tensors are taken in record order; those with a null pointer or
+ * no elements are skipped.  cluster_id -1 (singleton) builds its own table;
+ * the first compressed tensor of a cluster builds the cluster's table with the
+ * full alphabet and the others reuse it (their anchor_name is the first record
+ * of the cluster).  Writes <dir>/rank_<r>_states.ansc, <dir>/mantissa/
+ * rank_<r>_mantissa.mant and <dir>/tables/rank_<r>_tables.dict.
+ * unit_bytes 0: the reference's .ansc v2 (one stream per tensor, byte for byte
+ * the reference's files; tensors must be below 4 GiB).  unit_bytes > 0: .ansc
+ * v3, this library's chunked layout: header {magic, 3, rank, n, u64 unit_bytes},
+ * 568-byte index entries (the v2 entry without its headers, then u64 n_units,
+ * u64 meta_offset), a metadata section (per tensor: n_units*256 headers, then
+ * n_units+1 u64 unit offsets), then the data.  repair_tables != 0 repairs a
+ * full-alphabet table that the reference's one-pass normalisation leaves above
+ * 4096 (such streams cannot be decoded) — a deliberate divergence, reported in
+ * h_stats.  h_stats (optional) gets one entry per written tensor. */
+typedef struct {
+    const char* name;
+    const void* d_ptr;
+    uint64_t    num_elements;
+    int32_t     dtype;
+    int32_t     cluster_id;
+} ckr_ckpt_tensor;
+
+typedef struct {
+    uint64_t record_index;
+    uint64_t original_bytes;
+    uint64_t ans_bytes;
+    uint64_t sidecar_bytes;
+    uint32_t owns_table;
+    uint32_t table_sum;      /* sum of the table's frequencies (4096 unless the H1 case) */
+    uint32_t table_repaired;
+    uint32_t pad;
+} ckr_ckpt_stats;
+
+CKR_API int ckr_ckpt_write(const char* output_dir, int rank, const ckr_ckpt_tensor* tensors, uint64_t n,
+                           uint64_t unit_bytes, int repair_tables, ckr_ckpt_stats* h_stats, void* stream);
+
+/* Reader (no counterpart in the reference): parses the three files of a rank
+ * (v2 or v3 states file) and restores any tensor, bit-exact, into device
+ * memory.  A tensor whose table does not sum to 4096 cannot be restored
+ * (CKR_E_TABLE). */
+typedef struct ckr_ckpt ckr_ckpt;
+typedef struct {
+    char     name[256];
+    char     anchor_name[256];
+    uint32_t dtype, is_raw, owns_table, version;
+    uint64_t original_bytes, num_elements, data_size, n_units, unit_bytes, sidecar_bytes;
+} ckr_ckpt_entry;
+CKR_API int ckr_ckpt_open(const char* dir, int rank, ckr_ckpt** out);
+CKR_API uint64_t ckr_ckpt_count(const ckr_ckpt* c);
+CKR_API int ckr_ckpt_info(const ckr_ckpt* c, uint64_t index, ckr_ckpt_entry* out);
+CKR_API int ckr_ckpt_restore(const ckr_ckpt* c, uint64_t index, void* d_dst, void* stream);
+CKR_API void ckr_ckpt_close(ckr_ckpt* c);
+
 /* ---- path selection, no counterpart in the reference.  mode 1 (default):
  * fast kernels — lanes of masked planes coded once per lane count (their
  * streams are identical), units of at most 64 KiB coded and decoded through

@@ -185,3 +185,84 @@ def repair_apply(raw, n, storage_bytes, masked_bits, rules, want_seq=False):
     m = int(lib().oc_repair_apply(_p(raw), n, storage_bytes, masked_bits, _p(rr), len(rules),
                                   _p(seq) if want_seq else None))
     return (m, seq[:m]) if want_seq else m
+
+
+# ---- fingerprint weights and clusters (small n: plain Python)
+def fingerprint_weights(fps):
+    """TensorAnalyzer::compute_fingerprint_weights (src/TensorAnalyzer.cpp:322-380)."""
+    fps = [[float(np.float32(v)) for v in row] for row in fps]
+    n = len(fps)
+    imp = []
+    for d in range(5):
+        m = sum(r[d] for r in fps)
+        m2 = sum(r[d] * r[d] for r in fps)
+        imp.append(m2 / n - (m / n) * (m / n) if n else 0.0)
+    tot = sum(v + 1e-8 for v in imp)
+    return [v / tot for v in imp]
+
+
+def category_of(name):
+    """build_knn_clusters name prefixes (src/TensorAnalyzer.cpp:452-457)."""
+    for p, c in (("optimizer.exp_avg_sq::", "exp_avg_sq"), ("optimizer.exp_avg::", "exp_avg"),
+                 ("master_weights::", "master_weights")):
+        if name.startswith(p):
+            return c
+    return "model_state"
+
+
+def cluster(names, fps):
+    """TensorAnalyzer::build_knn_clusters (src/TensorAnalyzer.cpp:440-598):
+    (cluster id per record or -1, thresholds per non-empty category)."""
+    import math
+    fps = [[float(np.float32(v)) for v in row] for row in fps]
+    cats = {}
+    for i, nm in enumerate(names):
+        cats.setdefault(category_of(nm), []).append(i)
+    out = [None] * len(names)
+    thr_out = []
+    nid = 0
+    for cat in sorted(cats):
+        idx = cats[cat]
+        k = len(idx)
+        mean = [sum(fps[i][d] for i in idx) / k for d in range(5)]
+        sd = []
+        for d in range(5):
+            v = sum((fps[i][d] - mean[d]) ** 2 for i in idx) / k
+            sd.append(1.0 if v < 1e-30 else math.sqrt(v))
+
+        def dist(a, b):
+            return math.sqrt(sum(((fps[idx[a]][d] - fps[idx[b]][d]) / sd[d]) ** 2 for d in range(5)))
+        alld = sorted(dist(a, b) for a in range(k) for b in range(a + 1, k))
+        thr = alld[len(alld) // 4] if alld else 0.0
+        thr_out.append(thr)
+        parent, rank = list(range(k)), [0] * k
+
+        def find(x):
+            while parent[x] != x:
+                parent[x] = parent[parent[x]]
+                x = parent[x]
+            return x
+
+        for a in range(k):
+            for b in range(a + 1, k):
+                if dist(a, b) < thr:
+                    ra, rb = find(a), find(b)
+                    if ra == rb:
+                        continue
+                    if rank[ra] < rank[rb]:
+                        ra, rb = rb, ra
+                    parent[rb] = ra
+                    if rank[ra] == rank[rb]:
+                        rank[ra] += 1
+        groups = {}
+        for a in range(k):
+            groups.setdefault(find(a), []).append(a)
+        for root in sorted(groups):
+            mem = groups[root]
+            if len(mem) >= 2:
+                for a in mem:
+                    out[idx[a]] = nid
+                nid += 1
+            else:
+                out[idx[mem[0]]] = -1
+    return out, thr_out
