@@ -658,28 +658,35 @@ struct FastEncParams {
     uint32_t canon_bytes;       // bytes per canonical entry in the LDS copy (stream order)
 };
 
-// LDS layout (bytes): table 4096 | loff 257 x u32 (+pad) | delta 256 x i32 |
-// canonical headers 12 x u32 | canonical bytes 3 x canon_bytes | rank-0 slots
-// 64 x stride0 | rank-1 slots 64 x stride1 | 32 bytes of read padding.
-static constexpr uint32_t FE_TAB = 0, FE_LOFF = 4096, FE_DELTA = 4096 + 1040, FE_CHDR = 4096 + 1040 + 1024,
-                          FE_CBYTES = FE_CHDR + 48;
+// LDS layout (bytes): table 4096 | canonical headers 12 x u32 | canonical bytes
+// 3 x canon_bytes | rank-0 slots 64 x stride0 | rank-1 slots 64 x stride1 | 32
+// bytes of read padding.  Once the unit is coded the table is dead and its
+// space holds the packer's lane tables: loff 257 x u32 (+pad) | delta 256 x i32.
+static constexpr uint32_t FE_TAB = 0, FE_LOFF = 0, FE_DELTA = 1040, FE_CHDR = 4096, FE_CBYTES = FE_CHDR + 48;
 
 // One symbol of rans_encode_kernel's loop body (ANSCompressor.cpp:180-202)
-// without branches: the (at most two) renormalisation bytes are always stored,
-// to the lane's slot when emitted and to a per-thread dummy byte otherwise; the
-// first byte emitted is the last byte of the stream (slot filled from its end).
-// ESC: the table may give f == 0 to a symbol of the data (raw-byte escape, no
-// state update, :185-192); tables built from the data itself never do.
+// without branches.  The stream fills the lane's slot from its end: byte e of
+// the emission order goes to slot[sl-1-e].  Both possible renormalisation
+// bytes are stored on every symbol, at the positions the next two bytes would
+// take; a byte that is not emitted lands where a later byte overwrites it, or
+// before the stream's first byte, outside the stream.  A store that would fall
+// before the slot's start goes to the slot's first padding byte, which no
+// stream uses (a lane that needs more than its slot has overflowed and its
+// unit is redone by the general kernels).  ESC: the table may give f == 0 to a symbol of the data
+// (raw-byte escape, no state update, :185-192); tables built from the data
+// itself never do.
 template <bool ESC>
 __device__ __forceinline__ void enc_sym_lds(uint32_t& x, uint32_t& e, uint32_t sym, const EncSym& s, uint8_t* slot,
-                                            uint32_t sl, uint8_t* dummy) {
+                                            uint32_t sl) {
     const bool esc = ESC && s.xmax == 0;
     const bool e1 = esc || x >= s.xmax;
     const uint32_t x1 = (e1 && !esc) ? (x >> 8) : x;
     const bool e2 = !esc && e1 && x1 >= s.xmax;
     const uint32_t xr = e2 ? (x1 >> 8) : x1;
-    uint8_t* a1 = (e1 && e < sl) ? slot + (sl - 1 - e) : dummy;
-    uint8_t* a2 = (e2 && e + 1 < sl) ? slot + (sl - 2 - e) : dummy;
+    // u32 wrap-around: positions before the slot's start become slot[sl], the
+    // first byte of the slot's padding
+    uint8_t* a1 = slot + min(sl - 1u - e, sl);
+    uint8_t* a2 = slot + min(sl - 2u - e, sl);
     *a1 = (uint8_t)(esc ? sym : x);
     *a2 = (uint8_t)x1;
     e += (e1 ? 1u : 0u) + (e2 ? 1u : 0u);
@@ -811,7 +818,6 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
     const uint32_t lm = live_mask32<SPE>();
     uint8_t* slot0 = lds8 + st0_off + j * fp.stride0;
     uint8_t* slot1 = lds8 + st1_off + j * fp.stride1;
-    uint8_t* dummy = lds8 + st1_off + 64 * fp.stride1 + 4 * j;  // 256 bytes after the slots
     uint32_t x0 = L, x1 = L, e0 = 0, e1 = 0;
 
     const uint32_t col = 4 * j;
@@ -827,8 +833,8 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
             v &= lm;
             const uint32_t sy0 = (v >> (8 * FL)) & 255u, sy1 = v >> 24;
             const EncSym t0 = tab[sy0], t1 = tab[sy1];
-            enc_sym_lds<ESC>(x0, e0, sy0, t0, slot0, fp.sl0, dummy);
-            if (nvalid == 4) enc_sym_lds<ESC>(x1, e1, sy1, t1, slot1, fp.sl1, dummy);
+            enc_sym_lds<ESC>(x0, e0, sy0, t0, slot0, fp.sl0);
+            if (nvalid == 4) enc_sym_lds<ESC>(x1, e1, sy1, t1, slot1, fp.sl1);
         }
         // rows K-2 .. 0 in groups of 32; the next group's loads are in flight
         // while the current group is coded.  When the unit length is a multiple
@@ -863,8 +869,8 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
                     if (k < 0) break;
                     const uint32_t w = r[i0 + i];
                     if (SIDE) sc16[64 * k] = (uint16_t)(SPE == 2 ? (w & 0xFFFFu) : ((w & 0xFFu) | ((w >> 8) & 0xFF00u)));
-                    enc_sym_lds<ESC>(x0, e0, (w >> (8 * FL)) & 255u, t0[i], slot0, fp.sl0, dummy);
-                    enc_sym_lds<ESC>(x1, e1, w >> 24, t1[i], slot1, fp.sl1, dummy);
+                    enc_sym_lds<ESC>(x0, e0, (w >> (8 * FL)) & 255u, t0[i], slot0, fp.sl0);
+                    enc_sym_lds<ESC>(x1, e1, w >> 24, t1[i], slot1, fp.sl1);
                 }
             }
         };
@@ -947,69 +953,72 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
         return;
     }
     __syncthreads();
-    // packed bytes in 16-byte destination chunks, thread j taking chunks j,
-    // j+64, j+128, j+192 of every 256; the four binary searches for the lane
-    // at each chunk's first byte advance together.  A chunk is the OR of one
-    // masked 16-byte LDS read per lane it covers (usually one, at a lane
-    // boundary two).  The unit's first and last chunks are shared with the
-    // neighbouring units: bytes outside the unit are not stored.
+    // Packed bytes in 16-byte destination chunks (aligned in global memory).
+    // The streams of this thread's four lanes are one contiguous run of the
+    // output, [excl, excl + tsum); the thread writes every chunk whose first
+    // unit byte lies in that run (chunk 0, which may start before the unit,
+    // belongs to the run holding byte 0), walking its lanes in order; a chunk
+    // that runs past the end of the run takes its remaining bytes from the
+    // following lanes.  A chunk inside one lane is one unaligned 16-byte LDS
+    // read; a chunk over a lane boundary ORs one masked read per lane.  Bytes
+    // outside the unit (its first and last chunks are shared with the
+    // neighbouring units) are not stored.
     const uint64_t ab = reinterpret_cast<uintptr_t>(dst);
-    const uint64_t a0 = ab & ~15ull, a1 = (ab + size + 15) & ~15ull;
-    const uint32_t nchunk = (uint32_t)((a1 - a0) >> 4);
+    const uint64_t a0 = ab & ~15ull;
     const int32_t qbase = (int32_t)(a0 - ab);  // unit-relative byte of chunk 0 (-15..0)
-    for (uint32_t c0 = 0; c0 < nchunk; c0 += 256) {
-        uint32_t lo[4];
-        int32_t q0[4];
+    const int32_t isize = (int32_t)size;
+    const int32_t r0 = (int32_t)excl, r1 = (int32_t)(excl + tsum);
+    if (r1 > r0) {
+        // first owned chunk: the one containing byte r0 unless it starts before r0
+        int32_t c = (r0 - qbase) >> 4;
+        if (qbase + 16 * c < r0 && r0 > 0) c++;
+        uint32_t L = 4 * j;
+        int32_t lo = (int32_t)loff[L], hi = (int32_t)loff[L + 1], dl = delta[L];
+        for (;; c++) {
+            const int32_t q = qbase + 16 * c;
+            if (q >= r1) break;
+            const int32_t qs = max(q, 0), qe = min(q + 16, isize);
+            while (hi <= qs && L < 255) { L++; lo = hi; hi = (int32_t)loff[L + 1]; dl = delta[L]; }
+            uint4 v;
+            if (q >= lo && q + 16 <= hi) {
+                v = lds_read16(lds8, (uint32_t)(dl + q));
+            } else {
+                v = make_uint4(0, 0, 0, 0);
+                uint32_t L2 = L;
+                int32_t lo2 = lo, hi2 = hi, dl2 = dl;
+                for (;;) {
+                    const int32_t s0 = max(lo2, qs), s1 = min(hi2, qe);
+                    if (s1 > s0) {
+                        const uint4 r = lds_read16(lds8, (uint32_t)(dl2 + q));
+                        const uint32_t b0 = (uint32_t)(s0 - q), b1 = (uint32_t)(s1 - q);
+                        uint32_t m[4];
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            q0[k] = qbase + 16 * (int32_t)(c0 + j + 64 * k);
-            lo[k] = 0;
-        }
+                        for (int w4 = 0; w4 < 4; w4++) {
+                            uint32_t mm = 0;
 #pragma unroll
-        for (uint32_t step = 128; step > 0; step >>= 1)
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t qf = q0[k] < 0 ? 0u : (uint32_t)q0[k];
-                if (loff[lo[k] + step] <= qf) lo[k] += step;
-            }
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const uint32_t c = c0 + j + 64 * k;
-            if (c >= nchunk) break;
-            const int32_t q = q0[k];
-            uint4 v = make_uint4(0, 0, 0, 0);
-            // lanes covering [max(q,0), min(q+16, size)), each contributing its bytes
-            uint32_t Lc = lo[k];
-            const int32_t qend = min(q + 16, (int32_t)size);
-            while (Lc < 256 && (int32_t)loff[Lc] < qend) {
-                const int32_t s0 = max((int32_t)loff[Lc], q), s1 = min((int32_t)loff[Lc + 1], qend);
-                if (s1 > s0) {
-                    const uint4 r = lds_read16(lds8, (uint32_t)(delta[Lc] + q));
-                    // byte b of the chunk belongs to this lane iff s0 - q <= b < s1 - q
-                    const uint32_t b0 = (uint32_t)(s0 - q), b1 = (uint32_t)(s1 - q);
-                    uint32_t m[4];
-#pragma unroll
-                    for (int w4 = 0; w4 < 4; w4++) {
-                        uint32_t mm = 0;
-#pragma unroll
-                        for (int bb = 0; bb < 4; bb++) {
-                            const uint32_t bi = 4 * w4 + bb;
-                            mm |= (bi >= b0 && bi < b1) ? (0xFFu << (8 * bb)) : 0u;
+                            for (int bb = 0; bb < 4; bb++) {
+                                const uint32_t bi = 4 * w4 + bb;
+                                mm |= (bi >= b0 && bi < b1) ? (0xFFu << (8 * bb)) : 0u;
+                            }
+                            m[w4] = mm;
                         }
-                        m[w4] = mm;
+                        v.x |= r.x & m[0]; v.y |= r.y & m[1]; v.z |= r.z & m[2]; v.w |= r.w & m[3];
                     }
-                    v.x |= r.x & m[0]; v.y |= r.y & m[1]; v.z |= r.z & m[2]; v.w |= r.w & m[3];
+                    if (hi2 >= qe || L2 >= 255) break;
+                    L2++;
+                    lo2 = hi2;
+                    hi2 = (int32_t)loff[L2 + 1];
+                    dl2 = delta[L2];
                 }
-                Lc++;
             }
-            uint8_t* wp = reinterpret_cast<uint8_t*>(a0 + 16ull * c);
-            if (q >= 0 && q + 16 <= (int32_t)size) {
+            uint8_t* wp = reinterpret_cast<uint8_t*>(a0 + 16ull * (uint32_t)c);
+            if (q >= 0 && q + 16 <= isize) {
                 *reinterpret_cast<uint4*>(wp) = v;
             } else {
                 const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                 for (int bb = 0; bb < 16; bb++)
-                    if (q + bb >= 0 && q + bb < (int32_t)size) wp[bb] = (uint8_t)(vv[bb >> 2] >> (8 * (bb & 3)));
+                    if (q + bb >= 0 && q + bb < isize) wp[bb] = (uint8_t)(vv[bb >> 2] >> (8 * (bb & 3)));
             }
         }
     }
@@ -1031,7 +1040,7 @@ static uint32_t slot_stride(uint32_t sl) {
 }
 
 uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p) {
-    return FE_CBYTES + 3 * p.canon_bytes + 64 * (slot_stride(p.sl0) + slot_stride(p.sl1)) + 256 + 32;
+    return FE_CBYTES + 3 * p.canon_bytes + 64 * (slot_stride(p.sl0) + slot_stride(p.sl1)) + 32;
 }
 
 hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
