@@ -658,41 +658,81 @@ struct FastEncParams {
     uint32_t canon_bytes;       // bytes per canonical entry in the LDS copy (stream order)
 };
 
-// LDS layout (bytes): table 4096 | canonical headers 12 x u32 | canonical bytes
-// 3 x canon_bytes | rank-0 slots 64 x stride0 | rank-1 slots 64 x stride1 | 32
-// bytes of read padding.  Once the unit is coded the table is dead and its
+// LDS layout (bytes): guard 512 | rank-0 slots 64 x stride0 | rank-1 slots 64 x
+// stride1 | table 3 x 1024 (SoA: rcp, cmpl | rsh << 24, bias | 8f << 16) | canonical
+// headers 12 x u32 | canonical bytes 3 x canon_bytes | 32 bytes of read
+// padding.  A lane's dwords are flushed downward from the end of its slot; a
+// lane that outgrows its slot keeps flushing into the slots below it (lanes of
+// the same unit, whose bytes are then redone by the general kernels) and, for
+// the lowest slot, into the guard (at most 2 bytes per symbol, 256 symbols),
+// so the table and the canonical headers, which the unit's sizes depend on,
+// are never overwritten.  Once the unit is coded the table is dead and its
 // space holds the packer's lane tables: loff 257 x u32 (+pad) | delta 256 x i32.
-static constexpr uint32_t FE_TAB = 0, FE_LOFF = 0, FE_DELTA = 1040, FE_CHDR = 4096, FE_CBYTES = FE_CHDR + 48;
+static constexpr uint32_t FE_GUARD = 512;
+static constexpr uint32_t FE_TABSZ = 3 * 1024, FE_LOFF = 0, FE_DELTA = 1040, FE_XCH = 2080, FE_BCAST = 2592;
+// canonical headers 12 x u32 and the ticket, then the canonical bytes
+static constexpr uint32_t FE_CBYTES_REL = FE_TABSZ + 64;
+
+// Lane coder state.  x: rANS state.  {hi, lo}: the last 8 bytes emitted, the
+// newest in the top byte of hi.  sel: v_perm selector 0x08090A0B - P*0x01010101
+// with P (0..7) the emitted bytes not yet flushed (the top P bytes of the
+// window).  ptr: LDS byte address of the lane's next flushed dword.
+struct EncLane {
+    uint32_t x, hi, lo, sel, ptr;
+};
 
 // One symbol of rans_encode_kernel's loop body (ANSCompressor.cpp:180-202)
-// without branches.  The stream fills the lane's slot from its end: byte e of
-// the emission order goes to slot[sl-1-e].  Both possible renormalisation
-// bytes are stored on every symbol, at the positions the next two bytes would
-// take; a byte that is not emitted lands where a later byte overwrites it, or
-// before the stream's first byte, outside the stream.  A store that would fall
-// before the slot's start goes to the slot's first padding byte, which no
-// stream uses (a lane that needs more than its slot has overflowed and its
-// unit is redone by the general kernels).  ESC: the table may give f == 0 to a symbol of the data
-// (raw-byte escape, no state update, :185-192); tables built from the data
-// itself never do.
+// without branches.  tA = rcp, tB = cmpl | rsh << 24, tC = bias | 8f << 16
+// (see EncSym).  Renormalisation emits n in {0,1,2} bytes: x >= f*2^19 and
+// x >= f*2^27 are (x >> 16) >= 8f and (x >> 24) >= 8f.  The n low bytes of x,
+// low byte first (the reference's emission order), enter the window from the
+// top: one v_alignbyte per register shifts by n bytes.  ESC: the table may give
+// f == 0 to a symbol of the data (raw-byte escape, no state update, :185-192);
+// tables built from the data itself never do.
 template <bool ESC>
-__device__ __forceinline__ void enc_sym_lds(uint32_t& x, uint32_t& e, uint32_t sym, const EncSym& s, uint8_t* slot,
-                                            uint32_t sl) {
-    const bool esc = ESC && s.xmax == 0;
-    const bool e1 = esc || x >= s.xmax;
-    const uint32_t x1 = (e1 && !esc) ? (x >> 8) : x;
-    const bool e2 = !esc && e1 && x1 >= s.xmax;
-    const uint32_t xr = e2 ? (x1 >> 8) : x1;
-    // u32 wrap-around: positions before the slot's start become slot[sl], the
-    // first byte of the slot's padding
-    uint8_t* a1 = slot + min(sl - 1u - e, sl);
-    uint8_t* a2 = slot + min(sl - 2u - e, sl);
-    *a1 = (uint8_t)(esc ? sym : x);
-    *a2 = (uint8_t)x1;
-    e += (e1 ? 1u : 0u) + (e2 ? 1u : 0u);
-    const uint32_t q = __umulhi(xr, s.rcp) >> (s.cmpl_rsh >> 16);
-    const uint32_t xn = xr + s.bias + __umul24(q, s.cmpl_rsh & 0xFFFFu);
-    x = esc ? x : xn;
+__device__ __forceinline__ void enc_step(EncLane& s, uint32_t sym, uint32_t tA, uint32_t tB, uint32_t tC) {
+    const uint32_t f8 = tC >> 16;
+    const uint32_t x = s.x;
+    uint32_t n4 = ((x >> 24) >= f8) ? 0x02020202u : (((x >> 16) >= f8) ? 0x01010101u : 0u);
+    uint32_t ins = x;
+    bool esc = false;
+    if (ESC) {
+        esc = f8 == 0u;
+        n4 = esc ? 0x01010101u : n4;
+        ins = esc ? sym : x;
+    }
+    const uint32_t xr = __builtin_amdgcn_alignbyte(0u, x, n4);
+    s.lo = __builtin_amdgcn_alignbyte(s.hi, s.lo, n4);
+    s.hi = __builtin_amdgcn_alignbyte(ins, s.hi, n4);
+    s.sel -= n4;
+    const uint32_t q = __umulhi(xr, tA) >> (tB >> 24);
+    const uint32_t xn = (xr + (tC & 0xFFFFu)) + __umul24(q, tB);
+    s.x = (ESC && esc) ? x : xn;
+}
+
+// Flush the 4 oldest pending bytes when P >= 4 (called at least every 2
+// symbols, so P <= 7).  The dword holds them in stream order (the newest at the
+// lowest address): a byte-reversing select out of the 8-byte window.
+// The dword is stored whatever P: with P < 4 it lands at the lane's next
+// flush position, which a later flush or the final partial dword overwrites,
+// or, when the stream ends on a dword boundary, just below the stream (in the
+// slot, its padding or the guard).  P >= 4 exactly when bit 3 of the
+// selector's low byte (0x0B - P) is clear.
+__device__ __forceinline__ void enc_flush(EncLane& s, uint8_t* lds8) {
+    *reinterpret_cast<uint32_t*>(lds8 + s.ptr) = __builtin_amdgcn_perm(s.hi, s.lo, s.sel);
+    const bool fl = (s.sel & 8u) == 0u;
+    s.ptr -= fl ? 4u : 0u;
+    s.sel += fl ? 0x04040404u : 0u;
+}
+
+// End of the lane: the remaining P (< 4 after a flush) bytes go into the top of
+// one more dword (its lower bytes lie before the stream's start).  Returns the
+// byte count; the stream then occupies [slot_end - count, slot_end).
+__device__ __forceinline__ uint32_t enc_finish(EncLane& s, uint8_t* lds8, uint32_t slot_end) {
+    enc_flush(s, lds8);
+    const uint32_t P = 0x0Bu - (s.sel & 0xFFu);
+    *reinterpret_cast<uint32_t*>(lds8 + s.ptr) = __builtin_amdgcn_perm(s.hi, s.lo, s.sel);
+    return (slot_end - 4u - s.ptr) + P;
 }
 
 // Look-back status words.  Their values carry everything the protocol needs
@@ -760,54 +800,142 @@ __device__ __forceinline__ uint32_t lane_of(const uint32_t* loff, uint32_t q) {
     return lo;
 }
 
+// Coding of one wave's lane of every column of a unit whose rows are all full
+// (length a multiple of 256, so every column has the same nrows rows): W = 0
+// codes byte FL of each column, W = 1 byte 3.  Rows are taken from the top down.
+// The rows above the highest multiple of 32 go one at a time; then groups of
+// 32 rows, the next group's loads in flight while the current one is coded
+// (loads and table reads are unconditional, so the waits stay exact), and each
+// 8-row batch's table words read while the batch before it is coded.  Pending
+// bytes are flushed after every second row.  Wave W writes the sidecar of the
+// rows k with k & 1 == W.
+template <int SPE, bool ESC, bool SIDE, int W>
+__device__ __forceinline__ void enc_full_rows(EncLane& c, const uint8_t* ucol, uint8_t* sidecar, uint64_t ubase,
+                                              uint32_t j, uint32_t nrows, const uint32_t* tabA, uint8_t* lds8) {
+    constexpr int FL = SPE == 2 ? 2 : 1;
+    constexpr uint32_t SH = W ? 24u : 8u * FL;
+    const uint32_t* tabB = tabA + 256;
+    const uint32_t* tabC = tabA + 512;
+    const uint32_t* in32 = reinterpret_cast<const uint32_t*>(ucol);          // row k at in32[64 k]
+    uint16_t* sc16 = SIDE ? reinterpret_cast<uint16_t*>(sidecar + (ubase >> 1) + 2 * j) : nullptr;  // row k at sc16[64 k]
+    auto side = [&](uint16_t* p, uint32_t wd) {
+        if (SIDE) *p = (uint16_t)(SPE == 2 ? (wd & 0xFFFFu) : ((wd & 0xFFu) | ((wd >> 8) & 0xFF00u)));
+    };
+    const uint32_t ng = nrows >> 5;  // full groups: rows [0, 32 ng)
+    for (int32_t k = (int32_t)nrows - 1; k >= (int32_t)(32 * ng); k--) {
+        const uint32_t wd = in32[64 * k];
+        if ((uint32_t)(k & 1) == W) side(sc16 + 64 * k, wd);
+        const uint32_t sy = (wd >> SH) & 255u;
+        enc_step<ESC>(c, sy, tabA[sy], tabB[sy], tabC[sy]);
+        if ((k & 1) == 0) enc_flush(c, lds8);
+    }
+    enc_flush(c, lds8);
+    if (ng == 0) return;
+    // group g: rows 32g+31 (r[0]) down to 32g (r[31])
+    auto load = [&](uint32_t (&r)[32], uint32_t g) {
+        const uint32_t* p = in32 + 64 * (32 * g + 31);
+#pragma unroll
+        for (int i = 0; i < 32; i++) r[i] = p[-64 * i];
+    };
+    auto code = [&](const uint32_t (&r)[32], uint32_t g) {
+        uint32_t ta[2][8], tbw[2][8], tcw[2][8];
+        auto fetch = [&](int buf, int i0) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t sy = (r[i0 + i] >> SH) & 255u;
+                ta[buf][i] = tabA[sy]; tbw[buf][i] = tabB[sy]; tcw[buf][i] = tabC[sy];
+            }
+        };
+        uint16_t* scp = SIDE ? sc16 + 64 * (32 * g + 31) : nullptr;
+        fetch(0, 0);
+#pragma unroll
+        for (int bt = 0; bt < 4; bt++) {
+            if (bt < 3) fetch((bt + 1) & 1, 8 * (bt + 1));
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int ii = 8 * bt + i;               // row 32g+31-ii: parity (ii & 1) ^ 1
+                if (((ii & 1) ^ 1) == W) side(scp - 64 * ii, r[ii]);
+                enc_step<ESC>(c, (r[ii] >> SH) & 255u, ta[bt & 1][i], tbw[bt & 1][i], tcw[bt & 1][i]);
+                if (i & 1) enc_flush(c, lds8);
+            }
+        }
+    };
+    uint32_t ra[32], rb[32];
+    uint32_t g = ng - 1;
+    load(ra, g);
+    for (;;) {
+        if (g == 0) { code(ra, 0); break; }
+        load(rb, g - 1);
+        code(ra, g);
+        g--;
+        if (g == 0) { code(rb, 0); break; }
+        load(ra, g - 1);
+        code(rb, g);
+        g--;
+    }
+}
+
 template <int SPE, bool ESC, bool SIDE>
-__global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
-                                                         const EncSym* __restrict__ d_enc,
-                                                         const uint32_t* __restrict__ canon, FastEncParams fp,
-                                                         ckr_stream_header* __restrict__ hdrs,
-                                                         uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out,
-                                                         uint64_t* __restrict__ unit_off,
-                                                         uint64_t* __restrict__ status, uint32_t* __restrict__ ctl,
-                                                         uint32_t* __restrict__ redo_list,
-                                                         uint64_t* __restrict__ phase) {
+__global__ void __launch_bounds__(128) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
+                                                          const EncSym* __restrict__ d_enc,
+                                                          const uint32_t* __restrict__ canon, FastEncParams fp,
+                                                          ckr_stream_header* __restrict__ hdrs,
+                                                          uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out,
+                                                          uint64_t* __restrict__ unit_off,
+                                                          uint64_t* __restrict__ status, uint32_t* __restrict__ ctl,
+                                                          uint32_t* __restrict__ redo_list,
+                                                          uint64_t* __restrict__ phase) {
     extern __shared__ uint32_t lds[];
     const uint64_t t_start = wall_clock64();
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
-    const EncSym* tab = reinterpret_cast<const EncSym*>(lds8 + FE_TAB);
-    uint32_t* loff = reinterpret_cast<uint32_t*>(lds8 + FE_LOFF);
-    int32_t* delta = reinterpret_cast<int32_t*>(lds8 + FE_DELTA);
-    uint32_t* chdr = reinterpret_cast<uint32_t*>(lds8 + FE_CHDR);
-    const uint32_t st0_off = FE_CBYTES + 3 * fp.canon_bytes;
+    const uint32_t st0_off = FE_GUARD;
     const uint32_t st1_off = st0_off + 64 * fp.stride0;
-    const uint32_t j = threadIdx.x;
+    const uint32_t tb = st1_off + 64 * fp.stride1;  // table (3 arrays of 256 u32)
+    const uint32_t* tabA = reinterpret_cast<const uint32_t*>(lds8 + tb);
+    const uint32_t* tabB = tabA + 256;
+    const uint32_t* tabC = tabA + 512;
+    uint32_t* loff = reinterpret_cast<uint32_t*>(lds8 + tb + FE_LOFF);
+    int32_t* delta = reinterpret_cast<int32_t*>(lds8 + tb + FE_DELTA);
+    uint32_t* xch = reinterpret_cast<uint32_t*>(lds8 + tb + FE_XCH);   // wave 1's chains: count, state
+    uint32_t* bc = reinterpret_cast<uint32_t*>(lds8 + tb + FE_BCAST);  // unit-wide values from wave 0
+    uint32_t* chdr = reinterpret_cast<uint32_t*>(lds8 + tb + FE_TABSZ);
+    const uint32_t cb_off = tb + FE_CBYTES_REL;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0: plane FL, 1: plane 3
+    const uint32_t j = tid & 63;                                  // column
 
-    {   // table, canonical headers and canonical streams (byte order), loads batched
-        const uint32_t* d_tab = reinterpret_cast<const uint32_t*>(d_enc);
-        uint32_t tv[16];
+    {   // table (EncSym → SoA), canonical headers and canonical streams (byte order), loads batched
+        const uint4* d_tab = reinterpret_cast<const uint4*>(d_enc);
+        uint4 tv[2];
 #pragma unroll
-        for (int k = 0; k < 16; k++) tv[k] = d_tab[j + 64 * k];
+        for (int k = 0; k < 2; k++) tv[k] = d_tab[tid + 128 * k];
+        uint32_t* wA = reinterpret_cast<uint32_t*>(lds8 + tb);
 #pragma unroll
-        for (int k = 0; k < 16; k++) lds[j + 64 * k] = tv[k];
+        for (int k = 0; k < 2; k++) {
+            const EncSym e = {tv[k].x, tv[k].y, tv[k].z, tv[k].w};
+            wA[tid + 128 * k] = e.rcp;
+            wA[256 + tid + 128 * k] = (e.cmpl_rsh & 0xFFFFu) | ((e.cmpl_rsh >> 16) << 24);
+            wA[512 + tid + 128 * k] = e.bias | ((e.xmax >> 16) << 16);  // xmax = f << 19: 8f in the top half
+        }
         const uint32_t* cs = canon + 3 * (4 + fp.cw);
-        uint32_t* cb32 = reinterpret_cast<uint32_t*>(lds8 + FE_CBYTES);
+        uint32_t* cb32 = reinterpret_cast<uint32_t*>(lds8 + cb_off);
         const uint32_t ncb = 3 * fp.canon_bytes / 4;
         const uint32_t cb_per = fp.canon_bytes / 4;
         for (uint32_t i0 = 0; i0 < ncb; i0 += 512) {
-            uint32_t cv[8];
+            uint32_t cv[4];
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                const uint32_t i = i0 + j + 64 * k;
+            for (int k = 0; k < 4; k++) {
+                const uint32_t i = i0 + tid + 128 * k;
                 cv[k] = i < ncb ? cs[(i / cb_per) * fp.cw + (i % cb_per)] : 0u;
             }
 #pragma unroll
-            for (int k = 0; k < 8; k++) { const uint32_t i = i0 + j + 64 * k; if (i < ncb) cb32[i] = cv[k]; }
+            for (int k = 0; k < 4; k++) { const uint32_t i = i0 + tid + 128 * k; if (i < ncb) cb32[i] = cv[k]; }
         }
-        if (j < 12) chdr[j] = canon[(j >> 2) * (4 + fp.cw) + (j & 3)];
+        if (tid < 12) chdr[tid] = canon[(tid >> 2) * (4 + fp.cw) + (tid & 3)];
+        if (tid == 0) chdr[12] = atomicAdd(&ctl[0], 1u);  // ticket
     }
-    uint32_t tk = 0;
-    if (j == 0) tk = atomicAdd(&ctl[0], 1u);
-    const uint64_t u = __shfl(tk, 0, 64);
     __syncthreads();
+    const uint64_t u = __builtin_amdgcn_readfirstlane(chdr[12]);
     if (u >= g.n_units) return;
 
     const uint64_t t_ready = wall_clock64();
@@ -816,112 +944,81 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
     const uint8_t* usrc = src + ubase;
     constexpr int FL = SPE == 2 ? 2 : 1;  // byte of the first live lane in a column
     const uint32_t lm = live_mask32<SPE>();
-    uint8_t* slot0 = lds8 + st0_off + j * fp.stride0;
-    uint8_t* slot1 = lds8 + st1_off + j * fp.stride1;
-    uint32_t x0 = L, x1 = L, e0 = 0, e1 = 0;
+    const uint32_t sh = w ? 24u : 8u * FL;  // this wave's byte of the column
+    const uint32_t end0 = st0_off + j * fp.stride0 + fp.sl0;  // slot ends (LDS byte addresses)
+    const uint32_t end1 = st1_off + j * fp.stride1 + fp.sl1;
+    const uint32_t endw = w ? end1 : end0;
+    EncLane c{L, 0u, 0u, 0x08090A0Bu, endw - 4u};
 
     const uint32_t col = 4 * j;
     const uint32_t K = len > col ? (len - col + 255) / 256 : 0u;
-    if (K > 0) {
-        {   // top row: may be partial (bf16 tail: lane 4j+3 has one symbol fewer)
-            const uint32_t p = 256 * (K - 1) + col;
+    if ((len & 255u) == 0) {
+        if (w == 0) enc_full_rows<SPE, ESC, SIDE, 0>(c, usrc + col, sidecar, ubase, j, len >> 8, tabA, lds8);
+        else enc_full_rows<SPE, ESC, SIDE, 1>(c, usrc + col, sidecar, ubase, j, len >> 8, tabA, lds8);
+    } else {
+        // A tensor's last unit: rows from the top down, one at a time; the top
+        // row may be partial (bf16: lane 4j+3 has one symbol fewer).
+        for (int32_t k = (int32_t)K - 1; k >= 0; k--) {
+            const uint32_t p = 256 * (uint32_t)k + col;
             const uint32_t nvalid = (len - p) < 4 ? (len - p) : 4;
             uint32_t v = 0;
             if (nvalid == 4) v = *reinterpret_cast<const uint32_t*>(usrc + p);
             else for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)usrc[p + b] << (8 * b);
-            if (SIDE) write_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
+            if (SIDE && (uint32_t)(k & 1) == w) write_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
             v &= lm;
-            const uint32_t sy0 = (v >> (8 * FL)) & 255u, sy1 = v >> 24;
-            const EncSym t0 = tab[sy0], t1 = tab[sy1];
-            enc_sym_lds<ESC>(x0, e0, sy0, t0, slot0, fp.sl0);
-            if (nvalid == 4) enc_sym_lds<ESC>(x1, e1, sy1, t1, slot1, fp.sl1);
-        }
-        // rows K-2 .. 0 in groups of 32; the next group's loads are in flight
-        // while the current group is coded.  When the unit length is a multiple
-        // of 256 every column has the same K: kk is then wave-uniform and the
-        // row guards are scalar.
-        int32_t kk = (int32_t)K - 2;
-        if ((len & 255u) == 0) kk = __builtin_amdgcn_readfirstlane(kk);
-        uint32_t ra[32], rb[32];
-        // row k of this column: 32 bits at usrc + 256k + 4j; its sidecar: 16 bits at
-        // sidecar + (ubase + 256k + 4j) / 2
-        const uint32_t* in32 = reinterpret_cast<const uint32_t*>(usrc + col);
-        uint16_t* sc16 = SIDE ? reinterpret_cast<uint16_t*>(sidecar + (ubase >> 1) + 2 * j) : nullptr;
-        auto load_rows = [&](uint32_t (&r)[32], int32_t top) {
-#pragma unroll
-            for (int i = 0; i < 32; i++) r[i] = (top - i >= 0) ? in32[64 * (top - i)] : 0u;
-        };
-        // 8 rows at a time: the 16 table entries are read before any of the
-        // slot stores of those rows, so their LDS latency overlaps
-        auto code_rows = [&](const uint32_t (&r)[32], int32_t top) {
-#pragma unroll
-            for (int i0 = 0; i0 < 32; i0 += 8) {
-                if (top - i0 < 0) break;
-                EncSym t0[8], t1[8];
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    t0[i] = tab[(r[i0 + i] >> (8 * FL)) & 255u];
-                    t1[i] = tab[r[i0 + i] >> 24];
-                }
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const int32_t k = top - i0 - i;
-                    if (k < 0) break;
-                    const uint32_t w = r[i0 + i];
-                    if (SIDE) sc16[64 * k] = (uint16_t)(SPE == 2 ? (w & 0xFFFFu) : ((w & 0xFFu) | ((w >> 8) & 0xFF00u)));
-                    enc_sym_lds<ESC>(x0, e0, (w >> (8 * FL)) & 255u, t0[i], slot0, fp.sl0);
-                    enc_sym_lds<ESC>(x1, e1, w >> 24, t1[i], slot1, fp.sl1);
-                }
-            }
-        };
-        if (kk >= 0) load_rows(ra, kk);
-        while (kk >= 0) {
-            if (kk - 32 >= 0) load_rows(rb, kk - 32);
-            code_rows(ra, kk);
-            kk -= 32;
-            if (kk < 0) break;
-            if (kk - 32 >= 0) load_rows(ra, kk - 32);
-            code_rows(rb, kk);
-            kk -= 32;
+            const uint32_t sy = (v >> sh) & 255u;
+            if (w == 0 || nvalid == 4) enc_step<ESC>(c, sy, tabA[sy], tabB[sy], tabC[sy]);
+            if ((k & 1) == 0) enc_flush(c, lds8);
         }
     }
-    // byte counts, final states and LDS stream starts of the four lanes of this column
-    uint32_t cnt[4], fs[4], sa[4];
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-        if (b == FL) { cnt[b] = e0; fs[b] = x0; sa[b] = st0_off + j * fp.stride0 + fp.sl0 - min(e0, fp.sl0); }
-        else if (b == 3) { cnt[b] = e1; fs[b] = x1; sa[b] = st1_off + j * fp.stride1 + fp.sl1 - min(e1, fp.sl1); }
-        else {
-            const uint32_t pb = col + b;
-            const uint32_t Kb = len > pb ? (len - pb + 255) / 256 : 0u;
-            const uint32_t ent = (chdr[0] == Kb) ? 0u : ((chdr[4] == Kb) ? 1u : 2u);
-            fs[b] = chdr[4 * ent + 1];
-            cnt[b] = chdr[4 * ent + 2];
-            sa[b] = FE_CBYTES + ent * fp.canon_bytes;
-        }
-    }
-    const uint32_t tsum = cnt[0] + cnt[1] + cnt[2] + cnt[3];
-    uint32_t incl = tsum;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        const uint32_t v = __shfl_up(incl, d, 64);
-        if ((int)j >= d) incl += v;
-    }
-    const uint32_t total = __shfl(incl, 63, 64);
-    const uint32_t excl = incl - tsum;
-    const bool raw = total >= len;
-    const uint32_t size = raw ? len : total;
-    const bool over = e0 > fp.sl0 || e1 > fp.sl1;
-    const bool any_over = __ballot(over) != 0;
+    const uint32_t e = enc_finish(c, lds8, endw);
+    __syncthreads();  // both waves done: the table is dead
+    if (w == 1) { xch[j] = e; xch[64 + j] = c.x; }
+    __syncthreads();
 
-    const uint64_t t_coded = wall_clock64();
-    const uint64_t off = lookback_wave(status, u, size, &ctl[2], j);
-    const uint64_t t_placed = wall_clock64();
-    if (j == 0) {
-        unit_off[u] = off;
-        if (u + 1 == g.n_units) unit_off[u + 1] = off + size;
-    }
-    {   // headers (4 per thread, 64 contiguous bytes) and the lane tables for packing
+    if (w == 0) {
+        // byte counts, final states and LDS stream starts of the four lanes of this column
+        const uint32_t e1 = xch[j], x1 = xch[64 + j];
+        uint32_t cnt[4], fs[4], sa[4];
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            if (b == FL) { cnt[b] = e; fs[b] = c.x; sa[b] = end0 - e; }
+            else if (b == 3) { cnt[b] = e1; fs[b] = x1; sa[b] = end1 - e1; }
+            else {
+                const uint32_t pb = col + b;
+                const uint32_t Kb = len > pb ? (len - pb + 255) / 256 : 0u;
+                const uint32_t ent = (chdr[0] == Kb) ? 0u : ((chdr[4] == Kb) ? 1u : 2u);
+                fs[b] = chdr[4 * ent + 1];
+                cnt[b] = chdr[4 * ent + 2];
+                sa[b] = cb_off + ent * fp.canon_bytes;
+            }
+        }
+        const uint32_t tsum = cnt[0] + cnt[1] + cnt[2] + cnt[3];
+        uint32_t incl = tsum;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t v = __shfl_up(incl, d, 64);
+            if ((int)j >= d) incl += v;
+        }
+        const uint32_t total = __shfl(incl, 63, 64);
+        const uint32_t excl = incl - tsum;
+        const bool raw = total >= len;
+        const uint32_t size = raw ? len : total;
+        // the lowest dword a lane wrote must lie in its slot
+        const bool over = ((e + 3u) & ~3u) > fp.sl0 || ((e1 + 3u) & ~3u) > fp.sl1;
+        const bool any_over = __ballot(over) != 0;
+
+        const uint64_t t_coded = wall_clock64();
+        const uint64_t off = lookback_wave(status, u, size, &ctl[2], j);
+        const uint64_t t_placed = wall_clock64();
+        if (j == 0) {
+            unit_off[u] = off;
+            if (u + 1 == g.n_units) unit_off[u + 1] = off + size;
+            bc[0] = (uint32_t)off; bc[1] = (uint32_t)(off >> 32); bc[2] = size;
+            bc[3] = (raw ? 1u : 0u) | (any_over ? 2u : 0u);
+            if (phase) { uint64_t* ph = phase + 5 * u; ph[0] = t_start; ph[1] = t_ready; ph[2] = t_coded; ph[3] = t_placed; }
+        }
+        // headers (4 per thread, 64 contiguous bytes) and the lane tables for packing
         ckr_stream_header* uh = hdrs + u * 256 + 4 * j;
         uint32_t run = excl;
 #pragma unroll
@@ -940,42 +1037,54 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
         }
         if (j == 63) loff[256] = total;
     }
+    __syncthreads();
+    const uint64_t off = (uint64_t)bc[0] | ((uint64_t)bc[1] << 32);
+    const uint32_t size = bc[2], flags = bc[3];
     uint8_t* dst = out + off;
-    if (raw) {  // masked bytes of the unit, byte stores (rare)
-        for (uint32_t q = j; q < len; q += 64) {
+    if (flags & 1u) {  // raw: masked bytes of the unit, byte stores (rare)
+        for (uint32_t q = tid; q < len; q += 128) {
             const uint8_t v = usrc[q];
             dst[q] = byte_live(q, g.es, g.spe) ? v : 0;
         }
+        if (phase && tid == 0) phase[5 * u + 4] = wall_clock64();
         return;
     }
-    if (any_over) {  // bytes come from the general kernels
-        if (j == 0) redo_list[atomicAdd(&ctl[1], 1u)] = (uint32_t)u;
+    if (flags & 2u) {  // bytes come from the general kernels
+        if (tid == 0) {
+            redo_list[atomicAdd(&ctl[1], 1u)] = (uint32_t)u;
+            if (phase) phase[5 * u + 4] = wall_clock64();
+        }
         return;
     }
-    __syncthreads();
     // Packed bytes in 16-byte destination chunks (aligned in global memory).
-    // The streams of this thread's four lanes are one contiguous run of the
-    // output, [excl, excl + tsum); the thread writes every chunk whose first
-    // unit byte lies in that run (chunk 0, which may start before the unit,
-    // belongs to the run holding byte 0), walking its lanes in order; a chunk
-    // that runs past the end of the run takes its remaining bytes from the
-    // following lanes.  A chunk inside one lane is one unaligned 16-byte LDS
-    // read; a chunk over a lane boundary ORs one masked read per lane.  Bytes
-    // outside the unit (its first and last chunks are shared with the
-    // neighbouring units) are not stored.
+    // The four lanes of column j are one contiguous run of the output; wave 0
+    // takes its first half [r0, mid), wave 1 the rest [mid, r1).  A thread
+    // writes every chunk whose first unit byte lies in its range (chunk 0, which
+    // may start before the unit, belongs to the range holding byte 0), walking
+    // the lanes in order; a chunk that runs past the end of the range takes its
+    // remaining bytes from the following lanes.  A chunk inside one lane is one
+    // unaligned 16-byte LDS read; a chunk over a lane boundary ORs one masked
+    // read per lane.  Bytes outside the unit (its first and last chunks are
+    // shared with the neighbouring units) are not stored.
     const uint64_t ab = reinterpret_cast<uintptr_t>(dst);
     const uint64_t a0 = ab & ~15ull;
     const int32_t qbase = (int32_t)(a0 - ab);  // unit-relative byte of chunk 0 (-15..0)
     const int32_t isize = (int32_t)size;
-    const int32_t r0 = (int32_t)excl, r1 = (int32_t)(excl + tsum);
+    const int32_t c0 = (int32_t)loff[4 * j], c4 = (int32_t)loff[4 * j + 4];
+    const int32_t mid = (c0 + c4) >> 1;
+    const int32_t r0 = w ? mid : c0, r1 = w ? c4 : mid;
     if (r1 > r0) {
         // first owned chunk: the one containing byte r0 unless it starts before r0
-        int32_t c = (r0 - qbase) >> 4;
-        if (qbase + 16 * c < r0 && r0 > 0) c++;
-        uint32_t L = 4 * j;
+        int32_t ck = (r0 - qbase) >> 4;
+        if (qbase + 16 * ck < r0 && r0 > 0) ck++;
+        uint32_t L = 4 * j;  // lane holding r0: the last lane of the column starting at or before it
+        if (w) {
+#pragma unroll
+            for (int b = 1; b < 4; b++) if ((int32_t)loff[4 * j + b] <= r0) L = 4 * j + b;
+        }
         int32_t lo = (int32_t)loff[L], hi = (int32_t)loff[L + 1], dl = delta[L];
-        for (;; c++) {
-            const int32_t q = qbase + 16 * c;
+        for (;; ck++) {
+            const int32_t q = qbase + 16 * ck;
             if (q >= r1) break;
             const int32_t qs = max(q, 0), qe = min(q + 16, isize);
             while (hi <= qs && L < 255) { L++; lo = hi; hi = (int32_t)loff[L + 1]; dl = delta[L]; }
@@ -1011,7 +1120,7 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
                     dl2 = delta[L2];
                 }
             }
-            uint8_t* wp = reinterpret_cast<uint8_t*>(a0 + 16ull * (uint32_t)c);
+            uint8_t* wp = reinterpret_cast<uint8_t*>(a0 + 16ull * (uint32_t)ck);
             if (q >= 0 && q + 16 <= isize) {
                 *reinterpret_cast<uint4*>(wp) = v;
             } else {
@@ -1022,10 +1131,7 @@ __global__ void __launch_bounds__(64) encode_fast_kernel(const uint8_t* __restri
             }
         }
     }
-    if (phase && j == 0) {  // per-unit phase stamps (100 MHz clock) for ckr_profile_end
-        uint64_t* ph = phase + 5 * u;
-        ph[0] = t_start; ph[1] = t_ready; ph[2] = t_coded; ph[3] = t_placed; ph[4] = wall_clock64();
-    }
+    if (phase && tid == 0) phase[5 * u + 4] = wall_clock64();  // per-unit phase stamps (100 MHz clock)
 }
 
 __global__ void encode_fast_reset_kernel(uint64_t* status, uint64_t n, uint32_t* ctl) {
@@ -1040,7 +1146,7 @@ static uint32_t slot_stride(uint32_t sl) {
 }
 
 uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p) {
-    return FE_CBYTES + 3 * p.canon_bytes + 64 * (slot_stride(p.sl0) + slot_stride(p.sl1)) + 32;
+    return FE_GUARD + 64 * (slot_stride(p.sl0) + slot_stride(p.sl1)) + FE_CBYTES_REL + 3 * p.canon_bytes + 32;
 }
 
 hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
@@ -1061,7 +1167,7 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&encode_fast_kernel<SPE_, ESC_, SIDE_>),      \
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);                       \
         CKR_LAUNCH("encode_fast_kernel", s,                                                                   \
-                   encode_fast_kernel<SPE_, ESC_, SIDE_><<<(uint32_t)n, 64, lb, s>>>(                         \
+                   encode_fast_kernel<SPE_, ESC_, SIDE_><<<(uint32_t)n, 128, lb, s>>>(                         \
                        src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status, ctl, redo_list, phase)); \
     } while (0)
     const bool side = sidecar != nullptr;
