@@ -182,7 +182,7 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     L.off_enc = o;     o = align_up(o + 256 * sizeof(ckr::EncSym), kAlign);
     L.off_hist = o;    o = align_up(o + 768 * 4, kAlign);
     L.off_canon = o;   o = align_up(o + 3ull * (4 + 2 * ck.cw) * 4, kAlign);
-    L.off_status = o;  o = align_up(o + g.n_units * 8, kAlign);
+    L.off_status = o;  o = align_up(o + ckr::encode_fast_status_words(g.n_units) * 8, kAlign);
     L.off_ctl = o;     o = align_up(o + 16, kAlign);
     L.off_redo = o;    o = align_up(o + g.n_units * 4, kAlign);
     L.off_usize = o;   o = align_up(o + bu * 4, kAlign);
@@ -257,7 +257,7 @@ uint64_t* prof_phase_buffer(uint64_t n, hipStream_t s) {
     void* p = nullptr;
     if (hipMalloc(&p, n * 8) != hipSuccess) return nullptr;
     if (hipMemsetAsync(p, 0, n * 8, s) != hipSuccess) { (void)hipFree(p); return nullptr; }
-    g_phase.push_back({static_cast<uint64_t*>(p), n / 5, s});
+    g_phase.push_back({static_cast<uint64_t*>(p), n / 8, s});
     return static_cast<uint64_t*>(p);
 }
 }  // namespace ckr
@@ -290,20 +290,26 @@ int ckr_profile_end(char* buf, uint64_t buflen) {
         (void)hipEventDestroy(r.a);
     }
     g_prof.clear();
-    // fast-encode phases: mean per unit (us) of prologue+ticket, coding,
-    // look-back and packing, and the mean unit lifetime
+    // fast-encode phases: mean per unit (us) of ticket, coding (with the lane
+    // sums), look-back, the barrier before packing, packing (thread 0), the
+    // closing barrier, and the chunks thread 0 packed
     {
-        double sum[4] = {0, 0, 0, 0}, life = 0;
+        constexpr int NS = 8;
+        double sum[6] = {0, 0, 0, 0, 0, 0}, life = 0, chunks = 0;
         uint64_t units = 0;
+        std::vector<float> code_t, look_t;  // for percentiles
         for (auto& pr : g_phase) {
-            std::vector<uint64_t> h(pr.n * 5);
+            std::vector<uint64_t> h(pr.n * NS);
             if (hipStreamSynchronize(pr.s) == hipSuccess &&
                 hipMemcpy(h.data(), pr.buf, h.size() * 8, hipMemcpyDeviceToHost) == hipSuccess) {
                 for (uint64_t u = 0; u < pr.n; u++) {
-                    const uint64_t* t = &h[5 * u];
-                    if (!t[4]) continue;  // unit left to the general kernels
-                    for (int k = 0; k < 4; k++) sum[k] += (double)(t[k + 1] - t[k]) * 0.01;
-                    life += (double)(t[4] - t[0]) * 0.01;
+                    const uint64_t* t = &h[NS * u];
+                    if (!t[6]) continue;  // unit not stamped
+                    for (int k = 0; k < 6; k++) sum[k] += t[k + 1] >= t[k] ? (double)(t[k + 1] - t[k]) * 0.01 : 0.0;
+                    code_t.push_back(t[2] >= t[1] ? (float)(t[2] - t[1]) * 0.01f : 0.f);
+                    look_t.push_back(t[3] >= t[2] ? (float)(t[3] - t[2]) * 0.01f : 0.f);
+                    life += (double)(t[6] - t[0]) * 0.01;
+                    chunks += (double)t[7];
                     units++;
                 }
             }
@@ -311,10 +317,24 @@ int ckr_profile_end(char* buf, uint64_t buflen) {
         }
         g_phase.clear();
         if (units) {
-            const char* nm[4] = {"encode_fast.phase_prologue_us", "encode_fast.phase_code_us",
-                                 "encode_fast.phase_lookback_us", "encode_fast.phase_pack_us"};
-            for (int k = 0; k < 4; k++) agg[nm[k]] = {units, sum[k] / 1000.0};
+            const char* nm[6] = {"encode_fast.phase_ticket_us", "encode_fast.phase_code_us",
+                                 "encode_fast.phase_lookback_us", "encode_fast.phase_barrier_us",
+                                 "encode_fast.phase_pack_us", "encode_fast.phase_end_barrier_us"};
+            for (int k = 0; k < 6; k++) agg[nm[k]] = {units, sum[k] / 1000.0};
             agg["encode_fast.unit_lifetime_us"] = {units, life / 1000.0};
+            agg["encode_fast.thread0_chunks"] = {units, chunks / 1000.0};
+            // percentiles (reported as a "total" over one launch so that avg = value)
+            auto pct = [](std::vector<float>& v, double q) {
+                const size_t k = std::min(v.size() - 1, (size_t)(q * (double)(v.size() - 1)));
+                std::nth_element(v.begin(), v.begin() + k, v.end());
+                return (double)v[k];
+            };
+            const double qs[3] = {0.1, 0.5, 0.9};
+            const char* qn[3] = {"p10", "p50", "p90"};
+            for (int i = 0; i < 3; i++) {
+                agg[std::string("encode_fast.code_us_") + qn[i]] = {1, pct(code_t, qs[i]) / 1000.0};
+                agg[std::string("encode_fast.lookback_us_") + qn[i]] = {1, pct(look_t, qs[i]) / 1000.0};
+            }
         }
     }
     std::string out;

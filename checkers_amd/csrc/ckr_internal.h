@@ -81,13 +81,15 @@ hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t
                                hipStream_t s);
 
 // LDS-staged encode of all units (masked dtypes, units <= 64 KiB).  status:
-// n_units u64, ctl: 4 u32 ({ticket, redo count, error, 0}), redo_list: n_units
+// encode_fast_status_words(n_units) u64, ctl: 4 u32 ({ticket, redo count, error, 0}), redo_list: n_units
 // u32 — units whose bytes must then be produced by launch_encode_batch.
 struct FastEncParamsHost {
     uint32_t sl0, sl1, cw, canon_bytes;
     bool escapes;  // the data may hold symbols with f == 0 (table not built from it)
 };
 uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p);
+// u64 look-back words of the fast encoder for n units (status argument size).
+uint64_t encode_fast_status_words(uint64_t n_units);
 hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
                               const FastEncParamsHost& hp, ckr_stream_header* hdrs, uint8_t* sidecar, uint8_t* out,
                               uint64_t* unit_off, uint64_t* status, uint32_t* ctl, uint32_t* redo_list,

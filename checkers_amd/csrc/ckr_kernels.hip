@@ -659,19 +659,30 @@ struct FastEncParams {
 };
 
 // LDS layout (bytes): guard 512 | rank-0 slots 64 x stride0 | rank-1 slots 64 x
-// stride1 | table 3 x 1024 (SoA: rcp, cmpl | rsh << 24, bias | 8f << 16) | canonical
-// headers 12 x u32 | canonical bytes 3 x canon_bytes | 32 bytes of read
-// padding.  A lane's dwords are flushed downward from the end of its slot; a
-// lane that outgrows its slot keeps flushing into the slots below it (lanes of
-// the same unit, whose bytes are then redone by the general kernels) and, for
-// the lowest slot, into the guard (at most 2 bytes per symbol, 256 symbols),
-// so the table and the canonical headers, which the unit's sizes depend on,
-// are never overwritten.  Once the unit is coded the table is dead and its
-// space holds the packer's lane tables: loff 257 x u32 (+pad) | delta 256 x i32.
+// stride1 | table 256 x 8 (see EncPair) | lane tables: loff 257 x u32 (+pad),
+// delta 256 x i32, the two waves' chains (count, state) 4 x 64 x u32 and 8 u32
+// of unit-wide values | canonical headers 12 x u32 | canonical bytes 3 x
+// canon_bytes | 32 bytes of read padding.  A lane's dwords are flushed
+// downward from the end of its slot; a lane that outgrows its slot keeps
+// flushing into the slots below it (lanes of the same unit, whose bytes are
+// then redone by the general kernels) and, for the lowest slot, into the guard
+// (at most 2 bytes per symbol, 256 symbols), so the table and the canonical
+// headers, which the unit's sizes depend on, are never overwritten.
 static constexpr uint32_t FE_GUARD = 512;
-static constexpr uint32_t FE_TABSZ = 3 * 1024, FE_LOFF = 0, FE_DELTA = 1040, FE_XCH = 2080, FE_BCAST = 2592;
-// canonical headers 12 x u32 and the ticket, then the canonical bytes
-static constexpr uint32_t FE_CBYTES_REL = FE_TABSZ + 64;
+#ifndef FE_NW
+#define FE_NW 2  // waves per unit of the fast encoder (1 or 2)
+#endif
+static constexpr uint32_t FE_TABSZ = 2048;                       // table, after the slots
+static constexpr uint32_t FE_LOFF = FE_TABSZ, FE_DELTA = FE_LOFF + 1040, FE_XCH = FE_DELTA + 1024,
+                          FE_BCAST = FE_XCH + 1024, FE_CHDR = FE_BCAST + 32, FE_CBYTES_REL = FE_CHDR + 48;
+
+// Encode table entry in LDS, 8 bytes (one ds_read_b64 per symbol, which costs
+// the LDS no more than a 32-bit read): x = rcp; y = cmpl | rsh << 12 | bias << 16
+// (see EncSym: cmpl = M - f < 4096, rsh < 12, bias < 8192).  y = ~0u marks f == 0.
+__device__ __forceinline__ uint32_t enc_pair_y(const EncSym& e) {
+    if (e.xmax == 0) return 0xFFFFFFFFu;
+    return (e.cmpl_rsh & 0xFFFu) | ((e.cmpl_rsh >> 16) << 12) | (e.bias << 16);
+}
 
 // Lane coder state.  x: rANS state.  {hi, lo}: the last 8 bytes emitted, the
 // newest in the top byte of hi.  sel: v_perm selector 0x08090A0B - P*0x01010101
@@ -682,22 +693,23 @@ struct EncLane {
 };
 
 // One symbol of rans_encode_kernel's loop body (ANSCompressor.cpp:180-202)
-// without branches.  tA = rcp, tB = cmpl | rsh << 24, tC = bias | 8f << 16
-// (see EncSym).  Renormalisation emits n in {0,1,2} bytes: x >= f*2^19 and
-// x >= f*2^27 are (x >> 16) >= 8f and (x >> 24) >= 8f.  The n low bytes of x,
-// low byte first (the reference's emission order), enter the window from the
-// top: one v_alignbyte per register shifts by n bytes.  ESC: the table may give
-// f == 0 to a symbol of the data (raw-byte escape, no state update, :185-192);
-// tables built from the data itself never do.
+// without branches, from the table entry t (see enc_pair_y).  Renormalisation
+// emits n in {0,1,2} bytes: x >= f*2^19 and x >= f*2^27 are (x >> 16) >= 8f and
+// (x >> 24) >= 8f, with 8f = 32768 - 8 cmpl.  The n low bytes of x, low byte
+// first (the reference's emission order), enter the window from the top: one
+// v_alignbyte per register shifts by n bytes.  ESC: the table may give f == 0
+// to a symbol of the data (raw-byte escape, no state update, :185-192); tables
+// built from the data itself never do.
 template <bool ESC>
-__device__ __forceinline__ void enc_step(EncLane& s, uint32_t sym, uint32_t tA, uint32_t tB, uint32_t tC) {
-    const uint32_t f8 = tC >> 16;
+__device__ __forceinline__ void enc_step(EncLane& s, uint32_t sym, uint2 t) {
+    const uint32_t cm = t.y & 0xFFFu;
+    const uint32_t f8 = 32768u - (cm << 3);
     const uint32_t x = s.x;
     uint32_t n4 = ((x >> 24) >= f8) ? 0x02020202u : (((x >> 16) >= f8) ? 0x01010101u : 0u);
     uint32_t ins = x;
     bool esc = false;
     if (ESC) {
-        esc = f8 == 0u;
+        esc = t.y == 0xFFFFFFFFu;
         n4 = esc ? 0x01010101u : n4;
         ins = esc ? sym : x;
     }
@@ -705,8 +717,8 @@ __device__ __forceinline__ void enc_step(EncLane& s, uint32_t sym, uint32_t tA, 
     s.lo = __builtin_amdgcn_alignbyte(s.hi, s.lo, n4);
     s.hi = __builtin_amdgcn_alignbyte(ins, s.hi, n4);
     s.sel -= n4;
-    const uint32_t q = __umulhi(xr, tA) >> (tB >> 24);
-    const uint32_t xn = (xr + (tC & 0xFFFFu)) + __umul24(q, tB);
+    const uint32_t q = __umulhi(xr, t.x) >> ((t.y >> 12) & 15u);
+    const uint32_t xn = (xr + (t.y >> 16)) + __umul24(q, cm);
     s.x = (ESC && esc) ? x : xn;
 }
 
@@ -746,28 +758,68 @@ __device__ __forceinline__ void lb_store(uint64_t* p, uint64_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+__device__ __forceinline__ void lb_max(uint64_t* p, uint64_t v) {
+    (void)__hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Exclusive prefix of the packed sizes of units [0, u), computed by the whole
-// wave: lane j reads the status of unit base-1-j, the nearest published
-// inclusive prefix (ballot) ends the walk, aggregates before it are summed;
-// each step covers 64 units.  Every unit before u holds a ticket taken earlier,
-// so it is running or done and will publish; the wait is bounded all the same
-// (error flag, no hang).  Publishes u's aggregate first and its prefix last.
-__device__ uint64_t lookback_wave(uint64_t* status, uint64_t u, uint64_t size, uint32_t* err, uint32_t j) {
-    if (j == 0) lb_store(&status[u], (u == 0 ? LB_PFX : LB_AGG) | size);
+// wave, in two levels.  Unit words status[v] hold v's size (AGG) and then its
+// inclusive prefix (PFX).  Units form blocks of 64; block words bs[c] (after the
+// n unit words) hold the block's size once all of its units have published
+// theirs (the last one to add itself to the block's count in bacc[c], which
+// packs count << 40 | sum, publishes it) and then the inclusive prefix through
+// the block (published by the block's last unit).  Block words only ever grow
+// (atomic max; PFX > AGG), so a late AGG cannot overwrite a PFX.  The walk
+// reads the units of u's own block before u (one step of 64 lanes) and then
+// whole blocks, 64 per step, back to the nearest prefix, so that a unit whose
+// nearest published prefix lies hundreds of units back still needs about two
+// round trips.  Every unit before u holds a ticket taken earlier, so it is
+// running or done and will publish; the wait is bounded all the same (error
+// flag, no hang).
+__device__ uint64_t lookback_wave(uint64_t* status, uint64_t n_units, uint64_t u, uint64_t size, uint32_t* err,
+                                  uint32_t j) {
+    const uint64_t nblk = (n_units + 63) >> 6;
+    uint64_t* bs = status + n_units;
+    uint64_t* bacc = bs + nblk;
+    const uint64_t b = u >> 6, u0 = b << 6;
+    if (j == 0) {
+        lb_store(&status[u], (u == 0 ? LB_PFX : LB_AGG) | size);
+        const uint64_t old = __hip_atomic_fetch_add(&bacc[b], (1ull << 40) | size, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t in_blk = (n_units - u0 < 64) ? n_units - u0 : 64;
+        if ((old >> 40) + 1 == in_blk) lb_max(&bs[b], LB_AGG | ((old & ((1ull << 40) - 1)) + size));
+    }
     uint64_t excl = 0;
-    int64_t base = (int64_t)u;  // walk covers units < base
+    bool done = u == 0;
     uint32_t spins = 0;
-    while (base > 0) {
-        const int64_t idx = base - 1 - (int64_t)j;
-        const uint64_t st = idx >= 0 ? lb_load(&status[idx]) : LB_PFX;
+    const uint32_t na = (uint32_t)(u - u0);  // units of u's block before u
+    while (!done && na > 0) {
+        const bool act = j < na;
+        const uint64_t st = act ? lb_load(&status[u - 1 - j]) : 0ull;
+        const uint64_t pfx = __ballot(act && (st >> 62) == 2);
+        const uint32_t stop = pfx ? (uint32_t)__builtin_ctzll(pfx) : 64u;  // nearest prefix
+        const bool need = act && j <= stop;
+        if (__ballot(need && (st >> 62) == 0)) {  // a unit not published yet
+            if (++spins > LB_SPIN_LIMIT) { if (j == 0) atomicOr(err, 1u); done = true; break; }
+            __builtin_amdgcn_s_sleep(2);
+            continue;
+        }
+        uint64_t v = need ? (st & LB_VAL) : 0ull;
+#pragma unroll
+        for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
+        excl += v;
+        done = pfx != 0;
+        break;
+    }
+    int64_t bb = (int64_t)b;  // blocks < bb remain
+    while (!done && bb > 0) {
+        const int64_t idx = bb - 1 - (int64_t)j;
+        const uint64_t st = idx >= 0 ? lb_load(&bs[idx]) : LB_PFX;
         const uint64_t pfx = __ballot((st >> 62) == 2);
         const uint32_t stop = pfx ? (uint32_t)__builtin_ctzll(pfx) : 63u;  // last lane needed
         const uint64_t need = (stop == 63u) ? ~0ull : ((2ull << stop) - 1);
-        if (__ballot((st >> 62) == 0) & need) {  // a unit in the window has not published yet
-            if (++spins > LB_SPIN_LIMIT) {
-                if (j == 0) atomicOr(err, 1u);
-                break;
-            }
+        if (__ballot((st >> 62) == 0) & need) {  // a block not complete yet
+            if (++spins > LB_SPIN_LIMIT) { if (j == 0) atomicOr(err, 1u); break; }
             __builtin_amdgcn_s_sleep(2);
             continue;
         }
@@ -776,9 +828,12 @@ __device__ uint64_t lookback_wave(uint64_t* status, uint64_t u, uint64_t size, u
         for (int d = 32; d > 0; d >>= 1) v += __shfl_xor(v, d, 64);
         excl += v;
         if (pfx) break;
-        base -= 64;
+        bb -= 64;
     }
-    if (j == 0 && u > 0) lb_store(&status[u], LB_PFX | (excl + size));
+    if (j == 0) {
+        if (u > 0) lb_store(&status[u], LB_PFX | (excl + size));
+        if (u == u0 + 63 || u + 1 == n_units) lb_max(&bs[b], LB_PFX | (excl + size));
+    }
     return excl;
 }
 
@@ -791,6 +846,17 @@ __device__ __forceinline__ uint4 lds_read16(const uint8_t* lds8, uint32_t a) {
                       __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh));
 }
 
+// Bytes [s, 16) of r over those of v (0 <= s < 16): one bitfield insert per
+// dword, the mask of dword d being the bytes at or above s - 4d.
+__device__ __forceinline__ uint4 merge16_from(uint4 v, uint4 r, uint32_t s) {
+    auto m = [&](int d) {
+        const int32_t k = min(max((int32_t)s - 4 * d, 0), 4);  // bytes kept from v
+        return k >= 4 ? 0u : (0xFFFFFFFFu << (8 * k));
+    };
+    return make_uint4((r.x & m(0)) | (v.x & ~m(0)), (r.y & m(1)) | (v.y & ~m(1)), (r.z & m(2)) | (v.z & ~m(2)),
+                      (r.w & m(3)) | (v.w & ~m(3)));
+}
+
 // Largest lane L with loff[L] <= q (q < loff[256]).
 __device__ __forceinline__ uint32_t lane_of(const uint32_t* loff, uint32_t q) {
     uint32_t lo = 0;
@@ -800,36 +866,41 @@ __device__ __forceinline__ uint32_t lane_of(const uint32_t* loff, uint32_t q) {
     return lo;
 }
 
-// Coding of one wave's lane of every column of a unit whose rows are all full
-// (length a multiple of 256, so every column has the same nrows rows): W = 0
-// codes byte FL of each column, W = 1 byte 3.  Rows are taken from the top down.
+// Coding of the live lanes of every column of a unit whose rows are all full
+// (length a multiple of 256, so every column has the same nrows rows).  P = 0:
+// byte FL of each column (chain c0); P = 1: byte 3 (chain c0); P = 2: both
+// (c0: byte FL, c1: byte 3, interleaved).  Rows are taken from the top down.
 // The rows above the highest multiple of 32 go one at a time; then groups of
 // 32 rows, the next group's loads in flight while the current one is coded
 // (loads and table reads are unconditional, so the waits stay exact), and each
-// 8-row batch's table words read while the batch before it is coded.  Pending
-// bytes are flushed after every second row.  Wave W writes the sidecar of the
-// rows k with k & 1 == W.
-template <int SPE, bool ESC, bool SIDE, int W>
-__device__ __forceinline__ void enc_full_rows(EncLane& c, const uint8_t* ucol, uint8_t* sidecar, uint64_t ubase,
-                                              uint32_t j, uint32_t nrows, const uint32_t* tabA, uint8_t* lds8) {
+// 8-row batch's table entries read while the batch before it is coded.
+// Pending bytes are flushed after every second row.  The sidecar rows are
+// written by the thread coding plane 0 and 1 alternately (row k by P == k & 1),
+// or all of them when P = 2.
+template <int SPE, bool ESC, bool SIDE, int P>
+__device__ __forceinline__ void enc_full_rows(EncLane& c0, EncLane& c1, const uint8_t* ucol, uint8_t* sidecar,
+                                              uint64_t ubase, uint32_t j, uint32_t nrows, const uint2* tab,
+                                              uint8_t* lds8) {
     constexpr int FL = SPE == 2 ? 2 : 1;
-    constexpr uint32_t SH = W ? 24u : 8u * FL;
-    const uint32_t* tabB = tabA + 256;
-    const uint32_t* tabC = tabA + 512;
+    constexpr uint32_t SH0 = P == 1 ? 24u : 8u * FL;  // byte of chain c0
+    constexpr uint32_t SH1 = 24u;                     // byte of chain c1 (P = 2)
     const uint32_t* in32 = reinterpret_cast<const uint32_t*>(ucol);          // row k at in32[64 k]
     uint16_t* sc16 = SIDE ? reinterpret_cast<uint16_t*>(sidecar + (ubase >> 1) + 2 * j) : nullptr;  // row k at sc16[64 k]
     auto side = [&](uint16_t* p, uint32_t wd) {
         if (SIDE) *p = (uint16_t)(SPE == 2 ? (wd & 0xFFFFu) : ((wd & 0xFFu) | ((wd >> 8) & 0xFF00u)));
     };
+    auto mine = [&](uint32_t k) { return P == 2 || (k & 1u) == (uint32_t)P; };  // sidecar row k written here
     const uint32_t ng = nrows >> 5;  // full groups: rows [0, 32 ng)
     for (int32_t k = (int32_t)nrows - 1; k >= (int32_t)(32 * ng); k--) {
         const uint32_t wd = in32[64 * k];
-        if ((uint32_t)(k & 1) == W) side(sc16 + 64 * k, wd);
-        const uint32_t sy = (wd >> SH) & 255u;
-        enc_step<ESC>(c, sy, tabA[sy], tabB[sy], tabC[sy]);
-        if ((k & 1) == 0) enc_flush(c, lds8);
+        if (mine((uint32_t)k)) side(sc16 + 64 * k, wd);
+        const uint32_t s0 = (wd >> SH0) & 255u;
+        enc_step<ESC>(c0, s0, tab[s0]);
+        if (P == 2) { const uint32_t s1 = wd >> SH1; enc_step<ESC>(c1, s1, tab[s1]); }
+        if ((k & 1) == 0) { enc_flush(c0, lds8); if (P == 2) enc_flush(c1, lds8); }
     }
-    enc_flush(c, lds8);
+    enc_flush(c0, lds8);
+    if (P == 2) enc_flush(c1, lds8);
     if (ng == 0) return;
     // group g: rows 32g+31 (r[0]) down to 32g (r[31])
     auto load = [&](uint32_t (&r)[32], uint32_t g) {
@@ -838,12 +909,12 @@ __device__ __forceinline__ void enc_full_rows(EncLane& c, const uint8_t* ucol, u
         for (int i = 0; i < 32; i++) r[i] = p[-64 * i];
     };
     auto code = [&](const uint32_t (&r)[32], uint32_t g) {
-        uint32_t ta[2][8], tbw[2][8], tcw[2][8];
+        uint2 t0[2][8], t1[2][8];
         auto fetch = [&](int buf, int i0) {
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const uint32_t sy = (r[i0 + i] >> SH) & 255u;
-                ta[buf][i] = tabA[sy]; tbw[buf][i] = tabB[sy]; tcw[buf][i] = tabC[sy];
+                t0[buf][i] = tab[(r[i0 + i] >> SH0) & 255u];
+                if (P == 2) t1[buf][i] = tab[r[i0 + i] >> SH1];
             }
         };
         uint16_t* scp = SIDE ? sc16 + 64 * (32 * g + 31) : nullptr;
@@ -854,9 +925,10 @@ __device__ __forceinline__ void enc_full_rows(EncLane& c, const uint8_t* ucol, u
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const int ii = 8 * bt + i;               // row 32g+31-ii: parity (ii & 1) ^ 1
-                if (((ii & 1) ^ 1) == W) side(scp - 64 * ii, r[ii]);
-                enc_step<ESC>(c, (r[ii] >> SH) & 255u, ta[bt & 1][i], tbw[bt & 1][i], tcw[bt & 1][i]);
-                if (i & 1) enc_flush(c, lds8);
+                if (P == 2 || ((ii & 1) ^ 1) == P) side(scp - 64 * ii, r[ii]);
+                enc_step<ESC>(c0, (r[ii] >> SH0) & 255u, t0[bt & 1][i]);
+                if (P == 2) enc_step<ESC>(c1, r[ii] >> SH1, t1[bt & 1][i]);
+                if (i & 1) { enc_flush(c0, lds8); if (P == 2) enc_flush(c1, lds8); }
             }
         }
     };
@@ -875,8 +947,14 @@ __device__ __forceinline__ void enc_full_rows(EncLane& c, const uint8_t* ucol, u
     }
 }
 
-template <int SPE, bool ESC, bool SIDE>
-__global__ void __launch_bounds__(128) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
+// Persistent: each workgroup stages the table and the canonical streams once,
+// then takes units from the ticket counter until none is left.  NW = 1: one
+// wave per unit, each thread codes both live lanes of its column.  NW = 2: wave
+// 0 codes byte FL of every column, wave 1 byte 3; both waves compute the
+// unit's lane sizes, wave 0 runs the look-back while wave 1 writes the headers
+// and the packer's lane tables, and both waves pack.
+template <int SPE, bool ESC, bool SIDE, int NW>
+__global__ void __launch_bounds__(64 * NW) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
                                                           const EncSym* __restrict__ d_enc,
                                                           const uint32_t* __restrict__ canon, FastEncParams fp,
                                                           ckr_stream_header* __restrict__ hdrs,
@@ -886,103 +964,112 @@ __global__ void __launch_bounds__(128) encode_fast_kernel(const uint8_t* __restr
                                                           uint32_t* __restrict__ redo_list,
                                                           uint64_t* __restrict__ phase) {
     extern __shared__ uint32_t lds[];
-    const uint64_t t_start = wall_clock64();
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
     const uint32_t st0_off = FE_GUARD;
     const uint32_t st1_off = st0_off + 64 * fp.stride0;
-    const uint32_t tb = st1_off + 64 * fp.stride1;  // table (3 arrays of 256 u32)
-    const uint32_t* tabA = reinterpret_cast<const uint32_t*>(lds8 + tb);
-    const uint32_t* tabB = tabA + 256;
-    const uint32_t* tabC = tabA + 512;
+    const uint32_t tb = st1_off + 64 * fp.stride1;  // table
+    const uint2* tab = reinterpret_cast<const uint2*>(lds8 + tb);
     uint32_t* loff = reinterpret_cast<uint32_t*>(lds8 + tb + FE_LOFF);
     int32_t* delta = reinterpret_cast<int32_t*>(lds8 + tb + FE_DELTA);
-    uint32_t* xch = reinterpret_cast<uint32_t*>(lds8 + tb + FE_XCH);   // wave 1's chains: count, state
-    uint32_t* bc = reinterpret_cast<uint32_t*>(lds8 + tb + FE_BCAST);  // unit-wide values from wave 0
-    uint32_t* chdr = reinterpret_cast<uint32_t*>(lds8 + tb + FE_TABSZ);
+    uint32_t* xch = reinterpret_cast<uint32_t*>(lds8 + tb + FE_XCH);   // [wave][count 64 | state 64]
+    uint32_t* bc = reinterpret_cast<uint32_t*>(lds8 + tb + FE_BCAST);  // ticket, offset, flags
+    uint32_t* chdr = reinterpret_cast<uint32_t*>(lds8 + tb + FE_CHDR);
     const uint32_t cb_off = tb + FE_CBYTES_REL;
     const uint32_t tid = threadIdx.x;
-    const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0: plane FL, 1: plane 3
+    const uint32_t w = NW == 1 ? 0u : __builtin_amdgcn_readfirstlane(tid >> 6);  // NW = 2: 0 plane FL, 1 plane 3
+    constexpr uint32_t NT = 64 * NW;
     const uint32_t j = tid & 63;                                  // column
+    constexpr int FL = SPE == 2 ? 2 : 1;  // byte of the first live lane in a column
+    const uint32_t lm = live_mask32<SPE>();
+    const uint32_t sh = w ? 24u : 8u * FL;  // this wave's byte of the column
 
-    {   // table (EncSym → SoA), canonical headers and canonical streams (byte order), loads batched
+    {   // table (EncSym → EncPair), canonical headers and canonical streams (byte order), loads batched
         const uint4* d_tab = reinterpret_cast<const uint4*>(d_enc);
-        uint4 tv[2];
+        uint4 tv[256 / NT];
 #pragma unroll
-        for (int k = 0; k < 2; k++) tv[k] = d_tab[tid + 128 * k];
-        uint32_t* wA = reinterpret_cast<uint32_t*>(lds8 + tb);
+        for (uint32_t k = 0; k < 256 / NT; k++) tv[k] = d_tab[tid + NT * k];
+        uint2* wt = reinterpret_cast<uint2*>(lds8 + tb);
 #pragma unroll
-        for (int k = 0; k < 2; k++) {
+        for (uint32_t k = 0; k < 256 / NT; k++) {
             const EncSym e = {tv[k].x, tv[k].y, tv[k].z, tv[k].w};
-            wA[tid + 128 * k] = e.rcp;
-            wA[256 + tid + 128 * k] = (e.cmpl_rsh & 0xFFFFu) | ((e.cmpl_rsh >> 16) << 24);
-            wA[512 + tid + 128 * k] = e.bias | ((e.xmax >> 16) << 16);  // xmax = f << 19: 8f in the top half
+            wt[tid + NT * k] = make_uint2(e.rcp, enc_pair_y(e));
         }
         const uint32_t* cs = canon + 3 * (4 + fp.cw);
         uint32_t* cb32 = reinterpret_cast<uint32_t*>(lds8 + cb_off);
         const uint32_t ncb = 3 * fp.canon_bytes / 4;
         const uint32_t cb_per = fp.canon_bytes / 4;
         for (uint32_t i0 = 0; i0 < ncb; i0 += 512) {
-            uint32_t cv[4];
+            uint32_t cv[512 / NT];
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t i = i0 + tid + 128 * k;
+            for (uint32_t k = 0; k < 512 / NT; k++) {
+                const uint32_t i = i0 + tid + NT * k;
                 cv[k] = i < ncb ? cs[(i / cb_per) * fp.cw + (i % cb_per)] : 0u;
             }
 #pragma unroll
-            for (int k = 0; k < 4; k++) { const uint32_t i = i0 + tid + 128 * k; if (i < ncb) cb32[i] = cv[k]; }
+            for (uint32_t k = 0; k < 512 / NT; k++) { const uint32_t i = i0 + tid + NT * k; if (i < ncb) cb32[i] = cv[k]; }
         }
         if (tid < 12) chdr[tid] = canon[(tid >> 2) * (4 + fp.cw) + (tid & 3)];
-        if (tid == 0) chdr[12] = atomicAdd(&ctl[0], 1u);  // ticket
     }
-    __syncthreads();
-    const uint64_t u = __builtin_amdgcn_readfirstlane(chdr[12]);
-    if (u >= g.n_units) return;
 
-    const uint64_t t_ready = wall_clock64();
-    const uint64_t ubase = u * g.unit;
-    const uint32_t len = (uint32_t)((g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit);
-    const uint8_t* usrc = src + ubase;
-    constexpr int FL = SPE == 2 ? 2 : 1;  // byte of the first live lane in a column
-    const uint32_t lm = live_mask32<SPE>();
-    const uint32_t sh = w ? 24u : 8u * FL;  // this wave's byte of the column
-    const uint32_t end0 = st0_off + j * fp.stride0 + fp.sl0;  // slot ends (LDS byte addresses)
-    const uint32_t end1 = st1_off + j * fp.stride1 + fp.sl1;
-    const uint32_t endw = w ? end1 : end0;
-    EncLane c{L, 0u, 0u, 0x08090A0Bu, endw - 4u};
+    for (;;) {
+        // phase stamps only when profiling: a clock read is a scalar-memory op whose
+        // return every later LDS wait (lgkmcnt) would also wait for
+        const uint64_t t_start = phase ? wall_clock64() : 0;
+        if (tid == 0) bc[0] = atomicAdd(&ctl[0], 1u);  // ticket
+        __syncthreads();
+        const uint64_t u = __builtin_amdgcn_readfirstlane(bc[0]);
+        if (u >= g.n_units) break;
 
-    const uint32_t col = 4 * j;
-    const uint32_t K = len > col ? (len - col + 255) / 256 : 0u;
-    if ((len & 255u) == 0) {
-        if (w == 0) enc_full_rows<SPE, ESC, SIDE, 0>(c, usrc + col, sidecar, ubase, j, len >> 8, tabA, lds8);
-        else enc_full_rows<SPE, ESC, SIDE, 1>(c, usrc + col, sidecar, ubase, j, len >> 8, tabA, lds8);
-    } else {
-        // A tensor's last unit: rows from the top down, one at a time; the top
-        // row may be partial (bf16: lane 4j+3 has one symbol fewer).
-        for (int32_t k = (int32_t)K - 1; k >= 0; k--) {
-            const uint32_t p = 256 * (uint32_t)k + col;
-            const uint32_t nvalid = (len - p) < 4 ? (len - p) : 4;
-            uint32_t v = 0;
-            if (nvalid == 4) v = *reinterpret_cast<const uint32_t*>(usrc + p);
-            else for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)usrc[p + b] << (8 * b);
-            if (SIDE && (uint32_t)(k & 1) == w) write_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
-            v &= lm;
-            const uint32_t sy = (v >> sh) & 255u;
-            if (w == 0 || nvalid == 4) enc_step<ESC>(c, sy, tabA[sy], tabB[sy], tabC[sy]);
-            if ((k & 1) == 0) enc_flush(c, lds8);
+        const uint64_t t_ready = phase ? wall_clock64() : 0;
+        const uint64_t ubase = u * g.unit;
+        const uint32_t len = (uint32_t)((g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit);
+        const uint8_t* usrc = src + ubase;
+        const uint32_t end0 = st0_off + j * fp.stride0 + fp.sl0;  // slot ends (LDS byte addresses)
+        const uint32_t end1 = st1_off + j * fp.stride1 + fp.sl1;
+        const uint32_t endw = w ? end1 : end0;
+        EncLane c{L, 0u, 0u, 0x08090A0Bu, endw - 4u};   // NW = 1: byte FL; NW = 2: this wave's byte
+        EncLane c1{L, 0u, 0u, 0x08090A0Bu, end1 - 4u};  // NW = 1: byte 3
+
+        const uint32_t col = 4 * j;
+        const uint32_t K = len > col ? (len - col + 255) / 256 : 0u;
+        if ((len & 255u) == 0) {
+            if (NW == 1) enc_full_rows<SPE, ESC, SIDE, 2>(c, c1, usrc + col, sidecar, ubase, j, len >> 8, tab, lds8);
+            else if (w == 0) enc_full_rows<SPE, ESC, SIDE, 0>(c, c1, usrc + col, sidecar, ubase, j, len >> 8, tab, lds8);
+            else enc_full_rows<SPE, ESC, SIDE, 1>(c, c1, usrc + col, sidecar, ubase, j, len >> 8, tab, lds8);
+        } else {
+            // A tensor's last unit: rows from the top down, one at a time; the top
+            // row may be partial (bf16: lane 4j+3 has one symbol fewer).
+            for (int32_t k = (int32_t)K - 1; k >= 0; k--) {
+                const uint32_t p = 256 * (uint32_t)k + col;
+                const uint32_t nvalid = (len - p) < 4 ? (len - p) : 4;
+                uint32_t v = 0;
+                if (nvalid == 4) v = *reinterpret_cast<const uint32_t*>(usrc + p);
+                else for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)usrc[p + b] << (8 * b);
+                if (SIDE && (NW == 1 || (uint32_t)(k & 1) == w)) write_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
+                v &= lm;
+                const uint32_t sy = (v >> sh) & 255u;
+                if (w == 0 || nvalid == 4) enc_step<ESC>(c, sy, tab[sy]);
+                if (NW == 1 && nvalid == 4) { const uint32_t s1 = v >> 24; enc_step<ESC>(c1, s1, tab[s1]); }
+                if ((k & 1) == 0) { enc_flush(c, lds8); if (NW == 1) enc_flush(c1, lds8); }
+            }
         }
-    }
-    const uint32_t e = enc_finish(c, lds8, endw);
-    __syncthreads();  // both waves done: the table is dead
-    if (w == 1) { xch[j] = e; xch[64 + j] = c.x; }
-    __syncthreads();
-
-    if (w == 0) {
-        // byte counts, final states and LDS stream starts of the four lanes of this column
-        const uint32_t e1 = xch[j], x1 = xch[64 + j];
+        const uint32_t e = enc_finish(c, lds8, endw);
+        uint32_t e0, x0, e1, x1;
+        if (NW == 1) {
+            e0 = e; x0 = c.x;
+            e1 = enc_finish(c1, lds8, end1); x1 = c1.x;
+        } else {
+            xch[128 * w + j] = e;
+            xch[128 * w + 64 + j] = c.x;
+            __syncthreads();
+            e0 = xch[j]; x0 = xch[64 + j]; e1 = xch[128 + j]; x1 = xch[192 + j];
+        }
+        // byte counts, final states and LDS stream starts of the four lanes of
+        // column j (with NW = 2 both waves compute them; the scan is wave-local)
         uint32_t cnt[4], fs[4], sa[4];
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-            if (b == FL) { cnt[b] = e; fs[b] = c.x; sa[b] = end0 - e; }
+            if (b == FL) { cnt[b] = e0; fs[b] = x0; sa[b] = end0 - e0; }
             else if (b == 3) { cnt[b] = e1; fs[b] = x1; sa[b] = end1 - e1; }
             else {
                 const uint32_t pb = col + b;
@@ -1005,133 +1092,135 @@ __global__ void __launch_bounds__(128) encode_fast_kernel(const uint8_t* __restr
         const bool raw = total >= len;
         const uint32_t size = raw ? len : total;
         // the lowest dword a lane wrote must lie in its slot
-        const bool over = ((e + 3u) & ~3u) > fp.sl0 || ((e1 + 3u) & ~3u) > fp.sl1;
+        const bool over = ((e0 + 3u) & ~3u) > fp.sl0 || ((e1 + 3u) & ~3u) > fp.sl1;
         const bool any_over = __ballot(over) != 0;
 
-        const uint64_t t_coded = wall_clock64();
-        const uint64_t off = lookback_wave(status, u, size, &ctl[2], j);
-        const uint64_t t_placed = wall_clock64();
-        if (j == 0) {
-            unit_off[u] = off;
-            if (u + 1 == g.n_units) unit_off[u + 1] = off + size;
-            bc[0] = (uint32_t)off; bc[1] = (uint32_t)(off >> 32); bc[2] = size;
-            bc[3] = (raw ? 1u : 0u) | (any_over ? 2u : 0u);
-            if (phase) { uint64_t* ph = phase + 5 * u; ph[0] = t_start; ph[1] = t_ready; ph[2] = t_coded; ph[3] = t_placed; }
-        }
-        // headers (4 per thread, 64 contiguous bytes) and the lane tables for packing
-        ckr_stream_header* uh = hdrs + u * 256 + 4 * j;
-        uint32_t run = excl;
+        const uint64_t t_coded = phase ? wall_clock64() : 0;
+        if (NW == 1 || w == 1) {
+            // headers (4 per thread, 64 contiguous bytes) and the lane tables for packing
+            ckr_stream_header* uh = hdrs + u * 256 + 4 * j;
+            uint32_t run = excl;
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            ckr_stream_header h;
-            if (raw) {
-                h.final_state = 0; h.byte_count = (j == 0 && b == 0) ? len : 0u; h.buf_offset = 0;
-            } else {
-                h.final_state = fs[b]; h.byte_count = cnt[b]; h.buf_offset = run;
+            for (int b = 0; b < 4; b++) {
+                ckr_stream_header h;
+                if (raw) {
+                    h.final_state = 0; h.byte_count = (j == 0 && b == 0) ? len : 0u; h.buf_offset = 0;
+                } else {
+                    h.final_state = fs[b]; h.byte_count = cnt[b]; h.buf_offset = run;
+                }
+                h.pad = 0;
+                uh[b] = h;
+                loff[4 * j + b] = run;
+                delta[4 * j + b] = (int32_t)sa[b] - (int32_t)run;
+                run += cnt[b];
             }
-            h.pad = 0;
-            uh[b] = h;
-            loff[4 * j + b] = run;
-            delta[4 * j + b] = (int32_t)sa[b] - (int32_t)run;
-            run += cnt[b];
+            if (j == 63) loff[256] = total;
         }
-        if (j == 63) loff[256] = total;
-    }
-    __syncthreads();
-    const uint64_t off = (uint64_t)bc[0] | ((uint64_t)bc[1] << 32);
-    const uint32_t size = bc[2], flags = bc[3];
-    uint8_t* dst = out + off;
-    if (flags & 1u) {  // raw: masked bytes of the unit, byte stores (rare)
-        for (uint32_t q = tid; q < len; q += 128) {
-            const uint8_t v = usrc[q];
-            dst[q] = byte_live(q, g.es, g.spe) ? v : 0;
+        if (w == 0) {
+            const uint64_t off = lookback_wave(status, g.n_units, u, size, &ctl[2], j);
+            if (j == 0) {
+                unit_off[u] = off;
+                if (u + 1 == g.n_units) unit_off[u + 1] = off + size;
+                bc[1] = (uint32_t)off; bc[2] = (uint32_t)(off >> 32);
+                if (phase) { uint64_t* ph = phase + 8 * u; ph[0] = t_start; ph[1] = t_ready; ph[2] = t_coded; ph[3] = wall_clock64(); }
+            }
         }
-        if (phase && tid == 0) phase[5 * u + 4] = wall_clock64();
-        return;
-    }
-    if (flags & 2u) {  // bytes come from the general kernels
-        if (tid == 0) {
-            redo_list[atomicAdd(&ctl[1], 1u)] = (uint32_t)u;
-            if (phase) phase[5 * u + 4] = wall_clock64();
-        }
-        return;
-    }
-    // Packed bytes in 16-byte destination chunks (aligned in global memory).
-    // The four lanes of column j are one contiguous run of the output; wave 0
-    // takes its first half [r0, mid), wave 1 the rest [mid, r1).  A thread
-    // writes every chunk whose first unit byte lies in its range (chunk 0, which
-    // may start before the unit, belongs to the range holding byte 0), walking
-    // the lanes in order; a chunk that runs past the end of the range takes its
-    // remaining bytes from the following lanes.  A chunk inside one lane is one
-    // unaligned 16-byte LDS read; a chunk over a lane boundary ORs one masked
-    // read per lane.  Bytes outside the unit (its first and last chunks are
-    // shared with the neighbouring units) are not stored.
-    const uint64_t ab = reinterpret_cast<uintptr_t>(dst);
-    const uint64_t a0 = ab & ~15ull;
-    const int32_t qbase = (int32_t)(a0 - ab);  // unit-relative byte of chunk 0 (-15..0)
-    const int32_t isize = (int32_t)size;
-    const int32_t c0 = (int32_t)loff[4 * j], c4 = (int32_t)loff[4 * j + 4];
-    const int32_t mid = (c0 + c4) >> 1;
-    const int32_t r0 = w ? mid : c0, r1 = w ? c4 : mid;
-    if (r1 > r0) {
-        // first owned chunk: the one containing byte r0 unless it starts before r0
-        int32_t ck = (r0 - qbase) >> 4;
-        if (qbase + 16 * ck < r0 && r0 > 0) ck++;
-        uint32_t L = 4 * j;  // lane holding r0: the last lane of the column starting at or before it
-        if (w) {
-#pragma unroll
-            for (int b = 1; b < 4; b++) if ((int32_t)loff[4 * j + b] <= r0) L = 4 * j + b;
-        }
-        int32_t lo = (int32_t)loff[L], hi = (int32_t)loff[L + 1], dl = delta[L];
-        for (;; ck++) {
-            const int32_t q = qbase + 16 * ck;
-            if (q >= r1) break;
-            const int32_t qs = max(q, 0), qe = min(q + 16, isize);
-            while (hi <= qs && L < 255) { L++; lo = hi; hi = (int32_t)loff[L + 1]; dl = delta[L]; }
-            uint4 v;
-            if (q >= lo && q + 16 <= hi) {
-                v = lds_read16(lds8, (uint32_t)(dl + q));
-            } else {
-                v = make_uint4(0, 0, 0, 0);
-                uint32_t L2 = L;
-                int32_t lo2 = lo, hi2 = hi, dl2 = dl;
-                for (;;) {
-                    const int32_t s0 = max(lo2, qs), s1 = min(hi2, qe);
-                    if (s1 > s0) {
-                        const uint4 r = lds_read16(lds8, (uint32_t)(dl2 + q));
-                        const uint32_t b0 = (uint32_t)(s0 - q), b1 = (uint32_t)(s1 - q);
-                        uint32_t m[4];
-#pragma unroll
-                        for (int w4 = 0; w4 < 4; w4++) {
-                            uint32_t mm = 0;
-#pragma unroll
-                            for (int bb = 0; bb < 4; bb++) {
-                                const uint32_t bi = 4 * w4 + bb;
-                                mm |= (bi >= b0 && bi < b1) ? (0xFFu << (8 * bb)) : 0u;
-                            }
-                            m[w4] = mm;
-                        }
-                        v.x |= r.x & m[0]; v.y |= r.y & m[1]; v.z |= r.z & m[2]; v.w |= r.w & m[3];
+        __syncthreads();
+        if (phase && tid == 0) phase[8 * u + 4] = wall_clock64();
+        uint32_t nchunks = 0;
+        const uint64_t off = (uint64_t)bc[1] | ((uint64_t)bc[2] << 32);
+        uint8_t* dst = out + off;
+        if (raw) {  // masked bytes of the unit, byte stores (rare)
+            for (uint32_t q = tid; q < len; q += NT) {
+                const uint8_t v = usrc[q];
+                dst[q] = byte_live(q, g.es, g.spe) ? v : 0;
+            }
+        } else if (any_over) {  // bytes come from the general kernels
+            if (tid == 0) redo_list[atomicAdd(&ctl[1], 1u)] = (uint32_t)u;
+        } else {
+            // Packed bytes in 16-byte destination chunks (aligned in global memory).
+            // The four lanes of column j are one contiguous run of the output; with
+            // NW = 2 wave 0 takes its first half [r0, mid), wave 1 the rest.  A thread
+            // writes every chunk whose first unit byte lies in its range (chunk 0, which
+            // may start before the unit, belongs to the range holding byte 0).  It walks
+            // the column's lanes (bounds and LDS starts in registers): the chunks that
+            // lie inside a lane are unaligned 16-byte LDS reads, four issued at a time;
+            // the chunk that starts in a lane and runs past its end takes its remaining
+            // bytes from the following non-empty lanes (lane tables in LDS).  Bytes
+            // outside the unit (its first and last chunks are shared with the
+            // neighbouring units) are not stored.
+            const uint64_t ab = reinterpret_cast<uintptr_t>(dst);
+            const int32_t qbase = (int32_t)((ab & ~15ull) - ab);  // unit-relative byte of chunk 0 (-15..0)
+            const int32_t isize = (int32_t)size;
+            const int32_t c0 = (int32_t)excl, c4 = (int32_t)(excl + tsum);
+            const int32_t mid = (c0 + c4) >> 1;
+            const int32_t r0 = (NW == 2 && w) ? mid : c0, r1 = (NW == 1 || w) ? c4 : mid;
+            // a chunk starting at q whose bytes from pos on come from the lanes after L
+            auto gather_tail = [&](uint4 v, int32_t q, int32_t pos, int32_t L) {
+                const int32_t qe = min(q + 16, isize);
+                while (pos < qe && L < 255) {
+                    L++;
+                    const int32_t lo2 = (int32_t)loff[L], hi2 = (int32_t)loff[L + 1];
+                    if (hi2 > lo2) {
+                        v = merge16_from(v, lds_read16(lds8, (uint32_t)(delta[L] + q)), (uint32_t)(pos - q));
+                        pos = hi2;
                     }
-                    if (hi2 >= qe || L2 >= 255) break;
-                    L2++;
-                    lo2 = hi2;
-                    hi2 = (int32_t)loff[L2 + 1];
-                    dl2 = delta[L2];
+                }
+                return v;
+            };
+            // derived from dst (not from an integer address) so that the stores stay
+            // global: a flat store would also count against the next LDS wait
+            auto put = [&](int32_t q, uint4 v) {
+                uint8_t* wp = dst + q;
+                nchunks++;
+                if (q >= 0 && q + 16 <= isize) {
+                    *reinterpret_cast<uint4*>(wp) = v;
+                } else {
+                    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int bb = 0; bb < 16; bb++)
+                        if (q + bb >= 0 && q + bb < isize) wp[bb] = (uint8_t)(vv[bb >> 2] >> (8 * (bb & 3)));
+                }
+            };
+            if (r1 > r0) {
+                // first owned chunk: the one containing byte r0 unless it starts before r0
+                int32_t q = qbase + 16 * ((r0 - qbase) >> 4);
+                if (q < r0 && r0 > 0) q += 16;
+                if (q < 0) {  // chunk 0 starts before the unit: its bytes from 0 on
+                    put(q, gather_tail(make_uint4(0, 0, 0, 0), q, 0, (int32_t)(4 * j) - 1));
+                    q += 16;
+                }
+                int32_t lo = c0;
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const int32_t hi = lo + (int32_t)cnt[b];
+                    const int32_t dl = (int32_t)sa[b] - lo;
+                    // chunks that lie inside lane b, four at a time
+                    while (q + 64 <= hi && q + 48 < r1) {
+                        const uint4 v0 = lds_read16(lds8, (uint32_t)(dl + q));
+                        const uint4 v1 = lds_read16(lds8, (uint32_t)(dl + q + 16));
+                        const uint4 v2 = lds_read16(lds8, (uint32_t)(dl + q + 32));
+                        const uint4 v3 = lds_read16(lds8, (uint32_t)(dl + q + 48));
+                        put(q, v0); put(q + 16, v1); put(q + 32, v2); put(q + 48, v3);
+                        q += 64;
+                    }
+                    while (q + 16 <= hi && q < r1) {
+                        put(q, lds_read16(lds8, (uint32_t)(dl + q)));
+                        q += 16;
+                    }
+                    // the chunk that starts in lane b and runs past its end
+                    if (q >= lo && q < hi && q < r1) {
+                        put(q, gather_tail(lds_read16(lds8, (uint32_t)(dl + q)), q, hi, (int32_t)(4 * j) + b));
+                        q += 16;
+                    }
+                    lo = hi;
                 }
             }
-            uint8_t* wp = reinterpret_cast<uint8_t*>(a0 + 16ull * (uint32_t)ck);
-            if (q >= 0 && q + 16 <= isize) {
-                *reinterpret_cast<uint4*>(wp) = v;
-            } else {
-                const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int bb = 0; bb < 16; bb++)
-                    if (q + bb >= 0 && q + bb < isize) wp[bb] = (uint8_t)(vv[bb >> 2] >> (8 * (bb & 3)));
-            }
         }
+        if (phase && tid == 0) { phase[8 * u + 5] = wall_clock64(); phase[8 * u + 7] = nchunks; }
+        __syncthreads();  // the slots, lane tables and bc are reused by the next unit
+        if (phase && tid == 0) phase[8 * u + 6] = wall_clock64();  // per-unit phase stamps (100 MHz clock)
     }
-    if (phase && tid == 0) phase[5 * u + 4] = wall_clock64();  // per-unit phase stamps (100 MHz clock)
 }
 
 __global__ void encode_fast_reset_kernel(uint64_t* status, uint64_t n, uint32_t* ctl) {
@@ -1145,6 +1234,8 @@ static uint32_t slot_stride(uint32_t sl) {
     return ((sl >> 2) & 1u) ? sl + 8 : sl + 4;
 }
 
+uint64_t encode_fast_status_words(uint64_t n_units) { return n_units + 2 * ((n_units + 63) / 64); }
+
 uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p) {
     return FE_GUARD + 64 * (slot_stride(p.sl0) + slot_stride(p.sl1)) + FE_CBYTES_REL + 3 * p.canon_bytes + 32;
 }
@@ -1153,21 +1244,32 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
                               const FastEncParamsHost& hp, ckr_stream_header* hdrs, uint8_t* sidecar, uint8_t* out,
                               uint64_t* unit_off, uint64_t* status, uint32_t* ctl, uint32_t* redo_list,
                               hipStream_t s) {
-    uint64_t* phase = prof_phase_buffer(g.n_units * 5, s);
+    uint64_t* phase = prof_phase_buffer(g.n_units * 8, s);
     FastEncParams fp;
     fp.sl0 = hp.sl0; fp.sl1 = hp.sl1; fp.cw = hp.cw; fp.canon_bytes = hp.canon_bytes;
     fp.stride0 = slot_stride(hp.sl0); fp.stride1 = slot_stride(hp.sl1);
     const uint64_t n = g.n_units;
-    CKR_LAUNCH("encode_fast_reset_kernel", s, encode_fast_reset_kernel<<<(uint32_t)((n + 255) / 256), 256, 0, s>>>(status, n, ctl));
+    const uint64_t nst = encode_fast_status_words(n);  // unit words, block words, block counts
+    CKR_LAUNCH("encode_fast_reset_kernel", s, encode_fast_reset_kernel<<<(uint32_t)((nst + 255) / 256), 256, 0, s>>>(status, nst, ctl));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const uint32_t lb = encode_fast_lds_bytes(hp);
+    // persistent grid: as many workgroups as fit on the device at once (more
+    // would only find the tickets gone), never more than there are units
+    int dev = 0, ncu = 0;
+    if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+    if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
 #define CKR_FAST_ENC(SPE_, ESC_, SIDE_)                                                                        \
     do {                                                                                                      \
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&encode_fast_kernel<SPE_, ESC_, SIDE_>),      \
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);                       \
+        const void* kf = reinterpret_cast<const void*>(&encode_fast_kernel<SPE_, ESC_, SIDE_, FE_NW>);        \
+        (void)hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);                   \
+        int per_cu = 0;                                                                                       \
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, encode_fast_kernel<SPE_, ESC_, SIDE_, FE_NW>, \
+                                                         64 * FE_NW, lb) != hipSuccess || per_cu < 1)          \
+            per_cu = 1;                                                                                       \
+        const uint32_t grid = (uint32_t)std::min<uint64_t>(n, (uint64_t)per_cu * (uint64_t)std::max(ncu, 1)); \
         CKR_LAUNCH("encode_fast_kernel", s,                                                                   \
-                   encode_fast_kernel<SPE_, ESC_, SIDE_><<<(uint32_t)n, 128, lb, s>>>(                         \
+                   encode_fast_kernel<SPE_, ESC_, SIDE_, FE_NW><<<grid, 64 * FE_NW, lb, s>>>(                  \
                        src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status, ctl, redo_list, phase)); \
     } while (0)
     const bool side = sidecar != nullptr;
