@@ -541,7 +541,9 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
             fp.sl0 = lane_slot_bytes(h_planes, h_table, K);
             fp.sl1 = lane_slot_bytes(h_planes ? h_planes + 256 : nullptr, h_table, K);
         }
-        fast = (int)ckr::encode_fast_lds_bytes(fp) <= max_lds_per_block();
+        // the lane tables hold LDS addresses in 16 bits
+        const uint32_t lds = ckr::encode_fast_lds_bytes(fp);
+        fast = (int)lds <= max_lds_per_block() && lds <= 65536u;
     }
     if (fast) {
         auto* status = reinterpret_cast<uint64_t*>(ws + L.off_status);

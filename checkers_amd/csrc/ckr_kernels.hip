@@ -658,30 +658,29 @@ struct FastEncParams {
     uint32_t canon_bytes;       // bytes per canonical entry in the LDS copy (stream order)
 };
 
-// LDS layout (bytes): guard 512 | rank-0 slots 64 x stride0 | rank-1 slots 64 x
-// stride1 | table 256 x 8 (see EncPair) | lane tables: loff 257 x u32 (+pad),
-// delta 256 x i32, the two waves' chains (count, state) 4 x 64 x u32 and 8 u32
-// of unit-wide values | canonical headers 12 x u32 | canonical bytes 3 x
-// canon_bytes | 32 bytes of read padding.  A lane's dwords are flushed
-// downward from the end of its slot; a lane that outgrows its slot keeps
+// LDS layout (bytes): lane tables | rank-0 slots 64 x stride0 | rank-1 slots
+// 64 x stride1 | table 256 x 16 (see enc_quad) | canonical headers 12 x u32 |
+// canonical bytes 3 x canon_bytes | 32 bytes of read padding.  The lane tables
+// (lane offsets and LDS stream starts, 16 bits each, the waves' chain counts
+// and states, unit-wide values) are only written after every lane is coded, so
+// the region doubles as the guard under the slots: a lane's dwords are flushed
+// downward from the end of its slot, and a lane that outgrows its slot keeps
 // flushing into the slots below it (lanes of the same unit, whose bytes are
-// then redone by the general kernels) and, for the lowest slot, into the guard
-// (at most 2 bytes per symbol, 256 symbols), so the table and the canonical
-// headers, which the unit's sizes depend on, are never overwritten.
-static constexpr uint32_t FE_GUARD = 512;
-#ifndef FE_NW
-#define FE_NW 2  // waves per unit of the fast encoder (1 or 2)
-#endif
-static constexpr uint32_t FE_TABSZ = 2048;                       // table, after the slots
-static constexpr uint32_t FE_LOFF = FE_TABSZ, FE_DELTA = FE_LOFF + 1040, FE_XCH = FE_DELTA + 1024,
-                          FE_BCAST = FE_XCH + 1024, FE_CHDR = FE_BCAST + 32, FE_CBYTES_REL = FE_CHDR + 48;
+// then redone by the general kernels) and, for the lowest slot, into the lane
+// tables (at most 2 bytes per symbol, 256 symbols: 516 bytes), so the table
+// and the canonical headers, which the unit's sizes depend on, are never
+// overwritten.
+static constexpr uint32_t FE_LOFF = 0, FE_SA = 520, FE_XCH = 1032, FE_BCAST = 1800, FE_META = 1824;
+static constexpr uint32_t FE_TABSZ = 4096, FE_CHDR_REL = FE_TABSZ, FE_CBYTES_REL = FE_TABSZ + 48;
+static_assert(FE_META >= 516 && FE_META % 16 == 0, "lane tables: guard size and table alignment");
 
-// Encode table entry in LDS, 8 bytes (one ds_read_b64 per symbol, which costs
-// the LDS no more than a 32-bit read): x = rcp; y = cmpl | rsh << 12 | bias << 16
-// (see EncSym: cmpl = M - f < 4096, rsh < 12, bias < 8192).  y = ~0u marks f == 0.
-__device__ __forceinline__ uint32_t enc_pair_y(const EncSym& e) {
-    if (e.xmax == 0) return 0xFFFFFFFFu;
-    return (e.cmpl_rsh & 0xFFFu) | ((e.cmpl_rsh >> 16) << 12) | (e.bias << 16);
+// Encode table entry in LDS, 16 bytes, every field ready for its instruction
+// (one ds_read_b128 per symbol): x = rcp; y = cmpl | rsh << 24 (the 24-bit
+// multiply reads cmpl, the shift reads byte 3); z = bias; w = 8f (the
+// renormalisation compares read it against bytes of the state).  See EncSym:
+// cmpl = M - f, rsh < 12, bias < 8192; w = 0 marks f == 0.
+__device__ __forceinline__ uint4 enc_quad(const EncSym& e) {
+    return make_uint4(e.rcp, (e.cmpl_rsh & 0xFFFu) | ((e.cmpl_rsh >> 16) << 24), e.bias, e.xmax >> 16);
 }
 
 // Lane coder state.  x: rANS state.  {hi, lo}: the last 8 bytes emitted, the
@@ -693,23 +692,22 @@ struct EncLane {
 };
 
 // One symbol of rans_encode_kernel's loop body (ANSCompressor.cpp:180-202)
-// without branches, from the table entry t (see enc_pair_y).  Renormalisation
-// emits n in {0,1,2} bytes: x >= f*2^19 and x >= f*2^27 are (x >> 16) >= 8f and
-// (x >> 24) >= 8f, with 8f = 32768 - 8 cmpl.  The n low bytes of x, low byte
-// first (the reference's emission order), enter the window from the top: one
-// v_alignbyte per register shifts by n bytes.  ESC: the table may give f == 0
-// to a symbol of the data (raw-byte escape, no state update, :185-192); tables
-// built from the data itself never do.
+// without branches, from the table entry t (see enc_quad).  Renormalisation
+// emits n in {0,1,2} bytes: x >= f*2^19 and x >= f*2^27 are (x >> 16) >= 8f
+// and (x >> 24) >= 8f.  The n low bytes of x, low byte first (the reference's
+// emission order), enter the window from the top: one v_alignbyte per register
+// shifts by n bytes.  ESC: the table may give f == 0 to a symbol of the data
+// (raw-byte escape, no state update, :185-192); tables built from the data
+// itself never do.
 template <bool ESC>
-__device__ __forceinline__ void enc_step(EncLane& s, uint32_t sym, uint2 t) {
-    const uint32_t cm = t.y & 0xFFFu;
-    const uint32_t f8 = 32768u - (cm << 3);
+__device__ __forceinline__ void enc_step(EncLane& s, uint32_t sym, uint4 t) {
+    const uint32_t f8 = t.w;
     const uint32_t x = s.x;
     uint32_t n4 = ((x >> 24) >= f8) ? 0x02020202u : (((x >> 16) >= f8) ? 0x01010101u : 0u);
     uint32_t ins = x;
     bool esc = false;
     if (ESC) {
-        esc = t.y == 0xFFFFFFFFu;
+        esc = f8 == 0u;
         n4 = esc ? 0x01010101u : n4;
         ins = esc ? sym : x;
     }
@@ -717,8 +715,8 @@ __device__ __forceinline__ void enc_step(EncLane& s, uint32_t sym, uint2 t) {
     s.lo = __builtin_amdgcn_alignbyte(s.hi, s.lo, n4);
     s.hi = __builtin_amdgcn_alignbyte(ins, s.hi, n4);
     s.sel -= n4;
-    const uint32_t q = __umulhi(xr, t.x) >> ((t.y >> 12) & 15u);
-    const uint32_t xn = (xr + (t.y >> 16)) + __umul24(q, cm);
+    const uint32_t q = __umulhi(xr, t.x) >> (t.y >> 24);
+    const uint32_t xn = xr + t.z + __umul24(q, t.y);
     s.x = (ESC && esc) ? x : xn;
 }
 
@@ -857,14 +855,6 @@ __device__ __forceinline__ uint4 merge16_from(uint4 v, uint4 r, uint32_t s) {
                       (r.w & m(3)) | (v.w & ~m(3)));
 }
 
-// Largest lane L with loff[L] <= q (q < loff[256]).
-__device__ __forceinline__ uint32_t lane_of(const uint32_t* loff, uint32_t q) {
-    uint32_t lo = 0;
-#pragma unroll
-    for (uint32_t step = 128; step > 0; step >>= 1)
-        if (loff[lo + step] <= q) lo += step;
-    return lo;
-}
 
 // Coding of the live lanes of every column of a unit whose rows are all full
 // (length a multiple of 256, so every column has the same nrows rows).  P = 0:
@@ -879,7 +869,7 @@ __device__ __forceinline__ uint32_t lane_of(const uint32_t* loff, uint32_t q) {
 // or all of them when P = 2.
 template <int SPE, bool ESC, bool SIDE, int P>
 __device__ __forceinline__ void enc_full_rows(EncLane& c0, EncLane& c1, const uint8_t* ucol, uint8_t* sidecar,
-                                              uint64_t ubase, uint32_t j, uint32_t nrows, const uint2* tab,
+                                              uint64_t ubase, uint32_t j, uint32_t nrows, const uint4* tab,
                                               uint8_t* lds8) {
     constexpr int FL = SPE == 2 ? 2 : 1;
     constexpr uint32_t SH0 = P == 1 ? 24u : 8u * FL;  // byte of chain c0
@@ -909,7 +899,7 @@ __device__ __forceinline__ void enc_full_rows(EncLane& c0, EncLane& c1, const ui
         for (int i = 0; i < 32; i++) r[i] = p[-64 * i];
     };
     auto code = [&](const uint32_t (&r)[32], uint32_t g) {
-        uint2 t0[2][8], t1[2][8];
+        uint4 t0[2][8], t1[2][8];
         auto fetch = [&](int buf, int i0) {
 #pragma unroll
             for (int i = 0; i < 8; i++) {
@@ -947,6 +937,8 @@ __device__ __forceinline__ void enc_full_rows(EncLane& c0, EncLane& c1, const ui
     }
 }
 
+static constexpr int kFastEncWaves = 2;  // waves per unit of the fast encoder (1 or 2)
+
 // Persistent: each workgroup stages the table and the canonical streams once,
 // then takes units from the ticket counter until none is left.  NW = 1: one
 // wave per unit, each thread codes both live lanes of its column.  NW = 2: wave
@@ -965,15 +957,15 @@ __global__ void __launch_bounds__(64 * NW) encode_fast_kernel(const uint8_t* __r
                                                           uint64_t* __restrict__ phase) {
     extern __shared__ uint32_t lds[];
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
-    const uint32_t st0_off = FE_GUARD;
+    const uint32_t st0_off = FE_META;
     const uint32_t st1_off = st0_off + 64 * fp.stride0;
     const uint32_t tb = st1_off + 64 * fp.stride1;  // table
-    const uint2* tab = reinterpret_cast<const uint2*>(lds8 + tb);
-    uint32_t* loff = reinterpret_cast<uint32_t*>(lds8 + tb + FE_LOFF);
-    int32_t* delta = reinterpret_cast<int32_t*>(lds8 + tb + FE_DELTA);
-    uint32_t* xch = reinterpret_cast<uint32_t*>(lds8 + tb + FE_XCH);   // [wave][count 64 | state 64]
-    uint32_t* bc = reinterpret_cast<uint32_t*>(lds8 + tb + FE_BCAST);  // ticket, offset, flags
-    uint32_t* chdr = reinterpret_cast<uint32_t*>(lds8 + tb + FE_CHDR);
+    const uint4* tab = reinterpret_cast<const uint4*>(lds8 + tb);
+    uint16_t* loff = reinterpret_cast<uint16_t*>(lds8 + FE_LOFF);  // lane offsets in the unit (257)
+    uint16_t* lsa = reinterpret_cast<uint16_t*>(lds8 + FE_SA);     // LDS stream starts (256)
+    uint32_t* xch = reinterpret_cast<uint32_t*>(lds8 + FE_XCH);    // byte FL: count, state | byte 3: count
+    uint32_t* bc = reinterpret_cast<uint32_t*>(lds8 + FE_BCAST);   // ticket, offset
+    uint32_t* chdr = reinterpret_cast<uint32_t*>(lds8 + tb + FE_CHDR_REL);
     const uint32_t cb_off = tb + FE_CBYTES_REL;
     const uint32_t tid = threadIdx.x;
     const uint32_t w = NW == 1 ? 0u : __builtin_amdgcn_readfirstlane(tid >> 6);  // NW = 2: 0 plane FL, 1 plane 3
@@ -988,11 +980,11 @@ __global__ void __launch_bounds__(64 * NW) encode_fast_kernel(const uint8_t* __r
         uint4 tv[256 / NT];
 #pragma unroll
         for (uint32_t k = 0; k < 256 / NT; k++) tv[k] = d_tab[tid + NT * k];
-        uint2* wt = reinterpret_cast<uint2*>(lds8 + tb);
+        uint4* wt = reinterpret_cast<uint4*>(lds8 + tb);
 #pragma unroll
         for (uint32_t k = 0; k < 256 / NT; k++) {
             const EncSym e = {tv[k].x, tv[k].y, tv[k].z, tv[k].w};
-            wt[tid + NT * k] = make_uint2(e.rcp, enc_pair_y(e));
+            wt[tid + NT * k] = enc_quad(e);
         }
         const uint32_t* cs = canon + 3 * (4 + fp.cw);
         uint32_t* cb32 = reinterpret_cast<uint32_t*>(lds8 + cb_off);
@@ -1059,10 +1051,16 @@ __global__ void __launch_bounds__(64 * NW) encode_fast_kernel(const uint8_t* __r
             e0 = e; x0 = c.x;
             e1 = enc_finish(c1, lds8, end1); x1 = c1.x;
         } else {
-            xch[128 * w + j] = e;
-            xch[128 * w + 64 + j] = c.x;
+            // the lane tables double as the slots' guard: written only once both
+            // waves are done coding
             __syncthreads();
-            e0 = xch[j]; x0 = xch[64 + j]; e1 = xch[128 + j]; x1 = xch[192 + j];
+            if (w == 0) { xch[j] = e; xch[64 + j] = c.x; }
+            else xch[128 + j] = e;
+            __syncthreads();
+            e0 = w ? xch[j] : e;
+            x0 = w ? xch[64 + j] : c.x;
+            e1 = w ? e : xch[128 + j];
+            x1 = w ? c.x : 0u;  // states of byte 3 are only needed by wave 1 (headers)
         }
         // byte counts, final states and LDS stream starts of the four lanes of
         // column j (with NW = 2 both waves compute them; the scan is wave-local)
@@ -1110,11 +1108,11 @@ __global__ void __launch_bounds__(64 * NW) encode_fast_kernel(const uint8_t* __r
                 }
                 h.pad = 0;
                 uh[b] = h;
-                loff[4 * j + b] = run;
-                delta[4 * j + b] = (int32_t)sa[b] - (int32_t)run;
+                loff[4 * j + b] = (uint16_t)run;
+                lsa[4 * j + b] = (uint16_t)sa[b];
                 run += cnt[b];
             }
-            if (j == 63) loff[256] = total;
+            if (j == 63) loff[256] = (uint16_t)total;
         }
         if (w == 0) {
             const uint64_t off = lookback_wave(status, g.n_units, u, size, &ctl[2], j);
@@ -1162,7 +1160,7 @@ __global__ void __launch_bounds__(64 * NW) encode_fast_kernel(const uint8_t* __r
                     L++;
                     const int32_t lo2 = (int32_t)loff[L], hi2 = (int32_t)loff[L + 1];
                     if (hi2 > lo2) {
-                        v = merge16_from(v, lds_read16(lds8, (uint32_t)(delta[L] + q)), (uint32_t)(pos - q));
+                        v = merge16_from(v, lds_read16(lds8, (uint32_t)((int32_t)lsa[L] - lo2 + q)), (uint32_t)(pos - q));
                         pos = hi2;
                     }
                 }
@@ -1230,14 +1228,15 @@ __global__ void encode_fast_reset_kernel(uint64_t* status, uint64_t n, uint32_t*
 }
 
 static uint32_t slot_stride(uint32_t sl) {
-    // consecutive lanes' slots start (stride / 4) banks apart: keep that odd
-    return ((sl >> 2) & 1u) ? sl + 8 : sl + 4;
+    // 4 bytes between slots: a stream that fills its slot exactly still writes one
+    // dword below its start (the final partial dword, empty)
+    return sl + 4;
 }
 
 uint64_t encode_fast_status_words(uint64_t n_units) { return n_units + 2 * ((n_units + 63) / 64); }
 
 uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p) {
-    return FE_GUARD + 64 * (slot_stride(p.sl0) + slot_stride(p.sl1)) + FE_CBYTES_REL + 3 * p.canon_bytes + 32;
+    return FE_META + 64 * (slot_stride(p.sl0) + slot_stride(p.sl1)) + FE_CBYTES_REL + 3 * p.canon_bytes + 32;
 }
 
 hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
@@ -1261,15 +1260,15 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
     if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
 #define CKR_FAST_ENC(SPE_, ESC_, SIDE_)                                                                        \
     do {                                                                                                      \
-        const void* kf = reinterpret_cast<const void*>(&encode_fast_kernel<SPE_, ESC_, SIDE_, FE_NW>);        \
+        const void* kf = reinterpret_cast<const void*>(&encode_fast_kernel<SPE_, ESC_, SIDE_, kFastEncWaves>);        \
         (void)hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);                   \
         int per_cu = 0;                                                                                       \
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, encode_fast_kernel<SPE_, ESC_, SIDE_, FE_NW>, \
-                                                         64 * FE_NW, lb) != hipSuccess || per_cu < 1)          \
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, encode_fast_kernel<SPE_, ESC_, SIDE_, kFastEncWaves>, \
+                                                         64 * kFastEncWaves, lb) != hipSuccess || per_cu < 1)          \
             per_cu = 1;                                                                                       \
         const uint32_t grid = (uint32_t)std::min<uint64_t>(n, (uint64_t)per_cu * (uint64_t)std::max(ncu, 1)); \
         CKR_LAUNCH("encode_fast_kernel", s,                                                                   \
-                   encode_fast_kernel<SPE_, ESC_, SIDE_, FE_NW><<<grid, 64 * FE_NW, lb, s>>>(                  \
+                   encode_fast_kernel<SPE_, ESC_, SIDE_, kFastEncWaves><<<grid, 64 * kFastEncWaves, lb, s>>>(                  \
                        src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status, ctl, redo_list, phase)); \
     } while (0)
     const bool side = sidecar != nullptr;
