@@ -199,7 +199,7 @@ struct DecodeLayout {
 DecodeLayout decode_layout(const ckr::EncodeGeom& g) {
     DecodeLayout L{};
     const CanonKs ck = canon_ks(g);
-    L.fast = g_fast_paths != 0 && g.spe > 0 && g.n_units > 0 && ck.cw <= ckr::decode_fast_max_cw();
+    L.fast = g_fast_paths != 0 && g.spe > 0 && g.n_units > 0 && use_dedup(g);
     uint64_t o = 0;
     L.off_enc = o;   o = align_up(o + 256 * sizeof(ckr::EncSym), kAlign);
     L.off_canon = o; o = align_up(o + (L.fast ? 3ull * (4 + 2 * ck.cw) * 4 : 0), kAlign);

@@ -101,11 +101,10 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
 hipError_t launch_canon(const EncSym* d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw, uint32_t* canon,
                         hipStream_t s);
 
-// Decode; with canon and unit_mask (n_units u32) the LDS-staged fast kernel runs
-// first for units <= 64 KiB of masked dtypes (canonical entries of cw <=
-// decode_fast_max_cw() dwords) and the general kernel takes the units it left.
+// Decode; with canon and unit_mask (n_units u32) the fast kernel runs first for
+// the units of masked dtypes whose length is a multiple of 256 (and raw units),
+// and the general kernel takes the units it left.
 uint32_t decode_fast_lds_bytes();
-uint32_t decode_fast_max_cw();
 hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
                          const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
                          unsigned long long* bad, const uint32_t* canon, uint32_t cw, uint32_t* unit_mask,

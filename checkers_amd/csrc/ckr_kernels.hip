@@ -1343,12 +1343,13 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
                                                      uint8_t* __restrict__ dst, unsigned long long* bad,
                                                      const uint32_t* __restrict__ unit_mask) {
     __shared__ uint32_t tab[4096];
-    for (uint32_t i = threadIdx.x; i < 4096; i += 256) tab[i] = d_dec[i];
-    __syncthreads();
     const uint32_t j = threadIdx.x & 63;
     const uint64_t u = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (u >= g.n_units) return;
-    if (unit_mask && unit_mask[u] == 0) return;
+    const bool mine = u < g.n_units && (!unit_mask || unit_mask[u] != 0);
+    if (!__syncthreads_or(mine)) return;  // no unit of this block left to this kernel
+    for (uint32_t i = threadIdx.x; i < 4096; i += 256) tab[i] = d_dec[i];
+    __syncthreads();
+    if (!mine) return;
     const uint64_t ubase = u * g.unit;
     const uint32_t len = unit_len(g, ubase);
     const uint8_t* ud = data + unit_off[u];
@@ -1397,204 +1398,299 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
     if (nbad) atomicAdd(bad, (unsigned long long)nbad);
 }
 
-// Fast decoder for units of at most 64 KiB with masked planes (spe > 0).
-// Block = 4 waves, one unit per wave; LDS holds the decode table (16 KiB,
-// shared), the canonical zero-plane streams, and per wave its unit's packed
-// bytes, brought in with coalesced 16-byte loads.  Live lanes decode from LDS
-// (two per thread) with the sidecar of the next 32 rows already requested;
-// zero-plane lanes are checked against the canonical stream (header and bytes)
-// and produce zeros.  A unit larger than the per-wave budget is left to
-// decode_kernel (marked in unit_mask).
-static constexpr uint32_t FAST_STAGE_BYTES = 35 * 1024;  // per wave
-static constexpr uint32_t FAST_CANON_DWORDS = 3 * (4 + 130);
+// Fast decoder (masked planes, spe > 0; units whose length is a multiple of
+// 256).  One block of DF_WAVES waves per CU, persistent over the units; a wave
+// decodes one unit at a time, thread j taking column j, whose two live lanes
+// it decodes side by side.  LDS holds the decode table, 4096 entries of
+// {f | sym << 24, slot - cum} (the state update is one 24-bit multiply-add),
+// and per live lane a ring with 128 bytes of its stream: two 64-byte chunks,
+// chunk k of the stream (from the unit's 64-byte aligned base) in slot k & 1.
+// A ring is stored dword-major: its dword r (stream bytes 4r..4r+3 modulo 128)
+// is in row r, a row being 64 dwords, one per thread, so the lanes of a wave
+// always read distinct banks; row 32 repeats row 0, so the two dwords around
+// any byte are one ds_read2st64.  Stream bytes are taken in pairs of symbols:
+// the 4 bytes at p serve both.  Rows go in groups of 8, which consume at most
+// 16 bytes of a lane: when a group ends with p in chunk ch + 1 (ch: the chunk of
+// p at the previous check), the lane moves on to it and fetches chunk ch + 2
+// (four 16-byte loads of one 64-byte span, so each line of the stream is read
+// from L2 in two pieces at most), written into the slot of chunk ch at the end
+// of the next group, three groups at least before it is read.  The decoded
+// tensor and the sidecar are streamed with non-temporal accesses so that they
+// do not push the streams' lines out of L2.  Zero-plane lanes are checked
+// against the canonical stream (header and bytes) and produce zeros.  Units of
+// other lengths (a tensor's last), and units whose chunks could pass the end of
+// the data buffer, are left to decode_kernel (marked in unit_mask).
+static constexpr uint32_t DF_WAVES = 7;
+static constexpr uint32_t DF_TAB_BYTES = 4096 * 8;
+static constexpr uint32_t DF_RING_BYTES = 33 * 256;  // 32 rows + the copy of row 0
+static constexpr uint32_t DF_WAVE_BYTES = 2 * DF_RING_BYTES;
 
-// 16 bytes at data[a..a+16) of which only those below data_len exist.
-__device__ __forceinline__ uint4 load_tail16(const uint8_t* data, uint64_t a, uint64_t data_len) {
-    uint32_t w0 = 0, w1 = 0, w2 = 0, w3 = 0;
+// The dword at byte offset o (a multiple of 4) of the data buffer.
+__device__ __forceinline__ const uint32_t* data32_at(const uint8_t* data, uint64_t o) {
+    return reinterpret_cast<const uint32_t*>(data + o);
+}
+
+// One live lane of the fast decoder.
+struct DfLane {
+    uint32_t x;        // rANS state
+    uint32_t p8;       // 8 x (position of the next stream byte, from the unit's 64-byte aligned base)
+    uint32_t ch;       // chunk of p at the last check
+    uint32_t tb;       // LDS address of this lane's ring column (row 0)
+    bool pend;         // chunk ch + 1 is in flight in c[], to be written at the end of this group
+    uint4 c0, c1, c2, c3;
+};
+
+// Chunk k (64 bytes) of the unit's aligned base.
+__device__ __forceinline__ void df_fetch(const uint8_t* ua, uint32_t k, uint4& c0, uint4& c1, uint4& c2, uint4& c3) {
+    const uint4* q = reinterpret_cast<const uint4*>(ua + ((size_t)k << 6));
+    c0 = q[0]; c1 = q[1]; c2 = q[2]; c3 = q[3];
+}
+
+// Writes chunk k into ring slot k & 1 (rows 16s..16s+15; slot 0 also into row 32).
+__device__ __forceinline__ void df_put(uint8_t* lds8, uint32_t tb, uint32_t k, const uint4& c0, const uint4& c1,
+                                       const uint4& c2, const uint4& c3) {
+    uint32_t* w = reinterpret_cast<uint32_t*>(lds8 + tb + ((k & 1u) << 12));
+    w[0] = c0.x; w[64] = c0.y; w[128] = c0.z; w[192] = c0.w;
+    w[256] = c1.x; w[320] = c1.y; w[384] = c1.z; w[448] = c1.w;
+    w[512] = c2.x; w[576] = c2.y; w[640] = c2.z; w[704] = c2.w;
+    w[768] = c3.x; w[832] = c3.y; w[896] = c3.z; w[960] = c3.w;
+    if ((k & 1u) == 0) w[2048] = c0.x;
+}
+
+// The 4 stream bytes at p, byte p in bits 31..24.
+__device__ __forceinline__ uint32_t df_window(const DfLane& d, const uint8_t* lds8) {
+    const uint32_t* r = reinterpret_cast<const uint32_t*>(lds8 + d.tb + (__builtin_amdgcn_ubfe(d.p8, 5, 5) << 8));
+    const uint32_t d0 = r[0], d1 = r[64];
+    return __builtin_amdgcn_perm(0u, __builtin_amdgcn_alignbit(d1, d0, d.p8), 0x00010203u);
+}
+
+// One symbol (the inverse of rans_encode_kernel's step, ANSCompressor.cpp:180-202):
+// x = f*(x >> 12) + slot - cum, then renormalise with 8n bits from the top of w
+// (stream order), n = 0, 1, 2 for x >= 2^23, 2^15 <= x < 2^23, x < 2^15 (x >= 2^11
+// here), i.e. 8n = (clz(x) - 1) & 24.  Returns the table word (symbol in bits
+// 31..24) and the bits consumed in sh.
+__device__ __forceinline__ uint32_t df_sym(uint32_t& x, uint32_t& w, uint32_t& sh, const uint2* tab) {
+    const uint2 e = tab[x & (M - 1u)];
+    const uint32_t xx = __umul24(e.x, x >> 12) + e.y;
+    sh = ((uint32_t)__builtin_clz(xx) - 1u) & 24u;
+    const uint64_t t = (((uint64_t)xx << 32) | w) << sh;
+    x = (uint32_t)(t >> 32);
+    w = (uint32_t)t;
+    return e.x;
+}
+
+// End of a group: write the chunk fetched at the end of the previous group,
+// then move on if p has reached the next chunk and fetch the one after it.
+__device__ __forceinline__ void df_step(DfLane& d, uint8_t* lds8, const uint8_t* ua, uint32_t lim_ch) {
+    if (d.pend) df_put(lds8, d.tb, d.ch + 1u, d.c0, d.c1, d.c2, d.c3);
+    const bool adv = (d.p8 >> 9) > d.ch;
+    d.ch += adv ? 1u : 0u;
+    d.pend = adv;
+    if (adv) df_fetch(ua, min(d.ch + 1u, lim_ch), d.c0, d.c1, d.c2, d.c3);
+}
+
+template <int SPE>
+__device__ __forceinline__ uint32_t df_pack(uint32_t e0, uint32_t e1, uint32_t sw, uint32_t sel) {
+    return __builtin_amdgcn_perm(__builtin_amdgcn_perm(e1, e0, SPE == 2 ? 0x07030C0Cu : 0x070C030Cu), sw, sel);
+}
+
+// The decoded tensor and the sidecar are streamed once (non-temporal).
+__device__ __forceinline__ void df_store(uint32_t* p, uint32_t v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ uint32_t df_ld(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+
+// Byte selector for df_pack: o = 0 or 2, the offset of the column's sidecar
+// bytes in their dword.  SPE 2: bytes {s0, s1, sym FL, sym 3}; SPE 1: {s0, sym
+// FL, s1, sym 3}.
+template <int SPE>
+__device__ __forceinline__ uint32_t df_sel(uint32_t o) {
+    return SPE == 2 ? 0x07060100u + o * 0x0101u : 0x07010500u + o * 0x00010001u;
+}
+
+// Two rows: one window read per lane, two symbols from it.
+template <int SPE>
+__device__ __forceinline__ void df_pair(DfLane& a, DfLane& b, const uint8_t* lds8, const uint2* tab, uint32_t* out,
+                                        uint32_t sv0, uint32_t sv1, uint32_t sel) {
+    uint32_t wa = df_window(a, lds8), wb = df_window(b, lds8);
+    uint32_t ha0, ha1, hb0, hb1;
+    const uint32_t a0 = df_sym(a.x, wa, ha0, tab);
+    const uint32_t b0 = df_sym(b.x, wb, hb0, tab);
+    df_store(out, df_pack<SPE>(a0, b0, sv0, sel));
+    const uint32_t a1 = df_sym(a.x, wa, ha1, tab);
+    const uint32_t b1 = df_sym(b.x, wb, hb1, tab);
+    df_store(out + 64, df_pack<SPE>(a1, b1, sv1, sel));
+    a.p8 += ha0 + ha1;
+    b.p8 += hb0 + hb1;
+}
+
+// Eight rows (sidecar words sc), then the window step.
+template <int SPE>
+__device__ __forceinline__ void df_group(DfLane& a, DfLane& b, uint8_t* lds8, const uint2* tab, uint32_t* out,
+                                         const uint32_t (&sc)[8], uint32_t sel, const uint8_t* ua, uint32_t lim_ch) {
 #pragma unroll
-    for (int b = 0; b < 16; b++) {
-        const uint32_t v = (a + b < data_len) ? (uint32_t)data[a + b] : 0u;
-        if (b < 4) w0 |= v << (8 * b);
-        else if (b < 8) w1 |= v << (8 * (b - 4));
-        else if (b < 12) w2 |= v << (8 * (b - 8));
-        else w3 |= v << (8 * (b - 12));
-    }
-    return make_uint4(w0, w1, w2, w3);
+    for (int r = 0; r < 8; r += 2) df_pair<SPE>(a, b, lds8, tab, out + 64 * r, sc[r], sc[r + 1], sel);
+    df_step(a, lds8, ua, lim_ch);
+    df_step(b, lds8, ua, lim_ch);
+}
+
+__device__ __forceinline__ void df_load_sc(uint32_t (&sc)[8], const uint32_t* p) {
+#pragma unroll
+    for (int r = 0; r < 8; r++) sc[r] = df_ld(p + 32 * r);  // rows are 128 sidecar bytes apart
 }
 
 template <int SPE>
-__device__ __forceinline__ uint32_t decode_live_sym(uint32_t& x, uint32_t& p, uint32_t e, const uint8_t* stage,
-                                                    const uint32_t* tab) {
-    const uint32_t c0 = stage[p], c1 = stage[p + 1];  // speculative: used only if consumed
-    const uint32_t slot = x & (M - 1u);
-    const uint32_t te = tab[slot];
-    const uint32_t f = ((te >> 8) & 4095u) + 1u, cum = te >> 20;
-    uint32_t xx = f * (x >> 12) + slot - cum;
-    const uint32_t t1 = (xx < L && p < e) ? 1u : 0u;
-    xx = t1 ? ((xx << 8) | c0) : xx;
-    const uint32_t t2 = (t1 && xx < L && p + 1 < e) ? 1u : 0u;
-    xx = t2 ? ((xx << 8) | c1) : xx;
-    p += t1 + t2;
-    x = xx;
-    return te & 255u;
-}
-
-template <int SPE>
-__global__ void __launch_bounds__(256) decode_fast_kernel(const uint8_t* __restrict__ data,
-                                                          const ckr_stream_header* __restrict__ hdrs,
-                                                          const uint64_t* __restrict__ unit_off,
-                                                          const uint32_t* __restrict__ d_dec,
-                                                          const uint32_t* __restrict__ canon, uint32_t cw,
-                                                          EncodeGeom g, const uint8_t* __restrict__ sidecar,
-                                                          uint8_t* __restrict__ dst, unsigned long long* bad,
-                                                          uint32_t* __restrict__ unit_mask) {
+__global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_t* __restrict__ data,
+                                                                   const ckr_stream_header* __restrict__ hdrs,
+                                                                   const uint64_t* __restrict__ unit_off,
+                                                                   const uint32_t* __restrict__ d_dec,
+                                                                   const uint32_t* __restrict__ canon, uint32_t cw,
+                                                                   EncodeGeom g, const uint8_t* __restrict__ sidecar,
+                                                                   uint8_t* __restrict__ dst, unsigned long long* bad,
+                                                                   uint32_t* __restrict__ unit_mask) {
     extern __shared__ uint32_t lds[];
-    uint32_t* tab = lds;                                   // 4096
-    uint32_t* can = lds + 4096;                            // FAST_CANON_DWORDS
-    uint8_t* stage_all = reinterpret_cast<uint8_t*>(lds + 4096 + FAST_CANON_DWORDS);
-    {
-        uint32_t tv[16];
-#pragma unroll
-        for (int k = 0; k < 16; k++) tv[k] = d_dec[threadIdx.x + 256 * k];
-#pragma unroll
-        for (int k = 0; k < 16; k++) tab[threadIdx.x + 256 * k] = tv[k];
-    }
-    // canonical entries: header words as they are, then the stream in byte order
-    for (uint32_t i = threadIdx.x; i < 3 * (4 + cw); i += 256) {
-        const uint32_t ent = i / (4 + cw), w = i % (4 + cw);
-        can[i] = (w < 4) ? canon[i] : canon[3 * (4 + cw) + ent * cw + (w - 4)];
+    uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
+    const uint2* tab = reinterpret_cast<const uint2*>(lds);
+    for (uint32_t i = threadIdx.x; i < 4096; i += 64 * DF_WAVES) {
+        const uint32_t e = d_dec[i];  // sym | (f - 1) << 8 | cum << 20
+        reinterpret_cast<uint2*>(lds)[i] = make_uint2((((e >> 8) & 4095u) + 1u) | ((e & 255u) << 24), i - (e >> 20));
     }
     __syncthreads();
 
-    const uint32_t j = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const uint64_t u = (uint64_t)blockIdx.x * 4 + wv;
-    if (u >= g.n_units) return;
-    uint8_t* stage = stage_all + wv * (FAST_STAGE_BYTES + 32);
-    const uint64_t ubase = u * g.unit;
-    const uint32_t len = unit_len(g, ubase);
-    const uint64_t uoff = unit_off[u];
-    const uint8_t* ud = data + uoff;
-    const uint32_t usize = (uint32_t)(unit_off[u + 1] - uoff);
-    const uint64_t data_len = unit_off[g.n_units];
-    const ckr_stream_header* uh = hdrs + u * 256;
-    if (usize == len && uh[0].byte_count == len) {
-        if (j == 0) unit_mask[u] = 0;
-        decode_raw_unit<SPE>(ud, ubase, len, j, sidecar, dst);
-        return;
-    }
-    // stage [uoff, uoff+usize) with 16-byte loads from the enclosing aligned blocks
-    const uint64_t gs = uoff & ~15ull, ge = (uoff + usize + 15) & ~15ull;
-    const uint32_t nst = (uint32_t)(ge - gs), shift = (uint32_t)(uoff - gs);
-    if (nst > FAST_STAGE_BYTES) {
-        if (j == 0) unit_mask[u] = 1;
-        return;
-    }
-    if (j == 0) unit_mask[u] = 0;
-    {
-        const uint32_t nv = nst >> 4;
-        const uint4* gsrc = reinterpret_cast<const uint4*>(data + gs);
-        uint4* sdst = reinterpret_cast<uint4*>(stage);
-        for (uint32_t i0 = 0; i0 < nv; i0 += 64 * 12) {
-            uint4 v[12];
-#pragma unroll
-            for (int k = 0; k < 12; k++) {
-                const uint32_t i = i0 + j + 64 * k;
-                v[k] = make_uint4(0, 0, 0, 0);
-                if (i < nv) {
-                    if (gs + 16ull * (i + 1) <= data_len) v[k] = gsrc[i];
-                    else v[k] = load_tail16(data, gs + 16ull * i, data_len);  // holds the data's end
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < 12; k++) {
-                const uint32_t i = i0 + j + 64 * k;
-                if (i < nv) sdst[i] = v[k];
-            }
-        }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
+    const uint32_t j = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     constexpr int FL = SPE == 2 ? 2 : 1;  // first live lane of a column
-    uint32_t x[2], p[2], e[2];
-    uint32_t nbad = 0;
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int b = i == 0 ? FL : 3;
-        const ckr_stream_header h = uh[4 * j + b];
-        x[i] = h.final_state;
-        const bool ok = (uint64_t)h.buf_offset + h.byte_count <= usize;
-        p[i] = ok ? shift + h.buf_offset : shift;
-        e[i] = ok ? shift + h.buf_offset + h.byte_count : shift;
-        nbad += ok ? 0u : 1u;
-    }
-    const uint64_t col = 4ull * j;
-    const uint32_t K = len > col ? (uint32_t)((len - col + 255) / 256) : 0u;
-    uint8_t* udst = dst + ubase;
-    // rows 0 .. K-2 are full 32-bit columns; row K-1 may be partial (bf16 tail)
-    const uint32_t Kf = K ? K - 1 : 0;
-    // sidecar of row k for this column: 16 bits at (ubase + 256k + 4j) / 2
-    const uint16_t* sc16 = reinterpret_cast<const uint16_t*>(sidecar + (ubase >> 1) + 2 * j);
-    uint32_t* out32 = reinterpret_cast<uint32_t*>(udst + col);
-    uint32_t sa[32], sb[32];
-    auto load_sc = [&](uint32_t (&sc)[32], uint32_t k0) {
-#pragma unroll
-        for (int r = 0; r < 32; r++) sc[r] = (k0 + r < Kf) ? (uint32_t)sc16[64 * (k0 + r)] : 0u;
-    };
-    auto decode_rows = [&](const uint32_t (&sc)[32], uint32_t k0) {
-#pragma unroll
-        for (int r = 0; r < 32; r++) {
-            if (k0 + r >= Kf) break;
-            const uint32_t s0 = decode_live_sym<SPE>(x[0], p[0], e[0], stage, tab);
-            const uint32_t s1 = decode_live_sym<SPE>(x[1], p[1], e[1], stage, tab);
-            const uint32_t side = SPE == 2 ? sc[r] : ((sc[r] & 0xFFu) | ((sc[r] & 0xFF00u) << 8));
-            out32[64 * (k0 + r)] = (SPE == 2 ? (s0 << 16) : (s0 << 8)) | (s1 << 24) | side;
+    const uint64_t data_len = unit_off[g.n_units];
+    const uintptr_t d0 = reinterpret_cast<uintptr_t>(data), d1 = d0 + data_len;
+    const uint32_t* cbytes = canon + 3 * (4 + cw);  // canonical streams in byte order, cw dwords each
+    const uint32_t tb0 = DF_TAB_BYTES + wv * DF_WAVE_BYTES + 4 * j;
+    unsigned long long nbad_total = 0;
+
+    for (uint64_t u = (uint64_t)blockIdx.x * DF_WAVES + wv; u < g.n_units; u += (uint64_t)gridDim.x * DF_WAVES) {
+        const uint64_t ubase = u * g.unit;
+        const uint32_t len = unit_len(g, ubase);
+        const uint64_t uoff = unit_off[u];
+        const uint8_t* ud = data + uoff;
+        const uint32_t usize = (uint32_t)(unit_off[u + 1] - uoff);
+        const ckr_stream_header* uh = hdrs + u * 256;
+        if (usize == len && uh[0].byte_count == len) {
+            if (j == 0) unit_mask[u] = 0;
+            decode_raw_unit<SPE>(ud, ubase, len, j, sidecar, dst);
+            continue;
         }
-    };
-    uint32_t k0 = 0;
-    if (Kf) load_sc(sa, 0);
-    while (k0 < Kf) {
-        if (k0 + 32 < Kf) load_sc(sb, k0 + 32);
-        decode_rows(sa, k0);
-        k0 += 32;
-        if (k0 >= Kf) break;
-        if (k0 + 32 < Kf) load_sc(sa, k0 + 32);
-        decode_rows(sb, k0);
-        k0 += 32;
-    }
-    if (K) {  // last row
-        const uint32_t pos = 256 * Kf + (uint32_t)col;
-        const uint32_t nvalid = (len - pos) < 4 ? (len - pos) : 4;
-        const uint32_t s0 = decode_live_sym<SPE>(x[0], p[0], e[0], stage, tab);
-        uint32_t s1 = 0;
-        if (nvalid == 4) s1 = decode_live_sym<SPE>(x[1], p[1], e[1], stage, tab);
-        const uint32_t v = merge_sidecar_row<SPE>(sidecar, ubase + pos, (SPE == 2 ? (s0 << 16) : (s0 << 8)) | (s1 << 24), nvalid);
-        if (nvalid == 4) *reinterpret_cast<uint32_t*>(udst + pos) = v;
-        else for (uint32_t b = 0; b < nvalid; b++) udst[pos + b] = (uint8_t)(v >> (8 * b));
-    }
-#pragma unroll
-    for (int i = 0; i < 2; i++) nbad += (x[i] != L || p[i] != e[i]) ? 1u : 0u;
-    // zero-plane lanes: header and bytes must be the canonical stream
-#pragma unroll
-    for (int b = 0; b < 4; b++) {
-        if (lane_is_live<SPE>(b)) continue;
-        const uint64_t pb = col + b;
-        const uint32_t Kb = (uint32_t)(len > pb ? (len - pb + 255) / 256 : 0);
-        const uint32_t* ce = canon_entry(can, cw, Kb);
-        const ckr_stream_header h = uh[4 * j + b];
-        bool ok = h.final_state == ce[1] && h.byte_count == ce[2] &&
-                  (uint64_t)h.buf_offset + h.byte_count <= usize;
-        if (ok) {
-            const uint8_t* cb = reinterpret_cast<const uint8_t*>(ce + 4);
-            const uint8_t* sl = stage + shift + h.buf_offset;
-            uint32_t diff = 0;
-            for (uint32_t q = 0; q < h.byte_count; q++) diff |= sl[q] ^ cb[q];
-            ok = diff == 0;
+        // chunks are read from the unit's 64-byte aligned base up to 2 chunks past
+        // the unit's end (valid streams); the rest are clamped to lim_ch
+        const uintptr_t ua = reinterpret_cast<uintptr_t>(ud) & ~(uintptr_t)63;
+        const uint32_t g0 = (uint32_t)(reinterpret_cast<uintptr_t>(ud) - ua);
+        if ((len & 255u) || ua < d0 || ua + (((uintptr_t)(g0 + usize) >> 6) + 3) * 64 > d1) {
+            if (j == 0) unit_mask[u] = 1;
+            continue;
         }
-        nbad += ok ? 0u : 1u;
+        if (j == 0) unit_mask[u] = 0;
+        const uint8_t* uab = data + (ua - d0);
+        const uint32_t lim_ch = (uint32_t)min<uintptr_t>((d1 - ua) >> 6, 0x01000000u) - 1u;
+        uint32_t nbad = 0;
+        DfLane da, db;
+        uint32_t gea8, geb8;
+        {
+            auto init = [&](DfLane& d, uint32_t& ge8, int b) __attribute__((always_inline)) {
+                const ckr_stream_header h = uh[4 * j + b];
+                const bool ok = (uint64_t)h.buf_offset + h.byte_count <= usize;
+                nbad += ok ? 0u : 1u;
+                const uint32_t p = g0 + (ok ? h.buf_offset : 0u);
+                d.x = h.final_state;
+                d.p8 = p << 3;
+                ge8 = (p + (ok ? h.byte_count : 0u)) << 3;
+                d.ch = p >> 6;
+                d.pend = false;
+            };
+            init(da, gea8, FL);
+            init(db, geb8, 3);
+            da.tb = tb0;
+            db.tb = tb0 + DF_RING_BYTES;
+            uint4 a0, a1, a2, a3, a4, a5, a6, a7, b0, b1, b2, b3, b4, b5, b6, b7;
+            df_fetch(uab, min(da.ch, lim_ch), a0, a1, a2, a3);
+            df_fetch(uab, min(da.ch + 1u, lim_ch), a4, a5, a6, a7);
+            df_fetch(uab, min(db.ch, lim_ch), b0, b1, b2, b3);
+            df_fetch(uab, min(db.ch + 1u, lim_ch), b4, b5, b6, b7);
+            df_put(lds8, da.tb, da.ch, a0, a1, a2, a3);
+            df_put(lds8, da.tb, da.ch + 1u, a4, a5, a6, a7);
+            df_put(lds8, db.tb, db.ch, b0, b1, b2, b3);
+            df_put(lds8, db.tb, db.ch + 1u, b4, b5, b6, b7);
+        }
+        const uint32_t K = len >> 8;  // rows (every column has K, all full)
+        // sidecar of row k for this column: 16 bits at (ubase + 256k + 4j) / 2, read
+        // as the aligned dword around them (sidecar is 16-byte aligned, ubase a
+        // multiple of 256)
+        const uint32_t* sc32 = reinterpret_cast<const uint32_t*>(sidecar + (ubase >> 1) + 4 * (j >> 1));
+        const uint32_t sel = df_sel<SPE>(2 * (j & 1));
+        uint32_t* out32 = reinterpret_cast<uint32_t*>(dst + ubase + 4 * j);
+        // rows in groups of 8 (one window step); the next group's sidecar is in
+        // flight while the current group is decoded.  Full groups have no row
+        // guards and their loads are unconditional (the waits stay exact).
+        const uint32_t ng = K >> 3;  // full groups
+        if (ng) {
+            // two groups per iteration with no exit in between (fixed buffer roles,
+            // exact waits); the last one or two groups after the loop
+            uint32_t sa[8], sb[8];
+            uint32_t gi = 0;
+            df_load_sc(sa, sc32);
+            for (; gi + 2 < ng; gi += 2) {
+                df_load_sc(sb, sc32 + 256 * (gi + 1));
+                df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, uab, lim_ch);
+                df_load_sc(sa, sc32 + 256 * (gi + 2));
+                df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 1), sb, sel, uab, lim_ch);
+            }
+            if (gi + 1 < ng) {
+                df_load_sc(sb, sc32 + 256 * (gi + 1));
+                df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, uab, lim_ch);
+                df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 1), sb, sel, uab, lim_ch);
+            } else {
+                df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, uab, lim_ch);
+            }
+        }
+        // at most 7 rows left: no window step needed
+        uint32_t k = 8 * ng;
+        for (; k + 2 <= K; k += 2) df_pair<SPE>(da, db, lds8, tab, out32 + 64 * k, sc32[32 * k], sc32[32 * (k + 1)], sel);
+        if (k < K) {
+            uint32_t wa = df_window(da, lds8), wb = df_window(db, lds8);
+            uint32_t ha, hb;
+            const uint32_t a0 = df_sym(da.x, wa, ha, tab);
+            const uint32_t b0 = df_sym(db.x, wb, hb, tab);
+            out32[64 * k] = df_pack<SPE>(a0, b0, sc32[32 * k], sel);
+            da.p8 += ha;
+            db.p8 += hb;
+        }
+        nbad += (da.x != L || da.p8 != gea8) ? 1u : 0u;
+        nbad += (db.x != L || db.p8 != geb8) ? 1u : 0u;
+        // zero-plane lanes: header and bytes must be the canonical stream
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            if (lane_is_live<SPE>(b)) continue;
+            const uint32_t ent = (canon[0] == K) ? 0u : ((canon[4 + cw] == K) ? 1u : 2u);
+            const uint32_t* ce = canon + ent * (4 + cw);
+            const ckr_stream_header h = uh[4 * j + b];
+            bool ok = h.final_state == ce[1] && h.byte_count == ce[2] && (uint64_t)h.buf_offset + h.byte_count <= usize;
+            if (ok) {
+                const uint8_t* cb = reinterpret_cast<const uint8_t*>(cbytes + (uint64_t)ent * cw);
+                const uint8_t* sl = ud + h.buf_offset;
+                uint32_t diff = 0;
+                uint32_t q = 0;
+                // stream dwords (any alignment, from the aligned dwords around them,
+                // which lie in the data buffer) against the canonical dwords
+                for (; q + 4 <= h.byte_count; q += 4) {
+                    const uintptr_t a = reinterpret_cast<uintptr_t>(sl + q);
+                    const uintptr_t aa = a & ~(uintptr_t)3;
+                    if (aa < d0 || aa + 8 > d1) break;  // the rest byte by byte
+                    const uint32_t* ap = data32_at(data, aa - d0);
+                    const uint32_t sh = (uint32_t)(a & 3u);
+                    diff |= __builtin_amdgcn_alignbyte(ap[1], ap[0], sh) ^ *reinterpret_cast<const uint32_t*>(cb + q);
+                }
+                for (; q < h.byte_count; q++) diff |= sl[q] ^ cb[q];
+                ok = diff == 0;
+            }
+            nbad += ok ? 0u : 1u;
+        }
+        nbad_total += nbad;
     }
-    if (nbad) atomicAdd(bad, (unsigned long long)nbad);
+    if (nbad_total) atomicAdd(bad, nbad_total);
 }
 
 hipError_t launch_build_enc_table(const TableArg& t, EncSym* d_enc, hipStream_t s) {
@@ -1606,8 +1702,7 @@ hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, hipStream_
     return hipGetLastError();
 }
 
-uint32_t decode_fast_lds_bytes() { return (4096 + FAST_CANON_DWORDS) * 4 + 4 * (FAST_STAGE_BYTES + 32); }
-uint32_t decode_fast_max_cw() { return 130; }
+uint32_t decode_fast_lds_bytes() { return DF_TAB_BYTES + DF_WAVES * DF_WAVE_BYTES; }
 
 hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
                          const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
@@ -1616,20 +1711,29 @@ hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, con
     const uint32_t grid = (uint32_t)((g.n_units + 3) / 4);
     if (grid == 0) return hipSuccess;
     hipError_t e;
+    bool fast_ran = false;
     if (canon && unit_mask && g.spe > 0) {  // fast path, then the general kernel for the units it left
         const uint32_t lb = decode_fast_lds_bytes();
-        if (g.spe == 2) {
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_fast_kernel<2>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);
-            CKR_LAUNCH("decode_fast_kernel", s, decode_fast_kernel<2><<<grid, 256, lb, s>>>(data, hdrs, unit_off, d_dec, canon, cw, g, sidecar, dst, bad, unit_mask));
-        } else {
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_fast_kernel<1>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);
-            CKR_LAUNCH("decode_fast_kernel", s, decode_fast_kernel<1><<<grid, 256, lb, s>>>(data, hdrs, unit_off, d_dec, canon, cw, g, sidecar, dst, bad, unit_mask));
-        }
-        if ((e = hipGetLastError()) != hipSuccess) return e;
+        int dev = 0, ncu = 0;
+        if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+        if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+        auto fast = [&](auto kern) -> hipError_t {
+            int per_cu = 0;
+            if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb) != hipSuccess ||
+                hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * DF_WAVES, lb) != hipSuccess || per_cu < 1) {
+                (void)hipGetLastError();
+                return hipSuccess;  // LDS too small on this device: the general kernel takes every unit
+            }
+            // persistent: the blocks that fit at once, never more than needed
+            const uint64_t need = (g.n_units + DF_WAVES - 1) / DF_WAVES;
+            const uint32_t fg = (uint32_t)std::min<uint64_t>(need, (uint64_t)per_cu * (uint64_t)std::max(ncu, 1));
+            CKR_LAUNCH("decode_fast_kernel", s, kern<<<fg, 64 * DF_WAVES, lb, s>>>(data, hdrs, unit_off, d_dec, canon, cw, g, sidecar, dst, bad, unit_mask));
+            fast_ran = true;
+            return hipGetLastError();
+        };
+        if ((e = (g.spe == 2 ? fast(decode_fast_kernel<2>) : fast(decode_fast_kernel<1>))) != hipSuccess) return e;
     }
-    const uint32_t* mask = (canon && unit_mask && g.spe > 0) ? unit_mask : nullptr;
+    const uint32_t* mask = fast_ran ? unit_mask : nullptr;
     if (g.spe == 2) CKR_LAUNCH("decode_kernel", s, decode_kernel<2><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad, mask));
     else if (g.spe == 1) CKR_LAUNCH("decode_kernel", s, decode_kernel<1><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad, mask));
     else CKR_LAUNCH("decode_kernel", s, decode_kernel<0><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad, mask));
