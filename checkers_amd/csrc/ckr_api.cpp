@@ -191,9 +191,9 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     return L;
 }
 
-// Decode workspace: enc table, canonical streams, decode table, bad-lane counter, unit mask.
+// Decode workspace: enc table, canonical streams, decode table, bad-lane counter.
 struct DecodeLayout {
-    uint64_t off_enc, off_canon, off_dec, off_bad, off_mask, total;
+    uint64_t off_enc, off_canon, off_dec, off_bad, total;
     bool fast;
 };
 DecodeLayout decode_layout(const ckr::EncodeGeom& g) {
@@ -205,7 +205,6 @@ DecodeLayout decode_layout(const ckr::EncodeGeom& g) {
     L.off_canon = o; o = align_up(o + (L.fast ? 3ull * (4 + 2 * ck.cw) * 4 : 0), kAlign);
     L.off_dec = o;   o = align_up(o + 4096 * 4, kAlign);
     L.off_bad = o;   o = align_up(o + 8, kAlign);
-    L.off_mask = o;  o = align_up(o + (L.fast ? g.n_units * 4 : 0), kAlign);
     L.total = o;
     return L;
 }
@@ -290,9 +289,9 @@ int ckr_profile_end(char* buf, uint64_t buflen) {
         (void)hipEventDestroy(r.a);
     }
     g_prof.clear();
-    // fast-encode phases: mean per unit (us) of ticket, coding (with the lane
-    // sums), look-back, the barrier before packing, packing (thread 0), the
-    // closing barrier, and the chunks thread 0 packed
+    // fast-encode phases: mean per unit (us) of the coders' wait for a free set,
+    // coding, the hand-over to the packers, look-back, packing (thread 0), the
+    // packers' closing barrier, and the chunks thread 0 packed
     {
         constexpr int NS = 8;
         double sum[6] = {0, 0, 0, 0, 0, 0}, life = 0, chunks = 0;
@@ -307,7 +306,7 @@ int ckr_profile_end(char* buf, uint64_t buflen) {
                     if (!t[6]) continue;  // unit not stamped
                     for (int k = 0; k < 6; k++) sum[k] += t[k + 1] >= t[k] ? (double)(t[k + 1] - t[k]) * 0.01 : 0.0;
                     code_t.push_back(t[2] >= t[1] ? (float)(t[2] - t[1]) * 0.01f : 0.f);
-                    look_t.push_back(t[3] >= t[2] ? (float)(t[3] - t[2]) * 0.01f : 0.f);
+                    look_t.push_back(t[4] >= t[3] ? (float)(t[4] - t[3]) * 0.01f : 0.f);
                     life += (double)(t[6] - t[0]) * 0.01;
                     chunks += (double)t[7];
                     units++;
@@ -317,9 +316,9 @@ int ckr_profile_end(char* buf, uint64_t buflen) {
         }
         g_phase.clear();
         if (units) {
-            const char* nm[6] = {"encode_fast.phase_ticket_us", "encode_fast.phase_code_us",
-                                 "encode_fast.phase_lookback_us", "encode_fast.phase_barrier_us",
-                                 "encode_fast.phase_pack_us", "encode_fast.phase_end_barrier_us"};
+            const char* nm[6] = {"encode_fast.phase_setwait_us", "encode_fast.phase_code_us",
+                                 "encode_fast.phase_handoff_us", "encode_fast.phase_lookback_us",
+                                 "encode_fast.phase_pack_us", "encode_fast.phase_release_us"};
             for (int k = 0; k < 6; k++) agg[nm[k]] = {units, sum[k] / 1000.0};
             agg["encode_fast.unit_lifetime_us"] = {units, life / 1000.0};
             agg["encode_fast.thread0_chunks"] = {units, chunks / 1000.0};
@@ -541,16 +540,15 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
             fp.sl0 = lane_slot_bytes(h_planes, h_table, K);
             fp.sl1 = lane_slot_bytes(h_planes ? h_planes + 256 : nullptr, h_table, K);
         }
-        // the lane tables hold LDS addresses in 16 bits
-        const uint32_t lds = ckr::encode_fast_lds_bytes(fp);
-        fast = (int)lds <= max_lds_per_block() && lds <= 65536u;
+        fast = ckr::encode_fast_lds_bytes(fp, (uint32_t)max_lds_per_block()) != 0;
     }
     if (fast) {
         auto* status = reinterpret_cast<uint64_t*>(ws + L.off_status);
         auto* ctl = reinterpret_cast<uint32_t*>(ws + L.off_ctl);
         auto* redo = reinterpret_cast<uint32_t*>(ws + L.off_redo);
-        CKR_HIP(ckr::launch_encode_fast(static_cast<const uint8_t*>(d_src), g, enc, canon, fp, d_headers, side, d_out,
-                                        d_unit_offsets, status, ctl, redo, s));
+        CKR_HIP(ckr::launch_encode_fast(static_cast<const uint8_t*>(d_src), g, enc, canon, fp,
+                                        (uint32_t)max_lds_per_block(), d_headers, side, d_out, d_unit_offsets, status,
+                                        ctl, redo, s));
         uint32_t hctl[4];
         CKR_HIP(hipMemcpyAsync(hctl, ctl, sizeof(hctl), hipMemcpyDeviceToHost, s));
         CKR_HIP(hipStreamSynchronize(s));
@@ -648,7 +646,6 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
     auto* canon = reinterpret_cast<uint32_t*>(ws + L.off_canon);
     auto* dec = reinterpret_cast<uint32_t*>(ws + L.off_dec);
     auto* bad = reinterpret_cast<unsigned long long*>(ws + L.off_bad);
-    auto* mask = reinterpret_cast<uint32_t*>(ws + L.off_mask);
     const CanonKs ck = canon_ks(g);
     CKR_HIP(ckr::launch_build_dec_table(ta, dec, s));
     if (L.fast) {
@@ -657,7 +654,7 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
     }
     CKR_HIP(ckr::launch_set_counter(bad, 0, s));
     CKR_HIP(ckr::launch_decode(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, static_cast<uint8_t*>(d_dst),
-                               bad, L.fast ? canon : nullptr, ck.cw, L.fast ? mask : nullptr, s));
+                               bad, L.fast ? canon : nullptr, ck.cw, s));
     if (h_bad_lanes) {
         unsigned long long nb = 0;
         CKR_HIP(hipMemcpyAsync(&nb, bad, 8, hipMemcpyDeviceToHost, s));

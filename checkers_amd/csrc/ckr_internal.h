@@ -87,13 +87,14 @@ struct FastEncParamsHost {
     uint32_t sl0, sl1, cw, canon_bytes;
     bool escapes;  // the data may hold symbols with f == 0 (table not built from it)
 };
-uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p);
+// LDS bytes of the fast encoder's workgroup within lds_limit (0: it does not fit).
+uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p, uint32_t lds_limit);
 // u64 look-back words of the fast encoder for n units (status argument size).
 uint64_t encode_fast_status_words(uint64_t n_units);
 hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
-                              const FastEncParamsHost& hp, ckr_stream_header* hdrs, uint8_t* sidecar, uint8_t* out,
-                              uint64_t* unit_off, uint64_t* status, uint32_t* ctl, uint32_t* redo_list,
-                              hipStream_t s);
+                              const FastEncParamsHost& hp, uint32_t lds_limit, ckr_stream_header* hdrs,
+                              uint8_t* sidecar, uint8_t* out, uint64_t* unit_off, uint64_t* status, uint32_t* ctl,
+                              uint32_t* redo_list, hipStream_t s);
 
 // Canonical zero-plane streams for lane counts k0, k1, k2: 3 entries of 4 + cw
 // dwords (header, then the stream in slot format), followed by the 3 streams in
@@ -101,14 +102,12 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
 hipError_t launch_canon(const EncSym* d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw, uint32_t* canon,
                         hipStream_t s);
 
-// Decode; with canon and unit_mask (n_units u32) the fast kernel runs first for
-// the units of masked dtypes whose length is a multiple of 256 (and raw units),
-// and the general kernel takes the units it left.
+// Decode; with canon (masked dtypes) the fast kernel decodes every unit,
+// otherwise the general kernel does.
 uint32_t decode_fast_lds_bytes();
 hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
                          const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
-                         unsigned long long* bad, const uint32_t* canon, uint32_t cw, uint32_t* unit_mask,
-                         hipStream_t s);
+                         unsigned long long* bad, const uint32_t* canon, uint32_t cw, hipStream_t s);
 
 // Analyzer.
 struct StatsParams {     // per record, device resident between passes

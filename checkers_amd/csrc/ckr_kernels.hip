@@ -304,37 +304,54 @@ __device__ __forceinline__ uint32_t lane_bytes(const LaneOut& o) { return o.w * 
 // and the table: it is coded once per distinct K (at most three per tensor:
 // full units, and the two lane counts of the last unit) instead of once per
 // lane.  Entry i: {K, final_state, byte_count, pad} then cw dword slots.
-__global__ void canon_kernel(const EncSym* __restrict__ d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw,
-                             uint32_t* __restrict__ canon) {
+// Wave i codes entry i into LDS (K <= CANON_MAX_K) with wave-uniform values,
+// so the serial state chain runs on the scalar unit; the block then writes the
+// slots and the byte-order copies out together.
+static constexpr uint32_t CANON_MAX_K = 4096;
+static constexpr uint32_t CANON_MAX_CW = (2 * CANON_MAX_K + 3) / 4 + 1;
+
+__global__ void __launch_bounds__(256) canon_kernel(const EncSym* __restrict__ d_enc, uint32_t k0, uint32_t k1,
+                                                    uint32_t k2, uint32_t cw, uint32_t* __restrict__ canon) {
+    __shared__ uint32_t slots[3][CANON_MAX_CW];
+    __shared__ uint32_t meta[3][2];  // final state, byte count
     const uint32_t t = threadIdx.x;
-    __shared__ EncSym e0[1];
-    if (t == 0) e0[0] = d_enc[0];
-    __syncthreads();
-    if (t >= 3) return;
-    const uint32_t K = t == 0 ? k0 : (t == 1 ? k1 : k2);
-    uint32_t* base = canon + (uint64_t)t * (4 + cw);
-    LaneOut o;
-    lane_init(o);
-    for (uint32_t k = 0; k < K; k++) encode_symbol<1>(o, 0u, e0, base + 4);
-    lane_flush<1>(o, base + 4);
-    base[0] = K;
-    base[1] = o.x;
-    base[2] = lane_bytes(o);
-    base[3] = 0;
-    // the same stream in byte order (cw dwords per entry after the three entries)
-    uint32_t* sb = canon + 3ull * (4 + cw) + (uint64_t)t * cw;
-    const uint32_t B = lane_bytes(o), W = B >> 2, r = B & 3;
-    for (uint32_t d = 0; d < cw; d++) {
-        uint32_t v = 0;
-        for (uint32_t b = 0; b < 4; b++) {
-            const uint32_t q = 4 * d + b;
-            if (q >= B) break;
-            uint32_t slot, byte;
-            if (q < r) { slot = W; byte = q; }
-            else { slot = W - 1 - ((q - r) >> 2); byte = (q - r) & 3; }
-            v |= ((base[4 + slot] >> (8 * byte)) & 255u) << (8 * b);
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    if (wv < 3) {
+        const EncSym e0 = d_enc[0];  // every symbol is 0: its entry stays in registers
+        const uint32_t K = __builtin_amdgcn_readfirstlane(wv == 0 ? k0 : (wv == 1 ? k1 : k2));
+        LaneOut o;
+        lane_init(o);
+        for (uint32_t k = 0; k < K; k++) encode_symbol<1>(o, 0u, &e0, slots[wv]);
+        lane_flush<1>(o, slots[wv]);
+        if ((t & 63) == 0) {
+            meta[wv][0] = o.x;
+            meta[wv][1] = lane_bytes(o);
         }
-        sb[d] = v;
+    }
+    __syncthreads();
+    for (uint32_t e = 0; e < 3; e++) {
+        uint32_t* base = canon + (uint64_t)e * (4 + cw);
+        uint32_t* sb = canon + 3ull * (4 + cw) + (uint64_t)e * cw;  // the stream in byte order
+        const uint32_t B = meta[e][1], W = B >> 2, r = B & 3;
+        if (t == 0) {
+            base[0] = e == 0 ? k0 : (e == 1 ? k1 : k2);
+            base[1] = meta[e][0];
+            base[2] = B;
+            base[3] = 0;
+        }
+        for (uint32_t d = t; d < cw; d += blockDim.x) {
+            base[4 + d] = (d < W || (d == W && r)) ? slots[e][d] : 0u;
+            uint32_t v = 0;
+            for (uint32_t b = 0; b < 4; b++) {
+                const uint32_t q = 4 * d + b;
+                if (q >= B) break;
+                uint32_t slot, byte;
+                if (q < r) { slot = W; byte = q; }
+                else { slot = W - 1 - ((q - r) >> 2); byte = (q - r) & 3; }
+                v |= ((slots[e][slot] >> (8 * byte)) & 255u) << (8 * b);
+            }
+            sb[d] = v;
+        }
     }
 }
 
@@ -599,7 +616,8 @@ __global__ void __launch_bounds__(256) compact_kernel(const uint8_t* __restrict_
 
 hipError_t launch_canon(const EncSym* d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw, uint32_t* canon,
                         hipStream_t s) {
-    CKR_LAUNCH("canon_kernel", s, canon_kernel<<<1, 64, 0, s>>>(d_enc, k0, k1, k2, cw, canon));
+    if (cw > CANON_MAX_CW || k0 > CANON_MAX_K || k1 > CANON_MAX_K || k2 > CANON_MAX_K) return hipErrorInvalidValue;
+    CKR_LAUNCH("canon_kernel", s, canon_kernel<<<1, 256, 0, s>>>(d_enc, k0, k1, k2, cw, canon));
     return hipGetLastError();
 }
 
@@ -636,9 +654,9 @@ hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t
 }
 
 // ------------------------------------------------------------------ fast encode (LDS-staged, look-back)
-// Units of at most 64 KiB of masked dtypes.  One wave per unit (taken in order
-// from a ticket counter), one thread per 32-bit column, coding only the two
-// live lanes of its column.  Each live lane writes its stream backward into its
+// Units of at most 64 KiB of masked dtypes, taken in order from a ticket
+// counter; one thread per 32-bit column, coding only the two live lanes of its
+// column (one coder wave per live plane).  Each live lane writes its stream backward into its
 // own LDS slot, so that the stream ends up contiguous and in stream order; the
 // slot stride is chosen so that the 64 threads writing their e-th bytes hit
 // different banks.  The zero-plane lanes are the canonical streams.  When the
@@ -657,22 +675,6 @@ struct FastEncParams {
     uint32_t cw;                // canonical entry size (dwords after the 4 header words)
     uint32_t canon_bytes;       // bytes per canonical entry in the LDS copy (stream order)
 };
-
-// LDS layout (bytes): lane tables | rank-0 slots 64 x stride0 | rank-1 slots
-// 64 x stride1 | table 256 x 16 (see enc_quad) | canonical headers 12 x u32 |
-// canonical bytes 3 x canon_bytes | 32 bytes of read padding.  The lane tables
-// (lane offsets and LDS stream starts, 16 bits each, the waves' chain counts
-// and states, unit-wide values) are only written after every lane is coded, so
-// the region doubles as the guard under the slots: a lane's dwords are flushed
-// downward from the end of its slot, and a lane that outgrows its slot keeps
-// flushing into the slots below it (lanes of the same unit, whose bytes are
-// then redone by the general kernels) and, for the lowest slot, into the lane
-// tables (at most 2 bytes per symbol, 256 symbols: 516 bytes), so the table
-// and the canonical headers, which the unit's sizes depend on, are never
-// overwritten.
-static constexpr uint32_t FE_LOFF = 0, FE_SA = 520, FE_XCH = 1032, FE_BCAST = 1800, FE_META = 1824;
-static constexpr uint32_t FE_TABSZ = 4096, FE_CHDR_REL = FE_TABSZ, FE_CBYTES_REL = FE_TABSZ + 48;
-static_assert(FE_META >= 516 && FE_META % 16 == 0, "lane tables: guard size and table alignment");
 
 // Encode table entry in LDS, 16 bytes, every field ready for its instruction
 // (one ds_read_b128 per symbol): x = rcp; y = cmpl | rsh << 24 (the 24-bit
@@ -937,133 +939,203 @@ __device__ __forceinline__ void enc_full_rows(EncLane& c0, EncLane& c1, const ui
     }
 }
 
-static constexpr int kFastEncWaves = 2;  // waves per unit of the fast encoder (1 or 2)
+// Warp-specialised persistent workgroups, one per CU: WS pairs of (2 coder
+// waves, 2 packer waves), each pair with two LDS slot sets used in turn.  The
+// coder waves of a pair (byte FL and byte 3 of every column) take a unit from
+// the ticket counter, code it into the free set and hand it over; the packer
+// waves compute its lane sizes, publish its size, run the look-back, write its
+// headers and packed bytes, and give the set back.  Coding therefore never
+// waits for the look-back; it waits only while both sets of its pair are in
+// the packers' hands.  Hand-overs are workgroup-scope LDS counters (a release
+// fence, then one lane's atomic add, on the producer side; acquire polls with
+// s_sleep on the consumer side).
+//
+// LDS layout (bytes): table 256 x 16 (see enc_quad) | canonical headers 12 x
+// u32 | canonical bytes 3 x canon_bytes | pair control blocks | 2 x WS regions
+// | 32 bytes of read padding.  A region holds one set: the packers' lane
+// tables (lane offsets in the unit, u16, and LDS stream starts, u32), then the
+// rank-0 slots (64 x stride0) and the rank-1 slots (64 x stride1).  The lane
+// tables are only written once both coders are done with the set, so they
+// double as the guard under the slots: a lane's dwords are flushed downward
+// from the end of its slot, and a lane that outgrows its slot keeps flushing
+// into the slots below it (lanes of the same unit, whose bytes are then redone
+// by the general kernels) and, for the lowest slot, into the lane tables (at
+// most 2 bytes per symbol, 256 symbols: 516 bytes), never out of its region.
+static constexpr uint32_t FE_TABSZ = 4096, FE_CHDR = FE_TABSZ, FE_CBYTES = FE_TABSZ + 48;
+static constexpr uint32_t R_LOFF = 0, R_SA = 520, R_SLOTS = 1544;
+static_assert(R_SLOTS >= 516 && R_SLOTS % 4 == 0 && R_SA >= 257 * 2, "region: lane tables and guard under the slots");
 
-// Persistent: each workgroup stages the table and the canonical streams once,
-// then takes units from the ticket counter until none is left.  NW = 1: one
-// wave per unit, each thread codes both live lanes of its column.  NW = 2: wave
-// 0 codes byte FL of every column, wave 1 byte 3; both waves compute the
-// unit's lane sizes, wave 0 runs the look-back while wave 1 writes the headers
-// and the packer's lane tables, and both waves pack.
-template <int SPE, bool ESC, bool SIDE, int NW>
-__global__ void __launch_bounds__(64 * NW) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
-                                                          const EncSym* __restrict__ d_enc,
-                                                          const uint32_t* __restrict__ canon, FastEncParams fp,
-                                                          ckr_stream_header* __restrict__ hdrs,
-                                                          uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out,
-                                                          uint64_t* __restrict__ unit_off,
-                                                          uint64_t* __restrict__ status, uint32_t* __restrict__ ctl,
-                                                          uint32_t* __restrict__ redo_list,
-                                                          uint64_t* __restrict__ phase) {
+struct WsPairCtl {
+    uint32_t unit[2];         // unit in set s (>= n_units: none left, the pair stops)
+    uint32_t coded[2];        // +1 by each coder wave per use of set s
+    uint32_t freed[2];        // +1 by the packers per use of set s
+    uint32_t tick;            // uses started by the plane-FL coder (unit published)
+    uint32_t pbar;            // barrier count of the two packer waves
+    uint32_t off[2][2];       // packed offset of the unit in set s (lo, hi)
+    uint32_t pad[4];
+    uint32_t xch[2][4][64];   // per set and column: count FL, state FL, count 3, state 3
+};
+static_assert(sizeof(WsPairCtl) % 16 == 0, "control block alignment");
+
+__device__ __forceinline__ uint32_t ws_load(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void ws_wait_ge(const uint32_t* p, uint32_t v) {
+    while (ws_load(p) < v) __builtin_amdgcn_s_sleep(1);
+}
+// Makes the wave's earlier LDS (and global) writes visible in the workgroup,
+// then adds v to *p once for the wave.
+__device__ __forceinline__ void ws_signal(uint32_t* p, uint32_t v, uint32_t lane) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (lane == 0) (void)__hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__host__ __device__ constexpr uint32_t ws_ctl_offset(uint32_t canon_bytes) {
+    return (FE_CBYTES + 3 * canon_bytes + 15u) & ~15u;
+}
+__host__ __device__ constexpr uint32_t ws_region_bytes(uint32_t stride0, uint32_t stride1) {
+    return (R_SLOTS + 64 * stride0 + 64 * stride1 + 15u) & ~15u;
+}
+__host__ __device__ constexpr uint32_t ws_lds_bytes(uint32_t pairs, uint32_t canon_bytes, uint32_t stride0,
+                                                    uint32_t stride1) {
+    return ws_ctl_offset(canon_bytes) + pairs * (uint32_t)sizeof(WsPairCtl) +
+           2 * pairs * ws_region_bytes(stride0, stride1) + 32;
+}
+
+template <int SPE, bool ESC, bool SIDE, int PAIRS>
+__global__ void __launch_bounds__(256 * PAIRS) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
+                                                                  const EncSym* __restrict__ d_enc,
+                                                                  const uint32_t* __restrict__ canon, FastEncParams fp,
+                                                                  ckr_stream_header* __restrict__ hdrs,
+                                                                  uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out,
+                                                                  uint64_t* __restrict__ unit_off,
+                                                                  uint64_t* __restrict__ status, uint32_t* __restrict__ ctl,
+                                                                  uint32_t* __restrict__ redo_list,
+                                                                  uint64_t* __restrict__ phase) {
     extern __shared__ uint32_t lds[];
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
-    const uint32_t st0_off = FE_META;
-    const uint32_t st1_off = st0_off + 64 * fp.stride0;
-    const uint32_t tb = st1_off + 64 * fp.stride1;  // table
-    const uint4* tab = reinterpret_cast<const uint4*>(lds8 + tb);
-    uint16_t* loff = reinterpret_cast<uint16_t*>(lds8 + FE_LOFF);  // lane offsets in the unit (257)
-    uint16_t* lsa = reinterpret_cast<uint16_t*>(lds8 + FE_SA);     // LDS stream starts (256)
-    uint32_t* xch = reinterpret_cast<uint32_t*>(lds8 + FE_XCH);    // byte FL: count, state | byte 3: count
-    uint32_t* bc = reinterpret_cast<uint32_t*>(lds8 + FE_BCAST);   // ticket, offset
-    uint32_t* chdr = reinterpret_cast<uint32_t*>(lds8 + tb + FE_CHDR_REL);
-    const uint32_t cb_off = tb + FE_CBYTES_REL;
+    constexpr uint32_t NT = 256 * PAIRS;
+    const uint4* tab = reinterpret_cast<const uint4*>(lds8 + 0);
+    uint32_t* chdr = reinterpret_cast<uint32_t*>(lds8 + FE_CHDR);
+    const uint32_t cb_off = FE_CBYTES;
+    const uint32_t ctl_off = ws_ctl_offset(fp.canon_bytes);
+    const uint32_t rbytes = ws_region_bytes(fp.stride0, fp.stride1);
+    const uint32_t reg0 = ctl_off + PAIRS * (uint32_t)sizeof(WsPairCtl);
     const uint32_t tid = threadIdx.x;
-    const uint32_t w = NW == 1 ? 0u : __builtin_amdgcn_readfirstlane(tid >> 6);  // NW = 2: 0 plane FL, 1 plane 3
-    constexpr uint32_t NT = 64 * NW;
-    const uint32_t j = tid & 63;                                  // column
+    const uint32_t j = tid & 63;  // column
     constexpr int FL = SPE == 2 ? 2 : 1;  // byte of the first live lane in a column
     const uint32_t lm = live_mask32<SPE>();
-    const uint32_t sh = w ? 24u : 8u * FL;  // this wave's byte of the column
 
-    {   // table (EncSym → EncPair), canonical headers and canonical streams (byte order), loads batched
+    {   // table (EncSym → enc_quad), canonical headers and canonical streams (byte order), control blocks
         const uint4* d_tab = reinterpret_cast<const uint4*>(d_enc);
-        uint4 tv[256 / NT];
-#pragma unroll
-        for (uint32_t k = 0; k < 256 / NT; k++) tv[k] = d_tab[tid + NT * k];
-        uint4* wt = reinterpret_cast<uint4*>(lds8 + tb);
-#pragma unroll
-        for (uint32_t k = 0; k < 256 / NT; k++) {
-            const EncSym e = {tv[k].x, tv[k].y, tv[k].z, tv[k].w};
-            wt[tid + NT * k] = enc_quad(e);
+        uint4* wt = reinterpret_cast<uint4*>(lds8 + 0);
+        for (uint32_t k = tid; k < 256; k += NT) {
+            const uint4 tv = d_tab[k];
+            const EncSym e = {tv.x, tv.y, tv.z, tv.w};
+            wt[k] = enc_quad(e);
         }
         const uint32_t* cs = canon + 3 * (4 + fp.cw);
         uint32_t* cb32 = reinterpret_cast<uint32_t*>(lds8 + cb_off);
         const uint32_t ncb = 3 * fp.canon_bytes / 4;
         const uint32_t cb_per = fp.canon_bytes / 4;
-        for (uint32_t i0 = 0; i0 < ncb; i0 += 512) {
-            uint32_t cv[512 / NT];
-#pragma unroll
-            for (uint32_t k = 0; k < 512 / NT; k++) {
-                const uint32_t i = i0 + tid + NT * k;
-                cv[k] = i < ncb ? cs[(i / cb_per) * fp.cw + (i % cb_per)] : 0u;
-            }
-#pragma unroll
-            for (uint32_t k = 0; k < 512 / NT; k++) { const uint32_t i = i0 + tid + NT * k; if (i < ncb) cb32[i] = cv[k]; }
-        }
+        for (uint32_t i = tid; i < ncb; i += NT) cb32[i] = cs[(i / cb_per) * fp.cw + (i % cb_per)];
         if (tid < 12) chdr[tid] = canon[(tid >> 2) * (4 + fp.cw) + (tid & 3)];
+        uint32_t* c32 = reinterpret_cast<uint32_t*>(lds8 + ctl_off);
+        for (uint32_t i = tid; i < PAIRS * (uint32_t)sizeof(WsPairCtl) / 4; i += NT) c32[i] = 0;
+    }
+    __syncthreads();
+
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // waves 0 .. 2 PAIRS - 1 code, the others pack (wave w runs on SIMD w mod 4,
+    // so every SIMD holds one coder and one packer)
+    const bool coder = wv < 2 * PAIRS;
+    const uint32_t pr = coder ? (wv >> 1) : ((wv - 2 * PAIRS) >> 1);  // pair
+    const uint32_t rl = wv & 1;  // coder: 0 byte FL, 1 byte 3; packer: 0 look-back, 1 headers
+    WsPairCtl& pc = *reinterpret_cast<WsPairCtl*>(lds8 + ctl_off + pr * (uint32_t)sizeof(WsPairCtl));
+    const uint32_t col = 4 * j;
+
+    if (coder) {
+        const uint32_t sh = rl ? 24u : 8u * FL;  // this wave's byte of the column
+        for (uint32_t i = 0;; i++) {
+            const uint32_t s = i & 1;
+            const uint64_t t_wait = phase ? wall_clock64() : 0;
+            if (i >= 2) ws_wait_ge(&pc.freed[s], i >> 1);  // set s given back
+            if (rl == 0) {
+                if (j == 0) pc.unit[s] = atomicAdd(&ctl[0], 1u);  // ticket
+                ws_signal(&pc.tick, 1u, j);
+            } else {
+                ws_wait_ge(&pc.tick, i + 1);
+            }
+            const uint32_t u = __builtin_amdgcn_readfirstlane(ws_load(&pc.unit[s]));
+            if (u >= g.n_units) {
+                ws_signal(&pc.coded[s], 1u, j);
+                break;
+            }
+            const uint64_t t_start = phase ? wall_clock64() : 0;
+            const uint64_t ubase = (uint64_t)u * g.unit;
+            const uint32_t len = (uint32_t)((g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit);
+            const uint8_t* usrc = src + ubase;
+            const uint32_t rb = reg0 + (2 * pr + s) * rbytes;
+            const uint32_t endw = rl ? rb + R_SLOTS + 64 * fp.stride0 + j * fp.stride1 + fp.sl1
+                                     : rb + R_SLOTS + j * fp.stride0 + fp.sl0;
+            EncLane c{L, 0u, 0u, 0x08090A0Bu, endw - 4u};
+            EncLane c_unused = c;
+            const uint32_t K = len > col ? (len - col + 255) / 256 : 0u;
+            if ((len & 255u) == 0) {
+                if (rl == 0) enc_full_rows<SPE, ESC, SIDE, 0>(c, c_unused, usrc + col, sidecar, ubase, j, len >> 8, tab, lds8);
+                else enc_full_rows<SPE, ESC, SIDE, 1>(c, c_unused, usrc + col, sidecar, ubase, j, len >> 8, tab, lds8);
+            } else {
+                // A tensor's last unit: rows from the top down, one at a time; the top
+                // row may be partial (bf16: lane 4j+3 has one symbol fewer).
+                for (int32_t k = (int32_t)K - 1; k >= 0; k--) {
+                    const uint32_t p = 256 * (uint32_t)k + col;
+                    const uint32_t nvalid = (len - p) < 4 ? (len - p) : 4;
+                    uint32_t v = 0;
+                    if (nvalid == 4) v = *reinterpret_cast<const uint32_t*>(usrc + p);
+                    else for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)usrc[p + b] << (8 * b);
+                    if (SIDE && (uint32_t)(k & 1) == rl) write_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
+                    v &= lm;
+                    const uint32_t sy = (v >> sh) & 255u;
+                    if (rl == 0 || nvalid == 4) enc_step<ESC>(c, sy, tab[sy]);
+                    if ((k & 1) == 0) enc_flush(c, lds8);
+                }
+            }
+            const uint32_t e = enc_finish(c, lds8, endw);
+            pc.xch[s][2 * rl][j] = e;
+            pc.xch[s][2 * rl + 1][j] = c.x;
+            ws_signal(&pc.coded[s], 1u, j);
+            if (phase && rl == 0 && j == 0) {
+                uint64_t* ph = phase + 8 * (uint64_t)u;
+                ph[0] = t_wait; ph[1] = t_start; ph[2] = wall_clock64();
+            }
+        }
+        return;
     }
 
-    for (;;) {
-        // phase stamps only when profiling: a clock read is a scalar-memory op whose
-        // return every later LDS wait (lgkmcnt) would also wait for
-        const uint64_t t_start = phase ? wall_clock64() : 0;
-        if (tid == 0) bc[0] = atomicAdd(&ctl[0], 1u);  // ticket
-        __syncthreads();
-        const uint64_t u = __builtin_amdgcn_readfirstlane(bc[0]);
+    // packer waves
+    uint32_t bar = 0;
+    auto pbar_sync = [&]() {
+        bar += 2;
+        ws_signal(&pc.pbar, 1u, j);
+        ws_wait_ge(&pc.pbar, bar);
+    };
+    for (uint32_t i = 0;; i++) {
+        const uint32_t s = i & 1;
+        ws_wait_ge(&pc.coded[s], 2 * ((i >> 1) + 1));
+        const uint32_t u = __builtin_amdgcn_readfirstlane(ws_load(&pc.unit[s]));
         if (u >= g.n_units) break;
-
-        const uint64_t t_ready = phase ? wall_clock64() : 0;
-        const uint64_t ubase = u * g.unit;
+        const uint64_t t_seen = phase ? wall_clock64() : 0;
+        const uint64_t ubase = (uint64_t)u * g.unit;
         const uint32_t len = (uint32_t)((g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit);
         const uint8_t* usrc = src + ubase;
-        const uint32_t end0 = st0_off + j * fp.stride0 + fp.sl0;  // slot ends (LDS byte addresses)
-        const uint32_t end1 = st1_off + j * fp.stride1 + fp.sl1;
-        const uint32_t endw = w ? end1 : end0;
-        EncLane c{L, 0u, 0u, 0x08090A0Bu, endw - 4u};   // NW = 1: byte FL; NW = 2: this wave's byte
-        EncLane c1{L, 0u, 0u, 0x08090A0Bu, end1 - 4u};  // NW = 1: byte 3
-
-        const uint32_t col = 4 * j;
-        const uint32_t K = len > col ? (len - col + 255) / 256 : 0u;
-        if ((len & 255u) == 0) {
-            if (NW == 1) enc_full_rows<SPE, ESC, SIDE, 2>(c, c1, usrc + col, sidecar, ubase, j, len >> 8, tab, lds8);
-            else if (w == 0) enc_full_rows<SPE, ESC, SIDE, 0>(c, c1, usrc + col, sidecar, ubase, j, len >> 8, tab, lds8);
-            else enc_full_rows<SPE, ESC, SIDE, 1>(c, c1, usrc + col, sidecar, ubase, j, len >> 8, tab, lds8);
-        } else {
-            // A tensor's last unit: rows from the top down, one at a time; the top
-            // row may be partial (bf16: lane 4j+3 has one symbol fewer).
-            for (int32_t k = (int32_t)K - 1; k >= 0; k--) {
-                const uint32_t p = 256 * (uint32_t)k + col;
-                const uint32_t nvalid = (len - p) < 4 ? (len - p) : 4;
-                uint32_t v = 0;
-                if (nvalid == 4) v = *reinterpret_cast<const uint32_t*>(usrc + p);
-                else for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)usrc[p + b] << (8 * b);
-                if (SIDE && (NW == 1 || (uint32_t)(k & 1) == w)) write_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
-                v &= lm;
-                const uint32_t sy = (v >> sh) & 255u;
-                if (w == 0 || nvalid == 4) enc_step<ESC>(c, sy, tab[sy]);
-                if (NW == 1 && nvalid == 4) { const uint32_t s1 = v >> 24; enc_step<ESC>(c1, s1, tab[s1]); }
-                if ((k & 1) == 0) { enc_flush(c, lds8); if (NW == 1) enc_flush(c1, lds8); }
-            }
-        }
-        const uint32_t e = enc_finish(c, lds8, endw);
-        uint32_t e0, x0, e1, x1;
-        if (NW == 1) {
-            e0 = e; x0 = c.x;
-            e1 = enc_finish(c1, lds8, end1); x1 = c1.x;
-        } else {
-            // the lane tables double as the slots' guard: written only once both
-            // waves are done coding
-            __syncthreads();
-            if (w == 0) { xch[j] = e; xch[64 + j] = c.x; }
-            else xch[128 + j] = e;
-            __syncthreads();
-            e0 = w ? xch[j] : e;
-            x0 = w ? xch[64 + j] : c.x;
-            e1 = w ? e : xch[128 + j];
-            x1 = w ? c.x : 0u;  // states of byte 3 are only needed by wave 1 (headers)
-        }
-        // byte counts, final states and LDS stream starts of the four lanes of
-        // column j (with NW = 2 both waves compute them; the scan is wave-local)
+        const uint32_t rb = reg0 + (2 * pr + s) * rbytes;
+        uint16_t* loff = reinterpret_cast<uint16_t*>(lds8 + rb + R_LOFF);  // lane offsets in the unit (257)
+        uint32_t* lsa = reinterpret_cast<uint32_t*>(lds8 + rb + R_SA);     // LDS stream starts (256)
+        const uint32_t end0 = rb + R_SLOTS + j * fp.stride0 + fp.sl0;
+        const uint32_t end1 = rb + R_SLOTS + 64 * fp.stride0 + j * fp.stride1 + fp.sl1;
+        const uint32_t e0 = pc.xch[s][0][j], x0 = pc.xch[s][1][j];
+        const uint32_t e1 = pc.xch[s][2][j], x1 = pc.xch[s][3][j];
+        // byte counts, final states and LDS stream starts of the four lanes of column j
         uint32_t cnt[4], fs[4], sa[4];
 #pragma unroll
         for (int b = 0; b < 4; b++) {
@@ -1093,10 +1165,10 @@ __global__ void __launch_bounds__(64 * NW) encode_fast_kernel(const uint8_t* __r
         const bool over = ((e0 + 3u) & ~3u) > fp.sl0 || ((e1 + 3u) & ~3u) > fp.sl1;
         const bool any_over = __ballot(over) != 0;
 
-        const uint64_t t_coded = phase ? wall_clock64() : 0;
-        if (NW == 1 || w == 1) {
+        uint64_t t_off = 0;
+        if (rl == 1) {
             // headers (4 per thread, 64 contiguous bytes) and the lane tables for packing
-            ckr_stream_header* uh = hdrs + u * 256 + 4 * j;
+            ckr_stream_header* uh = hdrs + (uint64_t)u * 256 + 4 * j;
             uint32_t run = excl;
 #pragma unroll
             for (int b = 0; b < 4; b++) {
@@ -1109,38 +1181,37 @@ __global__ void __launch_bounds__(64 * NW) encode_fast_kernel(const uint8_t* __r
                 h.pad = 0;
                 uh[b] = h;
                 loff[4 * j + b] = (uint16_t)run;
-                lsa[4 * j + b] = (uint16_t)sa[b];
+                lsa[4 * j + b] = sa[b];
                 run += cnt[b];
             }
             if (j == 63) loff[256] = (uint16_t)total;
-        }
-        if (w == 0) {
+        } else {
             const uint64_t off = lookback_wave(status, g.n_units, u, size, &ctl[2], j);
             if (j == 0) {
                 unit_off[u] = off;
                 if (u + 1 == g.n_units) unit_off[u + 1] = off + size;
-                bc[1] = (uint32_t)off; bc[2] = (uint32_t)(off >> 32);
-                if (phase) { uint64_t* ph = phase + 8 * u; ph[0] = t_start; ph[1] = t_ready; ph[2] = t_coded; ph[3] = wall_clock64(); }
+                pc.off[s][0] = (uint32_t)off;
+                pc.off[s][1] = (uint32_t)(off >> 32);
             }
+            t_off = phase ? wall_clock64() : 0;
         }
-        __syncthreads();
-        if (phase && tid == 0) phase[8 * u + 4] = wall_clock64();
+        pbar_sync();
         uint32_t nchunks = 0;
-        const uint64_t off = (uint64_t)bc[1] | ((uint64_t)bc[2] << 32);
+        const uint64_t off = (uint64_t)pc.off[s][0] | ((uint64_t)pc.off[s][1] << 32);
         uint8_t* dst = out + off;
         if (raw) {  // masked bytes of the unit, byte stores (rare)
-            for (uint32_t q = tid; q < len; q += NT) {
+            for (uint32_t q = 64 * rl + j; q < len; q += 128) {
                 const uint8_t v = usrc[q];
                 dst[q] = byte_live(q, g.es, g.spe) ? v : 0;
             }
         } else if (any_over) {  // bytes come from the general kernels
-            if (tid == 0) redo_list[atomicAdd(&ctl[1], 1u)] = (uint32_t)u;
+            if (rl == 0 && j == 0) redo_list[atomicAdd(&ctl[1], 1u)] = u;
         } else {
             // Packed bytes in 16-byte destination chunks (aligned in global memory).
-            // The four lanes of column j are one contiguous run of the output; with
-            // NW = 2 wave 0 takes its first half [r0, mid), wave 1 the rest.  A thread
-            // writes every chunk whose first unit byte lies in its range (chunk 0, which
-            // may start before the unit, belongs to the range holding byte 0).  It walks
+            // The four lanes of column j are one contiguous run of the output; packer
+            // 0 takes its first half [r0, mid), packer 1 the rest.  A thread writes
+            // every chunk whose first unit byte lies in its range (chunk 0, which may
+            // start before the unit, belongs to the range holding byte 0).  It walks
             // the column's lanes (bounds and LDS starts in registers): the chunks that
             // lie inside a lane are unaligned 16-byte LDS reads, four issued at a time;
             // the chunk that starts in a lane and runs past its end takes its remaining
@@ -1152,15 +1223,15 @@ __global__ void __launch_bounds__(64 * NW) encode_fast_kernel(const uint8_t* __r
             const int32_t isize = (int32_t)size;
             const int32_t c0 = (int32_t)excl, c4 = (int32_t)(excl + tsum);
             const int32_t mid = (c0 + c4) >> 1;
-            const int32_t r0 = (NW == 2 && w) ? mid : c0, r1 = (NW == 1 || w) ? c4 : mid;
+            const int32_t r0 = rl ? mid : c0, r1 = rl ? c4 : mid;
             // a chunk starting at q whose bytes from pos on come from the lanes after L
-            auto gather_tail = [&](uint4 v, int32_t q, int32_t pos, int32_t L) {
+            auto gather_tail = [&](uint4 v, int32_t q, int32_t pos, int32_t Ln) {
                 const int32_t qe = min(q + 16, isize);
-                while (pos < qe && L < 255) {
-                    L++;
-                    const int32_t lo2 = (int32_t)loff[L], hi2 = (int32_t)loff[L + 1];
+                while (pos < qe && Ln < 255) {
+                    Ln++;
+                    const int32_t lo2 = (int32_t)loff[Ln], hi2 = (int32_t)loff[Ln + 1];
                     if (hi2 > lo2) {
-                        v = merge16_from(v, lds_read16(lds8, (uint32_t)((int32_t)lsa[L] - lo2 + q)), (uint32_t)(pos - q));
+                        v = merge16_from(v, lds_read16(lds8, (uint32_t)((int32_t)lsa[Ln] - lo2 + q)), (uint32_t)(pos - q));
                         pos = hi2;
                     }
                 }
@@ -1215,9 +1286,15 @@ __global__ void __launch_bounds__(64 * NW) encode_fast_kernel(const uint8_t* __r
                 }
             }
         }
-        if (phase && tid == 0) { phase[8 * u + 5] = wall_clock64(); phase[8 * u + 7] = nchunks; }
-        __syncthreads();  // the slots, lane tables and bc are reused by the next unit
-        if (phase && tid == 0) phase[8 * u + 6] = wall_clock64();  // per-unit phase stamps (100 MHz clock)
+        const uint64_t t_packed = phase ? wall_clock64() : 0;
+        pbar_sync();  // both packers are done with the set
+        if (rl == 0) {
+            ws_signal(&pc.freed[s], 1u, j);
+            if (phase && j == 0) {
+                uint64_t* ph = phase + 8 * (uint64_t)u;
+                ph[3] = t_seen; ph[4] = t_off; ph[5] = t_packed; ph[6] = wall_clock64(); ph[7] = nchunks;
+            }
+        }
     }
 }
 
@@ -1235,52 +1312,65 @@ static uint32_t slot_stride(uint32_t sl) {
 
 uint64_t encode_fast_status_words(uint64_t n_units) { return n_units + 2 * ((n_units + 63) / 64); }
 
-uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p) {
-    return FE_META + 64 * (slot_stride(p.sl0) + slot_stride(p.sl1)) + FE_CBYTES_REL + 3 * p.canon_bytes + 32;
+// Coder pairs per workgroup that fit the LDS limit (0: none).
+static uint32_t fast_enc_pairs(const FastEncParamsHost& p, uint32_t lds_limit) {
+    for (uint32_t pairs = 2; pairs >= 1; pairs--)
+        if (ws_lds_bytes(pairs, p.canon_bytes, slot_stride(p.sl0), slot_stride(p.sl1)) <= lds_limit) return pairs;
+    return 0;
+}
+
+uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p, uint32_t lds_limit) {
+    const uint32_t pairs = fast_enc_pairs(p, lds_limit);
+    return pairs ? ws_lds_bytes(pairs, p.canon_bytes, slot_stride(p.sl0), slot_stride(p.sl1)) : 0u;
 }
 
 hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
-                              const FastEncParamsHost& hp, ckr_stream_header* hdrs, uint8_t* sidecar, uint8_t* out,
-                              uint64_t* unit_off, uint64_t* status, uint32_t* ctl, uint32_t* redo_list,
-                              hipStream_t s) {
+                              const FastEncParamsHost& hp, uint32_t lds_limit, ckr_stream_header* hdrs,
+                              uint8_t* sidecar, uint8_t* out, uint64_t* unit_off, uint64_t* status, uint32_t* ctl,
+                              uint32_t* redo_list, hipStream_t s) {
     uint64_t* phase = prof_phase_buffer(g.n_units * 8, s);
     FastEncParams fp;
     fp.sl0 = hp.sl0; fp.sl1 = hp.sl1; fp.cw = hp.cw; fp.canon_bytes = hp.canon_bytes;
     fp.stride0 = slot_stride(hp.sl0); fp.stride1 = slot_stride(hp.sl1);
+    const uint32_t pairs = fast_enc_pairs(hp, lds_limit);
+    if (!pairs) return hipErrorInvalidValue;
+    const uint32_t lb = ws_lds_bytes(pairs, fp.canon_bytes, fp.stride0, fp.stride1);
     const uint64_t n = g.n_units;
     const uint64_t nst = encode_fast_status_words(n);  // unit words, block words, block counts
     CKR_LAUNCH("encode_fast_reset_kernel", s, encode_fast_reset_kernel<<<(uint32_t)((nst + 255) / 256), 256, 0, s>>>(status, nst, ctl));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const uint32_t lb = encode_fast_lds_bytes(hp);
     // persistent grid: as many workgroups as fit on the device at once (more
-    // would only find the tickets gone), never more than there are units
+    // would only find the tickets gone), never more than the units need
     int dev = 0, ncu = 0;
     if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
     if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
-#define CKR_FAST_ENC(SPE_, ESC_, SIDE_)                                                                        \
-    do {                                                                                                      \
-        const void* kf = reinterpret_cast<const void*>(&encode_fast_kernel<SPE_, ESC_, SIDE_, kFastEncWaves>);        \
-        (void)hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);                   \
-        int per_cu = 0;                                                                                       \
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, encode_fast_kernel<SPE_, ESC_, SIDE_, kFastEncWaves>, \
-                                                         64 * kFastEncWaves, lb) != hipSuccess || per_cu < 1)          \
-            per_cu = 1;                                                                                       \
-        const uint32_t grid = (uint32_t)std::min<uint64_t>(n, (uint64_t)per_cu * (uint64_t)std::max(ncu, 1)); \
-        CKR_LAUNCH("encode_fast_kernel", s,                                                                   \
-                   encode_fast_kernel<SPE_, ESC_, SIDE_, kFastEncWaves><<<grid, 64 * kFastEncWaves, lb, s>>>(                  \
-                       src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status, ctl, redo_list, phase)); \
-    } while (0)
+    auto run = [&](auto kern, uint32_t nthreads) -> hipError_t {
+        const void* kf = reinterpret_cast<const void*>(kern);
+        hipError_t r = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);
+        if (r != hipSuccess) return r;
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nthreads, lb) != hipSuccess || per_cu < 1)
+            per_cu = 1;
+        const uint64_t need = (n + pairs - 1) / pairs;
+        const uint32_t grid = (uint32_t)std::min<uint64_t>(need, (uint64_t)per_cu * (uint64_t)std::max(ncu, 1));
+        CKR_LAUNCH("encode_fast_kernel", s,
+                   kern<<<grid, nthreads, lb, s>>>(src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status,
+                                                   ctl, redo_list, phase));
+        return hipGetLastError();
+    };
+#define CKR_FAST_ENC(SPE_, ESC_, SIDE_)                                                                          \
+    (pairs == 2 ? run(encode_fast_kernel<SPE_, ESC_, SIDE_, 2>, 512u) : run(encode_fast_kernel<SPE_, ESC_, SIDE_, 1>, 256u))
     const bool side = sidecar != nullptr;
     if (g.spe == 2) {
-        if (hp.escapes) { if (side) CKR_FAST_ENC(2, true, true); else CKR_FAST_ENC(2, true, false); }
-        else { if (side) CKR_FAST_ENC(2, false, true); else CKR_FAST_ENC(2, false, false); }
+        if (hp.escapes) e = side ? CKR_FAST_ENC(2, true, true) : CKR_FAST_ENC(2, true, false);
+        else e = side ? CKR_FAST_ENC(2, false, true) : CKR_FAST_ENC(2, false, false);
     } else {
-        if (hp.escapes) { if (side) CKR_FAST_ENC(1, true, true); else CKR_FAST_ENC(1, true, false); }
-        else { if (side) CKR_FAST_ENC(1, false, true); else CKR_FAST_ENC(1, false, false); }
+        if (hp.escapes) e = side ? CKR_FAST_ENC(1, true, true) : CKR_FAST_ENC(1, true, false);
+        else e = side ? CKR_FAST_ENC(1, false, true) : CKR_FAST_ENC(1, false, false);
     }
 #undef CKR_FAST_ENC
-    return hipGetLastError();
+    return e;
 }
 
 // ------------------------------------------------------------------ rANS decode
@@ -1317,8 +1407,8 @@ __device__ __forceinline__ void decode_raw_unit(const uint8_t* ud, uint64_t ubas
     }
 }
 
-// General decoder: any unit size; every lane decoded from global memory.  With
-// unit_mask, only units whose mask entry is non-zero are decoded.
+// General decoder: any unit size, any dtype; every lane decoded from global
+// memory.
 struct LaneIn {
     uint32_t x;
     const uint8_t* p;
@@ -1340,16 +1430,13 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
                                                      const uint64_t* __restrict__ unit_off,
                                                      const uint32_t* __restrict__ d_dec, EncodeGeom g,
                                                      const uint8_t* __restrict__ sidecar,
-                                                     uint8_t* __restrict__ dst, unsigned long long* bad,
-                                                     const uint32_t* __restrict__ unit_mask) {
+                                                     uint8_t* __restrict__ dst, unsigned long long* bad) {
     __shared__ uint32_t tab[4096];
     const uint32_t j = threadIdx.x & 63;
     const uint64_t u = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const bool mine = u < g.n_units && (!unit_mask || unit_mask[u] != 0);
-    if (!__syncthreads_or(mine)) return;  // no unit of this block left to this kernel
     for (uint32_t i = threadIdx.x; i < 4096; i += 256) tab[i] = d_dec[i];
     __syncthreads();
-    if (!mine) return;
+    if (u >= g.n_units) return;
     const uint64_t ubase = u * g.unit;
     const uint32_t len = unit_len(g, ubase);
     const uint8_t* ud = data + unit_off[u];
@@ -1398,8 +1485,7 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
     if (nbad) atomicAdd(bad, (unsigned long long)nbad);
 }
 
-// Fast decoder (masked planes, spe > 0; units whose length is a multiple of
-// 256).  One block of DF_WAVES waves per CU, persistent over the units; a wave
+// Fast decoder (masked planes, spe > 0; every unit of a tensor).  One block of DF_WAVES waves per CU, persistent over the units; a wave
 // decodes one unit at a time, thread j taking column j, whose two live lanes
 // it decodes side by side.  LDS holds the decode table, 4096 entries of
 // {f | sym << 24, slot - cum} (the state update is one 24-bit multiply-add),
@@ -1417,9 +1503,12 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
 // of the next group, three groups at least before it is read.  The decoded
 // tensor and the sidecar are streamed with non-temporal accesses so that they
 // do not push the streams' lines out of L2.  Zero-plane lanes are checked
-// against the canonical stream (header and bytes) and produce zeros.  Units of
-// other lengths (a tensor's last), and units whose chunks could pass the end of
-// the data buffer, are left to decode_kernel (marked in unit_mask).
+// against the canonical stream (header and bytes) and produce zeros.  A
+// tensor's last unit may end in a partial row, decoded after the full rows
+// with exact-size sidecar loads and byte stores.  Chunks that do not lie wholly
+// inside the data buffer (the first unit of a buffer that is not 64-byte
+// aligned, the units at its end, streams running past their end) are
+// assembled byte by byte, with zeros outside the buffer.
 static constexpr uint32_t DF_WAVES = 7;
 static constexpr uint32_t DF_TAB_BYTES = 4096 * 8;
 static constexpr uint32_t DF_RING_BYTES = 33 * 256;  // 32 rows + the copy of row 0
@@ -1440,10 +1529,44 @@ struct DfLane {
     uint4 c0, c1, c2, c3;
 };
 
-// Chunk k (64 bytes) of the unit's aligned base.
-__device__ __forceinline__ void df_fetch(const uint8_t* ua, uint32_t k, uint4& c0, uint4& c1, uint4& c2, uint4& c3) {
-    const uint4* q = reinterpret_cast<const uint4*>(ua + ((size_t)k << 6));
-    c0 = q[0]; c1 = q[1]; c2 = q[2]; c3 = q[3];
+// Where a unit's chunks come from: chunk k is the 64 bytes at ua + 64 k; the
+// chunks k_lo .. k_lo + n_in - 1 lie wholly inside the data buffer [d0, d0 + dlen).
+struct DfSrc {
+    const uint8_t* d0;
+    uint64_t dlen;
+    int64_t ua;  // the unit's 64-byte aligned base, relative to d0 (-63..)
+    uint32_t k_lo, n_in;  // chunks k_lo .. k_lo + n_in - 1 lie wholly inside the buffer
+};
+
+// 16 bytes at byte offset a of the buffer, with zeros outside [0, dlen): the
+// rare path of df_fetch, kept out of line.
+__device__ __attribute__((noinline)) uint4 df_load16_clipped(const uint8_t* d0, uint64_t dlen, int64_t a) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t v = 0;
+        for (int b = 0; b < 4; b++) {
+            const int64_t o = a + 4 * i + b;
+            if (o >= 0 && (uint64_t)o < dlen) v |= (uint32_t)d0[o] << (8 * b);
+        }
+        w[i] = v;
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// Chunk k of the unit: four 16-byte loads, or, for a chunk that is not wholly
+// inside the buffer, its bytes one at a time with zeros outside.
+__device__ __forceinline__ void df_fetch(const DfSrc& sr, uint32_t k, uint4& c0, uint4& c1, uint4& c2, uint4& c3) {
+    const int64_t a = sr.ua + ((int64_t)k << 6);
+    if (k - sr.k_lo < sr.n_in) {
+        const uint4* q = reinterpret_cast<const uint4*>(sr.d0 + a);
+        c0 = q[0]; c1 = q[1]; c2 = q[2]; c3 = q[3];
+    } else {
+        c0 = df_load16_clipped(sr.d0, sr.dlen, a);
+        c1 = df_load16_clipped(sr.d0, sr.dlen, a + 16);
+        c2 = df_load16_clipped(sr.d0, sr.dlen, a + 32);
+        c3 = df_load16_clipped(sr.d0, sr.dlen, a + 48);
+    }
 }
 
 // Writes chunk k into ring slot k & 1 (rows 16s..16s+15; slot 0 also into row 32).
@@ -1481,12 +1604,12 @@ __device__ __forceinline__ uint32_t df_sym(uint32_t& x, uint32_t& w, uint32_t& s
 
 // End of a group: write the chunk fetched at the end of the previous group,
 // then move on if p has reached the next chunk and fetch the one after it.
-__device__ __forceinline__ void df_step(DfLane& d, uint8_t* lds8, const uint8_t* ua, uint32_t lim_ch) {
+__device__ __forceinline__ void df_step(DfLane& d, uint8_t* lds8, const DfSrc& sr) {
     if (d.pend) df_put(lds8, d.tb, d.ch + 1u, d.c0, d.c1, d.c2, d.c3);
     const bool adv = (d.p8 >> 9) > d.ch;
     d.ch += adv ? 1u : 0u;
     d.pend = adv;
-    if (adv) df_fetch(ua, min(d.ch + 1u, lim_ch), d.c0, d.c1, d.c2, d.c3);
+    if (adv) df_fetch(sr, d.ch + 1u, d.c0, d.c1, d.c2, d.c3);
 }
 
 template <int SPE>
@@ -1525,11 +1648,11 @@ __device__ __forceinline__ void df_pair(DfLane& a, DfLane& b, const uint8_t* lds
 // Eight rows (sidecar words sc), then the window step.
 template <int SPE>
 __device__ __forceinline__ void df_group(DfLane& a, DfLane& b, uint8_t* lds8, const uint2* tab, uint32_t* out,
-                                         const uint32_t (&sc)[8], uint32_t sel, const uint8_t* ua, uint32_t lim_ch) {
+                                         const uint32_t (&sc)[8], uint32_t sel, const DfSrc& sr) {
 #pragma unroll
     for (int r = 0; r < 8; r += 2) df_pair<SPE>(a, b, lds8, tab, out + 64 * r, sc[r], sc[r + 1], sel);
-    df_step(a, lds8, ua, lim_ch);
-    df_step(b, lds8, ua, lim_ch);
+    df_step(a, lds8, sr);
+    df_step(b, lds8, sr);
 }
 
 __device__ __forceinline__ void df_load_sc(uint32_t (&sc)[8], const uint32_t* p) {
@@ -1544,8 +1667,7 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
                                                                    const uint32_t* __restrict__ d_dec,
                                                                    const uint32_t* __restrict__ canon, uint32_t cw,
                                                                    EncodeGeom g, const uint8_t* __restrict__ sidecar,
-                                                                   uint8_t* __restrict__ dst, unsigned long long* bad,
-                                                                   uint32_t* __restrict__ unit_mask) {
+                                                                   uint8_t* __restrict__ dst, unsigned long long* bad) {
     extern __shared__ uint32_t lds[];
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
     const uint2* tab = reinterpret_cast<const uint2*>(lds);
@@ -1571,21 +1693,21 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
         const uint32_t usize = (uint32_t)(unit_off[u + 1] - uoff);
         const ckr_stream_header* uh = hdrs + u * 256;
         if (usize == len && uh[0].byte_count == len) {
-            if (j == 0) unit_mask[u] = 0;
             decode_raw_unit<SPE>(ud, ubase, len, j, sidecar, dst);
             continue;
         }
-        // chunks are read from the unit's 64-byte aligned base up to 2 chunks past
-        // the unit's end (valid streams); the rest are clamped to lim_ch
+        // chunks are read from the unit's 64-byte aligned base
         const uintptr_t ua = reinterpret_cast<uintptr_t>(ud) & ~(uintptr_t)63;
         const uint32_t g0 = (uint32_t)(reinterpret_cast<uintptr_t>(ud) - ua);
-        if ((len & 255u) || ua < d0 || ua + (((uintptr_t)(g0 + usize) >> 6) + 3) * 64 > d1) {
-            if (j == 0) unit_mask[u] = 1;
-            continue;
+        DfSrc sr;
+        sr.d0 = data;
+        sr.dlen = data_len;
+        sr.ua = (int64_t)ua - (int64_t)d0;
+        sr.k_lo = ua >= d0 ? 0u : 1u;
+        {   // chunks [k_lo, k_end) end at or before d1
+            const int64_t k_end = min<int64_t>(((int64_t)d1 - (int64_t)ua) >> 6, 0x40000000ll);
+            sr.n_in = k_end > (int64_t)sr.k_lo ? (uint32_t)(k_end - (int64_t)sr.k_lo) : 0u;
         }
-        if (j == 0) unit_mask[u] = 0;
-        const uint8_t* uab = data + (ua - d0);
-        const uint32_t lim_ch = (uint32_t)min<uintptr_t>((d1 - ua) >> 6, 0x01000000u) - 1u;
         uint32_t nbad = 0;
         DfLane da, db;
         uint32_t gea8, geb8;
@@ -1606,16 +1728,16 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
             da.tb = tb0;
             db.tb = tb0 + DF_RING_BYTES;
             uint4 a0, a1, a2, a3, a4, a5, a6, a7, b0, b1, b2, b3, b4, b5, b6, b7;
-            df_fetch(uab, min(da.ch, lim_ch), a0, a1, a2, a3);
-            df_fetch(uab, min(da.ch + 1u, lim_ch), a4, a5, a6, a7);
-            df_fetch(uab, min(db.ch, lim_ch), b0, b1, b2, b3);
-            df_fetch(uab, min(db.ch + 1u, lim_ch), b4, b5, b6, b7);
+            df_fetch(sr, da.ch, a0, a1, a2, a3);
+            df_fetch(sr, da.ch + 1u, a4, a5, a6, a7);
+            df_fetch(sr, db.ch, b0, b1, b2, b3);
+            df_fetch(sr, db.ch + 1u, b4, b5, b6, b7);
             df_put(lds8, da.tb, da.ch, a0, a1, a2, a3);
             df_put(lds8, da.tb, da.ch + 1u, a4, a5, a6, a7);
             df_put(lds8, db.tb, db.ch, b0, b1, b2, b3);
             df_put(lds8, db.tb, db.ch + 1u, b4, b5, b6, b7);
         }
-        const uint32_t K = len >> 8;  // rows (every column has K, all full)
+        const uint32_t K = len >> 8;  // full rows; a partial row K follows when len % 256 != 0
         // sidecar of row k for this column: 16 bits at (ubase + 256k + 4j) / 2, read
         // as the aligned dword around them (sidecar is 16-byte aligned, ubase a
         // multiple of 256)
@@ -1634,16 +1756,16 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
             df_load_sc(sa, sc32);
             for (; gi + 2 < ng; gi += 2) {
                 df_load_sc(sb, sc32 + 256 * (gi + 1));
-                df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, uab, lim_ch);
+                df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, sr);
                 df_load_sc(sa, sc32 + 256 * (gi + 2));
-                df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 1), sb, sel, uab, lim_ch);
+                df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 1), sb, sel, sr);
             }
             if (gi + 1 < ng) {
                 df_load_sc(sb, sc32 + 256 * (gi + 1));
-                df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, uab, lim_ch);
-                df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 1), sb, sel, uab, lim_ch);
+                df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, sr);
+                df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 1), sb, sel, sr);
             } else {
-                df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, uab, lim_ch);
+                df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, sr);
             }
         }
         // at most 7 rows left: no window step needed
@@ -1658,13 +1780,31 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
             da.p8 += ha;
             db.p8 += hb;
         }
+        // the partial top row of a tensor's last unit: r bytes, nv of them in this
+        // column; a live lane takes part when its byte is among them
+        const uint32_t r = len & 255u;
+        if (r > 4 * j) {
+            const uint32_t nv = min(r - 4 * j, 4u);
+            uint32_t wa = df_window(da, lds8), wb = df_window(db, lds8);
+            uint32_t ha = 0, hb = 0, v = 0;
+            if (nv > (uint32_t)FL) v |= (df_sym(da.x, wa, ha, tab) >> 24) << (8 * FL);
+            if (nv > 3u) v |= df_sym(db.x, wb, hb, tab) & 0xFF000000u;
+            da.p8 += ha;
+            db.p8 += hb;
+            const uint64_t pos = ubase + 256ull * K + 4 * j;
+            v = merge_sidecar_row<SPE>(sidecar, pos, v, nv);
+            uint8_t* d8 = dst + pos;
+            if (nv == 4) *reinterpret_cast<uint32_t*>(d8) = v;
+            else for (uint32_t b = 0; b < nv; b++) d8[b] = (uint8_t)(v >> (8 * b));
+        }
         nbad += (da.x != L || da.p8 != gea8) ? 1u : 0u;
         nbad += (db.x != L || db.p8 != geb8) ? 1u : 0u;
         // zero-plane lanes: header and bytes must be the canonical stream
 #pragma unroll
         for (int b = 0; b < 4; b++) {
             if (lane_is_live<SPE>(b)) continue;
-            const uint32_t ent = (canon[0] == K) ? 0u : ((canon[4 + cw] == K) ? 1u : 2u);
+            const uint32_t Kb = K + ((4 * j + b < r) ? 1u : 0u);  // symbols of lane 4j+b
+            const uint32_t ent = (canon[0] == Kb) ? 0u : ((canon[4 + cw] == Kb) ? 1u : 2u);
             const uint32_t* ce = canon + ent * (4 + cw);
             const ckr_stream_header h = uh[4 * j + b];
             bool ok = h.final_state == ce[1] && h.byte_count == ce[2] && (uint64_t)h.buf_offset + h.byte_count <= usize;
@@ -1706,13 +1846,12 @@ uint32_t decode_fast_lds_bytes() { return DF_TAB_BYTES + DF_WAVES * DF_WAVE_BYTE
 
 hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
                          const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
-                         unsigned long long* bad, const uint32_t* canon, uint32_t cw, uint32_t* unit_mask,
-                         hipStream_t s) {
+                         unsigned long long* bad, const uint32_t* canon, uint32_t cw, hipStream_t s) {
     const uint32_t grid = (uint32_t)((g.n_units + 3) / 4);
     if (grid == 0) return hipSuccess;
     hipError_t e;
     bool fast_ran = false;
-    if (canon && unit_mask && g.spe > 0) {  // fast path, then the general kernel for the units it left
+    if (canon && g.spe > 0) {  // fast path
         const uint32_t lb = decode_fast_lds_bytes();
         int dev = 0, ncu = 0;
         if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
@@ -1727,16 +1866,16 @@ hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, con
             // persistent: the blocks that fit at once, never more than needed
             const uint64_t need = (g.n_units + DF_WAVES - 1) / DF_WAVES;
             const uint32_t fg = (uint32_t)std::min<uint64_t>(need, (uint64_t)per_cu * (uint64_t)std::max(ncu, 1));
-            CKR_LAUNCH("decode_fast_kernel", s, kern<<<fg, 64 * DF_WAVES, lb, s>>>(data, hdrs, unit_off, d_dec, canon, cw, g, sidecar, dst, bad, unit_mask));
+            CKR_LAUNCH("decode_fast_kernel", s, kern<<<fg, 64 * DF_WAVES, lb, s>>>(data, hdrs, unit_off, d_dec, canon, cw, g, sidecar, dst, bad));
             fast_ran = true;
             return hipGetLastError();
         };
         if ((e = (g.spe == 2 ? fast(decode_fast_kernel<2>) : fast(decode_fast_kernel<1>))) != hipSuccess) return e;
+        if (fast_ran) return hipSuccess;  // the fast kernel decodes every unit
     }
-    const uint32_t* mask = fast_ran ? unit_mask : nullptr;
-    if (g.spe == 2) CKR_LAUNCH("decode_kernel", s, decode_kernel<2><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad, mask));
-    else if (g.spe == 1) CKR_LAUNCH("decode_kernel", s, decode_kernel<1><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad, mask));
-    else CKR_LAUNCH("decode_kernel", s, decode_kernel<0><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad, mask));
+    if (g.spe == 2) CKR_LAUNCH("decode_kernel", s, decode_kernel<2><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
+    else if (g.spe == 1) CKR_LAUNCH("decode_kernel", s, decode_kernel<1><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
+    else CKR_LAUNCH("decode_kernel", s, decode_kernel<0><<<grid, 256, 0, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
     return hipGetLastError();
 }
 

@@ -205,3 +205,31 @@ def test_analyzer_parity(dt, n, bins, gen, gpu):
     fp = got["fingerprint"]
     assert np.array_equal(fp[:4], got["moments"], equal_nan=True)
     assert np.array_equal(fp[4:], np.float32(got["minmax"][1] - got["minmax"][0]).reshape(1), equal_nan=True)
+
+
+@pytest.mark.parametrize("dt,n,unit,gen", [
+    (dg.F32, 16384 * 3 + 77, 65536, lambda n: dg.normal_f32(n, 1e-3, 21)),
+    (dg.BF16, 32768 + 4099, 4096, lambda n: dg.normal_bf16(n, 0.02, 22)),
+    (dg.F32, 300, 1024, lambda n: dg.exp_avg_sq(n, 23)),
+])
+@pytest.mark.parametrize("shift", [0, 5, 61])
+def test_decode_from_relocated_stream(dt, n, unit, gen, shift, gpu):
+    """The packed bytes moved to a buffer that ends right after them and starts
+    `shift` bytes past a 64-byte boundary: chunks around both ends of the buffer
+    are read only inside it, and decoding stays bit-exact."""
+    import torch
+    ck = _ck()
+    print(f"[case] relocated dtype={dt} n={n} unit={unit} shift={shift}", flush=True)
+    raw = gen(n)
+    src = _to_dev(raw, gpu)
+    enc = ck.compress(src, dt, unit, n_elems=n)
+    torch.cuda.synchronize()
+    base = torch.zeros(enc.total + 64, dtype=torch.uint8, device=gpu)
+    moved = base[shift: shift + enc.total]
+    moved.copy_(enc.data[: enc.total])
+    dst = torch.empty(n * ck.element_size(dt), dtype=torch.uint8, device=gpu)
+    d = ck.Decoder(n, dt, unit, device=gpu)
+    bad = d.decode(moved, enc.headers, enc.unit_offsets, enc.table, enc.sidecar, dst)
+    torch.cuda.synchronize()
+    assert bad == 0
+    assert np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
