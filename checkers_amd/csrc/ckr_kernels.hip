@@ -1744,29 +1744,28 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
         const uint32_t* sc32 = reinterpret_cast<const uint32_t*>(sidecar + (ubase >> 1) + 4 * (j >> 1));
         const uint32_t sel = df_sel<SPE>(2 * (j & 1));
         uint32_t* out32 = reinterpret_cast<uint32_t*>(dst + ubase + 4 * j);
-        // rows in groups of 8 (one window step); the next group's sidecar is in
-        // flight while the current group is decoded.  Full groups have no row
-        // guards and their loads are unconditional (the waits stay exact).
+        // rows in groups of 8 (one window step).  A group's sidecar is loaded two
+        // groups ahead: a load completes after every store issued before it (one
+        // in-order counter), so the loads of group g + 2 are issued before group g's
+        // output stores and wait only for stores two groups old.  Loads are
+        // unconditional (indices clamped to the last group) so the waits stay exact.
         const uint32_t ng = K >> 3;  // full groups
         if (ng) {
-            // two groups per iteration with no exit in between (fixed buffer roles,
-            // exact waits); the last one or two groups after the loop
-            uint32_t sa[8], sb[8];
+            const uint32_t gl = ng - 1;
+            uint32_t sa[8], sb[8], sc[8];
             uint32_t gi = 0;
             df_load_sc(sa, sc32);
-            for (; gi + 2 < ng; gi += 2) {
-                df_load_sc(sb, sc32 + 256 * (gi + 1));
+            df_load_sc(sb, sc32 + 256 * min(1u, gl));
+            for (; gi + 3 <= ng; gi += 3) {
+                df_load_sc(sc, sc32 + 256 * min(gi + 2, gl));
                 df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, sr);
-                df_load_sc(sa, sc32 + 256 * (gi + 2));
+                df_load_sc(sa, sc32 + 256 * min(gi + 3, gl));
                 df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 1), sb, sel, sr);
+                df_load_sc(sb, sc32 + 256 * min(gi + 4, gl));
+                df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 2), sc, sel, sr);
             }
-            if (gi + 1 < ng) {
-                df_load_sc(sb, sc32 + 256 * (gi + 1));
-                df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, sr);
-                df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 1), sb, sel, sr);
-            } else {
-                df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, sr);
-            }
+            if (gi < ng) df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, sr);
+            if (gi + 1 < ng) df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 1), sb, sel, sr);
         }
         // at most 7 rows left: no window step needed
         uint32_t k = 8 * ng;
