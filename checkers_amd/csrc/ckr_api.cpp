@@ -122,6 +122,62 @@ uint32_t canon_stream_bytes(const ckr_freq_table* t, uint32_t K) {
     return bytes;
 }
 
+// The canonical zero-plane entries (the layout canon_kernel writes: per lane
+// count K, {K, final state, byte count, 0} and the stream in dword slots counted
+// from its end, then the three streams in byte order) computed here from the
+// reference's state update for symbol 0 (cum 0; f == 0: every symbol a raw
+// byte), when they fit a kernel argument.
+bool canon_host(const ckr_freq_table* t, const CanonKs& ck, ckr::CanonArg* a) {
+    const uint32_t cw = ck.cw;
+    const uint32_t n = 3 * (4 + cw) + 3 * cw;
+    if (n > ckr::CANON_ARG_DWORDS) return false;
+    std::fill(a->w, a->w + n, 0u);
+    a->n = n;
+    const uint32_t f = t->norm_freq[0];
+    const uint32_t Ks[3] = {ck.k0, ck.k1, ck.k2};
+    for (int e = 0; e < 3; e++) {
+        uint32_t* base = a->w + e * (4 + cw);
+        uint32_t* slots = base + 4;
+        uint32_t x = CKR_L, nacc = 0, w = 0;
+        uint64_t acc = 0;
+        auto push = [&](uint32_t byte) {
+            acc = (acc << 8) | byte;
+            if (++nacc == 4) { slots[w++] = (uint32_t)acc; nacc = 0; }
+        };
+        for (uint32_t k = 0; k < Ks[e]; k++) {
+            if (f == 0) { push(0u); continue; }
+            while (x >= (f << 19)) { push(x & 255u); x >>= 8; }
+            x = ((x / f) << CKR_SCALE_BITS) + (x % f);
+        }
+        if (nacc) slots[w] = (uint32_t)acc;
+        const uint32_t B = 4 * w + nacc, r = nacc;
+        base[0] = Ks[e];
+        base[1] = x;
+        base[2] = B;
+        base[3] = 0;
+        uint32_t* sb = a->w + 3 * (4 + cw) + e * cw;
+        for (uint32_t d = 0; d < cw; d++) {
+            uint32_t v = 0;
+            for (uint32_t b = 0; b < 4; b++) {
+                const uint32_t q = 4 * d + b;
+                if (q >= B) break;
+                const uint32_t slot = q < r ? w : w - 1 - ((q - r) >> 2);
+                const uint32_t byte = q < r ? q : (q - r) & 3;
+                v |= ((slots[slot] >> (8 * byte)) & 255u) << (8 * b);
+            }
+            sb[d] = v;
+        }
+    }
+    return true;
+}
+
+hipError_t canon_launch(const ckr_freq_table* t, const ckr::EncSym* enc, const CanonKs& ck, uint32_t* canon,
+                        hipStream_t s) {
+    ckr::CanonArg a;
+    if (canon_host(t, ck, &a)) return ckr::launch_canon_store(a, canon, s);
+    return ckr::launch_canon(enc, ck.k0, ck.k1, ck.k2, ck.cw, canon, s);
+}
+
 bool use_fast_encode(const ckr::EncodeGeom& g) { return use_dedup(g) && (g.unit + 255) / 256 <= kFastMaxK; }
 
 int max_lds_per_block() {
@@ -516,7 +572,7 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
     const CanonKs ck = canon_ks(g);
     uint8_t* side = g.spe ? d_sidecar : nullptr;
     CKR_HIP(ckr::launch_build_enc_table(ta, enc, s));
-    if (dedup) CKR_HIP(ckr::launch_canon(enc, ck.k0, ck.k1, ck.k2, ck.cw, canon, s));
+    if (dedup) CKR_HIP(canon_launch(h_table, enc, ck, canon, s));
 
     bool fast = use_fast_encode(g);
     ckr::FastEncParamsHost fp{};
@@ -650,7 +706,7 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
     CKR_HIP(ckr::launch_build_dec_table(ta, dec, s));
     if (L.fast) {
         CKR_HIP(ckr::launch_build_enc_table(ta, enc, s));
-        CKR_HIP(ckr::launch_canon(enc, ck.k0, ck.k1, ck.k2, ck.cw, canon, s));
+        CKR_HIP(canon_launch(h_table, enc, ck, canon, s));
     }
     CKR_HIP(ckr::launch_set_counter(bad, 0, s));
     CKR_HIP(ckr::launch_decode(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, static_cast<uint8_t*>(d_dst),

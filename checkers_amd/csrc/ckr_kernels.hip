@@ -614,6 +614,16 @@ __global__ void __launch_bounds__(256) compact_kernel(const uint8_t* __restrict_
     s.finish();
 }
 
+__global__ void __launch_bounds__(256) canon_store_kernel(CanonArg a, uint32_t* __restrict__ canon) {
+    for (uint32_t i = threadIdx.x; i < a.n; i += blockDim.x) canon[i] = a.w[i];
+}
+
+hipError_t launch_canon_store(const CanonArg& a, uint32_t* canon, hipStream_t s) {
+    if (a.n > CANON_ARG_DWORDS) return hipErrorInvalidValue;
+    CKR_LAUNCH("canon_store_kernel", s, canon_store_kernel<<<1, 256, 0, s>>>(a, canon));
+    return hipGetLastError();
+}
+
 hipError_t launch_canon(const EncSym* d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw, uint32_t* canon,
                         hipStream_t s) {
     if (cw > CANON_MAX_CW || k0 > CANON_MAX_K || k1 > CANON_MAX_K || k2 > CANON_MAX_K) return hipErrorInvalidValue;
