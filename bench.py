@@ -13,6 +13,13 @@ step.  Decode of the same shard is timed the same way right after and reported
 beside it, with the compression ratios, a bit-exact round-trip check, the
 dominant kernel's roofline, and the CPU oracle timed on a bounded sample.
 
+Config 5 (the Llama-3-70B rank shard, 123.5 GB resident in HBM, 1 MiB units)
+streams: per tensor the masked histogram and table of the whole tensor, then the
+tensor's 4 GiB slices encoded with that table one after the other into reused
+buffers (slices end on unit boundaries, and units are independent given the
+table, so each slice's units are the whole-tensor encode's), each decoded into
+a reused window and compared with its source outside the timed regions.
+
 Usage: python bench.py [--steps K] [--warmup W] [--config 3] [--unit 65536]
 """
 import argparse
@@ -52,9 +59,8 @@ def make_shard(cfg, torch, dev, seed=0):
         tensors.append(("params_bf16", p))
         tensors.append(("master_weights", p.float()))
         tensors.append(("exp_avg", torch.randn(n, generator=g, device=dev) * 1e-3))
-        x = torch.randn(n, generator=g, device=dev) * 1e-3
-        tensors.append(("exp_avg_sq", x * x + 1e-12))
-        del x
+        x = torch.randn(n, generator=g, device=dev).mul_(1e-3)
+        tensors.append(("exp_avg_sq", x.mul_(x).add_(1e-12)))
     elif cfg == 2:
         shapes = [("q_proj", 4096 * 4096), ("k_proj", 1024 * 4096), ("v_proj", 1024 * 4096),
                   ("o_proj", 4096 * 4096), ("gate_proj", 14336 * 4096), ("up_proj", 14336 * 4096),
@@ -121,6 +127,57 @@ def cpu_baseline(shard, ck, sample_bytes_per_tensor, unit):
                 seconds=round(t_all, 3))
 
 
+def stream_bench(shard, ck, torch, dev, unit, steps, slice_bytes):
+    """Config 5: histogram + table per tensor, then encode/decode slice by slice
+    (reused buffers), every slice checked bit-exact against its source.
+    Returns (encode seconds, decode seconds, C, S, H, n_units, ok)."""
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    enc_s = dec_s = 0.0
+    C = S = H = units = 0
+    ok = True
+    for step in range(steps):
+        C = S = H = units = 0
+        for name, t in shard:
+            tag = ck.torch_tag(t.dtype)
+            es = t.element_size()
+            n = t.numel()
+            per = max(unit // es, (slice_bytes // unit) * (unit // es))  # elements per slice, whole units
+            a, b = ev(), ev()
+            a.record()
+            hist = ck.byte_histogram(t, tag)
+            table, tsum = ck.build_table(hist.cpu().numpy().view(np.uint32))
+            b.record()
+            torch.cuda.synchronize()
+            enc_s += a.elapsed_time(b) / 1e3
+            encs, decs = {}, {}
+            window = None
+            for s0 in range(0, n, per):
+                m = min(per, n - s0)
+                if m not in encs:
+                    encs[m] = ck.Encoder(m, tag, unit, device=dev)
+                    decs[m] = ck.Decoder(m, tag, unit, device=dev)
+                if window is None:
+                    window = torch.empty(per * es, dtype=torch.uint8, device=dev)
+                src = t[s0:s0 + m]
+                a, b, c = ev(), ev(), ev()
+                a.record()
+                r = encs[m].encode(src, table)
+                b.record()
+                bad = decs[m].decode(r.data, r.headers, r.unit_offsets, r.table, r.sidecar, window, check=True)
+                c.record()
+                torch.cuda.synchronize()
+                enc_s += a.elapsed_time(b) / 1e3
+                dec_s += b.elapsed_time(c) / 1e3
+                ok = ok and bad == 0 and torch.equal(window[: m * es], src.view(torch.uint8))
+                C += r.total
+                S += m * ck.sidecar_bytes_per_elem(tag)
+                units += encs[m].n_units
+            del encs, decs, window
+            log(f"[bench] {name}: {n * es / 1e9:.2f} GB streamed, ok={ok}")
+        H = units * 256 * 16 + units * 8
+    return enc_s / steps, dec_s / steps, C, S, H, units, ok
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -129,6 +186,7 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--unit", type=int, default=65536)
     ap.add_argument("--cpu-sample-mib", type=int, default=128)
+    ap.add_argument("--slice-gib", type=int, default=4, help="config 5: slice size of the streamed encode/decode")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -150,6 +208,9 @@ def main():
     shard = make_shard(args.config, torch, dev)
     n_in = sum(t.numel() * t.element_size() for _, t in shard)
     log(f"[bench] {len(shard)} tensors, {n_in / 1e9:.3f} GB; unit {unit}")
+    if args.config == 5:
+        run_streamed(args, shard, ck, torch, dev, unit, n_in)
+        return
 
     encs = [ck.Encoder(t.numel(), ck.torch_tag(t.dtype), unit, device=dev) for _, t in shard]
     decs = [ck.Decoder(t.numel(), ck.torch_tag(t.dtype), unit, device=dev) for _, t in shard]
@@ -289,6 +350,40 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernels": kernels,
+    }
+    print(json.dumps(out), flush=True)
+    if not ok:
+        sys.exit(1)
+
+
+def run_streamed(args, shard, ck, torch, dev, unit, n_in):
+    """Config 5 driver: warm-up on the first slice of the first tensor, then the
+    streamed passes; one JSON line like the resident configs."""
+    name0, t0 = shard[0]
+    w = min(t0.numel(), (args.slice_gib << 30) // t0.element_size())
+    for _ in range(max(args.warmup, 1)):
+        stream_bench([(name0, t0[:w])], ck, torch, dev, unit, 1, args.slice_gib << 30)
+    steps = max(1, min(args.steps, 2))
+    enc_s, dec_s, C, S, H, n_units, ok = stream_bench(shard, ck, torch, dev, unit, steps, args.slice_gib << 30)
+    log(f"[bench] streamed: encode {enc_s * 1e3:.1f} ms, decode {dec_s * 1e3:.1f} ms, roundtrip={ok}")
+    B = n_in + S + C + H
+    out = {
+        "metric": METRIC, "value": round(n_in / enc_s / 1e9, 3), "unit": "GB/s", "n_gpus": 1,
+        "steps": steps, "warmup": max(args.warmup, 1), "ms_per_step": round(enc_s * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic: torch Philox on the GPU, seed 0, distributions of BASELINE.json configs",
+        "config": {"workload": "cfg5 llama3-70b zero3 rank0-of-8 shard, streamed in "
+                               f"{args.slice_gib} GiB slices", "elements_per_tensor": [t.numel() for _, t in shard],
+                   "tensors": [n for n, _ in shard], "unit_bytes": unit, "input_bytes": n_in,
+                   "table_bits": 12, "lanes": 256},
+        "encode_GBps": round(n_in / enc_s / 1e9, 3), "decode_GBps": round(n_in / dec_s / 1e9, 3),
+        "encode_ms": round(enc_s * 1e3, 3), "decode_ms": round(dec_s * 1e3, 3),
+        "encode_roofline_frac": round(B / enc_s / 1e9 / HBM_PEAK_GBPS, 4),
+        "decode_roofline_frac": round(B / dec_s / 1e9 / HBM_PEAK_GBPS, 4),
+        "compressed_bytes": C, "sidecar_bytes": S, "header_bytes": H,
+        "ans_ratio": round(n_in / C, 4), "disk_ratio": round(n_in / (C + S), 4),
+        "container_ratio": round(n_in / (C + S + H), 4), "roundtrip_bit_exact": ok,
+        "roofline": None, "cpu_baseline": None, "kernels": {},
     }
     print(json.dumps(out), flush=True)
     if not ok:

@@ -126,17 +126,14 @@ uint32_t canon_stream_bytes(const ckr_freq_table* t, uint32_t K) {
 // count K, {K, final state, byte count, 0} and the stream in dword slots counted
 // from its end, then the three streams in byte order) computed here from the
 // reference's state update for symbol 0 (cum 0; f == 0: every symbol a raw
-// byte), when they fit a kernel argument.
-bool canon_host(const ckr_freq_table* t, const CanonKs& ck, ckr::CanonArg* a) {
+// byte).
+void canon_host(const ckr_freq_table* t, const CanonKs& ck, std::vector<uint32_t>& out) {
     const uint32_t cw = ck.cw;
-    const uint32_t n = 3 * (4 + cw) + 3 * cw;
-    if (n > ckr::CANON_ARG_DWORDS) return false;
-    std::fill(a->w, a->w + n, 0u);
-    a->n = n;
+    out.assign(3 * (4 + cw) + 3 * cw, 0u);
     const uint32_t f = t->norm_freq[0];
     const uint32_t Ks[3] = {ck.k0, ck.k1, ck.k2};
     for (int e = 0; e < 3; e++) {
-        uint32_t* base = a->w + e * (4 + cw);
+        uint32_t* base = out.data() + e * (4 + cw);
         uint32_t* slots = base + 4;
         uint32_t x = CKR_L, nacc = 0, w = 0;
         uint64_t acc = 0;
@@ -155,7 +152,7 @@ bool canon_host(const ckr_freq_table* t, const CanonKs& ck, ckr::CanonArg* a) {
         base[1] = x;
         base[2] = B;
         base[3] = 0;
-        uint32_t* sb = a->w + 3 * (4 + cw) + e * cw;
+        uint32_t* sb = out.data() + 3 * (4 + cw) + e * cw;
         for (uint32_t d = 0; d < cw; d++) {
             uint32_t v = 0;
             for (uint32_t b = 0; b < 4; b++) {
@@ -168,14 +165,22 @@ bool canon_host(const ckr_freq_table* t, const CanonKs& ck, ckr::CanonArg* a) {
             sb[d] = v;
         }
     }
-    return true;
 }
 
-hipError_t canon_launch(const ckr_freq_table* t, const ckr::EncSym* enc, const CanonKs& ck, uint32_t* canon,
-                        hipStream_t s) {
+// Stores the host-computed entries with small kernels whose arguments carry
+// them (CANON_ARG_DWORDS each: one launch for units up to 64 KiB).
+hipError_t canon_launch(const ckr_freq_table* t, const CanonKs& ck, uint32_t* canon, hipStream_t s) {
+    std::vector<uint32_t> w;
+    canon_host(t, ck, w);
     ckr::CanonArg a;
-    if (canon_host(t, ck, &a)) return ckr::launch_canon_store(a, canon, s);
-    return ckr::launch_canon(enc, ck.k0, ck.k1, ck.k2, ck.cw, canon, s);
+    for (size_t off = 0; off < w.size(); off += ckr::CANON_ARG_DWORDS) {
+        a.n = (uint32_t)std::min<size_t>(ckr::CANON_ARG_DWORDS, w.size() - off);
+        a.off = (uint32_t)off;
+        std::copy(w.begin() + off, w.begin() + off + a.n, a.w);
+        const hipError_t e = ckr::launch_canon_store(a, canon, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 bool use_fast_encode(const ckr::EncodeGeom& g) { return use_dedup(g) && (g.unit + 255) / 256 <= kFastMaxK; }
@@ -249,7 +254,7 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
 
 // Decode workspace: enc table, canonical streams, decode table, bad-lane counter.
 struct DecodeLayout {
-    uint64_t off_enc, off_canon, off_dec, off_bad, total;
+    uint64_t off_canon, off_dec, off_bad, total;
     bool fast;
 };
 DecodeLayout decode_layout(const ckr::EncodeGeom& g) {
@@ -257,7 +262,6 @@ DecodeLayout decode_layout(const ckr::EncodeGeom& g) {
     const CanonKs ck = canon_ks(g);
     L.fast = g_fast_paths != 0 && g.spe > 0 && g.n_units > 0 && use_dedup(g);
     uint64_t o = 0;
-    L.off_enc = o;   o = align_up(o + 256 * sizeof(ckr::EncSym), kAlign);
     L.off_canon = o; o = align_up(o + (L.fast ? 3ull * (4 + 2 * ck.cw) * 4 : 0), kAlign);
     L.off_dec = o;   o = align_up(o + 4096 * 4, kAlign);
     L.off_bad = o;   o = align_up(o + 8, kAlign);
@@ -572,7 +576,7 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
     const CanonKs ck = canon_ks(g);
     uint8_t* side = g.spe ? d_sidecar : nullptr;
     CKR_HIP(ckr::launch_build_enc_table(ta, enc, s));
-    if (dedup) CKR_HIP(canon_launch(h_table, enc, ck, canon, s));
+    if (dedup) CKR_HIP(canon_launch(h_table, ck, canon, s));
 
     bool fast = use_fast_encode(g);
     ckr::FastEncParamsHost fp{};
@@ -698,16 +702,12 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
     if (!table_arg(h_table, &ta)) return CKR_E_TABLE;
     hipStream_t s = (hipStream_t)stream;
     uint8_t* ws = static_cast<uint8_t*>(d_workspace);
-    auto* enc = reinterpret_cast<ckr::EncSym*>(ws + L.off_enc);
     auto* canon = reinterpret_cast<uint32_t*>(ws + L.off_canon);
     auto* dec = reinterpret_cast<uint32_t*>(ws + L.off_dec);
     auto* bad = reinterpret_cast<unsigned long long*>(ws + L.off_bad);
     const CanonKs ck = canon_ks(g);
     CKR_HIP(ckr::launch_build_dec_table(ta, dec, s));
-    if (L.fast) {
-        CKR_HIP(ckr::launch_build_enc_table(ta, enc, s));
-        CKR_HIP(canon_launch(h_table, enc, ck, canon, s));
-    }
+    if (L.fast) CKR_HIP(canon_launch(h_table, ck, canon, s));
     CKR_HIP(ckr::launch_set_counter(bad, 0, s));
     CKR_HIP(ckr::launch_decode(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, static_cast<uint8_t*>(d_dst),
                                bad, L.fast ? canon : nullptr, ck.cw, s));

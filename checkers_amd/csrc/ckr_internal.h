@@ -99,17 +99,14 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
 // Canonical zero-plane streams for lane counts k0, k1, k2: 3 entries of 4 + cw
 // dwords (header, then the stream in slot format), followed by the 3 streams in
 // byte order (cw dwords each).
-// The same entries when the host has computed them (n dwords, at most
-// CANON_ARG_DWORDS: units of up to 64 KiB), stored by one small kernel whose
-// argument carries them.
+// The same entries when the host has computed them, stored by small kernels
+// whose argument carries n <= CANON_ARG_DWORDS of them, for canon[off .. off + n).
 static constexpr uint32_t CANON_ARG_DWORDS = 900;
 struct CanonArg {
-    uint32_t n;
+    uint32_t n, off;
     uint32_t w[CANON_ARG_DWORDS];
 };
 hipError_t launch_canon_store(const CanonArg& a, uint32_t* canon, hipStream_t s);
-hipError_t launch_canon(const EncSym* d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw, uint32_t* canon,
-                        hipStream_t s);
 
 // Decode; with canon (masked dtypes) the fast kernel decodes every unit,
 // otherwise the general kernel does.

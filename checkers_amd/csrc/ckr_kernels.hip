@@ -303,58 +303,9 @@ __device__ __forceinline__ uint32_t lane_bytes(const LaneOut& o) { return o.w * 
 // zero bytes from state L whatever the data, so its stream depends only on K
 // and the table: it is coded once per distinct K (at most three per tensor:
 // full units, and the two lane counts of the last unit) instead of once per
-// lane.  Entry i: {K, final_state, byte_count, pad} then cw dword slots.
-// Wave i codes entry i into LDS (K <= CANON_MAX_K) with wave-uniform values,
-// so the serial state chain runs on the scalar unit; the block then writes the
-// slots and the byte-order copies out together.
-static constexpr uint32_t CANON_MAX_K = 4096;
-static constexpr uint32_t CANON_MAX_CW = (2 * CANON_MAX_K + 3) / 4 + 1;
-
-__global__ void __launch_bounds__(256) canon_kernel(const EncSym* __restrict__ d_enc, uint32_t k0, uint32_t k1,
-                                                    uint32_t k2, uint32_t cw, uint32_t* __restrict__ canon) {
-    __shared__ uint32_t slots[3][CANON_MAX_CW];
-    __shared__ uint32_t meta[3][2];  // final state, byte count
-    const uint32_t t = threadIdx.x;
-    const uint32_t wv = __builtin_amdgcn_readfirstlane(t >> 6);
-    if (wv < 3) {
-        const EncSym e0 = d_enc[0];  // every symbol is 0: its entry stays in registers
-        const uint32_t K = __builtin_amdgcn_readfirstlane(wv == 0 ? k0 : (wv == 1 ? k1 : k2));
-        LaneOut o;
-        lane_init(o);
-        for (uint32_t k = 0; k < K; k++) encode_symbol<1>(o, 0u, &e0, slots[wv]);
-        lane_flush<1>(o, slots[wv]);
-        if ((t & 63) == 0) {
-            meta[wv][0] = o.x;
-            meta[wv][1] = lane_bytes(o);
-        }
-    }
-    __syncthreads();
-    for (uint32_t e = 0; e < 3; e++) {
-        uint32_t* base = canon + (uint64_t)e * (4 + cw);
-        uint32_t* sb = canon + 3ull * (4 + cw) + (uint64_t)e * cw;  // the stream in byte order
-        const uint32_t B = meta[e][1], W = B >> 2, r = B & 3;
-        if (t == 0) {
-            base[0] = e == 0 ? k0 : (e == 1 ? k1 : k2);
-            base[1] = meta[e][0];
-            base[2] = B;
-            base[3] = 0;
-        }
-        for (uint32_t d = t; d < cw; d += blockDim.x) {
-            base[4 + d] = (d < W || (d == W && r)) ? slots[e][d] : 0u;
-            uint32_t v = 0;
-            for (uint32_t b = 0; b < 4; b++) {
-                const uint32_t q = 4 * d + b;
-                if (q >= B) break;
-                uint32_t slot, byte;
-                if (q < r) { slot = W; byte = q; }
-                else { slot = W - 1 - ((q - r) >> 2); byte = (q - r) & 3; }
-                v |= ((slots[e][slot] >> (8 * byte)) & 255u) << (8 * b);
-            }
-            sb[d] = v;
-        }
-    }
-}
-
+// lane, on the host, and stored with launch_canon_store.  Entry i: {K,
+// final_state, byte_count, pad} then cw dword slots (the encoder's lane slot
+// order); after the three entries, the three streams in byte order.
 __device__ __forceinline__ const uint32_t* canon_entry(const uint32_t* canon, uint32_t cw, uint32_t K) {
     // entries hold distinct K values except when two coincide; first match wins
     if (canon[0] == K) return canon;
@@ -615,19 +566,12 @@ __global__ void __launch_bounds__(256) compact_kernel(const uint8_t* __restrict_
 }
 
 __global__ void __launch_bounds__(256) canon_store_kernel(CanonArg a, uint32_t* __restrict__ canon) {
-    for (uint32_t i = threadIdx.x; i < a.n; i += blockDim.x) canon[i] = a.w[i];
+    for (uint32_t i = threadIdx.x; i < a.n; i += blockDim.x) canon[a.off + i] = a.w[i];
 }
 
 hipError_t launch_canon_store(const CanonArg& a, uint32_t* canon, hipStream_t s) {
     if (a.n > CANON_ARG_DWORDS) return hipErrorInvalidValue;
     CKR_LAUNCH("canon_store_kernel", s, canon_store_kernel<<<1, 256, 0, s>>>(a, canon));
-    return hipGetLastError();
-}
-
-hipError_t launch_canon(const EncSym* d_enc, uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw, uint32_t* canon,
-                        hipStream_t s) {
-    if (cw > CANON_MAX_CW || k0 > CANON_MAX_K || k1 > CANON_MAX_K || k2 > CANON_MAX_K) return hipErrorInvalidValue;
-    CKR_LAUNCH("canon_kernel", s, canon_kernel<<<1, 256, 0, s>>>(d_enc, k0, k1, k2, cw, canon));
     return hipGetLastError();
 }
 

@@ -233,3 +233,31 @@ def test_decode_from_relocated_stream(dt, n, unit, gen, shift, gpu):
     torch.cuda.synchronize()
     assert bad == 0
     assert np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
+
+
+def test_histogram_counts_wrap_like_reference(gpu):
+    """Counts are uint32 and wrap modulo 2^32 past 4 Gi occurrences of one byte
+    value, as the reference's g_hist does (src/ANSCompressor.cpp:109-126,
+    uint32_t atomicAdd); the table is then normalised from the wrapped counts
+    (src/ANSCompressor.cpp:416-451).  6.4 GB bf16: a seeded prefix, zeros after."""
+    import torch
+    ck = _ck()
+    n, m = (1 << 31) + (1 << 30) + 12345, 1 << 20
+    print(f"[case] hist wrap bf16 n={n}", flush=True)
+    pat = dg.normal_bf16(m, 0.02, 5)
+    masked, _ = oc.extract_mantissa(pat, m, dg.BF16)
+    want = oc.byte_hist(masked).astype(np.uint64)
+    want[0] += 2 * (n - m)
+    want = (want % (1 << 32)).astype(np.uint32)
+    assert int(want[0]) != 2 * (n - m) + int(oc.byte_hist(masked)[0])  # the case does wrap
+    t = torch.zeros(n, dtype=torch.int16, device=gpu)
+    t[:m].copy_(torch.from_numpy(pat.view(np.int16).copy()))
+    h = ck.byte_histogram(t, dg.BF16, n_elems=n)
+    torch.cuda.synchronize()
+    del t
+    got = h.cpu().numpy().view(np.uint32)
+    assert np.array_equal(got, want)
+    tab, tsum = ck.build_table(got)
+    ref, rsum = oc.normalize_histogram(want)
+    assert np.array_equal(tab.norm, ref["norm_freq"]) and np.array_equal(tab.cum, ref["cum_freq"])
+    assert tsum == rsum  # 4115 here: the reference's over-full table for a dominant symbol
