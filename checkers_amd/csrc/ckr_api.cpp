@@ -184,6 +184,8 @@ hipError_t canon_launch(const ckr_freq_table* t, const CanonKs& ck, uint32_t* ca
 }
 
 bool use_fast_encode(const ckr::EncodeGeom& g) { return use_dedup(g) && (g.unit + 255) / 256 <= kFastMaxK; }
+// Units above 64 KiB (up to the dedup limit): the two-pass kernels.
+bool use_seg_encode(const ckr::EncodeGeom& g) { return use_dedup(g) && (g.unit + 255) / 256 > kFastMaxK; }
 
 int max_lds_per_block() {
     static int v = -1;
@@ -228,7 +230,7 @@ uint32_t lane_slot_bytes(const uint32_t* plane_hist, const ckr_freq_table* t, ui
 // look-back state and redo list, and lane scratch for general-kernel batches
 // (sized for the whole tensor's units, capped by kScratchBudget).
 struct EncodeLayout {
-    uint64_t off_enc, off_hist, off_canon, off_status, off_ctl, off_redo, off_usize, off_scratch, total;
+    uint64_t off_enc, off_hist, off_canon, off_status, off_ctl, off_redo, off_usize, off_rec, off_aux, off_scratch, total;
     uint64_t batch_units;
 };
 
@@ -246,8 +248,11 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     L.off_status = o;  o = align_up(o + ckr::encode_fast_status_words(g.n_units) * 8, kAlign);
     L.off_ctl = o;     o = align_up(o + 16, kAlign);
     L.off_redo = o;    o = align_up(o + g.n_units * 4, kAlign);
-    L.off_usize = o;   o = align_up(o + bu * 4, kAlign);
-    L.off_scratch = o; o = align_up(o + bu * per_unit, kAlign);
+    const bool seg = use_seg_encode(g);  // two passes: checkpoint records instead of lane scratch
+    L.off_usize = o;   o = align_up(o + (seg ? g.n_units : bu) * 4, kAlign);
+    L.off_rec = o;     o = align_up(o + (seg ? g.n_units * ckr::encode_seg_segments(g.unit) * 128 * 8 : 0), kAlign);
+    L.off_aux = o;     o = align_up(o + (seg ? 512 : 0), kAlign);
+    L.off_scratch = o; o = align_up(o + (seg ? 0 : bu * per_unit), kAlign);
     L.total = o;
     return L;
 }
@@ -578,17 +583,31 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
     CKR_HIP(ckr::launch_build_enc_table(ta, enc, s));
     if (dedup) CKR_HIP(canon_launch(h_table, ck, canon, s));
 
+    // escapes are possible unless the data's own live-plane histograms show
+    // every symbol it contains has a slot
+    bool escapes = true;
+    if (h_planes) {
+        escapes = false;
+        for (int s2 = 0; s2 < 256; s2++)
+            if ((h_planes[s2] || h_planes[256 + s2]) && !h_table->norm_freq[s2]) escapes = true;
+    }
+    if (use_seg_encode(g)) {
+        auto* rec = reinterpret_cast<uint2*>(ws + L.off_rec);
+        auto* aux = reinterpret_cast<uint32_t*>(ws + L.off_aux);
+        CKR_HIP(ckr::launch_encode_seg(static_cast<const uint8_t*>(d_src), g, enc, canon, ck.cw, escapes, rec,
+                                       d_headers, usize, d_unit_offsets, side, d_out, aux, s));
+        uint32_t herr = 0;
+        CKR_HIP(hipMemcpyAsync(&herr, aux, 4, hipMemcpyDeviceToHost, s));
+        if (h_total_out) CKR_HIP(hipMemcpyAsync(h_total_out, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
+        CKR_HIP(hipStreamSynchronize(s));
+        if (herr) return fail(CKR_E_HIP, "[ckr] two-pass encode: a segment did not end at its checkpoint");
+        return CKR_OK;
+    }
+
     bool fast = use_fast_encode(g);
     ckr::FastEncParamsHost fp{};
     if (fast) {
-        // with the data's own live-plane histograms at hand, escapes are excluded
-        // when every symbol they contain has a slot
-        fp.escapes = true;
-        if (h_planes) {
-            fp.escapes = false;
-            for (int s2 = 0; s2 < 256; s2++)
-                if ((h_planes[s2] || h_planes[256 + s2]) && !h_table->norm_freq[s2]) fp.escapes = true;
-        }
+        fp.escapes = escapes;
         const uint32_t K = (uint32_t)((g.unit + 255) / 256);
         fp.cw = ck.cw;
         const uint32_t cbmax = std::max(canon_stream_bytes(h_table, ck.k0),

@@ -96,6 +96,15 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
                               uint8_t* sidecar, uint8_t* out, uint64_t* unit_off, uint64_t* status, uint32_t* ctl,
                               uint32_t* redo_list, hipStream_t s);
 
+// Units above 64 KiB of masked dtypes, in two passes (no lane scratch): rec
+// holds n_units * encode_seg_segments(unit) * 128 checkpoint records, unit_size
+// n_units words, aux 128 words (aux[0]: nonzero when a segment did not end where
+// its checkpoints say, which would be a bug).
+uint32_t encode_seg_segments(uint64_t unit);
+hipError_t launch_encode_seg(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
+                             uint32_t cw, bool escapes, uint2* rec, ckr_stream_header* hdrs, uint32_t* unit_size,
+                             uint64_t* unit_off, uint8_t* sidecar, uint8_t* out, uint32_t* aux, hipStream_t s);
+
 // Canonical zero-plane streams for lane counts k0, k1, k2: 3 entries of 4 + cw
 // dwords (header, then the stream in slot format), followed by the 3 streams in
 // byte order (cw dwords each).

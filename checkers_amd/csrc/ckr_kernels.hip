@@ -1327,6 +1327,532 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
     return e;
 }
 
+// ------------------------------------------------------------------ large units: two passes
+// Units of more than 256 rows (above 64 KiB) of masked dtypes.  A lane's
+// stream is one serial state chain over every row of its unit, but running the
+// chain needs none of its output.  Pass 1 (seg_size_kernel, one wave per unit)
+// runs it for both live lanes of every column, counting renorm bytes, and
+// records each lane's state and byte count at the entry of every SEG_ROWS-row
+// segment; at the end it knows every lane's size, so it writes the headers
+// (lane offsets, passthrough decision) and the unit size.  After the scan of
+// unit sizes, pass 2 (seg_code_kernel, one wave per segment) codes every
+// segment from its recorded state straight into its place: within a lane's
+// stream, segment s's bytes are [total - E(s-1), total - E(s)) from its start,
+// E(s) being the bytes the rows above segment s emit, E(-1) = total.  No lane
+// scratch, and units x segments independent work items.
+static constexpr uint32_t SEG_ROWS = 256;
+
+__host__ __device__ constexpr uint32_t seg_count(uint64_t unit) {
+    return (uint32_t)((unit + 256ull * SEG_ROWS - 1) / (256ull * SEG_ROWS));
+}
+
+// enc_step's state update without the bytes: returns how many it emits.
+template <bool ESC>
+__device__ __forceinline__ uint32_t seg_size_step(uint32_t& x, uint4 t) {
+    const uint32_t f8 = t.w;
+    uint32_t n = ((x >> 24) >= f8) ? 2u : (((x >> 16) >= f8) ? 1u : 0u);
+    const uint32_t xr = x >> (8u * n);
+    const uint32_t q = __umulhi(xr, t.x) >> (t.y >> 24);
+    const uint32_t xn = xr + t.z + __umul24(q, t.y);
+    if (ESC) {
+        const bool esc = f8 == 0u;
+        n = esc ? 1u : n;
+        x = esc ? x : xn;
+    } else {
+        x = xn;
+    }
+    return n;
+}
+
+__device__ __forceinline__ void seg_load_table(uint4* tab, const EncSym* d_enc) {
+    const uint4 tv = reinterpret_cast<const uint4*>(d_enc)[threadIdx.x];
+    const EncSym e = {tv.x, tv.y, tv.z, tv.w};
+    tab[threadIdx.x] = enc_quad(e);
+}
+
+// Index (0..2) of the canonical entry for K symbols (see canon_entry).
+__device__ __forceinline__ uint32_t canon_index(const uint32_t* canon, uint32_t cw, uint32_t K) {
+    return canon[0] == K ? 0u : (canon[4 + cw] == K ? 1u : 2u);
+}
+
+// Checkpoint records: rec[((u * S + s) * 2 + p) * 64 + j] = {state, bytes
+// emitted so far} of live lane p (0: byte FL, 1: byte 3) of column j at the
+// entry of segment s (before its top row is coded).
+template <int SPE, bool ESC>
+__global__ void __launch_bounds__(256) seg_size_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
+                                                       const EncSym* __restrict__ d_enc,
+                                                       const uint32_t* __restrict__ canon, uint32_t cw, uint32_t S,
+                                                       uint2* __restrict__ rec, ckr_stream_header* __restrict__ hdrs,
+                                                       uint32_t* __restrict__ unit_size, uint32_t* __restrict__ err) {
+    __shared__ uint4 tab[256];
+    seg_load_table(tab, d_enc);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *err = 0;  // pass 2 runs after this grid
+    __syncthreads();
+    constexpr int FL = SPE == 2 ? 2 : 1;
+    constexpr uint32_t SH0 = 8u * FL;
+    const uint32_t j = threadIdx.x & 63;
+    const uint64_t u = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (u >= g.n_units) return;
+    const uint64_t ubase = u * g.unit;
+    const uint32_t len = (uint32_t)((g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit);
+    const uint32_t kf = len >> 8, r = len & 255u, K = kf + (r ? 1u : 0u);
+    uint32_t x0 = L, x1 = L, e0 = 0, e1 = 0;
+    uint2* ur = rec + u * S * 128 + j;
+    auto record = [&](uint32_t s) {
+        ur[s * 128] = make_uint2(x0, e0);
+        ur[s * 128 + 64] = make_uint2(x1, e1);
+    };
+    record((K - 1) / SEG_ROWS);
+    if (r) {  // the tensor's partial top row: lane 4j + b holds a byte when 4j + b < r
+        const uint8_t* p = src + ubase + 256ull * kf + 4 * j;
+        if (4 * j + FL < r) e0 += seg_size_step<ESC>(x0, tab[p[FL]]);
+        if (4 * j + 3 < r) e1 += seg_size_step<ESC>(x1, tab[p[3]]);
+        if (kf && kf % SEG_ROWS == 0) record(kf / SEG_ROWS - 1);
+    }
+    const uint32_t* in32 = reinterpret_cast<const uint32_t*>(src + ubase) + j;  // row k at in32[64 k]
+    const uint32_t ng = kf >> 5;
+    for (int32_t k = (int32_t)kf - 1; k >= (int32_t)(32 * ng); k--) {
+        const uint32_t wd = in32[64 * k];
+        const uint4 t0 = tab[(wd >> SH0) & 255u], t1 = tab[wd >> 24];
+        e0 += seg_size_step<ESC>(x0, t0);
+        e1 += seg_size_step<ESC>(x1, t1);
+        if (k && k % SEG_ROWS == 0) record(k / SEG_ROWS - 1);
+    }
+    if (ng) {
+        // groups of 32 rows from the top down, the next group's loads in flight
+        // while the current one is coded; table entries read 4 rows ahead
+        auto load = [&](uint32_t (&rr)[32], uint32_t gi) {
+            const uint32_t* p = in32 + 64 * (32 * gi + 31);
+#pragma unroll
+            for (int i = 0; i < 32; i++) rr[i] = p[-64 * i];
+        };
+        auto code = [&](const uint32_t (&rr)[32], uint32_t gi) {
+            uint4 ta[2][4], tb[2][4];
+            auto fetch = [&](int buf, int i0) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    ta[buf][i] = tab[(rr[i0 + i] >> SH0) & 255u];
+                    tb[buf][i] = tab[rr[i0 + i] >> 24];
+                }
+            };
+            fetch(0, 0);
+#pragma unroll
+            for (int bt = 0; bt < 8; bt++) {
+                if (bt < 7) fetch((bt + 1) & 1, 4 * (bt + 1));
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    e0 += seg_size_step<ESC>(x0, ta[bt & 1][i]);
+                    e1 += seg_size_step<ESC>(x1, tb[bt & 1][i]);
+                }
+            }
+            const uint32_t k = 32 * gi;  // the row just coded
+            if (k && k % SEG_ROWS == 0) record(k / SEG_ROWS - 1);
+        };
+        uint32_t ra[32], rb[32];
+        uint32_t gi = ng - 1;
+        load(ra, gi);
+        for (;;) {
+            if (gi == 0) { code(ra, 0); break; }
+            load(rb, gi - 1);
+            code(ra, gi);
+            gi--;
+            if (gi == 0) { code(rb, 0); break; }
+            load(ra, gi - 1);
+            code(rb, gi);
+            gi--;
+        }
+    }
+    // headers: the live lanes' sizes and final states, the zero-plane lanes'
+    // canonical ones; lane offsets by a wave scan; passthrough when the packed
+    // unit would not be smaller (ANSCompressor.cpp:694-713)
+    uint32_t c[4], fs[4];
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        if (b == FL) { c[b] = e0; fs[b] = x0; }
+        else if (b == 3) { c[b] = e1; fs[b] = x1; }
+        else {
+            const uint32_t Kb = kf + ((4 * j + b < r) ? 1u : 0u);
+            const uint32_t* ce = canon_entry(canon, cw, Kb);
+            fs[b] = ce[1];
+            c[b] = ce[2];
+        }
+    }
+    const uint32_t tsum = c[0] + c[1] + c[2] + c[3];
+    uint32_t incl = tsum;
+#pragma unroll
+    for (uint32_t d = 1; d < 64; d <<= 1) {
+        const uint32_t v = __shfl_up(incl, d, 64);
+        if (j >= d) incl += v;
+    }
+    const uint32_t total = __shfl(incl, 63, 64);
+    const bool raw = total >= len;
+    uint32_t off = incl - tsum;
+    ckr_stream_header* uh = hdrs + u * 256 + 4 * j;
+#pragma unroll
+    for (int b = 0; b < 4; b++) {
+        ckr_stream_header h;
+        h.final_state = raw ? 0u : fs[b];
+        h.byte_count = raw ? ((j == 0 && b == 0) ? len : 0u) : c[b];
+        h.buf_offset = raw ? 0u : off;
+        h.pad = 0;
+        uh[b] = h;
+        off += c[b];
+    }
+    if (j == 0) unit_size[u] = raw ? len : total;
+}
+
+// A live lane of pass 2: the coder window of EncLane, whose dwords go into an
+// LDS line buffer of SEG_LINE bytes indexed by their address in memory (ud +
+// offset) mod SEG_LINE; a run's bytes are written to memory a whole line at a
+// time (measured: dword stores straight to memory, each lane filling its line
+// over ~100 rows, wrote 4.4x the bytes out of L2).  The run's end e
+// may be unaligned: a = -e mod 4 (in memory) phantom bytes prime the window, so
+// every flush is an aligned dword.  A store that is not a flush (fewer than 4
+// bytes pending) lands in the buffer at the next dword, which a later flush
+// overwrites (or which the final copy does not read).
+static constexpr uint32_t SEG_LINE = 64;  // bytes a line buffer holds (a multiple of 16)
+
+struct SegLane {
+    EncLane c;
+    int32_t go;    // next dword to flush (offset from the unit's output base, aligned in memory)
+    int32_t rs;    // the run's first byte
+    int32_t e;     // one past its last byte
+    int32_t lc;    // start of the lowest line written out (e until one is)
+    uint32_t lb;   // LDS byte address of the line buffer
+};
+
+__device__ __forceinline__ void seg_lane_init(SegLane& l, uint32_t x, int32_t rs, int32_t e, uint32_t ua, uint32_t lb) {
+    const uint32_t a = (0u - (ua + (uint32_t)e)) & 3u;
+    l.c.x = x;
+    l.c.hi = 0;
+    l.c.lo = 0;
+    l.c.sel = 0x08090A0Bu - a * 0x01010101u;
+    l.c.ptr = 0;
+    l.go = e + (int32_t)a - 4;
+    l.rs = rs;
+    l.e = e;
+    l.lc = e;
+    l.lb = lb;
+}
+
+// Bytes [lo, hi) of one line (offsets from ud) from the lane's line buffer to
+// memory: dword stores where a whole aligned dword is inside, byte stores else.
+__device__ __attribute__((noinline)) void seg_line_bytes(const uint8_t* lds8, uint32_t lb, uint32_t ua, uint8_t* ud,
+                                                         int32_t lo, int32_t hi) {
+    for (int32_t d = lo - (int32_t)((ua + (uint32_t)lo) & 3u); d < hi; d += 4) {
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(lds8 + lb + ((ua + (uint32_t)d) & (SEG_LINE - 1)));
+        if (d >= lo && d + 4 <= hi) *reinterpret_cast<uint32_t*>(ud + d) = v;
+        else
+            for (int32_t b = 0; b < 4; b++)
+                if (d + b >= lo && d + b < hi) ud[d + b] = (uint8_t)(v >> (8 * b));
+    }
+}
+
+// One flush.  Returns the line start (offset) when this flush completed a
+// line (wrote its first dword), else INT32_MIN.
+__device__ __forceinline__ int32_t seg_flush(SegLane& l, uint8_t* lds8, uint32_t ua) {
+    const uint32_t v = __builtin_amdgcn_perm(l.c.hi, l.c.lo, l.c.sel);
+    const bool fl = (l.c.sel & 8u) == 0u;
+    const uint32_t o = (ua + (uint32_t)l.go) & (SEG_LINE - 1);
+    *reinterpret_cast<uint32_t*>(lds8 + l.lb + o) = v;
+    const int32_t done = (fl && o == 0u) ? l.go : INT32_MIN;
+    l.go -= fl ? 4 : 0;
+    l.c.sel += fl ? 0x04040404u : 0u;
+    return done;
+}
+
+// After the flushes of a step: lines completed by them go out.  A line wholly
+// inside its run goes out as 16-byte stores, the wave copying 64 / (SEG_LINE /
+// 16) such lines per round; the run's top line, which shares bytes with the
+// next run, goes out byte-exact by its own thread.
+struct SegCopyEnt { uint32_t lb; int32_t g; };
+__device__ __forceinline__ void seg_lines_out(SegLane& l0, SegLane& l1, int32_t d0, int32_t d1, uint8_t* lds8,
+                                              SegCopyEnt* tbl, uint32_t ua, uint8_t* ud, uint32_t j) {
+    const bool f0 = d0 != INT32_MIN && d0 + (int32_t)SEG_LINE <= l0.e;
+    const bool f1 = d1 != INT32_MIN && d1 + (int32_t)SEG_LINE <= l1.e;
+    if (d0 != INT32_MIN) { if (!f0) seg_line_bytes(lds8, l0.lb, ua, ud, d0, l0.e); l0.lc = d0; }
+    if (d1 != INT32_MIN) { if (!f1) seg_line_bytes(lds8, l1.lb, ua, ud, d1, l1.e); l1.lc = d1; }
+    const uint64_t m0 = __ballot(f0), m1 = __ballot(f1);
+    if ((m0 | m1) == 0) return;
+    const uint32_t n0 = (uint32_t)__popcll(m0), n = n0 + (uint32_t)__popcll(m1);
+    const uint64_t below = (1ull << j) - 1ull;
+    if (f0) tbl[__popcll(m0 & below)] = SegCopyEnt{l0.lb, d0};
+    if (f1) tbl[n0 + __popcll(m1 & below)] = SegCopyEnt{l1.lb, d1};
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    constexpr uint32_t TPL = SEG_LINE / 16;  // threads per line
+    for (uint32_t k0 = 0; k0 < n; k0 += 64 / TPL) {
+        const uint32_t k = k0 + j / TPL, c = j % TPL;
+        if (k < n) {
+            const SegCopyEnt t = tbl[k];
+            const uint4 v = *reinterpret_cast<const uint4*>(lds8 + t.lb + 16 * c);
+            *reinterpret_cast<uint4*>(ud + t.g + 16 * c) = v;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// End of the item: the last flush, the pending bytes (the run's first ones)
+// into the buffer, and the bytes below the lowest line written out.  True when
+// they end exactly at the run start.
+__device__ __forceinline__ bool seg_finish_lane(SegLane& l, uint8_t* lds8, uint32_t ua, uint8_t* ud) {
+    const uint32_t P = 0x0Bu - (l.c.sel & 0xFFu);  // < 4 after the last flush
+    const uint32_t v = __builtin_amdgcn_perm(l.c.hi, l.c.lo, l.c.sel);  // its top P bytes
+    *reinterpret_cast<uint32_t*>(lds8 + l.lb + ((ua + (uint32_t)l.go) & (SEG_LINE - 1))) = v;
+    const bool ok = l.go + 4 - (int32_t)P == l.rs && l.lc - l.rs <= (int32_t)SEG_LINE;
+    if (ok && l.rs < l.lc) seg_line_bytes(lds8, l.lb, ua, ud, l.rs, l.lc);
+    return ok;
+}
+
+// n bytes of a dword-aligned byte stream (readable for one dword past its end)
+// to dst by one thread: aligned dword stores, byte stores at the two ends.
+__device__ __forceinline__ void seg_copy_thread(uint8_t* dst, const uint32_t* src32, uint32_t n) {
+    if (n == 0) return;
+    const uint32_t lead = (uint32_t)(reinterpret_cast<uintptr_t>(dst) & 3u);
+    uint8_t* d0 = dst - lead;
+    const uint32_t nd = (lead + n + 3) >> 2;  // src32[0 .. nd) are read: nd - 1 <= (n + 2) / 4
+    // dword i of dst's aligned span holds stream bytes 4i - lead .. 4i - lead + 3
+    uint32_t prev = 0;
+    for (uint32_t i0 = 0; i0 < nd; i0 += 8) {
+        uint32_t w[8];
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) w[k] = i0 + k < nd ? src32[i0 + k] : 0u;
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++) {
+            const uint32_t i = i0 + k;
+            if (i >= nd) break;
+            const uint32_t v = lead ? __builtin_amdgcn_alignbyte(w[k], prev, 4u - lead) : w[k];
+            const uint32_t b1 = 4 * i + 4 <= lead + n ? 4u : lead + n - 4 * i;
+            if ((i > 0 || lead == 0) && b1 == 4) *reinterpret_cast<uint32_t*>(d0 + 4 * i) = v;
+            else
+                for (uint32_t b = (i == 0 ? lead : 0u); b < b1; b++) d0[4 * i + b] = (uint8_t)(v >> (8 * b));
+            prev = w[k];
+        }
+    }
+}
+
+// LDS of seg_code_kernel: table | per wave: 128 line buffers of SEG_LINE bytes, then
+// 128 copy-table entries.
+static constexpr uint32_t SEG_WAVE_LDS = 128 * SEG_LINE + 128 * 8;
+static constexpr uint32_t SEG_LDS = 4096 + 4 * SEG_WAVE_LDS;
+
+// One wave per item of G consecutive segments [s0, s0 + G) of a unit, coded
+// from the top of segment s0 + G - 1 down.
+template <int SPE, bool ESC>
+__global__ void __launch_bounds__(256) seg_code_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
+                                                       const EncSym* __restrict__ d_enc,
+                                                       const uint32_t* __restrict__ canon, uint32_t cw, uint32_t S,
+                                                       uint32_t G, const uint2* __restrict__ rec,
+                                                       const ckr_stream_header* __restrict__ hdrs,
+                                                       const uint32_t* __restrict__ unit_size,
+                                                       const uint64_t* __restrict__ unit_off,
+                                                       uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out,
+                                                       uint32_t* __restrict__ aux) {
+    extern __shared__ uint4 seg_lds[];
+    uint4* tab = seg_lds;
+    uint8_t* lds8 = reinterpret_cast<uint8_t*>(seg_lds);
+    seg_load_table(tab, d_enc);
+    __syncthreads();
+    constexpr int FL = SPE == 2 ? 2 : 1;
+    constexpr uint32_t SH0 = 8u * FL;
+    const uint32_t j = threadIdx.x & 63;
+    const uint32_t wv = threadIdx.x >> 6;
+    // workgroups go round-robin over the 8 XCDs: those of one XCD take
+    // consecutive items, so the neighbouring runs of a lane share its L2
+    const uint32_t nb = gridDim.x, q8 = nb >> 3, r8 = nb & 7u, xcd = blockIdx.x & 7u;
+    const uint32_t lbk = xcd * q8 + min(xcd, r8) + (blockIdx.x >> 3);
+    const uint32_t ipu = (S + G - 1) / G;  // items per unit
+    const uint64_t item = (uint64_t)lbk * 4 + wv;
+    const uint64_t u = item / ipu;
+    const uint32_t s0 = (uint32_t)(item % ipu) * G;
+    if (u >= g.n_units) return;
+    const uint64_t ubase = u * g.unit;
+    const uint32_t len = (uint32_t)((g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit);
+    const uint32_t kf = len >> 8, r = len & 255u, K = kf + (r ? 1u : 0u);
+    const uint32_t Su = (K + SEG_ROWS - 1) / SEG_ROWS;
+    if (s0 >= Su) return;
+    const uint32_t s1 = min(s0 + G, Su) - 1;  // top segment of the item
+    const uint32_t lo = s0 * SEG_ROWS, hi = min((s1 + 1) * SEG_ROWS, K), fhi = min(hi, kf);
+    const bool ptop = r && hi == K;  // the partial row kf is the item's top row
+    uint8_t* ud = out + unit_off[u];
+    const uint32_t ua = (uint32_t)reinterpret_cast<uintptr_t>(ud);
+    const ckr_stream_header* uh = hdrs + u * 256;
+    const bool raw = unit_size[u] >= len;
+    const uint32_t* in32 = reinterpret_cast<const uint32_t*>(src + ubase) + j;  // row k at in32[64 k]
+    uint16_t* sc16 = reinterpret_cast<uint16_t*>(sidecar + (ubase >> 1) + 2 * j);  // row k at sc16[64 k]
+    auto side = [&](uint32_t k, uint32_t wd) {
+        sc16[64 * k] = (uint16_t)(SPE == 2 ? (wd & 0xFFFFu) : ((wd & 0xFFu) | ((wd >> 8) & 0xFF00u)));
+    };
+    const uint32_t lm = live_mask32<SPE>();
+    if (raw) {  // passthrough: the masked bytes, and the sidecar
+        const bool al = (ua & 3u) == 0;
+        for (uint32_t k = lo; k < fhi; k++) {
+            const uint32_t wd = in32[64 * k];
+            side(k, wd);
+            uint8_t* d = ud + 256 * k + 4 * j;
+            if (al) *reinterpret_cast<uint32_t*>(d) = wd & lm;
+            else
+                for (int b = 0; b < 4; b++) d[b] = (uint8_t)((wd & lm) >> (8 * b));
+        }
+        if (ptop && 4 * j < r) {
+            const uint8_t* p = src + ubase + 256ull * kf + 4 * j;
+            const uint32_t nv = min(r - 4 * j, 4u);
+            uint32_t wd = 0;
+            for (uint32_t b = 0; b < nv; b++) wd |= (uint32_t)p[b] << (8 * b);
+            write_sidecar_row<SPE>(sidecar, ubase + 256ull * kf + 4 * j, wd, nv);
+            for (uint32_t b = 0; b < nv; b++) ud[256 * kf + 4 * j + b] = (uint8_t)((wd & lm) >> (8 * b));
+        }
+        return;
+    }
+    const uint32_t wbase = 4096 + wv * SEG_WAVE_LDS;
+    SegCopyEnt* tbl = reinterpret_cast<SegCopyEnt*>(lds8 + wbase + 128 * SEG_LINE);
+    {
+        const ckr_stream_header h0 = uh[4 * j + FL], h1 = uh[4 * j + 3];
+        const uint2* rp = rec + (u * S + s1) * 128 + j;  // entry of the top segment
+        const uint2 c0 = rp[0], c1 = rp[64];
+        uint2 n0, n1;  // state and bytes after the item
+        if (s0) {
+            const uint2* rq = rec + (u * S + s0 - 1) * 128 + j;
+            n0 = rq[0];
+            n1 = rq[64];
+        } else {
+            n0 = make_uint2(h0.final_state, h0.byte_count);
+            n1 = make_uint2(h1.final_state, h1.byte_count);
+        }
+        SegLane l0, l1;
+        seg_lane_init(l0, c0.x, (int32_t)(h0.buf_offset + h0.byte_count - n0.y),
+                      (int32_t)(h0.buf_offset + h0.byte_count - c0.y), ua, wbase + SEG_LINE * j);
+        seg_lane_init(l1, c1.x, (int32_t)(h1.buf_offset + h1.byte_count - n1.y),
+                      (int32_t)(h1.buf_offset + h1.byte_count - c1.y), ua, wbase + SEG_LINE * (64 + j));
+        auto flush2 = [&]() {
+            const int32_t d0 = seg_flush(l0, lds8, ua);
+            const int32_t d1 = seg_flush(l1, lds8, ua);
+            seg_lines_out(l0, l1, d0, d1, lds8, tbl, ua, ud, j);
+        };
+        if (ptop) {
+            const uint8_t* p = src + ubase + 256ull * kf + 4 * j;
+            if (4 * j < r) {
+                const uint32_t nv = min(r - 4 * j, 4u);
+                uint32_t wd = 0;
+                for (uint32_t b = 0; b < nv; b++) wd |= (uint32_t)p[b] << (8 * b);
+                write_sidecar_row<SPE>(sidecar, ubase + 256ull * kf + 4 * j, wd, nv);
+            }
+            if (4 * j + FL < r) { const uint32_t sy = p[FL]; enc_step<ESC>(l0.c, sy, tab[sy]); }
+            if (4 * j + 3 < r) { const uint32_t sy = p[3]; enc_step<ESC>(l1.c, sy, tab[sy]); }
+            flush2();
+        }
+        auto row = [&](uint32_t k, uint32_t wd, uint4 t0, uint4 t1) {
+            side(k, wd);
+            enc_step<ESC>(l0.c, (wd >> SH0) & 255u, t0);
+            enc_step<ESC>(l1.c, wd >> 24, t1);
+        };
+        const uint32_t nf = fhi - lo, ng = nf >> 4;
+        for (int32_t k = (int32_t)fhi - 1; k >= (int32_t)(lo + 16 * ng); k--) {
+            const uint32_t wd = in32[64 * k];
+            row((uint32_t)k, wd, tab[(wd >> SH0) & 255u], tab[wd >> 24]);
+            flush2();
+        }
+        if (ng) {
+            // groups of 16 rows from the top down, the next group's loads in
+            // flight while the current one is coded; table entries 2 rows ahead
+            auto load = [&](uint32_t (&rr)[16], uint32_t gi) {
+                const uint32_t* p = in32 + 64 * (lo + 16 * gi + 15);
+#pragma unroll
+                for (int i = 0; i < 16; i++) rr[i] = p[-64 * i];
+            };
+            auto code = [&](const uint32_t (&rr)[16], uint32_t gi) {
+                const uint32_t ktop = lo + 16 * gi + 15;
+                uint4 ta[2][2], tb[2][2];
+                auto fetch = [&](int buf, int i0) {
+#pragma unroll
+                    for (int i = 0; i < 2; i++) {
+                        ta[buf][i] = tab[(rr[i0 + i] >> SH0) & 255u];
+                        tb[buf][i] = tab[rr[i0 + i] >> 24];
+                    }
+                };
+                fetch(0, 0);
+#pragma unroll
+                for (int bt = 0; bt < 8; bt++) {
+                    if (bt < 7) fetch((bt + 1) & 1, 2 * (bt + 1));
+                    row(ktop - 2 * bt, rr[2 * bt], ta[bt & 1][0], tb[bt & 1][0]);
+                    row(ktop - 2 * bt - 1, rr[2 * bt + 1], ta[bt & 1][1], tb[bt & 1][1]);
+                    flush2();
+                }
+            };
+            uint32_t ra[16], rb[16];
+            uint32_t gi = ng - 1;
+            load(ra, gi);
+            for (;;) {
+                if (gi == 0) { code(ra, 0); break; }
+                load(rb, gi - 1);
+                code(ra, gi);
+                gi--;
+                if (gi == 0) { code(rb, 0); break; }
+                load(ra, gi - 1);
+                code(rb, gi);
+                gi--;
+            }
+        }
+        flush2();
+        const bool ok0 = seg_finish_lane(l0, lds8, ua, ud) && l0.c.x == n0.x;
+        const bool ok1 = seg_finish_lane(l1, lds8, ua, ud) && l1.c.x == n1.x;
+        if (!(ok0 && ok1)) atomicOr(aux, 1u);
+    }
+    // the zero-plane lanes copy their canonical stream: thread j those of
+    // column j, in the unit's item j mod (items of the unit)
+    const uint32_t iu = (Su + G - 1) / G;
+    if (j % iu == s0 / G) {
+        const uint32_t* cbytes = canon + 3 * (4 + cw);
+        constexpr uint32_t ZB1 = SPE == 2 ? 1u : 2u;  // zero bytes of a column: 0 and ZB1
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t lane = 4 * j + (h ? ZB1 : 0u);
+            const ckr_stream_header hz = uh[lane];
+            const uint32_t Kb = kf + ((lane < r) ? 1u : 0u);
+            seg_copy_thread(ud + hz.buf_offset, cbytes + canon_index(canon, cw, Kb) * cw, hz.byte_count);
+        }
+    }
+}
+
+uint32_t encode_seg_segments(uint64_t unit) { return seg_count(unit); }
+
+hipError_t launch_encode_seg(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
+                             uint32_t cw, bool escapes, uint2* rec, ckr_stream_header* hdrs, uint32_t* unit_size,
+                             uint64_t* unit_off, uint8_t* sidecar, uint8_t* out, uint32_t* aux, hipStream_t s) {
+    const uint32_t S = seg_count(g.unit);
+    const uint32_t g1 = (uint32_t)((g.n_units + 3) / 4);
+    // segments per pass-2 item: whole units while there are units enough to
+    // fill the device (>= 4096 waves), fewer otherwise
+    const uint64_t G = std::max<uint64_t>(1, std::min<uint64_t>(S, g.n_units * S / 4096));
+    const uint64_t items = g.n_units * ((S + G - 1) / G);
+    const uint32_t g2 = (uint32_t)((items + 3) / 4);
+    hipError_t e;
+#define CKR_SEG(SPE_, ESC_)                                                                                         \
+    do {                                                                                                            \
+        CKR_LAUNCH("seg_size_kernel", s, seg_size_kernel<SPE_, ESC_><<<g1, 256, 0, s>>>(src, g, d_enc, canon, cw,    \
+                                                                                        S, rec, hdrs, unit_size, aux)); \
+        if ((e = hipGetLastError()) != hipSuccess) return e;                                                        \
+        CKR_LAUNCH("unit_scan_kernel", s, unit_scan_kernel<<<1, 1024, 0, s>>>(unit_size, 0, g.n_units, unit_off));  \
+        if ((e = hipGetLastError()) != hipSuccess) return e;                                                        \
+        if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(seg_code_kernel<SPE_, ESC_>),                    \
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)SEG_LDS)) != hipSuccess)      \
+            return e;                                                                                               \
+        CKR_LAUNCH("seg_code_kernel", s, seg_code_kernel<SPE_, ESC_><<<g2, 256, SEG_LDS, s>>>(src, g, d_enc, canon, \
+                   cw, S, (uint32_t)G, rec, hdrs, unit_size, unit_off, sidecar, out, aux));                         \
+        return hipGetLastError();                                                                                   \
+    } while (0)
+    if (g.spe == 2) {
+        if (escapes) CKR_SEG(2, true);
+        CKR_SEG(2, false);
+    }
+    if (escapes) CKR_SEG(1, true);
+    CKR_SEG(1, false);
+#undef CKR_SEG
+}
+
 // ------------------------------------------------------------------ rANS decode
 __device__ __forceinline__ uint32_t unit_len(const EncodeGeom& g, uint64_t ubase) {
     return (uint32_t)((g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit);

@@ -50,6 +50,9 @@ CASES = [
     ("random_bits_bf16", dg.BF16, 32768 * 2 + 6, 65536,
      lambda n: np.random.default_rng(14).integers(0, 2**16, n).astype(np.uint16)),
     ("f32_1mib_units", dg.F32, 262144 * 2 + 4097, 1 << 20, lambda n: dg.normal_f32(n, 1e-3, 15)),
+    ("f32_expavgsq_128k_units", dg.F32, 32832 * 4 + 100, 131328, lambda n: dg.exp_avg_sq(n, 17)),
+    ("bf16_1mib_units", dg.BF16, 524288 * 2 + 1111, 1 << 20, lambda n: dg.normal_bf16(n, 0.02, 18)),
+    ("bf16_256k_one_unit", dg.BF16, 131072, 262144, lambda n: dg.normal_bf16(n, 0.02, 19)),
     ("bf16_partial_units", dg.BF16, 3 * 512 + 1, 1024, lambda n: dg.normal_bf16(n, 0.02, 16)),
     ("tiny_f32_1", dg.F32, 1, 65536, lambda n: np.array([1.5], np.float32)),
     ("tiny_bf16_3", dg.BF16, 3, 0, lambda n: dg.normal_bf16(n, 0.02, 12)),
@@ -147,6 +150,48 @@ def test_passthrough_unit_with_mismatched_table(gpu):
     assert np.array_equal(enc.data_np(), data)
     assert np.array_equal(enc.headers_np()[: hdr.size], hdr)
     dst, bad = ck.decode(enc)
+    assert bad == 0 and np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
+
+
+@pytest.mark.parametrize("dt,unit,n", [
+    (dg.F32, 1 << 20, (1 << 18) * 3 + 5000),
+    (dg.F32, 131328, 32832 * 4 + 17),
+    (dg.BF16, 1 << 18, (1 << 17) * 2 + 333),
+])
+def test_large_units_with_foreign_table(dt, unit, n, paths, gpu):
+    """Units above 64 KiB under a table that does not fit the data: alternate
+    units expand (stored raw, ANSCompressor.cpp:694-713) and contain symbols
+    with f == 0 (raw-byte escape, :185-192)."""
+    import torch
+    ck = _ck()
+    es = 4 if dt == dg.F32 else 2
+    print(f"[case] large units foreign table dtype={dt} unit={unit} n={n} fast={paths}", flush=True)
+    rng = np.random.default_rng(50)
+    b = rng.integers(0, 256, (n, es), dtype=np.uint8)
+    cheap = (np.arange(n) // (unit // es)) % 2 == 0
+    for c in ([2, 3] if es == 4 else [1]):  # live bytes of the cheap units: symbols 1..8
+        b[cheap, c] = rng.integers(1, 9, int(cheap.sum()))
+    raw = b.reshape(-1).view(np.uint32 if es == 4 else np.uint16)
+    h = np.full(256, 16, np.uint32)
+    h[1:9] = 1000
+    h[200:] = 0
+    t_ck, s_ck = ck.build_table(h)
+    t_oc, s_oc = oc.normalize_histogram(h)
+    assert s_ck == s_oc == 4096
+    masked, side = oc.extract_mantissa(raw, n, dt)
+    data, hdr, off = oc.encode(masked, t_oc, unit)
+    sizes = np.diff(off.astype(np.int64))
+    lens = np.minimum(unit, n * es - unit * np.arange(sizes.size))
+    assert (sizes == lens).any() and (sizes < lens).any()  # both kinds of unit present
+    enc = ck.encode(_to_dev(raw, gpu), dt, t_ck, unit, n_elems=n)
+    torch.cuda.synchronize()
+    assert enc.total == data.size
+    assert np.array_equal(enc.unit_offsets[: off.size].cpu().numpy().view(np.uint64), off)
+    assert np.array_equal(enc.headers_np()[: hdr.size], hdr)
+    assert np.array_equal(enc.data_np(), data)
+    assert np.array_equal(enc.sidecar[: side.size].cpu().numpy(), side)
+    dst, bad = ck.decode(enc)
+    torch.cuda.synchronize()
     assert bad == 0 and np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
 
 
