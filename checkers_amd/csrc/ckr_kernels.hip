@@ -2288,21 +2288,30 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
             const ckr_stream_header h = uh[4 * j + b];
             bool ok = h.final_state == ce[1] && h.byte_count == ce[2] && (uint64_t)h.buf_offset + h.byte_count <= usize;
             if (ok) {
-                const uint8_t* cb = reinterpret_cast<const uint8_t*>(cbytes + (uint64_t)ent * cw);
+                const uint32_t* cp = cbytes + (uint64_t)ent * cw;
+                const uint8_t* cb = reinterpret_cast<const uint8_t*>(cp);
                 const uint8_t* sl = ud + h.buf_offset;
-                uint32_t diff = 0;
-                uint32_t q = 0;
-                // stream dwords (any alignment, from the aligned dwords around them,
-                // which lie in the data buffer) against the canonical dwords
-                for (; q + 4 <= h.byte_count; q += 4) {
-                    const uintptr_t a = reinterpret_cast<uintptr_t>(sl + q);
-                    const uintptr_t aa = a & ~(uintptr_t)3;
-                    if (aa < d0 || aa + 8 > d1) break;  // the rest byte by byte
-                    const uint32_t* ap = data32_at(data, aa - d0);
-                    const uint32_t sh = (uint32_t)(a & 3u);
-                    diff |= __builtin_amdgcn_alignbyte(ap[1], ap[0], sh) ^ *reinterpret_cast<const uint32_t*>(cb + q);
+                // stream dwords (any alignment: two aligned dwords around each, the
+                // first nq of which lie in the data buffer) against the canonical
+                // dwords, 8 at a time; the rest byte by byte
+                const uintptr_t a0 = reinterpret_cast<uintptr_t>(sl), aa0 = a0 & ~(uintptr_t)3;
+                const uint32_t sh = (uint32_t)(a0 & 3u);
+                uint32_t nq = h.byte_count >> 2;
+                if (aa0 < d0 || aa0 + 8 > d1) nq = 0;
+                else nq = (uint32_t)min<uint64_t>(nq, (d1 - aa0 - 8) / 4 + 1);
+                const uint32_t* bp = data32_at(data, aa0 - d0);
+                uint32_t diff = 0, i = 0;
+                for (; i + 8 <= nq; i += 8) {
+                    uint32_t w[9], c[8];
+#pragma unroll
+                    for (int k = 0; k < 9; k++) w[k] = bp[i + k];
+#pragma unroll
+                    for (int k = 0; k < 8; k++) c[k] = cp[i + k];
+#pragma unroll
+                    for (int k = 0; k < 8; k++) diff |= __builtin_amdgcn_alignbyte(w[k + 1], w[k], sh) ^ c[k];
                 }
-                for (; q < h.byte_count; q++) diff |= sl[q] ^ cb[q];
+                for (; i < nq; i++) diff |= __builtin_amdgcn_alignbyte(bp[i + 1], bp[i], sh) ^ cp[i];
+                for (uint32_t q = 4 * nq; q < h.byte_count; q++) diff |= sl[q] ^ cb[q];
                 ok = diff == 0;
             }
             nbad += ok ? 0u : 1u;

@@ -306,3 +306,32 @@ def test_histogram_counts_wrap_like_reference(gpu):
     ref, rsum = oc.normalize_histogram(want)
     assert np.array_equal(tab.norm, ref["norm_freq"]) and np.array_equal(tab.cum, ref["cum_freq"])
     assert tsum == rsum  # 4115 here: the reference's over-full table for a dominant symbol
+
+
+@pytest.mark.parametrize("unit", [65536, 1 << 20])
+@pytest.mark.parametrize("where", ["live", "zero", "state"])
+def test_decode_counts_corrupted_lanes(unit, where, gpu):
+    """A flipped byte in a live lane's stream or a zero-plane lane's stream, or a
+    wrong final state, is reported as a bad lane (the decoder's postconditions:
+    final state L, every byte consumed, canonical zero-plane streams)."""
+    import torch
+    ck = _ck()
+    n = (unit // 4) * 2 + 777
+    print(f"[case] corruption {where} unit={unit}", flush=True)
+    raw = dg.normal_f32(n, 1e-3, 60)
+    enc = ck.compress(_to_dev(raw, gpu), dg.F32, unit, n_elems=n)
+    torch.cuda.synchronize()
+    dst, bad = ck.decode(enc)
+    assert bad == 0 and np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
+    hdr = enc.headers_np()
+    lane = {"live": 3, "zero": 0, "state": 2}[where]  # fp32 columns: bytes 0, 1 masked, 2, 3 live
+    h = hdr[lane]
+    assert h["byte_count"] > 8
+    if where == "state":
+        enc.headers.view(-1)[4 * lane] ^= 0x40  # final_state of unit 0, lane 2
+    else:
+        enc.data[int(h["buf_offset"]) + 5] ^= 0x10
+    torch.cuda.synchronize()
+    _, bad = ck.decode(enc)
+    torch.cuda.synchronize()
+    assert bad >= 1
