@@ -187,6 +187,7 @@ def main():
     ap.add_argument("--unit", type=int, default=65536)
     ap.add_argument("--cpu-sample-mib", type=int, default=128)
     ap.add_argument("--slice-gib", type=int, default=4, help="config 5: slice size of the streamed encode/decode")
+    ap.add_argument("--sequential", action="store_true", help="one ckr_compress per tensor, no overlap")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -216,8 +217,12 @@ def main():
     decs = [ck.Decoder(t.numel(), ck.torch_tag(t.dtype), unit, device=dev) for _, t in shard]
     dsts = [torch.empty_like(t) for _, t in shard]
 
-    def encode_all(sync_total=False):
-        return [e.compress(t) if sync_total else e.compress(t) for e, (_, t) in zip(encs, shard)]
+    def encode_all():
+        # the shard's tensors in one call: each histogram overlaps the previous
+        # tensor's encode (--sequential: one ckr_compress per tensor)
+        if args.sequential:
+            return [e.compress(t) for e, (_, t) in zip(encs, shard)]
+        return ck.compress_many(encs, [t for _, t in shard])
 
     def decode_all(results, check=False):
         bads = []

@@ -27,7 +27,7 @@ EXPORTED = [  # every symbol include/checkers_amd.h declares
     "ckr_last_error", "ckr_version", "ckr_element_size", "ckr_sidecar_bytes_per_elem",
     "ckr_extract_mantissa", "ckr_byte_histogram", "ckr_byte_histogram_raw", "ckr_build_table",
     "ckr_num_units", "ckr_encode_max_output_bytes", "ckr_encode_workspace_bytes", "ckr_encode",
-    "ckr_compress", "ckr_decode_workspace_bytes", "ckr_decode", "ckr_analyze_workspace_bytes",
+    "ckr_compress", "ckr_compress_many", "ckr_decode_workspace_bytes", "ckr_decode", "ckr_analyze_workspace_bytes",
     "ckr_analyze", "ckr_profile_begin", "ckr_profile_end", "ckr_set_fast_paths",
     "ckr_repair_masked_bits", "ckr_repair_bucket_count", "ckr_repair_workspace_bytes",
     "ckr_repair_build", "ckr_repair_apply",
@@ -122,6 +122,7 @@ def lib():
         "ckr_encode_workspace_bytes": (u64, [u64, i32, u64]),
         "ckr_encode": (i32, [vp, u64, i32, vp, u64, vp, u64, vp, vp, vp, vp, u64, vp, vp]),
         "ckr_compress": (i32, [vp, u64, i32, u64, i32, vp, u64, vp, vp, vp, vp, u64, vp, vp, vp]),
+        "ckr_compress_many": (i32, [vp, u64, u64, i32, vp]),
         "ckr_decode_workspace_bytes": (u64, [u64, i32, u64]),
         "ckr_decode": (i32, [vp, vp, vp, vp, u64, i32, u64, vp, vp, vp, u64, vp, vp]),
         "ckr_analyze_workspace_bytes": (u64, [vp, u64]),
@@ -299,6 +300,38 @@ class Encoder:
             self.ws.data_ptr(), self.ws_bytes, t.ptr, ctypes.byref(tot), _stream(stream)))
         return Encoded(self.out, self.headers, self.unit_offsets, self.sidecar, tot.value, self.n_elems,
                        self.dtype, self.unit_bytes, t)
+
+
+class CompressJob(ctypes.Structure):
+    _fields_ = [("d_src", ctypes.c_void_p), ("n_elems", ctypes.c_uint64), ("dtype", ctypes.c_int32),
+                ("pad", ctypes.c_int32), ("d_out", ctypes.c_void_p), ("out_capacity", ctypes.c_uint64),
+                ("d_headers", ctypes.c_void_p), ("d_unit_offsets", ctypes.c_void_p), ("d_sidecar", ctypes.c_void_p),
+                ("d_workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_uint64), ("h_table", ctypes.c_void_p),
+                ("total", ctypes.c_uint64)]
+
+
+def compress_many(encoders, srcs, ensure_full_alphabet=False, stream=None):
+    """ckr_compress_many: each (Encoder, source) pair compressed as Encoder.compress
+    would, the next tensor's histogram overlapping the current one's encode.
+    Every encoder must use the same unit size.  Returns one Encoded per pair."""
+    assert len(encoders) == len(srcs) and len({e.unit_bytes for e in encoders}) <= 1
+    if not encoders:
+        return []
+    jobs = (CompressJob * len(encoders))()
+    tables = []
+    for jb, e, src in zip(jobs, encoders, srcs):
+        e._check_src(src)
+        t = aligned_table()
+        tables.append(t)
+        jb.d_src, jb.n_elems, jb.dtype = src.data_ptr(), e.n_elems, e.dtype
+        jb.d_out, jb.out_capacity = e.out.data_ptr(), e.out_cap
+        jb.d_headers, jb.d_unit_offsets = e.headers.data_ptr(), e.unit_offsets.data_ptr()
+        jb.d_sidecar = e.sidecar.data_ptr() if e.sidecar is not None else None
+        jb.d_workspace, jb.workspace_bytes, jb.h_table = e.ws.data_ptr(), e.ws_bytes, ctypes.addressof(t.table)
+    _check(lib().ckr_compress_many(ctypes.addressof(jobs), len(encoders), encoders[0].unit_bytes,
+                                   int(bool(ensure_full_alphabet)), _stream(stream)))
+    return [Encoded(e.out, e.headers, e.unit_offsets, e.sidecar, jb.total, e.n_elems, e.dtype, e.unit_bytes, t)
+            for jb, e, t in zip(jobs, encoders, tables)]
 
 
 def byte_histogram(src, dtype, n_elems=None, stream=None):

@@ -14,6 +14,7 @@
 #include <cstring>
 #include <string>
 #include <unordered_map>
+#include <functional>
 #include <vector>
 
 #include "checkers_amd.h"
@@ -546,10 +547,13 @@ namespace {
 
 // Encode with an optional pair of live-plane histograms (host) used to size the
 // fast path's LDS slots.
+// after_launch (may be null) runs once the encode kernels are queued, before
+// the host waits for them: work for other streams goes in there.
+using AfterLaunch = std::function<hipError_t()>;
 int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table, uint64_t unit_bytes,
                 uint8_t* d_out, uint64_t out_capacity, ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
                 uint8_t* d_sidecar, void* d_workspace, uint64_t workspace_bytes, uint64_t* h_total_out,
-                const uint32_t* h_planes, void* stream) {
+                const uint32_t* h_planes, void* stream, const AfterLaunch* after_launch = nullptr) {
     if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
     ckr::EncodeGeom g;
     if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
@@ -596,6 +600,7 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         auto* aux = reinterpret_cast<uint32_t*>(ws + L.off_aux);
         CKR_HIP(ckr::launch_encode_seg(static_cast<const uint8_t*>(d_src), g, enc, canon, ck.cw, escapes, rec,
                                        d_headers, usize, d_unit_offsets, side, d_out, aux, s));
+        if (after_launch) CKR_HIP((*after_launch)());
         uint32_t herr = 0;
         CKR_HIP(hipMemcpyAsync(&herr, aux, 4, hipMemcpyDeviceToHost, s));
         if (h_total_out) CKR_HIP(hipMemcpyAsync(h_total_out, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
@@ -628,6 +633,7 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         CKR_HIP(ckr::launch_encode_fast(static_cast<const uint8_t*>(d_src), g, enc, canon, fp,
                                         (uint32_t)max_lds_per_block(), d_headers, side, d_out, d_unit_offsets, status,
                                         ctl, redo, s));
+        if (after_launch) CKR_HIP((*after_launch)());
         uint32_t hctl[4];
         CKR_HIP(hipMemcpyAsync(hctl, ctl, sizeof(hctl), hipMemcpyDeviceToHost, s));
         CKR_HIP(hipStreamSynchronize(s));
@@ -645,6 +651,7 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
             CKR_HIP(ckr::launch_encode_batch(static_cast<const uint8_t*>(d_src), g, u0, nb, enc, canon, ck.cw, dedup,
                                              scratch, d_headers, side, usize, d_unit_offsets, d_out, nullptr, s));
         }
+        if (after_launch) CKR_HIP((*after_launch)());
     }
     if (h_total_out) {
         CKR_HIP(hipMemcpyAsync(h_total_out, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
@@ -691,6 +698,94 @@ int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_b
     if (rc) return rc;
     return encode_impl(d_src, n_elems, dtype, t, unit_bytes, d_out, out_capacity, d_headers, d_unit_offsets,
                        d_sidecar, d_workspace, workspace_bytes, h_total_out, g.spe ? hh + 256 : nullptr, stream);
+}
+
+// The second stream, its event and the pinned histogram buffers of
+// ckr_compress_many, one set per device per thread (kept for the thread's life).
+namespace {
+struct ManyAux {
+    hipStream_t s2 = nullptr;
+    hipEvent_t ev = nullptr;
+    uint32_t* pinned = nullptr;  // 2 x 768 words
+};
+hipError_t many_aux(ManyAux** out) {
+    thread_local std::vector<ManyAux> per_dev;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if ((int)per_dev.size() <= dev) per_dev.resize(dev + 1);
+    ManyAux& a = per_dev[dev];
+    if (!a.s2) {
+        if ((e = hipStreamCreateWithFlags(&a.s2, hipStreamNonBlocking)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&a.ev, hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipHostMalloc(reinterpret_cast<void**>(&a.pinned), 2 * 768 * sizeof(uint32_t), hipHostMallocDefault)) !=
+            hipSuccess)
+            return e;
+    }
+    *out = &a;
+    return hipSuccess;
+}
+}  // namespace
+
+int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, int ensure_full_alphabet,
+                      void* stream) {
+    if (n == 0) return CKR_OK;
+    if (!jobs) return fail(CKR_E_INVALID, "[ckr] null job list");
+    // every job checked before anything is launched
+    std::vector<ckr::EncodeGeom> geo(n);
+    for (uint64_t i = 0; i < n; i++) {
+        const ckr_compress_job& jb = jobs[i];
+        if (!dtype_ok(jb.dtype)) return fail(CKR_E_INVALID, "[ckr] job %llu: unknown dtype %d", (unsigned long long)i, jb.dtype);
+        if (!make_geom(jb.n_elems, jb.dtype, unit_bytes, &geo[i])) return CKR_E_INVALID;
+        const EncodeLayout L = encode_layout(geo[i]);
+        if (!jb.d_workspace || jb.workspace_bytes < L.total || !aligned16(jb.d_workspace))
+            return fail(CKR_E_CAPACITY, "[ckr] job %llu: workspace too small or misaligned", (unsigned long long)i);
+        if (jb.n_elems && (!jb.d_src || !aligned16(jb.d_src)))
+            return fail(CKR_E_INVALID, "[ckr] job %llu: source must be 16-byte aligned", (unsigned long long)i);
+    }
+    hipStream_t s = (hipStream_t)stream;
+    ManyAux* a = nullptr;
+    CKR_HIP(many_aux(&a));
+    CKR_HIP(hipEventRecord(a->ev, s));  // inputs ready in the caller's stream order
+    CKR_HIP(hipStreamWaitEvent(a->s2, a->ev, 0));
+    auto hist = [&](uint64_t i, uint32_t* h_dst) -> hipError_t {
+        const ckr_compress_job& jb = jobs[i];
+        const EncodeLayout L = encode_layout(geo[i]);
+        uint32_t* d_hist = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(jb.d_workspace) + L.off_hist);
+        const int es = ckr_element_size(jb.dtype);
+        hipError_t e = ckr::launch_masked_hist(static_cast<const uint8_t*>(jb.d_src), jb.n_elems * (uint64_t)es, es,
+                                               geo[i].spe, d_hist, d_hist + 256, a->s2);
+        if (e != hipSuccess) return e;
+        return hipMemcpyAsync(h_dst, d_hist, 768 * sizeof(uint32_t), hipMemcpyDeviceToHost, a->s2);
+    };
+    CKR_HIP(hist(0, a->pinned));
+    CKR_HIP(hipStreamSynchronize(a->s2));
+    for (uint64_t i = 0; i < n; i++) {
+        ckr_compress_job& jb = jobs[i];
+        uint32_t* hh = a->pinned + 768 * (i & 1);
+        ckr_freq_table local;
+        ckr_freq_table* t = jb.h_table ? jb.h_table : &local;
+        int rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
+        if (rc) return rc;
+        // job i + 1's histogram is queued once job i's encode kernels are, so
+        // that the encoder's workgroups take their CUs first
+        bool queued = i + 1 >= n;
+        const AfterLaunch next = [&]() -> hipError_t {
+            if (queued) return hipSuccess;
+            queued = true;
+            return hist(i + 1, a->pinned + 768 * ((i + 1) & 1));
+        };
+        rc = encode_impl(jb.d_src, jb.n_elems, jb.dtype, t, unit_bytes, jb.d_out, jb.out_capacity, jb.d_headers,
+                         jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace, jb.workspace_bytes, &jb.total,
+                         geo[i].spe ? hh + 256 : nullptr, stream, &next);
+        if (rc) {
+            (void)hipStreamSynchronize(a->s2);
+            return rc;
+        }
+        CKR_HIP(next());  // an empty job launches nothing
+        if (i + 1 < n) CKR_HIP(hipStreamSynchronize(a->s2));
+    }
+    return CKR_OK;
 }
 
 uint64_t ckr_decode_workspace_bytes(uint64_t n_elems, int dtype, uint64_t unit_bytes) {

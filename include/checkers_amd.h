@@ -166,6 +166,32 @@ CKR_API int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_
                          void* d_workspace, uint64_t workspace_bytes,
                          ckr_freq_table* h_table, uint64_t* h_total_out, void* stream);
 
+/* ---- several tensors, as compress_and_save_all's workers take its items
+ * (src/ANSCompressor.cpp:1118-1300, the GPU phases of each item): the same
+ * results as ckr_compress called on each job in order, with job i+1's
+ * histogram computed on a second, library-owned stream while job i is encoded
+ * on `stream`.  Every job has its own buffers and workspace (sizes as for
+ * ckr_compress).  The inputs must be ready in `stream` order; the call returns
+ * when every job is done, with table and total filled in.  On error, jobs
+ * before the failing one are complete. ---- */
+typedef struct {
+    const void* d_src;
+    uint64_t n_elems;
+    int32_t dtype;
+    int32_t pad;
+    uint8_t* d_out;
+    uint64_t out_capacity;
+    ckr_stream_header* d_headers;
+    uint64_t* d_unit_offsets;
+    uint8_t* d_sidecar;
+    void* d_workspace;
+    uint64_t workspace_bytes;
+    ckr_freq_table* h_table;  /* filled (may be NULL) */
+    uint64_t total;           /* filled: packed bytes */
+} ckr_compress_job;
+CKR_API int ckr_compress_many(ckr_compress_job* jobs, uint64_t n_jobs, uint64_t unit_bytes,
+                              int ensure_full_alphabet, void* stream);
+
 /* ---- decode: inverse of ckr_encode, sidecar merged back (original bits).
  * d_sidecar may be NULL only for dtypes without a sidecar.  The table must sum
  * to 4096.  Stream checks (every lane ends in state 2^23 having consumed

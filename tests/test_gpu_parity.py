@@ -335,3 +335,35 @@ def test_decode_counts_corrupted_lanes(unit, where, gpu):
     _, bad = ck.decode(enc)
     torch.cuda.synchronize()
     assert bad >= 1
+
+
+@pytest.mark.parametrize("unit", [65536, 1 << 20])
+def test_compress_many_matches_single_calls(unit, gpu):
+    """ckr_compress_many (histograms overlapped with the previous encode) gives
+    each job exactly what ckr_compress gives it, and the oracle's bytes."""
+    import torch
+    ck = _ck()
+    specs = [(dg.F32, 300001, lambda n: dg.normal_f32(n, 1e-3, 70)),
+             (dg.BF16, 400003, lambda n: dg.normal_bf16(n, 0.02, 71)),
+             (dg.F32, 0, lambda n: np.zeros(0, np.float32)),
+             (dg.F32, 50000, lambda n: dg.exp_avg_sq(n, 72)),
+             (dg.I8, 70001, lambda n: np.random.default_rng(73).integers(-4, 4, n).astype(np.int8))]
+    print(f"[case] compress_many unit={unit}", flush=True)
+    raws = [gen(n) for _, n, gen in specs]
+    srcs = [_to_dev(r, gpu) for r in raws]
+    encs = [ck.Encoder(n, dt, unit, device=gpu) for dt, n, _ in specs]
+    many = ck.compress_many(encs, srcs)
+    torch.cuda.synchronize()
+    for (dt, n, _), raw, src, m in zip(specs, raws, srcs, many):
+        ref = oc.compress_tensor(raw, n, dt, unit)
+        assert np.array_equal(m.table.norm, ref["table"]["norm_freq"])
+        assert m.total == ref["data"].size
+        assert np.array_equal(m.data_np(), ref["data"])
+        nu = ref["unit_offsets"].size - 1
+        assert np.array_equal(m.unit_offsets[: nu + 1].cpu().numpy().view(np.uint64), ref["unit_offsets"])
+        assert np.array_equal(m.headers_np()[: nu * 256], ref["headers"])
+        if oc.SPE[dt]:
+            assert np.array_equal(m.sidecar[: n * oc.SPE[dt]].cpu().numpy(), ref["sidecar"])
+        dst, bad = ck.decode(m)
+        torch.cuda.synchronize()
+        assert bad == 0 and np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
