@@ -181,8 +181,8 @@ def stream_bench(shard, ck, torch, dev, unit, steps, slice_bytes):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--unit", type=int, default=65536)
     ap.add_argument("--cpu-sample-mib", type=int, default=128)
