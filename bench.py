@@ -107,8 +107,8 @@ def cpu_baseline(shard, ck, sample_bytes_per_tensor, unit):
     except AttributeError:
         cores = os.cpu_count() or 1
     cores = max(1, min(cores, 16))
-    total = 0
-    t_all = 0.0
+    total = total1 = 0
+    t_all = t_one = 0.0
     for name, t in shard:
         tag = ck.torch_tag(t.dtype)
         es = t.element_size()
@@ -120,11 +120,24 @@ def cpu_baseline(shard, ck, sample_bytes_per_tensor, unit):
         oc.encode(masked, table, unit, n_threads=cores)
         t_all += time.perf_counter() - t0
         total += n * es
+        # the same steps on one thread (the reference's sequential-policy analogue),
+        # on the first eighth of the sample
+        n1 = max(1, n // 8)
+        t0 = time.perf_counter()
+        m1, _ = oc.extract_mantissa(raw[: n1 * es], n1, tag)
+        tb1, _ = oc.normalize_histogram(oc.byte_hist(m1))
+        oc.encode(m1, tb1, unit, n_threads=1)
+        t_one += time.perf_counter() - t0
+        total1 += n1 * es
     return dict(value=round(total / t_all / 1e9, 4), unit="GB/s", cores=cores, kind="port",
                 sample=f"first {sample_bytes_per_tensor >> 20} MiB of each of the {len(shard)} tensors "
                        f"({total / 1e6:.0f} MB): oracle mask+histogram+table single-thread, "
                        f"rANS encode OpenMP over {unit}-byte units",
-                seconds=round(t_all, 3))
+                seconds=round(t_all, 3),
+                single_thread=dict(value=round(total1 / t_one / 1e9, 4), unit="GB/s", cores=1,
+                                   sample=f"first {(sample_bytes_per_tensor // 8) >> 20} MiB of each tensor "
+                                          f"({total1 / 1e6:.0f} MB), every step on one thread",
+                                   seconds=round(t_one, 3)))
 
 
 def stream_bench(shard, ck, torch, dev, unit, steps, slice_bytes):
@@ -185,7 +198,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--unit", type=int, default=65536)
-    ap.add_argument("--cpu-sample-mib", type=int, default=128)
+    ap.add_argument("--cpu-sample-mib", type=int, default=1024)
     ap.add_argument("--slice-gib", type=int, default=4, help="config 5: slice size of the streamed encode/decode")
     ap.add_argument("--sequential", action="store_true", help="one ckr_compress per tensor, no overlap")
     ap.add_argument("--no-cpu", action="store_true")
