@@ -15,7 +15,7 @@ dominant kernel's roofline, and the CPU oracle timed on a bounded sample.
 
 Config 5 (the Llama-3-70B rank shard, 123.5 GB resident in HBM, 1 MiB units)
 streams: per tensor the masked histogram and table of the whole tensor, then the
-tensor's 4 GiB slices encoded with that table one after the other into reused
+tensor's 8 GiB slices encoded with that table one after the other into reused
 buffers (slices end on unit boundaries, and units are independent given the
 table, so each slice's units are the whole-tensor encode's), each decoded into
 a reused window and compared with its source outside the timed regions.
@@ -199,7 +199,7 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--unit", type=int, default=65536)
     ap.add_argument("--cpu-sample-mib", type=int, default=1024)
-    ap.add_argument("--slice-gib", type=int, default=4, help="config 5: slice size of the streamed encode/decode")
+    ap.add_argument("--slice-gib", type=int, default=8, help="config 5: slice size of the streamed encode/decode")
     ap.add_argument("--sequential", action="store_true", help="one ckr_compress per tensor, no overlap")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
@@ -378,7 +378,9 @@ def run_streamed(args, shard, ck, torch, dev, unit, n_in):
     """Config 5 driver: warm-up on the first slice of the first tensor, then the
     streamed passes; one JSON line like the resident configs."""
     name0, t0 = shard[0]
-    w = min(t0.numel(), (args.slice_gib << 30) // t0.element_size())
+    # a warm-up slice of at most 4 GiB: a larger one, taken as a tensor of its own,
+    # could wrap the u32 histogram counts into a table that cannot be decoded
+    w = min(t0.numel(), (min(args.slice_gib, 4) << 30) // t0.element_size())
     for _ in range(max(args.warmup, 1)):
         stream_bench([(name0, t0[:w])], ck, torch, dev, unit, 1, args.slice_gib << 30)
     steps = max(1, min(args.steps, 2))
