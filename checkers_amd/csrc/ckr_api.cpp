@@ -188,6 +188,25 @@ bool use_fast_encode(const ckr::EncodeGeom& g) { return use_dedup(g) && (g.unit 
 // Units above 64 KiB (up to the dedup limit): the two-pass kernels.
 bool use_seg_encode(const ckr::EncodeGeom& g) { return use_dedup(g) && (g.unit + 255) / 256 > kFastMaxK; }
 
+// A small pinned host buffer per thread and device for the few words the host
+// reads back (histograms, control words, totals): copies into pinned memory are
+// plain DMA, where pageable ones are staged by the runtime (~27 us each).
+// Kept for the thread's life.
+struct PinnedWords {
+    uint32_t* w = nullptr;  // kPinnedWords words
+};
+constexpr uint32_t kPinnedWords = 1024;
+uint32_t* pinned_words() {
+    thread_local std::vector<PinnedWords> per_dev;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    if ((int)per_dev.size() <= dev) per_dev.resize(dev + 1);
+    PinnedWords& p = per_dev[dev];
+    if (!p.w && hipHostMalloc(reinterpret_cast<void**>(&p.w), kPinnedWords * 4, hipHostMallocDefault) != hipSuccess)
+        p.w = nullptr;
+    return p.w;
+}
+
 int max_lds_per_block() {
     static int v = -1;
     if (v < 0) {
@@ -601,11 +620,13 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         CKR_HIP(ckr::launch_encode_seg(static_cast<const uint8_t*>(d_src), g, enc, canon, ck.cw, escapes, rec,
                                        d_headers, usize, d_unit_offsets, side, d_out, aux, s));
         if (after_launch) CKR_HIP((*after_launch)());
-        uint32_t herr = 0;
-        CKR_HIP(hipMemcpyAsync(&herr, aux, 4, hipMemcpyDeviceToHost, s));
-        if (h_total_out) CKR_HIP(hipMemcpyAsync(h_total_out, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
+        uint32_t* pw = pinned_words();
+        if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
+        CKR_HIP(hipMemcpyAsync(pw, aux, 4, hipMemcpyDeviceToHost, s));
+        CKR_HIP(hipMemcpyAsync(pw + 2, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
         CKR_HIP(hipStreamSynchronize(s));
-        if (herr) return fail(CKR_E_HIP, "[ckr] two-pass encode: a segment did not end at its checkpoint");
+        if (pw[0]) return fail(CKR_E_HIP, "[ckr] two-pass encode: a segment did not end at its checkpoint");
+        if (h_total_out) std::memcpy(h_total_out, pw + 2, 8);
         return CKR_OK;
     }
 
@@ -634,10 +655,17 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
                                         (uint32_t)max_lds_per_block(), d_headers, side, d_out, d_unit_offsets, status,
                                         ctl, redo, s));
         if (after_launch) CKR_HIP((*after_launch)());
-        uint32_t hctl[4];
-        CKR_HIP(hipMemcpyAsync(hctl, ctl, sizeof(hctl), hipMemcpyDeviceToHost, s));
+        // control words and the total in one synchronisation (the fast kernel
+        // publishes every unit's offset, redo units included)
+        uint32_t* pw = pinned_words();
+        if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
+        CKR_HIP(hipMemcpyAsync(pw, ctl, 16, hipMemcpyDeviceToHost, s));
+        CKR_HIP(hipMemcpyAsync(pw + 4, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
         CKR_HIP(hipStreamSynchronize(s));
+        uint32_t hctl[4];
+        std::memcpy(hctl, pw, 16);
         if (hctl[2]) return fail(CKR_E_HIP, "[ckr] encode look-back did not complete (flag %u)", hctl[2]);
+        if (h_total_out) std::memcpy(h_total_out, pw + 4, 8);
         // units whose lanes outgrew their LDS slots: bytes from the general kernels,
         // at the offsets the fast kernel published
         for (uint64_t r0 = 0; r0 < hctl[1]; r0 += L.batch_units) {
@@ -645,6 +673,8 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
             CKR_HIP(ckr::launch_encode_batch(static_cast<const uint8_t*>(d_src), g, r0, nb, enc, canon, ck.cw, true,
                                              scratch, d_headers, nullptr, usize, d_unit_offsets, d_out, redo, s));
         }
+        if (h_total_out && hctl[1]) CKR_HIP(hipStreamSynchronize(s));  // the output complete, as on the other paths
+        return CKR_OK;
     } else {
         for (uint64_t u0 = 0; u0 < g.n_units; u0 += L.batch_units) {
             const uint64_t nb = std::min<uint64_t>(L.batch_units, g.n_units - u0);
@@ -654,8 +684,11 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         if (after_launch) CKR_HIP((*after_launch)());
     }
     if (h_total_out) {
-        CKR_HIP(hipMemcpyAsync(h_total_out, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
+        uint32_t* pw = pinned_words();
+        if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
+        CKR_HIP(hipMemcpyAsync(pw, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
         CKR_HIP(hipStreamSynchronize(s));
+        std::memcpy(h_total_out, pw, 8);
     }
     return CKR_OK;
 }
@@ -689,9 +722,12 @@ int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_b
     const int es = ckr_element_size(dtype);
     CKR_HIP(ckr::launch_masked_hist(static_cast<const uint8_t*>(d_src), n_elems * (uint64_t)es, es, g.spe, d_hist,
                                     d_hist + 256, s));
-    uint32_t hh[768];
-    CKR_HIP(hipMemcpyAsync(hh, d_hist, sizeof(hh), hipMemcpyDeviceToHost, s));
+    uint32_t* pw = pinned_words();
+    if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
+    CKR_HIP(hipMemcpyAsync(pw, d_hist, 768 * 4, hipMemcpyDeviceToHost, s));
     CKR_HIP(hipStreamSynchronize(s));
+    uint32_t hh[768];
+    std::memcpy(hh, pw, sizeof(hh));
     ckr_freq_table local;
     ckr_freq_table* t = h_table ? h_table : &local;
     int rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
@@ -826,9 +862,12 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
     CKR_HIP(ckr::launch_decode(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, static_cast<uint8_t*>(d_dst),
                                bad, L.fast ? canon : nullptr, ck.cw, s));
     if (h_bad_lanes) {
-        unsigned long long nb = 0;
-        CKR_HIP(hipMemcpyAsync(&nb, bad, 8, hipMemcpyDeviceToHost, s));
+        uint32_t* pw = pinned_words();
+        if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
+        CKR_HIP(hipMemcpyAsync(pw, bad, 8, hipMemcpyDeviceToHost, s));
         CKR_HIP(hipStreamSynchronize(s));
+        unsigned long long nb = 0;
+        std::memcpy(&nb, pw, 8);
         *h_bad_lanes = nb;
     }
     return CKR_OK;
