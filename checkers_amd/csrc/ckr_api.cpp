@@ -569,10 +569,31 @@ namespace {
 // after_launch (may be null) runs once the encode kernels are queued, before
 // the host waits for them: work for other streams goes in there.
 using AfterLaunch = std::function<hipError_t()>;
+
+// An encode whose read-backs are left queued (ckr_compress_many): the words the
+// host checks go into pinned slots, read after one synchronisation for the
+// whole batch by encode_complete, which also queues any redo batches.
+struct EncodeDeferred {
+    uint32_t* pin = nullptr;  // 8 words: [0..3] control words (fast) or [0] error flag (two-pass); [4..5] total
+    int kind = 0;             // 0 none (empty tensor), 1 fast, 2 two-pass, 3 general
+    const uint8_t* src = nullptr;
+    ckr::EncodeGeom g{};
+    const ckr::EncSym* enc = nullptr;
+    const uint32_t* canon = nullptr;
+    uint32_t cw = 0;
+    uint32_t* scratch = nullptr;
+    ckr_stream_header* hdrs = nullptr;
+    uint32_t* usize = nullptr;
+    uint64_t* unit_off = nullptr;
+    uint8_t* out = nullptr;
+    const uint32_t* redo = nullptr;
+    uint64_t batch_units = 0;
+};
 int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table, uint64_t unit_bytes,
                 uint8_t* d_out, uint64_t out_capacity, ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
                 uint8_t* d_sidecar, void* d_workspace, uint64_t workspace_bytes, uint64_t* h_total_out,
-                const uint32_t* h_planes, void* stream, const AfterLaunch* after_launch = nullptr) {
+                const uint32_t* h_planes, void* stream, const AfterLaunch* after_launch = nullptr,
+                EncodeDeferred* defer = nullptr) {
     if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
     ckr::EncodeGeom g;
     if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
@@ -581,6 +602,10 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
     if (g.n_units == 0) {
         CKR_HIP(ckr::launch_set_u64(d_unit_offsets, 0, s));
         if (h_total_out) *h_total_out = 0;
+        if (defer) {
+            defer->kind = 0;
+            std::memset(defer->pin, 0, 32);
+        }
         return CKR_OK;
     }
     if (!d_src || !d_out || !d_headers || !d_workspace) return fail(CKR_E_INVALID, "[ckr] null pointer");
@@ -620,6 +645,12 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         CKR_HIP(ckr::launch_encode_seg(static_cast<const uint8_t*>(d_src), g, enc, canon, ck.cw, escapes, rec,
                                        d_headers, usize, d_unit_offsets, side, d_out, aux, s));
         if (after_launch) CKR_HIP((*after_launch)());
+        if (defer) {
+            defer->kind = 2;
+            CKR_HIP(hipMemcpyAsync(defer->pin, aux, 4, hipMemcpyDeviceToHost, s));
+            CKR_HIP(hipMemcpyAsync(defer->pin + 4, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
+            return CKR_OK;
+        }
         uint32_t* pw = pinned_words();
         if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
         CKR_HIP(hipMemcpyAsync(pw, aux, 4, hipMemcpyDeviceToHost, s));
@@ -655,6 +686,24 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
                                         (uint32_t)max_lds_per_block(), d_headers, side, d_out, d_unit_offsets, status,
                                         ctl, redo, s));
         if (after_launch) CKR_HIP((*after_launch)());
+        if (defer) {
+            defer->kind = 1;
+            defer->src = static_cast<const uint8_t*>(d_src);
+            defer->g = g;
+            defer->enc = enc;
+            defer->canon = canon;
+            defer->cw = ck.cw;
+            defer->scratch = scratch;
+            defer->hdrs = d_headers;
+            defer->usize = usize;
+            defer->unit_off = d_unit_offsets;
+            defer->out = d_out;
+            defer->redo = redo;
+            defer->batch_units = L.batch_units;
+            CKR_HIP(hipMemcpyAsync(defer->pin, ctl, 16, hipMemcpyDeviceToHost, s));
+            CKR_HIP(hipMemcpyAsync(defer->pin + 4, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
+            return CKR_OK;
+        }
         // control words and the total in one synchronisation (the fast kernel
         // publishes every unit's offset, redo units included)
         uint32_t* pw = pinned_words();
@@ -683,6 +732,11 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         }
         if (after_launch) CKR_HIP((*after_launch)());
     }
+    if (defer) {
+        defer->kind = 3;
+        CKR_HIP(hipMemcpyAsync(defer->pin + 4, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
+        return CKR_OK;
+    }
     if (h_total_out) {
         uint32_t* pw = pinned_words();
         if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
@@ -690,6 +744,23 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         CKR_HIP(hipStreamSynchronize(s));
         std::memcpy(h_total_out, pw, 8);
     }
+    return CKR_OK;
+}
+
+// After the stream has passed a deferred encode: its checks, its total, and the
+// redo batches of the fast path (queued; the caller synchronises once more).
+int encode_complete(const EncodeDeferred& d, uint64_t* total, bool* queued_more, hipStream_t s) {
+    if (d.kind == 2 && d.pin[0]) return fail(CKR_E_HIP, "[ckr] two-pass encode: a segment did not end at its checkpoint");
+    if (d.kind == 1) {
+        if (d.pin[2]) return fail(CKR_E_HIP, "[ckr] encode look-back did not complete (flag %u)", d.pin[2]);
+        for (uint64_t r0 = 0; r0 < d.pin[1]; r0 += d.batch_units) {
+            const uint64_t nb = std::min<uint64_t>(d.batch_units, d.pin[1] - r0);
+            CKR_HIP(ckr::launch_encode_batch(d.src, d.g, r0, nb, d.enc, d.canon, d.cw, true, d.scratch, d.hdrs, nullptr,
+                                             d.usize, d.unit_off, d.out, d.redo, s));
+            *queued_more = true;
+        }
+    }
+    std::memcpy(total, d.pin + 4, 8);
     return CKR_OK;
 }
 
@@ -742,7 +813,10 @@ namespace {
 struct ManyAux {
     hipStream_t s2 = nullptr;
     hipEvent_t ev = nullptr;
+    hipEvent_t ev_prev = nullptr;  // the stream's work before the encode being queued
     uint32_t* pinned = nullptr;  // 2 x 768 words
+    uint32_t* slots = nullptr;   // 8 words per job: the deferred read-backs
+    uint64_t slot_jobs = 0;
 };
 hipError_t many_aux(ManyAux** out) {
     thread_local std::vector<ManyAux> per_dev;
@@ -754,6 +828,7 @@ hipError_t many_aux(ManyAux** out) {
     if (!a.s2) {
         if ((e = hipStreamCreateWithFlags(&a.s2, hipStreamNonBlocking)) != hipSuccess) return e;
         if ((e = hipEventCreateWithFlags(&a.ev, hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&a.ev_prev, hipEventDisableTiming)) != hipSuccess) return e;
         if ((e = hipHostMalloc(reinterpret_cast<void**>(&a.pinned), 2 * 768 * sizeof(uint32_t), hipHostMallocDefault)) !=
             hipSuccess)
             return e;
@@ -782,6 +857,27 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
     hipStream_t s = (hipStream_t)stream;
     ManyAux* a = nullptr;
     CKR_HIP(many_aux(&a));
+    if (a->slot_jobs < n) {
+        if (a->slots) CKR_HIP(hipHostFree(a->slots));
+        a->slots = nullptr;
+        a->slot_jobs = 0;
+        CKR_HIP(hipHostMalloc(reinterpret_cast<void**>(&a->slots), n * 8 * sizeof(uint32_t), hipHostMallocDefault));
+        a->slot_jobs = n;
+    }
+    std::vector<EncodeDeferred> defs(n);
+    for (uint64_t i = 0; i < n; i++) defs[i].pin = a->slots + 8 * i;
+    // completes the encodes queued so far (jobs [0, upto)) once the stream has passed them
+    auto complete = [&](uint64_t upto) -> int {
+        CKR_HIP(hipStreamSynchronize(s));
+        bool more = false;
+        int first = CKR_OK;
+        for (uint64_t k = 0; k < upto; k++) {
+            const int r = encode_complete(defs[k], &jobs[k].total, &more, s);
+            if (r && !first) first = r;
+        }
+        if (more) CKR_HIP(hipStreamSynchronize(s));
+        return first;
+    };
     CKR_HIP(hipEventRecord(a->ev, s));  // inputs ready in the caller's stream order
     CKR_HIP(hipStreamWaitEvent(a->s2, a->ev, 0));
     auto hist = [&](uint64_t i, uint32_t* h_dst) -> hipError_t {
@@ -803,25 +899,33 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         ckr_freq_table* t = jb.h_table ? jb.h_table : &local;
         int rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
         if (rc) return rc;
-        // job i + 1's histogram is queued once job i's encode kernels are, so
-        // that the encoder's workgroups take their CUs first
+        // job i + 1's histogram is queued once job i's encode kernels are, and
+        // waits for the work queued before them (the host does not wait for
+        // encodes), so that it starts with job i's encode and the encoder's
+        // workgroups take their CUs first
+        CKR_HIP(hipEventRecord(a->ev_prev, s));
         bool queued = i + 1 >= n;
         const AfterLaunch next = [&]() -> hipError_t {
             if (queued) return hipSuccess;
             queued = true;
+            const hipError_t e2 = hipStreamWaitEvent(a->s2, a->ev_prev, 0);
+            if (e2 != hipSuccess) return e2;
             return hist(i + 1, a->pinned + 768 * ((i + 1) & 1));
         };
+        // the encode is only queued: its read-backs are checked at the end, so
+        // the next encode follows it on the stream without a host round trip
         rc = encode_impl(jb.d_src, jb.n_elems, jb.dtype, t, unit_bytes, jb.d_out, jb.out_capacity, jb.d_headers,
-                         jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace, jb.workspace_bytes, &jb.total,
-                         geo[i].spe ? hh + 256 : nullptr, stream, &next);
+                         jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace, jb.workspace_bytes, nullptr,
+                         geo[i].spe ? hh + 256 : nullptr, stream, &next, &defs[i]);
         if (rc) {
             (void)hipStreamSynchronize(a->s2);
+            (void)complete(i);
             return rc;
         }
         CKR_HIP(next());  // an empty job launches nothing
         if (i + 1 < n) CKR_HIP(hipStreamSynchronize(a->s2));
     }
-    return CKR_OK;
+    return complete(n);
 }
 
 uint64_t ckr_decode_workspace_bytes(uint64_t n_elems, int dtype, uint64_t unit_bytes) {
