@@ -1989,8 +1989,8 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
 // inside the data buffer (the first unit of a buffer that is not 64-byte
 // aligned, the units at its end, streams running past their end) are
 // assembled byte by byte, with zeros outside the buffer.
-static constexpr uint32_t DF_WAVES = 7;
-static constexpr uint32_t DF_TAB_BYTES = 4096 * 8;
+static constexpr uint32_t DF_WAVES = 8;
+static constexpr uint32_t DF_TAB_BYTES = 4096 * 4;
 static constexpr uint32_t DF_RING_BYTES = 33 * 256;  // 32 rows + the copy of row 0
 static constexpr uint32_t DF_WAVE_BYTES = 2 * DF_RING_BYTES;
 
@@ -2070,16 +2070,19 @@ __device__ __forceinline__ uint32_t df_window(const DfLane& d, const uint8_t* ld
 // One symbol (the inverse of rans_encode_kernel's step, ANSCompressor.cpp:180-202):
 // x = f*(x >> 12) + slot - cum, then renormalise with 8n bits from the top of w
 // (stream order), n = 0, 1, 2 for x >= 2^23, 2^15 <= x < 2^23, x < 2^15 (x >= 2^11
-// here), i.e. 8n = (clz(x) - 1) & 24.  Returns the table word (symbol in bits
-// 31..24) and the bits consumed in sh.
-__device__ __forceinline__ uint32_t df_sym(uint32_t& x, uint32_t& w, uint32_t& sh, const uint2* tab) {
-    const uint2 e = tab[x & (M - 1u)];
-    const uint32_t xx = __umul24(e.x, x >> 12) + e.y;
+// here), i.e. 8n = (clz(x) - 1) & 24.  The LDS table word of a slot is
+// sym << 24 | (f - 1) << 12 | (slot - cum): 4 bytes, so the table takes 16 KiB
+// and an eighth wave fits (f*t = (f-1)*t + t).  Returns the table word (symbol
+// in bits 31..24) and the bits consumed in sh.
+__device__ __forceinline__ uint32_t df_sym(uint32_t& x, uint32_t& w, uint32_t& sh, const uint32_t* tab) {
+    const uint32_t te = tab[x & (M - 1u)];
+    const uint32_t t = x >> 12;
+    const uint32_t xx = __umul24(__builtin_amdgcn_ubfe(te, 12, 12), t) + t + (te & 4095u);
     sh = ((uint32_t)__builtin_clz(xx) - 1u) & 24u;
-    const uint64_t t = (((uint64_t)xx << 32) | w) << sh;
-    x = (uint32_t)(t >> 32);
-    w = (uint32_t)t;
-    return e.x;
+    const uint64_t v = (((uint64_t)xx << 32) | w) << sh;
+    x = (uint32_t)(v >> 32);
+    w = (uint32_t)v;
+    return te;
 }
 
 // End of a group: write the chunk fetched at the end of the previous group,
@@ -2111,7 +2114,7 @@ __device__ __forceinline__ uint32_t df_sel(uint32_t o) {
 
 // Two rows: one window read per lane, two symbols from it.
 template <int SPE>
-__device__ __forceinline__ void df_pair(DfLane& a, DfLane& b, const uint8_t* lds8, const uint2* tab, uint32_t* out,
+__device__ __forceinline__ void df_pair(DfLane& a, DfLane& b, const uint8_t* lds8, const uint32_t* tab, uint32_t* out,
                                         uint32_t sv0, uint32_t sv1, uint32_t sel) {
     uint32_t wa = df_window(a, lds8), wb = df_window(b, lds8);
     uint32_t ha0, ha1, hb0, hb1;
@@ -2127,7 +2130,7 @@ __device__ __forceinline__ void df_pair(DfLane& a, DfLane& b, const uint8_t* lds
 
 // Eight rows (sidecar words sc), then the window step.
 template <int SPE>
-__device__ __forceinline__ void df_group(DfLane& a, DfLane& b, uint8_t* lds8, const uint2* tab, uint32_t* out,
+__device__ __forceinline__ void df_group(DfLane& a, DfLane& b, uint8_t* lds8, const uint32_t* tab, uint32_t* out,
                                          const uint32_t (&sc)[8], uint32_t sel, const DfSrc& sr) {
 #pragma unroll
     for (int r = 0; r < 8; r += 2) df_pair<SPE>(a, b, lds8, tab, out + 64 * r, sc[r], sc[r + 1], sel);
@@ -2150,10 +2153,10 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
                                                                    uint8_t* __restrict__ dst, unsigned long long* bad) {
     extern __shared__ uint32_t lds[];
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
-    const uint2* tab = reinterpret_cast<const uint2*>(lds);
+    const uint32_t* tab = reinterpret_cast<const uint32_t*>(lds);
     for (uint32_t i = threadIdx.x; i < 4096; i += 64 * DF_WAVES) {
         const uint32_t e = d_dec[i];  // sym | (f - 1) << 8 | cum << 20
-        reinterpret_cast<uint2*>(lds)[i] = make_uint2((((e >> 8) & 4095u) + 1u) | ((e & 255u) << 24), i - (e >> 20));
+        lds[i] = (e & 0x000FFF00u) << 4 | (i - (e >> 20)) | (e & 255u) << 24;  // sym<<24 | (f-1)<<12 | slot-cum
     }
     __syncthreads();
 
