@@ -886,7 +886,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         uint32_t* d_hist = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(jb.d_workspace) + L.off_hist);
         const int es = ckr_element_size(jb.dtype);
         hipError_t e = ckr::launch_masked_hist(static_cast<const uint8_t*>(jb.d_src), jb.n_elems * (uint64_t)es, es,
-                                               geo[i].spe, d_hist, d_hist + 256, a->s2);
+                                               geo[i].spe, d_hist, d_hist + 256, a->s2, i > 0);
         if (e != hipSuccess) return e;
         return hipMemcpyAsync(h_dst, d_hist, 768 * sizeof(uint32_t), hipMemcpyDeviceToHost, a->s2);
     };

@@ -58,9 +58,11 @@ hipError_t launch_extract_mantissa(const uint8_t* src, uint64_t n_elems, int es,
 
 // Masked histogram into d_hist[256] (overwritten); for masked dtypes, when
 // d_planes is not null, d_planes[512] receives the two live planes' histograms.
+// lean: a variant with 8 KiB of LDS per workgroup, which fits on a CU beside
+// the fast encoder's workgroup, and one workgroup per CU (same counts).
 uint32_t hist_num_blocks(uint64_t n_bytes);
 hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int spe, uint32_t* d_hist,
-                              uint32_t* d_planes, hipStream_t s);
+                              uint32_t* d_planes, hipStream_t s, bool lean = false);
 hipError_t launch_set_u64(uint64_t* p, uint64_t v, hipStream_t s);
 hipError_t launch_set_counter(unsigned long long* p, unsigned long long v, hipStream_t s);
 

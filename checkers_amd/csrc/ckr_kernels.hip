@@ -125,22 +125,22 @@ hipError_t launch_extract_mantissa(const uint8_t* src, uint64_t n_elems, int es,
 // with integer atomics (order-independent, so the result is deterministic).
 static constexpr uint32_t HIST_COPIES = 32;
 
-// LDS slot of a count: raw dtypes 32 copies of one histogram; masked dtypes 16
+// LDS slot of a count: raw dtypes 32 copies of one histogram; masked dtypes PC
 // copies of each of the two live planes (rank 0: byte 2 of fp32 / byte 1 of a
 // 16-bit pair, rank 1: byte 3), so per-plane histograms come for free.
-template <int SPE>
+template <int SPE, int PC = 16>
 __device__ __forceinline__ uint32_t hist_slot(uint32_t bin, uint32_t rank, uint32_t c) {
     if (SPE == 0) return bin * HIST_COPIES + c;
-    return (rank * 256 + bin) * 16 + (c & 15);
+    return (rank * 256 + bin) * PC + (c & (PC - 1));
 }
 
-template <int SPE>
+template <int SPE, int PC = 16>
 __device__ __forceinline__ void hist_add_dword(uint32_t* sh, uint32_t v, uint32_t c) {
 #pragma unroll
     for (int b = 0; b < 4; b++) {
         if (SPE == 2 && b < 2) continue;
         if (SPE == 1 && (b & 1) == 0) continue;
-        atomicAdd(&sh[hist_slot<SPE>((v >> (8 * b)) & 255u, b == 3 ? 1u : 0u, c)], 1u);
+        atomicAdd(&sh[hist_slot<SPE, PC>((v >> (8 * b)) & 255u, b == 3 ? 1u : 0u, c)], 1u);
     }
 }
 
@@ -152,12 +152,16 @@ __global__ void __launch_bounds__(256) hist_init_kernel(uint32_t* __restrict__ h
     if (planes) { planes[threadIdx.x] = 0; planes[256 + threadIdx.x] = 0; }
 }
 
-template <int SPE>
+// PC: copies per live plane (masked dtypes).  16 (32 KiB of LDS) when the
+// kernel has the device to itself; 4 (8 KiB) when it runs beside the fast
+// encoder, whose workgroup leaves about 14 KiB of a CU's LDS free.
+template <int SPE, int PC>
 __global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restrict__ src, uint64_t n_bytes,
                                                           int es, uint32_t* __restrict__ hist,
                                                           uint32_t* __restrict__ planes) {
-    __shared__ uint32_t sh[256 * HIST_COPIES];
-    for (uint32_t i = threadIdx.x; i < 256 * HIST_COPIES; i += blockDim.x) sh[i] = 0;
+    constexpr uint32_t NSH = SPE == 0 ? 256 * HIST_COPIES : 512 * PC;
+    __shared__ uint32_t sh[NSH];
+    for (uint32_t i = threadIdx.x; i < NSH; i += blockDim.x) sh[i] = 0;
     __syncthreads();
     const uint32_t c = threadIdx.x & (HIST_COPIES - 1);
     const uint64_t nvec = n_bytes / 16;
@@ -166,26 +170,26 @@ __global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restr
     uint64_t v = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     for (; v + 3 * stride < nvec; v += 4 * stride) {  // 4 loads in flight per thread
         uint4 a = v4[v], b = v4[v + stride], d = v4[v + 2 * stride], e = v4[v + 3 * stride];
-        hist_add_dword<SPE>(sh, a.x, c); hist_add_dword<SPE>(sh, a.y, c);
-        hist_add_dword<SPE>(sh, a.z, c); hist_add_dword<SPE>(sh, a.w, c);
-        hist_add_dword<SPE>(sh, b.x, c); hist_add_dword<SPE>(sh, b.y, c);
-        hist_add_dword<SPE>(sh, b.z, c); hist_add_dword<SPE>(sh, b.w, c);
-        hist_add_dword<SPE>(sh, d.x, c); hist_add_dword<SPE>(sh, d.y, c);
-        hist_add_dword<SPE>(sh, d.z, c); hist_add_dword<SPE>(sh, d.w, c);
-        hist_add_dword<SPE>(sh, e.x, c); hist_add_dword<SPE>(sh, e.y, c);
-        hist_add_dword<SPE>(sh, e.z, c); hist_add_dword<SPE>(sh, e.w, c);
+        hist_add_dword<SPE, PC>(sh, a.x, c); hist_add_dword<SPE, PC>(sh, a.y, c);
+        hist_add_dword<SPE, PC>(sh, a.z, c); hist_add_dword<SPE, PC>(sh, a.w, c);
+        hist_add_dword<SPE, PC>(sh, b.x, c); hist_add_dword<SPE, PC>(sh, b.y, c);
+        hist_add_dword<SPE, PC>(sh, b.z, c); hist_add_dword<SPE, PC>(sh, b.w, c);
+        hist_add_dword<SPE, PC>(sh, d.x, c); hist_add_dword<SPE, PC>(sh, d.y, c);
+        hist_add_dword<SPE, PC>(sh, d.z, c); hist_add_dword<SPE, PC>(sh, d.w, c);
+        hist_add_dword<SPE, PC>(sh, e.x, c); hist_add_dword<SPE, PC>(sh, e.y, c);
+        hist_add_dword<SPE, PC>(sh, e.z, c); hist_add_dword<SPE, PC>(sh, e.w, c);
     }
     for (; v < nvec; v += stride) {
         uint4 a = v4[v];
-        hist_add_dword<SPE>(sh, a.x, c); hist_add_dword<SPE>(sh, a.y, c);
-        hist_add_dword<SPE>(sh, a.z, c); hist_add_dword<SPE>(sh, a.w, c);
+        hist_add_dword<SPE, PC>(sh, a.x, c); hist_add_dword<SPE, PC>(sh, a.y, c);
+        hist_add_dword<SPE, PC>(sh, a.z, c); hist_add_dword<SPE, PC>(sh, a.w, c);
     }
     if (blockIdx.x == 0) {  // tail bytes
         for (uint64_t p = nvec * 16 + threadIdx.x; p < n_bytes; p += blockDim.x) {
             const int plane = (int)(p % (uint64_t)es);
             if (plane < SPE) continue;
             const uint32_t r = (SPE > 0 && (p & 3) == 3) ? 1u : 0u;  // live-plane rank
-            atomicAdd(&sh[hist_slot<SPE>((uint32_t)src[p], r, c)], 1u);
+            atomicAdd(&sh[hist_slot<SPE, PC>((uint32_t)src[p], r, c)], 1u);
         }
     }
     __syncthreads();
@@ -198,9 +202,9 @@ __global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restr
     } else {
         uint32_t s0 = 0, s1 = 0;
 #pragma unroll 8
-        for (uint32_t k = 0; k < 16; k++) {
-            s0 += sh[hist_slot<SPE>(bin, 0, (k + bin) & 15)];
-            s1 += sh[hist_slot<SPE>(bin, 1, (k + bin) & 15)];
+        for (uint32_t k = 0; k < (uint32_t)PC; k++) {
+            s0 += sh[hist_slot<SPE, PC>(bin, 0, (k + bin) & (PC - 1))];
+            s1 += sh[hist_slot<SPE, PC>(bin, 1, (k + bin) & (PC - 1))];
         }
         if (s0 + s1) atomicAdd(&hist[bin], s0 + s1);
         if (planes) {  // per live plane, rank 0 / rank 1
@@ -219,17 +223,27 @@ uint32_t hist_num_blocks(uint64_t n_bytes) {
 }
 
 hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int spe, uint32_t* d_hist,
-                              uint32_t* d_planes, hipStream_t s) {
+                              uint32_t* d_planes, hipStream_t s, bool lean) {
     const uint64_t zero_count = (es > 0) ? (n_bytes / (uint64_t)es) * (uint64_t)spe : 0;
     if (spe == 0) d_planes = nullptr;
     CKR_LAUNCH("hist_init_kernel", s, hist_init_kernel<<<1, 256, 0, s>>>(d_hist, zero_count, d_planes));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (n_bytes == 0) return hipSuccess;
-    const uint32_t nblk = hist_num_blocks(n_bytes);
-    if (spe == 2) CKR_LAUNCH("masked_hist_kernel", s, masked_hist_kernel<2><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist, d_planes));
-    else if (spe == 1) CKR_LAUNCH("masked_hist_kernel", s, masked_hist_kernel<1><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist, d_planes));
-    else CKR_LAUNCH("masked_hist_kernel", s, masked_hist_kernel<0><<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist, nullptr));
+    uint32_t nblk = hist_num_blocks(n_bytes);
+    if (lean) {
+        // one workgroup per CU: beside a running encoder the pass then takes
+        // about the encoder's spare HBM bandwidth; at full width it takes all of
+        // it and the latency-bound encoder slows by as much as the pass saves
+        int dev = 0, ncu = 0;
+        if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+        if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+        if (ncu > 0 && nblk > (uint32_t)ncu) nblk = (uint32_t)ncu;
+    }
+    auto run = [&](auto kern) { CKR_LAUNCH("masked_hist_kernel", s, kern<<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist, d_planes)); };
+    if (spe == 2) lean ? run(masked_hist_kernel<2, 4>) : run(masked_hist_kernel<2, 16>);
+    else if (spe == 1) lean ? run(masked_hist_kernel<1, 4>) : run(masked_hist_kernel<1, 16>);
+    else run(masked_hist_kernel<0, 16>);
     return hipGetLastError();
 }
 

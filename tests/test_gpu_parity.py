@@ -367,3 +367,28 @@ def test_compress_many_matches_single_calls(unit, gpu):
         dst, bad = ck.decode(m)
         torch.cuda.synchronize()
         assert bad == 0 and np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
+
+
+def test_compress_many_large_overlapped_histogram(gpu):
+    """A tensor large enough that the histogram run beside the previous encode
+    (8 KiB of LDS, one workgroup per CU) covers it in several strides per
+    thread: compress_many still gives exactly what ckr_compress gives."""
+    import torch
+    ck = _ck()
+    unit = 65536
+    g = torch.Generator(device=gpu).manual_seed(80)
+    a = (torch.randn(3_000_001, device=gpu, generator=g) * 0.02).to(torch.bfloat16)
+    b = torch.randn(16_777_216 + 4096 + 7, device=gpu, generator=g) * 1e-3
+    srcs = [a.view(torch.uint8), b.view(torch.uint8)]
+    specs = [(dg.BF16, a.numel()), (dg.F32, b.numel())]
+    print("[case] compress_many large overlapped histogram", flush=True)
+    many = ck.compress_many([ck.Encoder(n, dt, unit, device=gpu) for dt, n in specs], srcs)
+    one = [ck.Encoder(n, dt, unit, device=gpu).compress(t) for (dt, n), t in zip(specs, srcs)]
+    torch.cuda.synchronize()
+    for m, o in zip(many, one):
+        assert np.array_equal(m.table.norm, o.table.norm)
+        assert m.total == o.total
+        assert np.array_equal(m.data_np(), o.data_np())
+        assert np.array_equal(m.headers_np(), o.headers_np())
+        assert torch.equal(m.unit_offsets, o.unit_offsets)
+        assert torch.equal(m.sidecar, o.sidecar)
