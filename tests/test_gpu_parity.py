@@ -392,3 +392,38 @@ def test_compress_many_large_overlapped_histogram(gpu):
         assert np.array_equal(m.headers_np(), o.headers_np())
         assert torch.equal(m.unit_offsets, o.unit_offsets)
         assert torch.equal(m.sidecar, o.sidecar)
+
+
+def test_cfg3_size_tensors_through_compress_many(gpu):
+    """One bf16 and one fp32 tensor of cfg3's shape (1,003,782,656 elements,
+    the Llama-3-8B ZeRO-3 rank-0-of-8 share; 6 GB) through ckr_compress_many,
+    at a size the oracle cannot code in seconds.  Checked by what holds at any
+    size: the table equals the oracle's normalize_histogram of a histogram
+    torch counts independently (the zero planes counted in closed form), the
+    sidecar equals the input's low bytes, unit offsets are monotone and end at
+    the total, and the decode is bit-exact with every lane's postconditions met."""
+    import torch
+    ck = _ck()
+    n, unit = 1_003_782_656, 65536
+    g = torch.Generator(device=gpu).manual_seed(90)
+    tensors = [(dg.BF16, (torch.randn(n, device=gpu, generator=g) * 0.02).to(torch.bfloat16)),
+               (dg.F32, torch.randn(n, device=gpu, generator=g) * 1e-3)]
+    print("[case] cfg3-size bf16 + fp32 through compress_many", flush=True)
+    encs = [ck.Encoder(n, dt, unit, device=gpu) for dt, _ in tensors]
+    res = ck.compress_many(encs, [t.view(torch.uint8) for _, t in tensors])
+    torch.cuda.synchronize()
+    for (dt, t), r in zip(tensors, res):
+        es, spe = oc.ES[dt], oc.SPE[dt]
+        by = t.view(torch.uint8).view(n, es)
+        hist = torch.bincount(by[:, spe:].reshape(-1), minlength=256).cpu().numpy().astype(np.uint64)
+        hist[0] += n * spe
+        assert int(hist.max()) < (1 << 32)  # no u32 wrap at this size
+        want, tsum = oc.normalize_histogram(hist.astype(np.uint32))
+        assert tsum == 4096 and np.array_equal(r.table.norm, want["norm_freq"])
+        assert torch.equal(r.sidecar[: n * spe].view(n, spe), by[:, :spe])
+        uo = r.unit_offsets
+        assert int(uo[0]) == 0 and int(uo[-1]) == r.total and bool((uo[1:] >= uo[:-1]).all())
+        dst, bad = ck.decode(r)
+        torch.cuda.synchronize()
+        assert bad == 0 and torch.equal(dst, t.view(torch.uint8))
+        del dst
