@@ -246,6 +246,10 @@ class Encoded:
         self.data, self.headers, self.unit_offsets, self.sidecar = data, headers, unit_offsets, sidecar
         self.total, self.n_elems, self.dtype, self.unit_bytes, self.table = total, n_elems, dtype, unit_bytes, table
 
+    @property
+    def n_units(self):
+        return self.unit_offsets.numel() - 1
+
     def headers_np(self):
         return self.headers.cpu().numpy().view(HEADER_DTYPE).reshape(-1)
 
@@ -314,7 +318,10 @@ def compress_many(encoders, srcs, ensure_full_alphabet=False, stream=None):
     """ckr_compress_many: each (Encoder, source) pair compressed as Encoder.compress
     would, the next tensor's histogram overlapping the current one's encode.
     Every encoder must use the same unit size.  Returns one Encoded per pair."""
-    assert len(encoders) == len(srcs) and len({e.unit_bytes for e in encoders}) <= 1
+    if len(encoders) != len(srcs) or len({e.unit_bytes for e in encoders}) > 1:
+        raise CkrError(CKR_E_INVALID, "compress_many: one source per encoder, all encoders of one unit size")
+    if len({id(e) for e in encoders}) != len(encoders):
+        raise CkrError(CKR_E_INVALID, "compress_many: an Encoder appears twice (its buffers would be shared)")
     if not encoders:
         return []
     jobs = (CompressJob * len(encoders))()

@@ -55,6 +55,66 @@ constexpr uint64_t kScratchBudget = 2ull << 30;  // lane scratch per encode batc
 
 inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned_to(const void* p, uint64_t a) { return a == 0 || reinterpret_cast<uintptr_t>(p) % a == 0; }
+
+// Device-pointer check before anything is launched on a caller's buffer.  The
+// reference validates each tensor pointer with hipPointerGetAttributes before
+// its kernels run (src/ANSCompressor.cpp:567-585, :1177-1202), so that a
+// freed or foreign pointer is an error instead of a GPU fault; here the byte
+// range [p, p + bytes) must also lie inside the allocation holding p.  A
+// failed query leaves an error in the runtime's last-error slot, which would
+// be taken for a failed launch later, so it is cleared.
+int check_buffer(const void* p, uint64_t bytes, const char* what) {
+    if (bytes == 0) return CKR_OK;
+    if (!p) return fail(CKR_E_INVALID, "[ckr] null %s pointer", what);
+    hipPointerAttribute_t a;
+    std::memset(&a, 0, sizeof(a));
+    const hipError_t e = hipPointerGetAttributes(&a, p);
+    if (e != hipSuccess || a.type == hipMemoryTypeUnregistered) {
+        (void)hipGetLastError();
+        return fail(CKR_E_INVALID, "[ckr] %s pointer %p is not device-accessible memory (%s)", what, p,
+                    e != hipSuccess ? hipGetErrorString(e) : "unregistered host memory");
+    }
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    if (hipMemGetAddressRange(&base, &size, const_cast<void*>(p)) == hipSuccess && base) {
+        const uintptr_t b = reinterpret_cast<uintptr_t>(base), q = reinterpret_cast<uintptr_t>(p);
+        if (q < b || q - b > size || bytes > size - (q - b))
+            return fail(CKR_E_INVALID, "[ckr] %s [%p, +%llu bytes) runs past its allocation (%llu bytes at %p)", what, p,
+                        (unsigned long long)bytes, (unsigned long long)size, base);
+    } else {
+        (void)hipGetLastError();  // memory the range query does not cover (pinned host): type check only
+    }
+    return CKR_OK;
+}
+
+// A source the kernels can read with 32-bit loads at its 4-byte columns.  A
+// tensor that is only element-aligned (a 16-bit or 8-bit tensor starting at an
+// address that is not a multiple of 4, e.g. a slice at an odd element offset
+// of a flat buffer) is copied once into a stream-ordered aligned buffer, freed
+// again in stream order after the last kernel that reads it.
+struct Staged {
+    const void* p = nullptr;
+    void* tmp = nullptr;
+    int make(const void* src, uint64_t bytes, hipStream_t s) {
+        p = src;
+        if (bytes == 0 || aligned_to(src, 4)) return CKR_OK;
+        if (hipMallocAsync(&tmp, bytes, s) != hipSuccess) {
+            (void)hipGetLastError();
+            tmp = nullptr;
+            return fail(CKR_E_HIP, "[ckr] staging buffer for an unaligned source (%llu bytes) unavailable",
+                        (unsigned long long)bytes);
+        }
+        if (hipMemcpyAsync(tmp, src, bytes, hipMemcpyDeviceToDevice, s) != hipSuccess)
+            return fail(CKR_E_HIP, "[ckr] staging copy of an unaligned source failed");
+        p = tmp;
+        return CKR_OK;
+    }
+    void release(hipStream_t s) {
+        if (tmp) (void)hipFreeAsync(tmp, s);
+        tmp = nullptr;
+    }
+};
 
 bool dtype_ok(int dt) { return dt == CKR_F32 || dt == CKR_BF16 || dt == CKR_F16 || dt == CKR_I8 || dt == CKR_I32; }
 
@@ -464,8 +524,13 @@ int ckr_extract_mantissa(const void* d_src, uint64_t n_elems, int dtype, void* d
     if (spe == 0) return fail(CKR_E_INVALID, "[ckr] dtype %d has no mantissa sidecar", dtype);
     if (n_elems == 0) return CKR_OK;
     if (!d_src || !d_masked || !d_sidecar) return fail(CKR_E_INVALID, "[ckr] null pointer");
-    if (!aligned16(d_src) || !aligned16(d_masked) || !aligned16(d_sidecar))
-        return fail(CKR_E_INVALID, "[ckr] buffers must be 16-byte aligned");
+    const int es = ckr_element_size(dtype);
+    if (!aligned_to(d_src, es) || !aligned_to(d_masked, es))
+        return fail(CKR_E_INVALID, "[ckr] source and masked copy must be aligned to the element size");
+    int rc;
+    if ((rc = check_buffer(d_src, n_elems * es, "source")) || (rc = check_buffer(d_masked, n_elems * es, "masked copy")) ||
+        (rc = check_buffer(d_sidecar, n_elems * spe, "sidecar")))
+        return rc;
     CKR_HIP(ckr::launch_extract_mantissa(static_cast<const uint8_t*>(d_src), n_elems, ckr_element_size(dtype), spe,
                                          static_cast<uint8_t*>(d_masked), static_cast<uint8_t*>(d_sidecar),
                                          (hipStream_t)stream));
@@ -475,8 +540,11 @@ int ckr_extract_mantissa(const void* d_src, uint64_t n_elems, int dtype, void* d
 int ckr_byte_histogram(const void* d_src, uint64_t n_elems, int dtype, uint32_t* d_hist, void* stream) {
     if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
     if (!d_hist || (n_elems && !d_src)) return fail(CKR_E_INVALID, "[ckr] null pointer");
-    if (n_elems && !aligned16(d_src)) return fail(CKR_E_INVALID, "[ckr] source must be 16-byte aligned");
     const int es = ckr_element_size(dtype);
+    if (!aligned_to(d_src, es) || !aligned_to(d_hist, 4))
+        return fail(CKR_E_INVALID, "[ckr] source must be aligned to the element size, histogram to 4 bytes");
+    int rc;
+    if ((rc = check_buffer(d_src, n_elems * es, "source")) || (rc = check_buffer(d_hist, 1024, "histogram"))) return rc;
     CKR_HIP(ckr::launch_masked_hist(static_cast<const uint8_t*>(d_src), n_elems * (uint64_t)es, es,
                                     ckr_sidecar_bytes_per_elem(dtype), d_hist, nullptr, (hipStream_t)stream));
     return CKR_OK;
@@ -609,8 +677,8 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         return CKR_OK;
     }
     if (!d_src || !d_out || !d_headers || !d_workspace) return fail(CKR_E_INVALID, "[ckr] null pointer");
-    if (!aligned16(d_src) || !aligned16(d_workspace) || (d_sidecar && !aligned16(d_sidecar)))
-        return fail(CKR_E_INVALID, "[ckr] source, sidecar and workspace must be 16-byte aligned");
+    if (!aligned_to(d_src, 4) || !aligned16(d_workspace) || (d_sidecar && !aligned16(d_sidecar)))
+        return fail(CKR_E_INVALID, "[ckr] sidecar and workspace must be 16-byte aligned");
     if (out_capacity < g.n_bytes)
         return fail(CKR_E_CAPACITY, "[ckr] output capacity %llu < %llu", (unsigned long long)out_capacity,
                     (unsigned long long)g.n_bytes);
@@ -747,6 +815,31 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
     return CKR_OK;
 }
 
+// The caller buffers of an encode, checked before anything is queued: the
+// source element-aligned and inside its allocation, the outputs and the
+// workspace inside theirs at the sizes the header documents.
+int check_encode_args(const void* src, const ckr::EncodeGeom& g, uint64_t n_elems, const void* out,
+                      uint64_t out_capacity, const void* hdrs, const void* offs, const void* side, const void* ws,
+                      uint64_t ws_bytes) {
+    if (!aligned_to(src, (uint64_t)g.es))
+        return fail(CKR_E_INVALID, "[ckr] source %p is not aligned to its element size (%d bytes)", src, g.es);
+    if (g.n_units && out_capacity < g.n_bytes)
+        return fail(CKR_E_CAPACITY, "[ckr] output capacity %llu < %llu", (unsigned long long)out_capacity,
+                    (unsigned long long)g.n_bytes);
+    if (g.n_units && ws_bytes < encode_layout(g).total)
+        return fail(CKR_E_CAPACITY, "[ckr] workspace %llu < %llu", (unsigned long long)ws_bytes,
+                    (unsigned long long)encode_layout(g).total);
+    int rc;
+    if ((rc = check_buffer(offs, (g.n_units + 1) * 8, "unit offsets"))) return rc;
+    if (g.n_units == 0) return CKR_OK;
+    if ((rc = check_buffer(src, g.n_bytes, "source")) || (rc = check_buffer(out, out_capacity, "output")) ||
+        (rc = check_buffer(hdrs, g.n_units * 256 * sizeof(ckr_stream_header), "headers")) ||
+        (rc = check_buffer(ws, ws_bytes, "workspace")))
+        return rc;
+    if (side && g.spe && (rc = check_buffer(side, n_elems * (uint64_t)g.spe, "sidecar"))) return rc;
+    return CKR_OK;
+}
+
 // After the stream has passed a deferred encode: its checks, its total, and the
 // redo batches of the fast path (queued; the caller synchronises once more).
 int encode_complete(const EncodeDeferred& d, uint64_t* total, bool* queued_more, hipStream_t s) {
@@ -772,8 +865,20 @@ int ckr_encode(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_ta
                uint8_t* d_out, uint64_t out_capacity, ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
                uint8_t* d_sidecar, void* d_workspace, uint64_t workspace_bytes, uint64_t* h_total_out,
                void* stream) {
-    return encode_impl(d_src, n_elems, dtype, h_table, unit_bytes, d_out, out_capacity, d_headers, d_unit_offsets,
-                       d_sidecar, d_workspace, workspace_bytes, h_total_out, nullptr, stream);
+    if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
+    ckr::EncodeGeom g;
+    if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
+    if (!h_table || !d_unit_offsets) return fail(CKR_E_INVALID, "[ckr] null table or offsets");
+    int rc = check_encode_args(d_src, g, n_elems, d_out, out_capacity, d_headers, d_unit_offsets, d_sidecar, d_workspace,
+                               workspace_bytes);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    Staged st;
+    if ((rc = st.make(d_src, g.n_bytes, s))) return rc;
+    rc = encode_impl(st.p, n_elems, dtype, h_table, unit_bytes, d_out, out_capacity, d_headers, d_unit_offsets,
+                     d_sidecar, d_workspace, workspace_bytes, h_total_out, nullptr, stream);
+    st.release(s);
+    return rc;
 }
 
 int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_bytes, int ensure_full_alphabet,
@@ -787,24 +892,36 @@ int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_b
     if (!d_workspace || workspace_bytes < L.total)
         return fail(CKR_E_CAPACITY, "[ckr] workspace too small (%llu < %llu)", (unsigned long long)workspace_bytes,
                     (unsigned long long)L.total);
-    if (n_elems && (!d_src || !aligned16(d_src))) return fail(CKR_E_INVALID, "[ckr] source must be 16-byte aligned");
+    if (n_elems && !d_src) return fail(CKR_E_INVALID, "[ckr] null source");
+    if (!d_unit_offsets) return fail(CKR_E_INVALID, "[ckr] null offsets");
+    int rc = check_encode_args(d_src, g, n_elems, d_out, out_capacity, d_headers, d_unit_offsets, d_sidecar, d_workspace,
+                               workspace_bytes);
+    if (rc) return rc;
     hipStream_t s = (hipStream_t)stream;
+    Staged st;
+    if ((rc = st.make(d_src, g.n_bytes, s))) return rc;
     uint32_t* d_hist = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(d_workspace) + L.off_hist);
     const int es = ckr_element_size(dtype);
-    CKR_HIP(ckr::launch_masked_hist(static_cast<const uint8_t*>(d_src), n_elems * (uint64_t)es, es, g.spe, d_hist,
-                                    d_hist + 256, s));
+    hipError_t he = ckr::launch_masked_hist(static_cast<const uint8_t*>(st.p), n_elems * (uint64_t)es, es, g.spe, d_hist,
+                                            d_hist + 256, s);
     uint32_t* pw = pinned_words();
-    if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
-    CKR_HIP(hipMemcpyAsync(pw, d_hist, 768 * 4, hipMemcpyDeviceToHost, s));
-    CKR_HIP(hipStreamSynchronize(s));
+    if (he == hipSuccess && pw) he = hipMemcpyAsync(pw, d_hist, 768 * 4, hipMemcpyDeviceToHost, s);
+    if (he == hipSuccess && pw) he = hipStreamSynchronize(s);
+    if (he != hipSuccess || !pw) {
+        st.release(s);
+        return pw ? fail(CKR_E_HIP, "[ckr] histogram failed: %s", hipGetErrorString(he))
+                  : fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
+    }
     uint32_t hh[768];
     std::memcpy(hh, pw, sizeof(hh));
     ckr_freq_table local;
     ckr_freq_table* t = h_table ? h_table : &local;
-    int rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
-    if (rc) return rc;
-    return encode_impl(d_src, n_elems, dtype, t, unit_bytes, d_out, out_capacity, d_headers, d_unit_offsets,
-                       d_sidecar, d_workspace, workspace_bytes, h_total_out, g.spe ? hh + 256 : nullptr, stream);
+    rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
+    if (rc == CKR_OK)
+        rc = encode_impl(st.p, n_elems, dtype, t, unit_bytes, d_out, out_capacity, d_headers, d_unit_offsets, d_sidecar,
+                         d_workspace, workspace_bytes, h_total_out, g.spe ? hh + 256 : nullptr, stream);
+    st.release(s);
+    return rc;
 }
 
 // The second stream, its event and the pinned histogram buffers of
@@ -838,6 +955,10 @@ hipError_t many_aux(ManyAux** out) {
 }
 }  // namespace
 
+static int set_job_error(int rc, uint64_t i) {
+    return ckr::set_error(rc, "job " + std::to_string(i) + ": " + ckr_last_error());
+}
+
 int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, int ensure_full_alphabet,
                       void* stream) {
     if (n == 0) return CKR_OK;
@@ -851,12 +972,37 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         const EncodeLayout L = encode_layout(geo[i]);
         if (!jb.d_workspace || jb.workspace_bytes < L.total || !aligned16(jb.d_workspace))
             return fail(CKR_E_CAPACITY, "[ckr] job %llu: workspace too small or misaligned", (unsigned long long)i);
-        if (jb.n_elems && (!jb.d_src || !aligned16(jb.d_src)))
-            return fail(CKR_E_INVALID, "[ckr] job %llu: source must be 16-byte aligned", (unsigned long long)i);
+        if ((jb.n_elems && !jb.d_src) || !jb.d_unit_offsets)
+            return fail(CKR_E_INVALID, "[ckr] job %llu: null source or offsets", (unsigned long long)i);
+        const int rc = check_encode_args(jb.d_src, geo[i], jb.n_elems, jb.d_out, jb.out_capacity, jb.d_headers,
+                                         jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace, jb.workspace_bytes);
+        if (rc) return set_job_error(rc, i);
+        for (uint64_t k = 0; k < i; k++)  // jobs share no output or workspace
+            if (jobs[k].d_workspace == jb.d_workspace || (jb.n_elems && jobs[k].d_out == jb.d_out))
+                return fail(CKR_E_INVALID, "[ckr] jobs %llu and %llu share an output or workspace buffer",
+                            (unsigned long long)k, (unsigned long long)i);
     }
     hipStream_t s = (hipStream_t)stream;
     ManyAux* a = nullptr;
     CKR_HIP(many_aux(&a));
+    // sources that are only element-aligned: aligned copies, queued before the
+    // event the histogram stream waits for, freed once every job is complete
+    std::vector<Staged> staged(n);
+    struct Release {
+        std::vector<Staged>& v;
+        hipStream_t s, s2;
+        ~Release() {
+            bool any = false;
+            for (auto& x : v) any = any || x.tmp;
+            if (!any) return;
+            (void)hipStreamSynchronize(s2);  // an error path may leave a histogram reading them
+            for (auto& x : v) x.release(s);
+        }
+    } release_staged{staged, s, a->s2};
+    for (uint64_t i = 0; i < n; i++) {
+        const int rc = staged[i].make(jobs[i].d_src, geo[i].n_bytes, s);
+        if (rc) return rc;
+    }
     if (a->slot_jobs < n) {
         if (a->slots) CKR_HIP(hipHostFree(a->slots));
         a->slots = nullptr;
@@ -885,7 +1031,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         const EncodeLayout L = encode_layout(geo[i]);
         uint32_t* d_hist = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(jb.d_workspace) + L.off_hist);
         const int es = ckr_element_size(jb.dtype);
-        hipError_t e = ckr::launch_masked_hist(static_cast<const uint8_t*>(jb.d_src), jb.n_elems * (uint64_t)es, es,
+        hipError_t e = ckr::launch_masked_hist(static_cast<const uint8_t*>(staged[i].p), jb.n_elems * (uint64_t)es, es,
                                                geo[i].spe, d_hist, d_hist + 256, a->s2, i > 0);
         if (e != hipSuccess) return e;
         return hipMemcpyAsync(h_dst, d_hist, 768 * sizeof(uint32_t), hipMemcpyDeviceToHost, a->s2);
@@ -914,7 +1060,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         };
         // the encode is only queued: its read-backs are checked at the end, so
         // the next encode follows it on the stream without a host round trip
-        rc = encode_impl(jb.d_src, jb.n_elems, jb.dtype, t, unit_bytes, jb.d_out, jb.out_capacity, jb.d_headers,
+        rc = encode_impl(staged[i].p, jb.n_elems, jb.dtype, t, unit_bytes, jb.d_out, jb.out_capacity, jb.d_headers,
                          jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace, jb.workspace_bytes, nullptr,
                          geo[i].spe ? hh + 256 : nullptr, stream, &next, &defs[i]);
         if (rc) {
@@ -946,10 +1092,21 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
     if (!h_table || !d_data || !d_headers || !d_unit_offsets || !d_dst || !d_workspace)
         return fail(CKR_E_INVALID, "[ckr] null pointer");
     if (g.spe && !d_sidecar) return fail(CKR_E_INVALID, "[ckr] dtype %d needs its sidecar", dtype);
-    if (!aligned16(d_dst) || !aligned16(d_workspace) || (d_sidecar && !aligned16(d_sidecar)))
-        return fail(CKR_E_INVALID, "[ckr] destination, sidecar and workspace must be 16-byte aligned");
+    if (!aligned_to(d_dst, (uint64_t)g.es) || !aligned16(d_workspace) || (d_sidecar && !aligned16(d_sidecar)))
+        return fail(CKR_E_INVALID, "[ckr] destination must be aligned to the element size, sidecar and workspace to 16 bytes");
     const DecodeLayout L = decode_layout(g);
     if (workspace_bytes < L.total) return fail(CKR_E_CAPACITY, "[ckr] decode workspace too small");
+    if (h_table->cum_freq[256] != CKR_M)
+        return fail(CKR_E_TABLE, "[ckr] table sums to %u, not 4096: stream not decodable", h_table->cum_freq[256]);
+    {
+        int rc;
+        if ((rc = check_buffer(d_data, 1, "compressed data")) ||
+            (rc = check_buffer(d_headers, g.n_units * 256 * sizeof(ckr_stream_header), "headers")) ||
+            (rc = check_buffer(d_unit_offsets, (g.n_units + 1) * 8, "unit offsets")) ||
+            (rc = check_buffer(d_dst, g.n_bytes, "destination")) || (rc = check_buffer(d_workspace, L.total, "workspace")))
+            return rc;
+        if (g.spe && (rc = check_buffer(d_sidecar, n_elems * (uint64_t)g.spe, "sidecar"))) return rc;
+    }
     if (h_table->cum_freq[256] != CKR_M)
         return fail(CKR_E_TABLE, "[ckr] table sums to %u, not 4096: stream not decodable", h_table->cum_freq[256]);
     ckr::TableArg ta;
@@ -963,8 +1120,24 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
     CKR_HIP(ckr::launch_build_dec_table(ta, dec, s));
     if (L.fast) CKR_HIP(canon_launch(h_table, ck, canon, s));
     CKR_HIP(ckr::launch_set_counter(bad, 0, s));
-    CKR_HIP(ckr::launch_decode(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, static_cast<uint8_t*>(d_dst),
-                               bad, L.fast ? canon : nullptr, ck.cw, s));
+    // the decoders store 32-bit words at the 4-byte columns of the destination:
+    // a destination that is only element-aligned receives a copy
+    uint8_t* out = static_cast<uint8_t*>(d_dst);
+    void* tmp = nullptr;
+    if (!aligned_to(d_dst, 4)) {
+        if (hipMallocAsync(&tmp, g.n_bytes, s) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(CKR_E_HIP, "[ckr] staging buffer for an unaligned destination unavailable");
+        }
+        out = static_cast<uint8_t*>(tmp);
+    }
+    hipError_t de = ckr::launch_decode(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, out, bad,
+                                       L.fast ? canon : nullptr, ck.cw, s);
+    if (tmp) {
+        if (de == hipSuccess) de = hipMemcpyAsync(d_dst, tmp, g.n_bytes, hipMemcpyDeviceToDevice, s);
+        (void)hipFreeAsync(tmp, s);
+    }
+    if (de != hipSuccess) return fail(CKR_E_HIP, "[ckr] decode launch failed: %s", hipGetErrorString(de));
     if (h_bad_lanes) {
         uint32_t* pw = pinned_words();
         if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");

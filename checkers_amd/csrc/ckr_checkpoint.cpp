@@ -456,6 +456,36 @@ bool read_at(std::ifstream& f, uint64_t off, void* p, uint64_t n) {
     return (uint64_t)f.gcount() == n;
 }
 std::string cstr(const char* b) { return std::string(b, strnlen(b, 256)); }
+// Unit offsets and lane headers read from a file, checked on the host before
+// anything reaches the device (the decoders take them as an encode wrote them):
+// offsets start at 0, never decrease and end at the data size; no unit is
+// longer than its input bytes (the passthrough rule bounds every unit by its
+// length); a raw unit is exactly its length with only header 0 set; every
+// lane's stream lies inside its unit.
+int check_unit_metadata(const std::vector<ckr_stream_header>& hdr, const std::vector<uint64_t>& uoff, uint64_t nu,
+                        uint64_t n_bytes, uint64_t unit, uint64_t data_size, const std::string& name) {
+    const std::string what = "[ckr] corrupt unit metadata for " + name + ": ";
+    if (uoff.size() != nu + 1 || hdr.size() != nu * 256) return err(CKR_E_CORRUPT, what + "sizes");
+    if (uoff[0] != 0) return err(CKR_E_CORRUPT, what + "first unit offset is not 0");
+    if (uoff[nu] != data_size) return err(CKR_E_CORRUPT, what + "last unit offset is not the data size");
+    for (uint64_t u = 0; u < nu; u++) {
+        if (uoff[u + 1] < uoff[u]) return err(CKR_E_CORRUPT, what + "unit offsets decrease at unit " + std::to_string(u));
+        const uint64_t size = uoff[u + 1] - uoff[u];
+        const uint64_t len = std::min<uint64_t>(unit, n_bytes - u * unit);
+        if (size > len) return err(CKR_E_CORRUPT, what + "unit " + std::to_string(u) + " is longer than its input");
+        const ckr_stream_header* h = &hdr[u * 256];
+        if (size == len && h[0].byte_count == len) {
+            for (int t = 1; t < 256; t++)
+                if (h[t].byte_count) return err(CKR_E_CORRUPT, what + "raw unit " + std::to_string(u) + " has lane bytes");
+            continue;
+        }
+        for (int t = 0; t < 256; t++)
+            if ((uint64_t)h[t].buf_offset + h[t].byte_count > size)
+                return err(CKR_E_CORRUPT, what + "lane " + std::to_string(t) + " of unit " + std::to_string(u) +
+                                              " runs past its unit");
+    }
+    return CKR_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -585,7 +615,12 @@ int ckr_ckpt_restore(const ckr_ckpt* c, uint64_t i, void* d_dst, void* stream) {
     const uint64_t unit = c->version == 3 ? c->unit_bytes : 0;
     const uint64_t nu = ckr_num_units(x.n_elems, x.dtype, unit);
     if (nu != x.n_units) return err(CKR_E_CORRUPT, "[ckr] unit count mismatch for " + x.name);
-    std::ifstream f(c->dir / ("rank_" + std::to_string(c->rank) + "_states.ansc"), std::ios::binary);
+    const fs::path sp = c->dir / ("rank_" + std::to_string(c->rank) + "_states.ansc");
+    std::error_code fec;
+    const uint64_t fsize = fs::file_size(sp, fec);
+    if (fec || nu > fsize / 4096 + 1 || x.data_size > fsize)
+        return err(CKR_E_CORRUPT, "[ckr] entry " + x.name + " does not fit its file");
+    std::ifstream f(sp, std::ios::binary);
     std::vector<ckr_stream_header> hdr(nu * 256);
     std::vector<uint64_t> uoff(nu + 1);
     if (c->version == 3) {
@@ -597,7 +632,8 @@ int ckr_ckpt_restore(const ckr_ckpt* c, uint64_t i, void* d_dst, void* stream) {
         uoff[0] = 0;
         uoff[1] = x.data_size;
     }
-    if (uoff[nu] != x.data_size) return err(CKR_E_CORRUPT, "[ckr] data size mismatch for " + x.name);
+    if (int rc = check_unit_metadata(hdr, uoff, nu, x.original, unit ? unit : x.original, x.data_size, x.name))
+        return rc;
     std::vector<uint8_t> data(std::max<uint64_t>(x.data_size, 1));
     if (x.data_size && !read_at(f, c->data_base + x.data_off, data.data(), x.data_size))
         return err(CKR_E_CORRUPT, "[ckr] truncated data for " + x.name);

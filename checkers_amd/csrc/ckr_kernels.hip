@@ -106,12 +106,37 @@ __global__ void __launch_bounds__(256) extract_mantissa_kernel(const uint8_t* __
     }
 }
 
+// The same split one byte per thread, for buffers that are only element-aligned.
+template <int SPE>
+__global__ void __launch_bounds__(256) extract_mantissa_bytes_kernel(const uint8_t* __restrict__ src,
+                                                                     uint64_t n_bytes,
+                                                                     uint8_t* __restrict__ masked,
+                                                                     uint8_t* __restrict__ sidecar) {
+    constexpr int es = SPE == 2 ? 4 : 2;
+    for (uint64_t p = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; p < n_bytes;
+         p += (uint64_t)gridDim.x * blockDim.x) {
+        const uint8_t b = src[p];
+        const int plane = (int)(p % es);
+        masked[p] = plane < SPE ? 0 : b;
+        if (plane < SPE) sidecar[(p / es) * SPE + plane] = b;
+    }
+}
+
 hipError_t launch_extract_mantissa(const uint8_t* src, uint64_t n_elems, int es, int spe,
                                    uint8_t* masked, uint8_t* sidecar, hipStream_t s) {
     const uint64_t n_bytes = n_elems * (uint64_t)es;
     const uint64_t nvec = n_bytes / 16;
     uint32_t grid = (uint32_t)std::min<uint64_t>((nvec + 255) / 256, 8192);
     if (grid == 0) grid = 1;
+    const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(masked) |
+                       reinterpret_cast<uintptr_t>(sidecar)) & 15u) == 0;
+    if (!vec) {
+        grid = (uint32_t)std::min<uint64_t>((n_bytes + 255) / 256, 8192);
+        if (grid == 0) grid = 1;
+        if (spe == 2) CKR_LAUNCH("extract_mantissa_bytes_kernel", s, extract_mantissa_bytes_kernel<2><<<grid, 256, 0, s>>>(src, n_bytes, masked, sidecar));
+        else CKR_LAUNCH("extract_mantissa_bytes_kernel", s, extract_mantissa_bytes_kernel<1><<<grid, 256, 0, s>>>(src, n_bytes, masked, sidecar));
+        return hipGetLastError();
+    }
     if (spe == 2) CKR_LAUNCH("extract_mantissa_kernel", s, extract_mantissa_kernel<2><<<grid, 256, 0, s>>>(src, n_bytes, masked, sidecar));
     else CKR_LAUNCH("extract_mantissa_kernel", s, extract_mantissa_kernel<1><<<grid, 256, 0, s>>>(src, n_bytes, masked, sidecar));
     return hipGetLastError();
@@ -155,15 +180,29 @@ __global__ void __launch_bounds__(256) hist_init_kernel(uint32_t* __restrict__ h
 // PC: copies per live plane (masked dtypes).  16 (32 KiB of LDS) when the
 // kernel has the device to itself; 4 (8 KiB) when it runs beside the fast
 // encoder, whose workgroup leaves about 14 KiB of a CU's LDS free.
+//
+// src is 16-byte aligned; the head_n (< 16) bytes before it, at src - head_n,
+// are the tensor's first bytes when the tensor itself is only element-aligned
+// (head_n is then a multiple of the element size, so every byte keeps its
+// plane).  Positions below are counted from src; a head byte at src - head_n +
+// i is at position i - head_n.
 template <int SPE, int PC>
 __global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restrict__ src, uint64_t n_bytes,
                                                           int es, uint32_t* __restrict__ hist,
-                                                          uint32_t* __restrict__ planes) {
+                                                          uint32_t* __restrict__ planes, uint32_t head_n) {
     constexpr uint32_t NSH = SPE == 0 ? 256 * HIST_COPIES : 512 * PC;
     __shared__ uint32_t sh[NSH];
     for (uint32_t i = threadIdx.x; i < NSH; i += blockDim.x) sh[i] = 0;
     __syncthreads();
     const uint32_t c = threadIdx.x & (HIST_COPIES - 1);
+    if (blockIdx.x == 0 && threadIdx.x < head_n) {  // head bytes
+        const int64_t p = (int64_t)threadIdx.x - (int64_t)head_n;
+        const int plane = (int)(((p % es) + es) % es);
+        if (plane >= SPE) {
+            const uint32_t r = (SPE > 0 && (p & 3) == 3) ? 1u : 0u;
+            atomicAdd(&sh[hist_slot<SPE, PC>((uint32_t)src[p], r, c)], 1u);
+        }
+    }
     const uint64_t nvec = n_bytes / 16;
     const uint4* v4 = reinterpret_cast<const uint4*>(src);
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
@@ -230,6 +269,12 @@ hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (n_bytes == 0) return hipSuccess;
+    // an element-aligned source: its bytes up to the next 16-byte boundary are
+    // counted one at a time, the rest with 16-byte loads
+    const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(src) & 15u);
+    const uint32_t head_n = (uint32_t)std::min<uint64_t>(mis ? 16u - mis : 0u, n_bytes);
+    src += head_n;
+    n_bytes -= head_n;
     uint32_t nblk = hist_num_blocks(n_bytes);
     if (lean) {
         // one workgroup per CU: beside a running encoder the pass then takes
@@ -240,7 +285,9 @@ hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int 
         if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
         if (ncu > 0 && nblk > (uint32_t)ncu) nblk = (uint32_t)ncu;
     }
-    auto run = [&](auto kern) { CKR_LAUNCH("masked_hist_kernel", s, kern<<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist, d_planes)); };
+    auto run = [&](auto kern) {
+        CKR_LAUNCH("masked_hist_kernel", s, kern<<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist, d_planes, head_n));
+    };
     if (spe == 2) lean ? run(masked_hist_kernel<2, 4>) : run(masked_hist_kernel<2, 16>);
     else if (spe == 1) lean ? run(masked_hist_kernel<1, 4>) : run(masked_hist_kernel<1, 16>);
     else run(masked_hist_kernel<0, 16>);

@@ -146,11 +146,12 @@ def tensor_stats(raw, n, dtype, bins=256):
     return dict(histogram=h[:nb], moments=mom, minmax=mm, moments64=m64)
 
 
-def compress_tensor(raw, n, dtype, unit, ensure_full_alphabet=False):
-    """Whole reference compress path for one tensor: mask → histogram → table → encode."""
+def compress_tensor(raw, n, dtype, unit, ensure_full_alphabet=False, n_threads=1):
+    """Whole reference compress path for one tensor: mask → histogram → table → encode
+    (the encode's units spread over n_threads host threads; same bytes)."""
     masked, side = extract_mantissa(raw, n, dtype)
     table, tsum = normalize_histogram(byte_hist(masked), ensure_full_alphabet)
-    data, hdr, off = encode(masked, table, unit)
+    data, hdr, off = encode(masked, table, unit, n_threads)
     return dict(masked=masked, sidecar=side, table=table, table_sum=tsum, data=data, headers=hdr, unit_offsets=off)
 
 

@@ -1,0 +1,347 @@
+"""Every benchmark configuration at its stated size, on the GPU.
+
+Configurations (BASELINE.json configs[0..4]):
+  cfg1  fp32 4096x4096 ~N(0, 1e-3), 64 KiB units             — every byte against the oracle
+  cfg2  one Llama-3-8B decoder layer in bf16, 9 tensors        — codec, analyzer and repair against
+                                                                 the oracle (repair by properties on
+                                                                 the tensors the oracle cannot finish)
+  cfg3  Llama-3-8B ZeRO-3 rank-0-of-8 shard, 4 x 1,003,782,656 — size-independent properties plus
+                                                                 sampled units against the oracle
+  cfg4  adversarial fp32, 268,435,456 elements with a 16 Mi
+        random block, 64 KiB units                              — every byte against the oracle
+  cfg5  one 8,819,213,312-element fp32 tensor of the 70B shard,
+        1 MiB units                                             — properties (histogram with the
+                                                                 reference's u32 wrap, table, offsets,
+                                                                 bit-exact decode) plus sampled units
+
+Inputs are generated on the GPU with torch's seeded generator.  "Sampled units
+against the oracle": a unit is an independent reference stream under the
+tensor's table, so the oracle encodes the unit's own bytes with the GPU's table
+and its data, 256 headers and sidecar must equal the GPU's bytes for that unit.
+The table itself is checked against the oracle's normalize_histogram of a
+histogram torch counts independently.
+"""
+import numpy as np
+import pytest
+
+import oracle as oc
+
+pytestmark = pytest.mark.gpu
+
+UNIT64K = 65536
+U32 = 1 << 32
+
+
+def _ck():
+    import checkers_amd as ck
+    return ck
+
+
+def _gen(gpu, seed):
+    import torch
+    return torch.Generator(device=gpu).manual_seed(seed)
+
+
+def _oracle_table(enc):
+    t = np.zeros(1, oc.TABLE_DTYPE)
+    t.view(np.uint8)[:39940] = np.frombuffer(enc.table.raw_bytes(), np.uint8)
+    return t[0]
+
+
+def _torch_masked_hist(t8, n, dt, chunk=1 << 28):
+    """Masked byte histogram counted by torch (live planes by bincount, the zero
+    planes in closed form), reduced mod 2^32 as the reference's u32 counts are."""
+    import torch
+    es, spe = oc.ES[dt], oc.SPE[dt]
+    h = torch.zeros(256, dtype=torch.int64, device=t8.device)
+    for i in range(0, n, chunk):
+        m = min(chunk, n - i)
+        by = t8[i * es:(i + m) * es].view(m, es)[:, spe:].reshape(-1)
+        h += torch.bincount(by, minlength=256)
+    h = h.cpu().numpy().astype(np.uint64)
+    h[0] += np.uint64(n * spe)
+    return (h % np.uint64(U32)).astype(np.uint32)
+
+
+def _check_table(enc, t8, n, dt):
+    hist = _torch_masked_hist(t8, n, dt)
+    want, tsum = oc.normalize_histogram(hist)
+    assert np.array_equal(enc.table.norm, want["norm_freq"])
+    assert np.array_equal(enc.table.cum, want["cum_freq"])
+    return tsum
+
+
+def _check_sampled_units(enc, t8, dt, unit, units):
+    """Units of a GPU encode against the oracle's encode of each unit's bytes."""
+    import torch
+    es, spe = oc.ES[dt], oc.SPE[dt]
+    nb = enc.n_elems * es
+    table = _oracle_table(enc)
+    for u in units:
+        lo, hi = u * unit, min(nb, (u + 1) * unit)
+        raw = t8[lo:hi].cpu().numpy()
+        masked, side = oc.extract_mantissa(raw, (hi - lo) // es, dt)
+        data, hdr, off = oc.encode(masked, table, unit)
+        o0, o1 = (int(v) for v in enc.unit_offsets[u:u + 2].cpu())
+        assert o1 - o0 == data.size, (u, o1 - o0, data.size)
+        assert np.array_equal(enc.data[o0:o1].cpu().numpy(), data), u
+        gh = enc.headers[u * 1024:(u + 1) * 1024].cpu().numpy().view(oc.HEADER_DTYPE)
+        assert np.array_equal(gh, hdr), u
+        if spe:
+            gs = enc.sidecar[lo // es * spe:hi // es * spe].cpu().numpy()
+            assert np.array_equal(gs, side), u
+    torch.cuda.synchronize()
+
+
+def _check_offsets(enc):
+    uo = enc.unit_offsets
+    assert int(uo[0]) == 0 and int(uo[-1]) == enc.total and bool((uo[1:] >= uo[:-1]).all())
+
+
+def _check_decode(enc, t8, chunk=1 << 32):
+    """Bit-exact decode with every lane's postconditions met, compared in slices."""
+    import torch
+    ck = _ck()
+    dst, bad = ck.decode(enc)
+    torch.cuda.synchronize()
+    assert bad == 0
+    nb = t8.numel()
+    for i in range(0, nb, chunk):
+        assert torch.equal(dst[i:i + chunk], t8[i:i + chunk]), i
+    del dst
+
+
+def _full_oracle(enc, raw, n, dt, unit, n_threads=16):
+    ref = oc.compress_tensor(raw, n, dt, unit, n_threads=n_threads)
+    assert np.array_equal(enc.table.norm, ref["table"]["norm_freq"])
+    assert np.array_equal(enc.table.cum, ref["table"]["cum_freq"])
+    assert enc.total == ref["data"].size
+    nu = ref["unit_offsets"].size - 1
+    assert np.array_equal(enc.unit_offsets[: nu + 1].cpu().numpy().view(np.uint64), ref["unit_offsets"])
+    assert np.array_equal(enc.headers_np()[: nu * 256], ref["headers"])
+    assert np.array_equal(enc.data_np(), ref["data"])
+    spe = oc.SPE[dt]
+    if spe:
+        assert np.array_equal(enc.sidecar[: n * spe].cpu().numpy(), ref["sidecar"])
+    return ref
+
+
+def test_cfg1_fp32_4096x4096_every_byte_against_oracle(gpu):
+    import torch
+    ck = _ck()
+    n = 4096 * 4096
+    print("[case] cfg1 fp32 4096x4096 N(0,1e-3) seed 0, 64 KiB units", flush=True)
+    x = torch.randn(n, device=gpu, generator=_gen(gpu, 0)) * 1e-3
+    t8 = x.view(torch.uint8)
+    enc = ck.compress(t8, ck.F32, UNIT64K, n_elems=n)
+    torch.cuda.synchronize()
+    ref = _full_oracle(enc, t8.cpu().numpy(), n, ck.F32, UNIT64K)
+    assert ref["table_sum"] == 4096
+    _check_decode(enc, t8)
+
+
+# cfg2: one Llama-3-8B decoder layer in group order (name, rows, cols, kind)
+CFG2 = [("q_proj", 4096, 4096, "n"), ("k_proj", 1024, 4096, "n"), ("v_proj", 1024, 4096, "n"),
+        ("o_proj", 4096, 4096, "n"), ("gate_proj", 14336, 4096, "n"), ("up_proj", 14336, 4096, "n"),
+        ("down_proj", 4096, 14336, "n"), ("input_layernorm", 1, 4096, "ones"),
+        ("post_attention_layernorm", 1, 4096, "ones")]
+
+
+def _cfg2_tensors(gpu):
+    import torch
+    g = _gen(gpu, 2)
+    out = []
+    for name, r, c, kind in CFG2:
+        if kind == "ones":
+            t = torch.ones(r * c, dtype=torch.bfloat16, device=gpu)
+        else:
+            t = (torch.randn(r * c, device=gpu, generator=g) * 0.02).to(torch.bfloat16)
+        out.append((name, t))
+    return out
+
+
+def test_cfg2_llama3_8b_layer_codec_against_oracle(gpu):
+    import torch
+    ck = _ck()
+    print("[case] cfg2 nine bf16 tensors through compress_many", flush=True)
+    ts = _cfg2_tensors(gpu)
+    encs = [ck.Encoder(t.numel(), ck.BF16, UNIT64K, device=gpu) for _, t in ts]
+    res = ck.compress_many(encs, [t.view(torch.uint8) for _, t in ts])
+    torch.cuda.synchronize()
+    for (name, t), e in zip(ts, res):
+        print(f"[case] cfg2 {name} against the oracle", flush=True)
+        ref = _full_oracle(e, t.view(torch.uint8).cpu().numpy(), t.numel(), ck.BF16, UNIT64K)
+        assert ref["table_sum"] == 4096
+        _check_decode(e, t.view(torch.uint8))
+
+
+def test_cfg2_llama3_8b_layer_analyzer_against_oracle(gpu):
+    """Per-tensor statistics: histogram and min/max bit-exact, moments within the
+    stated tolerance of the fp64 values (mean 1e-6 * range, variance rtol 1e-4,
+    skewness and kurtosis 1e-4 * max(1, |m|))."""
+    import torch
+    ck = _ck()
+    print("[case] cfg2 analyzer, nine bf16 tensors in one call", flush=True)
+    ts = _cfg2_tensors(gpu)
+    st = ck.analyze([t for _, t in ts], [ck.BF16] * len(ts), bins=256)
+    for (name, t), s in zip(ts, st):
+        ref = oc.tensor_stats(t.view(torch.uint8).cpu().numpy(), t.numel(), ck.BF16, 256)
+        assert np.array_equal(s["histogram"], ref["histogram"]), name
+        assert np.array_equal(s["minmax"], ref["minmax"]), name
+        m64 = ref["moments64"]
+        rng = float(ref["minmax"][1]) - float(ref["minmax"][0])
+        assert abs(s["moments"][0] - m64[0]) <= 1e-6 * max(rng, 1e-30) + 1e-12, name
+        assert abs(s["moments"][1] - m64[1]) <= 1e-4 * abs(m64[1]) + 1e-30, name
+        for k in (2, 3):
+            assert abs(s["moments"][k] - m64[k]) <= 1e-4 * max(1.0, abs(m64[k])), (name, k)
+
+
+def _masked_words(t, k):
+    import torch
+    w = t.view(torch.int16).to(torch.int64) & 0xFFFF
+    return w & ~((1 << k) - 1)
+
+
+def _expand(seq, rules):
+    """The grammar undone: every rule symbol replaced by its pair, last rule first."""
+    import torch
+    def s64(v):  # a reference symbol (u64) as the signed 64-bit value torch holds
+        return v - (1 << 64) if v >= (1 << 63) else v
+
+    for rep, lhs, rhs, _ in reversed(rules):
+        m = seq == s64(rep)
+        cnt = int(m.sum())
+        if not cnt:
+            continue
+        out = torch.repeat_interleave(seq, (1 + m.to(torch.int64)))
+        pos = torch.nonzero(m).reshape(-1) + torch.arange(cnt, device=seq.device)
+        out[pos] = s64(lhs)
+        out[pos + 1] = s64(rhs)
+        seq = out
+    return seq
+
+
+@pytest.mark.parametrize("name", [c[0] for c in CFG2])
+def test_cfg2_llama3_8b_layer_prefix_mask_repair(gpu, name):
+    """build_shared_grammar on each tensor of the layer (group = the tensor,
+    all 7 bf16 mantissa bits masked, 50 rules).  k_proj / v_proj and the two
+    norms: rules, token count and largest pair count equal the oracle's.  The
+    others (16.8M and 58.7M words, beyond what the oracle finishes in seconds):
+    the grammar expands back to the masked words exactly, applying the rules
+    gives the same token count, and the chosen pair counts never increase."""
+    import torch
+    ck = _ck()
+    ts = dict(_cfg2_tensors(gpu))
+    t = ts[name]
+    n = t.numel()
+    k = ck.repair_masked_bits(ck.BF16)
+    print(f"[case] cfg2 repair {name} n={n}", flush=True)
+    rp = ck.Repairer(n, ck.BF16, max_rules=50, device=gpu)
+    r = rp.build(t.view(torch.uint8), want_seq=True)
+    if n <= 1024 * 4096:
+        ref = oc.repair_build(t.view(torch.uint8).cpu().numpy(), n, 2, k, 50)
+        assert r["rules"] == ref["rules"]
+        assert r["out_len"] == ref["out_len"] and r["max_pair"] == ref["max_pair"]
+    else:
+        freqs = [f for _, _, _, f in r["rules"]]
+        assert all(a >= b for a, b in zip(freqs, freqs[1:])) and all(f >= 2 for f in freqs)
+        assert rp.apply(t.view(torch.uint8), r["rules"]) == r["out_len"]
+        seq = torch.from_numpy(r["seq"].view(np.int64)).to(gpu)
+        assert torch.equal(_expand(seq, r["rules"]), _masked_words(t, k))
+
+
+def _check_at_size(enc, t8, n, dt, unit, samples):
+    _check_table(enc, t8, n, dt)
+    _check_offsets(enc)
+    if oc.SPE[dt]:
+        import torch
+        es, spe = oc.ES[dt], oc.SPE[dt]
+        assert torch.equal(enc.sidecar[: n * spe].view(n, spe), t8.view(n, es)[:, :spe])
+    _check_sampled_units(enc, t8, dt, unit, samples)
+    _check_decode(enc, t8)
+
+
+def test_cfg3_rank_shard_all_four_tensors(gpu):
+    """The four tensors of the Llama-3-8B rank-0-of-8 shard (1,003,782,656
+    elements each, 14.05 GB) through one compress_many call."""
+    import torch
+    ck = _ck()
+    n = 1_003_782_656
+    g = _gen(gpu, 3)
+    print("[case] cfg3 four tensors at full size", flush=True)
+    params = (torch.randn(n, device=gpu, generator=g) * 0.02).to(torch.bfloat16)
+    master = params.float()
+    exp_avg = torch.randn(n, device=gpu, generator=g) * 1e-3
+    exp_avg_sq = (torch.randn(n, device=gpu, generator=g) * 1e-3) ** 2 + 1e-12
+    tensors = [("params_bf16", ck.BF16, params), ("master", ck.F32, master), ("exp_avg", ck.F32, exp_avg),
+               ("exp_avg_sq", ck.F32, exp_avg_sq)]
+    encs = [ck.Encoder(n, dt, UNIT64K, device=gpu) for _, dt, _ in tensors]
+    res = ck.compress_many(encs, [t.view(torch.uint8) for _, _, t in tensors])
+    torch.cuda.synchronize()
+    for (name, dt, t), e in zip(tensors, res):
+        print(f"[case] cfg3 {name}", flush=True)
+        nu = e.n_units
+        _check_at_size(e, t.view(torch.uint8), n, dt, UNIT64K, [0, 1, nu // 2, nu - 2, nu - 1])
+
+
+def _adversarial_gpu(n, seed, gpu, block=(100_000_000, 100_000_000 + 16_777_216)):
+    """cfg4's distribution on the GPU: lognormal over ~30 binades, 0.1% exact
+    zeros, 0.01% denormals, 0.001% +-inf/NaN, one block of uniform random bits."""
+    import torch
+    g = _gen(gpu, seed)
+    x = torch.exp(torch.randn(n, device=gpu, generator=g) * 5.0 - 12.0)
+    idx = torch.randint(0, n, (n // 1000,), device=gpu, generator=g)
+    x[idx] = 0.0
+    idx = torch.randint(0, n, (n // 10000,), device=gpu, generator=g)
+    x[idx] = torch.rand(idx.numel(), device=gpu, generator=g) * 1e-39
+    idx = torch.randint(0, n, (n // 100000,), device=gpu, generator=g)
+    special = torch.tensor([float("inf"), float("-inf"), float("nan")], device=gpu)
+    x[idx] = special[torch.randint(0, 3, (idx.numel(),), device=gpu, generator=g)]
+    a, b = block
+    bits = torch.randint(-(1 << 31), 1 << 31, (b - a,), dtype=torch.int64, device=gpu, generator=g).to(torch.int32)
+    x[a:b] = bits.view(torch.float32)
+    return x
+
+
+def test_cfg4_adversarial_256m_every_byte_against_oracle(gpu):
+    import torch
+    ck = _ck()
+    n = 268_435_456
+    print("[case] cfg4 adversarial fp32 268M with a 16M random block", flush=True)
+    x = _adversarial_gpu(n, 4, gpu)
+    t8 = x.view(torch.uint8)
+    assert int(torch.isinf(x).sum()) > 0 and int(torch.isnan(x).sum()) > 0 and int((x == 0).sum()) > 0
+    enc = ck.compress(t8, ck.F32, UNIT64K, n_elems=n)
+    torch.cuda.synchronize()
+    print("[case] cfg4 oracle comparison", flush=True)
+    _full_oracle(enc, t8.cpu().numpy(), n, ck.F32, UNIT64K)
+    # the random block's units hold live planes of ~8 bits per symbol: they must
+    # still round-trip, and some of them are stored raw (passthrough)
+    _check_decode(enc, t8)
+
+
+def test_cfg5_70b_rank_tensor_1mib_units(gpu):
+    """One fp32 tensor of the Llama-3-70B rank-0-of-8 shard (8,819,213,312
+    elements, 35.3 GB) in 1 MiB units.  Its masked byte counts exceed 2^32: the
+    table must be the oracle's normalisation of the counts reduced mod 2^32, as
+    the reference's u32 histogram leaves them."""
+    import torch
+    ck = _ck()
+    n = 8_819_213_312
+    unit = 1 << 20
+    print("[case] cfg5 one 8.8G-element fp32 tensor, 1 MiB units", flush=True)
+    x = torch.randn(n, device=gpu, generator=_gen(gpu, 5)) * 1e-3
+    t8 = x.view(torch.uint8)
+    enc = ck.compress(t8, ck.F32, unit, n_elems=n)
+    torch.cuda.synchronize()
+    print(f"[case] cfg5 encoded: {enc.total} bytes, {enc.n_units} units", flush=True)
+    tsum = _check_table(enc, t8, n, ck.F32)
+    assert tsum == 4096
+    _check_offsets(enc)
+    nu = enc.n_units
+    _check_sampled_units(enc, t8, ck.F32, unit, [0, 1, nu // 3, nu - 2, nu - 1])
+    es, spe = 4, 2
+    for i in range(0, n, 1 << 30):
+        m = min(1 << 30, n - i)
+        assert torch.equal(enc.sidecar[i * spe:(i + m) * spe].view(m, spe), t8[i * es:(i + m) * es].view(m, es)[:, :spe])
+    _check_decode(enc, t8)

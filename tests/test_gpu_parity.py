@@ -338,7 +338,7 @@ def test_decode_counts_corrupted_lanes(unit, where, gpu):
 
 
 @pytest.mark.parametrize("unit", [65536, 1 << 20])
-def test_compress_many_matches_single_calls(unit, gpu):
+def test_compress_many_matches_single_calls(unit, paths, gpu):
     """ckr_compress_many (histograms overlapped with the previous encode) gives
     each job exactly what ckr_compress gives it, and the oracle's bytes."""
     import torch
@@ -348,7 +348,7 @@ def test_compress_many_matches_single_calls(unit, gpu):
              (dg.F32, 0, lambda n: np.zeros(0, np.float32)),
              (dg.F32, 50000, lambda n: dg.exp_avg_sq(n, 72)),
              (dg.I8, 70001, lambda n: np.random.default_rng(73).integers(-4, 4, n).astype(np.int8))]
-    print(f"[case] compress_many unit={unit}", flush=True)
+    print(f"[case] compress_many unit={unit} fast={paths}", flush=True)
     raws = [gen(n) for _, n, gen in specs]
     srcs = [_to_dev(r, gpu) for r in raws]
     encs = [ck.Encoder(n, dt, unit, device=gpu) for dt, n, _ in specs]
@@ -367,6 +367,8 @@ def test_compress_many_matches_single_calls(unit, gpu):
         dst, bad = ck.decode(m)
         torch.cuda.synchronize()
         assert bad == 0 and np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
+    with pytest.raises(ck.CkrError):  # one Encoder twice would share its buffers
+        ck.compress_many([encs[0], encs[0]], [srcs[0], srcs[0]])
 
 
 def test_compress_many_large_overlapped_histogram(gpu):
@@ -427,3 +429,46 @@ def test_cfg3_size_tensors_through_compress_many(gpu):
         torch.cuda.synchronize()
         assert bad == 0 and torch.equal(dst, t.view(torch.uint8))
         del dst
+
+
+@pytest.mark.parametrize("dt,shift", [(dg.F32, 4), (dg.F32, 12), (dg.BF16, 2), (dg.BF16, 6), (dg.BF16, 8),
+                                      (dg.F16, 14), (dg.I8, 1), (dg.I8, 3)])
+@pytest.mark.parametrize("unit", [65536, 1 << 20])
+def test_element_aligned_sources_and_destinations(dt, shift, unit, paths, gpu):
+    """A tensor that starts `shift` bytes into its allocation (a slice of a flat
+    buffer at an element offset that is not a multiple of 16 bytes): histogram,
+    compress, compress_many and decode into an equally shifted destination give
+    the oracle's bytes and the original bits."""
+    import torch
+    ck = _ck()
+    n = 300_007
+    gen = {dg.F32: lambda: dg.normal_f32(n, 1e-3, 90), dg.BF16: lambda: dg.normal_bf16(n, 0.02, 91),
+           dg.F16: lambda: (np.random.default_rng(92).standard_normal(n) * 0.02).astype(np.float16),
+           dg.I8: lambda: np.random.default_rng(93).integers(-5, 5, n).astype(np.int8)}[dt]
+    raw = gen()
+    b = dg.raw_bytes(raw)
+    print(f"[case] element-aligned dt={dt} shift={shift} unit={unit} fast={paths}", flush=True)
+    buf = torch.zeros(b.size + 64, dtype=torch.uint8, device=gpu)
+    buf[shift:shift + b.size].copy_(torch.from_numpy(b.copy()))
+    src = buf[shift:shift + b.size]
+    assert src.data_ptr() % 16 == shift % 16
+    ref = oc.compress_tensor(raw, n, dt, unit)
+    h = ck.byte_histogram(src, dt, n_elems=n)
+    assert np.array_equal(h.cpu().numpy().view(np.uint32), oc.byte_hist(ref["masked"]))
+    one = ck.compress(src, dt, unit, n_elems=n)
+    many = ck.compress_many([ck.Encoder(n, dt, unit, device=gpu), ck.Encoder(n, dt, unit, device=gpu)], [src, src])
+    torch.cuda.synchronize()
+    for e in [one] + many:
+        assert np.array_equal(e.table.norm, ref["table"]["norm_freq"])
+        assert e.total == ref["data"].size and np.array_equal(e.data_np(), ref["data"])
+        nu = ref["unit_offsets"].size - 1
+        assert np.array_equal(e.headers_np()[: nu * 256], ref["headers"])
+        if oc.SPE[dt]:
+            assert np.array_equal(e.sidecar[: n * oc.SPE[dt]].cpu().numpy(), ref["sidecar"])
+    out = torch.full((b.size + 64,), 0xA5, dtype=torch.uint8, device=gpu)
+    dst, bad = ck.decode(one, dst=out[shift:shift + b.size])
+    torch.cuda.synchronize()
+    assert bad == 0 and np.array_equal(dst.cpu().numpy(), b)
+    o = out.cpu().numpy()
+    assert (o[:shift] == 0xA5).all() and (o[shift + b.size:] == 0xA5).all()  # nothing written outside
+
