@@ -472,3 +472,45 @@ def test_element_aligned_sources_and_destinations(dt, shift, unit, paths, gpu):
     o = out.cpu().numpy()
     assert (o[:shift] == 0xA5).all() and (o[shift + b.size:] == 0xA5).all()  # nothing written outside
 
+
+
+def test_invalid_device_pointers_are_errors(gpu):
+    """Host memory, freed device memory and ranges that run past their
+    allocation are rejected on the host before any launch (the reference checks
+    each pointer with hipPointerGetAttributes, src/ANSCompressor.cpp:567-585):
+    hipPointerGetAttributes reports unregistered memory for the first two, and
+    hipMemGetAddressRange bounds the third."""
+    import ctypes
+    import torch
+    ck = _ck()
+    hip = ctypes.CDLL("libamdhip64.so")
+    n = 4096
+    enc = ck.Encoder(n, ck.F32, 65536, device=gpu)
+    hist = torch.zeros(256, dtype=torch.int32, device=gpu)
+
+    def compress_from(p, nbytes_elems=n):
+        return ck.lib().ckr_compress(ctypes.c_void_p(p), nbytes_elems, ck.F32, 65536, 0, enc.out.data_ptr(),
+                                     enc.out_cap, enc.headers.data_ptr(), enc.unit_offsets.data_ptr(),
+                                     enc.sidecar.data_ptr(), enc.ws.data_ptr(), enc.ws_bytes, None, None, None)
+
+    host = np.zeros(n, np.float32)
+    assert compress_from(host.ctypes.data) == ck.CKR_E_INVALID
+    assert b"device-accessible" in ck.lib().ckr_last_error()
+    d = ctypes.c_void_p()
+    assert hip.hipMalloc(ctypes.byref(d), ctypes.c_size_t(1 << 20)) == 0
+    try:
+        # the last 4 KiB of a 1 MiB allocation, read as 16 KiB
+        assert compress_from(d.value + (1 << 20) - 4096) == ck.CKR_E_INVALID
+        assert b"past its allocation" in ck.lib().ckr_last_error()
+        assert ck.lib().ckr_byte_histogram(ctypes.c_void_p(d.value + 4096), 1 << 20, ck.I8, hist.data_ptr(),
+                                           None) == ck.CKR_E_INVALID
+    finally:
+        assert hip.hipFree(d) == 0
+    assert compress_from(d.value) == ck.CKR_E_INVALID  # freed
+    assert ck.lib().ckr_byte_histogram(d, 4096, ck.I8, hist.data_ptr(), None) == ck.CKR_E_INVALID
+    # a valid call afterwards still works (no error left behind by the queries)
+    t = torch.randn(n, device=gpu) * 1e-3
+    e = enc.compress(t.view(torch.uint8))
+    dst, bad = ck.decode(e)
+    torch.cuda.synchronize()
+    assert bad == 0 and torch.equal(dst, t.view(torch.uint8))
