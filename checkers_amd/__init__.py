@@ -27,7 +27,8 @@ EXPORTED = [  # every symbol include/checkers_amd.h declares
     "ckr_last_error", "ckr_version", "ckr_element_size", "ckr_sidecar_bytes_per_elem",
     "ckr_extract_mantissa", "ckr_byte_histogram", "ckr_byte_histogram_raw", "ckr_build_table",
     "ckr_num_units", "ckr_encode_max_output_bytes", "ckr_encode_workspace_bytes", "ckr_encode",
-    "ckr_compress", "ckr_compress_many", "ckr_decode_workspace_bytes", "ckr_decode", "ckr_analyze_workspace_bytes",
+    "ckr_compress", "ckr_compress_many", "ckr_decode_workspace_bytes", "ckr_decode", "ckr_decode_noalloc",
+    "ckr_analyze_workspace_bytes",
     "ckr_analyze", "ckr_profile_begin", "ckr_profile_end", "ckr_set_fast_paths",
     "ckr_repair_masked_bits", "ckr_repair_bucket_count", "ckr_repair_workspace_bytes",
     "ckr_repair_build", "ckr_repair_apply",
@@ -125,6 +126,7 @@ def lib():
         "ckr_compress_many": (i32, [vp, u64, u64, i32, vp]),
         "ckr_decode_workspace_bytes": (u64, [u64, i32, u64]),
         "ckr_decode": (i32, [vp, vp, vp, vp, u64, i32, u64, vp, vp, vp, u64, vp, vp]),
+        "ckr_decode_noalloc": (i32, [vp, vp, vp, vp, u64, i32, u64, vp, vp, vp, vp]),
         "ckr_analyze_workspace_bytes": (u64, [vp, u64]),
         "ckr_analyze": (i32, [vp, u64, vp, u64, vp]),
         "ckr_set_fast_paths": (i32, [i32]),
@@ -395,6 +397,18 @@ def decode(enc, dst=None, stream=None):
     d = Decoder(enc.n_elems, enc.dtype, enc.unit_bytes, device=enc.data.device)
     bad = d.decode(enc.data, enc.headers, enc.unit_offsets, enc.table, enc.sidecar, dst, stream=stream)
     return dst[:nb], bad
+
+
+def decode_noalloc(enc, dst, stream=None, check=True):
+    """ckr_decode_noalloc: decode an Encoded into dst (a 4-byte aligned device
+    tensor of its byte size) with no device allocation; returns the bad-lane
+    count (None when check is False)."""
+    bad = ctypes.c_uint64(0)
+    _check(lib().ckr_decode_noalloc(
+        enc.data.data_ptr(), enc.headers.data_ptr(), enc.unit_offsets.data_ptr(), enc.table.ptr, enc.n_elems,
+        enc.dtype, enc.unit_bytes, enc.sidecar.data_ptr() if enc.sidecar is not None else None, dst.data_ptr(),
+        ctypes.byref(bad) if check else None, _stream(stream)))
+    return bad.value if check else None
 
 
 def analyze(tensors, tags, bins=256, stream=None):

@@ -385,8 +385,11 @@ std::vector<PhaseRec> g_phase;
 }  // namespace
 
 namespace ckr {
+// Set while a no-allocation entry point runs on this thread: profiling, which
+// creates events and buffers, stays out of it.
+thread_local bool t_noalloc = false;
 void prof_mark(const char* name, hipStream_t s, bool begin) {
-    if (!g_prof_on) return;
+    if (!g_prof_on || t_noalloc) return;
     std::lock_guard<std::mutex> lk(g_prof_mu);
     hipEvent_t e;
     if (hipEventCreate(&e) != hipSuccess) return;
@@ -396,7 +399,7 @@ void prof_mark(const char* name, hipStream_t s, bool begin) {
     else (void)hipEventDestroy(e);
 }
 uint64_t* prof_phase_buffer(uint64_t n, hipStream_t s) {
-    if (!g_prof_on || n == 0) return nullptr;
+    if (!g_prof_on || t_noalloc || n == 0) return nullptr;
     std::lock_guard<std::mutex> lk(g_prof_mu);
     void* p = nullptr;
     if (hipMalloc(&p, n * 8) != hipSuccess) return nullptr;
@@ -1080,10 +1083,16 @@ uint64_t ckr_decode_workspace_bytes(uint64_t n_elems, int dtype, uint64_t unit_b
     return decode_layout(g).total;
 }
 
-int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const uint64_t* d_unit_offsets,
-               const ckr_freq_table* h_table, uint64_t n_elems, int dtype, uint64_t unit_bytes,
-               const uint8_t* d_sidecar, void* d_dst, void* d_workspace, uint64_t workspace_bytes,
-               uint64_t* h_bad_lanes, void* stream) {
+}  // extern "C"
+
+namespace {
+// ckr_decode and its no-allocation variant.  noalloc: the workspace is the
+// device's scratch array, the destination must be 4-byte aligned (no staging
+// copy), and the bad-lane count is read back through the caller's stack.
+int decode_impl(const uint8_t* d_data, const ckr_stream_header* d_headers, const uint64_t* d_unit_offsets,
+                const ckr_freq_table* h_table, uint64_t n_elems, int dtype, uint64_t unit_bytes,
+                const uint8_t* d_sidecar, void* d_dst, void* d_workspace, uint64_t workspace_bytes,
+                uint64_t* h_bad_lanes, void* stream, bool noalloc) {
     if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
     ckr::EncodeGeom g;
     if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
@@ -1125,6 +1134,7 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
     uint8_t* out = static_cast<uint8_t*>(d_dst);
     void* tmp = nullptr;
     if (!aligned_to(d_dst, 4)) {
+        if (noalloc) return fail(CKR_E_INVALID, "[ckr] the no-allocation decode needs a 4-byte aligned destination");
         if (hipMallocAsync(&tmp, g.n_bytes, s) != hipSuccess) {
             (void)hipGetLastError();
             return fail(CKR_E_HIP, "[ckr] staging buffer for an unaligned destination unavailable");
@@ -1138,7 +1148,12 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
         (void)hipFreeAsync(tmp, s);
     }
     if (de != hipSuccess) return fail(CKR_E_HIP, "[ckr] decode launch failed: %s", hipGetErrorString(de));
-    if (h_bad_lanes) {
+    if (h_bad_lanes && noalloc) {
+        unsigned long long nb = 0;
+        CKR_HIP(hipMemcpyAsync(&nb, bad, 8, hipMemcpyDeviceToHost, s));
+        CKR_HIP(hipStreamSynchronize(s));
+        *h_bad_lanes = nb;
+    } else if (h_bad_lanes) {
         uint32_t* pw = pinned_words();
         if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
         CKR_HIP(hipMemcpyAsync(pw, bad, 8, hipMemcpyDeviceToHost, s));
@@ -1148,6 +1163,64 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
         *h_bad_lanes = nb;
     }
     return CKR_OK;
+}
+
+// The scratch of ckr_decode_noalloc: a file-scope device array, one copy per
+// GPU the library runs on, held until the process ends.  Host code never
+// passes `scratch` itself (on the host it is only a stand-in symbol): its
+// device address is looked up once per device with hipGetSymbolAddress, with
+// that device current, and that address is what the kernels receive.
+constexpr uint64_t kNoAllocScratchBytes = 128 * 1024;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+int noalloc_scratch(void** out) {
+    static std::mutex mu;
+    static std::vector<void*> per_dev;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(CKR_E_HIP, "[ckr] no current device");
+    std::lock_guard<std::mutex> lk(mu);
+    if ((int)per_dev.size() <= dev) per_dev.resize(dev + 1, nullptr);
+    if (!per_dev[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return fail(CKR_E_HIP, "[ckr] scratch address lookup failed: %s", hipGetErrorString(e));
+        }
+        per_dev[dev] = p;
+    }
+    *out = per_dev[dev];
+    return CKR_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const uint64_t* d_unit_offsets,
+               const ckr_freq_table* h_table, uint64_t n_elems, int dtype, uint64_t unit_bytes,
+               const uint8_t* d_sidecar, void* d_dst, void* d_workspace, uint64_t workspace_bytes,
+               uint64_t* h_bad_lanes, void* stream) {
+    return decode_impl(d_data, d_headers, d_unit_offsets, h_table, n_elems, dtype, unit_bytes, d_sidecar, d_dst,
+                       d_workspace, workspace_bytes, h_bad_lanes, stream, false);
+}
+
+int ckr_decode_noalloc(const uint8_t* d_data, const ckr_stream_header* d_headers, const uint64_t* d_unit_offsets,
+                       const ckr_freq_table* h_table, uint64_t n_elems, int dtype, uint64_t unit_bytes,
+                       const uint8_t* d_sidecar, void* d_dst, uint64_t* h_bad_lanes, void* stream) {
+    if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
+    ckr::EncodeGeom g;
+    if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
+    const uint64_t need = decode_layout(g).total;
+    if (need > kNoAllocScratchBytes)
+        return fail(CKR_E_CAPACITY, "[ckr] decode needs %llu bytes of scratch, above the no-allocation limit of %llu",
+                    (unsigned long long)need, (unsigned long long)kNoAllocScratchBytes);
+    void* ws = nullptr;
+    if (int rc = noalloc_scratch(&ws)) return rc;
+    ckr::t_noalloc = true;
+    const int rc = decode_impl(d_data, d_headers, d_unit_offsets, h_table, n_elems, dtype, unit_bytes, d_sidecar, d_dst,
+                               ws, kNoAllocScratchBytes, h_bad_lanes, stream, true);
+    ckr::t_noalloc = false;
+    return rc;
 }
 
 // ---- analyzer: per record [p1 nblk][p2 nblk][params][hist partial nblk*256]

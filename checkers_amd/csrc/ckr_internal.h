@@ -36,6 +36,7 @@ struct EncSym {
 // Optional per-kernel timing (ckr_profile_begin / ckr_profile_end): when on,
 // every launch below is bracketed by HIP events recorded on its own stream.
 void prof_mark(const char* name, hipStream_t s, bool begin);
+extern thread_local bool t_noalloc;
 // With profiling on, a device buffer of n u64 for per-unit phase stamps (else
 // null); ckr_profile_end reduces the stamps of the last launch that used it.
 uint64_t* prof_phase_buffer(uint64_t n, hipStream_t s);

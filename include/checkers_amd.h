@@ -206,6 +206,23 @@ CKR_API int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers
                        void* d_workspace, uint64_t workspace_bytes,
                        uint64_t* h_bad_lanes, void* stream);
 
+/* ---- decode that allocates nothing; no counterpart in the reference.  For
+ * callers that cannot allocate device memory: code under HIP graph capture,
+ * serving loops that restore shards on the fly, harnesses that forbid
+ * hipMalloc.  Same arguments and results as ckr_decode without the workspace:
+ * the decoder's tables, canonical streams and bad-lane counter live in a
+ * 128 KiB device array owned by the library, one per GPU, held until the
+ * process ends (enough for every unit size up to 1 MiB and for the single-unit
+ * layout; a larger need is CKR_E_CAPACITY).  The destination must be 4-byte
+ * aligned (no staging copy is made).  Every call on a GPU uses that GPU's one
+ * array, cleared by the call itself: calls that overlap on one GPU race, so
+ * serialise them. ---- */
+CKR_API int ckr_decode_noalloc(const uint8_t* d_data, const ckr_stream_header* d_headers,
+                               const uint64_t* d_unit_offsets,
+                               const ckr_freq_table* h_table, uint64_t n_elems, int dtype,
+                               uint64_t unit_bytes, const uint8_t* d_sidecar, void* d_dst,
+                               uint64_t* h_bad_lanes, void* stream);
+
 /* ---- TensorAnalyzer statistics pass over n records ---- */
 CKR_API uint64_t ckr_analyze_workspace_bytes(const ckr_stats_record* h_records, uint64_t n);
 CKR_API int ckr_analyze(const ckr_stats_record* h_records, uint64_t n,
