@@ -179,7 +179,7 @@ __global__ void __launch_bounds__(256) hist_init_kernel(uint32_t* __restrict__ h
 
 // PC: copies per live plane (masked dtypes).  16 (32 KiB of LDS) when the
 // kernel has the device to itself; 4 (8 KiB) when it runs beside the fast
-// encoder, whose workgroup leaves about 14 KiB of a CU's LDS free.
+// encoder, whose workgroup leaves about 10 KiB of a CU's LDS free.
 //
 // src is 16-byte aligned; the head_n (< 16) bytes before it, at src - head_n,
 // are the tensor's first bytes when the tensor itself is only element-aligned
@@ -968,27 +968,30 @@ __device__ __forceinline__ void enc_full_rows(EncLane& c0, EncLane& c1, const ui
 // LDS layout (bytes): table 256 x 16 (see enc_quad) | canonical headers 12 x
 // u32 | canonical bytes 3 x canon_bytes | pair control blocks | 2 x WS regions
 // | 32 bytes of read padding.  A region holds one set: the packers' lane
-// tables (lane offsets in the unit, u16, and LDS stream starts, u32), then the
-// rank-0 slots (64 x stride0) and the rank-1 slots (64 x stride1).  The lane
-// tables are only written once both coders are done with the set, so they
+// records (per lane {LDS address of unit byte 0 as if it were in the lane, end
+// of the lane in the unit}, 8 bytes) and block map (u8 lane per 64 bytes of
+// packed output), then the rank-0 slots (64 x stride0) and the rank-1 slots
+// (64 x stride1).  The records and the map are only written once both coders
+// are done with the set, so they
 // double as the guard under the slots: a lane's dwords are flushed downward
 // from the end of its slot, and a lane that outgrows its slot keeps flushing
 // into the slots below it (lanes of the same unit, whose bytes are then redone
 // by the general kernels) and, for the lowest slot, into the lane tables (at
 // most 2 bytes per symbol, 256 symbols: 516 bytes), never out of its region.
 static constexpr uint32_t FE_TABSZ = 4096, FE_CHDR = FE_TABSZ, FE_CBYTES = FE_TABSZ + 48;
-static constexpr uint32_t R_LOFF = 0, R_SA = 520, R_SLOTS = 1544;
-static_assert(R_SLOTS >= 516 && R_SLOTS % 4 == 0 && R_SA >= 257 * 2, "region: lane tables and guard under the slots");
+static constexpr uint32_t R_REC = 0, R_MAP = 2048, R_SLOTS = 3076;
+static_assert(R_SLOTS >= 516 && R_SLOTS % 4 == 0 && R_MAP >= R_REC + 256 * 8 && R_SLOTS >= R_MAP + 1025,
+              "region: lane records, block map and guard under the slots");
 
 struct WsPairCtl {
     uint32_t unit[2];         // unit in set s (>= n_units: none left, the pair stops)
     uint32_t coded[2];        // +1 by each coder wave per use of set s
     uint32_t freed[2];        // +1 by the packers per use of set s
     uint32_t tick;            // uses started by the plane-FL coder (unit published)
-    uint32_t pbar;            // barrier count of the two packer waves
+    uint32_t pbar;            // barrier count of the packer waves
     uint32_t off[2][2];       // packed offset of the unit in set s (lo, hi)
-    uint32_t pad[4];
-    uint32_t xch[2][4][64];   // per set and column: count FL, state FL, count 3, state 3
+    uint32_t xread;           // units whose exchange words the look-back packer has read
+    uint32_t pad[3];
 };
 static_assert(sizeof(WsPairCtl) % 16 == 0, "control block alignment");
 
@@ -1017,8 +1020,8 @@ __host__ __device__ constexpr uint32_t ws_lds_bytes(uint32_t pairs, uint32_t can
            2 * pairs * ws_region_bytes(stride0, stride1) + 32;
 }
 
-template <int SPE, bool ESC, bool SIDE, int PAIRS>
-__global__ void __launch_bounds__(256 * PAIRS) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
+template <int SPE, bool ESC, bool SIDE, int PAIRS, int NPK>
+__global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
                                                                   const EncSym* __restrict__ d_enc,
                                                                   const uint32_t* __restrict__ canon, FastEncParams fp,
                                                                   ckr_stream_header* __restrict__ hdrs,
@@ -1029,7 +1032,7 @@ __global__ void __launch_bounds__(256 * PAIRS) encode_fast_kernel(const uint8_t*
                                                                   uint64_t* __restrict__ phase) {
     extern __shared__ uint32_t lds[];
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
-    constexpr uint32_t NT = 256 * PAIRS;
+    constexpr uint32_t NT = 64 * (2 + NPK) * PAIRS;
     const uint4* tab = reinterpret_cast<const uint4*>(lds8 + 0);
     uint32_t* chdr = reinterpret_cast<uint32_t*>(lds8 + FE_CHDR);
     const uint32_t cb_off = FE_CBYTES;
@@ -1061,11 +1064,12 @@ __global__ void __launch_bounds__(256 * PAIRS) encode_fast_kernel(const uint8_t*
     __syncthreads();
 
     const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // waves 0 .. 2 PAIRS - 1 code, the others pack (wave w runs on SIMD w mod 4,
-    // so every SIMD holds one coder and one packer)
+    // waves 0 .. 2 PAIRS - 1 code, the others pack, NPK per pair (wave w runs on
+    // SIMD w mod 4, so the coders are on four different SIMDs)
     const bool coder = wv < 2 * PAIRS;
-    const uint32_t pr = coder ? (wv >> 1) : ((wv - 2 * PAIRS) >> 1);  // pair
-    const uint32_t rl = wv & 1;  // coder: 0 byte FL, 1 byte 3; packer: 0 look-back, 1 headers
+    const uint32_t pr = coder ? (wv >> 1) : (wv - 2 * PAIRS) / NPK;  // pair
+    const uint32_t rl = wv & 1;  // coder: 0 byte FL, 1 byte 3
+    const uint32_t pw = coder ? 0u : (wv - 2 * PAIRS) % NPK;  // packer: 0 look-back, 1 headers, all pack
     WsPairCtl& pc = *reinterpret_cast<WsPairCtl*>(lds8 + ctl_off + pr * (uint32_t)sizeof(WsPairCtl));
     const uint32_t col = 4 * j;
 
@@ -1116,8 +1120,12 @@ __global__ void __launch_bounds__(256 * PAIRS) encode_fast_kernel(const uint8_t*
                 }
             }
             const uint32_t e = enc_finish(c, lds8, endw);
-            pc.xch[s][2 * rl][j] = e;
-            pc.xch[s][2 * rl + 1][j] = c.x;
+            // per column: count FL, state FL, count 3, state 3, in the set's lane-record
+            // area (the records are written only after both packers have read them;
+            // it lies below the guard that an outgrown lowest slot may write into)
+            uint32_t* xch = reinterpret_cast<uint32_t*>(lds8 + rb + R_REC);
+            xch[2 * rl * 64 + j] = e;
+            xch[(2 * rl + 1) * 64 + j] = c.x;
             ws_signal(&pc.coded[s], 1u, j);
             if (phase && rl == 0 && j == 0) {
                 uint64_t* ph = phase + 8 * (uint64_t)u;
@@ -1130,7 +1138,7 @@ __global__ void __launch_bounds__(256 * PAIRS) encode_fast_kernel(const uint8_t*
     // packer waves
     uint32_t bar = 0;
     auto pbar_sync = [&]() {
-        bar += 2;
+        bar += NPK;
         ws_signal(&pc.pbar, 1u, j);
         ws_wait_ge(&pc.pbar, bar);
     };
@@ -1144,12 +1152,15 @@ __global__ void __launch_bounds__(256 * PAIRS) encode_fast_kernel(const uint8_t*
         const uint32_t len = (uint32_t)((g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit);
         const uint8_t* usrc = src + ubase;
         const uint32_t rb = reg0 + (2 * pr + s) * rbytes;
-        uint16_t* loff = reinterpret_cast<uint16_t*>(lds8 + rb + R_LOFF);  // lane offsets in the unit (257)
-        uint32_t* lsa = reinterpret_cast<uint32_t*>(lds8 + rb + R_SA);     // LDS stream starts (256)
+        uint2* lrec = reinterpret_cast<uint2*>(lds8 + rb + R_REC);  // per lane {LDS address of unit byte 0, lane end}
+        static_assert(R_REC + 1024 <= R_SLOTS - 516, "exchange words below the guard of the lowest slot");
+        uint8_t* bmap_w = lds8 + rb + R_MAP;                           // 64-byte block → lane (1025)
         const uint32_t end0 = rb + R_SLOTS + j * fp.stride0 + fp.sl0;
         const uint32_t end1 = rb + R_SLOTS + 64 * fp.stride0 + j * fp.stride1 + fp.sl1;
-        const uint32_t e0 = pc.xch[s][0][j], x0 = pc.xch[s][1][j];
-        const uint32_t e1 = pc.xch[s][2][j], x1 = pc.xch[s][3][j];
+        const uint32_t* xch = reinterpret_cast<const uint32_t*>(lds8 + rb + R_REC);
+        const uint32_t e0 = xch[j], x0 = xch[64 + j];
+        const uint32_t e1 = xch[128 + j], x1 = xch[192 + j];
+        if (pw == 0) ws_signal(&pc.xread, 1u, j);  // the records may now overwrite them
         // byte counts, final states and LDS stream starts of the four lanes of column j
         uint32_t cnt[4], fs[4], sa[4];
 #pragma unroll
@@ -1181,7 +1192,7 @@ __global__ void __launch_bounds__(256 * PAIRS) encode_fast_kernel(const uint8_t*
         const bool any_over = __ballot(over) != 0;
 
         uint64_t t_off = 0;
-        if (rl == 1) {
+        if (pw == 1) {
             // headers (4 per thread, 64 contiguous bytes) and the lane tables for packing
             ckr_stream_header* uh = hdrs + (uint64_t)u * 256 + 4 * j;
             uint32_t run = excl;
@@ -1195,12 +1206,21 @@ __global__ void __launch_bounds__(256 * PAIRS) encode_fast_kernel(const uint8_t*
                 }
                 h.pad = 0;
                 uh[b] = h;
-                loff[4 * j + b] = (uint16_t)run;
-                lsa[4 * j + b] = sa[b];
                 run += cnt[b];
             }
-            if (j == 63) loff[256] = (uint16_t)total;
-        } else {
+            // lane records and the block map (the lane holding the first byte of each
+            // 64-byte block of the packed unit), the records written over the exchange
+            // words once both packers hold them
+            ws_wait_ge(&pc.xread, i + 1);
+            run = excl;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                lrec[4 * j + b] = make_uint2(sa[b] - run, run + cnt[b]);
+                if (!raw)
+                    for (uint32_t blk = (run + 63u) >> 6; (blk << 6) < run + cnt[b]; blk++) bmap_w[blk] = (uint8_t)(4 * j + b);
+                run += cnt[b];
+            }
+        } else if (pw == 0) {
             const uint64_t off = lookback_wave(status, g.n_units, u, size, &ctl[2], j);
             if (j == 0) {
                 unit_off[u] = off;
@@ -1215,95 +1235,92 @@ __global__ void __launch_bounds__(256 * PAIRS) encode_fast_kernel(const uint8_t*
         const uint64_t off = (uint64_t)pc.off[s][0] | ((uint64_t)pc.off[s][1] << 32);
         uint8_t* dst = out + off;
         if (raw) {  // masked bytes of the unit, byte stores (rare)
-            for (uint32_t q = 64 * rl + j; q < len; q += 128) {
+            for (uint32_t q = 64 * pw + j; q < len; q += 64 * NPK) {
                 const uint8_t v = usrc[q];
                 dst[q] = byte_live(q, g.es, g.spe) ? v : 0;
             }
         } else if (any_over) {  // bytes come from the general kernels
-            if (rl == 0 && j == 0) redo_list[atomicAdd(&ctl[1], 1u)] = u;
+            if (pw == 0 && j == 0) redo_list[atomicAdd(&ctl[1], 1u)] = u;
         } else {
-            // Packed bytes in 16-byte destination chunks (aligned in global memory).
-            // The four lanes of column j are one contiguous run of the output; packer
-            // 0 takes its first half [r0, mid), packer 1 the rest.  A thread writes
-            // every chunk whose first unit byte lies in its range (chunk 0, which may
-            // start before the unit, belongs to the range holding byte 0).  It walks
-            // the column's lanes (bounds and LDS starts in registers): the chunks that
-            // lie inside a lane are unaligned 16-byte LDS reads, four issued at a time;
-            // the chunk that starts in a lane and runs past its end takes its remaining
-            // bytes from the following non-empty lanes (lane tables in LDS).  Bytes
-            // outside the unit (its first and last chunks are shared with the
-            // neighbouring units) are not stored.
+            // Packed bytes in 16-byte destination chunks aligned in global memory,
+            // 64 consecutive chunks (1 KiB of output, whole cache lines) per wave
+            // store: the two packer waves take alternate rounds of 64 chunks.  Chunk
+            // c starts at unit byte q = qbase + 16c (chunk 0 may start up to 15
+            // bytes before the unit).  Its first lane: the block map gives the lane
+            // holding the first byte of the chunk's 64-byte block, and the lanes
+            // after it are stepped over while they end at or before the chunk's
+            // first byte; the bytes past that lane's end come from the following
+            // non-empty lanes.  Bytes outside the unit (its first and last chunks
+            // are shared with the neighbouring units) are not stored.
             const uint64_t ab = reinterpret_cast<uintptr_t>(dst);
             const int32_t qbase = (int32_t)((ab & ~15ull) - ab);  // unit-relative byte of chunk 0 (-15..0)
             const int32_t isize = (int32_t)size;
-            const int32_t c0 = (int32_t)excl, c4 = (int32_t)(excl + tsum);
-            const int32_t mid = (c0 + c4) >> 1;
-            const int32_t r0 = rl ? mid : c0, r1 = rl ? c4 : mid;
-            // a chunk starting at q whose bytes from pos on come from the lanes after L
-            auto gather_tail = [&](uint4 v, int32_t q, int32_t pos, int32_t Ln) {
-                const int32_t qe = min(q + 16, isize);
-                while (pos < qe && Ln < 255) {
-                    Ln++;
-                    const int32_t lo2 = (int32_t)loff[Ln], hi2 = (int32_t)loff[Ln + 1];
-                    if (hi2 > lo2) {
-                        v = merge16_from(v, lds_read16(lds8, (uint32_t)((int32_t)lsa[Ln] - lo2 + q)), (uint32_t)(pos - q));
-                        pos = hi2;
-                    }
-                }
-                return v;
-            };
-            // derived from dst (not from an integer address) so that the stores stay
-            // global: a flat store would also count against the next LDS wait
-            auto put = [&](int32_t q, uint4 v) {
-                uint8_t* wp = dst + q;
-                nchunks++;
-                if (q >= 0 && q + 16 <= isize) {
-                    *reinterpret_cast<uint4*>(wp) = v;
-                } else {
-                    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+            const uint32_t nch = isize > 0 ? (uint32_t)((isize - qbase + 15) >> 4) : 0u;
+            const uint8_t* bmap = lds8 + rb + R_MAP;
+            // Four chunks per thread at a time (this wave's next four rounds), each
+            // step done for all four before the next, so that their LDS reads are
+            // independent and in flight together.
+            constexpr int NK = 4;
+            for (uint32_t cr = 64 * pw; cr < nch; cr += 64 * NPK * NK) {
+                int32_t q[NK], pk[NK], Ln[NK];
+                uint2 r[NK];
+                bool act[NK];
+                uint4 v[NK];
 #pragma unroll
-                    for (int bb = 0; bb < 16; bb++)
-                        if (q + bb >= 0 && q + bb < isize) wp[bb] = (uint8_t)(vv[bb >> 2] >> (8 * (bb & 3)));
+                for (int k = 0; k < NK; k++) {
+                    const uint32_t c = cr + 64 * NPK * k + j;
+                    act[k] = c < nch;
+                    q[k] = qbase + 16 * (int32_t)c;
+                    pk[k] = act[k] ? max(q[k], 0) : 0;
+                    Ln[k] = bmap[pk[k] >> 6];
                 }
-            };
-            if (r1 > r0) {
-                // first owned chunk: the one containing byte r0 unless it starts before r0
-                int32_t q = qbase + 16 * ((r0 - qbase) >> 4);
-                if (q < r0 && r0 > 0) q += 16;
-                if (q < 0) {  // chunk 0 starts before the unit: its bytes from 0 on
-                    put(q, gather_tail(make_uint4(0, 0, 0, 0), q, 0, (int32_t)(4 * j) - 1));
-                    q += 16;
-                }
-                int32_t lo = c0;
 #pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    const int32_t hi = lo + (int32_t)cnt[b];
-                    const int32_t dl = (int32_t)sa[b] - lo;
-                    // chunks that lie inside lane b, four at a time
-                    while (q + 64 <= hi && q + 48 < r1) {
-                        const uint4 v0 = lds_read16(lds8, (uint32_t)(dl + q));
-                        const uint4 v1 = lds_read16(lds8, (uint32_t)(dl + q + 16));
-                        const uint4 v2 = lds_read16(lds8, (uint32_t)(dl + q + 32));
-                        const uint4 v3 = lds_read16(lds8, (uint32_t)(dl + q + 48));
-                        put(q, v0); put(q + 16, v1); put(q + 32, v2); put(q + 48, v3);
-                        q += 64;
+                for (int k = 0; k < NK; k++) r[k] = lrec[Ln[k]];
+                // lanes that end at or before the chunk's first byte (short lanes in
+                // the chunk's 64-byte block before it)
+#pragma unroll
+                for (int k = 0; k < NK; k++)
+                    while ((int32_t)r[k].y <= pk[k]) r[k] = lrec[++Ln[k]];
+#pragma unroll
+                for (int k = 0; k < NK; k++) v[k] = lds_read16(lds8, (uint32_t)((int32_t)r[k].x + q[k]));
+                // bytes past the lane's end from the following non-empty lanes, one lane
+                // per step for every chunk that still needs bytes
+                for (;;) {
+                    bool more = false;
+#pragma unroll
+                    for (int k = 0; k < NK; k++) {
+                        if (act[k] && (int32_t)r[k].y < min(q[k] + 16, isize) && Ln[k] < 255) {
+                            const int32_t from = (int32_t)r[k].y;  // the next lane starts where this one ends
+                            r[k] = lrec[++Ln[k]];
+                            if ((int32_t)r[k].y > from)
+                                v[k] = merge16_from(v[k], lds_read16(lds8, (uint32_t)((int32_t)r[k].x + q[k])),
+                                                    (uint32_t)(from - q[k]));
+                            more = true;
+                        }
                     }
-                    while (q + 16 <= hi && q < r1) {
-                        put(q, lds_read16(lds8, (uint32_t)(dl + q)));
-                        q += 16;
+                    if (__ballot(more) == 0) break;
+                }
+#pragma unroll
+                for (int k = 0; k < NK; k++) {
+                    if (!act[k]) continue;
+                    // derived from dst (not from an integer address) so that the stores
+                    // stay global: a flat store would also count against the next LDS wait
+                    uint8_t* wp = dst + q[k];
+                    nchunks++;
+                    if (q[k] >= 0 && q[k] + 16 <= isize) {
+                        *reinterpret_cast<uint4*>(wp) = v[k];
+                    } else {
+                        const uint32_t vv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+                        for (int bb = 0; bb < 16; bb++)
+                            if (q[k] + bb >= 0 && q[k] + bb < isize) wp[bb] = (uint8_t)(vv[bb >> 2] >> (8 * (bb & 3)));
                     }
-                    // the chunk that starts in lane b and runs past its end
-                    if (q >= lo && q < hi && q < r1) {
-                        put(q, gather_tail(lds_read16(lds8, (uint32_t)(dl + q)), q, hi, (int32_t)(4 * j) + b));
-                        q += 16;
-                    }
-                    lo = hi;
                 }
             }
         }
         const uint64_t t_packed = phase ? wall_clock64() : 0;
-        pbar_sync();  // both packers are done with the set
-        if (rl == 0) {
+        pbar_sync();  // every packer is done with the set
+        if (pw == 0) {
             ws_signal(&pc.freed[s], 1u, j);
             if (phase && j == 0) {
                 uint64_t* ph = phase + 8 * (uint64_t)u;
@@ -1374,8 +1391,10 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
                                                    ctl, redo_list, phase));
         return hipGetLastError();
     };
-#define CKR_FAST_ENC(SPE_, ESC_, SIDE_)                                                                          \
-    (pairs == 2 ? run(encode_fast_kernel<SPE_, ESC_, SIDE_, 2>, 512u) : run(encode_fast_kernel<SPE_, ESC_, SIDE_, 1>, 256u))
+#define CKR_FAST_ENC_P(SPE_, ESC_, SIDE_, NPK_)                                                                  \
+    (pairs == 2 ? run(encode_fast_kernel<SPE_, ESC_, SIDE_, 2, NPK_>, 128u * (2 + NPK_))                           \
+                : run(encode_fast_kernel<SPE_, ESC_, SIDE_, 1, NPK_>, 64u * (2 + NPK_)))
+#define CKR_FAST_ENC(SPE_, ESC_, SIDE_) CKR_FAST_ENC_P(SPE_, ESC_, SIDE_, 2)
     const bool side = sidecar != nullptr;
     if (g.spe == 2) {
         if (hp.escapes) e = side ? CKR_FAST_ENC(2, true, true) : CKR_FAST_ENC(2, true, false);
@@ -1385,6 +1404,7 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
         else e = side ? CKR_FAST_ENC(1, false, true) : CKR_FAST_ENC(1, false, false);
     }
 #undef CKR_FAST_ENC
+#undef CKR_FAST_ENC_P
     return e;
 }
 
