@@ -1259,11 +1259,16 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) encode_fast_kernel(con
             const uint8_t* bmap = lds8 + rb + R_MAP;
             // Four chunks per thread at a time (this wave's next four rounds), each
             // step done for all four before the next, so that their LDS reads are
-            // independent and in flight together.
+            // independent and in flight together.  A lane's record is read with the
+            // next lane's, and the next lane's window is read with the lane's own
+            // when the chunk runs past the lane's end, so that a chunk crossing one
+            // lane boundary (the common case) takes no extra step.
             constexpr int NK = 4;
+            const uint32_t c_last = nch - 1;
+            const bool first_partial = qbase < 0, last_partial = nch && qbase + 16 * (int32_t)nch > isize;
             for (uint32_t cr = 64 * pw; cr < nch; cr += 64 * NPK * NK) {
-                int32_t q[NK], pk[NK], Ln[NK];
-                uint2 r[NK];
+                int32_t q[NK], pk[NK], qe[NK], Ln[NK];
+                uint2 r0[NK], r1[NK];
                 bool act[NK];
                 uint4 v[NK];
 #pragma unroll
@@ -1272,28 +1277,49 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) encode_fast_kernel(con
                     act[k] = c < nch;
                     q[k] = qbase + 16 * (int32_t)c;
                     pk[k] = act[k] ? max(q[k], 0) : 0;
+                    qe[k] = act[k] ? min(q[k] + 16, isize) : 0;
                     Ln[k] = bmap[pk[k] >> 6];
                 }
 #pragma unroll
-                for (int k = 0; k < NK; k++) r[k] = lrec[Ln[k]];
-                // lanes that end at or before the chunk's first byte (short lanes in
-                // the chunk's 64-byte block before it)
+                for (int k = 0; k < NK; k++) {
+                    r0[k] = lrec[Ln[k]];
+                    r1[k] = lrec[min(Ln[k] + 1, 255)];
+                }
+                // lanes that end at or before the chunk's first byte (short lanes in the
+                // chunk's 64-byte block before it)
 #pragma unroll
                 for (int k = 0; k < NK; k++)
-                    while ((int32_t)r[k].y <= pk[k]) r[k] = lrec[++Ln[k]];
+                    while ((int32_t)r0[k].y <= pk[k]) {
+                        Ln[k]++;
+                        r0[k] = r1[k];
+                        r1[k] = lrec[min(Ln[k] + 1, 255)];
+                    }
+                bool cross[NK];
+                uint4 w[NK];
 #pragma unroll
-                for (int k = 0; k < NK; k++) v[k] = lds_read16(lds8, (uint32_t)((int32_t)r[k].x + q[k]));
-                // bytes past the lane's end from the following non-empty lanes, one lane
-                // per step for every chunk that still needs bytes
+                for (int k = 0; k < NK; k++) {
+                    v[k] = lds_read16(lds8, (uint32_t)((int32_t)r0[k].x + q[k]));
+                    cross[k] = (int32_t)r0[k].y < qe[k] && Ln[k] < 255;
+                    if (cross[k]) w[k] = lds_read16(lds8, (uint32_t)((int32_t)r1[k].x + q[k]));
+                }
+#pragma unroll
+                for (int k = 0; k < NK; k++)
+                    if (cross[k]) {
+                        v[k] = merge16_from(v[k], w[k], (uint32_t)((int32_t)r0[k].y - q[k]));
+                        Ln[k]++;
+                    }
+                // bytes past lane Ln's end (the next lane was empty or short): the
+                // following non-empty lanes one by one
                 for (;;) {
                     bool more = false;
 #pragma unroll
                     for (int k = 0; k < NK; k++) {
-                        if (act[k] && (int32_t)r[k].y < min(q[k] + 16, isize) && Ln[k] < 255) {
-                            const int32_t from = (int32_t)r[k].y;  // the next lane starts where this one ends
-                            r[k] = lrec[++Ln[k]];
-                            if ((int32_t)r[k].y > from)
-                                v[k] = merge16_from(v[k], lds_read16(lds8, (uint32_t)((int32_t)r[k].x + q[k])),
+                        const int32_t from = (int32_t)(cross[k] ? r1[k].y : r0[k].y);  // end of lane Ln
+                        if (act[k] && from < qe[k] && Ln[k] < 255) {
+                            r1[k] = lrec[++Ln[k]];
+                            cross[k] = true;
+                            if ((int32_t)r1[k].y > from)
+                                v[k] = merge16_from(v[k], lds_read16(lds8, (uint32_t)((int32_t)r1[k].x + q[k])),
                                                     (uint32_t)(from - q[k]));
                             more = true;
                         }
@@ -1302,19 +1328,27 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) encode_fast_kernel(con
                 }
 #pragma unroll
                 for (int k = 0; k < NK; k++) {
-                    if (!act[k]) continue;
                     // derived from dst (not from an integer address) so that the stores
                     // stay global: a flat store would also count against the next LDS wait
-                    uint8_t* wp = dst + q[k];
-                    nchunks++;
-                    if (q[k] >= 0 && q[k] + 16 <= isize) {
-                        *reinterpret_cast<uint4*>(wp) = v[k];
-                    } else {
-                        const uint32_t vv[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-#pragma unroll
-                        for (int bb = 0; bb < 16; bb++)
-                            if (q[k] + bb >= 0 && q[k] + bb < isize) wp[bb] = (uint8_t)(vv[bb >> 2] >> (8 * (bb & 3)));
-                    }
+                    nchunks += act[k] ? 1u : 0u;
+                    if (act[k] && q[k] >= 0 && q[k] + 16 <= isize) *reinterpret_cast<uint4*>(dst + q[k]) = v[k];
+                    // the unit's first and last chunks are shared with the neighbouring
+                    // units: their bytes inside this unit go out as one byte store spread
+                    // over 16 lanes (lane b stores byte b), from the owner lane's registers
+                    const uint32_t c0 = cr + 64 * NPK * k;
+                    auto spread = [&](uint32_t owner) {
+                        const int32_t qq = qbase + 16 * (int32_t)(c0 + owner);
+                        const uint32_t x0 = __builtin_amdgcn_readlane(v[k].x, owner);
+                        const uint32_t x1 = __builtin_amdgcn_readlane(v[k].y, owner);
+                        const uint32_t x2 = __builtin_amdgcn_readlane(v[k].z, owner);
+                        const uint32_t x3 = __builtin_amdgcn_readlane(v[k].w, owner);
+                        const uint32_t wd = j < 4 ? x0 : (j < 8 ? x1 : (j < 12 ? x2 : x3));
+                        const int32_t b = qq + (int32_t)j;
+                        if (j < 16 && b >= 0 && b < isize) dst[b] = (uint8_t)(wd >> (8 * (j & 3)));
+                    };
+                    if (first_partial && c0 == 0) spread(0);
+                    if (last_partial && c0 <= c_last && c_last < c0 + 64 && !(first_partial && c_last == 0))
+                        spread(c_last - c0);
                 }
             }
         }
