@@ -877,14 +877,14 @@ __device__ __forceinline__ uint4 merge16_from(uint4 v, uint4 r, uint32_t s) {
 // (length a multiple of 256, so every column has the same nrows rows).  P = 0:
 // byte FL of each column (chain c0); P = 1: byte 3 (chain c0); P = 2: both
 // (c0: byte FL, c1: byte 3, interleaved).  Rows are taken from the top down.
-// The rows above the highest multiple of 32 go one at a time; then groups of
-// 32 rows, the next group's loads in flight while the current one is coded
+// The rows above the highest multiple of GR go one at a time; then groups of
+// GR rows, the next group's loads in flight while the current one is coded
 // (loads and table reads are unconditional, so the waits stay exact), and each
-// 8-row batch's table entries read while the batch before it is coded.
+// TB-row batch's table entries read while the batch before it is coded.
 // Pending bytes are flushed after every second row.  The sidecar rows are
 // written by the thread coding plane 0 and 1 alternately (row k by P == k & 1),
 // or all of them when P = 2.
-template <int SPE, bool ESC, bool SIDE, int P>
+template <int SPE, bool ESC, bool SIDE, int P, int GR, int TB, int NBUF>
 __device__ __forceinline__ void enc_full_rows(EncLane& c0, EncLane& c1, const uint8_t* ucol, uint8_t* sidecar,
                                               uint64_t ubase, uint32_t j, uint32_t nrows, const uint4* tab,
                                               uint8_t* lds8) {
@@ -897,8 +897,9 @@ __device__ __forceinline__ void enc_full_rows(EncLane& c0, EncLane& c1, const ui
         if (SIDE) *p = (uint16_t)(SPE == 2 ? (wd & 0xFFFFu) : ((wd & 0xFFu) | ((wd >> 8) & 0xFF00u)));
     };
     auto mine = [&](uint32_t k) { return P == 2 || (k & 1u) == (uint32_t)P; };  // sidecar row k written here
-    const uint32_t ng = nrows >> 5;  // full groups: rows [0, 32 ng)
-    for (int32_t k = (int32_t)nrows - 1; k >= (int32_t)(32 * ng); k--) {
+    static_assert(GR % TB == 0 && TB % 2 == 0 && GR % 2 == 0, "row groups of whole table batches");
+    const uint32_t ng = nrows / GR;  // full groups: rows [0, GR ng)
+    for (int32_t k = (int32_t)nrows - 1; k >= (int32_t)(GR * ng); k--) {
         const uint32_t wd = in32[64 * k];
         if (mine((uint32_t)k)) side(sc16 + 64 * k, wd);
         const uint32_t s0 = (wd >> SH0) & 255u;
@@ -909,29 +910,31 @@ __device__ __forceinline__ void enc_full_rows(EncLane& c0, EncLane& c1, const ui
     enc_flush(c0, lds8);
     if (P == 2) enc_flush(c1, lds8);
     if (ng == 0) return;
-    // group g: rows 32g+31 (r[0]) down to 32g (r[31])
-    auto load = [&](uint32_t (&r)[32], uint32_t g) {
-        const uint32_t* p = in32 + 64 * (32 * g + 31);
+    // group g: rows GR g + GR - 1 (r[0]) down to GR g (r[GR - 1])
+    auto load = [&](uint32_t (&r)[GR], uint32_t g) {
+        const uint32_t* p = in32 + 64 * (GR * g + GR - 1);
 #pragma unroll
-        for (int i = 0; i < 32; i++) r[i] = p[-64 * i];
+        for (int i = 0; i < GR; i++) r[i] = p[-64 * i];
     };
-    auto code = [&](const uint32_t (&r)[32], uint32_t g) {
-        uint4 t0[2][8], t1[2][8];
+    auto code = [&](const uint32_t (&r)[GR], uint32_t g) {
+        uint4 t0[2][TB], t1[2][TB];
+        (void)t1;
         auto fetch = [&](int buf, int i0) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
+            for (int i = 0; i < TB; i++) {
                 t0[buf][i] = tab[(r[i0 + i] >> SH0) & 255u];
                 if (P == 2) t1[buf][i] = tab[r[i0 + i] >> SH1];
             }
         };
-        uint16_t* scp = SIDE ? sc16 + 64 * (32 * g + 31) : nullptr;
+        uint16_t* scp = SIDE ? sc16 + 64 * (GR * g + GR - 1) : nullptr;
+        constexpr int NB = GR / TB;
         fetch(0, 0);
 #pragma unroll
-        for (int bt = 0; bt < 4; bt++) {
-            if (bt < 3) fetch((bt + 1) & 1, 8 * (bt + 1));
+        for (int bt = 0; bt < NB; bt++) {
+            if (bt < NB - 1) fetch((bt + 1) & 1, TB * (bt + 1));
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int ii = 8 * bt + i;               // row 32g+31-ii: parity (ii & 1) ^ 1
+            for (int i = 0; i < TB; i++) {
+                const int ii = TB * bt + i;              // row GR g + GR - 1 - ii: parity (ii & 1) ^ 1
                 if (P == 2 || ((ii & 1) ^ 1) == P) side(scp - 64 * ii, r[ii]);
                 enc_step<ESC>(c0, (r[ii] >> SH0) & 255u, t0[bt & 1][i]);
                 if (P == 2) enc_step<ESC>(c1, r[ii] >> SH1, t1[bt & 1][i]);
@@ -939,27 +942,51 @@ __device__ __forceinline__ void enc_full_rows(EncLane& c0, EncLane& c1, const ui
             }
         }
     };
-    uint32_t ra[32], rb[32];
-    uint32_t g = ng - 1;
-    load(ra, g);
-    for (;;) {
-        if (g == 0) { code(ra, 0); break; }
-        load(rb, g - 1);
-        code(ra, g);
-        g--;
-        if (g == 0) { code(rb, 0); break; }
-        load(ra, g - 1);
-        code(rb, g);
-        g--;
+    if (NBUF == 2) {
+        uint32_t ra[GR], rb[GR];
+        uint32_t g = ng - 1;
+        load(ra, g);
+        for (;;) {
+            if (g == 0) { code(ra, 0); break; }
+            load(rb, g - 1);
+            code(ra, g);
+            g--;
+            if (g == 0) { code(rb, 0); break; }
+            load(ra, g - 1);
+            code(rb, g);
+            g--;
+        }
+    } else {
+        // three buffers: group g - 2's loads issued while group g is coded (the
+        // last groups load group 0 again, so that every load is unconditional)
+        uint32_t ra[GR], rb[GR], rc[GR];
+        int32_t g = (int32_t)ng - 1;
+        load(ra, (uint32_t)g);
+        load(rb, (uint32_t)max(g - 1, 0));
+        for (;;) {
+            load(rc, (uint32_t)max(g - 2, 0));
+            code(ra, (uint32_t)g);
+            if (g == 0) break;
+            g--;
+            load(ra, (uint32_t)max(g - 2, 0));
+            code(rb, (uint32_t)g);
+            if (g == 0) break;
+            g--;
+            load(rb, (uint32_t)max(g - 2, 0));
+            code(rc, (uint32_t)g);
+            if (g == 0) break;
+            g--;
+        }
     }
 }
 
 // Warp-specialised persistent workgroups, one per CU: WS pairs of (2 coder
-// waves, 2 packer waves), each pair with two LDS slot sets used in turn.  The
+// waves, NPK packer waves), each pair with two LDS slot sets used in turn.  The
 // coder waves of a pair (byte FL and byte 3 of every column) take a unit from
 // the ticket counter, code it into the free set and hand it over; the packer
-// waves compute its lane sizes, publish its size, run the look-back, write its
-// headers and packed bytes, and give the set back.  Coding therefore never
+// waves compute its lane sizes, publish its size, run the look-back (one
+// wave), write its headers and lane records (another), pack its bytes (all of
+// them), and give the set back.  Coding therefore never
 // waits for the look-back; it waits only while both sets of its pair are in
 // the packers' hands.  Hand-overs are workgroup-scope LDS counters (a release
 // fence, then one lane's atomic add, on the producer side; acquire polls with
@@ -979,6 +1006,12 @@ __device__ __forceinline__ void enc_full_rows(EncLane& c0, EncLane& c1, const ui
 // by the general kernels) and, for the lowest slot, into the lane tables (at
 // most 2 bytes per symbol, 256 symbols: 516 bytes), never out of its region.
 static constexpr uint32_t FE_TABSZ = 4096, FE_CHDR = FE_TABSZ, FE_CBYTES = FE_TABSZ + 48;
+// Rows per load group and per table batch of the fast encoder's coders.
+static constexpr int ENC_GR = 32, ENC_TB = 2, ENC_NBUF = 2;
+// Packer waves per coder pair.  With four, a workgroup of two pairs is 12
+// waves (3 per SIMD); the coders are held to 128 VGPRs (4 waves per SIMD) so
+// that the overlapped histogram's wave still fits on every SIMD beside them.
+static constexpr int ENC_NPK = 4;
 static constexpr uint32_t R_REC = 0, R_MAP = 2048, R_SLOTS = 3076;
 static_assert(R_SLOTS >= 516 && R_SLOTS % 4 == 0 && R_MAP >= R_REC + 256 * 8 && R_SLOTS >= R_MAP + 1025,
               "region: lane records, block map and guard under the slots");
@@ -1021,7 +1054,7 @@ __host__ __device__ constexpr uint32_t ws_lds_bytes(uint32_t pairs, uint32_t can
 }
 
 template <int SPE, bool ESC, bool SIDE, int PAIRS, int NPK>
-__global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
+__global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_waves_per_eu(4))) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
                                                                   const EncSym* __restrict__ d_enc,
                                                                   const uint32_t* __restrict__ canon, FastEncParams fp,
                                                                   ckr_stream_header* __restrict__ hdrs,
@@ -1101,8 +1134,8 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) encode_fast_kernel(con
             EncLane c_unused = c;
             const uint32_t K = len > col ? (len - col + 255) / 256 : 0u;
             if ((len & 255u) == 0) {
-                if (rl == 0) enc_full_rows<SPE, ESC, SIDE, 0>(c, c_unused, usrc + col, sidecar, ubase, j, len >> 8, tab, lds8);
-                else enc_full_rows<SPE, ESC, SIDE, 1>(c, c_unused, usrc + col, sidecar, ubase, j, len >> 8, tab, lds8);
+                if (rl == 0) enc_full_rows<SPE, ESC, SIDE, 0, ENC_GR, ENC_TB, ENC_NBUF>(c, c_unused, usrc + col, sidecar, ubase, j, len >> 8, tab, lds8);
+                else enc_full_rows<SPE, ESC, SIDE, 1, ENC_GR, ENC_TB, ENC_NBUF>(c, c_unused, usrc + col, sidecar, ubase, j, len >> 8, tab, lds8);
             } else {
                 // A tensor's last unit: rows from the top down, one at a time; the top
                 // row may be partial (bf16: lane 4j+3 has one symbol fewer).
@@ -1428,7 +1461,7 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
 #define CKR_FAST_ENC_P(SPE_, ESC_, SIDE_, NPK_)                                                                  \
     (pairs == 2 ? run(encode_fast_kernel<SPE_, ESC_, SIDE_, 2, NPK_>, 128u * (2 + NPK_))                           \
                 : run(encode_fast_kernel<SPE_, ESC_, SIDE_, 1, NPK_>, 64u * (2 + NPK_)))
-#define CKR_FAST_ENC(SPE_, ESC_, SIDE_) CKR_FAST_ENC_P(SPE_, ESC_, SIDE_, 2)
+#define CKR_FAST_ENC(SPE_, ESC_, SIDE_) CKR_FAST_ENC_P(SPE_, ESC_, SIDE_, ENC_NPK)
     const bool side = sidecar != nullptr;
     if (g.spe == 2) {
         if (hp.escapes) e = side ? CKR_FAST_ENC(2, true, true) : CKR_FAST_ENC(2, true, false);
