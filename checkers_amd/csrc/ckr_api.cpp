@@ -11,6 +11,7 @@
 #include <map>
 #include <mutex>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -399,7 +400,14 @@ void prof_mark(const char* name, hipStream_t s, bool begin) {
     else (void)hipEventDestroy(e);
 }
 uint64_t* prof_phase_buffer(uint64_t n, hipStream_t s) {
-    if (!g_prof_on || t_noalloc || n == 0) return nullptr;
+    // per-unit phase stamps are extra work inside the encoder, so they are taken
+    // only on request (CKR_PROFILE_PHASES=1): the kernel times are then those of
+    // the kernel as it runs without profiling
+    static const bool phases = [] {
+        const char* v = std::getenv("CKR_PROFILE_PHASES");
+        return v && v[0] == '1';
+    }();
+    if (!g_prof_on || !phases || t_noalloc || n == 0) return nullptr;
     std::lock_guard<std::mutex> lk(g_prof_mu);
     void* p = nullptr;
     if (hipMalloc(&p, n * 8) != hipSuccess) return nullptr;

@@ -354,7 +354,9 @@ CKR_API int ckr_set_fast_paths(int mode);
 /* ---- per-kernel timing, no counterpart in the reference (its only timings are
  * host wall clocks, ANSCompressor.hpp:105-110).  Between begin and end every
  * kernel the library launches is bracketed by HIP events on its stream; end
- * synchronises them and writes "<kernel> <launches> <total_ms>" lines. ---- */
+ * synchronises them and writes "<kernel> <launches> <total_ms>" lines.  With
+ * CKR_PROFILE_PHASES=1 in the environment the fast encoder also stamps each
+ * unit's phases (extra work inside the kernel), reported as encode_fast.* lines. ---- */
 CKR_API int ckr_profile_begin(void);
 CKR_API int ckr_profile_end(char* buf, uint64_t buflen);
 
