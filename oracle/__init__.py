@@ -39,6 +39,8 @@ def lib():
             "oc_sidecar_per_elem": (i32, [i32]),
             "oc_extract_mantissa": (i32, [vp, u64, i32, vp, vp]),
             "oc_byte_hist": (None, [vp, u64, vp]),
+            "oc_extract_mantissa_mt": (i32, [vp, u64, i32, vp, vp, i32]),
+            "oc_byte_hist_mt": (None, [vp, u64, vp, i32]),
             "oc_normalize_histogram": (u32, [vp, i32, vp]),
             "oc_num_units": (u64, [u64, u64]),
             "oc_encode": (u64, [vp, u64, vp, u64, vp, vp, vp, i32]),
@@ -69,22 +71,28 @@ def as_bytes(arr):
     return np.ascontiguousarray(arr).view(np.uint8).reshape(-1)
 
 
-def extract_mantissa(raw, n, dtype):
+def extract_mantissa(raw, n, dtype, n_threads=1):
     """(masked bytes, sidecar bytes) of n elements given as raw bytes."""
     es, spe = ES[dtype], SPE[dtype]
     raw = as_bytes(raw)
     masked = np.empty(n * es, np.uint8)
     side = np.empty(max(n * spe, 1), np.uint8)
-    got = lib().oc_extract_mantissa(_p(raw), n, dtype, _p(masked), _p(side))
+    if n_threads > 1:
+        got = lib().oc_extract_mantissa_mt(_p(raw), n, dtype, _p(masked), _p(side), n_threads)
+    else:
+        got = lib().oc_extract_mantissa(_p(raw), n, dtype, _p(masked), _p(side))
     if got == 0:
         return raw[: n * es].copy(), np.empty(0, np.uint8)
     return masked, side[: n * spe]
 
 
-def byte_hist(data):
+def byte_hist(data, n_threads=1):
     data = as_bytes(data)
     h = np.zeros(256, np.uint32)
-    lib().oc_byte_hist(_p(data), data.size, _p(h))
+    if n_threads > 1:
+        lib().oc_byte_hist_mt(_p(data), data.size, _p(h), n_threads)
+    else:
+        lib().oc_byte_hist(_p(data), data.size, _p(h))
     return h
 
 

@@ -81,6 +81,33 @@ void oc_byte_hist(const uint8_t* data, uint64_t n, uint32_t* hist) {
     for (uint64_t i = 0; i < n; i++) hist[data[i]]++;
 }
 
+// The same two steps on n_threads host threads (OpenMP over element / byte
+// ranges; per-thread counts summed), for the CPU baseline's threaded leg.
+// Results equal the single-thread functions' (u32 counts wrap alike).
+int oc_extract_mantissa_mt(const uint8_t* src, uint64_t n, int dtype, uint8_t* masked, uint8_t* sidecar,
+                           int n_threads) {
+    const int es = oc_element_size(dtype), spe = oc_sidecar_per_elem(dtype);
+    if (spe == 0) return 0;
+#pragma omp parallel for num_threads(n_threads) schedule(static)
+    for (int64_t i = 0; i < (int64_t)n; i++) {
+        for (int j = 0; j < es; j++) masked[i * es + j] = (j < spe) ? 0 : src[i * es + j];
+        for (int j = 0; j < spe; j++) sidecar[i * spe + j] = src[i * es + j];
+    }
+    return spe;
+}
+
+void oc_byte_hist_mt(const uint8_t* data, uint64_t n, uint32_t* hist, int n_threads) {
+    for (int i = 0; i < 256; i++) hist[i] = 0;
+#pragma omp parallel num_threads(n_threads)
+    {
+        uint32_t h[256] = {};
+#pragma omp for schedule(static)
+        for (int64_t i = 0; i < (int64_t)n; i++) h[data[i]]++;
+#pragma omp critical
+        for (int i = 0; i < 256; i++) hist[i] += h[i];
+    }
+}
+
 // ---------------------------------------------------------------- table
 // src/ANSCompressor.cpp:416-503, step by step.  The decode arrays are written
 // only for slots < 4096: the reference writes past them when the table sum

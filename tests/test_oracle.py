@@ -311,3 +311,16 @@ def test_stats_initial_bounds_quirk():
     x = np.full(10, np.inf, np.float32)
     r = oc.tensor_stats(x, 10, dg.F32, 256)
     assert r["minmax"][0] == np.float32(1e37) and np.isinf(r["minmax"][1])
+
+
+def test_threaded_split_and_histogram_equal_single_thread():
+    """The CPU baseline's threaded split and histogram give the single-thread
+    functions' bytes and counts (fp32, bf16, int8; a length that splits unevenly)."""
+    for dt, gen in ((dg.F32, lambda n: dg.normal_f32(n, 1e-3, 5)), (dg.BF16, lambda n: dg.normal_bf16(n, 0.02, 6)),
+                    (dg.I8, lambda n: np.random.default_rng(7).integers(-128, 128, n).astype(np.int8))):
+        n = 300_007
+        raw = gen(n)
+        m1, s1 = oc.extract_mantissa(raw, n, dt)
+        m8, s8 = oc.extract_mantissa(raw, n, dt, n_threads=8)
+        assert np.array_equal(m1, m8) and np.array_equal(s1, s8)
+        assert np.array_equal(oc.byte_hist(m1), oc.byte_hist(m1, n_threads=8))
