@@ -227,7 +227,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--unit", type=int, default=65536)
-    ap.add_argument("--cpu-sample-mib", type=int, default=256)
+    ap.add_argument("--cpu-sample-mib", type=int, default=1024)
     ap.add_argument("--slice-gib", type=int, default=8, help="config 5: slice size of the streamed encode/decode")
     ap.add_argument("--sequential", action="store_true", help="one ckr_compress per tensor, no overlap")
     ap.add_argument("--no-cpu", action="store_true")
