@@ -34,6 +34,9 @@ EXPORTED = [  # every symbol include/checkers_amd.h declares
     "ckr_repair_build", "ckr_repair_apply",
     "ckr_fingerprint_weights", "ckr_cluster", "ckr_ckpt_write", "ckr_ckpt_open", "ckr_ckpt_count",
     "ckr_ckpt_info", "ckr_ckpt_restore", "ckr_ckpt_close",
+    "ckr_arena_create", "ckr_arena_alloc", "ckr_arena_used", "ckr_arena_reset", "ckr_arena_destroy",
+    "ckr_stats_slab_bytes", "ckr_carve_stats_slab", "ckr_analyze_device_records",
+    "ckr_analyze_device_records_workspace_bytes", "ckr_make_contiguous",
 ]
 
 
@@ -145,6 +148,16 @@ def lib():
         "ckr_ckpt_info": (i32, [vp, u64, vp]),
         "ckr_ckpt_restore": (i32, [vp, u64, vp, vp]),
         "ckr_ckpt_close": (None, [vp]),
+        "ckr_arena_create": (i32, [u64, vp]),
+        "ckr_arena_alloc": (i32, [vp, u64, u64, vp]),
+        "ckr_arena_used": (u64, [vp]),
+        "ckr_arena_reset": (None, [vp]),
+        "ckr_arena_destroy": (None, [vp]),
+        "ckr_stats_slab_bytes": (u64, [ctypes.c_uint32, u64]),
+        "ckr_carve_stats_slab": (i32, [vp, ctypes.c_uint32, u64, vp]),
+        "ckr_analyze_device_records": (i32, [vp, u64, vp, u64, vp]),
+        "ckr_analyze_device_records_workspace_bytes": (u64, [vp, u64]),
+        "ckr_make_contiguous": (i32, [vp, i32, vp, vp, i32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L_, name)
@@ -209,7 +222,7 @@ def _torch():
 
 
 def torch_tag(dtype):
-    """C tag of a torch dtype (explicit; see checkers_py for the reference's string parser)."""
+    """C tag of a torch dtype (explicit; checkers_py parses dtype strings as the reference does)."""
     torch = _torch()
     return {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.int8: I8,
             torch.int32: I32}.get(dtype, UNKNOWN)

@@ -16,7 +16,7 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcheckers_amd.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["ckr_kernels.hip", "ckr_repair.hip", "ckr_api.cpp", "ckr_checkpoint.cpp"]
+SOURCES = ["ckr_kernels.hip", "ckr_repair.hip", "ckr_api.cpp", "ckr_checkpoint.cpp", "ckr_context.hip"]
 
 # -packed-fp32-ops: no v_pk_*_f32 generated anywhere (wrong results seen with
 # some of their forms on these machines).
@@ -29,6 +29,26 @@ FLAGS = [
 
 
 CLI = os.path.join(HERE, "ckr_prefix_mask_repair")
+
+# the pybind11 module `checkers_py` (the reference's module name), at the
+# repository root so that `import checkers_py` finds it; host code only, not
+# linked to the library or the HIP runtime (it loads checkers_amd/ at run time)
+PY_SOURCES = ["checkers_api.cpp", "python_bindings.cpp"]
+
+
+def py_module_path():
+    import sysconfig
+    return os.path.join(ROOT, "checkers_py" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def _py_module_cmd():
+    import sysconfig
+    import pybind11
+    return (["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-fvisibility=hidden", "-Wall",
+             "-D__HIP_PLATFORM_AMD__", "-I", "/opt/rocm/include", "-I", os.path.join(ROOT, "include"),
+             "-I", pybind11.get_include(), "-I", sysconfig.get_paths()["include"]]
+            + [os.path.join(CSRC, s) for s in PY_SOURCES]
+            + ["-o", py_module_path() + ".tmp", "-ldl"])
 
 
 def _run(cmd, verbose):
@@ -67,6 +87,12 @@ def build(verbose=True, incremental=False):
           os.path.join(CSRC, "ckr_repair_cli.cpp"), "-o", CLI + ".tmp",
           "-L", HERE, "-lcheckers_amd", "-Wl,-rpath,$ORIGIN"], verbose)
     os.replace(CLI + ".tmp", CLI)
+    mod = py_module_path()
+    if not incremental or any(not os.path.exists(mod) or os.path.getmtime(d) > os.path.getmtime(mod)
+                              for d in [LIB, os.path.join(ROOT, "include", "checkers_api.hpp")]
+                              + [os.path.join(CSRC, s) for s in PY_SOURCES]):
+        _run(_py_module_cmd(), verbose)
+        os.replace(mod + ".tmp", mod)
     return LIB
 
 

@@ -372,6 +372,7 @@ int ckr_ckpt_write(const char* output_dir, int rank, const ckr_ckpt_tensor* tens
         for (void* p : {d_ws, d_out, d_hdr, d_off, d_side}) if (p) (void)hipFree(p);
     };
     auto alloc = [&](void** p, uint64_t b) { return hipMalloc(p, std::max<uint64_t>(b, 256)); };
+    if (cap_out == 0) return write_files(fs::path(output_dir), rank, unit_bytes, outs);  // nothing to compress
     if (alloc(&d_ws, cap_ws) != hipSuccess || alloc(&d_out, cap_out) != hipSuccess ||
         alloc(&d_hdr, cap_hdr) != hipSuccess || alloc(&d_off, cap_off) != hipSuccess ||
         alloc(&d_side, cap_side) != hipSuccess) {

@@ -341,6 +341,61 @@ CKR_API int ckr_ckpt_info(const ckr_ckpt* c, uint64_t index, ckr_ckpt_entry* out
 CKR_API int ckr_ckpt_restore(const ckr_ckpt* c, uint64_t index, void* d_dst, void* stream);
 CKR_API void ckr_ckpt_close(ckr_ckpt* c);
 
+/* ---- context memory: device records, arena, slabs, gather ----
+ * ckr_device_tensor_record ← DeviceTensorRecord (include/checkers/MemoryManager.hpp:60-72),
+ * the same 72-byte layout: the tensor's device pointer, its statistics buffers
+ * carved from a slab, its element count, requested bins, dtype tag and
+ * contiguity (0 contiguous, 1 non-contiguous, 2 scalar: TensorResource.hpp:53-57).
+ * d_statistics is never set (the reference leaves it null as well). */
+typedef struct ckr_device_tensor_record {
+    const char* name;
+    void*       d_ptr;
+    uint32_t*   d_histogram;
+    float*      d_raw_moments;
+    void*       d_statistics;
+    float*      d_fingerprint;
+    float*      d_minmax;
+    uint64_t    num_elements;
+    uint32_t    histogram_bins;
+    uint8_t     data_type;
+    uint8_t     contiguity;
+    uint8_t     pad_[2];
+} ckr_device_tensor_record;
+
+/* Arena: one hipMalloc of `capacity` bytes, handed out by bump allocation
+ * (replaces the Umpire pools of MemoryManager / TensorResource,
+ * src/MemoryManager.cpp:19-25, :403-425; src/TensorResource.cpp:38-55, :85-153).
+ * ckr_arena_alloc returns CKR_E_CAPACITY when the arena is full; reset makes
+ * all of it free again; destroy frees the device memory. */
+typedef struct ckr_arena ckr_arena;
+CKR_API int ckr_arena_create(uint64_t capacity, ckr_arena** out);
+CKR_API int ckr_arena_alloc(ckr_arena* a, uint64_t bytes, uint64_t alignment, void** d_out);
+CKR_API uint64_t ckr_arena_used(const ckr_arena* a);
+CKR_API void ckr_arena_reset(ckr_arena* a);
+CKR_API void ckr_arena_destroy(ckr_arena* a);
+
+/* BufferPlan.total_bytes of one tensor (compute_buffer_plan,
+ * src/MemoryManager.cpp:692-707): histogram (all requested bins, 4 bytes
+ * each), 4 moments, min/max and the 5-float fingerprint, each rounded up to
+ * `alignment` (the reference's default 256).  ckr_carve_stats_slab sets the
+ * record's four buffer pointers in that order (the slab carving of
+ * src/MemoryManager.cpp:440-466). */
+CKR_API uint64_t ckr_stats_slab_bytes(uint32_t histogram_bins, uint64_t alignment);
+CKR_API int ckr_carve_stats_slab(void* d_slab, uint32_t histogram_bins, uint64_t alignment,
+                                 ckr_device_tensor_record* rec);
+/* ckr_analyze over device records (their statistics buffers). */
+CKR_API uint64_t ckr_analyze_device_records_workspace_bytes(const ckr_device_tensor_record* h_recs, uint64_t n);
+CKR_API int ckr_analyze_device_records(const ckr_device_tensor_record* h_recs, uint64_t n, void* d_workspace,
+                                       uint64_t workspace_bytes, void* stream);
+
+/* make_contiguous ← TensorResource::make_contiguous (src/TensorResource.cpp:85-153):
+ * copies a strided tensor (ndim <= 8, shape and strides in elements, element
+ * size 1/2/4/8) into d_dst in row-major order.  The reference's fragments
+ * (MemoryManager.cpp:709-740) assume rows with a unit inner stride; this
+ * gather follows every stride, which is the same copy wherever that holds. */
+CKR_API int ckr_make_contiguous(const void* d_src, int ndim, const int64_t* shape, const int64_t* strides,
+                                int elem_size, void* d_dst, void* stream);
+
 /* ---- path selection, no counterpart in the reference.  mode 1 (default):
  * fast kernels — lanes of masked planes coded once per lane count (their
  * streams are identical), units of at most 64 KiB coded and decoded through
