@@ -602,7 +602,7 @@ def write_checkpoint(output_dir, rank, tensors, unit_bytes=0, repair_tables=Fals
 
 
 class Checkpoint:
-    """Reader of a rank's .ansc (v2 or v3) / .mant / .dict files; restores
+    """Reader of a rank's .ansc (v2 or v4) / .mant / .dict files; restores
     tensors on the device."""
 
     def __init__(self, directory, rank=0):

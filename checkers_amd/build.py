@@ -16,7 +16,8 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libcheckers_amd.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["ckr_kernels.hip", "ckr_repair.hip", "ckr_api.cpp", "ckr_checkpoint.cpp", "ckr_context.hip"]
+SOURCES = ["ckr_kernels.hip", "ckr_repair.hip", "ckr_api.cpp", "ckr_checkpoint.cpp", "ckr_context.hip",
+           "ckr_container.hip"]
 
 # -packed-fp32-ops: no v_pk_*_f32 generated anywhere (wrong results seen with
 # some of their forms on these machines).
@@ -67,7 +68,8 @@ def _stale(src, obj):
     """An object older than its source or a shared header."""
     if not os.path.exists(obj):
         return True
-    deps = [src, os.path.join(ROOT, "include", "checkers_amd.h"), os.path.join(CSRC, "ckr_internal.h")]
+    deps = [src, os.path.join(ROOT, "include", "checkers_amd.h"), os.path.join(CSRC, "ckr_internal.h"),
+            os.path.join(CSRC, "ckr_container.h")]
     return any(os.path.getmtime(d) > os.path.getmtime(obj) for d in deps)
 
 

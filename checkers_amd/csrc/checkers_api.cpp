@@ -470,7 +470,7 @@ void compress_and_save(const std::string& output_path) {
     try {
         if (!g_ctx) throw std::runtime_error("Context not initialized: call initialize_context first.");
         Context& c = *g_ctx;
-        // CHECKERS_UNIT_BYTES: unit size of the chunked states file (.ansc v3,
+        // CHECKERS_UNIT_BYTES: unit size of the chunked states file (.ansc v4,
         // default 65536); 0 writes the reference's v2 layout (one stream per
         // tensor, tensors below 4 GiB, encoded 256 lanes wide only)
         uint64_t unit = 65536;

@@ -10,21 +10,29 @@
 //   write_rank_states_file / _mantissa_ / _tables_ src/ANSCompressor.cpp:721-931
 // The reference has no reader; ckr_ckpt_open / ckr_ckpt_restore are this
 // library's own, over the same formats.
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <unistd.h>
 
 #include <algorithm>
+#include <cerrno>
 #include <cmath>
+#include <condition_variable>
 #include <cstdio>
 #include <cstring>
+#include <deque>
 #include <filesystem>
 #include <fstream>
 #include <map>
+#include <mutex>
 #include <numeric>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
 #include "checkers_amd.h"
+#include "ckr_container.h"
 #include "ckr_internal.h"
 
 namespace {
@@ -35,7 +43,8 @@ constexpr uint32_t kAnscMagic = 0x414E5343u;  // "ANSC"
 constexpr uint32_t kMantMagic = 0x4D414E54u;  // "MANT"
 constexpr uint32_t kDictMagic = 0x44494354u;  // "DICT"
 constexpr uint64_t kV2Entry = 256 + 8 + 32 + 256 + 256 * 16;  // 4648
-constexpr uint64_t kV3Entry = 256 + 8 + 32 + 256 + 16;        // 568
+constexpr uint64_t kV4Entry = 256 + 8 + 32 + 256 + 24;        // 576
+constexpr uint64_t kV4Header = 32;
 constexpr uint64_t kMantEntry = 288;
 constexpr uint64_t kDictEntry = 2308;
 
@@ -75,34 +84,6 @@ struct DisjointSets {
     }
 };
 
-// ---- little-endian file helpers
-struct Out {
-    std::ofstream f;
-    explicit Out(const fs::path& p) : f(p, std::ios::binary | std::ios::trunc) {}
-    void put(const void* p, size_t n) { f.write(static_cast<const char*>(p), (std::streamsize)n); }
-    void u8(uint8_t v) { put(&v, 1); }
-    void u32(uint32_t v) { put(&v, 4); }
-    void u64(uint64_t v) { put(&v, 8); }
-    void zeros(size_t n) { static const char z[64] = {}; while (n) { size_t k = std::min<size_t>(n, 64); put(z, k); n -= k; } }
-    void name(const std::string& s) {  // 256 bytes, at most 255 copied, NUL padded
-        char b[256] = {};
-        std::memcpy(b, s.data(), std::min<size_t>(s.size(), 255));
-        put(b, 256);
-    }
-};
-
-struct TensorOut {
-    std::string name, anchor;
-    int dtype = 0;
-    bool owns = false;
-    uint64_t n_elems = 0, original = 0;
-    std::vector<uint8_t> data, sidecar;
-    std::vector<ckr_stream_header> headers;  // n_units * 256
-    std::vector<uint64_t> unit_off;          // n_units + 1
-    uint32_t spe = 0;
-    ckr_freq_table* table = nullptr;         // owners: the table they built
-};
-
 bool unit_is_raw(const ckr_stream_header* h, uint64_t len) {
     if (h[0].byte_count != (uint32_t)len) return false;
     for (int t = 1; t < 256; t++)
@@ -110,107 +91,227 @@ bool unit_is_raw(const ckr_stream_header* h, uint64_t len) {
     return true;
 }
 
-int write_files(const fs::path& dir, int rank, uint64_t unit_bytes, const std::vector<TensorOut>& ts) {
-    std::error_code ec;
-    fs::create_directories(dir / "mantissa", ec);
-    fs::create_directories(dir / "tables", ec);
-    if (ec) return err(CKR_E_INVALID, "[ckr] cannot create " + dir.string() + ": " + ec.message());
-    const uint32_t r = (uint32_t)(rank < 0 ? 0 : rank);
-    const std::string tag = "rank_" + std::to_string(rank < 0 ? 0 : rank);
-    {
-        const fs::path p = dir / (tag + "_states.ansc");
-        Out o(p);
-        if (!o.f) return err(CKR_E_INVALID, "[ANS] cannot open for write: " + p.string());
-        const bool v3 = unit_bytes != 0;
-        o.u32(kAnscMagic);
-        o.u32(v3 ? 3u : 2u);
-        o.u32(r);
-        o.u32((uint32_t)ts.size());
-        if (v3) o.u64(unit_bytes);
-        // per-unit metadata section of v3: headers then unit offsets, tensor after tensor
-        std::vector<uint64_t> meta_off(ts.size() + 1, 0);
-        for (size_t i = 0; i < ts.size(); i++)
-            meta_off[i + 1] = meta_off[i] + ts[i].headers.size() * 16 + ts[i].unit_off.size() * 8;
-        uint64_t doff = 0;
-        for (const auto& t : ts) {
-            o.name(t.name);
-            const uint64_t nu = t.unit_off.empty() ? 0 : t.unit_off.size() - 1;
-            bool raw = nu > 0;
-            for (uint64_t u = 0; u < nu && raw; u++) {
-                const uint64_t len = v3 ? std::min<uint64_t>(unit_bytes, t.original - u * unit_bytes) : t.original;
-                raw = unit_is_raw(&t.headers[u * 256], len);
-            }
-            o.u8((uint8_t)t.dtype);
-            o.u8(raw ? 1 : 0);
-            o.u8(t.owns ? 1 : 0);
-            o.zeros(5);
-            o.u64(t.original);
-            o.u64(t.n_elems);
-            o.u64(doff);
-            o.u64(t.data.size());
-            doff += t.data.size();
-            o.name(t.owns ? std::string() : t.anchor);
-            if (v3) {
-                o.u64(nu);
-                o.u64(meta_off[&t - ts.data()]);
-            } else {
-                o.put(t.headers.data(), 256 * 16);
-            }
-        }
-        if (v3)
-            for (const auto& t : ts) {
-                o.put(t.headers.data(), t.headers.size() * 16);
-                o.put(t.unit_off.data(), t.unit_off.size() * 8);
-            }
-        for (const auto& t : ts) o.put(t.data.data(), t.data.size());
-        if (!o.f) return err(CKR_E_INVALID, "[ckr] write failed: " + p.string());
+// ---- the writer's staging: device buffers go to the files through a pinned
+// host ring.  A copy thread queues each range's D2H chunks on its own stream
+// as ring slots come free; writer threads wait for a chunk's copy and pwrite
+// it.  Meanwhile the calling thread encodes the next tensor into the other of
+// two buffer sets.
+constexpr uint64_t kSlotBytes = 32ull << 20;
+constexpr uint32_t kSlots = 8;
+
+struct PinnedRing {
+    std::mutex use;  // held by one ckr_ckpt_write for its whole duration
+    uint8_t* base = nullptr;
+};
+PinnedRing g_ring;
+
+struct Range {
+    int fd;
+    uint64_t off;
+    const uint8_t* d_src;
+    uint64_t len;
+};
+
+class Stager {
+  public:
+    Stager(uint8_t* ring, int device, hipStream_t cs, int writers) : ring_(ring), device_(device), cs_(cs) {
+        for (uint32_t i = 0; i < kSlots; i++) free_.push_back(i);
+        for (auto& e : slot_ev_) (void)hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventBlockingSync);
+        for (auto& e : set_ev_) (void)hipEventCreateWithFlags(&e, hipEventDisableTiming);
+        copier_ = std::thread([this] { copy_loop(); });
+        for (int i = 0; i < writers; i++) writers_.emplace_back([this] { write_loop(); });
     }
-    {
-        const fs::path p = dir / "mantissa" / (tag + "_mantissa.mant");
-        Out o(p);
-        if (!o.f) return err(CKR_E_INVALID, "[ANS] cannot open mantissa for write: " + p.string());
-        uint32_t cnt = 0;
-        for (const auto& t : ts) cnt += t.spe > 0;
-        o.u32(kMantMagic);
-        o.u32(2u);
-        o.u32(r);
-        o.u32(cnt);
-        uint64_t doff = 0;
-        for (const auto& t : ts) {
-            if (!t.spe) continue;
-            o.name(t.name);
-            o.u8((uint8_t)t.dtype);
-            o.u8((uint8_t)t.spe);
-            o.zeros(6);
-            o.u64(t.n_elems);
-            o.u64(doff);
-            o.u64(t.sidecar.size());
-            doff += t.sidecar.size();
-        }
-        for (const auto& t : ts)
-            if (t.spe) o.put(t.sidecar.data(), t.sidecar.size());
-        if (!o.f) return err(CKR_E_INVALID, "[ckr] write failed: " + p.string());
+    ~Stager() {
+        finish();
+        for (auto e : slot_ev_) (void)hipEventDestroy(e);
+        for (auto e : set_ev_) (void)hipEventDestroy(e);
     }
-    {
-        const fs::path p = dir / "tables" / (tag + "_tables.dict");
-        Out o(p);
-        if (!o.f) return err(CKR_E_INVALID, "[ANS] cannot open tables for write: " + p.string());
-        uint32_t cnt = 0;
-        for (const auto& t : ts) cnt += t.owns;
-        o.u32(kDictMagic);
-        o.u32(1u);
-        o.u32(r);
-        o.u32(cnt);
-        for (const auto& t : ts) {
-            if (!t.owns) continue;
-            o.name(t.name);
-            o.put(t.table->norm_freq, 256 * 4);
-            o.put(t.table->cum_freq, 257 * 4);
-        }
-        if (!o.f) return err(CKR_E_INVALID, "[ckr] write failed: " + p.string());
+    // Waits until the previous task of buffer set `set` is queued on the copy
+    // stream; returns the event its copies complete at (null for a first use).
+    hipEvent_t acquire_set(int set) {
+        std::unique_lock<std::mutex> l(m_);
+        cv_.wait(l, [&] { return !set_busy_[set]; });
+        return set_used_[set] ? set_ev_[set] : nullptr;
     }
-    return CKR_OK;
+    // Copies `ranges` once `ready` (recorded on the encoding stream) has completed.
+    void submit(std::vector<Range> ranges, int set, hipEvent_t ready) {
+        std::lock_guard<std::mutex> l(m_);
+        set_busy_[set] = set_used_[set] = true;
+        tasks_.push_back({std::move(ranges), set, ready});
+        cv_.notify_all();
+    }
+    int finish() {
+        {
+            std::lock_guard<std::mutex> l(m_);
+            if (closed_) return rc_;
+            closed_ = true;
+            cv_.notify_all();
+        }
+        if (copier_.joinable()) copier_.join();
+        {
+            std::lock_guard<std::mutex> l(m_);
+            writers_done_ = true;
+            cv_.notify_all();
+        }
+        for (auto& t : writers_) t.join();
+        return rc_;
+    }
+    int status() {
+        std::lock_guard<std::mutex> l(m_);
+        return rc_;
+    }
+    std::string message() {
+        std::lock_guard<std::mutex> l(m_);
+        return msg_;
+    }
+
+  private:
+    struct Task {
+        std::vector<Range> ranges;
+        int set;
+        hipEvent_t ready;
+    };
+    struct Chunk {
+        int fd;
+        uint64_t off, len;
+        uint32_t slot;
+    };
+    void fail(int rc, const std::string& m) {  // with m_ held
+        if (rc_ == CKR_OK) {
+            rc_ = rc;
+            msg_ = m;
+        }
+    }
+    void copy_loop() {
+        (void)hipSetDevice(device_);
+        for (;;) {
+            Task t;
+            {
+                std::unique_lock<std::mutex> l(m_);
+                cv_.wait(l, [&] { return !tasks_.empty() || closed_; });
+                if (tasks_.empty()) return;
+                t = std::move(tasks_.front());
+                tasks_.pop_front();
+            }
+            hipError_t e = hipStreamWaitEvent(cs_, t.ready, 0);
+            for (const Range& r : t.ranges)
+                for (uint64_t k = 0; k < r.len && e == hipSuccess; k += kSlotBytes) {
+                    uint32_t slot;
+                    {
+                        std::unique_lock<std::mutex> l(m_);
+                        cv_.wait(l, [&] { return !free_.empty(); });
+                        if (rc_ != CKR_OK) break;
+                        slot = free_.front();
+                        free_.pop_front();
+                    }
+                    const uint64_t len = std::min(kSlotBytes, r.len - k);
+                    e = hipMemcpyAsync(ring_ + slot * kSlotBytes, r.d_src + k, len, hipMemcpyDeviceToHost, cs_);
+                    if (e == hipSuccess) e = hipEventRecord(slot_ev_[slot], cs_);
+                    std::lock_guard<std::mutex> l(m_);
+                    if (e != hipSuccess) {
+                        free_.push_back(slot);
+                        break;
+                    }
+                    chunks_.push_back({r.fd, r.off + k, len, slot});
+                    cv_.notify_all();
+                }
+            const hipError_t e2 = hipEventRecord(set_ev_[t.set], cs_);
+            std::lock_guard<std::mutex> l(m_);
+            if (e != hipSuccess || e2 != hipSuccess)
+                fail(CKR_E_HIP, std::string("[ckr] staging copy failed: ") + hipGetErrorString(e != hipSuccess ? e : e2));
+            set_busy_[t.set] = false;
+            cv_.notify_all();
+        }
+    }
+    void write_loop() {
+        (void)hipSetDevice(device_);
+        for (;;) {
+            Chunk c;
+            {
+                std::unique_lock<std::mutex> l(m_);
+                cv_.wait(l, [&] { return !chunks_.empty() || writers_done_; });
+                if (chunks_.empty()) return;
+                c = chunks_.front();
+                chunks_.pop_front();
+            }
+            int rc = CKR_OK;
+            std::string m;
+            const hipError_t e = hipEventSynchronize(slot_ev_[c.slot]);
+            if (e != hipSuccess) {
+                rc = CKR_E_HIP;
+                m = std::string("[ckr] staging copy failed: ") + hipGetErrorString(e);
+            } else if (status() == CKR_OK) {
+                const uint8_t* p = ring_ + c.slot * kSlotBytes;
+                for (uint64_t done = 0; done < c.len;) {
+                    const ssize_t w = ::pwrite(c.fd, p + done, c.len - done, (off_t)(c.off + done));
+                    if (w <= 0) {
+                        if (w < 0 && errno == EINTR) continue;
+                        rc = CKR_E_INVALID;
+                        m = std::string("[ckr] write failed: ") + std::strerror(w < 0 ? errno : EIO);
+                        break;
+                    }
+                    done += (uint64_t)w;
+                }
+            }
+            std::lock_guard<std::mutex> l(m_);
+            if (rc != CKR_OK) fail(rc, m);
+            free_.push_back(c.slot);
+            cv_.notify_all();
+        }
+    }
+
+    uint8_t* ring_;
+    int device_;
+    hipStream_t cs_;
+    std::mutex m_;
+    std::condition_variable cv_;
+    std::deque<Task> tasks_;
+    std::deque<Chunk> chunks_;
+    std::deque<uint32_t> free_;
+    hipEvent_t slot_ev_[kSlots] = {};
+    hipEvent_t set_ev_[2] = {};
+    bool set_busy_[2] = {false, false}, set_used_[2] = {false, false};
+    bool closed_ = false, writers_done_ = false;
+    int rc_ = CKR_OK;
+    std::string msg_;
+    std::thread copier_;
+    std::vector<std::thread> writers_;
+};
+
+// Little-endian serialisation of the small parts (headers, index entries, tables).
+struct Buf {
+    std::vector<uint8_t> b;
+    void put(const void* p, size_t n) { b.insert(b.end(), (const uint8_t*)p, (const uint8_t*)p + n); }
+    void u8(uint8_t v) { put(&v, 1); }
+    void u32(uint32_t v) { put(&v, 4); }
+    void u64(uint64_t v) { put(&v, 8); }
+    void zeros(size_t n) { b.insert(b.end(), n, 0); }
+    void name(const std::string& s) {  // 256 bytes, at most 255 copied, NUL padded
+        char z[256] = {};
+        std::memcpy(z, s.data(), std::min<size_t>(s.size(), 255));
+        put(z, 256);
+    }
+};
+
+bool pwrite_all(int fd, const void* p, uint64_t n, uint64_t off) {
+    const uint8_t* q = static_cast<const uint8_t*>(p);
+    while (n) {
+        const ssize_t w = ::pwrite(fd, q, n, (off_t)off);
+        if (w < 0 && errno == EINTR) continue;
+        if (w <= 0) return false;
+        q += w;
+        n -= (uint64_t)w;
+        off += (uint64_t)w;
+    }
+    return true;
 }
+
+struct Fd {
+    int fd = -1;
+    ~Fd() {
+        if (fd >= 0) ::close(fd);
+    }
+};
 
 // Table from stored norm/cum (the decode arrays are rebuilt by the decoder).
 void table_from_norm(const uint32_t* norm, const uint32_t* cum, ckr_freq_table* t) {
@@ -248,7 +349,7 @@ struct ckr_ckpt {
     struct Entry {
         std::string name, anchor;
         uint8_t dtype = 0, raw = 0, owns = 0;
-        uint64_t original = 0, n_elems = 0, data_off = 0, data_size = 0, n_units = 0, meta_off = 0;
+        uint64_t original = 0, n_elems = 0, data_off = 0, data_size = 0, n_units = 0, meta_off = 0, meta_size = 0;
         std::vector<ckr_stream_header> v2_headers;
     };
     std::vector<Entry> entries;
@@ -342,6 +443,54 @@ int ckr_ckpt_write(const char* output_dir, int rank, const ckr_ckpt_tensor* tens
     if (!output_dir || (n && !tensors)) return err(CKR_E_INVALID, "[ckr] null pointer");
     if (unit_bytes % 256) return err(CKR_E_INVALID, "[ckr] unit_bytes must be a multiple of 256");
     hipStream_t s = (hipStream_t)stream;
+    const bool v4 = unit_bytes != 0;
+    // the tensors written, in record order, and the layout of the three files
+    struct Item {
+        uint64_t i, nu, n_bytes;
+        int es, spe;
+        uint64_t side_off;
+    };
+    std::vector<Item> items;
+    uint64_t cap_ws = 0, cap_out = 0, cap_hdr = 0, side_total = 0, cap_side = 0, n_side = 0, nu_max = 0;
+    for (uint64_t i = 0; i < n; i++) {
+        const auto& t = tensors[i];
+        if (!t.d_ptr || !t.num_elements) continue;
+        const int es = ckr_element_size(t.dtype);
+        if (!es) return err(CKR_E_INVALID, "[ckr] unknown dtype for tensor " + std::string(t.name ? t.name : ""));
+        if (!v4 && t.num_elements * es > 0xFFFFFFFFull)
+            return err(CKR_E_INVALID, "[ckr] tensor " + std::string(t.name ? t.name : "") + " needs unit_bytes (over 4 GiB)");
+        Item it{i, ckr_num_units(t.num_elements, t.dtype, unit_bytes), t.num_elements * (uint64_t)es, es,
+                ckr_sidecar_bytes_per_elem(t.dtype), side_total};
+        const uint64_t side = t.num_elements * (uint64_t)it.spe;
+        side_total += side;
+        n_side += it.spe > 0;
+        cap_side = std::max(cap_side, side);
+        cap_ws = std::max(cap_ws, ckr_encode_workspace_bytes(t.num_elements, t.dtype, unit_bytes));
+        cap_out = std::max(cap_out, ckr_encode_max_output_bytes(t.num_elements, t.dtype, unit_bytes));
+        cap_hdr = std::max(cap_hdr, it.nu * 256 * 16);
+        nu_max = std::max(nu_max, it.nu);
+        items.push_back(it);
+    }
+    const fs::path dir(output_dir);
+    std::error_code ec;
+    fs::create_directories(dir / "mantissa", ec);
+    fs::create_directories(dir / "tables", ec);
+    if (ec) return err(CKR_E_INVALID, "[ckr] cannot create " + dir.string() + ": " + ec.message());
+    const uint32_t r = (uint32_t)(rank < 0 ? 0 : rank);
+    const std::string tag = "rank_" + std::to_string(r);
+    const fs::path sp = dir / (tag + "_states.ansc"), mp = dir / "mantissa" / (tag + "_mantissa.mant"),
+                   dp = dir / "tables" / (tag + "_tables.dict");
+    Fd fs_, fm, fd_;
+    fs_.fd = ::open(sp.c_str(), O_WRONLY | O_CREAT | O_TRUNC, 0644);
+    if (fs_.fd < 0) return err(CKR_E_INVALID, "[ANS] cannot open for write: " + sp.string());
+    fm.fd = ::open(mp.c_str(), O_WRONLY | O_CREAT | O_TRUNC, 0644);
+    if (fm.fd < 0) return err(CKR_E_INVALID, "[ANS] cannot open mantissa for write: " + mp.string());
+    fd_.fd = ::open(dp.c_str(), O_WRONLY | O_CREAT | O_TRUNC, 0644);
+    if (fd_.fd < 0) return err(CKR_E_INVALID, "[ANS] cannot open tables for write: " + dp.string());
+    const uint64_t nw = items.size();
+    const uint64_t data_base = v4 ? kV4Header + nw * kV4Entry : 16 + nw * kV2Entry;
+    const uint64_t mant_base = 16 + n_side * kMantEntry;
+
     // anchors: the first record of each cluster (cluster_anchor); the table
     // owner is the first one that is compressed (compress_and_save_all :1057-1069)
     std::unordered_map<int32_t, std::string> anchor_name;
@@ -349,101 +498,255 @@ int ckr_ckpt_write(const char* output_dir, int rank, const ckr_ckpt_tensor* tens
         if (tensors[i].cluster_id >= 0 && !anchor_name.count(tensors[i].cluster_id))
             anchor_name[tensors[i].cluster_id] = tensors[i].name ? tensors[i].name : "";
     std::unordered_map<int32_t, ckr_freq_table*> cluster_table;
-    std::vector<TensorOut> outs;
-    std::vector<ckr_freq_table> tables(n);
-    outs.reserve(n);
-    uint64_t cap_ws = 0, cap_out = 0, cap_hdr = 0, cap_off = 0, cap_side = 0;
-    for (uint64_t i = 0; i < n; i++) {
-        const auto& t = tensors[i];
-        if (!t.d_ptr || !t.num_elements) continue;
-        const int es = ckr_element_size(t.dtype);
-        if (!es) return err(CKR_E_INVALID, "[ckr] unknown dtype for tensor " + std::string(t.name ? t.name : ""));
-        const uint64_t nu = ckr_num_units(t.num_elements, t.dtype, unit_bytes);
-        if (!unit_bytes && t.num_elements * es > 0xFFFFFFFFull)
-            return err(CKR_E_INVALID, "[ckr] tensor " + std::string(t.name) + " needs unit_bytes (over 4 GiB)");
-        cap_ws = std::max(cap_ws, ckr_encode_workspace_bytes(t.num_elements, t.dtype, unit_bytes));
-        cap_out = std::max(cap_out, t.num_elements * es);
-        cap_hdr = std::max(cap_hdr, nu * 256 * 16);
-        cap_off = std::max(cap_off, (nu + 1) * 8);
-        cap_side = std::max(cap_side, t.num_elements * (uint64_t)ckr_sidecar_bytes_per_elem(t.dtype));
-    }
-    void *d_ws = nullptr, *d_out = nullptr, *d_hdr = nullptr, *d_off = nullptr, *d_side = nullptr;
-    auto release = [&]() {
-        for (void* p : {d_ws, d_out, d_hdr, d_off, d_side}) if (p) (void)hipFree(p);
+    std::vector<ckr_freq_table> tables(nw);
+
+    // per written tensor: what the index needs
+    struct Out {
+        uint64_t data_off = 0, data_size = 0, meta_off = 0;
+        bool raw = false, owns = false;
+        std::string anchor;
+        ckr_freq_table* table = nullptr;
+        std::vector<ckr_stream_header> v2_headers;
+        std::vector<uint8_t> meta;
     };
-    auto alloc = [&](void** p, uint64_t b) { return hipMalloc(p, std::max<uint64_t>(b, 256)); };
-    if (cap_out == 0) return write_files(fs::path(output_dir), rank, unit_bytes, outs);  // nothing to compress
-    if (alloc(&d_ws, cap_ws) != hipSuccess || alloc(&d_out, cap_out) != hipSuccess ||
-        alloc(&d_hdr, cap_hdr) != hipSuccess || alloc(&d_off, cap_off) != hipSuccess ||
-        alloc(&d_side, cap_side) != hipSuccess) {
+    std::vector<Out> outs(nw);
+
+    // device buffers: a workspace, and two sets of encode outputs (plus the
+    // stored-byte runs and unit records of v4) that alternate between tensors
+    struct Set {
+        void *out = nullptr, *hdr = nullptr, *off = nullptr, *side = nullptr, *stored = nullptr, *rec = nullptr,
+             *plan = nullptr;
+        std::vector<uint64_t> rec_off, out_off;  // host copies kept until the set is reused
+    };
+    Set sets[2];
+    void* d_ws = nullptr;
+    hipStream_t cs = nullptr;
+    hipEvent_t ready[2] = {nullptr, nullptr};
+    std::vector<void*> owned;
+    auto release = [&]() {
+        for (void* p : owned) (void)hipFree(p);
+        for (auto e : ready) if (e) (void)hipEventDestroy(e);
+        if (cs) (void)hipStreamDestroy(cs);
+    };
+    auto alloc = [&](void** p, uint64_t b) {
+        const hipError_t e = hipMalloc(p, std::max<uint64_t>(b, 256));
+        if (e == hipSuccess) owned.push_back(*p);
+        return e == hipSuccess;
+    };
+    bool ok = true;
+    if (nw) {
+        ok = alloc(&d_ws, cap_ws);
+        for (int k = 0; k < 2 && ok; k++) {
+            Set& z = sets[k];
+            ok = alloc(&z.out, cap_out) && alloc(&z.hdr, cap_hdr) && alloc(&z.off, (nu_max + 1) * 8) &&
+                 alloc(&z.side, cap_side) &&
+                 (!v4 || (alloc(&z.stored, cap_out) && alloc(&z.rec, nu_max * (uint64_t)ckr::kUnitRecordMax) &&
+                          alloc(&z.plan, nu_max * 24)));
+        }
+        ok = ok && hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) == hipSuccess &&
+             hipEventCreateWithFlags(&ready[0], hipEventDisableTiming) == hipSuccess &&
+             hipEventCreateWithFlags(&ready[1], hipEventDisableTiming) == hipSuccess;
+    }
+    if (!ok) {
+        (void)hipGetLastError();
         release();
         return err(CKR_E_HIP, "[ckr] device allocation for the checkpoint writer failed");
     }
-    int rc = CKR_OK;
-    uint64_t si = 0;
-    for (uint64_t i = 0; i < n && rc == CKR_OK; i++) {
-        const auto& t = tensors[i];
-        if (!t.d_ptr || !t.num_elements) continue;
-        TensorOut o;
-        o.name = t.name ? t.name : "";
-        o.dtype = t.dtype;
-        o.n_elems = t.num_elements;
-        o.original = t.num_elements * (uint64_t)ckr_element_size(t.dtype);
-        o.spe = (uint32_t)ckr_sidecar_bytes_per_elem(t.dtype);
-        const bool singleton = t.cluster_id < 0;
-        auto it = cluster_table.find(t.cluster_id);
-        o.owns = singleton || it == cluster_table.end();
-        ckr_freq_table* tab = &tables[i];
-        const uint64_t ws = ckr_encode_workspace_bytes(t.num_elements, t.dtype, unit_bytes);
-        uint64_t total = 0;
-        uint32_t tsum = CKR_M;
-        if (o.owns) {
-            rc = ckr_compress(t.d_ptr, t.num_elements, t.dtype, unit_bytes, singleton ? 0 : 1, (uint8_t*)d_out, cap_out,
-                              (ckr_stream_header*)d_hdr, (uint64_t*)d_off, (uint8_t*)d_side, d_ws, ws, tab, &total, s);
-            tsum = tab->cum_freq[256];
-            if (rc == CKR_OK && repair_tables && tsum > CKR_M) {
-                repair_table(tab);
-                rc = ckr_encode(t.d_ptr, t.num_elements, t.dtype, tab, unit_bytes, (uint8_t*)d_out, cap_out,
-                                (ckr_stream_header*)d_hdr, (uint64_t*)d_off, (uint8_t*)d_side, d_ws, ws, &total, s);
-            }
-            if (!singleton) cluster_table[t.cluster_id] = tab;
-            o.table = tab;
-        } else {
-            tab = it->second;
-            tsum = tab->cum_freq[256];
-            o.anchor = anchor_name[t.cluster_id];
-            rc = ckr_encode(t.d_ptr, t.num_elements, t.dtype, tab, unit_bytes, (uint8_t*)d_out, cap_out,
-                            (ckr_stream_header*)d_hdr, (uint64_t*)d_off, (uint8_t*)d_side, d_ws, ws, &total, s);
-        }
-        if (rc != CKR_OK) break;
-        const uint64_t nu = ckr_num_units(t.num_elements, t.dtype, unit_bytes);
-        o.data.resize(total);
-        o.headers.resize(nu * 256);
-        o.unit_off.resize(nu + 1);
-        o.sidecar.resize(t.num_elements * o.spe);
-        if (total && hipMemcpyAsync(o.data.data(), d_out, total, hipMemcpyDeviceToHost, s) != hipSuccess) rc = CKR_E_HIP;
-        if (hipMemcpyAsync(o.headers.data(), d_hdr, nu * 256 * 16, hipMemcpyDeviceToHost, s) != hipSuccess) rc = CKR_E_HIP;
-        if (hipMemcpyAsync(o.unit_off.data(), d_off, (nu + 1) * 8, hipMemcpyDeviceToHost, s) != hipSuccess) rc = CKR_E_HIP;
-        if (o.spe && hipMemcpyAsync(o.sidecar.data(), d_side, o.sidecar.size(), hipMemcpyDeviceToHost, s) != hipSuccess)
-            rc = CKR_E_HIP;
-        if (hipStreamSynchronize(s) != hipSuccess) rc = CKR_E_HIP;
-        if (rc != CKR_OK) { err(rc, "[ckr] copy of compressed tensor failed"); break; }
-        if (h_stats) {
-            ckr_ckpt_stats& st = h_stats[si];
-            st.record_index = i;
-            st.original_bytes = o.original;
-            st.ans_bytes = total;
-            st.sidecar_bytes = o.sidecar.size();
-            st.owns_table = o.owns;
-            st.table_sum = tsum;
-            st.table_repaired = (o.owns && repair_tables && tsum > CKR_M) ? 1 : 0;
-        }
-        si++;
-        outs.push_back(std::move(o));
+    std::unique_lock<std::mutex> ring_lock(g_ring.use);
+    if (nw && !g_ring.base && hipHostMalloc(reinterpret_cast<void**>(&g_ring.base), kSlots * kSlotBytes, hipHostMallocDefault) != hipSuccess) {
+        g_ring.base = nullptr;
+        (void)hipGetLastError();
+        release();
+        return err(CKR_E_HIP, "[ckr] pinned staging allocation failed");
     }
+    int device = 0;
+    if (nw) (void)hipGetDevice(&device);
+    const unsigned hw = std::max(2u, std::thread::hardware_concurrency());
+    int rc = CKR_OK;
+    uint64_t data_cursor = 0, meta_cursor = 0;
+    if (nw) {
+        Stager st(g_ring.base, device, cs, (int)std::min(8u, std::max(2u, hw / 2)));
+        for (uint64_t k = 0; k < nw && rc == CKR_OK; k++) {
+            const Item& it = items[k];
+            const auto& t = tensors[it.i];
+            Out& o = outs[k];
+            Set& z = sets[k & 1];
+            if (hipEvent_t prev = st.acquire_set((int)(k & 1))) {
+                if (hipStreamWaitEvent(s, prev, 0) != hipSuccess) { rc = err(CKR_E_HIP, "[ckr] stream wait failed"); break; }
+            }
+            if ((rc = st.status()) != CKR_OK) break;
+            const bool singleton = t.cluster_id < 0;
+            auto cit = cluster_table.find(t.cluster_id);
+            o.owns = singleton || cit == cluster_table.end();
+            ckr_freq_table* tab = &tables[k];
+            const uint64_t ws = ckr_encode_workspace_bytes(t.num_elements, t.dtype, unit_bytes);
+            uint64_t total = 0;
+            uint32_t tsum = CKR_M;
+            if (o.owns) {
+                rc = ckr_compress(t.d_ptr, t.num_elements, t.dtype, unit_bytes, singleton ? 0 : 1, (uint8_t*)z.out,
+                                  cap_out, (ckr_stream_header*)z.hdr, (uint64_t*)z.off, (uint8_t*)z.side, d_ws, ws, tab,
+                                  &total, s);
+                tsum = tab->cum_freq[256];
+                if (rc == CKR_OK && repair_tables && tsum > CKR_M) {
+                    repair_table(tab);
+                    rc = ckr_encode(t.d_ptr, t.num_elements, t.dtype, tab, unit_bytes, (uint8_t*)z.out, cap_out,
+                                    (ckr_stream_header*)z.hdr, (uint64_t*)z.off, (uint8_t*)z.side, d_ws, ws, &total, s);
+                }
+                if (!singleton) cluster_table[t.cluster_id] = tab;
+                o.table = tab;
+            } else {
+                tab = cit->second;
+                tsum = tab->cum_freq[256];
+                o.anchor = anchor_name[t.cluster_id];
+                rc = ckr_encode(t.d_ptr, t.num_elements, t.dtype, tab, unit_bytes, (uint8_t*)z.out, cap_out,
+                                (ckr_stream_header*)z.hdr, (uint64_t*)z.off, (uint8_t*)z.side, d_ws, ws, &total, s);
+            }
+            if (rc != CKR_OK) break;
+            const void* stored = z.out;
+            uint64_t stored_size = total;
+            if (v4) {
+                // unit records and the bytes a unit keeps: sizes, host scan, pack
+                const ckr::UnitGeomArg g{it.n_bytes, std::min(unit_bytes, it.n_bytes), it.nu, it.es, it.spe};
+                const ckr::ZeroLanes zl = ckr::zero_lanes(tab, it.n_bytes, g.unit);
+                uint32_t* d_rs = static_cast<uint32_t*>(z.plan);
+                uint32_t* d_ds = d_rs + it.nu;
+                uint64_t* d_ro = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(z.plan) + it.nu * 8);
+                uint64_t* d_oo = d_ro + it.nu;
+                std::vector<uint32_t> sz(2 * it.nu);
+                hipError_t e = ckr::launch_unit_plan((const ckr_stream_header*)z.hdr, g, zl.arg, d_rs, d_ds, s);
+                if (e == hipSuccess) e = hipMemcpyAsync(sz.data(), d_rs, sz.size() * 4, hipMemcpyDeviceToHost, s);
+                if (e == hipSuccess) e = hipStreamSynchronize(s);
+                if (e != hipSuccess) { rc = err(CKR_E_HIP, std::string("[ckr] unit plan failed: ") + hipGetErrorString(e)); break; }
+                z.rec_off.assign(it.nu, 0);
+                z.out_off.assign(it.nu, 0);
+                uint64_t ra = 0, oa = 0;
+                for (uint64_t u = 0; u < it.nu; u++) {
+                    z.rec_off[u] = ra;
+                    z.out_off[u] = oa;
+                    ra += sz[u];
+                    oa += sz[it.nu + u];
+                }
+                e = hipMemcpyAsync(d_ro, z.rec_off.data(), it.nu * 8, hipMemcpyHostToDevice, s);
+                if (e == hipSuccess) e = hipMemcpyAsync(d_oo, z.out_off.data(), it.nu * 8, hipMemcpyHostToDevice, s);
+                if (e == hipSuccess)
+                    e = ckr::launch_unit_pack((const uint8_t*)z.out, (const uint64_t*)z.off, (const ckr_stream_header*)z.hdr,
+                                              g, zl.arg, d_ro, d_oo, (uint8_t*)z.rec, (uint8_t*)z.stored, s);
+                o.meta.resize(ra);
+                if (e == hipSuccess && ra) e = hipMemcpyAsync(o.meta.data(), z.rec, ra, hipMemcpyDeviceToHost, s);
+                if (e == hipSuccess) e = hipStreamSynchronize(s);
+                if (e != hipSuccess) { rc = err(CKR_E_HIP, std::string("[ckr] unit pack failed: ") + hipGetErrorString(e)); break; }
+                o.raw = it.nu > 0;
+                for (uint64_t u = 0, p = 0; u < it.nu && o.raw; u++) {
+                    o.raw = o.meta[p] == 1;
+                    p += sz[u];
+                }
+                stored = z.stored;
+                stored_size = oa;
+                o.meta_off = meta_cursor;
+                meta_cursor += ra;
+            } else {
+                o.v2_headers.resize(256);
+                if (hipMemcpyAsync(o.v2_headers.data(), z.hdr, 256 * 16, hipMemcpyDeviceToHost, s) != hipSuccess ||
+                    hipStreamSynchronize(s) != hipSuccess) {
+                    rc = err(CKR_E_HIP, "[ckr] copy of stream headers failed");
+                    break;
+                }
+                o.raw = unit_is_raw(o.v2_headers.data(), it.n_bytes);
+            }
+            o.data_off = data_cursor;
+            o.data_size = stored_size;
+            data_cursor += stored_size;
+            if (hipEventRecord(ready[k & 1], s) != hipSuccess) { rc = err(CKR_E_HIP, "[ckr] event record failed"); break; }
+            std::vector<Range> ranges;
+            if (stored_size) ranges.push_back({fs_.fd, data_base + o.data_off, (const uint8_t*)stored, stored_size});
+            if (it.spe) ranges.push_back({fm.fd, mant_base + it.side_off, (const uint8_t*)z.side, t.num_elements * (uint64_t)it.spe});
+            st.submit(std::move(ranges), (int)(k & 1), ready[k & 1]);
+            if (h_stats) {
+                ckr_ckpt_stats& hs = h_stats[k];
+                hs.record_index = it.i;
+                hs.original_bytes = it.n_bytes;
+                hs.ans_bytes = total;
+                hs.sidecar_bytes = t.num_elements * (uint64_t)it.spe;
+                hs.owns_table = o.owns;
+                hs.table_sum = tsum;
+                hs.table_repaired = (o.owns && repair_tables && tsum > CKR_M) ? 1 : 0;
+            }
+        }
+        const int src = st.finish();
+        if (rc == CKR_OK && src != CKR_OK) rc = err(src, st.message());
+    }
+    ring_lock.unlock();
     release();
     if (rc != CKR_OK) return rc;
-    return write_files(fs::path(output_dir), rank, unit_bytes, outs);
+
+    // the small parts: states header, index and (v4) unit records; mantissa
+    // index; tables
+    Buf b;
+    b.u32(kAnscMagic);
+    b.u32(v4 ? 4u : 2u);
+    b.u32(r);
+    b.u32((uint32_t)nw);
+    if (v4) {
+        b.u64(unit_bytes);
+        b.u64(data_base + data_cursor);  // where the unit records begin
+    }
+    for (uint64_t k = 0; k < nw; k++) {
+        const auto& t = tensors[items[k].i];
+        const Out& o = outs[k];
+        b.name(t.name ? t.name : "");
+        b.u8((uint8_t)t.dtype);
+        b.u8(o.raw ? 1 : 0);
+        b.u8(o.owns ? 1 : 0);
+        b.zeros(5);
+        b.u64(items[k].n_bytes);
+        b.u64(t.num_elements);
+        b.u64(o.data_off);
+        b.u64(o.data_size);
+        b.name(o.owns ? std::string() : o.anchor);
+        if (v4) {
+            b.u64(items[k].nu);
+            b.u64(o.meta_off);
+            b.u64(o.meta.size());
+        } else {
+            b.put(o.v2_headers.data(), 256 * 16);
+        }
+    }
+    bool wok = pwrite_all(fs_.fd, b.b.data(), b.b.size(), 0);
+    for (uint64_t k = 0; k < nw && v4 && wok; k++)
+        wok = pwrite_all(fs_.fd, outs[k].meta.data(), outs[k].meta.size(), data_base + data_cursor + outs[k].meta_off);
+    Buf m;
+    m.u32(kMantMagic);
+    m.u32(2u);
+    m.u32(r);
+    m.u32((uint32_t)n_side);
+    for (uint64_t k = 0; k < nw; k++) {
+        if (!items[k].spe) continue;
+        const auto& t = tensors[items[k].i];
+        m.name(t.name ? t.name : "");
+        m.u8((uint8_t)t.dtype);
+        m.u8((uint8_t)items[k].spe);
+        m.zeros(6);
+        m.u64(t.num_elements);
+        m.u64(items[k].side_off);
+        m.u64(t.num_elements * (uint64_t)items[k].spe);
+    }
+    wok = wok && pwrite_all(fm.fd, m.b.data(), m.b.size(), 0);
+    Buf d;
+    uint32_t owners = 0;
+    for (const Out& o : outs) owners += o.owns;
+    d.u32(kDictMagic);
+    d.u32(1u);
+    d.u32(r);
+    d.u32(owners);
+    for (uint64_t k = 0; k < nw; k++) {
+        if (!outs[k].owns) continue;
+        d.name(tensors[items[k].i].name ? tensors[items[k].i].name : "");
+        d.put(outs[k].table->norm_freq, 256 * 4);
+        d.put(outs[k].table->cum_freq, 257 * 4);
+    }
+    wok = wok && pwrite_all(fd_.fd, d.b.data(), d.b.size(), 0);
+    if (!wok) return err(CKR_E_INVALID, std::string("[ckr] write failed in ") + dir.string() + ": " + std::strerror(errno));
+    return CKR_OK;
 }
 
 }  // extern "C"
@@ -501,19 +804,22 @@ int ckr_ckpt_open(const char* dir, int rank, ckr_ckpt** out) {
     std::ifstream f(sp, std::ios::binary);
     if (!f) return err(CKR_E_INVALID, "[ckr] cannot open " + sp.string());
     uint32_t h[4];
-    if (!read_at(f, 0, h, 16) || h[0] != kAnscMagic || (h[1] != 2 && h[1] != 3))
-        return err(CKR_E_CORRUPT, "[ckr] not an .ansc v2/v3 file: " + sp.string());
+    if (!read_at(f, 0, h, 16) || h[0] != kAnscMagic || (h[1] != 2 && h[1] != 4))
+        return err(CKR_E_CORRUPT, "[ckr] not an .ansc v2/v4 file: " + sp.string());
     c->version = h[1];
     c->rank = h[2];
     const uint32_t nt = h[3];
     uint64_t pos = 16;
-    if (c->version == 3) {
-        if (!read_at(f, 16, &c->unit_bytes, 8)) return err(CKR_E_CORRUPT, "[ckr] truncated header");
-        pos = 24;
+    if (c->version == 4) {
+        uint64_t u[2];
+        if (!read_at(f, 16, u, 16)) return err(CKR_E_CORRUPT, "[ckr] truncated header");
+        c->unit_bytes = u[0];
+        c->meta_base = u[1];
+        pos = kV4Header;
+        if (c->unit_bytes == 0 || c->unit_bytes % 256) return err(CKR_E_CORRUPT, "[ckr] bad unit size in " + sp.string());
     }
-    const uint64_t esz = c->version == 3 ? kV3Entry : kV2Entry;
+    const uint64_t esz = c->version == 4 ? kV4Entry : kV2Entry;
     std::vector<uint8_t> buf(esz);
-    uint64_t meta_total = 0;
     for (uint32_t i = 0; i < nt; i++, pos += esz) {
         if (!read_at(f, pos, buf.data(), esz)) return err(CKR_E_CORRUPT, "[ckr] truncated index");
         ckr_ckpt::Entry e;
@@ -527,10 +833,10 @@ int ckr_ckpt_open(const char* dir, int rank, ckr_ckpt** out) {
         std::memcpy(&e.data_off, b + 280, 8);
         std::memcpy(&e.data_size, b + 288, 8);
         e.anchor = cstr(reinterpret_cast<const char*>(b + 296));
-        if (c->version == 3) {
+        if (c->version == 4) {
             std::memcpy(&e.n_units, b + 552, 8);
             std::memcpy(&e.meta_off, b + 560, 8);
-            meta_total += e.n_units * 256 * 16 + (e.n_units + 1) * 8;
+            std::memcpy(&e.meta_size, b + 568, 8);
         } else {
             e.n_units = 1;
             e.v2_headers.resize(256);
@@ -538,8 +844,7 @@ int ckr_ckpt_open(const char* dir, int rank, ckr_ckpt** out) {
         }
         c->entries.push_back(std::move(e));
     }
-    c->meta_base = pos;
-    c->data_base = pos + meta_total;
+    c->data_base = pos;
     // sidecars
     const fs::path mp = c->dir / "mantissa" / (tag + "_mantissa.mant");
     std::ifstream m(mp, std::ios::binary);
@@ -596,7 +901,7 @@ int ckr_ckpt_info(const ckr_ckpt* c, uint64_t i, ckr_ckpt_entry* e) {
     e->num_elements = x.n_elems;
     e->data_size = x.data_size;
     e->n_units = x.n_units;
-    e->unit_bytes = c->version == 3 ? c->unit_bytes : 0;
+    e->unit_bytes = c->version == 4 ? c->unit_bytes : 0;
     const auto s = c->sidecars.find(x.name);
     e->sidecar_bytes = s == c->sidecars.end() ? 0 : s->second.size;
     return CKR_OK;
@@ -613,31 +918,40 @@ int ckr_ckpt_restore(const ckr_ckpt* c, uint64_t i, void* d_dst, void* stream) {
     if (tit == c->tables.end()) return err(CKR_E_CORRUPT, "[ckr] no table for " + x.name);
     ckr_freq_table tab;
     table_from_norm(tit->second.first.data(), tit->second.second.data(), &tab);
-    const uint64_t unit = c->version == 3 ? c->unit_bytes : 0;
+    const uint64_t unit = c->version == 4 ? c->unit_bytes : 0;
     const uint64_t nu = ckr_num_units(x.n_elems, x.dtype, unit);
     if (nu != x.n_units) return err(CKR_E_CORRUPT, "[ckr] unit count mismatch for " + x.name);
     const fs::path sp = c->dir / ("rank_" + std::to_string(c->rank) + "_states.ansc");
     std::error_code fec;
     const uint64_t fsize = fs::file_size(sp, fec);
-    if (fec || nu > fsize / 4096 + 1 || x.data_size > fsize)
+    // every unit has a record of at least one byte (v4); sizes within the file
+    if (fec || x.data_size > fsize || x.meta_size > fsize || (c->version == 4 && nu > x.meta_size))
         return err(CKR_E_CORRUPT, "[ckr] entry " + x.name + " does not fit its file");
     std::ifstream f(sp, std::ios::binary);
-    std::vector<ckr_stream_header> hdr(nu * 256);
-    std::vector<uint64_t> uoff(nu + 1);
-    if (c->version == 3) {
-        if (!read_at(f, c->meta_base + x.meta_off, hdr.data(), hdr.size() * 16) ||
-            !read_at(f, c->meta_base + x.meta_off + hdr.size() * 16, uoff.data(), uoff.size() * 8))
-            return err(CKR_E_CORRUPT, "[ckr] truncated unit metadata for " + x.name);
-    } else {
-        hdr = x.v2_headers;
-        uoff[0] = 0;
-        uoff[1] = x.data_size;
-    }
-    if (int rc = check_unit_metadata(hdr, uoff, nu, x.original, unit ? unit : x.original, x.data_size, x.name))
-        return rc;
+    std::vector<ckr_stream_header> hdr;
+    std::vector<uint64_t> uoff;
     std::vector<uint8_t> data(std::max<uint64_t>(x.data_size, 1));
     if (x.data_size && !read_at(f, c->data_base + x.data_off, data.data(), x.data_size))
         return err(CKR_E_CORRUPT, "[ckr] truncated data for " + x.name);
+    const uint64_t ulen = unit ? std::min(unit, x.original) : x.original;
+    if (c->version == 4) {
+        std::vector<uint8_t> meta(std::max<uint64_t>(x.meta_size, 1));
+        if (!read_at(f, c->meta_base + x.meta_off, meta.data(), x.meta_size))
+            return err(CKR_E_CORRUPT, "[ckr] truncated unit records for " + x.name);
+        const ckr::ZeroLanes zl = ckr::zero_lanes(&tab, x.original, ulen);
+        std::vector<uint8_t> full;
+        std::string why;
+        if (ckr::expand_units(meta.data(), x.meta_size, data.data(), x.data_size, x.original, ulen, es, (int)spe, zl,
+                              hdr, uoff, full, why) != CKR_OK)
+            return err(CKR_E_CORRUPT, "[ckr] corrupt unit records for " + x.name + ": " + why);
+        data.swap(full);
+        if (data.empty()) data.resize(1);
+    } else {
+        hdr = x.v2_headers;
+        uoff = {0, x.data_size};
+    }
+    const uint64_t full_size = uoff.empty() ? 0 : uoff.back();
+    if (int rc = check_unit_metadata(hdr, uoff, nu, x.original, ulen, full_size, x.name)) return rc;
     std::vector<uint8_t> side;
     if (spe) {
         const auto sit = c->sidecars.find(x.name);

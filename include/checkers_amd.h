@@ -295,10 +295,18 @@ CKR_API int ckr_cluster(const char* const* names, const float* h_fp, uint64_t n,
  * rank_<r>_mantissa.mant and <dir>/tables/rank_<r>_tables.dict.
  * unit_bytes 0: the reference's .ansc v2 (one stream per tensor, byte for byte
  * the reference's files; tensors must be below 4 GiB).  unit_bytes > 0: .ansc
- * v3, this library's chunked layout: header {magic, 3, rank, n, u64 unit_bytes},
- * 568-byte index entries (the v2 entry without its headers, then u64 n_units,
- * u64 meta_offset), a metadata section (per tensor: n_units*256 headers, then
- * n_units+1 u64 unit offsets), then the data.  repair_tables != 0 repairs a
+ * v4, this library's chunked layout: header {magic, 4, rank, n, u64 unit_bytes,
+ * u64 records_offset}, 576-byte index entries (the v2 entry without its
+ * headers, then u64 n_units, u64 records offset, u64 records size), the stored
+ * bytes of every tensor, then the unit records.  A unit record replaces the
+ * unit's 256 lane headers: a raw unit is one byte; a coded unit keeps its live
+ * lanes' final states (31 bits) and byte counts (as bit-packed deltas from the
+ * least count of each byte plane), while the lanes of masked-out byte planes,
+ * whose streams the table and the unit length determine, are stored neither
+ * as headers nor as bytes (ckr_container.hip gives the exact layout).  Writes
+ * stream: tensor k+1 is encoded while tensor k goes to the files through a
+ * pinned host ring (8 x 32 MiB, allocated on first use and kept; calls
+ * serialise on it) and writer threads.  repair_tables != 0 repairs a
  * full-alphabet table that the reference's one-pass normalisation leaves above
  * 4096 (such streams cannot be decoded) — a deliberate divergence, reported in
  * h_stats.  h_stats (optional) gets one entry per written tensor. */
@@ -325,7 +333,7 @@ CKR_API int ckr_ckpt_write(const char* output_dir, int rank, const ckr_ckpt_tens
                            uint64_t unit_bytes, int repair_tables, ckr_ckpt_stats* h_stats, void* stream);
 
 /* Reader (no counterpart in the reference): parses the three files of a rank
- * (v2 or v3 states file) and restores any tensor, bit-exact, into device
+ * (v2 or v4 states file) and restores any tensor, bit-exact, into device
  * memory.  A tensor whose table does not sum to 4096 cannot be restored
  * (CKR_E_TABLE). */
 typedef struct ckr_ckpt ckr_ckpt;

@@ -144,33 +144,54 @@ def test_repaired_tables_restore_everything(gpu, tmp_path, unit):
     assert len(c) == len(live)
     for i, (name, arr, tag, cid) in enumerate(live):
         info = c.info(i)
-        assert info["version"] == (3 if unit else 2) and info["num_elements"] == arr.size
+        assert info["version"] == (4 if unit else 2) and info["num_elements"] == arr.size
         out = c.restore(i).cpu().numpy()
         assert np.array_equal(out, np.ascontiguousarray(arr).view(np.uint8).reshape(-1)), name
 
 
-def test_v3_streams_match_oracle_units(gpu, tmp_path):
-    # the v3 data section holds, per tensor, exactly the oracle's chunked stream
+@pytest.mark.parametrize("unit", [65536, 4096])
+def test_v4_records_and_stored_bytes_match_oracle_units(gpu, tmp_path, unit):
+    """The v4 states file holds, per tensor, the unit records and stored bytes
+    that the Python restatement of the format (tests/ckpt_format.py) makes of
+    the oracle's chunked streams."""
+    from tests import ckpt_format as cf
     ck = _ck()
-    recs = [("a", dg.normal_f32(70000, 1e-3, 9), dg.F32, -1), ("b", dg.normal_bf16(50001, 0.02, 10), dg.BF16, -1)]
-    _write(ck, gpu, recs, tmp_path, 1, 65536)
+    recs = [("a", dg.normal_f32(70000, 1e-3, 9), dg.F32, -1), ("b", dg.normal_bf16(50001, 0.02, 10), dg.BF16, -1),
+            ("c", dg.exp_avg_sq(33333, 11), dg.F32, -1),
+            ("d", np.random.default_rng(12).integers(0, 256, 360000).astype(np.uint8).view(np.int8), dg.I8, -1),
+            # a cluster whose full-alphabet table sums to 4096; its member of
+            # random bytes expands under that table, so its units pass through raw
+            ("e", np.random.default_rng(13).integers(-100, 100, 50000).astype(np.int8), dg.I8, 0),
+            ("f", np.random.default_rng(14).integers(0, 256, 100000).astype(np.uint8).view(np.int8), dg.I8, 0)]
+    _write(ck, gpu, recs, tmp_path, 1, unit)
     blob = open(os.path.join(tmp_path, "rank_1_states.ansc"), "rb").read()
-    magic, ver, rank, n, unit = struct.unpack_from("<4IQ", blob, 0)
-    assert (magic, ver, rank, n, unit) == (0x414E5343, 3, 1, 2, 65536)
-    pos, metas = 24, []
-    for _ in range(n):
-        dsz, = struct.unpack_from("<Q", blob, pos + 288)
-        doff, = struct.unpack_from("<Q", blob, pos + 280)
-        nu, moff = struct.unpack_from("<2Q", blob, pos + 552)
-        metas.append((doff, dsz, nu, moff))
-        pos += 568
-    meta_base = pos
-    data_base = meta_base + sum(nu * 4096 + (nu + 1) * 8 for _, _, nu, _ in metas)
-    for (doff, dsz, nu, moff), (name, arr, tag, cid) in zip(metas, recs):
+    magic, ver, rank, n, u, meta_base = struct.unpack_from("<4I2Q", blob, 0)
+    assert (magic, ver, rank, n, u) == (0x414E5343, 4, 1, len(recs), unit)
+    data_base = 32 + 576 * n
+    total_stored, tables = 0, {}
+    for k, (name, arr, tag, cid) in enumerate(recs):
+        e = 32 + 576 * k
+        doff, dsz = struct.unpack_from("<2Q", blob, e + 280)
+        nu, moff, msz = struct.unpack_from("<3Q", blob, e + 552)
         raw = np.ascontiguousarray(arr).view(np.uint8).reshape(-1)
-        ref = oc.compress_tensor(raw, arr.size, tag, 65536)
-        assert nu == oc.num_units(raw.size, 65536)
-        assert blob[meta_base + moff: meta_base + moff + nu * 4096] == ref["headers"].tobytes()
-        uo = np.frombuffer(blob, np.uint64, nu + 1, meta_base + moff + nu * 4096)
-        assert np.array_equal(uo, ref["unit_offsets"])
-        assert blob[data_base + doff: data_base + doff + dsz] == ref["data"].tobytes()
+        masked, _ = oc.extract_mantissa(raw, arr.size, tag)
+        if cid < 0 or cid not in tables:
+            table, tsum = oc.normalize_histogram(oc.byte_hist(masked), cid >= 0)
+            assert tsum == 4096
+            tables.setdefault(cid, table)
+        table = tables[cid] if cid >= 0 else table
+        data, hdr, uoff = oc.encode(masked, table, unit)
+        assert nu == oc.num_units(raw.size, unit)
+        rec, stored = cf.pack_tensor(hdr, uoff, data.tobytes(), raw.size, unit, oc.ES[tag], oc.SPE[tag],
+                                     int(table["norm_freq"][0]))
+        assert blob[meta_base + moff: meta_base + moff + msz] == rec, name
+        assert blob[data_base + doff: data_base + doff + dsz] == stored, name
+        assert blob[e + 257] == (rec == b"\x01" * nu)     # raw: every unit passed through
+        assert name != "f" or rec[:1] == b"\x01"      # the raw-unit path is exercised
+        total_stored += dsz
+    assert meta_base == data_base + total_stored
+    c = ck.Checkpoint(str(tmp_path), 1)
+    for i, (name, arr, tag, cid) in enumerate(recs):
+        out = c.restore(i).cpu().numpy()
+        assert np.array_equal(out, np.ascontiguousarray(arr).view(np.uint8).reshape(-1)), name
+    c.close()
