@@ -20,6 +20,12 @@ buffers (slices end on unit boundaries, and units are independent given the
 table, so each slice's units are the whole-tensor encode's), each decoded into
 a reused window and compared with its source outside the timed regions.
 
+After the timed steps, the drop-in path runs end to end once per repetition:
+checkers_py.initialize_context / analyze_tensors / compress_and_save on a
+stand-in engine over the resident shard, writing the rank's files (v4, same
+unit size) to a temporary directory; `compress_and_save` reports its wall time
+and `container_ratio` is the shard's bytes over the bytes of those files.
+
 Usage: python bench.py [--steps K] [--warmup W] [--config 3] [--unit 65536]
 """
 import argparse
@@ -169,6 +175,66 @@ def cpu_baseline(shard, ck, sample_bytes_per_tensor, unit, reps=5):
                                    seconds=round(sec1, 4), runs_s=all_t1))
 
 
+class _ZeroParam:
+    """A ZeRO-3 parameter as api.cpp reads it: requires_grad and ds_numel."""
+
+    def __init__(self, n):
+        self.requires_grad = True
+        self.ds_numel = n
+
+
+def save_leg(shard, torch, unit, reps=2):
+    """End to end through the pybind drop-in: initialize_context on a stand-in
+    engine holding the resident shard, analyze_tensors, then compress_and_save
+    into a fresh directory (v4 states file with `unit`-byte units), timed on the
+    wall clock from the call to its return with every file written.  cfg3's
+    four tensors are one ZeRO-3 flat group (fp16 flat = params, fp32 flat =
+    master, optimizer state = exp_avg, exp_avg_sq); other configs are plain
+    parameters."""
+    import shutil
+    import tempfile
+    import types
+
+    import checkers_py
+    named = dict(shard)
+    if set(named) == {"params_bf16", "master_weights", "exp_avg", "exp_avg_sq"}:
+        n = named["master_weights"].numel()
+        p = _ZeroParam(n)
+        opt = types.SimpleNamespace(
+            fp16_partitioned_groups_flat=[named["params_bf16"]], fp32_partitioned_groups_flat=[named["master_weights"]],
+            optimizer=types.SimpleNamespace(state={named["master_weights"]: {"exp_avg": named["exp_avg"],
+                                                                            "exp_avg_sq": named["exp_avg_sq"]}}),
+            grad_position={id(p): [0, 0, n]}, get_param_id=id)
+        params = [("layers.flat", p)]
+    else:
+        opt, params = None, list(shard)
+    eng = types.SimpleNamespace(module=types.SimpleNamespace(named_parameters=lambda: iter(params)),
+                                optimizer=opt, global_rank=0)
+    os.environ["CHECKERS_UNIT_BYTES"] = str(unit)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    checkers_py.initialize_context(eng)
+    t_init = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    checkers_py.analyze_tensors()
+    t_an = time.perf_counter() - t0
+    times, files = [], 0
+    for r in range(reps):
+        d = tempfile.mkdtemp(prefix="ckr_bench_")
+        try:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            checkers_py.compress_and_save(d)
+            times.append(time.perf_counter() - t0)
+            files = sum(os.path.getsize(os.path.join(a, f)) for a, _, fs in os.walk(d) for f in fs)
+        finally:
+            shutil.rmtree(d, ignore_errors=True)
+        log(f"[bench] compress_and_save {r + 1}/{reps}: {times[-1]:.3f} s, {files / 1e9:.3f} GB of files")
+    return dict(seconds=[round(t, 4) for t in times], best_s=round(min(times), 4), file_bytes=files,
+                initialize_context_s=round(t_init, 4), analyze_tensors_s=round(t_an, 4), unit_bytes=unit,
+                records=4 if opt is not None else len(params))
+
+
 def stream_bench(shard, ck, torch, dev, unit, steps, slice_bytes):
     """Config 5: histogram + table per tensor, then encode/decode slice by slice
     (reused buffers), every slice checked bit-exact against its source.
@@ -232,6 +298,7 @@ def main():
     ap.add_argument("--sequential", action="store_true", help="one ckr_compress per tensor, no overlap")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
+    ap.add_argument("--no-save", action="store_true", help="skip the end-to-end compress_and_save leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device-to-device copy (known HBM traffic) for counter scaling")
     args = ap.parse_args()
@@ -366,6 +433,12 @@ def main():
             if k in prof:
                 kernels[k]["achieved_GBps"] = round(alg[k] / (prof[k][1] / 1e3) / 1e9, 2)
 
+    save = None
+    if not args.no_save:
+        res = r2 = None
+        save = save_leg(shard, torch, unit)
+        save["GBps"] = round(n_in / save["best_s"] / 1e9, 3)
+
     cpu = None
     if not args.no_cpu:
         log("[bench] cpu baseline")
@@ -404,8 +477,10 @@ def main():
         "header_bytes": H,
         "ans_ratio": round(n_in / C, 4),
         "disk_ratio": round(n_in / (C + S), 4),
-        "container_ratio": round(n_in / (C + S + H), 4),
+        "device_ratio": round(n_in / (C + S + H), 4),
+        "container_ratio": round(n_in / save["file_bytes"], 4) if save else None,
         "roundtrip_bit_exact": ok,
+        "compress_and_save": save,
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernels": kernels,

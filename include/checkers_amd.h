@@ -305,8 +305,8 @@ CKR_API int ckr_cluster(const char* const* names, const float* h_fp, uint64_t n,
  * whose streams the table and the unit length determine, are stored neither
  * as headers nor as bytes (ckr_container.hip gives the exact layout).  Writes
  * stream: tensor k+1 is encoded while tensor k goes to the files through a
- * pinned host ring (8 x 32 MiB, allocated on first use and kept; calls
- * serialise on it) and writer threads.  repair_tables != 0 repairs a
+ * pinned host ring (16 x 32 MiB by default, CKR_CKPT_SLOTS; allocated on first
+ * use and kept; calls serialise on it) and writer threads (CKR_CKPT_WRITERS).  repair_tables != 0 repairs a
  * full-alphabet table that the reference's one-pass normalisation leaves above
  * 4096 (such streams cannot be decoded) — a deliberate divergence, reported in
  * h_stats.  h_stats (optional) gets one entry per written tensor. */
