@@ -25,6 +25,8 @@ checkers_py.initialize_context / analyze_tensors / compress_and_save on a
 stand-in engine over the resident shard, writing the rank's files (v4, same
 unit size) to a temporary directory; `compress_and_save` reports its wall time
 and `container_ratio` is the shard's bytes over the bytes of those files.
+`analyze` times ckr_analyze on the shard (one call, one record per tensor) and
+`repair` cfg2's per-tensor prefix-mask repair build and apply.
 
 Usage: python bench.py [--steps K] [--warmup W] [--config 3] [--unit 65536]
 """
@@ -235,6 +237,80 @@ def save_leg(shard, torch, unit, reps=2):
                 records=4 if opt is not None else len(params))
 
 
+def analyzer_leg(shard, ck, torch, steps):
+    """ckr_analyze on the shard: one call with one record per tensor, timed with
+    HIP events on the stream it runs on, then one profiled call for the
+    per-kernel times.  Rooflines: B = n_in (the data read once, the bound of
+    any statistics pass) and 2 n_in (what the two passes read: min/max and the
+    sums, then histogram and central moments)."""
+    an = ck.Analyzer([t for _, t in shard], [ck.torch_tag(t.dtype) for _, t in shard], bins=256)
+    n_in = sum(t.numel() * t.element_size() for _, t in shard)
+    for _ in range(2):
+        an.run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        an.run()
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) / 1e3 / steps
+    ck.profile_begin()
+    an.run()
+    prof = ck.profile_end()
+    kern = {k: dict(launches=c, total_ms=round(ms, 4)) for k, (c, ms) in prof.items()}
+    passes = sum(prof[k][1] for k in ("stats_pass1_kernel", "stats_pass2_kernel") if k in prof) / 1e3
+    for k in ("stats_pass1_kernel", "stats_pass2_kernel"):
+        if k in prof:
+            kern[k]["achieved_GBps"] = round(n_in / (prof[k][1] / 1e3) / 1e9, 2)
+    log(f"[bench] analyze {t * 1e3:.3f} ms per call ({len(shard)} records)")
+    return dict(ms=round(t * 1e3, 4), records=len(shard), input_bytes=n_in, GBps=round(n_in / t / 1e9, 2),
+                roofline=dict(bound="hbm", kernel="stats_pass1_kernel + stats_pass2_kernel", peak=HBM_PEAK_GBPS,
+                              unit="GB/s", achieved=round(n_in / t / 1e9, 2),
+                              frac=round(n_in / t / 1e9 / HBM_PEAK_GBPS, 4),
+                              achieved_two_pass=round(2 * n_in / t / 1e9, 2),
+                              frac_two_pass=round(2 * n_in / t / 1e9 / HBM_PEAK_GBPS, 4),
+                              passes_ms=round(passes * 1e3, 4)),
+                kernels=kern)
+
+
+def repair_leg(ck, torch, dev):
+    """cfg2's prefix-mask repair, per tensor (the group is the tensor): the
+    grammar build (at most 50 rounds, all 7 bf16 mantissa bits masked), then
+    applying it again, each timed on the wall clock around its call (the build
+    returns its rules to the host, so the call is complete when it returns).
+    Roofline per SURVEY's measure for this row: B = n_in per round."""
+    shard = make_shard(2, torch, dev)
+    out, tot_b, tot_a, tot_bytes_rounds = [], 0.0, 0.0, 0
+    n_max = max(t.numel() for _, t in shard)
+    rp = ck.Repairer(n_max, ck.BF16, max_rules=50, device=dev)
+    for name, t in shard:
+        src = t.view(torch.uint8)
+        rp.build(src)   # warm-up (first-use allocations, code paths)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        r = rp.build(src)
+        tb = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        n_tok = rp.apply(src, r["rules"])
+        ta = time.perf_counter() - t0
+        assert n_tok == r["out_len"]
+        rounds = len(r["rules"]) + (1 if len(r["rules"]) < 50 else 0)
+        nb = t.numel() * t.element_size()
+        tot_b += tb
+        tot_a += ta
+        tot_bytes_rounds += rounds * nb
+        out.append(dict(tensor=name, elements=t.numel(), rules=len(r["rules"]), rounds=rounds, tokens=r["out_len"],
+                        build_ms=round(tb * 1e3, 3), apply_ms=round(ta * 1e3, 3)))
+    log(f"[bench] repair cfg2: build {tot_b * 1e3:.1f} ms, apply {tot_a * 1e3:.1f} ms over {len(shard)} tensors")
+    ach = tot_bytes_rounds / tot_b / 1e9
+    return dict(workload="cfg2 llama3-8b decoder layer bf16, group = each tensor, 50 rules", tensors=out,
+                build_ms=round(tot_b * 1e3, 3), apply_ms=round(tot_a * 1e3, 3),
+                roofline=dict(bound="hbm", kernel="repair build (all rounds)", unit="GB/s", peak=HBM_PEAK_GBPS,
+                              achieved=round(ach, 2), frac=round(ach / HBM_PEAK_GBPS, 4),
+                              algorithmic_bytes=tot_bytes_rounds))
+
+
 def stream_bench(shard, ck, torch, dev, unit, steps, slice_bytes):
     """Config 5: histogram + table per tensor, then encode/decode slice by slice
     (reused buffers), every slice checked bit-exact against its source.
@@ -299,6 +375,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-save", action="store_true", help="skip the end-to-end compress_and_save leg")
+    ap.add_argument("--no-analyze", action="store_true", help="skip the analyzer leg")
+    ap.add_argument("--no-repair", action="store_true", help="skip cfg2's prefix-mask repair leg")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device-to-device copy (known HBM traffic) for counter scaling")
     args = ap.parse_args()
@@ -433,6 +511,9 @@ def main():
             if k in prof:
                 kernels[k]["achieved_GBps"] = round(alg[k] / (prof[k][1] / 1e3) / 1e9, 2)
 
+    analyze = None if args.no_analyze else analyzer_leg(shard, ck, torch, args.steps)
+    repair = None if args.no_repair else repair_leg(ck, torch, dev)
+
     save = None
     if not args.no_save:
         res = r2 = None
@@ -481,6 +562,8 @@ def main():
         "container_ratio": round(n_in / save["file_bytes"], 4) if save else None,
         "roundtrip_bit_exact": ok,
         "compress_and_save": save,
+        "analyze": analyze,
+        "repair": repair,
         "roofline": roof,
         "cpu_baseline": cpu,
         "kernels": kernels,

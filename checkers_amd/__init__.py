@@ -424,40 +424,53 @@ def decode_noalloc(enc, dst, stream=None, check=True):
     return bad.value if check else None
 
 
+class Analyzer:
+    """ckr_analyze over a fixed list of device tensors, with its outputs and
+    workspace allocated once: run() enqueues the statistics pass on the stream
+    (no synchronisation), results() waits and copies them to the host."""
+
+    def __init__(self, tensors, tags, bins=256):
+        torch = _torch()
+        n = len(tensors)
+        dev = tensors[0].device if n else "cuda"
+        self.n, self.nb = n, min(bins, 256)
+        self.hist = torch.zeros((max(n, 1), max(self.nb, 1)), dtype=torch.int32, device=dev)
+        self.mom = torch.zeros((max(n, 1), 4), dtype=torch.float32, device=dev)
+        self.mm = torch.zeros((max(n, 1), 2), dtype=torch.float32, device=dev)
+        self.fp = torch.zeros((max(n, 1), 5), dtype=torch.float32, device=dev)
+        self.tensors = list(tensors)
+        self.recs = (StatsRecord * max(n, 1))()
+        for i, (t, tag) in enumerate(zip(tensors, tags)):
+            ne = _n_elems(t, tag, None)
+            self.recs[i].d_ptr = t.data_ptr() if ne else None
+            self.recs[i].num_elements = ne
+            self.recs[i].histogram_bins = bins
+            self.recs[i].data_type = tag
+            self.recs[i].d_histogram = self.hist[i].data_ptr()
+            self.recs[i].d_raw_moments = self.mom[i].data_ptr()
+            self.recs[i].d_minmax = self.mm[i].data_ptr()
+            self.recs[i].d_fingerprint = self.fp[i].data_ptr()
+        self.wsb = int(lib().ckr_analyze_workspace_bytes(self.recs, n))
+        self.ws = _empty(self.wsb, dev)
+
+    def run(self, stream=None):
+        _check(lib().ckr_analyze(self.recs, self.n, self.ws.data_ptr(), self.wsb, _stream(stream)))
+
+    def results(self):
+        _torch().cuda.synchronize()
+        return [dict(histogram=self.hist[i, :self.nb].cpu().numpy().view(np.uint32).copy(),
+                     moments=self.mom[i].cpu().numpy().copy(), minmax=self.mm[i].cpu().numpy().copy(),
+                     fingerprint=self.fp[i].cpu().numpy().copy()) for i in range(self.n)]
+
+
 def analyze(tensors, tags, bins=256, stream=None):
     """TensorAnalyzer statistics for a list of device tensors.
 
     Returns a list of dicts with histogram (np.uint32), moments (mean, var,
     skew, kurt), minmax and fingerprint, all copied to the host."""
-    torch = _torch()
-    n = len(tensors)
-    dev = tensors[0].device if n else "cuda"
-    nb = min(bins, 256)
-    hist = torch.zeros((max(n, 1), max(nb, 1)), dtype=torch.int32, device=dev)
-    mom = torch.zeros((max(n, 1), 4), dtype=torch.float32, device=dev)
-    mm = torch.zeros((max(n, 1), 2), dtype=torch.float32, device=dev)
-    fp = torch.zeros((max(n, 1), 5), dtype=torch.float32, device=dev)
-    recs = (StatsRecord * max(n, 1))()
-    for i, (t, tag) in enumerate(zip(tensors, tags)):
-        ne = _n_elems(t, tag, None)
-        recs[i].d_ptr = t.data_ptr() if ne else None
-        recs[i].num_elements = ne
-        recs[i].histogram_bins = bins
-        recs[i].data_type = tag
-        recs[i].d_histogram = hist[i].data_ptr()
-        recs[i].d_raw_moments = mom[i].data_ptr()
-        recs[i].d_minmax = mm[i].data_ptr()
-        recs[i].d_fingerprint = fp[i].data_ptr()
-    wsb = int(lib().ckr_analyze_workspace_bytes(recs, n))
-    ws = _empty(wsb, dev)
-    _check(lib().ckr_analyze(recs, n, ws.data_ptr(), wsb, _stream(stream)))
-    torch.cuda.synchronize()
-    out = []
-    for i in range(n):
-        out.append(dict(histogram=hist[i, :nb].cpu().numpy().view(np.uint32).copy(),
-                        moments=mom[i].cpu().numpy().copy(), minmax=mm[i].cpu().numpy().copy(),
-                        fingerprint=fp[i].cpu().numpy().copy()))
-    return out
+    a = Analyzer(tensors, tags, bins)
+    a.run(stream)
+    return a.results()
 
 
 # ---- tensor-group prefix-mask repair

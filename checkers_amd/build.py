@@ -17,7 +17,7 @@ LIB = os.path.join(HERE, "libcheckers_amd.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = ["ckr_kernels.hip", "ckr_repair.hip", "ckr_api.cpp", "ckr_checkpoint.cpp", "ckr_context.hip",
-           "ckr_container.hip"]
+           "ckr_container.hip", "ckr_analyzer.hip"]
 
 # -packed-fp32-ops: no v_pk_*_f32 generated anywhere (wrong results seen with
 # some of their forms on these machines).

@@ -1232,39 +1232,24 @@ int ckr_decode_noalloc(const uint8_t* d_data, const ckr_stream_header* d_headers
 }
 
 // ---- analyzer: per record [p1 nblk][p2 nblk][params][hist partial nblk*256]
-static uint64_t stats_record_bytes(uint32_t nblk) {
-    return align_up(nblk * sizeof(ckr::StatsPartial1), kAlign) + align_up(nblk * sizeof(ckr::StatsPartial2), kAlign) +
-           align_up(sizeof(ckr::StatsParams), kAlign) + align_up((uint64_t)nblk * 256 * 4, kAlign);
-}
-
 uint64_t ckr_analyze_workspace_bytes(const ckr_stats_record* recs, uint64_t n) {
-    uint64_t tot = 0;
-    for (uint64_t i = 0; i < n; i++) tot += stats_record_bytes(ckr::stats_num_blocks(recs[i].num_elements));
-    return tot;
+    if (n && !recs) return 0;
+    return ckr::analyze_workspace_bytes(recs, n);
 }
 
 int ckr_analyze(const ckr_stats_record* recs, uint64_t n, void* d_workspace, uint64_t workspace_bytes, void* stream) {
     if (n && !recs) return fail(CKR_E_INVALID, "[ckr] null records");
     const uint64_t need = ckr_analyze_workspace_bytes(recs, n);
     if (need && (!d_workspace || workspace_bytes < need)) return fail(CKR_E_CAPACITY, "[ckr] analyze workspace too small");
-    uint8_t* ws = static_cast<uint8_t*>(d_workspace);
-    hipStream_t s = (hipStream_t)stream;
     for (uint64_t i = 0; i < n; i++) {
         const ckr_stats_record& r = recs[i];
-        const uint32_t nblk = ckr::stats_num_blocks(r.num_elements);
-        uint8_t* base = ws;
-        ws += stats_record_bytes(nblk);
-        if (!r.d_ptr || r.num_elements == 0) continue;  // TensorAnalyzer.cpp:68
-        if (!dtype_ok((int)r.data_type)) continue;       // tensor_stats_kernel default branch
-        auto* p1 = reinterpret_cast<ckr::StatsPartial1*>(base);
-        base += align_up(nblk * sizeof(ckr::StatsPartial1), kAlign);
-        auto* p2 = reinterpret_cast<ckr::StatsPartial2*>(base);
-        base += align_up(nblk * sizeof(ckr::StatsPartial2), kAlign);
-        auto* prm = reinterpret_cast<ckr::StatsParams*>(base);
-        base += align_up(sizeof(ckr::StatsParams), kAlign);
-        auto* hp = reinterpret_cast<uint32_t*>(base);
-        CKR_HIP(ckr::launch_stats(r, nblk, p1, p2, prm, hp, s));
+        if (!r.d_ptr || !r.num_elements || !dtype_ok((int)r.data_type)) continue;  // skipped, as the reference does
+        const int es = ckr_element_size((int)r.data_type);
+        if (reinterpret_cast<uintptr_t>(r.d_ptr) % (uintptr_t)es)
+            return fail(CKR_E_INVALID, "[ckr] record %llu: data pointer not aligned to its element size",
+                        (unsigned long long)i);
     }
+    CKR_HIP(ckr::launch_analyze(recs, n, d_workspace, (hipStream_t)stream));
     return CKR_OK;
 }
 

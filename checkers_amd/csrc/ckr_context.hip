@@ -66,6 +66,21 @@ __global__ void __launch_bounds__(256) gather_kernel(const T* __restrict__ src, 
     }
 }
 
+std::vector<ckr_stats_record> stats_records(const ckr_device_tensor_record* h_recs, uint64_t n) {
+    std::vector<ckr_stats_record> r(n);
+    for (uint64_t i = 0; i < n; i++) {
+        r[i].d_ptr = h_recs[i].d_ptr;
+        r[i].num_elements = h_recs[i].num_elements;
+        r[i].histogram_bins = h_recs[i].histogram_bins;
+        r[i].data_type = h_recs[i].data_type;
+        r[i].d_histogram = h_recs[i].d_histogram;
+        r[i].d_raw_moments = h_recs[i].d_raw_moments;
+        r[i].d_minmax = h_recs[i].d_minmax;
+        r[i].d_fingerprint = h_recs[i].d_fingerprint;
+    }
+    return r;
+}
+
 }  // namespace
 
 extern "C" {
@@ -140,24 +155,13 @@ int ckr_carve_stats_slab(void* d_slab, uint32_t histogram_bins, uint64_t alignme
 int ckr_analyze_device_records(const ckr_device_tensor_record* h_recs, uint64_t n, void* d_workspace,
                                uint64_t workspace_bytes, void* stream) {
     if (n && !h_recs) return err(CKR_E_INVALID, "[ckr] null records");
-    std::vector<ckr_stats_record> r(n);
-    for (uint64_t i = 0; i < n; i++) {
-        r[i].d_ptr = h_recs[i].d_ptr;
-        r[i].num_elements = h_recs[i].num_elements;
-        r[i].histogram_bins = h_recs[i].histogram_bins;
-        r[i].data_type = h_recs[i].data_type;
-        r[i].d_histogram = h_recs[i].d_histogram;
-        r[i].d_raw_moments = h_recs[i].d_raw_moments;
-        r[i].d_minmax = h_recs[i].d_minmax;
-        r[i].d_fingerprint = h_recs[i].d_fingerprint;
-    }
+    const std::vector<ckr_stats_record> r = stats_records(h_recs, n);
     return ckr_analyze(r.data(), n, d_workspace, workspace_bytes, stream);
 }
 
 uint64_t ckr_analyze_device_records_workspace_bytes(const ckr_device_tensor_record* h_recs, uint64_t n) {
     if (n && !h_recs) return 0;
-    std::vector<ckr_stats_record> r(n);
-    for (uint64_t i = 0; i < n; i++) r[i].num_elements = h_recs[i].num_elements;
+    const std::vector<ckr_stats_record> r = stats_records(h_recs, n);
     return ckr_analyze_workspace_bytes(r.data(), n);
 }
 

@@ -127,7 +127,7 @@ hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, con
                          const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
                          unsigned long long* bad, const uint32_t* canon, uint32_t cw, hipStream_t s);
 
-// Analyzer.
+// Analyzer (ckr_analyzer.hip): every record in one grid per pass.
 struct StatsParams {     // per record, device resident between passes
     float smin, smax, mean, scale;
     uint32_t use_range;  // range > 1e-9f
@@ -136,10 +136,8 @@ struct StatsParams {     // per record, device resident between passes
 };
 struct StatsPartial1 { float mn, mx; double sum; };
 struct StatsPartial2 { double m2, m3, m4, pad; };
-uint32_t stats_num_blocks(uint64_t n);
-hipError_t launch_stats(const ckr_stats_record& r, uint32_t nblk, StatsPartial1* p1,
-                        StatsPartial2* p2, StatsParams* prm, uint32_t* hist_partial,
-                        hipStream_t s);
+uint64_t analyze_workspace_bytes(const ckr_stats_record* recs, uint64_t n);
+hipError_t launch_analyze(const ckr_stats_record* recs, uint64_t n, void* ws, hipStream_t s);
 
 // Prefix-mask repair (ckr_repair.hip).
 struct RepairCtl {

@@ -2518,151 +2518,4 @@ hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, con
     return hipGetLastError();
 }
 
-// ------------------------------------------------------------------ analyzer
-// compute_tensor_stats<T> (TensorAnalyzer.cpp:64-198) spread over many blocks.
-// min/max are exact whatever the order; the histogram is bit-exact given them
-// (scale rounded once from an fp64 quotient: double rounding of a float/float
-// quotient through fp64 is innocuous since 53 >= 2*24+2); sums are fp64.
-__device__ __forceinline__ float elem_as_float(const void* p, uint64_t i, uint32_t dt) {
-    switch (dt) {
-        case CKR_F32: return reinterpret_cast<const float*>(p)[i];
-        case CKR_BF16: return __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(p)[i] << 16);
-        case CKR_F16: return (float)reinterpret_cast<const _Float16*>(p)[i];
-        case CKR_I8: return (float)reinterpret_cast<const int8_t*>(p)[i];
-        case CKR_I32: return (float)reinterpret_cast<const int32_t*>(p)[i];
-        default: return 0.f;
-    }
-}
-
-__global__ void __launch_bounds__(256) stats_pass1_kernel(const void* __restrict__ p, uint64_t n, uint32_t dt,
-                                                          StatsPartial1* __restrict__ out) {
-    __shared__ float smn[256], smx[256];
-    __shared__ double ssm[256];
-    float mn = 1e37f, mx = -1e37f;
-    double sm = 0.0;
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
-        const float x = elem_as_float(p, i, dt);
-        mn = fminf(mn, x);
-        mx = fmaxf(mx, x);
-        sm += (double)x;
-    }
-    smn[threadIdx.x] = mn; smx[threadIdx.x] = mx; ssm[threadIdx.x] = sm;
-    __syncthreads();
-    for (uint32_t s = 128; s > 0; s >>= 1) {
-        if (threadIdx.x < s) {
-            smn[threadIdx.x] = fminf(smn[threadIdx.x], smn[threadIdx.x + s]);
-            smx[threadIdx.x] = fmaxf(smx[threadIdx.x], smx[threadIdx.x + s]);
-            ssm[threadIdx.x] += ssm[threadIdx.x + s];
-        }
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) { out[blockIdx.x].mn = smn[0]; out[blockIdx.x].mx = smx[0]; out[blockIdx.x].sum = ssm[0]; }
-}
-
-__global__ void stats_mid_kernel(const StatsPartial1* __restrict__ p1, uint32_t nblk, uint64_t n, uint32_t bins_in,
-                                 StatsParams* __restrict__ prm) {
-    if (threadIdx.x != 0) return;
-    float mn = 1e37f, mx = -1e37f;
-    double sm = 0.0;
-    for (uint32_t b = 0; b < nblk; b++) { mn = fminf(mn, p1[b].mn); mx = fmaxf(mx, p1[b].mx); sm += p1[b].sum; }
-    const uint32_t bins = bins_in < 256u ? bins_in : 256u;
-    const float range = mx - mn;
-    StatsParams q;
-    q.smin = mn; q.smax = mx;
-    q.mean = (float)(sm / (double)n);
-    q.use_range = range > 1e-9f ? 1u : 0u;
-    q.scale = q.use_range ? (float)((double)((float)bins - 1.0f) / (double)range) : 0.0f;
-    q.bins = bins; q.pad[0] = q.pad[1] = 0;
-    *prm = q;
-}
-
-__global__ void __launch_bounds__(256) stats_pass2_kernel(const void* __restrict__ p, uint64_t n, uint32_t dt,
-                                                          const StatsParams* __restrict__ prm,
-                                                          StatsPartial2* __restrict__ out,
-                                                          uint32_t* __restrict__ hist_partial) {
-    __shared__ uint32_t sh[256 * 8];
-    __shared__ double r2[256], r3[256], r4[256];
-    for (uint32_t i = threadIdx.x; i < 256 * 8; i += 256) sh[i] = 0;
-    __syncthreads();
-    const StatsParams q = *prm;
-    const uint32_t c = threadIdx.x & 7;
-    double a2 = 0, a3 = 0, a4 = 0;
-    const double mean = (double)q.mean;
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
-        const float x = elem_as_float(p, i, dt);
-        if (q.bins > 0) {
-            int b = 0;
-            if (q.use_range) {
-                const float t = __fmul_rn(__fsub_rn(x, q.smin), q.scale);
-                b = (t != t) ? 0 : (int)fminf(fmaxf(t, -2147483648.0f), 2147483520.0f);
-                b = max(0, min(b, (int)q.bins - 1));
-            }
-            atomicAdd(&sh[b * 8 + c], 1u);
-        }
-        const double d = (double)x - mean, d2 = d * d;
-        a2 += d2; a3 += d2 * d; a4 += d2 * d2;
-    }
-    r2[threadIdx.x] = a2; r3[threadIdx.x] = a3; r4[threadIdx.x] = a4;
-    __syncthreads();
-    for (uint32_t s = 128; s > 0; s >>= 1) {
-        if (threadIdx.x < s) { r2[threadIdx.x] += r2[threadIdx.x + s]; r3[threadIdx.x] += r3[threadIdx.x + s]; r4[threadIdx.x] += r4[threadIdx.x + s]; }
-        __syncthreads();
-    }
-    uint32_t hs = 0;
-    for (uint32_t k = 0; k < 8; k++) hs += sh[threadIdx.x * 8 + k];
-    hist_partial[(uint64_t)blockIdx.x * 256 + threadIdx.x] = hs;
-    if (threadIdx.x == 0) { out[blockIdx.x].m2 = r2[0]; out[blockIdx.x].m3 = r3[0]; out[blockIdx.x].m4 = r4[0]; out[blockIdx.x].pad = 0; }
-}
-
-__global__ void __launch_bounds__(256) stats_final_kernel(const StatsPartial2* __restrict__ p2,
-                                                          const uint32_t* __restrict__ hist_partial, uint32_t nblk,
-                                                          uint64_t n, const StatsParams* __restrict__ prm,
-                                                          ckr_stats_record r) {
-    const StatsParams q = *prm;
-    const uint32_t t = threadIdx.x;
-    if (t < q.bins && r.d_histogram) {
-        uint32_t s = 0;
-        for (uint32_t b = 0; b < nblk; b++) s += hist_partial[(uint64_t)b * 256 + t];
-        r.d_histogram[t] = s;
-    }
-    if (t == 0) {
-        double m2 = 0, m3 = 0, m4 = 0;
-        for (uint32_t b = 0; b < nblk; b++) { m2 += p2[b].m2; m3 += p2[b].m3; m4 += p2[b].m4; }
-        const float M2 = (float)(m2 / (double)n), M3 = (float)(m3 / (double)n), M4 = (float)(m4 / (double)n);
-        const float var = M2;
-        float skew = 0.f, kurt = 0.f;
-        if (var > 1e-9f) {
-            const float sd = sqrtf(var);
-            skew = M3 / (var * sd);
-            kurt = M4 / (var * var);
-        }
-        if (r.d_raw_moments) { r.d_raw_moments[0] = q.mean; r.d_raw_moments[1] = var; r.d_raw_moments[2] = skew; r.d_raw_moments[3] = kurt; }
-        if (r.d_minmax) { r.d_minmax[0] = q.smin; r.d_minmax[1] = q.smax; }
-        if (r.d_fingerprint) {  // TensorAnalyzer.cpp:281-290
-            r.d_fingerprint[0] = q.mean; r.d_fingerprint[1] = var; r.d_fingerprint[2] = skew;
-            r.d_fingerprint[3] = kurt; r.d_fingerprint[4] = q.smax - q.smin;
-        }
-    }
-}
-
-uint32_t stats_num_blocks(uint64_t n) {
-    uint64_t nb = (n + 4095) / 4096;
-    if (nb < 1) nb = 1;
-    if (nb > 2048) nb = 2048;
-    return (uint32_t)nb;
-}
-
-hipError_t launch_stats(const ckr_stats_record& r, uint32_t nblk, StatsPartial1* p1, StatsPartial2* p2,
-                        StatsParams* prm, uint32_t* hist_partial, hipStream_t s) {
-    CKR_LAUNCH("stats_pass1_kernel", s, stats_pass1_kernel<<<nblk, 256, 0, s>>>(r.d_ptr, r.num_elements, r.data_type, p1));
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    CKR_LAUNCH("stats_mid_kernel", s, stats_mid_kernel<<<1, 64, 0, s>>>(p1, nblk, r.num_elements, r.histogram_bins, prm));
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    CKR_LAUNCH("stats_pass2_kernel", s, stats_pass2_kernel<<<nblk, 256, 0, s>>>(r.d_ptr, r.num_elements, r.data_type, prm, p2, hist_partial));
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    CKR_LAUNCH("stats_final_kernel", s, stats_final_kernel<<<1, 256, 0, s>>>(p2, hist_partial, nblk, r.num_elements, prm, r));
-    return hipGetLastError();
-}
-
 }  // namespace ckr

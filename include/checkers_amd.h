@@ -223,7 +223,12 @@ CKR_API int ckr_decode_noalloc(const uint8_t* d_data, const ckr_stream_header* d
                                uint64_t unit_bytes, const uint8_t* d_sidecar, void* d_dst,
                                uint64_t* h_bad_lanes, void* stream);
 
-/* ---- TensorAnalyzer statistics pass over n records ---- */
+/* ---- TensorAnalyzer statistics pass over n records ----
+ * All records go through four launches (two passes over the data, each with
+ * every record's blocks in one grid).  The workspace size depends on each
+ * record's pointer, element count and dtype (records with a null pointer, no
+ * elements or an unknown dtype are skipped, as the reference skips them);
+ * data pointers must be aligned to their element size. */
 CKR_API uint64_t ckr_analyze_workspace_bytes(const ckr_stats_record* h_records, uint64_t n);
 CKR_API int ckr_analyze(const ckr_stats_record* h_records, uint64_t n,
                         void* d_workspace, uint64_t workspace_bytes, void* stream);
