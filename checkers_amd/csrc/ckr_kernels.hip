@@ -2128,7 +2128,10 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
 // p at the previous check), the lane moves on to it and fetches chunk ch + 2
 // (four 16-byte loads of one 64-byte span, so each line of the stream is read
 // from L2 in two pieces at most), written into the slot of chunk ch at the end
-// of the next group, three groups at least before it is read.  The decoded
+// of the next group, three groups at least before it is read.  No chunk after
+// the one holding the stream's last byte is fetched: a window may take bytes
+// past the end from a stale slot, but a valid stream never consumes them (a
+// corrupt one fails the final state check).  The decoded
 // tensor and the sidecar are streamed with non-temporal accesses so that they
 // do not push the streams' lines out of L2.  Zero-plane lanes are checked
 // against the canonical stream (header and bytes) and produce zeros.  A
@@ -2152,6 +2155,7 @@ struct DfLane {
     uint32_t x;        // rANS state
     uint32_t p8;       // 8 x (position of the next stream byte, from the unit's 64-byte aligned base)
     uint32_t ch;       // chunk of p at the last check
+    uint32_t last;     // chunk of the stream's last byte: no chunk after it is fetched
     uint32_t tb;       // LDS address of this lane's ring column (row 0)
     bool pend;         // chunk ch + 1 is in flight in c[], to be written at the end of this group
     uint4 c0, c1, c2, c3;
@@ -2239,8 +2243,8 @@ __device__ __forceinline__ void df_step(DfLane& d, uint8_t* lds8, const DfSrc& s
     if (d.pend) df_put(lds8, d.tb, d.ch + 1u, d.c0, d.c1, d.c2, d.c3);
     const bool adv = (d.p8 >> 9) > d.ch;
     d.ch += adv ? 1u : 0u;
-    d.pend = adv;
-    if (adv) df_fetch(sr, d.ch + 1u, d.c0, d.c1, d.c2, d.c3);
+    d.pend = adv && d.ch + 1u <= d.last;
+    if (d.pend) df_fetch(sr, d.ch + 1u, d.c0, d.c1, d.c2, d.c3);
 }
 
 template <int SPE>
@@ -2350,23 +2354,27 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
                 const uint32_t p = g0 + (ok ? h.buf_offset : 0u);
                 d.x = h.final_state;
                 d.p8 = p << 3;
-                ge8 = (p + (ok ? h.byte_count : 0u)) << 3;
+                const uint32_t pe = p + (ok ? h.byte_count : 0u);
+                ge8 = pe << 3;
                 d.ch = p >> 6;
+                d.last = pe > p ? (pe - 1u) >> 6 : d.ch;
                 d.pend = false;
             };
             init(da, gea8, FL);
             init(db, geb8, 3);
             da.tb = tb0;
             db.tb = tb0 + DF_RING_BYTES;
+            // the first two chunks of each stream (the second only if the stream reaches it)
             uint4 a0, a1, a2, a3, a4, a5, a6, a7, b0, b1, b2, b3, b4, b5, b6, b7;
             df_fetch(sr, da.ch, a0, a1, a2, a3);
-            df_fetch(sr, da.ch + 1u, a4, a5, a6, a7);
             df_fetch(sr, db.ch, b0, b1, b2, b3);
-            df_fetch(sr, db.ch + 1u, b4, b5, b6, b7);
+            const bool a2nd = da.ch + 1u <= da.last, b2nd = db.ch + 1u <= db.last;
+            if (a2nd) df_fetch(sr, da.ch + 1u, a4, a5, a6, a7);
+            if (b2nd) df_fetch(sr, db.ch + 1u, b4, b5, b6, b7);
             df_put(lds8, da.tb, da.ch, a0, a1, a2, a3);
-            df_put(lds8, da.tb, da.ch + 1u, a4, a5, a6, a7);
             df_put(lds8, db.tb, db.ch, b0, b1, b2, b3);
-            df_put(lds8, db.tb, db.ch + 1u, b4, b5, b6, b7);
+            if (a2nd) df_put(lds8, da.tb, da.ch + 1u, a4, a5, a6, a7);
+            if (b2nd) df_put(lds8, db.tb, db.ch + 1u, b4, b5, b6, b7);
         }
         const uint32_t K = len >> 8;  // full rows; a partial row K follows when len % 256 != 0
         // sidecar of row k for this column: 16 bits at (ubase + 256k + 4j) / 2, read
