@@ -2295,6 +2295,42 @@ __device__ __forceinline__ void df_load_sc(uint32_t (&sc)[8], const uint32_t* p)
     for (int r = 0; r < 8; r++) sc[r] = df_ld(p + 32 * r);  // rows are 128 sidecar bytes apart
 }
 
+// A zero-plane lane against the canonical stream of its symbol count: header
+// (state, count, inside the unit) and bytes.  The bytes are compared 32 at a
+// time, all loads of a step issued together (9 stream dwords around the bytes,
+// 8 canonical dwords) so that the check waits for memory once per step; near
+// the ends of the data buffer, byte by byte.
+__device__ __forceinline__ bool df_zero_lane_ok(const ckr_stream_header& h, const uint32_t* ce, const uint32_t* cp,
+                                                uint32_t cw, const uint8_t* ud, uint32_t usize, uintptr_t d0,
+                                                uintptr_t d1) {
+    if (h.final_state != ce[1] || h.byte_count != ce[2] || (uint64_t)h.buf_offset + h.byte_count > usize) return false;
+    const uint8_t* sl = ud + h.buf_offset;
+    const uint32_t bc = h.byte_count;
+    uint32_t diff = 0;
+    for (uint32_t q0 = 0; q0 < bc; q0 += 32) {
+        const uintptr_t a = reinterpret_cast<uintptr_t>(sl) + q0, aa = a & ~(uintptr_t)3;
+        const uint32_t sh = (uint32_t)(a & 3u), rem = bc - q0;
+        if (aa >= d0 && aa + 36 <= d1 && (q0 >> 2) + 8 <= cw) {
+            const uint32_t* bp = reinterpret_cast<const uint32_t*>(aa);
+            uint32_t w[9], c[8];
+#pragma unroll
+            for (int k = 0; k < 9; k++) w[k] = bp[k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) c[k] = cp[(q0 >> 2) + k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint32_t r = rem > 4u * k ? rem - 4u * k : 0u;  // bytes of this dword inside the stream
+                const uint32_t m = r >= 4 ? ~0u : (1u << (8 * r)) - 1u;
+                diff |= (__builtin_amdgcn_alignbyte(w[k + 1], w[k], sh) ^ c[k]) & m;
+            }
+        } else {
+            const uint8_t* cb = reinterpret_cast<const uint8_t*>(cp);
+            for (uint32_t q = q0; q < min(bc, q0 + 32); q++) diff |= sl[q] ^ cb[q];
+        }
+    }
+    return diff == 0;
+}
+
 template <int SPE>
 __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_t* __restrict__ data,
                                                                    const ckr_stream_header* __restrict__ hdrs,
@@ -2371,6 +2407,17 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
             const bool a2nd = da.ch + 1u <= da.last, b2nd = db.ch + 1u <= db.last;
             if (a2nd) df_fetch(sr, da.ch + 1u, a4, a5, a6, a7);
             if (b2nd) df_fetch(sr, db.ch + 1u, b4, b5, b6, b7);
+            // zero-plane lanes: header and bytes must be the canonical stream (their
+            // loads wait together with the chunks above)
+            const uint32_t Kz = len >> 8, rz = len & 255u;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                if (lane_is_live<SPE>(b)) continue;
+                const uint32_t Kb = Kz + ((4 * j + b < rz) ? 1u : 0u);  // symbols of lane 4j+b
+                const uint32_t ent = (canon[0] == Kb) ? 0u : ((canon[4 + cw] == Kb) ? 1u : 2u);
+                nbad += df_zero_lane_ok(uh[4 * j + b], canon + ent * (4 + cw), cbytes + (uint64_t)ent * cw, cw, ud,
+                                        usize, d0, d1) ? 0u : 1u;
+            }
             df_put(lds8, da.tb, da.ch, a0, a1, a2, a3);
             df_put(lds8, db.tb, db.ch, b0, b1, b2, b3);
             if (a2nd) df_put(lds8, da.tb, da.ch + 1u, a4, a5, a6, a7);
@@ -2437,44 +2484,6 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
         }
         nbad += (da.x != L || da.p8 != gea8) ? 1u : 0u;
         nbad += (db.x != L || db.p8 != geb8) ? 1u : 0u;
-        // zero-plane lanes: header and bytes must be the canonical stream
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            if (lane_is_live<SPE>(b)) continue;
-            const uint32_t Kb = K + ((4 * j + b < r) ? 1u : 0u);  // symbols of lane 4j+b
-            const uint32_t ent = (canon[0] == Kb) ? 0u : ((canon[4 + cw] == Kb) ? 1u : 2u);
-            const uint32_t* ce = canon + ent * (4 + cw);
-            const ckr_stream_header h = uh[4 * j + b];
-            bool ok = h.final_state == ce[1] && h.byte_count == ce[2] && (uint64_t)h.buf_offset + h.byte_count <= usize;
-            if (ok) {
-                const uint32_t* cp = cbytes + (uint64_t)ent * cw;
-                const uint8_t* cb = reinterpret_cast<const uint8_t*>(cp);
-                const uint8_t* sl = ud + h.buf_offset;
-                // stream dwords (any alignment: two aligned dwords around each, the
-                // first nq of which lie in the data buffer) against the canonical
-                // dwords, 8 at a time; the rest byte by byte
-                const uintptr_t a0 = reinterpret_cast<uintptr_t>(sl), aa0 = a0 & ~(uintptr_t)3;
-                const uint32_t sh = (uint32_t)(a0 & 3u);
-                uint32_t nq = h.byte_count >> 2;
-                if (aa0 < d0 || aa0 + 8 > d1) nq = 0;
-                else nq = (uint32_t)min<uint64_t>(nq, (d1 - aa0 - 8) / 4 + 1);
-                const uint32_t* bp = data32_at(data, aa0 - d0);
-                uint32_t diff = 0, i = 0;
-                for (; i + 8 <= nq; i += 8) {
-                    uint32_t w[9], c[8];
-#pragma unroll
-                    for (int k = 0; k < 9; k++) w[k] = bp[i + k];
-#pragma unroll
-                    for (int k = 0; k < 8; k++) c[k] = cp[i + k];
-#pragma unroll
-                    for (int k = 0; k < 8; k++) diff |= __builtin_amdgcn_alignbyte(w[k + 1], w[k], sh) ^ c[k];
-                }
-                for (; i < nq; i++) diff |= __builtin_amdgcn_alignbyte(bp[i + 1], bp[i], sh) ^ cp[i];
-                for (uint32_t q = 4 * nq; q < h.byte_count; q++) diff |= sl[q] ^ cb[q];
-                ok = diff == 0;
-            }
-            nbad += ok ? 0u : 1u;
-        }
         nbad_total += nbad;
     }
     if (nbad_total) atomicAdd(bad, nbad_total);
