@@ -2356,14 +2356,27 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
     const uint32_t tb0 = DF_TAB_BYTES + wv * DF_WAVE_BYTES + 4 * j;
     unsigned long long nbad_total = 0;
 
-    for (uint64_t u = (uint64_t)blockIdx.x * DF_WAVES + wv; u < g.n_units; u += (uint64_t)gridDim.x * DF_WAVES) {
+    // the next unit's headers (this thread's four lanes) are loaded while the
+    // current unit is decoded
+    const uint64_t ustride = (uint64_t)gridDim.x * DF_WAVES;
+    ckr_stream_header hn[4];
+    auto load_headers = [&](uint64_t v) __attribute__((always_inline)) {
+        const ckr_stream_header* vh = hdrs + v * 256 + 4 * j;
+#pragma unroll
+        for (int b = 0; b < 4; b++) hn[b] = vh[b];
+    };
+    if ((uint64_t)blockIdx.x * DF_WAVES + wv < g.n_units) load_headers((uint64_t)blockIdx.x * DF_WAVES + wv);
+    for (uint64_t u = (uint64_t)blockIdx.x * DF_WAVES + wv; u < g.n_units; u += ustride) {
+        ckr_stream_header uh[4];
+#pragma unroll
+        for (int b = 0; b < 4; b++) uh[b] = hn[b];
+        if (u + ustride < g.n_units) load_headers(u + ustride);
         const uint64_t ubase = u * g.unit;
         const uint32_t len = unit_len(g, ubase);
         const uint64_t uoff = unit_off[u];
         const uint8_t* ud = data + uoff;
         const uint32_t usize = (uint32_t)(unit_off[u + 1] - uoff);
-        const ckr_stream_header* uh = hdrs + u * 256;
-        if (usize == len && uh[0].byte_count == len) {
+        if (usize == len && __shfl(uh[0].byte_count, 0, 64) == len) {
             decode_raw_unit<SPE>(ud, ubase, len, j, sidecar, dst);
             continue;
         }
@@ -2384,7 +2397,7 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
         uint32_t gea8, geb8;
         {
             auto init = [&](DfLane& d, uint32_t& ge8, int b) __attribute__((always_inline)) {
-                const ckr_stream_header h = uh[4 * j + b];
+                const ckr_stream_header h = uh[b];
                 const bool ok = (uint64_t)h.buf_offset + h.byte_count <= usize;
                 nbad += ok ? 0u : 1u;
                 const uint32_t p = g0 + (ok ? h.buf_offset : 0u);
@@ -2415,7 +2428,7 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
                 if (lane_is_live<SPE>(b)) continue;
                 const uint32_t Kb = Kz + ((4 * j + b < rz) ? 1u : 0u);  // symbols of lane 4j+b
                 const uint32_t ent = (canon[0] == Kb) ? 0u : ((canon[4 + cw] == Kb) ? 1u : 2u);
-                nbad += df_zero_lane_ok(uh[4 * j + b], canon + ent * (4 + cw), cbytes + (uint64_t)ent * cw, cw, ud,
+                nbad += df_zero_lane_ok(uh[b], canon + ent * (4 + cw), cbytes + (uint64_t)ent * cw, cw, ud,
                                         usize, d0, d1) ? 0u : 1u;
             }
             df_put(lds8, da.tb, da.ch, a0, a1, a2, a3);
