@@ -70,6 +70,15 @@ __device__ __forceinline__ float one(const uint8_t* p, uint64_t i, uint32_t dt) 
     }
 }
 
+// float → int32 as the hardware converts: out-of-range values (infinities
+// included) saturate, NaN gives 0 — the clamp the bin index needs, in one
+// instruction (the reference's int cast runs on the same conversion).
+__device__ __forceinline__ int cvt_i32_sat(float t) {
+    int r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(t));
+    return r;
+}
+
 // The 16 bytes v as DT's elements, each handed to f.
 template <uint32_t DT, typename F>
 __device__ __forceinline__ void unpack(const uint4 v, F&& f) {
@@ -243,8 +252,7 @@ __device__ void pass2_share(const StatsDesc& d, uint32_t lb, const StatsParams& 
                 int b = 0;
                 if (q.use_range) {  // TensorAnalyzer.cpp:150-160
                     const float t = __fmul_rn(__fsub_rn(x, q.smin), q.scale);
-                    b = (t != t) ? 0 : (int)fminf(fmaxf(t, -2147483648.0f), 2147483520.0f);
-                    b = max(0, min(b, (int)q.bins - 1));
+                    b = max(0, min(cvt_i32_sat(t), (int)q.bins - 1));
                 }
                 atomicAdd(&sh[b * kHistCopies + c], 1u);
             }
