@@ -601,7 +601,7 @@ def run_streamed(args, shard, ck, torch, dev, unit, n_in):
         "decode_roofline_frac": round(B / dec_s / 1e9 / HBM_PEAK_GBPS, 4),
         "compressed_bytes": C, "sidecar_bytes": S, "header_bytes": H,
         "ans_ratio": round(n_in / C, 4), "disk_ratio": round(n_in / (C + S), 4),
-        "container_ratio": round(n_in / (C + S + H), 4), "roundtrip_bit_exact": ok,
+        "device_ratio": round(n_in / (C + S + H), 4), "container_ratio": None, "roundtrip_bit_exact": ok,
         "roofline": None, "cpu_baseline": None, "kernels": {},
     }
     print(json.dumps(out), flush=True)
