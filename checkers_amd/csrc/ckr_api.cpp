@@ -311,7 +311,8 @@ uint32_t lane_slot_bytes(const uint32_t* plane_hist, const ckr_freq_table* t, ui
 // look-back state and redo list, and lane scratch for general-kernel batches
 // (sized for the whole tensor's units, capped by kScratchBudget).
 struct EncodeLayout {
-    uint64_t off_enc, off_hist, off_canon, off_status, off_ctl, off_redo, off_usize, off_rec, off_aux, off_scratch, total;
+    uint64_t off_enc, off_hist, off_canon, off_status, off_ctl, off_redo, off_usize, off_rec, off_aux, off_list,
+        off_scratch, total;
     uint64_t batch_units;
 };
 
@@ -333,6 +334,7 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     L.off_usize = o;   o = align_up(o + (seg ? g.n_units : bu) * 4, kAlign);
     L.off_rec = o;     o = align_up(o + (seg ? g.n_units * ckr::encode_seg_segments(g.unit) * 128 * 8 : 0), kAlign);
     L.off_aux = o;     o = align_up(o + (seg ? 512 : 0), kAlign);
+    L.off_list = o;    o = align_up(o + (seg ? ckr::encode_seg_list_items(g.n_units, g.unit) * 8 : 0), kAlign);
     L.off_scratch = o; o = align_up(o + (seg ? 0 : bu * per_unit), kAlign);
     L.total = o;
     return L;
@@ -721,8 +723,43 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
     if (use_seg_encode(g)) {
         auto* rec = reinterpret_cast<uint2*>(ws + L.off_rec);
         auto* aux = reinterpret_cast<uint32_t*>(ws + L.off_aux);
+        // Pass 2 of whole units on the fast encoder's waves: slots for 256 rows.
+        // Pass 1 knows every lane's piece length, so a segment that does not fit
+        // its slots simply goes to seg_code_kernel: the slots are made as large
+        // as two coder pairs' LDS allows, starting from the plane histograms'
+        // estimate and growing both planes alike.  Without plane histograms (a
+        // caller's table) the two planes' needs are unknown and an even split
+        // sends most segments of high-entropy data to seg_code_kernel, so
+        // seg_code_kernel takes all of pass 2.  Mode 2 keeps minimal slots, so
+        // that every segment takes seg_code_kernel.
+        ckr::FastEncParamsHost sp{};
+        sp.escapes = escapes;
+        sp.cw = ck.cw;
+        // the whole units' zero-plane lanes share one canonical stream (k0 symbols)
+        sp.canon_bytes = std::min<uint32_t>((canon_stream_bytes(h_table, ck.k0) + 3) & ~3u, 4 * ck.cw);
+        const uint32_t lds_limit = (uint32_t)max_lds_per_block();
+        auto fits = [&](uint32_t a, uint32_t b) {
+            sp.sl0 = a;
+            sp.sl1 = b;
+            return ckr::encode_seg_fast_lds_bytes(sp, lds_limit) != 0;
+        };
+        uint32_t a = 8, b = 8;
+        if (g_fast_paths != 2) {
+            constexpr uint32_t cap = 2 * 256 + 8;  // the most 256 symbols can emit, and the final dword
+            if (h_planes) {
+                a = std::min(cap, lane_slot_bytes(h_planes, h_table, 256));
+                b = std::min(cap, lane_slot_bytes(h_planes + 256, h_table, 256));
+            }
+            while (!fits(a, b) && (a > 8 || b > 8)) (a >= b ? a : b) -= 4;
+            while ((a < cap || b < cap) && fits(std::min(a + 4, cap), std::min(b + 4, cap))) {
+                a = std::min(a + 4, cap);
+                b = std::min(b + 4, cap);
+            }
+        }
+        const bool seg_fast = (h_planes || g_fast_paths == 2) && fits(a, b);
         CKR_HIP(ckr::launch_encode_seg(static_cast<const uint8_t*>(d_src), g, enc, canon, ck.cw, escapes, rec,
-                                       d_headers, usize, d_unit_offsets, side, d_out, aux, s));
+                                       d_headers, usize, d_unit_offsets, side, d_out, aux, seg_fast ? &sp : nullptr,
+                                       lds_limit, aux + 64, ws + L.off_list, s));
         if (after_launch) CKR_HIP((*after_launch)());
         if (defer) {
             defer->kind = 2;

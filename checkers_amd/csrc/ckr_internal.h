@@ -102,11 +102,20 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
 // Units above 64 KiB of masked dtypes, in two passes (no lane scratch): rec
 // holds n_units * encode_seg_segments(unit) * 128 checkpoint records, unit_size
 // n_units words, aux 128 words (aux[0]: nonzero when a segment did not end where
-// its checkpoints say, which would be a bug).
+// its checkpoints say, which would be a bug).  With fp (slots sized for 256
+// rows; units a multiple of 64 KiB), pass 2 runs on the fast encoder's waves,
+// one 256-row segment per item, and seg_code_kernel takes the segments that do
+// not fit the slots; ctl then holds 2 words and list
+// encode_seg_list_items(n_units, unit) entries of 8 bytes.
 uint32_t encode_seg_segments(uint64_t unit);
+uint64_t encode_seg_list_items(uint64_t n_units, uint64_t unit);
+// LDS bytes of pass 2 on the fast encoder's waves within lds_limit (0: it does not fit).
+uint32_t encode_seg_fast_lds_bytes(const FastEncParamsHost& p, uint32_t lds_limit);
 hipError_t launch_encode_seg(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
                              uint32_t cw, bool escapes, uint2* rec, ckr_stream_header* hdrs, uint32_t* unit_size,
-                             uint64_t* unit_off, uint8_t* sidecar, uint8_t* out, uint32_t* aux, hipStream_t s);
+                             uint64_t* unit_off, uint8_t* sidecar, uint8_t* out, uint32_t* aux,
+                             const FastEncParamsHost* fp, uint32_t lds_limit, uint32_t* ctl, void* list,
+                             hipStream_t s);
 
 // Canonical zero-plane streams for lane counts k0, k1, k2: 3 entries of 4 + cw
 // dwords (header, then the stream in slot format), followed by the 3 streams in

@@ -1782,40 +1782,29 @@ __device__ __forceinline__ void seg_copy_thread(uint8_t* dst, const uint32_t* sr
     }
 }
 
+// An item of pass 2 by list: unit u, segments [sg & 0xFFFF, + sg >> 16).
+struct SegItem {
+    uint32_t u, sg;
+};
+
 // LDS of seg_code_kernel: table | per wave: 128 line buffers of SEG_LINE bytes, then
 // 128 copy-table entries.
 static constexpr uint32_t SEG_WAVE_LDS = 128 * SEG_LINE + 128 * 8;
 static constexpr uint32_t SEG_LDS = 4096 + 4 * SEG_WAVE_LDS;
 
-// One wave per item of G consecutive segments [s0, s0 + G) of a unit, coded
-// from the top of segment s0 + G - 1 down.
+// Pass 2 for one item, G consecutive segments [s0, s0 + G) of unit u, coded by
+// one wave from the top of segment s0 + G - 1 down (wv: the wave's index in
+// its workgroup, which selects its LDS buffers).
 template <int SPE, bool ESC>
-__global__ void __launch_bounds__(256) seg_code_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
-                                                       const EncSym* __restrict__ d_enc,
-                                                       const uint32_t* __restrict__ canon, uint32_t cw, uint32_t S,
-                                                       uint32_t G, const uint2* __restrict__ rec,
-                                                       const ckr_stream_header* __restrict__ hdrs,
-                                                       const uint32_t* __restrict__ unit_size,
-                                                       const uint64_t* __restrict__ unit_off,
-                                                       uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out,
-                                                       uint32_t* __restrict__ aux) {
-    extern __shared__ uint4 seg_lds[];
-    uint4* tab = seg_lds;
-    uint8_t* lds8 = reinterpret_cast<uint8_t*>(seg_lds);
-    seg_load_table(tab, d_enc);
-    __syncthreads();
+__device__ void seg_code_item(const uint8_t* __restrict__ src, const EncodeGeom& g,
+                              const uint32_t* __restrict__ canon, uint32_t cw, uint32_t S, uint32_t G,
+                              const uint2* __restrict__ rec, const ckr_stream_header* __restrict__ hdrs,
+                              const uint32_t* __restrict__ unit_size, const uint64_t* __restrict__ unit_off,
+                              uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out, uint32_t* __restrict__ aux,
+                              uint64_t u, uint32_t s0, uint32_t wv, const uint4* tab, uint8_t* lds8) {
     constexpr int FL = SPE == 2 ? 2 : 1;
     constexpr uint32_t SH0 = 8u * FL;
     const uint32_t j = threadIdx.x & 63;
-    const uint32_t wv = threadIdx.x >> 6;
-    // workgroups go round-robin over the 8 XCDs: those of one XCD take
-    // consecutive items, so the neighbouring runs of a lane share its L2
-    const uint32_t nb = gridDim.x, q8 = nb >> 3, r8 = nb & 7u, xcd = blockIdx.x & 7u;
-    const uint32_t lbk = xcd * q8 + min(xcd, r8) + (blockIdx.x >> 3);
-    const uint32_t ipu = (S + G - 1) / G;  // items per unit
-    const uint64_t item = (uint64_t)lbk * 4 + wv;
-    const uint64_t u = item / ipu;
-    const uint32_t s0 = (uint32_t)(item % ipu) * G;
     if (u >= g.n_units) return;
     const uint64_t ubase = u * g.unit;
     const uint32_t len = (uint32_t)((g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit);
@@ -1965,11 +1954,388 @@ __global__ void __launch_bounds__(256) seg_code_kernel(const uint8_t* __restrict
     }
 }
 
+// One wave per item.  Grid mode (LIST false): items of G consecutive segments
+// in unit order, G segments per item.  List mode: the items in list[0,
+// *list_count), each wave taking every n-th one (n: the grid's waves).
+template <int SPE, bool ESC, bool LIST>
+__global__ void __launch_bounds__(256) seg_code_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
+                                                       const EncSym* __restrict__ d_enc,
+                                                       const uint32_t* __restrict__ canon, uint32_t cw, uint32_t S,
+                                                       uint32_t G, const uint2* __restrict__ rec,
+                                                       const ckr_stream_header* __restrict__ hdrs,
+                                                       const uint32_t* __restrict__ unit_size,
+                                                       const uint64_t* __restrict__ unit_off,
+                                                       uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out,
+                                                       uint32_t* __restrict__ aux, const SegItem* __restrict__ list,
+                                                       const uint32_t* __restrict__ list_count) {
+    extern __shared__ uint4 seg_lds[];
+    uint4* tab = seg_lds;
+    uint8_t* lds8 = reinterpret_cast<uint8_t*>(seg_lds);
+    seg_load_table(tab, d_enc);
+    __syncthreads();
+    const uint32_t wv = threadIdx.x >> 6;
+    // workgroups go round-robin over the 8 XCDs: those of one XCD take
+    // consecutive items, so the neighbouring runs of a lane share its L2
+    const uint32_t nb = gridDim.x, q8 = nb >> 3, r8 = nb & 7u, xcd = blockIdx.x & 7u;
+    const uint32_t lbk = xcd * q8 + min(xcd, r8) + (blockIdx.x >> 3);
+    const uint32_t ipu = (S + G - 1) / G;  // items per unit
+    const uint32_t n = LIST ? *list_count : 1u;
+    const uint32_t k0 = LIST ? blockIdx.x * 4 + wv : 0u, step = LIST ? gridDim.x * 4 : 1u;
+    for (uint32_t k = k0; k < n; k += step) {
+        uint64_t u;
+        uint32_t s0, gk;
+        if constexpr (LIST) {
+            const SegItem it = list[k];
+            u = it.u;
+            s0 = it.sg & 0xFFFFu;
+            gk = it.sg >> 16;
+        } else {
+            const uint64_t item = (uint64_t)lbk * 4 + wv;
+            u = item / ipu;
+            s0 = (uint32_t)(item % ipu) * G;
+            gk = G;
+        }
+        seg_code_item<SPE, ESC>(src, g, canon, cw, S, gk, rec, hdrs, unit_size, unit_off, sidecar, out, aux, u, s0,
+                                wv, tab, lds8);
+    }
+}
+
+// Pass 2 of a two-pass encode on encode_fast_kernel's coder and packer waves.
+// seg_size_kernel has written every lane's {state, bytes so far} at the entry
+// of each 256-row segment, the headers and the unit sizes; unit_scan_kernel
+// the unit offsets.  An item is one 256-row segment (64 KiB of input; the top
+// segment of a partial last unit may be shorter), taken in address order from
+// a ticket counter.
+// What lane l emits in segment s has a known place: with o and c its header's
+// buf_offset and byte_count, B its bytes so far at the entry of s and B' the
+// same at the entry of s - 1 (c for s = 0), the piece is [o + c - B', o + c -
+// B) of the unit's output, B' - B bytes.  The two coder waves of a pair code
+// the segment from the recorded entry states into the pair's LDS slots (sized
+// for 256 rows, as for 64 KiB units) and check that every lane ends in the
+// state and at the byte count the next record gives (a mismatch sets *err).
+// The packer waves copy each piece to its place, 16-byte stores aligned in
+// memory and byte stores at its two ends (the lines there are shared with the
+// neighbouring segments' pieces, not their bytes), and copy the canonical
+// streams of the unit's zero-plane lanes (the columns j with j mod S = s).
+// A segment with a lane whose piece is longer than its slot is not coded here
+// but appended to `list`, which seg_code_kernel then codes; a passthrough
+// unit's segment is its masked bytes and sidecar, written by one coder wave.
+// ctl[0]: ticket counter, ctl[1]: list length (both set before the launch).
+template <int SPE, bool ESC, int PAIRS, int NPK>
+__global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_waves_per_eu(4)))
+seg_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g, const EncSym* __restrict__ d_enc,
+                const uint32_t* __restrict__ canon, uint32_t cw, uint32_t S, uint32_t n_full, uint32_t n_last,
+                FastEncParams fp,
+                const uint2* __restrict__ rec, const ckr_stream_header* __restrict__ hdrs,
+                const uint32_t* __restrict__ unit_size, const uint64_t* __restrict__ unit_off,
+                uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out, uint32_t* __restrict__ ctl,
+                SegItem* __restrict__ list, uint32_t* __restrict__ err) {
+    extern __shared__ uint32_t lds[];
+    uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
+    constexpr uint32_t NT = 64 * (2 + NPK) * PAIRS;
+    constexpr int FL = SPE == 2 ? 2 : 1;
+    const uint4* tab = reinterpret_cast<const uint4*>(lds8);
+    const uint32_t ctl_off = ws_ctl_offset(fp.canon_bytes);
+    const uint32_t rbytes = ws_region_bytes(fp.stride0, fp.stride1);
+    const uint32_t reg0 = ctl_off + PAIRS * (uint32_t)sizeof(WsPairCtl);
+    const uint32_t tid = threadIdx.x;
+    const uint32_t j = tid & 63;
+    const uint32_t col = 4 * j;
+    const uint32_t lm = live_mask32<SPE>();
+    const uint32_t Kf = (uint32_t)(g.unit >> 8);  // rows of a whole unit: every lane's symbol count
+    {   // table (EncSym → enc_quad), the canonical stream of Kf zero symbols (byte
+        // order, at FE_CBYTES), control blocks
+        const uint4* d_tab = reinterpret_cast<const uint4*>(d_enc);
+        uint4* wt = reinterpret_cast<uint4*>(lds8);
+        for (uint32_t k = tid; k < 256; k += NT) {
+            const uint4 tv = d_tab[k];
+            const EncSym e = {tv.x, tv.y, tv.z, tv.w};
+            wt[k] = enc_quad(e);
+        }
+        const uint32_t* cs = canon + 3 * (4 + cw) + canon_index(canon, cw, Kf) * cw;
+        uint32_t* cb32 = reinterpret_cast<uint32_t*>(lds8 + FE_CBYTES);
+        for (uint32_t i = tid; i < fp.canon_bytes / 4; i += NT) cb32[i] = cs[i];
+        uint32_t* c32 = reinterpret_cast<uint32_t*>(lds8 + ctl_off);
+        for (uint32_t i = tid; i < PAIRS * (uint32_t)sizeof(WsPairCtl) / 4; i += NT) c32[i] = 0;
+    }
+    __syncthreads();
+
+    const uint32_t wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool coder = wv < 2 * PAIRS;
+    const uint32_t pr = coder ? (wv >> 1) : (wv - 2 * PAIRS) / NPK;  // pair
+    const uint32_t rl = wv & 1;                                       // coder: 0 byte FL, 1 byte 3
+    const uint32_t pw = coder ? 0u : (wv - 2 * PAIRS) % NPK;          // packer index in the pair
+    WsPairCtl& pc = *reinterpret_cast<WsPairCtl*>(lds8 + ctl_off + pr * (uint32_t)sizeof(WsPairCtl));
+    // items: the n_last segments of a partial last unit (unit n_full), if there
+    // is one, first (its top segment is coded row by row, the slowest item, so
+    // it should not come last), then the S segments of each whole unit
+    const uint32_t n_items = n_full * S + n_last;
+    auto item_of = [&](uint32_t t, uint32_t& u, uint32_t& sg, uint32_t& len) {
+        const bool whole = t >= n_last;
+        u = whole ? (t - n_last) / S : n_full;
+        sg = whole ? (t - n_last) % S : n_last - 1 - t;
+        len = whole ? (uint32_t)g.unit : (uint32_t)(g.n_bytes - (uint64_t)n_full * g.unit);
+    };
+    // exchange words of a set (lane index li = 64 rank + column): [0, 128)
+    // piece bytes, [128, 256) piece offset in the unit's output, [256, 384)
+    // flags (1: longer than its slot, 2: not at its checkpoint)
+    constexpr uint32_t X_LEN = 0, X_DST = 128, X_FLAG = 256;
+    static_assert(NPK == 4, "four packer waves, 32 lanes' pieces each");
+    static_assert(R_REC + 4 * 384 <= R_SLOTS - 516, "exchange words below the guard of the lowest slot");
+
+    if (coder) {
+        const uint32_t li = 64 * rl + j;
+        const uint32_t lane = col + (rl ? 3u : (uint32_t)FL);
+        for (uint32_t i = 0;; i++) {
+            const uint32_t s = i & 1;
+            if (i >= 2) ws_wait_ge(&pc.freed[s], i >> 1);  // set s given back
+            if (rl == 0) {
+                if (j == 0) pc.unit[s] = atomicAdd(&ctl[0], 1u);  // ticket
+                ws_signal(&pc.tick, 1u, j);
+            } else {
+                ws_wait_ge(&pc.tick, i + 1);
+            }
+            const uint32_t t = __builtin_amdgcn_readfirstlane(ws_load(&pc.unit[s]));
+            if (t >= n_items) {
+                ws_signal(&pc.coded[s], 1u, j);
+                break;
+            }
+            uint32_t u, sg, len;
+            item_of(t, u, sg, len);
+            const uint64_t ubase0 = (uint64_t)u * g.unit;       // the unit's first byte
+            const uint64_t ubase = ubase0 + 65536ull * sg;      // the segment's first byte
+            const uint32_t lo = 256 * sg;                      // the segment's rows [lo, lo + 256), clipped
+            // all 256 rows of the segment full (always so in a whole unit)
+            const bool full = (lo + 256) * 256 <= len;
+            const uint32_t rb = reg0 + (2 * pr + s) * rbytes;
+            uint32_t* xch = reinterpret_cast<uint32_t*>(lds8 + rb + R_REC);
+            uint32_t e = 0, flag = 0;
+            if (unit_size[u] >= len) {
+                // passthrough unit: the segment's masked bytes in place, and its sidecar
+                if (rl == 0) {
+                    uint8_t* ud = out + unit_off[u];
+                    const uint8_t* us = src + ubase0;
+                    const uint32_t khi = min(lo + 256, (len + 255) / 256);
+                    for (uint32_t k = lo; k < khi; k++) {
+                        const uint32_t p = 256 * k + col;
+                        if (p >= len) break;
+                        const uint32_t nv = min(len - p, 4u);
+                        uint32_t wd = 0;
+                        if (nv == 4) wd = *reinterpret_cast<const uint32_t*>(us + p);
+                        else for (uint32_t b = 0; b < nv; b++) wd |= (uint32_t)us[p + b] << (8 * b);
+                        write_sidecar_row<SPE>(sidecar, ubase0 + p, wd, nv);
+                        uint8_t* d = ud + p;
+                        if (nv == 4 && (reinterpret_cast<uintptr_t>(d) & 3u) == 0) *reinterpret_cast<uint32_t*>(d) = wd & lm;
+                        else
+                            for (uint32_t b = 0; b < nv; b++) d[b] = (uint8_t)((wd & lm) >> (8 * b));
+                    }
+                }
+            } else {
+                uint32_t x0;
+                {
+                    const ckr_stream_header h = hdrs[(uint64_t)u * 256 + lane];
+                    const uint2 ent = rec[((uint64_t)u * S + sg) * 128 + li];
+                    const uint2 nxt = sg ? rec[((uint64_t)u * S + sg - 1) * 128 + li]
+                                         : make_uint2(h.final_state, h.byte_count);
+                    // the piece's place, its length and the state after it wait in
+                    // the set's exchange words while the segment is coded
+                    xch[X_DST + li] = h.buf_offset + h.byte_count - nxt.y;
+                    xch[X_LEN + li] = nxt.y - ent.y;
+                    xch[X_FLAG + li] = nxt.x;
+                    x0 = ent.x;
+                }
+                const uint32_t sl = rl ? fp.sl1 : fp.sl0;
+                if (__ballot(xch[X_LEN + li] > sl) != 0) {
+                    flag = 1;  // the whole segment goes to seg_code_kernel
+                } else {
+                    const uint32_t endw = rl ? rb + R_SLOTS + 64 * fp.stride0 + j * fp.stride1 + fp.sl1
+                                             : rb + R_SLOTS + j * fp.stride0 + fp.sl0;
+                    EncLane c{x0, 0u, 0u, 0x08090A0Bu, endw - 4u};
+                    EncLane c_unused = c;
+                    if (full) {
+                        const uint8_t* ucol = src + ubase + col;
+                        if (rl == 0) enc_full_rows<SPE, ESC, true, 0, ENC_GR, ENC_TB, ENC_NBUF>(c, c_unused, ucol, sidecar, ubase, j, 256, tab, lds8);
+                        else enc_full_rows<SPE, ESC, true, 1, ENC_GR, ENC_TB, ENC_NBUF>(c, c_unused, ucol, sidecar, ubase, j, 256, tab, lds8);
+                    } else {
+                        // the top segment of a partial last unit: rows from the top down,
+                        // one at a time (as in encode_fast_kernel); the top row may be
+                        // partial (bf16: lane 4j+3 has one symbol fewer)
+                        const uint8_t* us = src + ubase0;
+                        const uint32_t kc = len > col ? (len - col + 255) / 256 : 0u;  // rows of column j
+                        const uint32_t khi = min(lo + 256, kc);
+                        const uint32_t sh = rl ? 24u : 8u * FL;
+                        for (int32_t k = (int32_t)khi - 1; k >= (int32_t)lo; k--) {
+                            const uint32_t p = 256 * (uint32_t)k + col;
+                            const uint32_t nvalid = (len - p) < 4 ? (len - p) : 4;
+                            uint32_t v = 0;
+                            if (nvalid == 4) v = *reinterpret_cast<const uint32_t*>(us + p);
+                            else for (uint32_t b = 0; b < nvalid; b++) v |= (uint32_t)us[p + b] << (8 * b);
+                            if ((uint32_t)(k & 1) == rl) write_sidecar_row<SPE>(sidecar, ubase0 + p, v, nvalid);
+                            v &= lm;
+                            const uint32_t sy = (v >> sh) & 255u;
+                            if (rl == 0 || nvalid == 4) enc_step<ESC>(c, sy, tab[sy]);
+                            if ((k & 1) == 0) enc_flush(c, lds8);
+                        }
+                    }
+                    e = enc_finish(c, lds8, endw);
+                    flag = (e == xch[X_LEN + li] && c.x == xch[X_FLAG + li]) ? 0u : 2u;
+                    if (flag) e = 0;  // nothing is copied from a lane off its checkpoints
+                }
+            }
+            xch[X_LEN + li] = e;
+            xch[X_FLAG + li] = flag;
+            ws_signal(&pc.coded[s], 1u, j);
+        }
+        return;
+    }
+
+    // packer waves
+    uint32_t bar = 0;
+    auto pbar_sync = [&]() {
+        bar += NPK;
+        ws_signal(&pc.pbar, 1u, j);
+        ws_wait_ge(&pc.pbar, bar);
+    };
+    for (uint32_t i = 0;; i++) {
+        const uint32_t s = i & 1;
+        ws_wait_ge(&pc.coded[s], 2 * ((i >> 1) + 1));
+        const uint32_t t = __builtin_amdgcn_readfirstlane(ws_load(&pc.unit[s]));
+        if (t >= n_items) break;
+        uint32_t u, sg, len;
+        item_of(t, u, sg, len);
+        const uint32_t rb = reg0 + (2 * pr + s) * rbytes;
+        const uint32_t* xch = reinterpret_cast<const uint32_t*>(lds8 + rb + R_REC);
+        const bool raw = unit_size[u] >= len;
+        const uint32_t f = xch[X_FLAG + j] | xch[X_FLAG + 64 + j];
+        const bool over = __ballot(f & 1u) != 0;
+        const bool bad = __ballot(f & 2u) != 0;
+        uint8_t* ud = out + unit_off[u];
+        if (!raw && over) {
+            if (pw == 0 && j == 0) {
+                const uint32_t k = atomicAdd(&ctl[1], 1u);
+                list[k] = SegItem{u, sg | (1u << 16)};
+            }
+        } else if (!raw) {
+            if (bad && pw == 0 && j == 0) atomicOr(err, 1u);
+            // pieces of lanes [32 pw, 32 pw + 32), in 16-byte chunks aligned in
+            // memory.  First the chunks wholly inside a piece, four lanes at a time
+            // (thread j: lane li0 + j / 16, chunks j mod 16, +16, ...); then the
+            // piece's first and last chunks where they are partial, one per thread
+            // (lane 32 pw + j / 2, its first chunk for even j, its last for odd j),
+            // in byte stores.
+            auto piece = [&](uint32_t li, uint32_t& e, uint8_t*& p0, int32_t& lead, uint32_t& endl) {
+                e = xch[X_LEN + li];
+                p0 = ud + xch[X_DST + li];
+                lead = (int32_t)(reinterpret_cast<uintptr_t>(p0) & 15u);
+                endl = li < 64 ? rb + R_SLOTS + li * fp.stride0 + fp.sl0
+                               : rb + R_SLOTS + 64 * fp.stride0 + (li - 64) * fp.stride1 + fp.sl1;
+            };
+            for (uint32_t li0 = 32 * pw; li0 < 32 * pw + 32; li0 += 4) {
+                uint32_t e, endl;
+                uint8_t* p0;
+                int32_t lead;
+                piece(li0 + (j >> 4), e, p0, lead, endl);
+                const uint32_t nch = e ? (uint32_t)((lead + (int32_t)e + 15) >> 4) : 0u;
+                for (uint32_t ch = j & 15u; ch < nch; ch += 16) {
+                    const int32_t q = 16 * (int32_t)ch - lead;  // piece offset of the chunk's first byte
+                    if (q >= 0 && q + 16 <= (int32_t)e)
+                        *reinterpret_cast<uint4*>(p0 + q) = lds_read16(lds8, (uint32_t)((int32_t)(endl - e) + q));
+                }
+            }
+            {
+                uint32_t e, endl;
+                uint8_t* p0;
+                int32_t lead;
+                piece(32 * pw + (j >> 1), e, p0, lead, endl);
+                const uint32_t nch = e ? (uint32_t)((lead + (int32_t)e + 15) >> 4) : 0u;
+                const uint32_t ch = (j & 1u) ? nch - 1 : 0u;
+                const int32_t q = 16 * (int32_t)ch - lead;
+                const bool part = nch && (q < 0 || q + 16 > (int32_t)e) && !((j & 1u) && nch == 1);
+                if (part) {
+                    const uint4 v = lds_read16(lds8, (uint32_t)((int32_t)(endl - e) + q));
+                    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int b = 0; b < 16; b++) {
+                        const int32_t x = q + b;
+                        if (x >= 0 && x < (int32_t)e) p0[x] = (uint8_t)(w4[b >> 2] >> (8 * (b & 3)));
+                    }
+                }
+            }
+            // the unit's zero-plane lanes (2 per column; the columns j with j mod
+            // S = s): their canonical streams, one lane at a time per packer wave.
+            // A partial last unit's (whose lanes have two lengths): by thread,
+            // from the canonical entries in memory, the columns j with j mod
+            // n_last = s.
+            constexpr uint32_t ZB1 = SPE == 2 ? 1u : 2u;  // zero bytes of a column: 0 and ZB1
+            if (u == n_full) {
+                if (pw == 0 && j % n_last == sg) {
+                    const uint32_t* cbytes = canon + 3 * (4 + cw);
+                    const uint32_t kf = len >> 8, r = len & 255u;
+#pragma unroll
+                    for (int hz2 = 0; hz2 < 2; hz2++) {
+                        const uint32_t lane = col + (hz2 ? ZB1 : 0u);
+                        const ckr_stream_header hz = hdrs[(uint64_t)u * 256 + lane];
+                        const uint32_t Kb = kf + ((lane < r) ? 1u : 0u);
+                        seg_copy_thread(ud + hz.buf_offset, cbytes + canon_index(canon, cw, Kb) * cw, hz.byte_count);
+                    }
+                }
+            }
+            const uint32_t nz = u == n_full ? 0u : 2 * ((64 - sg + S - 1) / S);
+            for (uint32_t z = pw; z < nz; z += NPK) {
+                const uint32_t lane = 4 * (sg + S * (z >> 1)) + ((z & 1) ? ZB1 : 0u);
+                const ckr_stream_header hz = hdrs[(uint64_t)u * 256 + lane];
+                const uint32_t e = hz.byte_count <= fp.canon_bytes ? hz.byte_count : 0u;
+                if (hz.byte_count > fp.canon_bytes && j == 0) atomicOr(err, 1u);
+                uint8_t* p0 = ud + hz.buf_offset;
+                const int32_t lead = (int32_t)(reinterpret_cast<uintptr_t>(p0) & 15u);
+                const uint32_t nch = e ? (uint32_t)((lead + (int32_t)e + 15) >> 4) : 0u;
+                for (uint32_t ch = j; ch < nch; ch += 64) {
+                    const int32_t q = 16 * (int32_t)ch - lead;
+                    const uint4 v = lds_read16(lds8, (uint32_t)((int32_t)FE_CBYTES + q));
+                    if (q >= 0 && q + 16 <= (int32_t)e) {
+                        *reinterpret_cast<uint4*>(p0 + q) = v;
+                    } else {
+                        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                        for (int b2 = 0; b2 < 16; b2++) {
+                            const int32_t x = q + b2;
+                            if (x >= 0 && x < (int32_t)e) p0[x] = (uint8_t)(w4[b2 >> 2] >> (8 * (b2 & 3)));
+                        }
+                    }
+                }
+            }
+        }
+        pbar_sync();  // every packer is done with the set
+        if (pw == 0) ws_signal(&pc.freed[s], 1u, j);
+    }
+}
+
+__global__ void seg_fast_reset_kernel(uint32_t* ctl) {
+    if (threadIdx.x < 2) ctl[threadIdx.x] = 0;
+}
+
 uint32_t encode_seg_segments(uint64_t unit) { return seg_count(unit); }
+
+uint64_t encode_seg_list_items(uint64_t n_units, uint64_t unit) { return n_units * seg_count(unit) + 1; }
+
+// Coder pairs of seg_fast_kernel: 2 when they fit the LDS limit, else 0 (one
+// pair per CU codes about 1.7x slower than two, and slower than
+// seg_code_kernel; that happens with slots sized for the worst case, when no
+// plane histograms come with the table).
+static uint32_t seg_fast_pairs(const FastEncParamsHost& p, uint32_t lds_limit) {
+    return ws_lds_bytes(2, p.canon_bytes, slot_stride(p.sl0), slot_stride(p.sl1)) <= lds_limit ? 2u : 0u;
+}
+
+uint32_t encode_seg_fast_lds_bytes(const FastEncParamsHost& p, uint32_t lds_limit) {
+    const uint32_t pairs = seg_fast_pairs(p, lds_limit);
+    return pairs ? ws_lds_bytes(pairs, p.canon_bytes, slot_stride(p.sl0), slot_stride(p.sl1)) : 0u;
+}
 
 hipError_t launch_encode_seg(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
                              uint32_t cw, bool escapes, uint2* rec, ckr_stream_header* hdrs, uint32_t* unit_size,
-                             uint64_t* unit_off, uint8_t* sidecar, uint8_t* out, uint32_t* aux, hipStream_t s) {
+                             uint64_t* unit_off, uint8_t* sidecar, uint8_t* out, uint32_t* aux,
+                             const FastEncParamsHost* fph, uint32_t lds_limit, uint32_t* ctl, void* list_v,
+                             hipStream_t s) {
     const uint32_t S = seg_count(g.unit);
     const uint32_t g1 = (uint32_t)((g.n_units + 3) / 4);
     // segments per pass-2 item: whole units while there are units enough to
@@ -1977,7 +2343,43 @@ hipError_t launch_encode_seg(const uint8_t* src, const EncodeGeom& g, const EncS
     const uint64_t G = std::max<uint64_t>(1, std::min<uint64_t>(S, g.n_units * S / 4096));
     const uint64_t items = g.n_units * ((S + G - 1) / G);
     const uint32_t g2 = (uint32_t)((items + 3) / 4);
+    SegItem* list = static_cast<SegItem*>(list_v);
+    // pass 2 on the fast encoder's waves: whole units of 256-row segments only
+    const uint32_t pairs = (fph && (g.unit & 65535u) == 0 && ctl && list) ? seg_fast_pairs(*fph, lds_limit) : 0u;
     hipError_t e;
+    int dev = 0, ncu = 0;
+    if (pairs) {
+        if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+        if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+    }
+    const bool partial = g.n_bytes % g.unit != 0;
+    const uint32_t n_full = (uint32_t)(g.n_units - (partial ? 1 : 0));
+    // segments of the partial last unit (rows of up to 256 bytes, 256 rows each)
+    const uint64_t last_len = g.n_bytes - (g.n_units - 1) * g.unit;
+    const uint32_t n_last =
+        partial ? (uint32_t)((((last_len + 255) / 256) + SEG_ROWS - 1) / SEG_ROWS) : 0u;
+    FastEncParams fp{};
+    if (pairs) {
+        fp.sl0 = fph->sl0; fp.sl1 = fph->sl1; fp.cw = fph->cw; fp.canon_bytes = fph->canon_bytes;
+        fp.stride0 = slot_stride(fph->sl0); fp.stride1 = slot_stride(fph->sl1);
+    }
+    auto run_fast = [&](auto kern, uint32_t nthreads) -> hipError_t {
+        const void* kf = reinterpret_cast<const void*>(kern);
+        const uint32_t lb = ws_lds_bytes(pairs, fp.canon_bytes, fp.stride0, fp.stride1);
+        hipError_t r = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb);
+        if (r != hipSuccess) return r;
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nthreads, lb) != hipSuccess || per_cu < 1)
+            per_cu = 1;
+        const uint64_t need = ((uint64_t)n_full * S + n_last + pairs - 1) / pairs;
+        const uint32_t grid = (uint32_t)std::max<uint64_t>(
+            1, std::min<uint64_t>(need, (uint64_t)per_cu * (uint64_t)std::max(ncu, 1)));
+        CKR_LAUNCH("seg_fast_kernel", s,
+                   kern<<<grid, nthreads, lb, s>>>(src, g, d_enc, canon, cw, S, n_full, n_last, fp, rec, hdrs, unit_size,
+                                                   unit_off, sidecar, out, ctl, list, aux));
+        return hipGetLastError();
+    };
+#define CKR_SEG_FAST(SPE_, ESC_) run_fast(seg_fast_kernel<SPE_, ESC_, 2, ENC_NPK>, 128u * (2 + ENC_NPK))
 #define CKR_SEG(SPE_, ESC_)                                                                                         \
     do {                                                                                                            \
         CKR_LAUNCH("seg_size_kernel", s, seg_size_kernel<SPE_, ESC_><<<g1, 256, 0, s>>>(src, g, d_enc, canon, cw,    \
@@ -1985,11 +2387,26 @@ hipError_t launch_encode_seg(const uint8_t* src, const EncodeGeom& g, const EncS
         if ((e = hipGetLastError()) != hipSuccess) return e;                                                        \
         CKR_LAUNCH("unit_scan_kernel", s, unit_scan_kernel<<<1, 1024, 0, s>>>(unit_size, 0, g.n_units, unit_off));  \
         if ((e = hipGetLastError()) != hipSuccess) return e;                                                        \
-        if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(seg_code_kernel<SPE_, ESC_>),                    \
+        if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(seg_code_kernel<SPE_, ESC_, false>),             \
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)SEG_LDS)) != hipSuccess)      \
             return e;                                                                                               \
-        CKR_LAUNCH("seg_code_kernel", s, seg_code_kernel<SPE_, ESC_><<<g2, 256, SEG_LDS, s>>>(src, g, d_enc, canon, \
-                   cw, S, (uint32_t)G, rec, hdrs, unit_size, unit_off, sidecar, out, aux));                         \
+        if ((e = hipFuncSetAttribute(reinterpret_cast<const void*>(seg_code_kernel<SPE_, ESC_, true>),              \
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)SEG_LDS)) != hipSuccess)      \
+            return e;                                                                                               \
+        if (!pairs) {                                                                                               \
+            CKR_LAUNCH("seg_code_kernel", s, seg_code_kernel<SPE_, ESC_, false><<<g2, 256, SEG_LDS, s>>>(src, g,   \
+                       d_enc, canon, cw, S, (uint32_t)G, rec, hdrs, unit_size, unit_off, sidecar, out, aux,         \
+                       nullptr, nullptr));                                                                          \
+            return hipGetLastError();                                                                               \
+        }                                                                                                           \
+        CKR_LAUNCH("seg_fast_reset_kernel", s, seg_fast_reset_kernel<<<1, 64, 0, s>>>(ctl));                        \
+        if ((e = hipGetLastError()) != hipSuccess) return e;                                                        \
+        if ((e = CKR_SEG_FAST(SPE_, ESC_)) != hipSuccess) return e;                                                 \
+        /* the listed items (usually none): a resident grid whose waves stride over the list */                     \
+        const uint32_t gl = (uint32_t)std::max(ncu, 1) * 3u;                                                        \
+        CKR_LAUNCH("seg_code_kernel.list", s, seg_code_kernel<SPE_, ESC_, true><<<gl, 256, SEG_LDS, s>>>(src, g,    \
+                   d_enc, canon, cw, S, (uint32_t)G, rec, hdrs, unit_size, unit_off, sidecar, out, aux, list,       \
+                   ctl + 1));                                                                                       \
         return hipGetLastError();                                                                                   \
     } while (0)
     if (g.spe == 2) {
@@ -1999,6 +2416,7 @@ hipError_t launch_encode_seg(const uint8_t* src, const EncodeGeom& g, const EncS
     if (escapes) CKR_SEG(1, true);
     CKR_SEG(1, false);
 #undef CKR_SEG
+#undef CKR_SEG_FAST
 }
 
 // ------------------------------------------------------------------ rANS decode

@@ -53,6 +53,11 @@ CASES = [
     ("f32_expavgsq_128k_units", dg.F32, 32832 * 4 + 100, 131328, lambda n: dg.exp_avg_sq(n, 17)),
     ("bf16_1mib_units", dg.BF16, 524288 * 2 + 1111, 1 << 20, lambda n: dg.normal_bf16(n, 0.02, 18)),
     ("bf16_256k_one_unit", dg.BF16, 131072, 262144, lambda n: dg.normal_bf16(n, 0.02, 19)),
+    # 1 MiB units of random bits (passthrough units) and an adversarial mix at
+    # 256 KiB units, whole units and a partial last one
+    ("random_bits_f32_1mib", dg.F32, 262144 * 2 + 333, 1 << 20,
+     lambda n: np.random.default_rng(20).integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32).view(np.float32)),
+    ("adversarial_f32_256k", dg.F32, 65536 * 3 + 999, 262144, lambda n: dg.adversarial_f32(n, 21, (70000, 140000))),
     ("bf16_partial_units", dg.BF16, 3 * 512 + 1, 1024, lambda n: dg.normal_bf16(n, 0.02, 16)),
     ("tiny_f32_1", dg.F32, 1, 65536, lambda n: np.array([1.5], np.float32)),
     ("tiny_bf16_3", dg.BF16, 3, 0, lambda n: dg.normal_bf16(n, 0.02, 12)),
