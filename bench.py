@@ -328,8 +328,11 @@ def stream_bench(shard, ck, torch, dev, unit, steps, slice_bytes):
             per = max(unit // es, (slice_bytes // unit) * (unit // es))  # elements per slice, whole units
             a, b = ev(), ev()
             a.record()
-            hist = ck.byte_histogram(t, tag)
-            table, tsum = ck.build_table(hist.cpu().numpy().view(np.uint32))
+            # the masked histogram and the two live planes' (which size the
+            # two-pass encoder's slots for the slices)
+            hh = ck.byte_histogram(t, tag, planes=True).cpu().numpy().view(np.uint32)
+            table, tsum = ck.build_table(hh[:256])
+            planes = hh[256:] if ck.sidecar_bytes_per_elem(tag) else None
             b.record()
             torch.cuda.synchronize()
             enc_s += a.elapsed_time(b) / 1e3
@@ -345,7 +348,7 @@ def stream_bench(shard, ck, torch, dev, unit, steps, slice_bytes):
                 src = t[s0:s0 + m]
                 a, b, c = ev(), ev(), ev()
                 a.record()
-                r = encs[m].encode(src, table)
+                r = encs[m].encode(src, table, planes=planes)
                 b.record()
                 bad = decs[m].decode(r.data, r.headers, r.unit_offsets, r.table, r.sidecar, window, check=True)
                 c.record()

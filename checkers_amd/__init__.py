@@ -25,8 +25,10 @@ CKR_OK, CKR_E_INVALID, CKR_E_HIP, CKR_E_CAPACITY, CKR_E_TABLE, CKR_E_CORRUPT = 0
 
 EXPORTED = [  # every symbol include/checkers_amd.h declares
     "ckr_last_error", "ckr_version", "ckr_element_size", "ckr_sidecar_bytes_per_elem",
-    "ckr_extract_mantissa", "ckr_byte_histogram", "ckr_byte_histogram_raw", "ckr_build_table",
+    "ckr_extract_mantissa", "ckr_byte_histogram", "ckr_byte_histogram_raw", "ckr_byte_histogram_planes",
+    "ckr_build_table",
     "ckr_num_units", "ckr_encode_max_output_bytes", "ckr_encode_workspace_bytes", "ckr_encode",
+    "ckr_encode_planes",
     "ckr_compress", "ckr_compress_many", "ckr_decode_workspace_bytes", "ckr_decode", "ckr_decode_noalloc",
     "ckr_analyze_workspace_bytes",
     "ckr_analyze", "ckr_profile_begin", "ckr_profile_end", "ckr_set_fast_paths",
@@ -120,11 +122,13 @@ def lib():
         "ckr_extract_mantissa": (i32, [vp, u64, i32, vp, vp, vp]),
         "ckr_byte_histogram": (i32, [vp, u64, i32, vp, vp]),
         "ckr_byte_histogram_raw": (i32, [vp, u64, vp, vp]),
+        "ckr_byte_histogram_planes": (i32, [vp, u64, i32, vp, vp]),
         "ckr_build_table": (i32, [vp, i32, vp, vp]),
         "ckr_num_units": (u64, [u64, i32, u64]),
         "ckr_encode_max_output_bytes": (u64, [u64, i32, u64]),
         "ckr_encode_workspace_bytes": (u64, [u64, i32, u64]),
         "ckr_encode": (i32, [vp, u64, i32, vp, u64, vp, u64, vp, vp, vp, vp, u64, vp, vp]),
+        "ckr_encode_planes": (i32, [vp, u64, i32, vp, vp, u64, vp, u64, vp, vp, vp, vp, u64, vp, vp]),
         "ckr_compress": (i32, [vp, u64, i32, u64, i32, vp, u64, vp, vp, vp, vp, u64, vp, vp, vp]),
         "ckr_compress_many": (i32, [vp, u64, u64, i32, vp]),
         "ckr_decode_workspace_bytes": (u64, [u64, i32, u64]),
@@ -297,14 +301,22 @@ class Encoder:
         if src.numel() * src.element_size() < self.n_bytes:
             raise CkrError(CKR_E_INVALID, f"source holds {src.numel() * src.element_size()} bytes, need {self.n_bytes}")
 
-    def encode(self, src, table, stream=None, sync_total=True):
+    def encode(self, src, table, stream=None, sync_total=True, planes=None):
+        """ckr_encode under a given table; with planes (512 host uint32 words, the
+        live-plane histograms of byte_histogram(..., planes=True)), ckr_encode_planes."""
         self._check_src(src)
         tot = ctypes.c_uint64(0)
-        _check(lib().ckr_encode(
-            src.data_ptr(), self.n_elems, self.dtype, table.ptr, self.unit_bytes,
-            self.out.data_ptr(), self.out_cap, self.headers.data_ptr(), self.unit_offsets.data_ptr(),
-            self.sidecar.data_ptr() if self.sidecar is not None else None,
-            self.ws.data_ptr(), self.ws_bytes, ctypes.byref(tot) if sync_total else None, _stream(stream)))
+        tail = (self.out.data_ptr(), self.out_cap, self.headers.data_ptr(), self.unit_offsets.data_ptr(),
+                self.sidecar.data_ptr() if self.sidecar is not None else None,
+                self.ws.data_ptr(), self.ws_bytes, ctypes.byref(tot) if sync_total else None, _stream(stream))
+        if planes is None:
+            _check(lib().ckr_encode(src.data_ptr(), self.n_elems, self.dtype, table.ptr, self.unit_bytes, *tail))
+        else:
+            pl = np.ascontiguousarray(planes, dtype=np.uint32)
+            if pl.size != 512:
+                raise CkrError(CKR_E_INVALID, "encode: planes must hold 512 words")
+            _check(lib().ckr_encode_planes(src.data_ptr(), self.n_elems, self.dtype, table.ptr,
+                                           pl.ctypes.data_as(ctypes.c_void_p), self.unit_bytes, *tail))
         return Encoded(self.out, self.headers, self.unit_offsets, self.sidecar,
                        tot.value if sync_total else None, self.n_elems, self.dtype, self.unit_bytes, table)
 
@@ -356,12 +368,15 @@ def compress_many(encoders, srcs, ensure_full_alphabet=False, stream=None):
             for jb, e, t in zip(jobs, encoders, tables)]
 
 
-def byte_histogram(src, dtype, n_elems=None, stream=None):
-    """256-bin histogram of the masked byte stream of `src` (torch device tensor)."""
+def byte_histogram(src, dtype, n_elems=None, stream=None, planes=False):
+    """256-bin histogram of the masked byte stream of `src` (torch device tensor);
+    with planes=True, 768 bins: that histogram, then the two live planes'
+    (ckr_byte_histogram_planes)."""
     torch = _torch()
     n = _n_elems(src, dtype, n_elems)
-    h = torch.empty(256, dtype=torch.int32, device=src.device)
-    _check(lib().ckr_byte_histogram(src.data_ptr(), n, dtype, h.data_ptr(), _stream(stream)))
+    h = torch.empty(768 if planes else 256, dtype=torch.int32, device=src.device)
+    f = lib().ckr_byte_histogram_planes if planes else lib().ckr_byte_histogram
+    _check(f(src.data_ptr(), n, dtype, h.data_ptr(), _stream(stream)))
     return h
 
 

@@ -563,6 +563,21 @@ int ckr_byte_histogram(const void* d_src, uint64_t n_elems, int dtype, uint32_t*
     return CKR_OK;
 }
 
+int ckr_byte_histogram_planes(const void* d_src, uint64_t n_elems, int dtype, uint32_t* d_hist, void* stream) {
+    if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
+    if (!d_hist || (n_elems && !d_src)) return fail(CKR_E_INVALID, "[ckr] null pointer");
+    const int es = ckr_element_size(dtype);
+    if (!aligned_to(d_src, es) || !aligned_to(d_hist, 4))
+        return fail(CKR_E_INVALID, "[ckr] source must be aligned to the element size, histogram to 4 bytes");
+    int rc;
+    if ((rc = check_buffer(d_src, n_elems * es, "source")) || (rc = check_buffer(d_hist, 768 * 4, "histogram")))
+        return rc;
+    const int spe = ckr_sidecar_bytes_per_elem(dtype);
+    CKR_HIP(ckr::launch_masked_hist(static_cast<const uint8_t*>(d_src), n_elems * (uint64_t)es, es, spe, d_hist,
+                                    spe ? d_hist + 256 : nullptr, (hipStream_t)stream));
+    return CKR_OK;
+}
+
 int ckr_byte_histogram_raw(const void* d_bytes, uint64_t n_bytes, uint32_t* d_hist, void* stream) {
     return ckr_byte_histogram(d_bytes, n_bytes, CKR_I8, d_hist, stream);
 }
@@ -674,7 +689,7 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
                 uint8_t* d_out, uint64_t out_capacity, ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
                 uint8_t* d_sidecar, void* d_workspace, uint64_t workspace_bytes, uint64_t* h_total_out,
                 const uint32_t* h_planes, void* stream, const AfterLaunch* after_launch = nullptr,
-                EncodeDeferred* defer = nullptr) {
+                EncodeDeferred* defer = nullptr, bool planes_size_only = false) {
     if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
     ckr::EncodeGeom g;
     if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
@@ -714,8 +729,9 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
 
     // escapes are possible unless the data's own live-plane histograms show
     // every symbol it contains has a slot
+    // (planes_size_only: the histograms are a caller's, used for slot sizes only)
     bool escapes = true;
-    if (h_planes) {
+    if (h_planes && !planes_size_only) {
         escapes = false;
         for (int s2 = 0; s2 < 256; s2++)
             if ((h_planes[s2] || h_planes[256 + s2]) && !h_table->norm_freq[s2]) escapes = true;
@@ -925,6 +941,27 @@ int ckr_encode(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_ta
     if ((rc = st.make(d_src, g.n_bytes, s))) return rc;
     rc = encode_impl(st.p, n_elems, dtype, h_table, unit_bytes, d_out, out_capacity, d_headers, d_unit_offsets,
                      d_sidecar, d_workspace, workspace_bytes, h_total_out, nullptr, stream);
+    st.release(s);
+    return rc;
+}
+
+int ckr_encode_planes(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table,
+                      const uint32_t* h_planes, uint64_t unit_bytes, uint8_t* d_out, uint64_t out_capacity,
+                      ckr_stream_header* d_headers, uint64_t* d_unit_offsets, uint8_t* d_sidecar, void* d_workspace,
+                      uint64_t workspace_bytes, uint64_t* h_total_out, void* stream) {
+    if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
+    ckr::EncodeGeom g;
+    if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
+    if (!h_table || !d_unit_offsets) return fail(CKR_E_INVALID, "[ckr] null table or offsets");
+    int rc = check_encode_args(d_src, g, n_elems, d_out, out_capacity, d_headers, d_unit_offsets, d_sidecar, d_workspace,
+                               workspace_bytes);
+    if (rc) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    Staged st;
+    if ((rc = st.make(d_src, g.n_bytes, s))) return rc;
+    rc = encode_impl(st.p, n_elems, dtype, h_table, unit_bytes, d_out, out_capacity, d_headers, d_unit_offsets,
+                     d_sidecar, d_workspace, workspace_bytes, h_total_out, g.spe ? h_planes : nullptr, stream,
+                     nullptr, nullptr, true);
     st.release(s);
     return rc;
 }

@@ -117,6 +117,14 @@ CKR_API int ckr_byte_histogram(const void* d_src, uint64_t n_elems, int dtype,
 /* Histogram of an arbitrary byte buffer (d_hist overwritten). */
 CKR_API int ckr_byte_histogram_raw(const void* d_bytes, uint64_t n_bytes,
                                    uint32_t* d_hist, void* stream);
+/* No counterpart in the reference (its tensors are encoded whole): the same
+ * histogram into d_hist[0..256), and the histograms of the two live byte
+ * planes (byte 2 or 1 of each 32-bit column, and byte 3) into d_hist[256..512)
+ * and d_hist[512..768) (not written for dtypes without a sidecar).  With them,
+ * ckr_encode_planes sizes the two-pass encoder's LDS slots when a large tensor
+ * is encoded in slices under its whole-tensor table. */
+CKR_API int ckr_byte_histogram_planes(const void* d_src, uint64_t n_elems, int dtype,
+                                      uint32_t* d_hist, void* stream);
 
 /* ---- host: histogram → table, same arithmetic and std::sort tie order as the
  * reference.  Returns CKR_OK; *h_table_sum receives sum(norm_freq) (4096 for a
@@ -154,6 +162,16 @@ CKR_API int ckr_encode(const void* d_src, uint64_t n_elems, int dtype,
                        uint8_t* d_sidecar,
                        void* d_workspace, uint64_t workspace_bytes,
                        uint64_t* h_total_out, void* stream);
+/* No counterpart in the reference: ckr_encode with h_planes (host, 512 words:
+ * d_hist[256..768) of ckr_byte_histogram_planes, for this data or for a tensor
+ * it is a slice of), used only to size the encoders' LDS slots; the output is
+ * ckr_encode's, byte for byte, whatever h_planes holds. */
+CKR_API int ckr_encode_planes(const void* d_src, uint64_t n_elems, int dtype,
+                              const ckr_freq_table* h_table, const uint32_t* h_planes,
+                              uint64_t unit_bytes, uint8_t* d_out, uint64_t out_capacity,
+                              ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
+                              uint8_t* d_sidecar, void* d_workspace, uint64_t workspace_bytes,
+                              uint64_t* h_total_out, void* stream);
 
 /* ---- full tensor compression as ANSCompressor::compress_tensor does it for a
  * singleton (histogram → host table → encode), in one call.  The table built

@@ -342,6 +342,47 @@ def test_decode_counts_corrupted_lanes(unit, where, gpu):
     assert bad >= 1
 
 
+@pytest.mark.parametrize("tag,unit", [(dg.F32, 1 << 20), (dg.BF16, 1 << 20), (dg.F32, 65536)])
+def test_encode_planes_matches_encode(tag, unit, paths, gpu):
+    """ckr_byte_histogram_planes: the masked histogram and the two live planes'
+    (checked against numpy); ckr_encode_planes gives ckr_encode's bytes, and a
+    slice of whole units under the whole tensor's table gives the whole
+    encode's first units (units are independent given the table)."""
+    import torch
+    ck = _ck()
+    es = 4 if tag == dg.F32 else 2
+    n = (unit // es) * 3 + 771
+    print(f"[case] encode_planes tag={tag} unit={unit}", flush=True)
+    raw = dg.normal_f32(n, 1e-3, 40) if tag == dg.F32 else dg.normal_bf16(n, 0.02, 41)
+    t = _to_dev(raw, gpu)
+    hh = ck.byte_histogram(t, tag, n_elems=n, planes=True).cpu().numpy().view(np.uint32)
+    masked, _ = oc.extract_mantissa(raw, n, tag)
+    mb = np.frombuffer(masked.tobytes(), np.uint8)
+    fl = 2 if tag == dg.F32 else 1
+    assert np.array_equal(hh[:256], oc.byte_hist(masked))
+    assert np.array_equal(hh[256:512], np.bincount(mb[fl::4], minlength=256))
+    assert np.array_equal(hh[512:], np.bincount(mb[3::4], minlength=256))
+    assert np.array_equal(hh[:256], ck.byte_histogram(t, tag, n_elems=n).cpu().numpy().view(np.uint32))
+    table, _ = ck.build_table(hh[:256])
+    e1 = ck.Encoder(n, tag, unit, device=gpu).encode(t, table)
+    e2 = ck.Encoder(n, tag, unit, device=gpu).encode(t, table, planes=hh[256:])
+    torch.cuda.synchronize()
+    assert e1.total == e2.total
+    assert torch.equal(e1.data[: e1.total], e2.data[: e2.total])
+    assert torch.equal(e1.headers, e2.headers) and torch.equal(e1.unit_offsets, e2.unit_offsets)
+    assert torch.equal(e1.sidecar, e2.sidecar)
+    m = 2 * unit // es
+    e3 = ck.Encoder(m, tag, unit, device=gpu).encode(t[: m * es], table, planes=hh[256:])
+    torch.cuda.synchronize()
+    off = e1.unit_offsets.cpu().numpy()
+    assert e3.total == int(off[2])
+    assert torch.equal(e3.data[: e3.total], e1.data[: e3.total])
+    assert torch.equal(e3.headers.reshape(-1), e1.headers.reshape(-1)[: e3.headers.numel()])
+    assert np.array_equal(e3.unit_offsets.cpu().numpy(), off[:3])
+    spe = oc.SPE[tag]
+    assert torch.equal(e3.sidecar[: m * spe], e1.sidecar[: m * spe])
+
+
 @pytest.mark.parametrize("unit", [65536, 1 << 20])
 def test_compress_many_matches_single_calls(unit, paths, gpu):
     """ckr_compress_many (histograms overlapped with the previous encode) gives
