@@ -311,6 +311,32 @@ def repair_leg(ck, torch, dev):
                               algorithmic_bytes=tot_bytes_rounds))
 
 
+def copy_ceiling(torch, dev, nbytes=4 << 30, reps=10, batches=3):
+    """HBM rate of a plain device-to-device copy (the HIP runtime's copy kernel
+    under torch's copy_), read + written bytes per second, best of `batches`
+    batches of `reps` copies: the practical ceiling for traffic that mixes reads
+    and writes about evenly, as the encode and decode do."""
+    a = torch.empty(nbytes // 4, dtype=torch.int32, device=dev).fill_(7)
+    b = torch.empty_like(a)
+    for _ in range(2):
+        b.copy_(a)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    runs = []
+    for _ in range(batches):
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            b.copy_(a)
+        e1.record()
+        torch.cuda.synchronize()
+        runs.append(e0.elapsed_time(e1) / 1e3 / reps)
+    s = min(runs)
+    del a, b
+    return dict(GBps=round(2 * nbytes / s / 1e9, 2), bytes_per_copy=2 * nbytes, ms=round(s * 1e3, 4),
+                runs_ms=[round(r * 1e3, 4) for r in runs],
+                kind="torch copy_ of a 4 GiB buffer (device-to-device, read + write), best of 3 x 10")
+
+
 def stream_bench(shard, ck, torch, dev, unit, steps, slice_bytes):
     """Config 5: histogram + table per tensor, then encode/decode slice by slice
     (reused buffers), every slice checked bit-exact against its source.
@@ -514,6 +540,17 @@ def main():
             if k in prof:
                 kernels[k]["achieved_GBps"] = round(alg[k] / (prof[k][1] / 1e3) / 1e9, 2)
 
+    # the encode reads the tensors twice (histogram, then the coder); its whole
+    # HBM traffic and the decode's against a plain copy's rate
+    copy = copy_ceiling(torch, dev)
+    enc_traffic = 2 * n_in + S + C + H
+    dec_traffic = C + S + H + n_in
+    copy.update(encode_traffic_bytes=enc_traffic, decode_traffic_bytes=dec_traffic,
+                encode_GBps=round(enc_traffic / enc_wall / 1e9, 2), decode_GBps=round(dec_traffic / dec_wall / 1e9, 2))
+    copy.update(encode_frac=round(copy["encode_GBps"] / copy["GBps"], 4),
+                decode_frac=round(copy["decode_GBps"] / copy["GBps"], 4))
+    log(f"[bench] copy ceiling {copy['GBps']} GB/s; encode {copy['encode_frac']}, decode {copy['decode_frac']} of it")
+
     analyze = None if args.no_analyze else analyzer_leg(shard, ck, torch, args.steps)
     repair = None if args.no_repair else repair_leg(ck, torch, dev)
 
@@ -568,6 +605,7 @@ def main():
         "analyze": analyze,
         "repair": repair,
         "roofline": roof,
+        "copy_ceiling": copy,
         "cpu_baseline": cpu,
         "kernels": kernels,
     }
@@ -589,6 +627,14 @@ def run_streamed(args, shard, ck, torch, dev, unit, n_in):
     enc_s, dec_s, C, S, H, n_units, ok = stream_bench(shard, ck, torch, dev, unit, steps, args.slice_gib << 30)
     log(f"[bench] streamed: encode {enc_s * 1e3:.1f} ms, decode {dec_s * 1e3:.1f} ms, roundtrip={ok}")
     B = n_in + S + C + H
+    # the streamed encode reads each slice three times (the tensor's histogram,
+    # then the two passes of 1 MiB units)
+    copy = copy_ceiling(torch, dev)
+    enc_traffic, dec_traffic = 3 * n_in + S + C + H, B
+    copy.update(encode_traffic_bytes=enc_traffic, decode_traffic_bytes=dec_traffic,
+                encode_GBps=round(enc_traffic / enc_s / 1e9, 2), decode_GBps=round(dec_traffic / dec_s / 1e9, 2))
+    copy.update(encode_frac=round(copy["encode_GBps"] / copy["GBps"], 4),
+                decode_frac=round(copy["decode_GBps"] / copy["GBps"], 4))
     out = {
         "metric": METRIC, "value": round(n_in / enc_s / 1e9, 3), "unit": "GB/s", "n_gpus": 1,
         "steps": steps, "warmup": max(args.warmup, 1), "ms_per_step": round(enc_s * 1e3, 3),
@@ -605,7 +651,7 @@ def run_streamed(args, shard, ck, torch, dev, unit, n_in):
         "compressed_bytes": C, "sidecar_bytes": S, "header_bytes": H,
         "ans_ratio": round(n_in / C, 4), "disk_ratio": round(n_in / (C + S), 4),
         "device_ratio": round(n_in / (C + S + H), 4), "container_ratio": None, "roundtrip_bit_exact": ok,
-        "roofline": None, "cpu_baseline": None, "kernels": {},
+        "roofline": None, "copy_ceiling": copy, "cpu_baseline": None, "kernels": {},
     }
     print(json.dumps(out), flush=True)
     if not ok:

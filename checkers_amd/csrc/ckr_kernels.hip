@@ -2559,8 +2559,13 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
 // aligned, the units at its end, streams running past their end) are
 // assembled byte by byte, with zeros outside the buffer.
 static constexpr uint32_t DF_WAVES = 8;
+static constexpr uint32_t DF_AHEAD = 2;  // groups of sidecar words loaded ahead of the group decoded
+static constexpr uint32_t DF_CH_LOG = 6;  // chunk bytes 64 (32 also keeps every read behind the writes)
+static constexpr uint32_t DF_CH = 1u << DF_CH_LOG;
+static constexpr uint32_t DF_CQ = DF_CH / 16;  // 16-byte loads per chunk
+static constexpr uint32_t DF_RING_ROWS = DF_CH / 2;  // two chunks of DF_CH / 4 dwords
 static constexpr uint32_t DF_TAB_BYTES = 4096 * 4;
-static constexpr uint32_t DF_RING_BYTES = 33 * 256;  // 32 rows + the copy of row 0
+static constexpr uint32_t DF_RING_BYTES = (DF_RING_ROWS + 1) * 256;  // the rows + the copy of row 0
 static constexpr uint32_t DF_WAVE_BYTES = 2 * DF_RING_BYTES;
 
 // The dword at byte offset o (a multiple of 4) of the data buffer.
@@ -2576,10 +2581,10 @@ struct DfLane {
     uint32_t last;     // chunk of the stream's last byte: no chunk after it is fetched
     uint32_t tb;       // LDS address of this lane's ring column (row 0)
     bool pend;         // chunk ch + 1 is in flight in c[], to be written at the end of this group
-    uint4 c0, c1, c2, c3;
+    uint4 c[DF_CQ];
 };
 
-// Where a unit's chunks come from: chunk k is the 64 bytes at ua + 64 k; the
+// Where a unit's chunks come from: chunk k is the DF_CH bytes at ua + DF_CH k; the
 // chunks k_lo .. k_lo + n_in - 1 lie wholly inside the data buffer [d0, d0 + dlen).
 struct DfSrc {
     const uint8_t* d0;
@@ -2604,35 +2609,35 @@ __device__ __attribute__((noinline)) uint4 df_load16_clipped(const uint8_t* d0, 
     return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// Chunk k of the unit: four 16-byte loads, or, for a chunk that is not wholly
+// Chunk k of the unit: DF_CQ 16-byte loads, or, for a chunk that is not wholly
 // inside the buffer, its bytes one at a time with zeros outside.
-__device__ __forceinline__ void df_fetch(const DfSrc& sr, uint32_t k, uint4& c0, uint4& c1, uint4& c2, uint4& c3) {
-    const int64_t a = sr.ua + ((int64_t)k << 6);
+__device__ __forceinline__ void df_fetch(const DfSrc& sr, uint32_t k, uint4 (&c)[DF_CQ]) {
+    const int64_t a = sr.ua + ((int64_t)k << DF_CH_LOG);
     if (k - sr.k_lo < sr.n_in) {
         const uint4* q = reinterpret_cast<const uint4*>(sr.d0 + a);
-        c0 = q[0]; c1 = q[1]; c2 = q[2]; c3 = q[3];
+#pragma unroll
+        for (uint32_t i = 0; i < DF_CQ; i++) c[i] = q[i];
     } else {
-        c0 = df_load16_clipped(sr.d0, sr.dlen, a);
-        c1 = df_load16_clipped(sr.d0, sr.dlen, a + 16);
-        c2 = df_load16_clipped(sr.d0, sr.dlen, a + 32);
-        c3 = df_load16_clipped(sr.d0, sr.dlen, a + 48);
+#pragma unroll
+        for (uint32_t i = 0; i < DF_CQ; i++) c[i] = df_load16_clipped(sr.d0, sr.dlen, a + 16 * i);
     }
 }
 
-// Writes chunk k into ring slot k & 1 (rows 16s..16s+15; slot 0 also into row 32).
-__device__ __forceinline__ void df_put(uint8_t* lds8, uint32_t tb, uint32_t k, const uint4& c0, const uint4& c1,
-                                       const uint4& c2, const uint4& c3) {
-    uint32_t* w = reinterpret_cast<uint32_t*>(lds8 + tb + ((k & 1u) << 12));
-    w[0] = c0.x; w[64] = c0.y; w[128] = c0.z; w[192] = c0.w;
-    w[256] = c1.x; w[320] = c1.y; w[384] = c1.z; w[448] = c1.w;
-    w[512] = c2.x; w[576] = c2.y; w[640] = c2.z; w[704] = c2.w;
-    w[768] = c3.x; w[832] = c3.y; w[896] = c3.z; w[960] = c3.w;
-    if ((k & 1u) == 0) w[2048] = c0.x;
+// Writes chunk k into ring slot k & 1 (rows DF_CH/4 s .. DF_CH/4 s + DF_CH/4 - 1;
+// slot 0 also into row DF_RING_ROWS).
+__device__ __forceinline__ void df_put(uint8_t* lds8, uint32_t tb, uint32_t k, const uint4 (&c)[DF_CQ]) {
+    uint32_t* w = reinterpret_cast<uint32_t*>(lds8 + tb + ((k & 1u) << (DF_CH_LOG + 6)));
+#pragma unroll
+    for (uint32_t i = 0; i < DF_CQ; i++) {
+        w[256 * i] = c[i].x; w[256 * i + 64] = c[i].y; w[256 * i + 128] = c[i].z; w[256 * i + 192] = c[i].w;
+    }
+    if ((k & 1u) == 0) w[64 * DF_RING_ROWS] = c[0].x;
 }
 
 // The 4 stream bytes at p, byte p in bits 31..24.
 __device__ __forceinline__ uint32_t df_window(const DfLane& d, const uint8_t* lds8) {
-    const uint32_t* r = reinterpret_cast<const uint32_t*>(lds8 + d.tb + (__builtin_amdgcn_ubfe(d.p8, 5, 5) << 8));
+    const uint32_t* r = reinterpret_cast<const uint32_t*>(
+        lds8 + d.tb + (__builtin_amdgcn_ubfe(d.p8, 5, DF_CH_LOG - 1) << 8));
     const uint32_t d0 = r[0], d1 = r[64];
     return __builtin_amdgcn_perm(0u, __builtin_amdgcn_alignbit(d1, d0, d.p8), 0x00010203u);
 }
@@ -2658,11 +2663,11 @@ __device__ __forceinline__ uint32_t df_sym(uint32_t& x, uint32_t& w, uint32_t& s
 // End of a group: write the chunk fetched at the end of the previous group,
 // then move on if p has reached the next chunk and fetch the one after it.
 __device__ __forceinline__ void df_step(DfLane& d, uint8_t* lds8, const DfSrc& sr) {
-    if (d.pend) df_put(lds8, d.tb, d.ch + 1u, d.c0, d.c1, d.c2, d.c3);
-    const bool adv = (d.p8 >> 9) > d.ch;
+    if (d.pend) df_put(lds8, d.tb, d.ch + 1u, d.c);
+    const bool adv = (d.p8 >> (DF_CH_LOG + 3)) > d.ch;
     d.ch += adv ? 1u : 0u;
     d.pend = adv && d.ch + 1u <= d.last;
-    if (d.pend) df_fetch(sr, d.ch + 1u, d.c0, d.c1, d.c2, d.c3);
+    if (d.pend) df_fetch(sr, d.ch + 1u, d.c);
 }
 
 template <int SPE>
@@ -2807,7 +2812,7 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
         sr.ua = (int64_t)ua - (int64_t)d0;
         sr.k_lo = ua >= d0 ? 0u : 1u;
         {   // chunks [k_lo, k_end) end at or before d1
-            const int64_t k_end = min<int64_t>(((int64_t)d1 - (int64_t)ua) >> 6, 0x40000000ll);
+            const int64_t k_end = min<int64_t>(((int64_t)d1 - (int64_t)ua) >> DF_CH_LOG, 0x40000000ll);
             sr.n_in = k_end > (int64_t)sr.k_lo ? (uint32_t)(k_end - (int64_t)sr.k_lo) : 0u;
         }
         uint32_t nbad = 0;
@@ -2823,8 +2828,8 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
                 d.p8 = p << 3;
                 const uint32_t pe = p + (ok ? h.byte_count : 0u);
                 ge8 = pe << 3;
-                d.ch = p >> 6;
-                d.last = pe > p ? (pe - 1u) >> 6 : d.ch;
+                d.ch = p >> DF_CH_LOG;
+                d.last = pe > p ? (pe - 1u) >> DF_CH_LOG : d.ch;
                 d.pend = false;
             };
             init(da, gea8, FL);
@@ -2832,12 +2837,12 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
             da.tb = tb0;
             db.tb = tb0 + DF_RING_BYTES;
             // the first two chunks of each stream (the second only if the stream reaches it)
-            uint4 a0, a1, a2, a3, a4, a5, a6, a7, b0, b1, b2, b3, b4, b5, b6, b7;
-            df_fetch(sr, da.ch, a0, a1, a2, a3);
-            df_fetch(sr, db.ch, b0, b1, b2, b3);
+            uint4 ca[DF_CQ], cb[DF_CQ];
+            df_fetch(sr, da.ch, ca);
+            df_fetch(sr, db.ch, cb);
             const bool a2nd = da.ch + 1u <= da.last, b2nd = db.ch + 1u <= db.last;
-            if (a2nd) df_fetch(sr, da.ch + 1u, a4, a5, a6, a7);
-            if (b2nd) df_fetch(sr, db.ch + 1u, b4, b5, b6, b7);
+            if (a2nd) df_fetch(sr, da.ch + 1u, da.c);
+            if (b2nd) df_fetch(sr, db.ch + 1u, db.c);
             // zero-plane lanes: header and bytes must be the canonical stream (their
             // loads wait together with the chunks above)
             const uint32_t Kz = len >> 8, rz = len & 255u;
@@ -2849,10 +2854,10 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
                 nbad += df_zero_lane_ok(uh[b], canon + ent * (4 + cw), cbytes + (uint64_t)ent * cw, cw, ud,
                                         usize, d0, d1) ? 0u : 1u;
             }
-            df_put(lds8, da.tb, da.ch, a0, a1, a2, a3);
-            df_put(lds8, db.tb, db.ch, b0, b1, b2, b3);
-            if (a2nd) df_put(lds8, da.tb, da.ch + 1u, a4, a5, a6, a7);
-            if (b2nd) df_put(lds8, db.tb, db.ch + 1u, b4, b5, b6, b7);
+            df_put(lds8, da.tb, da.ch, ca);
+            df_put(lds8, db.tb, db.ch, cb);
+            if (a2nd) df_put(lds8, da.tb, da.ch + 1u, da.c);
+            if (b2nd) df_put(lds8, db.tb, db.ch + 1u, db.c);
         }
         const uint32_t K = len >> 8;  // full rows; a partial row K follows when len % 256 != 0
         // sidecar of row k for this column: 16 bits at (ubase + 256k + 4j) / 2, read
@@ -2861,28 +2866,29 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
         const uint32_t* sc32 = reinterpret_cast<const uint32_t*>(sidecar + (ubase >> 1) + 4 * (j >> 1));
         const uint32_t sel = df_sel<SPE>(2 * (j & 1));
         uint32_t* out32 = reinterpret_cast<uint32_t*>(dst + ubase + 4 * j);
-        // rows in groups of 8 (one window step).  A group's sidecar is loaded two
-        // groups ahead: a load completes after every store issued before it (one
-        // in-order counter), so the loads of group g + 2 are issued before group g's
-        // output stores and wait only for stores two groups old.  Loads are
+        // rows in groups of 8 (one window step).  A group's sidecar is loaded
+        // DF_AHEAD groups ahead: a load completes after every store issued before it
+        // (one in-order counter), so the loads of group g + DF_AHEAD are issued
+        // before group g's output stores and wait only for stores DF_AHEAD groups old.  Loads are
         // unconditional (indices clamped to the last group) so the waits stay exact.
         const uint32_t ng = K >> 3;  // full groups
         if (ng) {
+            constexpr uint32_t A = DF_AHEAD;
             const uint32_t gl = ng - 1;
-            uint32_t sa[8], sb[8], sc[8];
+            uint32_t sb[A + 1][8];  // buffer q holds group gi + q
             uint32_t gi = 0;
-            df_load_sc(sa, sc32);
-            df_load_sc(sb, sc32 + 256 * min(1u, gl));
-            for (; gi + 3 <= ng; gi += 3) {
-                df_load_sc(sc, sc32 + 256 * min(gi + 2, gl));
-                df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, sr);
-                df_load_sc(sa, sc32 + 256 * min(gi + 3, gl));
-                df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 1), sb, sel, sr);
-                df_load_sc(sb, sc32 + 256 * min(gi + 4, gl));
-                df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 2), sc, sel, sr);
+#pragma unroll
+            for (uint32_t q = 0; q < A; q++) df_load_sc(sb[q], sc32 + 256 * min(q, gl));
+            for (; gi + A + 1 <= ng; gi += A + 1) {
+#pragma unroll
+                for (uint32_t q = 0; q <= A; q++) {
+                    df_load_sc(sb[(q + A) % (A + 1)], sc32 + 256 * min(gi + q + A, gl));
+                    df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + q), sb[q], sel, sr);
+                }
             }
-            if (gi < ng) df_group<SPE>(da, db, lds8, tab, out32 + 512 * gi, sa, sel, sr);
-            if (gi + 1 < ng) df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + 1), sb, sel, sr);
+#pragma unroll
+            for (uint32_t q = 0; q < A; q++)
+                if (gi + q < ng) df_group<SPE>(da, db, lds8, tab, out32 + 512 * (gi + q), sb[q], sel, sr);
         }
         // at most 7 rows left: no window step needed
         uint32_t k = 8 * ng;
