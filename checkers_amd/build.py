@@ -31,6 +31,10 @@ FLAGS = [
 
 CLI = os.path.join(HERE, "ckr_prefix_mask_repair")
 
+# HBM probes for bench.py's ceiling figures, a library of their own
+PROBE_SRC = os.path.join(CSRC, "ckr_probe.hip")
+PROBE_LIB = os.path.join(HERE, "libckr_probe.so")
+
 # the pybind11 module `checkers_py` (the reference's module name), at the
 # repository root so that `import checkers_py` finds it; host code only, not
 # linked to the library or the HIP runtime (it loads checkers_amd/ at run time)
@@ -89,6 +93,9 @@ def build(verbose=True, incremental=False):
           os.path.join(CSRC, "ckr_repair_cli.cpp"), "-o", CLI + ".tmp",
           "-L", HERE, "-lcheckers_amd", "-Wl,-rpath,$ORIGIN"], verbose)
     os.replace(CLI + ".tmp", CLI)
+    if not incremental or not os.path.exists(PROBE_LIB) or os.path.getmtime(PROBE_SRC) > os.path.getmtime(PROBE_LIB):
+        _run([HIPCC] + FLAGS + ["-shared", "-x", "hip", PROBE_SRC, "-o", PROBE_LIB + ".tmp"], verbose)
+        os.replace(PROBE_LIB + ".tmp", PROBE_LIB)
     mod = py_module_path()
     if not incremental or any(not os.path.exists(mod) or os.path.getmtime(d) > os.path.getmtime(mod)
                               for d in [LIB, os.path.join(ROOT, "include", "checkers_api.hpp")]
