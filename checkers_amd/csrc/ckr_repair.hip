@@ -46,7 +46,9 @@ constexpr int CACHE_PROBES = 8;
 constexpr int SEG = 16;          // tokens per thread in the replace pass
 constexpr int BLK = RT * SEG;    // tokens per replace block
 constexpr int SCAN_T = 1024;     // threads of the single-workgroup scans
-constexpr uint32_t PAIR_CHUNK = 8192;
+constexpr uint32_t PAIR_CHUNK = 8192;  // least pairs per pair_pass workgroup
+constexpr uint32_t PAIR_BLOCKS_PER_CU = 4;  // pair_pass workgroups per CU at most, larger chunks above
+constexpr int PAIR_UNROLL = 4;   // pairs loaded together per pair_pass thread
 constexpr uint32_t OCC_BLK = 4096;
 
 // MurmurHash3 fmix64 / fmix32 finalizers (public domain): table slot hashes.
@@ -318,38 +320,51 @@ __device__ void tab_first(const PairTab& t, RepairCtl* ctl, uint64_t key, uint32
 // occurrence of every pair.
 template <bool FIRST>
 __global__ void __launch_bounds__(RT) pair_pass(const uint32_t* __restrict__ buf0, const uint32_t* __restrict__ buf1,
-                                                RepairCtl* ctl, PairTab tab) {
+                                                RepairCtl* ctl, PairTab tab, uint32_t chunk) {
     if (ctl->done) return;
     if (FIRST && (ctl->ncand <= 1 || ctl->best < 2)) return;
     const uint32_t n = ctl->n_cur;
     if (n < 2) return;
     const uint32_t np = n - 1;
-    const uint64_t base = (uint64_t)blockIdx.x * PAIR_CHUNK;
+    const uint64_t base = (uint64_t)blockIdx.x * chunk;
     if (base >= np) return;
     const uint32_t* tok = ctl->cur ? buf1 : buf0;
     __shared__ uint64_t ck[CACHE];
     __shared__ uint32_t cv[CACHE];
     for (int j = threadIdx.x; j < CACHE; j += RT) { ck[j] = EMPTY_KEY; cv[j] = FIRST ? NONE : 0u; }
     __syncthreads();
-    const uint32_t end = (uint32_t)min<uint64_t>(base + PAIR_CHUNK, np);
-    for (uint32_t i = (uint32_t)base + threadIdx.x; i < end; i += RT) {
-        const uint64_t key = ((uint64_t)tok[i] << 32) | tok[i + 1];
-        uint32_t s = mix64(key) & (CACHE - 1);
-        bool hit = false;
-        for (int p = 0; p < CACHE_PROBES; p++) {
-            uint64_t cur = ck[s];
-            if (cur == EMPTY_KEY) {
-                cur = atomicCAS((unsigned long long*)&ck[s], (unsigned long long)EMPTY_KEY, (unsigned long long)key);
-                if (cur == EMPTY_KEY) cur = key;
-            }
-            if (cur == key) {
-                if (FIRST) atomicMin(&cv[s], i); else atomicAdd(&cv[s], 1u);
-                hit = true;
-                break;
-            }
-            s = (s + 1) & (CACHE - 1);
+    const uint32_t end = (uint32_t)min<uint64_t>(base + chunk, np);
+    // PAIR_UNROLL pairs per thread per step, their tokens loaded before any is
+    // entered, so that the loads wait for memory together
+    for (uint32_t i0 = (uint32_t)base + threadIdx.x; i0 < end; i0 += PAIR_UNROLL * RT) {
+        uint64_t keys[PAIR_UNROLL];
+#pragma unroll
+        for (int u = 0; u < PAIR_UNROLL; u++) {
+            const uint32_t i = i0 + u * RT;
+            keys[u] = i < end ? ((uint64_t)tok[i] << 32) | tok[i + 1] : EMPTY_KEY;
         }
-        if (!hit) { if (FIRST) tab_first(tab, ctl, key, i); else tab_add(tab, ctl, key, 1u); }
+#pragma unroll
+        for (int u = 0; u < PAIR_UNROLL; u++) {
+            const uint32_t i = i0 + u * RT;
+            if (i >= end) break;
+            const uint64_t key = keys[u];
+            uint32_t s = mix64(key) & (CACHE - 1);
+            bool hit = false;
+            for (int p = 0; p < CACHE_PROBES; p++) {
+                uint64_t cur = ck[s];
+                if (cur == EMPTY_KEY) {
+                    cur = atomicCAS((unsigned long long*)&ck[s], (unsigned long long)EMPTY_KEY, (unsigned long long)key);
+                    if (cur == EMPTY_KEY) cur = key;
+                }
+                if (cur == key) {
+                    if (FIRST) atomicMin(&cv[s], i); else atomicAdd(&cv[s], 1u);
+                    hit = true;
+                    break;
+                }
+                s = (s + 1) & (CACHE - 1);
+            }
+            if (!hit) { if (FIRST) tab_first(tab, ctl, key, i); else tab_add(tab, ctl, key, 1u); }
+        }
     }
     __syncthreads();
     for (int j = threadIdx.x; j < CACHE; j += RT) {
@@ -591,24 +606,32 @@ __global__ void __launch_bounds__(RT) rep_apply(uint32_t* __restrict__ buf0, uin
     const uint32_t* tok = ctl->cur ? buf1 : buf0;
     uint32_t* out = ctl->cur ? buf0 : buf1;
     const uint32_t a = ctl->a, b = ctl->b, c = ctl->c;
+    // the block's output goes through LDS (index k at k + k / 32, so that the
+    // threads' runs fall in different banks) and out in coalesced stores
+    __shared__ uint32_t ob[BLK + BLK / 32];
     Seg s;
     load_seg(tok, n, (uint32_t)base + threadIdx.x * SEG, s);
     const SegFn f = seg_fn(s, a, b);
     block_fn_scan(f, sh);
     const SegFn pre = threadIdx.x ? sh[threadIdx.x - 1] : fn_identity();
+    const SegFn whole = sh[RT - 1];
     const uint32_t bo = boff[blockIdx.x];
     const uint32_t qb = bo >> 31;
     uint32_t q = (pre.q >> qb) & 1;
-    uint32_t o = (bo & 0x7FFFFFFFu) + (qb ? pre.c1 : pre.c0);
+    uint32_t o = qb ? pre.c1 : pre.c0;  // within the block's output
 #pragma unroll
     for (int j = 0; j < SEG; j++) {
         const bool valid = (uint32_t)j < s.len;
         const bool st = starts(s, j, a, b);
         const bool emit = valid && !q;
-        if (emit) out[o] = st ? c : s.t[j];
+        if (emit) ob[o + (o >> 5)] = st ? c : s.t[j];
         o += emit ? 1 : 0;
         q = emit && st ? 1 : 0;
     }
+    __syncthreads();
+    const uint32_t total = qb ? whole.c1 : whole.c0;
+    uint32_t* ob_out = out + (bo & 0x7FFFFFFFu);
+    for (uint32_t k = threadIdx.x; k < total; k += RT) ob_out[k] = ob[k + (k >> 5)];
 }
 
 __global__ void __launch_bounds__(RT) tab_clear(RepairCtl* ctl, PairTab tab) {
@@ -766,7 +789,15 @@ hipError_t repair_launch(const RepairArgs& A, hipStream_t s) {
     if ((e = build_alphabet(A.words, A.n, A.es, A.k, L, ws, s)) != hipSuccess) return e;
 
     const uint32_t n32 = (uint32_t)A.n;
-    const uint32_t gpair = (uint32_t)std::max<uint64_t>(1, (A.n + PAIR_CHUNK - 1) / PAIR_CHUNK);
+    // pair_pass: a few workgroups per CU, each over a contiguous chunk, so that
+    // the pairs every chunk shares (the frequent ones) are added to the global
+    // table once per chunk, not once per 8192 pairs
+    int dev = 0, ncu = 0;
+    if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+    if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+    const uint64_t pblocks = (uint64_t)std::max(ncu, 1) * PAIR_BLOCKS_PER_CU;
+    const uint32_t pchunk = (uint32_t)std::max<uint64_t>(PAIR_CHUNK, ((A.n + pblocks - 1) / pblocks + 255) & ~255ull);
+    const uint32_t gpair = (uint32_t)std::max<uint64_t>(1, (A.n + pchunk - 1) / pchunk);
     const uint32_t grep = (uint32_t)std::max<uint64_t>(1, (A.n + BLK - 1) / BLK);
     const uint32_t gsel = 512;
     if (A.build) {
@@ -788,10 +819,10 @@ hipError_t repair_launch(const RepairArgs& A, hipStream_t s) {
     const uint32_t rounds = A.build ? A.max_rules : A.n_rules;
     for (uint32_t r = 0; r < rounds; r++) {
         if (A.build) {
-            CKR_LAUNCH("repair_pair_kernel", s, pair_pass<false><<<gpair, RT, 0, s>>>(buf0, buf1, ctl, tab));
+            CKR_LAUNCH("repair_pair_kernel", s, pair_pass<false><<<gpair, RT, 0, s>>>(buf0, buf1, ctl, tab, pchunk));
             CKR_LAUNCH("repair_select_kernel", s, sel_max<<<gsel, RT, 0, s>>>(ctl, tab));
             CKR_LAUNCH("repair_select_kernel", s, sel_cand<<<gsel, RT, 0, s>>>(ctl, tab));
-            CKR_LAUNCH("repair_tie_kernel", s, pair_pass<true><<<gpair, RT, 0, s>>>(buf0, buf1, ctl, tab));
+            CKR_LAUNCH("repair_tie_kernel", s, pair_pass<true><<<gpair, RT, 0, s>>>(buf0, buf1, ctl, tab, pchunk));
             CKR_LAUNCH("repair_tie_kernel", s, tie_bucket<<<gsel, RT, 0, s>>>(ctl, tab, sym, primes, A.n_primes, bfirst));
             CKR_LAUNCH("repair_tie_kernel", s, tie_pick<<<gsel, RT, 0, s>>>(ctl, tab, sym, primes, A.n_primes, bfirst));
             CKR_LAUNCH("repair_tie_kernel", s, tie_resolve<<<gsel, RT, 0, s>>>(ctl, tab, sym, primes, A.n_primes, bfirst));
