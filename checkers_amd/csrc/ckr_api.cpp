@@ -1463,6 +1463,7 @@ static int repair_run(const void* d_words, uint64_t n, int dtype, int masked_bit
     a.h_primes = p.primes.data();
     a.n_primes = (uint32_t)p.primes.size();
     a.d_seq_out = d_seq_out;
+    a.recount_each_round = g_fast_paths == 0;
     a.ws = static_cast<uint8_t*>(d_ws);
     a.layout = p.layout;
     CKR_HIP(ckr::repair_launch(a, s));

@@ -155,6 +155,7 @@ struct RepairCtl {
     uint32_t best, ncand, chosen, d;   // d: occupied pair-table slots
     uint32_t a0, a, b, c;              // alphabet size; pair (a, b) → c of this round
     uint32_t skip, cur, err, max_pair; // cur: which token buffer holds the sequence
+    uint32_t recount, recount_next;    // build: count every pair this round / the next
 };
 constexpr uint32_t kRepairMaxPrimes = 512;
 struct RepairLayout {
@@ -179,6 +180,7 @@ struct RepairArgs {
     const uint64_t* h_primes;         // build: library bucket counts covering [2, n], ascending
     uint32_t n_primes;
     uint64_t* d_seq_out;
+    bool recount_each_round;          // build: every pair recounted each round
     uint8_t* ws;
     RepairLayout layout;
 };

@@ -12,8 +12,14 @@
 // that the rounds ping-pong between.
 //
 // One round (all on the device, no host synchronisation):
-//   pair_pass<count>   every adjacent pair counted: per-workgroup LDS cache of
+//   pair_pass<COUNT>   every adjacent pair counted (first round, or when the
+//                      table is to be rebuilt): per-workgroup LDS cache of
 //                      2048 pairs in front of a global open-addressing table;
+//                      later rounds keep the counts up to date instead: the
+//                      replacement subtracts the pairs it destroys (those with
+//                      a replaced token) and pair_pass<INC> adds the new
+//                      sequence's pairs holding the new symbol, the only new
+//                      pairs (a pair of two kept tokens was a pair before);
 //   sel_max/sel_cand   largest count and the number of pairs holding it;
 //   tie_*              only if several pairs hold it: the pair std::unordered_map
 //                      would visit first.  libstdc++ keeps one singly linked
@@ -28,11 +34,13 @@
 //                      first occurrence); the bucket is hash % P with P the
 //                      bucket count of reserve(size), taken from libstdc++ by
 //                      the host;
-//   round_commit       record the rule (or stop: best count < 2);
+//   round_commit       record the rule (or stop: best count < 2) and decide
+//                      whether the next round recounts (table above 3/4 full
+//                      once the new pairs are in);
 //   rep_*              greedy left-to-right replacement as a scan: the state
 //                      "previous token started a replacement" is a function of
 //                      the state entering a segment, so segments compose;
-//   tab_clear/round_end reset the touched table slots and advance.
+//   tab_clear/round_end reset the touched table slots (recount only) and advance.
 #include "ckr_internal.h"
 
 namespace ckr {
@@ -43,6 +51,7 @@ constexpr uint32_t NONE = 0xFFFFFFFFu;
 constexpr int RT = 256;          // threads per workgroup
 constexpr int CACHE = 2048;      // LDS pair cache entries
 constexpr int CACHE_PROBES = 8;
+constexpr int DCACHE = 1024;     // LDS cache of the pairs a replacement workgroup subtracts
 constexpr int SEG = 16;          // tokens per thread in the replace pass
 constexpr int BLK = RT * SEG;    // tokens per replace block
 constexpr int SCAN_T = 1024;     // threads of the single-workgroup scans
@@ -316,13 +325,20 @@ __device__ void tab_first(const PairTab& t, RepairCtl* ctl, uint64_t key, uint32
     atomicOr(&ctl->err, 4u);
 }
 
-// FIRST == false: count every adjacent pair.  FIRST == true (ties only): first
-// occurrence of every pair.
-template <bool FIRST>
+// COUNT: count every adjacent pair (a recount round).  FIRST (ties only): first
+// occurrence of every pair.  INC (after a round's replacement): count the pairs
+// holding the round's new symbol c.
+enum PairMode { COUNT = 0, FIRST_OCC = 1, INC = 2 };
+
+template <int MODE>
 __global__ void __launch_bounds__(RT) pair_pass(const uint32_t* __restrict__ buf0, const uint32_t* __restrict__ buf1,
                                                 RepairCtl* ctl, PairTab tab, uint32_t chunk) {
+    constexpr bool FIRST = MODE == FIRST_OCC;
     if (ctl->done) return;
+    if (MODE == COUNT && !ctl->recount) return;
     if (FIRST && (ctl->ncand <= 1 || ctl->best < 2)) return;
+    if (MODE == INC && ctl->recount) return;
+    const uint32_t c = ctl->c;
     const uint32_t n = ctl->n_cur;
     if (n < 2) return;
     const uint32_t np = n - 1;
@@ -348,6 +364,7 @@ __global__ void __launch_bounds__(RT) pair_pass(const uint32_t* __restrict__ buf
             const uint32_t i = i0 + u * RT;
             if (i >= end) break;
             const uint64_t key = keys[u];
+            if (MODE == INC && (uint32_t)(key >> 32) != c && (uint32_t)key != c) continue;
             uint32_t s = mix64(key) & (CACHE - 1);
             bool hit = false;
             for (int p = 0; p < CACHE_PROBES; p++) {
@@ -373,6 +390,13 @@ __global__ void __launch_bounds__(RT) pair_pass(const uint32_t* __restrict__ buf
         if (FIRST) tab_first(tab, ctl, key, cv[j]);
         else tab_add(tab, ctl, key, cv[j]);
     }
+}
+
+// Ties only: the first occurrences are taken afresh for the current sequence.
+__global__ void __launch_bounds__(RT) first_reset(RepairCtl* ctl, PairTab tab) {
+    if (ctl->done || ctl->best < 2 || ctl->ncand <= 1) return;
+    const uint32_t d = ctl->d;
+    for (uint32_t j = blockIdx.x * RT + threadIdx.x; j < d; j += gridDim.x * RT) tab.first[tab.touched[j]] = NONE;
 }
 
 __global__ void __launch_bounds__(RT) sel_max(RepairCtl* ctl, PairTab tab) {
@@ -447,7 +471,7 @@ __global__ void __launch_bounds__(RT) tie_resolve(RepairCtl* ctl, PairTab tab, c
 
 // Build mode: record the round's rule or stop.  Apply mode: load rule `round`.
 __global__ void round_commit(RepairCtl* ctl, PairTab tab, uint64_t* __restrict__ sym, ckr_repair_rule* rules,
-                             const uint32_t* __restrict__ rmap, int build) {
+                             const uint32_t* __restrict__ rmap, int build, uint32_t dlimit) {
     if (ctl->done) return;
     const uint32_t r = ctl->round;
     if (build) {
@@ -463,6 +487,11 @@ __global__ void round_commit(RepairCtl* ctl, PairTab tab, uint64_t* __restrict__
         rules[r].frequency = best;
         sym[c] = rs;
         ctl->a = a; ctl->b = b; ctl->c = c; ctl->skip = 0;
+        // the round's new pairs are (x, c) and (c, x): at most 2 per occurrence
+        // of c and 2 per symbol x (the a0 + r + 1 ids so far), plus (c, c)
+        const uint32_t fresh = 2u * min(best, ctl->a0 + r + 1u) + 1u;
+        ctl->recount = 0;
+        ctl->recount_next = (uint64_t)ctl->d + fresh > dlimit ? 1u : 0u;
     } else {
         ctl->a = rmap[3 * r]; ctl->b = rmap[3 * r + 1]; ctl->c = rmap[3 * r + 2];
         ctl->skip = (ctl->a == NONE || ctl->b == NONE) ? 1u : 0u;
@@ -596,21 +625,30 @@ __global__ void __launch_bounds__(SCAN_T) rep_scan(RepairCtl* ctl, const SegFn* 
     if (threadIdx.x == SCAN_T - 1) ctl->n_next = f.c0;
 }
 
+// DEC (build rounds that keep their counts): every pair of the old sequence
+// with a replaced token is subtracted from the table, through an LDS cache.
+template <bool DEC>
 __global__ void __launch_bounds__(RT) rep_apply(uint32_t* __restrict__ buf0, uint32_t* __restrict__ buf1,
-                                                RepairCtl* ctl, const uint32_t* __restrict__ boff) {
+                                                RepairCtl* ctl, const uint32_t* __restrict__ boff, PairTab tab) {
     CKR_REP_GUARD();
     __shared__ SegFn sh[RT];
+    __shared__ uint64_t dk[DEC ? DCACHE : 1];
+    __shared__ uint32_t dv[DEC ? DCACHE : 1];
     const uint32_t n = ctl->n_cur;
     const uint64_t base = (uint64_t)blockIdx.x * BLK;
     if (base >= n) return;
+    const bool dec = DEC && !ctl->recount_next;
+    if (dec)
+        for (int j = threadIdx.x; j < DCACHE; j += RT) { dk[j] = EMPTY_KEY; dv[j] = 0; }
     const uint32_t* tok = ctl->cur ? buf1 : buf0;
     uint32_t* out = ctl->cur ? buf0 : buf1;
     const uint32_t a = ctl->a, b = ctl->b, c = ctl->c;
     // the block's output goes through LDS (index k at k + k / 32, so that the
     // threads' runs fall in different banks) and out in coalesced stores
     __shared__ uint32_t ob[BLK + BLK / 32];
+    const uint32_t i0 = (uint32_t)base + threadIdx.x * SEG;
     Seg s;
-    load_seg(tok, n, (uint32_t)base + threadIdx.x * SEG, s);
+    load_seg(tok, n, i0, s);
     const SegFn f = seg_fn(s, a, b);
     block_fn_scan(f, sh);
     const SegFn pre = threadIdx.x ? sh[threadIdx.x - 1] : fn_identity();
@@ -619,23 +657,55 @@ __global__ void __launch_bounds__(RT) rep_apply(uint32_t* __restrict__ buf0, uin
     const uint32_t qb = bo >> 31;
     uint32_t q = (pre.q >> qb) & 1;
     uint32_t o = qb ? pre.c1 : pre.c0;  // within the block's output
+    uint32_t cons = 0;                  // bit j: token i0 + j is replaced
 #pragma unroll
     for (int j = 0; j < SEG; j++) {
         const bool valid = (uint32_t)j < s.len;
         const bool st = starts(s, j, a, b);
         const bool emit = valid && !q;
+        if (valid && (q || st)) cons |= 1u << j;
         if (emit) ob[o + (o >> 5)] = st ? c : s.t[j];
         o += emit ? 1 : 0;
         q = emit && st ? 1 : 0;
+    }
+    if (dec) {
+        // the token after the segment is replaced if token SEG - 1 starts a
+        // replacement or if it starts one itself
+        if (s.has_nxt) {
+            const bool has17 = (uint64_t)i0 + SEG + 1 < n;
+            const bool st16 = !q && has17 && s.nxt == a && tok[i0 + SEG + 1] == b;
+            if (q || st16) cons |= 1u << SEG;
+        }
+#pragma unroll
+        for (int j = 0; j < SEG; j++) {
+            const bool pair = (uint32_t)(j + 1) < s.len || (j == SEG - 1 && s.has_nxt);
+            if (!pair || ((cons >> j) & 3u) == 0) continue;
+            const uint64_t key = ((uint64_t)s.t[j] << 32) | (j + 1 < SEG ? s.t[(j + 1) & (SEG - 1)] : s.nxt);
+            uint32_t sl = mix64(key) & (DCACHE - 1);
+            bool hit = false;
+            for (int p = 0; p < CACHE_PROBES; p++) {
+                uint64_t cur = dk[sl];
+                if (cur == EMPTY_KEY) {
+                    cur = atomicCAS((unsigned long long*)&dk[sl], (unsigned long long)EMPTY_KEY, (unsigned long long)key);
+                    if (cur == EMPTY_KEY) cur = key;
+                }
+                if (cur == key) { atomicAdd(&dv[sl], 1u); hit = true; break; }
+                sl = (sl + 1) & (DCACHE - 1);
+            }
+            if (!hit) tab_add(tab, ctl, key, 0u - 1u);
+        }
     }
     __syncthreads();
     const uint32_t total = qb ? whole.c1 : whole.c0;
     uint32_t* ob_out = out + (bo & 0x7FFFFFFFu);
     for (uint32_t k = threadIdx.x; k < total; k += RT) ob_out[k] = ob[k + (k >> 5)];
+    if (dec)
+        for (int j = threadIdx.x; j < DCACHE; j += RT)
+            if (dk[j] != EMPTY_KEY) tab_add(tab, ctl, dk[j], 0u - dv[j]);
 }
 
 __global__ void __launch_bounds__(RT) tab_clear(RepairCtl* ctl, PairTab tab) {
-    if (ctl->done) return;
+    if (ctl->done || !ctl->recount_next) return;
     const uint32_t d = ctl->d;
     for (uint32_t j = blockIdx.x * RT + threadIdx.x; j < d; j += gridDim.x * RT) {
         const uint32_t s = tab.touched[j];
@@ -647,7 +717,10 @@ __global__ void round_end(RepairCtl* ctl) {
     if (ctl->done) return;
     if (!ctl->skip) { ctl->n_cur = ctl->n_next; ctl->cur ^= 1u; }
     ctl->round++;
-    ctl->best = 0; ctl->ncand = 0; ctl->pick = 0; ctl->d = 0; ctl->skip = 0;
+    ctl->best = 0; ctl->ncand = 0; ctl->pick = 0; ctl->skip = 0;
+    if (ctl->recount_next) ctl->d = 0;  // tab_clear has emptied the table
+    ctl->recount = ctl->recount_next;
+    ctl->recount_next = 0;
 }
 
 __global__ void __launch_bounds__(RT) seq_out_kernel(const uint32_t* __restrict__ buf0, const uint32_t* __restrict__ buf1,
@@ -669,6 +742,7 @@ __global__ void __launch_bounds__(RT) fill_kernel(T* __restrict__ p, uint64_t n,
 __global__ void ctl_init(RepairCtl* ctl, uint32_t n) {
     RepairCtl c = {};
     c.n_cur = n;
+    c.recount = 1;  // the first round counts every pair
     *ctl = c;
 }
 
@@ -798,6 +872,10 @@ hipError_t repair_launch(const RepairArgs& A, hipStream_t s) {
     const uint64_t pblocks = (uint64_t)std::max(ncu, 1) * PAIR_BLOCKS_PER_CU;
     const uint32_t pchunk = (uint32_t)std::max<uint64_t>(PAIR_CHUNK, ((A.n + pblocks - 1) / pblocks + 255) & ~255ull);
     const uint32_t gpair = (uint32_t)std::max<uint64_t>(1, (A.n + pchunk - 1) / pchunk);
+    // rounds keep their counts while the table stays at most 3/4 full (limit 0:
+    // every round recounts)
+    const uint32_t dlimit =
+        A.recount_each_round ? 0u : (uint32_t)std::min<uint64_t>(L.pair_cap - L.pair_cap / 4, 0xFFFFFFFFull);
     const uint32_t grep = (uint32_t)std::max<uint64_t>(1, (A.n + BLK - 1) / BLK);
     const uint32_t gsel = 512;
     if (A.build) {
@@ -819,20 +897,24 @@ hipError_t repair_launch(const RepairArgs& A, hipStream_t s) {
     const uint32_t rounds = A.build ? A.max_rules : A.n_rules;
     for (uint32_t r = 0; r < rounds; r++) {
         if (A.build) {
-            CKR_LAUNCH("repair_pair_kernel", s, pair_pass<false><<<gpair, RT, 0, s>>>(buf0, buf1, ctl, tab, pchunk));
+            CKR_LAUNCH("repair_pair_kernel", s, pair_pass<COUNT><<<gpair, RT, 0, s>>>(buf0, buf1, ctl, tab, pchunk));
             CKR_LAUNCH("repair_select_kernel", s, sel_max<<<gsel, RT, 0, s>>>(ctl, tab));
             CKR_LAUNCH("repair_select_kernel", s, sel_cand<<<gsel, RT, 0, s>>>(ctl, tab));
-            CKR_LAUNCH("repair_tie_kernel", s, pair_pass<true><<<gpair, RT, 0, s>>>(buf0, buf1, ctl, tab, pchunk));
+            CKR_LAUNCH("repair_tie_kernel", s, first_reset<<<gsel, RT, 0, s>>>(ctl, tab));
+            CKR_LAUNCH("repair_tie_kernel", s, pair_pass<FIRST_OCC><<<gpair, RT, 0, s>>>(buf0, buf1, ctl, tab, pchunk));
             CKR_LAUNCH("repair_tie_kernel", s, tie_bucket<<<gsel, RT, 0, s>>>(ctl, tab, sym, primes, A.n_primes, bfirst));
             CKR_LAUNCH("repair_tie_kernel", s, tie_pick<<<gsel, RT, 0, s>>>(ctl, tab, sym, primes, A.n_primes, bfirst));
             CKR_LAUNCH("repair_tie_kernel", s, tie_resolve<<<gsel, RT, 0, s>>>(ctl, tab, sym, primes, A.n_primes, bfirst));
         }
-        CKR_LAUNCH("repair_commit_kernel", s, round_commit<<<1, 1, 0, s>>>(ctl, tab, sym, rules, rmap, A.build));
+        CKR_LAUNCH("repair_commit_kernel", s,
+                   round_commit<<<1, 1, 0, s>>>(ctl, tab, sym, rules, rmap, A.build, dlimit));
         CKR_LAUNCH("repair_replace_kernel", s, rep_summary<<<grep, RT, 0, s>>>(buf0, buf1, ctl, bfun));
         CKR_LAUNCH("repair_replace_kernel", s, rep_scan<<<1, SCAN_T, 0, s>>>(ctl, bfun, boff));
-        CKR_LAUNCH("repair_replace_kernel", s, rep_apply<<<grep, RT, 0, s>>>(buf0, buf1, ctl, boff));
+        if (A.build) CKR_LAUNCH("repair_replace_kernel", s, rep_apply<true><<<grep, RT, 0, s>>>(buf0, buf1, ctl, boff, tab));
+        else CKR_LAUNCH("repair_replace_kernel", s, rep_apply<false><<<grep, RT, 0, s>>>(buf0, buf1, ctl, boff, tab));
         if (A.build) CKR_LAUNCH("repair_select_kernel", s, tab_clear<<<gsel, RT, 0, s>>>(ctl, tab));
         CKR_LAUNCH("repair_commit_kernel", s, round_end<<<1, 1, 0, s>>>(ctl));
+        if (A.build) CKR_LAUNCH("repair_pair_kernel", s, pair_pass<INC><<<gpair, RT, 0, s>>>(buf0, buf1, ctl, tab, pchunk));
         if ((e = hipGetLastError()) != hipSuccess) return e;
         // every 8 rounds, stop launching once the device says the grammar is done
         if (A.build && (r & 7) == 7 && r + 1 < rounds) {

@@ -122,18 +122,27 @@ SYNTH = [
 ]
 
 
+@pytest.fixture(params=[1, 0], ids=["kept_counts", "recount"])
+def counting(request):
+    # mode 0 of ckr_set_fast_paths: the build recounts every pair each round
+    import checkers_amd as ck
+    prev = ck.set_fast_paths(request.param)
+    yield request.param
+    ck.set_fast_paths(prev)
+
+
 @pytest.mark.parametrize("name,dtype,masked,max_rules,gen", SYNTH, ids=[c[0] for c in SYNTH])
-def test_repair_parity(gpu, name, dtype, masked, max_rules, gen):
+def test_repair_parity(gpu, name, dtype, masked, max_rules, gen, counting):
     raw = gen()
-    print(f"[repair] {name} n={raw.size}", flush=True)
+    print(f"[repair] {name} n={raw.size} counting={counting}", flush=True)
     other = np.roll(raw, 7)[: max(raw.size - 5, 0)] if raw.size else raw
     _check_case(gpu, raw, dtype, masked, max_rules, other=other)
 
 
-def test_repair_many_blocks(gpu):
+def test_repair_many_blocks(gpu, counting):
     # more replace blocks than the single-workgroup scan has threads (4096 tokens each)
     raw = _bf16(4_500_000, 0.02, 21)
-    print("[repair] many_blocks n=4.5M", flush=True)
+    print(f"[repair] many_blocks n=4.5M counting={counting}", flush=True)
     _check_case(gpu, raw, 1, None, 3)
 
 
