@@ -561,18 +561,27 @@ __device__ __forceinline__ SegFn seg_fn(const Seg& s, uint32_t a, uint32_t b) {
     return SegFn{c0, c1, q0 | (q1 << 1)};
 }
 
-// Inclusive scan of segment functions over the block (Hillis–Steele in LDS).
+// Inclusive scan of segment functions over the block: within each wave by
+// shuffles, then the waves' totals through LDS.  Leaves thread i's inclusive
+// function in sh[i].
 __device__ SegFn block_fn_scan(SegFn f, SegFn* sh) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        SegFn g;
+        g.c0 = (uint32_t)__shfl_up((int)f.c0, o);
+        g.c1 = (uint32_t)__shfl_up((int)f.c1, o);
+        g.q = (uint32_t)__shfl_up((int)f.q, o);
+        if (lane >= o) f = fn_compose(g, f);
+    }
+    if (lane == 63) sh[w] = f;
+    __syncthreads();
+    SegFn pre = fn_identity();
+    for (int i = 0; i < w; i++) pre = fn_compose(pre, sh[i]);
+    f = fn_compose(pre, f);
+    __syncthreads();
     sh[threadIdx.x] = f;
     __syncthreads();
-    for (int o = 1; o < RT; o <<= 1) {
-        SegFn g = f;
-        if ((int)threadIdx.x >= o) g = fn_compose(sh[threadIdx.x - o], f);
-        __syncthreads();
-        sh[threadIdx.x] = g;
-        f = g;
-        __syncthreads();
-    }
     return f;
 }
 
