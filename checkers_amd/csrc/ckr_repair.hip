@@ -492,6 +492,9 @@ __global__ void round_commit(RepairCtl* ctl, PairTab tab, uint64_t* __restrict__
         const uint32_t fresh = 2u * min(best, ctl->a0 + r + 1u) + 1u;
         ctl->recount = 0;
         ctl->recount_next = (uint64_t)ctl->d + fresh > dlimit ? 1u : 0u;
+        // every occurrence of (a, b) is replaced or loses a token to an
+        // overlapping replacement: its count after the round is 0
+        tab.cnt[ctl->chosen] = 0;
     } else {
         ctl->a = rmap[3 * r]; ctl->b = rmap[3 * r + 1]; ctl->c = rmap[3 * r + 2];
         ctl->skip = (ctl->a == NONE || ctl->b == NONE) ? 1u : 0u;
@@ -678,6 +681,7 @@ __global__ void __launch_bounds__(RT) rep_apply(uint32_t* __restrict__ buf0, uin
         q = emit && st ? 1 : 0;
     }
     if (dec) {
+        const uint64_t ab = ((uint64_t)a << 32) | b;
         // the token after the segment is replaced if token SEG - 1 starts a
         // replacement or if it starts one itself
         if (s.has_nxt) {
@@ -690,6 +694,7 @@ __global__ void __launch_bounds__(RT) rep_apply(uint32_t* __restrict__ buf0, uin
             const bool pair = (uint32_t)(j + 1) < s.len || (j == SEG - 1 && s.has_nxt);
             if (!pair || ((cons >> j) & 3u) == 0) continue;
             const uint64_t key = ((uint64_t)s.t[j] << 32) | (j + 1 < SEG ? s.t[(j + 1) & (SEG - 1)] : s.nxt);
+            if (key == ab) continue;  // every (a, b) is destroyed: round_commit zeroed its count
             uint32_t sl = mix64(key) & (DCACHE - 1);
             bool hit = false;
             for (int p = 0; p < CACHE_PROBES; p++) {
