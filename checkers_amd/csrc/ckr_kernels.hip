@@ -1023,7 +1023,7 @@ struct WsPairCtl {
     uint32_t tick;            // uses started by the plane-FL coder (unit published)
     uint32_t pbar;            // barrier count of the packer waves
     uint32_t off[2][2];       // packed offset of the unit in set s (lo, hi)
-    uint32_t xread;           // units whose exchange words the look-back packer has read
+    uint32_t xread;           // +1 by each packer wave per use, once it holds the exchange words
     uint32_t pad[3];
 };
 static_assert(sizeof(WsPairCtl) % 16 == 0, "control block alignment");
@@ -1154,8 +1154,8 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
             }
             const uint32_t e = enc_finish(c, lds8, endw);
             // per column: count FL, state FL, count 3, state 3, in the set's lane-record
-            // area (the records are written only after both packers have read them;
-            // it lies below the guard that an outgrown lowest slot may write into)
+            // area (the records are written only after every packer wave has read
+            // them; it lies below the guard that an outgrown lowest slot may write into)
             uint32_t* xch = reinterpret_cast<uint32_t*>(lds8 + rb + R_REC);
             xch[2 * rl * 64 + j] = e;
             xch[(2 * rl + 1) * 64 + j] = c.x;
@@ -1193,7 +1193,7 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
         const uint32_t* xch = reinterpret_cast<const uint32_t*>(lds8 + rb + R_REC);
         const uint32_t e0 = xch[j], x0 = xch[64 + j];
         const uint32_t e1 = xch[128 + j], x1 = xch[192 + j];
-        if (pw == 0) ws_signal(&pc.xread, 1u, j);  // the records may now overwrite them
+        ws_signal(&pc.xread, 1u, j);  // once all NPK have, the records may overwrite them
         // byte counts, final states and LDS stream starts of the four lanes of column j
         uint32_t cnt[4], fs[4], sa[4];
 #pragma unroll
@@ -1243,8 +1243,8 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
             }
             // lane records and the block map (the lane holding the first byte of each
             // 64-byte block of the packed unit), the records written over the exchange
-            // words once both packers hold them
-            ws_wait_ge(&pc.xread, i + 1);
+            // words once every packer wave holds them
+            ws_wait_ge(&pc.xread, (i + 1) * NPK);
             run = excl;
 #pragma unroll
             for (int b = 0; b < 4; b++) {
@@ -2560,10 +2560,17 @@ __global__ void __launch_bounds__(256) decode_kernel(const uint8_t* __restrict__
 // assembled byte by byte, with zeros outside the buffer.
 static constexpr uint32_t DF_WAVES = 8;
 static constexpr uint32_t DF_AHEAD = 2;  // groups of sidecar words loaded ahead of the group decoded
-static constexpr uint32_t DF_CH_LOG = 6;  // chunk bytes 64 (32 also keeps every read behind the writes)
+static constexpr uint32_t DF_CH_LOG = 6;  // chunk bytes
 static constexpr uint32_t DF_CH = 1u << DF_CH_LOG;
 static constexpr uint32_t DF_CQ = DF_CH / 16;  // 16-byte loads per chunk
 static constexpr uint32_t DF_RING_ROWS = DF_CH / 2;  // two chunks of DF_CH / 4 dwords
+// Group ends between a chunk's fetch and its write to LDS.  A lane enters
+// chunk ch + 1 at a group end with p <= DF_CH (ch + 1) + 15 and takes at most 16
+// bytes a group; a window reads up to 7 bytes past p.  The chunk after must be
+// in LDS before any read can reach it, also in the rows after the last full
+// group (at most 8 symbols, 16 bytes, no group end): 16 DF_PUT_AFTER + 21 <= DF_CH.
+static constexpr uint32_t DF_PUT_AFTER = 1;
+static_assert(DF_PUT_AFTER >= 1 && 16 * DF_PUT_AFTER + 21 <= DF_CH, "a chunk would be read before it is written");
 static constexpr uint32_t DF_TAB_BYTES = 4096 * 4;
 static constexpr uint32_t DF_RING_BYTES = (DF_RING_ROWS + 1) * 256;  // the rows + the copy of row 0
 static constexpr uint32_t DF_WAVE_BYTES = 2 * DF_RING_BYTES;
@@ -2580,7 +2587,7 @@ struct DfLane {
     uint32_t ch;       // chunk of p at the last check
     uint32_t last;     // chunk of the stream's last byte: no chunk after it is fetched
     uint32_t tb;       // LDS address of this lane's ring column (row 0)
-    bool pend;         // chunk ch + 1 is in flight in c[], to be written at the end of this group
+    uint32_t age;      // chunk ch + 1 in flight in c[]: 0 none, else group ends since its fetch
     uint4 c[DF_CQ];
 };
 
@@ -2660,14 +2667,16 @@ __device__ __forceinline__ uint32_t df_sym(uint32_t& x, uint32_t& w, uint32_t& s
     return te;
 }
 
-// End of a group: write the chunk fetched at the end of the previous group,
-// then move on if p has reached the next chunk and fetch the one after it.
+// End of a group: write the chunk fetched DF_PUT_AFTER group ends ago, then
+// move on if p has reached the next chunk and fetch the one after it.  Each
+// group of waiting lets the fetch's load, and the output stores issued before
+// it (one in-order counter), complete while the lane decodes.
 __device__ __forceinline__ void df_step(DfLane& d, uint8_t* lds8, const DfSrc& sr) {
-    if (d.pend) df_put(lds8, d.tb, d.ch + 1u, d.c);
+    if (d.age == DF_PUT_AFTER) { df_put(lds8, d.tb, d.ch + 1u, d.c); d.age = 0; }
+    else if (d.age) d.age++;
     const bool adv = (d.p8 >> (DF_CH_LOG + 3)) > d.ch;
     d.ch += adv ? 1u : 0u;
-    d.pend = adv && d.ch + 1u <= d.last;
-    if (d.pend) df_fetch(sr, d.ch + 1u, d.c);
+    if (adv && d.ch + 1u <= d.last) { df_fetch(sr, d.ch + 1u, d.c); d.age = 1; }
 }
 
 template <int SPE>
@@ -2830,7 +2839,7 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
                 ge8 = pe << 3;
                 d.ch = p >> DF_CH_LOG;
                 d.last = pe > p ? (pe - 1u) >> DF_CH_LOG : d.ch;
-                d.pend = false;
+                d.age = 0;
             };
             init(da, gea8, FL);
             init(db, geb8, 3);

@@ -417,6 +417,35 @@ def test_compress_many_matches_single_calls(unit, paths, gpu):
         ck.compress_many([encs[0], encs[0]], [srcs[0], srcs[0]])
 
 
+def test_compress_many_repeated_byte_identical(gpu):
+    """Regression for a race between the fast encoder's packer waves (one of them
+    wrote the lane records over the exchange words before the others had read
+    them, so a late packer could pack with wrong lane sizes while the headers
+    stayed right): many compress_many calls, each tensor byte-identical to one
+    ckr_compress of it every time."""
+    import torch
+    ck = _ck()
+    g = torch.Generator(device=gpu)
+    g.manual_seed(80)
+    ts = [(torch.randn(n, device=gpu, generator=g) * s).to(dt) for n, s, dt in
+          ((16 << 20, 0.02, torch.bfloat16), (4 << 20, 0.02, torch.bfloat16), (8 << 20, 1e-3, torch.float32),
+           (6 << 20, 0.02, torch.bfloat16), (2 << 20, 1e-3, torch.float32))]
+    tags = [ck.torch_tag(t.dtype) for t in ts]
+    srcs = [t.view(torch.uint8) for t in ts]
+    refs = []
+    for t, tag, s in zip(ts, tags, srcs):
+        e = ck.Encoder(t.numel(), tag, 65536, device=gpu).compress(s)
+        torch.cuda.synchronize()
+        refs.append(e.data[: e.total].clone())
+    encs = [ck.Encoder(t.numel(), tag, 65536, device=gpu) for t, tag in zip(ts, tags)]
+    for it in range(25):
+        print(f"[case] compress_many repeat {it}", flush=True)
+        res = ck.compress_many(encs, srcs)
+        torch.cuda.synchronize()
+        for k, (r, ref) in enumerate(zip(res, refs)):
+            assert r.total == ref.numel() and torch.equal(r.data[: r.total], ref), (it, k)
+
+
 def test_compress_many_large_overlapped_histogram(gpu):
     """A tensor large enough that the histogram run beside the previous encode
     (8 KiB of LDS, one workgroup per CU) covers it in several strides per
