@@ -489,9 +489,9 @@ __global__ void round_commit(RepairCtl* ctl, PairTab tab, uint64_t* __restrict__
         ctl->a = a; ctl->b = b; ctl->c = c; ctl->skip = 0;
         // the round's new pairs are (x, c) and (c, x): at most 2 per occurrence
         // of c and 2 per symbol x (the a0 + r + 1 ids so far), plus (c, c)
-        const uint32_t fresh = 2u * min(best, ctl->a0 + r + 1u) + 1u;
+        const uint64_t fresh = 2ull * min((uint64_t)best, (uint64_t)ctl->a0 + r + 1u) + 1u;
         ctl->recount = 0;
-        ctl->recount_next = (uint64_t)ctl->d + fresh > dlimit ? 1u : 0u;
+        ctl->recount_next = ctl->d + fresh > dlimit ? 1u : 0u;
         // every occurrence of (a, b) is replaced or loses a token to an
         // overlapping replacement: its count after the round is 0
         tab.cnt[ctl->chosen] = 0;
