@@ -371,6 +371,13 @@ def test_encode_planes_matches_encode(tag, unit, paths, gpu):
     assert torch.equal(e1.data[: e1.total], e2.data[: e2.total])
     assert torch.equal(e1.headers, e2.headers) and torch.equal(e1.unit_offsets, e2.unit_offsets)
     assert torch.equal(e1.sidecar, e2.sidecar)
+    # plane histograms that say nothing true about the data (empty, one hot bin)
+    # only size the slots: the bytes stay ckr_encode's
+    for bogus in (np.zeros(512, np.uint32), np.eye(1, 512, 7, dtype=np.uint32).reshape(-1) * 1000):
+        e4 = ck.Encoder(n, tag, unit, device=gpu).encode(t, table, planes=bogus)
+        torch.cuda.synchronize()
+        assert e4.total == e1.total and torch.equal(e4.data[: e4.total], e1.data[: e1.total])
+        assert torch.equal(e4.headers, e1.headers) and torch.equal(e4.unit_offsets, e1.unit_offsets)
     m = 2 * unit // es
     e3 = ck.Encoder(m, tag, unit, device=gpu).encode(t[: m * es], table, planes=hh[256:])
     torch.cuda.synchronize()
