@@ -1277,7 +1277,7 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
         } else {
             // Packed bytes in 16-byte destination chunks aligned in global memory,
             // 64 consecutive chunks (1 KiB of output, whole cache lines) per wave
-            // store: the two packer waves take alternate rounds of 64 chunks.  Chunk
+            // store: the NPK packer waves take rounds of 64 chunks in turn.  Chunk
             // c starts at unit byte q = qbase + 16c (chunk 0 may start up to 15
             // bytes before the unit).  Its first lane: the block map gives the lane
             // holding the first byte of the chunk's 64-byte block, and the lanes
