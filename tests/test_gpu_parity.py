@@ -314,11 +314,14 @@ def test_histogram_counts_wrap_like_reference(gpu):
 
 
 @pytest.mark.parametrize("unit", [65536, 1 << 20])
-@pytest.mark.parametrize("where", ["live", "zero", "state"])
+@pytest.mark.parametrize("where", ["live", "zero", "state", "zero_last", "zero_header"])
 def test_decode_counts_corrupted_lanes(unit, where, gpu):
     """A flipped byte in a live lane's stream or a zero-plane lane's stream, or a
     wrong final state, is reported as a bad lane (the decoder's postconditions:
-    final state L, every byte consumed, canonical zero-plane streams)."""
+    final state L, every byte consumed, canonical zero-plane streams).  A
+    zero-plane lane's bytes are compared step by step during the decode: a flip
+    in its first or last byte, in the second unit, or in its header counts that
+    one lane."""
     import torch
     ck = _ck()
     n = (unit // 4) * 2 + 777
@@ -329,17 +332,25 @@ def test_decode_counts_corrupted_lanes(unit, where, gpu):
     dst, bad = ck.decode(enc)
     assert bad == 0 and np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
     hdr = enc.headers_np()
-    lane = {"live": 3, "zero": 0, "state": 2}[where]  # fp32 columns: bytes 0, 1 masked, 2, 3 live
-    h = hdr[lane]
+    lane = {"live": 3, "zero": 0, "state": 2, "zero_last": 256 + 1, "zero_header": 256 + 4}[where]
+    h = hdr[lane]  # fp32 columns: bytes 0, 1 masked, 2, 3 live; lanes 256.. are unit 1's
     assert h["byte_count"] > 8
+    uo = int(enc.unit_offsets[lane // 256].cpu())
     if where == "state":
         enc.headers.view(-1)[4 * lane] ^= 0x40  # final_state of unit 0, lane 2
+    elif where == "zero_header":
+        enc.headers.view(-1)[4 * lane] ^= 0x40  # final_state of unit 1, lane 4 (zero-plane)
+    elif where == "zero_last":
+        enc.data[uo + int(h["buf_offset"]) + int(h["byte_count"]) - 1] ^= 0x01
     else:
-        enc.data[int(h["buf_offset"]) + 5] ^= 0x10
+        enc.data[uo + int(h["buf_offset"]) + 5] ^= 0x10
     torch.cuda.synchronize()
     _, bad = ck.decode(enc)
     torch.cuda.synchronize()
-    assert bad >= 1
+    if where.startswith("zero"):
+        assert bad == 1
+    else:
+        assert bad >= 1
 
 
 @pytest.mark.parametrize("tag,unit", [(dg.F32, 1 << 20), (dg.BF16, 1 << 20), (dg.F32, 65536)])
