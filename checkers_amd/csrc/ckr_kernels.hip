@@ -253,11 +253,17 @@ __global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restr
     }
 }
 
+// Every workgroup ends with up to 768 global atomics (the sums of its LDS
+// copies), so the grid is kept small: 256 workgroups (one per CU) below 256
+// MiB, 512 above.  Measured on MI355X for a 4 GB fp32 tensor: 0.69 ms with 512
+// workgroups, 0.77 ms with 2048; for a 64 MiB one 17 us with 256, 46 us with
+// 2048.
 uint32_t hist_num_blocks(uint64_t n_bytes) {
     const uint64_t nvec = n_bytes / 16;
     uint64_t nb = (nvec + 1023) / 1024;  // >= 4 vectors per thread
+    const uint64_t cap = nvec >= (16ull << 20) ? 512 : 256;
     if (nb < 1) nb = 1;
-    if (nb > 2048) nb = 2048;
+    if (nb > cap) nb = cap;
     return (uint32_t)nb;
 }
 
