@@ -32,11 +32,15 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kHistCopies = 16;  // 8, 16, 32 within 2%; 64 (a copy per lane) 35% slower
-// loads in flight per thread: pass 1 is fastest with 4, pass 2 (more registers
-// for the histogram and the three power sums) with 2 (2.71 against 3.14 ms on cfg3)
-constexpr int kUnroll1 = 4, kUnroll2 = 2;
+// Loads in flight per thread, and the grid: at most 256 workgroups per record,
+// so that pass 2's closing global atomics (one per histogram bin and
+// workgroup) stay few.  Measured on the cfg3 shard (4 records of 1G elements):
+// 2048 workgroups per record and 2 loads in pass 2, 5.18 ms per call; 512,
+// 4.95; 256, 4.70; 256 with 4 loads in pass 2, 4.61 (passes at 6.27 and 6.01
+// TB/s); 128, 6.34 (pass 2 then lacks waves to hide its latency).
+constexpr int kUnroll1 = 4, kUnroll2 = 4;
 constexpr uint64_t kBytesPerBlock = 128 * 1024;
-constexpr uint32_t kMaxBlocksPerRecord = 2048;
+constexpr uint32_t kMaxBlocksPerRecord = 256;
 constexpr uint32_t kDescPerStore = 40;
 
 // A record as the kernels see it.
