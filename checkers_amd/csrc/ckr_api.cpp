@@ -257,6 +257,9 @@ struct PinnedWords {
     uint32_t* w = nullptr;  // kPinnedWords words
 };
 constexpr uint32_t kPinnedWords = 1024;
+// ckr_compress_many counts every histogram before any encode when no job is
+// larger than this (cfg2's largest tensor, gate_proj, is 117 MB).
+constexpr uint64_t kManySmallJobBytes = 256ull << 20;
 uint32_t* pinned_words() {
     thread_local std::vector<PinnedWords> per_dev;
     int dev = 0;
@@ -1019,6 +1022,8 @@ struct ManyAux {
     uint32_t* pinned = nullptr;  // 2 x 768 words
     uint32_t* slots = nullptr;   // 8 words per job: the deferred read-backs
     uint64_t slot_jobs = 0;
+    uint32_t* hists = nullptr;   // 768 words per job: histograms counted before any encode
+    uint64_t hist_jobs = 0;
 };
 hipError_t many_aux(ManyAux** out) {
     thread_local std::vector<ManyAux> per_dev;
@@ -1111,17 +1116,50 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
     };
     CKR_HIP(hipEventRecord(a->ev, s));  // inputs ready in the caller's stream order
     CKR_HIP(hipStreamWaitEvent(a->s2, a->ev, 0));
-    auto hist = [&](uint64_t i, uint32_t* h_dst) -> hipError_t {
+    auto hist = [&](uint64_t i, uint32_t* h_dst, bool lean) -> hipError_t {
         const ckr_compress_job& jb = jobs[i];
         const EncodeLayout L = encode_layout(geo[i]);
         uint32_t* d_hist = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(jb.d_workspace) + L.off_hist);
         const int es = ckr_element_size(jb.dtype);
         hipError_t e = ckr::launch_masked_hist(static_cast<const uint8_t*>(staged[i].p), jb.n_elems * (uint64_t)es, es,
-                                               geo[i].spe, d_hist, d_hist + 256, a->s2, i > 0);
+                                               geo[i].spe, d_hist, d_hist + 256, a->s2, lean);
         if (e != hipSuccess) return e;
         return hipMemcpyAsync(h_dst, d_hist, 768 * sizeof(uint32_t), hipMemcpyDeviceToHost, a->s2);
     };
-    CKR_HIP(hist(0, a->pinned));
+    // A shard of small tensors: every histogram first (full width, back to
+    // back), one synchronisation, then every encode queued without a host wait.
+    // Beside an encode of a few tens of microseconds the host round trip from a
+    // histogram to the next table (30-50 us) costs more than the histogram.
+    bool small = n > 1;
+    for (uint64_t i = 0; i < n && small; i++) small = geo[i].n_bytes <= kManySmallJobBytes;
+    if (small) {
+        if (a->hist_jobs < n) {
+            if (a->hists) CKR_HIP(hipHostFree(a->hists));
+            a->hists = nullptr;
+            a->hist_jobs = 0;
+            CKR_HIP(hipHostMalloc(reinterpret_cast<void**>(&a->hists), n * 768 * sizeof(uint32_t), hipHostMallocDefault));
+            a->hist_jobs = n;
+        }
+        for (uint64_t i = 0; i < n; i++) CKR_HIP(hist(i, a->hists + 768 * i, false));
+        CKR_HIP(hipStreamSynchronize(a->s2));
+        for (uint64_t i = 0; i < n; i++) {
+            ckr_compress_job& jb = jobs[i];
+            const uint32_t* hh = a->hists + 768 * i;
+            ckr_freq_table local;
+            ckr_freq_table* t = jb.h_table ? jb.h_table : &local;
+            int rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
+            if (rc == CKR_OK)
+                rc = encode_impl(staged[i].p, jb.n_elems, jb.dtype, t, unit_bytes, jb.d_out, jb.out_capacity,
+                                 jb.d_headers, jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace, jb.workspace_bytes,
+                                 nullptr, geo[i].spe ? hh + 256 : nullptr, stream, nullptr, &defs[i]);
+            if (rc) {
+                (void)complete(i);
+                return rc;
+            }
+        }
+        return complete(n);
+    }
+    CKR_HIP(hist(0, a->pinned, false));
     CKR_HIP(hipStreamSynchronize(a->s2));
     for (uint64_t i = 0; i < n; i++) {
         ckr_compress_job& jb = jobs[i];
@@ -1141,7 +1179,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             queued = true;
             const hipError_t e2 = hipStreamWaitEvent(a->s2, a->ev_prev, 0);
             if (e2 != hipSuccess) return e2;
-            return hist(i + 1, a->pinned + 768 * ((i + 1) & 1));
+            return hist(i + 1, a->pinned + 768 * ((i + 1) & 1), true);
         };
         // the encode is only queued: its read-backs are checked at the end, so
         // the next encode follows it on the stream without a host round trip

@@ -188,7 +188,9 @@ CKR_API int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_
  * (src/ANSCompressor.cpp:1118-1300, the GPU phases of each item): the same
  * results as ckr_compress called on each job in order, with job i+1's
  * histogram computed on a second, library-owned stream while job i is encoded
- * on `stream`, and the encodes queued back to back (each job's completion
+ * on `stream` (when no job exceeds 256 MiB, every histogram is computed first
+ * instead, with one host synchronisation for all of them), and the encodes
+ * queued back to back (each job's completion
  * words are read once, after the last).  Every job has its own buffers and
  * workspace (sizes as for ckr_compress).  The inputs must be ready in `stream`
  * order; the call returns when every job is done, with table and total filled

@@ -403,8 +403,9 @@ def test_encode_planes_matches_encode(tag, unit, paths, gpu):
 
 @pytest.mark.parametrize("unit", [65536, 1 << 20])
 def test_compress_many_matches_single_calls(unit, paths, gpu):
-    """ckr_compress_many (histograms overlapped with the previous encode) gives
-    each job exactly what ckr_compress gives it, and the oracle's bytes."""
+    """ckr_compress_many (jobs this small: every histogram first, then the
+    encodes back to back) gives each job exactly what ckr_compress gives it, and
+    the oracle's bytes."""
     import torch
     ck = _ck()
     specs = [(dg.F32, 300001, lambda n: dg.normal_f32(n, 1e-3, 70)),
@@ -465,15 +466,16 @@ def test_compress_many_repeated_byte_identical(gpu):
 
 
 def test_compress_many_large_overlapped_histogram(gpu):
-    """A tensor large enough that the histogram run beside the previous encode
-    (8 KiB of LDS, one workgroup per CU) covers it in several strides per
+    """A tensor above the 256 MiB bound under which compress_many counts every
+    histogram first, so that its histogram runs beside the previous encode (8
+    KiB of LDS, one workgroup per CU) and covers it in several strides per
     thread: compress_many still gives exactly what ckr_compress gives."""
     import torch
     ck = _ck()
     unit = 65536
     g = torch.Generator(device=gpu).manual_seed(80)
     a = (torch.randn(3_000_001, device=gpu, generator=g) * 0.02).to(torch.bfloat16)
-    b = torch.randn(16_777_216 + 4096 + 7, device=gpu, generator=g) * 1e-3
+    b = torch.randn(70_000_000 + 7, device=gpu, generator=g) * 1e-3
     srcs = [a.view(torch.uint8), b.view(torch.uint8)]
     specs = [(dg.BF16, a.numel()), (dg.F32, b.numel())]
     print("[case] compress_many large overlapped histogram", flush=True)
