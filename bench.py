@@ -422,7 +422,7 @@ def main():
     ap.add_argument("--unit", type=int, default=65536)
     ap.add_argument("--cpu-sample-mib", type=int, default=1024)
     ap.add_argument("--slice-gib", type=int, default=8, help="config 5: slice size of the streamed encode/decode")
-    ap.add_argument("--sequential", action="store_true", help="one ckr_compress per tensor, no overlap")
+    ap.add_argument("--sequential", action="store_true", help="one ckr_compress and one ckr_decode per tensor, no overlap")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-profile", action="store_true")
     ap.add_argument("--no-save", action="store_true", help="skip the end-to-end compress_and_save leg")
@@ -463,10 +463,12 @@ def main():
         return ck.compress_many(encs, [t for _, t in shard])
 
     def decode_all(results, check=False):
-        bads = []
-        for d, r, dst in zip(decs, results, dsts):
-            bads.append(d.decode(r.data, r.headers, r.unit_offsets, r.table, r.sidecar, dst, check=check))
-        return bads
+        # the shard's tensors in one ckr_decode_many call (tensors up to 256 MiB
+        # decoded side by side; --sequential: one ckr_decode per tensor)
+        if args.sequential:
+            return [d.decode(r.data, r.headers, r.unit_offsets, r.table, r.sidecar, dst, check=check)
+                    for d, r, dst in zip(decs, results, dsts)]
+        return ck.decode_many(decs, results, dsts, check=check)
 
     if args.copy_calibration:  # 1 GiB read + 1 GiB written by one elementwise copy kernel
         a = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)

@@ -29,8 +29,8 @@ EXPORTED = [  # every symbol include/checkers_amd.h declares
     "ckr_build_table",
     "ckr_num_units", "ckr_encode_max_output_bytes", "ckr_encode_workspace_bytes", "ckr_encode",
     "ckr_encode_planes",
-    "ckr_compress", "ckr_compress_many", "ckr_decode_workspace_bytes", "ckr_decode", "ckr_decode_noalloc",
-    "ckr_analyze_workspace_bytes",
+    "ckr_compress", "ckr_compress_many", "ckr_decode_workspace_bytes", "ckr_decode", "ckr_decode_many",
+    "ckr_decode_noalloc", "ckr_analyze_workspace_bytes",
     "ckr_analyze", "ckr_profile_begin", "ckr_profile_end", "ckr_set_fast_paths",
     "ckr_repair_masked_bits", "ckr_repair_bucket_count", "ckr_repair_workspace_bytes",
     "ckr_repair_build", "ckr_repair_apply",
@@ -133,6 +133,7 @@ def lib():
         "ckr_compress_many": (i32, [vp, u64, u64, i32, vp]),
         "ckr_decode_workspace_bytes": (u64, [u64, i32, u64]),
         "ckr_decode": (i32, [vp, vp, vp, vp, u64, i32, u64, vp, vp, vp, u64, vp, vp]),
+        "ckr_decode_many": (i32, [vp, u64, u64, i32, vp]),
         "ckr_decode_noalloc": (i32, [vp, vp, vp, vp, u64, i32, u64, vp, vp, vp, vp]),
         "ckr_analyze_workspace_bytes": (u64, [vp, u64]),
         "ckr_analyze": (i32, [vp, u64, vp, u64, vp]),
@@ -414,6 +415,35 @@ class Decoder:
             self.unit_bytes, sidecar.data_ptr() if sidecar is not None else None, dst.data_ptr(),
             self.ws.data_ptr(), self.ws_bytes, ctypes.byref(bad) if check else None, _stream(stream)))
         return bad.value if check else None
+
+
+class DecodeJob(ctypes.Structure):
+    _fields_ = [("d_data", ctypes.c_void_p), ("d_headers", ctypes.c_void_p), ("d_unit_offsets", ctypes.c_void_p),
+                ("h_table", ctypes.c_void_p), ("n_elems", ctypes.c_uint64), ("dtype", ctypes.c_int32),
+                ("pad", ctypes.c_int32), ("d_sidecar", ctypes.c_void_p), ("d_dst", ctypes.c_void_p),
+                ("d_workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_uint64), ("bad_lanes", ctypes.c_uint64)]
+
+
+def decode_many(decoders, encoded, dsts, check=True, stream=None):
+    """ckr_decode_many: encoded[k] (an Encoded, or any object with data,
+    headers, unit_offsets, table and sidecar) decoded by decoders[k] into
+    dsts[k], as Decoder.decode would; small tensors are decoded side by side on
+    several streams.  Returns the bad-lane counts (None when check is False)."""
+    if not (len(decoders) == len(encoded) == len(dsts)) or len({d.unit_bytes for d in decoders}) > 1:
+        raise CkrError(CKR_E_INVALID, "decode_many: one item and destination per decoder, one unit size")
+    if len({id(d) for d in decoders}) != len(decoders):
+        raise CkrError(CKR_E_INVALID, "decode_many: a Decoder appears twice (its workspace would be shared)")
+    if not decoders:
+        return [] if check else None
+    jobs = (DecodeJob * len(decoders))()
+    for jb, d, e, dst in zip(jobs, decoders, encoded, dsts):
+        jb.d_data, jb.d_headers, jb.d_unit_offsets = e.data.data_ptr(), e.headers.data_ptr(), e.unit_offsets.data_ptr()
+        jb.h_table, jb.n_elems, jb.dtype = ctypes.addressof(e.table.table), d.n_elems, d.dtype
+        jb.d_sidecar = e.sidecar.data_ptr() if e.sidecar is not None else None
+        jb.d_dst, jb.d_workspace, jb.workspace_bytes = dst.data_ptr(), d.ws.data_ptr(), d.ws_bytes
+    _check(lib().ckr_decode_many(ctypes.addressof(jobs), len(decoders), decoders[0].unit_bytes, int(bool(check)),
+                                 _stream(stream)))
+    return [jb.bad_lanes for jb in jobs] if check else None
 
 
 def decode(enc, dst=None, stream=None):

@@ -1017,6 +1017,7 @@ int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_b
 namespace {
 struct ManyAux {
     hipStream_t s2 = nullptr;
+    hipStream_t sx[2] = {nullptr, nullptr};  // with s2, the encodes of a shard of small tensors
     hipEvent_t ev = nullptr;
     hipEvent_t ev_prev = nullptr;  // the stream's work before the encode being queued
     uint32_t* pinned = nullptr;  // 2 x 768 words
@@ -1024,6 +1025,9 @@ struct ManyAux {
     uint64_t slot_jobs = 0;
     uint32_t* hists = nullptr;   // 768 words per job: histograms counted before any encode
     uint64_t hist_jobs = 0;
+    hipEvent_t ev_x[3] = {nullptr, nullptr, nullptr};  // s2, sx[0], sx[1] done (ckr_decode_many)
+    uint64_t* bads = nullptr;    // ckr_decode_many's bad-lane counts, one per job
+    uint64_t bad_jobs = 0;
 };
 hipError_t many_aux(ManyAux** out) {
     thread_local std::vector<ManyAux> per_dev;
@@ -1034,6 +1038,10 @@ hipError_t many_aux(ManyAux** out) {
     ManyAux& a = per_dev[dev];
     if (!a.s2) {
         if ((e = hipStreamCreateWithFlags(&a.s2, hipStreamNonBlocking)) != hipSuccess) return e;
+        for (hipStream_t& x : a.sx)
+            if ((e = hipStreamCreateWithFlags(&x, hipStreamNonBlocking)) != hipSuccess) return e;
+        for (hipEvent_t& x : a.ev_x)
+            if ((e = hipEventCreateWithFlags(&x, hipEventDisableTiming)) != hipSuccess) return e;
         if ((e = hipEventCreateWithFlags(&a.ev, hipEventDisableTiming)) != hipSuccess) return e;
         if ((e = hipEventCreateWithFlags(&a.ev_prev, hipEventDisableTiming)) != hipSuccess) return e;
         if ((e = hipHostMalloc(reinterpret_cast<void**>(&a.pinned), 2 * 768 * sizeof(uint32_t), hipHostMallocDefault)) !=
@@ -1102,9 +1110,12 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
     }
     std::vector<EncodeDeferred> defs(n);
     for (uint64_t i = 0; i < n; i++) defs[i].pin = a->slots + 8 * i;
-    // completes the encodes queued so far (jobs [0, upto)) once the stream has passed them
+    // the streams the encodes are queued on: the caller's, and in the
+    // histograms-first mode below three of the library's as well
+    std::vector<hipStream_t> enc_streams{s};
+    // completes the encodes queued so far (jobs [0, upto)) once the streams have passed them
     auto complete = [&](uint64_t upto) -> int {
-        CKR_HIP(hipStreamSynchronize(s));
+        for (hipStream_t x : enc_streams) CKR_HIP(hipStreamSynchronize(x));
         bool more = false;
         int first = CKR_OK;
         for (uint64_t k = 0; k < upto; k++) {
@@ -1127,9 +1138,15 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         return hipMemcpyAsync(h_dst, d_hist, 768 * sizeof(uint32_t), hipMemcpyDeviceToHost, a->s2);
     };
     // A shard of small tensors: every histogram first (full width, back to
-    // back), one synchronisation, then every encode queued without a host wait.
-    // Beside an encode of a few tens of microseconds the host round trip from a
-    // histogram to the next table (30-50 us) costs more than the histogram.
+    // back), one synchronisation, then every encode queued without a host wait,
+    // round robin over four streams.  Beside an encode of a few tens of
+    // microseconds the host round trip from a histogram to the next table
+    // (30-50 us) costs more than the histogram, and the encoder of a small
+    // tensor has too few units to fill the device (a unit takes tens of
+    // microseconds), so encodes of different tensors run side by side.  Each
+    // job has its own workspace and outputs; the fast encoder's look-back waits
+    // only for units whose tickets resident workgroups hold, so kernels that
+    // share the device still finish.
     bool small = n > 1;
     for (uint64_t i = 0; i < n && small; i++) small = geo[i].n_bytes <= kManySmallJobBytes;
     if (small) {
@@ -1141,7 +1158,9 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             a->hist_jobs = n;
         }
         for (uint64_t i = 0; i < n; i++) CKR_HIP(hist(i, a->hists + 768 * i, false));
+        for (hipStream_t x : a->sx) CKR_HIP(hipStreamWaitEvent(x, a->ev, 0));  // inputs ready
         CKR_HIP(hipStreamSynchronize(a->s2));
+        enc_streams = {s, a->s2, a->sx[0], a->sx[1]};
         for (uint64_t i = 0; i < n; i++) {
             ckr_compress_job& jb = jobs[i];
             const uint32_t* hh = a->hists + 768 * i;
@@ -1151,7 +1170,8 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             if (rc == CKR_OK)
                 rc = encode_impl(staged[i].p, jb.n_elems, jb.dtype, t, unit_bytes, jb.d_out, jb.out_capacity,
                                  jb.d_headers, jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace, jb.workspace_bytes,
-                                 nullptr, geo[i].spe ? hh + 256 : nullptr, stream, nullptr, &defs[i]);
+                                 nullptr, geo[i].spe ? hh + 256 : nullptr, enc_streams[i % enc_streams.size()],
+                                 nullptr, &defs[i]);
             if (rc) {
                 (void)complete(i);
                 return rc;
@@ -1322,6 +1342,83 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
                uint64_t* h_bad_lanes, void* stream) {
     return decode_impl(d_data, d_headers, d_unit_offsets, h_table, n_elems, dtype, unit_bytes, d_sidecar, d_dst,
                        d_workspace, workspace_bytes, h_bad_lanes, stream, false);
+}
+
+int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int check, void* stream) {
+    if (n == 0) return CKR_OK;
+    if (!jobs) return fail(CKR_E_INVALID, "[ckr] null job list");
+    for (uint64_t i = 0; i < n; i++) {
+        ckr::EncodeGeom g;
+        if (!dtype_ok(jobs[i].dtype) || !make_geom(jobs[i].n_elems, jobs[i].dtype, unit_bytes, &g))
+            return fail(CKR_E_INVALID, "[ckr] job %llu: bad dtype or size", (unsigned long long)i);
+        for (uint64_t k = 0; k < i; k++)  // jobs share no destination or workspace
+            if (jobs[k].d_workspace == jobs[i].d_workspace || (jobs[i].n_elems && jobs[k].d_dst == jobs[i].d_dst))
+                return fail(CKR_E_INVALID, "[ckr] jobs %llu and %llu share a destination or workspace buffer",
+                            (unsigned long long)k, (unsigned long long)i);
+        jobs[i].bad_lanes = 0;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    ManyAux* a = nullptr;
+    CKR_HIP(many_aux(&a));
+    // Jobs of up to 256 MiB each go round robin over four streams (the
+    // caller's and three of the library's): a small tensor has too few units to
+    // fill the device, and a unit takes tens of microseconds.  A larger job
+    // fills the device by itself: then every job goes on the caller's stream.
+    bool small = n > 1;
+    for (uint64_t i = 0; i < n && small; i++) {
+        ckr::EncodeGeom g;
+        make_geom(jobs[i].n_elems, jobs[i].dtype, unit_bytes, &g);
+        small = g.n_bytes <= kManySmallJobBytes;
+    }
+    std::vector<hipStream_t> pool{s};
+    if (small) {
+        pool = {s, a->s2, a->sx[0], a->sx[1]};
+        CKR_HIP(hipEventRecord(a->ev, s));  // inputs ready in the caller's stream order
+        for (size_t k = 1; k < pool.size(); k++) CKR_HIP(hipStreamWaitEvent(pool[k], a->ev, 0));
+    }
+    if (check && a->bad_jobs < n) {
+        if (a->bads) CKR_HIP(hipHostFree(a->bads));
+        a->bads = nullptr;
+        a->bad_jobs = 0;
+        CKR_HIP(hipHostMalloc(reinterpret_cast<void**>(&a->bads), n * sizeof(uint64_t), hipHostMallocDefault));
+        a->bad_jobs = n;
+    }
+    // every stream joins the caller's again, also when a job fails to queue
+    auto join = [&]() -> hipError_t {
+        for (size_t k = 1; k < pool.size(); k++) {
+            hipError_t e = hipEventRecord(a->ev_x[k - 1], pool[k]);
+            if (e == hipSuccess) e = hipStreamWaitEvent(s, a->ev_x[k - 1], 0);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    };
+    for (uint64_t i = 0; i < n; i++) {
+        const ckr_decode_job& jb = jobs[i];
+        hipStream_t js = pool[i % pool.size()];
+        int rc = decode_impl(jb.d_data, jb.d_headers, jb.d_unit_offsets, jb.h_table, jb.n_elems, jb.dtype, unit_bytes,
+                             jb.d_sidecar, jb.d_dst, jb.d_workspace, jb.workspace_bytes, nullptr, js, false);
+        if (rc == CKR_OK && check) {
+            ckr::EncodeGeom g;
+            make_geom(jb.n_elems, jb.dtype, unit_bytes, &g);
+            a->bads[i] = 0;
+            if (g.n_units) {
+                const DecodeLayout L = decode_layout(g);
+                if (hipMemcpyAsync(a->bads + i, static_cast<uint8_t*>(jb.d_workspace) + L.off_bad, 8,
+                                   hipMemcpyDeviceToHost, js) != hipSuccess)
+                    rc = fail(CKR_E_HIP, "[ckr] job %llu: bad-lane read-back failed", (unsigned long long)i);
+            }
+        }
+        if (rc) {
+            (void)join();
+            return set_job_error(rc, i);
+        }
+    }
+    CKR_HIP(join());
+    if (check) {
+        CKR_HIP(hipStreamSynchronize(s));
+        for (uint64_t i = 0; i < n; i++) jobs[i].bad_lanes = a->bads[i];
+    }
+    return CKR_OK;
 }
 
 int ckr_decode_noalloc(const uint8_t* d_data, const ckr_stream_header* d_headers, const uint64_t* d_unit_offsets,

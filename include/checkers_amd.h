@@ -226,6 +226,33 @@ CKR_API int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers
                        void* d_workspace, uint64_t workspace_bytes,
                        uint64_t* h_bad_lanes, void* stream);
 
+/* ---- several decodes in one call; no counterpart in the reference (it has
+ * no decoder).  For restoring a shard: the same results as ckr_decode called
+ * on each job.  When no job's output exceeds 256 MiB the jobs go round robin
+ * over the caller's stream and three library-owned streams, so that the
+ * decodes of small tensors (too few units to fill the device) run side by
+ * side; otherwise they run in order on `stream`.  The inputs must be ready in
+ * `stream` order, and the outputs are ready in `stream` order when the call
+ * returns work queued (check == 0, no synchronisation).  check != 0: the call
+ * synchronises and fills each job's bad_lanes.  Jobs share no destination or
+ * workspace (sizes as for ckr_decode). ---- */
+typedef struct {
+    const uint8_t* d_data;
+    const ckr_stream_header* d_headers;
+    const uint64_t* d_unit_offsets;
+    const ckr_freq_table* h_table;
+    uint64_t n_elems;
+    int32_t dtype;
+    int32_t pad;
+    const uint8_t* d_sidecar;
+    void* d_dst;
+    void* d_workspace;
+    uint64_t workspace_bytes;
+    uint64_t bad_lanes;  /* filled when check != 0 */
+} ckr_decode_job;
+CKR_API int ckr_decode_many(ckr_decode_job* jobs, uint64_t n_jobs, uint64_t unit_bytes, int check,
+                            void* stream);
+
 /* ---- decode that allocates nothing; no counterpart in the reference.  For
  * callers that cannot allocate device memory: code under HIP graph capture,
  * serving loops that restore shards on the fly, harnesses that forbid

@@ -436,6 +436,47 @@ def test_compress_many_matches_single_calls(unit, paths, gpu):
         ck.compress_many([encs[0], encs[0]], [srcs[0], srcs[0]])
 
 
+def test_decode_many_matches_single_decodes(gpu):
+    """ckr_decode_many (tensors this small decoded side by side on four
+    streams) restores every job bit-exact and reports each job's bad lanes as
+    ckr_decode does: a job whose stream bytes were corrupted counts its own bad
+    lanes and no other job counts any; check=False queues the same work without
+    a synchronisation; one Decoder twice is refused."""
+    import torch
+    ck = _ck()
+    g = torch.Generator(device=gpu).manual_seed(81)
+    ts = [(torch.randn(n, device=gpu, generator=g) * sc).to(dt) for n, sc, dt in
+          ((300_001, 0.02, torch.bfloat16), (1 << 20, 1e-3, torch.float32), (5, 1e-3, torch.float32),
+           (2_000_003, 0.02, torch.bfloat16), (0, 1.0, torch.float32), (700_000, 1e-3, torch.float32))]
+    tags = [ck.torch_tag(t.dtype) for t in ts]
+    srcs = [t.view(torch.uint8) for t in ts]
+    print("[case] decode_many", flush=True)
+    encs = ck.compress_many([ck.Encoder(t.numel(), tag, 65536, device=gpu) for t, tag in zip(ts, tags)], srcs)
+    decs = [ck.Decoder(t.numel(), tag, 65536, device=gpu) for t, tag in zip(ts, tags)]
+    dsts = [torch.empty(max(s.numel(), 1), dtype=torch.uint8, device=gpu) for s in srcs]
+    bads = ck.decode_many(decs, encs, dsts)
+    assert bads == [0] * len(ts)
+    for s, d in zip(srcs, dsts):
+        assert torch.equal(d[: s.numel()], s)
+    for d in dsts:
+        d.zero_()
+    assert ck.decode_many(decs, encs, dsts, check=False) is None
+    torch.cuda.synchronize()
+    for s, d in zip(srcs, dsts):
+        assert torch.equal(d[: s.numel()], s)
+    # corrupt job 3's stream bytes in the middle of its data
+    e3 = encs[3]
+    mid = e3.total // 2
+    e3.data[mid: mid + 64] ^= 0x5A
+    one = decs[3].decode(e3.data, e3.headers, e3.unit_offsets, e3.table, e3.sidecar,
+                         torch.empty_like(dsts[3]))
+    assert one > 0
+    bads = ck.decode_many(decs, encs, dsts)
+    assert bads[3] == one and all(b == 0 for k, b in enumerate(bads) if k != 3)
+    with pytest.raises(ck.CkrError):
+        ck.decode_many([decs[0], decs[0]], encs[:2], dsts[:2])
+
+
 def test_compress_many_repeated_byte_identical(gpu):
     """Regression for a race between the fast encoder's packer waves (one of them
     wrote the lane records over the exchange words before the others had read
