@@ -1179,6 +1179,17 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         }
         return complete(n);
     }
+    // Larger tensors: job i's encode goes on es[i % 2] (the caller's stream and
+    // one of the library's), so that job i+1's encode takes the CUs that job
+    // i's workgroups leave as its last units finish, instead of waiting for the
+    // last of them.  Job i+1's histogram waits for job i-1's encode (the work
+    // before job i's), so that it starts with job i's encode.
+    hipStream_t es[2] = {s, a->sx[0]};
+    if (n > 1) {
+        CKR_HIP(hipStreamWaitEvent(a->sx[0], a->ev, 0));  // inputs ready
+        enc_streams = {s, a->sx[0]};
+    }
+    CKR_HIP(hipEventRecord(a->ev_prev, s));  // before job 0's encode: the inputs
     CKR_HIP(hist(0, a->pinned, false));
     CKR_HIP(hipStreamSynchronize(a->s2));
     for (uint64_t i = 0; i < n; i++) {
@@ -1189,10 +1200,9 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         int rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
         if (rc) return rc;
         // job i + 1's histogram is queued once job i's encode kernels are, and
-        // waits for the work queued before them (the host does not wait for
-        // encodes), so that it starts with job i's encode and the encoder's
-        // workgroups take their CUs first
-        CKR_HIP(hipEventRecord(a->ev_prev, s));
+        // waits for job i-1's encode (the host does not wait for encodes), so
+        // that it starts with job i's encode and the encoder's workgroups take
+        // their CUs first
         bool queued = i + 1 >= n;
         const AfterLaunch next = [&]() -> hipError_t {
             if (queued) return hipSuccess;
@@ -1205,13 +1215,14 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         // the next encode follows it on the stream without a host round trip
         rc = encode_impl(staged[i].p, jb.n_elems, jb.dtype, t, unit_bytes, jb.d_out, jb.out_capacity, jb.d_headers,
                          jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace, jb.workspace_bytes, nullptr,
-                         geo[i].spe ? hh + 256 : nullptr, stream, &next, &defs[i]);
+                         geo[i].spe ? hh + 256 : nullptr, es[i & 1], &next, &defs[i]);
         if (rc) {
             (void)hipStreamSynchronize(a->s2);
             (void)complete(i);
             return rc;
         }
         CKR_HIP(next());  // an empty job launches nothing
+        CKR_HIP(hipEventRecord(a->ev_prev, es[i & 1]));  // job i queued: job i+2's histogram waits for it
         if (i + 1 < n) CKR_HIP(hipStreamSynchronize(a->s2));
     }
     return complete(n);
@@ -1363,16 +1374,19 @@ int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int c
     // Jobs of up to 256 MiB each go round robin over four streams (the
     // caller's and three of the library's): a small tensor has too few units to
     // fill the device, and a unit takes tens of microseconds.  A larger job
-    // fills the device by itself: then every job goes on the caller's stream.
-    bool small = n > 1;
+    // fills the device by itself: then the jobs alternate between two streams,
+    // so that job i+1 takes the CUs job i leaves as its last units finish
+    // (cfg3 decode 6.42-6.47 -> 6.29 ms).
+    bool small = true;
     for (uint64_t i = 0; i < n && small; i++) {
         ckr::EncodeGeom g;
         make_geom(jobs[i].n_elems, jobs[i].dtype, unit_bytes, &g);
         small = g.n_bytes <= kManySmallJobBytes;
     }
     std::vector<hipStream_t> pool{s};
-    if (small) {
-        pool = {s, a->s2, a->sx[0], a->sx[1]};
+    if (n > 1) {
+        if (small) pool = {s, a->s2, a->sx[0], a->sx[1]};
+        else pool = {s, a->s2};
         CKR_HIP(hipEventRecord(a->ev, s));  // inputs ready in the caller's stream order
         for (size_t k = 1; k < pool.size(); k++) CKR_HIP(hipStreamWaitEvent(pool[k], a->ev, 0));
     }

@@ -187,10 +187,11 @@ CKR_API int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_
 /* ---- several tensors, as compress_and_save_all's workers take its items
  * (src/ANSCompressor.cpp:1118-1300, the GPU phases of each item): the same
  * results as ckr_compress called on each job in order, with job i+1's
- * histogram computed on a second, library-owned stream while job i is encoded
- * on `stream` (when no job exceeds 256 MiB, every histogram is computed first
- * instead, with one host synchronisation for all of them), and the encodes
- * queued back to back (each job's completion
+ * histogram computed on a second, library-owned stream while job i is encoded,
+ * the encodes alternating between `stream` and a third library-owned stream
+ * (when no job exceeds 256 MiB, every histogram is computed first instead, with
+ * one host synchronisation for all of them, and the encodes go round robin over
+ * four streams), and the encodes queued back to back (each job's completion
  * words are read once, after the last).  Every job has its own buffers and
  * workspace (sizes as for ckr_compress).  The inputs must be ready in `stream`
  * order; the call returns when every job is done, with table and total filled
@@ -231,7 +232,9 @@ CKR_API int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers
  * on each job.  When no job's output exceeds 256 MiB the jobs go round robin
  * over the caller's stream and three library-owned streams, so that the
  * decodes of small tensors (too few units to fill the device) run side by
- * side; otherwise they run in order on `stream`.  The inputs must be ready in
+ * side; otherwise they alternate between `stream` and one library-owned
+ * stream, so that each decode starts as the previous one's last units finish.
+ * The inputs must be ready in
  * `stream` order, and the outputs are ready in `stream` order when the call
  * returns work queued (check == 0, no synchronisation).  check != 0: the call
  * synchronises and fills each job's bad_lanes.  Jobs share no destination or
