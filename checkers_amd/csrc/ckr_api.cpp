@@ -1160,7 +1160,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         for (uint64_t i = 0; i < n; i++) CKR_HIP(hist(i, a->hists + 768 * i, false));
         for (hipStream_t x : a->sx) CKR_HIP(hipStreamWaitEvent(x, a->ev, 0));  // inputs ready
         CKR_HIP(hipStreamSynchronize(a->s2));
-        enc_streams = {s, a->s2, a->sx[0], a->sx[1]};
+        if (!g_prof_on) enc_streams = {s, a->s2, a->sx[0], a->sx[1]};
         for (uint64_t i = 0; i < n; i++) {
             ckr_compress_job& jb = jobs[i];
             const uint32_t* hh = a->hists + 768 * i;
@@ -1183,9 +1183,13 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
     // one of the library's), so that job i+1's encode takes the CUs that job
     // i's workgroups leave as its last units finish, instead of waiting for the
     // last of them.  Job i+1's histogram waits for job i-1's encode (the work
-    // before job i's), so that it starts with job i's encode.
-    hipStream_t es[2] = {s, a->sx[0]};
-    if (n > 1) {
+    // before job i's), so that it starts with job i's encode.  While
+    // ckr_profile_begin is in effect every encode goes on the caller's stream
+    // (here and in the small-shard mode above): a launch's profiling events
+    // then bracket its own kernel and not the one still draining on another
+    // stream.
+    hipStream_t es[2] = {s, g_prof_on ? s : a->sx[0]};
+    if (n > 1 && !g_prof_on) {
         CKR_HIP(hipStreamWaitEvent(a->sx[0], a->ev, 0));  // inputs ready
         enc_streams = {s, a->sx[0]};
     }
@@ -1376,7 +1380,9 @@ int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int c
     // fill the device, and a unit takes tens of microseconds.  A larger job
     // fills the device by itself: then the jobs alternate between two streams,
     // so that job i+1 takes the CUs job i leaves as its last units finish
-    // (cfg3 decode 6.42-6.47 -> 6.29 ms).
+    // (cfg3 decode 6.42-6.47 -> 6.29 ms).  While ckr_profile_begin is in
+    // effect every job goes on the caller's stream, so that a launch's
+    // profiling events bracket its own kernel.
     bool small = true;
     for (uint64_t i = 0; i < n && small; i++) {
         ckr::EncodeGeom g;
@@ -1384,7 +1390,7 @@ int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int c
         small = g.n_bytes <= kManySmallJobBytes;
     }
     std::vector<hipStream_t> pool{s};
-    if (n > 1) {
+    if (n > 1 && !g_prof_on) {
         if (small) pool = {s, a->s2, a->sx[0], a->sx[1]};
         else pool = {s, a->s2};
         CKR_HIP(hipEventRecord(a->ev, s));  // inputs ready in the caller's stream order

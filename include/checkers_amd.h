@@ -474,7 +474,10 @@ CKR_API int ckr_set_fast_paths(int mode);
 /* ---- per-kernel timing, no counterpart in the reference (its only timings are
  * host wall clocks, ANSCompressor.hpp:105-110).  Between begin and end every
  * kernel the library launches is bracketed by HIP events on its stream; end
- * synchronises them and writes "<kernel> <launches> <total_ms>" lines.  With
+ * synchronises them and writes "<kernel> <launches> <total_ms>" lines.
+ * Meanwhile ckr_compress_many and ckr_decode_many queue every encode and decode
+ * on the caller's stream, so that each launch's events bracket its own kernel
+ * and not one still running on another stream.  With
  * CKR_PROFILE_PHASES=1 in the environment the fast encoder also stamps each
  * unit's phases (extra work inside the kernel), reported as encode_fast.* lines. ---- */
 CKR_API int ckr_profile_begin(void);
