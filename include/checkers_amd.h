@@ -238,7 +238,8 @@ CKR_API int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers
  * `stream` order, and the outputs are ready in `stream` order when the call
  * returns work queued (check == 0, no synchronisation).  check != 0: the call
  * synchronises and fills each job's bad_lanes.  Jobs share no destination or
- * workspace (sizes as for ckr_decode). ---- */
+ * workspace (sizes as for ckr_decode).  On error, the jobs before the failing
+ * one are queued and complete in `stream` order. ---- */
 typedef struct {
     const uint8_t* d_data;
     const ckr_stream_header* d_headers;

@@ -477,6 +477,33 @@ def test_decode_many_matches_single_decodes(gpu):
         ck.decode_many([decs[0], decs[0]], encs[:2], dsts[:2])
 
 
+def test_decode_many_large_jobs_alternate_streams(gpu):
+    """Jobs above 256 MiB (decoded alternately on two streams, each starting as
+    the previous one drains): every job bit-exact with no bad lanes, with and
+    without the synchronising check."""
+    import torch
+    ck = _ck()
+    g = torch.Generator(device=gpu).manual_seed(82)
+    ts = [torch.randn(70_000_003, device=gpu, generator=g) * 1e-3,
+          (torch.randn(3_000_001, device=gpu, generator=g) * 0.02).to(torch.bfloat16),
+          torch.randn(68_000_000, device=gpu, generator=g) * 1e-3]
+    tags = [ck.torch_tag(t.dtype) for t in ts]
+    srcs = [t.view(torch.uint8) for t in ts]
+    print("[case] decode_many large jobs", flush=True)
+    encs = ck.compress_many([ck.Encoder(t.numel(), tag, 65536, device=gpu) for t, tag in zip(ts, tags)], srcs)
+    decs = [ck.Decoder(t.numel(), tag, 65536, device=gpu) for t, tag in zip(ts, tags)]
+    dsts = [torch.empty_like(s) for s in srcs]
+    assert ck.decode_many(decs, encs, dsts) == [0, 0, 0]
+    for s, d in zip(srcs, dsts):
+        assert torch.equal(d, s)
+    for d in dsts:
+        d.zero_()
+    ck.decode_many(decs, encs, dsts, check=False)
+    torch.cuda.synchronize()
+    for s, d in zip(srcs, dsts):
+        assert torch.equal(d, s)
+
+
 def test_compress_many_repeated_byte_identical(gpu):
     """Regression for a race between the fast encoder's packer waves (one of them
     wrote the lane records over the exchange words before the others had read
@@ -517,8 +544,9 @@ def test_compress_many_large_overlapped_histogram(gpu):
     g = torch.Generator(device=gpu).manual_seed(80)
     a = (torch.randn(3_000_001, device=gpu, generator=g) * 0.02).to(torch.bfloat16)
     b = torch.randn(70_000_000 + 7, device=gpu, generator=g) * 1e-3
-    srcs = [a.view(torch.uint8), b.view(torch.uint8)]
-    specs = [(dg.BF16, a.numel()), (dg.F32, b.numel())]
+    c = (torch.randn(5_000_011, device=gpu, generator=g) * 0.02).to(torch.bfloat16)
+    srcs = [a.view(torch.uint8), b.view(torch.uint8), c.view(torch.uint8)]
+    specs = [(dg.BF16, a.numel()), (dg.F32, b.numel()), (dg.BF16, c.numel())]
     print("[case] compress_many large overlapped histogram", flush=True)
     many = ck.compress_many([ck.Encoder(n, dt, unit, device=gpu) for dt, n in specs], srcs)
     one = [ck.Encoder(n, dt, unit, device=gpu).compress(t) for (dt, n), t in zip(specs, srcs)]
