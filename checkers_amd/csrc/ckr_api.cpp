@@ -331,7 +331,7 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     L.off_hist = o;    o = align_up(o + 768 * 4, kAlign);
     L.off_canon = o;   o = align_up(o + 3ull * (4 + 2 * ck.cw) * 4, kAlign);
     L.off_status = o;  o = align_up(o + ckr::encode_fast_status_words(g.n_units) * 8, kAlign);
-    L.off_ctl = o;     o = align_up(o + 16, kAlign);
+    L.off_ctl = o;     o = align_up(o + 24, kAlign);
     L.off_redo = o;    o = align_up(o + g.n_units * 4, kAlign);
     const bool seg = use_seg_encode(g);  // two passes: checkpoint records instead of lane scratch
     L.off_usize = o;   o = align_up(o + (seg ? g.n_units : bu) * 4, kAlign);
@@ -727,9 +727,6 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
     const bool dedup = use_dedup(g);
     const CanonKs ck = canon_ks(g);
     uint8_t* side = g.spe ? d_sidecar : nullptr;
-    CKR_HIP(ckr::launch_build_enc_table(ta, enc, s));
-    if (dedup) CKR_HIP(canon_launch(h_table, ck, canon, s));
-
     // escapes are possible unless the data's own live-plane histograms show
     // every symbol it contains has a slot
     // (planes_size_only: the histograms are a caller's, used for slot sizes only)
@@ -739,6 +736,32 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         for (int s2 = 0; s2 < 256; s2++)
             if ((h_planes[s2] || h_planes[256 + s2]) && !h_table->norm_freq[s2]) escapes = true;
     }
+    bool fast = use_fast_encode(g);
+    ckr::FastEncParamsHost fp{};
+    if (fast) {
+        fp.escapes = escapes;
+        const uint32_t K = (uint32_t)((g.unit + 255) / 256);
+        fp.cw = ck.cw;
+        const uint32_t cbmax = std::max(canon_stream_bytes(h_table, ck.k0),
+                                        std::max(canon_stream_bytes(h_table, ck.k1), canon_stream_bytes(h_table, ck.k2)));
+        fp.canon_bytes = std::min<uint32_t>((cbmax + 3) & ~3u, 4 * ck.cw);
+        if (g_fast_paths == 2) {
+            fp.sl0 = fp.sl1 = 8;
+        } else {
+            fp.sl0 = lane_slot_bytes(h_planes, h_table, K);
+            fp.sl1 = lane_slot_bytes(h_planes ? h_planes + 256 : nullptr, h_table, K);
+        }
+        fast = ckr::encode_fast_lds_bytes(fp, (uint32_t)max_lds_per_block()) != 0;
+    }
+    // the fast encoder's look-back status and control words are cleared by the
+    // launch that builds the encode entries
+    if (fast)
+        CKR_HIP(ckr::launch_build_enc_table_reset(ta, enc, reinterpret_cast<uint64_t*>(ws + L.off_status), g.n_units,
+                                                  reinterpret_cast<uint32_t*>(ws + L.off_ctl), s));
+    else
+        CKR_HIP(ckr::launch_build_enc_table(ta, enc, s));
+    if (dedup) CKR_HIP(canon_launch(h_table, ck, canon, s));
+
     if (use_seg_encode(g)) {
         auto* rec = reinterpret_cast<uint2*>(ws + L.off_rec);
         auto* aux = reinterpret_cast<uint32_t*>(ws + L.off_aux);
@@ -796,23 +819,6 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         return CKR_OK;
     }
 
-    bool fast = use_fast_encode(g);
-    ckr::FastEncParamsHost fp{};
-    if (fast) {
-        fp.escapes = escapes;
-        const uint32_t K = (uint32_t)((g.unit + 255) / 256);
-        fp.cw = ck.cw;
-        const uint32_t cbmax = std::max(canon_stream_bytes(h_table, ck.k0),
-                                        std::max(canon_stream_bytes(h_table, ck.k1), canon_stream_bytes(h_table, ck.k2)));
-        fp.canon_bytes = std::min<uint32_t>((cbmax + 3) & ~3u, 4 * ck.cw);
-        if (g_fast_paths == 2) {
-            fp.sl0 = fp.sl1 = 8;
-        } else {
-            fp.sl0 = lane_slot_bytes(h_planes, h_table, K);
-            fp.sl1 = lane_slot_bytes(h_planes ? h_planes + 256 : nullptr, h_table, K);
-        }
-        fast = ckr::encode_fast_lds_bytes(fp, (uint32_t)max_lds_per_block()) != 0;
-    }
     if (fast) {
         auto* status = reinterpret_cast<uint64_t*>(ws + L.off_status);
         auto* ctl = reinterpret_cast<uint32_t*>(ws + L.off_ctl);
@@ -835,16 +841,15 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
             defer->out = d_out;
             defer->redo = redo;
             defer->batch_units = L.batch_units;
-            CKR_HIP(hipMemcpyAsync(defer->pin, ctl, 16, hipMemcpyDeviceToHost, s));
-            CKR_HIP(hipMemcpyAsync(defer->pin + 4, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
+            // the control words and, in ctl[4..5], the total: one read-back
+            CKR_HIP(hipMemcpyAsync(defer->pin, ctl, 24, hipMemcpyDeviceToHost, s));
             return CKR_OK;
         }
-        // control words and the total in one synchronisation (the fast kernel
-        // publishes every unit's offset, redo units included)
+        // control words and the total (ctl[4..5]) in one read-back (the fast
+        // kernel publishes every unit's offset, redo units included)
         uint32_t* pw = pinned_words();
         if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
-        CKR_HIP(hipMemcpyAsync(pw, ctl, 16, hipMemcpyDeviceToHost, s));
-        CKR_HIP(hipMemcpyAsync(pw + 4, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
+        CKR_HIP(hipMemcpyAsync(pw, ctl, 24, hipMemcpyDeviceToHost, s));
         CKR_HIP(hipStreamSynchronize(s));
         uint32_t hctl[4];
         std::memcpy(hctl, pw, 16);
@@ -1080,6 +1085,13 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
                 return fail(CKR_E_INVALID, "[ckr] jobs %llu and %llu share an output or workspace buffer",
                             (unsigned long long)k, (unsigned long long)i);
     }
+    if (n == 1) {  // one job: ckr_compress on the caller's stream, no second stream or events
+        ckr_compress_job& jb = jobs[0];
+        const int rc = ckr_compress(jb.d_src, jb.n_elems, jb.dtype, unit_bytes, ensure_full_alphabet, jb.d_out,
+                                    jb.out_capacity, jb.d_headers, jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace,
+                                    jb.workspace_bytes, jb.h_table, &jb.total, stream);
+        return rc ? set_job_error(rc, 0) : CKR_OK;
+    }
     hipStream_t s = (hipStream_t)stream;
     ManyAux* a = nullptr;
     CKR_HIP(many_aux(&a));
@@ -1281,9 +1293,8 @@ int decode_impl(const uint8_t* d_data, const ckr_stream_header* d_headers, const
     auto* dec = reinterpret_cast<uint32_t*>(ws + L.off_dec);
     auto* bad = reinterpret_cast<unsigned long long*>(ws + L.off_bad);
     const CanonKs ck = canon_ks(g);
-    CKR_HIP(ckr::launch_build_dec_table(ta, dec, s));
+    CKR_HIP(ckr::launch_build_dec_table(ta, dec, bad, s));  // also clears the bad-lane counter
     if (L.fast) CKR_HIP(canon_launch(h_table, ck, canon, s));
-    CKR_HIP(ckr::launch_set_counter(bad, 0, s));
     // the decoders store 32-bit words at the 4-byte columns of the destination:
     // a destination that is only element-aligned receives a copy
     uint8_t* out = static_cast<uint8_t*>(d_dst);

@@ -52,7 +52,12 @@ int set_error(int code, const std::string& msg);
 // ------------------------------------------------------------------ launchers
 // All return hipError_t of the launch; geometry is decided inside.
 hipError_t launch_build_enc_table(const TableArg& t, EncSym* d_enc, hipStream_t s);
-hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, hipStream_t s);
+// The encode entries and the fast encoder's status and control words cleared,
+// in one launch (launch_encode_fast expects them).
+hipError_t launch_build_enc_table_reset(const TableArg& t, EncSym* d_enc, uint64_t* status, uint64_t n_units,
+                                        uint32_t* ctl, hipStream_t s);
+// bad (may be null): a bad-lane counter to clear in the same launch.
+hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, unsigned long long* bad, hipStream_t s);
 
 hipError_t launch_extract_mantissa(const uint8_t* src, uint64_t n_elems, int es, int spe,
                                    uint8_t* masked, uint8_t* sidecar, hipStream_t s);
@@ -84,8 +89,9 @@ hipError_t launch_encode_batch(const uint8_t* src, const EncodeGeom& g, uint64_t
                                hipStream_t s);
 
 // LDS-staged encode of all units (masked dtypes, units <= 64 KiB).  status:
-// encode_fast_status_words(n_units) u64, ctl: 4 u32 ({ticket, redo count, error, 0}), redo_list: n_units
-// u32 — units whose bytes must then be produced by launch_encode_batch.
+// encode_fast_status_words(n_units) u64, ctl: 6 u32 ({ticket, redo count, error, 0, total lo, total hi}),
+// both cleared beforehand by launch_build_enc_table_reset; redo_list: n_units u32 — units whose bytes
+// must then be produced by launch_encode_batch.
 struct FastEncParamsHost {
     uint32_t sl0, sl1, cw, canon_bytes;
     bool escapes;  // the data may hold symbols with f == 0 (table not built from it)

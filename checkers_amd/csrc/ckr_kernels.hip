@@ -26,8 +26,7 @@ static constexpr uint32_t L = 1u << 23;
 
 // ------------------------------------------------------------------ tables
 // Encode entries from norm/cum (see EncSym in ckr_internal.h for the algebra).
-__global__ void __launch_bounds__(256) build_enc_table_kernel(TableArg t, EncSym* out) {
-    const uint32_t s = threadIdx.x;
+__device__ __forceinline__ EncSym enc_entry(const TableArg& t, uint32_t s) {
     const uint32_t f = t.norm[s], cum = t.cum[s];
     EncSym e;
     if (f == 0) {
@@ -40,13 +39,33 @@ __global__ void __launch_bounds__(256) build_enc_table_kernel(TableArg t, EncSym
         const uint64_t rcp = ((1ull << (31 + l)) + f - 1) / f;
         e.rcp = (uint32_t)rcp; e.bias = cum; e.cmpl_rsh = (M - f) | ((l - 1) << 16); e.xmax = f << 19;
     }
-    out[s] = e;
+    return e;
+}
+
+__global__ void __launch_bounds__(256) build_enc_table_kernel(TableArg t, EncSym* out) {
+    out[threadIdx.x] = enc_entry(t, threadIdx.x);
+}
+
+// The fast encoder's set-up in one launch: the encode entries (block 0), its
+// look-back status words cleared, and its control words (ctl[0]: ticket
+// counter, ctl[1]: redo-list length, ctl[2]: look-back failure flag, ctl[4..5]:
+// the packed total, written with the last unit's offset) cleared.
+__global__ void __launch_bounds__(256) build_enc_table_reset_kernel(TableArg t, EncSym* out, uint64_t* status,
+                                                                    uint64_t n, uint32_t* ctl) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (blockIdx.x == 0) {
+        out[threadIdx.x] = enc_entry(t, threadIdx.x);
+        if (threadIdx.x < 6) ctl[threadIdx.x] = 0;
+    }
+    if (i < n) status[i] = 0;
 }
 
 // Decode slots from norm/cum: slot j in [cum[s], cum[s]+norm[s]) → s.  One
 // thread per slot (16 blocks of 256): the symbol is the last s with cum[s] <= j
-// and norm[s] > 0, found by binary search over the prefix sums.
-__global__ void __launch_bounds__(256) build_dec_table_kernel(TableArg t, uint32_t* out) {
+// and norm[s] > 0, found by binary search over the prefix sums.  bad (when not
+// null): the decoder's bad-lane counter, cleared here for the launch after.
+__global__ void __launch_bounds__(256) build_dec_table_kernel(TableArg t, uint32_t* out, unsigned long long* bad) {
+    if (bad && blockIdx.x == 0 && threadIdx.x == 0) *bad = 0;
     __shared__ uint32_t cum[257];
     for (uint32_t i = threadIdx.x; i < 257; i += 256) cum[i] = t.cum[i];
     __syncthreads();
@@ -1263,7 +1282,10 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
             const uint64_t off = lookback_wave(status, g.n_units, u, size, &ctl[2], j);
             if (j == 0) {
                 unit_off[u] = off;
-                if (u + 1 == g.n_units) unit_off[u + 1] = off + size;
+                if (u + 1 == g.n_units) {  // the total, also beside the control words (one read-back)
+                    unit_off[u + 1] = off + size;
+                    *reinterpret_cast<unsigned long long*>(ctl + 4) = off + size;
+                }
                 pc.off[s][0] = (uint32_t)off;
                 pc.off[s][1] = (uint32_t)(off >> 32);
             }
@@ -1403,12 +1425,6 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
     }
 }
 
-__global__ void encode_fast_reset_kernel(uint64_t* status, uint64_t n, uint32_t* ctl) {
-    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) status[i] = 0;
-    if (i < 4) ctl[i] = 0;
-}
-
 static uint32_t slot_stride(uint32_t sl) {
     // 4 bytes between slots: a stream that fills its slot exactly still writes one
     // dword below its start (the final partial dword, empty)
@@ -1441,10 +1457,7 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
     if (!pairs) return hipErrorInvalidValue;
     const uint32_t lb = ws_lds_bytes(pairs, fp.canon_bytes, fp.stride0, fp.stride1);
     const uint64_t n = g.n_units;
-    const uint64_t nst = encode_fast_status_words(n);  // unit words, block words, block counts
-    CKR_LAUNCH("encode_fast_reset_kernel", s, encode_fast_reset_kernel<<<(uint32_t)((nst + 255) / 256), 256, 0, s>>>(status, nst, ctl));
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    hipError_t e = hipSuccess;
     // persistent grid: as many workgroups as fit on the device at once (more
     // would only find the tickets gone), never more than the units need
     int dev = 0, ncu = 0;
@@ -2945,8 +2958,16 @@ hipError_t launch_build_enc_table(const TableArg& t, EncSym* d_enc, hipStream_t 
     CKR_LAUNCH("build_enc_table_kernel", s, build_enc_table_kernel<<<1, 256, 0, s>>>(t, d_enc));
     return hipGetLastError();
 }
-hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, hipStream_t s) {
-    CKR_LAUNCH("build_dec_table_kernel", s, build_dec_table_kernel<<<16, 256, 0, s>>>(t, d_dec));
+hipError_t launch_build_enc_table_reset(const TableArg& t, EncSym* d_enc, uint64_t* status, uint64_t n_units,
+                                        uint32_t* ctl, hipStream_t s) {
+    const uint64_t nst = encode_fast_status_words(n_units);  // unit words, block words, block counts
+    const uint32_t grid = (uint32_t)std::max<uint64_t>(1, (nst + 255) / 256);
+    CKR_LAUNCH("build_enc_table_reset_kernel", s,
+               build_enc_table_reset_kernel<<<grid, 256, 0, s>>>(t, d_enc, status, nst, ctl));
+    return hipGetLastError();
+}
+hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, unsigned long long* bad, hipStream_t s) {
+    CKR_LAUNCH("build_dec_table_kernel", s, build_dec_table_kernel<<<16, 256, 0, s>>>(t, d_dec, bad));
     return hipGetLastError();
 }
 
