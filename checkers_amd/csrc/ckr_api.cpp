@@ -1030,6 +1030,8 @@ struct ManyAux {
     uint64_t slot_jobs = 0;
     uint32_t* hists = nullptr;   // 768 words per job: histograms counted before any encode
     uint64_t hist_jobs = 0;
+    uint32_t* d_hists = nullptr;  // their device copy (one grid counts them all)
+    uint64_t d_hist_jobs = 0;
     hipEvent_t ev_x[3] = {nullptr, nullptr, nullptr};  // s2, sx[0], sx[1] done (ckr_decode_many)
     uint64_t* bads = nullptr;    // ckr_decode_many's bad-lane counts, one per job
     uint64_t bad_jobs = 0;
@@ -1169,7 +1171,21 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             CKR_HIP(hipHostMalloc(reinterpret_cast<void**>(&a->hists), n * 768 * sizeof(uint32_t), hipHostMallocDefault));
             a->hist_jobs = n;
         }
-        for (uint64_t i = 0; i < n; i++) CKR_HIP(hist(i, a->hists + 768 * i, false));
+        if (a->d_hist_jobs < n) {  // no earlier call is still using it: each returns complete
+            if (a->d_hists) CKR_HIP(hipFree(a->d_hists));
+            a->d_hists = nullptr;
+            a->d_hist_jobs = 0;
+            CKR_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_hists), n * 768 * sizeof(uint32_t)));
+            a->d_hist_jobs = n;
+        }
+        // every histogram in one grid (per 16 jobs) and one read-back: a launch
+        // and a copy per job cost more host time than their kernels take
+        std::vector<ckr::HistSrc> hs(n);
+        for (uint64_t i = 0; i < n; i++)
+            hs[i] = {static_cast<const uint8_t*>(staged[i].p), geo[i].n_bytes, ckr_element_size(jobs[i].dtype),
+                     (int)geo[i].spe};
+        CKR_HIP(ckr::launch_masked_hist_multi(hs.data(), (uint32_t)n, a->d_hists, a->s2));
+        CKR_HIP(hipMemcpyAsync(a->hists, a->d_hists, n * 768 * sizeof(uint32_t), hipMemcpyDeviceToHost, a->s2));
         for (hipStream_t x : a->sx) CKR_HIP(hipStreamWaitEvent(x, a->ev, 0));  // inputs ready
         CKR_HIP(hipStreamSynchronize(a->s2));
         if (!g_prof_on) enc_streams = {s, a->s2, a->sx[0], a->sx[1]};

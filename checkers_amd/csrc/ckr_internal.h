@@ -67,6 +67,27 @@ hipError_t launch_extract_mantissa(const uint8_t* src, uint64_t n_elems, int es,
 // lean: a variant with 8 KiB of LDS per workgroup, which fits on a CU beside
 // the fast encoder's workgroup, and one workgroup per CU (same counts).
 uint32_t hist_num_blocks(uint64_t n_bytes);
+// Several tensors' masked histograms (each with its live planes', 768 words at
+// d_hists + 768 k, overwritten) in one grid per kMaxHistJobs of them.
+struct HistSrc {
+    const uint8_t* src;
+    uint64_t n_bytes;
+    int es, spe;
+};
+static constexpr uint32_t kMaxHistJobs = 16;
+struct HistJob {
+    const uint8_t* src;   // 16-byte aligned; the head_n bytes before it are the tensor's first
+    uint64_t n_bytes;     // from src
+    uint64_t zero_count;  // bytes of the masked planes, counted into bin 0 in closed form
+    uint32_t* hist;       // 768 words
+    uint32_t blk0, nblk, head_n;
+    int32_t es, spe;
+};
+struct HistJobs {
+    uint32_t n;
+    HistJob j[kMaxHistJobs];
+};
+hipError_t launch_masked_hist_multi(const HistSrc* srcs, uint32_t n, uint32_t* d_hists, hipStream_t s);
 hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int spe, uint32_t* d_hist,
                               uint32_t* d_planes, hipStream_t s, bool lean = false);
 hipError_t launch_set_u64(uint64_t* p, uint64_t v, hipStream_t s);

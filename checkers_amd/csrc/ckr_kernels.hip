@@ -205,16 +205,17 @@ __global__ void __launch_bounds__(256) hist_init_kernel(uint32_t* __restrict__ h
 // (head_n is then a multiple of the element size, so every byte keeps its
 // plane).  Positions below are counted from src; a head byte at src - head_n +
 // i is at position i - head_n.
+// One workgroup's share (block b of nb) of one tensor's histogram, added into
+// hist (and planes) at the end; sh: the workgroup's LDS copies.
 template <int SPE, int PC>
-__global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restrict__ src, uint64_t n_bytes,
-                                                          int es, uint32_t* __restrict__ hist,
-                                                          uint32_t* __restrict__ planes, uint32_t head_n) {
+__device__ __forceinline__ void masked_hist_share(uint32_t* sh, const uint8_t* __restrict__ src, uint64_t n_bytes,
+                                                  int es, uint32_t* __restrict__ hist, uint32_t* __restrict__ planes,
+                                                  uint32_t head_n, uint32_t b, uint32_t nb) {
     constexpr uint32_t NSH = SPE == 0 ? 256 * HIST_COPIES : 512 * PC;
-    __shared__ uint32_t sh[NSH];
     for (uint32_t i = threadIdx.x; i < NSH; i += blockDim.x) sh[i] = 0;
     __syncthreads();
     const uint32_t c = threadIdx.x & (HIST_COPIES - 1);
-    if (blockIdx.x == 0 && threadIdx.x < head_n) {  // head bytes
+    if (b == 0 && threadIdx.x < head_n) {  // head bytes
         const int64_t p = (int64_t)threadIdx.x - (int64_t)head_n;
         const int plane = (int)(((p % es) + es) % es);
         if (plane >= SPE) {
@@ -224,8 +225,8 @@ __global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restr
     }
     const uint64_t nvec = n_bytes / 16;
     const uint4* v4 = reinterpret_cast<const uint4*>(src);
-    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-    uint64_t v = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const uint64_t stride = (uint64_t)nb * blockDim.x;
+    uint64_t v = (uint64_t)b * blockDim.x + threadIdx.x;
     for (; v + 3 * stride < nvec; v += 4 * stride) {  // 4 loads in flight per thread
         uint4 a = v4[v], b = v4[v + stride], d = v4[v + 2 * stride], e = v4[v + 3 * stride];
         hist_add_dword<SPE, PC>(sh, a.x, c); hist_add_dword<SPE, PC>(sh, a.y, c);
@@ -242,7 +243,7 @@ __global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restr
         hist_add_dword<SPE, PC>(sh, a.x, c); hist_add_dword<SPE, PC>(sh, a.y, c);
         hist_add_dword<SPE, PC>(sh, a.z, c); hist_add_dword<SPE, PC>(sh, a.w, c);
     }
-    if (blockIdx.x == 0) {  // tail bytes
+    if (b == 0) {  // tail bytes
         for (uint64_t p = nvec * 16 + threadIdx.x; p < n_bytes; p += blockDim.x) {
             const int plane = (int)(p % (uint64_t)es);
             if (plane < SPE) continue;
@@ -270,6 +271,34 @@ __global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restr
             if (s1) atomicAdd(&planes[256 + bin], s1);
         }
     }
+}
+
+template <int SPE, int PC>
+__global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restrict__ src, uint64_t n_bytes,
+                                                          int es, uint32_t* __restrict__ hist,
+                                                          uint32_t* __restrict__ planes, uint32_t head_n) {
+    __shared__ uint32_t sh[SPE == 0 ? 256 * HIST_COPIES : 512 * PC];
+    masked_hist_share<SPE, PC>(sh, src, n_bytes, es, hist, planes, head_n, blockIdx.x, gridDim.x);
+}
+
+// Several tensors' histograms in one grid (ckr_compress_many on a shard of
+// small tensors): block b works for the last job whose first block is <= b.
+// Each job's 768 words (histogram, then the two live planes') are set up by
+// hist_init_multi_kernel, one block per job, before it.
+__global__ void __launch_bounds__(256) hist_init_multi_kernel(HistJobs jobs) {
+    const HistJob& j = jobs.j[blockIdx.x];
+    for (uint32_t i = threadIdx.x; i < 768; i += blockDim.x) j.hist[i] = (i == 0) ? (uint32_t)j.zero_count : 0u;
+}
+
+__global__ void __launch_bounds__(256) masked_hist_multi_kernel(HistJobs jobs) {
+    __shared__ uint32_t sh[256 * HIST_COPIES];  // = 512 x 16, the masked dtypes' copies
+    uint32_t k = 0;
+    while (k + 1 < jobs.n && jobs.j[k + 1].blk0 <= blockIdx.x) k++;
+    const HistJob& j = jobs.j[k];
+    const uint32_t b = blockIdx.x - j.blk0;
+    if (j.spe == 2) masked_hist_share<2, 16>(sh, j.src, j.n_bytes, j.es, j.hist, j.hist + 256, j.head_n, b, j.nblk);
+    else if (j.spe == 1) masked_hist_share<1, 16>(sh, j.src, j.n_bytes, j.es, j.hist, j.hist + 256, j.head_n, b, j.nblk);
+    else masked_hist_share<0, 16>(sh, j.src, j.n_bytes, j.es, j.hist, nullptr, j.head_n, b, j.nblk);
 }
 
 // Every workgroup ends with up to 768 global atomics (the sums of its LDS
@@ -317,6 +346,42 @@ hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int 
     else if (spe == 1) lean ? run(masked_hist_kernel<1, 4>) : run(masked_hist_kernel<1, 16>);
     else run(masked_hist_kernel<0, 16>);
     return hipGetLastError();
+}
+
+hipError_t launch_masked_hist_multi(const HistSrc* srcs, uint32_t n, uint32_t* d_hists, hipStream_t s) {
+    // one grid of about 512 workgroups over all jobs, in proportion to their
+    // bytes (each workgroup ends with up to 768 global atomics), at least one
+    // each and never more than a lone launch would take
+    for (uint32_t j0 = 0; j0 < n; j0 += kMaxHistJobs) {
+        const uint32_t m = std::min<uint32_t>(kMaxHistJobs, n - j0);
+        HistJobs jobs{};
+        jobs.n = m;
+        uint64_t total = 0;
+        for (uint32_t k = 0; k < m; k++) total += srcs[j0 + k].n_bytes;
+        uint32_t nb = 0;
+        for (uint32_t k = 0; k < m; k++) {
+            const HistSrc& x = srcs[j0 + k];
+            HistJob& j = jobs.j[k];
+            const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(x.src) & 15u);
+            j.head_n = (uint32_t)std::min<uint64_t>(mis ? 16u - mis : 0u, x.n_bytes);
+            j.src = x.src + j.head_n;
+            j.n_bytes = x.n_bytes - j.head_n;
+            j.es = x.es;
+            j.spe = x.spe;
+            j.zero_count = (x.es > 0) ? (x.n_bytes / (uint64_t)x.es) * (uint64_t)x.spe : 0;
+            j.hist = d_hists + 768ull * (j0 + k);
+            const uint64_t share = total ? (512ull * x.n_bytes + total - 1) / total : 1;
+            j.nblk = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(share, hist_num_blocks(j.n_bytes)));
+            j.blk0 = nb;
+            nb += j.nblk;
+        }
+        CKR_LAUNCH("hist_init_multi_kernel", s, hist_init_multi_kernel<<<m, 256, 0, s>>>(jobs));
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        CKR_LAUNCH("masked_hist_multi_kernel", s, masked_hist_multi_kernel<<<nb, 256, 0, s>>>(jobs));
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 // Small fills used instead of hipMemsetAsync (safe inside captured graphs).
