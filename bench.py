@@ -177,6 +177,211 @@ def cpu_baseline(shard, ck, sample_bytes_per_tensor, unit, reps=5):
                                    seconds=round(sec1, 4), runs_s=all_t1))
 
 
+def sha256_tensors(shard, chunk=1 << 28):
+    """SHA-256 of each tensor's bytes (the seeded inputs behind a number), hashed
+    on the host in 256 MiB pieces, one thread per tensor."""
+    import hashlib
+    from concurrent.futures import ThreadPoolExecutor
+    import torch
+
+    def one(t):
+        h = hashlib.sha256()
+        b = t.reshape(-1).view(torch.uint8)
+        for i in range(0, b.numel(), chunk):
+            h.update(b[i:i + chunk].cpu().numpy())
+        return h.hexdigest()
+
+    with ThreadPoolExecutor(max_workers=min(len(shard), 8)) as ex:
+        return dict(zip([n for n, _ in shard], ex.map(one, [t for _, t in shard])))
+
+
+def analyze_cpu_baseline(shard, ck, sample_bytes_per_tensor=512 << 20, piece=64 << 20, reps=3):
+    """The oracle's statistics pass (its fp32 reduction order follows the
+    reference kernel's 256 threads) on a bounded sample: the first
+    `sample_bytes_per_tensor` of each tensor cut into `piece`-byte ranges, the
+    ranges spread over the threads this GPU's share of the host allows; best of
+    `reps` after a warm-up."""
+    from concurrent.futures import ThreadPoolExecutor
+    import oracle as oc
+    import torch
+    nproc, avail, model = host_cpu()
+    threads = max(1, min(avail, 16))
+    jobs = []
+    for _, t in shard:
+        tag = ck.torch_tag(t.dtype)
+        es = t.element_size()
+        n = min(t.numel(), sample_bytes_per_tensor // es)
+        raw = t[:n].contiguous().view(torch.uint8).cpu().numpy()
+        step = piece // es
+        for i in range(0, n, step):
+            m = min(step, n - i)
+            jobs.append((raw[i * es:(i + m) * es], m, tag))
+    total = sum(j[0].size for j in jobs)
+
+    def run():
+        t0 = time.perf_counter()
+        with ThreadPoolExecutor(max_workers=threads) as ex:
+            list(ex.map(lambda j: oc.tensor_stats(j[0], j[1], j[2], 256), jobs))
+        return time.perf_counter() - t0
+
+    run()
+    sec = min(run() for _ in range(reps))
+    return dict(value=round(total / sec / 1e9, 4), unit="GB/s", cores=threads, kind="port",
+                sample=f"first {sample_bytes_per_tensor >> 20} MiB of each of the {len(shard)} tensors "
+                       f"({total / 1e6:.0f} MB) in {piece >> 20} MiB ranges: the oracle's two-pass statistics "
+                       f"(min/max/sum, then 256-bin histogram and central moments), {threads} threads over the "
+                       f"ranges, best of {reps}", seconds=round(sec, 4), host=dict(nproc=nproc, model=model))
+
+
+def repair_cpu_baseline(shard, names=("k_proj", "v_proj", "input_layernorm", "post_attention_layernorm")):
+    """The oracle's Re-Pair (the reference CLI's loop: one std::unordered_map of
+    pair counts per round, one thread) on cfg2's smaller tensors, 50 rules each,
+    as the reference's CLI runs it."""
+    import oracle as oc
+    import torch
+    d = dict(shard)
+    per, tot_t, tot_n = [], 0.0, 0
+    for name in names:
+        t = d[name]
+        raw = t.view(torch.uint8).cpu().numpy()
+        t0 = time.perf_counter()
+        r = oc.repair_build(raw, t.numel(), 2, 7, 50)
+        sec = time.perf_counter() - t0
+        per.append(dict(tensor=name, elements=t.numel(), rules=len(r["rules"]), build_ms=round(sec * 1e3, 2)))
+        tot_t += sec
+        tot_n += t.numel()
+    return dict(value=round(tot_n / tot_t / 1e6, 3), unit="M elements/s", cores=1, kind="port",
+                sample=f"grammar builds of {', '.join(names)} ({tot_n} bf16 words, 50 rules, all 7 mantissa bits "
+                       "masked), one thread", seconds=round(tot_t, 3), tensors=per)
+
+
+def reference_layout_leg(shard, ck, torch, dev):
+    """The reference's own stream layout (unit_bytes 0: one stream of 256 lanes
+    per tensor, the .ansc v2 files byte for byte) on one cfg3 fp32 tensor:
+    encode (histogram, table, one-unit encode on the general kernels) and decode,
+    each timed once with HIP events after a warm-up on the first 64 MiB."""
+    name, t = [x for x in shard if x[1].dtype == torch.float32][0]
+    tag = ck.torch_tag(t.dtype)
+    n = t.numel()
+    w = t[: 16 << 20]
+    ck.decode(ck.compress(w, tag, 0))
+    torch.cuda.synchronize()
+    e = ck.Encoder(n, tag, 0, device=dev)
+    a, b, c = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    a.record()
+    r = e.compress(t)
+    b.record()
+    torch.cuda.synchronize()
+    dst = torch.empty(n * 4, dtype=torch.uint8, device=dev)
+    d = ck.Decoder(n, tag, 0, device=dev)
+    b2 = torch.cuda.Event(enable_timing=True)
+    b2.record()
+    bad = d.decode(r.data, r.headers, r.unit_offsets, r.table, r.sidecar, dst)
+    c.record()
+    torch.cuda.synchronize()
+    ok = bad == 0 and torch.equal(dst, t.view(torch.uint8))
+    enc_ms, dec_ms = a.elapsed_time(b), b2.elapsed_time(c)
+    nb = n * 4
+    log(f"[bench] reference layout (one stream) {name}: encode {enc_ms:.1f} ms, decode {dec_ms:.1f} ms, ok={ok}")
+    out = dict(tensor=name, elements=n, unit_bytes=0, encode_ms=round(enc_ms, 3), decode_ms=round(dec_ms, 3),
+               encode_GBps=round(nb / enc_ms / 1e6, 3), decode_GBps=round(nb / dec_ms / 1e6, 3),
+               ans_ratio=round(nb / r.total, 4), roundtrip_bit_exact=ok,
+               note="one unit: 256 lanes, each coding n/256 symbols in order, so 64 threads of one wave "
+                    "do the whole tensor (the reference's own kernel runs 256 threads)")
+    del e, r, d, dst
+    torch.cuda.empty_cache()
+    return out
+
+
+def time_resident(shard, ck, torch, dev, unit, steps, warmup, sequential=False):
+    """Warm-up, then `steps` timed whole-shard encodes (ckr_compress_many) and
+    decodes (ckr_decode_many) with the inputs resident in HBM; then the bit-exact
+    round trip and lane checks.  Returns the measurements and the objects."""
+    encs = [ck.Encoder(t.numel(), ck.torch_tag(t.dtype), unit, device=dev) for _, t in shard]
+    decs = [ck.Decoder(t.numel(), ck.torch_tag(t.dtype), unit, device=dev) for _, t in shard]
+    dsts = [torch.empty_like(t) for _, t in shard]
+
+    def encode_all():
+        # the shard's tensors in one call: each histogram overlaps the previous
+        # tensor's encode (sequential: one ckr_compress per tensor)
+        if sequential:
+            return [e.compress(t) for e, (_, t) in zip(encs, shard)]
+        return ck.compress_many(encs, [t for _, t in shard])
+
+    def decode_all(results, check=False):
+        # the shard's tensors in one ckr_decode_many call (tensors up to 256 MiB
+        # decoded side by side; sequential: one ckr_decode per tensor)
+        if sequential:
+            return [d.decode(r.data, r.headers, r.unit_offsets, r.table, r.sidecar, dst, check=check)
+                    for d, r, dst in zip(decs, results, dsts)]
+        return ck.decode_many(decs, results, dsts, check=check)
+
+    for i in range(warmup):
+        res = encode_all()
+        decode_all(res)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        res = encode_all()
+    ev1.record()
+    torch.cuda.synchronize()
+    enc_wall = (time.perf_counter() - t0) / steps
+    enc_ev = ev0.elapsed_time(ev1) / 1e3 / steps
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        decode_all(res)
+    ev1.record()
+    torch.cuda.synchronize()
+    dec_wall = (time.perf_counter() - t0) / steps
+    dec_ev = ev0.elapsed_time(ev1) / 1e3 / steps
+    bads = decode_all(res, check=True)
+    roundtrip = all(torch.equal(d.view(torch.uint8), t.view(torch.uint8)) for d, (_, t) in zip(dsts, shard))
+    ok = roundtrip and all(b == 0 for b in bads)
+    n_in = sum(t.numel() * t.element_size() for _, t in shard)
+    C = sum(r.total for r in res)
+    S = sum(r.sidecar.numel() if r.sidecar is not None else 0 for r in res)
+    n_units = sum(e.n_units for e in encs)
+    H = n_units * 256 * 16 + (n_units + len(encs)) * 8 + len(encs) * 2308
+    B = n_in + S + C + H
+    m = dict(input_bytes=n_in, encode_ms=round(enc_wall * 1e3, 4), decode_ms=round(dec_wall * 1e3, 4),
+             encode_ms_events=round(enc_ev * 1e3, 4), decode_ms_events=round(dec_ev * 1e3, 4),
+             encode_GBps=round(n_in / enc_wall / 1e9, 3), decode_GBps=round(n_in / dec_wall / 1e9, 3),
+             encode_roofline_frac=round(B / enc_wall / 1e9 / HBM_PEAK_GBPS, 4),
+             decode_roofline_frac=round(B / dec_wall / 1e9 / HBM_PEAK_GBPS, 4),
+             compressed_bytes=C, sidecar_bytes=S, header_bytes=H, units=n_units,
+             ans_ratio=round(n_in / C, 4), disk_ratio=round(n_in / (C + S), 4),
+             device_ratio=round(n_in / (C + S + H), 4), roundtrip_bit_exact=ok)
+    state = dict(encs=encs, decs=decs, dsts=dsts, res=res, encode_all=encode_all, decode_all=decode_all,
+                 enc_wall=enc_wall, dec_wall=dec_wall, enc_ev=enc_ev, dec_ev=dec_ev, C=C, S=S, H=H, ok=ok)
+    return m, state
+
+
+WORKLOADS = {1: "cfg1 fp32 4096x4096 N(0,1e-3)", 2: "cfg2 llama3-8b decoder layer bf16",
+             3: "cfg3 llama3-8b zero3 rank0-of-8 shard (bf16 params, fp32 master, exp_avg, exp_avg_sq)",
+             4: "cfg4 adversarial fp32 256M", 5: "cfg5 llama3-70b zero3 rank0-of-8 shard"}
+
+
+def config_leg(cfg, ck, torch, dev, unit, steps, warmup):
+    """One of the other resident configurations, measured as the headline is
+    (encode and decode of the whole shard, round trip checked), with its
+    inputs' SHA-256."""
+    shard = make_shard(cfg, torch, dev)
+    sha = sha256_tensors(shard)
+    m, st = time_resident(shard, ck, torch, dev, unit, steps, warmup)
+    m.update(workload=WORKLOADS[cfg], unit_bytes=unit, tensors=[n for n, _ in shard],
+             elements_per_tensor=[t.numel() for _, t in shard], input_sha256=sha)
+    log(f"[bench] cfg{cfg}: encode {m['encode_ms']:.3f} ms ({m['encode_roofline_frac']}), decode "
+        f"{m['decode_ms']:.3f} ms ({m['decode_roofline_frac']}), ok={m['roundtrip_bit_exact']}")
+    del st, shard
+    torch.cuda.empty_cache()
+    return m
+
+
 class _ZeroParam:
     """A ZeRO-3 parameter as api.cpp reads it: requires_grad and ds_numel."""
 
@@ -221,6 +426,8 @@ def save_leg(shard, torch, unit, reps=2):
     checkers_py.analyze_tensors()
     t_an = time.perf_counter() - t0
     times, files = [], 0
+    logf = tempfile.mktemp(prefix="ckr_bench_log_")
+    os.environ["CHECKERS_LOG"] = logf   # the per-tensor lines of the reference's logger
     for r in range(reps):
         d = tempfile.mkdtemp(prefix="ckr_bench_")
         try:
@@ -232,9 +439,28 @@ def save_leg(shard, torch, unit, reps=2):
         finally:
             shutil.rmtree(d, ignore_errors=True)
         log(f"[bench] compress_and_save {r + 1}/{reps}: {times[-1]:.3f} s, {files / 1e9:.3f} GB of files")
+    del os.environ["CHECKERS_LOG"]
+    per_tensor, timing = [], {}
+    if os.path.exists(logf):
+        lines = open(logf).read().splitlines()
+        os.unlink(logf)
+        # the last call's lines: its tensors, then its summary and [TIMING] lines
+        last = max(i for i, ln in enumerate(lines) if "[summary]" in ln)
+        first = max([i + 1 for i, ln in enumerate(lines[:last]) if ln.startswith("[TIMING]")] or [0])
+        for ln in lines[first:last]:
+            kv = dict(x.split("=", 1) for x in ln.split("] ", 2)[-1].split() if "=" in x)
+            per_tensor.append({k: (v if k == "name" else float(v)) for k, v in kv.items()})
+        for ln in lines[last + 1:]:
+            if ln.startswith("[TIMING]"):
+                k, v = ln.split()[1].split("=")
+                timing[k] = float(v)
+    # a context over an engine with no parameters replaces this one: its arena,
+    # the writer's buffers and its references to the shard go
+    checkers_py.initialize_context(types.SimpleNamespace(
+        module=types.SimpleNamespace(named_parameters=lambda: iter([])), optimizer=None, global_rank=0))
     return dict(seconds=[round(t, 4) for t in times], best_s=round(min(times), 4), file_bytes=files,
                 initialize_context_s=round(t_init, 4), analyze_tensors_s=round(t_an, 4), unit_bytes=unit,
-                records=4 if opt is not None else len(params))
+                records=4 if opt is not None else len(params), per_tensor=per_tensor, timing=timing)
 
 
 def analyzer_leg(shard, ck, torch, steps):
@@ -274,7 +500,7 @@ def analyzer_leg(shard, ck, torch, steps):
                 kernels=kern)
 
 
-def repair_leg(ck, torch, dev):
+def repair_leg(ck, torch, dev, cpu=True):
     """cfg2's prefix-mask repair, per tensor (the group is the tensor): the
     grammar build (at most 50 rounds, all 7 bf16 mantissa bits masked), then
     applying it again, each timed on the wall clock around its call (the build
@@ -304,11 +530,22 @@ def repair_leg(ck, torch, dev):
                         build_ms=round(tb * 1e3, 3), apply_ms=round(ta * 1e3, 3)))
     log(f"[bench] repair cfg2: build {tot_b * 1e3:.1f} ms, apply {tot_a * 1e3:.1f} ms over {len(shard)} tensors")
     ach = tot_bytes_rounds / tot_b / 1e9
-    return dict(workload="cfg2 llama3-8b decoder layer bf16, group = each tensor, 50 rules", tensors=out,
-                build_ms=round(tot_b * 1e3, 3), apply_ms=round(tot_a * 1e3, 3),
-                roofline=dict(bound="hbm", kernel="repair build (all rounds)", unit="GB/s", peak=HBM_PEAK_GBPS,
-                              achieved=round(ach, 2), frac=round(ach / HBM_PEAK_GBPS, 4),
-                              algorithmic_bytes=tot_bytes_rounds))
+    leg = dict(workload="cfg2 llama3-8b decoder layer bf16, group = each tensor, 50 rules", tensors=out,
+               build_ms=round(tot_b * 1e3, 3), apply_ms=round(tot_a * 1e3, 3),
+               roofline=dict(bound="hbm", kernel="repair build (all rounds)", unit="GB/s", peak=HBM_PEAK_GBPS,
+                             achieved=round(ach, 2), frac=round(ach / HBM_PEAK_GBPS, 4),
+                             algorithmic_bytes=tot_bytes_rounds),
+               input_sha256=sha256_tensors(shard))
+    if cpu:
+        cb = repair_cpu_baseline(shard)
+        names = {x["tensor"] for x in cb["tensors"]}
+        g_ms = sum(x["build_ms"] for x in out if x["tensor"] in names)
+        g_n = sum(x["elements"] for x in out if x["tensor"] in names)
+        cb["gpu_same_sample"] = dict(value=round(g_n / (g_ms / 1e3) / 1e6, 3), unit="M elements/s",
+                                     build_ms=round(g_ms, 3))
+        leg["cpu_baseline"] = cb
+        log(f"[bench] repair cpu {cb['value']} M elements/s (GPU {cb['gpu_same_sample']['value']} on the same tensors)")
+    return leg
 
 
 def copy_ceiling(torch, dev, nbytes=4 << 30, reps=10, batches=3):
@@ -428,6 +665,10 @@ def main():
     ap.add_argument("--no-save", action="store_true", help="skip the end-to-end compress_and_save leg")
     ap.add_argument("--no-analyze", action="store_true", help="skip the analyzer leg")
     ap.add_argument("--no-repair", action="store_true", help="skip cfg2's prefix-mask repair leg")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other configurations' legs (cfg1/2/4/5)")
+    ap.add_argument("--no-cfg5", action="store_true", help="skip the cfg5 leg of the default run")
+    ap.add_argument("--no-reference-layout", action="store_true", help="skip the one-stream (v2) leg")
+    ap.add_argument("--no-sha", action="store_true", help="do not hash the inputs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device-to-device copy (known HBM traffic) for counter scaling")
     args = ap.parse_args()
@@ -446,29 +687,16 @@ def main():
     log(f"[bench] generating config {args.config} shard")
     shard = make_shard(args.config, torch, dev)
     n_in = sum(t.numel() * t.element_size() for _, t in shard)
+    names, elems = [n for n, _ in shard], [t.numel() for _, t in shard]
     log(f"[bench] {len(shard)} tensors, {n_in / 1e9:.3f} GB; unit {unit}")
+    sha = None if args.no_sha else sha256_tensors(shard)
     if args.config == 5:
-        run_streamed(args, shard, ck, torch, dev, unit, n_in)
+        out = run_streamed(args, shard, ck, torch, dev, unit, n_in)
+        out["config"]["input_sha256"] = sha
+        print(json.dumps(out), flush=True)
+        if not out["roundtrip_bit_exact"]:
+            sys.exit(1)
         return
-
-    encs = [ck.Encoder(t.numel(), ck.torch_tag(t.dtype), unit, device=dev) for _, t in shard]
-    decs = [ck.Decoder(t.numel(), ck.torch_tag(t.dtype), unit, device=dev) for _, t in shard]
-    dsts = [torch.empty_like(t) for _, t in shard]
-
-    def encode_all():
-        # the shard's tensors in one call: each histogram overlaps the previous
-        # tensor's encode (--sequential: one ckr_compress per tensor)
-        if args.sequential:
-            return [e.compress(t) for e, (_, t) in zip(encs, shard)]
-        return ck.compress_many(encs, [t for _, t in shard])
-
-    def decode_all(results, check=False):
-        # the shard's tensors in one ckr_decode_many call (tensors up to 256 MiB
-        # decoded side by side; --sequential: one ckr_decode per tensor)
-        if args.sequential:
-            return [d.decode(r.data, r.headers, r.unit_offsets, r.table, r.sidecar, dst, check=check)
-                    for d, r, dst in zip(decs, results, dsts)]
-        return ck.decode_many(decs, results, dsts, check=check)
 
     if args.copy_calibration:  # 1 GiB read + 1 GiB written by one elementwise copy kernel
         a = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
@@ -477,46 +705,13 @@ def main():
         torch.cuda.synchronize()
         del a, b
 
-    for i in range(args.warmup):
-        res = encode_all()
-        decode_all(res)
-        log(f"[bench] warmup {i + 1}/{args.warmup} done")
-    torch.cuda.synchronize()
-
-    # ---- timed encode steps
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record()
-    for _ in range(args.steps):
-        res = encode_all()
-    ev1.record()
-    torch.cuda.synchronize()
-    enc_wall = (time.perf_counter() - t0) / args.steps
-    enc_ev = ev0.elapsed_time(ev1) / 1e3 / args.steps
+    m, st = time_resident(shard, ck, torch, dev, unit, args.steps, args.warmup, args.sequential)
+    enc_wall, dec_wall, enc_ev, dec_ev = st["enc_wall"], st["dec_wall"], st["enc_ev"], st["dec_ev"]
+    C, S, H, ok = st["C"], st["S"], st["H"], st["ok"]
+    encs, encode_all, decode_all = st["encs"], st["encode_all"], st["decode_all"]
     log(f"[bench] encode {enc_wall * 1e3:.2f} ms/step wall, {enc_ev * 1e3:.2f} ms/step events")
-
-    # ---- timed decode steps
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record()
-    for _ in range(args.steps):
-        decode_all(res)
-    ev1.record()
-    torch.cuda.synchronize()
-    dec_wall = (time.perf_counter() - t0) / args.steps
-    dec_ev = ev0.elapsed_time(ev1) / 1e3 / args.steps
     log(f"[bench] decode {dec_wall * 1e3:.2f} ms/step wall, {dec_ev * 1e3:.2f} ms/step events")
-
-    # ---- size-independent checks: bit-exact round trip, lane postconditions
-    bads = decode_all(res, check=True)
-    roundtrip = all(torch.equal(d.view(torch.uint8), t.view(torch.uint8)) for d, (_, t) in zip(dsts, shard))
-    ok = roundtrip and all(b == 0 for b in bads)
-    C = sum(r.total for r in res)
-    S = sum(r.sidecar.numel() if r.sidecar is not None else 0 for r in res)
-    n_units = sum(e.n_units for e in encs)
-    H = n_units * 256 * 16 + (n_units + len(encs)) * 8 + len(encs) * 2308
-    log(f"[bench] roundtrip={ok} C={C / 1e9:.3f} GB S={S / 1e9:.3f} GB units={n_units}")
+    log(f"[bench] roundtrip={ok} C={C / 1e9:.3f} GB S={S / 1e9:.3f} GB units={m['units']}")
 
     # ---- per-kernel profile of one encode + one decode
     kernels, roof = {}, None
@@ -526,7 +721,6 @@ def main():
         decode_all(r2)
         prof = ck.profile_end()
         kernels = {k: dict(launches=c, total_ms=round(ms, 4), avg_ms=round(ms / c, 5)) for k, (c, ms) in prof.items()}
-        # algorithmic bytes per kernel over the whole shard (one encode / one decode)
         # algorithmic bytes of each kernel over the whole shard (one encode, one
         # decode): what it must read and write at least once
         alg = {
@@ -563,6 +757,7 @@ def main():
         for k in alg:
             if k in prof:
                 kernels[k]["achieved_GBps"] = round(alg[k] / (prof[k][1] / 1e3) / 1e9, 2)
+        del r2
 
     # the encode reads the tensors twice (histogram, then the coder); its whole
     # HBM traffic and the decode's against a plain copy's rate
@@ -574,13 +769,23 @@ def main():
     copy.update(encode_frac=round(copy["encode_GBps"] / copy["GBps"], 4),
                 decode_frac=round(copy["decode_GBps"] / copy["GBps"], 4))
     log(f"[bench] copy ceiling {copy['GBps']} GB/s; encode {copy['encode_frac']}, decode {copy['decode_frac']} of it")
+    del st, encs, encode_all, decode_all
+    torch.cuda.empty_cache()
 
-    analyze = None if args.no_analyze else analyzer_leg(shard, ck, torch, args.steps)
-    repair = None if args.no_repair else repair_leg(ck, torch, dev)
+    analyze = None
+    if not args.no_analyze:
+        analyze = analyzer_leg(shard, ck, torch, args.steps)
+        if not args.no_cpu:
+            analyze["cpu_baseline"] = analyze_cpu_baseline(shard, ck)
+            log(f"[bench] analyze cpu {analyze['cpu_baseline']['value']} GB/s")
+    repair = None if args.no_repair else repair_leg(ck, torch, dev, cpu=not args.no_cpu)
+
+    reflayout = None
+    if not args.no_reference_layout and args.config == 3:
+        reflayout = reference_layout_leg(shard, ck, torch, dev)
 
     save = None
     if not args.no_save:
-        res = r2 = None
         save = save_leg(shard, torch, unit)
         save["GBps"] = round(n_in / save["best_s"] / 1e9, 3)
 
@@ -590,9 +795,31 @@ def main():
         cpu = cpu_baseline(shard, ck, args.cpu_sample_mib << 20, unit)
         log(f"[bench] cpu {cpu}")
 
-    workload = {1: "cfg1 fp32 4096x4096 N(0,1e-3)", 2: "cfg2 llama3-8b decoder layer bf16",
-                3: "cfg3 llama3-8b zero3 rank0-of-8 shard (bf16 params, fp32 master, exp_avg, exp_avg_sq)",
-                4: "cfg4 adversarial fp32 256M", 5: "cfg5 llama3-70b zero3 rank0-of-8 shard"}[args.config]
+    # the other configurations, each measured the same way (the headline's
+    # shard is freed first; cfg5 streams 123.5 GB held in HBM)
+    others = None
+    if not args.no_configs and args.config == 3:
+        del shard
+        torch.cuda.empty_cache()
+        others = {}
+        for c in (1, 2, 4):
+            others[f"cfg{c}"] = config_leg(c, ck, torch, dev, unit, args.steps, args.warmup)
+        if not args.no_cfg5:
+            sh5 = make_shard(5, torch, dev)
+            n5 = sum(t.numel() * t.element_size() for _, t in sh5)
+            sha5 = None if args.no_sha else sha256_tensors(sh5)
+            o5 = run_streamed(argparse.Namespace(warmup=1, steps=1, slice_gib=args.slice_gib), sh5, ck, torch, dev,
+                              1 << 20, n5)
+            del sh5
+            torch.cuda.empty_cache()
+            keep = ("encode_ms", "decode_ms", "encode_GBps", "decode_GBps", "encode_roofline_frac",
+                    "decode_roofline_frac", "compressed_bytes", "sidecar_bytes", "header_bytes", "ans_ratio",
+                    "disk_ratio", "device_ratio", "roundtrip_bit_exact", "copy_ceiling")
+            others["cfg5"] = {k: o5[k] for k in keep}
+            others["cfg5"].update(workload=o5["config"]["workload"], unit_bytes=1 << 20, input_bytes=n5,
+                                  steps=o5["steps"], input_sha256=sha5)
+        ok = ok and all(v["roundtrip_bit_exact"] for v in others.values())
+
     out = {
         "metric": METRIC,
         "value": round(n_in / enc_wall / 1e9, 3),
@@ -606,28 +833,29 @@ def main():
         "vs_baseline": None,
         "dtype": "u8",
         "data": "synthetic: torch Philox on the GPU, seed 0, distributions of BASELINE.json configs",
-        "config": {"workload": workload, "elements_per_tensor": [t.numel() for _, t in shard],
-                   "tensors": [n for n, _ in shard], "unit_bytes": unit, "input_bytes": n_in,
-                   "table_bits": 12, "lanes": 256},
-        "encode_GBps": round(n_in / enc_wall / 1e9, 3),
-        "decode_GBps": round(n_in / dec_wall / 1e9, 3),
+        "config": {"workload": WORKLOADS[args.config], "elements_per_tensor": elems, "tensors": names,
+                   "unit_bytes": unit, "input_bytes": n_in, "table_bits": 12, "lanes": 256, "input_sha256": sha},
+        "encode_GBps": m["encode_GBps"],
+        "decode_GBps": m["decode_GBps"],
         "encode_ms": round(enc_wall * 1e3, 3),
         "decode_ms": round(dec_wall * 1e3, 3),
         "encode_ms_events": round(enc_ev * 1e3, 3),
         "decode_ms_events": round(dec_ev * 1e3, 3),
-        "encode_roofline_frac": round((n_in + S + C + H) / enc_wall / 1e9 / HBM_PEAK_GBPS, 4),
-        "decode_roofline_frac": round((n_in + S + C + H) / dec_wall / 1e9 / HBM_PEAK_GBPS, 4),
+        "encode_roofline_frac": m["encode_roofline_frac"],
+        "decode_roofline_frac": m["decode_roofline_frac"],
         "compressed_bytes": C,
         "sidecar_bytes": S,
         "header_bytes": H,
-        "ans_ratio": round(n_in / C, 4),
-        "disk_ratio": round(n_in / (C + S), 4),
-        "device_ratio": round(n_in / (C + S + H), 4),
+        "ans_ratio": m["ans_ratio"],
+        "disk_ratio": m["disk_ratio"],
+        "device_ratio": m["device_ratio"],
         "container_ratio": round(n_in / save["file_bytes"], 4) if save else None,
         "roundtrip_bit_exact": ok,
         "compress_and_save": save,
         "analyze": analyze,
         "repair": repair,
+        "reference_layout": reflayout,
+        "configs": others,
         "roofline": roof,
         "copy_ceiling": copy,
         "cpu_baseline": cpu,
@@ -677,9 +905,7 @@ def run_streamed(args, shard, ck, torch, dev, unit, n_in):
         "device_ratio": round(n_in / (C + S + H), 4), "container_ratio": None, "roundtrip_bit_exact": ok,
         "roofline": None, "copy_ceiling": copy, "cpu_baseline": None, "kernels": {},
     }
-    print(json.dumps(out), flush=True)
-    if not ok:
-        sys.exit(1)
+    return out
 
 
 if __name__ == "__main__":

@@ -34,7 +34,9 @@ EXPORTED = [  # every symbol include/checkers_amd.h declares
     "ckr_analyze", "ckr_profile_begin", "ckr_profile_end", "ckr_set_fast_paths",
     "ckr_repair_masked_bits", "ckr_repair_bucket_count", "ckr_repair_workspace_bytes",
     "ckr_repair_build", "ckr_repair_apply",
-    "ckr_fingerprint_weights", "ckr_cluster", "ckr_ckpt_write", "ckr_ckpt_open", "ckr_ckpt_count",
+    "ckr_fingerprint_weights", "ckr_cluster", "ckr_ckpt_write", "ckr_ckpt_set_slice_bytes",
+    "ckr_ckpt_slice_bytes", "ckr_ckpt_reserve", "ckr_ckpt_pool_bytes", "ckr_ckpt_release",
+    "ckr_ckpt_open", "ckr_ckpt_count",
     "ckr_ckpt_info", "ckr_ckpt_restore", "ckr_ckpt_close",
     "ckr_arena_create", "ckr_arena_alloc", "ckr_arena_used", "ckr_arena_reset", "ckr_arena_destroy",
     "ckr_stats_slab_bytes", "ckr_carve_stats_slab", "ckr_analyze_device_records",
@@ -148,6 +150,11 @@ def lib():
         "ckr_fingerprint_weights": (i32, [vp, u64, vp]),
         "ckr_cluster": (i32, [vp, vp, u64, vp, vp]),
         "ckr_ckpt_write": (i32, [ctypes.c_char_p, i32, vp, u64, u64, i32, vp, vp]),
+        "ckr_ckpt_set_slice_bytes": (i32, [u64]),
+        "ckr_ckpt_slice_bytes": (u64, []),
+        "ckr_ckpt_reserve": (i32, [vp, u64, u64]),
+        "ckr_ckpt_pool_bytes": (u64, []),
+        "ckr_ckpt_release": (None, []),
         "ckr_ckpt_open": (i32, [ctypes.c_char_p, i32, vp]),
         "ckr_ckpt_count": (u64, [vp]),
         "ckr_ckpt_info": (i32, [vp, u64, vp]),
@@ -628,7 +635,10 @@ class CkptStats(ctypes.Structure):
     _fields_ = [("record_index", ctypes.c_uint64), ("original_bytes", ctypes.c_uint64),
                 ("ans_bytes", ctypes.c_uint64), ("sidecar_bytes", ctypes.c_uint64),
                 ("owns_table", ctypes.c_uint32), ("table_sum", ctypes.c_uint32),
-                ("table_repaired", ctypes.c_uint32), ("pad", ctypes.c_uint32)]
+                ("table_repaired", ctypes.c_uint32), ("n_slices", ctypes.c_uint32),
+                ("stored_bytes", ctypes.c_uint64), ("record_bytes", ctypes.c_uint64),
+                ("hist_ms", ctypes.c_double), ("table_ms", ctypes.c_double),
+                ("encode_ms", ctypes.c_double), ("copy_ms", ctypes.c_double)]
 
 
 class CkptEntry(ctypes.Structure):
@@ -639,9 +649,7 @@ class CkptEntry(ctypes.Structure):
                 ("unit_bytes", ctypes.c_uint64), ("sidecar_bytes", ctypes.c_uint64)]
 
 
-def write_checkpoint(output_dir, rank, tensors, unit_bytes=0, repair_tables=False, stream=None):
-    """compress_and_save_all: tensors is a list of (name, device tensor or None,
-    dtype tag, cluster id); returns one stats dict per written tensor."""
+def _ckpt_tensors(tensors):
     n = len(tensors)
     names = [t[0].encode() for t in tensors]
     arr = (CkptTensor * max(n, 1))()
@@ -652,11 +660,42 @@ def write_checkpoint(output_dir, rank, tensors, unit_bytes=0, repair_tables=Fals
         arr[i].num_elements = ne
         arr[i].dtype = tag
         arr[i].cluster_id = cid
+    return arr, names
+
+
+def set_ckpt_slice_bytes(nbytes):
+    """Slice size of the checkpoint writer (0: CKR_CKPT_SLICE_BYTES or 4 GiB)."""
+    _check(lib().ckr_ckpt_set_slice_bytes(nbytes))
+
+
+def ckpt_slice_bytes():
+    return int(lib().ckr_ckpt_slice_bytes())
+
+
+def reserve_checkpoint(tensors, unit_bytes=0):
+    """Allocate the writer's buffers for these tensors ahead of write_checkpoint."""
+    arr, _names = _ckpt_tensors(tensors)
+    _check(lib().ckr_ckpt_reserve(arr, len(tensors), unit_bytes))
+
+
+def ckpt_pool_bytes():
+    return int(lib().ckr_ckpt_pool_bytes())
+
+
+def release_checkpoint_buffers():
+    lib().ckr_ckpt_release()
+
+
+def write_checkpoint(output_dir, rank, tensors, unit_bytes=0, repair_tables=False, stream=None):
+    """compress_and_save_all: tensors is a list of (name, device tensor or None,
+    dtype tag, cluster id); returns one stats dict per written tensor."""
+    n = len(tensors)
+    arr, _names = _ckpt_tensors(tensors)
     st = (CkptStats * max(n, 1))()
     _check(lib().ckr_ckpt_write(os.fsencode(output_dir), rank, arr, n, unit_bytes, int(bool(repair_tables)), st,
                                 _stream(stream)))
     written = sum(1 for i in range(n) if arr[i].d_ptr and arr[i].num_elements)
-    return [{f[0]: getattr(st[i], f[0]) for f in CkptStats._fields_ if f[0] != "pad"} for i in range(written)]
+    return [{f[0]: getattr(st[i], f[0]) for f in CkptStats._fields_} for i in range(written)]
 
 
 class Checkpoint:

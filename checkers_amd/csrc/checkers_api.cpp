@@ -28,10 +28,13 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdint>
 #include <cstdlib>
+#include <fstream>
 #include <iostream>
 #include <memory>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -97,9 +100,13 @@ struct Context {
     size_t skipped = 0;
     std::vector<Record> recs;
     ckr_arena* arena = nullptr;
+    void* analyze_ws = nullptr;  // the statistics pass's workspace, kept for the context's life
+    uint64_t analyze_wsb = 0;
     std::vector<int32_t> cluster_of;  // after analyze_tensors
     ~Context() {
+        if (analyze_ws) (void)HIPFN(hipFree, void*)(analyze_ws);
         if (arena) CKR(ckr_arena_destroy)(arena);
+        CKR(ckr_ckpt_release)();  // the checkpoint writer's buffers, reserved for this context
     }
 };
 
@@ -135,6 +142,15 @@ void* current_stream() {
         PyErr_Clear();
         return nullptr;
     }
+}
+
+// CHECKERS_UNIT_BYTES: unit size of the chunked states file (.ansc v4,
+// default 65536); 0 writes the reference's v2 layout (one stream per tensor,
+// tensors below 4 GiB, encoded 256 lanes wide only).
+uint64_t unit_bytes_setting() {
+    uint64_t unit = 65536;
+    if (const char* v = std::getenv("CHECKERS_UNIT_BYTES")) unit = std::strtoull(v, nullptr, 10);
+    return unit;
 }
 
 // parse_dtype (api.cpp:887-893): substring tests in this order.
@@ -398,6 +414,50 @@ void place_records(Context& c, void* stream) {
     }
 }
 
+// CHECKERS_LOG: where compress_and_save reports what the reference's logger
+// records per tensor and in total (src/ANSCompressor.cpp:1292-1312,
+// :1387-1399, same fields and prefix): unset or empty, nowhere; "stderr" or
+// "1", standard error; anything else, a file the lines are appended to.
+void log_compress_stats(const Context& c, const std::vector<ckr_ckpt_tensor>& ts,
+                        const std::vector<ckr_ckpt_stats>& stats, double wall_ms, const std::string& dir,
+                        uint64_t unit) {
+    const char* where = std::getenv("CHECKERS_LOG");
+    if (!where || !*where) return;
+    std::ostringstream o;
+    const std::string lp = "[ANS][rank=" + std::to_string(c.rank) + "]";
+    size_t written = 0;
+    double compute_ms = 0;
+    for (const ckr_ckpt_tensor& t : ts) written += (t.d_ptr && t.num_elements) ? 1 : 0;
+    for (size_t k = 0; k < written; k++) {
+        const ckr_ckpt_stats& s = stats[k];
+        const double ans_ratio = s.ans_bytes ? (double)s.original_bytes / (double)s.ans_bytes : 1.0;
+        const double disk_ratio =
+            s.original_bytes ? (double)s.original_bytes / (double)(s.ans_bytes + s.sidecar_bytes) : 1.0;
+        compute_ms += s.hist_ms + s.table_ms + s.encode_ms + s.copy_ms;
+        o << lp << "[tensor] name=" << ts[s.record_index].name << " original_bytes=" << s.original_bytes
+          << " ans_bytes=" << s.ans_bytes << " sidecar_bytes=" << s.sidecar_bytes
+          << " ans_ratio=" << std::to_string(ans_ratio) << " disk_ratio=" << std::to_string(disk_ratio)
+          << " owns_table=" << s.owns_table << " hist_ms=" << std::to_string(s.hist_ms)
+          << " table_ms=" << std::to_string(s.table_ms) << " encode_ms=" << std::to_string(s.encode_ms)
+          << " copy_ms=" << std::to_string(s.copy_ms) << " stored_bytes=" << s.stored_bytes
+          << " unit_records=" << s.record_bytes << " slices=" << s.n_slices << "\n";
+    }
+    const std::string tag = "rank_" + std::to_string(std::max(c.rank, 0));
+    o << lp << "[summary] tensors=" << written << " total_wall_ms=" << std::to_string(wall_ms)
+      << " total_compute_ms=" << std::to_string(compute_ms) << " states=" << dir << "/" << tag << "_states.ansc"
+      << " mantissa=" << dir << "/mantissa/" << tag << "_mantissa.mant tables=" << dir << "/tables/" << tag
+      << "_tables.dict version=" << (unit ? 4 : 2) << "\n";
+    o << "[TIMING] compress_and_save_total_ms=" << std::to_string(wall_ms) << "\n";
+    o << "[TIMING] compress_computation_ms=" << std::to_string(compute_ms) << "\n";
+    const std::string w(where);
+    if (w == "stderr" || w == "1") {
+        std::cerr << o.str() << std::flush;
+    } else {
+        std::ofstream f(w, std::ios::app);
+        f << o.str();
+    }
+}
+
 }  // namespace
 
 void initialize_context(py::object model_engine, py::object optimizer, size_t histogram_bins,
@@ -425,6 +485,22 @@ void initialize_context(py::object model_engine, py::object optimizer, size_t hi
         register_release_at_exit();
         release_context();  // the previous context's arena goes first
         place_records(*c, current_stream());
+        // what analyze_tensors and compress_and_save will need, allocated now so
+        // that neither allocates device memory (the reference plans its buffers
+        // here too: compute_buffer_plan, MemoryManager.cpp:692-707)
+        std::vector<ckr_device_tensor_record> recs;
+        std::vector<ckr_ckpt_tensor> ts;
+        for (const auto& r : c->recs) {
+            recs.push_back(r.rec);
+            if (r.rec.data_type == CKR_UNKNOWN) continue;
+            ts.push_back(ckr_ckpt_tensor{r.name.c_str(), r.rec.d_ptr, r.rec.num_elements, r.rec.data_type, 0});
+        }
+        c->analyze_wsb = CKR(ckr_analyze_device_records_workspace_bytes)(recs.data(), recs.size());
+        if (c->analyze_wsb && HIPFN(hipMalloc, void**, size_t)(&c->analyze_ws, c->analyze_wsb) != hipSuccess) {
+            c->analyze_ws = nullptr;
+            throw std::runtime_error("analyze workspace allocation failed");
+        }
+        check(CKR(ckr_ckpt_reserve)(ts.data(), ts.size(), unit_bytes_setting()), "checkpoint buffers");
         g_ctx = c.release();
     } catch (const std::exception& e) {
         throw std::runtime_error("[checkers] Context initialization failed: " + std::string(e.what()));
@@ -439,16 +515,12 @@ void analyze_tensors() {
         std::vector<ckr_device_tensor_record> recs;
         for (const auto& r : c.recs) recs.push_back(r.rec);
         void* stream = current_stream();
-        const uint64_t wsb = CKR(ckr_analyze_device_records_workspace_bytes)(recs.data(), recs.size());
-        void* ws = nullptr;
-        if (wsb && HIPFN(hipMalloc, void**, size_t)(&ws, wsb) != hipSuccess) throw std::runtime_error("analyze workspace allocation failed");
-        const int rc = CKR(ckr_analyze_device_records)(recs.data(), recs.size(), ws, wsb, stream);
+        const int rc = CKR(ckr_analyze_device_records)(recs.data(), recs.size(), c.analyze_ws, c.analyze_wsb, stream);
         std::vector<float> fp(recs.size() * 5, 0.f);
         hipError_t e = hipSuccess;
         for (size_t i = 0; i < recs.size() && rc == CKR_OK && e == hipSuccess; i++)
             e = HIPFN(hipMemcpyAsync, void*, const void*, size_t, hipMemcpyKind, hipStream_t)(&fp[i * 5], recs[i].d_fingerprint, 20, hipMemcpyDeviceToHost, (hipStream_t)stream);
         if (e == hipSuccess) e = HIPFN(hipStreamSynchronize, hipStream_t)((hipStream_t)stream);
-        if (ws) (void)HIPFN(hipFree, void*)(ws);
         check(rc, "analyze");
         if (e != hipSuccess) throw std::runtime_error(std::string("fingerprint copy failed: ") + hip_error(e));
         // compute_fingerprint_weights (TensorAnalyzer.cpp:322-380); the reference
@@ -470,11 +542,7 @@ void compress_and_save(const std::string& output_path) {
     try {
         if (!g_ctx) throw std::runtime_error("Context not initialized: call initialize_context first.");
         Context& c = *g_ctx;
-        // CHECKERS_UNIT_BYTES: unit size of the chunked states file (.ansc v4,
-        // default 65536); 0 writes the reference's v2 layout (one stream per
-        // tensor, tensors below 4 GiB, encoded 256 lanes wide only)
-        uint64_t unit = 65536;
-        if (const char* v = std::getenv("CHECKERS_UNIT_BYTES")) unit = std::strtoull(v, nullptr, 10);
+        const uint64_t unit = unit_bytes_setting();
         // CHECKERS_REPAIR_TABLES (default 1): a cluster table that the
         // reference's one-pass normalisation leaves above 4096 is repaired so that
         // its members can be decoded; 0 writes the reference's table unchanged
@@ -492,9 +560,13 @@ void compress_and_save(const std::string& output_path) {
             t.cluster_id = c.cluster_of.empty() ? -1 : c.cluster_of[i];
             ts.push_back(t);
         }
-        check(CKR(ckr_ckpt_write)(output_path.c_str(), std::max(c.rank, 0), ts.data(), ts.size(), unit, repair, nullptr,
-                             current_stream()),
+        std::vector<ckr_ckpt_stats> stats(std::max<size_t>(ts.size(), 1));
+        const auto t0 = std::chrono::steady_clock::now();
+        check(CKR(ckr_ckpt_write)(output_path.c_str(), std::max(c.rank, 0), ts.data(), ts.size(), unit, repair,
+                                  stats.data(), current_stream()),
               "compress_and_save");
+        const double wall_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        log_compress_stats(c, ts, stats, wall_ms, output_path, unit);
     } catch (const std::exception& e) {
         std::cerr << "[CHECKERS CRITICAL ERROR] compress_and_save: " << e.what() << std::endl;
         throw;

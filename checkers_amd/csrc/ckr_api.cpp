@@ -887,6 +887,33 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
     return CKR_OK;
 }
 
+// Output buffers of the jobs of one batched call ([lo, hi) device ranges):
+// jobs run concurrently on several streams, so no two outputs may overlap,
+// within a job or across jobs (inputs may be shared).
+struct Span {
+    uintptr_t lo, hi;
+    uint64_t job;
+    const char* what;
+};
+int check_disjoint(std::vector<Span>& v) {
+    std::sort(v.begin(), v.end(), [](const Span& a, const Span& b) { return a.lo < b.lo; });
+    uintptr_t hi = 0;
+    size_t at = 0;
+    for (size_t i = 0; i < v.size(); i++) {
+        if (i && v[i].lo < hi)
+            return fail(CKR_E_INVALID, "[ckr] job %llu's %s overlaps job %llu's %s", (unsigned long long)v[i].job,
+                        v[i].what, (unsigned long long)v[at].job, v[at].what);
+        if (v[i].hi > hi) {
+            hi = v[i].hi;
+            at = i;
+        }
+    }
+    return CKR_OK;
+}
+void add_span(std::vector<Span>& v, const void* p, uint64_t bytes, uint64_t job, const char* what) {
+    if (p && bytes) v.push_back({(uintptr_t)p, (uintptr_t)p + bytes, job, what});
+}
+
 // The caller buffers of an encode, checked before anything is queued: the
 // source element-aligned and inside its allocation, the outputs and the
 // workspace inside theirs at the sizes the header documents.
@@ -953,10 +980,14 @@ int ckr_encode(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_ta
     return rc;
 }
 
-int ckr_encode_planes(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table,
-                      const uint32_t* h_planes, uint64_t unit_bytes, uint8_t* d_out, uint64_t out_capacity,
-                      ckr_stream_header* d_headers, uint64_t* d_unit_offsets, uint8_t* d_sidecar, void* d_workspace,
-                      uint64_t workspace_bytes, uint64_t* h_total_out, void* stream) {
+}  // extern "C"
+
+namespace {
+int encode_planes_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table,
+                       const uint32_t* h_planes, bool planes_cover_data, uint64_t unit_bytes, uint8_t* d_out,
+                       uint64_t out_capacity, ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
+                       uint8_t* d_sidecar, void* d_workspace, uint64_t workspace_bytes, uint64_t* h_total_out,
+                       void* stream) {
     if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
     ckr::EncodeGeom g;
     if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
@@ -969,9 +1000,29 @@ int ckr_encode_planes(const void* d_src, uint64_t n_elems, int dtype, const ckr_
     if ((rc = st.make(d_src, g.n_bytes, s))) return rc;
     rc = encode_impl(st.p, n_elems, dtype, h_table, unit_bytes, d_out, out_capacity, d_headers, d_unit_offsets,
                      d_sidecar, d_workspace, workspace_bytes, h_total_out, g.spe ? h_planes : nullptr, stream,
-                     nullptr, nullptr, true);
+                     nullptr, nullptr, !planes_cover_data);
     st.release(s);
     return rc;
+}
+}  // namespace
+
+int ckr::encode_slice_of_counted(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table,
+                                 const uint32_t* h_planes, uint64_t unit_bytes, uint8_t* d_out, uint64_t out_capacity,
+                                 ckr_stream_header* d_headers, uint64_t* d_unit_offsets, uint8_t* d_sidecar,
+                                 void* d_workspace, uint64_t workspace_bytes, uint64_t* h_total_out, void* stream) {
+    return encode_planes_impl(d_src, n_elems, dtype, h_table, h_planes, h_planes != nullptr, unit_bytes, d_out,
+                              out_capacity, d_headers, d_unit_offsets, d_sidecar, d_workspace, workspace_bytes,
+                              h_total_out, stream);
+}
+
+extern "C" {
+
+int ckr_encode_planes(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table,
+                      const uint32_t* h_planes, uint64_t unit_bytes, uint8_t* d_out, uint64_t out_capacity,
+                      ckr_stream_header* d_headers, uint64_t* d_unit_offsets, uint8_t* d_sidecar, void* d_workspace,
+                      uint64_t workspace_bytes, uint64_t* h_total_out, void* stream) {
+    return encode_planes_impl(d_src, n_elems, dtype, h_table, h_planes, false, unit_bytes, d_out, out_capacity,
+                              d_headers, d_unit_offsets, d_sidecar, d_workspace, workspace_bytes, h_total_out, stream);
 }
 
 int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_bytes, int ensure_full_alphabet,
@@ -1082,10 +1133,20 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         const int rc = check_encode_args(jb.d_src, geo[i], jb.n_elems, jb.d_out, jb.out_capacity, jb.d_headers,
                                          jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace, jb.workspace_bytes);
         if (rc) return set_job_error(rc, i);
-        for (uint64_t k = 0; k < i; k++)  // jobs share no output or workspace
-            if (jobs[k].d_workspace == jb.d_workspace || (jb.n_elems && jobs[k].d_out == jb.d_out))
-                return fail(CKR_E_INVALID, "[ckr] jobs %llu and %llu share an output or workspace buffer",
-                            (unsigned long long)k, (unsigned long long)i);
+    }
+    {  // jobs share no output or workspace bytes
+        std::vector<Span> v;
+        for (uint64_t i = 0; i < n; i++) {
+            const ckr_compress_job& jb = jobs[i];
+            const ckr::EncodeGeom& g = geo[i];
+            add_span(v, jb.d_workspace, encode_layout(g).total, i, "workspace");
+            add_span(v, jb.d_unit_offsets, (g.n_units + 1) * 8, i, "unit offsets");
+            if (!g.n_units) continue;
+            add_span(v, jb.d_out, g.n_bytes, i, "output");
+            add_span(v, jb.d_headers, g.n_units * 256 * sizeof(ckr_stream_header), i, "headers");
+            if (g.spe) add_span(v, jb.d_sidecar, jb.n_elems * (uint64_t)g.spe, i, "sidecar");
+        }
+        if (int rc = check_disjoint(v)) return rc;
     }
     if (n == 1) {  // one job: ckr_compress on the caller's stream, no second stream or events
         ckr_compress_job& jb = jobs[0];
@@ -1111,6 +1172,21 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             for (auto& x : v) x.release(s);
         }
     } release_staged{staged, s, a->s2};
+    // An error after the first launch leaves work queued on the library's
+    // streams (encodes, histograms, read-backs into its pinned slots): every
+    // stream is drained before the call returns, and before the staged copies
+    // above are freed.
+    struct Drain {
+        ManyAux* a;
+        hipStream_t s;
+        bool ok = false;
+        ~Drain() {
+            if (ok) return;
+            (void)hipStreamSynchronize(s);
+            (void)hipStreamSynchronize(a->s2);
+            for (hipStream_t x : a->sx) (void)hipStreamSynchronize(x);
+        }
+    } drain{a, s};
     for (uint64_t i = 0; i < n; i++) {
         const int rc = staged[i].make(jobs[i].d_src, geo[i].n_bytes, s);
         if (rc) return rc;
@@ -1205,6 +1281,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
                 return rc;
             }
         }
+        drain.ok = true;  // complete() waits for every stream it queued on
         return complete(n);
     }
     // Larger tensors: job i's encode goes on es[i % 2] (the caller's stream and
@@ -1257,6 +1334,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         CKR_HIP(hipEventRecord(a->ev_prev, es[i & 1]));  // job i queued: job i+2's histogram waits for it
         if (i + 1 < n) CKR_HIP(hipStreamSynchronize(a->s2));
     }
+    drain.ok = true;  // complete() waits for every stream it queued on
     return complete(n);
 }
 
@@ -1393,11 +1471,18 @@ int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int c
         ckr::EncodeGeom g;
         if (!dtype_ok(jobs[i].dtype) || !make_geom(jobs[i].n_elems, jobs[i].dtype, unit_bytes, &g))
             return fail(CKR_E_INVALID, "[ckr] job %llu: bad dtype or size", (unsigned long long)i);
-        for (uint64_t k = 0; k < i; k++)  // jobs share no destination or workspace
-            if (jobs[k].d_workspace == jobs[i].d_workspace || (jobs[i].n_elems && jobs[k].d_dst == jobs[i].d_dst))
-                return fail(CKR_E_INVALID, "[ckr] jobs %llu and %llu share a destination or workspace buffer",
-                            (unsigned long long)k, (unsigned long long)i);
         jobs[i].bad_lanes = 0;
+    }
+    {  // jobs share no destination or workspace bytes
+        std::vector<Span> v;
+        for (uint64_t i = 0; i < n; i++) {
+            ckr::EncodeGeom g;
+            make_geom(jobs[i].n_elems, jobs[i].dtype, unit_bytes, &g);
+            if (!g.n_units) continue;
+            add_span(v, jobs[i].d_workspace, decode_layout(g).total, i, "workspace");
+            add_span(v, jobs[i].d_dst, g.n_bytes, i, "destination");
+        }
+        if (int rc = check_disjoint(v)) return rc;
     }
     hipStream_t s = (hipStream_t)stream;
     ManyAux* a = nullptr;
@@ -1478,6 +1563,20 @@ int ckr_decode_noalloc(const uint8_t* d_data, const ckr_stream_header* d_headers
     if (need > kNoAllocScratchBytes)
         return fail(CKR_E_CAPACITY, "[ckr] decode needs %llu bytes of scratch, above the no-allocation limit of %llu",
                     (unsigned long long)need, (unsigned long long)kNoAllocScratchBytes);
+    if (g.n_units && d_dst && !aligned_to(d_dst, 4))
+        return fail(CKR_E_INVALID, "[ckr] the no-allocation decode needs a 4-byte aligned destination");
+    // the bad-lane count is read back with a synchronisation, which a stream
+    // being captured into a graph cannot take: under capture it must be NULL
+    if (h_bad_lanes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(CKR_E_HIP, "[ckr] cannot query the stream's capture status");
+        }
+        if (cs != hipStreamCaptureStatusNone)
+            return fail(CKR_E_INVALID, "[ckr] h_bad_lanes must be NULL while the stream is captured (reading the "
+                                       "count back needs a synchronisation)");
+    }
     void* ws = nullptr;
     if (int rc = noalloc_scratch(&ws)) return rc;
     ckr::t_noalloc = true;

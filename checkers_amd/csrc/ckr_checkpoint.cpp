@@ -15,6 +15,8 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <cerrno>
 #include <cmath>
 #include <condition_variable>
@@ -112,12 +114,6 @@ uint32_t env_count(const char* name, uint32_t dflt, uint32_t lo, uint32_t hi) {
     return (uint32_t)std::min<long>(std::max<long>(x, lo), hi);
 }
 
-struct PinnedRing {
-    std::mutex use;  // held by one ckr_ckpt_write for its whole duration
-    uint8_t* base = nullptr;
-    uint32_t slots = 0;
-};
-PinnedRing g_ring;
 
 struct Range {
     int fd;
@@ -355,6 +351,162 @@ void repair_table(ckr_freq_table* t) {
     t->cum_freq[256] = c;
 }
 
+
+// ---- the writer's buffers, kept across calls: a workspace, the histogram
+// words and two sets of encode outputs that alternate between slices, plus
+// the pinned host ring.  Tensors are encoded in slices of whole units under
+// their whole-tensor table (units are independent streams given the table), so
+// the sizes depend on the slice size and not on the largest tensor.
+// ckr_ckpt_reserve sizes them ahead of a write (so that the first write
+// allocates nothing), a write grows what is too small, ckr_ckpt_release frees
+// everything.
+struct DevBuf {
+    void* p = nullptr;
+    uint64_t size = 0;
+};
+struct WriterSet {
+    DevBuf out, hdr, off, side, stored, rec, plan;
+    std::vector<uint64_t> rec_off, out_off;  // host copies kept until the set is reused
+};
+struct WriterNeeds {
+    uint64_t ws = 0, out = 0, hdr = 0, off = 0, side = 0, rec = 0, plan = 0;
+};
+struct WriterPool {
+    std::mutex use;  // held by one writer, reserve or release for its whole duration
+    int device = -1;
+    DevBuf ws, hist;
+    WriterSet sets[2];
+    uint8_t* ring = nullptr;
+    uint32_t slots = 0;
+    uint64_t device_bytes() const {
+        uint64_t b = ws.size + hist.size;
+        for (const WriterSet& z : sets)
+            for (const DevBuf* d : {&z.out, &z.hdr, &z.off, &z.side, &z.stored, &z.rec, &z.plan}) b += d->size;
+        return b;
+    }
+};
+WriterPool g_pool;
+
+constexpr uint64_t kDefaultSliceBytes = 4ull << 30;
+std::atomic<uint64_t> g_slice_bytes{0};  // 0: CKR_CKPT_SLICE_BYTES, else kDefaultSliceBytes
+
+uint64_t slice_bytes_setting() {
+    if (const uint64_t v = g_slice_bytes.load()) return v;
+    if (const char* e = std::getenv("CKR_CKPT_SLICE_BYTES")) {
+        const unsigned long long v = std::strtoull(e, nullptr, 10);
+        if (v >= 256) return v;
+    }
+    return kDefaultSliceBytes;
+}
+
+// How a tensor is cut: slices of slice_units whole units (the last may hold
+// fewer, and the tensor's ragged last unit); one slice when the tensor is one
+// unit (v2, or a unit at least the tensor's size).
+struct SliceGeom {
+    uint64_t n_bytes = 0, unit = 0, nu = 0, slice_units = 0, slice_elems = 0, n_slices = 0;
+    int es = 0, spe = 0;
+};
+SliceGeom slice_geom(uint64_t n_elems, int dtype, uint64_t unit_bytes, uint64_t slice_bytes) {
+    SliceGeom g;
+    g.es = ckr_element_size(dtype);
+    g.spe = ckr_sidecar_bytes_per_elem(dtype);
+    g.n_bytes = n_elems * (uint64_t)g.es;
+    g.nu = ckr_num_units(n_elems, dtype, unit_bytes);
+    if (!g.nu) return g;
+    if (!unit_bytes || unit_bytes >= g.n_bytes) {
+        g.unit = g.n_bytes;
+        g.slice_units = g.nu;
+        g.slice_elems = n_elems;
+        g.n_slices = 1;
+        return g;
+    }
+    g.unit = unit_bytes;
+    g.slice_units = std::min(g.nu, std::max<uint64_t>(1, slice_bytes / unit_bytes));
+    g.slice_elems = g.slice_units * unit_bytes / (uint64_t)g.es;
+    g.n_slices = (g.nu + g.slice_units - 1) / g.slice_units;
+    return g;
+}
+
+// Buffer sizes one tensor needs (the largest slice and the last one).
+void add_needs(WriterNeeds& w, uint64_t n_elems, int dtype, uint64_t unit_bytes, uint64_t slice_bytes, bool v4) {
+    const SliceGeom g = slice_geom(n_elems, dtype, unit_bytes, slice_bytes);
+    if (!g.nu) return;
+    const uint64_t last = n_elems - (g.n_slices - 1) * g.slice_elems;
+    for (const uint64_t ne : {std::min(n_elems, g.slice_elems), last}) {
+        const uint64_t nu = ckr_num_units(ne, dtype, unit_bytes);
+        w.ws = std::max(w.ws, ckr_encode_workspace_bytes(ne, dtype, unit_bytes));
+        w.out = std::max(w.out, ckr_encode_max_output_bytes(ne, dtype, unit_bytes));
+        w.hdr = std::max(w.hdr, nu * 256 * 16);
+        w.off = std::max(w.off, (nu + 1) * 8);
+        w.side = std::max(w.side, ne * (uint64_t)g.spe);
+        if (v4) {
+            w.rec = std::max(w.rec, nu * (uint64_t)ckr::kUnitRecordMax);
+            w.plan = std::max(w.plan, nu * 24);
+        }
+    }
+}
+
+void pool_free_all() {  // with g_pool.use held
+    if (g_pool.device >= 0) {
+        int cur = 0;
+        (void)hipGetDevice(&cur);
+        (void)hipSetDevice(g_pool.device);
+        (void)hipDeviceSynchronize();
+        for (DevBuf* d : {&g_pool.ws, &g_pool.hist})
+            if (d->p) (void)hipFree(d->p);
+        for (WriterSet& z : g_pool.sets)
+            for (DevBuf* d : {&z.out, &z.hdr, &z.off, &z.side, &z.stored, &z.rec, &z.plan})
+                if (d->p) (void)hipFree(d->p);
+        (void)hipSetDevice(cur);
+    }
+    g_pool.ws = g_pool.hist = DevBuf{};
+    for (WriterSet& z : g_pool.sets) z = WriterSet{};
+    g_pool.device = -1;
+}
+
+// Grows the pool's buffers to `w` on the current device (with g_pool.use held).
+int pool_ensure(const WriterNeeds& w, uint32_t slots) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return err(CKR_E_HIP, "[ckr] no current device");
+    if (g_pool.device != dev) {
+        pool_free_all();
+        g_pool.device = dev;
+    }
+    auto grow = [](DevBuf& d, uint64_t need) {
+        if (need == 0 || d.size >= need) return true;
+        if (d.p) (void)hipFree(d.p);
+        d = DevBuf{};
+        const uint64_t b = std::max<uint64_t>(need, 256);
+        if (hipMalloc(&d.p, b) != hipSuccess) {
+            (void)hipGetLastError();
+            d.p = nullptr;
+            return false;
+        }
+        d.size = b;
+        return true;
+    };
+    bool ok = grow(g_pool.ws, w.ws) && grow(g_pool.hist, 768 * 4);
+    for (WriterSet& z : g_pool.sets)
+        ok = ok && grow(z.out, w.out) && grow(z.hdr, w.hdr) && grow(z.off, w.off) && grow(z.side, w.side) &&
+             grow(z.stored, w.rec ? w.out : 0) && grow(z.rec, w.rec) && grow(z.plan, w.plan);
+    if (!ok) return err(CKR_E_HIP, "[ckr] device allocation for the checkpoint writer failed");
+    if (slots && g_pool.slots < slots) {
+        if (g_pool.ring) (void)hipHostFree(g_pool.ring);
+        g_pool.ring = nullptr;
+        g_pool.slots = 0;
+        if (hipHostMalloc(reinterpret_cast<void**>(&g_pool.ring), slots * kSlotBytes, hipHostMallocDefault) != hipSuccess) {
+            g_pool.ring = nullptr;
+            (void)hipGetLastError();
+            return err(CKR_E_HIP, "[ckr] pinned staging allocation failed");
+        }
+        g_pool.slots = slots;
+    }
+    return CKR_OK;
+}
+
+double ms_since(std::chrono::steady_clock::time_point t0) {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+}
 }  // namespace
 
 // ---------------------------------------------------------------- reader state
@@ -454,20 +606,60 @@ int ckr_cluster(const char* const* names, const float* h_fp, uint64_t n, int32_t
     return CKR_OK;
 }
 
+int ckr_ckpt_set_slice_bytes(uint64_t bytes) {
+    if (bytes && bytes < 256) return err(CKR_E_INVALID, "[ckr] slice size below 256 bytes");
+    g_slice_bytes.store(bytes);
+    return CKR_OK;
+}
+
+uint64_t ckr_ckpt_slice_bytes(void) { return slice_bytes_setting(); }
+
+int ckr_ckpt_reserve(const ckr_ckpt_tensor* tensors, uint64_t n, uint64_t unit_bytes) {
+    if (n && !tensors) return err(CKR_E_INVALID, "[ckr] null pointer");
+    if (unit_bytes % 256) return err(CKR_E_INVALID, "[ckr] unit_bytes must be a multiple of 256");
+    const uint64_t slice = slice_bytes_setting();
+    WriterNeeds w;
+    bool any = false;
+    for (uint64_t i = 0; i < n; i++) {
+        const auto& t = tensors[i];
+        if (!t.d_ptr || !t.num_elements || !ckr_element_size(t.dtype)) continue;
+        add_needs(w, t.num_elements, t.dtype, unit_bytes, slice, unit_bytes != 0);
+        any = true;
+    }
+    if (!any) return CKR_OK;
+    std::lock_guard<std::mutex> lk(g_pool.use);
+    return pool_ensure(w, env_count("CKR_CKPT_SLOTS", 16, 2, kMaxSlots));
+}
+
+uint64_t ckr_ckpt_pool_bytes(void) {
+    std::lock_guard<std::mutex> lk(g_pool.use);
+    return g_pool.device_bytes();
+}
+
+void ckr_ckpt_release(void) {
+    std::lock_guard<std::mutex> lk(g_pool.use);
+    pool_free_all();
+    if (g_pool.ring) (void)hipHostFree(g_pool.ring);
+    g_pool.ring = nullptr;
+    g_pool.slots = 0;
+}
+
 int ckr_ckpt_write(const char* output_dir, int rank, const ckr_ckpt_tensor* tensors, uint64_t n, uint64_t unit_bytes,
                    int repair_tables, ckr_ckpt_stats* h_stats, void* stream) {
     if (!output_dir || (n && !tensors)) return err(CKR_E_INVALID, "[ckr] null pointer");
     if (unit_bytes % 256) return err(CKR_E_INVALID, "[ckr] unit_bytes must be a multiple of 256");
     hipStream_t s = (hipStream_t)stream;
     const bool v4 = unit_bytes != 0;
+    const uint64_t slice_bytes = slice_bytes_setting();
     // the tensors written, in record order, and the layout of the three files
     struct Item {
-        uint64_t i, nu, n_bytes;
-        int es, spe;
+        uint64_t i;
+        SliceGeom g;
         uint64_t side_off;
     };
     std::vector<Item> items;
-    uint64_t cap_ws = 0, cap_out = 0, cap_hdr = 0, side_total = 0, cap_side = 0, n_side = 0, nu_max = 0;
+    WriterNeeds needs;
+    uint64_t side_total = 0, n_side = 0;
     for (uint64_t i = 0; i < n; i++) {
         const auto& t = tensors[i];
         if (!t.d_ptr || !t.num_elements) continue;
@@ -475,16 +667,10 @@ int ckr_ckpt_write(const char* output_dir, int rank, const ckr_ckpt_tensor* tens
         if (!es) return err(CKR_E_INVALID, "[ckr] unknown dtype for tensor " + std::string(t.name ? t.name : ""));
         if (!v4 && t.num_elements * es > 0xFFFFFFFFull)
             return err(CKR_E_INVALID, "[ckr] tensor " + std::string(t.name ? t.name : "") + " needs unit_bytes (over 4 GiB)");
-        Item it{i, ckr_num_units(t.num_elements, t.dtype, unit_bytes), t.num_elements * (uint64_t)es, es,
-                ckr_sidecar_bytes_per_elem(t.dtype), side_total};
-        const uint64_t side = t.num_elements * (uint64_t)it.spe;
-        side_total += side;
-        n_side += it.spe > 0;
-        cap_side = std::max(cap_side, side);
-        cap_ws = std::max(cap_ws, ckr_encode_workspace_bytes(t.num_elements, t.dtype, unit_bytes));
-        cap_out = std::max(cap_out, ckr_encode_max_output_bytes(t.num_elements, t.dtype, unit_bytes));
-        cap_hdr = std::max(cap_hdr, it.nu * 256 * 16);
-        nu_max = std::max(nu_max, it.nu);
+        Item it{i, slice_geom(t.num_elements, t.dtype, unit_bytes, slice_bytes), side_total};
+        side_total += t.num_elements * (uint64_t)it.g.spe;
+        n_side += it.g.spe > 0;
+        add_needs(needs, t.num_elements, t.dtype, unit_bytes, slice_bytes, v4);
         items.push_back(it);
     }
     const fs::path dir(output_dir);
@@ -527,60 +713,24 @@ int ckr_ckpt_write(const char* output_dir, int rank, const ckr_ckpt_tensor* tens
     };
     std::vector<Out> outs(nw);
 
-    // device buffers: a workspace, and two sets of encode outputs (plus the
-    // stored-byte runs and unit records of v4) that alternate between tensors
-    struct Set {
-        void *out = nullptr, *hdr = nullptr, *off = nullptr, *side = nullptr, *stored = nullptr, *rec = nullptr,
-             *plan = nullptr;
-        std::vector<uint64_t> rec_off, out_off;  // host copies kept until the set is reused
-    };
-    Set sets[2];
-    void* d_ws = nullptr;
+    const uint32_t slots = env_count("CKR_CKPT_SLOTS", 16, 2, kMaxSlots);
+    std::unique_lock<std::mutex> pool_lock(g_pool.use);
+    if (nw) {
+        if (int rc = pool_ensure(needs, slots)) return rc;
+    }
     hipStream_t cs = nullptr;
     hipEvent_t ready[2] = {nullptr, nullptr};
-    std::vector<void*> owned;
     auto release = [&]() {
-        for (void* p : owned) (void)hipFree(p);
-        for (auto e : ready) if (e) (void)hipEventDestroy(e);
+        for (auto e : ready)
+            if (e) (void)hipEventDestroy(e);
         if (cs) (void)hipStreamDestroy(cs);
     };
-    auto alloc = [&](void** p, uint64_t b) {
-        const hipError_t e = hipMalloc(p, std::max<uint64_t>(b, 256));
-        if (e == hipSuccess) owned.push_back(*p);
-        return e == hipSuccess;
-    };
-    bool ok = true;
-    if (nw) {
-        ok = alloc(&d_ws, cap_ws);
-        for (int k = 0; k < 2 && ok; k++) {
-            Set& z = sets[k];
-            ok = alloc(&z.out, cap_out) && alloc(&z.hdr, cap_hdr) && alloc(&z.off, (nu_max + 1) * 8) &&
-                 alloc(&z.side, cap_side) &&
-                 (!v4 || (alloc(&z.stored, cap_out) && alloc(&z.rec, nu_max * (uint64_t)ckr::kUnitRecordMax) &&
-                          alloc(&z.plan, nu_max * 24)));
-        }
-        ok = ok && hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) == hipSuccess &&
-             hipEventCreateWithFlags(&ready[0], hipEventDisableTiming) == hipSuccess &&
-             hipEventCreateWithFlags(&ready[1], hipEventDisableTiming) == hipSuccess;
-    }
-    if (!ok) {
+    if (nw && (hipStreamCreateWithFlags(&cs, hipStreamNonBlocking) != hipSuccess ||
+               hipEventCreateWithFlags(&ready[0], hipEventDisableTiming) != hipSuccess ||
+               hipEventCreateWithFlags(&ready[1], hipEventDisableTiming) != hipSuccess)) {
         (void)hipGetLastError();
         release();
-        return err(CKR_E_HIP, "[ckr] device allocation for the checkpoint writer failed");
-    }
-    const uint32_t slots = env_count("CKR_CKPT_SLOTS", 16, 2, kMaxSlots);
-    std::unique_lock<std::mutex> ring_lock(g_ring.use);
-    if (nw && g_ring.slots < slots) {
-        if (g_ring.base) (void)hipHostFree(g_ring.base);
-        g_ring.base = nullptr;
-        g_ring.slots = 0;
-        if (hipHostMalloc(reinterpret_cast<void**>(&g_ring.base), slots * kSlotBytes, hipHostMallocDefault) != hipSuccess) {
-            g_ring.base = nullptr;
-            (void)hipGetLastError();
-            release();
-            return err(CKR_E_HIP, "[ckr] pinned staging allocation failed");
-        }
-        g_ring.slots = slots;
+        return err(CKR_E_HIP, "[ckr] stream or event creation for the checkpoint writer failed");
     }
     int device = 0;
     if (nw) (void)hipGetDevice(&device);
@@ -588,118 +738,161 @@ int ckr_ckpt_write(const char* output_dir, int rank, const ckr_ckpt_tensor* tens
     int rc = CKR_OK;
     uint64_t data_cursor = 0, meta_cursor = 0;
     if (nw) {
-        Stager st(g_ring.base, slots, device, cs, (int)env_count("CKR_CKPT_WRITERS", std::min(8u, std::max(2u, hw / 2)), 1, 32));
+        Stager st(g_pool.ring, slots, device, cs, (int)env_count("CKR_CKPT_WRITERS", std::min(8u, std::max(2u, hw / 2)), 1, 32));
+        uint32_t* d_hist = static_cast<uint32_t*>(g_pool.hist.p);
+        uint64_t j = 0;  // slices so far: slice j is encoded into buffer set j & 1
         for (uint64_t k = 0; k < nw && rc == CKR_OK; k++) {
             const Item& it = items[k];
+            const SliceGeom& g = it.g;
             const auto& t = tensors[it.i];
             Out& o = outs[k];
-            Set& z = sets[k & 1];
-            if (hipEvent_t prev = st.acquire_set((int)(k & 1))) {
-                if (hipStreamWaitEvent(s, prev, 0) != hipSuccess) { rc = err(CKR_E_HIP, "[ckr] stream wait failed"); break; }
-            }
-            if ((rc = st.status()) != CKR_OK) break;
             const bool singleton = t.cluster_id < 0;
             auto cit = cluster_table.find(t.cluster_id);
             o.owns = singleton || cit == cluster_table.end();
             ckr_freq_table* tab = &tables[k];
-            const uint64_t ws = ckr_encode_workspace_bytes(t.num_elements, t.dtype, unit_bytes);
-            uint64_t total = 0;
             uint32_t tsum = CKR_M;
+            double hist_ms = 0, table_ms = 0, encode_ms = 0, copy_ms = 0;
+            // the table: owners count the whole tensor (masked histogram and the
+            // two live planes' histograms, which size the encoder's slots); members
+            // take their cluster's
+            uint32_t planes[768];
+            const uint32_t* h_planes = nullptr;
             if (o.owns) {
-                rc = ckr_compress(t.d_ptr, t.num_elements, t.dtype, unit_bytes, singleton ? 0 : 1, (uint8_t*)z.out,
-                                  cap_out, (ckr_stream_header*)z.hdr, (uint64_t*)z.off, (uint8_t*)z.side, d_ws, ws, tab,
-                                  &total, s);
-                tsum = tab->cum_freq[256];
-                if (rc == CKR_OK && repair_tables && tsum > CKR_M) {
-                    repair_table(tab);
-                    rc = ckr_encode(t.d_ptr, t.num_elements, t.dtype, tab, unit_bytes, (uint8_t*)z.out, cap_out,
-                                    (ckr_stream_header*)z.hdr, (uint64_t*)z.off, (uint8_t*)z.side, d_ws, ws, &total, s);
+                auto t0 = std::chrono::steady_clock::now();
+                rc = ckr_byte_histogram_planes(t.d_ptr, t.num_elements, t.dtype, d_hist, s);
+                if (rc != CKR_OK) break;
+                if (hipMemcpyAsync(planes, d_hist, sizeof(planes), hipMemcpyDeviceToHost, s) != hipSuccess ||
+                    hipStreamSynchronize(s) != hipSuccess) {
+                    rc = err(CKR_E_HIP, "[ckr] histogram read-back failed");
+                    break;
                 }
+                hist_ms = ms_since(t0);
+                t0 = std::chrono::steady_clock::now();
+                rc = ckr_build_table(planes, singleton ? 0 : 1, tab, &tsum);
+                if (rc != CKR_OK) break;
+                if (repair_tables && tsum > CKR_M) repair_table(tab);
+                table_ms = ms_since(t0);
+                if (g.spe) h_planes = planes + 256;
                 if (!singleton) cluster_table[t.cluster_id] = tab;
                 o.table = tab;
             } else {
                 tab = cit->second;
                 tsum = tab->cum_freq[256];
                 o.anchor = anchor_name[t.cluster_id];
-                rc = ckr_encode(t.d_ptr, t.num_elements, t.dtype, tab, unit_bytes, (uint8_t*)z.out, cap_out,
-                                (ckr_stream_header*)z.hdr, (uint64_t*)z.off, (uint8_t*)z.side, d_ws, ws, &total, s);
+            }
+            o.raw = true;
+            o.data_off = data_cursor;
+            o.meta_off = meta_cursor;
+            uint64_t total = 0, stored_total = 0;
+            for (uint64_t sl = 0; sl < g.n_slices && rc == CKR_OK; sl++, j++) {
+                WriterSet& z = g_pool.sets[j & 1];
+                if (hipEvent_t prev = st.acquire_set((int)(j & 1))) {
+                    if (hipStreamWaitEvent(s, prev, 0) != hipSuccess) { rc = err(CKR_E_HIP, "[ckr] stream wait failed"); break; }
+                }
+                if ((rc = st.status()) != CKR_OK) break;
+                const uint64_t e0 = sl * g.slice_elems;
+                const uint64_t ne = std::min(g.slice_elems, t.num_elements - e0);
+                const uint64_t nb = ne * (uint64_t)g.es;
+                const uint64_t snu = ckr_num_units(ne, t.dtype, unit_bytes);
+                const uint8_t* src = static_cast<const uint8_t*>(t.d_ptr) + e0 * (uint64_t)g.es;
+                auto t0 = std::chrono::steady_clock::now();
+                uint64_t stotal = 0;
+                rc = ckr::encode_slice_of_counted(src, ne, t.dtype, tab, h_planes, unit_bytes, (uint8_t*)z.out.p, z.out.size,
+                                       (ckr_stream_header*)z.hdr.p, (uint64_t*)z.off.p, (uint8_t*)z.side.p, g_pool.ws.p,
+                                       g_pool.ws.size, &stotal, s);
+                encode_ms += ms_since(t0);
+                if (rc != CKR_OK) break;
+                total += stotal;
+                t0 = std::chrono::steady_clock::now();
+                const void* stored = z.out.p;
+                uint64_t stored_size = stotal;
+                if (v4) {
+                    // unit records and the bytes a unit keeps: sizes, host scan, pack
+                    const ckr::UnitGeomArg ug{nb, std::min(g.unit, nb), snu, g.es, g.spe};
+                    const ckr::ZeroLanes zl = ckr::zero_lanes(tab, nb, ug.unit);
+                    uint32_t* d_rs = static_cast<uint32_t*>(z.plan.p);
+                    uint32_t* d_ds = d_rs + snu;
+                    uint64_t* d_ro = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(z.plan.p) + snu * 8);
+                    uint64_t* d_oo = d_ro + snu;
+                    std::vector<uint32_t> sz(2 * snu);
+                    hipError_t e = ckr::launch_unit_plan((const ckr_stream_header*)z.hdr.p, ug, zl.arg, d_rs, d_ds, s);
+                    if (e == hipSuccess) e = hipMemcpyAsync(sz.data(), d_rs, sz.size() * 4, hipMemcpyDeviceToHost, s);
+                    if (e == hipSuccess) e = hipStreamSynchronize(s);
+                    if (e != hipSuccess) { rc = err(CKR_E_HIP, std::string("[ckr] unit plan failed: ") + hipGetErrorString(e)); break; }
+                    z.rec_off.assign(snu, 0);
+                    z.out_off.assign(snu, 0);
+                    uint64_t ra = 0, oa = 0;
+                    for (uint64_t u = 0; u < snu; u++) {
+                        z.rec_off[u] = ra;
+                        z.out_off[u] = oa;
+                        ra += sz[u];
+                        oa += sz[snu + u];
+                    }
+                    e = hipMemcpyAsync(d_ro, z.rec_off.data(), snu * 8, hipMemcpyHostToDevice, s);
+                    if (e == hipSuccess) e = hipMemcpyAsync(d_oo, z.out_off.data(), snu * 8, hipMemcpyHostToDevice, s);
+                    if (e == hipSuccess)
+                        e = ckr::launch_unit_pack((const uint8_t*)z.out.p, (const uint64_t*)z.off.p,
+                                                  (const ckr_stream_header*)z.hdr.p, ug, zl.arg, d_ro, d_oo,
+                                                  (uint8_t*)z.rec.p, (uint8_t*)z.stored.p, s);
+                    const uint64_t m0 = o.meta.size();
+                    o.meta.resize(m0 + ra);
+                    if (e == hipSuccess && ra) e = hipMemcpyAsync(o.meta.data() + m0, z.rec.p, ra, hipMemcpyDeviceToHost, s);
+                    if (e == hipSuccess) e = hipStreamSynchronize(s);
+                    if (e != hipSuccess) { rc = err(CKR_E_HIP, std::string("[ckr] unit pack failed: ") + hipGetErrorString(e)); break; }
+                    for (uint64_t u = 0, p = m0; u < snu && o.raw; u++) {
+                        o.raw = o.meta[p] == 1;
+                        p += sz[u];
+                    }
+                    stored = z.stored.p;
+                    stored_size = oa;
+                } else {
+                    o.v2_headers.resize(256);
+                    if (hipMemcpyAsync(o.v2_headers.data(), z.hdr.p, 256 * 16, hipMemcpyDeviceToHost, s) != hipSuccess ||
+                        hipStreamSynchronize(s) != hipSuccess) {
+                        rc = err(CKR_E_HIP, "[ckr] copy of stream headers failed");
+                        break;
+                    }
+                    o.raw = unit_is_raw(o.v2_headers.data(), nb);
+                }
+                copy_ms += ms_since(t0);
+                if (hipEventRecord(ready[j & 1], s) != hipSuccess) { rc = err(CKR_E_HIP, "[ckr] event record failed"); break; }
+                std::vector<Range> ranges;
+                if (stored_size)
+                    ranges.push_back({fs_.fd, data_base + o.data_off + stored_total, (const uint8_t*)stored, stored_size});
+                if (g.spe)
+                    ranges.push_back({fm.fd, mant_base + it.side_off + e0 * (uint64_t)g.spe, (const uint8_t*)z.side.p,
+                                      ne * (uint64_t)g.spe});
+                st.submit(std::move(ranges), (int)(j & 1), ready[j & 1]);
+                stored_total += stored_size;
             }
             if (rc != CKR_OK) break;
-            const void* stored = z.out;
-            uint64_t stored_size = total;
-            if (v4) {
-                // unit records and the bytes a unit keeps: sizes, host scan, pack
-                const ckr::UnitGeomArg g{it.n_bytes, std::min(unit_bytes, it.n_bytes), it.nu, it.es, it.spe};
-                const ckr::ZeroLanes zl = ckr::zero_lanes(tab, it.n_bytes, g.unit);
-                uint32_t* d_rs = static_cast<uint32_t*>(z.plan);
-                uint32_t* d_ds = d_rs + it.nu;
-                uint64_t* d_ro = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(z.plan) + it.nu * 8);
-                uint64_t* d_oo = d_ro + it.nu;
-                std::vector<uint32_t> sz(2 * it.nu);
-                hipError_t e = ckr::launch_unit_plan((const ckr_stream_header*)z.hdr, g, zl.arg, d_rs, d_ds, s);
-                if (e == hipSuccess) e = hipMemcpyAsync(sz.data(), d_rs, sz.size() * 4, hipMemcpyDeviceToHost, s);
-                if (e == hipSuccess) e = hipStreamSynchronize(s);
-                if (e != hipSuccess) { rc = err(CKR_E_HIP, std::string("[ckr] unit plan failed: ") + hipGetErrorString(e)); break; }
-                z.rec_off.assign(it.nu, 0);
-                z.out_off.assign(it.nu, 0);
-                uint64_t ra = 0, oa = 0;
-                for (uint64_t u = 0; u < it.nu; u++) {
-                    z.rec_off[u] = ra;
-                    z.out_off[u] = oa;
-                    ra += sz[u];
-                    oa += sz[it.nu + u];
-                }
-                e = hipMemcpyAsync(d_ro, z.rec_off.data(), it.nu * 8, hipMemcpyHostToDevice, s);
-                if (e == hipSuccess) e = hipMemcpyAsync(d_oo, z.out_off.data(), it.nu * 8, hipMemcpyHostToDevice, s);
-                if (e == hipSuccess)
-                    e = ckr::launch_unit_pack((const uint8_t*)z.out, (const uint64_t*)z.off, (const ckr_stream_header*)z.hdr,
-                                              g, zl.arg, d_ro, d_oo, (uint8_t*)z.rec, (uint8_t*)z.stored, s);
-                o.meta.resize(ra);
-                if (e == hipSuccess && ra) e = hipMemcpyAsync(o.meta.data(), z.rec, ra, hipMemcpyDeviceToHost, s);
-                if (e == hipSuccess) e = hipStreamSynchronize(s);
-                if (e != hipSuccess) { rc = err(CKR_E_HIP, std::string("[ckr] unit pack failed: ") + hipGetErrorString(e)); break; }
-                o.raw = it.nu > 0;
-                for (uint64_t u = 0, p = 0; u < it.nu && o.raw; u++) {
-                    o.raw = o.meta[p] == 1;
-                    p += sz[u];
-                }
-                stored = z.stored;
-                stored_size = oa;
-                o.meta_off = meta_cursor;
-                meta_cursor += ra;
-            } else {
-                o.v2_headers.resize(256);
-                if (hipMemcpyAsync(o.v2_headers.data(), z.hdr, 256 * 16, hipMemcpyDeviceToHost, s) != hipSuccess ||
-                    hipStreamSynchronize(s) != hipSuccess) {
-                    rc = err(CKR_E_HIP, "[ckr] copy of stream headers failed");
-                    break;
-                }
-                o.raw = unit_is_raw(o.v2_headers.data(), it.n_bytes);
-            }
-            o.data_off = data_cursor;
-            o.data_size = stored_size;
-            data_cursor += stored_size;
-            if (hipEventRecord(ready[k & 1], s) != hipSuccess) { rc = err(CKR_E_HIP, "[ckr] event record failed"); break; }
-            std::vector<Range> ranges;
-            if (stored_size) ranges.push_back({fs_.fd, data_base + o.data_off, (const uint8_t*)stored, stored_size});
-            if (it.spe) ranges.push_back({fm.fd, mant_base + it.side_off, (const uint8_t*)z.side, t.num_elements * (uint64_t)it.spe});
-            st.submit(std::move(ranges), (int)(k & 1), ready[k & 1]);
+            o.data_size = stored_total;
+            data_cursor += stored_total;
+            meta_cursor += o.meta.size();
             if (h_stats) {
                 ckr_ckpt_stats& hs = h_stats[k];
+                std::memset(&hs, 0, sizeof(hs));
                 hs.record_index = it.i;
-                hs.original_bytes = it.n_bytes;
+                hs.original_bytes = g.n_bytes;
                 hs.ans_bytes = total;
-                hs.sidecar_bytes = t.num_elements * (uint64_t)it.spe;
+                hs.sidecar_bytes = t.num_elements * (uint64_t)g.spe;
                 hs.owns_table = o.owns;
                 hs.table_sum = tsum;
                 hs.table_repaired = (o.owns && repair_tables && tsum > CKR_M) ? 1 : 0;
+                hs.n_slices = (uint32_t)g.n_slices;
+                hs.stored_bytes = stored_total;
+                hs.record_bytes = o.meta.size();
+                hs.hist_ms = hist_ms;
+                hs.table_ms = table_ms;
+                hs.encode_ms = encode_ms;
+                hs.copy_ms = copy_ms;
             }
         }
         const int src = st.finish();
         if (rc == CKR_OK && src != CKR_OK) rc = err(src, st.message());
     }
-    ring_lock.unlock();
     release();
+    pool_lock.unlock();
     if (rc != CKR_OK) return rc;
 
     // the small parts: states header, index and (v4) unit records; mantissa
@@ -721,13 +914,13 @@ int ckr_ckpt_write(const char* output_dir, int rank, const ckr_ckpt_tensor* tens
         b.u8(o.raw ? 1 : 0);
         b.u8(o.owns ? 1 : 0);
         b.zeros(5);
-        b.u64(items[k].n_bytes);
+        b.u64(items[k].g.n_bytes);
         b.u64(t.num_elements);
         b.u64(o.data_off);
         b.u64(o.data_size);
         b.name(o.owns ? std::string() : o.anchor);
         if (v4) {
-            b.u64(items[k].nu);
+            b.u64(items[k].g.nu);
             b.u64(o.meta_off);
             b.u64(o.meta.size());
         } else {
@@ -743,15 +936,15 @@ int ckr_ckpt_write(const char* output_dir, int rank, const ckr_ckpt_tensor* tens
     m.u32(r);
     m.u32((uint32_t)n_side);
     for (uint64_t k = 0; k < nw; k++) {
-        if (!items[k].spe) continue;
+        if (!items[k].g.spe) continue;
         const auto& t = tensors[items[k].i];
         m.name(t.name ? t.name : "");
         m.u8((uint8_t)t.dtype);
-        m.u8((uint8_t)items[k].spe);
+        m.u8((uint8_t)items[k].g.spe);
         m.zeros(6);
         m.u64(t.num_elements);
         m.u64(items[k].side_off);
-        m.u64(t.num_elements * (uint64_t)items[k].spe);
+        m.u64(t.num_elements * (uint64_t)items[k].g.spe);
     }
     wok = wok && pwrite_all(fm.fd, m.b.data(), m.b.size(), 0);
     Buf d;

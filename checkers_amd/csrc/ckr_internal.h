@@ -49,6 +49,15 @@ uint64_t* prof_phase_buffer(uint64_t n, hipStream_t s);
 // Sets the calling thread's last error (ckr_last_error) and returns code.
 int set_error(int code, const std::string& msg);
 
+// ckr_encode_planes for a slice of a tensor whose own plane histograms are
+// h_planes: every symbol of the slice is then known to have a slot, so the
+// coders need no escape handling (ckr_encode_planes assumes escapes, since its
+// histograms may belong to other data).  Same bytes either way.
+int encode_slice_of_counted(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table,
+                            const uint32_t* h_planes, uint64_t unit_bytes, uint8_t* d_out, uint64_t out_capacity,
+                            ckr_stream_header* d_headers, uint64_t* d_unit_offsets, uint8_t* d_sidecar,
+                            void* d_workspace, uint64_t workspace_bytes, uint64_t* h_total_out, void* stream);
+
 // ------------------------------------------------------------------ launchers
 // All return hipError_t of the launch; geometry is decided inside.
 hipError_t launch_build_enc_table(const TableArg& t, EncSym* d_enc, hipStream_t s);

@@ -579,7 +579,10 @@ __global__ void __launch_bounds__(256) unit_finalize_kernel(EncodeGeom g, uint64
                                                             ckr_stream_header* __restrict__ hdrs,
                                                             uint32_t* __restrict__ unit_size,
                                                             const uint32_t* __restrict__ ulist) {
-    __shared__ uint32_t sc[256];
+    // 64-bit sums: the lanes of a single-unit tensor just below 4 GiB can
+    // together exceed 2^32 bytes when the data does not compress (such a unit
+    // is then stored raw; the offsets of a coded unit are below its length)
+    __shared__ uint64_t sc[256];
     const uint64_t u = ulist ? (uint64_t)ulist[u0 + blockIdx.x] : u0 + blockIdx.x;
     const uint64_t ubase = u * g.unit;
     const uint64_t len = (g.n_bytes - ubase < g.unit) ? (g.n_bytes - ubase) : g.unit;
@@ -589,7 +592,7 @@ __global__ void __launch_bounds__(256) unit_finalize_kernel(EncodeGeom g, uint64
     sc[t] = c;
     __syncthreads();
     for (uint32_t d = 1; d < 256; d <<= 1) {  // inclusive Hillis-Steele scan
-        uint32_t v = (t >= d) ? sc[t - d] : 0u;
+        uint64_t v = (t >= d) ? sc[t - d] : 0ull;
         __syncthreads();
         sc[t] += v;
         __syncthreads();
@@ -601,7 +604,7 @@ __global__ void __launch_bounds__(256) unit_finalize_kernel(EncodeGeom g, uint64
         h.final_state = 0; h.byte_count = (t == 0) ? (uint32_t)len : 0u; h.buf_offset = 0; h.pad = 0;
         uh[t] = h;
     } else {
-        uh[t].buf_offset = sc[t] - c;
+        uh[t].buf_offset = (uint32_t)(sc[t] - c);
     }
     if (t == 0) unit_size[blockIdx.x] = raw ? (uint32_t)len : (uint32_t)total;
 }

@@ -267,7 +267,10 @@ CKR_API int ckr_decode_many(ckr_decode_job* jobs, uint64_t n_jobs, uint64_t unit
  * layout; a larger need is CKR_E_CAPACITY).  The destination must be 4-byte
  * aligned (no staging copy is made).  Every call on a GPU uses that GPU's one
  * array, cleared by the call itself: calls that overlap on one GPU race, so
- * serialise them. ---- */
+ * serialise them.  Under graph capture the call queues kernels only (the table
+ * and canonical streams travel as kernel arguments); h_bad_lanes must then be
+ * NULL (reading the count back synchronises; CKR_E_INVALID otherwise), and the
+ * count stays in the scratch array until the next call. ---- */
 CKR_API int ckr_decode_noalloc(const uint8_t* d_data, const ckr_stream_header* d_headers,
                                const uint64_t* d_unit_offsets,
                                const ckr_freq_table* h_table, uint64_t n_elems, int dtype,
@@ -360,7 +363,7 @@ CKR_API int ckr_cluster(const char* const* names, const float* h_fp, uint64_t n,
  * least count of each byte plane), while the lanes of masked-out byte planes,
  * whose streams the table and the unit length determine, are stored neither
  * as headers nor as bytes (ckr_container.hip gives the exact layout).  Writes
- * stream: tensor k+1 is encoded while tensor k goes to the files through a
+ * stream: slice k+1 is encoded while slice k goes to the files through a
  * pinned host ring (16 x 32 MiB by default, CKR_CKPT_SLOTS; allocated on first
  * use and kept; calls serialise on it) and writer threads (CKR_CKPT_WRITERS).  repair_tables != 0 repairs a
  * full-alphabet table that the reference's one-pass normalisation leaves above
@@ -374,19 +377,46 @@ typedef struct {
     int32_t     cluster_id;
 } ckr_ckpt_tensor;
 
+/* Per written tensor: the fields of the reference's per-tensor log line
+ * (src/ANSCompressor.cpp:1292-1312) and its timing fields
+ * (include/checkers/ANSCompressor.hpp:105-110): hist_ms = histogram and its
+ * read-back, table_ms = host normalisation, encode_ms = encode launches until
+ * the packed size is known, copy_ms = unit records and their read-back (the
+ * file writes overlap the next encode and are not per tensor). */
 typedef struct {
     uint64_t record_index;
     uint64_t original_bytes;
-    uint64_t ans_bytes;
+    uint64_t ans_bytes;      /* packed streams (unit records excluded)          */
     uint64_t sidecar_bytes;
     uint32_t owns_table;
     uint32_t table_sum;      /* sum of the table's frequencies (4096 unless the H1 case) */
     uint32_t table_repaired;
-    uint32_t pad;
+    uint32_t n_slices;       /* slices the tensor was encoded in                */
+    uint64_t stored_bytes;   /* bytes of the tensor in the states file's data    */
+    uint64_t record_bytes;   /* v4 unit records of the tensor                    */
+    double   hist_ms, table_ms, encode_ms, copy_ms;
 } ckr_ckpt_stats;
 
 CKR_API int ckr_ckpt_write(const char* output_dir, int rank, const ckr_ckpt_tensor* tensors, uint64_t n,
                            uint64_t unit_bytes, int repair_tables, ckr_ckpt_stats* h_stats, void* stream);
+
+/* The writer's device buffers (no counterpart in the reference, which sizes
+ * its shared buffers for the largest tensor): a tensor is encoded in slices of
+ * whole units under its whole-tensor table (units are independent streams
+ * given the table, so the files are the same for any slice size), through two
+ * buffer sets sized for one slice, kept from call to call.  The slice size is
+ * CKR_CKPT_SLICE_BYTES (default 4 GiB) unless ckr_ckpt_set_slice_bytes set it
+ * (0 returns to that default); a tensor that is one unit (v2) is one slice.
+ * ckr_ckpt_reserve allocates the buffers and the pinned ring that
+ * ckr_ckpt_write would need for these tensors, so that the write itself
+ * allocates nothing; ckr_ckpt_write grows them when they are too small;
+ * ckr_ckpt_pool_bytes reports the device bytes held; ckr_ckpt_release frees
+ * all of it (also the pinned ring). */
+CKR_API int ckr_ckpt_set_slice_bytes(uint64_t bytes);
+CKR_API uint64_t ckr_ckpt_slice_bytes(void);
+CKR_API int ckr_ckpt_reserve(const ckr_ckpt_tensor* tensors, uint64_t n, uint64_t unit_bytes);
+CKR_API uint64_t ckr_ckpt_pool_bytes(void);
+CKR_API void ckr_ckpt_release(void);
 
 /* Reader (no counterpart in the reference): parses the three files of a rank
  * (v2 or v4 states file) and restores any tensor, bit-exact, into device

@@ -50,6 +50,7 @@ def lib():
             "oc_repair_bucket_count": (u64, [u64]),
             "oc_repair_build": (u32, [vp, u64, i32, u32, u32, vp, vp, vp, vp]),
             "oc_repair_apply": (u64, [vp, u64, i32, u32, vp, u32, vp]),
+            "oc_repair_last_tied_rounds": (u32, []),
         }
         for k, (r, a) in sig.items():
             f = getattr(L, k)
@@ -181,7 +182,7 @@ def repair_build(raw, n, storage_bytes, masked_bits, max_rules=50, want_seq=Fals
     nr = lib().oc_repair_build(_p(raw), n, storage_bytes, masked_bits, max_rules, _p(rules), _p(out_len),
                                _p(mp), _p(seq) if want_seq else None)
     r = dict(rules=[tuple(int(v) for v in rules[4 * i:4 * i + 4]) for i in range(nr)],
-             out_len=int(out_len[0]), max_pair=int(mp[0]))
+             out_len=int(out_len[0]), max_pair=int(mp[0]), tied_rounds=int(lib().oc_repair_last_tied_rounds()))
     if want_seq:
         r["seq"] = seq[: r["out_len"]]
     return r

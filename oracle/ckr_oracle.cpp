@@ -489,6 +489,11 @@ uint64_t oc_repair_bucket_count(uint64_t n) {
     return m.bucket_count();
 }
 
+// Rounds of the last oc_repair_build whose largest pair count was shared by
+// more than one pair (the rounds in which the map's iteration order decides).
+static uint32_t g_tied_rounds = 0;
+uint32_t oc_repair_last_tied_rounds() { return g_tied_rounds; }
+
 // build_shared_grammar on the masked sequence.  rules[4*i..] = {replacement,
 // lhs, rhs, frequency}.  Returns the rule count; *out_len the compressed
 // length, *max_pair the largest pair count seen in any round.  seq_out (n
@@ -499,6 +504,7 @@ uint32_t oc_repair_build(const uint8_t* raw, uint64_t n, int storage_bytes, uint
     std::vector<uint64_t> t = repair_masked_words(raw, n, storage_bytes, masked_bits);
     uint64_t next = (uint64_t)1 << 63, maxf = 0;
     uint32_t nr = 0;
+    g_tied_rounds = 0;
     for (uint32_t ri = 0; ri < max_rules; ri++) {
         if (t.size() < 2) break;
         std::unordered_map<oc_pair, size_t, oc_pair_hash> counts;
@@ -511,6 +517,9 @@ uint32_t oc_repair_build(const uint8_t* raw, uint64_t n, int storage_bytes, uint
             if (kv.second > best) { best = kv.second; bp = kv.first; }
         }
         if (best < 2) break;
+        size_t at_best = 0;
+        for (const auto& kv : counts) at_best += kv.second == best;
+        g_tied_rounds += at_best > 1;
         const uint64_t sym = next++;
         const size_t before = t.size();
         const uint64_t rep = repair_apply_rule(t, bp.l, bp.r, sym);

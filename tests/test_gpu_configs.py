@@ -224,9 +224,11 @@ def _expand(seq, rules):
 @pytest.mark.parametrize("name", [c[0] for c in CFG2])
 def test_cfg2_llama3_8b_layer_prefix_mask_repair(gpu, name):
     """build_shared_grammar on each tensor of the layer (group = the tensor,
-    all 7 bf16 mantissa bits masked, 50 rules).  k_proj / v_proj and the two
-    norms: rules, token count and largest pair count equal the oracle's.  The
-    others (16.8M and 58.7M words, beyond what the oracle finishes in seconds):
+    all 7 bf16 mantissa bits masked, 50 rules), against the oracle
+    (src/tensor_group_prefix_mask_repair.cpp:376-457): rules, token count and
+    largest pair count equal on k_proj, v_proj, the norms, q_proj and o_proj
+    (16.8M words, 50 rules); gate/up/down (58.7M words) equal the oracle's
+    first 5 rules (the oracle's 50 take about a minute each), and for all 50
     the grammar expands back to the masked words exactly, applying the rules
     gives the same token count, and the chosen pair counts never increase."""
     import torch
@@ -238,16 +240,51 @@ def test_cfg2_llama3_8b_layer_prefix_mask_repair(gpu, name):
     print(f"[case] cfg2 repair {name} n={n}", flush=True)
     rp = ck.Repairer(n, ck.BF16, max_rules=50, device=gpu)
     r = rp.build(t.view(torch.uint8), want_seq=True)
-    if n <= 1024 * 4096:
-        ref = oc.repair_build(t.view(torch.uint8).cpu().numpy(), n, 2, k, 50)
+    raw = t.view(torch.uint8).cpu().numpy()
+    if n <= 4096 * 4096:
+        print(f"[case] cfg2 repair {name}: oracle, 50 rules", flush=True)
+        ref = oc.repair_build(raw, n, 2, k, 50)
         assert r["rules"] == ref["rules"]
         assert r["out_len"] == ref["out_len"] and r["max_pair"] == ref["max_pair"]
     else:
+        print(f"[case] cfg2 repair {name}: oracle, 5 rules", flush=True)
+        rp5 = ck.Repairer(n, ck.BF16, max_rules=5, device=gpu)
+        r5 = rp5.build(t.view(torch.uint8))
+        ref = oc.repair_build(raw, n, 2, k, 5)
+        assert r5["rules"] == ref["rules"] == r["rules"][:5]
+        assert r5["out_len"] == ref["out_len"] and r5["max_pair"] == ref["max_pair"]
         freqs = [f for _, _, _, f in r["rules"]]
         assert all(a >= b for a, b in zip(freqs, freqs[1:])) and all(f >= 2 for f in freqs)
         assert rp.apply(t.view(torch.uint8), r["rules"]) == r["out_len"]
         seq = torch.from_numpy(r["seq"].view(np.int64)).to(gpu)
         assert torch.equal(_expand(seq, r["rules"]), _masked_words(t, k))
+
+
+@pytest.mark.parametrize("n", [4096 * 4096, 14336 * 4096])
+def test_cfg2_size_tie_order_against_oracle(gpu, n):
+    """The tie order at cfg2's sizes.  The layer's own tensors never tie at the
+    top count in 50 rounds (the oracle counts 0 tied rounds on them), so here
+    nearly every round ties: masked words cycle through 61 exponent values
+    (random low bits, which the mask clears), so adjacent pairs occur equally
+    often up to one, and the pair chosen in a tied round is the first the
+    reference's std::unordered_map visits, whose bucket count reserve(n) sets
+    for this n (the oracle counts 49 tied rounds of 50 at 16.8M words, 19 of
+    20 at 58.7M)."""
+    import torch
+    ck = _ck()
+    k = ck.repair_masked_bits(ck.BF16)
+    g = _gen(gpu, 77)
+    hi = (torch.arange(n, device=gpu, dtype=torch.int64) % 61 + 60) << 7
+    lo = torch.randint(0, 128, (n,), device=gpu, generator=g, dtype=torch.int64)
+    t = (hi | lo).to(torch.int16)
+    print(f"[case] cfg2-size repair, all pairs tied, n={n}", flush=True)
+    rules = 50 if n <= 4096 * 4096 else 20
+    rp = ck.Repairer(n, ck.BF16, max_rules=rules, device=gpu)
+    r = rp.build(t.view(torch.uint8))
+    ref = oc.repair_build(t.view(torch.uint8).cpu().numpy(), n, 2, k, rules)
+    assert len(ref["rules"]) == rules and ref["tied_rounds"] >= rules - 2
+    assert r["rules"] == ref["rules"]
+    assert r["out_len"] == ref["out_len"] and r["max_pair"] == ref["max_pair"]
 
 
 def _check_at_size(enc, t8, n, dt, unit, samples):
@@ -318,6 +355,60 @@ def test_cfg4_adversarial_256m_every_byte_against_oracle(gpu):
     # the random block's units hold live planes of ~8 bits per symbol: they must
     # still round-trip, and some of them are stored raw (passthrough)
     _check_decode(enc, t8)
+
+
+CFG5_N = 8_819_213_312
+
+
+def _cfg5_tensor(gpu, kind):
+    """One of the Llama-3-70B rank shard's four tensors at full size."""
+    import torch
+    g = _gen(gpu, 5)
+    if kind in ("params_bf16", "master_weights"):
+        p = (torch.randn(CFG5_N, device=gpu, generator=g) * 0.02).to(torch.bfloat16)
+        if kind == "params_bf16":
+            return p, _ck().BF16
+        x = p.float()
+        del p
+        return x, _ck().F32
+    x = torch.randn(CFG5_N, device=gpu, generator=g).mul_(1e-3)
+    return x.mul_(x).add_(1e-12), _ck().F32
+
+
+@pytest.mark.parametrize("kind", ["params_bf16", "master_weights", "exp_avg_sq"])
+def test_cfg5_70b_rank_other_tensors_1mib_units(gpu, kind):
+    """The shard's bf16 parameters (17.6 GB), the fp32 master copy upcast from
+    them and exp_avg_sq (35.3 GB each), 8,819,213,312 elements in 1 MiB units.
+    Every one of them has masked byte counts above 2^32 (the zero symbol alone
+    counts 1 or 2 per element): the table must be the oracle's normalisation of
+    torch's counts reduced mod 2^32, as the reference's u32 histogram leaves
+    them; sampled units are byte-identical to the oracle's encode, the sidecar
+    is the input's low bytes and the decode is bit-exact (where the wrapped
+    counts normalise to exactly 4096; an over-full table is refused)."""
+    import torch
+    ck = _ck()
+    unit = 1 << 20
+    print(f"[case] cfg5 {kind}, 8.8G elements, 1 MiB units", flush=True)
+    x, dt = _cfg5_tensor(gpu, kind)
+    n = x.numel()
+    t8 = x.view(torch.uint8)
+    enc = ck.compress(t8, dt, unit, n_elems=n)
+    torch.cuda.synchronize()
+    print(f"[case] cfg5 {kind} encoded: {enc.total} bytes, {enc.n_units} units", flush=True)
+    tsum = _check_table(enc, t8, n, dt)
+    _check_offsets(enc)
+    nu = enc.n_units
+    _check_sampled_units(enc, t8, dt, unit, [0, 1, nu // 3, nu - 2, nu - 1])
+    es, spe = oc.ES[dt], oc.SPE[dt]
+    step = 1 << 30
+    for i in range(0, n, step):
+        m = min(step, n - i)
+        assert torch.equal(enc.sidecar[i * spe:(i + m) * spe].view(m, spe), t8[i * es:(i + m) * es].view(m, es)[:, :spe])
+    if tsum == 4096:
+        _check_decode(enc, t8)
+    else:
+        with pytest.raises(ck.CkrError):
+            ck.decode(enc)
 
 
 def test_cfg5_70b_rank_tensor_1mib_units(gpu):

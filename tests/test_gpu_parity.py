@@ -678,3 +678,30 @@ def test_invalid_device_pointers_are_errors(gpu):
     dst, bad = ck.decode(e)
     torch.cuda.synchronize()
     assert bad == 0 and torch.equal(dst, t.view(torch.uint8))
+
+
+def test_batched_calls_refuse_overlapping_outputs(gpu):
+    """ckr_compress_many and ckr_decode_many run jobs on several streams at
+    once: an output range of one job that overlaps another output (headers
+    inside another job's headers, a destination inside another's) is refused
+    before anything is queued."""
+    import torch
+    ck = _ck()
+    a = torch.randn(200_000, device=gpu) * 1e-3
+    b = torch.randn(50_000, device=gpu) * 1e-3
+    ea, eb = ck.Encoder(a.numel(), ck.F32, 65536, device=gpu), ck.Encoder(b.numel(), ck.F32, 65536, device=gpu)
+    eb.headers = ea.headers[1024:]          # job 1's headers start at job 0's unit 1
+    with pytest.raises(ck.CkrError) as e:
+        ck.compress_many([ea, eb], [a.view(torch.uint8), b.view(torch.uint8)])
+    assert e.value.code == ck.CKR_E_INVALID and "overlaps" in str(e.value)
+    eb = ck.Encoder(b.numel(), ck.F32, 65536, device=gpu)
+    ra, rb = ck.compress_many([ea, eb], [a.view(torch.uint8), b.view(torch.uint8)])
+    da, db = ck.Decoder(a.numel(), ck.F32, 65536, device=gpu), ck.Decoder(b.numel(), ck.F32, 65536, device=gpu)
+    dst = torch.zeros(a.numel() * 4, dtype=torch.uint8, device=gpu)
+    with pytest.raises(ck.CkrError) as e:
+        ck.decode_many([da, db], [ra, rb], [dst, dst[4096:4096 + b.numel() * 4]])
+    assert e.value.code == ck.CKR_E_INVALID and "overlaps" in str(e.value)
+    db2 = torch.zeros(b.numel() * 4, dtype=torch.uint8, device=gpu)
+    assert ck.decode_many([da, db], [ra, rb], [dst, db2]) == [0, 0]
+    torch.cuda.synchronize()
+    assert torch.equal(dst, a.view(torch.uint8)) and torch.equal(db2, b.view(torch.uint8))

@@ -57,3 +57,43 @@ def test_decode_noalloc_refuses_what_it_cannot_do_without_allocating(gpu):
         ck.decode_noalloc(enc, buf[2:2 + 20_000])
     assert e.value.code == ck.CKR_E_INVALID and "4-byte aligned" in str(e.value)
     torch.cuda.synchronize()
+
+
+def test_decode_noalloc_captured_in_a_graph(gpu):
+    """Captured into a HIP graph (h_bad_lanes NULL, as capture requires), the
+    decode replays bit-exact, several times, with eager work between the
+    replays; a capture that asks for the bad-lane count is refused; an eager
+    call leaves the device's free memory unchanged."""
+    import torch
+    import checkers_amd as ck
+    n = 1_000_003
+    t, enc = _case(ck, gpu, n, ck.F32, 65536, 9)
+    nb = n * 4
+    ref, bad_ref = ck.decode(enc)
+    assert bad_ref == 0
+    dst = torch.zeros(nb, dtype=torch.uint8, device=gpu)
+    assert ck.decode_noalloc(enc, dst) == 0          # warm-up: scratch address, code objects
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    assert ck.decode_noalloc(enc, dst) == 0
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    print("[case] noalloc decode under graph capture", flush=True)
+    dst.zero_()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, capture_error_mode="relaxed"):
+        with pytest.raises(ck.CkrError) as e:
+            ck.decode_noalloc(enc, dst, check=True)
+        ck.decode_noalloc(enc, dst, check=False)
+    assert e.value.code == ck.CKR_E_INVALID and "captured" in str(e.value)
+    torch.cuda.synchronize()
+    assert not bool(dst.any())                        # capture ran nothing
+    for r in range(4):
+        dst.fill_(r + 1)                              # eager work between the replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(dst, ref[:nb]), r
+    assert torch.equal(dst, t.view(torch.uint8))
+    del g
