@@ -391,6 +391,7 @@ std::vector<PhaseRec> g_phase;
 }  // namespace
 
 namespace ckr {
+bool profiling() { return g_prof_on; }
 // Set while a no-allocation entry point runs on this thread: profiling, which
 // creates events and buffers, stays out of it.
 thread_local bool t_noalloc = false;
@@ -1665,6 +1666,12 @@ int repair_prep(uint64_t n, int dtype, int masked_bits, uint32_t max_rules, bool
         nb = p->primes.back();
     }
     p->layout = ckr::repair_layout(n, p->es, p->k, max_rules, nb);
+    // token ids (alphabet, then one per rule) must stay below the tombstones
+    const uint32_t w = 8u * (uint32_t)p->es - p->k;
+    const uint64_t ids = std::min<uint64_t>(n, 1ull << std::min<uint32_t>(w, 40)) + max_rules;
+    if (ids > ckr::kRepairTomb32)
+        return fail(CKR_E_INVALID, "[ckr] repair of %llu words with %u rules needs more than 32-bit token ids",
+                    (unsigned long long)n, max_rules);
     return CKR_OK;
 }
 

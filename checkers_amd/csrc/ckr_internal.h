@@ -36,6 +36,8 @@ struct EncSym {
 // Optional per-kernel timing (ckr_profile_begin / ckr_profile_end): when on,
 // every launch below is bracketed by HIP events recorded on its own stream.
 void prof_mark(const char* name, hipStream_t s, bool begin);
+// Whether ckr_profile_begin is in effect (launches are then timed one by one).
+bool profiling();
 extern thread_local bool t_noalloc;
 // With profiling on, a device buffer of n u64 for per-unit phase stamps (else
 // null); ckr_profile_end reduces the stamps of the last launch that used it.
@@ -187,19 +189,26 @@ hipError_t launch_analyze(const ckr_stats_record* recs, uint64_t n, void* ws, hi
 // Prefix-mask repair (ckr_repair.hip).
 struct RepairCtl {
     uint64_t pick;        // tie-break: max of (bucket first occurrence << 32 | first occurrence)
-    uint32_t n_cur, n_next, done, round;
+    uint32_t n_cur, occ, done, round;  // live tokens; occurrences found this round
     uint32_t best, ncand, chosen, d;   // d: occupied pair-table slots
     uint32_t a0, a, b, c;              // alphabet size; pair (a, b) → c of this round
-    uint32_t skip, cur, err, max_pair; // cur: which token buffer holds the sequence
+    uint32_t skip, tie, err, max_pair; // tie: several pairs hold the top count
     uint32_t recount, recount_next;    // build: count every pair this round / the next
+    uint32_t run_mode;                 // a == b: occurrences depend on the run parity
+    uint32_t pad[4];
 };
 constexpr uint32_t kRepairMaxPrimes = 512;
+// Token ids of the repair sequence lie below these; the values from here up
+// are tombstones (positions no live token holds) carrying span lengths.
+constexpr uint32_t kRepairTomb16 = 0xF000u;
+constexpr uint32_t kRepairTomb32 = 0xFFFF0000u;
 struct RepairLayout {
     uint32_t w;           // live bits per word
     bool direct;          // w <= 16: alphabet by bitmap, else by hash set
-    uint64_t pair_cap, vcap, n_buckets;
-    uint64_t o_ctl, o_buf0, o_buf1, o_sym, o_bitmap, o_rank, o_vkey, o_vrank, o_occ;
-    uint64_t o_pkey, o_pcnt, o_pfirst, o_touched, o_bfirst, o_primes, o_bfun, o_boff, o_rules, o_rmap;
+    bool tok16;           // token ids (alphabet + rules) lie below kRepairTomb16
+    uint64_t pair_cap, vcap, n_buckets, list_entries;
+    uint64_t o_ctl, o_tok, o_len, o_back, o_list, o_bcount, o_sym, o_bitmap, o_rank, o_vkey, o_vrank, o_occ;
+    uint64_t o_pkey, o_pcnt, o_pfirst, o_touched, o_bfirst, o_primes, o_bfun, o_rules, o_rmap;
     uint64_t bytes;
 };
 // n_buckets: bucket count of reserve(n) (size of the bucket first-occurrence array).

@@ -6,41 +6,75 @@
 // build_shared_grammar (:428-457), apply_existing_grammar (:459-467).
 //
 // Layout.  Each masked word (word with its low k mantissa bits cleared) is
-// replaced by a dense u32 id, its rank in the tensor's alphabet; rule r gets
-// id A0 + r.  sym[id] keeps the reference's 64-bit symbol (the masked word, or
-// 2^63 + r) for the tie-break hash.  The sequence lives in two u32 buffers
-// that the rounds ping-pong between.
+// replaced by a dense id, its rank in the tensor's alphabet; rule r gets id
+// A0 + r.  sym[id] keeps the reference's 64-bit symbol (the masked word, or
+// 2^63 + r) for the tie-break hash.  Ids are 16 bits wide when the alphabet,
+// the rules and the tombstone fit (bf16 with all 7 mantissa bits masked: at
+// most 512 words), else 32.
 //
-// One round (all on the device, no host synchronisation):
-//   pair_pass<COUNT>   every adjacent pair counted (first round, or when the
-//                      table is to be rebuilt): per-workgroup LDS cache of
-//                      2048 pairs in front of a global open-addressing table;
-//                      later rounds keep the counts up to date instead: the
-//                      replacement subtracts the pairs it destroys (those with
-//                      a replaced token) and pair_pass<INC> adds the new
-//                      sequence's pairs holding the new symbol, the only new
-//                      pairs (a pair of two kept tokens was a pair before);
-//   sel_max/sel_cand   largest count and the number of pairs holding it;
-//   tie_*              only if several pairs hold it: the pair std::unordered_map
-//                      would visit first.  libstdc++ keeps one singly linked
-//                      list; a node for an empty bucket goes to the list head,
-//                      a node for a used bucket goes to the front of that
-//                      bucket's run.  With reserve(size) no rehash happens, so
-//                      the visit order is: buckets by decreasing time of their
-//                      first insertion, and within a bucket pairs by decreasing
-//                      time of insertion.  Insertion time is the position of a
-//                      pair's first occurrence.  The winner maximises
-//                      (first occurrence of any pair in its bucket, its own
-//                      first occurrence); the bucket is hash % P with P the
-//                      bucket count of reserve(size), taken from libstdc++ by
-//                      the host;
-//   round_commit       record the rule (or stop: best count < 2) and decide
-//                      whether the next round recounts (table above 3/4 full
-//                      once the new pairs are in);
-//   rep_*              greedy left-to-right replacement as a scan: the state
-//                      "previous token started a replacement" is a function of
-//                      the state entering a segment, so segments compose;
-//   tab_clear/round_end reset the touched table slots (recount only) and advance.
+// The sequence is never compacted between rounds.  It keeps its n positions;
+// a replacement of the pair at live positions (p, q) writes the new id at p
+// and tombstones over the rest of the merged span, so every live token heads a
+// span of positions (itself and the tombstones of what it absorbed).  Ids from
+// kRepairTomb16 / kRepairTomb32 up are tombstones: the first and the last
+// tombstone of a span of L positions (one position for L = 2) hold
+// tomb + min(L - 1, LMAX), and the all-ones value (LMAX, long spans) sends the
+// reader to len[head] and back[last position], written only for such spans.
+// So the next live token after p is p + 1 or p + 1 + (tok[p + 1] - tomb), the
+// previous one before p is p - 1 or p - 1 - (tok[p - 1] - tomb): one or two
+// reads near p, and a replacement writes 2 to 4 tokens of the tok array (no
+// other array for spans under LMAX).  Positions are monotone in the compacted
+// sequence, so first occurrences compare as the reference's do.
+//
+// One round (all on the device, no host synchronisation), five launches:
+//   rp_count     (rounds that recount: the first, or when the table could pass
+//                3/4 full) every adjacent pair of live tokens counted, through a
+//                per-workgroup LDS cache of 2048 pairs in front of a global
+//                open-addressing table; the last workgroup to finish selects;
+//   rp_first     (rounds where several pairs hold the top count) the first
+//                occurrence of every pair; the last workgroup breaks the tie
+//                as std::unordered_map's iteration order would (below) and
+//                commits the rule;
+//   rp_runs      (rounds whose pair is (x, x)) the run parity: which x
+//                starts an occurrence depends on how many x precede it in its
+//                run, a function of the state entering a block of positions,
+//                so blocks compose; the last workgroup scans the blocks;
+//   rp_find      every occurrence of the pair (a, b): its start goes to a list,
+//                and (build rounds) the pair counts change by what the
+//                replacement destroys and creates around it, all read from the
+//                old sequence (no position is written in this pass);
+//   rp_write     the list's occurrences replaced in place; the last workgroup
+//                closes the round (live count, round number, the table emptied
+//                before a recount) and selects the next round's pair from the
+//                kept counts, committing it when no tie needs rp_first.
+// Selection: the largest count and the number of pairs holding it; a unique
+// holder is the rule.  Ties: libstdc++ keeps one singly linked list; a node
+// for an empty bucket goes to the list head, a node for a used bucket goes to
+// the front of that bucket's run.  With reserve(size) no rehash happens, so
+// the visit order is: buckets by decreasing time of their first insertion,
+// and within a bucket pairs by decreasing time of insertion (first
+// occurrence).  The winner maximises (first occurrence of any pair in its
+// bucket, its own first occurrence); the bucket is hash % P with P the bucket
+// count of reserve(size), taken from libstdc++ by the host.
+//
+// Kept counts: a pair of two old live tokens that are both untouched by the
+// round's replacements stays a pair, so only the pairs around an occurrence
+// change.  For an occurrence (p, q) of (a, b) → c with x = prev(p) and
+// r = next(q), a != b:
+//   left:  x is the second token of an earlier occurrence (x holds b and
+//          prev(x) holds a): (b, a) becomes (c, c); else (x, a) becomes (x, c);
+//   right: r starts an occurrence (r holds a, next(r) holds b): that one's
+//          left side accounts for the pair; else (b, r) becomes (c, r);
+// and a == b == x (occurrences pair up the x of a run from its start):
+//   left:  x at prev(p) is a replaced second, so the new pair is (c, c); any
+//          other token t: (t, x) becomes (t, c);
+//   right: r holds x and starts an occurrence: nothing; r holds x and does not
+//          (the odd last x of its run): (c, x) is new; else (x, r) becomes (c, r).
+// Every occurrence of (a, b) is replaced or loses a token to an overlapping
+// replacement, so its count is set to 0 at the commit.
+#include <mutex>
+#include <vector>
+
 #include "ckr_internal.h"
 
 namespace ckr {
@@ -51,14 +85,23 @@ constexpr uint32_t NONE = 0xFFFFFFFFu;
 constexpr int RT = 256;          // threads per workgroup
 constexpr int CACHE = 2048;      // LDS pair cache entries
 constexpr int CACHE_PROBES = 8;
-constexpr int DCACHE = 1024;     // LDS cache of the pairs a replacement workgroup subtracts
-constexpr int SEG = 16;          // tokens per thread in the replace pass
-constexpr int BLK = RT * SEG;    // tokens per replace block
-constexpr int SCAN_T = 1024;     // threads of the single-workgroup scans
-constexpr uint32_t PAIR_CHUNK = 8192;  // least pairs per pair_pass workgroup
-constexpr uint32_t PAIR_BLOCKS_PER_CU = 4;  // pair_pass workgroups per CU at most, larger chunks above
-constexpr int PAIR_UNROLL = 4;   // pairs loaded together per pair_pass thread
+constexpr int SEG = 16;          // positions per thread in rp_runs / rp_find
+constexpr int BLK = RT * SEG;    // positions per rp_runs / rp_find block
+constexpr int SCAN_T = 1024;     // threads of the single-workgroup alphabet scan
+constexpr uint32_t PAIR_CHUNK = 8192;  // least positions per rp_count / rp_first workgroup
+constexpr int PAIR_UNROLL = 4;   // pairs loaded together per rp_count thread
 constexpr uint32_t OCC_BLK = 4096;
+constexpr uint32_t CHUNK = 64 * SEG;    // positions a wave takes at once
+constexpr uint32_t FIND_GRID = 1024;   // rp_runs / rp_find / rp_write workgroups (4 units each)
+constexpr int CLOSE_T = 1024;          // rp_close threads
+
+template <typename T>
+__host__ __device__ __forceinline__ constexpr T tomb() { return (T)~(T)0; }
+// The least tombstone id, and the span-length field's "look it up" value.
+template <typename T>
+__host__ __device__ __forceinline__ constexpr uint32_t tb0() { return sizeof(T) == 2 ? kRepairTomb16 : kRepairTomb32; }
+template <typename T>
+__host__ __device__ __forceinline__ constexpr uint32_t lmax() { return (uint32_t)tomb<T>() - tb0<T>(); }
 
 // MurmurHash3 fmix64 / fmix32 finalizers (public domain): table slot hashes.
 __device__ __forceinline__ uint64_t mix64(uint64_t x) {
@@ -79,11 +122,47 @@ __device__ __forceinline__ uint64_t ref_pair_hash(uint64_t l, uint64_t r) {
 __device__ __forceinline__ uint64_t ld_relaxed(const uint64_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ uint32_t ld_relaxed32(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 template <int ES>
 __device__ __forceinline__ uint32_t load_word(const uint8_t* w, uint64_t i) {
     if constexpr (ES == 2) return reinterpret_cast<const uint16_t*>(w)[i];
     else return reinterpret_cast<const uint32_t*>(w)[i];
+}
+
+// The live position after live position i (N if none), t1 being the token at
+// i + 1: i + 1 itself, or past i's span, whose first tombstone (i + 1) holds
+// its length (or says to read len[i]).
+template <typename T>
+__device__ __forceinline__ uint32_t next_from(const uint32_t* __restrict__ len, uint32_t i, uint32_t t1, uint32_t N) {
+    if (i + 1 >= N) return N;
+    if (t1 < tb0<T>()) return i + 1;
+    const uint32_t s = t1 - tb0<T>();
+    return min(s < lmax<T>() ? i + 1 + s : i + len[i], N);
+}
+template <typename T>
+__device__ __forceinline__ uint32_t next_live(const T* __restrict__ tok, const uint32_t* __restrict__ len, uint32_t i,
+                                              uint32_t N) {
+    if (i + 1 >= N) return N;
+    return next_from<T>(len, i, tok[i + 1], N);
+}
+// The live position before live position i (NONE if none), t0 being the token
+// at i - 1: i - 1 itself, or the head of the span whose last tombstone it is
+// (its length there, or back[i - 1]).
+template <typename T>
+__device__ __forceinline__ uint32_t prev_from(const uint32_t* __restrict__ back, uint32_t i, uint32_t t0) {
+    if (i == 0) return NONE;
+    if (t0 < tb0<T>()) return i - 1;
+    const uint32_t s = t0 - tb0<T>();
+    const uint32_t h = s < lmax<T>() ? (s < i ? i - 1 - s : NONE) : back[i - 1];
+    return h < i ? h : NONE;  // (a head lies before its span's end)
+}
+template <typename T>
+__device__ __forceinline__ uint32_t prev_live(const T* __restrict__ tok, const uint32_t* __restrict__ back, uint32_t i) {
+    if (i == 0) return NONE;
+    return prev_from<T>(back, i, tok[i - 1]);
 }
 
 struct PairTab {
@@ -94,18 +173,9 @@ struct PairTab {
     uint64_t mask;  // capacity - 1 (power of two)
 };
 
-// ------------------------------------------------------------------ block helpers
-__device__ uint32_t block_reduce_max(uint32_t v, uint32_t* sh) {
-    for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o));
-    const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) sh[w] = v;
-    __syncthreads();
-    uint32_t r = 0;
-    for (int i = 0; i < nw; i++) r = max(r, sh[i]);
-    return r;
-}
+__device__ __forceinline__ uint64_t pair_key(uint32_t l, uint32_t r) { return ((uint64_t)l << 32) | r; }
 
+// ------------------------------------------------------------------ block helpers
 // Exclusive scan of u32 over the block (blockDim.x <= 1024); returns the
 // exclusive prefix, *total the sum.
 __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* sh, uint32_t* total) {
@@ -120,6 +190,7 @@ __device__ uint32_t block_excl_scan(uint32_t v, uint32_t* sh, uint32_t* total) {
     __syncthreads();
     uint32_t base = 0, tot = 0;
     for (int i = 0; i < nw; i++) { if (i < w) base += sh[i]; tot += sh[i]; }
+    __syncthreads();
     *total = tot;
     return base + x - v;
 }
@@ -162,10 +233,10 @@ __global__ void __launch_bounds__(SCAN_T) alpha_rank_direct(const uint32_t* __re
     if (t == 0) ctl->a0 = total;
 }
 
-template <int ES>
+template <int ES, typename T>
 __global__ void __launch_bounds__(RT) alpha_map_direct(const uint8_t* __restrict__ words, uint64_t n, uint32_t k,
                                                        const uint32_t* __restrict__ rank, uint32_t nv,
-                                                       uint32_t* __restrict__ tok) {
+                                                       T* __restrict__ tok) {
     extern __shared__ uint32_t lrank[];
     const bool staged = nv <= 16384;
     if (staged) {
@@ -174,7 +245,7 @@ __global__ void __launch_bounds__(RT) alpha_map_direct(const uint8_t* __restrict
     }
     for (uint64_t i = (uint64_t)blockIdx.x * RT + threadIdx.x; i < n; i += (uint64_t)gridDim.x * RT) {
         const uint32_t v = load_word<ES>(words, i) >> k;
-        tok[i] = staged ? lrank[v] : rank[v];
+        tok[i] = (T)(staged ? lrank[v] : rank[v]);
     }
 }
 
@@ -259,11 +330,13 @@ __global__ void __launch_bounds__(RT) occ_rank(const uint64_t* __restrict__ vkey
 template <int ES>
 __global__ void __launch_bounds__(RT) alpha_map_hash(const uint8_t* __restrict__ words, uint64_t n, uint32_t k,
                                                      const uint64_t* __restrict__ vkey, uint64_t mask,
-                                                     const uint32_t* __restrict__ vrank, uint32_t* __restrict__ tok) {
+                                                     const uint32_t* __restrict__ vrank, uint32_t* __restrict__ tok,
+                                                     RepairCtl* ctl) {
     for (uint64_t i = (uint64_t)blockIdx.x * RT + threadIdx.x; i < n; i += (uint64_t)gridDim.x * RT) {
         const uint32_t v = load_word<ES>(words, i) >> k;
         const uint64_t s = vslot_find(vkey, mask, v);
-        tok[i] = (s == EMPTY_KEY) ? NONE : vrank[s];
+        if (s == EMPTY_KEY) atomicOr(&ctl->err, 1u);
+        tok[i] = (s == EMPTY_KEY) ? 0u : vrank[s];
     }
 }
 
@@ -325,99 +398,69 @@ __device__ void tab_first(const PairTab& t, RepairCtl* ctl, uint64_t key, uint32
     atomicOr(&ctl->err, 4u);
 }
 
-// COUNT: count every adjacent pair (a recount round).  FIRST (ties only): first
-// occurrence of every pair.  INC (after a round's replacement): count the pairs
-// holding the round's new symbol c.
-enum PairMode { COUNT = 0, FIRST_OCC = 1, INC = 2 };
-
-template <int MODE>
-__global__ void __launch_bounds__(RT) pair_pass(const uint32_t* __restrict__ buf0, const uint32_t* __restrict__ buf1,
-                                                RepairCtl* ctl, PairTab tab, uint32_t chunk) {
-    constexpr bool FIRST = MODE == FIRST_OCC;
-    if (ctl->done) return;
-    if (MODE == COUNT && !ctl->recount) return;
-    if (FIRST && (ctl->ncand <= 1 || ctl->best < 2)) return;
-    if (MODE == INC && ctl->recount) return;
-    const uint32_t c = ctl->c;
-    const uint32_t n = ctl->n_cur;
-    if (n < 2) return;
-    const uint32_t np = n - 1;
-    const uint64_t base = (uint64_t)blockIdx.x * chunk;
-    if (base >= np) return;
-    const uint32_t* tok = ctl->cur ? buf1 : buf0;
-    __shared__ uint64_t ck[CACHE];
-    __shared__ uint32_t cv[CACHE];
+// LDS cache of pair updates in front of the global table: adds (FIRST: the
+// least position) accumulate per key, misses go to the table directly.
+template <bool FIRST>
+__device__ __forceinline__ void cache_put(uint64_t* ck, uint32_t* cv, const PairTab& tab, RepairCtl* ctl,
+                                          uint64_t key, uint32_t v) {
+    uint32_t s = (uint32_t)mix64(key) & (CACHE - 1);
+    for (int p = 0; p < CACHE_PROBES; p++) {
+        uint64_t cur = ck[s];
+        if (cur == EMPTY_KEY) {
+            cur = atomicCAS((unsigned long long*)&ck[s], (unsigned long long)EMPTY_KEY, (unsigned long long)key);
+            if (cur == EMPTY_KEY) cur = key;
+        }
+        if (cur == key) {
+            if (FIRST) atomicMin(&cv[s], v); else atomicAdd(&cv[s], v);
+            return;
+        }
+        s = (s + 1) & (CACHE - 1);
+    }
+    if (FIRST) tab_first(tab, ctl, key, v); else tab_add(tab, ctl, key, v);
+}
+template <bool FIRST>
+__device__ void cache_init(uint64_t* ck, uint32_t* cv) {
     for (int j = threadIdx.x; j < CACHE; j += RT) { ck[j] = EMPTY_KEY; cv[j] = FIRST ? NONE : 0u; }
     __syncthreads();
-    const uint32_t end = (uint32_t)min<uint64_t>(base + chunk, np);
-    // PAIR_UNROLL pairs per thread per step, their tokens loaded before any is
-    // entered, so that the loads wait for memory together
-    for (uint32_t i0 = (uint32_t)base + threadIdx.x; i0 < end; i0 += PAIR_UNROLL * RT) {
-        uint64_t keys[PAIR_UNROLL];
-#pragma unroll
-        for (int u = 0; u < PAIR_UNROLL; u++) {
-            const uint32_t i = i0 + u * RT;
-            keys[u] = i < end ? ((uint64_t)tok[i] << 32) | tok[i + 1] : EMPTY_KEY;
-        }
-#pragma unroll
-        for (int u = 0; u < PAIR_UNROLL; u++) {
-            const uint32_t i = i0 + u * RT;
-            if (i >= end) break;
-            const uint64_t key = keys[u];
-            if (MODE == INC && (uint32_t)(key >> 32) != c && (uint32_t)key != c) continue;
-            uint32_t s = mix64(key) & (CACHE - 1);
-            bool hit = false;
-            for (int p = 0; p < CACHE_PROBES; p++) {
-                uint64_t cur = ck[s];
-                if (cur == EMPTY_KEY) {
-                    cur = atomicCAS((unsigned long long*)&ck[s], (unsigned long long)EMPTY_KEY, (unsigned long long)key);
-                    if (cur == EMPTY_KEY) cur = key;
-                }
-                if (cur == key) {
-                    if (FIRST) atomicMin(&cv[s], i); else atomicAdd(&cv[s], 1u);
-                    hit = true;
-                    break;
-                }
-                s = (s + 1) & (CACHE - 1);
-            }
-            if (!hit) { if (FIRST) tab_first(tab, ctl, key, i); else tab_add(tab, ctl, key, 1u); }
-        }
-    }
+}
+template <bool FIRST>
+__device__ void cache_flush(const uint64_t* ck, const uint32_t* cv, const PairTab& tab, RepairCtl* ctl) {
     __syncthreads();
-    for (int j = threadIdx.x; j < CACHE; j += RT) {
-        const uint64_t key = ck[j];
-        if (key == EMPTY_KEY) continue;
-        if (FIRST) tab_first(tab, ctl, key, cv[j]);
-        else tab_add(tab, ctl, key, cv[j]);
+    // A thread's CACHE / RT entries go out together: their home slots' keys are
+    // loaded at once (keys only go from empty to set while the counting kernels
+    // run, so a plain load that finds the key is right; one that finds anything
+    // else takes the probing path), then the adds.  Each workgroup starts at its
+    // own slot, so that the workgroups' updates of the same frequent pairs do not
+    // all reach the table at the same moment.
+    constexpr int PER = CACHE / RT;
+    uint64_t key[PER], slot[PER], cur[PER];
+    uint32_t val[PER];
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int j = (threadIdx.x + i * RT + blockIdx.x * 97) & (CACHE - 1);
+        key[i] = ck[j];
+        val[i] = cv[j];
+    }
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        slot[i] = mix64(key[i]) & tab.mask;
+        cur[i] = key[i] != EMPTY_KEY ? tab.key[slot[i]] : EMPTY_KEY;
+    }
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        if (key[i] == EMPTY_KEY || (!FIRST && val[i] == 0)) continue;
+        if (cur[i] == key[i]) {
+            if (FIRST) atomicMin(&tab.first[slot[i]], val[i]);
+            else atomicAdd(&tab.cnt[slot[i]], val[i]);
+        } else if (FIRST) {
+            tab_first(tab, ctl, key[i], val[i]);
+        } else {
+            tab_add(tab, ctl, key[i], val[i]);
+        }
     }
 }
 
-// Ties only: the first occurrences are taken afresh for the current sequence.
-__global__ void __launch_bounds__(RT) first_reset(RepairCtl* ctl, PairTab tab) {
-    if (ctl->done || ctl->best < 2 || ctl->ncand <= 1) return;
-    const uint32_t d = ctl->d;
-    for (uint32_t j = blockIdx.x * RT + threadIdx.x; j < d; j += gridDim.x * RT) tab.first[tab.touched[j]] = NONE;
-}
-
-__global__ void __launch_bounds__(RT) sel_max(RepairCtl* ctl, PairTab tab) {
-    __shared__ uint32_t sh[16];
-    if (ctl->done) return;
-    const uint32_t d = ctl->d;
-    uint32_t m = 0;
-    for (uint32_t j = blockIdx.x * RT + threadIdx.x; j < d; j += gridDim.x * RT) m = max(m, tab.cnt[tab.touched[j]]);
-    m = block_reduce_max(m, sh);
-    if (threadIdx.x == 0 && m) atomicMax(&ctl->best, m);
-}
-
-__global__ void __launch_bounds__(RT) sel_cand(RepairCtl* ctl, PairTab tab) {
-    if (ctl->done) return;
-    const uint32_t d = ctl->d, best = ctl->best;
-    for (uint32_t j = blockIdx.x * RT + threadIdx.x; j < d; j += gridDim.x * RT) {
-        const uint32_t s = tab.touched[j];
-        if (tab.cnt[s] == best) { atomicAdd(&ctl->ncand, 1u); ctl->chosen = s; }
-    }
-}
-
+// ------------------------------------------------------------------ round control (one workgroup)
 __device__ __forceinline__ uint64_t bucket_count_of(const uint64_t* primes, uint32_t np, uint64_t n) {
     uint32_t lo = 0, hi = np;  // first entry >= n
     while (lo < hi) { const uint32_t mid = (lo + hi) >> 1; if (primes[mid] < n) lo = mid + 1; else hi = mid; }
@@ -428,323 +471,642 @@ __device__ __forceinline__ uint64_t bucket_of(uint64_t key, const uint64_t* sym,
     return ref_pair_hash(sym[key >> 32], sym[key & 0xFFFFFFFFu]) % P;
 }
 
-#define CKR_TIE_GUARD() if (ctl->done || ctl->best < 2 || ctl->ncand <= 1) return
-
-__global__ void __launch_bounds__(RT) tie_bucket(RepairCtl* ctl, PairTab tab, const uint64_t* __restrict__ sym,
-                                                 const uint64_t* __restrict__ primes, uint32_t np,
-                                                 uint32_t* __restrict__ bfirst) {
-    CKR_TIE_GUARD();
-    const uint64_t P = bucket_count_of(primes, np, ctl->n_cur);
-    const uint32_t d = ctl->d;
-    for (uint32_t j = blockIdx.x * RT + threadIdx.x; j < d; j += gridDim.x * RT) {
-        const uint32_t s = tab.touched[j];
-        atomicMin(&bfirst[bucket_of(tab.key[s], sym, P)], tab.first[s]);
-    }
-}
-
-__global__ void __launch_bounds__(RT) tie_pick(RepairCtl* ctl, PairTab tab, const uint64_t* __restrict__ sym,
-                                               const uint64_t* __restrict__ primes, uint32_t np,
-                                               const uint32_t* __restrict__ bfirst) {
-    CKR_TIE_GUARD();
-    const uint64_t P = bucket_count_of(primes, np, ctl->n_cur);
-    const uint32_t d = ctl->d, best = ctl->best;
-    for (uint32_t j = blockIdx.x * RT + threadIdx.x; j < d; j += gridDim.x * RT) {
-        const uint32_t s = tab.touched[j];
-        if (tab.cnt[s] != best) continue;
-        const uint64_t v = ((uint64_t)bfirst[bucket_of(tab.key[s], sym, P)] << 32) | tab.first[s];
-        atomicMax((unsigned long long*)&ctl->pick, (unsigned long long)v);
-    }
-}
-
-__global__ void __launch_bounds__(RT) tie_resolve(RepairCtl* ctl, PairTab tab, const uint64_t* __restrict__ sym,
-                                                  const uint64_t* __restrict__ primes, uint32_t np,
-                                                  uint32_t* __restrict__ bfirst) {
-    CKR_TIE_GUARD();
-    const uint64_t P = bucket_count_of(primes, np, ctl->n_cur);
-    const uint32_t d = ctl->d, best = ctl->best, pf = (uint32_t)ctl->pick;
-    for (uint32_t j = blockIdx.x * RT + threadIdx.x; j < d; j += gridDim.x * RT) {
-        const uint32_t s = tab.touched[j];
-        if (tab.cnt[s] == best && tab.first[s] == pf) ctl->chosen = s;
-        bfirst[bucket_of(tab.key[s], sym, P)] = NONE;
-    }
-}
-
-// Build mode: record the round's rule or stop.  Apply mode: load rule `round`.
-__global__ void round_commit(RepairCtl* ctl, PairTab tab, uint64_t* __restrict__ sym, ckr_repair_rule* rules,
-                             const uint32_t* __restrict__ rmap, int build, uint32_t dlimit) {
-    if (ctl->done) return;
-    const uint32_t r = ctl->round;
-    if (build) {
-        const uint32_t best = ctl->best;
-        if (best > ctl->max_pair) ctl->max_pair = best;
-        if (ctl->n_cur < 2 || best < 2) { ctl->done = 1; return; }
-        const uint64_t key = tab.key[ctl->chosen];
-        const uint32_t a = (uint32_t)(key >> 32), b = (uint32_t)key, c = ctl->a0 + r;
-        const uint64_t rs = (1ull << 63) + r;
-        rules[r].replacement = rs;
-        rules[r].lhs = sym[a];
-        rules[r].rhs = sym[b];
-        rules[r].frequency = best;
-        sym[c] = rs;
-        ctl->a = a; ctl->b = b; ctl->c = c; ctl->skip = 0;
-        // the round's new pairs are (x, c) and (c, x): at most 2 per occurrence
-        // of c and 2 per symbol x (the a0 + r + 1 ids so far), plus (c, c)
-        const uint64_t fresh = 2ull * min((uint64_t)best, (uint64_t)ctl->a0 + r + 1u) + 1u;
-        ctl->recount = 0;
-        ctl->recount_next = ctl->d + fresh > dlimit ? 1u : 0u;
-        // every occurrence of (a, b) is replaced or loses a token to an
-        // overlapping replacement: its count after the round is 0
-        tab.cnt[ctl->chosen] = 0;
-    } else {
-        ctl->a = rmap[3 * r]; ctl->b = rmap[3 * r + 1]; ctl->c = rmap[3 * r + 2];
-        ctl->skip = (ctl->a == NONE || ctl->b == NONE) ? 1u : 0u;
-        sym[ctl->c] = (1ull << 63) + r;
-    }
-}
-
-// ------------------------------------------------------------------ replacement
-// Segment function: for entering state q (1 = the previous token started a
-// replacement, so this one is consumed), the emitted count and leaving state.
-struct SegFn { uint32_t c0, c1, q; };  // q: bit0 = leaving state for q=0, bit1 = for q=1
-
-__device__ __forceinline__ SegFn fn_compose(const SegFn& f, const SegFn& g) {  // f first, then g
-    SegFn h;
-    const uint32_t f0 = f.q & 1, f1 = (f.q >> 1) & 1;
-    h.c0 = f.c0 + (f0 ? g.c1 : g.c0);
-    h.c1 = f.c1 + (f1 ? g.c1 : g.c0);
-    h.q = ((g.q >> f0) & 1) | (((g.q >> f1) & 1) << 1);
-    return h;
-}
-__device__ __forceinline__ SegFn fn_identity() { return SegFn{0, 0, 2}; }
-
-// Thread segment [i0, i0+SEG) ∩ [0, n) of the token sequence.
-struct Seg {
-    uint32_t t[SEG];
-    uint32_t nxt;   // token after the segment
-    uint32_t len;   // tokens inside [0, n)
-    bool has_nxt;
+struct RoundArgs {
+    PairTab tab;
+    uint64_t* sym;
+    ckr_repair_rule* rules;
+    const uint32_t* rmap;
+    const uint64_t* primes;
+    uint32_t n_primes;
+    uint32_t* bfirst;
+    uint32_t rounds;   // rules to build / apply
+    uint32_t dlimit;   // build: recount when the table could pass this many pairs (0: every round)
+    int build;
 };
 
-__device__ __forceinline__ void load_seg(const uint32_t* tok, uint32_t n, uint32_t i0, Seg& s) {
-    s.len = i0 < n ? min<uint32_t>(SEG, n - i0) : 0;
-    if (s.len == SEG) {
-        const uint4* p = reinterpret_cast<const uint4*>(tok + i0);
+// Build: record the round's rule (or stop: best count < 2).  Thread 0 only.
+__device__ void commit_rule(RepairCtl* ctl, const RoundArgs& A) {
+    const uint32_t r = ctl->round;
+    const uint32_t best = ctl->best;
+    if (r >= A.rounds) { ctl->done = 1; return; }  // the last rule is built: no round r is counted
+    if (best > ctl->max_pair) ctl->max_pair = best;
+    if (ctl->n_cur < 2 || best < 2) { ctl->done = 1; return; }
+    const uint64_t key = A.tab.key[ctl->chosen];
+    const uint32_t a = (uint32_t)(key >> 32), b = (uint32_t)key, c = ctl->a0 + r;
+    const uint64_t rs = (1ull << 63) + r;
+    A.rules[r].replacement = rs;
+    A.rules[r].lhs = A.sym[a];
+    A.rules[r].rhs = A.sym[b];
+    A.rules[r].frequency = best;
+    A.sym[c] = rs;
+    ctl->a = a; ctl->b = b; ctl->c = c; ctl->skip = 0; ctl->tie = 0;
+    ctl->run_mode = a == b ? 1u : 0u;
+    // the round's new pairs are (x, c) and (c, x): at most 2 per occurrence
+    // of c and 2 per symbol x (the a0 + r + 1 ids so far), plus (c, c)
+    const uint64_t fresh = 2ull * min((uint64_t)best, (uint64_t)ctl->a0 + r + 1u) + 1u;
+    ctl->recount = 0;
+    ctl->recount_next = (uint64_t)ctl->d + fresh > A.dlimit ? 1u : 0u;
+    A.tab.cnt[ctl->chosen] = 0;
+}
+
+// Apply: load rule `round` (or stop after the last).  Thread 0 only.
+__device__ void load_rule(RepairCtl* ctl, const RoundArgs& A) {
+    const uint32_t r = ctl->round;
+    if (r >= A.rounds) { ctl->done = 1; return; }
+    ctl->a = A.rmap[3 * r]; ctl->b = A.rmap[3 * r + 1]; ctl->c = A.rmap[3 * r + 2];
+    ctl->skip = (ctl->a == NONE || ctl->b == NONE) ? 1u : 0u;
+    ctl->run_mode = ctl->a == ctl->b ? 1u : 0u;
+    A.sym[ctl->c] = (1ull << 63) + r;
+}
+
+// The largest count over the table's used slots, the number of slots holding
+// it and one of them, in one pass: each thread reduces its slots (four loads
+// in flight), then the threads' results are combined by wave shuffles and the
+// waves' through LDS.  Every thread gets the result.
+struct TopCount {
+    uint32_t best, n, slot;
+};
+__device__ __forceinline__ TopCount top_combine(TopCount x, TopCount y) {
+    if (y.best > x.best) return y;
+    if (y.best == x.best) x.n += y.n;
+    return x;
+}
+__device__ TopCount table_top(RepairCtl* ctl, const PairTab& t) {
+    __shared__ TopCount sw[16];
+    const uint32_t d = ld_relaxed32(&ctl->d), bs = blockDim.x;
+    TopCount r{0, 0, 0};
+    uint32_t j = threadIdx.x;
+    for (; j + 3 * bs < d; j += 4 * bs) {
+        uint32_t sl[4], v[4];
 #pragma unroll
-        for (int q = 0; q < SEG / 4; q++) {
-            const uint4 v = p[q];
-            s.t[4 * q] = v.x; s.t[4 * q + 1] = v.y; s.t[4 * q + 2] = v.z; s.t[4 * q + 3] = v.w;
-        }
-    } else {
+        for (int i = 0; i < 4; i++) sl[i] = t.touched[j + i * bs];
 #pragma unroll
-        for (int j = 0; j < SEG; j++) s.t[j] = (uint32_t)j < s.len ? tok[i0 + j] : NONE;
+        for (int i = 0; i < 4; i++) v[i] = ld_relaxed32(&t.cnt[sl[i]]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) r = top_combine(r, TopCount{v[i], 1, sl[i]});
     }
-    s.has_nxt = i0 + SEG < n;
-    s.nxt = s.has_nxt ? tok[i0 + SEG] : NONE;
+    for (; j < d; j += bs) {
+        const uint32_t sl = t.touched[j];
+        r = top_combine(r, TopCount{ld_relaxed32(&t.cnt[sl]), 1, sl});
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        TopCount y;
+        y.best = (uint32_t)__shfl_xor((int)r.best, o);
+        y.n = (uint32_t)__shfl_xor((int)r.n, o);
+        y.slot = (uint32_t)__shfl_xor((int)r.slot, o);
+        r = top_combine(r, y);
+    }
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sw[threadIdx.x >> 6] = r;
+    __syncthreads();
+    TopCount all{0, 0, 0};
+    for (uint32_t w = 0; w < bs / 64; w++) all = top_combine(all, sw[w]);
+    __syncthreads();
+    return all;
 }
 
-// Does position j of the segment start a replacement (given it is not consumed)?
-__device__ __forceinline__ bool starts(const Seg& s, int j, uint32_t a, uint32_t b) {
-    if ((uint32_t)j >= s.len) return false;
-    const bool nx = (j + 1 < SEG) ? ((uint32_t)(j + 1) < s.len) : s.has_nxt;
-    const uint32_t next = (j + 1 < SEG) ? s.t[(j + 1) & (SEG - 1)] : s.nxt;
-    return s.t[j] == a && nx && next == b;
+// Build: the largest count and its holders over the table's used slots; a
+// unique holder (or none worth a rule) commits, several set up the tie-break
+// (their first occurrences are taken by rp_pairs<FIRST>).
+__device__ void select_round(RepairCtl* ctl, const RoundArgs& A) {
+    const TopCount top = table_top(ctl, A.tab);
+    const uint32_t ncand = top.best >= 2 ? top.n : 0u;
+    if (threadIdx.x == 0) {
+        ctl->best = top.best;
+        ctl->ncand = ncand;
+        ctl->chosen = top.slot;
+        if (top.best >= 2 && ncand > 1 && ctl->n_cur >= 2) ctl->tie = 1;  // first[] is NONE outside a tie
+        else commit_rule(ctl, A);
+    }
+    __syncthreads();
 }
 
-__device__ __forceinline__ SegFn seg_fn(const Seg& s, uint32_t a, uint32_t b) {
-    uint32_t q0 = 0, q1 = 1, c0 = 0, c1 = 0;
+// Build, after rp_first: the holder of the top count that std::unordered_map
+// visits first, then the commit.
+__device__ void break_tie(RepairCtl* ctl, const RoundArgs& A) {
+    __shared__ unsigned long long s_pick;
+    __shared__ uint32_t s_chosen;
+    const PairTab& t = A.tab;
+    const uint64_t P = bucket_count_of(A.primes, A.n_primes, ctl->n_cur);
+    const uint32_t d = ctl->d, best = ctl->best;
+    for (uint32_t j = threadIdx.x; j < d; j += blockDim.x) {
+        const uint32_t s = t.touched[j];
+        atomicMin(&A.bfirst[bucket_of(t.key[s], A.sym, P)], ld_relaxed32(&t.first[s]));
+    }
+    if (threadIdx.x == 0) { s_pick = 0; s_chosen = 0; }
+    __threadfence();
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < d; j += blockDim.x) {
+        const uint32_t s = t.touched[j];
+        if (t.cnt[s] != best) continue;
+        const uint64_t v = ((uint64_t)ld_relaxed32(&A.bfirst[bucket_of(t.key[s], A.sym, P)]) << 32) |
+                           ld_relaxed32(&t.first[s]);
+        atomicMax(&s_pick, (unsigned long long)v);
+    }
+    __syncthreads();
+    const uint32_t pf = (uint32_t)s_pick;
+    for (uint32_t j = threadIdx.x; j < d; j += blockDim.x) {
+        const uint32_t s = t.touched[j];
+        if (t.cnt[s] == best && ld_relaxed32(&t.first[s]) == pf) s_chosen = s;
+    }
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < d; j += blockDim.x) {
+        const uint32_t s = t.touched[j];
+        A.bfirst[bucket_of(t.key[s], A.sym, P)] = NONE;
+        t.first[s] = NONE;  // NONE again until the next tie
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        ctl->chosen = s_chosen;
+        commit_rule(ctl, A);
+    }
+    __syncthreads();
+}
+
+// Whether the table's top count (at least 2) is held by several pairs: the
+// selection's question, asked by every workgroup of rp_pairs<FIRST> in a
+// recount round (all get the same answer from the same counts).
+__device__ bool table_tied(RepairCtl* ctl, const PairTab& t) {
+    const TopCount top = table_top(ctl, t);
+    return top.best >= 2 && top.n > 1 && ctl->n_cur >= 2;
+}
+
+// ------------------------------------------------------------------ counting passes
+// COUNT (rounds that recount): every adjacent pair of live tokens; FIRST
+// (tied rounds): the first occurrence of every pair.  Workgroups take
+// contiguous chunks of positions; the last one to finish selects (COUNT) or
+// breaks the tie (FIRST).
+template <typename T, bool FIRST>
+__global__ void __launch_bounds__(RT) rp_pairs(const T* __restrict__ tok, const uint32_t* __restrict__ len,
+                                               uint32_t N, RepairCtl* ctl, RoundArgs A, uint32_t chunk) {
+    if (ctl->done) return;
+    if (FIRST) {
+        // a tie found by the previous round's selection, or, in a recount round,
+        // one the selection after rp_pairs<COUNT> is about to find
+        if (!ctl->tie && !(ctl->recount && table_tied(ctl, A.tab))) return;
+    } else if (!ctl->recount) {
+        return;
+    }
+    __shared__ uint64_t ck[CACHE];
+    __shared__ uint32_t cv[CACHE];
+    cache_init<FIRST>(ck, cv);
+    const uint64_t base = (uint64_t)blockIdx.x * chunk;
+    const uint32_t end = (uint32_t)min<uint64_t>(base + chunk, N);
+    // PAIR_UNROLL positions per thread per step, their tokens loaded before any
+    // pair is entered, so that the loads wait for memory together
+    for (uint32_t i0 = (uint32_t)base + threadIdx.x; i0 < end; i0 += PAIR_UNROLL * RT) {
+        uint32_t l[PAIR_UNROLL], r[PAIR_UNROLL];
+#pragma unroll
+        for (int u = 0; u < PAIR_UNROLL; u++) {
+            const uint32_t i = i0 + u * RT;
+            l[u] = (i < end) ? (uint32_t)tok[i] : (uint32_t)tomb<T>();
+            r[u] = (i + 1 < N && i < end) ? (uint32_t)tok[i + 1] : (uint32_t)tomb<T>();
+        }
+#pragma unroll
+        for (int u = 0; u < PAIR_UNROLL; u++) {
+            const uint32_t i = i0 + u * RT;
+            if (i >= end || l[u] >= tb0<T>() || i + 1 >= N) continue;
+            uint32_t rr = r[u];
+            if (rr >= tb0<T>()) {  // the next head, past i's span
+                const uint32_t j = next_from<T>(len, i, rr, N);
+                if (j >= N) continue;
+                rr = tok[j];
+            }
+            cache_put<FIRST>(ck, cv, A.tab, ctl, pair_key(l[u], rr), FIRST ? i : 1u);
+        }
+    }
+    cache_flush<FIRST>(ck, cv, A.tab, ctl);
+}
+
+// One workgroup after rp_pairs<FIRST>: in a recount round the selection
+// (committing a unique pair), then any tie broken and its pair committed.
+__global__ void __launch_bounds__(CLOSE_T) rp_tie(RepairCtl* ctl, RoundArgs A) {
+    if (ctl->done) return;
+    if (ctl->recount) select_round(ctl, A);
+    if (ctl->done || !ctl->tie) return;
+    break_tie(ctl, A);
+}
+
+// ------------------------------------------------------------------ run parity ((x, x) rounds)
+// State entering a position: 1 if the previous live token started an
+// occurrence (this one is its second).  A segment of positions maps the entering
+// state to the leaving one: bit q of f is the leaving state for entering q
+// (identity 0b10).  Tombstones leave the state as it is.
+__device__ __forceinline__ uint32_t fn_compose(uint32_t f, uint32_t g) {  // f first, then g
+    return ((g >> (f & 1)) & 1) | (((g >> ((f >> 1) & 1)) & 1) << 1);
+}
+constexpr uint32_t FN_ID = 2;
+
+__device__ __forceinline__ uint32_t seg_fn(uint32_t live, uint32_t st) {
+    uint32_t q0 = 0, q1 = 1;
 #pragma unroll
     for (int j = 0; j < SEG; j++) {
-        const bool valid = (uint32_t)j < s.len;
-        const bool st = starts(s, j, a, b);
-        c0 += (valid && !q0) ? 1 : 0;
-        c1 += (valid && !q1) ? 1 : 0;
-        q0 = valid ? ((q0 || !st) ? 0 : 1) : q0;
-        q1 = valid ? ((q1 || !st) ? 0 : 1) : q1;
+        if (!((live >> j) & 1)) continue;
+        const uint32_t s = (st >> j) & 1;
+        q0 = q0 ? 0 : s;
+        q1 = q1 ? 0 : s;
     }
-    return SegFn{c0, c1, q0 | (q1 << 1)};
+    return q0 | (q1 << 1);
 }
 
-// Inclusive scan of segment functions over the block: within each wave by
-// shuffles, then the waves' totals through LDS.  Leaves thread i's inclusive
-// function in sh[i].
-__device__ SegFn block_fn_scan(SegFn f, SegFn* sh) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+// rp_runs, rp_find and rp_write share one partition of the sequence into
+// units, one per wave: unit u takes the contiguous chunks [u K, (u + 1) K) of
+// CHUNK positions (a wave's 64 lanes x SEG), K = ceil(chunks / units).  A wave
+// works through its unit on its own (no workgroup barrier), lane l taking
+// positions [i0, i0 + SEG) of each chunk, i0 = chunk CHUNK + l SEG.
+struct Unit {
+    uint32_t u, c0, c1;  // unit, its chunks [c0, c1)
+};
+__device__ __forceinline__ Unit unit_of(uint32_t N, uint32_t K) {
+    Unit x;
+    x.u = blockIdx.x * (RT / 64) + (threadIdx.x >> 6);
+    const uint32_t nch = (N + CHUNK - 1) / CHUNK;
+    x.c0 = min(nch, x.u * K);
+    x.c1 = min(nch, x.c0 + K);
+    return x;
+}
+
+// The tokens around a lane's positions, token k (k < 32) = tok[i0 - 8 + k],
+// with tombstones for positions outside [0, N) (the array carries 32
+// tombstones past its end), packed as loaded: R words of 32 bits.  i0 is a
+// multiple of SEG, so every load is 16-byte aligned.  sel(k) takes token k
+// by a tree of selects over the words, so that a run-time k needs no indexed
+// register access (which would go to scratch memory); a constant k folds to
+// one word.
+template <typename T>
+struct Win {
+    static constexpr int PER = 16 / sizeof(T);  // tokens per 16-byte load
+    static constexpr int R = 32 * sizeof(T) / 4;
+    uint32_t r[R];
+    __device__ __forceinline__ void load(const T* __restrict__ tok, uint32_t N, uint32_t i0) {
+        const uint4* v = reinterpret_cast<const uint4*>(tok + i0) - 8 / PER;
+#pragma unroll
+        for (int q = 0; q < R / 4; q++) {
+            uint4 x;
+            // before position 0, or a lane wholly past the end: tombstones
+            if ((q < 8 / PER && i0 == 0) || i0 >= N) x = make_uint4(~0u, ~0u, ~0u, ~0u);
+            else x = v[q];
+            r[4 * q] = x.x; r[4 * q + 1] = x.y; r[4 * q + 2] = x.z; r[4 * q + 3] = x.w;
+        }
+    }
+    __device__ __forceinline__ uint32_t word_tok(uint32_t w, uint32_t k) const {
+        return sizeof(T) == 4 ? w : ((w >> (16 * (k & 1))) & 0xFFFFu);
+    }
+    __device__ __forceinline__ uint32_t sel(uint32_t k) const {
+        const uint32_t idx = sizeof(T) == 4 ? k : k >> 1;
+        uint32_t t[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) t[i] = r[i];
+#pragma unroll
+        for (int half = R / 2, bit = 1; half >= 1; half >>= 1, bit <<= 1) {
+#pragma unroll
+            for (int i = 0; i < half; i++) t[i] = (idx & bit) ? t[2 * i + 1] : t[2 * i];
+        }
+        return word_tok(t[0], k);
+    }
+    static constexpr uint32_t TB0 = tb0<T>();  // tokens from here up are tombstones
+};
+
+// Wave-wide inclusive scan of segment functions (lane order); returns this
+// lane's exclusive prefix, *whole the wave's function.
+__device__ __forceinline__ uint32_t wave_fn_scan(uint32_t f, uint32_t* whole) {
+    const int lane = threadIdx.x & 63;
+    uint32_t inc = f;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
-        SegFn g;
-        g.c0 = (uint32_t)__shfl_up((int)f.c0, o);
-        g.c1 = (uint32_t)__shfl_up((int)f.c1, o);
-        g.q = (uint32_t)__shfl_up((int)f.q, o);
-        if (lane >= o) f = fn_compose(g, f);
+        const uint32_t g = (uint32_t)__shfl_up((int)inc, o);
+        if (lane >= o) inc = fn_compose(g, inc);
     }
-    if (lane == 63) sh[w] = f;
-    __syncthreads();
-    SegFn pre = fn_identity();
-    for (int i = 0; i < w; i++) pre = fn_compose(pre, sh[i]);
-    f = fn_compose(pre, f);
-    __syncthreads();
-    sh[threadIdx.x] = f;
-    __syncthreads();
-    return f;
+    *whole = (uint32_t)__shfl((int)inc, 63);
+    const uint32_t ex = (uint32_t)__shfl_up((int)inc, 1);
+    return lane ? ex : FN_ID;
 }
 
-#define CKR_REP_GUARD() if (ctl->done || ctl->skip) return
-
-__global__ void __launch_bounds__(RT) rep_summary(const uint32_t* __restrict__ buf0, const uint32_t* __restrict__ buf1,
-                                                  RepairCtl* ctl, SegFn* __restrict__ bfun) {
-    CKR_REP_GUARD();
-    __shared__ SegFn sh[RT];
-    const uint32_t n = ctl->n_cur;
-    const uint64_t base = (uint64_t)blockIdx.x * BLK;
-    if (base >= n) return;
-    const uint32_t* tok = ctl->cur ? buf1 : buf0;
-    Seg s;
-    load_seg(tok, n, (uint32_t)base + threadIdx.x * SEG, s);
-    const SegFn f = block_fn_scan(seg_fn(s, ctl->a, ctl->b), sh);
-    if (threadIdx.x == RT - 1) bfun[blockIdx.x] = f;
+// Live positions and, for the pair (x, x), the positions that would start an
+// occurrence if not consumed, among the lane's SEG positions (window w).
+template <typename T>
+__device__ __forceinline__ void win_runs(const Win<T>& w, const T* __restrict__ tok, const uint32_t* __restrict__ len,
+                                         uint32_t N, uint32_t i0, uint32_t x, uint32_t* live, uint32_t* st) {
+    uint32_t lv = 0, s = 0;
+    constexpr uint32_t TB0 = Win<T>::TB0;
+#pragma unroll
+    for (int j = 0; j < SEG; j++) {  // unrolled: every sel() index is a constant
+        const uint32_t t = w.sel(8 + j);
+        if (t >= TB0) continue;
+        lv |= 1u << j;
+        if (t != x || i0 + j + 1 >= N) continue;
+        uint32_t nx = w.sel(9 + j);
+        if (nx >= TB0) {
+            const uint32_t q = next_from<T>(len, i0 + j, nx, N);
+            if (q >= N) continue;
+            nx = tok[q];
+        }
+        if (nx == x) s |= 1u << j;
+    }
+    *live = lv;
+    *st = s;
 }
 
-// One workgroup: per-block entering state and output offset.
-__global__ void __launch_bounds__(SCAN_T) rep_scan(RepairCtl* ctl, const SegFn* __restrict__ bfun,
-                                                   uint32_t* __restrict__ boff) {
-    CKR_REP_GUARD();
-    __shared__ SegFn sh[SCAN_T];
-    const uint32_t n = ctl->n_cur;
-    const uint32_t nb = (n + BLK - 1) / BLK;
-    const uint32_t per = (nb + SCAN_T - 1) / SCAN_T;
-    const uint32_t lo = threadIdx.x * per, hi = min(nb, lo + per);
-    SegFn f = fn_identity();
-    for (uint32_t j = lo; j < hi; j++) f = fn_compose(f, bfun[j]);
-    sh[threadIdx.x] = f;
-    __syncthreads();
-    for (int o = 1; o < SCAN_T; o <<= 1) {
-        SegFn g = f;
-        if ((int)threadIdx.x >= o) g = fn_compose(sh[threadIdx.x - o], f);
-        __syncthreads();
-        sh[threadIdx.x] = g;
-        f = g;
-        __syncthreads();
+// (x, x) rounds: each unit's function (the composition of its chunks'), in
+// rstate[u].
+template <typename T>
+__global__ void __launch_bounds__(RT) rp_runs(const T* __restrict__ tok, const uint32_t* __restrict__ len, uint32_t N,
+                                              uint32_t K, RepairCtl* ctl, uint32_t* __restrict__ rstate) {
+    if (ctl->done || ctl->skip || !ctl->run_mode) return;
+    const uint32_t x = ctl->a;
+    const Unit un = unit_of(N, K);
+    const uint32_t lane = threadIdx.x & 63;
+    uint32_t f = FN_ID;
+    Win<T> wn;  // the next chunk's window, loaded while this one is worked on
+    if (un.c0 < un.c1) wn.load(tok, N, un.c0 * CHUNK + lane * SEG);
+    for (uint32_t ch = un.c0; ch < un.c1; ch++) {
+        const uint32_t i0 = ch * CHUNK + lane * SEG;
+        const Win<T> w = wn;
+        if (ch + 1 < un.c1) wn.load(tok, N, i0 + CHUNK);
+        uint32_t live, st, whole;
+        win_runs<T>(w, tok, len, N, i0, x, &live, &st);
+        wave_fn_scan(seg_fn(live, st), &whole);
+        f = fn_compose(f, whole);
     }
-    // exclusive prefix of this thread = inclusive of the previous one
-    SegFn pre = threadIdx.x ? sh[threadIdx.x - 1] : fn_identity();
-    uint32_t q = pre.q & 1, off = pre.c0;  // the sequence starts in state 0
-    for (uint32_t j = lo; j < hi; j++) {
-        boff[j] = off | (q << 31);
-        const SegFn& b = bfun[j];
-        off += q ? b.c1 : b.c0;
-        q = (b.q >> q) & 1;
-    }
-    if (threadIdx.x == SCAN_T - 1) ctl->n_next = f.c0;
+    if (lane == 0) rstate[un.u] = f;
 }
 
-// DEC (build rounds that keep their counts): every pair of the old sequence
-// with a replaced token is subtracted from the table, through an LDS cache.
-template <bool DEC>
-__global__ void __launch_bounds__(RT) rep_apply(uint32_t* __restrict__ buf0, uint32_t* __restrict__ buf1,
-                                                RepairCtl* ctl, const uint32_t* __restrict__ boff, PairTab tab) {
-    CKR_REP_GUARD();
-    __shared__ SegFn sh[RT];
-    __shared__ uint64_t dk[DEC ? DCACHE : 1];
-    __shared__ uint32_t dv[DEC ? DCACHE : 1];
-    const uint32_t n = ctl->n_cur;
-    const uint64_t base = (uint64_t)blockIdx.x * BLK;
-    if (base >= n) return;
-    const bool dec = DEC && !ctl->recount_next;
-    if (dec)
-        for (int j = threadIdx.x; j < DCACHE; j += RT) { dk[j] = EMPTY_KEY; dv[j] = 0; }
-    const uint32_t* tok = ctl->cur ? buf1 : buf0;
-    uint32_t* out = ctl->cur ? buf0 : buf1;
+// ------------------------------------------------------------------ find and replace
+// Every occurrence (p, q) of (a, b) in the unit: (p, q, e) to the unit's part
+// of the list, e the position after q's span (the next live token or N), and
+// (build rounds keeping their counts) the pair count changes around the
+// occurrence (see the file comment), all read from the old sequence.  The
+// neighbours come from the lane's window when they lie in it and are live,
+// else from the span lengths and heads.
+template <typename T, bool BUILD>
+__global__ void __launch_bounds__(RT) rp_find(const T* __restrict__ tok, const uint32_t* __restrict__ len,
+                                              const uint32_t* __restrict__ back, uint32_t N, uint32_t K,
+                                              RepairCtl* ctl, PairTab tab, const uint32_t* __restrict__ rstate,
+                                              uint32_t* __restrict__ ucount, uint32_t* __restrict__ lp,
+                                              uint32_t* __restrict__ lq, uint32_t* __restrict__ le) {
+    if (ctl->done || ctl->skip) return;
+    __shared__ uint64_t ck[CACHE];
+    __shared__ uint32_t cv[CACHE];
+    constexpr uint32_t TB0 = Win<T>::TB0;
     const uint32_t a = ctl->a, b = ctl->b, c = ctl->c;
-    // the block's output goes through LDS (index k at k + k / 32, so that the
-    // threads' runs fall in different banks) and out in coalesced stores
-    __shared__ uint32_t ob[BLK + BLK / 32];
-    const uint32_t i0 = (uint32_t)base + threadIdx.x * SEG;
-    Seg s;
-    load_seg(tok, n, i0, s);
-    const SegFn f = seg_fn(s, a, b);
-    block_fn_scan(f, sh);
-    const SegFn pre = threadIdx.x ? sh[threadIdx.x - 1] : fn_identity();
-    const SegFn whole = sh[RT - 1];
-    const uint32_t bo = boff[blockIdx.x];
-    const uint32_t qb = bo >> 31;
-    uint32_t q = (pre.q >> qb) & 1;
-    uint32_t o = qb ? pre.c1 : pre.c0;  // within the block's output
-    uint32_t cons = 0;                  // bit j: token i0 + j is replaced
-#pragma unroll
-    for (int j = 0; j < SEG; j++) {
-        const bool valid = (uint32_t)j < s.len;
-        const bool st = starts(s, j, a, b);
-        const bool emit = valid && !q;
-        if (valid && (q || st)) cons |= 1u << j;
-        if (emit) ob[o + (o >> 5)] = st ? c : s.t[j];
-        o += emit ? 1 : 0;
-        q = emit && st ? 1 : 0;
+    const bool run = ctl->run_mode != 0;
+    const bool count = BUILD && !ctl->recount_next;  // a recount follows: no count to keep
+    if (count) cache_init<false>(ck, cv);
+    auto upd = [&](uint32_t l, uint32_t r, uint32_t v) { cache_put<false>(ck, cv, tab, ctl, pair_key(l, r), v); };
+    const uint32_t DEC = 0u - 1u;
+    const Unit un = unit_of(N, K);
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t base = (uint64_t)un.u * K * (CHUNK / 2);  // the unit's slots: at most CHUNK / 2 per chunk
+    uint32_t wcount = 0;                                      // slots used (uniform over the wave)
+    uint32_t qw = 0;                                          // state entering the chunk
+    if (run) {
+        // the state entering this wave's unit: the units before it composed
+        // (rp_runs left each unit's function in rstate), the sequence starting
+        // in state 0.  The workgroup composes the units before its first
+        // unit together, in order; each wave then adds the ones before its own.
+        __shared__ uint32_t swf[RT / 64];
+        const uint32_t u0 = blockIdx.x * (RT / 64);
+        const uint32_t per = (u0 + RT - 1) / RT;
+        const uint32_t lo = min(u0, threadIdx.x * per), hi = min(u0, lo + per);
+        uint32_t f = FN_ID;
+        for (uint32_t j = lo; j < hi; j++) f = fn_compose(f, rstate[j]);
+        uint32_t whole;
+        wave_fn_scan(f, &whole);
+        if (lane == 0) swf[threadIdx.x >> 6] = whole;
+        __syncthreads();
+        uint32_t all = FN_ID;
+        for (int i = 0; i < RT / 64; i++) all = fn_compose(all, swf[i]);
+        qw = all & 1;
+        for (uint32_t v = u0; v < un.u; v++) qw = (rstate[v] >> qw) & 1;
     }
-    if (dec) {
-        const uint64_t ab = ((uint64_t)a << 32) | b;
-        // the token after the segment is replaced if token SEG - 1 starts a
-        // replacement or if it starts one itself
-        if (s.has_nxt) {
-            const bool has17 = (uint64_t)i0 + SEG + 1 < n;
-            const bool st16 = !q && has17 && s.nxt == a && tok[i0 + SEG + 1] == b;
-            if (q || st16) cons |= 1u << SEG;
-        }
+    Win<T> wn;  // the next chunk's window, loaded while this one is worked on
+    if (un.c0 < un.c1) wn.load(tok, N, un.c0 * CHUNK + lane * SEG);
+    for (uint32_t ch = un.c0; ch < un.c1; ch++) {
+        const uint32_t i0 = ch * CHUNK + lane * SEG;
+        const Win<T> w = wn;
+        if (ch + 1 < un.c1) wn.load(tok, N, i0 + CHUNK);
+        uint32_t starts = 0;
+        if (run) {
+            uint32_t live, st, whole;
+            win_runs<T>(w, tok, len, N, i0, a, &live, &st);
+            const uint32_t pre = wave_fn_scan(seg_fn(live, st), &whole);
+            uint32_t q = (pre >> qw) & 1;
 #pragma unroll
-        for (int j = 0; j < SEG; j++) {
-            const bool pair = (uint32_t)(j + 1) < s.len || (j == SEG - 1 && s.has_nxt);
-            if (!pair || ((cons >> j) & 3u) == 0) continue;
-            const uint64_t key = ((uint64_t)s.t[j] << 32) | (j + 1 < SEG ? s.t[(j + 1) & (SEG - 1)] : s.nxt);
-            if (key == ab) continue;  // every (a, b) is destroyed: round_commit zeroed its count
-            uint32_t sl = mix64(key) & (DCACHE - 1);
-            bool hit = false;
-            for (int p = 0; p < CACHE_PROBES; p++) {
-                uint64_t cur = dk[sl];
-                if (cur == EMPTY_KEY) {
-                    cur = atomicCAS((unsigned long long*)&dk[sl], (unsigned long long)EMPTY_KEY, (unsigned long long)key);
-                    if (cur == EMPTY_KEY) cur = key;
-                }
-                if (cur == key) { atomicAdd(&dv[sl], 1u); hit = true; break; }
-                sl = (sl + 1) & (DCACHE - 1);
+            for (int j = 0; j < SEG; j++) {
+                if (!((live >> j) & 1)) continue;
+                const uint32_t s0 = q ? 0u : ((st >> j) & 1);
+                starts |= s0 << j;
+                q = s0;
             }
-            if (!hit) tab_add(tab, ctl, key, 0u - 1u);
+            qw = (whole >> qw) & 1;
+        } else {
+#pragma unroll
+            for (int j = 0; j < SEG; j++) {  // unrolled: every sel() index is a constant
+                if (w.sel(8 + j) != a || i0 + j + 1 >= N) continue;
+                uint32_t nx = w.sel(9 + j);
+                if (nx >= TB0) {
+                    const uint32_t q = next_from<T>(len, i0 + j, nx, N);
+                    if (q >= N) continue;
+                    nx = tok[q];
+                }
+                if (nx == b) starts |= 1u << j;
+            }
         }
+        // slots: the wave's exclusive prefix of the lanes' counts
+        const uint32_t nst = __popc(starts);
+        uint32_t inc = nst;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t g = (uint32_t)__shfl_up((int)inc, o);
+            if ((int)lane >= o) inc += g;
+        }
+        const uint32_t total = (uint32_t)__shfl((int)inc, 63);
+        uint64_t k = base + wcount + inc - nst;
+        wcount += total;
+        // each lane through its own occurrences; neighbours from the window
+        // (k - 8 relative to i0) when they lie in it and are live
+        uint32_t m = starts;
+        while (m) {
+            const uint32_t j = __ffs(m) - 1;
+            m &= m - 1;
+            const uint32_t p = i0 + j;
+            // q: the next live position after p (p + 1 < N: p starts an occurrence)
+            const uint32_t q = next_from<T>(len, p, w.sel(9 + j), N);
+            // r: the next live position after q (the end of the merged span)
+            uint32_t r, tr = 0;
+            if (q == p + 1) {
+                const uint32_t w10 = w.sel(10 + j);
+                r = next_from<T>(len, q, w10, N);
+                if (r == p + 2) tr = w10;
+                else if (r < N) tr = tok[r];
+            } else {
+                r = next_live<T>(tok, len, q, N);
+                if (r < N) tr = tok[r];
+            }
+            lp[k] = p; lq[k] = q; le[k] = r;
+            k++;
+            if (!count) continue;
+            // x: the live position before p
+            uint32_t x = NONE, tx = 0;
+            if (p > 0) {
+                const uint32_t w7 = w.sel(7 + j);
+                x = prev_from<T>(back, p, w7);
+                if (x == p - 1) tx = w7;
+                else if (x != NONE) tx = tok[x];
+            }
+            // the token after r (only asked when r holds a)
+            auto after_r = [&]() -> uint32_t {
+                if (r == p + 2) {
+                    const uint32_t w11 = w.sel(11 + j);
+                    const uint32_t nr = next_from<T>(len, r, w11, N);
+                    return nr == r + 1 ? w11 : nr < N ? (uint32_t)tok[nr] : NONE;
+                }
+                const uint32_t nr = next_live<T>(tok, len, r, N);
+                return nr < N ? (uint32_t)tok[nr] : NONE;
+            };
+            if (run) {
+                if (x != NONE) {
+                    if (tx == a) upd(c, c, 1u);
+                    else { upd(tx, a, DEC); upd(tx, c, 1u); }
+                }
+                if (r < N) {
+                    if (tr == a) {
+                        if (after_r() != a) upd(c, a, 1u);
+                    } else {
+                        upd(a, tr, DEC);
+                        upd(c, tr, 1u);
+                    }
+                }
+            } else {
+                if (x != NONE) {
+                    bool second = false;
+                    if (tx == b) {
+                        uint32_t txx = NONE;
+                        if (x == p - 1) {
+                            const uint32_t w6 = w.sel(6 + j);
+                            const uint32_t xx = prev_from<T>(back, x, w6);
+                            if (xx == x - 1) txx = w6;
+                            else if (xx != NONE) txx = tok[xx];
+                        } else {
+                            const uint32_t xx = prev_live<T>(tok, back, x);
+                            if (xx != NONE) txx = tok[xx];
+                        }
+                        second = txx == a;
+                    }
+                    if (second) { upd(b, a, DEC); upd(c, c, 1u); }
+                    else { upd(tx, a, DEC); upd(tx, c, 1u); }
+                }
+                if (r < N && !(tr == a && after_r() == b)) { upd(b, tr, DEC); upd(c, tr, 1u); }
+            }
+        }
+    }
+    if (lane == 0) ucount[un.u] = wcount;
+    if (count) cache_flush<false>(ck, cv, tab, ctl);
+}
+
+// The round's occurrences replaced in place (no two share a position): each
+// wave writes its unit's, whose positions lie in the unit's chunks.
+template <typename T>
+__global__ void __launch_bounds__(RT) rp_write(T* __restrict__ tok, uint32_t* __restrict__ len,
+                                               uint32_t* __restrict__ back, uint32_t N, uint32_t K, RepairCtl* ctl,
+                                               const uint32_t* __restrict__ ucount, const uint32_t* __restrict__ lp,
+                                               const uint32_t* __restrict__ lq, const uint32_t* __restrict__ le) {
+    if (ctl->done || ctl->skip) return;
+    const T c = (T)ctl->c;
+    const Unit un = unit_of(N, K);
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t base = (uint64_t)un.u * K * (CHUNK / 2);
+    const uint32_t m = ucount[un.u];
+    for (uint32_t k = lane; k < m; k += 64) {
+        const uint32_t p = lp[base + k], q = lq[base + k], e = le[base + k];
+        if (p >= q || q >= e || e > N) continue;  // (never: p < q < e <= N)
+        // the merged span [p, e): its first and last tombstones carry its
+        // length, q (when it is neither) becomes a plain tombstone
+        const uint32_t L = e - p, sl = min(L - 1, lmax<T>());
+        const T ts = (T)(tb0<T>() + sl);
+        tok[p] = c;
+        tok[p + 1] = ts;
+        if (q != p + 1 && q != e - 1) tok[q] = ts;
+        tok[e - 1] = ts;
+        if (sl == lmax<T>()) { len[p] = L; back[e - 1] = p; }
+    }
+}
+
+// One workgroup: the round closed (live count, round number, the table
+// emptied before a recount), then the next round's pair selected from the kept
+// counts (build; committed when no tie needs rp_first) or loaded (apply).
+__global__ void __launch_bounds__(CLOSE_T) rp_close(uint32_t nb, RepairCtl* ctl, const uint32_t* __restrict__ bcount,
+                                                    RoundArgs A) {
+    if (ctl->done) return;
+    __shared__ uint32_t sh[16];
+    __shared__ uint32_t s_recount;
+    uint32_t occ = 0;
+    if (!ctl->skip) {
+        uint32_t j = threadIdx.x;
+        for (; j + 3 * CLOSE_T < nb; j += 4 * CLOSE_T)
+            occ += bcount[j] + bcount[j + CLOSE_T] + bcount[j + 2 * CLOSE_T] + bcount[j + 3 * CLOSE_T];
+        for (; j < nb; j += CLOSE_T) occ += bcount[j];
+    }
+    uint32_t total;
+    block_excl_scan(occ, sh, &total);
+    if (threadIdx.x == 0) {
+        ctl->n_cur -= total;
+        ctl->round++;
+        ctl->best = 0; ctl->ncand = 0; ctl->pick = 0; ctl->skip = 0; ctl->tie = 0; ctl->run_mode = 0;
+        ctl->recount = A.build ? ctl->recount_next : 0u;
+        ctl->recount_next = 0;
+        s_recount = ctl->recount;
     }
     __syncthreads();
-    const uint32_t total = qb ? whole.c1 : whole.c0;
-    uint32_t* ob_out = out + (bo & 0x7FFFFFFFu);
-    for (uint32_t k = threadIdx.x; k < total; k += RT) ob_out[k] = ob[k + (k >> 5)];
-    if (dec)
-        for (int j = threadIdx.x; j < DCACHE; j += RT)
-            if (dk[j] != EMPTY_KEY) tab_add(tab, ctl, dk[j], 0u - dv[j]);
-}
-
-__global__ void __launch_bounds__(RT) tab_clear(RepairCtl* ctl, PairTab tab) {
-    if (ctl->done || !ctl->recount_next) return;
-    const uint32_t d = ctl->d;
-    for (uint32_t j = blockIdx.x * RT + threadIdx.x; j < d; j += gridDim.x * RT) {
-        const uint32_t s = tab.touched[j];
-        tab.key[s] = EMPTY_KEY; tab.cnt[s] = 0; tab.first[s] = NONE;
+    if (A.build) {
+        if (s_recount) {  // rp_pairs fills the table again
+            const uint32_t d = ctl->d;
+            for (uint32_t j = threadIdx.x; j < d; j += blockDim.x) {
+                const uint32_t s = A.tab.touched[j];
+                A.tab.key[s] = EMPTY_KEY; A.tab.cnt[s] = 0; A.tab.first[s] = NONE;
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) ctl->d = 0;
+        } else {
+            select_round(ctl, A);
+        }
+    } else if (threadIdx.x == 0) {
+        load_rule(ctl, A);
     }
 }
 
-__global__ void round_end(RepairCtl* ctl) {
-    if (ctl->done) return;
-    if (!ctl->skip) { ctl->n_cur = ctl->n_next; ctl->cur ^= 1u; }
-    ctl->round++;
-    ctl->best = 0; ctl->ncand = 0; ctl->pick = 0; ctl->skip = 0;
-    if (ctl->recount_next) ctl->d = 0;  // tab_clear has emptied the table
-    ctl->recount = ctl->recount_next;
-    ctl->recount_next = 0;
+// Apply mode, before the first round: rule 0.
+__global__ void rp_load_first(RepairCtl* ctl, RoundArgs A) { load_rule(ctl, A); }
+
+// ------------------------------------------------------------------ output
+// The live tokens as reference symbols, in order: per block of BLK positions
+// the live count, one scan, then the writes.
+template <typename T>
+__global__ void __launch_bounds__(RT) seq_count(const T* __restrict__ tok, uint32_t N, uint32_t* __restrict__ bcount) {
+    __shared__ uint32_t sh[16];
+    const uint32_t i0 = blockIdx.x * BLK + threadIdx.x * SEG;
+    uint32_t c = 0;
+    for (int j = 0; j < SEG; j++) c += (i0 + j < N && tok[i0 + j] < tb0<T>()) ? 1u : 0u;
+    uint32_t tot;
+    block_excl_scan(c, sh, &tot);
+    if (threadIdx.x == 0) bcount[blockIdx.x] = tot;
 }
 
-__global__ void __launch_bounds__(RT) seq_out_kernel(const uint32_t* __restrict__ buf0, const uint32_t* __restrict__ buf1,
-                                                     const RepairCtl* ctl, const uint64_t* __restrict__ sym,
-                                                     uint64_t* __restrict__ out) {
-    const uint32_t n = ctl->n_cur;
-    const uint32_t* tok = ctl->cur ? buf1 : buf0;
-    for (uint32_t i = blockIdx.x * RT + threadIdx.x; i < n; i += gridDim.x * RT) {
-        const uint32_t t = tok[i];
-        out[i] = t == NONE ? EMPTY_KEY : sym[t];
+template <typename T>
+__global__ void __launch_bounds__(RT) seq_write(const T* __restrict__ tok, uint32_t N,
+                                                const uint32_t* __restrict__ bbase, const uint64_t* __restrict__ sym,
+                                                uint64_t* __restrict__ out) {
+    __shared__ uint32_t sh[16];
+    const uint32_t i0 = blockIdx.x * BLK + threadIdx.x * SEG;
+    uint32_t c = 0;
+    for (int j = 0; j < SEG; j++) c += (i0 + j < N && tok[i0 + j] < tb0<T>()) ? 1u : 0u;
+    uint32_t tot;
+    uint32_t o = bbase[blockIdx.x] + block_excl_scan(c, sh, &tot);
+    for (int j = 0; j < SEG; j++) {
+        if (i0 + j >= N) break;
+        const T t = tok[i0 + j];
+        if (t < tb0<T>()) out[o++] = sym[t];
     }
 }
 
@@ -775,11 +1137,29 @@ hipError_t fill(T* p, uint64_t n, T v, hipStream_t s) {
 }  // namespace
 
 // ------------------------------------------------------------------ host side
+namespace {
+// The units of rp_runs / rp_find / rp_write: at most FIND_GRID workgroups of
+// four waves, each unit K chunks.
+struct FindGeom {
+    uint32_t nch, G, U, K;
+};
+FindGeom find_geom(uint64_t n) {
+    FindGeom g;
+    g.nch = (uint32_t)std::max<uint64_t>(1, (n + CHUNK - 1) / CHUNK);
+    g.G = std::min<uint32_t>(FIND_GRID, (g.nch + 3) / 4);
+    g.U = 4 * g.G;
+    g.K = (g.nch + g.U - 1) / g.U;
+    return g;
+}
+}  // namespace
+
 RepairLayout repair_layout(uint64_t n, int es, uint32_t k, uint32_t max_rules, uint64_t n_buckets) {
     RepairLayout L{};
     const uint32_t w = 8u * (uint32_t)es - k;
     L.w = w;
     L.direct = w <= 16;
+    // ids 0 .. alphabet + rules - 1, and the tombstone (all ones)
+    L.tok16 = L.direct && (1ull << w) + max_rules <= kRepairTomb16;
     const uint64_t nv = L.direct ? (1ull << w) : 0;
     const uint64_t amax = std::min<uint64_t>(n, 1ull << std::min<uint32_t>(w, 40)) + max_rules;
     uint64_t pairs = n > 1 ? n - 1 : 1;
@@ -793,37 +1173,45 @@ RepairLayout repair_layout(uint64_t n, int es, uint32_t k, uint32_t max_rules, u
     L.n_buckets = std::max<uint64_t>(n_buckets, 1);
     const uint64_t nblk = (n + BLK - 1) / BLK + 1;
     const uint64_t nocc = vcap ? (vcap + OCC_BLK - 1) / OCC_BLK : 0;
+    const uint64_t nn = std::max<uint64_t>(n, 1);
     uint64_t off = 0;
     auto take = [&](uint64_t bytes) { const uint64_t o = off; off += (bytes + 255) / 256 * 256; return o; };
     L.o_ctl = take(sizeof(RepairCtl));
-    L.o_buf0 = take(4 * std::max<uint64_t>(n, 1));
-    L.o_buf1 = take(4 * std::max<uint64_t>(n, 1));
+    L.o_tok = take((L.tok16 ? 2 : 4) * nn + 128);  // 32 tombstones past the end
+    L.o_len = take(4 * nn);
+    L.o_back = take(4 * nn);
+    const FindGeom fg = find_geom(n);
+    L.list_entries = (uint64_t)fg.U * fg.K * (CHUNK / 2);
+    L.o_list = take(12 * L.list_entries);  // p, q and e of each occurrence
+    L.o_bcount = take(4 * fg.U);
     L.o_sym = take(8 * amax);
     L.o_bitmap = take(L.direct ? 2048 * 4 : 0);
     L.o_rank = take(4 * nv);
     L.o_vkey = take(8 * vcap);
     L.o_vrank = take(4 * vcap);
-    L.o_occ = take(4 * (nocc + 1));
+    L.o_occ = take(4 * (std::max<uint64_t>(nocc, nblk) + 1));
     L.o_pkey = take(8 * cap);
     L.o_pcnt = take(4 * cap);
     L.o_pfirst = take(4 * cap);
     L.o_touched = take(4 * cap);
     L.o_bfirst = take(4 * L.n_buckets);
     L.o_primes = take(8 * kRepairMaxPrimes);
-    L.o_bfun = take(sizeof(SegFn) * nblk);
-    L.o_boff = take(4 * nblk);
+    L.o_bfun = take(4 * (uint64_t)fg.U);
     L.o_rules = take(sizeof(ckr_repair_rule) * std::max<uint32_t>(max_rules, 1));
     L.o_rmap = take(12 * std::max<uint32_t>(max_rules, 1));
     L.bytes = off;
     return L;
 }
 
-// Alphabet and token sequence into buf0; returns the launch status.
-static hipError_t build_alphabet(const uint8_t* words, uint64_t n, int es, uint32_t k, const RepairLayout& L,
-                                 uint8_t* ws, hipStream_t s) {
+namespace {
+
+// Alphabet and token sequence; returns the launch status.
+template <typename T>
+hipError_t build_alphabet(const uint8_t* words, uint64_t n, int es, uint32_t k, const RepairLayout& L, uint8_t* ws,
+                          hipStream_t s) {
     auto P = [&](uint64_t o) { return ws + o; };
     RepairCtl* ctl = reinterpret_cast<RepairCtl*>(P(L.o_ctl));
-    uint32_t* tok = reinterpret_cast<uint32_t*>(P(L.o_buf0));
+    T* tok = reinterpret_cast<T*>(P(L.o_tok));
     uint64_t* sym = reinterpret_cast<uint64_t*>(P(L.o_sym));
     const uint32_t g = grid_for(n, 2048);
     if (L.direct) {
@@ -836,102 +1224,193 @@ static hipError_t build_alphabet(const uint8_t* words, uint64_t n, int es, uint3
         CKR_LAUNCH("repair_alpha_kernel", s, alpha_rank_direct<<<1, SCAN_T, 0, s>>>(bitmap, L.w, k, rank, sym, ctl));
         const uint32_t nv = 1u << L.w;
         const size_t lds = nv <= 16384 ? nv * 4 : 0;
-        if (es == 2) CKR_LAUNCH("repair_alpha_kernel", s, alpha_map_direct<2><<<g, RT, lds, s>>>(words, n, k, rank, nv, tok));
-        else CKR_LAUNCH("repair_alpha_kernel", s, alpha_map_direct<4><<<g, RT, lds, s>>>(words, n, k, rank, nv, tok));
+        if (es == 2) CKR_LAUNCH("repair_alpha_kernel", s, (alpha_map_direct<2, T><<<g, RT, lds, s>>>(words, n, k, rank, nv, tok)));
+        else CKR_LAUNCH("repair_alpha_kernel", s, (alpha_map_direct<4, T><<<g, RT, lds, s>>>(words, n, k, rank, nv, tok)));
     } else {
-        uint64_t* vkey = reinterpret_cast<uint64_t*>(P(L.o_vkey));
-        uint32_t* vrank = reinterpret_cast<uint32_t*>(P(L.o_vrank));
-        uint32_t* occ = reinterpret_cast<uint32_t*>(P(L.o_occ));
-        hipError_t e = fill<uint64_t>(vkey, L.vcap, EMPTY_KEY, s);
-        if (e != hipSuccess) return e;
-        const uint32_t nocc = (uint32_t)((L.vcap + OCC_BLK - 1) / OCC_BLK);
-        CKR_LAUNCH("repair_alpha_kernel", s, alpha_insert_hash<4><<<g, RT, 0, s>>>(words, n, k, vkey, L.vcap - 1, ctl));
-        CKR_LAUNCH("repair_alpha_kernel", s, occ_count<<<nocc, RT, 0, s>>>(vkey, L.vcap, occ));
-        CKR_LAUNCH("repair_alpha_kernel", s, scan_single<<<1, SCAN_T, 0, s>>>(occ, nocc, &ctl->a0));
-        CKR_LAUNCH("repair_alpha_kernel", s, occ_rank<<<nocc, RT, 0, s>>>(vkey, L.vcap, occ, k, vrank, sym));
-        CKR_LAUNCH("repair_alpha_kernel", s, alpha_map_hash<4><<<g, RT, 0, s>>>(words, n, k, vkey, L.vcap - 1, vrank, tok));
+        if constexpr (sizeof(T) == 4) {
+            uint64_t* vkey = reinterpret_cast<uint64_t*>(P(L.o_vkey));
+            uint32_t* vrank = reinterpret_cast<uint32_t*>(P(L.o_vrank));
+            uint32_t* occ = reinterpret_cast<uint32_t*>(P(L.o_occ));
+            hipError_t e = fill<uint64_t>(vkey, L.vcap, EMPTY_KEY, s);
+            if (e != hipSuccess) return e;
+            const uint32_t nocc = (uint32_t)((L.vcap + OCC_BLK - 1) / OCC_BLK);
+            CKR_LAUNCH("repair_alpha_kernel", s, alpha_insert_hash<4><<<g, RT, 0, s>>>(words, n, k, vkey, L.vcap - 1, ctl));
+            CKR_LAUNCH("repair_alpha_kernel", s, occ_count<<<nocc, RT, 0, s>>>(vkey, L.vcap, occ));
+            CKR_LAUNCH("repair_alpha_kernel", s, scan_single<<<1, SCAN_T, 0, s>>>(occ, nocc, &ctl->a0));
+            CKR_LAUNCH("repair_alpha_kernel", s, occ_rank<<<nocc, RT, 0, s>>>(vkey, L.vcap, occ, k, vrank, sym));
+            CKR_LAUNCH("repair_alpha_kernel", s,
+                       alpha_map_hash<4><<<g, RT, 0, s>>>(words, n, k, vkey, L.vcap - 1, vrank, tok, ctl));
+        } else {
+            return hipErrorInvalidValue;  // hash mode always takes 32-bit ids
+        }
     }
     return hipGetLastError();
 }
 
-hipError_t repair_launch(const RepairArgs& A, hipStream_t s) {
+constexpr uint32_t kRoundBatch = 8;
+
+// The captured graphs of kRoundBatch rounds, keyed by what their kernels'
+// arguments derive from (the workspace and its layout's inputs).  A graph is
+// captured on a library stream, instantiated once and kept; at most
+// kMaxRoundGraphs are kept (the oldest goes).
+struct RoundGraphKey {
+    const void* ws;
+    uint64_t n;
+    int es, build, device, tok16;
+    uint32_t k, rounds, dlimit;
+    bool operator==(const RoundGraphKey& o) const {
+        return ws == o.ws && n == o.n && es == o.es && build == o.build && device == o.device && tok16 == o.tok16 &&
+               k == o.k && rounds == o.rounds && dlimit == o.dlimit;
+    }
+};
+struct RoundGraph {
+    RoundGraphKey key;
+    hipGraph_t g;
+    hipGraphExec_t x;
+};
+constexpr size_t kMaxRoundGraphs = 64;
+std::mutex g_rg_mu;
+std::vector<RoundGraph> g_rgs;
+
+template <typename RoundFn>
+hipGraphExec_t round_graph(const RepairArgs& A, const RepairLayout& L, RoundFn& round) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) { (void)hipGetLastError(); return nullptr; }
+    const RoundGraphKey key{A.ws, A.n, A.es, A.build, dev, L.tok16 ? 1 : 0, A.k, A.build ? A.max_rules : A.n_rules,
+                            A.recount_each_round ? 1u : 0u};
+    std::lock_guard<std::mutex> lk(g_rg_mu);
+    for (const RoundGraph& r : g_rgs)
+        if (r.key == key) return r.x;
+    static std::vector<hipStream_t> cap;  // one capture stream per device
+    if ((int)cap.size() <= dev) cap.resize(dev + 1, nullptr);
+    if (!cap[dev] && hipStreamCreateWithFlags(&cap[dev], hipStreamNonBlocking) != hipSuccess) {
+        (void)hipGetLastError();
+        cap[dev] = nullptr;
+        return nullptr;
+    }
+    hipStream_t cs = cap[dev];
+    hipGraph_t g = nullptr;
+    hipGraphExec_t x = nullptr;
+    if (hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal) != hipSuccess) { (void)hipGetLastError(); return nullptr; }
+    hipError_t e = hipSuccess;
+    for (uint32_t i = 0; i < kRoundBatch && e == hipSuccess; i++) e = round(cs);
+    const hipError_t e2 = hipStreamEndCapture(cs, &g);
+    if (e != hipSuccess || e2 != hipSuccess || !g || hipGraphInstantiate(&x, g, nullptr, nullptr, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        if (g) (void)hipGraphDestroy(g);
+        return nullptr;  // the rounds are then launched one by one
+    }
+    if (g_rgs.size() >= kMaxRoundGraphs) {
+        (void)hipDeviceSynchronize();  // the oldest graph may still run somewhere
+        (void)hipGraphExecDestroy(g_rgs.front().x);
+        (void)hipGraphDestroy(g_rgs.front().g);
+        g_rgs.erase(g_rgs.begin());
+    }
+    g_rgs.push_back({key, g, x});
+    return x;
+}
+
+template <typename T>
+hipError_t run_rounds(const RepairArgs& A, hipStream_t s) {
     const RepairLayout& L = A.layout;
     uint8_t* ws = A.ws;
     auto P = [&](uint64_t o) { return ws + o; };
     RepairCtl* ctl = reinterpret_cast<RepairCtl*>(P(L.o_ctl));
-    uint32_t* buf0 = reinterpret_cast<uint32_t*>(P(L.o_buf0));
-    uint32_t* buf1 = reinterpret_cast<uint32_t*>(P(L.o_buf1));
+    T* tok = reinterpret_cast<T*>(P(L.o_tok));
+    uint32_t* len = reinterpret_cast<uint32_t*>(P(L.o_len));
+    uint32_t* back = reinterpret_cast<uint32_t*>(P(L.o_back));
     uint64_t* sym = reinterpret_cast<uint64_t*>(P(L.o_sym));
-    PairTab tab{reinterpret_cast<uint64_t*>(P(L.o_pkey)), reinterpret_cast<uint32_t*>(P(L.o_pcnt)),
-                reinterpret_cast<uint32_t*>(P(L.o_pfirst)), reinterpret_cast<uint32_t*>(P(L.o_touched)),
-                L.pair_cap - 1};
-    uint32_t* bfirst = reinterpret_cast<uint32_t*>(P(L.o_bfirst));
-    uint64_t* primes = reinterpret_cast<uint64_t*>(P(L.o_primes));
-    SegFn* bfun = reinterpret_cast<SegFn*>(P(L.o_bfun));
-    uint32_t* boff = reinterpret_cast<uint32_t*>(P(L.o_boff));
-    ckr_repair_rule* rules = reinterpret_cast<ckr_repair_rule*>(P(L.o_rules));
-    uint32_t* rmap = reinterpret_cast<uint32_t*>(P(L.o_rmap));
+    uint32_t* bfun = reinterpret_cast<uint32_t*>(P(L.o_bfun));
+    RoundArgs R{};
+    R.tab = PairTab{reinterpret_cast<uint64_t*>(P(L.o_pkey)), reinterpret_cast<uint32_t*>(P(L.o_pcnt)),
+                    reinterpret_cast<uint32_t*>(P(L.o_pfirst)), reinterpret_cast<uint32_t*>(P(L.o_touched)),
+                    L.pair_cap - 1};
+    R.sym = sym;
+    R.rules = reinterpret_cast<ckr_repair_rule*>(P(L.o_rules));
+    R.rmap = reinterpret_cast<const uint32_t*>(P(L.o_rmap));
+    R.primes = reinterpret_cast<const uint64_t*>(P(L.o_primes));
+    R.n_primes = A.n_primes;
+    R.bfirst = reinterpret_cast<uint32_t*>(P(L.o_bfirst));
+    R.build = A.build;
+    R.rounds = A.build ? A.max_rules : A.n_rules;
+    // rounds keep their counts while the table stays at most 3/4 full (limit 0:
+    // every round recounts)
+    R.dlimit = A.recount_each_round ? 0u : (uint32_t)std::min<uint64_t>(L.pair_cap - L.pair_cap / 4, 0xFFFFFFFFull);
     hipError_t e;
 
     CKR_LAUNCH("repair_init_kernel", s, ctl_init<<<1, 1, 0, s>>>(ctl, (uint32_t)A.n));
-    if ((e = build_alphabet(A.words, A.n, A.es, A.k, L, ws, s)) != hipSuccess) return e;
+    if ((e = build_alphabet<T>(A.words, A.n, A.es, A.k, L, ws, s)) != hipSuccess) return e;
+    // 32 tombstones past the end: the windows of the last positions read them
+    if ((e = fill<T>(tok + A.n, 32, tomb<T>(), s)) != hipSuccess) return e;
 
-    const uint32_t n32 = (uint32_t)A.n;
-    // pair_pass: a few workgroups per CU, each over a contiguous chunk, so that
-    // the pairs every chunk shares (the frequent ones) are added to the global
-    // table once per chunk, not once per 8192 pairs
+    const uint32_t N = (uint32_t)A.n;
     int dev = 0, ncu = 0;
     if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
     if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
-    const uint64_t pblocks = (uint64_t)std::max(ncu, 1) * PAIR_BLOCKS_PER_CU;
+    // counting passes: a few workgroups per CU, each over a contiguous chunk, so
+    // that the pairs every chunk shares (the frequent ones) reach the global
+    // table once per chunk
+    const uint64_t pblocks = (uint64_t)std::max(ncu, 1);  // (runs only in recount and tie rounds; exits cheaply)
     const uint32_t pchunk = (uint32_t)std::max<uint64_t>(PAIR_CHUNK, ((A.n + pblocks - 1) / pblocks + 255) & ~255ull);
     const uint32_t gpair = (uint32_t)std::max<uint64_t>(1, (A.n + pchunk - 1) / pchunk);
-    // rounds keep their counts while the table stays at most 3/4 full (limit 0:
-    // every round recounts)
-    const uint32_t dlimit =
-        A.recount_each_round ? 0u : (uint32_t)std::min<uint64_t>(L.pair_cap - L.pair_cap / 4, 0xFFFFFFFFull);
-    const uint32_t grep = (uint32_t)std::max<uint64_t>(1, (A.n + BLK - 1) / BLK);
-    const uint32_t gsel = 512;
+    const uint32_t nblk = (uint32_t)((A.n + BLK - 1) / BLK);
+    const FindGeom fg = find_geom(A.n);
+    uint32_t* bcount = reinterpret_cast<uint32_t*>(P(L.o_bcount));
+    uint32_t* lp = reinterpret_cast<uint32_t*>(P(L.o_list));
+    uint32_t* lq = lp + L.list_entries;
+    uint32_t* le = lq + L.list_entries;
     if (A.build) {
-        if ((e = fill<uint64_t>(tab.key, L.pair_cap, EMPTY_KEY, s)) != hipSuccess) return e;
-        if ((e = fill<uint32_t>(tab.cnt, L.pair_cap, 0u, s)) != hipSuccess) return e;
-        if ((e = fill<uint32_t>(tab.first, L.pair_cap, NONE, s)) != hipSuccess) return e;
-        if ((e = fill<uint32_t>(bfirst, L.n_buckets, NONE, s)) != hipSuccess) return e;
-        e = hipMemcpyAsync(primes, A.h_primes, 8 * A.n_primes, hipMemcpyHostToDevice, s);
+        if ((e = fill<uint64_t>(R.tab.key, L.pair_cap, EMPTY_KEY, s)) != hipSuccess) return e;
+        if ((e = fill<uint32_t>(R.tab.cnt, L.pair_cap, 0u, s)) != hipSuccess) return e;
+        if ((e = fill<uint32_t>(R.tab.first, L.pair_cap, NONE, s)) != hipSuccess) return e;
+        if ((e = fill<uint32_t>(R.bfirst, L.n_buckets, NONE, s)) != hipSuccess) return e;
+        e = hipMemcpyAsync(const_cast<uint64_t*>(R.primes), A.h_primes, 8 * A.n_primes, hipMemcpyHostToDevice, s);
         if (e != hipSuccess) return e;
-    } else if (A.n_rules) {
-        e = hipMemcpyAsync(rules, A.h_rules, sizeof(ckr_repair_rule) * A.n_rules, hipMemcpyHostToDevice, s);
+    } else {
+        e = hipMemcpyAsync(R.rules, A.h_rules, sizeof(ckr_repair_rule) * A.n_rules, hipMemcpyHostToDevice, s);
         if (e != hipSuccess) return e;
         const uint32_t* rank = L.direct ? reinterpret_cast<const uint32_t*>(P(L.o_rank)) : nullptr;
         CKR_LAUNCH("repair_commit_kernel", s,
                    map_rules_kernel<<<(A.n_rules + 63) / 64, 64, 0, s>>>(
-                       rules, A.n_rules, A.k, L.w, rank, reinterpret_cast<const uint64_t*>(P(L.o_vkey)),
-                       L.vcap ? L.vcap - 1 : 0, reinterpret_cast<const uint32_t*>(P(L.o_vrank)), ctl, rmap));
+                       R.rules, A.n_rules, A.k, L.w, rank, reinterpret_cast<const uint64_t*>(P(L.o_vkey)),
+                       L.vcap ? L.vcap - 1 : 0, reinterpret_cast<const uint32_t*>(P(L.o_vrank)), ctl,
+                       const_cast<uint32_t*>(R.rmap)));
+        CKR_LAUNCH("repair_commit_kernel", s, rp_load_first<<<1, 1, 0, s>>>(ctl, R));
     }
-    const uint32_t rounds = A.build ? A.max_rules : A.n_rules;
-    for (uint32_t r = 0; r < rounds; r++) {
+    // one round: every kernel reads what to do from ctl, so the rounds are
+    // identical launches
+    auto round = [&](hipStream_t x) -> hipError_t {
         if (A.build) {
-            CKR_LAUNCH("repair_pair_kernel", s, pair_pass<COUNT><<<gpair, RT, 0, s>>>(buf0, buf1, ctl, tab, pchunk));
-            CKR_LAUNCH("repair_select_kernel", s, sel_max<<<gsel, RT, 0, s>>>(ctl, tab));
-            CKR_LAUNCH("repair_select_kernel", s, sel_cand<<<gsel, RT, 0, s>>>(ctl, tab));
-            CKR_LAUNCH("repair_tie_kernel", s, first_reset<<<gsel, RT, 0, s>>>(ctl, tab));
-            CKR_LAUNCH("repair_tie_kernel", s, pair_pass<FIRST_OCC><<<gpair, RT, 0, s>>>(buf0, buf1, ctl, tab, pchunk));
-            CKR_LAUNCH("repair_tie_kernel", s, tie_bucket<<<gsel, RT, 0, s>>>(ctl, tab, sym, primes, A.n_primes, bfirst));
-            CKR_LAUNCH("repair_tie_kernel", s, tie_pick<<<gsel, RT, 0, s>>>(ctl, tab, sym, primes, A.n_primes, bfirst));
-            CKR_LAUNCH("repair_tie_kernel", s, tie_resolve<<<gsel, RT, 0, s>>>(ctl, tab, sym, primes, A.n_primes, bfirst));
+            CKR_LAUNCH("repair_count_kernel", x, (rp_pairs<T, false><<<gpair, RT, 0, x>>>(tok, len, N, ctl, R, pchunk)));
+            CKR_LAUNCH("repair_first_kernel", x, (rp_pairs<T, true><<<gpair, RT, 0, x>>>(tok, len, N, ctl, R, pchunk)));
+            CKR_LAUNCH("repair_select_kernel", x, rp_tie<<<1, CLOSE_T, 0, x>>>(ctl, R));
         }
-        CKR_LAUNCH("repair_commit_kernel", s,
-                   round_commit<<<1, 1, 0, s>>>(ctl, tab, sym, rules, rmap, A.build, dlimit));
-        CKR_LAUNCH("repair_replace_kernel", s, rep_summary<<<grep, RT, 0, s>>>(buf0, buf1, ctl, bfun));
-        CKR_LAUNCH("repair_replace_kernel", s, rep_scan<<<1, SCAN_T, 0, s>>>(ctl, bfun, boff));
-        if (A.build) CKR_LAUNCH("repair_replace_kernel", s, rep_apply<true><<<grep, RT, 0, s>>>(buf0, buf1, ctl, boff, tab));
-        else CKR_LAUNCH("repair_replace_kernel", s, rep_apply<false><<<grep, RT, 0, s>>>(buf0, buf1, ctl, boff, tab));
-        if (A.build) CKR_LAUNCH("repair_select_kernel", s, tab_clear<<<gsel, RT, 0, s>>>(ctl, tab));
-        CKR_LAUNCH("repair_commit_kernel", s, round_end<<<1, 1, 0, s>>>(ctl));
-        if (A.build) CKR_LAUNCH("repair_pair_kernel", s, pair_pass<INC><<<gpair, RT, 0, s>>>(buf0, buf1, ctl, tab, pchunk));
-        if ((e = hipGetLastError()) != hipSuccess) return e;
-        // every 8 rounds, stop launching once the device says the grammar is done
-        if (A.build && (r & 7) == 7 && r + 1 < rounds) {
+        CKR_LAUNCH("repair_runs_kernel", x, rp_runs<T><<<fg.G, RT, 0, x>>>(tok, len, N, fg.K, ctl, bfun));
+        if (A.build)
+            CKR_LAUNCH("repair_find_kernel", x,
+                       (rp_find<T, true><<<fg.G, RT, 0, x>>>(tok, len, back, N, fg.K, ctl, R.tab, bfun, bcount, lp, lq, le)));
+        else
+            CKR_LAUNCH("repair_find_kernel", x,
+                       (rp_find<T, false><<<fg.G, RT, 0, x>>>(tok, len, back, N, fg.K, ctl, R.tab, bfun, bcount, lp, lq, le)));
+        CKR_LAUNCH("repair_write_kernel", x, rp_write<T><<<fg.G, RT, 0, x>>>(tok, len, back, N, fg.K, ctl, bcount, lp, lq, le));
+        CKR_LAUNCH("repair_close_kernel", x, rp_close<<<1, CLOSE_T, 0, x>>>(fg.U, ctl, bcount, R));
+        return hipGetLastError();
+    };
+    // Rounds go in batches of kRoundBatch, each batch one launch of a graph
+    // captured once per workspace and shape and kept (a round is ~9 launches,
+    // whose host cost would otherwise exceed a small tensor's GPU work).
+    // Rounds past the last rule find the grammar done and return at once.
+    // While ckr_profile_begin is in effect the kernels are launched one by one.
+    hipGraphExec_t gx = ckr::profiling() ? nullptr : round_graph(A, L, round);
+    for (uint32_t r = 0; r < R.rounds; r += kRoundBatch) {
+        if (gx) {
+            if ((e = hipGraphLaunch(gx, s)) != hipSuccess) return e;
+        } else {
+            for (uint32_t i = r; i < std::min(R.rounds, r + kRoundBatch); i++)
+                if ((e = round(s)) != hipSuccess) return e;
+        }
+        // stop launching once the device says the grammar is done
+        if (A.build && r + kRoundBatch < R.rounds) {
             uint32_t done = 0;
             if ((e = hipMemcpyAsync(&done, &ctl->done, 4, hipMemcpyDeviceToHost, s)) != hipSuccess) return e;
             if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
@@ -939,11 +1418,18 @@ hipError_t repair_launch(const RepairArgs& A, hipStream_t s) {
         }
     }
     if (A.d_seq_out) {
-        CKR_LAUNCH("repair_seq_kernel", s,
-                   seq_out_kernel<<<grid_for(A.n), RT, 0, s>>>(buf0, buf1, ctl, sym, A.d_seq_out));
+        uint32_t* occ = reinterpret_cast<uint32_t*>(P(L.o_occ));
+        CKR_LAUNCH("repair_seq_kernel", s, seq_count<T><<<nblk, RT, 0, s>>>(tok, N, occ));
+        CKR_LAUNCH("repair_seq_kernel", s, scan_single<<<1, SCAN_T, 0, s>>>(occ, nblk, occ + nblk));
+        CKR_LAUNCH("repair_seq_kernel", s, seq_write<T><<<nblk, RT, 0, s>>>(tok, N, occ, sym, A.d_seq_out));
     }
-    (void)n32;
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t repair_launch(const RepairArgs& A, hipStream_t s) {
+    return A.layout.tok16 ? run_rounds<uint16_t>(A, s) : run_rounds<uint32_t>(A, s);
 }
 
 }  // namespace ckr

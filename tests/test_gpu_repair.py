@@ -102,6 +102,17 @@ def _bf16(n, s, seed):
     return dg.normal_bf16(n, s, seed)
 
 
+def _long_runs(seed):
+    """Runs of one word, 5,000 to 40,000 long, between stretches of normal
+    bf16: long spans next to short ones on both sides."""
+    rng = np.random.default_rng(seed)
+    parts = []
+    for i in range(12):
+        parts.append(_bf16(int(rng.integers(1, 300)), 0.02, seed + i))
+        parts.append(np.full(int(rng.integers(5_000, 40_000)), [0x3F80, 0xBC00, 0x3F80][i % 3], np.uint16))
+    return np.concatenate(parts)
+
+
 SYNTH = [
     # (name, dtype, masked request, max_rules, generator)
     ("bf16_normal_300k", 1, None, 50, lambda: _bf16(300_000, 0.02, 11)),
@@ -119,6 +130,11 @@ SYNTH = [
     ("f16_empty", 2, 0, 50, lambda: np.array([], np.uint16)),
     ("f16_random_ties", 2, 0, 50, lambda: np.random.default_rng(16).integers(0, 6, 777).astype(np.uint16)),
     ("adversarial_f32", 0, None, 50, lambda: dg.adversarial_f32(100_000, 17).view(np.uint32)),
+    # spans longer than a tombstone's length field holds (4095 positions with
+    # 16-bit ids, 65535 with 32-bit): their lengths go through len / back
+    ("bf16_const_long_spans", 1, None, 50, lambda: np.full(200_003, 0x3F80, np.uint16)),
+    ("f32_const_long_spans_hash", 0, 12, 50, lambda: np.full(150_001, 0x3F800000, np.uint32)),
+    ("bf16_long_runs_mixed", 1, None, 50, lambda: _long_runs(17)),
 ]
 
 
@@ -169,3 +185,26 @@ def test_repair_errors(gpu):
         rp.build(x)           # 200 words > workspace of 100
     with pytest.raises(ck.CkrError):
         rp.apply(x[:100], [(5, 1, 2, 3)])   # replacement must be 2^63 + index
+
+
+def test_repeated_builds_and_applies_on_one_workspace(gpu):
+    """The rounds of a build or apply on a workspace already used for the same
+    shape replay a captured graph: four builds and applies of different data on
+    one Repairer, with other device work between them, each against the oracle."""
+    import torch
+    ck = _ck()
+    n = 300_000
+    rp = ck.Repairer(n, 1, None, 50)
+    k = ck.repair_masked_bits(1, None)
+    for rep in range(4):
+        raw = _bf16(n, 0.02 * (1 + rep), 40 + rep).view(np.uint8)
+        got = rp.build(_dev(raw, gpu), want_seq=True)
+        torch.ones(1 << 20, device=gpu).mul_(3.0).sum().item()   # eager work between the replays
+        ref = oc.repair_build(raw, n, 2, k, 50, want_seq=True)
+        assert got["rules"] == ref["rules"], rep
+        assert got["out_len"] == ref["out_len"] and got["max_pair"] == ref["max_pair"]
+        assert np.array_equal(got["seq"], ref["seq"]), rep
+        other = _bf16(n, 0.03, 50 + rep).view(np.uint8)
+        g_len, g_seq = rp.apply(_dev(other, gpu), got["rules"], want_seq=True)
+        r_len, r_seq = oc.repair_apply(other, n, 2, k, ref["rules"], want_seq=True)
+        assert g_len == r_len and np.array_equal(g_seq, r_seq), rep
