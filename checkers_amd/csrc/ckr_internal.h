@@ -207,8 +207,10 @@ struct RepairLayout {
     bool direct;          // w <= 16: alphabet by bitmap, else by hash set
     bool tok16;           // token ids (alphabet + rules) lie below kRepairTomb16
     uint64_t pair_cap, vcap, n_buckets, list_entries;
+    uint32_t nids;        // bound of the token ids: alphabet (at most n, at most 2^w) + rules
+    uint32_t hist_rows, hist_len;  // small alphabets: per-workgroup rows of count changes
     uint64_t o_ctl, o_tok, o_len, o_back, o_list, o_bcount, o_sym, o_bitmap, o_rank, o_vkey, o_vrank, o_occ;
-    uint64_t o_pkey, o_pcnt, o_pfirst, o_touched, o_bfirst, o_primes, o_bfun, o_rules, o_rmap;
+    uint64_t o_pkey, o_pcnt, o_pfirst, o_touched, o_bfirst, o_primes, o_bfun, o_rules, o_rmap, o_hist;
     uint64_t bytes;
 };
 // n_buckets: bucket count of reserve(n) (size of the bucket first-occurrence array).

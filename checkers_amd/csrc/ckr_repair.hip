@@ -26,27 +26,39 @@
 // other array for spans under LMAX).  Positions are monotone in the compacted
 // sequence, so first occurrences compare as the reference's do.
 //
-// One round (all on the device, no host synchronisation), five launches:
-//   rp_count     (rounds that recount: the first, or when the table could pass
-//                3/4 full) every adjacent pair of live tokens counted, through a
-//                per-workgroup LDS cache of 2048 pairs in front of a global
-//                open-addressing table; the last workgroup to finish selects;
-//   rp_first     (rounds where several pairs hold the top count) the first
-//                occurrence of every pair; the last workgroup breaks the tie
-//                as std::unordered_map's iteration order would (below) and
-//                commits the rule;
-//   rp_runs      (rounds whose pair is (x, x)) the run parity: which x
-//                starts an occurrence depends on how many x precede it in its
-//                run, a function of the state entering a block of positions,
-//                so blocks compose; the last workgroup scans the blocks;
-//   rp_find      every occurrence of the pair (a, b): its start goes to a list,
-//                and (build rounds) the pair counts change by what the
-//                replacement destroys and creates around it, all read from the
-//                old sequence (no position is written in this pass);
-//   rp_write     the list's occurrences replaced in place; the last workgroup
-//                closes the round (live count, round number, the table emptied
-//                before a recount) and selects the next round's pair from the
-//                kept counts, committing it when no tie needs rp_first.
+// Rounds run on the device with no host synchronisation inside a batch of
+// eight (one replay of a captured graph).  A build round is up to seven
+// launches, each returning at once when its case does not arise:
+//   rp_pairs<COUNT>  (recount rounds: the first, or when the table could pass
+//                    3/4 full) every adjacent pair of live tokens counted,
+//                    through a per-workgroup LDS cache of 2048 pairs in front
+//                    of a global open-addressing table;
+//   rp_pairs<FIRST>  (rounds where several pairs hold the top count) the first
+//                    occurrence of every pair;
+//   rp_tie           (one workgroup) a recount round's selection, then any tie
+//                    broken as std::unordered_map's iteration order would
+//                    (below) and the rule committed;
+//   rp_runs          ((x, x) rounds) the run parity: which x starts an
+//                    occurrence depends on how many x precede it in its run,
+//                    a function of the state entering a unit of positions, so
+//                    units compose; each wave leaves its unit's function;
+//   rp_find          every occurrence of the pair (a, b) to a per-unit list,
+//                    and the pair counts' changes around it (what the
+//                    replacement destroys and creates), all read from the old
+//                    sequence: with ids below 4096, two LDS histograms over the
+//                    neighbour ids written out as one row per workgroup, else
+//                    the LDS pair cache;
+//   rp_write         the lists' occurrences replaced in place, and the count
+//                    rows summed in tiles and added to the table;
+//   rp_close         (one workgroup) the round closed (live count, round
+//                    number, the table emptied before a recount) and the next
+//                    pair selected from the kept counts, committed when no tie
+//                    needs rp_pairs<FIRST>.
+// An apply round is rp_runs and rp_find alone: the rules are known, so each
+// kernel reads its rule (the batch's base round in ctl plus the round's place
+// in the batch), and rp_find replaces each occurrence as it finds it (see
+// rp_find for why that is safe when no counts are kept); the live count is
+// taken once at the end.
 // Selection: the largest count and the number of pairs holding it; a unique
 // holder is the rule.  Ties: libstdc++ keeps one singly linked list; a node
 // for an empty bucket goes to the list head, a node for a used bucket goes to
@@ -86,14 +98,16 @@ constexpr int RT = 256;          // threads per workgroup
 constexpr int CACHE = 2048;      // LDS pair cache entries
 constexpr int CACHE_PROBES = 8;
 constexpr int SEG = 16;          // positions per thread in rp_runs / rp_find
-constexpr int BLK = RT * SEG;    // positions per rp_runs / rp_find block
+constexpr int BLK = RT * SEG;    // positions per seq_count / seq_write block
 constexpr int SCAN_T = 1024;     // threads of the single-workgroup alphabet scan
-constexpr uint32_t PAIR_CHUNK = 8192;  // least positions per rp_count / rp_first workgroup
-constexpr int PAIR_UNROLL = 4;   // pairs loaded together per rp_count thread
+constexpr uint32_t PAIR_CHUNK = 8192;  // least positions per rp_pairs workgroup
+constexpr int PAIR_UNROLL = 4;   // pairs loaded together per rp_pairs thread
 constexpr uint32_t OCC_BLK = 4096;
 constexpr uint32_t CHUNK = 64 * SEG;    // positions a wave takes at once
 constexpr uint32_t FIND_GRID = 1024;   // rp_runs / rp_find / rp_write workgroups (4 units each)
 constexpr int CLOSE_T = 1024;          // rp_close threads
+constexpr uint32_t HV = 4096;          // ids up to which rp_find gathers count changes in direct LDS histograms
+constexpr uint32_t MERGE_RG = 64;      // row groups of the histogram merge in rp_write
 
 template <typename T>
 __host__ __device__ __forceinline__ constexpr T tomb() { return (T)~(T)0; }
@@ -341,11 +355,12 @@ __global__ void __launch_bounds__(RT) alpha_map_hash(const uint8_t* __restrict__
 }
 
 // Apply mode: rule symbols → ids of this tensor (NONE if a base symbol is not
-// in its alphabet, or is not a masked word of this width).
+// in its alphabet, or is not a masked word of this width); rule r's id
+// A0 + r gets its symbol 2^63 + r.
 __global__ void map_rules_kernel(const ckr_repair_rule* __restrict__ rules, uint32_t n_rules, uint32_t k, uint32_t w,
                                  const uint32_t* __restrict__ rank, const uint64_t* __restrict__ vkey,
                                  uint64_t vmask, const uint32_t* __restrict__ vrank, RepairCtl* ctl,
-                                 uint32_t* __restrict__ rmap) {
+                                 uint32_t* __restrict__ rmap, uint64_t* __restrict__ sym) {
     const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= n_rules) return;
     const uint32_t a0 = ctl->a0;
@@ -365,6 +380,7 @@ __global__ void map_rules_kernel(const ckr_repair_rule* __restrict__ rules, uint
     rmap[3 * r + 0] = id_of(rules[r].lhs);
     rmap[3 * r + 1] = id_of(rules[r].rhs);
     rmap[3 * r + 2] = a0 + r;
+    sym[a0 + r] = (1ull << 63) + r;
 }
 
 // ------------------------------------------------------------------ pair table
@@ -396,6 +412,38 @@ __device__ void tab_first(const PairTab& t, RepairCtl* ctl, uint64_t key, uint32
         s = (s + 1) & t.mask;
     }
     atomicOr(&ctl->err, 4u);
+}
+
+// K adds to the table at once (val 0: nothing): the home slots' keys are
+// loaded together (keys only go from empty to set while the counting kernels
+// run, so a plain load that finds the key is right), empty home slots are
+// claimed together, and what is left (a home slot held by another key) takes
+// the probing path.
+template <int K>
+__device__ __forceinline__ void tab_add_many(const PairTab& t, RepairCtl* ctl, const uint64_t (&key)[K],
+                                             const uint32_t (&val)[K]) {
+    uint64_t slot[K], cur[K];
+#pragma unroll
+    for (int i = 0; i < K; i++) {
+        slot[i] = mix64(key[i]) & t.mask;
+        cur[i] = val[i] ? t.key[slot[i]] : key[i];
+    }
+#pragma unroll
+    for (int i = 0; i < K; i++) {
+        if (!val[i] || cur[i] != EMPTY_KEY) continue;
+        cur[i] = atomicCAS((unsigned long long*)&t.key[slot[i]], (unsigned long long)EMPTY_KEY,
+                           (unsigned long long)key[i]);
+        if (cur[i] == EMPTY_KEY) {
+            t.touched[atomicAdd(&ctl->d, 1u)] = (uint32_t)slot[i];
+            cur[i] = key[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < K; i++) {
+        if (!val[i]) continue;
+        if (cur[i] == key[i]) atomicAdd(&t.cnt[slot[i]], val[i]);
+        else tab_add(t, ctl, key[i], val[i]);
+    }
 }
 
 // LDS cache of pair updates in front of the global table: adds (FIRST: the
@@ -509,14 +557,36 @@ __device__ void commit_rule(RepairCtl* ctl, const RoundArgs& A) {
     A.tab.cnt[ctl->chosen] = 0;
 }
 
-// Apply: load rule `round` (or stop after the last).  Thread 0 only.
-__device__ void load_rule(RepairCtl* ctl, const RoundArgs& A) {
-    const uint32_t r = ctl->round;
-    if (r >= A.rounds) { ctl->done = 1; return; }
-    ctl->a = A.rmap[3 * r]; ctl->b = A.rmap[3 * r + 1]; ctl->c = A.rmap[3 * r + 2];
-    ctl->skip = (ctl->a == NONE || ctl->b == NONE) ? 1u : 0u;
-    ctl->run_mode = ctl->a == ctl->b ? 1u : 0u;
-    A.sym[ctl->c] = (1ull << 63) + r;
+// The pair of the round a grid kernel works on.  Build: the one committed in
+// ctl (by rp_close or the tie-break).  Apply: rule ctl->round + ri of the
+// mapped rules, ri being the round's place in its batch (ctl->round moves once
+// per batch), so that apply rounds need no closing launch.
+struct RoundSel {
+    const uint32_t* rmap;  // apply: (a, b, c) per rule; null in build
+    uint32_t rounds;       // apply: rule count
+    uint32_t ri;           // apply: the round's index within its batch
+};
+struct Cur {
+    uint32_t a, b, c;
+    bool live, run;  // live: there is a pair to replace
+};
+__device__ __forceinline__ Cur cur_round(const RepairCtl* ctl, const RoundSel& rs) {
+    Cur x;
+    if (!rs.rmap) {
+        x.live = !ctl->done && !ctl->skip;
+        x.a = ctl->a; x.b = ctl->b; x.c = ctl->c;
+        x.run = ctl->run_mode != 0;
+        return x;
+    }
+    const uint32_t r = ctl->round + rs.ri;
+    x.live = r < rs.rounds;
+    x.a = x.b = x.c = NONE;
+    if (x.live) {
+        x.a = rs.rmap[3 * r]; x.b = rs.rmap[3 * r + 1]; x.c = rs.rmap[3 * r + 2];
+        x.live = x.a != NONE && x.b != NONE;
+    }
+    x.run = x.a == x.b;
+    return x;
 }
 
 // The largest count over the table's used slots, the number of slots holding
@@ -582,7 +652,7 @@ __device__ void select_round(RepairCtl* ctl, const RoundArgs& A) {
     __syncthreads();
 }
 
-// Build, after rp_first: the holder of the top count that std::unordered_map
+// Build, after rp_pairs<FIRST>: the holder of the top count that std::unordered_map
 // visits first, then the commit.
 __device__ void break_tie(RepairCtl* ctl, const RoundArgs& A) {
     __shared__ unsigned long long s_pick;
@@ -812,9 +882,11 @@ __device__ __forceinline__ void win_runs(const Win<T>& w, const T* __restrict__ 
 // rstate[u].
 template <typename T>
 __global__ void __launch_bounds__(RT) rp_runs(const T* __restrict__ tok, const uint32_t* __restrict__ len, uint32_t N,
-                                              uint32_t K, RepairCtl* ctl, uint32_t* __restrict__ rstate) {
-    if (ctl->done || ctl->skip || !ctl->run_mode) return;
-    const uint32_t x = ctl->a;
+                                              uint32_t K, RepairCtl* ctl, uint32_t* __restrict__ rstate,
+                                              RoundSel rs) {
+    const Cur cr = cur_round(ctl, rs);
+    if (!cr.live || !cr.run) return;
+    const uint32_t x = cr.a;
     const Unit un = unit_of(N, K);
     const uint32_t lane = threadIdx.x & 63;
     uint32_t f = FN_ID;
@@ -839,22 +911,75 @@ __global__ void __launch_bounds__(RT) rp_runs(const T* __restrict__ tok, const u
 // occurrence (see the file comment), all read from the old sequence.  The
 // neighbours come from the lane's window when they lie in it and are live,
 // else from the span lengths and heads.
+// The occurrence (p, q) replaced by c, its merged span [p, e) (e: the next live
+// position after q, or N): the first and last tombstones of the span carry its
+// length, q (when it is neither) becomes a plain tombstone.
+template <typename T>
+__device__ __forceinline__ void merge_span(T* tok, uint32_t* len, uint32_t* back, uint32_t p, uint32_t q, uint32_t e,
+                                           T c) {
+    const uint32_t L = e - p, sl = min(L - 1, lmax<T>());
+    const T ts = (T)(tb0<T>() + sl);
+    tok[p] = c;
+    tok[p + 1] = ts;
+    if (q != p + 1 && q != e - 1) tok[q] = ts;
+    tok[e - 1] = ts;
+    if (sl == lmax<T>()) { len[p] = L; back[e - 1] = p; }
+}
+
+// Apply rounds (BUILD false) replace each occurrence in place as they find it,
+// in the same pass: every read that decides an occurrence (is p a start, where
+// is q, where is r) lands on the positions of its own span or on positions
+// whose old and new values lead to the same decision (a start or a live token
+// stays live; a written a becomes c, and neither is b or, in (x, x) rounds,
+// changes a decision the run states already fixed), and windows are loaded
+// before the chunk's writes.  Build rounds read farther neighbours for the
+// counts and leave the writing to rp_write.
 template <typename T, bool BUILD>
-__global__ void __launch_bounds__(RT) rp_find(const T* __restrict__ tok, const uint32_t* __restrict__ len,
-                                              const uint32_t* __restrict__ back, uint32_t N, uint32_t K,
+__global__ void __launch_bounds__(RT) rp_find(T* tok, uint32_t* len, uint32_t* back, uint32_t N, uint32_t K,
                                               RepairCtl* ctl, PairTab tab, const uint32_t* __restrict__ rstate,
                                               uint32_t* __restrict__ ucount, uint32_t* __restrict__ lp,
-                                              uint32_t* __restrict__ lq, uint32_t* __restrict__ le) {
-    if (ctl->done || ctl->skip) return;
-    __shared__ uint64_t ck[CACHE];
-    __shared__ uint32_t cv[CACHE];
+                                              uint32_t* __restrict__ lq, uint32_t* __restrict__ le, uint32_t nids,
+                                              uint32_t* __restrict__ hist, RoundSel rs) {
+    const Cur cr = cur_round(ctl, rs);
+    if (!cr.live) return;
+    // count changes: with ids below nids <= HV, two histograms over the ids
+    // (hl[t]: occurrences whose left neighbour t loses (t, a) and gains (t, c);
+    // hr[t]: right neighbour t, (b, t) to (c, t)) and three counters for the
+    // pairs of the run and overlap cases (hs: (c, c), (b, a) to (c, c), (c, a));
+    // else an LDS cache of pair keys
+    __shared__ uint64_t lds[HV];
+    __shared__ uint32_t hs[3];
+    uint64_t* ck = lds;
+    uint32_t* cv = reinterpret_cast<uint32_t*>(lds + CACHE);
+    uint32_t* hl = reinterpret_cast<uint32_t*>(lds);
+    uint32_t* hr = hl + HV;
     constexpr uint32_t TB0 = Win<T>::TB0;
-    const uint32_t a = ctl->a, b = ctl->b, c = ctl->c;
-    const bool run = ctl->run_mode != 0;
+    const uint32_t a = cr.a, b = cr.b, c = cr.c;
+    const bool run = cr.run;
     const bool count = BUILD && !ctl->recount_next;  // a recount follows: no count to keep
-    if (count) cache_init<false>(ck, cv);
+    const bool direct = nids <= HV;
+    if (count) {
+        if (direct) {
+            for (uint32_t j = threadIdx.x; j < nids; j += RT) { hl[j] = 0; hr[j] = 0; }
+            if (threadIdx.x < 3) hs[threadIdx.x] = 0;
+            __syncthreads();
+        } else {
+            cache_init<false>(ck, cv);
+        }
+    }
     auto upd = [&](uint32_t l, uint32_t r, uint32_t v) { cache_put<false>(ck, cv, tab, ctl, pair_key(l, r), v); };
     const uint32_t DEC = 0u - 1u;
+    auto left = [&](uint32_t t) {
+        if (direct) atomicAdd(&hl[t], 1u);
+        else { upd(t, a, DEC); upd(t, c, 1u); }
+    };
+    auto right = [&](uint32_t t) {
+        if (direct) atomicAdd(&hr[t], 1u);
+        else { upd(b, t, DEC); upd(c, t, 1u); }
+    };
+    auto cc = [&]() { if (direct) atomicAdd(&hs[0], 1u); else upd(c, c, 1u); };
+    auto ba = [&]() { if (direct) atomicAdd(&hs[1], 1u); else { upd(b, a, DEC); upd(c, c, 1u); } };
+    auto ca = [&]() { if (direct) atomicAdd(&hs[2], 1u); else upd(c, a, 1u); };
     const Unit un = unit_of(N, K);
     const uint32_t lane = threadIdx.x & 63;
     const uint64_t base = (uint64_t)un.u * K * (CHUNK / 2);  // the unit's slots: at most CHUNK / 2 per chunk
@@ -913,17 +1038,20 @@ __global__ void __launch_bounds__(RT) rp_find(const T* __restrict__ tok, const u
                 if (nx == b) starts |= 1u << j;
             }
         }
-        // slots: the wave's exclusive prefix of the lanes' counts
-        const uint32_t nst = __popc(starts);
-        uint32_t inc = nst;
+        // slots (build): the wave's exclusive prefix of the lanes' counts
+        uint64_t k = 0;
+        if constexpr (BUILD) {
+            const uint32_t nst = __popc(starts);
+            uint32_t inc = nst;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t g = (uint32_t)__shfl_up((int)inc, o);
-            if ((int)lane >= o) inc += g;
+            for (int o = 1; o < 64; o <<= 1) {
+                const uint32_t g = (uint32_t)__shfl_up((int)inc, o);
+                if ((int)lane >= o) inc += g;
+            }
+            const uint32_t total = (uint32_t)__shfl((int)inc, 63);
+            k = base + wcount + inc - nst;
+            wcount += total;
         }
-        const uint32_t total = (uint32_t)__shfl((int)inc, 63);
-        uint64_t k = base + wcount + inc - nst;
-        wcount += total;
         // each lane through its own occurrences; neighbours from the window
         // (k - 8 relative to i0) when they lie in it and are live
         uint32_t m = starts;
@@ -943,6 +1071,10 @@ __global__ void __launch_bounds__(RT) rp_find(const T* __restrict__ tok, const u
             } else {
                 r = next_live<T>(tok, len, q, N);
                 if (r < N) tr = tok[r];
+            }
+            if constexpr (!BUILD) {
+                merge_span<T>(tok, len, back, p, q, r, (T)c);
+                continue;
             }
             lp[k] = p; lq[k] = q; le[k] = r;
             k++;
@@ -965,17 +1097,16 @@ __global__ void __launch_bounds__(RT) rp_find(const T* __restrict__ tok, const u
                 const uint32_t nr = next_live<T>(tok, len, r, N);
                 return nr < N ? (uint32_t)tok[nr] : NONE;
             };
-            if (run) {
+            if (run) {  // (b == a)
                 if (x != NONE) {
-                    if (tx == a) upd(c, c, 1u);
-                    else { upd(tx, a, DEC); upd(tx, c, 1u); }
+                    if (tx == a) cc();
+                    else left(tx);
                 }
                 if (r < N) {
                     if (tr == a) {
-                        if (after_r() != a) upd(c, a, 1u);
+                        if (after_r() != a) ca();
                     } else {
-                        upd(a, tr, DEC);
-                        upd(c, tr, 1u);
+                        right(tr);
                     }
                 }
             } else {
@@ -994,26 +1125,46 @@ __global__ void __launch_bounds__(RT) rp_find(const T* __restrict__ tok, const u
                         }
                         second = txx == a;
                     }
-                    if (second) { upd(b, a, DEC); upd(c, c, 1u); }
-                    else { upd(tx, a, DEC); upd(tx, c, 1u); }
+                    if (second) ba();
+                    else left(tx);
                 }
-                if (r < N && !(tr == a && after_r() == b)) { upd(b, tr, DEC); upd(c, tr, 1u); }
+                if (r < N && !(tr == a && after_r() == b)) right(tr);
             }
         }
     }
-    if (lane == 0) ucount[un.u] = wcount;
-    if (count) cache_flush<false>(ck, cv, tab, ctl);
+    if (BUILD && lane == 0) ucount[un.u] = wcount;
+    if (!count) return;
+    if (!direct) {
+        cache_flush<false>(ck, cv, tab, ctl);
+        return;
+    }
+    // the histograms as this workgroup's row (hl | hr | hs), summed over the
+    // workgroups and added to the table by rp_write
+    __syncthreads();
+    uint32_t* row = hist + (uint64_t)blockIdx.x * (2 * nids + 3);
+    for (uint32_t j = threadIdx.x; j < nids; j += RT) {
+        row[j] = hl[j];
+        row[nids + j] = hr[j];
+    }
+    if (threadIdx.x < 3) row[2 * nids + threadIdx.x] = hs[threadIdx.x];
 }
 
 // The round's occurrences replaced in place (no two share a position): each
-// wave writes its unit's, whose positions lie in the unit's chunks.
+// wave writes its unit's, whose positions lie in the unit's chunks.  Build
+// rounds that keep counts with ids below HV (merge): the count-change rows that
+// rp_find left (one per workgroup: hl | hr | hs) are summed in tiles of 256
+// columns x a group of rows, and each tile's sums go to the table, so each
+// pair takes one add per row group rather than one per workgroup.
 template <typename T>
 __global__ void __launch_bounds__(RT) rp_write(T* __restrict__ tok, uint32_t* __restrict__ len,
                                                uint32_t* __restrict__ back, uint32_t N, uint32_t K, RepairCtl* ctl,
                                                const uint32_t* __restrict__ ucount, const uint32_t* __restrict__ lp,
-                                               const uint32_t* __restrict__ lq, const uint32_t* __restrict__ le) {
-    if (ctl->done || ctl->skip) return;
-    const T c = (T)ctl->c;
+                                               const uint32_t* __restrict__ lq, const uint32_t* __restrict__ le,
+                                               const uint32_t* __restrict__ hist, uint32_t nids, uint32_t nrows,
+                                               PairTab tab, int merge, RoundSel rs) {
+    const Cur cr = cur_round(ctl, rs);
+    if (!cr.live) return;
+    const T c = (T)cr.c;
     const Unit un = unit_of(N, K);
     const uint32_t lane = threadIdx.x & 63;
     const uint64_t base = (uint64_t)un.u * K * (CHUNK / 2);
@@ -1021,21 +1172,55 @@ __global__ void __launch_bounds__(RT) rp_write(T* __restrict__ tok, uint32_t* __
     for (uint32_t k = lane; k < m; k += 64) {
         const uint32_t p = lp[base + k], q = lq[base + k], e = le[base + k];
         if (p >= q || q >= e || e > N) continue;  // (never: p < q < e <= N)
-        // the merged span [p, e): its first and last tombstones carry its
-        // length, q (when it is neither) becomes a plain tombstone
-        const uint32_t L = e - p, sl = min(L - 1, lmax<T>());
-        const T ts = (T)(tb0<T>() + sl);
-        tok[p] = c;
-        tok[p + 1] = ts;
-        if (q != p + 1 && q != e - 1) tok[q] = ts;
-        tok[e - 1] = ts;
-        if (sl == lmax<T>()) { len[p] = L; back[e - 1] = p; }
+        merge_span<T>(tok, len, back, p, q, e, c);
+    }
+    if (!merge || ctl->recount_next) return;
+    const uint32_t a = cr.a, b = cr.b;
+    const uint32_t rowlen = 2 * nids + 3, ncb = (rowlen + RT - 1) / RT;
+    const uint32_t ngrp = min(MERGE_RG, nrows), rpt = (nrows + ngrp - 1) / ngrp;
+    const uint32_t ntiles = ncb * ngrp;  // tiles of RT columns x rpt rows
+    // a workgroup takes up to four tiles at a time (when there are more tiles
+    // than workgroups), their table adds issued together
+    for (uint32_t t0 = blockIdx.x; t0 < ntiles; t0 += 4 * gridDim.x) {
+        uint64_t key[8];
+        uint32_t val[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t tile = t0 + i * gridDim.x;
+            const uint32_t col = (tile % ncb) * RT + threadIdx.x;
+            const uint32_t r0 = (tile / ncb) * rpt, r1 = tile < ntiles ? min(nrows, r0 + rpt) : 0u;
+            uint32_t sum = 0;
+            if (col < rowlen) {
+                uint32_t r = r0;
+                for (; r + 4 <= r1; r += 4) {
+                    const uint32_t* h = hist + (uint64_t)r * rowlen + col;
+                    sum += h[0] + h[rowlen] + h[2 * rowlen] + h[3 * rowlen];
+                }
+                for (; r < r1; r++) sum += hist[(uint64_t)r * rowlen + col];
+            }
+            uint64_t k0 = 0, k1 = 0;
+            uint32_t v0 = 0u - sum, v1 = sum;
+            if (col < nids) {                       // left neighbour col: (col, a) to (col, c)
+                k0 = pair_key(col, a); k1 = pair_key(col, c);
+            } else if (col < 2 * nids) {            // right neighbour: (b, t) to (c, t)
+                k0 = pair_key(b, col - nids); k1 = pair_key(c, col - nids);
+            } else if (col == 2 * nids) {           // (c, c) made by runs
+                k0 = k1 = pair_key(c, c); v0 = 0;
+            } else if (col == 2 * nids + 1) {       // (b, a) to (c, c)
+                k0 = pair_key(b, a); k1 = pair_key(c, c);
+            } else {                                // (c, a) after an odd run
+                k0 = k1 = pair_key(c, a); v0 = 0;
+            }
+            key[2 * i] = k0; key[2 * i + 1] = k1;
+            val[2 * i] = v0; val[2 * i + 1] = v1;
+        }
+        tab_add_many<8>(tab, ctl, key, val);
     }
 }
 
-// One workgroup: the round closed (live count, round number, the table
+// Build, one workgroup: the round closed (live count, round number, the table
 // emptied before a recount), then the next round's pair selected from the kept
-// counts (build; committed when no tie needs rp_first) or loaded (apply).
+// counts (committed when no tie needs rp_pairs<FIRST>).
 __global__ void __launch_bounds__(CLOSE_T) rp_close(uint32_t nb, RepairCtl* ctl, const uint32_t* __restrict__ bcount,
                                                     RoundArgs A) {
     if (ctl->done) return;
@@ -1054,30 +1239,26 @@ __global__ void __launch_bounds__(CLOSE_T) rp_close(uint32_t nb, RepairCtl* ctl,
         ctl->n_cur -= total;
         ctl->round++;
         ctl->best = 0; ctl->ncand = 0; ctl->pick = 0; ctl->skip = 0; ctl->tie = 0; ctl->run_mode = 0;
-        ctl->recount = A.build ? ctl->recount_next : 0u;
+        ctl->recount = ctl->recount_next;
         ctl->recount_next = 0;
         s_recount = ctl->recount;
     }
     __syncthreads();
-    if (A.build) {
-        if (s_recount) {  // rp_pairs fills the table again
-            const uint32_t d = ctl->d;
-            for (uint32_t j = threadIdx.x; j < d; j += blockDim.x) {
-                const uint32_t s = A.tab.touched[j];
-                A.tab.key[s] = EMPTY_KEY; A.tab.cnt[s] = 0; A.tab.first[s] = NONE;
-            }
-            __syncthreads();
-            if (threadIdx.x == 0) ctl->d = 0;
-        } else {
-            select_round(ctl, A);
+    if (s_recount) {  // rp_pairs fills the table again
+        const uint32_t d = ctl->d;
+        for (uint32_t j = threadIdx.x; j < d; j += blockDim.x) {
+            const uint32_t s = A.tab.touched[j];
+            A.tab.key[s] = EMPTY_KEY; A.tab.cnt[s] = 0; A.tab.first[s] = NONE;
         }
-    } else if (threadIdx.x == 0) {
-        load_rule(ctl, A);
+        __syncthreads();
+        if (threadIdx.x == 0) ctl->d = 0;
+    } else {
+        select_round(ctl, A);
     }
 }
 
-// Apply mode, before the first round: rule 0.
-__global__ void rp_load_first(RepairCtl* ctl, RoundArgs A) { load_rule(ctl, A); }
+// Apply, after a batch of rounds: the batch's rounds are done.
+__global__ void rp_batch_end(RepairCtl* ctl, uint32_t rounds) { ctl->round += rounds; }
 
 // ------------------------------------------------------------------ output
 // The live tokens as reference symbols, in order: per block of BLK positions
@@ -1197,6 +1378,12 @@ RepairLayout repair_layout(uint64_t n, int es, uint32_t k, uint32_t max_rules, u
     L.o_bfirst = take(4 * L.n_buckets);
     L.o_primes = take(8 * kRepairMaxPrimes);
     L.o_bfun = take(4 * (uint64_t)fg.U);
+    // ids: the alphabet (at most n words, at most 2^w), then one per rule
+    L.nids = (uint32_t)std::min<uint64_t>(std::min<uint64_t>(n, 1ull << std::min<uint32_t>(w, 40)) + max_rules,
+                                          0xFFFFFFFFull);
+    L.hist_rows = L.nids <= HV ? fg.G : 0;
+    L.hist_len = L.nids <= HV ? 2 * L.nids + 3 : 0;
+    L.o_hist = take(4ull * L.hist_rows * L.hist_len);
     L.o_rules = take(sizeof(ckr_repair_rule) * std::max<uint32_t>(max_rules, 1));
     L.o_rmap = take(12 * std::max<uint32_t>(max_rules, 1));
     L.bytes = off;
@@ -1249,18 +1436,19 @@ hipError_t build_alphabet(const uint8_t* words, uint64_t n, int es, uint32_t k, 
 
 constexpr uint32_t kRoundBatch = 8;
 
-// The captured graphs of kRoundBatch rounds, keyed by what their kernels'
-// arguments derive from (the workspace and its layout's inputs).  A graph is
+// The captured graphs of a batch of rounds (kRoundBatch, or the last batch's
+// remainder), keyed by what their kernels' arguments derive from (the
+// workspace and its layout's inputs) and the batch length.  A graph is
 // captured on a library stream, instantiated once and kept; at most
 // kMaxRoundGraphs are kept (the oldest goes).
 struct RoundGraphKey {
     const void* ws;
     uint64_t n;
     int es, build, device, tok16;
-    uint32_t k, rounds, dlimit;
+    uint32_t k, rounds, dlimit, batch;
     bool operator==(const RoundGraphKey& o) const {
         return ws == o.ws && n == o.n && es == o.es && build == o.build && device == o.device && tok16 == o.tok16 &&
-               k == o.k && rounds == o.rounds && dlimit == o.dlimit;
+               k == o.k && rounds == o.rounds && dlimit == o.dlimit && batch == o.batch;
     }
 };
 struct RoundGraph {
@@ -1272,28 +1460,32 @@ constexpr size_t kMaxRoundGraphs = 64;
 std::mutex g_rg_mu;
 std::vector<RoundGraph> g_rgs;
 
-template <typename RoundFn>
-hipGraphExec_t round_graph(const RepairArgs& A, const RepairLayout& L, RoundFn& round) {
+// A library stream per device, made on first use (graph capture).
+hipStream_t side_stream(int dev, std::vector<hipStream_t>& v) {
+    if ((int)v.size() <= dev) v.resize(dev + 1, nullptr);
+    if (!v[dev] && hipStreamCreateWithFlags(&v[dev], hipStreamNonBlocking) != hipSuccess) {
+        (void)hipGetLastError();
+        v[dev] = nullptr;
+    }
+    return v[dev];
+}
+
+template <typename BatchFn>
+hipGraphExec_t round_graph(const RepairArgs& A, const RepairLayout& L, uint32_t len, BatchFn& batch) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) { (void)hipGetLastError(); return nullptr; }
     const RoundGraphKey key{A.ws, A.n, A.es, A.build, dev, L.tok16 ? 1 : 0, A.k, A.build ? A.max_rules : A.n_rules,
-                            A.recount_each_round ? 1u : 0u};
+                            A.recount_each_round ? 1u : 0u, len};
     std::lock_guard<std::mutex> lk(g_rg_mu);
     for (const RoundGraph& r : g_rgs)
         if (r.key == key) return r.x;
     static std::vector<hipStream_t> cap;  // one capture stream per device
-    if ((int)cap.size() <= dev) cap.resize(dev + 1, nullptr);
-    if (!cap[dev] && hipStreamCreateWithFlags(&cap[dev], hipStreamNonBlocking) != hipSuccess) {
-        (void)hipGetLastError();
-        cap[dev] = nullptr;
-        return nullptr;
-    }
-    hipStream_t cs = cap[dev];
+    hipStream_t cs = side_stream(dev, cap);
+    if (!cs) return nullptr;
     hipGraph_t g = nullptr;
     hipGraphExec_t x = nullptr;
     if (hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal) != hipSuccess) { (void)hipGetLastError(); return nullptr; }
-    hipError_t e = hipSuccess;
-    for (uint32_t i = 0; i < kRoundBatch && e == hipSuccess; i++) e = round(cs);
+    const hipError_t e = batch(cs, len);
     const hipError_t e2 = hipStreamEndCapture(cs, &g);
     if (e != hipSuccess || e2 != hipSuccess || !g || hipGraphInstantiate(&x, g, nullptr, nullptr, 0) != hipSuccess) {
         (void)hipGetLastError();
@@ -1355,6 +1547,9 @@ hipError_t run_rounds(const RepairArgs& A, hipStream_t s) {
     const uint32_t gpair = (uint32_t)std::max<uint64_t>(1, (A.n + pchunk - 1) / pchunk);
     const uint32_t nblk = (uint32_t)((A.n + BLK - 1) / BLK);
     const FindGeom fg = find_geom(A.n);
+    const uint32_t nids = L.nids;
+    uint32_t* hist = reinterpret_cast<uint32_t*>(P(L.o_hist));
+    const int merge = A.build && nids <= HV && L.hist_rows >= fg.G ? 1 : 0;
     uint32_t* bcount = reinterpret_cast<uint32_t*>(P(L.o_bcount));
     uint32_t* lp = reinterpret_cast<uint32_t*>(P(L.o_list));
     uint32_t* lq = lp + L.list_entries;
@@ -1374,54 +1569,69 @@ hipError_t run_rounds(const RepairArgs& A, hipStream_t s) {
                    map_rules_kernel<<<(A.n_rules + 63) / 64, 64, 0, s>>>(
                        R.rules, A.n_rules, A.k, L.w, rank, reinterpret_cast<const uint64_t*>(P(L.o_vkey)),
                        L.vcap ? L.vcap - 1 : 0, reinterpret_cast<const uint32_t*>(P(L.o_vrank)), ctl,
-                       const_cast<uint32_t*>(R.rmap)));
-        CKR_LAUNCH("repair_commit_kernel", s, rp_load_first<<<1, 1, 0, s>>>(ctl, R));
+                       const_cast<uint32_t*>(R.rmap), sym));
     }
-    // one round: every kernel reads what to do from ctl, so the rounds are
-    // identical launches
-    auto round = [&](hipStream_t x) -> hipError_t {
+    // One round.  Build: every kernel reads what to do from ctl, so the rounds
+    // are identical launches.  Apply: the grid kernels take the round's place
+    // in its batch and read the rule themselves, rp_find writes in place; no
+    // write or closing launch.
+    auto round = [&](hipStream_t x, uint32_t ri) -> hipError_t {
+        const RoundSel rs{A.build ? nullptr : R.rmap, R.rounds, ri};
         if (A.build) {
             CKR_LAUNCH("repair_count_kernel", x, (rp_pairs<T, false><<<gpair, RT, 0, x>>>(tok, len, N, ctl, R, pchunk)));
             CKR_LAUNCH("repair_first_kernel", x, (rp_pairs<T, true><<<gpair, RT, 0, x>>>(tok, len, N, ctl, R, pchunk)));
             CKR_LAUNCH("repair_select_kernel", x, rp_tie<<<1, CLOSE_T, 0, x>>>(ctl, R));
         }
-        CKR_LAUNCH("repair_runs_kernel", x, rp_runs<T><<<fg.G, RT, 0, x>>>(tok, len, N, fg.K, ctl, bfun));
+        CKR_LAUNCH("repair_runs_kernel", x, rp_runs<T><<<fg.G, RT, 0, x>>>(tok, len, N, fg.K, ctl, bfun, rs));
         if (A.build)
             CKR_LAUNCH("repair_find_kernel", x,
-                       (rp_find<T, true><<<fg.G, RT, 0, x>>>(tok, len, back, N, fg.K, ctl, R.tab, bfun, bcount, lp, lq, le)));
+                       (rp_find<T, true><<<fg.G, RT, 0, x>>>(tok, len, back, N, fg.K, ctl, R.tab, bfun, bcount, lp, lq,
+                                                              le, nids, hist, rs)));
         else
             CKR_LAUNCH("repair_find_kernel", x,
-                       (rp_find<T, false><<<fg.G, RT, 0, x>>>(tok, len, back, N, fg.K, ctl, R.tab, bfun, bcount, lp, lq, le)));
-        CKR_LAUNCH("repair_write_kernel", x, rp_write<T><<<fg.G, RT, 0, x>>>(tok, len, back, N, fg.K, ctl, bcount, lp, lq, le));
-        CKR_LAUNCH("repair_close_kernel", x, rp_close<<<1, CLOSE_T, 0, x>>>(fg.U, ctl, bcount, R));
+                       (rp_find<T, false><<<fg.G, RT, 0, x>>>(tok, len, back, N, fg.K, ctl, R.tab, bfun, bcount, lp,
+                                                               lq, le, nids, hist, rs)));
+        if (A.build) {
+            CKR_LAUNCH("repair_write_kernel", x,
+                       rp_write<T><<<fg.G, RT, 0, x>>>(tok, len, back, N, fg.K, ctl, bcount, lp, lq, le, hist, nids,
+                                                       fg.G, R.tab, merge, rs));
+            CKR_LAUNCH("repair_close_kernel", x, rp_close<<<1, CLOSE_T, 0, x>>>(fg.U, ctl, bcount, R));
+        }
         return hipGetLastError();
     };
-    // Rounds go in batches of kRoundBatch, each batch one launch of a graph
-    // captured once per workspace and shape and kept (a round is ~9 launches,
-    // whose host cost would otherwise exceed a small tensor's GPU work).
-    // Rounds past the last rule find the grammar done and return at once.
+    auto batch = [&](hipStream_t x, uint32_t n_rounds) -> hipError_t {
+        for (uint32_t i = 0; i < n_rounds; i++) {
+            const hipError_t er = round(x, i);
+            if (er != hipSuccess) return er;
+        }
+        if (!A.build) CKR_LAUNCH("repair_close_kernel", x, rp_batch_end<<<1, 1, 0, x>>>(ctl, n_rounds));
+        return hipGetLastError();
+    };
+    // Rounds go in batches of kRoundBatch (the last one shorter), each batch
+    // one launch of a graph captured once per workspace, shape and batch
+    // length and kept (a round is up to 7 launches, whose host cost would
+    // otherwise exceed a small tensor's GPU work).  A build reads the device's
+    // done flag after each batch but the last and stops there once it is set
+    // (rounds past the last rule find the grammar done and return at once).
     // While ckr_profile_begin is in effect the kernels are launched one by one.
-    hipGraphExec_t gx = ckr::profiling() ? nullptr : round_graph(A, L, round);
     for (uint32_t r = 0; r < R.rounds; r += kRoundBatch) {
-        if (gx) {
-            if ((e = hipGraphLaunch(gx, s)) != hipSuccess) return e;
-        } else {
-            for (uint32_t i = r; i < std::min(R.rounds, r + kRoundBatch); i++)
-                if ((e = round(s)) != hipSuccess) return e;
-        }
-        // stop launching once the device says the grammar is done
-        if (A.build && r + kRoundBatch < R.rounds) {
-            uint32_t done = 0;
-            if ((e = hipMemcpyAsync(&done, &ctl->done, 4, hipMemcpyDeviceToHost, s)) != hipSuccess) return e;
-            if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
-            if (done) break;
-        }
+        const uint32_t n_rounds = std::min(kRoundBatch, R.rounds - r);
+        hipGraphExec_t gx = ckr::profiling() ? nullptr : round_graph(A, L, n_rounds, batch);
+        if ((e = gx ? hipGraphLaunch(gx, s) : batch(s, n_rounds)) != hipSuccess) return e;
+        if (!A.build || r + kRoundBatch >= R.rounds) continue;
+        uint32_t done = 0;
+        if ((e = hipMemcpyAsync(&done, &ctl->done, 4, hipMemcpyDeviceToHost, s)) != hipSuccess) return e;
+        if ((e = hipStreamSynchronize(s)) != hipSuccess) return e;
+        if (done) break;
     }
-    if (A.d_seq_out) {
+    // the live tokens counted per block and scanned: the output's offsets, and
+    // (apply, whose rounds keep no running count) the compressed length
+    if (A.d_seq_out || !A.build) {
         uint32_t* occ = reinterpret_cast<uint32_t*>(P(L.o_occ));
         CKR_LAUNCH("repair_seq_kernel", s, seq_count<T><<<nblk, RT, 0, s>>>(tok, N, occ));
-        CKR_LAUNCH("repair_seq_kernel", s, scan_single<<<1, SCAN_T, 0, s>>>(occ, nblk, occ + nblk));
-        CKR_LAUNCH("repair_seq_kernel", s, seq_write<T><<<nblk, RT, 0, s>>>(tok, N, occ, sym, A.d_seq_out));
+        CKR_LAUNCH("repair_seq_kernel", s, scan_single<<<1, SCAN_T, 0, s>>>(occ, nblk, A.build ? occ + nblk : &ctl->n_cur));
+        if (A.d_seq_out)
+            CKR_LAUNCH("repair_seq_kernel", s, seq_write<T><<<nblk, RT, 0, s>>>(tok, N, occ, sym, A.d_seq_out));
     }
     return hipGetLastError();
 }
