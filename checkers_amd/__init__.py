@@ -186,7 +186,9 @@ def _check(rc):
 
 def set_fast_paths(mode):
     """1: fast kernels (default); 0: general kernels; 2: fast kernels with minimal
-    LDS lane slots (overflow route).  Returns the previous mode."""
+    LDS lane slots (overflow route through the general kernels); 3: the same
+    slots, the overflowing units coded again by the fast encoder with slots
+    that hold any lane.  Returns the previous mode."""
     return int(lib().ckr_set_fast_paths(int(mode)))
 
 

@@ -166,7 +166,7 @@ CanonKs canon_ks(const ckr::EncodeGeom& g) {
 }
 constexpr uint32_t kDedupMaxK = 4096;  // zero-plane dedup up to 1 MiB units
 constexpr uint32_t kFastMaxK = 256;    // LDS-staged encode / decode up to 64 KiB units
-int g_fast_paths = 1;                  // ckr_set_fast_paths: 0 general, 1 fast, 2 fast with minimal LDS slots
+int g_fast_paths = 1;  // ckr_set_fast_paths: 0 general, 1 fast, 2 / 3 fast with minimal LDS slots (redo: general / fast)
 
 bool use_dedup(const ckr::EncodeGeom& g) {
     return g_fast_paths && g.spe > 0 && g.n_units > 0 && (g.unit + 255) / 256 <= kDedupMaxK;
@@ -516,7 +516,7 @@ const char* ckr_last_error(void) { return g_last_error.c_str(); }
 
 int ckr_set_fast_paths(int mode) {
     const int prev = g_fast_paths;
-    g_fast_paths = (mode < 0 || mode > 2) ? 1 : mode;
+    g_fast_paths = (mode < 0 || mode > 3) ? 1 : mode;
     return prev;
 }
 const char* ckr_version(void) { return "checkers_amd 0.1 gfx950"; }
@@ -688,6 +688,10 @@ struct EncodeDeferred {
     uint8_t* out = nullptr;
     const uint32_t* redo = nullptr;
     uint64_t batch_units = 0;
+    bool redo_fast = false;  // redo units go to the fast encoder with slots that hold any lane
+    ckr::FastEncParamsHost fp{};
+    uint64_t* status = nullptr;
+    uint32_t* ctl = nullptr;
 };
 int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_table* h_table, uint64_t unit_bytes,
                 uint8_t* d_out, uint64_t out_capacity, ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
@@ -746,7 +750,7 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         const uint32_t cbmax = std::max(canon_stream_bytes(h_table, ck.k0),
                                         std::max(canon_stream_bytes(h_table, ck.k1), canon_stream_bytes(h_table, ck.k2)));
         fp.canon_bytes = std::min<uint32_t>((cbmax + 3) & ~3u, 4 * ck.cw);
-        if (g_fast_paths == 2) {
+        if (g_fast_paths >= 2) {
             fp.sl0 = fp.sl1 = 8;
         } else {
             fp.sl0 = lane_slot_bytes(h_planes, h_table, K);
@@ -787,7 +791,7 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
             return ckr::encode_seg_fast_lds_bytes(sp, lds_limit) != 0;
         };
         uint32_t a = 8, b = 8;
-        if (g_fast_paths != 2) {
+        if (g_fast_paths < 2) {
             constexpr uint32_t cap = 2 * 256 + 8;  // the most 256 symbols can emit, and the final dword
             if (h_planes) {
                 a = std::min(cap, lane_slot_bytes(h_planes, h_table, 256));
@@ -799,7 +803,7 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
                 b = std::min(b + 4, cap);
             }
         }
-        const bool seg_fast = (h_planes || g_fast_paths == 2) && fits(a, b);
+        const bool seg_fast = (h_planes || g_fast_paths >= 2) && fits(a, b);
         CKR_HIP(ckr::launch_encode_seg(static_cast<const uint8_t*>(d_src), g, enc, canon, ck.cw, escapes, rec,
                                        d_headers, usize, d_unit_offsets, side, d_out, aux, seg_fast ? &sp : nullptr,
                                        lds_limit, aux + 64, ws + L.off_list, s));
@@ -827,6 +831,10 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         CKR_HIP(ckr::launch_encode_fast(static_cast<const uint8_t*>(d_src), g, enc, canon, fp,
                                         (uint32_t)max_lds_per_block(), d_headers, side, d_out, d_unit_offsets, status,
                                         ctl, redo, s));
+        // units whose lanes outgrew their LDS slots (the control words say how
+        // many): coded again by the fast encoder with slots that hold any lane,
+        // or, in mode 2 or when those slots do not fit, by the general kernels
+        const bool redo_fast = g_fast_paths != 2 && ckr::encode_fast_list_fits(fp, g, (uint32_t)max_lds_per_block());
         if (after_launch) CKR_HIP((*after_launch)());
         if (defer) {
             defer->kind = 1;
@@ -842,6 +850,10 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
             defer->out = d_out;
             defer->redo = redo;
             defer->batch_units = L.batch_units;
+            defer->redo_fast = redo_fast;
+            defer->fp = fp;
+            defer->status = status;
+            defer->ctl = ctl;
             // the control words and, in ctl[4..5], the total: one read-back
             CKR_HIP(hipMemcpyAsync(defer->pin, ctl, 24, hipMemcpyDeviceToHost, s));
             return CKR_OK;
@@ -854,11 +866,14 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         CKR_HIP(hipStreamSynchronize(s));
         uint32_t hctl[4];
         std::memcpy(hctl, pw, 16);
-        if (hctl[2]) return fail(CKR_E_HIP, "[ckr] encode look-back did not complete (flag %u)", hctl[2]);
+        if (hctl[2]) return fail(CKR_E_HIP, "[ckr] fast encode did not complete (flags %u: 1 look-back, 2 redo slots)", hctl[2]);
         if (h_total_out) std::memcpy(h_total_out, pw + 4, 8);
-        // units whose lanes outgrew their LDS slots: bytes from the general kernels,
-        // at the offsets the fast kernel published
-        for (uint64_t r0 = 0; r0 < hctl[1]; r0 += L.batch_units) {
+        // the redo units, at the offsets the fast kernel published
+        if (hctl[1] && redo_fast)
+            CKR_HIP(ckr::launch_encode_fast_list(static_cast<const uint8_t*>(d_src), g, enc, canon, fp,
+                                                 (uint32_t)max_lds_per_block(), d_headers, d_out, d_unit_offsets,
+                                                 status, ctl, redo, s));
+        for (uint64_t r0 = 0; !redo_fast && r0 < hctl[1]; r0 += L.batch_units) {
             const uint64_t nb = std::min<uint64_t>(L.batch_units, hctl[1] - r0);
             CKR_HIP(ckr::launch_encode_batch(static_cast<const uint8_t*>(d_src), g, r0, nb, enc, canon, ck.cw, true,
                                              scratch, d_headers, nullptr, usize, d_unit_offsets, d_out, redo, s));
@@ -945,8 +960,13 @@ int check_encode_args(const void* src, const ckr::EncodeGeom& g, uint64_t n_elem
 int encode_complete(const EncodeDeferred& d, uint64_t* total, bool* queued_more, hipStream_t s) {
     if (d.kind == 2 && d.pin[0]) return fail(CKR_E_HIP, "[ckr] two-pass encode: a segment did not end at its checkpoint");
     if (d.kind == 1) {
-        if (d.pin[2]) return fail(CKR_E_HIP, "[ckr] encode look-back did not complete (flag %u)", d.pin[2]);
-        for (uint64_t r0 = 0; r0 < d.pin[1]; r0 += d.batch_units) {
+        if (d.pin[2]) return fail(CKR_E_HIP, "[ckr] fast encode did not complete (flags %u: 1 look-back, 2 redo slots)", d.pin[2]);
+        if (d.pin[1] && d.redo_fast) {
+            CKR_HIP(ckr::launch_encode_fast_list(d.src, d.g, d.enc, d.canon, d.fp, (uint32_t)max_lds_per_block(), d.hdrs,
+                                                 d.out, d.unit_off, d.status, d.ctl, const_cast<uint32_t*>(d.redo), s));
+            *queued_more = true;
+        }
+        for (uint64_t r0 = 0; !d.redo_fast && r0 < d.pin[1]; r0 += d.batch_units) {
             const uint64_t nb = std::min<uint64_t>(d.batch_units, d.pin[1] - r0);
             CKR_HIP(ckr::launch_encode_batch(d.src, d.g, r0, nb, d.enc, d.canon, d.cw, true, d.scratch, d.hdrs, nullptr,
                                              d.usize, d.unit_off, d.out, d.redo, s));

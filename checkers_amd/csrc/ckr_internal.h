@@ -130,6 +130,14 @@ struct FastEncParamsHost {
 };
 // LDS bytes of the fast encoder's workgroup within lds_limit (0: it does not fit).
 uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p, uint32_t lds_limit);
+// The fast encoder's redo list (ctl[1] units) coded again: one coder pair per
+// workgroup with slots that hold any lane; false/error when those slots do not
+// fit lds_limit.
+bool encode_fast_list_fits(const FastEncParamsHost& p, const EncodeGeom& g, uint32_t lds_limit);
+hipError_t launch_encode_fast_list(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
+                                   const FastEncParamsHost& hp, uint32_t lds_limit, ckr_stream_header* hdrs,
+                                   uint8_t* out, uint64_t* unit_off, uint64_t* status, uint32_t* ctl,
+                                   uint32_t* redo_list, hipStream_t s);
 // u64 look-back words of the fast encoder for n units (status argument size).
 uint64_t encode_fast_status_words(uint64_t n_units);
 hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,

@@ -48,8 +48,9 @@ __global__ void __launch_bounds__(256) build_enc_table_kernel(TableArg t, EncSym
 
 // The fast encoder's set-up in one launch: the encode entries (block 0), its
 // look-back status words cleared, and its control words (ctl[0]: ticket
-// counter, ctl[1]: redo-list length, ctl[2]: look-back failure flag, ctl[4..5]:
-// the packed total, written with the last unit's offset) cleared.
+// counter, ctl[1]: redo-list length, ctl[2]: failure flags, ctl[3]: the redo
+// launch's ticket counter, ctl[4..5]: the packed total, written with the last
+// unit's offset) cleared.
 __global__ void __launch_bounds__(256) build_enc_table_reset_kernel(TableArg t, EncSym* out, uint64_t* status,
                                                                     uint64_t n, uint32_t* ctl) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -1146,7 +1147,11 @@ __host__ __device__ constexpr uint32_t ws_lds_bytes(uint32_t pairs, uint32_t can
            2 * pairs * ws_region_bytes(stride0, stride1) + 32;
 }
 
-template <int SPE, bool ESC, bool SIDE, int PAIRS, int NPK>
+// LIST: the units a previous launch put on the redo list (ctl[1] of them in
+// redo_list) coded again with slots large enough for any lane (2 bytes per
+// row), at the offsets that launch published; tickets from ctl[3]; no sidecar,
+// no look-back.  A lane that outgrew even those slots would set ctl[2] bit 1.
+template <int SPE, bool ESC, bool SIDE, int PAIRS, int NPK, bool LIST = false>
 __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_waves_per_eu(4))) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
                                                                   const EncSym* __restrict__ d_enc,
                                                                   const uint32_t* __restrict__ canon, FastEncParams fp,
@@ -1156,6 +1161,7 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
                                                                   uint64_t* __restrict__ status, uint32_t* __restrict__ ctl,
                                                                   uint32_t* __restrict__ redo_list,
                                                                   uint64_t* __restrict__ phase) {
+    if (LIST && __hip_atomic_load(&ctl[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) return;  // nothing to redo
     extern __shared__ uint32_t lds[];
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
     constexpr uint32_t NT = 64 * (2 + NPK) * PAIRS;
@@ -1206,7 +1212,14 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
             const uint64_t t_wait = phase ? wall_clock64() : 0;
             if (i >= 2) ws_wait_ge(&pc.freed[s], i >> 1);  // set s given back
             if (rl == 0) {
-                if (j == 0) pc.unit[s] = atomicAdd(&ctl[0], 1u);  // ticket
+                if (j == 0) {  // ticket
+                    if (LIST) {
+                        const uint32_t t = atomicAdd(&ctl[3], 1u);
+                        pc.unit[s] = t < ctl[1] ? redo_list[t] : (uint32_t)g.n_units;
+                    } else {
+                        pc.unit[s] = atomicAdd(&ctl[0], 1u);
+                    }
+                }
                 ws_signal(&pc.tick, 1u, j);
             } else {
                 ws_wait_ge(&pc.tick, i + 1);
@@ -1346,6 +1359,12 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
                     for (uint32_t blk = (run + 63u) >> 6; (blk << 6) < run + cnt[b]; blk++) bmap_w[blk] = (uint8_t)(4 * j + b);
                 run += cnt[b];
             }
+        } else if (pw == 0 && LIST) {  // the offset published by the first launch
+            if (j == 0) {
+                const uint64_t off = unit_off[u];
+                pc.off[s][0] = (uint32_t)off;
+                pc.off[s][1] = (uint32_t)(off >> 32);
+            }
         } else if (pw == 0) {
             const uint64_t off = lookback_wave(status, g.n_units, u, size, &ctl[2], j);
             if (j == 0) {
@@ -1368,8 +1387,11 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
                 const uint8_t v = usrc[q];
                 dst[q] = byte_live(q, g.es, g.spe) ? v : 0;
             }
-        } else if (any_over) {  // bytes come from the general kernels
-            if (pw == 0 && j == 0) redo_list[atomicAdd(&ctl[1], 1u)] = u;
+        } else if (any_over) {  // bytes come from a redo launch
+            if (pw == 0 && j == 0) {
+                if (LIST) atomicOr(&ctl[2], 2u);  // (never: these slots hold 2 bytes per row)
+                else redo_list[atomicAdd(&ctl[1], 1u)] = u;
+            }
         } else {
             // Packed bytes in 16-byte destination chunks aligned in global memory,
             // 64 consecutive chunks (1 KiB of output, whole cache lines) per wave
@@ -1560,6 +1582,49 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
 #undef CKR_FAST_ENC
 #undef CKR_FAST_ENC_P
     return e;
+}
+
+// The redo list of a launch_encode_fast launch (ctl[1] units, queued once the
+// host has seen that there are some): one coder pair per workgroup with slots
+// of 2 bytes per row (any lane fits), one workgroup per CU.
+static uint32_t encode_fast_list_slot(const EncodeGeom& g) {
+    return (uint32_t)(2 * ((g.unit + 255) / 256) + 8 + 3) & ~3u;
+}
+
+bool encode_fast_list_fits(const FastEncParamsHost& hp, const EncodeGeom& g, uint32_t lds_limit) {
+    const uint32_t st = slot_stride(encode_fast_list_slot(g));
+    return ws_lds_bytes(1, hp.canon_bytes, st, st) <= lds_limit;
+}
+
+hipError_t launch_encode_fast_list(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
+                                   const FastEncParamsHost& hp, uint32_t lds_limit, ckr_stream_header* hdrs,
+                                   uint8_t* out, uint64_t* unit_off, uint64_t* status, uint32_t* ctl,
+                                   uint32_t* redo_list, hipStream_t s) {
+    if (!encode_fast_list_fits(hp, g, lds_limit)) return hipErrorInvalidValue;
+    FastEncParams fp;
+    fp.sl0 = fp.sl1 = encode_fast_list_slot(g);
+    fp.cw = hp.cw; fp.canon_bytes = hp.canon_bytes;
+    fp.stride0 = slot_stride(fp.sl0); fp.stride1 = slot_stride(fp.sl1);
+    const uint32_t lb = ws_lds_bytes(1, fp.canon_bytes, fp.stride0, fp.stride1);
+    int dev = 0, ncu = 0;
+    hipError_t e;
+    if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+    if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+    auto run = [&](auto kern) -> hipError_t {
+        const uint32_t nthreads = 64u * (2 + ENC_NPK);
+        hipError_t r = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)lb);
+        if (r != hipSuccess) return r;
+        const uint32_t grid = (uint32_t)std::min<uint64_t>(g.n_units, (uint64_t)std::max(ncu, 1));
+        CKR_LAUNCH("encode_fast_redo_kernel", s,
+                   kern<<<grid, nthreads, lb, s>>>(src, g, d_enc, canon, fp, hdrs, nullptr, out, unit_off, status, ctl,
+                                                   redo_list, nullptr));
+        return hipGetLastError();
+    };
+    if (g.spe == 2) return hp.escapes ? run(encode_fast_kernel<2, true, false, 1, ENC_NPK, true>)
+                                      : run(encode_fast_kernel<2, false, false, 1, ENC_NPK, true>);
+    return hp.escapes ? run(encode_fast_kernel<1, true, false, 1, ENC_NPK, true>)
+                      : run(encode_fast_kernel<1, false, false, 1, ENC_NPK, true>);
 }
 
 // ------------------------------------------------------------------ large units: two passes

@@ -495,7 +495,9 @@ CKR_API int ckr_make_contiguous(const void* d_src, int ndim, const int64_t* shap
  * streams are identical), units of at most 64 KiB coded and decoded through
  * LDS; mode 0: every lane coded and decoded independently through global
  * memory; mode 2: fast kernels with minimal LDS lane slots, so that nearly
- * every unit takes the overflow route back through the general kernels.  In
+ * every unit takes the overflow route back through the general kernels; mode
+ * 3: the same minimal slots, the overflowing units coded again by the fast
+ * encoder with slots that hold any lane (mode 1's overflow route).  In
  * mode 0 the prefix-mask repair build also recounts every pair each round
  * instead of keeping the counts up to date.  The output bytes are identical in
  * every mode; tests use this to cover all routes.  Process-wide; returns the

@@ -68,7 +68,7 @@ CASES = [
 ]
 
 
-@pytest.fixture(params=[1, 0, 2], ids=["fast", "general", "overflow"])
+@pytest.fixture(params=[1, 0, 2, 3], ids=["fast", "general", "overflow", "overflow_fast_redo"])
 def paths(request):
     ck = _ck()
     prev = ck.set_fast_paths(request.param)
@@ -106,6 +106,43 @@ def test_compress_parity_and_roundtrip(case, paths, gpu):
     torch.cuda.synchronize()
     assert bad == 0
     assert np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
+
+
+@pytest.mark.parametrize("mode", [1, 3, 2])
+def test_overflowing_units_take_the_redo_route(mode, gpu):
+    """Units of uniform random bits inside lognormal data outgrow the LDS slots
+    sized from the whole tensor: by default (mode 1) they, and in mode 3 (minimal
+    slots) every unit, are coded again by the fast encoder with slots that hold
+    any lane, with no general-kernel launch; mode 2 sends them through the
+    general kernels.  Bytes equal the oracle's."""
+    import torch
+    ck = _ck()
+    n = 65536 // 4 * 40 + 77
+    raw = dg.adversarial_f32(n, 31, (16384 * 7, 16384 * 12))
+    ref = oc.compress_tensor(raw, n, dg.F32, 65536)
+    src = _to_dev(raw, gpu)
+    prev = ck.set_fast_paths(mode)
+    try:
+        ck.compress(src, dg.F32, 65536, n_elems=n)   # warm-up
+        torch.cuda.synchronize()
+        ck.profile_begin()
+        enc = ck.compress(src, dg.F32, 65536, n_elems=n)
+        torch.cuda.synchronize()
+        prof = ck.profile_end()
+    finally:
+        ck.set_fast_paths(prev)
+    print(f"[case] redo route mode={mode}: {sorted(prof)}", flush=True)
+    if mode == 2:
+        assert "encode_kernel" in prof and "encode_fast_redo_kernel" not in prof
+    else:
+        assert "encode_kernel" not in prof and "compact_kernel" not in prof
+        assert mode == 1 or "encode_fast_redo_kernel" in prof
+    assert enc.total == ref["data"].size
+    assert np.array_equal(enc.headers_np()[: 41 * 256], ref["headers"])
+    assert np.array_equal(enc.data_np(), ref["data"])
+    dst, bad = ck.decode(enc)
+    torch.cuda.synchronize()
+    assert bad == 0 and np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
 
 
 @pytest.mark.parametrize("dt,gen", [

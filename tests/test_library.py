@@ -106,8 +106,10 @@ def test_argument_errors_are_status_codes():
 def test_fast_path_switch_round_trips():
     prev = ck.set_fast_paths(0)
     assert ck.set_fast_paths(2) == 0
-    assert ck.set_fast_paths(prev) == 2
-    assert ck.set_fast_paths(prev) == prev
+    assert ck.set_fast_paths(3) == 2
+    assert ck.set_fast_paths(prev) == 3
+    assert ck.set_fast_paths(4) == prev   # out of range: back to 1
+    assert ck.set_fast_paths(prev) == 1
 
 
 def test_repair_host_helpers():
