@@ -26,7 +26,7 @@ CKR_OK, CKR_E_INVALID, CKR_E_HIP, CKR_E_CAPACITY, CKR_E_TABLE, CKR_E_CORRUPT = 0
 EXPORTED = [  # every symbol include/checkers_amd.h declares
     "ckr_last_error", "ckr_version", "ckr_element_size", "ckr_sidecar_bytes_per_elem",
     "ckr_extract_mantissa", "ckr_byte_histogram", "ckr_byte_histogram_raw", "ckr_byte_histogram_planes",
-    "ckr_build_table",
+    "ckr_build_table", "ckr_build_table_ranked", "ckr_build_tables_device",
     "ckr_num_units", "ckr_encode_max_output_bytes", "ckr_encode_workspace_bytes", "ckr_encode",
     "ckr_encode_planes",
     "ckr_compress", "ckr_compress_many", "ckr_decode_workspace_bytes", "ckr_decode", "ckr_decode_many",
@@ -126,6 +126,8 @@ def lib():
         "ckr_byte_histogram_raw": (i32, [vp, u64, vp, vp]),
         "ckr_byte_histogram_planes": (i32, [vp, u64, i32, vp, vp]),
         "ckr_build_table": (i32, [vp, i32, vp, vp]),
+        "ckr_build_table_ranked": (i32, [vp, i32, vp, vp]),
+        "ckr_build_tables_device": (i32, [vp, u64, i32, vp, vp]),
         "ckr_num_units": (u64, [u64, i32, u64]),
         "ckr_encode_max_output_bytes": (u64, [u64, i32, u64]),
         "ckr_encode_workspace_bytes": (u64, [u64, i32, u64]),
@@ -227,6 +229,28 @@ def build_table(hist, ensure_full_alphabet=False):
     s = ctypes.c_uint32(0)
     _check(lib().ckr_build_table(h.ctypes.data, int(bool(ensure_full_alphabet)), t.ptr, ctypes.byref(s)))
     return t, s.value
+
+
+def build_table_ranked(hist, ensure_full_alphabet=False):
+    """The same table by ranks, without the sort (ckr_build_table_ranked):
+    (table, ambiguous); ambiguous: only the reference's sort order decides."""
+    h = np.ascontiguousarray(np.asarray(hist, dtype=np.uint32))
+    assert h.shape == (256,)
+    t = aligned_table()
+    amb = ctypes.c_int(0)
+    _check(lib().ckr_build_table_ranked(h.ctypes.data, int(bool(ensure_full_alphabet)), t.ptr, ctypes.byref(amb)))
+    return t, bool(amb.value)
+
+
+def build_tables_device(d_hists, ensure_full_alphabet=False, stream=None):
+    """n tables by ranks on the device from a (n, 256) uint32 (int32) device
+    tensor: a (n, 258) tensor of rows {norm_freq[256], sum, ambiguity flag}."""
+    torch = _torch()
+    assert d_hists.dim() == 2 and d_hists.shape[1] == 256 and d_hists.element_size() == 4 and d_hists.is_contiguous()
+    rows = torch.empty((d_hists.shape[0], 258), dtype=torch.int32, device=d_hists.device)
+    _check(lib().ckr_build_tables_device(d_hists.data_ptr(), d_hists.shape[0], int(bool(ensure_full_alphabet)),
+                                         rows.data_ptr(), _stream(stream)))
+    return rows
 
 
 # --------------------------------------------------------------- torch helpers

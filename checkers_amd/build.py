@@ -73,6 +73,7 @@ def _stale(src, obj):
     if not os.path.exists(obj):
         return True
     deps = [src, os.path.join(ROOT, "include", "checkers_amd.h"), os.path.join(CSRC, "ckr_internal.h"),
+            os.path.join(CSRC, "ckr_table.h"),
             os.path.join(CSRC, "ckr_container.h")]
     return any(os.path.getmtime(d) > os.path.getmtime(obj) for d in deps)
 

@@ -20,6 +20,7 @@
 
 #include "checkers_amd.h"
 #include "ckr_internal.h"
+#include "ckr_table.h"
 
 namespace {
 
@@ -256,7 +257,7 @@ bool use_seg_encode(const ckr::EncodeGeom& g) { return use_dedup(g) && (g.unit +
 struct PinnedWords {
     uint32_t* w = nullptr;  // kPinnedWords words
 };
-constexpr uint32_t kPinnedWords = 1024;
+constexpr uint32_t kPinnedWords = 2048;
 // ckr_compress_many counts every histogram before any encode when no job is
 // larger than this (cfg2's largest tensor, gate_proj, is 117 MB).
 constexpr uint64_t kManySmallJobBytes = 256ull << 20;
@@ -315,7 +316,7 @@ uint32_t lane_slot_bytes(const uint32_t* plane_hist, const ckr_freq_table* t, ui
 // (sized for the whole tensor's units, capped by kScratchBudget).
 struct EncodeLayout {
     uint64_t off_enc, off_hist, off_canon, off_status, off_ctl, off_redo, off_usize, off_rec, off_aux, off_list,
-        off_scratch, total;
+        off_scratch, off_tinfo, total;
     uint64_t batch_units;
 };
 
@@ -339,6 +340,7 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     L.off_aux = o;     o = align_up(o + (seg ? 512 : 0), kAlign);
     L.off_list = o;    o = align_up(o + (seg ? ckr::encode_seg_list_items(g.n_units, g.unit) * 8 : 0), kAlign);
     L.off_scratch = o; o = align_up(o + (seg ? 0 : bu * per_unit), kAlign);
+    L.off_tinfo = o;   o = align_up(o + ckr::kTinfoWords * 4, kAlign);
     L.total = o;
     return L;
 }
@@ -586,6 +588,59 @@ int ckr_byte_histogram_raw(const void* d_bytes, uint64_t n_bytes, uint32_t* d_hi
     return ckr_byte_histogram(d_bytes, n_bytes, CKR_I8, d_hist, stream);
 }
 
+}  // extern "C"
+
+namespace {
+// The rest of a table from its slot counts: cumulative counts, x_max and the
+// decode slots (normalize_histogram's tail and build_tables,
+// src/ANSCompressor.cpp:495-503).
+void fill_table(const uint32_t* norm, ckr_freq_table* t) {
+    t->cum_freq[0] = 0;
+    for (int i = 0; i < 256; i++) { t->norm_freq[i] = norm[i]; t->cum_freq[i + 1] = t->cum_freq[i] + norm[i]; }
+    for (int s = 0; s < 256; s++) {
+        if (!norm[s]) continue;
+        t->x_max[s] = CKR_NORM_BASE * norm[s];
+        for (uint32_t j = t->cum_freq[s]; j < t->cum_freq[s + 1] && j < CKR_M; j++) {
+            t->decode_sym[j] = (uint8_t)s;
+            t->decode_freq[j] = norm[s];
+            t->decode_cum[j] = t->cum_freq[s];
+        }
+    }
+}
+
+// The slot counts by ranks (ckr_table.h), one symbol at a time, as the device
+// computes them one symbol per thread; true when a correction boundary cuts a
+// group of equal fractional parts (then only libstdc++'s sort decides).
+bool ranked_norm(const uint32_t* h, bool ensure_full, uint32_t* norm) {
+    uint64_t total = 0;
+    int distinct = 0;
+    for (int i = 0; i < 256; i++) { total += h[i]; distinct += h[i] > 0; }
+    for (int i = 0; i < 256; i++) norm[i] = 0;
+    if ((ensure_full ? 256 : distinct) == 0) {
+        norm[0] = CKR_M;
+        return false;
+    }
+    ckr::NormStart r[256];
+    double up[256], down[256];
+    uint32_t assigned = 0;
+    for (int i = 0; i < 256; i++) {
+        r[i] = ckr::norm_start(h[i], total, ensure_full);
+        up[i] = ckr::norm_key_up(r[i]);
+        down[i] = ckr::norm_key_down(r[i]);
+        assigned += r[i].norm;
+    }
+    bool amb = false;
+    for (uint32_t i = 0; i < 256; i++) {
+        const int f = ckr::norm_fix(r[i].norm, r[i].frac, r[i].inc, up, down, assigned);
+        amb |= f == ckr::kNormAmbiguous;
+        norm[i] = r[i].norm + (f == 1 ? 1u : 0u) - (f == -1 ? 1u : 0u);
+    }
+    return amb;
+}
+}  // namespace
+
+extern "C" {
+
 // ANSCompressor::normalize_histogram (src/ANSCompressor.cpp:416-503): proportional
 // slots, then one correction pass ordered by libstdc++ std::sort of the
 // fractional parts (descending, ties in the order that sort leaves them).
@@ -628,18 +683,29 @@ int ckr_build_table(const uint32_t* h, int ensure_full_alphabet, ckr_freq_table*
         for (int k = (int)fr.size() - 1; k >= 0 && rem; k--)
             if (norm[fr[k].sym] > 1) { norm[fr[k].sym]--; rem--; }
     }
-    t->cum_freq[0] = 0;
-    for (int i = 0; i < 256; i++) { t->norm_freq[i] = norm[i]; t->cum_freq[i + 1] = t->cum_freq[i] + norm[i]; }
-    for (int s = 0; s < 256; s++) {
-        if (!norm[s]) continue;
-        t->x_max[s] = CKR_NORM_BASE * norm[s];
-        for (uint32_t j = t->cum_freq[s]; j < t->cum_freq[s + 1] && j < CKR_M; j++) {
-            t->decode_sym[j] = (uint8_t)s;
-            t->decode_freq[j] = norm[s];
-            t->decode_cum[j] = t->cum_freq[s];
-        }
-    }
+    fill_table(norm, t);
     if (h_table_sum) *h_table_sum = t->cum_freq[256];
+    return CKR_OK;
+}
+
+int ckr_build_tables_device(const uint32_t* d_hists, uint64_t n, int ensure_full_alphabet, uint32_t* d_rows,
+                            void* stream) {
+    if (n == 0) return CKR_OK;
+    if (!d_hists || !d_rows) return fail(CKR_E_INVALID, "[ckr] null pointer");
+    if (!aligned_to(d_hists, 4) || !aligned_to(d_rows, 4)) return fail(CKR_E_INVALID, "[ckr] tables need 4-byte alignment");
+    int rc;
+    if ((rc = check_buffer(d_hists, n * 256 * 4, "histograms")) || (rc = check_buffer(d_rows, n * 258 * 4, "rows")))
+        return rc;
+    CKR_HIP(ckr::launch_tables(d_hists, n, ensure_full_alphabet, d_rows, (hipStream_t)stream));
+    return CKR_OK;
+}
+
+int ckr_build_table_ranked(const uint32_t* h, int ensure_full_alphabet, ckr_freq_table* t, int* ambiguous) {
+    if (!h || !t || !ambiguous) return fail(CKR_E_INVALID, "[ckr] null pointer");
+    std::memset(t, 0, sizeof(*t));
+    uint32_t norm[256];
+    *ambiguous = ranked_norm(h, ensure_full_alphabet != 0, norm) ? 1 : 0;
+    fill_table(norm, t);
     return CKR_OK;
 }
 
@@ -1046,6 +1112,103 @@ int ckr_encode_planes(const void* d_src, uint64_t n_elems, int dtype, const ckr_
                               d_headers, d_unit_offsets, d_sidecar, d_workspace, workspace_bytes, h_total_out, stream);
 }
 
+}  // extern "C"
+
+namespace {
+constexpr int kUseHostTable = 1;  // compress_device_table: take the host's sorted table instead
+
+// The symbol-0 state chains of every count (ckr::launch_canon_chains), one
+// buffer per device, made and filled on first use on the caller's stream (so
+// that the first encode finds them filled) and kept for the process.
+const void* canon_chains(hipStream_t s) {
+    static std::mutex mu;
+    static std::vector<void*> per_dev;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) { (void)hipGetLastError(); return nullptr; }
+    std::lock_guard<std::mutex> lk(mu);
+    if ((int)per_dev.size() <= dev) per_dev.resize(dev + 1, nullptr);
+    if (!per_dev[dev]) {
+        void* p = nullptr;
+        if (hipMalloc(&p, ckr::kChainBytes) != hipSuccess) { (void)hipGetLastError(); return nullptr; }
+        if (ckr::launch_canon_chains(p, s) != hipSuccess) { (void)hipGetLastError(); (void)hipFree(p); return nullptr; }
+        per_dev[dev] = p;
+    }
+    return per_dev[dev];
+}
+
+// ckr_compress with the table built on the device (tensors the fast encoder
+// takes: masked dtypes, units of at most 64 KiB): histogram, table by ranks,
+// encode entries, canonical streams and slot sizes, and the encode queue
+// without a host round trip; one read-back of the control words and the table
+// at the end.  Returns kUseHostTable when the ranks leave the table to
+// libstdc++'s sort (a correction boundary inside a group of equal fractional
+// parts) or the LDS cannot hold the largest slots; the outputs are then
+// rewritten by the host-table path.
+int compress_device_table(const void* src, const ckr::EncodeGeom& g, int ensure_full_alphabet, uint8_t* d_out,
+                          ckr_stream_header* d_headers, uint64_t* d_unit_offsets, uint8_t* d_sidecar, uint8_t* ws,
+                          const EncodeLayout& L, ckr_freq_table* h_table, uint64_t* h_total_out, hipStream_t s) {
+    const CanonKs ck = canon_ks(g);
+    const uint32_t K = (uint32_t)((g.unit + 255) / 256);
+    const uint32_t lds_limit = (uint32_t)max_lds_per_block();
+    ckr::FastEncParamsHost fp{};
+    fp.escapes = false;  // the table is the data's own: every symbol present has a slot
+    fp.cw = ck.cw;
+    fp.canon_bytes = 4 * ck.cw;
+    const uint32_t smax = ckr::encode_fast_max_slot(fp.canon_bytes, K, lds_limit);
+    if (!smax || ck.cw > ckr::kCanonMaxCw) return kUseHostTable;
+    fp.sl0 = fp.sl1 = smax;
+    if (!ckr::encode_fast_lds_bytes(fp, lds_limit)) return kUseHostTable;
+    auto* enc = reinterpret_cast<ckr::EncSym*>(ws + L.off_enc);
+    auto* hist = reinterpret_cast<uint32_t*>(ws + L.off_hist);
+    auto* canon = reinterpret_cast<uint32_t*>(ws + L.off_canon);
+    auto* status = reinterpret_cast<uint64_t*>(ws + L.off_status);
+    auto* ctl = reinterpret_cast<uint32_t*>(ws + L.off_ctl);
+    auto* redo = reinterpret_cast<uint32_t*>(ws + L.off_redo);
+    auto* tinfo = reinterpret_cast<uint32_t*>(ws + L.off_tinfo);
+    uint32_t* pw = pinned_words();
+    if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
+    const void* chains = canon_chains(s);
+    if (!chains) return kUseHostTable;
+    const uint8_t* s8 = static_cast<const uint8_t*>(src);
+    CKR_HIP(ckr::launch_masked_hist(s8, g.n_bytes, g.es, g.spe, hist, hist + 256, s));
+    CKR_HIP(ckr::launch_table_enc(hist, g, ensure_full_alphabet, K, ck.k0, ck.k1, ck.k2, ck.cw, smax, enc, canon, tinfo,
+                                  status, ctl, chains, s));
+    CKR_HIP(ckr::launch_encode_fast(s8, g, enc, canon, fp, lds_limit, d_headers, d_sidecar, d_out, d_unit_offsets,
+                                    status, ctl, redo, s, tinfo + 258));
+    CKR_HIP(hipMemcpyAsync(pw, ctl, 24, hipMemcpyDeviceToHost, s));
+    CKR_HIP(hipMemcpyAsync(pw + 8, tinfo, ckr::kTinfoWords * 4, hipMemcpyDeviceToHost, s));
+    CKR_HIP(hipStreamSynchronize(s));
+    uint32_t hctl[6], ti[ckr::kTinfoWords];
+    std::memcpy(hctl, pw, sizeof(hctl));
+    std::memcpy(ti, pw + 8, sizeof(ti));
+    if (ti[257]) return kUseHostTable;
+    if (hctl[2]) return fail(CKR_E_HIP, "[ckr] fast encode did not complete (flags %u: 1 look-back, 2 redo slots)", hctl[2]);
+    if (h_table) {
+        std::memset(h_table, 0, sizeof(*h_table));
+        fill_table(ti, h_table);
+    }
+    if (h_total_out) std::memcpy(h_total_out, &hctl[4], 8);
+    if (hctl[1]) {  // units that outgrew their slots
+        if (ckr::encode_fast_list_fits(fp, g, lds_limit)) {
+            CKR_HIP(ckr::launch_encode_fast_list(s8, g, enc, canon, fp, lds_limit, d_headers, d_out, d_unit_offsets,
+                                                 status, ctl, redo, s));
+        } else {
+            auto* usize = reinterpret_cast<uint32_t*>(ws + L.off_usize);
+            auto* scratch = reinterpret_cast<uint32_t*>(ws + L.off_scratch);
+            for (uint64_t r0 = 0; r0 < hctl[1]; r0 += L.batch_units) {
+                const uint64_t nb = std::min<uint64_t>(L.batch_units, hctl[1] - r0);
+                CKR_HIP(ckr::launch_encode_batch(s8, g, r0, nb, enc, canon, ck.cw, true, scratch, d_headers, nullptr,
+                                                 usize, d_unit_offsets, d_out, redo, s));
+            }
+        }
+        CKR_HIP(hipStreamSynchronize(s));  // the output complete, as on the other paths
+    }
+    return CKR_OK;
+}
+}  // namespace
+
+extern "C" {
+
 int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_bytes, int ensure_full_alphabet,
                  uint8_t* d_out, uint64_t out_capacity, ckr_stream_header* d_headers, uint64_t* d_unit_offsets,
                  uint8_t* d_sidecar, void* d_workspace, uint64_t workspace_bytes, ckr_freq_table* h_table,
@@ -1065,6 +1228,16 @@ int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_b
     hipStream_t s = (hipStream_t)stream;
     Staged st;
     if ((rc = st.make(d_src, g.n_bytes, s))) return rc;
+    // the fast encoder's tensors: the table on the device, no host round trip
+    // before the encode (mode 1; modes 2 and 3 size the slots on the host)
+    if (g_fast_paths == 1 && use_fast_encode(g)) {
+        rc = compress_device_table(st.p, g, ensure_full_alphabet, d_out, d_headers, d_unit_offsets, d_sidecar,
+                                   static_cast<uint8_t*>(d_workspace), L, h_table, h_total_out, s);
+        if (rc != kUseHostTable) {
+            st.release(s);
+            return rc;
+        }
+    }
     uint32_t* d_hist = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(d_workspace) + L.off_hist);
     const int es = ckr_element_size(dtype);
     hipError_t he = ckr::launch_masked_hist(static_cast<const uint8_t*>(st.p), n_elems * (uint64_t)es, es, g.spe, d_hist,

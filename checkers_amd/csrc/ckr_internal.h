@@ -140,10 +140,34 @@ hipError_t launch_encode_fast_list(const uint8_t* src, const EncodeGeom& g, cons
                                    uint32_t* redo_list, hipStream_t s);
 // u64 look-back words of the fast encoder for n units (status argument size).
 uint64_t encode_fast_status_words(uint64_t n_units);
+// dsl (may be null): the two slot sizes in device memory (table_enc's tinfo +
+// 258), used instead of hp's; hp's are then the largest the LDS holds.
 hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
                               const FastEncParamsHost& hp, uint32_t lds_limit, ckr_stream_header* hdrs,
                               uint8_t* sidecar, uint8_t* out, uint64_t* unit_off, uint64_t* status, uint32_t* ctl,
-                              uint32_t* redo_list, hipStream_t s);
+                              uint32_t* redo_list, hipStream_t s, const uint32_t* dsl = nullptr);
+// Tables by ranks on the device (ckr_table.h): n histograms of 256 words into
+// rows of 258 (norm_freq[256], sum, ambiguity flag).
+hipError_t launch_tables(const uint32_t* hists, uint64_t n, int ensure_full, uint32_t* rows, hipStream_t s);
+// A tensor's encode set-up from its 768-word histograms (masked, plane FL,
+// plane 3) with no host round trip: table by ranks, encode entries, canonical
+// zero-plane streams for lane counts k0, k1, k2 (cw dwords), the fast
+// encoder's slot sizes (each at most smax, their sum at most 2 smax), and its
+// status and control words cleared.  tinfo: norm[256], sum, ambiguity, sl0, sl1.
+// chains: the state chains of symbol 0 for every count (launch_canon_chains,
+// kChainBytes, built once per device), from which the canonical streams are read.
+hipError_t launch_table_enc(const uint32_t* hist, const EncodeGeom& g, int ensure_full, uint32_t K, uint32_t k0,
+                            uint32_t k1, uint32_t k2, uint32_t cw, uint32_t smax, EncSym* d_enc, uint32_t* canon,
+                            uint32_t* tinfo, uint64_t* status, uint32_t* ctl, const void* chains, hipStream_t s);
+constexpr uint32_t kChainRows = 4097;  // symbol-0 counts 0 .. 4096
+constexpr uint32_t kChainSteps = 256;  // the most rows of a fast-encoder unit
+constexpr uint64_t kChainBytes = (4ull + 2ull) * (kChainSteps + 1) * kChainRows + (2ull * kChainSteps + 8) * kChainRows;
+hipError_t launch_canon_chains(void* chains, hipStream_t s);
+constexpr uint32_t kTinfoWords = 260;
+constexpr uint32_t kCanonMaxCw = 136;  // canonical stream dwords table_enc handles (K <= 256)
+// The largest slot (multiple of 4, at most 2K + 8) whose two-pair layout of the
+// fast encoder fits lds_cap (0: none).
+uint32_t encode_fast_max_slot(uint32_t canon_bytes, uint32_t K, uint32_t lds_cap);
 
 // Units above 64 KiB of masked dtypes, in two passes (no lane scratch): rec
 // holds n_units * encode_seg_segments(unit) * 128 checkpoint records, unit_size

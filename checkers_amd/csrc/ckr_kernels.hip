@@ -18,6 +18,7 @@
 #include <cstdint>
 
 #include "ckr_internal.h"
+#include "ckr_table.h"
 
 namespace ckr {
 
@@ -26,8 +27,7 @@ static constexpr uint32_t L = 1u << 23;
 
 // ------------------------------------------------------------------ tables
 // Encode entries from norm/cum (see EncSym in ckr_internal.h for the algebra).
-__device__ __forceinline__ EncSym enc_entry(const TableArg& t, uint32_t s) {
-    const uint32_t f = t.norm[s], cum = t.cum[s];
+__device__ __forceinline__ EncSym enc_entry_fc(uint32_t f, uint32_t cum) {
     EncSym e;
     if (f == 0) {
         e.rcp = 0; e.bias = 0; e.cmpl_rsh = 0; e.xmax = 0;
@@ -40,6 +40,219 @@ __device__ __forceinline__ EncSym enc_entry(const TableArg& t, uint32_t s) {
         e.rcp = (uint32_t)rcp; e.bias = cum; e.cmpl_rsh = (M - f) | ((l - 1) << 16); e.xmax = f << 19;
     }
     return e;
+}
+__device__ __forceinline__ EncSym enc_entry(const TableArg& t, uint32_t s) { return enc_entry_fc(t.norm[s], t.cum[s]); }
+
+// ------------------------------------------------------------------ tables on the device
+// A table by ranks (ckr_table.h) in one workgroup of 256 threads, thread s for
+// symbol s: the counts and their exclusive sums in LDS, the ambiguity flag.
+struct RankTable {
+    uint32_t norm[256], cum[257];
+    double up[256], down[256];
+    unsigned long long red64[4];
+    uint32_t red[4], amb;
+};
+
+__device__ __forceinline__ uint64_t block_sum64_256(uint64_t v, unsigned long long* sh) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return sh[0] + sh[1] + sh[2] + sh[3];
+}
+
+__device__ void rank_table(const uint32_t* __restrict__ hist, bool ensure_full, RankTable& T) {
+    const uint32_t s = threadIdx.x;
+    const uint32_t h = hist[s];
+    const uint64_t total = block_sum64_256(h, T.red64);
+    const uint64_t distinct = block_sum64_256(h ? 1u : 0u, T.red64);
+    if ((ensure_full ? 256u : distinct) == 0) {  // no symbol at all: every slot for symbol 0
+        T.norm[s] = s == 0 ? kTabM : 0u;
+        T.cum[s] = s == 0 ? 0u : kTabM;
+        if (s == 0) { T.cum[256] = kTabM; T.amb = 0; }
+        __syncthreads();
+        return;
+    }
+    const NormStart r = norm_start(h, total, ensure_full);
+    T.up[s] = norm_key_up(r);
+    T.down[s] = norm_key_down(r);
+    const uint32_t assigned = (uint32_t)block_sum64_256(r.norm, T.red64);  // (syncs: the keys visible)
+    const int f = norm_fix(r.norm, r.frac, r.inc, T.up, T.down, assigned);
+    const uint32_t nm = r.norm + (f == 1 ? 1u : 0u) - (f == -1 ? 1u : 0u);
+    T.norm[s] = nm;
+    const uint64_t amb = block_sum64_256(f == kNormAmbiguous ? 1u : 0u, T.red64);
+    // exclusive sum of the counts
+    uint32_t inc = nm;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t g = (uint32_t)__shfl_up((int)inc, o, 64);
+        if ((int)(s & 63) >= o) inc += g;
+    }
+    if ((s & 63) == 63) T.red[s >> 6] = inc;
+    __syncthreads();
+    uint32_t pre = 0;
+    for (uint32_t w = 0; w < (s >> 6); w++) pre += T.red[w];
+    T.cum[s + 1] = pre + inc;
+    if (s == 0) { T.cum[0] = 0; T.amb = amb ? 1u : 0u; }
+    __syncthreads();
+}
+
+// ckr_build_tables_device: one table per workgroup into a row of 258 words.
+__global__ void __launch_bounds__(256) tables_kernel(const uint32_t* __restrict__ hists, int ensure_full,
+                                                     uint32_t* __restrict__ rows) {
+    __shared__ RankTable T;
+    rank_table(hists + (uint64_t)blockIdx.x * 256, ensure_full != 0, T);
+    uint32_t* row = rows + (uint64_t)blockIdx.x * 258;
+    row[threadIdx.x] = T.norm[threadIdx.x];
+    if (threadIdx.x == 0) { row[256] = T.cum[256]; row[257] = T.amb; }
+}
+
+// The encode set-up of a tensor from its histograms on the device (no host
+// round trip): the table by ranks, the encode entries, the canonical
+// zero-plane streams, the fast encoder's LDS slot sizes, and its look-back
+// status and control words cleared (as build_enc_table_reset_kernel).  tinfo:
+// norm[256], sum, ambiguity flag, slot bytes of the two live planes.  The slot
+// sizes follow lane_slot_bytes on the host (expected coded size of K symbols
+// from the plane histograms plus six standard deviations), then the larger is
+// cut until both fit the launch's LDS (sum at most 2 smax).
+struct TableEncArg {
+    uint32_t K, k0, k1, k2, cw, smax;
+    int ensure_full;
+};
+
+// The state chains of symbol 0 for every count f in [0, 4096] (f == 0: every
+// symbol the raw-byte escape), 256 steps each from state L, computed once per
+// device (canon_chain_kernel, thread f): before step k, the state
+// chain_x[k * kChainRows + f] and the bytes pushed so far chain_n[..]; the
+// pushed bytes chain_b[j * kChainRows + f].  The canonical zero-plane streams
+// of a table are then lookups (canon_entries_dev) instead of a serial chain.
+__global__ void __launch_bounds__(256) canon_chain_kernel(uint32_t* __restrict__ chain_x, uint16_t* __restrict__ chain_n,
+                                                          uint8_t* __restrict__ chain_b) {
+    const uint32_t f = blockIdx.x * 256 + threadIdx.x;
+    if (f >= kChainRows) return;
+    const EncSym e = enc_entry_fc(f > M ? M : f, 0);
+    const uint32_t rsh = e.cmpl_rsh >> 16, cm = e.cmpl_rsh & 0xFFFFu;
+    uint32_t x = L, nb = 0;
+    for (uint32_t k = 0; k <= kChainSteps; k++) {
+        chain_x[k * kChainRows + f] = x;
+        chain_n[k * kChainRows + f] = (uint16_t)nb;
+        if (k == kChainSteps) break;
+        if (f == 0) { chain_b[nb++ * kChainRows + f] = 0; continue; }
+        const bool e1 = x >= e.xmax;
+        const uint32_t x1 = e1 ? x >> 8 : x;
+        const bool e2 = e1 && x1 >= e.xmax;
+        if (e1) chain_b[nb++ * kChainRows + f] = (uint8_t)x;
+        if (e2) chain_b[nb++ * kChainRows + f] = (uint8_t)x1;
+        const uint32_t xr = e2 ? x1 >> 8 : x1;
+        const uint32_t q = __umulhi(xr, e.rcp) >> rsh;
+        x = xr + e.bias + __umul24(q, cm);
+    }
+}
+
+// The canonical zero-plane streams (canon_host's layout) of lane counts Ks[3]
+// for symbol 0 of count f, from the chains: the pushed bytes into LDS, then
+// every dword of the three entries and streams in parallel.
+__device__ void canon_entries_dev(uint32_t f, const uint32_t (&Ks)[3], uint32_t cw, const uint32_t* __restrict__ chain_x,
+                                  const uint16_t* __restrict__ chain_n, const uint8_t* __restrict__ chain_b,
+                                  uint32_t* __restrict__ canon) {
+    __shared__ uint8_t pb[2 * kChainSteps + 8];
+    __shared__ uint32_t ex[3], eb[3];
+    __shared__ uint32_t slt[3][kCanonMaxCw];
+    const uint32_t s = threadIdx.x;
+    if (s < 3) { ex[s] = chain_x[Ks[s] * kChainRows + f]; eb[s] = chain_n[Ks[s] * kChainRows + f]; }
+    const uint32_t kmax = max(Ks[0], max(Ks[1], Ks[2]));
+    const uint32_t nmax = chain_n[kmax * kChainRows + f];
+    for (uint32_t j = s; j < nmax; j += blockDim.x) pb[j] = chain_b[j * kChainRows + f];
+    __syncthreads();
+    // slots: dword w of an entry holds pushed bytes 4w..4w+3, the first in the
+    // top byte; the last, partial one its r bytes the same way
+    for (uint32_t i = s; i < 3 * cw; i += blockDim.x) {
+        const uint32_t en = i / cw, d = i % cw, B = eb[en], w = B >> 2, r = B & 3u;
+        uint32_t v = 0;
+        if (d < w) v = ((uint32_t)pb[4 * d] << 24) | ((uint32_t)pb[4 * d + 1] << 16) | ((uint32_t)pb[4 * d + 2] << 8) | pb[4 * d + 3];
+        else if (d == w) for (uint32_t j = 0; j < r; j++) v = (v << 8) | pb[4 * w + j];
+        slt[en][d] = v;
+        canon[en * (4 + cw) + 4 + d] = v;
+    }
+    if (s < 3) {
+        uint32_t* base = canon + s * (4 + cw);
+        base[0] = Ks[s]; base[1] = ex[s]; base[2] = eb[s]; base[3] = 0;
+    }
+    __syncthreads();
+    // the streams in byte order
+    for (uint32_t i = s; i < 3 * cw; i += blockDim.x) {
+        const uint32_t en = i / cw, d = i % cw, B = eb[en], w = B >> 2, r = B & 3u;
+        uint32_t v = 0;
+        for (uint32_t b = 0; b < 4; b++) {
+            const uint32_t q = 4 * d + b;
+            if (q >= B) break;
+            const uint32_t slot = q < r ? w : w - 1 - ((q - r) >> 2);
+            const uint32_t byte = q < r ? q : (q - r) & 3;
+            v |= ((slt[en][slot] >> (8 * byte)) & 255u) << (8 * b);
+        }
+        canon[3 * (4 + cw) + en * cw + d] = v;
+    }
+}
+
+__global__ void __launch_bounds__(256) table_enc_kernel(const uint32_t* __restrict__ hist, TableEncArg a,
+                                                        EncSym* __restrict__ enc, uint32_t* __restrict__ canon,
+                                                        uint32_t* __restrict__ tinfo, uint64_t* __restrict__ status,
+                                                        uint64_t n_status, uint32_t* __restrict__ ctl,
+                                                        const uint32_t* __restrict__ chain_x,
+                                                        const uint16_t* __restrict__ chain_n,
+                                                        const uint8_t* __restrict__ chain_b) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n_status; i += (uint64_t)gridDim.x * 256)
+        status[i] = 0;
+    if (blockIdx.x != 0) return;
+    __shared__ RankTable T;
+    __shared__ double sm[2][4];
+    rank_table(hist, a.ensure_full != 0, T);
+    const uint32_t s = threadIdx.x;
+    enc[s] = enc_entry_fc(T.norm[s], T.cum[s]);
+    tinfo[s] = T.norm[s];
+    if (s < 6) ctl[s] = 0;
+    // slot sizes: per plane p, n = sum h_p, m = sum h_p cost / n, v = sum h_p (cost - m)^2 / n
+    const double cost = T.norm[s] ? log2((double)M / (double)T.norm[s]) : 8.0;
+    double mean[2], var[2], cnt[2];
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const double hp = (double)hist[256 + 256 * p + s];
+        double x0 = hp, x1 = hp * cost;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) { x0 += __shfl_xor(x0, o, 64); x1 += __shfl_xor(x1, o, 64); }
+        __syncthreads();
+        if ((s & 63) == 0) { sm[0][s >> 6] = x0; sm[1][s >> 6] = x1; }
+        __syncthreads();
+        cnt[p] = sm[0][0] + sm[0][1] + sm[0][2] + sm[0][3];
+        mean[p] = cnt[p] > 0 ? (sm[1][0] + sm[1][1] + sm[1][2] + sm[1][3]) / cnt[p] : 0.0;
+        double x2 = hp * (cost - mean[p]) * (cost - mean[p]);
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) x2 += __shfl_xor(x2, o, 64);
+        __syncthreads();
+        if ((s & 63) == 0) sm[0][s >> 6] = x2;
+        __syncthreads();
+        var[p] = cnt[p] > 0 ? (sm[0][0] + sm[0][1] + sm[0][2] + sm[0][3]) / cnt[p] : 0.0;
+    }
+    if (s == 0) {
+        uint32_t sl[2];
+        for (int p = 0; p < 2; p++) {
+            if (cnt[p] == 0) { sl[p] = 8; continue; }
+            const double bits = a.K * mean[p] + 6.0 * sqrt(a.K * var[p]) + 32.0;
+            uint64_t bytes = (uint64_t)ceil(bits / 8.0) + 8;
+            bytes = (bytes + 3) & ~3ull;
+            bytes = bytes < 8 ? 8 : bytes;
+            sl[p] = (uint32_t)(bytes < 2ull * a.K + 8 ? bytes : 2ull * a.K + 8);
+        }
+        while (sl[0] + sl[1] > 2 * a.smax && (sl[0] > 8 || sl[1] > 8)) (sl[0] >= sl[1] ? sl[0] : sl[1]) -= 4;
+        tinfo[256] = T.cum[256];
+        tinfo[257] = T.amb;
+        tinfo[258] = sl[0];
+        tinfo[259] = sl[1];
+    }
+    // canonical zero-plane streams of symbol 0 for the three lane counts
+    const uint32_t Ks[3] = {a.k0, a.k1, a.k2};
+    canon_entries_dev(T.norm[0], Ks, a.cw, chain_x, chain_n, chain_b, canon);
 }
 
 __global__ void __launch_bounds__(256) build_enc_table_kernel(TableArg t, EncSym* out) {
@@ -1135,6 +1348,9 @@ __device__ __forceinline__ void ws_signal(uint32_t* p, uint32_t v, uint32_t lane
     if (lane == 0) (void)__hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// 4 bytes between slots: a stream that fills its slot exactly still writes one
+// dword below its start (the final partial dword, empty)
+__host__ __device__ constexpr uint32_t slot_stride(uint32_t sl) { return sl + 4; }
 __host__ __device__ constexpr uint32_t ws_ctl_offset(uint32_t canon_bytes) {
     return (FE_CBYTES + 3 * canon_bytes + 15u) & ~15u;
 }
@@ -1160,8 +1376,13 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
                                                                   uint64_t* __restrict__ unit_off,
                                                                   uint64_t* __restrict__ status, uint32_t* __restrict__ ctl,
                                                                   uint32_t* __restrict__ redo_list,
-                                                                  uint64_t* __restrict__ phase) {
+                                                                  uint64_t* __restrict__ phase,
+                                                                  const uint32_t* __restrict__ dsl) {
     if (LIST && __hip_atomic_load(&ctl[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) return;  // nothing to redo
+    if (dsl) {  // slot sizes made on the device (table_enc_kernel), within the launch's LDS
+        fp.sl0 = dsl[0]; fp.sl1 = dsl[1];
+        fp.stride0 = slot_stride(fp.sl0); fp.stride1 = slot_stride(fp.sl1);
+    }
     extern __shared__ uint32_t lds[];
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
     constexpr uint32_t NT = 64 * (2 + NPK) * PAIRS;
@@ -1515,11 +1736,6 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
     }
 }
 
-static uint32_t slot_stride(uint32_t sl) {
-    // 4 bytes between slots: a stream that fills its slot exactly still writes one
-    // dword below its start (the final partial dword, empty)
-    return sl + 4;
-}
 
 uint64_t encode_fast_status_words(uint64_t n_units) { return n_units + 2 * ((n_units + 63) / 64); }
 
@@ -1538,7 +1754,7 @@ uint32_t encode_fast_lds_bytes(const FastEncParamsHost& p, uint32_t lds_limit) {
 hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, const uint32_t* canon,
                               const FastEncParamsHost& hp, uint32_t lds_limit, ckr_stream_header* hdrs,
                               uint8_t* sidecar, uint8_t* out, uint64_t* unit_off, uint64_t* status, uint32_t* ctl,
-                              uint32_t* redo_list, hipStream_t s) {
+                              uint32_t* redo_list, hipStream_t s, const uint32_t* dsl) {
     uint64_t* phase = prof_phase_buffer(g.n_units * 8, s);
     FastEncParams fp;
     fp.sl0 = hp.sl0; fp.sl1 = hp.sl1; fp.cw = hp.cw; fp.canon_bytes = hp.canon_bytes;
@@ -1564,7 +1780,7 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
         const uint32_t grid = (uint32_t)std::min<uint64_t>(need, (uint64_t)per_cu * (uint64_t)std::max(ncu, 1));
         CKR_LAUNCH("encode_fast_kernel", s,
                    kern<<<grid, nthreads, lb, s>>>(src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status,
-                                                   ctl, redo_list, phase));
+                                                   ctl, redo_list, phase, dsl));
         return hipGetLastError();
     };
 #define CKR_FAST_ENC_P(SPE_, ESC_, SIDE_, NPK_)                                                                  \
@@ -1618,7 +1834,7 @@ hipError_t launch_encode_fast_list(const uint8_t* src, const EncodeGeom& g, cons
         const uint32_t grid = (uint32_t)std::min<uint64_t>(g.n_units, (uint64_t)std::max(ncu, 1));
         CKR_LAUNCH("encode_fast_redo_kernel", s,
                    kern<<<grid, nthreads, lb, s>>>(src, g, d_enc, canon, fp, hdrs, nullptr, out, unit_off, status, ctl,
-                                                   redo_list, nullptr));
+                                                   redo_list, nullptr, nullptr));
         return hipGetLastError();
     };
     if (g.spe == 2) return hp.escapes ? run(encode_fast_kernel<2, true, false, 1, ENC_NPK, true>)
@@ -3098,6 +3314,42 @@ hipError_t launch_build_enc_table_reset(const TableArg& t, EncSym* d_enc, uint64
     CKR_LAUNCH("build_enc_table_reset_kernel", s,
                build_enc_table_reset_kernel<<<grid, 256, 0, s>>>(t, d_enc, status, nst, ctl));
     return hipGetLastError();
+}
+hipError_t launch_tables(const uint32_t* hists, uint64_t n, int ensure_full, uint32_t* rows, hipStream_t s) {
+    for (uint64_t b0 = 0; b0 < n; b0 += 1u << 30) {
+        const uint32_t nb = (uint32_t)std::min<uint64_t>(n - b0, 1u << 30);
+        CKR_LAUNCH("tables_kernel", s, tables_kernel<<<nb, 256, 0, s>>>(hists + b0 * 256, ensure_full, rows + b0 * 258));
+    }
+    return hipGetLastError();
+}
+hipError_t launch_canon_chains(void* chains, hipStream_t s) {
+    uint8_t* p = static_cast<uint8_t*>(chains);
+    auto* cx = reinterpret_cast<uint32_t*>(p);
+    auto* cn = reinterpret_cast<uint16_t*>(p + 4ull * (kChainSteps + 1) * kChainRows);
+    auto* cb = p + 6ull * (kChainSteps + 1) * kChainRows;
+    CKR_LAUNCH("canon_chain_kernel", s, canon_chain_kernel<<<(kChainRows + 255) / 256, 256, 0, s>>>(cx, cn, cb));
+    return hipGetLastError();
+}
+hipError_t launch_table_enc(const uint32_t* hist, const EncodeGeom& g, int ensure_full, uint32_t K, uint32_t k0,
+                            uint32_t k1, uint32_t k2, uint32_t cw, uint32_t smax, EncSym* d_enc, uint32_t* canon,
+                            uint32_t* tinfo, uint64_t* status, uint32_t* ctl, const void* chains, hipStream_t s) {
+    const uint64_t nst = encode_fast_status_words(g.n_units);
+    const uint32_t grid = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>((nst + 255) / 256, 4096));
+    const TableEncArg a{K, k0, k1, k2, cw, smax, ensure_full};
+    const uint8_t* p = static_cast<const uint8_t*>(chains);
+    const auto* cx = reinterpret_cast<const uint32_t*>(p);
+    const auto* cn = reinterpret_cast<const uint16_t*>(p + 4ull * (kChainSteps + 1) * kChainRows);
+    const uint8_t* cb = p + 6ull * (kChainSteps + 1) * kChainRows;
+    CKR_LAUNCH("table_enc_kernel", s,
+               table_enc_kernel<<<grid, 256, 0, s>>>(hist, a, d_enc, canon, tinfo, status, nst, ctl, cx, cn, cb));
+    return hipGetLastError();
+}
+// The largest slot (bytes, a multiple of 4, at most 2K + 8) whose two-pair
+// layout fits lds_cap.
+uint32_t encode_fast_max_slot(uint32_t canon_bytes, uint32_t K, uint32_t lds_cap) {
+    uint32_t sl = (2 * K + 8 + 3) & ~3u;
+    while (sl > 8 && ws_lds_bytes(2, canon_bytes, slot_stride(sl), slot_stride(sl)) > lds_cap) sl -= 4;
+    return ws_lds_bytes(2, canon_bytes, slot_stride(sl), slot_stride(sl)) <= lds_cap ? sl : 0u;
 }
 hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, unsigned long long* bad, hipStream_t s) {
     CKR_LAUNCH("build_dec_table_kernel", s, build_dec_table_kernel<<<16, 256, 0, s>>>(t, d_dec, bad));

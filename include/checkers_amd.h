@@ -15,6 +15,7 @@
  *                              (src/ANSCompressor.cpp:109-126, launch :1225-1236)
  *   - ckr_byte_histogram_raw ← ANSCompressor::build_byte_histogram (src/ANSCompressor.cpp:393-411)
  *   - ckr_build_table        ← ANSCompressor::normalize_histogram (src/ANSCompressor.cpp:416-503)
+ *   - ckr_build_table_ranked, ckr_build_tables_device ← the same, by ranks (host / device)
  *   - ckr_encode             ← rans_encode_kernel + compact_streams_kernel + the host prefix
  *                              sum and passthrough fallback of ANSCompressor::compress_tensor
  *                              (src/ANSCompressor.cpp:154-211, :225-238, :509-718)
@@ -132,6 +133,20 @@ CKR_API int ckr_byte_histogram_planes(const void* d_src, uint64_t n_elems, int d
  * the decode arrays are filled only up to slot 4095). ---- */
 CKR_API int ckr_build_table(const uint32_t* h_hist, int ensure_full_alphabet,
                             ckr_freq_table* h_table, uint32_t* h_table_sum);
+
+/* ---- the same table from ranks, on the host and on the device.  Replaces the
+ * same normalize_histogram (src/ANSCompressor.cpp:416-503) without its sort:
+ * each symbol's correction follows from how many fractional parts exceed or
+ * equal its own.  That equals the sorted result unless the correction's
+ * boundary falls inside a group of equal fractional parts, whose order only
+ * libstdc++'s std::sort fixes: *h_ambiguous (or word 257 of a device row) is
+ * then 1 and the caller must take ckr_build_table.  The device form builds
+ * n tables from n histograms of 256 words (d_hists[i * 256 ..]) into n rows of
+ * 258 words: norm_freq[256], their sum, the ambiguity flag. ---- */
+CKR_API int ckr_build_table_ranked(const uint32_t* h_hist, int ensure_full_alphabet,
+                                   ckr_freq_table* h_table, int* h_ambiguous);
+CKR_API int ckr_build_tables_device(const uint32_t* d_hists, uint64_t n, int ensure_full_alphabet,
+                                    uint32_t* d_rows, void* stream);
 
 /* ---- chunked rANS encode ----
  * The masked byte stream of the tensor (n_b = n_elems * element_size bytes) is
