@@ -314,9 +314,12 @@ uint32_t lane_slot_bytes(const uint32_t* plane_hist, const ckr_freq_table* t, ui
 // Encode workspace: tables, histograms, canonical streams, the fast path's
 // look-back state and redo list, and lane scratch for general-kernel batches
 // (sized for the whole tensor's units, capped by kScratchBudget).
+// The fast encoder's control words (ctl[0..5]) and, 8 words in, the device
+// table's words (norm[256], sum, ambiguity, slot sizes), read back together.
+constexpr uint32_t kCtlWords = 8 + ckr::kTinfoWords;
 struct EncodeLayout {
     uint64_t off_enc, off_hist, off_canon, off_status, off_ctl, off_redo, off_usize, off_rec, off_aux, off_list,
-        off_scratch, off_tinfo, total;
+        off_scratch, total;
     uint64_t batch_units;
 };
 
@@ -332,7 +335,7 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     L.off_hist = o;    o = align_up(o + 768 * 4, kAlign);
     L.off_canon = o;   o = align_up(o + 3ull * (4 + 2 * ck.cw) * 4, kAlign);
     L.off_status = o;  o = align_up(o + ckr::encode_fast_status_words(g.n_units) * 8, kAlign);
-    L.off_ctl = o;     o = align_up(o + 24, kAlign);
+    L.off_ctl = o;     o = align_up(o + kCtlWords * 4, kAlign);  // control words, then a device table's words
     L.off_redo = o;    o = align_up(o + g.n_units * 4, kAlign);
     const bool seg = use_seg_encode(g);  // two passes: checkpoint records instead of lane scratch
     L.off_usize = o;   o = align_up(o + (seg ? g.n_units : bu) * 4, kAlign);
@@ -340,7 +343,6 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     L.off_aux = o;     o = align_up(o + (seg ? 512 : 0), kAlign);
     L.off_list = o;    o = align_up(o + (seg ? ckr::encode_seg_list_items(g.n_units, g.unit) * 8 : 0), kAlign);
     L.off_scratch = o; o = align_up(o + (seg ? 0 : bu * per_unit), kAlign);
-    L.off_tinfo = o;   o = align_up(o + ckr::kTinfoWords * 4, kAlign);
     L.total = o;
     return L;
 }
@@ -1136,74 +1138,136 @@ const void* canon_chains(hipStream_t s) {
     return per_dev[dev];
 }
 
-// ckr_compress with the table built on the device (tensors the fast encoder
-// takes: masked dtypes, units of at most 64 KiB): histogram, table by ranks,
-// encode entries, canonical streams and slot sizes, and the encode queue
-// without a host round trip; one read-back of the control words and the table
-// at the end.  Returns kUseHostTable when the ranks leave the table to
-// libstdc++'s sort (a correction boundary inside a group of equal fractional
-// parts) or the LDS cannot hold the largest slots; the outputs are then
-// rewritten by the host-table path.
-int compress_device_table(const void* src, const ckr::EncodeGeom& g, int ensure_full_alphabet, uint8_t* d_out,
-                          ckr_stream_header* d_headers, uint64_t* d_unit_offsets, uint8_t* d_sidecar, uint8_t* ws,
-                          const EncodeLayout& L, ckr_freq_table* h_table, uint64_t* h_total_out, hipStream_t s) {
-    const CanonKs ck = canon_ks(g);
-    const uint32_t K = (uint32_t)((g.unit + 255) / 256);
-    const uint32_t lds_limit = (uint32_t)max_lds_per_block();
+// A tensor's encode with the table built on the device (tensors the fast
+// encoder takes: masked dtypes, units of at most 64 KiB): from its histograms
+// in device memory, the table by ranks, encode entries, canonical streams and
+// slot sizes, and the encode are queued with no host round trip, and the
+// control words and the table are read back into pinned words.  After the
+// stream has passed them, dev_enc_finish takes the table and the total and
+// queues any redo units; it returns kUseHostTable when the ranks leave the
+// table to libstdc++'s sort (a correction boundary inside a group of equal
+// fractional parts): the caller then encodes again under the host's sorted
+// table, over the same outputs.
+struct DevEnc {
+    const uint8_t* src = nullptr;
+    ckr::EncodeGeom g{};
+    EncodeLayout L{};
+    uint8_t* ws = nullptr;
     ckr::FastEncParamsHost fp{};
-    fp.escapes = false;  // the table is the data's own: every symbol present has a slot
-    fp.cw = ck.cw;
-    fp.canon_bytes = 4 * ck.cw;
-    const uint32_t smax = ckr::encode_fast_max_slot(fp.canon_bytes, K, lds_limit);
-    if (!smax || ck.cw > ckr::kCanonMaxCw) return kUseHostTable;
-    fp.sl0 = fp.sl1 = smax;
-    if (!ckr::encode_fast_lds_bytes(fp, lds_limit)) return kUseHostTable;
-    auto* enc = reinterpret_cast<ckr::EncSym*>(ws + L.off_enc);
-    auto* hist = reinterpret_cast<uint32_t*>(ws + L.off_hist);
-    auto* canon = reinterpret_cast<uint32_t*>(ws + L.off_canon);
-    auto* status = reinterpret_cast<uint64_t*>(ws + L.off_status);
-    auto* ctl = reinterpret_cast<uint32_t*>(ws + L.off_ctl);
-    auto* redo = reinterpret_cast<uint32_t*>(ws + L.off_redo);
-    auto* tinfo = reinterpret_cast<uint32_t*>(ws + L.off_tinfo);
-    uint32_t* pw = pinned_words();
-    if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
-    const void* chains = canon_chains(s);
-    if (!chains) return kUseHostTable;
-    const uint8_t* s8 = static_cast<const uint8_t*>(src);
-    CKR_HIP(ckr::launch_masked_hist(s8, g.n_bytes, g.es, g.spe, hist, hist + 256, s));
-    CKR_HIP(ckr::launch_table_enc(hist, g, ensure_full_alphabet, K, ck.k0, ck.k1, ck.k2, ck.cw, smax, enc, canon, tinfo,
-                                  status, ctl, chains, s));
-    CKR_HIP(ckr::launch_encode_fast(s8, g, enc, canon, fp, lds_limit, d_headers, d_sidecar, d_out, d_unit_offsets,
-                                    status, ctl, redo, s, tinfo + 258));
-    CKR_HIP(hipMemcpyAsync(pw, ctl, 24, hipMemcpyDeviceToHost, s));
-    CKR_HIP(hipMemcpyAsync(pw + 8, tinfo, ckr::kTinfoWords * 4, hipMemcpyDeviceToHost, s));
-    CKR_HIP(hipStreamSynchronize(s));
+    CanonKs ck{};
+    ckr_stream_header* hdrs = nullptr;
+    uint64_t* unit_off = nullptr;
+    uint8_t* out = nullptr;
+    uint8_t* side = nullptr;
+    uint32_t* dctl = nullptr;  // device: the control words, then the table's words (kCtlWords)
+    uint32_t* pin = nullptr;   // their pinned host copy
+};
+
+// Whether the device table can serve this tensor, and its encode parameters
+// (dctl: null for the workspace's own control words).
+bool dev_enc_setup(DevEnc& d, const void* src, const ckr::EncodeGeom& g, uint8_t* ws, uint8_t* out,
+                   ckr_stream_header* hdrs, uint64_t* unit_off, uint8_t* side, uint32_t* dctl, uint32_t* pin) {
+    if (g_fast_paths != 1 || !use_fast_encode(g)) return false;
+    d.src = static_cast<const uint8_t*>(src);
+    d.g = g;
+    d.L = encode_layout(g);
+    d.ws = ws;
+    d.ck = canon_ks(g);
+    d.out = out; d.hdrs = hdrs; d.unit_off = unit_off; d.side = g.spe ? side : nullptr;
+    d.dctl = dctl ? dctl : reinterpret_cast<uint32_t*>(ws + d.L.off_ctl);
+    d.pin = pin;
+    const uint32_t K = (uint32_t)((g.unit + 255) / 256);
+    d.fp.escapes = false;  // the table is the data's own: every symbol present has a slot
+    d.fp.cw = d.ck.cw;
+    d.fp.canon_bytes = 4 * d.ck.cw;
+    const uint32_t smax = ckr::encode_fast_max_slot(d.fp.canon_bytes, K, (uint32_t)max_lds_per_block());
+    if (!smax || d.ck.cw > ckr::kCanonMaxCw) return false;
+    d.fp.sl0 = d.fp.sl1 = smax;
+    return ckr::encode_fast_lds_bytes(d.fp, (uint32_t)max_lds_per_block()) != 0;
+}
+
+// The table set-up of one tensor, for launch_table_enc_multi.
+ckr::TableEncJob dev_enc_table_job(const DevEnc& d, const uint32_t* d_hist, int ensure_full) {
+    ckr::TableEncJob t{};
+    t.hist = d_hist;
+    t.enc = reinterpret_cast<ckr::EncSym*>(d.ws + d.L.off_enc);
+    t.canon = reinterpret_cast<uint32_t*>(d.ws + d.L.off_canon);
+    t.tinfo = d.dctl + 8;
+    t.status = reinterpret_cast<uint64_t*>(d.ws + d.L.off_status);
+    t.n_status = ckr::encode_fast_status_words(d.g.n_units);
+    t.ctl = d.dctl;
+    t.a = ckr::TableEncArg{(uint32_t)((d.g.unit + 255) / 256), d.ck.k0, d.ck.k1, d.ck.k2, d.ck.cw, d.fp.sl0, ensure_full};
+    return t;
+}
+
+// The encode, after its table set-up on the same stream (or one that waited for it).
+int dev_enc_queue_encode(const DevEnc& d, hipStream_t s) {
+    const EncodeLayout& L = d.L;
+    CKR_HIP(ckr::launch_encode_fast(d.src, d.g, reinterpret_cast<ckr::EncSym*>(d.ws + L.off_enc),
+                                    reinterpret_cast<uint32_t*>(d.ws + L.off_canon), d.fp, (uint32_t)max_lds_per_block(),
+                                    d.hdrs, d.side, d.out, d.unit_off, reinterpret_cast<uint64_t*>(d.ws + L.off_status),
+                                    d.dctl, reinterpret_cast<uint32_t*>(d.ws + L.off_redo), s, d.dctl + 8 + 258));
+    return CKR_OK;
+}
+
+int dev_enc_finish(const DevEnc& d, ckr_freq_table* h_table, uint64_t* h_total, bool* queued_more, hipStream_t s) {
     uint32_t hctl[6], ti[ckr::kTinfoWords];
-    std::memcpy(hctl, pw, sizeof(hctl));
-    std::memcpy(ti, pw + 8, sizeof(ti));
+    std::memcpy(hctl, d.pin, sizeof(hctl));
+    std::memcpy(ti, d.pin + 8, sizeof(ti));
     if (ti[257]) return kUseHostTable;
     if (hctl[2]) return fail(CKR_E_HIP, "[ckr] fast encode did not complete (flags %u: 1 look-back, 2 redo slots)", hctl[2]);
     if (h_table) {
         std::memset(h_table, 0, sizeof(*h_table));
         fill_table(ti, h_table);
     }
-    if (h_total_out) std::memcpy(h_total_out, &hctl[4], 8);
-    if (hctl[1]) {  // units that outgrew their slots
-        if (ckr::encode_fast_list_fits(fp, g, lds_limit)) {
-            CKR_HIP(ckr::launch_encode_fast_list(s8, g, enc, canon, fp, lds_limit, d_headers, d_out, d_unit_offsets,
-                                                 status, ctl, redo, s));
-        } else {
-            auto* usize = reinterpret_cast<uint32_t*>(ws + L.off_usize);
-            auto* scratch = reinterpret_cast<uint32_t*>(ws + L.off_scratch);
-            for (uint64_t r0 = 0; r0 < hctl[1]; r0 += L.batch_units) {
-                const uint64_t nb = std::min<uint64_t>(L.batch_units, hctl[1] - r0);
-                CKR_HIP(ckr::launch_encode_batch(s8, g, r0, nb, enc, canon, ck.cw, true, scratch, d_headers, nullptr,
-                                                 usize, d_unit_offsets, d_out, redo, s));
-            }
+    if (h_total) std::memcpy(h_total, &hctl[4], 8);
+    if (!hctl[1]) return CKR_OK;
+    // units that outgrew their slots
+    uint8_t* ws = d.ws;
+    const EncodeLayout& L = d.L;
+    auto* enc = reinterpret_cast<ckr::EncSym*>(ws + L.off_enc);
+    auto* canon = reinterpret_cast<uint32_t*>(ws + L.off_canon);
+    auto* status = reinterpret_cast<uint64_t*>(ws + L.off_status);
+    auto* redo = reinterpret_cast<uint32_t*>(ws + L.off_redo);
+    const uint32_t lds_limit = (uint32_t)max_lds_per_block();
+    if (ckr::encode_fast_list_fits(d.fp, d.g, lds_limit)) {
+        CKR_HIP(ckr::launch_encode_fast_list(d.src, d.g, enc, canon, d.fp, lds_limit, d.hdrs, d.out, d.unit_off, status,
+                                             d.dctl, redo, s));
+    } else {
+        auto* usize = reinterpret_cast<uint32_t*>(ws + L.off_usize);
+        auto* scratch = reinterpret_cast<uint32_t*>(ws + L.off_scratch);
+        for (uint64_t r0 = 0; r0 < hctl[1]; r0 += L.batch_units) {
+            const uint64_t nb = std::min<uint64_t>(L.batch_units, hctl[1] - r0);
+            CKR_HIP(ckr::launch_encode_batch(d.src, d.g, r0, nb, enc, canon, d.ck.cw, true, scratch, d.hdrs, nullptr,
+                                             usize, d.unit_off, d.out, redo, s));
         }
-        CKR_HIP(hipStreamSynchronize(s));  // the output complete, as on the other paths
     }
+    *queued_more = true;
     return CKR_OK;
+}
+
+// ckr_compress through the device table: histogram, queue, one synchronisation.
+int compress_device_table(const void* src, const ckr::EncodeGeom& g, int ensure_full_alphabet, uint8_t* d_out,
+                          ckr_stream_header* d_headers, uint64_t* d_unit_offsets, uint8_t* d_sidecar, uint8_t* ws,
+                          ckr_freq_table* h_table, uint64_t* h_total_out, hipStream_t s) {
+    uint32_t* pw = pinned_words();
+    if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
+    DevEnc d;
+    if (!dev_enc_setup(d, src, g, ws, d_out, d_headers, d_unit_offsets, d_sidecar, nullptr, pw)) return kUseHostTable;
+    const void* chains = canon_chains(s);
+    if (!chains) return kUseHostTable;
+    auto* hist = reinterpret_cast<uint32_t*>(ws + d.L.off_hist);
+    CKR_HIP(ckr::launch_masked_hist(d.src, g.n_bytes, g.es, g.spe, hist, hist + 256, s));
+    const ckr::TableEncJob t = dev_enc_table_job(d, hist, ensure_full_alphabet);
+    CKR_HIP(ckr::launch_table_enc_multi(&t, 1, chains, s));
+    int rc = dev_enc_queue_encode(d, s);
+    if (rc) return rc;
+    CKR_HIP(hipMemcpyAsync(pw, d.dctl, kCtlWords * 4, hipMemcpyDeviceToHost, s));
+    CKR_HIP(hipStreamSynchronize(s));
+    bool more = false;
+    rc = dev_enc_finish(d, h_table, h_total_out, &more, s);
+    if (rc == CKR_OK && more) CKR_HIP(hipStreamSynchronize(s));  // the output complete, as on the other paths
+    return rc;
 }
 }  // namespace
 
@@ -1232,7 +1296,7 @@ int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_b
     // before the encode (mode 1; modes 2 and 3 size the slots on the host)
     if (g_fast_paths == 1 && use_fast_encode(g)) {
         rc = compress_device_table(st.p, g, ensure_full_alphabet, d_out, d_headers, d_unit_offsets, d_sidecar,
-                                   static_cast<uint8_t*>(d_workspace), L, h_table, h_total_out, s);
+                                   static_cast<uint8_t*>(d_workspace), h_table, h_total_out, s);
         if (rc != kUseHostTable) {
             st.release(s);
             return rc;
@@ -1277,6 +1341,9 @@ struct ManyAux {
     uint64_t hist_jobs = 0;
     uint32_t* d_hists = nullptr;  // their device copy (one grid counts them all)
     uint64_t d_hist_jobs = 0;
+    uint32_t* tslots = nullptr;   // kCtlWords per job: device-table read-backs (pinned)
+    uint32_t* d_tslots = nullptr; // their device side: every job's control and table words
+    uint64_t tslot_jobs = 0;
     hipEvent_t ev_x[3] = {nullptr, nullptr, nullptr};  // s2, sx[0], sx[1] done (ckr_decode_many)
     uint64_t* bads = nullptr;    // ckr_decode_many's bad-lane counts, one per job
     uint64_t bad_jobs = 0;
@@ -1454,7 +1521,72 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         for (uint64_t i = 0; i < n; i++)
             hs[i] = {static_cast<const uint8_t*>(staged[i].p), geo[i].n_bytes, ckr_element_size(jobs[i].dtype),
                      (int)geo[i].spe};
+        // tables on the device when every job's tensor is one the fast encoder
+        // takes: no read-back or host table between the histograms and the
+        // encodes (a job whose ranks leave its table to the sort is encoded
+        // again under the host's table at the end)
+        std::vector<DevEnc> dv(n);
+        bool dev_all = true;
+        if (a->tslot_jobs < n) {
+            if (a->tslots) CKR_HIP(hipHostFree(a->tslots));
+            if (a->d_tslots) CKR_HIP(hipFree(a->d_tslots));
+            a->tslots = nullptr;
+            a->d_tslots = nullptr;
+            a->tslot_jobs = 0;
+            CKR_HIP(hipHostMalloc(reinterpret_cast<void**>(&a->tslots), n * kCtlWords * 4, hipHostMallocDefault));
+            CKR_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_tslots), n * kCtlWords * 4));
+            a->tslot_jobs = n;
+        }
+        for (uint64_t i = 0; i < n && dev_all; i++)
+            dev_all = dev_enc_setup(dv[i], staged[i].p, geo[i], static_cast<uint8_t*>(jobs[i].d_workspace),
+                                    jobs[i].d_out, jobs[i].d_headers, jobs[i].d_unit_offsets, jobs[i].d_sidecar,
+                                    a->d_tslots + kCtlWords * i, a->tslots + kCtlWords * i);
+        const void* chains = dev_all ? canon_chains(a->s2) : nullptr;
+        dev_all = dev_all && chains;
         CKR_HIP(ckr::launch_masked_hist_multi(hs.data(), (uint32_t)n, a->d_hists, a->s2));
+        if (dev_all) {
+            // every table in one launch behind the histograms, then the encodes
+            // round robin over four streams, then one read-back of every job's
+            // control and table words
+            std::vector<ckr::TableEncJob> tj(n);
+            for (uint64_t i = 0; i < n; i++) tj[i] = dev_enc_table_job(dv[i], a->d_hists + 768 * i, ensure_full_alphabet);
+            CKR_HIP(ckr::launch_table_enc_multi(tj.data(), (uint32_t)n, chains, a->s2));
+            CKR_HIP(hipEventRecord(a->ev, a->s2));
+            if (!g_prof_on) enc_streams = {s, a->s2, a->sx[0], a->sx[1]};
+            for (hipStream_t x : enc_streams)
+                if (x != a->s2) CKR_HIP(hipStreamWaitEvent(x, a->ev, 0));
+            for (uint64_t i = 0; i < n; i++) {
+                const int rc = dev_enc_queue_encode(dv[i], enc_streams[i % enc_streams.size()]);
+                if (rc) return rc;
+            }
+            for (size_t k = 0; k < enc_streams.size(); k++) {  // the caller's stream waits for the others
+                if (enc_streams[k] == s) continue;
+                CKR_HIP(hipEventRecord(a->ev_x[k % 3], enc_streams[k]));
+                CKR_HIP(hipStreamWaitEvent(s, a->ev_x[k % 3], 0));
+            }
+            CKR_HIP(hipMemcpyAsync(a->tslots, a->d_tslots, n * kCtlWords * 4, hipMemcpyDeviceToHost, s));
+            for (hipStream_t x : enc_streams) CKR_HIP(hipStreamSynchronize(x));
+            bool more = false;
+            for (uint64_t i = 0; i < n; i++) {
+                ckr_compress_job& jb = jobs[i];
+                int rc = dev_enc_finish(dv[i], jb.h_table, &jb.total, &more, s);
+                if (rc == kUseHostTable) {  // the sorted table decides: encode this job again
+                    uint32_t hh[768];
+                    CKR_HIP(hipMemcpy(hh, a->d_hists + 768 * i, sizeof(hh), hipMemcpyDeviceToHost));
+                    ckr_freq_table local;
+                    ckr_freq_table* t = jb.h_table ? jb.h_table : &local;
+                    rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
+                    if (rc == CKR_OK)
+                        rc = encode_impl(staged[i].p, jb.n_elems, jb.dtype, t, unit_bytes, jb.d_out, jb.out_capacity,
+                                         jb.d_headers, jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace,
+                                         jb.workspace_bytes, &jb.total, hh + 256, s);
+                }
+                if (rc) return rc;
+            }
+            if (more) CKR_HIP(hipStreamSynchronize(s));
+            drain.ok = true;
+            return CKR_OK;
+        }
         CKR_HIP(hipMemcpyAsync(a->hists, a->d_hists, n * 768 * sizeof(uint32_t), hipMemcpyDeviceToHost, a->s2));
         for (hipStream_t x : a->sx) CKR_HIP(hipStreamWaitEvent(x, a->ev, 0));  // inputs ready
         CKR_HIP(hipStreamSynchronize(a->s2));

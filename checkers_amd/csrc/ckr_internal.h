@@ -159,6 +159,28 @@ hipError_t launch_tables(const uint32_t* hists, uint64_t n, int ensure_full, uin
 hipError_t launch_table_enc(const uint32_t* hist, const EncodeGeom& g, int ensure_full, uint32_t K, uint32_t k0,
                             uint32_t k1, uint32_t k2, uint32_t cw, uint32_t smax, EncSym* d_enc, uint32_t* canon,
                             uint32_t* tinfo, uint64_t* status, uint32_t* ctl, const void* chains, hipStream_t s);
+// Batched: up to kMaxTableJobs tensors per launch (their status word counts
+// encode_fast_status_words(n_units) each).
+struct TableEncArg {
+    uint32_t K, k0, k1, k2, cw, smax;
+    int ensure_full;
+};
+struct TableEncJob {
+    const uint32_t* hist;
+    EncSym* enc;
+    uint32_t* canon;
+    uint32_t* tinfo;
+    uint64_t* status;
+    uint64_t n_status;
+    uint32_t* ctl;
+    TableEncArg a;
+};
+static constexpr uint32_t kMaxTableJobs = 16;
+struct TableEncJobs {
+    uint32_t n;
+    TableEncJob j[kMaxTableJobs];
+};
+hipError_t launch_table_enc_multi(const TableEncJob* jobs, uint32_t n, const void* chains, hipStream_t s);
 constexpr uint32_t kChainRows = 4097;  // symbol-0 counts 0 .. 4096
 constexpr uint32_t kChainSteps = 256;  // the most rows of a fast-encoder unit
 constexpr uint64_t kChainBytes = (4ull + 2ull) * (kChainSteps + 1) * kChainRows + (2ull * kChainSteps + 8) * kChainRows;

@@ -116,10 +116,6 @@ __global__ void __launch_bounds__(256) tables_kernel(const uint32_t* __restrict_
 // sizes follow lane_slot_bytes on the host (expected coded size of K symbols
 // from the plane histograms plus six standard deviations), then the larger is
 // cut until both fit the launch's LDS (sum at most 2 smax).
-struct TableEncArg {
-    uint32_t K, k0, k1, k2, cw, smax;
-    int ensure_full;
-};
 
 // The state chains of symbol 0 for every count f in [0, 4096] (f == 0: every
 // symbol the raw-byte escape), 256 steps each from state L, computed once per
@@ -195,16 +191,14 @@ __device__ void canon_entries_dev(uint32_t f, const uint32_t (&Ks)[3], uint32_t 
     }
 }
 
-__global__ void __launch_bounds__(256) table_enc_kernel(const uint32_t* __restrict__ hist, TableEncArg a,
-                                                        EncSym* __restrict__ enc, uint32_t* __restrict__ canon,
-                                                        uint32_t* __restrict__ tinfo, uint64_t* __restrict__ status,
-                                                        uint64_t n_status, uint32_t* __restrict__ ctl,
-                                                        const uint32_t* __restrict__ chain_x,
-                                                        const uint16_t* __restrict__ chain_n,
-                                                        const uint8_t* __restrict__ chain_b) {
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n_status; i += (uint64_t)gridDim.x * 256)
-        status[i] = 0;
-    if (blockIdx.x != 0) return;
+struct Chains {
+    const uint32_t* x;
+    const uint16_t* n;
+    const uint8_t* b;
+};
+__device__ void table_enc_body(const uint32_t* __restrict__ hist, const TableEncArg& a, EncSym* __restrict__ enc,
+                               uint32_t* __restrict__ canon, uint32_t* __restrict__ tinfo, uint32_t* __restrict__ ctl,
+                               const Chains& ch) {
     __shared__ RankTable T;
     __shared__ double sm[2][4];
     rank_table(hist, a.ensure_full != 0, T);
@@ -252,7 +246,28 @@ __global__ void __launch_bounds__(256) table_enc_kernel(const uint32_t* __restri
     }
     // canonical zero-plane streams of symbol 0 for the three lane counts
     const uint32_t Ks[3] = {a.k0, a.k1, a.k2};
-    canon_entries_dev(T.norm[0], Ks, a.cw, chain_x, chain_n, chain_b, canon);
+    canon_entries_dev(T.norm[0], Ks, a.cw, ch.x, ch.n, ch.b, canon);
+}
+
+// One tensor: block 0 the table work, every block a share of the status words.
+__global__ void __launch_bounds__(256) table_enc_kernel(const uint32_t* __restrict__ hist, TableEncArg a,
+                                                        EncSym* __restrict__ enc, uint32_t* __restrict__ canon,
+                                                        uint32_t* __restrict__ tinfo, uint64_t* __restrict__ status,
+                                                        uint64_t n_status, uint32_t* __restrict__ ctl, Chains ch) {
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n_status; i += (uint64_t)gridDim.x * 256)
+        status[i] = 0;
+    if (blockIdx.x == 0) table_enc_body(hist, a, enc, canon, tinfo, ctl, ch);
+}
+
+// Up to kMaxTableJobs tensors in one launch: job blockIdx.y, its block 0 the
+// table work, every block of the row a share of the job's status words.
+__global__ void __launch_bounds__(256) table_enc_multi_kernel(TableEncJobs J, Chains ch) {
+    const uint32_t jb = blockIdx.y;
+    if (jb >= J.n) return;
+    const TableEncJob& t = J.j[jb];
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < t.n_status; i += (uint64_t)gridDim.x * 256)
+        t.status[i] = 0;
+    if (blockIdx.x == 0) table_enc_body(t.hist, t.a, t.enc, t.canon, t.tinfo, t.ctl, ch);
 }
 
 __global__ void __launch_bounds__(256) build_enc_table_kernel(TableArg t, EncSym* out) {
@@ -3330,18 +3345,34 @@ hipError_t launch_canon_chains(void* chains, hipStream_t s) {
     CKR_LAUNCH("canon_chain_kernel", s, canon_chain_kernel<<<(kChainRows + 255) / 256, 256, 0, s>>>(cx, cn, cb));
     return hipGetLastError();
 }
+static Chains chains_of(const void* chains) {
+    const uint8_t* p = static_cast<const uint8_t*>(chains);
+    return Chains{reinterpret_cast<const uint32_t*>(p),
+                  reinterpret_cast<const uint16_t*>(p + 4ull * (kChainSteps + 1) * kChainRows),
+                  p + 6ull * (kChainSteps + 1) * kChainRows};
+}
 hipError_t launch_table_enc(const uint32_t* hist, const EncodeGeom& g, int ensure_full, uint32_t K, uint32_t k0,
                             uint32_t k1, uint32_t k2, uint32_t cw, uint32_t smax, EncSym* d_enc, uint32_t* canon,
                             uint32_t* tinfo, uint64_t* status, uint32_t* ctl, const void* chains, hipStream_t s) {
     const uint64_t nst = encode_fast_status_words(g.n_units);
     const uint32_t grid = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>((nst + 255) / 256, 4096));
     const TableEncArg a{K, k0, k1, k2, cw, smax, ensure_full};
-    const uint8_t* p = static_cast<const uint8_t*>(chains);
-    const auto* cx = reinterpret_cast<const uint32_t*>(p);
-    const auto* cn = reinterpret_cast<const uint16_t*>(p + 4ull * (kChainSteps + 1) * kChainRows);
-    const uint8_t* cb = p + 6ull * (kChainSteps + 1) * kChainRows;
     CKR_LAUNCH("table_enc_kernel", s,
-               table_enc_kernel<<<grid, 256, 0, s>>>(hist, a, d_enc, canon, tinfo, status, nst, ctl, cx, cn, cb));
+               table_enc_kernel<<<grid, 256, 0, s>>>(hist, a, d_enc, canon, tinfo, status, nst, ctl, chains_of(chains)));
+    return hipGetLastError();
+}
+hipError_t launch_table_enc_multi(const TableEncJob* jobs, uint32_t n, const void* chains, hipStream_t s) {
+    for (uint32_t j0 = 0; j0 < n; j0 += kMaxTableJobs) {
+        TableEncJobs J{};
+        J.n = std::min<uint32_t>(kMaxTableJobs, n - j0);
+        uint64_t most = 1;
+        for (uint32_t j = 0; j < J.n; j++) {
+            J.j[j] = jobs[j0 + j];
+            most = std::max<uint64_t>(most, (J.j[j].n_status + 255) / 256);
+        }
+        const dim3 grid((uint32_t)std::min<uint64_t>(most, 4096), J.n);
+        CKR_LAUNCH("table_enc_kernel", s, table_enc_multi_kernel<<<grid, 256, 0, s>>>(J, chains_of(chains)));
+    }
     return hipGetLastError();
 }
 // The largest slot (bytes, a multiple of 4, at most 2K + 8) whose two-pair
