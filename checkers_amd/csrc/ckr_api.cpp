@@ -249,6 +249,11 @@ hipError_t canon_launch(const ckr_freq_table* t, const CanonKs& ck, uint32_t* ca
 bool use_fast_encode(const ckr::EncodeGeom& g) { return use_dedup(g) && (g.unit + 255) / 256 <= kFastMaxK; }
 // Units above 64 KiB (up to the dedup limit): the two-pass kernels.
 bool use_seg_encode(const ckr::EncodeGeom& g) { return use_dedup(g) && (g.unit + 255) / 256 > kFastMaxK; }
+// Units above the dedup limit (the one-stream layout of a tensor above 1 MiB):
+// one chain per lane, then the segments side by side.
+bool use_long_units(const ckr::EncodeGeom& g) {
+    return g_fast_paths && g.spe > 0 && g.n_units > 0 && (g.unit + 255) / 256 > kDedupMaxK;
+}
 
 // A small pinned host buffer per thread and device for the few words the host
 // reads back (histograms, control words, totals): copies into pinned memory are
@@ -338,11 +343,14 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     L.off_ctl = o;     o = align_up(o + kCtlWords * 4, kAlign);  // control words, then a device table's words
     L.off_redo = o;    o = align_up(o + g.n_units * 4, kAlign);
     const bool seg = use_seg_encode(g);  // two passes: checkpoint records instead of lane scratch
-    L.off_usize = o;   o = align_up(o + (seg ? g.n_units : bu) * 4, kAlign);
-    L.off_rec = o;     o = align_up(o + (seg ? g.n_units * ckr::encode_seg_segments(g.unit) * 128 * 8 : 0), kAlign);
-    L.off_aux = o;     o = align_up(o + (seg ? 512 : 0), kAlign);
+    const bool lng = use_long_units(g);  // likewise, one chain per lane
+    L.off_usize = o;   o = align_up(o + (seg || lng ? g.n_units : bu) * 4, kAlign);
+    L.off_rec = o;
+    o = align_up(o + (seg ? g.n_units * ckr::encode_seg_segments(g.unit) * 128 * 8
+                          : (lng ? ckr::encode_long_rec_bytes(g.n_units, g.unit) : 0)), kAlign);
+    L.off_aux = o;     o = align_up(o + (seg || lng ? 512 : 0), kAlign);
     L.off_list = o;    o = align_up(o + (seg ? ckr::encode_seg_list_items(g.n_units, g.unit) * 8 : 0), kAlign);
-    L.off_scratch = o; o = align_up(o + (seg ? 0 : bu * per_unit), kAlign);
+    L.off_scratch = o; o = align_up(o + (seg || lng ? 0 : bu * per_unit), kAlign);
     L.total = o;
     return L;
 }
@@ -835,6 +843,27 @@ int encode_impl(const void* d_src, uint64_t n_elems, int dtype, const ckr_freq_t
         CKR_HIP(ckr::launch_build_enc_table(ta, enc, s));
     if (dedup) CKR_HIP(canon_launch(h_table, ck, canon, s));
 
+    if (use_long_units(g)) {
+        auto* aux = reinterpret_cast<uint32_t*>(ws + L.off_aux);
+        CKR_HIP(ckr::launch_encode_long(static_cast<const uint8_t*>(d_src), g, enc, escapes,
+                                        reinterpret_cast<uint2*>(ws + L.off_rec), d_headers, usize, d_unit_offsets,
+                                        side, d_out, aux, s));
+        if (after_launch) CKR_HIP((*after_launch)());
+        if (defer) {  // completed as the two-pass encode is: error word, then the total
+            defer->kind = 2;
+            CKR_HIP(hipMemcpyAsync(defer->pin, aux, 4, hipMemcpyDeviceToHost, s));
+            CKR_HIP(hipMemcpyAsync(defer->pin + 4, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
+            return CKR_OK;
+        }
+        uint32_t* pw = pinned_words();
+        if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
+        CKR_HIP(hipMemcpyAsync(pw, aux, 4, hipMemcpyDeviceToHost, s));
+        CKR_HIP(hipMemcpyAsync(pw + 2, d_unit_offsets + g.n_units, 8, hipMemcpyDeviceToHost, s));
+        CKR_HIP(hipStreamSynchronize(s));
+        if (pw[0]) return fail(CKR_E_HIP, "[ckr] two-pass encode: a segment did not end at its checkpoint");
+        if (h_total_out) std::memcpy(h_total_out, pw + 2, 8);
+        return CKR_OK;
+    }
     if (use_seg_encode(g)) {
         auto* rec = reinterpret_cast<uint2*>(ws + L.off_rec);
         auto* aux = reinterpret_cast<uint32_t*>(ws + L.off_aux);
@@ -1727,8 +1756,10 @@ int decode_impl(const uint8_t* d_data, const ckr_stream_header* d_headers, const
         }
         out = static_cast<uint8_t*>(tmp);
     }
-    hipError_t de = ckr::launch_decode(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, out, bad,
-                                       L.fast ? canon : nullptr, ck.cw, s);
+    hipError_t de = use_long_units(g)
+                        ? ckr::launch_decode_long(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, out, bad, s)
+                        : ckr::launch_decode(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, out, bad,
+                                             L.fast ? canon : nullptr, ck.cw, s);
     if (tmp) {
         if (de == hipSuccess) de = hipMemcpyAsync(d_dst, tmp, g.n_bytes, hipMemcpyDeviceToDevice, s);
         (void)hipFreeAsync(tmp, s);

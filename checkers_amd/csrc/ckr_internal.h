@@ -209,6 +209,21 @@ hipError_t launch_encode_seg(const uint8_t* src, const EncodeGeom& g, const EncS
                              const FastEncParamsHost* fp, uint32_t lds_limit, uint32_t* ctl, void* list,
                              hipStream_t s);
 
+// Units above 1 MiB of masked dtypes (the one-stream layout of a large tensor,
+// or large units), in two passes: one thread per lane chain records its state
+// every LU_SEG rows, then every segment is coded side by side.  rec holds
+// encode_long_rec_bytes(n_units, unit) bytes, unit_size n_units words, err one
+// word (nonzero when a segment did not end at its record: a bug).
+uint32_t encode_long_segments(uint64_t unit);
+uint64_t encode_long_rec_bytes(uint64_t n_units, uint64_t unit);
+hipError_t launch_encode_long(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, bool escapes, uint2* rec,
+                              ckr_stream_header* hdrs, uint32_t* unit_size, uint64_t* unit_off, uint8_t* sidecar,
+                              uint8_t* out, uint32_t* err, hipStream_t s);
+// Their decode: one block of two waves per unit (live lanes, zero-plane lanes).
+hipError_t launch_decode_long(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
+                              const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
+                              unsigned long long* bad, hipStream_t s);
+
 // Canonical zero-plane streams for lane counts k0, k1, k2: 3 entries of 4 + cw
 // dwords (header, then the stream in slot format), followed by the 3 streams in
 // byte order (cw dwords each).

@@ -3318,6 +3318,489 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
     if (nbad_total) atomicAdd(bad, nbad_total);
 }
 
+// ------------------------------------------------------------------ long units
+// Units of masked dtypes above 1 MiB: the reference's own one-stream layout of
+// a tensor (unit_bytes 0: 256 lanes of up to 2^24 symbols, coded by one block
+// of 256 threads in ANSCompressor.cpp:154-216) or large units.  A lane is one
+// chain of state updates from the unit's top row down
+// (ANSCompressor.cpp:178-203), the only serial part of the encode.  Pass 1
+// (lu_chain_kernel) follows each chain with one thread, rows fetched 64
+// ahead, and records its state and the bytes emitted so far at the entry of
+// every LU_SEG-row segment.  The lanes' offsets then follow from the chains'
+// byte counts (unit_finalize_kernel, unit_scan_kernel), and pass 2
+// (lu_code_kernel) codes every segment of every lane side by side from the
+// records, storing each segment's bytes at their place in its lane's stream,
+// and writes the sidecar.  A zero-plane lane codes K zeros from state L: its
+// stream depends on K alone, which takes two values in a unit (the lanes
+// inside the partial top row and the others), so two chains serve them all.
+static constexpr uint32_t LU_SEG = 1024;  // rows per segment (a multiple of 32)
+static constexpr uint32_t LU_CH = 130;    // chains per unit: 64 columns x 2 live lanes, 2 zero-plane counts
+
+// Record slots: rec[(u * S + s) * LU_CH + c] = {state, bytes emitted so far}
+// of chain c of unit u at the entry of segment s (before its top row is
+// coded); c = 64 p + j for live lane p (0: byte FL, 1: byte 3) of column j,
+// 128 for the zero-plane lanes of kf + 1 symbols, 129 for those of kf.
+template <int SPE, bool ESC>
+__global__ void __launch_bounds__(64) lu_chain_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
+                                                      const EncSym* __restrict__ d_enc, uint32_t S,
+                                                      uint2* __restrict__ rec, ckr_stream_header* __restrict__ hdrs,
+                                                      uint32_t* __restrict__ err) {
+    __shared__ uint4 tab[256];
+    for (uint32_t i = threadIdx.x; i < 256; i += 64) tab[i] = enc_quad(d_enc[i]);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *err = 0;  // pass 2 runs after this grid
+    __syncthreads();
+    constexpr int FL = SPE == 2 ? 2 : 1;
+    const uint32_t j = threadIdx.x;
+    const uint32_t role = blockIdx.x % 3;  // 0: lanes 4j + FL, 1: lanes 4j + 3, 2: the zero-plane chains
+    const uint64_t u = blockIdx.x / 3;
+    const uint64_t ubase = u * g.unit;
+    const uint32_t len = unit_len(g, ubase);
+    const uint32_t kf = len >> 8, r = len & 255u;
+    uint2* ur = rec + u * (uint64_t)S * LU_CH;
+    uint32_t x = L, e = 0;
+    if (role == 2) {
+        if (j < 2) {  // thread 0: kf + 1 symbols (kf when there is no partial row), thread 1: kf
+            const uint32_t K = kf + ((j == 0 && r) ? 1u : 0u);
+            const uint4 t0 = tab[0];
+            uint2* cr = ur + 128 + j;
+            for (int32_t s = (int32_t)((K + LU_SEG - 1) / LU_SEG) - 1; s >= 0; s--) {
+                cr[(uint64_t)s * LU_CH] = make_uint2(x, e);
+                const uint32_t n = min(K - (uint32_t)s * LU_SEG, LU_SEG);
+                uint32_t i = 0;
+                for (; i + 8 <= n; i += 8) {
+#pragma unroll
+                    for (int q = 0; q < 8; q++) e += seg_size_step<ESC>(x, t0);
+                }
+                for (; i < n; i++) e += seg_size_step<ESC>(x, t0);
+            }
+        }
+        const uint32_t x0 = __shfl(x, 0, 64), e0 = __shfl(e, 0, 64), x1 = __shfl(x, 1, 64), e1 = __shfl(e, 1, 64);
+        ckr_stream_header* uh = hdrs + u * 256 + 4 * j;
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            if (lane_is_live<SPE>(b)) continue;
+            const bool top = 4 * j + b < r;
+            ckr_stream_header h;
+            h.final_state = top ? x0 : x1;
+            h.byte_count = top ? e0 : e1;
+            h.buf_offset = 0;
+            h.pad = 0;
+            uh[b] = h;
+        }
+        return;
+    }
+    const uint32_t b = role == 0 ? FL : 3;
+    const uint32_t sh = 8 * b;
+    const uint32_t l = 4 * j + b;
+    const uint32_t K = kf + (l < r ? 1u : 0u);
+    uint2* cr = ur + 64 * role + j;
+    auto record = [&](uint32_t s) { cr[(uint64_t)s * LU_CH] = make_uint2(x, e); };
+    if (K) record((K - 1) / LU_SEG);
+    if (K > kf) e += seg_size_step<ESC>(x, tab[src[ubase + 256ull * kf + l]]);  // the partial top row
+    const uint32_t* in32 = reinterpret_cast<const uint32_t*>(src + ubase) + j;  // row k at in32[64 k]
+    const uint32_t ng = kf >> 5;
+    for (int32_t k = (int32_t)kf - 1; k >= (int32_t)(32 * ng); k--) {
+        if ((uint32_t)(k + 1) % LU_SEG == 0) record((uint32_t)k / LU_SEG);
+        e += seg_size_step<ESC>(x, tab[(in32[64 * (uint64_t)k] >> sh) & 255u]);
+    }
+    // groups of 32 rows from the top down, the next two groups' loads in flight
+    // while one is coded; table entries read 4 rows ahead
+    auto load = [&](uint32_t (&rr)[32], uint32_t gi) __attribute__((always_inline)) {
+        const uint32_t* p = in32 + 64 * (32 * (uint64_t)gi + 31);
+#pragma unroll
+        for (int i = 0; i < 32; i++) rr[i] = p[-64 * i];
+    };
+    auto code = [&](const uint32_t (&rr)[32], uint32_t gi) __attribute__((always_inline)) {
+        if ((32 * gi + 32) % LU_SEG == 0) record((32 * gi + 31) / LU_SEG);
+        uint4 ta[2][4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) ta[0][i] = tab[(rr[i] >> sh) & 255u];
+#pragma unroll
+        for (int bt = 0; bt < 8; bt++) {
+            if (bt < 7) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) ta[(bt + 1) & 1][i] = tab[(rr[4 * (bt + 1) + i] >> sh) & 255u];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) e += seg_size_step<ESC>(x, ta[bt & 1][i]);
+        }
+    };
+    if (ng) {
+        uint32_t ra[32], rb[32], rc[32];
+        int32_t gi = (int32_t)ng - 1;
+        load(ra, (uint32_t)gi);
+        if (gi >= 1) load(rb, (uint32_t)gi - 1);
+        for (;;) {
+            if (gi >= 2) load(rc, (uint32_t)gi - 2);
+            code(ra, (uint32_t)gi);
+            if (--gi < 0) break;
+            if (gi >= 2) load(ra, (uint32_t)gi - 2);
+            code(rb, (uint32_t)gi);
+            if (--gi < 0) break;
+            if (gi >= 2) load(rb, (uint32_t)gi - 2);
+            code(rc, (uint32_t)gi);
+            if (--gi < 0) break;
+        }
+    }
+    ckr_stream_header h;
+    h.final_state = x;
+    h.byte_count = e;
+    h.buf_offset = 0;
+    h.pad = 0;
+    hdrs[u * 256 + l] = h;
+}
+
+// Pass 2: block u * S + s codes segment s of unit u; wave b takes lanes 4j + b.
+// A segment's bytes [e0, e1) of the lane's emission order lie at stream
+// offsets (B - e1, B - e0] read backward (the first byte emitted is the
+// stream's last): they are stored from the top down, whole aligned dwords
+// inside the range and single bytes at its two ends, which share dwords with
+// the neighbouring segments.  Each segment must end at the next record (state
+// and count), else err is set (a bug, never expected).
+template <int SPE, bool ESC>
+__global__ void __launch_bounds__(256) lu_code_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
+                                                      const EncSym* __restrict__ d_enc, uint32_t S,
+                                                      const uint2* __restrict__ rec,
+                                                      const ckr_stream_header* __restrict__ hdrs,
+                                                      const uint32_t* __restrict__ unit_size,
+                                                      const uint64_t* __restrict__ unit_off,
+                                                      uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out,
+                                                      uint32_t* __restrict__ err) {
+    __shared__ uint4 tab[256];
+    tab[threadIdx.x] = enc_quad(d_enc[threadIdx.x]);
+    __syncthreads();
+    constexpr int FL = SPE == 2 ? 2 : 1;
+    const uint32_t j = threadIdx.x & 63, b = threadIdx.x >> 6;
+    const uint64_t u = blockIdx.x / S;
+    const uint32_t s = blockIdx.x % S;
+    const uint64_t ubase = u * g.unit;
+    const uint32_t len = unit_len(g, ubase);
+    const uint32_t kf = len >> 8, r = len & 255u;
+    const uint32_t k0 = s * LU_SEG, k1 = min(k0 + LU_SEG, kf + (r ? 1u : 0u));
+    const ckr_stream_header* uh = hdrs + u * 256;
+    uint8_t* uo = out + unit_off[u];
+    const uint8_t* us = src + ubase;
+    // the segment's sidecar (wave b: rows k0 + b, k0 + b + 4, ...), and, for a
+    // unit stored raw, its masked bytes
+    const bool raw = (uint64_t)unit_size[u] == len && uh[0].byte_count == len && uh[0].final_state == 0;
+    const uint32_t lm = live_mask32<SPE>();
+    for (uint32_t k = k0 + b; k < k1; k += 4) {
+        const uint32_t p = 256 * k + 4 * j;
+        if (p >= len) continue;
+        const uint32_t nvalid = min(len - p, 4u);
+        uint32_t v = 0;
+        if (nvalid == 4) v = *reinterpret_cast<const uint32_t*>(us + p);
+        else for (uint32_t q = 0; q < nvalid; q++) v |= (uint32_t)us[p + q] << (8 * q);
+        write_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
+        if (raw) {
+            v &= lm;
+            for (uint32_t q = 0; q < nvalid; q++) uo[p + q] = (uint8_t)(v >> (8 * q));
+        }
+    }
+    if (raw) return;
+    const uint32_t l = 4 * j + b;
+    const uint32_t kl = min(k1, kf + (l < r ? 1u : 0u));  // this lane's rows end below kl
+    if (k0 >= kl) return;
+    const bool live = SPE == 2 ? b >= 2 : (b & 1u) == 1u;
+    const uint32_t c = live ? (b == (uint32_t)FL ? 0u : 64u) + j : (l < r ? 128u : 129u);
+    const uint2 st = rec[(u * S + s) * LU_CH + c];
+    const ckr_stream_header h = uh[l];
+    uint32_t e1 = h.byte_count, xend = h.final_state;
+    if (s) {
+        const uint2 nx = rec[(u * S + s - 1) * LU_CH + c];
+        e1 = nx.y;
+        xend = nx.x;
+    }
+    uint8_t* sb = uo + h.buf_offset;
+    const uintptr_t hi = reinterpret_cast<uintptr_t>(sb) + h.byte_count - st.y;
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(sb) + h.byte_count - e1;
+    const uintptr_t blo = (lo + 3) & ~(uintptr_t)3, bhi = hi & ~(uintptr_t)3;
+    uintptr_t pos = hi;
+    uint32_t acc = 0;
+    auto put = [&](uint32_t v) __attribute__((always_inline)) {
+        pos--;
+        if (pos < lo) return;  // past the segment's bytes (never expected): counted below, not stored
+        if (pos >= blo && pos < bhi) {
+            acc = (acc << 8) | v;
+            if ((pos & 3u) == 0) *reinterpret_cast<uint32_t*>(pos) = acc;
+        } else {
+            *reinterpret_cast<uint8_t*>(pos) = (uint8_t)v;
+        }
+    };
+    uint32_t x = st.x;
+    const uint32_t sh = 8 * b;
+    for (int32_t k = (int32_t)kl - 1; k >= (int32_t)k0; k--) {
+        uint32_t sym = 0;
+        if (live) sym = (uint32_t)k < kf ? (*reinterpret_cast<const uint32_t*>(us + 256ull * k + 4 * j) >> sh) & 255u
+                                         : us[256ull * k + l];
+        const uint4 t = tab[sym];
+        const uint32_t f8 = t.w;
+        if (ESC && f8 == 0u) {  // raw-byte escape (ANSCompressor.cpp:185-192)
+            put(sym);
+            continue;
+        }
+        const uint32_t n = ((x >> 24) >= f8) ? 2u : (((x >> 16) >= f8) ? 1u : 0u);
+        if (n >= 1) put(x & 255u);
+        if (n == 2) put((x >> 8) & 255u);
+        const uint32_t xr = x >> (8 * n);
+        const uint32_t q = __umulhi(xr, t.x) >> (t.y >> 24);
+        x = xr + t.z + __umul24(q, t.y);
+    }
+    if (hi - pos != (uintptr_t)(e1 - st.y) || x != xend) atomicOr(err, 1u);
+}
+
+uint32_t encode_long_segments(uint64_t unit) { return (uint32_t)(((unit + 255) / 256 + LU_SEG - 1) / LU_SEG); }
+uint64_t encode_long_rec_bytes(uint64_t n_units, uint64_t unit) {
+    return n_units * (uint64_t)encode_long_segments(unit) * LU_CH * sizeof(uint2);
+}
+
+template <int SPE, bool ESC>
+static hipError_t encode_long_t(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, uint2* rec,
+                                ckr_stream_header* hdrs, uint32_t* unit_size, uint64_t* unit_off, uint8_t* sidecar,
+                                uint8_t* out, uint32_t* err, hipStream_t s) {
+    const uint32_t S = encode_long_segments(g.unit);
+    CKR_LAUNCH("lu_chain_kernel", s, lu_chain_kernel<SPE, ESC><<<(uint32_t)(3 * g.n_units), 64, 0, s>>>(src, g, d_enc, S, rec, hdrs, err));
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    CKR_LAUNCH("unit_finalize_kernel", s, unit_finalize_kernel<<<(uint32_t)g.n_units, 256, 0, s>>>(g, 0, hdrs, unit_size, nullptr));
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    CKR_LAUNCH("unit_scan_kernel", s, unit_scan_kernel<<<1, 1024, 0, s>>>(unit_size, 0, g.n_units, unit_off));
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    CKR_LAUNCH("lu_code_kernel", s, lu_code_kernel<SPE, ESC><<<(uint32_t)(g.n_units * S), 256, 0, s>>>(src, g, d_enc, S, rec, hdrs, unit_size, unit_off, sidecar, out, err));
+    return hipGetLastError();
+}
+
+hipError_t launch_encode_long(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, bool escapes, uint2* rec,
+                              ckr_stream_header* hdrs, uint32_t* unit_size, uint64_t* unit_off, uint8_t* sidecar,
+                              uint8_t* out, uint32_t* err, hipStream_t s) {
+    if (g.n_units == 0) return hipSuccess;
+    if (g.spe == 2)
+        return escapes ? encode_long_t<2, true>(src, g, d_enc, rec, hdrs, unit_size, unit_off, sidecar, out, err, s)
+                       : encode_long_t<2, false>(src, g, d_enc, rec, hdrs, unit_size, unit_off, sidecar, out, err, s);
+    if (g.spe == 1)
+        return escapes ? encode_long_t<1, true>(src, g, d_enc, rec, hdrs, unit_size, unit_off, sidecar, out, err, s)
+                       : encode_long_t<1, false>(src, g, d_enc, rec, hdrs, unit_size, unit_off, sidecar, out, err, s);
+    return hipErrorInvalidValue;
+}
+
+// Decoder of long units: each lane is one chain from its stream's start, so a
+// unit takes one block of two waves: wave 0 decodes the live lanes of every
+// column and stores the rows with their sidecar bytes, wave 1 decodes the
+// zero-plane lanes, which must give zeros and end where their streams end.
+// Stream bytes go through the fast decoder's LDS rings (df_*), each lane's
+// chunks counted from its own stream's 64-byte aligned start (so positions,
+// in bits, stay below 2^29 for a lane of 2^24 symbols).  The unit's other
+// LU_RAW_BLOCKS blocks copy it when it is stored raw.
+static constexpr uint32_t LU_RAW_BLOCKS = 64;
+
+__device__ __forceinline__ void lu_lane_init(DfLane& d, DfSrc& sr, uint32_t& ge8, const ckr_stream_header& h,
+                                             const uint8_t* data, uint64_t data_len, const uint8_t* ud,
+                                             uint64_t usize, uint32_t& nbad) {
+    const bool ok = (uint64_t)h.buf_offset + h.byte_count <= usize;
+    nbad += ok ? 0u : 1u;
+    const uint8_t* sp = ud + (ok ? h.buf_offset : 0u);
+    const uintptr_t ua = reinterpret_cast<uintptr_t>(sp) & ~(uintptr_t)63;
+    const uintptr_t d0 = reinterpret_cast<uintptr_t>(data), d1 = d0 + data_len;
+    const uint32_t g0 = (uint32_t)(reinterpret_cast<uintptr_t>(sp) - ua);
+    sr.d0 = data;
+    sr.dlen = data_len;
+    sr.ua = (int64_t)ua - (int64_t)d0;
+    sr.k_lo = ua >= d0 ? 0u : 1u;
+    const int64_t k_end = min<int64_t>(((int64_t)d1 - (int64_t)ua) >> DF_CH_LOG, 0x40000000ll);
+    sr.n_in = k_end > (int64_t)sr.k_lo ? (uint32_t)(k_end - (int64_t)sr.k_lo) : 0u;
+    d.x = h.final_state;
+    d.p8 = g0 << 3;
+    const uint32_t pe = g0 + (ok ? h.byte_count : 0u);
+    ge8 = pe << 3;
+    d.ch = 0;
+    d.last = pe > g0 ? (pe - 1u) >> DF_CH_LOG : 0u;
+    d.age = 0;
+}
+
+// Two rows of lanes a and b: stored (live lanes) or or-ed into za, zb (zero-plane lanes).
+template <int SPE, bool ZERO>
+__device__ __forceinline__ void lu_pair(DfLane& a, DfLane& b, const uint8_t* lds8, const uint32_t* tab, uint32_t* out,
+                                        uint32_t sv0, uint32_t sv1, uint32_t sel, uint32_t& za, uint32_t& zb) {
+    uint32_t wa = df_window(a, lds8), wb = df_window(b, lds8);
+    uint32_t ha0, ha1, hb0, hb1;
+    const uint32_t a0 = df_sym(a.x, wa, ha0, tab);
+    const uint32_t b0 = df_sym(b.x, wb, hb0, tab);
+    if (!ZERO) df_store(out, df_pack<SPE>(a0, b0, sv0, sel));
+    const uint32_t a1 = df_sym(a.x, wa, ha1, tab);
+    const uint32_t b1 = df_sym(b.x, wb, hb1, tab);
+    if (!ZERO) df_store(out + 64, df_pack<SPE>(a1, b1, sv1, sel));
+    if (ZERO) { za |= a0 | a1; zb |= b0 | b1; }
+    a.p8 += ha0 + ha1;
+    b.p8 += hb0 + hb1;
+}
+
+template <int SPE, bool ZERO>
+__device__ __forceinline__ void lu_group(DfLane& a, DfLane& b, uint8_t* lds8, const uint32_t* tab, uint32_t* out,
+                                         const uint32_t (&sc)[8], uint32_t sel, const DfSrc& sa, const DfSrc& sb,
+                                         uint32_t& za, uint32_t& zb) {
+#pragma unroll
+    for (int r = 0; r < 8; r += 2) lu_pair<SPE, ZERO>(a, b, lds8, tab, out + 64 * r, sc[r], sc[r + 1], sel, za, zb);
+    df_step(a, lds8, sa);
+    df_step(b, lds8, sb);
+}
+
+// One wave's two lanes of every column over the unit's rows.
+template <int SPE, bool ZERO>
+__device__ __forceinline__ uint32_t lu_decode_wave(const uint8_t* data, uint64_t data_len,
+                                                   const ckr_stream_header* uh, const uint8_t* ud, uint64_t usize,
+                                                   uint32_t len, uint64_t ubase, const uint32_t* tab, uint8_t* lds8,
+                                                   uint32_t tb0, const uint8_t* sidecar, uint8_t* dst, uint32_t j) {
+    constexpr int FL = SPE == 2 ? 2 : 1;
+    constexpr int BA = ZERO ? 0 : FL, BB = ZERO ? (SPE == 2 ? 1 : 2) : 3;  // lanes 4j + BA, 4j + BB
+    uint32_t nbad = 0, za = 0, zb = 0;  // zero-plane lanes: the or of their symbols (bits 31..24)
+    DfLane da, db;
+    DfSrc sa, sb;
+    uint32_t gea8, geb8;
+    lu_lane_init(da, sa, gea8, uh[4 * j + BA], data, data_len, ud, usize, nbad);
+    lu_lane_init(db, sb, geb8, uh[4 * j + BB], data, data_len, ud, usize, nbad);
+    da.tb = tb0;
+    db.tb = tb0 + DF_RING_BYTES;
+    {   // the first two chunks of each stream (the second only if the stream reaches it)
+        uint4 ca[DF_CQ], cb[DF_CQ];
+        df_fetch(sa, 0, ca);
+        df_fetch(sb, 0, cb);
+        const bool a2nd = da.last >= 1u, b2nd = db.last >= 1u;
+        if (a2nd) df_fetch(sa, 1, da.c);
+        if (b2nd) df_fetch(sb, 1, db.c);
+        df_put(lds8, da.tb, 0, ca);
+        df_put(lds8, db.tb, 0, cb);
+        if (a2nd) df_put(lds8, da.tb, 1, da.c);
+        if (b2nd) df_put(lds8, db.tb, 1, db.c);
+    }
+    const uint32_t K = len >> 8;  // full rows; a partial row K follows when len % 256 != 0
+    const uint32_t* sc32 = reinterpret_cast<const uint32_t*>(sidecar + (ubase >> 1) + 4 * (j >> 1));
+    const uint32_t sel = df_sel<SPE>(2 * (j & 1));
+    uint32_t* out32 = reinterpret_cast<uint32_t*>(dst + ubase + 4 * j);
+    const uint32_t ng = K >> 3;
+    if (ng) {
+        // sidecar words DF_AHEAD groups ahead, as in decode_fast_kernel
+        constexpr uint32_t A = DF_AHEAD;
+        const uint32_t gl = ng - 1;
+        uint32_t sbuf[A + 1][8];
+        uint32_t gi = 0;
+        if (!ZERO) {
+#pragma unroll
+            for (uint32_t q = 0; q < A; q++) df_load_sc(sbuf[q], sc32 + 256 * min(q, gl));
+        }
+        for (; gi + A + 1 <= ng; gi += A + 1) {
+#pragma unroll
+            for (uint32_t q = 0; q <= A; q++) {
+                if (!ZERO) df_load_sc(sbuf[(q + A) % (A + 1)], sc32 + 256 * min(gi + q + A, gl));
+                lu_group<SPE, ZERO>(da, db, lds8, tab, out32 + 512 * (gi + q), sbuf[q], sel, sa, sb, za, zb);
+            }
+        }
+#pragma unroll
+        for (uint32_t q = 0; q < A; q++)
+            if (gi + q < ng) lu_group<SPE, ZERO>(da, db, lds8, tab, out32 + 512 * (gi + q), sbuf[q], sel, sa, sb, za, zb);
+    }
+    uint32_t k = 8 * ng;
+    for (; k + 2 <= K; k += 2)
+        lu_pair<SPE, ZERO>(da, db, lds8, tab, out32 + 64 * k, ZERO ? 0u : sc32[32 * k], ZERO ? 0u : sc32[32 * (k + 1)],
+                           sel, za, zb);
+    if (k < K) {
+        uint32_t wa = df_window(da, lds8), wb = df_window(db, lds8);
+        uint32_t ha, hb;
+        const uint32_t a0 = df_sym(da.x, wa, ha, tab);
+        const uint32_t b0 = df_sym(db.x, wb, hb, tab);
+        if (!ZERO) out32[64 * k] = df_pack<SPE>(a0, b0, sc32[32 * k], sel);
+        else { za |= a0; zb |= b0; }
+        da.p8 += ha;
+        db.p8 += hb;
+    }
+    // the partial top row: r bytes, nv of them in this column
+    const uint32_t r = len & 255u;
+    if (r > 4 * j) {
+        const uint32_t nv = min(r - 4 * j, 4u);
+        uint32_t wa = df_window(da, lds8), wb = df_window(db, lds8);
+        uint32_t ha = 0, hb = 0, v = 0, sa0 = 0, sb0 = 0;
+        if (nv > (uint32_t)BA) sa0 = df_sym(da.x, wa, ha, tab) >> 24;
+        if (nv > (uint32_t)BB) sb0 = df_sym(db.x, wb, hb, tab) >> 24;
+        v = sa0 << (8 * BA) | sb0 << (8 * BB);
+        da.p8 += ha;
+        db.p8 += hb;
+        if (!ZERO) {
+            const uint64_t pos = ubase + 256ull * K + 4 * j;
+            v = merge_sidecar_row<SPE>(sidecar, pos, v, nv);
+            uint8_t* d8 = dst + pos;
+            if (nv == 4) *reinterpret_cast<uint32_t*>(d8) = v;
+            else for (uint32_t q = 0; q < nv; q++) d8[q] = (uint8_t)(v >> (8 * q));
+        } else {
+            za |= sa0 << 24;
+            zb |= sb0 << 24;
+        }
+    }
+    // a lane is bad when it does not end at state L with every byte consumed,
+    // or, in the zero planes, gave a nonzero symbol
+    nbad += (da.x != L || da.p8 != gea8 || (za >> 24)) ? 1u : 0u;
+    nbad += (db.x != L || db.p8 != geb8 || (zb >> 24)) ? 1u : 0u;
+    return nbad;
+}
+
+template <int SPE>
+__global__ void __launch_bounds__(128) decode_long_kernel(const uint8_t* __restrict__ data,
+                                                          const ckr_stream_header* __restrict__ hdrs,
+                                                          const uint64_t* __restrict__ unit_off,
+                                                          const uint32_t* __restrict__ d_dec, EncodeGeom g,
+                                                          const uint8_t* __restrict__ sidecar,
+                                                          uint8_t* __restrict__ dst, unsigned long long* bad) {
+    extern __shared__ uint32_t lds[];
+    const uint64_t u = blockIdx.x;
+    const uint32_t j = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint64_t ubase = u * g.unit;
+    const uint32_t len = unit_len(g, ubase);
+    const uint64_t uoff = unit_off[u];
+    const uint8_t* ud = data + uoff;
+    const uint64_t usize = unit_off[u + 1] - uoff;
+    const ckr_stream_header* uh = hdrs + u * 256;
+    const bool raw = usize == len && uh[0].byte_count == len;
+    if (blockIdx.y) {  // a raw unit: masked bytes | sidecar, rows shared by the blocks' waves
+        if (!raw) return;
+        const uint32_t W = 2 * LU_RAW_BLOCKS;
+        for (uint32_t k = (blockIdx.y - 1) * 2 + wv; 256ull * k < len; k += W) {
+            const uint32_t p = 256 * k + 4 * j;
+            if (p >= len) continue;
+            const uint32_t nvalid = min(len - p, 4u);
+            uint32_t v = 0;
+            for (uint32_t q = 0; q < nvalid; q++) v |= (uint32_t)ud[p + q] << (8 * q);
+            v = merge_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
+            uint8_t* d = dst + ubase + p;
+            if (nvalid == 4) *reinterpret_cast<uint32_t*>(d) = v;
+            else for (uint32_t q = 0; q < nvalid; q++) d[q] = (uint8_t)(v >> (8 * q));
+        }
+        return;
+    }
+    if (raw) return;
+    uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
+    for (uint32_t i = threadIdx.x; i < 4096; i += 128) {
+        const uint32_t e = d_dec[i];  // sym | (f - 1) << 8 | cum << 20
+        lds[i] = (e & 0x000FFF00u) << 4 | (i - (e >> 20)) | (e & 255u) << 24;  // sym<<24 | (f-1)<<12 | slot-cum
+    }
+    __syncthreads();
+    const uint64_t data_len = unit_off[g.n_units];
+    const uint32_t tb0 = DF_TAB_BYTES + wv * DF_WAVE_BYTES + 4 * j;
+    const uint32_t nbad =
+        wv == 0 ? lu_decode_wave<SPE, false>(data, data_len, uh, ud, usize, len, ubase, lds, lds8, tb0, sidecar, dst, j)
+                : lu_decode_wave<SPE, true>(data, data_len, uh, ud, usize, len, ubase, lds, lds8, tb0, sidecar, dst, j);
+    if (nbad) atomicAdd(bad, (unsigned long long)nbad);
+}
+
+hipError_t launch_decode_long(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
+                              const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
+                              unsigned long long* bad, hipStream_t s) {
+    if (g.n_units == 0) return hipSuccess;
+    if (g.spe != 1 && g.spe != 2) return hipErrorInvalidValue;
+    const uint32_t lb = DF_TAB_BYTES + 2 * DF_WAVE_BYTES;
+    const dim3 grid((uint32_t)g.n_units, 1 + LU_RAW_BLOCKS);
+    if (g.spe == 2) CKR_LAUNCH("decode_long_kernel", s, decode_long_kernel<2><<<grid, 128, lb, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
+    else CKR_LAUNCH("decode_long_kernel", s, decode_long_kernel<1><<<grid, 128, lb, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
+    return hipGetLastError();
+}
+
 hipError_t launch_build_enc_table(const TableArg& t, EncSym* d_enc, hipStream_t s) {
     CKR_LAUNCH("build_enc_table_kernel", s, build_enc_table_kernel<<<1, 256, 0, s>>>(t, d_enc));
     return hipGetLastError();

@@ -58,6 +58,14 @@ CASES = [
     ("random_bits_f32_1mib", dg.F32, 262144 * 2 + 333, 1 << 20,
      lambda n: np.random.default_rng(20).integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32).view(np.float32)),
     ("adversarial_f32_256k", dg.F32, 65536 * 3 + 999, 262144, lambda n: dg.adversarial_f32(n, 21, (70000, 140000))),
+    # units above 1 MiB (one chain per lane, then the 1024-row segments side by
+    # side): the one-stream layout of a tensor with a partial top row, one that
+    # ends on a segment boundary, and 4 MiB units with a partial last one
+    ("f32_whole_long", dg.F32, 600001, 0, lambda n: dg.normal_f32(n, 1e-3, 24)),
+    ("bf16_whole_long", dg.BF16, 1300001, 0, lambda n: dg.normal_bf16(n, 0.02, 25)),
+    ("f32_whole_long_segments", dg.F32, 256 * 1024 * 5 // 4, 0, lambda n: dg.exp_avg_sq(n, 26)),
+    ("f16_whole_long", dg.F16, 700003, 0, lambda n: (np.random.default_rng(27).standard_normal(n) * 0.02).astype(np.float16)),
+    ("f32_4mib_units", dg.F32, (1 << 20) * 2 + 12345, 4 << 20, lambda n: dg.adversarial_f32(n, 28, (300000, 400000))),
     ("bf16_partial_units", dg.BF16, 3 * 512 + 1, 1024, lambda n: dg.normal_bf16(n, 0.02, 16)),
     ("tiny_f32_1", dg.F32, 1, 65536, lambda n: np.array([1.5], np.float32)),
     ("tiny_bf16_3", dg.BF16, 3, 0, lambda n: dg.normal_bf16(n, 0.02, 12)),
@@ -199,6 +207,8 @@ def test_passthrough_unit_with_mismatched_table(gpu):
     (dg.F32, 1 << 20, (1 << 18) * 3 + 5000),
     (dg.F32, 131328, 32832 * 4 + 17),
     (dg.BF16, 1 << 18, (1 << 17) * 2 + 333),
+    (dg.F32, 2 << 20, (1 << 19) * 3 + 4321),
+    (dg.BF16, 3 << 20, (3 << 19) * 2 + 77),
 ])
 def test_large_units_with_foreign_table(dt, unit, n, paths, gpu):
     """Units above 64 KiB under a table that does not fit the data: alternate
@@ -350,15 +360,15 @@ def test_histogram_counts_wrap_like_reference(gpu):
     assert tsum == rsum  # 4115 here: the reference's over-full table for a dominant symbol
 
 
-@pytest.mark.parametrize("unit", [65536, 1 << 20])
+@pytest.mark.parametrize("unit", [65536, 1 << 20, 4 << 20])
 @pytest.mark.parametrize("where", ["live", "zero", "state", "zero_last", "zero_header"])
 def test_decode_counts_corrupted_lanes(unit, where, gpu):
     """A flipped byte in a live lane's stream or a zero-plane lane's stream, or a
     wrong final state, is reported as a bad lane (the decoder's postconditions:
     final state L, every byte consumed, canonical zero-plane streams).  A
-    zero-plane lane's bytes are compared step by step during the decode: a flip
-    in its first or last byte, in the second unit, or in its header counts that
-    one lane."""
+    zero-plane lane's bytes are compared step by step during the decode (units
+    up to 1 MiB) or decoded (above: they must give zeros): a flip in its first
+    or last byte, in the second unit, or in its header counts that one lane."""
     import torch
     ck = _ck()
     n = (unit // 4) * 2 + 777
