@@ -258,7 +258,7 @@ def repair_cpu_baseline(shard, names=("k_proj", "v_proj", "input_layernorm", "po
 def reference_layout_leg(shard, ck, torch, dev):
     """The reference's own stream layout (unit_bytes 0: one stream of 256 lanes
     per tensor, the .ansc v2 files byte for byte) on one cfg3 fp32 tensor:
-    encode (histogram, table, one-unit encode on the general kernels) and decode,
+    encode (histogram, table, the long-unit kernels' two passes) and decode,
     each timed once with HIP events after a warm-up on the first 64 MiB."""
     name, t = [x for x in shard if x[1].dtype == torch.float32][0]
     tag = ck.torch_tag(t.dtype)
@@ -286,8 +286,10 @@ def reference_layout_leg(shard, ck, torch, dev):
     out = dict(tensor=name, elements=n, unit_bytes=0, encode_ms=round(enc_ms, 3), decode_ms=round(dec_ms, 3),
                encode_GBps=round(nb / enc_ms / 1e6, 3), decode_GBps=round(nb / dec_ms / 1e6, 3),
                ans_ratio=round(nb / r.total, 4), roundtrip_bit_exact=ok,
-               note="one unit: 256 lanes, each coding n/256 symbols in order, so 64 threads of one wave "
-                    "do the whole tensor (the reference's own kernel runs 256 threads)")
+               note="one unit: 256 lanes, each coding n/256 symbols in order; one thread per lane chain "
+                    "records its state every 1024 rows (lu_chain_kernel), then every segment is coded side "
+                    "by side (lu_code_kernel); the decode follows one chain per lane (decode_long_kernel). "
+                    "The reference's own encode kernel runs 256 threads, one per lane")
     del e, r, d, dst
     torch.cuda.empty_cache()
     return out
@@ -454,6 +456,17 @@ def save_leg(shard, torch, unit, reps=2):
             if ln.startswith("[TIMING]"):
                 k, v = ln.split()[1].split("=")
                 timing[k] = float(v)
+        # every call's totals: the first call's extra time against the later
+        # ones, split into the writer's GPU work and the rest (files)
+        calls = []
+        for ln in lines:
+            if ln.startswith("[TIMING]"):
+                k, v = ln.split()[1].split("=")
+                if k == "compress_and_save_total_ms":
+                    calls.append({})
+                if calls:
+                    calls[-1][k] = float(v)
+        timing["per_call"] = calls
     # a context over an engine with no parameters replaces this one: its arena,
     # the writer's buffers and its references to the shard go
     checkers_py.initialize_context(types.SimpleNamespace(
