@@ -247,6 +247,38 @@ def test_large_units_with_foreign_table(dt, unit, n, paths, gpu):
     assert bad == 0 and np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
 
 
+@pytest.mark.parametrize("dt", [dg.F32, dg.BF16])
+def test_one_stream_tensor_stored_raw(dt, paths, gpu):
+    """The one-stream layout (unit_bytes 0) of a tensor above 1 MiB under a table
+    that prices its live bytes badly: the whole tensor expands and is stored raw
+    (ANSCompressor.cpp:694-713), with escapes for the symbols the table lacks
+    (:185-192); bytes equal the oracle's and the decode copies it back."""
+    import torch
+    ck = _ck()
+    es = 4 if dt == dg.F32 else 2
+    n = (3 << 20) // es + 37
+    print(f"[case] one-stream raw dtype={dt} n={n} fast={paths}", flush=True)
+    raw = np.random.default_rng(52).integers(0, 256, n * es, dtype=np.uint8).view(np.uint32 if es == 4 else np.uint16)
+    h = np.full(256, 1, np.uint32)
+    h[1] = 3000  # every other symbol, zero included, gets one slot (12 bits); the table sums to 4096
+    h[240:] = 0
+    t_ck, s_ck = ck.build_table(h)
+    t_oc, s_oc = oc.normalize_histogram(h)
+    assert s_ck == s_oc == 4096
+    masked, side = oc.extract_mantissa(raw, n, dt)
+    data, hdr, off = oc.encode(masked, t_oc, 0)
+    assert off[1] == n * es  # stored raw
+    enc = ck.encode(_to_dev(raw, gpu), dt, t_ck, 0, n_elems=n)
+    torch.cuda.synchronize()
+    assert enc.total == data.size
+    assert np.array_equal(enc.headers_np()[: hdr.size], hdr)
+    assert np.array_equal(enc.data_np(), data)
+    assert np.array_equal(enc.sidecar[: side.size].cpu().numpy(), side)
+    dst, bad = ck.decode(enc)
+    torch.cuda.synchronize()
+    assert bad == 0 and np.array_equal(dst.cpu().numpy(), dg.raw_bytes(raw))
+
+
 def test_escape_symbols_match_reference_bytes(gpu):
     """Symbols with f == 0 take the reference's raw-byte escape (ANSCompressor.cpp:185-192)."""
     import torch
