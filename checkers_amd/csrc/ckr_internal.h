@@ -219,7 +219,7 @@ uint64_t encode_long_rec_bytes(uint64_t n_units, uint64_t unit);
 hipError_t launch_encode_long(const uint8_t* src, const EncodeGeom& g, const EncSym* d_enc, bool escapes, uint2* rec,
                               ckr_stream_header* hdrs, uint32_t* unit_size, uint64_t* unit_off, uint8_t* sidecar,
                               uint8_t* out, uint32_t* err, hipStream_t s);
-// Their decode: one block of two waves per unit (live lanes, zero-plane lanes).
+// Their decode: one block of four waves per unit, one lane chain per thread.
 hipError_t launch_decode_long(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
                               const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
                               unsigned long long* bad, hipStream_t s);

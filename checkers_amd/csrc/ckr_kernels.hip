@@ -3584,13 +3584,14 @@ hipError_t launch_encode_long(const uint8_t* src, const EncodeGeom& g, const Enc
 }
 
 // Decoder of long units: each lane is one chain from its stream's start, so a
-// unit takes one block of two waves: wave 0 decodes the live lanes of every
-// column and stores the rows with their sidecar bytes, wave 1 decodes the
-// zero-plane lanes, which must give zeros and end where their streams end.
-// Stream bytes go through the fast decoder's LDS rings (df_*), each lane's
-// chunks counted from its own stream's 64-byte aligned start (so positions,
-// in bits, stay below 2^29 for a lane of 2^24 symbols).  The unit's other
-// LU_RAW_BLOCKS blocks copy it when it is stored raw.
+// unit takes one block of four waves, wave b decoding lanes 4j + b, one chain
+// per thread (two chains interleaved in one thread took 1.8x as long: their
+// table lookups end up serialised).  The zero-plane lanes must give zeros and
+// end where their streams end.  Stream bytes go through the fast decoder's LDS
+// rings (df_*), each lane's chunks counted from its own stream's 64-byte
+// aligned start (so positions, in bits, stay below 2^29 for a lane of 2^24
+// symbols).  The unit's other LU_RAW_BLOCKS blocks copy it when it is stored
+// raw.
 static constexpr uint32_t LU_RAW_BLOCKS = 64;
 
 __device__ __forceinline__ void lu_lane_init(DfLane& d, DfSrc& sr, uint32_t& ge8, const ckr_stream_header& h,
@@ -3617,132 +3618,108 @@ __device__ __forceinline__ void lu_lane_init(DfLane& d, DfSrc& sr, uint32_t& ge8
     d.age = 0;
 }
 
-// Two rows of lanes a and b: stored (live lanes) or or-ed into za, zb (zero-plane lanes).
-template <int SPE, bool ZERO>
-__device__ __forceinline__ void lu_pair(DfLane& a, DfLane& b, const uint8_t* lds8, const uint32_t* tab, uint32_t* out,
-                                        uint32_t sv0, uint32_t sv1, uint32_t sel, uint32_t& za, uint32_t& zb) {
-    uint32_t wa = df_window(a, lds8), wb = df_window(b, lds8);
-    uint32_t ha0, ha1, hb0, hb1;
-    const uint32_t a0 = df_sym(a.x, wa, ha0, tab);
-    const uint32_t b0 = df_sym(b.x, wb, hb0, tab);
-    if (!ZERO) df_store(out, df_pack<SPE>(a0, b0, sv0, sel));
-    const uint32_t a1 = df_sym(a.x, wa, ha1, tab);
-    const uint32_t b1 = df_sym(b.x, wb, hb1, tab);
-    if (!ZERO) df_store(out + 64, df_pack<SPE>(a1, b1, sv1, sel));
-    if (ZERO) { za |= a0 | a1; zb |= b0 | b1; }
-    a.p8 += ha0 + ha1;
-    b.p8 += hb0 + hb1;
-}
+// One lane per thread: wave b of a unit's block decodes lanes 4j + b of every
+// column and stores byte b of each row (a live lane its symbols, a zero-plane
+// lane, which must give zeros, the sidecar's byte, loaded LU_AHEAD groups of 8
+// rows ahead).
+static constexpr uint32_t LU_AHEAD = 2;
 
-template <int SPE, bool ZERO>
-__device__ __forceinline__ void lu_group(DfLane& a, DfLane& b, uint8_t* lds8, const uint32_t* tab, uint32_t* out,
-                                         const uint32_t (&sc)[8], uint32_t sel, const DfSrc& sa, const DfSrc& sb,
-                                         uint32_t& za, uint32_t& zb) {
-#pragma unroll
-    for (int r = 0; r < 8; r += 2) lu_pair<SPE, ZERO>(a, b, lds8, tab, out + 64 * r, sc[r], sc[r + 1], sel, za, zb);
-    df_step(a, lds8, sa);
-    df_step(b, lds8, sb);
-}
-
-// One wave's two lanes of every column over the unit's rows.
-template <int SPE, bool ZERO>
-__device__ __forceinline__ uint32_t lu_decode_wave(const uint8_t* data, uint64_t data_len,
+template <int SPE, int B>
+__device__ __forceinline__ uint32_t lu_decode_lane(const uint8_t* data, uint64_t data_len,
                                                    const ckr_stream_header* uh, const uint8_t* ud, uint64_t usize,
                                                    uint32_t len, uint64_t ubase, const uint32_t* tab, uint8_t* lds8,
-                                                   uint32_t tb0, const uint8_t* sidecar, uint8_t* dst, uint32_t j) {
-    constexpr int FL = SPE == 2 ? 2 : 1;
-    constexpr int BA = ZERO ? 0 : FL, BB = ZERO ? (SPE == 2 ? 1 : 2) : 3;  // lanes 4j + BA, 4j + BB
-    uint32_t nbad = 0, za = 0, zb = 0;  // zero-plane lanes: the or of their symbols (bits 31..24)
-    DfLane da, db;
-    DfSrc sa, sb;
-    uint32_t gea8, geb8;
-    lu_lane_init(da, sa, gea8, uh[4 * j + BA], data, data_len, ud, usize, nbad);
-    lu_lane_init(db, sb, geb8, uh[4 * j + BB], data, data_len, ud, usize, nbad);
-    da.tb = tb0;
-    db.tb = tb0 + DF_RING_BYTES;
-    {   // the first two chunks of each stream (the second only if the stream reaches it)
-        uint4 ca[DF_CQ], cb[DF_CQ];
-        df_fetch(sa, 0, ca);
-        df_fetch(sb, 0, cb);
-        const bool a2nd = da.last >= 1u, b2nd = db.last >= 1u;
-        if (a2nd) df_fetch(sa, 1, da.c);
-        if (b2nd) df_fetch(sb, 1, db.c);
-        df_put(lds8, da.tb, 0, ca);
-        df_put(lds8, db.tb, 0, cb);
-        if (a2nd) df_put(lds8, da.tb, 1, da.c);
-        if (b2nd) df_put(lds8, db.tb, 1, db.c);
+                                                   uint32_t tb, const uint8_t* sidecar, uint8_t* dst, uint32_t j) {
+    constexpr bool LIVE = lane_is_live<SPE>(B);
+    uint32_t nbad = 0, z = 0;
+    DfLane d;
+    DfSrc sr;
+    uint32_t ge8;
+    lu_lane_init(d, sr, ge8, uh[4 * j + B], data, data_len, ud, usize, nbad);
+    d.tb = tb;
+    {
+        uint4 c0[DF_CQ];
+        df_fetch(sr, 0, c0);
+        const bool second = d.last >= 1u;
+        if (second) df_fetch(sr, 1, d.c);
+        df_put(lds8, d.tb, 0, c0);
+        if (second) df_put(lds8, d.tb, 1, d.c);
     }
     const uint32_t K = len >> 8;  // full rows; a partial row K follows when len % 256 != 0
-    const uint32_t* sc32 = reinterpret_cast<const uint32_t*>(sidecar + (ubase >> 1) + 4 * (j >> 1));
-    const uint32_t sel = df_sel<SPE>(2 * (j & 1));
-    uint32_t* out32 = reinterpret_cast<uint32_t*>(dst + ubase + 4 * j);
+    uint8_t* o8 = dst + ubase + 4 * j + B;  // row k at o8[256 k]
+    // the zero planes' output bytes are the sidecar's: fp32 bytes 0, 1 of the
+    // element; bf16 byte 0 of each of the column's two elements
+    const uint8_t* s8 = sidecar + ((ubase + 4 * j) >> 1) + (SPE == 2 ? B : B / 2);  // row k at s8[128 k]
+    auto pair = [&](uint32_t k, uint32_t sv0, uint32_t sv1) __attribute__((always_inline)) {
+        uint32_t w = df_window(d, lds8), h0, h1;
+        const uint32_t t0 = df_sym(d.x, w, h0, tab);
+        const uint32_t t1 = df_sym(d.x, w, h1, tab);
+        d.p8 += h0 + h1;
+        if (LIVE) {
+            o8[256ull * k] = (uint8_t)(t0 >> 24);
+            o8[256ull * (k + 1)] = (uint8_t)(t1 >> 24);
+        } else {
+            z |= t0 | t1;
+            o8[256ull * k] = (uint8_t)sv0;
+            o8[256ull * (k + 1)] = (uint8_t)sv1;
+        }
+    };
     const uint32_t ng = K >> 3;
     if (ng) {
-        // sidecar words DF_AHEAD groups ahead, as in decode_fast_kernel
-        constexpr uint32_t A = DF_AHEAD;
         const uint32_t gl = ng - 1;
-        uint32_t sbuf[A + 1][8];
+        uint32_t sb[LU_AHEAD + 1][8];
+        auto load = [&](uint32_t (&v)[8], uint32_t g) __attribute__((always_inline)) {
+            if (!LIVE) {
+#pragma unroll
+                for (int r = 0; r < 8; r++) v[r] = s8[128ull * (8 * g + r)];
+            }
+        };
+#pragma unroll
+        for (uint32_t q = 0; q < LU_AHEAD; q++) load(sb[q], min(q, gl));
         uint32_t gi = 0;
-        if (!ZERO) {
+        for (; gi + LU_AHEAD + 1 <= ng; gi += LU_AHEAD + 1) {
 #pragma unroll
-            for (uint32_t q = 0; q < A; q++) df_load_sc(sbuf[q], sc32 + 256 * min(q, gl));
-        }
-        for (; gi + A + 1 <= ng; gi += A + 1) {
+            for (uint32_t q = 0; q <= LU_AHEAD; q++) {
+                load(sb[(q + LU_AHEAD) % (LU_AHEAD + 1)], min(gi + q + LU_AHEAD, gl));
 #pragma unroll
-            for (uint32_t q = 0; q <= A; q++) {
-                if (!ZERO) df_load_sc(sbuf[(q + A) % (A + 1)], sc32 + 256 * min(gi + q + A, gl));
-                lu_group<SPE, ZERO>(da, db, lds8, tab, out32 + 512 * (gi + q), sbuf[q], sel, sa, sb, za, zb);
+                for (int r = 0; r < 8; r += 2) pair(8 * (gi + q) + r, sb[q][r], sb[q][r + 1]);
+                df_step(d, lds8, sr);
             }
         }
 #pragma unroll
-        for (uint32_t q = 0; q < A; q++)
-            if (gi + q < ng) lu_group<SPE, ZERO>(da, db, lds8, tab, out32 + 512 * (gi + q), sbuf[q], sel, sa, sb, za, zb);
-    }
-    uint32_t k = 8 * ng;
-    for (; k + 2 <= K; k += 2)
-        lu_pair<SPE, ZERO>(da, db, lds8, tab, out32 + 64 * k, ZERO ? 0u : sc32[32 * k], ZERO ? 0u : sc32[32 * (k + 1)],
-                           sel, za, zb);
-    if (k < K) {
-        uint32_t wa = df_window(da, lds8), wb = df_window(db, lds8);
-        uint32_t ha, hb;
-        const uint32_t a0 = df_sym(da.x, wa, ha, tab);
-        const uint32_t b0 = df_sym(db.x, wb, hb, tab);
-        if (!ZERO) out32[64 * k] = df_pack<SPE>(a0, b0, sc32[32 * k], sel);
-        else { za |= a0; zb |= b0; }
-        da.p8 += ha;
-        db.p8 += hb;
-    }
-    // the partial top row: r bytes, nv of them in this column
-    const uint32_t r = len & 255u;
-    if (r > 4 * j) {
-        const uint32_t nv = min(r - 4 * j, 4u);
-        uint32_t wa = df_window(da, lds8), wb = df_window(db, lds8);
-        uint32_t ha = 0, hb = 0, v = 0, sa0 = 0, sb0 = 0;
-        if (nv > (uint32_t)BA) sa0 = df_sym(da.x, wa, ha, tab) >> 24;
-        if (nv > (uint32_t)BB) sb0 = df_sym(db.x, wb, hb, tab) >> 24;
-        v = sa0 << (8 * BA) | sb0 << (8 * BB);
-        da.p8 += ha;
-        db.p8 += hb;
-        if (!ZERO) {
-            const uint64_t pos = ubase + 256ull * K + 4 * j;
-            v = merge_sidecar_row<SPE>(sidecar, pos, v, nv);
-            uint8_t* d8 = dst + pos;
-            if (nv == 4) *reinterpret_cast<uint32_t*>(d8) = v;
-            else for (uint32_t q = 0; q < nv; q++) d8[q] = (uint8_t)(v >> (8 * q));
-        } else {
-            za |= sa0 << 24;
-            zb |= sb0 << 24;
+        for (uint32_t q = 0; q < LU_AHEAD; q++) {
+            if (gi + q < ng) {
+#pragma unroll
+                for (int r = 0; r < 8; r += 2) pair(8 * (gi + q) + r, sb[q][r], sb[q][r + 1]);
+                df_step(d, lds8, sr);
+            }
         }
     }
-    // a lane is bad when it does not end at state L with every byte consumed,
-    // or, in the zero planes, gave a nonzero symbol
-    nbad += (da.x != L || da.p8 != gea8 || (za >> 24)) ? 1u : 0u;
-    nbad += (db.x != L || db.p8 != geb8 || (zb >> 24)) ? 1u : 0u;
+    uint32_t k = 8 * ng;
+    for (; k + 2 <= K; k += 2) pair(k, LIVE ? 0u : s8[128ull * k], LIVE ? 0u : s8[128ull * (k + 1)]);
+    const bool top = 4 * j + B < (len & 255u);  // this lane holds a byte of the partial row K
+    if (k < K || top) {
+        uint32_t w = df_window(d, lds8), h0 = 0, h1 = 0;
+        if (k < K) {
+            const uint32_t t0 = df_sym(d.x, w, h0, tab);
+            if (LIVE) o8[256ull * k] = (uint8_t)(t0 >> 24);
+            else { z |= t0; o8[256ull * k] = s8[128ull * k]; }
+            k++;
+        }
+        if (top) {
+            const uint32_t t1 = df_sym(d.x, w, h1, tab);
+            if (LIVE) o8[256ull * K] = (uint8_t)(t1 >> 24);
+            else { z |= t1; o8[256ull * K] = s8[128ull * K]; }
+        }
+        d.p8 += h0 + h1;
+    }
+    // bad: not ending at state L with every byte consumed, or, in a zero
+    // plane, a nonzero symbol
+    nbad += (d.x != L || d.p8 != ge8 || (!LIVE && (z >> 24))) ? 1u : 0u;
     return nbad;
 }
 
 template <int SPE>
-__global__ void __launch_bounds__(128) decode_long_kernel(const uint8_t* __restrict__ data,
+__global__ void __launch_bounds__(256) decode_long_kernel(const uint8_t* __restrict__ data,
                                                           const ckr_stream_header* __restrict__ hdrs,
                                                           const uint64_t* __restrict__ unit_off,
                                                           const uint32_t* __restrict__ d_dec, EncodeGeom g,
@@ -3760,32 +3737,36 @@ __global__ void __launch_bounds__(128) decode_long_kernel(const uint8_t* __restr
     const bool raw = usize == len && uh[0].byte_count == len;
     if (blockIdx.y) {  // a raw unit: masked bytes | sidecar, rows shared by the blocks' waves
         if (!raw) return;
-        const uint32_t W = 2 * LU_RAW_BLOCKS;
-        for (uint32_t k = (blockIdx.y - 1) * 2 + wv; 256ull * k < len; k += W) {
+        const uint32_t W = 4 * LU_RAW_BLOCKS;
+        for (uint32_t k = (blockIdx.y - 1) * 4 + wv; 256ull * k < len; k += W) {
             const uint32_t p = 256 * k + 4 * j;
             if (p >= len) continue;
             const uint32_t nvalid = min(len - p, 4u);
             uint32_t v = 0;
             for (uint32_t q = 0; q < nvalid; q++) v |= (uint32_t)ud[p + q] << (8 * q);
             v = merge_sidecar_row<SPE>(sidecar, ubase + p, v, nvalid);
-            uint8_t* d = dst + ubase + p;
-            if (nvalid == 4) *reinterpret_cast<uint32_t*>(d) = v;
-            else for (uint32_t q = 0; q < nvalid; q++) d[q] = (uint8_t)(v >> (8 * q));
+            uint8_t* dd = dst + ubase + p;
+            if (nvalid == 4) *reinterpret_cast<uint32_t*>(dd) = v;
+            else for (uint32_t q = 0; q < nvalid; q++) dd[q] = (uint8_t)(v >> (8 * q));
         }
         return;
     }
     if (raw) return;
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
-    for (uint32_t i = threadIdx.x; i < 4096; i += 128) {
+    for (uint32_t i = threadIdx.x; i < 4096; i += 256) {
         const uint32_t e = d_dec[i];  // sym | (f - 1) << 8 | cum << 20
         lds[i] = (e & 0x000FFF00u) << 4 | (i - (e >> 20)) | (e & 255u) << 24;  // sym<<24 | (f-1)<<12 | slot-cum
     }
     __syncthreads();
     const uint64_t data_len = unit_off[g.n_units];
-    const uint32_t tb0 = DF_TAB_BYTES + wv * DF_WAVE_BYTES + 4 * j;
-    const uint32_t nbad =
-        wv == 0 ? lu_decode_wave<SPE, false>(data, data_len, uh, ud, usize, len, ubase, lds, lds8, tb0, sidecar, dst, j)
-                : lu_decode_wave<SPE, true>(data, data_len, uh, ud, usize, len, ubase, lds, lds8, tb0, sidecar, dst, j);
+    const uint32_t tb = DF_TAB_BYTES + wv * DF_RING_BYTES + 4 * j;
+    uint32_t nbad;
+    switch (wv) {
+        case 0: nbad = lu_decode_lane<SPE, 0>(data, data_len, uh, ud, usize, len, ubase, lds, lds8, tb, sidecar, dst, j); break;
+        case 1: nbad = lu_decode_lane<SPE, 1>(data, data_len, uh, ud, usize, len, ubase, lds, lds8, tb, sidecar, dst, j); break;
+        case 2: nbad = lu_decode_lane<SPE, 2>(data, data_len, uh, ud, usize, len, ubase, lds, lds8, tb, sidecar, dst, j); break;
+        default: nbad = lu_decode_lane<SPE, 3>(data, data_len, uh, ud, usize, len, ubase, lds, lds8, tb, sidecar, dst, j); break;
+    }
     if (nbad) atomicAdd(bad, (unsigned long long)nbad);
 }
 
@@ -3794,10 +3775,10 @@ hipError_t launch_decode_long(const uint8_t* data, const ckr_stream_header* hdrs
                               unsigned long long* bad, hipStream_t s) {
     if (g.n_units == 0) return hipSuccess;
     if (g.spe != 1 && g.spe != 2) return hipErrorInvalidValue;
-    const uint32_t lb = DF_TAB_BYTES + 2 * DF_WAVE_BYTES;
+    const uint32_t lb = DF_TAB_BYTES + 4 * DF_RING_BYTES;
     const dim3 grid((uint32_t)g.n_units, 1 + LU_RAW_BLOCKS);
-    if (g.spe == 2) CKR_LAUNCH("decode_long_kernel", s, decode_long_kernel<2><<<grid, 128, lb, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
-    else CKR_LAUNCH("decode_long_kernel", s, decode_long_kernel<1><<<grid, 128, lb, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
+    if (g.spe == 2) CKR_LAUNCH("decode_long_kernel", s, decode_long_kernel<2><<<grid, 256, lb, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
+    else CKR_LAUNCH("decode_long_kernel", s, decode_long_kernel<1><<<grid, 256, lb, s>>>(data, hdrs, unit_off, d_dec, g, sidecar, dst, bad));
     return hipGetLastError();
 }
 
