@@ -480,11 +480,12 @@ def test_encode_planes_matches_encode(tag, unit, paths, gpu):
     assert torch.equal(e3.sidecar[: m * spe], e1.sidecar[: m * spe])
 
 
-@pytest.mark.parametrize("unit", [65536, 1 << 20])
+@pytest.mark.parametrize("unit", [65536, 1 << 20, 0])
 def test_compress_many_matches_single_calls(unit, paths, gpu):
     """ckr_compress_many (jobs this small: every histogram first, then the
     encodes back to back) gives each job exactly what ckr_compress gives it, and
-    the oracle's bytes."""
+    the oracle's bytes; with unit 0 (one stream per tensor) the 1.2 MB fp32
+    tensor takes the long-unit kernels, the bf16 one the two-pass encoder."""
     import torch
     ck = _ck()
     specs = [(dg.F32, 300001, lambda n: dg.normal_f32(n, 1e-3, 70)),
