@@ -1239,6 +1239,29 @@ int dev_enc_queue_encode(const DevEnc& d, hipStream_t s) {
     return CKR_OK;
 }
 
+// The same encode as a job of launch_encode_fast_multi.
+ckr::FastJob dev_fast_job(const DevEnc& d) {
+    const EncodeLayout& L = d.L;
+    ckr::FastJob f{};
+    f.src = d.src;
+    f.g = d.g;
+    f.enc = reinterpret_cast<ckr::EncSym*>(d.ws + L.off_enc);
+    f.canon = reinterpret_cast<uint32_t*>(d.ws + L.off_canon);
+    f.hdrs = d.hdrs;
+    f.sidecar = d.side;
+    f.out = d.out;
+    f.unit_off = d.unit_off;
+    f.status = reinterpret_cast<uint64_t*>(d.ws + L.off_status);
+    f.ctl = d.dctl;
+    f.redo = reinterpret_cast<uint32_t*>(d.ws + L.off_redo);
+    f.dsl = d.dctl + 8 + 258;
+    f.sl0 = d.fp.sl0;
+    f.sl1 = d.fp.sl1;
+    f.cw = d.fp.cw;
+    f.canon_bytes = d.fp.canon_bytes;
+    return f;
+}
+
 int dev_enc_finish(const DevEnc& d, ckr_freq_table* h_table, uint64_t* h_total, bool* queued_more, hipStream_t s) {
     uint32_t hctl[6], ti[ckr::kTinfoWords];
     std::memcpy(hctl, d.pin, sizeof(hctl));
@@ -1580,19 +1603,24 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             std::vector<ckr::TableEncJob> tj(n);
             for (uint64_t i = 0; i < n; i++) tj[i] = dev_enc_table_job(dv[i], a->d_hists + 768 * i, ensure_full_alphabet);
             CKR_HIP(ckr::launch_table_enc_multi(tj.data(), (uint32_t)n, chains, a->s2));
-            CKR_HIP(hipEventRecord(a->ev, a->s2));
-            if (!g_prof_on) enc_streams = {s, a->s2, a->sx[0], a->sx[1]};
-            for (hipStream_t x : enc_streams)
-                if (x != a->s2) CKR_HIP(hipStreamWaitEvent(x, a->ev, 0));
-            for (uint64_t i = 0; i < n; i++) {
-                const int rc = dev_enc_queue_encode(dv[i], enc_streams[i % enc_streams.size()]);
-                if (rc) return rc;
+            // the encodes of all jobs of one kind (spe, sidecar) in one launch
+            // behind the tables, at most kMaxFastJobs a launch
+            {
+                std::vector<ckr::FastJob> fj[4];
+                for (uint64_t i = 0; i < n; i++) {
+                    if (!geo[i].n_units) continue;
+                    const ckr::FastJob f = dev_fast_job(dv[i]);
+                    fj[(f.g.spe == 2 ? 2 : 0) + (f.sidecar ? 1 : 0)].push_back(f);
+                }
+                for (auto& v : fj)
+                    for (size_t o = 0; o < v.size(); o += ckr::kMaxFastJobs)
+                        CKR_HIP(ckr::launch_encode_fast_multi(v.data() + o,
+                                                              (uint32_t)std::min<size_t>(ckr::kMaxFastJobs, v.size() - o),
+                                                              (uint32_t)max_lds_per_block(), a->s2));
             }
-            for (size_t k = 0; k < enc_streams.size(); k++) {  // the caller's stream waits for the others
-                if (enc_streams[k] == s) continue;
-                CKR_HIP(hipEventRecord(a->ev_x[k % 3], enc_streams[k]));
-                CKR_HIP(hipStreamWaitEvent(s, a->ev_x[k % 3], 0));
-            }
+            CKR_HIP(hipEventRecord(a->ev, a->s2));  // the caller's stream waits for them
+            CKR_HIP(hipStreamWaitEvent(s, a->ev, 0));
+            enc_streams = {s, a->s2};
             CKR_HIP(hipMemcpyAsync(a->tslots, a->d_tslots, n * kCtlWords * 4, hipMemcpyDeviceToHost, s));
             for (hipStream_t x : enc_streams) CKR_HIP(hipStreamSynchronize(x));
             bool more = false;

@@ -138,6 +138,32 @@ hipError_t launch_encode_fast_list(const uint8_t* src, const EncodeGeom& g, cons
                                    const FastEncParamsHost& hp, uint32_t lds_limit, ckr_stream_header* hdrs,
                                    uint8_t* out, uint64_t* unit_off, uint64_t* status, uint32_t* ctl,
                                    uint32_t* redo_list, hipStream_t s);
+// Several tensors' fast encodes in one launch (same spe, sidecars for all or
+// none, tables the data's own): each job's arguments as launch_encode_fast's,
+// dsl its device slot sizes (sl0, sl1: the largest the launch's LDS holds);
+// wg0 is set by the launcher.
+struct FastJob {
+    const uint8_t* src;
+    EncodeGeom g;
+    const EncSym* enc;
+    const uint32_t* canon;
+    ckr_stream_header* hdrs;
+    uint8_t* sidecar;
+    uint8_t* out;
+    uint64_t* unit_off;
+    uint64_t* status;
+    uint32_t* ctl;
+    uint32_t* redo;
+    const uint32_t* dsl;
+    uint32_t sl0, sl1, cw, canon_bytes;
+    uint32_t wg0;
+};
+constexpr uint32_t kMaxFastJobs = 16;
+struct FastJobs {
+    uint32_t n;
+    FastJob j[kMaxFastJobs];
+};
+hipError_t launch_encode_fast_multi(const FastJob* jobs, uint32_t n, uint32_t lds_limit, hipStream_t s);
 // u64 look-back words of the fast encoder for n units (status argument size).
 uint64_t encode_fast_status_words(uint64_t n_units);
 // dsl (may be null): the two slot sizes in device memory (table_enc's tinfo +

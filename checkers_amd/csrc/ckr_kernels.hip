@@ -1382,17 +1382,17 @@ __host__ __device__ constexpr uint32_t ws_lds_bytes(uint32_t pairs, uint32_t can
 // redo_list) coded again with slots large enough for any lane (2 bytes per
 // row), at the offsets that launch published; tickets from ctl[3]; no sidecar,
 // no look-back.  A lane that outgrew even those slots would set ctl[2] bit 1.
-template <int SPE, bool ESC, bool SIDE, int PAIRS, int NPK, bool LIST = false>
-__global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_waves_per_eu(4))) encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g,
-                                                                  const EncSym* __restrict__ d_enc,
-                                                                  const uint32_t* __restrict__ canon, FastEncParams fp,
-                                                                  ckr_stream_header* __restrict__ hdrs,
-                                                                  uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out,
-                                                                  uint64_t* __restrict__ unit_off,
-                                                                  uint64_t* __restrict__ status, uint32_t* __restrict__ ctl,
-                                                                  uint32_t* __restrict__ redo_list,
-                                                                  uint64_t* __restrict__ phase,
-                                                                  const uint32_t* __restrict__ dsl) {
+template <int SPE, bool ESC, bool SIDE, int PAIRS, int NPK, bool LIST>
+__device__ __forceinline__ void encode_fast_body(const uint8_t* __restrict__ src, EncodeGeom g,
+                                                 const EncSym* __restrict__ d_enc,
+                                                 const uint32_t* __restrict__ canon, FastEncParams fp,
+                                                 ckr_stream_header* __restrict__ hdrs,
+                                                 uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out,
+                                                 uint64_t* __restrict__ unit_off,
+                                                 uint64_t* __restrict__ status, uint32_t* __restrict__ ctl,
+                                                 uint32_t* __restrict__ redo_list,
+                                                 uint64_t* __restrict__ phase,
+                                                 const uint32_t* __restrict__ dsl) {
     if (LIST && __hip_atomic_load(&ctl[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) return;  // nothing to redo
     if (dsl) {  // slot sizes made on the device (table_enc_kernel), within the launch's LDS
         fp.sl0 = dsl[0]; fp.sl1 = dsl[1];
@@ -1752,6 +1752,35 @@ __global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_
 }
 
 
+template <int SPE, bool ESC, bool SIDE, int PAIRS, int NPK, bool LIST = false>
+__global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_waves_per_eu(4)))
+encode_fast_kernel(const uint8_t* __restrict__ src, EncodeGeom g, const EncSym* __restrict__ d_enc,
+                   const uint32_t* __restrict__ canon, FastEncParams fp, ckr_stream_header* __restrict__ hdrs,
+                   uint8_t* __restrict__ sidecar, uint8_t* __restrict__ out, uint64_t* __restrict__ unit_off,
+                   uint64_t* __restrict__ status, uint32_t* __restrict__ ctl, uint32_t* __restrict__ redo_list,
+                   uint64_t* __restrict__ phase, const uint32_t* __restrict__ dsl) {
+    encode_fast_body<SPE, ESC, SIDE, PAIRS, NPK, LIST>(src, g, d_enc, canon, fp, hdrs, sidecar, out, unit_off, status,
+                                                       ctl, redo_list, phase, dsl);
+}
+
+// Several tensors' fast encodes in one launch (a shard of small tensors): the
+// workgroups are shared out in proportion to the jobs' units, workgroup b
+// working for the last job whose first workgroup is <= b, each job with its
+// own tickets, look-back and outputs.  One launch instead of one per tensor,
+// and no tensor waits for another's workgroups to leave the CUs.
+template <int SPE, bool SIDE, int PAIRS, int NPK>
+__global__ void __launch_bounds__(64 * (2 + NPK) * PAIRS) __attribute__((amdgpu_waves_per_eu(4)))
+encode_fast_multi_kernel(FastJobs J) {
+    uint32_t k = 0;
+    while (k + 1 < J.n && J.j[k + 1].wg0 <= blockIdx.x) k++;
+    const FastJob& b = J.j[k];
+    FastEncParams fp;
+    fp.sl0 = b.sl0; fp.sl1 = b.sl1; fp.cw = b.cw; fp.canon_bytes = b.canon_bytes;
+    fp.stride0 = slot_stride(b.sl0); fp.stride1 = slot_stride(b.sl1);
+    encode_fast_body<SPE, false, SIDE, PAIRS, NPK, false>(b.src, b.g, b.enc, b.canon, fp, b.hdrs, b.sidecar, b.out,
+                                                          b.unit_off, b.status, b.ctl, b.redo, nullptr, b.dsl);
+}
+
 uint64_t encode_fast_status_words(uint64_t n_units) { return n_units + 2 * ((n_units + 63) / 64); }
 
 // Coder pairs per workgroup that fit the LDS limit (0: none).
@@ -1813,6 +1842,62 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
 #undef CKR_FAST_ENC
 #undef CKR_FAST_ENC_P
     return e;
+}
+
+hipError_t launch_encode_fast_multi(const FastJob* jobs, uint32_t n, uint32_t lds_limit, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    if (n > kMaxFastJobs) return hipErrorInvalidValue;
+    const int spe = jobs[0].g.spe;
+    const bool side = jobs[0].sidecar != nullptr;
+    uint32_t pairs = 2, lb = 0;
+    uint64_t units = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        if (jobs[i].g.spe != spe || (jobs[i].sidecar != nullptr) != side || (spe != 1 && spe != 2))
+            return hipErrorInvalidValue;
+        const FastEncParamsHost hp{jobs[i].sl0, jobs[i].sl1, jobs[i].cw, jobs[i].canon_bytes, false};
+        const uint32_t pj = fast_enc_pairs(hp, lds_limit);
+        if (!pj) return hipErrorInvalidValue;
+        pairs = std::min(pairs, pj);
+        units += jobs[i].g.n_units;
+    }
+    for (uint32_t i = 0; i < n; i++)
+        lb = std::max(lb, ws_lds_bytes(pairs, jobs[i].canon_bytes, slot_stride(jobs[i].sl0), slot_stride(jobs[i].sl1)));
+    int dev = 0, ncu = 0;
+    hipError_t e;
+    if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+    if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+    auto run = [&](auto kern, uint32_t nthreads) -> hipError_t {
+        hipError_t r = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)lb);
+        if (r != hipSuccess) return r;
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, nthreads, lb) != hipSuccess || per_cu < 1)
+            per_cu = 1;
+        // workgroups in proportion to the jobs' units (rounded up, so that a small
+        // job is not left behind), never more than a job's units need
+        const uint64_t slots = (uint64_t)per_cu * (uint64_t)std::max(ncu, 1);
+        FastJobs J{};
+        J.n = n;
+        uint32_t wg = 0;
+        for (uint32_t i = 0; i < n; i++) {
+            J.j[i] = jobs[i];
+            const uint64_t need = (jobs[i].g.n_units + pairs - 1) / pairs;
+            const uint64_t share = units ? (slots * jobs[i].g.n_units + units - 1) / units : 1;
+            J.j[i].wg0 = wg;
+            wg += (uint32_t)std::max<uint64_t>(1, std::min(need, share));
+        }
+        CKR_LAUNCH("encode_fast_kernel", s, kern<<<wg, nthreads, lb, s>>>(J));
+        return hipGetLastError();
+    };
+    if (spe == 2)
+        return pairs == 2 ? (side ? run(encode_fast_multi_kernel<2, true, 2, ENC_NPK>, 128u * (2 + ENC_NPK))
+                                  : run(encode_fast_multi_kernel<2, false, 2, ENC_NPK>, 128u * (2 + ENC_NPK)))
+                          : (side ? run(encode_fast_multi_kernel<2, true, 1, ENC_NPK>, 64u * (2 + ENC_NPK))
+                                  : run(encode_fast_multi_kernel<2, false, 1, ENC_NPK>, 64u * (2 + ENC_NPK)));
+    return pairs == 2 ? (side ? run(encode_fast_multi_kernel<1, true, 2, ENC_NPK>, 128u * (2 + ENC_NPK))
+                              : run(encode_fast_multi_kernel<1, false, 2, ENC_NPK>, 128u * (2 + ENC_NPK)))
+                      : (side ? run(encode_fast_multi_kernel<1, true, 1, ENC_NPK>, 64u * (2 + ENC_NPK))
+                              : run(encode_fast_multi_kernel<1, false, 1, ENC_NPK>, 64u * (2 + ENC_NPK)));
 }
 
 // The redo list of a launch_encode_fast launch (ctl[1] units, queued once the

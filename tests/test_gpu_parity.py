@@ -613,6 +613,36 @@ def test_compress_many_repeated_byte_identical(gpu):
             assert r.total == ref.numel() and torch.equal(r.data[: r.total], ref), (it, k)
 
 
+def test_compress_many_one_launch_for_many_jobs(gpu):
+    """A shard of more small tensors than one encode launch takes (22 bf16 of
+    sizes from 1 element to 3 MiB, 4 fp32): the encodes of each kind go in
+    launches of at most 16 jobs, workgroups shared in proportion to the jobs'
+    units; every tensor's bytes, headers and offsets equal one ckr_compress of
+    it, twice in a row."""
+    import torch
+    ck = _ck()
+    g = torch.Generator(device=gpu).manual_seed(83)
+    sizes = [1, 7, 4096, 32768, 32769, 100_000, 1 << 20, 1_500_001] + [(k * 97_531) % 1_600_000 + 1 for k in range(14)]
+    ts = [(torch.randn(n, device=gpu, generator=g) * 0.02).to(torch.bfloat16) for n in sizes]
+    ts += [torch.randn(n, device=gpu, generator=g) * 1e-3 for n in (3, 65536, 700_001, 250_000)]
+    tags = [ck.torch_tag(t.dtype) for t in ts]
+    srcs = [t.view(torch.uint8) for t in ts]
+    refs = []
+    for t, tag, s in zip(ts, tags, srcs):
+        e = ck.Encoder(t.numel(), tag, 65536, device=gpu).compress(s)
+        torch.cuda.synchronize()
+        refs.append((e.total, e.data[: e.total].clone(), e.headers.clone(), e.unit_offsets.clone(), e.table.norm.copy()))
+    encs = [ck.Encoder(t.numel(), tag, 65536, device=gpu) for t, tag in zip(ts, tags)]
+    for it in range(2):
+        print(f"[case] compress_many {len(ts)} jobs, call {it}", flush=True)
+        res = ck.compress_many(encs, srcs)
+        torch.cuda.synchronize()
+        for k, (r, (tot, data, hdr, off, norm)) in enumerate(zip(res, refs)):
+            assert r.total == tot and torch.equal(r.data[: r.total], data), (it, k)
+            assert torch.equal(r.headers, hdr) and torch.equal(r.unit_offsets, off), (it, k)
+            assert np.array_equal(r.table.norm, norm), (it, k)
+
+
 def test_compress_many_large_overlapped_histogram(gpu):
     """A tensor above the 256 MiB bound under which compress_many counts every
     histogram first, so that its histogram runs beside the previous encode (8
