@@ -76,12 +76,18 @@ class StatsRecord(ctypes.Structure):
                 ("d_minmax", ctypes.c_void_p), ("d_fingerprint", ctypes.c_void_p)]
 
 
-class _AlignedTable:
-    """A FreqTable placed at a 64-byte aligned address (the C type is alignas(64))."""
+_TABLE_SPAN = 40000 + 64  # sizeof(ckr_freq_table) and room to align it
 
-    def __init__(self):
-        self._buf = ctypes.create_string_buffer(40000 + 64)
-        addr = ctypes.addressof(self._buf)
+
+class _AlignedTable:
+    """A FreqTable placed at a 64-byte aligned address (the C type is alignas(64)).
+    The memory is not cleared: every library call that returns a table writes
+    all of it.  buf/off: a slice of a buffer shared by several tables."""
+
+    def __init__(self, buf=None, addr=None):
+        self._buf = np.empty(_TABLE_SPAN, np.uint8) if buf is None else buf
+        if addr is None:
+            addr = self._buf.ctypes.data
         self.table = FreqTable.from_address((addr + 63) & ~63)
 
     @property
@@ -102,6 +108,13 @@ class _AlignedTable:
 
 def aligned_table():
     return _AlignedTable()
+
+
+def _aligned_tables(n):
+    """n tables in one buffer (one allocation for a batched call)."""
+    buf = np.empty(n * _TABLE_SPAN, np.uint8)
+    a0 = buf.ctypes.data
+    return [_AlignedTable(buf, a0 + k * _TABLE_SPAN) for k in range(n)]
 
 
 _lib = None
@@ -310,6 +323,14 @@ class Encoded:
         return self.data[: self.total].cpu().numpy()
 
 
+class CompressJob(ctypes.Structure):
+    _fields_ = [("d_src", ctypes.c_void_p), ("n_elems", ctypes.c_uint64), ("dtype", ctypes.c_int32),
+                ("pad", ctypes.c_int32), ("d_out", ctypes.c_void_p), ("out_capacity", ctypes.c_uint64),
+                ("d_headers", ctypes.c_void_p), ("d_unit_offsets", ctypes.c_void_p), ("d_sidecar", ctypes.c_void_p),
+                ("d_workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_uint64), ("h_table", ctypes.c_void_p),
+                ("total", ctypes.c_uint64)]
+
+
 class Encoder:
     """Reusable buffers for repeated encodes of one tensor shape (bench / tests)."""
 
@@ -330,6 +351,12 @@ class Encoder:
         self.unit_offsets = torch.empty(self.n_units + 1, dtype=torch.int64, device=device)
         spe = Lb.ckr_sidecar_bytes_per_elem(dtype)
         self.sidecar = _empty(self.n_elems * spe, device) if spe else None
+        # this encoder's part of a compress_many job record, filled once
+        self._job = CompressJob(None, self.n_elems, self.dtype, 0, self.out.data_ptr(), self.out_cap,
+                                self.headers.data_ptr(), self.unit_offsets.data_ptr(),
+                                self.sidecar.data_ptr() if self.sidecar is not None else None,
+                                self.ws.data_ptr(), self.ws_bytes, None, 0)
+        self._job_addr = ctypes.addressof(self._job)
 
     def _check_src(self, src):
         if src.numel() * src.element_size() < self.n_bytes:
@@ -367,14 +394,6 @@ class Encoder:
                        self.dtype, self.unit_bytes, t)
 
 
-class CompressJob(ctypes.Structure):
-    _fields_ = [("d_src", ctypes.c_void_p), ("n_elems", ctypes.c_uint64), ("dtype", ctypes.c_int32),
-                ("pad", ctypes.c_int32), ("d_out", ctypes.c_void_p), ("out_capacity", ctypes.c_uint64),
-                ("d_headers", ctypes.c_void_p), ("d_unit_offsets", ctypes.c_void_p), ("d_sidecar", ctypes.c_void_p),
-                ("d_workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_uint64), ("h_table", ctypes.c_void_p),
-                ("total", ctypes.c_uint64)]
-
-
 def compress_many(encoders, srcs, ensure_full_alphabet=False, stream=None):
     """ckr_compress_many: each (Encoder, source) pair compressed as Encoder.compress
     would, the next tensor's histogram overlapping the current one's encode.
@@ -385,19 +404,18 @@ def compress_many(encoders, srcs, ensure_full_alphabet=False, stream=None):
         raise CkrError(CKR_E_INVALID, "compress_many: an Encoder appears twice (its buffers would be shared)")
     if not encoders:
         return []
-    jobs = (CompressJob * len(encoders))()
-    tables = []
-    for jb, e, src in zip(jobs, encoders, srcs):
-        e._check_src(src)
-        t = aligned_table()
-        tables.append(t)
-        jb.d_src, jb.n_elems, jb.dtype = src.data_ptr(), e.n_elems, e.dtype
-        jb.d_out, jb.out_capacity = e.out.data_ptr(), e.out_cap
-        jb.d_headers, jb.d_unit_offsets = e.headers.data_ptr(), e.unit_offsets.data_ptr()
-        jb.d_sidecar = e.sidecar.data_ptr() if e.sidecar is not None else None
-        jb.d_workspace, jb.workspace_bytes, jb.h_table = e.ws.data_ptr(), e.ws_bytes, ctypes.addressof(t.table)
-    _check(lib().ckr_compress_many(ctypes.addressof(jobs), len(encoders), encoders[0].unit_bytes,
-                                   int(bool(ensure_full_alphabet)), _stream(stream)))
+    n = len(encoders)
+    jobs = (CompressJob * n)()
+    tables = _aligned_tables(n)
+    base, size = ctypes.addressof(jobs), ctypes.sizeof(CompressJob)
+    for k, (e, src, t) in enumerate(zip(encoders, srcs, tables)):
+        if src.nbytes < e.n_bytes:
+            e._check_src(src)
+        ctypes.memmove(base + k * size, e._job_addr, size)
+        jb = jobs[k]
+        jb.d_src, jb.h_table = src.data_ptr(), ctypes.addressof(t.table)
+    _check(lib().ckr_compress_many(base, n, encoders[0].unit_bytes, int(bool(ensure_full_alphabet)),
+                                   _stream(stream)))
     return [Encoded(e.out, e.headers, e.unit_offsets, e.sidecar, jb.total, e.n_elems, e.dtype, e.unit_bytes, t)
             for jb, e, t in zip(jobs, encoders, tables)]
 

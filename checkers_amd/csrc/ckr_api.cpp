@@ -1568,11 +1568,13 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             a->d_hist_jobs = n;
         }
         // every histogram in one grid (per 16 jobs) and one read-back: a launch
-        // and a copy per job cost more host time than their kernels take
+        // and a copy per job cost more host time than their kernels take; the
+        // grid goes first, so that the host's set-up below overlaps it
         std::vector<ckr::HistSrc> hs(n);
         for (uint64_t i = 0; i < n; i++)
             hs[i] = {static_cast<const uint8_t*>(staged[i].p), geo[i].n_bytes, ckr_element_size(jobs[i].dtype),
                      (int)geo[i].spe};
+        CKR_HIP(ckr::launch_masked_hist_multi(hs.data(), (uint32_t)n, a->d_hists, a->s2));
         // tables on the device when every job's tensor is one the fast encoder
         // takes: no read-back or host table between the histograms and the
         // encodes (a job whose ranks leave its table to the sort is encoded
@@ -1595,7 +1597,6 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
                                     a->d_tslots + kCtlWords * i, a->tslots + kCtlWords * i);
         const void* chains = dev_all ? canon_chains(a->s2) : nullptr;
         dev_all = dev_all && chains;
-        CKR_HIP(ckr::launch_masked_hist_multi(hs.data(), (uint32_t)n, a->d_hists, a->s2));
         if (dev_all) {
             // every table in one launch behind the histograms, then the encodes
             // round robin over four streams, then one read-back of every job's
