@@ -351,7 +351,20 @@ class Encoder:
         self.unit_offsets = torch.empty(self.n_units + 1, dtype=torch.int64, device=device)
         spe = Lb.ckr_sidecar_bytes_per_elem(dtype)
         self.sidecar = _empty(self.n_elems * spe, device) if spe else None
-        # this encoder's part of a compress_many job record, filled once
+        self._make_job()
+
+    # the buffers a compress_many job record points at: replacing one of them
+    # rebuilds this encoder's record
+    _JOB_BUFFERS = frozenset(("ws", "out", "out_cap", "headers", "unit_offsets", "sidecar", "ws_bytes"))
+
+    def __setattr__(self, name, value):
+        object.__setattr__(self, name, value)
+        if name in Encoder._JOB_BUFFERS and "_job" in self.__dict__:
+            self._make_job()
+
+    def _make_job(self):
+        """This encoder's part of a compress_many job record (all but the
+        source and the table), copied into each call's records."""
         self._job = CompressJob(None, self.n_elems, self.dtype, 0, self.out.data_ptr(), self.out_cap,
                                 self.headers.data_ptr(), self.unit_offsets.data_ptr(),
                                 self.sidecar.data_ptr() if self.sidecar is not None else None,

@@ -337,7 +337,7 @@ EncodeLayout encode_layout(const ckr::EncodeGeom& g) {
     const CanonKs ck = canon_ks(g);
     uint64_t o = 0;
     L.off_enc = o;     o = align_up(o + 256 * sizeof(ckr::EncSym), kAlign);
-    L.off_hist = o;    o = align_up(o + 768 * 4, kAlign);
+    L.off_hist = o;    o = align_up(o + ckr::kHistTableWords * 4, kAlign);
     L.off_canon = o;   o = align_up(o + 3ull * (4 + 2 * ck.cw) * 4, kAlign);
     L.off_status = o;  o = align_up(o + ckr::encode_fast_status_words(g.n_units) * 8, kAlign);
     L.off_ctl = o;     o = align_up(o + kCtlWords * 4, kAlign);  // control words, then a device table's words
@@ -1190,6 +1190,8 @@ struct DevEnc {
     uint8_t* side = nullptr;
     uint32_t* dctl = nullptr;  // device: the control words, then the table's words (kCtlWords)
     uint32_t* pin = nullptr;   // their pinned host copy
+    uint64_t epoch = 0;        // of the histogram and table launch (ctl[6..7] once the table is built)
+    bool redo_queued = false;  // the list-mode redo pass follows the encode on its stream
 };
 
 // Whether the device table can serve this tensor, and its encode parameters
@@ -1215,10 +1217,9 @@ bool dev_enc_setup(DevEnc& d, const void* src, const ckr::EncodeGeom& g, uint8_t
     return ckr::encode_fast_lds_bytes(d.fp, (uint32_t)max_lds_per_block()) != 0;
 }
 
-// The table set-up of one tensor, for launch_table_enc_multi.
-ckr::TableEncJob dev_enc_table_job(const DevEnc& d, const uint32_t* d_hist, int ensure_full) {
+// The table set-up of one tensor, for launch_hist_table.
+ckr::TableEncJob dev_enc_table_job(const DevEnc& d, int ensure_full) {
     ckr::TableEncJob t{};
-    t.hist = d_hist;
     t.enc = reinterpret_cast<ckr::EncSym*>(d.ws + d.L.off_enc);
     t.canon = reinterpret_cast<uint32_t*>(d.ws + d.L.off_canon);
     t.tinfo = d.dctl + 8;
@@ -1263,9 +1264,11 @@ ckr::FastJob dev_fast_job(const DevEnc& d) {
 }
 
 int dev_enc_finish(const DevEnc& d, ckr_freq_table* h_table, uint64_t* h_total, bool* queued_more, hipStream_t s) {
-    uint32_t hctl[6], ti[ckr::kTinfoWords];
+    uint32_t hctl[8], ti[ckr::kTinfoWords];
     std::memcpy(hctl, d.pin, sizeof(hctl));
     std::memcpy(ti, d.pin + 8, sizeof(ti));
+    if ((hctl[6] | (uint64_t)hctl[7] << 32) != d.epoch || (hctl[2] & 4u))
+        return fail(CKR_E_HIP, "[ckr] histogram and table launch did not complete (flags %u)", hctl[2]);
     if (ti[257]) return kUseHostTable;
     if (hctl[2]) return fail(CKR_E_HIP, "[ckr] fast encode did not complete (flags %u: 1 look-back, 2 redo slots)", hctl[2]);
     if (h_table) {
@@ -1273,7 +1276,7 @@ int dev_enc_finish(const DevEnc& d, ckr_freq_table* h_table, uint64_t* h_total, 
         fill_table(ti, h_table);
     }
     if (h_total) std::memcpy(h_total, &hctl[4], 8);
-    if (!hctl[1]) return CKR_OK;
+    if (!hctl[1] || d.redo_queued) return CKR_OK;
     // units that outgrew their slots
     uint8_t* ws = d.ws;
     const EncodeLayout& L = d.L;
@@ -1308,12 +1311,22 @@ int compress_device_table(const void* src, const ckr::EncodeGeom& g, int ensure_
     if (!dev_enc_setup(d, src, g, ws, d_out, d_headers, d_unit_offsets, d_sidecar, nullptr, pw)) return kUseHostTable;
     const void* chains = canon_chains(s);
     if (!chains) return kUseHostTable;
-    auto* hist = reinterpret_cast<uint32_t*>(ws + d.L.off_hist);
-    CKR_HIP(ckr::launch_masked_hist(d.src, g.n_bytes, g.es, g.spe, hist, hist + 256, s));
-    const ckr::TableEncJob t = dev_enc_table_job(d, hist, ensure_full_alphabet);
-    CKR_HIP(ckr::launch_table_enc_multi(&t, 1, chains, s));
+    uint32_t* hist = reinterpret_cast<uint32_t*>(ws + d.L.off_hist);
+    const ckr::HistSrc hs{d.src, g.n_bytes, g.es, (int)g.spe};
+    const ckr::TableEncJob t = dev_enc_table_job(d, ensure_full_alphabet);
+    CKR_HIP(ckr::launch_hist_table(&hs, &hist, &t, 1, chains, &d.epoch, s));
     int rc = dev_enc_queue_encode(d, s);
     if (rc) return rc;
+    // the redo pass right behind the encode, with no read-back between them:
+    // it ends at once when no unit outgrew its slots
+    const uint32_t lds_limit = (uint32_t)max_lds_per_block();
+    if (ckr::encode_fast_list_fits(d.fp, g, lds_limit)) {
+        CKR_HIP(ckr::launch_encode_fast_list(d.src, g, reinterpret_cast<ckr::EncSym*>(ws + d.L.off_enc),
+                                             reinterpret_cast<uint32_t*>(ws + d.L.off_canon), d.fp, lds_limit, d.hdrs,
+                                             d.out, d.unit_off, reinterpret_cast<uint64_t*>(ws + d.L.off_status), d.dctl,
+                                             reinterpret_cast<uint32_t*>(ws + d.L.off_redo), s));
+        d.redo_queued = true;
+    }
     CKR_HIP(hipMemcpyAsync(pw, d.dctl, kCtlWords * 4, hipMemcpyDeviceToHost, s));
     CKR_HIP(hipStreamSynchronize(s));
     bool more = false;
@@ -1564,17 +1577,13 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             if (a->d_hists) CKR_HIP(hipFree(a->d_hists));
             a->d_hists = nullptr;
             a->d_hist_jobs = 0;
-            CKR_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_hists), n * 768 * sizeof(uint32_t)));
+            CKR_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_hists), n * ckr::kHistTableWords * sizeof(uint32_t)));
             a->d_hist_jobs = n;
         }
-        // every histogram in one grid (per 16 jobs) and one read-back: a launch
-        // and a copy per job cost more host time than their kernels take; the
-        // grid goes first, so that the host's set-up below overlaps it
         std::vector<ckr::HistSrc> hs(n);
         for (uint64_t i = 0; i < n; i++)
             hs[i] = {static_cast<const uint8_t*>(staged[i].p), geo[i].n_bytes, ckr_element_size(jobs[i].dtype),
                      (int)geo[i].spe};
-        CKR_HIP(ckr::launch_masked_hist_multi(hs.data(), (uint32_t)n, a->d_hists, a->s2));
         // tables on the device when every job's tensor is one the fast encoder
         // takes: no read-back or host table between the histograms and the
         // encodes (a job whose ranks leave its table to the sort is encoded
@@ -1598,12 +1607,18 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         const void* chains = dev_all ? canon_chains(a->s2) : nullptr;
         dev_all = dev_all && chains;
         if (dev_all) {
-            // every table in one launch behind the histograms, then the encodes
-            // round robin over four streams, then one read-back of every job's
-            // control and table words
+            // every histogram and table in one grid (per 16 jobs), the tables
+            // built by each job's last workgroup, then the encodes, then one
+            // read-back of every job's control and table words
+            std::vector<uint32_t*> hp(n);
             std::vector<ckr::TableEncJob> tj(n);
-            for (uint64_t i = 0; i < n; i++) tj[i] = dev_enc_table_job(dv[i], a->d_hists + 768 * i, ensure_full_alphabet);
-            CKR_HIP(ckr::launch_table_enc_multi(tj.data(), (uint32_t)n, chains, a->s2));
+            std::vector<uint64_t> ep(n);
+            for (uint64_t i = 0; i < n; i++) {
+                hp[i] = a->d_hists + ckr::kHistTableWords * i;
+                tj[i] = dev_enc_table_job(dv[i], ensure_full_alphabet);
+            }
+            CKR_HIP(ckr::launch_hist_table(hs.data(), hp.data(), tj.data(), (uint32_t)n, chains, ep.data(), a->s2));
+            for (uint64_t i = 0; i < n; i++) dv[i].epoch = ep[i];
             // the encodes of all jobs of one kind (spe, sidecar) in one launch
             // behind the tables, at most kMaxFastJobs a launch
             {
@@ -1630,7 +1645,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
                 int rc = dev_enc_finish(dv[i], jb.h_table, &jb.total, &more, s);
                 if (rc == kUseHostTable) {  // the sorted table decides: encode this job again
                     uint32_t hh[768];
-                    CKR_HIP(hipMemcpy(hh, a->d_hists + 768 * i, sizeof(hh), hipMemcpyDeviceToHost));
+                    CKR_HIP(hipMemcpy(hh, a->d_hists + ckr::kHistTableWords * i, sizeof(hh), hipMemcpyDeviceToHost));
                     ckr_freq_table local;
                     ckr_freq_table* t = jb.h_table ? jb.h_table : &local;
                     rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
@@ -1645,6 +1660,9 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             drain.ok = true;
             return CKR_OK;
         }
+        // every histogram in one grid (per 16 jobs) and one read-back: a launch
+        // and a copy per job cost more host time than their kernels take
+        CKR_HIP(ckr::launch_masked_hist_multi(hs.data(), (uint32_t)n, a->d_hists, a->s2));
         CKR_HIP(hipMemcpyAsync(a->hists, a->d_hists, n * 768 * sizeof(uint32_t), hipMemcpyDeviceToHost, a->s2));
         for (hipStream_t x : a->sx) CKR_HIP(hipStreamWaitEvent(x, a->ev, 0));  // inputs ready
         CKR_HIP(hipStreamSynchronize(a->s2));

@@ -175,24 +175,16 @@ hipError_t launch_encode_fast(const uint8_t* src, const EncodeGeom& g, const Enc
 // Tables by ranks on the device (ckr_table.h): n histograms of 256 words into
 // rows of 258 (norm_freq[256], sum, ambiguity flag).
 hipError_t launch_tables(const uint32_t* hists, uint64_t n, int ensure_full, uint32_t* rows, hipStream_t s);
-// A tensor's encode set-up from its 768-word histograms (masked, plane FL,
-// plane 3) with no host round trip: table by ranks, encode entries, canonical
-// zero-plane streams for lane counts k0, k1, k2 (cw dwords), the fast
-// encoder's slot sizes (each at most smax, their sum at most 2 smax), and its
-// status and control words cleared.  tinfo: norm[256], sum, ambiguity, sl0, sl1.
-// chains: the state chains of symbol 0 for every count (launch_canon_chains,
-// kChainBytes, built once per device), from which the canonical streams are read.
-hipError_t launch_table_enc(const uint32_t* hist, const EncodeGeom& g, int ensure_full, uint32_t K, uint32_t k0,
-                            uint32_t k1, uint32_t k2, uint32_t cw, uint32_t smax, EncSym* d_enc, uint32_t* canon,
-                            uint32_t* tinfo, uint64_t* status, uint32_t* ctl, const void* chains, hipStream_t s);
-// Batched: up to kMaxTableJobs tensors per launch (their status word counts
-// encode_fast_status_words(n_units) each).
+// A tensor's encode set-up from its histograms with no host round trip: table
+// by ranks, encode entries, canonical zero-plane streams for lane counts k0,
+// k1, k2 (cw dwords), the fast encoder's slot sizes (each at most smax, their
+// sum at most 2 smax), and its status and control words cleared.  tinfo:
+// norm[256], sum, ambiguity, sl0, sl1.
 struct TableEncArg {
     uint32_t K, k0, k1, k2, cw, smax;
     int ensure_full;
 };
 struct TableEncJob {
-    const uint32_t* hist;
     EncSym* enc;
     uint32_t* canon;
     uint32_t* tinfo;
@@ -201,12 +193,19 @@ struct TableEncJob {
     uint32_t* ctl;
     TableEncArg a;
 };
-static constexpr uint32_t kMaxTableJobs = 16;
-struct TableEncJobs {
-    uint32_t n;
-    TableEncJob j[kMaxTableJobs];
-};
-hipError_t launch_table_enc_multi(const TableEncJob* jobs, uint32_t n, const void* chains, hipStream_t s);
+// Histogram words of a device-table job: the 768 of launch_masked_hist (all
+// live bytes, plane FL, plane 3), then the launch's gate (u64) and done counter.
+constexpr uint32_t kHistTableWords = 784;
+// Masked histogram and table set-up of up to kMaxHistJobs tensors in one grid
+// (launch_masked_hist_multi's shares): each job's first workgroup clears its
+// histogram words and opens the job's gate with this launch's epoch, every
+// workgroup adds its counts once the gate is open, and the job's last
+// workgroup builds the table.  hist[j]: kHistTableWords words per job.
+// epochs[j]: the epoch of job j's launch (written to its ctl[6..7] with the table).
+// chains: the state chains of symbol 0 for every count (launch_canon_chains,
+// kChainBytes, built once per device), from which the canonical streams are read.
+hipError_t launch_hist_table(const HistSrc* srcs, uint32_t* const* hists, const TableEncJob* jobs, uint32_t n,
+                             const void* chains, uint64_t* epochs, hipStream_t s);
 constexpr uint32_t kChainRows = 4097;  // symbol-0 counts 0 .. 4096
 constexpr uint32_t kChainSteps = 256;  // the most rows of a fast-encoder unit
 constexpr uint64_t kChainBytes = (4ull + 2ull) * (kChainSteps + 1) * kChainRows + (2ull * kChainSteps + 8) * kChainRows;

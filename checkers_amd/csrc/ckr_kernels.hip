@@ -15,6 +15,7 @@
 //                          output backward from its end, 4 bytes per store;
 //   packed output          unit after unit, lane streams in lane order.
 #include <hip/hip_runtime.h>
+#include <atomic>
 #include <cstdint>
 
 #include "ckr_internal.h"
@@ -46,11 +47,23 @@ __device__ __forceinline__ EncSym enc_entry(const TableArg& t, uint32_t s) { ret
 // ------------------------------------------------------------------ tables on the device
 // A table by ranks (ckr_table.h) in one workgroup of 256 threads, thread s for
 // symbol s: the counts and their exclusive sums in LDS, the ambiguity flag.
+//
+// norm_fix's positions are counted by buckets of the fractional part: the
+// symbols that take part in the correction (included ones, for the -1 case
+// only those holding more than one slot) are counted into 1024 buckets,
+// bucket floor(frac * 1024), whose order is that of the parts.  A symbol's
+// position then lies between the count on its side of its bucket and that
+// plus its bucket's count, which decides +1/-1 or 0 for every symbol except
+// those of the one bucket the boundary cuts; only these compare exact parts,
+// with the other members of their bucket.  Counts, ambiguity flag and sums
+// equal norm_fix's over all 256 symbols.
 struct RankTable {
     uint32_t norm[256], cum[257];
-    double up[256], down[256];
+    double key[256];
+    uint32_t bcnt[1024], bpre[1024];
+    uint32_t blist[256];
     unsigned long long red64[4];
-    uint32_t red[4], amb;
+    uint32_t red[4], ambw[4], amb, nlist, bstar;
 };
 
 __device__ __forceinline__ uint64_t block_sum64_256(uint64_t v, unsigned long long* sh) {
@@ -62,11 +75,26 @@ __device__ __forceinline__ uint64_t block_sum64_256(uint64_t v, unsigned long lo
     return sh[0] + sh[1] + sh[2] + sh[3];
 }
 
+// Inclusive sum over the wave's lanes.
+__device__ __forceinline__ uint32_t wave_incl_sum(uint32_t v) {
+    const uint32_t ln = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t g = (uint32_t)__shfl_up((int)v, o, 64);
+        if ((int)ln >= o) v += g;
+    }
+    return v;
+}
+
+// hist: read with device-scope loads (it may have been summed by other
+// workgroups of the same launch).
 __device__ void rank_table(const uint32_t* __restrict__ hist, bool ensure_full, RankTable& T) {
     const uint32_t s = threadIdx.x;
-    const uint32_t h = hist[s];
-    const uint64_t total = block_sum64_256(h, T.red64);
-    const uint64_t distinct = block_sum64_256(h ? 1u : 0u, T.red64);
+    const uint32_t h = __hip_atomic_load(const_cast<uint32_t*>(hist) + s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (s == 0) T.nlist = 0;
+    // the total (below 2^40) and the number of symbols present, in one sum
+    const uint64_t tv = block_sum64_256((uint64_t)h | ((uint64_t)(h ? 1u : 0u) << 48), T.red64);
+    const uint64_t total = tv & ((1ull << 48) - 1ull), distinct = tv >> 48;
     if ((ensure_full ? 256u : distinct) == 0) {  // no symbol at all: every slot for symbol 0
         T.norm[s] = s == 0 ? kTabM : 0u;
         T.cum[s] = s == 0 ? 0u : kTabM;
@@ -75,26 +103,72 @@ __device__ void rank_table(const uint32_t* __restrict__ hist, bool ensure_full, 
         return;
     }
     const NormStart r = norm_start(h, total, ensure_full);
-    T.up[s] = norm_key_up(r);
-    T.down[s] = norm_key_down(r);
-    const uint32_t assigned = (uint32_t)block_sum64_256(r.norm, T.red64);  // (syncs: the keys visible)
-    const int f = norm_fix(r.norm, r.frac, r.inc, T.up, T.down, assigned);
+    const uint32_t assigned = (uint32_t)block_sum64_256(r.norm, T.red64);
+    int f = 0;
+    if (assigned != kTabM) {  // (the same in every thread)
+        const bool up = assigned < kTabM;
+        const uint32_t rem = up ? kTabM - assigned : assigned - kTabM;
+        const bool part = r.inc && (up || r.norm > 1u);
+        const uint32_t b = part ? min((uint32_t)(r.frac * 1024.0), 1023u) : 0u;
+        T.key[s] = r.frac;
+        reinterpret_cast<uint4*>(T.bcnt)[s] = make_uint4(0u, 0u, 0u, 0u);
+        __syncthreads();
+        if (part) atomicAdd(&T.bcnt[b], 1u);
+        __syncthreads();
+        // exclusive sums over the buckets, thread s holding buckets 4s .. 4s+3
+        const uint4 c4 = reinterpret_cast<const uint4*>(T.bcnt)[s];
+        const uint32_t tsum = c4.x + c4.y + c4.z + c4.w;
+        const uint32_t inc = wave_incl_sum(tsum);
+        if ((s & 63) == 63) T.red[s >> 6] = inc;
+        __syncthreads();
+        uint32_t pre = 0, npart = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < 4; w++) {
+            const uint32_t v = T.red[w];
+            pre += w < (s >> 6) ? v : 0u;
+            npart += v;
+        }
+        const uint32_t e0 = pre + inc - tsum;
+        reinterpret_cast<uint4*>(T.bpre)[s] = make_uint4(e0, e0 + c4.x, e0 + c4.x + c4.y, e0 + c4.x + c4.y + c4.z);
+        __syncthreads();
+        // up: the first rem of the descending order get +1; down: the last rem get -1.
+        // lo: the symbols strictly before s on that side, counted by whole buckets
+        bool need = false;
+        uint32_t lo = 0;
+        if (part) {
+            const uint32_t below = T.bpre[b], inb = T.bcnt[b];
+            lo = up ? npart - below - inb : below;
+            if (lo + inb <= rem) f = up ? 1 : -1;
+            else if (lo < rem) { need = true; T.bstar = b; }  // (one bucket at most)
+        }
+        if (__syncthreads_or(need)) {
+            if (part && b == T.bstar) T.blist[atomicAdd(&T.nlist, 1u)] = s;
+            __syncthreads();
+            if (need) {
+                const uint32_t n = T.nlist;
+                uint32_t side = lo, eq = 0;
+                for (uint32_t i = 0; i < n; i++) {
+                    const double k = T.key[T.blist[i]];
+                    side += (up ? k > r.frac : k < r.frac) ? 1u : 0u;
+                    eq += k == r.frac ? 1u : 0u;
+                }
+                if (side + eq <= rem) f = up ? 1 : -1;
+                else if (side >= rem) f = 0;
+                else f = kNormAmbiguous;
+            }
+        }
+    }
     const uint32_t nm = r.norm + (f == 1 ? 1u : 0u) - (f == -1 ? 1u : 0u);
     T.norm[s] = nm;
-    const uint64_t amb = block_sum64_256(f == kNormAmbiguous ? 1u : 0u, T.red64);
-    // exclusive sum of the counts
-    uint32_t inc = nm;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t g = (uint32_t)__shfl_up((int)inc, o, 64);
-        if ((int)(s & 63) >= o) inc += g;
-    }
-    if ((s & 63) == 63) T.red[s >> 6] = inc;
+    // exclusive sum of the counts, the ambiguity flag beside it
+    const uint32_t inc = wave_incl_sum(nm);
+    const bool any_amb = __ballot(f == kNormAmbiguous) != 0;
+    if ((s & 63) == 63) { T.red[s >> 6] = inc; T.ambw[s >> 6] = any_amb ? 1u : 0u; }
     __syncthreads();
     uint32_t pre = 0;
     for (uint32_t w = 0; w < (s >> 6); w++) pre += T.red[w];
     T.cum[s + 1] = pre + inc;
-    if (s == 0) { T.cum[0] = 0; T.amb = amb ? 1u : 0u; }
+    if (s == 0) { T.cum[0] = 0; T.amb = (T.ambw[0] | T.ambw[1] | T.ambw[2] | T.ambw[3]) ? 1u : 0u; }
     __syncthreads();
 }
 
@@ -108,21 +182,12 @@ __global__ void __launch_bounds__(256) tables_kernel(const uint32_t* __restrict_
     if (threadIdx.x == 0) { row[256] = T.cum[256]; row[257] = T.amb; }
 }
 
-// The encode set-up of a tensor from its histograms on the device (no host
-// round trip): the table by ranks, the encode entries, the canonical
-// zero-plane streams, the fast encoder's LDS slot sizes, and its look-back
-// status and control words cleared (as build_enc_table_reset_kernel).  tinfo:
-// norm[256], sum, ambiguity flag, slot bytes of the two live planes.  The slot
-// sizes follow lane_slot_bytes on the host (expected coded size of K symbols
-// from the plane histograms plus six standard deviations), then the larger is
-// cut until both fit the launch's LDS (sum at most 2 smax).
-
 // The state chains of symbol 0 for every count f in [0, 4096] (f == 0: every
 // symbol the raw-byte escape), 256 steps each from state L, computed once per
 // device (canon_chain_kernel, thread f): before step k, the state
 // chain_x[k * kChainRows + f] and the bytes pushed so far chain_n[..]; the
 // pushed bytes chain_b[j * kChainRows + f].  The canonical zero-plane streams
-// of a table are then lookups (canon_entries_dev) instead of a serial chain.
+// of a table are then lookups instead of a serial chain.
 __global__ void __launch_bounds__(256) canon_chain_kernel(uint32_t* __restrict__ chain_x, uint16_t* __restrict__ chain_n,
                                                           uint8_t* __restrict__ chain_b) {
     const uint32_t f = blockIdx.x * 256 + threadIdx.x;
@@ -146,93 +211,95 @@ __global__ void __launch_bounds__(256) canon_chain_kernel(uint32_t* __restrict__
     }
 }
 
-// The canonical zero-plane streams (canon_host's layout) of lane counts Ks[3]
-// for symbol 0 of count f, from the chains: the pushed bytes into LDS, then
-// every dword of the three entries and streams in parallel.
-__device__ void canon_entries_dev(uint32_t f, const uint32_t (&Ks)[3], uint32_t cw, const uint32_t* __restrict__ chain_x,
-                                  const uint16_t* __restrict__ chain_n, const uint8_t* __restrict__ chain_b,
-                                  uint32_t* __restrict__ canon) {
-    __shared__ uint8_t pb[2 * kChainSteps + 8];
-    __shared__ uint32_t ex[3], eb[3];
-    __shared__ uint32_t slt[3][kCanonMaxCw];
-    const uint32_t s = threadIdx.x;
-    if (s < 3) { ex[s] = chain_x[Ks[s] * kChainRows + f]; eb[s] = chain_n[Ks[s] * kChainRows + f]; }
-    const uint32_t kmax = max(Ks[0], max(Ks[1], Ks[2]));
-    const uint32_t nmax = chain_n[kmax * kChainRows + f];
-    for (uint32_t j = s; j < nmax; j += blockDim.x) pb[j] = chain_b[j * kChainRows + f];
-    __syncthreads();
-    // slots: dword w of an entry holds pushed bytes 4w..4w+3, the first in the
-    // top byte; the last, partial one its r bytes the same way
-    for (uint32_t i = s; i < 3 * cw; i += blockDim.x) {
-        const uint32_t en = i / cw, d = i % cw, B = eb[en], w = B >> 2, r = B & 3u;
-        uint32_t v = 0;
-        if (d < w) v = ((uint32_t)pb[4 * d] << 24) | ((uint32_t)pb[4 * d + 1] << 16) | ((uint32_t)pb[4 * d + 2] << 8) | pb[4 * d + 3];
-        else if (d == w) for (uint32_t j = 0; j < r; j++) v = (v << 8) | pb[4 * w + j];
-        slt[en][d] = v;
-        canon[en * (4 + cw) + 4 + d] = v;
-    }
-    if (s < 3) {
-        uint32_t* base = canon + s * (4 + cw);
-        base[0] = Ks[s]; base[1] = ex[s]; base[2] = eb[s]; base[3] = 0;
-    }
-    __syncthreads();
-    // the streams in byte order
-    for (uint32_t i = s; i < 3 * cw; i += blockDim.x) {
-        const uint32_t en = i / cw, d = i % cw, B = eb[en], w = B >> 2, r = B & 3u;
-        uint32_t v = 0;
-        for (uint32_t b = 0; b < 4; b++) {
-            const uint32_t q = 4 * d + b;
-            if (q >= B) break;
-            const uint32_t slot = q < r ? w : w - 1 - ((q - r) >> 2);
-            const uint32_t byte = q < r ? q : (q - r) & 3;
-            v |= ((slt[en][slot] >> (8 * byte)) & 255u) << (8 * b);
-        }
-        canon[3 * (4 + cw) + en * cw + d] = v;
-    }
-}
-
 struct Chains {
     const uint32_t* x;
     const uint16_t* n;
     const uint8_t* b;
 };
+
+// LDS of table_enc_body (the histogram kernel's copies, reused once they are
+// summed).
+constexpr uint32_t kPushedMax = 2 * kChainSteps + 8;  // rows of chain_b
+struct TableLds {
+    RankTable T;
+    float fred[4][8];
+    uint32_t ex[3], eb[3];
+    uint8_t pb[kPushedMax];
+};
+
+// The encode set-up of a tensor from its histograms on the device (no host
+// round trip): the table by ranks, the encode entries, the canonical
+// zero-plane streams, the fast encoder's LDS slot sizes, and its control words
+// cleared.  tinfo: norm[256], sum, ambiguity flag, slot bytes of the two live
+// planes.  The slot sizes follow lane_slot_bytes on the host (expected coded
+// size of K symbols from the plane histograms plus six standard deviations),
+// then the larger is cut until both fit the launch's LDS (sum at most 2 smax).
+// ctl[6..7] gets the launch's epoch, the sign for the host that the table was
+// built in this launch; ctl[2] (failure flags) starts as flags.
+//
+// Canonical streams (canon_host's layout) of lane counts K0, K1, K2 for symbol
+// 0 of count f = norm[0]: entry e's header {K, final state, bytes B, 0}, then
+// its slot dwords (dword w holds pushed bytes 4w .. 4w+3, the first in the top
+// byte; the last, partial one its r = B mod 4 bytes the same way), and after
+// the three entries their streams in byte order, which are the pushed bytes
+// reversed (stream byte q = pushed byte B - 1 - q).
 __device__ void table_enc_body(const uint32_t* __restrict__ hist, const TableEncArg& a, EncSym* __restrict__ enc,
                                uint32_t* __restrict__ canon, uint32_t* __restrict__ tinfo, uint32_t* __restrict__ ctl,
-                               const Chains& ch) {
-    __shared__ RankTable T;
-    __shared__ double sm[2][4];
+                               const Chains& ch, uint64_t epoch, uint32_t flags, TableLds& W) {
+    RankTable& T = W.T;
     rank_table(hist, a.ensure_full != 0, T);
     const uint32_t s = threadIdx.x;
-    enc[s] = enc_entry_fc(T.norm[s], T.cum[s]);
-    tinfo[s] = T.norm[s];
-    if (s < 6) ctl[s] = 0;
-    // slot sizes: per plane p, n = sum h_p, m = sum h_p cost / n, v = sum h_p (cost - m)^2 / n
-    const double cost = T.norm[s] ? log2((double)M / (double)T.norm[s]) : 8.0;
-    double mean[2], var[2], cnt[2];
+    // the chain data of the canonical streams, loaded now and used at the end
+    const uint32_t f0 = T.norm[0];
+    const uint32_t kmax = min(max(a.k0, max(a.k1, a.k2)), kChainSteps);
+    const uint32_t npb = 2 * kmax + 8;  // at least the bytes pushed in kmax steps
+    uint8_t b0 = 0, b1 = 0, b2 = 0;
+    if (s < npb) b0 = ch.b[s * kChainRows + f0];
+    if (s + 256 < npb) b1 = ch.b[(s + 256) * kChainRows + f0];
+    if (s + 512 < npb) b2 = ch.b[(s + 512) * kChainRows + f0];
+    uint32_t exv = 0, ebv = 0;
+    if (s < 3) {
+        const uint32_t K = s == 0 ? a.k0 : (s == 1 ? a.k1 : a.k2);
+        exv = ch.x[K * kChainRows + f0];
+        ebv = ch.n[K * kChainRows + f0];
+    }
+    const uint32_t nm = T.norm[s];
+    enc[s] = enc_entry_fc(nm, T.cum[s]);
+    tinfo[s] = nm;
+    if (s < 6) ctl[s] = s == 2 ? flags : 0u;
+    // slot sizes: per plane p, n = sum h_p, m = sum h_p cost / n, v = sum h_p cost^2 / n - m^2
+    const float cost = nm ? 12.0f - log2f((float)nm) : 8.0f;  // log2(M / norm)
+    float v[6];
 #pragma unroll
     for (int p = 0; p < 2; p++) {
-        const double hp = (double)hist[256 + 256 * p + s];
-        double x0 = hp, x1 = hp * cost;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) { x0 += __shfl_xor(x0, o, 64); x1 += __shfl_xor(x1, o, 64); }
-        __syncthreads();
-        if ((s & 63) == 0) { sm[0][s >> 6] = x0; sm[1][s >> 6] = x1; }
-        __syncthreads();
-        cnt[p] = sm[0][0] + sm[0][1] + sm[0][2] + sm[0][3];
-        mean[p] = cnt[p] > 0 ? (sm[1][0] + sm[1][1] + sm[1][2] + sm[1][3]) / cnt[p] : 0.0;
-        double x2 = hp * (cost - mean[p]) * (cost - mean[p]);
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) x2 += __shfl_xor(x2, o, 64);
-        __syncthreads();
-        if ((s & 63) == 0) sm[0][s >> 6] = x2;
-        __syncthreads();
-        var[p] = cnt[p] > 0 ? (sm[0][0] + sm[0][1] + sm[0][2] + sm[0][3]) / cnt[p] : 0.0;
+        const float hp = (float)__hip_atomic_load(const_cast<uint32_t*>(hist) + 256 + 256 * p + s, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+        v[3 * p] = hp;
+        v[3 * p + 1] = hp * cost;
+        v[3 * p + 2] = hp * cost * cost;
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+#pragma unroll
+        for (int i = 0; i < 6; i++) v[i] += __shfl_xor(v[i], o, 64);
+    if ((s & 63) == 0)
+#pragma unroll
+        for (int i = 0; i < 6; i++) W.fred[s >> 6][i] = v[i];
+    // the pushed bytes into LDS
+    W.pb[s] = b0;
+    if (s + 256 < kPushedMax) W.pb[s + 256] = b1;
+    if (s + 512 < kPushedMax) W.pb[s + 512] = b2;
+    if (s < 3) { W.ex[s] = exv; W.eb[s] = ebv; }
+    __syncthreads();
     if (s == 0) {
         uint32_t sl[2];
         for (int p = 0; p < 2; p++) {
-            if (cnt[p] == 0) { sl[p] = 8; continue; }
-            const double bits = a.K * mean[p] + 6.0 * sqrt(a.K * var[p]) + 32.0;
+            const double cnt = (double)W.fred[0][3 * p] + W.fred[1][3 * p] + W.fred[2][3 * p] + W.fred[3][3 * p];
+            if (cnt <= 0.0) { sl[p] = 8; continue; }
+            const double s1 = (double)W.fred[0][3 * p + 1] + W.fred[1][3 * p + 1] + W.fred[2][3 * p + 1] + W.fred[3][3 * p + 1];
+            const double s2 = (double)W.fred[0][3 * p + 2] + W.fred[1][3 * p + 2] + W.fred[2][3 * p + 2] + W.fred[3][3 * p + 2];
+            const double mean = s1 / cnt, var = fmax(s2 / cnt - mean * mean, 0.0);
+            const double bits = a.K * mean + 6.0 * sqrt(a.K * var) + 32.0;
             uint64_t bytes = (uint64_t)ceil(bits / 8.0) + 8;
             bytes = (bytes + 3) & ~3ull;
             bytes = bytes < 8 ? 8 : bytes;
@@ -243,31 +310,34 @@ __device__ void table_enc_body(const uint32_t* __restrict__ hist, const TableEnc
         tinfo[257] = T.amb;
         tinfo[258] = sl[0];
         tinfo[259] = sl[1];
+        ctl[6] = (uint32_t)epoch;
+        ctl[7] = (uint32_t)(epoch >> 32);
     }
-    // canonical zero-plane streams of symbol 0 for the three lane counts
-    const uint32_t Ks[3] = {a.k0, a.k1, a.k2};
-    canon_entries_dev(T.norm[0], Ks, a.cw, ch.x, ch.n, ch.b, canon);
-}
-
-// One tensor: block 0 the table work, every block a share of the status words.
-__global__ void __launch_bounds__(256) table_enc_kernel(const uint32_t* __restrict__ hist, TableEncArg a,
-                                                        EncSym* __restrict__ enc, uint32_t* __restrict__ canon,
-                                                        uint32_t* __restrict__ tinfo, uint64_t* __restrict__ status,
-                                                        uint64_t n_status, uint32_t* __restrict__ ctl, Chains ch) {
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n_status; i += (uint64_t)gridDim.x * 256)
-        status[i] = 0;
-    if (blockIdx.x == 0) table_enc_body(hist, a, enc, canon, tinfo, ctl, ch);
-}
-
-// Up to kMaxTableJobs tensors in one launch: job blockIdx.y, its block 0 the
-// table work, every block of the row a share of the job's status words.
-__global__ void __launch_bounds__(256) table_enc_multi_kernel(TableEncJobs J, Chains ch) {
-    const uint32_t jb = blockIdx.y;
-    if (jb >= J.n) return;
-    const TableEncJob& t = J.j[jb];
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < t.n_status; i += (uint64_t)gridDim.x * 256)
-        t.status[i] = 0;
-    if (blockIdx.x == 0) table_enc_body(t.hist, t.a, t.enc, t.canon, t.tinfo, t.ctl, ch);
+    // the canonical streams: dword d of each entry, in slot and in stream form
+    const uint32_t cw = a.cw;
+    for (uint32_t en = 0; en < 3; en++) {
+        const uint32_t B = W.eb[en], w = B >> 2, r = B & 3u;
+        for (uint32_t d = s; d < cw; d += 256) {
+            uint32_t sv = 0;
+            if (d < w) sv = ((uint32_t)W.pb[4 * d] << 24) | ((uint32_t)W.pb[4 * d + 1] << 16) | ((uint32_t)W.pb[4 * d + 2] << 8) | W.pb[4 * d + 3];
+            else if (d == w) for (uint32_t i = 0; i < r; i++) sv = (sv << 8) | W.pb[4 * w + i];
+            uint32_t bv = 0;
+#pragma unroll
+            for (uint32_t k = 0; k < 4; k++) {
+                const uint32_t q = 4 * d + k;
+                if (q < B) bv |= (uint32_t)W.pb[B - 1 - q] << (8 * k);
+            }
+            canon[en * (4 + cw) + 4 + d] = sv;
+            canon[3 * (4 + cw) + en * cw + d] = bv;
+        }
+    }
+    if (s < 3) {
+        uint32_t* base = canon + s * (4 + cw);
+        base[0] = s == 0 ? a.k0 : (s == 1 ? a.k1 : a.k2);
+        base[1] = W.ex[s];
+        base[2] = W.eb[s];
+        base[3] = 0;
+    }
 }
 
 __global__ void __launch_bounds__(256) build_enc_table_kernel(TableArg t, EncSym* out) {
@@ -436,10 +506,17 @@ __global__ void __launch_bounds__(256) hist_init_kernel(uint32_t* __restrict__ h
 // i is at position i - head_n.
 // One workgroup's share (block b of nb) of one tensor's histogram, added into
 // hist (and planes) at the end; sh: the workgroup's LDS copies.
+//
+// gate (hist_table_kernel): the sums are added only once *gate holds epoch, the
+// sign that the job's first workgroup has cleared hist; a wait that outlasts
+// kGateSpins polls skips the adds and stores epoch in *gate_err instead.
+constexpr uint32_t kGateSpins = 1u << 22;
 template <int SPE, int PC>
 __device__ __forceinline__ void masked_hist_share(uint32_t* sh, const uint8_t* __restrict__ src, uint64_t n_bytes,
                                                   int es, uint32_t* __restrict__ hist, uint32_t* __restrict__ planes,
-                                                  uint32_t head_n, uint32_t b, uint32_t nb) {
+                                                  uint32_t head_n, uint32_t b, uint32_t nb,
+                                                  unsigned long long* gate = nullptr, unsigned long long epoch = 0,
+                                                  unsigned long long* gate_err = nullptr) {
     constexpr uint32_t NSH = SPE == 0 ? 256 * HIST_COPIES : 512 * PC;
     for (uint32_t i = threadIdx.x; i < NSH; i += blockDim.x) sh[i] = 0;
     __syncthreads();
@@ -479,6 +556,20 @@ __device__ __forceinline__ void masked_hist_share(uint32_t* sh, const uint8_t* _
             const uint32_t r = (SPE > 0 && (p & 3) == 3) ? 1u : 0u;  // live-plane rank
             atomicAdd(&sh[hist_slot<SPE, PC>((uint32_t)src[p], r, c)], 1u);
         }
+    }
+    if (gate) {
+        __shared__ uint32_t open;
+        if (threadIdx.x == 0) {
+            uint32_t n = 0;
+            // relaxed polls (an acquire would invalidate the L2 at every poll): the
+            // adds after the loop are device-scope atomics and need no acquire
+            while (__hip_atomic_load(gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch && ++n < kGateSpins)
+                __builtin_amdgcn_s_sleep(2);
+            open = n < kGateSpins;
+            if (!open) __hip_atomic_store(gate_err, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!open) return;
     }
     __syncthreads();
     const uint32_t bin = threadIdx.x;
@@ -530,6 +621,62 @@ __global__ void __launch_bounds__(256) masked_hist_multi_kernel(HistJobs jobs) {
     else masked_hist_share<0, 16>(sh, j.src, j.n_bytes, j.es, j.hist, nullptr, j.head_n, b, j.nblk);
 }
 
+// Histograms and encode set-ups of up to kMaxHistJobs masked tensors in one
+// grid (launch_hist_table).  Job k's workgroups (blk0 .. blk0 + nblk): the
+// first clears the job's histogram words and done counter, then opens the
+// job's gate with the launch's epoch (no earlier launch used that value, so
+// whatever the words held before cannot open it); each counts its share into
+// LDS, adds its sums once the gate is open, and takes a done ticket; the one
+// that takes the last ticket builds the table in the same LDS
+// (table_enc_body).  Every workgroup also clears a share of the job's
+// look-back status words.  Words of hist: 768 counts, gate (768-769), done
+// counter (770), gate time-out stamp (772-773).
+struct HistTableJob {
+    HistJob h;
+    TableEncJob t;
+};
+struct HistTableJobs {
+    uint32_t n;
+    unsigned long long epoch;
+    HistTableJob j[kMaxHistJobs];
+};
+__global__ void __launch_bounds__(256) hist_table_kernel(HistTableJobs J, Chains ch) {
+    __shared__ __align__(16) uint32_t sh[512 * 16];
+    static_assert(sizeof(TableLds) <= sizeof(sh), "the table set-up reuses the histogram's LDS");
+    __shared__ uint32_t last;
+    uint32_t k = 0;
+    while (k + 1 < J.n && J.j[k + 1].h.blk0 <= blockIdx.x) k++;
+    const HistJob& j = J.j[k].h;
+    const TableEncJob& t = J.j[k].t;
+    const uint32_t b = blockIdx.x - j.blk0;
+    auto* gate = reinterpret_cast<unsigned long long*>(j.hist + 768);
+    auto* gate_err = reinterpret_cast<unsigned long long*>(j.hist + 772);
+    uint32_t* done = j.hist + 770;
+    for (uint64_t i = (uint64_t)b * 256 + threadIdx.x; i < t.n_status; i += (uint64_t)j.nblk * 256) t.status[i] = 0;
+    if (b == 0) {  // device-scope stores, complete (s_waitcnt) before the gate opens
+        for (uint32_t i = threadIdx.x; i < 768; i += 256)
+            __hip_atomic_store(j.hist + i, i == 0 ? (uint32_t)j.zero_count : 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (threadIdx.x == 0) __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0) __hip_atomic_store(gate, J.epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (j.spe == 2)
+        masked_hist_share<2, 16>(sh, j.src, j.n_bytes, j.es, j.hist, j.hist + 256, j.head_n, b, j.nblk, gate, J.epoch, gate_err);
+    else
+        masked_hist_share<1, 16>(sh, j.src, j.n_bytes, j.es, j.hist, j.hist + 256, j.head_n, b, j.nblk, gate, J.epoch, gate_err);
+    // this workgroup's adds complete (every wave waits for its own) before its
+    // ticket; the table reads the counts with device-scope loads
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == j.nblk - 1;
+    __syncthreads();
+    if (!last) return;
+    const uint32_t flags = __hip_atomic_load(gate_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == J.epoch ? 4u : 0u;
+    table_enc_body(j.hist, t.a, t.enc, t.canon, t.tinfo, t.ctl, ch, J.epoch, flags, *reinterpret_cast<TableLds*>(sh));
+}
+
 // Every workgroup ends with up to 768 global atomics (the sums of its LDS
 // copies), so the grid is kept small: 256 workgroups (one per CU) below 256
 // MiB, 512 above.  Measured on MI355X for a 4 GB fp32 tensor: 0.69 ms with 512
@@ -577,33 +724,39 @@ hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int 
     return hipGetLastError();
 }
 
+// Workgroup shares of a set of histogram jobs: about 512 in all, in proportion
+// to their bytes, at least one each and never more than a lone launch would
+// take (every workgroup ends with up to 768 global atomics).
+static uint32_t hist_shares(const HistSrc* srcs, uint32_t n, HistJob* out, uint32_t* const* hists) {
+    uint64_t total = 0;
+    for (uint32_t k = 0; k < n; k++) total += srcs[k].n_bytes;
+    uint32_t nb = 0;
+    for (uint32_t k = 0; k < n; k++) {
+        const HistSrc& x = srcs[k];
+        HistJob& j = out[k];
+        const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(x.src) & 15u);
+        j.head_n = (uint32_t)std::min<uint64_t>(mis ? 16u - mis : 0u, x.n_bytes);
+        j.src = x.src + j.head_n;
+        j.n_bytes = x.n_bytes - j.head_n;
+        j.es = x.es;
+        j.spe = x.spe;
+        j.zero_count = (x.es > 0) ? (x.n_bytes / (uint64_t)x.es) * (uint64_t)x.spe : 0;
+        j.hist = hists[k];
+        const uint64_t share = total ? (512ull * x.n_bytes + total - 1) / total : 1;
+        j.nblk = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(share, hist_num_blocks(j.n_bytes)));
+        j.blk0 = nb;
+        nb += j.nblk;
+    }
+    return nb;
+}
 hipError_t launch_masked_hist_multi(const HistSrc* srcs, uint32_t n, uint32_t* d_hists, hipStream_t s) {
-    // one grid of about 512 workgroups over all jobs, in proportion to their
-    // bytes (each workgroup ends with up to 768 global atomics), at least one
-    // each and never more than a lone launch would take
     for (uint32_t j0 = 0; j0 < n; j0 += kMaxHistJobs) {
         const uint32_t m = std::min<uint32_t>(kMaxHistJobs, n - j0);
         HistJobs jobs{};
         jobs.n = m;
-        uint64_t total = 0;
-        for (uint32_t k = 0; k < m; k++) total += srcs[j0 + k].n_bytes;
-        uint32_t nb = 0;
-        for (uint32_t k = 0; k < m; k++) {
-            const HistSrc& x = srcs[j0 + k];
-            HistJob& j = jobs.j[k];
-            const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(x.src) & 15u);
-            j.head_n = (uint32_t)std::min<uint64_t>(mis ? 16u - mis : 0u, x.n_bytes);
-            j.src = x.src + j.head_n;
-            j.n_bytes = x.n_bytes - j.head_n;
-            j.es = x.es;
-            j.spe = x.spe;
-            j.zero_count = (x.es > 0) ? (x.n_bytes / (uint64_t)x.es) * (uint64_t)x.spe : 0;
-            j.hist = d_hists + 768ull * (j0 + k);
-            const uint64_t share = total ? (512ull * x.n_bytes + total - 1) / total : 1;
-            j.nblk = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>(share, hist_num_blocks(j.n_bytes)));
-            j.blk0 = nb;
-            nb += j.nblk;
-        }
+        uint32_t* hp[kMaxHistJobs];
+        for (uint32_t k = 0; k < m; k++) hp[k] = d_hists + 768ull * (j0 + k);
+        const uint32_t nb = hist_shares(srcs + j0, m, jobs.j, hp);
         CKR_LAUNCH("hist_init_multi_kernel", s, hist_init_multi_kernel<<<m, 256, 0, s>>>(jobs));
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -3900,29 +4053,30 @@ static Chains chains_of(const void* chains) {
                   reinterpret_cast<const uint16_t*>(p + 4ull * (kChainSteps + 1) * kChainRows),
                   p + 6ull * (kChainSteps + 1) * kChainRows};
 }
-hipError_t launch_table_enc(const uint32_t* hist, const EncodeGeom& g, int ensure_full, uint32_t K, uint32_t k0,
-                            uint32_t k1, uint32_t k2, uint32_t cw, uint32_t smax, EncSym* d_enc, uint32_t* canon,
-                            uint32_t* tinfo, uint64_t* status, uint32_t* ctl, const void* chains, hipStream_t s) {
-    const uint64_t nst = encode_fast_status_words(g.n_units);
-    const uint32_t grid = (uint32_t)std::max<uint64_t>(1, std::min<uint64_t>((nst + 255) / 256, 4096));
-    const TableEncArg a{K, k0, k1, k2, cw, smax, ensure_full};
-    CKR_LAUNCH("table_enc_kernel", s,
-               table_enc_kernel<<<grid, 256, 0, s>>>(hist, a, d_enc, canon, tinfo, status, nst, ctl, chains_of(chains)));
-    return hipGetLastError();
-}
-hipError_t launch_table_enc_multi(const TableEncJob* jobs, uint32_t n, const void* chains, hipStream_t s) {
-    for (uint32_t j0 = 0; j0 < n; j0 += kMaxTableJobs) {
-        TableEncJobs J{};
-        J.n = std::min<uint32_t>(kMaxTableJobs, n - j0);
-        uint64_t most = 1;
-        for (uint32_t j = 0; j < J.n; j++) {
-            J.j[j] = jobs[j0 + j];
-            most = std::max<uint64_t>(most, (J.j[j].n_status + 255) / 256);
+hipError_t launch_hist_table(const HistSrc* srcs, uint32_t* const* hists, const TableEncJob* jobs, uint32_t n,
+                             const void* chains, uint64_t* epochs, hipStream_t s) {
+    // a value no earlier launch of this process used, and unlikely to be
+    // left in memory by another process
+    static std::atomic<uint64_t> next{0x5a17c0de00000000ull ^ ((uint64_t)reinterpret_cast<uintptr_t>(&next) << 8)};
+    for (uint32_t j0 = 0; j0 < n; j0 += kMaxHistJobs) {
+        const uint32_t m = std::min<uint32_t>(kMaxHistJobs, n - j0);
+        HistTableJobs J{};
+        J.n = m;
+        J.epoch = next.fetch_add(1, std::memory_order_relaxed) + 1;
+        HistJob hj[kMaxHistJobs];
+        for (uint32_t k = 0; k < m; k++)
+            if (srcs[j0 + k].spe != 1 && srcs[j0 + k].spe != 2) return hipErrorInvalidValue;
+        const uint32_t nb = hist_shares(srcs + j0, m, hj, hists + j0);
+        for (uint32_t k = 0; k < m; k++) {
+            J.j[k].h = hj[k];
+            J.j[k].t = jobs[j0 + k];
         }
-        const dim3 grid((uint32_t)std::min<uint64_t>(most, 4096), J.n);
-        CKR_LAUNCH("table_enc_kernel", s, table_enc_multi_kernel<<<grid, 256, 0, s>>>(J, chains_of(chains)));
+        for (uint32_t k = 0; k < m; k++) epochs[j0 + k] = J.epoch;
+        CKR_LAUNCH("hist_table_kernel", s, hist_table_kernel<<<nb, 256, 0, s>>>(J, chains_of(chains)));
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
     }
-    return hipGetLastError();
+    return hipSuccess;
 }
 // The largest slot (bytes, a multiple of 4, at most 2K + 8) whose two-pair
 // layout fits lds_cap.

@@ -126,3 +126,17 @@ def test_repair_host_helpers():
     with pytest.raises(ck.CkrError):
         ck.repair_masked_bits(ck.I32)
     assert ck.lib().ckr_repair_workspace_bytes(1 << 31, ck.F32, -1, 50) == 0
+
+
+def test_encoder_job_record_follows_its_buffers():
+    """compress_many copies each encoder's job record from a template: replacing
+    one of the encoder's buffers (as a caller may, to point two jobs at
+    overlapping ranges) must show in the record it passes."""
+    import torch
+    e = ck.Encoder(100_000, ck.F32, 65536, device="cpu")
+    assert e._job.d_headers == e.headers.data_ptr()
+    e.headers = torch.empty(e.headers.numel() + 16, dtype=torch.int32)
+    e.out = torch.empty(e.out_cap, dtype=torch.uint8)
+    assert e._job.d_headers == e.headers.data_ptr()
+    assert e._job.d_out == e.out.data_ptr()
+    assert e._job.d_workspace == e.ws.data_ptr() and e._job.workspace_bytes == e.ws_bytes
