@@ -1030,9 +1030,12 @@ void add_span(std::vector<Span>& v, const void* p, uint64_t bytes, uint64_t job,
 // The caller buffers of an encode, checked before anything is queued: the
 // source element-aligned and inside its allocation, the outputs and the
 // workspace inside theirs at the sizes the header documents.
-int check_encode_args(const void* src, const ckr::EncodeGeom& g, uint64_t n_elems, const void* out,
-                      uint64_t out_capacity, const void* hdrs, const void* offs, const void* side, const void* ws,
-                      uint64_t ws_bytes) {
+// An encode's arguments are checked in two parts: what its histogram and
+// table set-up touch (sizes and alignment, the source and the workspace), and
+// the output buffers, which the device-table paths check while that set-up
+// runs (it writes nothing but the workspace).
+int check_encode_inputs(const void* src, const ckr::EncodeGeom& g, uint64_t out_capacity, const void* ws,
+                        uint64_t ws_bytes) {
     if (!aligned_to(src, (uint64_t)g.es))
         return fail(CKR_E_INVALID, "[ckr] source %p is not aligned to its element size (%d bytes)", src, g.es);
     if (g.n_units && out_capacity < g.n_bytes)
@@ -1041,15 +1044,27 @@ int check_encode_args(const void* src, const ckr::EncodeGeom& g, uint64_t n_elem
     if (g.n_units && ws_bytes < encode_layout(g).total)
         return fail(CKR_E_CAPACITY, "[ckr] workspace %llu < %llu", (unsigned long long)ws_bytes,
                     (unsigned long long)encode_layout(g).total);
+    if (g.n_units == 0) return CKR_OK;
+    int rc;
+    if ((rc = check_buffer(src, g.n_bytes, "source")) || (rc = check_buffer(ws, ws_bytes, "workspace"))) return rc;
+    return CKR_OK;
+}
+int check_encode_outputs(const ckr::EncodeGeom& g, uint64_t n_elems, const void* out, uint64_t out_capacity,
+                         const void* hdrs, const void* offs, const void* side) {
     int rc;
     if ((rc = check_buffer(offs, (g.n_units + 1) * 8, "unit offsets"))) return rc;
     if (g.n_units == 0) return CKR_OK;
-    if ((rc = check_buffer(src, g.n_bytes, "source")) || (rc = check_buffer(out, out_capacity, "output")) ||
-        (rc = check_buffer(hdrs, g.n_units * 256 * sizeof(ckr_stream_header), "headers")) ||
-        (rc = check_buffer(ws, ws_bytes, "workspace")))
+    if ((rc = check_buffer(out, out_capacity, "output")) ||
+        (rc = check_buffer(hdrs, g.n_units * 256 * sizeof(ckr_stream_header), "headers")))
         return rc;
     if (side && g.spe && (rc = check_buffer(side, n_elems * (uint64_t)g.spe, "sidecar"))) return rc;
     return CKR_OK;
+}
+int check_encode_args(const void* src, const ckr::EncodeGeom& g, uint64_t n_elems, const void* out,
+                      uint64_t out_capacity, const void* hdrs, const void* offs, const void* side, const void* ws,
+                      uint64_t ws_bytes) {
+    int rc = check_encode_inputs(src, g, out_capacity, ws, ws_bytes);
+    return rc ? rc : check_encode_outputs(g, n_elems, out, out_capacity, hdrs, offs, side);
 }
 
 // After the stream has passed a deferred encode: its checks, its total, and the
@@ -1302,9 +1317,11 @@ int dev_enc_finish(const DevEnc& d, ckr_freq_table* h_table, uint64_t* h_total, 
 }
 
 // ckr_compress through the device table: histogram, queue, one synchronisation.
+// check_outputs: the output buffers' checks, made while the histogram runs.
 int compress_device_table(const void* src, const ckr::EncodeGeom& g, int ensure_full_alphabet, uint8_t* d_out,
                           ckr_stream_header* d_headers, uint64_t* d_unit_offsets, uint8_t* d_sidecar, uint8_t* ws,
-                          ckr_freq_table* h_table, uint64_t* h_total_out, hipStream_t s) {
+                          ckr_freq_table* h_table, uint64_t* h_total_out, hipStream_t s,
+                          const std::function<int()>& check_outputs) {
     uint32_t* pw = pinned_words();
     if (!pw) return fail(CKR_E_HIP, "[ckr] pinned host buffer unavailable");
     DevEnc d;
@@ -1315,7 +1332,12 @@ int compress_device_table(const void* src, const ckr::EncodeGeom& g, int ensure_
     const ckr::HistSrc hs{d.src, g.n_bytes, g.es, (int)g.spe};
     const ckr::TableEncJob t = dev_enc_table_job(d, ensure_full_alphabet);
     CKR_HIP(ckr::launch_hist_table(&hs, &hist, &t, 1, chains, &d.epoch, s));
-    int rc = dev_enc_queue_encode(d, s);
+    int rc = check_outputs();
+    if (rc) {
+        (void)hipStreamSynchronize(s);  // the set-up writes the caller's workspace
+        return rc;
+    }
+    rc = dev_enc_queue_encode(d, s);
     if (rc) return rc;
     // the redo pass right behind the encode, with no read-back between them:
     // it ends at once when no unit outgrew its slots
@@ -1346,14 +1368,16 @@ int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_b
     ckr::EncodeGeom g;
     if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
     const EncodeLayout L = encode_layout(g);
-    if (!d_workspace || workspace_bytes < L.total)
-        return fail(CKR_E_CAPACITY, "[ckr] workspace too small (%llu < %llu)", (unsigned long long)workspace_bytes,
-                    (unsigned long long)L.total);
+    if (!d_workspace || workspace_bytes < L.total || !aligned16(d_workspace))
+        return fail(CKR_E_CAPACITY, "[ckr] workspace too small or misaligned (%llu bytes, need %llu)",
+                    (unsigned long long)workspace_bytes, (unsigned long long)L.total);
     if (n_elems && !d_src) return fail(CKR_E_INVALID, "[ckr] null source");
     if (!d_unit_offsets) return fail(CKR_E_INVALID, "[ckr] null offsets");
-    int rc = check_encode_args(d_src, g, n_elems, d_out, out_capacity, d_headers, d_unit_offsets, d_sidecar, d_workspace,
-                               workspace_bytes);
+    int rc = check_encode_inputs(d_src, g, out_capacity, d_workspace, workspace_bytes);
     if (rc) return rc;
+    const auto check_outputs = [&]() {
+        return check_encode_outputs(g, n_elems, d_out, out_capacity, d_headers, d_unit_offsets, d_sidecar);
+    };
     hipStream_t s = (hipStream_t)stream;
     Staged st;
     if ((rc = st.make(d_src, g.n_bytes, s))) return rc;
@@ -1361,11 +1385,15 @@ int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_b
     // before the encode (mode 1; modes 2 and 3 size the slots on the host)
     if (g_fast_paths == 1 && use_fast_encode(g)) {
         rc = compress_device_table(st.p, g, ensure_full_alphabet, d_out, d_headers, d_unit_offsets, d_sidecar,
-                                   static_cast<uint8_t*>(d_workspace), h_table, h_total_out, s);
+                                   static_cast<uint8_t*>(d_workspace), h_table, h_total_out, s, check_outputs);
         if (rc != kUseHostTable) {
             st.release(s);
             return rc;
         }
+    }
+    if ((rc = check_outputs())) {
+        st.release(s);
+        return rc;
     }
     uint32_t* d_hist = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(d_workspace) + L.off_hist);
     const int es = ckr_element_size(dtype);
@@ -1445,7 +1473,15 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
                       void* stream) {
     if (n == 0) return CKR_OK;
     if (!jobs) return fail(CKR_E_INVALID, "[ckr] null job list");
-    // every job checked before anything is launched
+    if (n == 1) {  // one job: ckr_compress (which checks it) on the caller's stream, no second stream or events
+        ckr_compress_job& jb = jobs[0];
+        const int rc = ckr_compress(jb.d_src, jb.n_elems, jb.dtype, unit_bytes, ensure_full_alphabet, jb.d_out,
+                                    jb.out_capacity, jb.d_headers, jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace,
+                                    jb.workspace_bytes, jb.h_table, &jb.total, stream);
+        return rc ? set_job_error(rc, 0) : CKR_OK;
+    }
+    // every job's sizes, source and workspace checked before anything is
+    // launched; its output buffers before anything writes them
     std::vector<ckr::EncodeGeom> geo(n);
     for (uint64_t i = 0; i < n; i++) {
         const ckr_compress_job& jb = jobs[i];
@@ -1456,10 +1492,18 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             return fail(CKR_E_CAPACITY, "[ckr] job %llu: workspace too small or misaligned", (unsigned long long)i);
         if ((jb.n_elems && !jb.d_src) || !jb.d_unit_offsets)
             return fail(CKR_E_INVALID, "[ckr] job %llu: null source or offsets", (unsigned long long)i);
-        const int rc = check_encode_args(jb.d_src, geo[i], jb.n_elems, jb.d_out, jb.out_capacity, jb.d_headers,
-                                         jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace, jb.workspace_bytes);
+        const int rc = check_encode_inputs(jb.d_src, geo[i], jb.out_capacity, jb.d_workspace, jb.workspace_bytes);
         if (rc) return set_job_error(rc, i);
     }
+    const auto check_outputs = [&]() -> int {
+        for (uint64_t i = 0; i < n; i++) {
+            const ckr_compress_job& jb = jobs[i];
+            const int rc = check_encode_outputs(geo[i], jb.n_elems, jb.d_out, jb.out_capacity, jb.d_headers,
+                                                jb.d_unit_offsets, jb.d_sidecar);
+            if (rc) return set_job_error(rc, i);
+        }
+        return CKR_OK;
+    };
     {  // jobs share no output or workspace bytes
         std::vector<Span> v;
         for (uint64_t i = 0; i < n; i++) {
@@ -1473,13 +1517,6 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             if (g.spe) add_span(v, jb.d_sidecar, jb.n_elems * (uint64_t)g.spe, i, "sidecar");
         }
         if (int rc = check_disjoint(v)) return rc;
-    }
-    if (n == 1) {  // one job: ckr_compress on the caller's stream, no second stream or events
-        ckr_compress_job& jb = jobs[0];
-        const int rc = ckr_compress(jb.d_src, jb.n_elems, jb.dtype, unit_bytes, ensure_full_alphabet, jb.d_out,
-                                    jb.out_capacity, jb.d_headers, jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace,
-                                    jb.workspace_bytes, jb.h_table, &jb.total, stream);
-        return rc ? set_job_error(rc, 0) : CKR_OK;
     }
     hipStream_t s = (hipStream_t)stream;
     ManyAux* a = nullptr;
@@ -1619,6 +1656,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             }
             CKR_HIP(ckr::launch_hist_table(hs.data(), hp.data(), tj.data(), (uint32_t)n, chains, ep.data(), a->s2));
             for (uint64_t i = 0; i < n; i++) dv[i].epoch = ep[i];
+            if (int rc = check_outputs()) return rc;  // (the streams are drained on the way out)
             // the encodes of all jobs of one kind (spe, sidecar) in one launch
             // behind the tables, at most kMaxFastJobs a launch
             {
@@ -1660,6 +1698,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             drain.ok = true;
             return CKR_OK;
         }
+        if (int rc = check_outputs()) return rc;
         // every histogram in one grid (per 16 jobs) and one read-back: a launch
         // and a copy per job cost more host time than their kernels take
         CKR_HIP(ckr::launch_masked_hist_multi(hs.data(), (uint32_t)n, a->d_hists, a->s2));
@@ -1686,6 +1725,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         drain.ok = true;  // complete() waits for every stream it queued on
         return complete(n);
     }
+    if (int rc = check_outputs()) return rc;
     // Larger tensors: job i's encode goes on es[i % 2] (the caller's stream and
     // one of the library's), so that job i+1's encode takes the CUs that job
     // i's workgroups leave as its last units finish, instead of waiting for the
