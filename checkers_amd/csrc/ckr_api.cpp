@@ -69,14 +69,9 @@ inline bool aligned_to(const void* p, uint64_t a) { return a == 0 || reinterpret
 int check_buffer(const void* p, uint64_t bytes, const char* what) {
     if (bytes == 0) return CKR_OK;
     if (!p) return fail(CKR_E_INVALID, "[ckr] null %s pointer", what);
-    hipPointerAttribute_t a;
-    std::memset(&a, 0, sizeof(a));
-    const hipError_t e = hipPointerGetAttributes(&a, p);
-    if (e != hipSuccess || a.type == hipMemoryTypeUnregistered) {
-        (void)hipGetLastError();
-        return fail(CKR_E_INVALID, "[ckr] %s pointer %p is not device-accessible memory (%s)", what, p,
-                    e != hipSuccess ? hipGetErrorString(e) : "unregistered host memory");
-    }
+    // device memory: its allocation's range (one query); anything else (pinned
+    // host memory, which the range query does not cover, or no allocation at
+    // all): the pointer's type
     hipDeviceptr_t base = nullptr;
     size_t size = 0;
     if (hipMemGetAddressRange(&base, &size, const_cast<void*>(p)) == hipSuccess && base) {
@@ -84,8 +79,16 @@ int check_buffer(const void* p, uint64_t bytes, const char* what) {
         if (q < b || q - b > size || bytes > size - (q - b))
             return fail(CKR_E_INVALID, "[ckr] %s [%p, +%llu bytes) runs past its allocation (%llu bytes at %p)", what, p,
                         (unsigned long long)bytes, (unsigned long long)size, base);
-    } else {
-        (void)hipGetLastError();  // memory the range query does not cover (pinned host): type check only
+        return CKR_OK;
+    }
+    (void)hipGetLastError();
+    hipPointerAttribute_t a;
+    std::memset(&a, 0, sizeof(a));
+    const hipError_t e = hipPointerGetAttributes(&a, p);
+    if (e != hipSuccess || a.type == hipMemoryTypeUnregistered) {
+        (void)hipGetLastError();
+        return fail(CKR_E_INVALID, "[ckr] %s pointer %p is not device-accessible memory (%s)", what, p,
+                    e != hipSuccess ? hipGetErrorString(e) : "unregistered host memory");
     }
     return CKR_OK;
 }
