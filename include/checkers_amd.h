@@ -189,8 +189,15 @@ CKR_API int ckr_encode_planes(const void* d_src, uint64_t n_elems, int dtype,
                               uint64_t* h_total_out, void* stream);
 
 /* ---- full tensor compression as ANSCompressor::compress_tensor does it for a
- * singleton (histogram → host table → encode), in one call.  The table built
- * is returned in h_table (may be NULL). ---- */
+ * singleton (histogram → table → encode), in one call.  The table built is
+ * returned in h_table (may be NULL).  The workspace (16-byte aligned) as for
+ * ckr_encode.  For tensors of masked dtypes with units of at most 64 KiB the
+ * table is built on the device from the histogram in the same launch (the
+ * reference's normalisation, by ranks; a table whose correction falls inside
+ * a group of equal fractional parts is taken from the host's sort instead),
+ * and the output buffers are checked while that launch runs: a bad output
+ * buffer is reported once it has finished, with only the workspace written.
+ * ---- */
 CKR_API int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_t unit_bytes,
                          int ensure_full_alphabet,
                          uint8_t* d_out, uint64_t out_capacity,
@@ -203,14 +210,19 @@ CKR_API int ckr_compress(const void* d_src, uint64_t n_elems, int dtype, uint64_
  * (src/ANSCompressor.cpp:1118-1300, the GPU phases of each item): the same
  * results as ckr_compress called on each job in order, with job i+1's
  * histogram computed on a second, library-owned stream while job i is encoded,
- * the encodes alternating between `stream` and a third library-owned stream
- * (when no job exceeds 256 MiB, every histogram is computed first instead, with
- * one host synchronisation for all of them, and the encodes go round robin over
- * four streams), and the encodes queued back to back (each job's completion
- * words are read once, after the last).  Every job has its own buffers and
- * workspace (sizes as for ckr_compress).  The inputs must be ready in `stream`
- * order; the call returns when every job is done, with table and total filled
- * in.  On error, jobs before the failing one are complete. ---- */
+ * the encodes alternating between `stream` and a third library-owned stream,
+ * and the encodes queued back to back (each job's completion words are read
+ * once, after the last).  When no job exceeds 256 MiB, every job's histogram
+ * and table are built in one launch on the device instead and every encode of
+ * one kind (dtype class, sidecar) in one more, with no host round trip between
+ * them (tensors the device tables do not serve: every histogram first, one
+ * host synchronisation, then the encodes round robin over four streams).
+ * Every job has its own buffers and workspace (sizes as for ckr_compress).
+ * Every job's sizes, source and workspace are checked before anything is
+ * launched, its output buffers before anything writes them.  The inputs must
+ * be ready in `stream` order; the call returns when every job is done, with
+ * table and total filled in.  On error, jobs before the failing one are
+ * complete. ---- */
 typedef struct {
     const void* d_src;
     uint64_t n_elems;
