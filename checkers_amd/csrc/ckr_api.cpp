@@ -1430,6 +1430,7 @@ struct ManyAux {
     hipStream_t sx[2] = {nullptr, nullptr};  // with s2, the encodes of a shard of small tensors
     hipEvent_t ev = nullptr;
     hipEvent_t ev_prev = nullptr;  // the stream's work before the encode being queued
+    hipEvent_t ev_tail = nullptr;  // a histogram's wider tail done (ckr_compress_many)
     uint32_t* pinned = nullptr;  // 2 x 768 words
     uint32_t* slots = nullptr;   // 8 words per job: the deferred read-backs
     uint64_t slot_jobs = 0;
@@ -1459,6 +1460,7 @@ hipError_t many_aux(ManyAux** out) {
             if ((e = hipEventCreateWithFlags(&x, hipEventDisableTiming)) != hipSuccess) return e;
         if ((e = hipEventCreateWithFlags(&a.ev, hipEventDisableTiming)) != hipSuccess) return e;
         if ((e = hipEventCreateWithFlags(&a.ev_prev, hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&a.ev_tail, hipEventDisableTiming)) != hipSuccess) return e;
         if ((e = hipHostMalloc(reinterpret_cast<void**>(&a.pinned), 2 * 768 * sizeof(uint32_t), hipHostMallocDefault)) !=
             hipSuccess)
             return e;
@@ -1583,14 +1585,21 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
     };
     CKR_HIP(hipEventRecord(a->ev, s));  // inputs ready in the caller's stream order
     CKR_HIP(hipStreamWaitEvent(a->s2, a->ev, 0));
-    auto hist = [&](uint64_t i, uint32_t* h_dst, bool lean) -> hipError_t {
+    // job i's histogram words in its workspace (kHistTableWords; word 776 the
+    // lean pass's chunk counter)
+    auto hist_words = [&](uint64_t i) {
+        return reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(jobs[i].d_workspace) + encode_layout(geo[i]).off_hist);
+    };
+    // tail: the lean pass in chunks that a tail (launch_masked_hist_join) can
+    // join, the read-back left to the caller, behind that tail
+    auto hist = [&](uint64_t i, uint32_t* h_dst, bool lean, bool tail) -> hipError_t {
         const ckr_compress_job& jb = jobs[i];
-        const EncodeLayout L = encode_layout(geo[i]);
-        uint32_t* d_hist = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(jb.d_workspace) + L.off_hist);
+        uint32_t* d_hist = hist_words(i);
         const int es = ckr_element_size(jb.dtype);
         hipError_t e = ckr::launch_masked_hist(static_cast<const uint8_t*>(staged[i].p), jb.n_elems * (uint64_t)es, es,
-                                               geo[i].spe, d_hist, d_hist + 256, a->s2, lean);
-        if (e != hipSuccess) return e;
+                                               geo[i].spe, d_hist, d_hist + 256, a->s2, lean,
+                                               tail ? d_hist + 776 : nullptr);
+        if (e != hipSuccess || tail) return e;
         return hipMemcpyAsync(h_dst, d_hist, 768 * sizeof(uint32_t), hipMemcpyDeviceToHost, a->s2);
     };
     // A shard of small tensors: every histogram first (full width, back to
@@ -1744,7 +1753,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         enc_streams = {s, a->sx[0]};
     }
     CKR_HIP(hipEventRecord(a->ev_prev, s));  // before job 0's encode: the inputs
-    CKR_HIP(hist(0, a->pinned, false));
+    CKR_HIP(hist(0, a->pinned, false, false));
     CKR_HIP(hipStreamSynchronize(a->s2));
     for (uint64_t i = 0; i < n; i++) {
         ckr_compress_job& jb = jobs[i];
@@ -1758,12 +1767,20 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         // that it starts with job i's encode and the encoder's workgroups take
         // their CUs first
         bool queued = i + 1 >= n;
+        // A histogram of more than 1.5 times the bytes of the encode it runs
+        // beside outlasts it (the lean pass counts about as many bytes as
+        // the encode reads, or a little more): once that encode is done it
+        // gets three more workgroups per CU, on a third stream (nothing else
+        // could use the device then, the next encode waiting for its table).
+        // Queued at once, they would take CUs before the encode's workgroups
+        // reach them.
+        const bool tail = i + 1 < n && geo[i + 1].spe && 2 * geo[i + 1].n_bytes > 3 * geo[i].n_bytes;
         const AfterLaunch next = [&]() -> hipError_t {
             if (queued) return hipSuccess;
             queued = true;
             const hipError_t e2 = hipStreamWaitEvent(a->s2, a->ev_prev, 0);
             if (e2 != hipSuccess) return e2;
-            return hist(i + 1, a->pinned + 768 * ((i + 1) & 1), true);
+            return hist(i + 1, a->pinned + 768 * ((i + 1) & 1), true, tail);
         };
         // the encode is only queued: its read-backs are checked at the end, so
         // the next encode follows it on the stream without a host round trip
@@ -1777,6 +1794,19 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         }
         CKR_HIP(next());  // an empty job launches nothing
         CKR_HIP(hipEventRecord(a->ev_prev, es[i & 1]));  // job i queued: job i+2's histogram waits for it
+        if (tail) {
+            const ckr_compress_job& jn = jobs[i + 1];
+            uint32_t* d_hist = hist_words(i + 1);
+            const int esz = ckr_element_size(jn.dtype);
+            CKR_HIP(hipStreamWaitEvent(a->sx[1], a->ev_prev, 0));
+            CKR_HIP(ckr::launch_masked_hist_join(static_cast<const uint8_t*>(staged[i + 1].p),
+                                                 jn.n_elems * (uint64_t)esz, esz, geo[i + 1].spe, d_hist, d_hist + 256,
+                                                 d_hist + 776, 3, a->sx[1]));
+            CKR_HIP(hipEventRecord(a->ev_tail, a->sx[1]));
+            CKR_HIP(hipStreamWaitEvent(a->s2, a->ev_tail, 0));
+            CKR_HIP(hipMemcpyAsync(a->pinned + 768 * ((i + 1) & 1), d_hist, 768 * sizeof(uint32_t),
+                                   hipMemcpyDeviceToHost, a->s2));
+        }
         if (i + 1 < n) CKR_HIP(hipStreamSynchronize(a->s2));
     }
     drain.ok = true;  // complete() waits for every stream it queued on

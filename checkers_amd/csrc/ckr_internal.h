@@ -99,8 +99,16 @@ struct HistJobs {
     HistJob j[kMaxHistJobs];
 };
 hipError_t launch_masked_hist_multi(const HistSrc* srcs, uint32_t n, uint32_t* d_hists, hipStream_t s);
+// lean: the form that runs beside an encoder (4 copies per plane, one
+// workgroup per CU); with chunk_ctr (a word of device memory, masked dtypes)
+// its workgroups take chunks from that counter and the grid's others join in
+// as the encoder leaves the CUs.
 hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int spe, uint32_t* d_hist,
-                              uint32_t* d_planes, hipStream_t s, bool lean = false);
+                              uint32_t* d_planes, hipStream_t s, bool lean = false, uint32_t* chunk_ctr = nullptr);
+// More workgroups (per_cu per CU) for a lean chunked histogram already queued
+// with chunk_ctr: they take the chunks still left (none: they end at once).
+hipError_t launch_masked_hist_join(const uint8_t* src, uint64_t n_bytes, int es, int spe, uint32_t* d_hist,
+                                   uint32_t* d_planes, uint32_t* chunk_ctr, uint32_t per_cu, hipStream_t s);
 hipError_t launch_set_u64(uint64_t* p, uint64_t v, hipStream_t s);
 hipError_t launch_set_counter(unsigned long long* p, unsigned long long v, hipStream_t s);
 
@@ -193,8 +201,10 @@ struct TableEncJob {
     uint32_t* ctl;
     TableEncArg a;
 };
-// Histogram words of a device-table job: the 768 of launch_masked_hist (all
-// live bytes, plane FL, plane 3), then the launch's gate (u64) and done counter.
+// Histogram words of an encode workspace (and of a device-table job): the 768
+// of launch_masked_hist (all live bytes, plane FL, plane 3), then
+// launch_hist_table's gate (768-769), done counter (770) and gate time-out
+// stamp (772-773), and the lean histogram's chunk counter (776).
 constexpr uint32_t kHistTableWords = 784;
 // Masked histogram and table set-up of up to kMaxHistJobs tensors in one grid
 // (launch_masked_hist_multi's shares): each job's first workgroup clears its

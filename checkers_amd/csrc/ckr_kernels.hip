@@ -489,10 +489,12 @@ __device__ __forceinline__ void hist_add_dword(uint32_t* sh, uint32_t v, uint32_
 
 // hist[256]: total, the zero planes counted in closed form into bin 0;
 // planes[512] (optional, masked dtypes): the two live planes.
+// ctr (optional): masked_hist_chunks_kernel's chunk counter.
 __global__ void __launch_bounds__(256) hist_init_kernel(uint32_t* __restrict__ hist, uint64_t zero_count,
-                                                        uint32_t* __restrict__ planes) {
+                                                        uint32_t* __restrict__ planes, uint32_t* __restrict__ ctr) {
     hist[threadIdx.x] = (threadIdx.x == 0) ? (uint32_t)zero_count : 0u;
     if (planes) { planes[threadIdx.x] = 0; planes[256 + threadIdx.x] = 0; }
+    if (ctr && threadIdx.x == 0) *ctr = 0;
 }
 
 // PC: copies per live plane (masked dtypes).  16 (32 KiB of LDS) when the
@@ -511,17 +513,14 @@ __global__ void __launch_bounds__(256) hist_init_kernel(uint32_t* __restrict__ h
 // sign that the job's first workgroup has cleared hist; a wait that outlasts
 // kGateSpins polls skips the adds and stores epoch in *gate_err instead.
 constexpr uint32_t kGateSpins = 1u << 22;
+// Pieces of a workgroup's histogram pass (sh: its PC copies per live plane,
+// c: this thread's copy): the bytes before the 16-byte aligned start (head_n,
+// at src - head_n), the 16-byte vectors [v, end) with stride, the bytes after
+// the last whole vector, and the sums added to the global counters.
 template <int SPE, int PC>
-__device__ __forceinline__ void masked_hist_share(uint32_t* sh, const uint8_t* __restrict__ src, uint64_t n_bytes,
-                                                  int es, uint32_t* __restrict__ hist, uint32_t* __restrict__ planes,
-                                                  uint32_t head_n, uint32_t b, uint32_t nb,
-                                                  unsigned long long* gate = nullptr, unsigned long long epoch = 0,
-                                                  unsigned long long* gate_err = nullptr) {
-    constexpr uint32_t NSH = SPE == 0 ? 256 * HIST_COPIES : 512 * PC;
-    for (uint32_t i = threadIdx.x; i < NSH; i += blockDim.x) sh[i] = 0;
-    __syncthreads();
-    const uint32_t c = threadIdx.x & (HIST_COPIES - 1);
-    if (b == 0 && threadIdx.x < head_n) {  // head bytes
+__device__ __forceinline__ void hist_head_bytes(uint32_t* sh, const uint8_t* __restrict__ src, int es, uint32_t head_n,
+                                                uint32_t c) {
+    if (threadIdx.x < head_n) {
         const int64_t p = (int64_t)threadIdx.x - (int64_t)head_n;
         const int plane = (int)(((p % es) + es) % es);
         if (plane >= SPE) {
@@ -529,11 +528,11 @@ __device__ __forceinline__ void masked_hist_share(uint32_t* sh, const uint8_t* _
             atomicAdd(&sh[hist_slot<SPE, PC>((uint32_t)src[p], r, c)], 1u);
         }
     }
-    const uint64_t nvec = n_bytes / 16;
-    const uint4* v4 = reinterpret_cast<const uint4*>(src);
-    const uint64_t stride = (uint64_t)nb * blockDim.x;
-    uint64_t v = (uint64_t)b * blockDim.x + threadIdx.x;
-    for (; v + 3 * stride < nvec; v += 4 * stride) {  // 4 loads in flight per thread
+}
+template <int SPE, int PC>
+__device__ __forceinline__ void hist_vectors(uint32_t* sh, const uint4* __restrict__ v4, uint64_t v, uint64_t end,
+                                             uint64_t stride, uint32_t c) {
+    for (; v + 3 * stride < end; v += 4 * stride) {  // 4 loads in flight per thread
         uint4 a = v4[v], b = v4[v + stride], d = v4[v + 2 * stride], e = v4[v + 3 * stride];
         hist_add_dword<SPE, PC>(sh, a.x, c); hist_add_dword<SPE, PC>(sh, a.y, c);
         hist_add_dword<SPE, PC>(sh, a.z, c); hist_add_dword<SPE, PC>(sh, a.w, c);
@@ -544,34 +543,24 @@ __device__ __forceinline__ void masked_hist_share(uint32_t* sh, const uint8_t* _
         hist_add_dword<SPE, PC>(sh, e.x, c); hist_add_dword<SPE, PC>(sh, e.y, c);
         hist_add_dword<SPE, PC>(sh, e.z, c); hist_add_dword<SPE, PC>(sh, e.w, c);
     }
-    for (; v < nvec; v += stride) {
+    for (; v < end; v += stride) {
         uint4 a = v4[v];
         hist_add_dword<SPE, PC>(sh, a.x, c); hist_add_dword<SPE, PC>(sh, a.y, c);
         hist_add_dword<SPE, PC>(sh, a.z, c); hist_add_dword<SPE, PC>(sh, a.w, c);
     }
-    if (b == 0) {  // tail bytes
-        for (uint64_t p = nvec * 16 + threadIdx.x; p < n_bytes; p += blockDim.x) {
-            const int plane = (int)(p % (uint64_t)es);
-            if (plane < SPE) continue;
-            const uint32_t r = (SPE > 0 && (p & 3) == 3) ? 1u : 0u;  // live-plane rank
-            atomicAdd(&sh[hist_slot<SPE, PC>((uint32_t)src[p], r, c)], 1u);
-        }
+}
+template <int SPE, int PC>
+__device__ __forceinline__ void hist_tail_bytes(uint32_t* sh, const uint8_t* __restrict__ src, uint64_t n_bytes, int es,
+                                                uint32_t c) {
+    for (uint64_t p = (n_bytes / 16) * 16 + threadIdx.x; p < n_bytes; p += blockDim.x) {
+        const int plane = (int)(p % (uint64_t)es);
+        if (plane < SPE) continue;
+        const uint32_t r = (SPE > 0 && (p & 3) == 3) ? 1u : 0u;  // live-plane rank
+        atomicAdd(&sh[hist_slot<SPE, PC>((uint32_t)src[p], r, c)], 1u);
     }
-    if (gate) {
-        __shared__ uint32_t open;
-        if (threadIdx.x == 0) {
-            uint32_t n = 0;
-            // relaxed polls (an acquire would invalidate the L2 at every poll): the
-            // adds after the loop are device-scope atomics and need no acquire
-            while (__hip_atomic_load(gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch && ++n < kGateSpins)
-                __builtin_amdgcn_s_sleep(2);
-            open = n < kGateSpins;
-            if (!open) __hip_atomic_store(gate_err, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (!open) return;
-    }
-    __syncthreads();
+}
+template <int SPE, int PC>
+__device__ __forceinline__ void hist_flush(const uint32_t* sh, uint32_t* __restrict__ hist, uint32_t* __restrict__ planes) {
     const uint32_t bin = threadIdx.x;
     if (SPE == 0) {
         uint32_t sum = 0;
@@ -594,11 +583,87 @@ __device__ __forceinline__ void masked_hist_share(uint32_t* sh, const uint8_t* _
 }
 
 template <int SPE, int PC>
+__device__ __forceinline__ void masked_hist_share(uint32_t* sh, const uint8_t* __restrict__ src, uint64_t n_bytes,
+                                                  int es, uint32_t* __restrict__ hist, uint32_t* __restrict__ planes,
+                                                  uint32_t head_n, uint32_t b, uint32_t nb,
+                                                  unsigned long long* gate = nullptr, unsigned long long epoch = 0,
+                                                  unsigned long long* gate_err = nullptr) {
+    constexpr uint32_t NSH = SPE == 0 ? 256 * HIST_COPIES : 512 * PC;
+    for (uint32_t i = threadIdx.x; i < NSH; i += blockDim.x) sh[i] = 0;
+    __syncthreads();
+    const uint32_t c = threadIdx.x & (HIST_COPIES - 1);
+    if (b == 0) hist_head_bytes<SPE, PC>(sh, src, es, head_n, c);
+    const uint64_t stride = (uint64_t)nb * blockDim.x;
+    hist_vectors<SPE, PC>(sh, reinterpret_cast<const uint4*>(src), (uint64_t)b * blockDim.x + threadIdx.x, n_bytes / 16,
+                          stride, c);
+    if (b == 0) hist_tail_bytes<SPE, PC>(sh, src, n_bytes, es, c);
+    if (gate) {
+        __shared__ uint32_t open;
+        if (threadIdx.x == 0) {
+            uint32_t n = 0;
+            // relaxed polls (an acquire would invalidate the L2 at every poll): the
+            // adds after the loop are device-scope atomics and need no acquire
+            while (__hip_atomic_load(gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch && ++n < kGateSpins)
+                __builtin_amdgcn_s_sleep(2);
+            open = n < kGateSpins;
+            if (!open) __hip_atomic_store(gate_err, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!open) return;
+    }
+    __syncthreads();
+    hist_flush<SPE, PC>(sh, hist, planes);
+}
+
+template <int SPE, int PC>
 __global__ void __launch_bounds__(256) masked_hist_kernel(const uint8_t* __restrict__ src, uint64_t n_bytes,
                                                           int es, uint32_t* __restrict__ hist,
                                                           uint32_t* __restrict__ planes, uint32_t head_n) {
     __shared__ uint32_t sh[SPE == 0 ? 256 * HIST_COPIES : 512 * PC];
     masked_hist_share<SPE, PC>(sh, src, n_bytes, es, hist, planes, head_n, blockIdx.x, gridDim.x);
+}
+
+// The histogram beside a running encoder (PC copies per plane), its
+// workgroups taking chunks of kHistChunkVecs vectors from a counter (*ctr,
+// cleared by hist_init_kernel) instead of fixed shares.  Beside the encoder one
+// workgroup fits per CU; as the encoder's workgroups leave their CUs the
+// grid's other workgroups are dispatched there and join in, so that the pass
+// finishes at full width instead of on one workgroup per CU.  The workgroup
+// that first finds the chunks gone counts the head and tail bytes; a
+// workgroup that counted nothing adds nothing.
+constexpr uint64_t kHistChunkVecs = 16384;  // 256 KiB
+template <int SPE, int PC>
+__global__ void __launch_bounds__(256) masked_hist_chunks_kernel(const uint8_t* __restrict__ src, uint64_t n_bytes,
+                                                                 int es, uint32_t* __restrict__ hist,
+                                                                 uint32_t* __restrict__ planes, uint32_t head_n,
+                                                                 uint32_t* __restrict__ ctr) {
+    __shared__ uint32_t sh[SPE == 0 ? 256 * HIST_COPIES : 512 * PC];
+    __shared__ uint32_t ticket;
+    constexpr uint32_t NSH = SPE == 0 ? 256 * HIST_COPIES : 512 * PC;
+    for (uint32_t i = threadIdx.x; i < NSH; i += blockDim.x) sh[i] = 0;
+    const uint32_t c = threadIdx.x & (HIST_COPIES - 1);
+    const uint64_t nvec = n_bytes / 16;
+    const uint64_t nch = (nvec + kHistChunkVecs - 1) / kHistChunkVecs;
+    bool counted = false;
+    for (;;) {
+        __syncthreads();
+        if (threadIdx.x == 0) ticket = atomicAdd(ctr, 1u);
+        __syncthreads();
+        const uint64_t k = ticket;
+        if (k >= nch) {
+            if (k == nch) {  // (one workgroup)
+                hist_head_bytes<SPE, PC>(sh, src, es, head_n, c);
+                hist_tail_bytes<SPE, PC>(sh, src, n_bytes, es, c);
+                counted = true;
+            }
+            break;
+        }
+        counted = true;
+        const uint64_t v0 = k * kHistChunkVecs, v1 = v0 + kHistChunkVecs < nvec ? v0 + kHistChunkVecs : nvec;
+        hist_vectors<SPE, PC>(sh, reinterpret_cast<const uint4*>(src), v0 + threadIdx.x, v1, blockDim.x, c);
+    }
+    __syncthreads();
+    if (counted) hist_flush<SPE, PC>(sh, hist, planes);
 }
 
 // Several tensors' histograms in one grid (ckr_compress_many on a shard of
@@ -692,10 +757,11 @@ uint32_t hist_num_blocks(uint64_t n_bytes) {
 }
 
 hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int spe, uint32_t* d_hist,
-                              uint32_t* d_planes, hipStream_t s, bool lean) {
+                              uint32_t* d_planes, hipStream_t s, bool lean, uint32_t* chunk_ctr) {
     const uint64_t zero_count = (es > 0) ? (n_bytes / (uint64_t)es) * (uint64_t)spe : 0;
     if (spe == 0) d_planes = nullptr;
-    CKR_LAUNCH("hist_init_kernel", s, hist_init_kernel<<<1, 256, 0, s>>>(d_hist, zero_count, d_planes));
+    if (!lean || spe == 0) chunk_ctr = nullptr;
+    CKR_LAUNCH("hist_init_kernel", s, hist_init_kernel<<<1, 256, 0, s>>>(d_hist, zero_count, d_planes, chunk_ctr));
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (n_bytes == 0) return hipSuccess;
@@ -714,6 +780,14 @@ hipError_t launch_masked_hist(const uint8_t* src, uint64_t n_bytes, int es, int 
         if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
         if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
         if (ncu > 0 && nblk > (uint32_t)ncu) nblk = (uint32_t)ncu;
+        if (chunk_ctr) {  // chunks from a counter (launch_masked_hist_join can add workgroups)
+            const uint32_t grid = (uint32_t)std::max(ncu, 1);
+            if (spe == 2)
+                CKR_LAUNCH("masked_hist_kernel", s, masked_hist_chunks_kernel<2, 4><<<grid, 256, 0, s>>>(src, n_bytes, es, d_hist, d_planes, head_n, chunk_ctr));
+            else
+                CKR_LAUNCH("masked_hist_kernel", s, masked_hist_chunks_kernel<1, 4><<<grid, 256, 0, s>>>(src, n_bytes, es, d_hist, d_planes, head_n, chunk_ctr));
+            return hipGetLastError();
+        }
     }
     auto run = [&](auto kern) {
         CKR_LAUNCH("masked_hist_kernel", s, kern<<<nblk, 256, 0, s>>>(src, n_bytes, es, d_hist, d_planes, head_n));
@@ -749,6 +823,24 @@ static uint32_t hist_shares(const HistSrc* srcs, uint32_t n, HistJob* out, uint3
     }
     return nb;
 }
+hipError_t launch_masked_hist_join(const uint8_t* src, uint64_t n_bytes, int es, int spe, uint32_t* d_hist,
+                                   uint32_t* d_planes, uint32_t* chunk_ctr, uint32_t per_cu, hipStream_t s) {
+    if (spe != 1 && spe != 2) return hipErrorInvalidValue;
+    const uint32_t mis = (uint32_t)(reinterpret_cast<uintptr_t>(src) & 15u);
+    const uint32_t head_n = (uint32_t)std::min<uint64_t>(mis ? 16u - mis : 0u, n_bytes);
+    int dev = 0, ncu = 0;
+    hipError_t e;
+    if ((e = hipGetDevice(&dev)) != hipSuccess) return e;
+    if ((e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess) return e;
+    const uint32_t grid = per_cu * (uint32_t)std::max(ncu, 1);
+    // full-width copies (16 per plane): these workgroups run once the CUs are free
+    if (spe == 2)
+        CKR_LAUNCH("masked_hist_kernel", s, masked_hist_chunks_kernel<2, 16><<<grid, 256, 0, s>>>(src + head_n, n_bytes - head_n, es, d_hist, d_planes, head_n, chunk_ctr));
+    else
+        CKR_LAUNCH("masked_hist_kernel", s, masked_hist_chunks_kernel<1, 16><<<grid, 256, 0, s>>>(src + head_n, n_bytes - head_n, es, d_hist, d_planes, head_n, chunk_ctr));
+    return hipGetLastError();
+}
+
 hipError_t launch_masked_hist_multi(const HistSrc* srcs, uint32_t n, uint32_t* d_hists, hipStream_t s) {
     for (uint32_t j0 = 0; j0 < n; j0 += kMaxHistJobs) {
         const uint32_t m = std::min<uint32_t>(kMaxHistJobs, n - j0);
