@@ -1258,6 +1258,22 @@ int dev_enc_queue_encode(const DevEnc& d, hipStream_t s) {
     return CKR_OK;
 }
 
+// The encode and, right behind it with no read-back between them, the redo
+// pass (it ends at once when no unit outgrew its slots).
+int dev_enc_queue_encode_redo(DevEnc& d, hipStream_t s) {
+    if (int rc = dev_enc_queue_encode(d, s)) return rc;
+    const uint32_t lds_limit = (uint32_t)max_lds_per_block();
+    if (ckr::encode_fast_list_fits(d.fp, d.g, lds_limit)) {
+        const EncodeLayout& L = d.L;
+        CKR_HIP(ckr::launch_encode_fast_list(d.src, d.g, reinterpret_cast<ckr::EncSym*>(d.ws + L.off_enc),
+                                             reinterpret_cast<uint32_t*>(d.ws + L.off_canon), d.fp, lds_limit, d.hdrs,
+                                             d.out, d.unit_off, reinterpret_cast<uint64_t*>(d.ws + L.off_status), d.dctl,
+                                             reinterpret_cast<uint32_t*>(d.ws + L.off_redo), s));
+        d.redo_queued = true;
+    }
+    return CKR_OK;
+}
+
 // The same encode as a job of launch_encode_fast_multi.
 ckr::FastJob dev_fast_job(const DevEnc& d) {
     const EncodeLayout& L = d.L;
@@ -1340,18 +1356,8 @@ int compress_device_table(const void* src, const ckr::EncodeGeom& g, int ensure_
         (void)hipStreamSynchronize(s);  // the set-up writes the caller's workspace
         return rc;
     }
-    rc = dev_enc_queue_encode(d, s);
+    rc = dev_enc_queue_encode_redo(d, s);
     if (rc) return rc;
-    // the redo pass right behind the encode, with no read-back between them:
-    // it ends at once when no unit outgrew its slots
-    const uint32_t lds_limit = (uint32_t)max_lds_per_block();
-    if (ckr::encode_fast_list_fits(d.fp, g, lds_limit)) {
-        CKR_HIP(ckr::launch_encode_fast_list(d.src, g, reinterpret_cast<ckr::EncSym*>(ws + d.L.off_enc),
-                                             reinterpret_cast<uint32_t*>(ws + d.L.off_canon), d.fp, lds_limit, d.hdrs,
-                                             d.out, d.unit_off, reinterpret_cast<uint64_t*>(ws + d.L.off_status), d.dctl,
-                                             reinterpret_cast<uint32_t*>(ws + d.L.off_redo), s));
-        d.redo_queued = true;
-    }
     CKR_HIP(hipMemcpyAsync(pw, d.dctl, kCtlWords * 4, hipMemcpyDeviceToHost, s));
     CKR_HIP(hipStreamSynchronize(s));
     bool more = false;
@@ -1602,6 +1608,59 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
         if (e != hipSuccess || tail) return e;
         return hipMemcpyAsync(h_dst, d_hist, 768 * sizeof(uint32_t), hipMemcpyDeviceToHost, a->s2);
     };
+    // Tables on the device when every job's tensor is one the fast encoder
+    // takes (their control and table words in the library's pinned slots):
+    // dev_setup sets chains (null: the host's tables serve the shard).
+    std::vector<DevEnc> dv(n);
+    const void* chains = nullptr;
+    auto dev_setup = [&]() -> int {
+        if (a->tslot_jobs < n) {
+            if (a->tslots) CKR_HIP(hipHostFree(a->tslots));
+            if (a->d_tslots) CKR_HIP(hipFree(a->d_tslots));
+            a->tslots = nullptr;
+            a->d_tslots = nullptr;
+            a->tslot_jobs = 0;
+            CKR_HIP(hipHostMalloc(reinterpret_cast<void**>(&a->tslots), n * kCtlWords * 4, hipHostMallocDefault));
+            CKR_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_tslots), n * kCtlWords * 4));
+            a->tslot_jobs = n;
+        }
+        bool all = true;
+        for (uint64_t i = 0; i < n && all; i++)
+            all = dev_enc_setup(dv[i], staged[i].p, geo[i], static_cast<uint8_t*>(jobs[i].d_workspace), jobs[i].d_out,
+                                jobs[i].d_headers, jobs[i].d_unit_offsets, jobs[i].d_sidecar,
+                                a->d_tslots + kCtlWords * i, a->tslots + kCtlWords * i);
+        chains = all ? canon_chains(a->s2) : nullptr;
+        return CKR_OK;
+    };
+    // Once every device-table encode is queued and the caller's stream waits
+    // for them: one read-back of every job's words, then each job's table and
+    // total; a job whose ranks leave its table to the sort is encoded again
+    // under the host's table (hist_of(i): its 768 histogram words).
+    auto dev_finish = [&](std::initializer_list<hipStream_t> streams,
+                          const std::function<const uint32_t*(uint64_t)>& hist_of) -> int {
+        CKR_HIP(hipMemcpyAsync(a->tslots, a->d_tslots, n * kCtlWords * 4, hipMemcpyDeviceToHost, s));
+        for (hipStream_t x : streams) CKR_HIP(hipStreamSynchronize(x));
+        bool more = false;
+        for (uint64_t i = 0; i < n; i++) {
+            ckr_compress_job& jb = jobs[i];
+            int rc = dev_enc_finish(dv[i], jb.h_table, &jb.total, &more, s);
+            if (rc == kUseHostTable) {  // the sorted table decides: encode this job again
+                uint32_t hh[768];
+                CKR_HIP(hipMemcpy(hh, hist_of(i), sizeof(hh), hipMemcpyDeviceToHost));
+                ckr_freq_table local;
+                ckr_freq_table* t = jb.h_table ? jb.h_table : &local;
+                rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
+                if (rc == CKR_OK)
+                    rc = encode_impl(staged[i].p, jb.n_elems, jb.dtype, t, unit_bytes, jb.d_out, jb.out_capacity,
+                                     jb.d_headers, jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace, jb.workspace_bytes,
+                                     &jb.total, hh + 256, s);
+            }
+            if (rc) return rc;
+        }
+        if (more) CKR_HIP(hipStreamSynchronize(s));
+        drain.ok = true;
+        return CKR_OK;
+    };
     // A shard of small tensors: every histogram first (full width, back to
     // back), one synchronisation, then every encode queued without a host wait,
     // round robin over four streams.  Beside an encode of a few tens of
@@ -1635,27 +1694,9 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
                      (int)geo[i].spe};
         // tables on the device when every job's tensor is one the fast encoder
         // takes: no read-back or host table between the histograms and the
-        // encodes (a job whose ranks leave its table to the sort is encoded
-        // again under the host's table at the end)
-        std::vector<DevEnc> dv(n);
-        bool dev_all = true;
-        if (a->tslot_jobs < n) {
-            if (a->tslots) CKR_HIP(hipHostFree(a->tslots));
-            if (a->d_tslots) CKR_HIP(hipFree(a->d_tslots));
-            a->tslots = nullptr;
-            a->d_tslots = nullptr;
-            a->tslot_jobs = 0;
-            CKR_HIP(hipHostMalloc(reinterpret_cast<void**>(&a->tslots), n * kCtlWords * 4, hipHostMallocDefault));
-            CKR_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_tslots), n * kCtlWords * 4));
-            a->tslot_jobs = n;
-        }
-        for (uint64_t i = 0; i < n && dev_all; i++)
-            dev_all = dev_enc_setup(dv[i], staged[i].p, geo[i], static_cast<uint8_t*>(jobs[i].d_workspace),
-                                    jobs[i].d_out, jobs[i].d_headers, jobs[i].d_unit_offsets, jobs[i].d_sidecar,
-                                    a->d_tslots + kCtlWords * i, a->tslots + kCtlWords * i);
-        const void* chains = dev_all ? canon_chains(a->s2) : nullptr;
-        dev_all = dev_all && chains;
-        if (dev_all) {
+        // encodes
+        if (int rc = dev_setup()) return rc;
+        if (chains) {
             // every histogram and table in one grid (per 16 jobs), the tables
             // built by each job's last workgroup, then the encodes, then one
             // read-back of every job's control and table words
@@ -1686,29 +1727,7 @@ int ckr_compress_many(ckr_compress_job* jobs, uint64_t n, uint64_t unit_bytes, i
             }
             CKR_HIP(hipEventRecord(a->ev, a->s2));  // the caller's stream waits for them
             CKR_HIP(hipStreamWaitEvent(s, a->ev, 0));
-            enc_streams = {s, a->s2};
-            CKR_HIP(hipMemcpyAsync(a->tslots, a->d_tslots, n * kCtlWords * 4, hipMemcpyDeviceToHost, s));
-            for (hipStream_t x : enc_streams) CKR_HIP(hipStreamSynchronize(x));
-            bool more = false;
-            for (uint64_t i = 0; i < n; i++) {
-                ckr_compress_job& jb = jobs[i];
-                int rc = dev_enc_finish(dv[i], jb.h_table, &jb.total, &more, s);
-                if (rc == kUseHostTable) {  // the sorted table decides: encode this job again
-                    uint32_t hh[768];
-                    CKR_HIP(hipMemcpy(hh, a->d_hists + ckr::kHistTableWords * i, sizeof(hh), hipMemcpyDeviceToHost));
-                    ckr_freq_table local;
-                    ckr_freq_table* t = jb.h_table ? jb.h_table : &local;
-                    rc = ckr_build_table(hh, ensure_full_alphabet, t, nullptr);
-                    if (rc == CKR_OK)
-                        rc = encode_impl(staged[i].p, jb.n_elems, jb.dtype, t, unit_bytes, jb.d_out, jb.out_capacity,
-                                         jb.d_headers, jb.d_unit_offsets, jb.d_sidecar, jb.d_workspace,
-                                         jb.workspace_bytes, &jb.total, hh + 256, s);
-                }
-                if (rc) return rc;
-            }
-            if (more) CKR_HIP(hipStreamSynchronize(s));
-            drain.ok = true;
-            return CKR_OK;
+            return dev_finish({s, a->s2}, [&](uint64_t i) { return a->d_hists + ckr::kHistTableWords * i; });
         }
         if (int rc = check_outputs()) return rc;
         // every histogram in one grid (per 16 jobs) and one read-back: a launch

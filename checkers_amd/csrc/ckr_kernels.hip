@@ -50,8 +50,8 @@ __device__ __forceinline__ EncSym enc_entry(const TableArg& t, uint32_t s) { ret
 //
 // norm_fix's positions are counted by buckets of the fractional part: the
 // symbols that take part in the correction (included ones, for the -1 case
-// only those holding more than one slot) are counted into 1024 buckets,
-// bucket floor(frac * 1024), whose order is that of the parts.  A symbol's
+// only those holding more than one slot) are counted into 256 buckets,
+// bucket floor(frac * 256), whose order is that of the parts.  A symbol's
 // position then lies between the count on its side of its bucket and that
 // plus its bucket's count, which decides +1/-1 or 0 for every symbol except
 // those of the one bucket the boundary cuts; only these compare exact parts,
@@ -60,7 +60,7 @@ __device__ __forceinline__ EncSym enc_entry(const TableArg& t, uint32_t s) { ret
 struct RankTable {
     uint32_t norm[256], cum[257];
     double key[256];
-    uint32_t bcnt[1024], bpre[1024];
+    uint32_t bcnt[256], bpre[256];
     uint32_t blist[256];
     unsigned long long red64[4];
     uint32_t red[4], ambw[4], amb, nlist, bstar;
@@ -109,15 +109,14 @@ __device__ void rank_table(const uint32_t* __restrict__ hist, bool ensure_full, 
         const bool up = assigned < kTabM;
         const uint32_t rem = up ? kTabM - assigned : assigned - kTabM;
         const bool part = r.inc && (up || r.norm > 1u);
-        const uint32_t b = part ? min((uint32_t)(r.frac * 1024.0), 1023u) : 0u;
+        const uint32_t b = part ? min((uint32_t)(r.frac * 256.0), 255u) : 0u;
         T.key[s] = r.frac;
-        reinterpret_cast<uint4*>(T.bcnt)[s] = make_uint4(0u, 0u, 0u, 0u);
+        T.bcnt[s] = 0;
         __syncthreads();
         if (part) atomicAdd(&T.bcnt[b], 1u);
         __syncthreads();
-        // exclusive sums over the buckets, thread s holding buckets 4s .. 4s+3
-        const uint4 c4 = reinterpret_cast<const uint4*>(T.bcnt)[s];
-        const uint32_t tsum = c4.x + c4.y + c4.z + c4.w;
+        // exclusive sums over the buckets, thread s holding bucket s
+        const uint32_t tsum = T.bcnt[s];
         const uint32_t inc = wave_incl_sum(tsum);
         if ((s & 63) == 63) T.red[s >> 6] = inc;
         __syncthreads();
@@ -128,8 +127,7 @@ __device__ void rank_table(const uint32_t* __restrict__ hist, bool ensure_full, 
             pre += w < (s >> 6) ? v : 0u;
             npart += v;
         }
-        const uint32_t e0 = pre + inc - tsum;
-        reinterpret_cast<uint4*>(T.bpre)[s] = make_uint4(e0, e0 + c4.x, e0 + c4.x + c4.y, e0 + c4.x + c4.y + c4.z);
+        T.bpre[s] = pre + inc - tsum;
         __syncthreads();
         // up: the first rem of the descending order get +1; down: the last rem get -1.
         // lo: the symbols strictly before s on that side, counted by whole buckets
@@ -741,6 +739,7 @@ __global__ void __launch_bounds__(256) hist_table_kernel(HistTableJobs J, Chains
     const uint32_t flags = __hip_atomic_load(gate_err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == J.epoch ? 4u : 0u;
     table_enc_body(j.hist, t.a, t.enc, t.canon, t.tinfo, t.ctl, ch, J.epoch, flags, *reinterpret_cast<TableLds*>(sh));
 }
+
 
 // Every workgroup ends with up to 768 global atomics (the sums of its LDS
 // copies), so the grid is kept small: 256 workgroups (one per CU) below 256
@@ -4145,16 +4144,19 @@ static Chains chains_of(const void* chains) {
                   reinterpret_cast<const uint16_t*>(p + 4ull * (kChainSteps + 1) * kChainRows),
                   p + 6ull * (kChainSteps + 1) * kChainRows};
 }
+// A value no earlier launch of this process used, and unlikely to be left in
+// memory by another process.
+static uint64_t next_epoch() {
+    static std::atomic<uint64_t> next{0x5a17c0de00000000ull ^ ((uint64_t)reinterpret_cast<uintptr_t>(&next) << 8)};
+    return next.fetch_add(1, std::memory_order_relaxed) + 1;
+}
 hipError_t launch_hist_table(const HistSrc* srcs, uint32_t* const* hists, const TableEncJob* jobs, uint32_t n,
                              const void* chains, uint64_t* epochs, hipStream_t s) {
-    // a value no earlier launch of this process used, and unlikely to be
-    // left in memory by another process
-    static std::atomic<uint64_t> next{0x5a17c0de00000000ull ^ ((uint64_t)reinterpret_cast<uintptr_t>(&next) << 8)};
     for (uint32_t j0 = 0; j0 < n; j0 += kMaxHistJobs) {
         const uint32_t m = std::min<uint32_t>(kMaxHistJobs, n - j0);
         HistTableJobs J{};
         J.n = m;
-        J.epoch = next.fetch_add(1, std::memory_order_relaxed) + 1;
+        J.epoch = next_epoch();
         HistJob hj[kMaxHistJobs];
         for (uint32_t k = 0; k < m; k++)
             if (srcs[j0 + k].spe != 1 && srcs[j0 + k].spe != 2) return hipErrorInvalidValue;
