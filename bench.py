@@ -18,7 +18,9 @@ streams: per tensor the masked histogram and table of the whole tensor, then the
 tensor's 8 GiB slices encoded with that table one after the other into reused
 buffers (slices end on unit boundaries, and units are independent given the
 table, so each slice's units are the whole-tensor encode's), each decoded into
-a reused window and compared with its source outside the timed regions.
+a reused window; as for the resident configurations, the lane checks (a
+decode that counts failing lanes) and the comparison with the source run
+outside the timed regions.
 
 After the timed steps, the drop-in path runs end to end once per repetition:
 checkers_py.initialize_context / analyze_tensors / compress_and_save on a
@@ -649,11 +651,14 @@ def stream_bench(shard, ck, torch, dev, unit, steps, slice_bytes):
                 a.record()
                 r = encs[m].encode(src, table, planes=planes)
                 b.record()
-                bad = decs[m].decode(r.data, r.headers, r.unit_offsets, r.table, r.sidecar, window, check=True)
+                decs[m].decode(r.data, r.headers, r.unit_offsets, r.table, r.sidecar, window, check=False)
                 c.record()
                 torch.cuda.synchronize()
                 enc_s += a.elapsed_time(b) / 1e3
                 dec_s += b.elapsed_time(c) / 1e3
+                # as for the resident configurations, the lane checks in a decode
+                # of their own outside the timed region
+                bad = decs[m].decode(r.data, r.headers, r.unit_offsets, r.table, r.sidecar, window, check=True)
                 ok = ok and bad == 0 and torch.equal(window[: m * es], src.view(torch.uint8))
                 C += r.total
                 S += m * ck.sidecar_bytes_per_elem(tag)

@@ -1844,10 +1844,13 @@ namespace {
 // ckr_decode and its no-allocation variant.  noalloc: the workspace is the
 // device's scratch array, the destination must be 4-byte aligned (no staging
 // copy), and the bad-lane count is read back through the caller's stack.
+// counted: the caller reads the bad-lane count (h_bad_lanes, or
+// ckr_decode_many's check), so that the fast decoder also compares the
+// zero-plane lanes' bytes, which do not enter the output.
 int decode_impl(const uint8_t* d_data, const ckr_stream_header* d_headers, const uint64_t* d_unit_offsets,
                 const ckr_freq_table* h_table, uint64_t n_elems, int dtype, uint64_t unit_bytes,
                 const uint8_t* d_sidecar, void* d_dst, void* d_workspace, uint64_t workspace_bytes,
-                uint64_t* h_bad_lanes, void* stream, bool noalloc) {
+                uint64_t* h_bad_lanes, void* stream, bool noalloc, bool counted) {
     if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
     ckr::EncodeGeom g;
     if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
@@ -1898,7 +1901,7 @@ int decode_impl(const uint8_t* d_data, const ckr_stream_header* d_headers, const
     hipError_t de = use_long_units(g)
                         ? ckr::launch_decode_long(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, out, bad, s)
                         : ckr::launch_decode(d_data, d_headers, d_unit_offsets, dec, g, d_sidecar, out, bad,
-                                             L.fast ? canon : nullptr, ck.cw, s);
+                                             L.fast ? canon : nullptr, ck.cw, s, counted);
     if (tmp) {
         if (de == hipSuccess) de = hipMemcpyAsync(d_dst, tmp, g.n_bytes, hipMemcpyDeviceToDevice, s);
         (void)hipFreeAsync(tmp, s);
@@ -1957,7 +1960,7 @@ int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers, const 
                const uint8_t* d_sidecar, void* d_dst, void* d_workspace, uint64_t workspace_bytes,
                uint64_t* h_bad_lanes, void* stream) {
     return decode_impl(d_data, d_headers, d_unit_offsets, h_table, n_elems, dtype, unit_bytes, d_sidecar, d_dst,
-                       d_workspace, workspace_bytes, h_bad_lanes, stream, false);
+                       d_workspace, workspace_bytes, h_bad_lanes, stream, false, h_bad_lanes != nullptr);
 }
 
 int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int check, void* stream) {
@@ -2024,7 +2027,8 @@ int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int c
         const ckr_decode_job& jb = jobs[i];
         hipStream_t js = pool[i % pool.size()];
         int rc = decode_impl(jb.d_data, jb.d_headers, jb.d_unit_offsets, jb.h_table, jb.n_elems, jb.dtype, unit_bytes,
-                             jb.d_sidecar, jb.d_dst, jb.d_workspace, jb.workspace_bytes, nullptr, js, false);
+                             jb.d_sidecar, jb.d_dst, jb.d_workspace, jb.workspace_bytes, nullptr, js, false,
+                             check != 0);
         if (rc == CKR_OK && check) {
             ckr::EncodeGeom g;
             make_geom(jb.n_elems, jb.dtype, unit_bytes, &g);
@@ -2077,7 +2081,7 @@ int ckr_decode_noalloc(const uint8_t* d_data, const ckr_stream_header* d_headers
     if (int rc = noalloc_scratch(&ws)) return rc;
     ckr::t_noalloc = true;
     const int rc = decode_impl(d_data, d_headers, d_unit_offsets, h_table, n_elems, dtype, unit_bytes, d_sidecar, d_dst,
-                               ws, kNoAllocScratchBytes, h_bad_lanes, stream, true);
+                               ws, kNoAllocScratchBytes, h_bad_lanes, stream, true, h_bad_lanes != nullptr);
     ckr::t_noalloc = false;
     return rc;
 }

@@ -274,9 +274,14 @@ hipError_t launch_canon_store(const CanonArg& a, uint32_t* canon, hipStream_t s)
 // Decode; with canon (masked dtypes) the fast kernel decodes every unit,
 // otherwise the general kernel does.
 uint32_t decode_fast_lds_bytes();
+// zero_bytes: the fast decoder also compares the zero-plane lanes' bytes with
+// their canonical streams (their headers are checked either way); those bytes
+// do not enter the output, so only a caller that reads the bad-lane count
+// needs them read.
 hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
                          const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
-                         unsigned long long* bad, const uint32_t* canon, uint32_t cw, hipStream_t s);
+                         unsigned long long* bad, const uint32_t* canon, uint32_t cw, hipStream_t s,
+                         bool zero_bytes = true);
 
 // Analyzer (ckr_analyzer.hip): every record in one grid per pass.
 struct StatsParams {     // per record, device resident between passes

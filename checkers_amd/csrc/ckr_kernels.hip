@@ -3440,14 +3440,16 @@ __device__ __forceinline__ void df_load_sc(uint32_t (&sc)[8], const uint32_t* p)
 }
 
 // A zero-plane lane against the canonical stream of its symbol count: header
-// (state, count, inside the unit) and bytes.  The bytes are compared 32 at a
-// time, all loads of a step issued together (9 stream dwords around the bytes,
-// 8 canonical dwords) so that the check waits for memory once per step; near
-// the ends of the data buffer, byte by byte.
+// (state, count, inside the unit) and, with bytes, its bytes (they do not
+// enter the output: the zero planes' output bytes are the sidecar's).  The
+// bytes are compared 32 at a time, all loads of a step issued together (9
+// stream dwords around the bytes, 8 canonical dwords) so that the check waits
+// for memory once per step; near the ends of the data buffer, byte by byte.
 __device__ __forceinline__ bool df_zero_lane_ok(const ckr_stream_header& h, const uint32_t* ce, const uint32_t* cp,
                                                 uint32_t cw, const uint8_t* ud, uint32_t usize, uintptr_t d0,
-                                                uintptr_t d1) {
+                                                uintptr_t d1, bool bytes) {
     if (h.final_state != ce[1] || h.byte_count != ce[2] || (uint64_t)h.buf_offset + h.byte_count > usize) return false;
+    if (!bytes) return true;
     const uint8_t* sl = ud + h.buf_offset;
     const uint32_t bc = h.byte_count;
     uint32_t diff = 0;
@@ -3482,7 +3484,8 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
                                                                    const uint32_t* __restrict__ d_dec,
                                                                    const uint32_t* __restrict__ canon, uint32_t cw,
                                                                    EncodeGeom g, const uint8_t* __restrict__ sidecar,
-                                                                   uint8_t* __restrict__ dst, unsigned long long* bad) {
+                                                                   uint8_t* __restrict__ dst, unsigned long long* bad,
+                                                                   uint32_t zero_bytes) {
     extern __shared__ uint32_t lds[];
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
     const uint32_t* tab = reinterpret_cast<const uint32_t*>(lds);
@@ -3573,7 +3576,7 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
                 const uint32_t Kb = Kz + ((4 * j + b < rz) ? 1u : 0u);  // symbols of lane 4j+b
                 const uint32_t ent = (canon[0] == Kb) ? 0u : ((canon[4 + cw] == Kb) ? 1u : 2u);
                 nbad += df_zero_lane_ok(uh[b], canon + ent * (4 + cw), cbytes + (uint64_t)ent * cw, cw, ud,
-                                        usize, d0, d1) ? 0u : 1u;
+                                        usize, d0, d1, zero_bytes != 0) ? 0u : 1u;
             }
             df_put(lds8, da.tb, da.ch, ca);
             df_put(lds8, db.tb, db.ch, cb);
@@ -4188,7 +4191,7 @@ uint32_t decode_fast_lds_bytes() { return DF_TAB_BYTES + DF_WAVES * DF_WAVE_BYTE
 
 hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
                          const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
-                         unsigned long long* bad, const uint32_t* canon, uint32_t cw, hipStream_t s) {
+                         unsigned long long* bad, const uint32_t* canon, uint32_t cw, hipStream_t s, bool zero_bytes) {
     const uint32_t grid = (uint32_t)((g.n_units + 3) / 4);
     if (grid == 0) return hipSuccess;
     hipError_t e;
@@ -4208,7 +4211,7 @@ hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, con
             // persistent: the blocks that fit at once, never more than needed
             const uint64_t need = (g.n_units + DF_WAVES - 1) / DF_WAVES;
             const uint32_t fg = (uint32_t)std::min<uint64_t>(need, (uint64_t)per_cu * (uint64_t)std::max(ncu, 1));
-            CKR_LAUNCH("decode_fast_kernel", s, kern<<<fg, 64 * DF_WAVES, lb, s>>>(data, hdrs, unit_off, d_dec, canon, cw, g, sidecar, dst, bad));
+            CKR_LAUNCH("decode_fast_kernel", s, kern<<<fg, 64 * DF_WAVES, lb, s>>>(data, hdrs, unit_off, d_dec, canon, cw, g, sidecar, dst, bad, zero_bytes ? 1u : 0u));
             fast_ran = true;
             return hipGetLastError();
         };

@@ -245,7 +245,10 @@ CKR_API int ckr_compress_many(ckr_compress_job* jobs, uint64_t n_jobs, uint64_t 
  * d_sidecar may be NULL only for dtypes without a sidecar.  The table must sum
  * to 4096.  Stream checks (every lane ends in state 2^23 having consumed
  * exactly byte_count bytes) are accumulated on the device; if h_bad_lanes is
- * not NULL the call synchronises and stores the number of failing lanes. ---- */
+ * not NULL the call synchronises and stores the number of failing lanes.  The
+ * lanes of the masked (always zero) planes are checked against their
+ * canonical stream, header and bytes; their bytes, which do not enter the
+ * output, are read for that only when h_bad_lanes is not NULL. ---- */
 CKR_API uint64_t ckr_decode_workspace_bytes(uint64_t n_elems, int dtype, uint64_t unit_bytes);
 CKR_API int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers,
                        const uint64_t* d_unit_offsets,
