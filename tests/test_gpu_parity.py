@@ -400,7 +400,9 @@ def test_decode_counts_corrupted_lanes(unit, where, gpu):
     final state L, every byte consumed, canonical zero-plane streams).  A
     zero-plane lane's bytes are compared step by step during the decode (units
     up to 1 MiB) or decoded (above: they must give zeros): a flip in its first
-    or last byte, in the second unit, or in its header counts that one lane."""
+    or last byte, in the second unit, or in its header counts that one lane.
+    Those bytes do not enter the output, and a decode that does not read the
+    count gives the original bytes without comparing them."""
     import torch
     ck = _ck()
     n = (unit // 4) * 2 + 777
@@ -430,6 +432,19 @@ def test_decode_counts_corrupted_lanes(unit, where, gpu):
         assert bad == 1
     else:
         assert bad >= 1
+    if where in ("zero", "zero_last"):
+        # a zero-plane lane's bytes do not enter the output: a decode that does
+        # not read the count (and so does not compare them) still gives the
+        # original bytes, alone and in ckr_decode_many
+        d = ck.Decoder(n, dg.F32, unit, device=gpu)
+        out = torch.empty(n * 4, dtype=torch.uint8, device=gpu)
+        assert d.decode(enc.data, enc.headers, enc.unit_offsets, enc.table, enc.sidecar, out, check=False) is None
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), dg.raw_bytes(raw))
+        out.zero_()
+        assert ck.decode_many([d], [enc], [out], check=False) is None
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), dg.raw_bytes(raw))
 
 
 @pytest.mark.parametrize("tag,unit", [(dg.F32, 1 << 20), (dg.BF16, 1 << 20), (dg.F32, 65536)])
