@@ -1450,6 +1450,10 @@ struct ManyAux {
     hipEvent_t ev_x[3] = {nullptr, nullptr, nullptr};  // s2, sx[0], sx[1] done (ckr_decode_many)
     uint64_t* bads = nullptr;    // ckr_decode_many's bad-lane counts, one per job
     uint64_t bad_jobs = 0;
+    ckr::TableArg* dtabs = nullptr;    // ckr_decode_many's frequency tables, staged (pinned)
+    ckr::TableArg* d_dtabs = nullptr;  // and on the device
+    uint64_t dtab_jobs = 0;
+    hipEvent_t ev_dtab = nullptr;      // their last upload done (the pinned copy may be reused)
 };
 hipError_t many_aux(ManyAux** out) {
     thread_local std::vector<ManyAux> per_dev;
@@ -1467,6 +1471,7 @@ hipError_t many_aux(ManyAux** out) {
         if ((e = hipEventCreateWithFlags(&a.ev, hipEventDisableTiming)) != hipSuccess) return e;
         if ((e = hipEventCreateWithFlags(&a.ev_prev, hipEventDisableTiming)) != hipSuccess) return e;
         if ((e = hipEventCreateWithFlags(&a.ev_tail, hipEventDisableTiming)) != hipSuccess) return e;
+        if ((e = hipEventCreateWithFlags(&a.ev_dtab, hipEventDisableTiming)) != hipSuccess) return e;
         if ((e = hipHostMalloc(reinterpret_cast<void**>(&a.pinned), 2 * 768 * sizeof(uint32_t), hipHostMallocDefault)) !=
             hipSuccess)
             return e;
@@ -1844,17 +1849,18 @@ namespace {
 // ckr_decode and its no-allocation variant.  noalloc: the workspace is the
 // device's scratch array, the destination must be 4-byte aligned (no staging
 // copy), and the bad-lane count is read back through the caller's stack.
-// counted: the caller reads the bad-lane count (h_bad_lanes, or
-// ckr_decode_many's check), so that the fast decoder also compares the
-// zero-plane lanes' bytes, which do not enter the output.
-int decode_impl(const uint8_t* d_data, const ckr_stream_header* d_headers, const uint64_t* d_unit_offsets,
-                const ckr_freq_table* h_table, uint64_t n_elems, int dtype, uint64_t unit_bytes,
-                const uint8_t* d_sidecar, void* d_dst, void* d_workspace, uint64_t workspace_bytes,
-                uint64_t* h_bad_lanes, void* stream, bool noalloc, bool counted) {
+// A decode's arguments checked, with what its launches need (no launch).
+struct DecPrep {
+    ckr::EncodeGeom g{};
+    DecodeLayout L{};
+    ckr::TableArg ta{};
+};
+int decode_prepare(const uint8_t* d_data, const ckr_stream_header* d_headers, const uint64_t* d_unit_offsets,
+                   const ckr_freq_table* h_table, uint64_t n_elems, int dtype, uint64_t unit_bytes,
+                   const uint8_t* d_sidecar, void* d_dst, void* d_workspace, uint64_t workspace_bytes, DecPrep& p) {
     if (!dtype_ok(dtype)) return fail(CKR_E_INVALID, "[ckr] unknown dtype %d", dtype);
-    ckr::EncodeGeom g;
+    ckr::EncodeGeom& g = p.g;
     if (!make_geom(n_elems, dtype, unit_bytes, &g)) return CKR_E_INVALID;
-    if (h_bad_lanes) *h_bad_lanes = 0;
     if (g.n_units == 0) return CKR_OK;
     if (!h_table || !d_data || !d_headers || !d_unit_offsets || !d_dst || !d_workspace)
         return fail(CKR_E_INVALID, "[ckr] null pointer");
@@ -1876,8 +1882,27 @@ int decode_impl(const uint8_t* d_data, const ckr_stream_header* d_headers, const
     }
     if (h_table->cum_freq[256] != CKR_M)
         return fail(CKR_E_TABLE, "[ckr] table sums to %u, not 4096: stream not decodable", h_table->cum_freq[256]);
-    ckr::TableArg ta;
-    if (!table_arg(h_table, &ta)) return CKR_E_TABLE;
+    if (!table_arg(h_table, &p.ta)) return CKR_E_TABLE;
+    p.L = L;
+    return CKR_OK;
+}
+
+// counted: the caller reads the bad-lane count (h_bad_lanes, or
+// ckr_decode_many's check), so that the fast decoder also compares the
+// zero-plane lanes' bytes, which do not enter the output.
+int decode_impl(const uint8_t* d_data, const ckr_stream_header* d_headers, const uint64_t* d_unit_offsets,
+                const ckr_freq_table* h_table, uint64_t n_elems, int dtype, uint64_t unit_bytes,
+                const uint8_t* d_sidecar, void* d_dst, void* d_workspace, uint64_t workspace_bytes,
+                uint64_t* h_bad_lanes, void* stream, bool noalloc, bool counted) {
+    if (h_bad_lanes) *h_bad_lanes = 0;
+    DecPrep p;
+    if (int rc = decode_prepare(d_data, d_headers, d_unit_offsets, h_table, n_elems, dtype, unit_bytes, d_sidecar, d_dst,
+                                d_workspace, workspace_bytes, p))
+        return rc;
+    const ckr::EncodeGeom& g = p.g;
+    if (g.n_units == 0) return CKR_OK;
+    const DecodeLayout& L = p.L;
+    const ckr::TableArg& ta = p.ta;
     hipStream_t s = (hipStream_t)stream;
     uint8_t* ws = static_cast<uint8_t*>(d_workspace);
     auto* canon = reinterpret_cast<uint32_t*>(ws + L.off_canon);
@@ -2013,6 +2038,81 @@ int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int c
         a->bad_jobs = 0;
         CKR_HIP(hipHostMalloc(reinterpret_cast<void**>(&a->bads), n * sizeof(uint64_t), hipHostMallocDefault));
         a->bad_jobs = n;
+    }
+    // A shard of small tensors that the fast decoder takes whole (masked
+    // dtypes of one kind or two, 4-byte aligned destinations): one set-up
+    // launch for every job's decode table, canonical streams and bad-lane
+    // counter, from the frequency tables uploaded in one copy, then one decode
+    // launch over every job's units per dtype class, all on the caller's
+    // stream.  The per-job launches otherwise came 10-20 us apart, slower than
+    // the small decodes ran.  Any job that does not qualify, or fails its
+    // checks, sends the shard the per-job way below.
+    if (small && n > 1 && !g_prof_on) {
+        std::vector<DecPrep> pp(n);
+        bool all = true;
+        for (uint64_t i = 0; i < n && all; i++) {
+            const ckr_decode_job& jb = jobs[i];
+            all = decode_prepare(jb.d_data, jb.d_headers, jb.d_unit_offsets, jb.h_table, jb.n_elems, jb.dtype,
+                                 unit_bytes, jb.d_sidecar, jb.d_dst, jb.d_workspace, jb.workspace_bytes, pp[i]) == CKR_OK &&
+                  pp[i].g.n_units > 0 && pp[i].L.fast && !use_long_units(pp[i].g) && aligned_to(jb.d_dst, 4);
+        }
+        const void* chains = all ? canon_chains(s) : nullptr;
+        if (all && chains) {
+            if (a->dtab_jobs < n) {
+                CKR_HIP(hipEventSynchronize(a->ev_dtab));
+                if (a->dtabs) CKR_HIP(hipHostFree(a->dtabs));
+                if (a->d_dtabs) CKR_HIP(hipFree(a->d_dtabs));
+                a->dtabs = nullptr;
+                a->d_dtabs = nullptr;
+                a->dtab_jobs = 0;
+                CKR_HIP(hipHostMalloc(reinterpret_cast<void**>(&a->dtabs), n * sizeof(ckr::TableArg), hipHostMallocDefault));
+                CKR_HIP(hipMalloc(reinterpret_cast<void**>(&a->d_dtabs), n * sizeof(ckr::TableArg)));
+                a->dtab_jobs = n;
+            }
+            CKR_HIP(hipEventSynchronize(a->ev_dtab));  // the previous call's upload has left the pinned copy
+            std::vector<ckr::DecSetupJob> sj(n);
+            std::vector<ckr::DecJob> dj[2];
+            for (uint64_t i = 0; i < n; i++) {
+                const ckr_decode_job& jb = jobs[i];
+                const DecPrep& p = pp[i];
+                a->dtabs[i] = p.ta;
+                uint8_t* ws = static_cast<uint8_t*>(jb.d_workspace);
+                auto* canon = reinterpret_cast<uint32_t*>(ws + p.L.off_canon);
+                auto* dec = reinterpret_cast<uint32_t*>(ws + p.L.off_dec);
+                auto* bad = reinterpret_cast<unsigned long long*>(ws + p.L.off_bad);
+                const CanonKs ck = canon_ks(p.g);
+                sj[i] = ckr::DecSetupJob{a->d_dtabs + i, dec, canon, bad, ck.k0, ck.k1, ck.k2, ck.cw};
+                ckr::DecJob d{};
+                d.data = jb.d_data;
+                d.hdrs = jb.d_headers;
+                d.unit_off = jb.d_unit_offsets;
+                d.dec = dec;
+                d.canon = canon;
+                d.sidecar = jb.d_sidecar;
+                d.dst = static_cast<uint8_t*>(jb.d_dst);
+                d.bad = bad;
+                d.g = p.g;
+                d.cw = ck.cw;
+                d.zero_bytes = check ? 1u : 0u;
+                dj[p.g.spe == 2 ? 1 : 0].push_back(d);
+            }
+            CKR_HIP(hipMemcpyAsync(a->d_dtabs, a->dtabs, n * sizeof(ckr::TableArg), hipMemcpyHostToDevice, s));
+            CKR_HIP(hipEventRecord(a->ev_dtab, s));
+            CKR_HIP(ckr::launch_dec_setup_multi(sj.data(), (uint32_t)n, chains, s));
+            for (auto& v : dj)
+                for (size_t o = 0; o < v.size(); o += ckr::kMaxDecJobs) {
+                    const hipError_t e = ckr::launch_decode_fast_multi(
+                        v.data() + o, (uint32_t)std::min<size_t>(ckr::kMaxDecJobs, v.size() - o), s);
+                    if (e != hipSuccess) return fail(CKR_E_HIP, "[ckr] decode launch failed: %s", hipGetErrorString(e));
+                }
+            if (check) {
+                for (uint64_t i = 0; i < n; i++)
+                    CKR_HIP(hipMemcpyAsync(a->bads + i, sj[i].bad, 8, hipMemcpyDeviceToHost, s));
+                CKR_HIP(hipStreamSynchronize(s));
+                for (uint64_t i = 0; i < n; i++) jobs[i].bad_lanes = a->bads[i];
+            }
+            return CKR_OK;
+        }
     }
     // every stream joins the caller's again, also when a job fails to queue
     auto join = [&]() -> hipError_t {

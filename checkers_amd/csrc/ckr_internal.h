@@ -271,6 +271,45 @@ struct CanonArg {
 };
 hipError_t launch_canon_store(const CanonArg& a, uint32_t* canon, hipStream_t s);
 
+// Several small tensors' fast decodes (ckr_decode_many): one set-up launch
+// (each job's decode table from its frequency table staged in device memory,
+// its canonical zero-plane streams from the state chains, its bad-lane counter
+// cleared), then one decode launch over every job's units.
+static constexpr uint32_t kMaxDecJobs = 16;
+struct DecSetupJob {
+    const TableArg* tab;   // staged in device memory
+    uint32_t* dec;         // 4096 words
+    uint32_t* canon;       // canonical streams (cw dwords per entry)
+    unsigned long long* bad;
+    uint32_t k0, k1, k2, cw;
+};
+struct DecSetupJobs {
+    uint32_t n;
+    DecSetupJob j[kMaxDecJobs];
+};
+struct DecJob {
+    const uint8_t* data;
+    const ckr_stream_header* hdrs;
+    const uint64_t* unit_off;
+    const uint32_t* dec;
+    const uint32_t* canon;
+    const uint8_t* sidecar;
+    uint8_t* dst;           // 4-byte aligned
+    unsigned long long* bad;
+    EncodeGeom g;
+    uint32_t cw, zero_bytes;
+    uint32_t blk0, nblk;    // set by launch_decode_fast_multi
+};
+struct DecJobs {
+    uint32_t n;
+    DecJob j[kMaxDecJobs];
+};
+hipError_t launch_dec_setup_multi(const DecSetupJob* jobs, uint32_t n, const void* chains, hipStream_t s);
+// Jobs of one spe (masked dtypes); hipErrorInvalidValue when they are not, or
+// when the fast decoder's LDS does not fit the device (the caller then decodes
+// them one by one).
+hipError_t launch_decode_fast_multi(DecJob* jobs, uint32_t n, hipStream_t s);
+
 // Decode; with canon (masked dtypes) the fast kernel decodes every unit,
 // otherwise the general kernel does.
 uint32_t decode_fast_lds_bytes();

@@ -215,14 +215,80 @@ struct Chains {
     const uint8_t* b;
 };
 
+// Canonical zero-plane streams (canon_host's layout) of lane counts K0, K1,
+// K2 for symbol 0 of count f, from the state chains, in a workgroup of 256:
+// canon_load issues the chain loads (used after other work), canon_put puts
+// them in LDS (a barrier must follow), canon_write writes the entries: entry
+// e's header {K, final state, bytes B, 0}, then its slot dwords (dword w holds
+// pushed bytes 4w .. 4w+3, the first in the top byte; the last, partial one
+// its r = B mod 4 bytes the same way), and after the three entries their
+// streams in byte order, which are the pushed bytes reversed (stream byte q =
+// pushed byte B - 1 - q).
+constexpr uint32_t kPushedMax = 2 * kChainSteps + 8;  // rows of chain_b
+struct CanonLds {
+    uint32_t ex[3], eb[3];
+    uint8_t pb[kPushedMax];
+};
+struct CanonLoad {
+    uint8_t b0, b1, b2;
+    uint32_t exv, ebv;
+};
+__device__ __forceinline__ CanonLoad canon_load(uint32_t f, uint32_t k0, uint32_t k1, uint32_t k2, const Chains& ch) {
+    const uint32_t s = threadIdx.x;
+    const uint32_t kmax = min(max(k0, max(k1, k2)), kChainSteps);
+    const uint32_t npb = 2 * kmax + 8;  // at least the bytes pushed in kmax steps
+    CanonLoad c{0, 0, 0, 0u, 0u};
+    if (s < npb) c.b0 = ch.b[s * kChainRows + f];
+    if (s + 256 < npb) c.b1 = ch.b[(s + 256) * kChainRows + f];
+    if (s + 512 < npb) c.b2 = ch.b[(s + 512) * kChainRows + f];
+    if (s < 3) {
+        const uint32_t K = s == 0 ? k0 : (s == 1 ? k1 : k2);
+        c.exv = ch.x[K * kChainRows + f];
+        c.ebv = ch.n[K * kChainRows + f];
+    }
+    return c;
+}
+__device__ __forceinline__ void canon_put(const CanonLoad& c, CanonLds& C) {
+    const uint32_t s = threadIdx.x;
+    C.pb[s] = c.b0;
+    if (s + 256 < kPushedMax) C.pb[s + 256] = c.b1;
+    if (s + 512 < kPushedMax) C.pb[s + 512] = c.b2;
+    if (s < 3) { C.ex[s] = c.exv; C.eb[s] = c.ebv; }
+}
+__device__ __forceinline__ void canon_write(uint32_t k0, uint32_t k1, uint32_t k2, uint32_t cw, const CanonLds& C,
+                                            uint32_t* __restrict__ canon) {
+    const uint32_t s = threadIdx.x;
+    for (uint32_t en = 0; en < 3; en++) {
+        const uint32_t B = C.eb[en], w = B >> 2, r = B & 3u;
+        for (uint32_t d = s; d < cw; d += 256) {
+            uint32_t sv = 0;
+            if (d < w) sv = ((uint32_t)C.pb[4 * d] << 24) | ((uint32_t)C.pb[4 * d + 1] << 16) | ((uint32_t)C.pb[4 * d + 2] << 8) | C.pb[4 * d + 3];
+            else if (d == w) for (uint32_t i = 0; i < r; i++) sv = (sv << 8) | C.pb[4 * w + i];
+            uint32_t bv = 0;
+#pragma unroll
+            for (uint32_t k = 0; k < 4; k++) {
+                const uint32_t q = 4 * d + k;
+                if (q < B) bv |= (uint32_t)C.pb[B - 1 - q] << (8 * k);
+            }
+            canon[en * (4 + cw) + 4 + d] = sv;
+            canon[3 * (4 + cw) + en * cw + d] = bv;
+        }
+    }
+    if (s < 3) {
+        uint32_t* base = canon + s * (4 + cw);
+        base[0] = s == 0 ? k0 : (s == 1 ? k1 : k2);
+        base[1] = C.ex[s];
+        base[2] = C.eb[s];
+        base[3] = 0;
+    }
+}
+
 // LDS of table_enc_body (the histogram kernel's copies, reused once they are
 // summed).
-constexpr uint32_t kPushedMax = 2 * kChainSteps + 8;  // rows of chain_b
 struct TableLds {
     RankTable T;
     float fred[4][8];
-    uint32_t ex[3], eb[3];
-    uint8_t pb[kPushedMax];
+    CanonLds C;
 };
 
 // The encode set-up of a tensor from its histograms on the device (no host
@@ -233,14 +299,8 @@ struct TableLds {
 // size of K symbols from the plane histograms plus six standard deviations),
 // then the larger is cut until both fit the launch's LDS (sum at most 2 smax).
 // ctl[6..7] gets the launch's epoch, the sign for the host that the table was
-// built in this launch; ctl[2] (failure flags) starts as flags.
-//
-// Canonical streams (canon_host's layout) of lane counts K0, K1, K2 for symbol
-// 0 of count f = norm[0]: entry e's header {K, final state, bytes B, 0}, then
-// its slot dwords (dword w holds pushed bytes 4w .. 4w+3, the first in the top
-// byte; the last, partial one its r = B mod 4 bytes the same way), and after
-// the three entries their streams in byte order, which are the pushed bytes
-// reversed (stream byte q = pushed byte B - 1 - q).
+// built in this launch; ctl[2] (failure flags) starts as flags.  The
+// canonical streams are those of symbol 0 of count f = norm[0].
 __device__ void table_enc_body(const uint32_t* __restrict__ hist, const TableEncArg& a, EncSym* __restrict__ enc,
                                uint32_t* __restrict__ canon, uint32_t* __restrict__ tinfo, uint32_t* __restrict__ ctl,
                                const Chains& ch, uint64_t epoch, uint32_t flags, TableLds& W) {
@@ -248,19 +308,7 @@ __device__ void table_enc_body(const uint32_t* __restrict__ hist, const TableEnc
     rank_table(hist, a.ensure_full != 0, T);
     const uint32_t s = threadIdx.x;
     // the chain data of the canonical streams, loaded now and used at the end
-    const uint32_t f0 = T.norm[0];
-    const uint32_t kmax = min(max(a.k0, max(a.k1, a.k2)), kChainSteps);
-    const uint32_t npb = 2 * kmax + 8;  // at least the bytes pushed in kmax steps
-    uint8_t b0 = 0, b1 = 0, b2 = 0;
-    if (s < npb) b0 = ch.b[s * kChainRows + f0];
-    if (s + 256 < npb) b1 = ch.b[(s + 256) * kChainRows + f0];
-    if (s + 512 < npb) b2 = ch.b[(s + 512) * kChainRows + f0];
-    uint32_t exv = 0, ebv = 0;
-    if (s < 3) {
-        const uint32_t K = s == 0 ? a.k0 : (s == 1 ? a.k1 : a.k2);
-        exv = ch.x[K * kChainRows + f0];
-        ebv = ch.n[K * kChainRows + f0];
-    }
+    const CanonLoad cl = canon_load(T.norm[0], a.k0, a.k1, a.k2, ch);
     const uint32_t nm = T.norm[s];
     enc[s] = enc_entry_fc(nm, T.cum[s]);
     tinfo[s] = nm;
@@ -283,11 +331,7 @@ __device__ void table_enc_body(const uint32_t* __restrict__ hist, const TableEnc
     if ((s & 63) == 0)
 #pragma unroll
         for (int i = 0; i < 6; i++) W.fred[s >> 6][i] = v[i];
-    // the pushed bytes into LDS
-    W.pb[s] = b0;
-    if (s + 256 < kPushedMax) W.pb[s + 256] = b1;
-    if (s + 512 < kPushedMax) W.pb[s + 512] = b2;
-    if (s < 3) { W.ex[s] = exv; W.eb[s] = ebv; }
+    canon_put(cl, W.C);
     __syncthreads();
     if (s == 0) {
         uint32_t sl[2];
@@ -311,31 +355,7 @@ __device__ void table_enc_body(const uint32_t* __restrict__ hist, const TableEnc
         ctl[6] = (uint32_t)epoch;
         ctl[7] = (uint32_t)(epoch >> 32);
     }
-    // the canonical streams: dword d of each entry, in slot and in stream form
-    const uint32_t cw = a.cw;
-    for (uint32_t en = 0; en < 3; en++) {
-        const uint32_t B = W.eb[en], w = B >> 2, r = B & 3u;
-        for (uint32_t d = s; d < cw; d += 256) {
-            uint32_t sv = 0;
-            if (d < w) sv = ((uint32_t)W.pb[4 * d] << 24) | ((uint32_t)W.pb[4 * d + 1] << 16) | ((uint32_t)W.pb[4 * d + 2] << 8) | W.pb[4 * d + 3];
-            else if (d == w) for (uint32_t i = 0; i < r; i++) sv = (sv << 8) | W.pb[4 * w + i];
-            uint32_t bv = 0;
-#pragma unroll
-            for (uint32_t k = 0; k < 4; k++) {
-                const uint32_t q = 4 * d + k;
-                if (q < B) bv |= (uint32_t)W.pb[B - 1 - q] << (8 * k);
-            }
-            canon[en * (4 + cw) + 4 + d] = sv;
-            canon[3 * (4 + cw) + en * cw + d] = bv;
-        }
-    }
-    if (s < 3) {
-        uint32_t* base = canon + s * (4 + cw);
-        base[0] = s == 0 ? a.k0 : (s == 1 ? a.k1 : a.k2);
-        base[1] = W.ex[s];
-        base[2] = W.eb[s];
-        base[3] = 0;
-    }
+    canon_write(a.k0, a.k1, a.k2, a.cw, W.C, canon);
 }
 
 __global__ void __launch_bounds__(256) build_enc_table_kernel(TableArg t, EncSym* out) {
@@ -3477,15 +3497,17 @@ __device__ __forceinline__ bool df_zero_lane_ok(const ckr_stream_header& h, cons
     return diff == 0;
 }
 
+// One tensor's share of the decode: workgroup blk of nblk takes units blk *
+// DF_WAVES + wave, stepping by nblk * DF_WAVES.
 template <int SPE>
-__global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_t* __restrict__ data,
-                                                                   const ckr_stream_header* __restrict__ hdrs,
-                                                                   const uint64_t* __restrict__ unit_off,
-                                                                   const uint32_t* __restrict__ d_dec,
-                                                                   const uint32_t* __restrict__ canon, uint32_t cw,
-                                                                   EncodeGeom g, const uint8_t* __restrict__ sidecar,
-                                                                   uint8_t* __restrict__ dst, unsigned long long* bad,
-                                                                   uint32_t zero_bytes) {
+__device__ __forceinline__ void decode_fast_body(const uint8_t* __restrict__ data,
+                                                 const ckr_stream_header* __restrict__ hdrs,
+                                                 const uint64_t* __restrict__ unit_off,
+                                                 const uint32_t* __restrict__ d_dec,
+                                                 const uint32_t* __restrict__ canon, uint32_t cw, EncodeGeom g,
+                                                 const uint8_t* __restrict__ sidecar, uint8_t* __restrict__ dst,
+                                                 unsigned long long* bad, uint32_t zero_bytes, uint32_t blk,
+                                                 uint32_t nblk) {
     extern __shared__ uint32_t lds[];
     uint8_t* lds8 = reinterpret_cast<uint8_t*>(lds);
     const uint32_t* tab = reinterpret_cast<const uint32_t*>(lds);
@@ -3505,15 +3527,15 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
 
     // the next unit's headers (this thread's four lanes) are loaded while the
     // current unit is decoded
-    const uint64_t ustride = (uint64_t)gridDim.x * DF_WAVES;
+    const uint64_t ustride = (uint64_t)nblk * DF_WAVES;
     ckr_stream_header hn[4];
     auto load_headers = [&](uint64_t v) __attribute__((always_inline)) {
         const ckr_stream_header* vh = hdrs + v * 256 + 4 * j;
 #pragma unroll
         for (int b = 0; b < 4; b++) hn[b] = vh[b];
     };
-    if ((uint64_t)blockIdx.x * DF_WAVES + wv < g.n_units) load_headers((uint64_t)blockIdx.x * DF_WAVES + wv);
-    for (uint64_t u = (uint64_t)blockIdx.x * DF_WAVES + wv; u < g.n_units; u += ustride) {
+    if ((uint64_t)blk * DF_WAVES + wv < g.n_units) load_headers((uint64_t)blk * DF_WAVES + wv);
+    for (uint64_t u = (uint64_t)blk * DF_WAVES + wv; u < g.n_units; u += ustride) {
         ckr_stream_header uh[4];
 #pragma unroll
         for (int b = 0; b < 4; b++) uh[b] = hn[b];
@@ -3648,6 +3670,62 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_
         nbad_total += nbad;
     }
     if (nbad_total) atomicAdd(bad, nbad_total);
+}
+
+template <int SPE>
+__global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_kernel(const uint8_t* __restrict__ data,
+                                                                   const ckr_stream_header* __restrict__ hdrs,
+                                                                   const uint64_t* __restrict__ unit_off,
+                                                                   const uint32_t* __restrict__ d_dec,
+                                                                   const uint32_t* __restrict__ canon, uint32_t cw,
+                                                                   EncodeGeom g, const uint8_t* __restrict__ sidecar,
+                                                                   uint8_t* __restrict__ dst, unsigned long long* bad,
+                                                                   uint32_t zero_bytes) {
+    decode_fast_body<SPE>(data, hdrs, unit_off, d_dec, canon, cw, g, sidecar, dst, bad, zero_bytes, blockIdx.x,
+                          gridDim.x);
+}
+
+// Several tensors' decodes in one launch (ckr_decode_many on a shard of small
+// tensors): one workgroup per DF_WAVES units of a job, workgroup b working for
+// the last job whose first workgroup is <= b, with that job's table in its
+// LDS.  One launch instead of one per tensor on four
+// streams, whose launches the host could not issue as fast as the small
+// decodes ran.
+template <int SPE>
+__global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_multi_kernel(DecJobs J) {
+    uint32_t k = 0;
+    while (k + 1 < J.n && J.j[k + 1].blk0 <= blockIdx.x) k++;
+    const DecJob& b = J.j[k];
+    decode_fast_body<SPE>(b.data, b.hdrs, b.unit_off, b.dec, b.canon, b.cw, b.g, b.sidecar, b.dst, b.bad,
+                          b.zero_bytes, blockIdx.x - b.blk0, b.nblk);
+}
+
+// The decode set-up of several tensors in one launch, one workgroup per job:
+// its decode table from the frequency table staged in device memory
+// (TableArg's norm, cum), the canonical zero-plane streams from the state
+// chains, and its bad-lane counter cleared.
+__global__ void __launch_bounds__(256) dec_setup_multi_kernel(DecSetupJobs J, Chains ch) {
+    const DecSetupJob& t = J.j[blockIdx.x];
+    __shared__ uint32_t cum[257];
+    __shared__ CanonLds C;
+    const uint32_t s = threadIdx.x;
+    for (uint32_t i = s; i < 257; i += 256) cum[i] = t.tab->cum[i];
+    const CanonLoad cl = canon_load(t.tab->norm[0], t.k0, t.k1, t.k2, ch);
+    if (s == 0) *t.bad = 0;
+    canon_put(cl, C);
+    __syncthreads();
+    // slot j in [cum[x], cum[x] + norm[x]) decodes to x: the largest x with cum[x] <= j
+    for (uint32_t q = 0; q < 16; q++) {
+        const uint32_t j = q * 256 + s;
+        uint32_t lo = 0, hi = 256;
+        while (hi - lo > 1) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (cum[mid] <= j) lo = mid; else hi = mid;
+        }
+        const uint32_t f = t.tab->norm[lo];
+        if (j < cum[256] && f) t.dec[j] = lo | ((f - 1u) << 8) | (cum[lo] << 20);
+    }
+    canon_write(t.k0, t.k1, t.k2, t.cw, C, t.canon);
 }
 
 // ------------------------------------------------------------------ long units
@@ -4189,6 +4267,49 @@ hipError_t launch_build_dec_table(const TableArg& t, uint32_t* d_dec, unsigned l
 
 uint32_t decode_fast_lds_bytes() { return DF_TAB_BYTES + DF_WAVES * DF_WAVE_BYTES; }
 
+hipError_t launch_dec_setup_multi(const DecSetupJob* jobs, uint32_t n, const void* chains, hipStream_t s) {
+    for (uint32_t j0 = 0; j0 < n; j0 += kMaxDecJobs) {
+        DecSetupJobs J{};
+        J.n = std::min<uint32_t>(kMaxDecJobs, n - j0);
+        for (uint32_t k = 0; k < J.n; k++) J.j[k] = jobs[j0 + k];
+        CKR_LAUNCH("dec_setup_multi_kernel", s, dec_setup_multi_kernel<<<J.n, 256, 0, s>>>(J, chains_of(chains)));
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+hipError_t launch_decode_fast_multi(DecJob* jobs, uint32_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    if (n > kMaxDecJobs) return hipErrorInvalidValue;
+    const int spe = jobs[0].g.spe;
+    for (uint32_t i = 0; i < n; i++)
+        if (jobs[i].g.spe != spe || (spe != 1 && spe != 2)) return hipErrorInvalidValue;
+    const uint32_t lb = decode_fast_lds_bytes();
+    int per_cu = 0;
+    auto kern = spe == 2 ? decode_fast_multi_kernel<2> : decode_fast_multi_kernel<1>;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize, (int)lb) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 64 * DF_WAVES, lb) != hipSuccess || per_cu < 1) {
+        (void)hipGetLastError();
+        return hipErrorInvalidValue;
+    }
+    // one workgroup per DF_WAVES units of a job (a unit per wave): more than
+    // fit at once, so that the dispatcher hands the next workgroup to each CU
+    // a finished one leaves (fixed shares of the resident workgroups left every
+    // job several rounds, the last of them partly idle)
+    DecJobs J{};
+    J.n = n;
+    uint64_t nb = 0;
+    for (uint32_t i = 0; i < n; i++) {
+        DecJob& b = jobs[i];
+        b.nblk = (uint32_t)std::max<uint64_t>(1, (b.g.n_units + DF_WAVES - 1) / DF_WAVES);
+        b.blk0 = (uint32_t)nb;
+        nb += b.nblk;
+        J.j[i] = b;
+    }
+    if (nb > 0x7fffffffu) return hipErrorInvalidValue;
+    CKR_LAUNCH("decode_fast_kernel", s, kern<<<(uint32_t)nb, 64 * DF_WAVES, lb, s>>>(J));
+    return hipGetLastError();
+}
 hipError_t launch_decode(const uint8_t* data, const ckr_stream_header* hdrs, const uint64_t* unit_off,
                          const uint32_t* d_dec, const EncodeGeom& g, const uint8_t* sidecar, uint8_t* dst,
                          unsigned long long* bad, const uint32_t* canon, uint32_t cw, hipStream_t s, bool zero_bytes) {

@@ -259,11 +259,14 @@ CKR_API int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers
 
 /* ---- several decodes in one call; no counterpart in the reference (it has
  * no decoder).  For restoring a shard: the same results as ckr_decode called
- * on each job.  When no job's output exceeds 256 MiB the jobs go round robin
- * over the caller's stream and three library-owned streams, so that the
- * decodes of small tensors (too few units to fill the device) run side by
- * side; otherwise they alternate between `stream` and one library-owned
- * stream, so that each decode starts as the previous one's last units finish.
+ * on each job.  When no job's output exceeds 256 MiB and the fast decoder
+ * takes every job whole (masked dtypes, 4-byte aligned destinations), every
+ * job's set-up is one launch and every job's decode one more (per dtype
+ * class), on `stream`; other small jobs go round robin over the caller's
+ * stream and three library-owned streams, so that the decodes of small
+ * tensors (too few units to fill the device) run side by side; larger jobs
+ * alternate between `stream` and one library-owned stream, so that each
+ * decode starts as the previous one's last units finish.
  * The inputs must be ready in
  * `stream` order, and the outputs are ready in `stream` order when the call
  * returns work queued (check == 0, no synchronisation).  check != 0: the call
