@@ -2040,7 +2040,8 @@ int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int c
         a->bad_jobs = n;
     }
     // A shard of small tensors that the fast decoder takes whole (masked
-    // dtypes of one kind or two, 4-byte aligned destinations): one set-up
+    // dtypes of one kind or two, 4-byte aligned destinations; empty jobs have
+    // nothing to decode): one set-up
     // launch for every job's decode table, canonical streams and bad-lane
     // counter, from the frequency tables uploaded in one copy, then one decode
     // launch over every job's units per dtype class, all on the caller's
@@ -2054,7 +2055,8 @@ int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int c
             const ckr_decode_job& jb = jobs[i];
             all = decode_prepare(jb.d_data, jb.d_headers, jb.d_unit_offsets, jb.h_table, jb.n_elems, jb.dtype,
                                  unit_bytes, jb.d_sidecar, jb.d_dst, jb.d_workspace, jb.workspace_bytes, pp[i]) == CKR_OK &&
-                  pp[i].g.n_units > 0 && pp[i].L.fast && !use_long_units(pp[i].g) && aligned_to(jb.d_dst, 4);
+                  (pp[i].g.n_units == 0 ||
+                   (pp[i].L.fast && !use_long_units(pp[i].g) && aligned_to(jb.d_dst, 4)));
         }
         const void* chains = all ? canon_chains(s) : nullptr;
         if (all && chains) {
@@ -2070,18 +2072,22 @@ int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int c
                 a->dtab_jobs = n;
             }
             CKR_HIP(hipEventSynchronize(a->ev_dtab));  // the previous call's upload has left the pinned copy
-            std::vector<ckr::DecSetupJob> sj(n);
+            std::vector<ckr::DecSetupJob> sj;
+            std::vector<uint64_t> sj_job;  // the job of each set-up
             std::vector<ckr::DecJob> dj[2];
             for (uint64_t i = 0; i < n; i++) {
                 const ckr_decode_job& jb = jobs[i];
                 const DecPrep& p = pp[i];
-                a->dtabs[i] = p.ta;
+                if (!p.g.n_units) continue;
+                const uint64_t k = sj.size();
+                a->dtabs[k] = p.ta;
                 uint8_t* ws = static_cast<uint8_t*>(jb.d_workspace);
                 auto* canon = reinterpret_cast<uint32_t*>(ws + p.L.off_canon);
                 auto* dec = reinterpret_cast<uint32_t*>(ws + p.L.off_dec);
                 auto* bad = reinterpret_cast<unsigned long long*>(ws + p.L.off_bad);
                 const CanonKs ck = canon_ks(p.g);
-                sj[i] = ckr::DecSetupJob{a->d_dtabs + i, dec, canon, bad, ck.k0, ck.k1, ck.k2, ck.cw};
+                sj.push_back(ckr::DecSetupJob{a->d_dtabs + k, dec, canon, bad, ck.k0, ck.k1, ck.k2, ck.cw});
+                sj_job.push_back(i);
                 ckr::DecJob d{};
                 d.data = jb.d_data;
                 d.hdrs = jb.d_headers;
@@ -2096,9 +2102,11 @@ int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int c
                 d.zero_bytes = check ? 1u : 0u;
                 dj[p.g.spe == 2 ? 1 : 0].push_back(d);
             }
-            CKR_HIP(hipMemcpyAsync(a->d_dtabs, a->dtabs, n * sizeof(ckr::TableArg), hipMemcpyHostToDevice, s));
-            CKR_HIP(hipEventRecord(a->ev_dtab, s));
-            CKR_HIP(ckr::launch_dec_setup_multi(sj.data(), (uint32_t)n, chains, s));
+            if (!sj.empty()) {
+                CKR_HIP(hipMemcpyAsync(a->d_dtabs, a->dtabs, sj.size() * sizeof(ckr::TableArg), hipMemcpyHostToDevice, s));
+                CKR_HIP(hipEventRecord(a->ev_dtab, s));
+                CKR_HIP(ckr::launch_dec_setup_multi(sj.data(), (uint32_t)sj.size(), chains, s));
+            }
             for (auto& v : dj)
                 for (size_t o = 0; o < v.size(); o += ckr::kMaxDecJobs) {
                     const hipError_t e = ckr::launch_decode_fast_multi(
@@ -2106,10 +2114,10 @@ int ckr_decode_many(ckr_decode_job* jobs, uint64_t n, uint64_t unit_bytes, int c
                     if (e != hipSuccess) return fail(CKR_E_HIP, "[ckr] decode launch failed: %s", hipGetErrorString(e));
                 }
             if (check) {
-                for (uint64_t i = 0; i < n; i++)
-                    CKR_HIP(hipMemcpyAsync(a->bads + i, sj[i].bad, 8, hipMemcpyDeviceToHost, s));
+                for (size_t k = 0; k < sj.size(); k++)
+                    CKR_HIP(hipMemcpyAsync(a->bads + k, sj[k].bad, 8, hipMemcpyDeviceToHost, s));
                 CKR_HIP(hipStreamSynchronize(s));
-                for (uint64_t i = 0; i < n; i++) jobs[i].bad_lanes = a->bads[i];
+                for (size_t k = 0; k < sj.size(); k++) jobs[sj_job[k]].bad_lanes = a->bads[k];
             }
             return CKR_OK;
         }

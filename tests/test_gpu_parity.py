@@ -531,18 +531,23 @@ def test_compress_many_matches_single_calls(unit, paths, gpu):
         ck.compress_many([encs[0], encs[0]], [srcs[0], srcs[0]])
 
 
-def test_decode_many_matches_single_decodes(gpu):
-    """ckr_decode_many (tensors this small decoded side by side on four
-    streams) restores every job bit-exact and reports each job's bad lanes as
-    ckr_decode does: a job whose stream bytes were corrupted counts its own bad
-    lanes and no other job counts any; check=False queues the same work without
-    a synchronisation; one Decoder twice is refused."""
+@pytest.mark.parametrize("batched", [True, False])
+def test_decode_many_matches_single_decodes(batched, gpu):
+    """ckr_decode_many (tensors this small decoded together: in one set-up and
+    one decode launch per dtype class when the fast decoder takes every job,
+    else side by side on four streams, here forced by an int8 job) restores
+    every job bit-exact and reports each job's bad lanes as ckr_decode does: a
+    job whose stream bytes were corrupted counts its own bad lanes and no other
+    job counts any; check=False queues the same work without a
+    synchronisation; one Decoder twice is refused."""
     import torch
     ck = _ck()
     g = torch.Generator(device=gpu).manual_seed(81)
     ts = [(torch.randn(n, device=gpu, generator=g) * sc).to(dt) for n, sc, dt in
           ((300_001, 0.02, torch.bfloat16), (1 << 20, 1e-3, torch.float32), (5, 1e-3, torch.float32),
            (2_000_003, 0.02, torch.bfloat16), (0, 1.0, torch.float32), (700_000, 1e-3, torch.float32))]
+    if not batched:
+        ts.append(torch.randint(-128, 128, (100_003,), dtype=torch.int8, device=gpu, generator=g))
     tags = [ck.torch_tag(t.dtype) for t in ts]
     srcs = [t.view(torch.uint8) for t in ts]
     print("[case] decode_many", flush=True)
