@@ -260,7 +260,8 @@ CKR_API int ckr_decode(const uint8_t* d_data, const ckr_stream_header* d_headers
 /* ---- several decodes in one call; no counterpart in the reference (it has
  * no decoder).  For restoring a shard: the same results as ckr_decode called
  * on each job.  When no job's output exceeds 256 MiB and the fast decoder
- * takes every job whole (masked dtypes, 4-byte aligned destinations), every
+ * takes every non-empty job whole (masked dtypes, 4-byte aligned
+ * destinations), every
  * job's set-up is one launch and every job's decode one more (per dtype
  * class), on `stream`; other small jobs go round robin over the caller's
  * stream and three library-owned streams, so that the decodes of small
