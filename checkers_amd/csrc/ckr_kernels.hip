@@ -3705,27 +3705,31 @@ __global__ void __launch_bounds__(64 * DF_WAVES) decode_fast_multi_kernel(DecJob
 // (TableArg's norm, cum), the canonical zero-plane streams from the state
 // chains, and its bad-lane counter cleared.
 __global__ void __launch_bounds__(256) dec_setup_multi_kernel(DecSetupJobs J, Chains ch) {
-    const DecSetupJob& t = J.j[blockIdx.x];
+    // 16 workgroups per job, one slot each per thread; the first also writes
+    // the canonical streams and clears the bad-lane counter
+    const DecSetupJob& t = J.j[blockIdx.x >> 4];
+    const uint32_t part = blockIdx.x & 15u;
     __shared__ uint32_t cum[257];
     __shared__ CanonLds C;
     const uint32_t s = threadIdx.x;
     for (uint32_t i = s; i < 257; i += 256) cum[i] = t.tab->cum[i];
-    const CanonLoad cl = canon_load(t.tab->norm[0], t.k0, t.k1, t.k2, ch);
-    if (s == 0) *t.bad = 0;
-    canon_put(cl, C);
+    CanonLoad cl{};
+    if (part == 0) {
+        cl = canon_load(t.tab->norm[0], t.k0, t.k1, t.k2, ch);
+        if (s == 0) *t.bad = 0;
+        canon_put(cl, C);
+    }
     __syncthreads();
     // slot j in [cum[x], cum[x] + norm[x]) decodes to x: the largest x with cum[x] <= j
-    for (uint32_t q = 0; q < 16; q++) {
-        const uint32_t j = q * 256 + s;
-        uint32_t lo = 0, hi = 256;
-        while (hi - lo > 1) {
-            const uint32_t mid = (lo + hi) >> 1;
-            if (cum[mid] <= j) lo = mid; else hi = mid;
-        }
-        const uint32_t f = t.tab->norm[lo];
-        if (j < cum[256] && f) t.dec[j] = lo | ((f - 1u) << 8) | (cum[lo] << 20);
+    const uint32_t j = part * 256 + s;
+    uint32_t lo = 0, hi = 256;
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (cum[mid] <= j) lo = mid; else hi = mid;
     }
-    canon_write(t.k0, t.k1, t.k2, t.cw, C, t.canon);
+    const uint32_t f = t.tab->norm[lo];
+    if (j < cum[256] && f) t.dec[j] = lo | ((f - 1u) << 8) | (cum[lo] << 20);
+    if (part == 0) canon_write(t.k0, t.k1, t.k2, t.cw, C, t.canon);
 }
 
 // ------------------------------------------------------------------ long units
@@ -4272,7 +4276,7 @@ hipError_t launch_dec_setup_multi(const DecSetupJob* jobs, uint32_t n, const voi
         DecSetupJobs J{};
         J.n = std::min<uint32_t>(kMaxDecJobs, n - j0);
         for (uint32_t k = 0; k < J.n; k++) J.j[k] = jobs[j0 + k];
-        CKR_LAUNCH("dec_setup_multi_kernel", s, dec_setup_multi_kernel<<<J.n, 256, 0, s>>>(J, chains_of(chains)));
+        CKR_LAUNCH("dec_setup_multi_kernel", s, dec_setup_multi_kernel<<<16 * J.n, 256, 0, s>>>(J, chains_of(chains)));
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
