@@ -520,7 +520,8 @@ def repair_leg(ck, torch, dev, cpu=True):
     grammar build (at most 50 rounds, all 7 bf16 mantissa bits masked), then
     applying it again, each timed on the wall clock around its call (the build
     returns its rules to the host, so the call is complete when it returns).
-    Roofline per SURVEY's measure for this row: B = n_in per round."""
+    Roofline: each build round reads the tensor's words once, so the
+    algorithmic bytes are B = n_in per round."""
     shard = make_shard(2, torch, dev)
     out, tot_b, tot_a, tot_bytes_rounds = [], 0.0, 0.0, 0
     n_max = max(t.numel() for _, t in shard)
