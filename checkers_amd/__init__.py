@@ -491,8 +491,10 @@ class DecodeJob(ctypes.Structure):
 def decode_many(decoders, encoded, dsts, check=True, stream=None):
     """ckr_decode_many: encoded[k] (an Encoded, or any object with data,
     headers, unit_offsets, table and sidecar) decoded by decoders[k] into
-    dsts[k], as Decoder.decode would; small tensors are decoded side by side on
-    several streams.  Returns the bad-lane counts (None when check is False)."""
+    dsts[k], as Decoder.decode would; a shard of small tensors is decoded by one
+    set-up and one decode launch per dtype class (side by side on several
+    streams when the fast decoder does not take every job whole).  Returns the
+    bad-lane counts (None when check is False)."""
     if not (len(decoders) == len(encoded) == len(dsts)) or len({d.unit_bytes for d in decoders}) > 1:
         raise CkrError(CKR_E_INVALID, "decode_many: one item and destination per decoder, one unit size")
     if len({id(d) for d in decoders}) != len(decoders):
